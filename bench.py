@@ -1,0 +1,229 @@
+"""Benchmark of the MI355X quantized compute path (one GPU).
+
+Headline: batch-1 decode GEMV at the FFN shapes,
+Q4_K 14336x4096 (up/gate) and 4096x14336 (down). One step = quantize the
+activation (per-256, as the reference's matmul_q4_k does) + GEMV, for both
+shapes, on weight copies rotated so that the working set (>= 512 MB) exceeds
+the 256 MB Infinity Cache and every weight byte comes from HBM. Inputs are
+resident in HBM before timing. value = algorithmic bytes per step / step time.
+
+Also reported under "extra": the Q4_0 and Q8_0 GEMVs (configs 1-2), the Q6_K
+GEMV, each with its kernel-only bandwidth.
+
+`roofline` is the dominant kernel (Q4_K GEMV, up shape): algorithmic bytes per
+launch / average launch duration, from HIP events around back-to-back launches
+on the stream the kernels run on. `cpu_baseline` times the reference engine's
+own matmul_q4_k (oracle/_ref, compiled from the reference sources) on the
+host, over a bounded sample.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--only NAME] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "Q4_K/Q8_0 GEMV HBM GB/s (% of peak); prefill GEMM TFLOPS (% MFMA peak)"
+ROTATE_BYTES = 640 << 20  # >= 2x the 256 MB Infinity Cache
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_kernel_bytes(qtype, rows, cols):
+    """Algorithmic HBM bytes of one GEMV launch: the GGUF weight bytes, the
+    quantized activation (int8 + fp32 scale + int32 sum per 32) and y (fp32)."""
+    from desireeia_amd import synth
+    return rows * synth.row_bytes(qtype, cols) + cols + cols // 32 * 8 + rows * 4
+
+
+def step_bytes(qtype, rows, cols):
+    """Algorithmic bytes of one quantize+GEMV step: weights + x fp32 + y fp32
+    (the per-call figure of the benchmark plan)."""
+    from desireeia_amd import synth
+    return rows * synth.row_bytes(qtype, cols) + cols * 4 + rows * 4
+
+
+class GemvCase:
+    def __init__(self, qtype, rows, cols, seed, dev):
+        import torch
+        from desireeia_amd import ops, synth
+        self.qtype, self.rows, self.cols = qtype, rows, cols
+        w = synth.gen_weights(qtype, rows, cols, seed)
+        m0 = ops.QuantMatrix.from_gguf(qtype, w, rows, cols, device=dev)
+        ncopy = max(2, -(-ROTATE_BYTES // m0.buf.numel()))
+        self.mats = [m0] + [m0.clone() for _ in range(ncopy - 1)]
+        self.x = torch.from_numpy(synth.gen_act(cols, seed + 1)).to(dev)
+        self.kind = ops.act_kind_for(m0.fmt)
+        self.act = ops.quantize_act(self.x, self.kind)
+        self.y = torch.empty(rows, dtype=torch.float32, device=dev)
+        self.i = 0
+
+    def step(self):
+        from desireeia_amd import ops
+        m = self.mats[self.i]
+        self.i = (self.i + 1) % len(self.mats)
+        ops.gemv(m, ops.quantize_act(self.x, self.kind), out=self.y)
+
+    def kernel(self):
+        from desireeia_amd import ops
+        m = self.mats[self.i]
+        self.i = (self.i + 1) % len(self.mats)
+        ops.gemv(m, self.act, out=self.y)
+
+
+def time_loop(fn, n, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(n):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / n * 1e3  # us per call
+
+
+def kernel_stats(case, n=400):
+    """Average GEMV launch duration (us) over back-to-back launches."""
+    us = time_loop(case.kernel, n, warmup=20)
+    b = gemv_kernel_bytes(case.qtype, case.rows, case.cols)
+    return us, b / us / 1e3  # GB/s
+
+
+def cpu_baseline_q4k(budget_s=12.0):
+    """The reference's matmul_q4_k (oracle/_ref) on the host cores, 14336x4096,
+    distinct weight copies (DRAM regime), best of repeated passes."""
+    from desireeia_amd import synth
+    from oracle import oracle as orc
+    r = orc.ref()
+    kind = "reference"
+    cores = min(16, len(os.sched_getaffinity(0)))
+    if r is None:
+        r = orc.oracle()
+        kind = "port"
+        cores = 1
+    else:
+        r.set_threads(cores)
+    rows, cols = 14336, 4096
+    w0 = synth.gen_weights(synth.Q4_K, rows, cols, seed=99)
+    copies = [w0] + [np.roll(w0, k, axis=0) for k in range(1, 8)]  # 8 x 33 MB
+    x = synth.gen_act(cols, 100)
+    nbytes = rows * synth.row_bytes(synth.Q4_K, cols)
+    t_end = time.time() + budget_s
+    best, calls, total = 1e30, 0, 0.0
+    while time.time() < t_end or calls < 2:
+        w = copies[calls % len(copies)]
+        t0 = time.perf_counter()
+        if kind == "reference":
+            r.matmul(synth.Q4_K, w, rows, cols, x)
+        else:
+            r.matmul(synth.Q4_K, w, rows, cols, x, 0, 512)
+        dt = time.perf_counter() - t0
+        if kind == "port":
+            dt *= rows / 512.0
+        best = min(best, dt)
+        total += dt
+        calls += 1
+    return {"value": round(nbytes / best / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": f"Q4_K GEMV 14336x4096 (matmul_q4_k incl. its per-256 activation quantization), "
+                      f"8 distinct weight copies (264 MB), best of {calls} calls over {budget_s:.0f} s"
+                      + ("" if kind == "reference" else "; rows 0..511 timed and scaled to 14336")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", default=None, help="profile helper: run one kernel N times (q4k_up, q4k_down, ...)")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, sharding).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from desireeia_amd import _lib, synth
+    _lib.load()
+    dev = torch.device("cuda:0")
+
+    shapes = {
+        "q4k_up": (synth.Q4_K, 14336, 4096), "q4k_down": (synth.Q4_K, 4096, 14336),
+        "q40_up": (synth.Q4_0, 14336, 4096), "q40_down": (synth.Q4_0, 4096, 14336),
+        "q80": (synth.Q8_0, 4096, 4096),
+        "q6k_down": (synth.Q6_K, 4096, 14336),
+    }
+    if args.only:
+        qt, r, c = shapes[args.only]
+        case = GemvCase(qt, r, c, 11, dev)
+        us, gbs = kernel_stats(case, n=args.steps)
+        log(f"{args.only}: {us:.2f} us/launch, {gbs:.1f} GB/s")
+        return
+
+    cases = {k: GemvCase(qt, r, c, 11 + i, dev) for i, (k, (qt, r, c)) in enumerate(shapes.items())}
+
+    # ---- headline: Q4_K decode FFN GEMVs (up 14336x4096 + down 4096x14336), quantize + GEMV each
+    up, down = cases["q4k_up"], cases["q4k_down"]
+
+    def step():
+        up.step()
+        down.step()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    bytes_step = step_bytes(synth.Q4_K, 14336, 4096) + step_bytes(synth.Q4_K, 4096, 14336)
+    value = bytes_step / (ms_per_step * 1e-3) / 1e9
+
+    # ---- per-kernel figures
+    extra = {}
+    for k, c in cases.items():
+        us, gbs = kernel_stats(c)
+        extra[k] = {"shape": f"{c.rows}x{c.cols}", "kernel_us": round(us, 3), "kernel_GBps": round(gbs, 1),
+                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        log(f"{k}: {us:.2f} us  {gbs:.1f} GB/s  ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    dom = extra["q4k_up"]
+    roofline = {"bound": "hbm", "achieved": dom["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "gemv_kernel<Q4_K> 14336x4096",
+                "bytes_per_launch": gemv_kernel_bytes(synth.Q4_K, 14336, 4096)}
+
+    cpu = None if args.no_cpu else cpu_baseline_q4k()
+
+    out = {
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "config 2: Q4_K decode GEMV, up 14336x4096 + down 4096x14336, "
+                               "per-256 activation quantization + GEMV per matrix, weights rotated over "
+                               f">= {ROTATE_BYTES >> 20} MB",
+                   "bytes_per_step": bytes_step, "frac_hbm_step": round(value / HBM_PEAK_GBS, 4),
+                   "wall_s": round(wall, 3)},
+        "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

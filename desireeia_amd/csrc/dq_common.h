@@ -1,0 +1,133 @@
+// dq_common.h - shared device helpers and device-side weight layouts for the
+// gfx950 quantized compute path. Wave64 throughout.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/desireeia_hip.h"
+
+#define DQ_WAVE 64
+
+// GGUF block sizes (reference quant/quant.h:41-187).
+#define DQ_QK 32
+#define DQ_QKK 256
+#define DQ_SZ_Q4_0 18
+#define DQ_SZ_Q8_0 34
+#define DQ_SZ_Q8_1 36
+#define DQ_SZ_Q4_K 144
+#define DQ_SZ_Q6_K 210
+
+// Every on-device weight layout is split into 256-byte-aligned planes inside
+// one allocation so that the streaming kernels issue only 16-byte-aligned
+// global_load_dwordx4. Byte counts per row equal the GGUF row size, so the
+// HBM traffic of a kernel is the GGUF size of the matrix.
+//
+//   Q8_0: plane Q = int8 [rows][cols]            plane D = fp16 [rows][cols/32]
+//   Q4_0: plane Q = [rows][cols/32][16 B nibbles] plane D = fp16 [rows][cols/32]
+//   Q4_K: native GGUF blocks, 144 B per 256 (16-byte aligned as stored)
+//   Q6_K: plane Q = [rows][cols/256][4 items][48 B], item (n,k) = ql bytes
+//         64n+16k..+16, 64n+32+16k..+16, qh bytes 32n+16k..+16 (n = 128-half,
+//         k = 16-lane half); plane S = [rows][cols/256][4 items][4 int8 scales]
+//         with item (n,k) holding scales 8n+k, 8n+2+k, 8n+4+k, 8n+6+k;
+//         plane D = fp16 [rows][cols/256]
+struct DqLayout {
+    size_t q_off, q_row;   // plane Q offset and row stride (bytes)
+    size_t s_off, s_row;   // plane S (Q6_K only)
+    size_t d_off, d_row;   // plane D (fp16 scales)
+    size_t total;
+};
+
+static inline size_t dq_align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static inline bool dq_layout(int fmt, size_t rows, size_t cols, DqLayout* L) {
+    *L = DqLayout{};
+    switch (fmt) {
+    case DQ_FMT_Q8_0:
+        if (cols % 64) return false;
+        L->q_row = cols;
+        L->d_row = cols / 32 * 2;
+        break;
+    case DQ_FMT_Q4_0:
+        if (cols % 64) return false;
+        L->q_row = cols / 2;
+        L->d_row = cols / 32 * 2;
+        break;
+    case DQ_FMT_Q4_K:
+        if (cols % 256) return false;
+        L->q_row = cols / 256 * DQ_SZ_Q4_K;
+        break;
+    case DQ_FMT_Q6_K:
+        if (cols % 256) return false;
+        L->q_row = cols / 256 * 192;
+        L->s_row = cols / 256 * 16;
+        L->d_row = cols / 256 * 2;
+        break;
+    default:
+        return false;
+    }
+    L->q_off = 0;
+    L->s_off = dq_align256(rows * L->q_row);
+    L->d_off = dq_align256(L->s_off + rows * L->s_row);
+    L->total = dq_align256(L->d_off + rows * L->d_row);
+    return true;
+}
+
+static inline size_t dq_gguf_row_bytes(int fmt, size_t cols) {
+    switch (fmt) {
+    case DQ_FMT_Q8_0: return cols / 32 * DQ_SZ_Q8_0;
+    case DQ_FMT_Q4_0: return cols / 32 * DQ_SZ_Q4_0;
+    case DQ_FMT_Q4_K: return cols / 256 * DQ_SZ_Q4_K;
+    case DQ_FMT_Q6_K: return cols / 256 * DQ_SZ_Q6_K;
+    default: return 0;
+    }
+}
+
+// ---------------------------------------------------------------- device --
+
+__device__ __forceinline__ float dq_h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// fp32 -> fp16 bits, round to nearest even (v_cvt_f16_f32).
+__device__ __forceinline__ uint16_t dq_f2h(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ int dq_sdot4(int a, int b, int c) {
+    return __builtin_amdgcn_sdot4(a, b, c, false);
+}
+
+// Bytes v in [0,63] -> v - 32 as signed bytes, without borrows between bytes.
+__device__ __forceinline__ int dq_sub32_bytes(uint32_t v) {
+    return (int)(((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u);
+}
+
+typedef uint32_t dq_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t dq_u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ dq_u32x4 dq_ld16(const void* p) {
+    return *reinterpret_cast<const dq_u32x4*>(p);
+}
+
+// Non-temporal 16-byte load for data streamed exactly once (weights).
+__device__ __forceinline__ dq_u32x4 dq_ld16_stream(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const dq_u32x4*>(p));
+}
+
+// Full-wave float sum; every lane receives the total.
+__device__ __forceinline__ float dq_wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, DQ_WAVE);
+    return v;
+}
+
+__device__ __forceinline__ float dq_wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, DQ_WAVE));
+    return v;
+}
+
+// Host-side status from a HIP error.
+static inline int dq_status(hipError_t e) { return e == hipSuccess ? DQ_OK : DQ_ERR_IO; }
+static inline int dq_launch_status() { return dq_status(hipGetLastError()); }

@@ -1,0 +1,308 @@
+// dq_dequant.hip - GGUF block dequantization (bit-exact with the reference's
+// dequantize_row_*) and the GGUF -> device layout conversion used at upload.
+//
+// Bit-exactness: fp16 -> fp32 is v_cvt_f32_f16 (exact); Q4_K's d1*q - m1 is a
+// multiply then a subtract with two roundings, as quant/quant.cpp:269-270
+// writes it - this file is compiled with -ffp-contract=off, so the compiler
+// does not fuse them. Q6_K is (d*sc)*q (:532-535), Q4_0/Q8_0 one multiply.
+#include "dq_common.h"
+
+namespace {
+
+__device__ __forceinline__ uint16_t rd16(const uint8_t* p) {
+    return (uint16_t)(p[0] | ((uint16_t)p[1] << 8));
+}
+
+// quant/quant.cpp:22-29
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t* q, int* sc, int* mn) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4);
+        *mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// One lane per 32 outputs for every format.
+__global__ __launch_bounds__(256) void dequant_q4_0_kernel(const uint8_t* __restrict__ x, float* __restrict__ y,
+                                                           size_t nb) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const uint8_t* blk = x + b * DQ_SZ_Q4_0;
+    const float d = dq_h2f(rd16(blk));
+    float* o = y + b * 32;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint8_t v = blk[2 + j];
+        o[j] = (float)((v & 0x0F) - 8) * d;
+        o[j + 16] = (float)((v >> 4) - 8) * d;
+    }
+}
+
+__global__ __launch_bounds__(256) void dequant_q8_kernel(const uint8_t* __restrict__ x, float* __restrict__ y,
+                                                         size_t nb, int bsz, int qoff) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const uint8_t* blk = x + b * bsz;
+    const float d = dq_h2f(rd16(blk));
+    float* o = y + b * 32;
+#pragma unroll
+    for (int j = 0; j < 32; ++j) o[j] = (float)(int8_t)blk[qoff + j] * d;
+}
+
+__global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t* __restrict__ x, float* __restrict__ y,
+                                                           size_t n_sub) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_sub) return;
+    const size_t s = t / 8;
+    const int j = (int)(t % 8);
+    const uint8_t* blk = x + s * DQ_SZ_Q4_K;
+    const float d = dq_h2f(rd16(blk));
+    const float dmin = dq_h2f(rd16(blk + 2));
+    int sc, mn;
+    scale_min_k4(j, blk + 4, &sc, &mn);
+    const float d1 = d * (float)sc;
+    const float m1 = dmin * (float)mn;
+    const uint8_t* q = blk + 16 + 32 * (j / 2);
+    const int sh = 4 * (j & 1);
+    float* o = y + t * 32;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) o[l] = d1 * (float)((q[l] >> sh) & 0xF) - m1;
+}
+
+__global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t* __restrict__ x, float* __restrict__ y,
+                                                           size_t n_sub) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_sub) return;
+    const size_t s = t / 8;
+    const int n = (int)((t % 8) / 4);   // 128-half
+    const int qq = (int)(t % 4);        // quarter: outputs l + 32*qq
+    const uint8_t* blk = x + s * DQ_SZ_Q6_K;
+    const uint8_t* ql = blk + 64 * n + ((qq & 1) ? 32 : 0);
+    const uint8_t* qh = blk + 128 + 32 * n;
+    const int8_t* sc = (const int8_t*)(blk + 192 + 8 * n);
+    const float d = dq_h2f(rd16(blk + 208));
+    const int lsh = (qq >= 2) ? 4 : 0;
+    const int hsh = 2 * qq;
+    float* o = y + t * 32;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+        const int q = (int)(((ql[l] >> lsh) & 0xF) | (((qh[l] >> hsh) & 3) << 4)) - 32;
+        o[l] = d * (float)sc[l / 16 + 2 * qq] * (float)q;
+    }
+}
+
+// ---------------------------------------------------------------- packing --
+
+__global__ __launch_bounds__(256) void pack_q8_0_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
+                                                        uint16_t* __restrict__ dp, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const uint8_t* blk = x + b * DQ_SZ_Q8_0;
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        w[i] = (uint32_t)blk[2 + 4 * i] | ((uint32_t)blk[3 + 4 * i] << 8) | ((uint32_t)blk[4 + 4 * i] << 16) |
+               ((uint32_t)blk[5 + 4 * i] << 24);
+    dq_u32x4* o = reinterpret_cast<dq_u32x4*>(qp + b * 32);
+    o[0] = dq_u32x4{w[0], w[1], w[2], w[3]};
+    o[1] = dq_u32x4{w[4], w[5], w[6], w[7]};
+    dp[b] = rd16(blk);
+}
+
+__global__ __launch_bounds__(256) void pack_q4_0_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
+                                                        uint16_t* __restrict__ dp, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const uint8_t* blk = x + b * DQ_SZ_Q4_0;
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)blk[2 + 4 * i] | ((uint32_t)blk[3 + 4 * i] << 8) | ((uint32_t)blk[4 + 4 * i] << 16) |
+               ((uint32_t)blk[5 + 4 * i] << 24);
+    *reinterpret_cast<dq_u32x4*>(qp + b * 16) = dq_u32x4{w[0], w[1], w[2], w[3]};
+    dp[b] = rd16(blk);
+}
+
+__global__ __launch_bounds__(256) void pack_q6_k_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
+                                                        uint8_t* __restrict__ sp, uint16_t* __restrict__ dp,
+                                                        size_t ns) {
+    const size_t s = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= ns) return;
+    const uint8_t* blk = x + s * DQ_SZ_Q6_K;
+    uint8_t* q = qp + s * 192;
+    uint8_t* sc = sp + s * 16;
+    for (int n = 0; n < 2; ++n) {
+        for (int k = 0; k < 2; ++k) {
+            const int it = 2 * n + k;
+            for (int t = 0; t < 16; ++t) {
+                q[it * 48 + t] = blk[64 * n + 16 * k + t];
+                q[it * 48 + 16 + t] = blk[64 * n + 32 + 16 * k + t];
+                q[it * 48 + 32 + t] = blk[128 + 32 * n + 16 * k + t];
+            }
+            for (int qq = 0; qq < 4; ++qq) sc[it * 4 + qq] = blk[192 + 8 * n + k + 2 * qq];
+        }
+    }
+    dp[s] = rd16(blk + 208);
+}
+
+// Dequantization from the device layout (same values as from GGUF blocks).
+__global__ __launch_bounds__(256) void dequant_dev_q8_0_kernel(const uint8_t* __restrict__ qp,
+                                                               const uint16_t* __restrict__ dp,
+                                                               float* __restrict__ y, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const float d = dq_h2f(dp[b]);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) y[b * 32 + j] = (float)(int8_t)qp[b * 32 + j] * d;
+}
+
+__global__ __launch_bounds__(256) void dequant_dev_q4_0_kernel(const uint8_t* __restrict__ qp,
+                                                               const uint16_t* __restrict__ dp,
+                                                               float* __restrict__ y, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const float d = dq_h2f(dp[b]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint8_t v = qp[b * 16 + j];
+        y[b * 32 + j] = (float)((v & 0x0F) - 8) * d;
+        y[b * 32 + j + 16] = (float)((v >> 4) - 8) * d;
+    }
+}
+
+__global__ __launch_bounds__(256) void dequant_dev_q6_k_kernel(const uint8_t* __restrict__ qp,
+                                                               const int8_t* __restrict__ sp,
+                                                               const uint16_t* __restrict__ dp,
+                                                               float* __restrict__ y, size_t n_items) {
+    // one lane per item (n,k): 64 outputs at 128n + 16k + {0..15} + 32*quarter
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_items) return;
+    const size_t s = t / 4;
+    const int it = (int)(t % 4), n = it / 2, k = it % 2;
+    const uint8_t* q = qp + t * 48;
+    const int8_t* sc = sp + t * 4;
+    const float d = dq_h2f(dp[s]);
+    float* o = y + s * 256 + 128 * n + 16 * k;
+    for (int tt = 0; tt < 16; ++tt) {
+        const uint8_t a = q[tt], b = q[16 + tt], h = q[32 + tt];
+        const int q1 = (int)((a & 0xF) | (((h >> 0) & 3) << 4)) - 32;
+        const int q2 = (int)((b & 0xF) | (((h >> 2) & 3) << 4)) - 32;
+        const int q3 = (int)((a >> 4) | (((h >> 4) & 3) << 4)) - 32;
+        const int q4 = (int)((b >> 4) | (((h >> 6) & 3) << 4)) - 32;
+        o[tt] = d * (float)sc[0] * (float)q1;
+        o[tt + 32] = d * (float)sc[1] * (float)q2;
+        o[tt + 64] = d * (float)sc[2] * (float)q3;
+        o[tt + 96] = d * (float)sc[3] * (float)q4;
+    }
+}
+
+inline unsigned grid_for(size_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace
+
+extern "C" int dq_dequantize_row(int type, const void* d_src, float* d_dst, int64_t n, void* stream) {
+    if (n < 0) return DQ_ERR_INVALID_ARG;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t* x = (const uint8_t*)d_src;
+    switch (type) {
+    case DQ_TYPE_Q4_0:
+    case DQ_TYPE_Q8_0:
+    case DQ_TYPE_Q8_1: {
+        if (n % 32) return DQ_ERR_INVALID_ARG;
+        if (n == 0) return DQ_OK;
+        if (!d_src || !d_dst) return DQ_ERR_INVALID_ARG;
+        const size_t nb = (size_t)n / 32;
+        if (type == DQ_TYPE_Q4_0) dequant_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, d_dst, nb);
+        else if (type == DQ_TYPE_Q8_0) dequant_q8_kernel<<<grid_for(nb), 256, 0, s>>>(x, d_dst, nb, DQ_SZ_Q8_0, 2);
+        else dequant_q8_kernel<<<grid_for(nb), 256, 0, s>>>(x, d_dst, nb, DQ_SZ_Q8_1, 4);
+        return dq_launch_status();
+    }
+    case DQ_TYPE_Q4_K:
+    case DQ_TYPE_Q6_K: {
+        if (n % 256) return DQ_ERR_INVALID_ARG;
+        if (n == 0) return DQ_OK;
+        if (!d_src || !d_dst) return DQ_ERR_INVALID_ARG;
+        const size_t nsub = (size_t)n / 32;
+        if (type == DQ_TYPE_Q4_K) dequant_q4_k_kernel<<<grid_for(nsub), 256, 0, s>>>(x, d_dst, nsub);
+        else dequant_q6_k_kernel<<<grid_for(nsub), 256, 0, s>>>(x, d_dst, nsub);
+        return dq_launch_status();
+    }
+    default:
+        return DQ_ERR_NOT_SUPPORTED;
+    }
+}
+
+extern "C" int dq_weights_bytes(int fmt, size_t rows, size_t cols, size_t* bytes) {
+    DqLayout L;
+    if (!bytes) return DQ_ERR_INVALID_ARG;
+    if (!dq_layout(fmt, rows, cols, &L)) return DQ_ERR_NOT_SUPPORTED;
+    *bytes = L.total;
+    return DQ_OK;
+}
+
+extern "C" int dq_weights_pack(int fmt, const void* d_gguf, size_t rows, size_t cols, void* d_dev,
+                               void* stream) {
+    DqLayout L;
+    if (!dq_layout(fmt, rows, cols, &L)) return DQ_ERR_NOT_SUPPORTED;
+    if (!d_gguf || !d_dev) return DQ_ERR_INVALID_ARG;
+    if (rows == 0) return DQ_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t* x = (const uint8_t*)d_gguf;
+    uint8_t* base = (uint8_t*)d_dev;
+    switch (fmt) {
+    case DQ_FMT_Q8_0: {
+        const size_t nb = rows * cols / 32;
+        pack_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, (uint16_t*)(base + L.d_off), nb);
+        break;
+    }
+    case DQ_FMT_Q4_0: {
+        const size_t nb = rows * cols / 32;
+        pack_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, (uint16_t*)(base + L.d_off), nb);
+        break;
+    }
+    case DQ_FMT_Q4_K:
+        return dq_status(hipMemcpyAsync(base, x, rows * L.q_row, hipMemcpyDeviceToDevice, s));
+    case DQ_FMT_Q6_K: {
+        const size_t ns = rows * cols / 256;
+        pack_q6_k_kernel<<<grid_for(ns), 256, 0, s>>>(x, base + L.q_off, base + L.s_off,
+                                                      (uint16_t*)(base + L.d_off), ns);
+        break;
+    }
+    }
+    return dq_launch_status();
+}
+
+extern "C" int dq_weights_dequantize(int fmt, const void* d_dev, size_t rows, size_t cols, float* d_out,
+                                     void* stream) {
+    DqLayout L;
+    if (!dq_layout(fmt, rows, cols, &L)) return DQ_ERR_NOT_SUPPORTED;
+    if (!d_dev || !d_out) return DQ_ERR_INVALID_ARG;
+    if (rows == 0) return DQ_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t* base = (const uint8_t*)d_dev;
+    switch (fmt) {
+    case DQ_FMT_Q8_0: {
+        const size_t nb = rows * cols / 32;
+        dequant_dev_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, (const uint16_t*)(base + L.d_off),
+                                                             d_out, nb);
+        break;
+    }
+    case DQ_FMT_Q4_0: {
+        const size_t nb = rows * cols / 32;
+        dequant_dev_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, (const uint16_t*)(base + L.d_off),
+                                                             d_out, nb);
+        break;
+    }
+    case DQ_FMT_Q4_K:
+        return dq_dequantize_row(DQ_TYPE_Q4_K, d_dev, d_out, (int64_t)(rows * cols), stream);
+    case DQ_FMT_Q6_K: {
+        const size_t ni = rows * cols / 64;
+        dequant_dev_q6_k_kernel<<<grid_for(ni), 256, 0, s>>>(base + L.q_off, (const int8_t*)(base + L.s_off),
+                                                             (const uint16_t*)(base + L.d_off), d_out, ni);
+        break;
+    }
+    }
+    return dq_launch_status();
+}

@@ -1,0 +1,136 @@
+"""Host-side mirror of the reference's operator interface for the quantized
+path, over torch device tensors. torch only provides device memory and the
+current stream; every computation is a call into libdesireeia_hip.so.
+
+Names follow the reference operators (src/DesireeIA.LocaleEngine/):
+  dequantize_row      quant/quant.cpp:912   desireeia_dequantize_row
+  quantize_q8_0       core/quant.cpp:15     (per-32 activation quantizer)
+  quantize_act_q8k_rep core/matmul.cpp:1660 (per-256, replicated per 32)
+  matmul_q8_0/q4_0/q4_k/q6_k  core/matmul.cpp:294-417, :2008, :2569
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from .synth import BLOCK, FMT_OF_TYPE, Q4_0, Q4_K, Q6_K, Q8_0, TYPE_OF_FMT
+
+ACT_Q8_0, ACT_Q8K_REP = 0, 1
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _dev(t, device="cuda"):
+    if isinstance(t, torch.Tensor):
+        return t.to(device)
+    return torch.from_numpy(t).to(device)
+
+
+def dequantize_row(qtype, src, n):
+    """GGUF blocks (uint8 device tensor) -> n fp32 values, bit-exact."""
+    lib = _lib.load()
+    out = torch.empty(n, dtype=torch.float32, device=src.device)
+    _lib.check(lib.dq_dequantize_row(qtype, _ptr(src), _ptr(out), n, _stream()), "dq_dequantize_row")
+    return out
+
+
+class Activation:
+    """Quantized activation triple (q int8, scale per 32, isum per 32, fsum per 32)."""
+
+    def __init__(self, q, scale, isum, fsum, kind):
+        self.q, self.scale, self.isum, self.fsum, self.kind = q, scale, isum, fsum, kind
+
+
+def quantize_act(x, kind=ACT_Q8_0):
+    """x: fp32 [n_tok, cols] or [cols] device tensor."""
+    lib = _lib.load()
+    x = x.contiguous()
+    cols = x.shape[-1]
+    n_tok = x.numel() // cols
+    nb = cols // 32
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    scale = torch.empty(x.shape[:-1] + (nb,), dtype=torch.float32, device=x.device)
+    isum = torch.empty(x.shape[:-1] + (nb,), dtype=torch.int32, device=x.device)
+    fsum = torch.empty(x.shape[:-1] + (nb,), dtype=torch.float32, device=x.device)
+    _lib.check(lib.dq_quantize_act(kind, _ptr(x), cols, n_tok, _ptr(q), _ptr(scale), _ptr(isum), _ptr(fsum),
+                                   _stream()), "dq_quantize_act")
+    return Activation(q, scale, isum, fsum, kind)
+
+
+def quantize_q8_0(x):
+    return quantize_act(x, ACT_Q8_0)
+
+
+def quantize_act_q8k_rep(x):
+    return quantize_act(x, ACT_Q8K_REP)
+
+
+def quantize_q8_1_blocks(x):
+    """GGUF block_q8_1 bytes of a flat fp32 device tensor."""
+    lib = _lib.load()
+    x = x.contiguous()
+    out = torch.empty(x.numel() // 32 * 36, dtype=torch.uint8, device=x.device)
+    _lib.check(lib.dq_quantize_q8_1_blocks(_ptr(x), x.numel(), _ptr(out), _stream()), "dq_quantize_q8_1_blocks")
+    return out
+
+
+class QuantMatrix:
+    """A rows x cols quantized matrix in the on-device layout (cuda_upload_weights)."""
+
+    def __init__(self, fmt, rows, cols, buf):
+        self.fmt, self.rows, self.cols, self.buf = fmt, rows, cols, buf
+
+    @property
+    def qtype(self):
+        return TYPE_OF_FMT[self.fmt]
+
+    @staticmethod
+    def nbytes(fmt, rows, cols):
+        lib = _lib.load()
+        n = ctypes.c_size_t(0)
+        _lib.check(lib.dq_weights_bytes(fmt, rows, cols, ctypes.byref(n)), "dq_weights_bytes")
+        return n.value
+
+    @classmethod
+    def from_gguf(cls, qtype, gguf, rows, cols, device="cuda"):
+        """gguf: GGUF row bytes (numpy or tensor, rows*row_bytes uint8)."""
+        lib = _lib.load()
+        fmt = FMT_OF_TYPE[qtype]
+        src = _dev(gguf, device).reshape(-1).contiguous()
+        buf = torch.empty(cls.nbytes(fmt, rows, cols), dtype=torch.uint8, device=device)
+        _lib.check(lib.dq_weights_pack(fmt, _ptr(src), rows, cols, _ptr(buf), _stream()), "dq_weights_pack")
+        return cls(fmt, rows, cols, buf)
+
+    def clone(self):
+        return QuantMatrix(self.fmt, self.rows, self.cols, self.buf.clone())
+
+    def dequantize(self):
+        lib = _lib.load()
+        out = torch.empty(self.rows, self.cols, dtype=torch.float32, device=self.buf.device)
+        _lib.check(lib.dq_weights_dequantize(self.fmt, _ptr(self.buf), self.rows, self.cols, _ptr(out), _stream()),
+                   "dq_weights_dequantize")
+        return out
+
+
+def act_kind_for(fmt):
+    """The activation quantizer of the reference CPU GEMV for this format."""
+    return ACT_Q8_0 if fmt in (FMT_OF_TYPE[Q8_0], FMT_OF_TYPE[Q4_0]) else ACT_Q8K_REP
+
+
+def gemv(mat, act, out=None):
+    lib = _lib.load()
+    y = out if out is not None else torch.empty(mat.rows, dtype=torch.float32, device=mat.buf.device)
+    _lib.check(lib.dq_gemv(mat.fmt, _ptr(mat.buf), mat.rows, mat.cols, _ptr(act.q), _ptr(act.scale),
+                           _ptr(act.isum), _ptr(y), _stream()), "dq_gemv")
+    return y
+
+
+def matmul(mat, x):
+    """y = W x with the semantics of the reference's matmul_<fmt> (batch 1)."""
+    return gemv(mat, quantize_act(x, act_kind_for(mat.fmt)))

@@ -1,0 +1,98 @@
+/*
+ * desireeia_hip.h - C ABI of the MI355X (gfx950) quantized compute path.
+ *
+ * Two layers, both plain C (extern "C", pointers and sizes, no torch or C++
+ * types), all returning a desireeia_error code (0 = OK, -1 invalid argument,
+ * -2 not supported: shape/format not covered, nothing was done, -3 device
+ * failure). Reference paths are relative to src/DesireeIA.LocaleEngine/.
+ *
+ * 1. Kernel layer (dq_*): device pointers, stream-ordered, asynchronous, no
+ *    allocation. `stream` is a hipStream_t (NULL = the default stream).
+ *
+ * 2. Engine layer: the GPU operator entry points the reference engine's model
+ *    code calls (core/engine.h:502-811, compiled there under
+ *    DESIREEIA_CUDA_ENABLED), same names, argument meaning and error
+ *    behaviour, with host pointers for x/y and one synchronisation per call.
+ *    See INTEGRATION.md for the C++ shim the engine would link.
+ */
+#ifndef DESIREEIA_HIP_H
+#define DESIREEIA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: the values of desireeia_error (include/desireeia/abi.h:113-122). */
+#define DQ_OK 0
+#define DQ_ERR_INVALID_ARG (-1)
+#define DQ_ERR_NOT_SUPPORTED (-2)
+#define DQ_ERR_IO (-3)
+
+/* Device weight formats: the values of DESIREEIA_CUDA_FMT_* (core/engine.h:521-527),
+ * with 0 = Q8_0 as the reference backend uses it (core/engine.h:726). */
+#define DQ_FMT_Q8_0 0
+#define DQ_FMT_Q4_0 1
+#define DQ_FMT_Q4_K 5
+#define DQ_FMT_Q6_K 7
+
+/* GGUF type ids for dq_dequantize_row (quant/quant.h:439-476). */
+#define DQ_TYPE_Q4_0 2
+#define DQ_TYPE_Q8_0 8
+#define DQ_TYPE_Q8_1 9
+#define DQ_TYPE_Q4_K 12
+#define DQ_TYPE_Q6_K 14
+
+/* Activation quantizers for dq_quantize_act. */
+#define DQ_ACT_Q8_0 0   /* one scale per 32: core/quant.cpp:15-50 (quantize_q8_0) */
+#define DQ_ACT_Q8K_REP 1 /* one scale per 256, replicated per 32: core/matmul.cpp:1660-1778 */
+
+/* ------------------------------------------------------------ kernel layer */
+
+/* Library version / device query. dq_device_name writes at most len bytes. */
+int dq_version(void);
+int dq_device_count(void);
+
+/* Replaces desireeia_dequantize_row (quant/quant.cpp:912-984) for the on-path
+ * types Q4_0, Q8_0, Q8_1, Q4_K, Q6_K: GGUF blocks in, n fp32 values out,
+ * bit-exact. n must be a multiple of the block size. Other types: -2. */
+int dq_dequantize_row(int type, const void* d_src, float* d_dst, int64_t n, void* stream);
+
+/* Size of the on-device layout of a rows x cols matrix of format fmt, and the
+ * on-device conversion from GGUF rows (the layout cuda_upload_weights owns,
+ * backend_cuda.cu:2910-2923, 3024-3107). d_gguf and d_dev must not overlap. */
+int dq_weights_bytes(int fmt, size_t rows, size_t cols, size_t* bytes);
+int dq_weights_pack(int fmt, const void* d_gguf, size_t rows, size_t cols, void* d_dev,
+                    void* stream);
+/* Dequantizes a packed device matrix to fp32 [rows][cols]; the values are
+ * bit-identical to desireeia_dequantize_row on the GGUF rows. */
+int dq_weights_dequantize(int fmt, const void* d_dev, size_t rows, size_t cols, float* d_out,
+                          void* stream);
+
+/* Activation quantization of n_tok rows of cols floats (cols % 32 == 0; %256
+ * for DQ_ACT_Q8K_REP). Outputs: q int8 [n_tok][cols], scale float
+ * [n_tok][cols/32], isum int32 [n_tok][cols/32] (sum of the 32 q), fsum float
+ * [n_tok][cols/32] (sequential float sum of the 32 inputs, the min-term input
+ * of the prefill GEMM, core/i8gemm_impl.h:50-82). isum/fsum may be NULL.
+ * The integers and scales are bit-identical to the reference quantizer. */
+int dq_quantize_act(int kind, const float* d_x, size_t cols, size_t n_tok, int8_t* d_q,
+                    float* d_scale, int32_t* d_isum, float* d_fsum, void* stream);
+
+/* GGUF block_q8_1 form (quant/quant.h:105-116): fp16 d, fp16 s = d * sum(q),
+ * 32 int8, for n floats (n % 32 == 0), per-32 quantize_q8_0 integers. */
+int dq_quantize_q8_1_blocks(const float* d_x, size_t n, void* d_blocks, void* stream);
+
+/* Batch-1 GEMV y[rows] = W x on a packed device matrix, x given as the
+ * activation triple of dq_quantize_act (DQ_ACT_Q8_0 for Q8_0/Q4_0 - the
+ * semantics of matmul_q8_0/matmul_q4_0, core/matmul.cpp:294-417; DQ_ACT_Q8K_REP
+ * for Q4_K/Q6_K - matmul_q4_k_pq/matmul_q6_k_pq, :2023-2027, :2580-2584).
+ * d_xsum is required for Q4_0 and Q4_K. */
+int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
+            const float* d_xscale, const int32_t* d_xsum, float* d_y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,98 @@
+// ref_shim.cpp - C entry points into the reference engine's own CPU code,
+// compiled from the reference sources where they lie (see Makefile, target
+// `ref`). TEST INFRASTRUCTURE: the resulting oracle/_ref library is used only
+// to validate the restatement in dq_oracle.c and as the "reference" CPU
+// baseline timed by bench.py. It is never linked into the HIP library.
+//
+// Each wrapper forwards to one reference function (paths relative to
+// src/DesireeIA.LocaleEngine/):
+//   desireeia_dequantize_row ...... quant/quant.cpp:912
+//   desireeia_fp16<->fp32 ......... quant/quant.h:285-323
+//   quantize_q8_0 ................. core/quant.cpp:15
+//   quantize_act_q8k_rep .......... core/matmul.cpp:1660
+//   matmul_q8_0/q4_0/q4_k/q6_k .... core/matmul.cpp:294,343,2008,2569
+//   matmul_*_batch ................ core/matmul.cpp:2090-2125, :848-860
+//   kv_quantize_row/dot/axpy ...... kv/kv_quant.cpp:31,58,102
+//   moe_route ..................... models/moe_route.cpp:77
+//   ThreadPool::set_thread_override core/thread_pool.cpp:36
+#include "core/engine.h"
+#include "core/i8gemm.h"
+#include "core/thread_pool.h"
+#include "kv/kv_quant.h"
+#include "models/moe_route.h"
+#include "quant/quant.h"
+
+#include <cstring>
+#include <vector>
+
+using namespace desireeia;
+
+extern "C" {
+
+void dqr_set_threads(int n) { ThreadPool::set_thread_override(n); }
+int dqr_threads() { return (int)ThreadPool::global().worker_count(); }
+const char* dqr_i8_isa() { return i8_gemm_isa(); }
+
+float dqr_fp16_to_fp32(uint16_t h) { return desireeia_fp16_to_fp32(h); }
+uint16_t dqr_fp32_to_fp16(float f) { return desireeia_fp32_to_fp16(f); }
+
+int dqr_dequantize_row(int type, const void* src, float* dst, int64_t n) {
+    return desireeia_dequantize_row(type, src, dst, n);
+}
+
+void dqr_quantize_q8_0(const float* x, size_t n, int8_t* q, float* d) {
+    std::vector<int8_t> vq;
+    std::vector<float> vd;
+    std::vector<uint8_t> signs;
+    quantize_q8_0(x, n, vq, vd, signs);
+    std::memcpy(q, vq.data(), n);
+    std::memcpy(d, vd.data(), vd.size() * sizeof(float));
+}
+
+void dqr_quantize_q8k_rep(const float* x, size_t n, int8_t* q, float* d32, int32_t* isum32) {
+    std::vector<int8_t> vq;
+    std::vector<float> vd;
+    std::vector<int32_t> vs;
+    quantize_act_q8k_rep(x, n, vq, vd, vs);
+    std::memcpy(q, vq.data(), n);
+    std::memcpy(d32, vd.data(), vd.size() * sizeof(float));
+    std::memcpy(isum32, vs.data(), vs.size() * sizeof(int32_t));
+}
+
+int dqr_matmul(int type, const uint8_t* w, size_t rows, size_t cols, const float* x, float* y) {
+    switch (type) {
+    case 2: return matmul_q4_0(w, rows, cols, x, y);
+    case 8: return matmul_q8_0(w, rows, cols, x, y);
+    case 12: return matmul_q4_k(w, rows, cols, x, y);
+    case 14: return matmul_q6_k(w, rows, cols, x, y);
+    default: return DESIREEIA_ERR_NOT_SUPPORTED;
+    }
+}
+
+int dqr_matmul_batch(int type, const uint8_t* w, size_t rows, size_t cols, const float* x,
+                     size_t n_tok, float* y) {
+    switch (type) {
+    case 2: return matmul_q4_0_batch(w, rows, cols, x, n_tok, y);
+    case 8: return matmul_q8_0_batch(w, rows, cols, x, n_tok, y);
+    case 12: return matmul_q4_k_batch(w, rows, cols, x, n_tok, y);
+    case 14: return matmul_q6_k_batch(w, rows, cols, x, n_tok, y);
+    default: return DESIREEIA_ERR_NOT_SUPPORTED;
+    }
+}
+
+void dqr_kv_quantize_row(const float* x, size_t dim, uint8_t* out) { kv_quantize_row(x, dim, out); }
+float dqr_kv_dot_q8_0(const float* q, const uint8_t* row, size_t dim) { return kv_dot_q8_0(q, row, dim); }
+void dqr_kv_axpy_q8_0(float* y, const uint8_t* row, size_t dim, float w) { kv_axpy_q8_0(y, row, dim, w); }
+
+uint32_t dqr_moe_route(const float* logits, uint32_t n, uint32_t k, int norm_w, float w_scale,
+                       uint32_t* ids, float* wts) {
+    std::vector<float> l(logits, logits + n);
+    auto sel = moe_route(l, k, norm_w != 0, w_scale);
+    for (size_t i = 0; i < sel.size(); ++i) {
+        ids[i] = sel[i].first;
+        wts[i] = sel[i].second;
+    }
+    return (uint32_t)sel.size();
+}
+
+}  // extern "C"

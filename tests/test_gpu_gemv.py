@@ -1,0 +1,67 @@
+"""Batch-1 decode GEMV on the GPU against the oracle (reference CPU GEMV
+semantics, activation quantized the same way): norm-wise relative error
+<= 1e-3 (the fp32-accumulated GEMV tolerance), at the benchmark shapes and at
+ragged edge shapes."""
+import numpy as np
+import pytest
+import torch
+
+from desireeia_amd import _lib, ops, synth
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+CASES = [
+    (synth.Q8_0, 4096, 4096),      # config 1
+    (synth.Q4_0, 14336, 4096),     # config 2 up/gate
+    (synth.Q4_0, 4096, 14336),     # config 2 down
+    (synth.Q4_K, 14336, 4096),
+    (synth.Q4_K, 4096, 14336),
+    (synth.Q6_K, 1024, 4096),      # config 4 wv
+    (synth.Q6_K, 4096, 14336),     # config 4 down
+    (synth.Q8_0, 5, 64),           # ragged: rows not a multiple of the rows per wave
+    (synth.Q4_0, 3, 128),
+    (synth.Q4_K, 7, 256),
+    (synth.Q6_K, 9, 768),
+    (synth.Q4_K, 1, 32768),        # 8 items per lane
+    (synth.Q8_0, 333, 4160),       # items not a multiple of 64
+]
+
+
+def rel(a, b):
+    return float(np.linalg.norm(a.astype(np.float64) - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.mark.parametrize("qtype,rows,cols", CASES)
+def test_gemv_vs_oracle(gpu, orc, qtype, rows, cols):
+    print(f"gemv type={qtype} rows={rows} cols={cols}", flush=True)
+    w = synth.gen_weights(qtype, rows, cols, seed=rows * 3 + cols)
+    x = synth.gen_act(cols, seed=cols + 1)
+    m = ops.QuantMatrix.from_gguf(qtype, w, rows, cols)
+    y = ops.matmul(m, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = orc.matmul(qtype, w, rows, cols, x)
+    e = rel(y, want)
+    print(f"  rel err {e:.3e}")
+    assert e <= TOL
+    # per-row: no row may be wrong even if the norm hides it
+    scale = np.abs(want).max()
+    assert np.max(np.abs(y - want)) <= 1e-3 * scale
+
+
+def test_gemv_repeat_and_two_sizes(gpu, orc):
+    """Two matrices of different shape in a row give the same answers as alone."""
+    outs = []
+    for rows, cols in [(4096, 14336), (64, 512), (4096, 14336)]:
+        w = synth.gen_weights(synth.Q4_K, rows, cols, seed=5)
+        x = synth.gen_act(cols, seed=6)
+        m = ops.QuantMatrix.from_gguf(synth.Q4_K, w, rows, cols)
+        outs.append(ops.matmul(m, torch.from_numpy(x).to(gpu)).cpu().numpy())
+    assert np.array_equal(outs[0], outs[2])
+
+
+def test_gemv_unsupported_shapes(gpu):
+    lib = _lib.load()
+    assert lib.dq_gemv(synth.FMT_Q4_K, None, 4, 100, None, None, None, None, None) == -2
+    assert lib.dq_gemv(synth.FMT_Q8_0, None, 4, 96, None, None, None, None, None) == -2
+    assert lib.dq_gemv(9, None, 4, 256, None, None, None, None, None) == -2
+    assert lib.dq_gemv(synth.FMT_Q8_0, None, 0, 256, None, None, None, None, None) == 0
