@@ -12,7 +12,8 @@ GEMV, each with its kernel-only bandwidth.
 
 `roofline` is the dominant kernel (Q4_K GEMV, up shape): algorithmic bytes per
 launch / average launch duration, from HIP events around back-to-back launches
-on the stream the kernels run on. `cpu_baseline` times the reference engine's
+on the stream the kernels run on, captured in a HIP graph so host launch
+overhead is not counted. `cpu_baseline` times the reference engine's
 own matmul_q4_k (oracle/_ref, compiled from the reference sources) on the
 host, over a bounded sample.
 
@@ -71,7 +72,7 @@ class GemvCase:
         from desireeia_amd import ops
         m = self.mats[self.i]
         self.i = (self.i + 1) % len(self.mats)
-        ops.gemv(m, ops.quantize_act(self.x, self.kind), out=self.y)
+        ops.gemv(m, ops.quantize_act(self.x, self.kind, out=self.act), out=self.y)
 
     def kernel(self):
         from desireeia_amd import ops
@@ -80,23 +81,33 @@ class GemvCase:
         ops.gemv(m, self.act, out=self.y)
 
 
-def time_loop(fn, n, warmup):
+def graph_time(fn, calls_per_graph, reps, warmup_reps=2):
+    """Captures calls_per_graph calls of fn into one HIP graph and times `reps`
+    replays with HIP events on the capturing stream. Returns us per call."""
     import torch
-    for _ in range(warmup):
-        fn()
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls_per_graph):
+            fn()
+    for _ in range(warmup_reps):
+        g.replay()
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for _ in range(n):
-        fn()
+    for _ in range(reps):
+        g.replay()
     e.record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / n * 1e3  # us per call
+    return s.elapsed_time(e) / (reps * calls_per_graph) * 1e3
 
 
-def kernel_stats(case, n=400):
-    """Average GEMV launch duration (us) over back-to-back launches."""
-    us = time_loop(case.kernel, n, warmup=20)
+def kernel_stats(case, launches=400):
+    """Average GEMV launch duration (us): graph of back-to-back launches over
+    the rotated weight copies."""
+    per = 2 * len(case.mats)
+    us = graph_time(case.kernel, per, max(1, launches // per))
     b = gemv_kernel_bytes(case.qtype, case.rows, case.cols)
     return us, b / us / 1e3  # GB/s
 
@@ -165,10 +176,20 @@ def main():
         "q80": (synth.Q8_0, 4096, 4096),
         "q6k_down": (synth.Q6_K, 4096, 14336),
     }
+    if args.only == "copy":
+        # plain device copy of a known size: the calibration kernel for the
+        # FETCH_SIZE / WRITE_SIZE counters (33,030,144 bytes read and written)
+        src = torch.empty(33030144, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy: {args.steps} x {src.numel()} bytes")
+        return
     if args.only:
         qt, r, c = shapes[args.only]
         case = GemvCase(qt, r, c, 11, dev)
-        us, gbs = kernel_stats(case, n=args.steps)
+        us, gbs = kernel_stats(case, launches=args.steps)
         log(f"{args.only}: {us:.2f} us/launch, {gbs:.1f} GB/s")
         return
 
@@ -181,18 +202,16 @@ def main():
         up.step()
         down.step()
 
+    per_graph = max(len(up.mats), len(down.mats))
+    reps = max(1, args.steps // per_graph)
+    n_steps = reps * per_graph
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(args.steps):
-        step()
-    ev1.record()
-    torch.cuda.synchronize()
+    us_step = graph_time(step, per_graph, reps, warmup_reps=1)
     wall = time.perf_counter() - t0
-    ms_per_step = ev0.elapsed_time(ev1) / args.steps
+    ms_per_step = us_step / 1e3
     bytes_step = step_bytes(synth.Q4_K, 14336, 4096) + step_bytes(synth.Q4_K, 4096, 14336)
     value = bytes_step / (ms_per_step * 1e-3) / 1e9
 
@@ -212,7 +231,7 @@ def main():
     cpu = None if args.no_cpu else cpu_baseline_q4k()
 
     out = {
-        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": n_steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "config 2: Q4_K decode GEMV, up 14336x4096 + down 4096x14336, "

@@ -19,22 +19,32 @@
 #define DQ_SZ_Q6_K 210
 
 // Every on-device weight layout is split into 256-byte-aligned planes inside
-// one allocation so that the streaming kernels issue only 16-byte-aligned
-// global_load_dwordx4. Byte counts per row equal the GGUF row size, so the
-// HBM traffic of a kernel is the GGUF size of the matrix.
+// one allocation. A row is cut into items of 64 weights (cols/64 per row);
+// the quant bytes of an item are split over NP "sub-planes" of 16 bytes per
+// item, each sub-plane item-major ([rows][items][16 B]). A wave whose lane l
+// reads item 64j+l of a sub-plane thus issues one contiguous kilobyte per
+// global_load_dwordx4. Byte counts per row equal the GGUF row size, so the HBM
+// traffic of a kernel is the GGUF size of the matrix.
 //
-//   Q8_0: plane Q = int8 [rows][cols]            plane D = fp16 [rows][cols/32]
-//   Q4_0: plane Q = [rows][cols/32][16 B nibbles] plane D = fp16 [rows][cols/32]
-//   Q4_K: native GGUF blocks, 144 B per 256 (16-byte aligned as stored)
-//   Q6_K: plane Q = [rows][cols/256][4 items][48 B], item (n,k) = ql bytes
-//         64n+16k..+16, 64n+32+16k..+16, qh bytes 32n+16k..+16 (n = 128-half,
-//         k = 16-lane half); plane S = [rows][cols/256][4 items][4 int8 scales]
-//         with item (n,k) holding scales 8n+k, 8n+2+k, 8n+4+k, 8n+6+k;
-//         plane D = fp16 [rows][cols/256]
+//   Q8_0 (NP 4): sub-plane k of item i = int8 weights 64i+16k..+16
+//         D = fp16 [rows][cols/32] (item i: the scales of blocks 2i, 2i+1)
+//   Q4_0 (NP 2): sub-plane k of item i = the 16 nibble bytes of block 2i+k
+//         D = fp16 [rows][cols/32]
+//   Q4_K (NP 2): item i = (block s = i/4, group g = i%4); sub-plane k = qs bytes
+//         32g+16k..+16 of block s (positions 16k..16k+15 of sub-block 2g in the
+//         low nibbles and of sub-block 2g+1 in the high nibbles)
+//         H = [rows][cols/256][16 B]: bytes 0..15 of each block (d, dmin, scales)
+//   Q6_K (NP 3): item i = (block s = i/4, it = i%4 = 2n+k), n = 128-half,
+//         k = 16-position half; sub-plane 0 = ql bytes 64n+16k..+16, 1 = ql bytes
+//         64n+32+16k..+16, 2 = qh bytes 32n+16k..+16
+//         S = [rows][cols/256][4 items][4 int8]: scales 8n+k, 8n+2+k, 8n+4+k, 8n+6+k
+//         D = fp16 [rows][cols/256]
 struct DqLayout {
-    size_t q_off, q_row;   // plane Q offset and row stride (bytes)
-    size_t s_off, s_row;   // plane S (Q6_K only)
-    size_t d_off, d_row;   // plane D (fp16 scales)
+    int np;                // number of quant sub-planes
+    size_t q_off, q_row;   // sub-plane 0 offset, row stride of a sub-plane (items*16)
+    size_t p_stride;       // distance between sub-planes
+    size_t s_off, s_row;   // Q4_K header plane H, or Q6_K scale plane S
+    size_t d_off, d_row;   // fp16 scale plane D
     size_t total;
 };
 
@@ -45,29 +55,32 @@ static inline bool dq_layout(int fmt, size_t rows, size_t cols, DqLayout* L) {
     switch (fmt) {
     case DQ_FMT_Q8_0:
         if (cols % 64) return false;
-        L->q_row = cols;
+        L->np = 4;
         L->d_row = cols / 32 * 2;
         break;
     case DQ_FMT_Q4_0:
         if (cols % 64) return false;
-        L->q_row = cols / 2;
+        L->np = 2;
         L->d_row = cols / 32 * 2;
         break;
     case DQ_FMT_Q4_K:
         if (cols % 256) return false;
-        L->q_row = cols / 256 * DQ_SZ_Q4_K;
+        L->np = 2;
+        L->s_row = cols / 256 * 16;
         break;
     case DQ_FMT_Q6_K:
         if (cols % 256) return false;
-        L->q_row = cols / 256 * 192;
+        L->np = 3;
         L->s_row = cols / 256 * 16;
         L->d_row = cols / 256 * 2;
         break;
     default:
         return false;
     }
+    L->q_row = cols / 64 * 16;
     L->q_off = 0;
-    L->s_off = dq_align256(rows * L->q_row);
+    L->p_stride = dq_align256(rows * L->q_row);
+    L->s_off = L->p_stride * (size_t)L->np;
     L->d_off = dq_align256(L->s_off + rows * L->s_row);
     L->total = dq_align256(L->d_off + rows * L->d_row);
     return true;

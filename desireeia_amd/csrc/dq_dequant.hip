@@ -94,85 +94,124 @@ __global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t* __rest
 }
 
 // ---------------------------------------------------------------- packing --
+// Layouts: see dq_common.h. `ps` is the distance between quant sub-planes.
+
+__device__ __forceinline__ dq_u32x4 ld16_bytes(const uint8_t* src) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w[i] = (uint32_t)src[4 * i] | ((uint32_t)src[4 * i + 1] << 8) | ((uint32_t)src[4 * i + 2] << 16) |
+               ((uint32_t)src[4 * i + 3] << 24);
+    return dq_u32x4{w[0], w[1], w[2], w[3]};
+}
 
 __global__ __launch_bounds__(256) void pack_q8_0_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
-                                                        uint16_t* __restrict__ dp, size_t nb) {
+                                                        size_t ps, uint16_t* __restrict__ dp, size_t nb) {
+    // one lane per block b: its halves go to sub-planes 2(b%2), 2(b%2)+1 of item b/2
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nb) return;
     const uint8_t* blk = x + b * DQ_SZ_Q8_0;
-    uint32_t w[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-        w[i] = (uint32_t)blk[2 + 4 * i] | ((uint32_t)blk[3 + 4 * i] << 8) | ((uint32_t)blk[4 + 4 * i] << 16) |
-               ((uint32_t)blk[5 + 4 * i] << 24);
-    dq_u32x4* o = reinterpret_cast<dq_u32x4*>(qp + b * 32);
-    o[0] = dq_u32x4{w[0], w[1], w[2], w[3]};
-    o[1] = dq_u32x4{w[4], w[5], w[6], w[7]};
+    const size_t o = 16 * (b / 2), k = 2 * (b % 2);
+    *reinterpret_cast<dq_u32x4*>(qp + k * ps + o) = ld16_bytes(blk + 2);
+    *reinterpret_cast<dq_u32x4*>(qp + (k + 1) * ps + o) = ld16_bytes(blk + 18);
     dp[b] = rd16(blk);
 }
 
 __global__ __launch_bounds__(256) void pack_q4_0_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
-                                                        uint16_t* __restrict__ dp, size_t nb) {
+                                                        size_t ps, uint16_t* __restrict__ dp, size_t nb) {
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nb) return;
     const uint8_t* blk = x + b * DQ_SZ_Q4_0;
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        w[i] = (uint32_t)blk[2 + 4 * i] | ((uint32_t)blk[3 + 4 * i] << 8) | ((uint32_t)blk[4 + 4 * i] << 16) |
-               ((uint32_t)blk[5 + 4 * i] << 24);
-    *reinterpret_cast<dq_u32x4*>(qp + b * 16) = dq_u32x4{w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<dq_u32x4*>(qp + (b % 2) * ps + 16 * (b / 2)) = ld16_bytes(blk + 2);
     dp[b] = rd16(blk);
 }
 
-__global__ __launch_bounds__(256) void pack_q6_k_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
-                                                        uint8_t* __restrict__ sp, uint16_t* __restrict__ dp,
-                                                        size_t ns) {
-    const size_t s = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= ns) return;
-    const uint8_t* blk = x + s * DQ_SZ_Q6_K;
-    uint8_t* q = qp + s * 192;
-    uint8_t* sc = sp + s * 16;
-    for (int n = 0; n < 2; ++n) {
-        for (int k = 0; k < 2; ++k) {
-            const int it = 2 * n + k;
-            for (int t = 0; t < 16; ++t) {
-                q[it * 48 + t] = blk[64 * n + 16 * k + t];
-                q[it * 48 + 16 + t] = blk[64 * n + 32 + 16 * k + t];
-                q[it * 48 + 32 + t] = blk[128 + 32 * n + 16 * k + t];
-            }
-            for (int qq = 0; qq < 4; ++qq) sc[it * 4 + qq] = blk[192 + 8 * n + k + 2 * qq];
-        }
+__global__ __launch_bounds__(256) void pack_q4_k_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
+                                                        size_t ps, uint8_t* __restrict__ hp, size_t ns) {
+    // one lane per 16-byte piece: 9 pieces per block (header + 8 qs pieces)
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= ns * 9) return;
+    const size_t s = t / 9;
+    const int p = (int)(t % 9);
+    const dq_u32x4 v = ld16_bytes(x + s * DQ_SZ_Q4_K + 16 * p);
+    if (p == 0) {
+        *reinterpret_cast<dq_u32x4*>(hp + s * 16) = v;
+    } else {
+        const int q = p - 1, g = q / 2, k = q % 2;
+        *reinterpret_cast<dq_u32x4*>(qp + (size_t)k * ps + 64 * s + 16 * g) = v;
     }
-    dp[s] = rd16(blk + 208);
+}
+
+__global__ __launch_bounds__(256) void pack_q6_k_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
+                                                        size_t ps, uint8_t* __restrict__ sp,
+                                                        uint16_t* __restrict__ dp, size_t ns) {
+    // one lane per item t = 4s + it, it = 2n + k
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= ns * 4) return;
+    const size_t s = t / 4;
+    const int it = (int)(t % 4), n = it / 2, k = it % 2;
+    const uint8_t* blk = x + s * DQ_SZ_Q6_K;
+    *reinterpret_cast<dq_u32x4*>(qp + 16 * t) = ld16_bytes(blk + 64 * n + 16 * k);
+    *reinterpret_cast<dq_u32x4*>(qp + ps + 16 * t) = ld16_bytes(blk + 64 * n + 32 + 16 * k);
+    *reinterpret_cast<dq_u32x4*>(qp + 2 * ps + 16 * t) = ld16_bytes(blk + 128 + 32 * n + 16 * k);
+    for (int qq = 0; qq < 4; ++qq) sp[t * 4 + qq] = blk[192 + 8 * n + k + 2 * qq];
+    if (it == 0) dp[s] = rd16(blk + 208);
 }
 
 // Dequantization from the device layout (same values as from GGUF blocks).
-__global__ __launch_bounds__(256) void dequant_dev_q8_0_kernel(const uint8_t* __restrict__ qp,
+__global__ __launch_bounds__(256) void dequant_dev_q8_0_kernel(const uint8_t* __restrict__ qp, size_t ps,
                                                                const uint16_t* __restrict__ dp,
                                                                float* __restrict__ y, size_t nb) {
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nb) return;
     const float d = dq_h2f(dp[b]);
-#pragma unroll
-    for (int j = 0; j < 32; ++j) y[b * 32 + j] = (float)(int8_t)qp[b * 32 + j] * d;
-}
-
-__global__ __launch_bounds__(256) void dequant_dev_q4_0_kernel(const uint8_t* __restrict__ qp,
-                                                               const uint16_t* __restrict__ dp,
-                                                               float* __restrict__ y, size_t nb) {
-    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nb) return;
-    const float d = dq_h2f(dp[b]);
+    const size_t o = 16 * (b / 2), k = 2 * (b % 2);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-        const uint8_t v = qp[b * 16 + j];
+        y[b * 32 + j] = (float)(int8_t)qp[k * ps + o + j] * d;
+        y[b * 32 + 16 + j] = (float)(int8_t)qp[(k + 1) * ps + o + j] * d;
+    }
+}
+
+__global__ __launch_bounds__(256) void dequant_dev_q4_0_kernel(const uint8_t* __restrict__ qp, size_t ps,
+                                                               const uint16_t* __restrict__ dp,
+                                                               float* __restrict__ y, size_t nb) {
+    const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nb) return;
+    const float d = dq_h2f(dp[b]);
+    const uint8_t* q = qp + (b % 2) * ps + 16 * (b / 2);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint8_t v = q[j];
         y[b * 32 + j] = (float)((v & 0x0F) - 8) * d;
         y[b * 32 + j + 16] = (float)((v >> 4) - 8) * d;
     }
 }
 
-__global__ __launch_bounds__(256) void dequant_dev_q6_k_kernel(const uint8_t* __restrict__ qp,
+__global__ __launch_bounds__(256) void dequant_dev_q4_k_kernel(const uint8_t* __restrict__ qp, size_t ps,
+                                                               const uint8_t* __restrict__ hp,
+                                                               float* __restrict__ y, size_t n_sub) {
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n_sub) return;
+    const size_t s = t / 8;
+    const int j = (int)(t % 8), g = j / 2;
+    const uint8_t* h = hp + s * 16;
+    const float d = dq_h2f(rd16(h));
+    const float dmin = dq_h2f(rd16(h + 2));
+    int sc, mn;
+    scale_min_k4(j, h + 4, &sc, &mn);
+    const float d1 = d * (float)sc;
+    const float m1 = dmin * (float)mn;
+    const int sh = 4 * (j & 1);
+    float* o = y + t * 32;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+        const uint8_t v = qp[(size_t)(l / 16) * ps + 64 * s + 16 * g + (l % 16)];
+        o[l] = d1 * (float)((v >> sh) & 0xF) - m1;
+    }
+}
+
+__global__ __launch_bounds__(256) void dequant_dev_q6_k_kernel(const uint8_t* __restrict__ qp, size_t ps,
                                                                const int8_t* __restrict__ sp,
                                                                const uint16_t* __restrict__ dp,
                                                                float* __restrict__ y, size_t n_items) {
@@ -181,12 +220,11 @@ __global__ __launch_bounds__(256) void dequant_dev_q6_k_kernel(const uint8_t* __
     if (t >= n_items) return;
     const size_t s = t / 4;
     const int it = (int)(t % 4), n = it / 2, k = it % 2;
-    const uint8_t* q = qp + t * 48;
     const int8_t* sc = sp + t * 4;
     const float d = dq_h2f(dp[s]);
     float* o = y + s * 256 + 128 * n + 16 * k;
     for (int tt = 0; tt < 16; ++tt) {
-        const uint8_t a = q[tt], b = q[16 + tt], h = q[32 + tt];
+        const uint8_t a = qp[16 * t + tt], b = qp[ps + 16 * t + tt], h = qp[2 * ps + 16 * t + tt];
         const int q1 = (int)((a & 0xF) | (((h >> 0) & 3) << 4)) - 32;
         const int q2 = (int)((b & 0xF) | (((h >> 2) & 3) << 4)) - 32;
         const int q3 = (int)((a >> 4) | (((h >> 4) & 3) << 4)) - 32;
@@ -254,20 +292,23 @@ extern "C" int dq_weights_pack(int fmt, const void* d_gguf, size_t rows, size_t 
     switch (fmt) {
     case DQ_FMT_Q8_0: {
         const size_t nb = rows * cols / 32;
-        pack_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, (uint16_t*)(base + L.d_off), nb);
+        pack_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, L.p_stride, (uint16_t*)(base + L.d_off), nb);
         break;
     }
     case DQ_FMT_Q4_0: {
         const size_t nb = rows * cols / 32;
-        pack_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, (uint16_t*)(base + L.d_off), nb);
+        pack_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, L.p_stride, (uint16_t*)(base + L.d_off), nb);
         break;
     }
-    case DQ_FMT_Q4_K:
-        return dq_status(hipMemcpyAsync(base, x, rows * L.q_row, hipMemcpyDeviceToDevice, s));
+    case DQ_FMT_Q4_K: {
+        const size_t ns = rows * cols / 256;
+        pack_q4_k_kernel<<<grid_for(ns * 9), 256, 0, s>>>(x, base + L.q_off, L.p_stride, base + L.s_off, ns);
+        break;
+    }
     case DQ_FMT_Q6_K: {
         const size_t ns = rows * cols / 256;
-        pack_q6_k_kernel<<<grid_for(ns), 256, 0, s>>>(x, base + L.q_off, base + L.s_off,
-                                                      (uint16_t*)(base + L.d_off), ns);
+        pack_q6_k_kernel<<<grid_for(ns * 4), 256, 0, s>>>(x, base + L.q_off, L.p_stride, base + L.s_off,
+                                                          (uint16_t*)(base + L.d_off), ns);
         break;
     }
     }
@@ -285,21 +326,26 @@ extern "C" int dq_weights_dequantize(int fmt, const void* d_dev, size_t rows, si
     switch (fmt) {
     case DQ_FMT_Q8_0: {
         const size_t nb = rows * cols / 32;
-        dequant_dev_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, (const uint16_t*)(base + L.d_off),
-                                                             d_out, nb);
+        dequant_dev_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, L.p_stride,
+                                                             (const uint16_t*)(base + L.d_off), d_out, nb);
         break;
     }
     case DQ_FMT_Q4_0: {
         const size_t nb = rows * cols / 32;
-        dequant_dev_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, (const uint16_t*)(base + L.d_off),
-                                                             d_out, nb);
+        dequant_dev_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, L.p_stride,
+                                                             (const uint16_t*)(base + L.d_off), d_out, nb);
         break;
     }
-    case DQ_FMT_Q4_K:
-        return dq_dequantize_row(DQ_TYPE_Q4_K, d_dev, d_out, (int64_t)(rows * cols), stream);
+    case DQ_FMT_Q4_K: {
+        const size_t nsub = rows * cols / 32;
+        dequant_dev_q4_k_kernel<<<grid_for(nsub), 256, 0, s>>>(base + L.q_off, L.p_stride, base + L.s_off, d_out,
+                                                               nsub);
+        break;
+    }
     case DQ_FMT_Q6_K: {
         const size_t ni = rows * cols / 64;
-        dequant_dev_q6_k_kernel<<<grid_for(ni), 256, 0, s>>>(base + L.q_off, (const int8_t*)(base + L.s_off),
+        dequant_dev_q6_k_kernel<<<grid_for(ni), 256, 0, s>>>(base + L.q_off, L.p_stride,
+                                                             (const int8_t*)(base + L.s_off),
                                                              (const uint16_t*)(base + L.d_off), d_out, ni);
         break;
     }

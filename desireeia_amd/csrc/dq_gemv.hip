@@ -1,30 +1,29 @@
 // dq_gemv.hip - batch-1 decode GEMV for Q8_0, Q4_0, Q4_K and Q6_K weights.
 //
 // HBM-bound design (gfx950, wave64):
-//  * A row is cut into "items" of 64 weights (cols/64 per row). Lane l of a
-//    wave owns items l, l+64, l+128, ... of EVERY row it visits, so the 64
-//    activation bytes of each owned item (plus its scales/sums) are loaded
-//    into registers once per wave and reused for all its rows; only weights
-//    stream from HBM.
-//  * A wave computes R rows. All weight loads of the R rows (global_load
-//    dwordx4, non-temporal) are issued before any arithmetic, so each wave
-//    keeps R*NIT*(2..4) 16-byte loads in flight.
-//  * Nibble/6-bit unpack and 6-bit scale decode happen in registers; dots are
-//    v_dot4_i32_i8; a row's partials are combined with a wave reduction.
+//  * A row is cut into items of 64 weights (cols/64 per row); lane l of a wave
+//    owns items l, l+64, ... of every row it visits. Items sit contiguously in
+//    item-major planes (dq_common.h), so a wave's loads cover whole cache lines.
+//  * The activation bytes of a lane's items (x int8, scale, sums) are loaded
+//    into registers once per wave and reused for every row the wave visits;
+//    only weights stream from HBM.
+//  * Waves are persistent (a few per SIMD) and walk row groups of R rows with
+//    a two-deep software pipeline: the loads of group k+1 are issued before
+//    group k is computed, so dot products and scale decoding overlap the HBM
+//    stream instead of piling up after it. Past the last group the prefetch
+//    is redirected to a cached dummy address (no extra HBM traffic, and the
+//    compiler's in-order vmcnt accounting stays static).
+//  * Nibble/6-bit unpack and 6-bit scale decode in registers (one decode per
+//    64 weights), v_dot4_i32_i8 dots, and a butterfly reduce-scatter that
+//    finishes the R row sums of a group in log2(64) shuffle steps.
 //
-// Semantics follow the reference CPU GEMVs (see include/desireeia_hip.h):
-// integer partial sums are exact; only the float summation order differs.
-#include "dq_common.h"
-
+// Semantics follow the reference CPU GEMVs (include/desireeia_hip.h): integer
+// partial sums are exact; only the float summation order differs.
 #include <cstdlib>
 
-namespace {
+#include "dq_common.h"
 
-struct XItem {
-    dq_u32x4 x[4];  // 64 activation bytes of the item
-    float s0, s1;   // activation scales (per 32 / per 256)
-    int i0, i1;     // activation integer sums
-};
+namespace {
 
 __device__ __forceinline__ int dot16(const dq_u32x4& w, const dq_u32x4& x, int acc) {
     acc = dq_sdot4((int)w.x, (int)x.x, acc);
@@ -34,24 +33,32 @@ __device__ __forceinline__ int dot16(const dq_u32x4& w, const dq_u32x4& x, int a
     return acc;
 }
 
-__device__ __forceinline__ dq_u32x4 nib_lo(const dq_u32x4& v) {
-    return dq_u32x4{v.x & 0x0F0F0F0Fu, v.y & 0x0F0F0F0Fu, v.z & 0x0F0F0F0Fu, v.w & 0x0F0F0F0Fu};
+__device__ __forceinline__ dq_u32x4 nib_lo(const dq_u32x4& v) { return v & 0x0F0F0F0Fu; }
+__device__ __forceinline__ dq_u32x4 nib_hi(const dq_u32x4& v) { return (v >> 4) & 0x0F0F0F0Fu; }
+
+__device__ __forceinline__ uint32_t ld_u32_nt(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
 }
-__device__ __forceinline__ dq_u32x4 nib_hi(const dq_u32x4& v) {
-    return dq_u32x4{(v.x >> 4) & 0x0F0F0F0Fu, (v.y >> 4) & 0x0F0F0F0Fu, (v.z >> 4) & 0x0F0F0F0Fu,
-                    (v.w >> 4) & 0x0F0F0F0Fu};
+__device__ __forceinline__ uint16_t ld_u16_nt(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(p));
 }
 
 // ---------------------------------------------------------------- formats --
-// Each format: NW = 16-byte weight loads per item; load_x / load_w / dot.
+// X: activation registers of an item; W: its weight registers; load_w reads
+// the item's 16-byte pieces from the quant sub-planes (ps apart) and its scales.
+
+struct XItem {
+    dq_u32x4 x[4];  // the 64 activation bytes the item multiplies
+    float s0, s1;   // activation scales
+    int i0, i1;     // activation integer sums
+};
 
 template <int FMT>
 struct Fmt;
 
-// Q8_0: item = blocks 2i, 2i+1 (64 int8 in plane Q) + 2 fp16 scales (plane D).
+// Q8_0: item i = blocks 2i, 2i+1: 64 int8 (plane Q) + 2 fp16 scales (plane D).
 template <>
 struct Fmt<DQ_FMT_Q8_0> {
-    static constexpr int NW = 4;
     struct W {
         dq_u32x4 q[4];
         uint32_t d;
@@ -62,15 +69,17 @@ struct Fmt<DQ_FMT_Q8_0> {
         X.s0 = xs[2 * i];
         X.s1 = xs[2 * i + 1];
     }
-    __device__ static void load_w(W& w, const uint8_t* base, const DqLayout& L, size_t r, int i) {
-        const uint8_t* q = base + L.q_off + r * L.q_row + 64 * (size_t)i;
+    __device__ static void load_w(W& w, const uint8_t* q, size_t ps, const uint8_t* d) {
         w.q[0] = dq_ld16_stream(q);
-        w.q[1] = dq_ld16_stream(q + 16);
-        w.q[2] = dq_ld16_stream(q + 32);
-        w.q[3] = dq_ld16_stream(q + 48);
-        w.d = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(base + L.d_off + r * L.d_row + 4 * (size_t)i));
+        w.q[1] = dq_ld16_stream(q + ps);
+        w.q[2] = dq_ld16_stream(q + 2 * ps);
+        w.q[3] = dq_ld16_stream(q + 3 * ps);
+        w.d = ld_u32_nt(d);
     }
-    __device__ static float dot(const W& w, const XItem& X) {
+    __device__ static const uint8_t* aux(const uint8_t* base, const DqLayout& L, size_t r, int i) {
+        return base + L.d_off + r * L.d_row + 4 * (size_t)i;
+    }
+    __device__ static float dot(const W& w, const XItem& X, int) {
         const int a = dot16(w.q[1], X.x[1], dot16(w.q[0], X.x[0], 0));
         const int b = dot16(w.q[3], X.x[3], dot16(w.q[2], X.x[2], 0));
         const float d0 = dq_h2f((uint16_t)(w.d & 0xFFFF)), d1 = dq_h2f((uint16_t)(w.d >> 16));
@@ -78,11 +87,10 @@ struct Fmt<DQ_FMT_Q8_0> {
     }
 };
 
-// Q4_0: item = blocks 2i, 2i+1 (2 x 16 nibble bytes) + 2 fp16 scales.
+// Q4_0: item i = blocks 2i, 2i+1: 2 x 16 nibble bytes + 2 fp16 scales.
 // sum (nib-8)*x = sum nib*x - 8*sum x.
 template <>
 struct Fmt<DQ_FMT_Q4_0> {
-    static constexpr int NW = 2;
     struct W {
         dq_u32x4 q[2];
         uint32_t d;
@@ -95,13 +103,15 @@ struct Fmt<DQ_FMT_Q4_0> {
         X.i0 = xsum[2 * i];
         X.i1 = xsum[2 * i + 1];
     }
-    __device__ static void load_w(W& w, const uint8_t* base, const DqLayout& L, size_t r, int i) {
-        const uint8_t* q = base + L.q_off + r * L.q_row + 32 * (size_t)i;
+    __device__ static void load_w(W& w, const uint8_t* q, size_t ps, const uint8_t* d) {
         w.q[0] = dq_ld16_stream(q);
-        w.q[1] = dq_ld16_stream(q + 16);
-        w.d = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(base + L.d_off + r * L.d_row + 4 * (size_t)i));
+        w.q[1] = dq_ld16_stream(q + ps);
+        w.d = ld_u32_nt(d);
     }
-    __device__ static float dot(const W& w, const XItem& X) {
+    __device__ static const uint8_t* aux(const uint8_t* base, const DqLayout& L, size_t r, int i) {
+        return base + L.d_off + r * L.d_row + 4 * (size_t)i;
+    }
+    __device__ static float dot(const W& w, const XItem& X, int) {
         const int a = dot16(nib_hi(w.q[0]), X.x[1], dot16(nib_lo(w.q[0]), X.x[0], 0)) - 8 * X.i0;
         const int b = dot16(nib_hi(w.q[1]), X.x[3], dot16(nib_lo(w.q[1]), X.x[2], 0)) - 8 * X.i1;
         const float d0 = dq_h2f((uint16_t)(w.d & 0xFFFF)), d1 = dq_h2f((uint16_t)(w.d >> 16));
@@ -109,14 +119,13 @@ struct Fmt<DQ_FMT_Q4_0> {
     }
 };
 
-// Q4_K (native 144-byte blocks): item (s = i/4, g = i%4) = sub-blocks 2g
-// (low nibbles) and 2g+1 (high nibbles) of super-block s; header = first 16
-// bytes of the block (d, dmin, 12 scale bytes).
+// Q4_K: item i = (s = i/4, g = i%4): qs bytes 32g..32g+31 of block s = sub-blocks
+// 2g (low nibbles) and 2g+1 (high nibbles); header (d, dmin, 12 scale bytes)
+// of block s from plane H.
 template <>
 struct Fmt<DQ_FMT_Q4_K> {
-    static constexpr int NW = 3;
     struct W {
-        dq_u32x4 h, qa, qb;
+        dq_u32x4 qa, qb, h;
     };
     __device__ static void load_x(XItem& X, int i, const int8_t* xq, const float* xs, const int32_t* xsum) {
         const dq_u32x4* p = reinterpret_cast<const dq_u32x4*>(xq + 64 * (size_t)i);
@@ -125,33 +134,34 @@ struct Fmt<DQ_FMT_Q4_K> {
         X.i0 = xsum[2 * i];
         X.i1 = xsum[2 * i + 1];
     }
-    __device__ static void load_w(W& w, const uint8_t* base, const DqLayout& L, size_t r, int i) {
-        const uint8_t* blk = base + r * L.q_row + (size_t)(i >> 2) * DQ_SZ_Q4_K;
-        w.h = dq_ld16_stream(blk);
-        w.qa = dq_ld16_stream(blk + 16 + 32 * (i & 3));
-        w.qb = dq_ld16_stream(blk + 32 + 32 * (i & 3));
+    __device__ static void load_w(W& w, const uint8_t* q, size_t ps, const uint8_t* h) {
+        w.qa = dq_ld16_stream(q);
+        w.qb = dq_ld16_stream(q + ps);
+        w.h = dq_ld16_stream(h);
     }
-    __device__ static float dot(const W& w, const XItem& X, int g) {
-        // low nibbles: sub-block 2g elements 0..31 (x bytes 0..31)
+    __device__ static const uint8_t* aux(const uint8_t* base, const DqLayout& L, size_t r, int i) {
+        return base + L.s_off + r * L.s_row + 16 * (size_t)(i >> 2);
+    }
+    __device__ static float dot(const W& w, const XItem& X, int i) {
         const int da = dot16(nib_lo(w.qb), X.x[1], dot16(nib_lo(w.qa), X.x[0], 0));
         const int db = dot16(nib_hi(w.qb), X.x[3], dot16(nib_hi(w.qa), X.x[2], 0));
-        // 6-bit scales/mins of sub-blocks j = 2g, 2g+1 (quant/quant.cpp:22-29)
-        // scale bytes q[0..11] = header bytes 4..15 = words h.y, h.z, h.w
+        // 6-bit scale/min of sub-blocks j = 2g, 2g+1 (quant/quant.cpp:22-29);
+        // scale bytes q[0..11] are header words h.y, h.z, h.w.
+        const int g = i & 3;
         const uint32_t w0 = w.h.y, w1 = w.h.z, w2 = w.h.w;
         int sca, mna, scb, mnb;
         if (g < 2) {
-            // j = 2g, 2g+1 < 4: sc = q[j] & 63, m = q[j+4] & 63
-            const int sh = 16 * g;
+            const int sh = 16 * g;  // j < 4: sc = q[j] & 63, m = q[j+4] & 63
             sca = (w0 >> sh) & 63;
             scb = (w0 >> (sh + 8)) & 63;
             mna = (w1 >> sh) & 63;
             mnb = (w1 >> (sh + 8)) & 63;
         } else {
             // j >= 4: sc = (q[j+4]&15) | ((q[j-4]>>6)<<4), m = (q[j+4]>>4) | ((q[j]>>6)<<4)
-            const int sh = 16 * (g - 2);  // byte index (j-4) within a word
-            const uint32_t qa8 = (w2 >> sh) & 0xFF, qb8 = (w2 >> (sh + 8)) & 0xFF;       // q[j+4]
-            const uint32_t la = (w0 >> sh) & 0xFF, lb = (w0 >> (sh + 8)) & 0xFF;         // q[j-4]
-            const uint32_t ma = (w1 >> sh) & 0xFF, mb = (w1 >> (sh + 8)) & 0xFF;         // q[j]
+            const int sh = 16 * (g - 2);
+            const uint32_t qa8 = (w2 >> sh) & 0xFF, qb8 = (w2 >> (sh + 8)) & 0xFF;
+            const uint32_t la = (w0 >> sh) & 0xFF, lb = (w0 >> (sh + 8)) & 0xFF;
+            const uint32_t ma = (w1 >> sh) & 0xFF, mb = (w1 >> (sh + 8)) & 0xFF;
             sca = (int)((qa8 & 0xF) | ((la >> 6) << 4));
             scb = (int)((qb8 & 0xF) | ((lb >> 6) << 4));
             mna = (int)((qa8 >> 4) | ((ma >> 6) << 4));
@@ -165,12 +175,11 @@ struct Fmt<DQ_FMT_Q4_K> {
     }
 };
 
-// Q6_K (planes): item (s = i/4, n = (i/2)%2, k = i%2) = 48 bytes of plane Q,
-// 4 scales of plane S, d of plane D. Activation bytes of the item:
-// x[256s + 128n + 16k + 32*quarter + 0..15], quarter = 0..3.
+// Q6_K: item i = (s = i/4, it = i%4 = 2n+k): 16 bytes of each of QA, QB, QH,
+// 4 scales (plane S) and d (plane D); its 64 weights sit at positions
+// 256s + 128n + 16k + 32*quarter + 0..15.
 template <>
 struct Fmt<DQ_FMT_Q6_K> {
-    static constexpr int NW = 3;
     struct W {
         dq_u32x4 a, b, h;
         uint32_t sc;
@@ -184,18 +193,17 @@ struct Fmt<DQ_FMT_Q6_K> {
         X.x[3] = dq_ld16(base + 96);
         X.s0 = xs[8 * (i >> 2)];
     }
-    __device__ static void load_w(W& w, const uint8_t* base, const DqLayout& L, size_t r, int i) {
-        const uint8_t* q = base + L.q_off + r * L.q_row + 48 * (size_t)i;
+    __device__ static void load_w6(W& w, const uint8_t* q, size_t ps, const uint8_t* s, const uint8_t* d) {
         w.a = dq_ld16_stream(q);
-        w.b = dq_ld16_stream(q + 16);
-        w.h = dq_ld16_stream(q + 32);
-        w.sc = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(base + L.s_off + r * L.s_row + 4 * (size_t)i));
-        w.d = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(base + L.d_off + r * L.d_row + 2 * (size_t)(i >> 2)));
+        w.b = dq_ld16_stream(q + ps);
+        w.h = dq_ld16_stream(q + 2 * ps);
+        w.sc = ld_u32_nt(s);
+        w.d = ld_u16_nt(d);
     }
     __device__ static int q6dot(uint32_t lo4, uint32_t hi2, uint32_t x, int acc) {
         return dq_sdot4(dq_sub32_bytes((lo4 & 0x0F0F0F0Fu) | ((hi2 & 0x03030303u) << 4)), (int)x, acc);
     }
-    __device__ static float dot(const W& w, const XItem& X) {
+    __device__ static float dot(const W& w, const XItem& X, int) {
         int d0 = 0, d1 = 0, d2 = 0, d3 = 0;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -212,98 +220,217 @@ struct Fmt<DQ_FMT_Q6_K> {
     }
 };
 
+// Loads the weights of item i of row r (or, when `live` is false, reads a
+// cached dummy location instead: the pipeline's prefetch past the last group).
 template <int FMT>
-__device__ __forceinline__ float item_dot(const typename Fmt<FMT>::W& w, const XItem& X, int i) {
-    if constexpr (FMT == DQ_FMT_Q4_K) return Fmt<FMT>::dot(w, X, i & 3);
-    else return Fmt<FMT>::dot(w, X);
+__device__ __forceinline__ void load_item(typename Fmt<FMT>::W& w, const uint8_t* base, const DqLayout& L, size_t r,
+                                          int i, bool live, const uint8_t* dummy) {
+    const uint8_t* q = live ? base + L.q_off + r * L.q_row + 16 * (size_t)i : dummy;
+    const size_t ps = live ? L.p_stride : 0;
+    if constexpr (FMT == DQ_FMT_Q6_K) {
+        const uint8_t* s = live ? base + L.s_off + r * L.s_row + 4 * (size_t)i : dummy;
+        const uint8_t* d = live ? base + L.d_off + r * L.d_row + 2 * (size_t)(i >> 2) : dummy;
+        Fmt<FMT>::load_w6(w, q, ps, s, d);
+    } else {
+        Fmt<FMT>::load_w(w, q, ps, live ? Fmt<FMT>::aux(base, L, r, i) : dummy);
+    }
 }
 
-// ----------------------------------------------------------------- kernel --
-
-template <int FMT, int R, int NIT>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w, DqLayout L, int rows, int ipr,
-                                                   const int8_t* __restrict__ xq, const float* __restrict__ xs,
-                                                   const int32_t* __restrict__ xsum, float* __restrict__ y) {
-    using F = Fmt<FMT>;
-    const int lane = threadIdx.x & (DQ_WAVE - 1);
-    const int wave = (int)((blockIdx.x * blockDim.x + threadIdx.x) / DQ_WAVE);
-    const int r0 = wave * R;
-    if (r0 >= rows) return;
-
-    XItem X[NIT];
-    bool on[NIT];
+// Butterfly reduce-scatter of R per-lane partial sums: returns, in every lane
+// of the group of 64/R lanes that holds row rr = lane / (64/R), the full sum of
+// row rr across the wave.
+template <int R>
+__device__ __forceinline__ float reduce_rows(float (&acc)[R], int lane) {
+    int n = R;
+    int off = 32;
 #pragma unroll
-    for (int j = 0; j < NIT; ++j) {
-        const int i = lane + DQ_WAVE * j;
-        on[j] = i < ipr;
-        F::load_x(X[j], on[j] ? i : ipr - 1, xq, xs, xsum);
-    }
-
-    typename F::W wr[R][NIT];
+    for (int step = 0; step < 3; ++step) {
+        if (n > 1) {
+            const bool upper = (lane & off) != 0;
+            const int h = n / 2;
 #pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-        const size_t r = (size_t)min(r0 + rr, rows - 1);
-#pragma unroll
-        for (int j = 0; j < NIT; ++j) {
-            const int i = lane + DQ_WAVE * j;
-            F::load_w(wr[rr][j], w, L, r, on[j] ? i : ipr - 1);
+            for (int k = 0; k < R / 2; ++k) {
+                if (k < h) {
+                    const float mine = upper ? acc[h + k] : acc[k];
+                    const float other = upper ? acc[k] : acc[h + k];
+                    acc[k] = mine + __shfl_xor(other, off, DQ_WAVE);
+                }
+            }
+            n = h;
+            off >>= 1;
         }
     }
+    float v = acc[0];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        if (o <= off) v += __shfl_xor(v, o, DQ_WAVE);
+    return v;
+}
 
+// Items of a wave: [i0, i1) of every row; lane owns i0 + lane + 64j.
+template <int FMT, int R, int NIT>
+__device__ __forceinline__ void load_group(typename Fmt<FMT>::W (&wr)[R][NIT], const uint8_t* base,
+                                           const DqLayout& L, int g, int ngroups, int rows, int i0, int i1, int lane,
+                                           const uint8_t* dummy) {
+    const bool live = g < ngroups;
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+        const size_t r = (size_t)min(g * R + rr, rows - 1);
+#pragma unroll
+        for (int j = 0; j < NIT; ++j)
+            load_item<FMT>(wr[rr][j], base, L, r, min(i0 + lane + DQ_WAVE * j, i1 - 1), live, dummy);
+    }
+}
+
+// Row sums of group g. KS == 1: the wave owns whole rows and stores them.
+// KS == 4: the 4 waves of the workgroup own a quarter of the items each; their
+// partial sums meet in LDS (double-buffered by `buf`, one barrier per group)
+// and wave 0 adds them in a fixed order.
+template <int FMT, int R, int NIT, int KS>
+__device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R][NIT], const XItem (&X)[NIT], int g,
+                                              int rows, int i0, int i1, int lane, int ks, float (*part)[R][4],
+                                              int buf, float* __restrict__ y) {
     float acc[R];
 #pragma unroll
     for (int rr = 0; rr < R; ++rr) {
         float a = 0.0f;
 #pragma unroll
         for (int j = 0; j < NIT; ++j) {
-            const float p = item_dot<FMT>(wr[rr][j], X[j], lane + DQ_WAVE * j);
-            a += on[j] ? p : 0.0f;
+            const int i = i0 + lane + DQ_WAVE * j;
+            const float p = Fmt<FMT>::dot(wr[rr][j], X[j], i);
+            a += i < i1 ? p : 0.0f;
         }
         acc[rr] = a;
     }
-#pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-        const float s = dq_wave_sum(acc[rr]);
-        if (lane == rr && r0 + rr < rows) y[r0 + rr] = s;
+    const float s = reduce_rows<R>(acc, lane);
+    constexpr int GROUP = DQ_WAVE / R;
+    if constexpr (KS == 1) {
+        if ((lane & (GROUP - 1)) == 0) {
+            const int r = g * R + lane / GROUP;
+            if (r < rows) y[r] = s;
+        }
+    } else {
+        if ((lane & (GROUP - 1)) == 0) part[buf][lane / GROUP][ks] = s;
+        __syncthreads();
+        if (ks == 0 && lane < R) {
+            const int r = g * R + lane;
+            if (r < rows) y[r] = ((part[buf][lane][0] + part[buf][lane][1]) + part[buf][lane][2]) + part[buf][lane][3];
+        }
     }
 }
 
-template <int FMT, int R>
-int launch_r(const uint8_t* w, const DqLayout& L, int rows, int ipr, const int8_t* xq, const float* xs,
-             const int32_t* xsum, float* y, hipStream_t s) {
-    const int nit = (ipr + DQ_WAVE - 1) / DQ_WAVE;
-    const int waves = (rows + R - 1) / R;
-    const unsigned grid = (unsigned)((waves + 3) / 4);
-    if (nit <= 1) gemv_kernel<FMT, R, 1><<<grid, 256, 0, s>>>(w, L, rows, ipr, xq, xs, xsum, y);
-    else if (nit <= 2) gemv_kernel<FMT, R, 2><<<grid, 256, 0, s>>>(w, L, rows, ipr, xq, xs, xsum, y);
-    else if (nit <= 4) gemv_kernel<FMT, R, 4><<<grid, 256, 0, s>>>(w, L, rows, ipr, xq, xs, xsum, y);
-    else if (nit <= 8) gemv_kernel<FMT, R, 8><<<grid, 256, 0, s>>>(w, L, rows, ipr, xq, xs, xsum, y);
-    else return DQ_ERR_NOT_SUPPORTED;
+// ----------------------------------------------------------------- kernel --
+
+// Grid: persistent 256-thread workgroups walking "units" u = blockIdx.x,
+// blockIdx.x + gridDim.x, ... KS == 1: unit u = groups 4u..4u+3, one per wave.
+// KS == 4: unit u = group u, shared by the 4 waves (K split in quarters).
+template <int FMT, int R, int NIT, int KS>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w, DqLayout L, int rows, int items,
+                                                   const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                                                   const int32_t* __restrict__ xsum, float* __restrict__ y) {
+    using W = typename Fmt<FMT>::W;
+    __shared__ float part[2][R][4];
+    const int lane = threadIdx.x & (DQ_WAVE - 1);
+    const int wv = (int)(threadIdx.x / DQ_WAVE);
+    const int ks = KS == 1 ? 0 : wv;
+    const int per = KS == 1 ? items : (items + 3) / 4;
+    const int i0 = min(ks * per, items);
+    const int i1 = min(i0 + per, items);
+    const int ngroups = (rows + R - 1) / R;
+    const int stride = KS == 1 ? 4 * (int)gridDim.x : (int)gridDim.x;
+    int g = KS == 1 ? 4 * (int)blockIdx.x + wv : (int)blockIdx.x;
+    if (g >= ngroups || i0 >= i1) return;  // uniform per wave (KS 1) / per workgroup (KS 4)
+    const uint8_t* dummy = reinterpret_cast<const uint8_t*>(xq);
+
+    W b0[R][NIT], b1[R][NIT];
+    load_group<FMT, R, NIT>(b0, w, L, g, ngroups, rows, i0, i1, lane, dummy);
+    XItem X[NIT];
+#pragma unroll
+    for (int j = 0; j < NIT; ++j) Fmt<FMT>::load_x(X[j], min(i0 + lane + DQ_WAVE * j, i1 - 1), xq, xs, xsum);
+
+    // Two-deep pipeline, unrolled by two so the buffers never move.
+    for (;;) {
+        load_group<FMT, R, NIT>(b1, w, L, g + stride, ngroups, rows, i0, i1, lane, dummy);
+        compute_group<FMT, R, NIT, KS>(b0, X, g, rows, i0, i1, lane, ks, part, 0, y);
+        g += stride;
+        if (g >= ngroups) break;
+        load_group<FMT, R, NIT>(b0, w, L, g + stride, ngroups, rows, i0, i1, lane, dummy);
+        compute_group<FMT, R, NIT, KS>(b1, X, g, rows, i0, i1, lane, ks, part, 1, y);
+        g += stride;
+        if (g >= ngroups) break;
+    }
+}
+
+int g_num_cus = 0;
+
+int num_cus() {
+    if (g_num_cus == 0) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+            g_num_cus = n;
+        else
+            g_num_cus = 256;
+    }
+    return g_num_cus;
+}
+
+int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
+}
+
+template <int FMT, int R, int NIT, int KS>
+int launch(const uint8_t* w, const DqLayout& L, int rows, int items, const int8_t* xq, const float* xs,
+           const int32_t* xsum, float* y, hipStream_t s) {
+    static const int wpc = env_int("DQ_GEMV_WPC", 8);  // persistent waves per CU
+    const int ngroups = (rows + R - 1) / R;
+    const int units = KS == 1 ? (ngroups + 3) / 4 : ngroups;
+    const int max_wg = max(1, num_cus() * wpc / 4);
+    const int iters = (units + max_wg - 1) / max_wg;  // balance: every workgroup walks `iters` units
+    const unsigned grid = (unsigned)((units + iters - 1) / iters);
+    gemv_kernel<FMT, R, NIT, KS><<<grid, 256, 0, s>>>(w, L, rows, items, xq, xs, xsum, y);
     return dq_launch_status();
 }
 
-// Rows per wave: enough loads in flight per wave, few enough registers.
-int pick_r(int ipr) {
-    static int forced = -1;
-    if (forced < 0) {
-        const char* e = getenv("DQ_GEMV_R");
-        forced = e ? atoi(e) : 0;
+template <int FMT, int R, int KS>
+int launch_nit(int nit, const uint8_t* w, const DqLayout& L, int rows, int items, const int8_t* xq,
+               const float* xs, const int32_t* xsum, float* y, hipStream_t s) {
+    switch (nit) {
+    case 1: return launch<FMT, R, 1, KS>(w, L, rows, items, xq, xs, xsum, y, s);
+    case 2: return launch<FMT, R, 2, KS>(w, L, rows, items, xq, xs, xsum, y, s);
+    case 3: return launch<FMT, R, 3, KS>(w, L, rows, items, xq, xs, xsum, y, s);
+    case 4: return launch<FMT, R, 4, KS>(w, L, rows, items, xq, xs, xsum, y, s);
+    default:
+        if (nit <= 6) return launch<FMT, R, 6, KS>(w, L, rows, items, xq, xs, xsum, y, s);
+        if (nit <= 8) return launch<FMT, R, 8, KS>(w, L, rows, items, xq, xs, xsum, y, s);
+        return DQ_ERR_NOT_SUPPORTED;
     }
-    if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
-    if (ipr <= 64) return 4;
-    if (ipr <= 128) return 2;
-    return 2;
 }
 
 template <int FMT>
-int launch_fmt(const uint8_t* w, const DqLayout& L, int rows, int ipr, const int8_t* xq, const float* xs,
+int launch_fmt(const uint8_t* w, const DqLayout& L, size_t rows, size_t cols, const int8_t* xq, const float* xs,
                const int32_t* xsum, float* y, hipStream_t s) {
-    switch (pick_r(ipr)) {
-    case 1: return launch_r<FMT, 1>(w, L, rows, ipr, xq, xs, xsum, y, s);
-    case 2: return launch_r<FMT, 2>(w, L, rows, ipr, xq, xs, xsum, y, s);
-    case 8: return launch_r<FMT, 8>(w, L, rows, ipr, xq, xs, xsum, y, s);
-    default: return launch_r<FMT, 4>(w, L, rows, ipr, xq, xs, xsum, y, s);
+    const int items = (int)(cols / 64);
+    // K split: rows wider than 128 items are shared by the 4 waves of a workgroup
+    int ks = env_int("DQ_GEMV_KS", 0);
+    if (ks != 1 && ks != 4) ks = items > 2 * DQ_WAVE ? 4 : 1;
+    const int per = ks == 1 ? items : (items + 3) / 4;
+    const int nit = (per + DQ_WAVE - 1) / DQ_WAVE;
+    if (nit > 8) return DQ_ERR_NOT_SUPPORTED;
+    // rows per group: enough loads in flight per wave, bounded registers
+    int r = env_int("DQ_GEMV_R", 0);
+    if (r != 1 && r != 2 && r != 4) r = nit == 1 ? 2 : 1;
+    if (nit > 4 && r > 1) r = 1;
+    const int R_ = r;
+    if (ks == 1) {
+        if (R_ == 1) return launch_nit<FMT, 1, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
+        if (R_ == 2) return launch_nit<FMT, 2, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
+        return launch_nit<FMT, 4, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
     }
+    if (R_ == 1) return launch_nit<FMT, 1, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
+    if (R_ == 2) return launch_nit<FMT, 2, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
+    return launch_nit<FMT, 4, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
 }
 
 }  // namespace
@@ -315,15 +442,14 @@ extern "C" int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const
     if (rows == 0) return DQ_OK;
     if (!d_w || !d_xq || !d_xscale || !d_y) return DQ_ERR_INVALID_ARG;
     if ((fmt == DQ_FMT_Q4_0 || fmt == DQ_FMT_Q4_K) && !d_xsum) return DQ_ERR_INVALID_ARG;
-    if (rows > 0x7FFFFFFF) return DQ_ERR_NOT_SUPPORTED;
-    const int ipr = (int)(cols / 64);
+    if (rows > 0x3FFFFFFF) return DQ_ERR_NOT_SUPPORTED;
     const uint8_t* w = (const uint8_t*)d_w;
     hipStream_t s = (hipStream_t)stream;
     switch (fmt) {
-    case DQ_FMT_Q8_0: return launch_fmt<DQ_FMT_Q8_0>(w, L, (int)rows, ipr, d_xq, d_xscale, d_xsum, d_y, s);
-    case DQ_FMT_Q4_0: return launch_fmt<DQ_FMT_Q4_0>(w, L, (int)rows, ipr, d_xq, d_xscale, d_xsum, d_y, s);
-    case DQ_FMT_Q4_K: return launch_fmt<DQ_FMT_Q4_K>(w, L, (int)rows, ipr, d_xq, d_xscale, d_xsum, d_y, s);
-    case DQ_FMT_Q6_K: return launch_fmt<DQ_FMT_Q6_K>(w, L, (int)rows, ipr, d_xq, d_xscale, d_xsum, d_y, s);
+    case DQ_FMT_Q8_0: return launch_fmt<DQ_FMT_Q8_0>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, s);
+    case DQ_FMT_Q4_0: return launch_fmt<DQ_FMT_Q4_0>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, s);
+    case DQ_FMT_Q4_K: return launch_fmt<DQ_FMT_Q4_K>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, s);
+    case DQ_FMT_Q6_K: return launch_fmt<DQ_FMT_Q6_K>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, s);
     }
     return DQ_ERR_NOT_SUPPORTED;
 }

@@ -47,20 +47,27 @@ class Activation:
         self.q, self.scale, self.isum, self.fsum, self.kind = q, scale, isum, fsum, kind
 
 
-def quantize_act(x, kind=ACT_Q8_0):
+def empty_act(shape, kind, device):
+    """Preallocated activation buffers for quantize_act(out=...)."""
+    nb = shape[-1] // 32
+    q = torch.empty(shape, dtype=torch.int8, device=device)
+    scale = torch.empty(tuple(shape[:-1]) + (nb,), dtype=torch.float32, device=device)
+    isum = torch.empty(tuple(shape[:-1]) + (nb,), dtype=torch.int32, device=device)
+    fsum = torch.empty(tuple(shape[:-1]) + (nb,), dtype=torch.float32, device=device)
+    return Activation(q, scale, isum, fsum, kind)
+
+
+def quantize_act(x, kind=ACT_Q8_0, out=None):
     """x: fp32 [n_tok, cols] or [cols] device tensor."""
     lib = _lib.load()
     x = x.contiguous()
     cols = x.shape[-1]
     n_tok = x.numel() // cols
-    nb = cols // 32
-    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
-    scale = torch.empty(x.shape[:-1] + (nb,), dtype=torch.float32, device=x.device)
-    isum = torch.empty(x.shape[:-1] + (nb,), dtype=torch.int32, device=x.device)
-    fsum = torch.empty(x.shape[:-1] + (nb,), dtype=torch.float32, device=x.device)
-    _lib.check(lib.dq_quantize_act(kind, _ptr(x), cols, n_tok, _ptr(q), _ptr(scale), _ptr(isum), _ptr(fsum),
-                                   _stream()), "dq_quantize_act")
-    return Activation(q, scale, isum, fsum, kind)
+    a = out if out is not None else empty_act(tuple(x.shape), kind, x.device)
+    _lib.check(lib.dq_quantize_act(kind, _ptr(x), cols, n_tok, _ptr(a.q), _ptr(a.scale), _ptr(a.isum),
+                                   _ptr(a.fsum), _stream()), "dq_quantize_act")
+    a.kind = kind
+    return a
 
 
 def quantize_q8_0(x):
