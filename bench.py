@@ -81,6 +81,40 @@ class GemvCase:
         ops.gemv(m, self.act, out=self.y)
 
 
+class GemmCase:
+    """Prefill GEMM (config 3): X [n_tok][cols] fp32 -> Y [n_tok][rows]."""
+
+    def __init__(self, qtype, rows, cols, n_tok, seed, dev):
+        import torch
+        from desireeia_amd import ops, synth
+        self.qtype, self.rows, self.cols, self.n_tok = qtype, rows, cols, n_tok
+        w = synth.gen_weights(qtype, rows, cols, seed)
+        m0 = ops.QuantMatrix.from_gguf(qtype, w, rows, cols, device=dev)
+        self.mats = [m0, m0.clone()]
+        self.x = torch.from_numpy(synth.gen_act((n_tok, cols), seed + 1)).to(dev)
+        self.work = ops.gemm_workspace(m0, n_tok)
+        self.y = torch.empty(n_tok, rows, dtype=torch.float32, device=dev)
+        self.i = 0
+        ops.gemm(m0, self.x, out=self.y, work=self.work)
+
+    def step(self):
+        from desireeia_amd import ops
+        m = self.mats[self.i]
+        self.i ^= 1
+        ops.gemm(m, self.x, out=self.y, work=self.work)
+
+    def kernel(self):
+        from desireeia_amd import _lib, ops
+        m = self.mats[self.i]
+        self.i ^= 1
+        lib = _lib.load()
+        _lib.check(lib.dq_gemm_f16act(m.fmt, ops._ptr(m.buf), m.rows, m.cols, ops._ptr(self.work), self.n_tok,
+                                      ops._ptr(self.y), ops._stream()), "dq_gemm_f16act")
+
+    def flops(self):
+        return 2.0 * self.n_tok * self.rows * self.cols
+
+
 def graph_time(fn, calls_per_graph, reps, warmup_reps=2):
     """Captures calls_per_graph calls of fn into one HIP graph and times `reps`
     replays with HIP events on the capturing stream. Returns us per call."""
@@ -185,6 +219,15 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copy: {args.steps} x {src.numel()} bytes")
+        return
+    gemm_shapes = {"gemm_q4k": (synth.Q4_K, 14336, 4096, 512), "gemm_q6k": (synth.Q6_K, 4096, 14336, 512)}
+    if args.only in gemm_shapes:
+        qt, r, c, t = gemm_shapes[args.only]
+        g = GemmCase(qt, r, c, t, 21, dev)
+        us = graph_time(g.kernel, 10, max(1, args.steps // 10))
+        us_step = graph_time(g.step, 10, max(1, args.steps // 10))
+        log(f"{args.only}: gemm kernel {us:.1f} us = {g.flops() / us / 1e6:.1f} TFLOP/s; "
+            f"quantize+gemm {us_step:.1f} us")
         return
     if args.only:
         qt, r, c = shapes[args.only]

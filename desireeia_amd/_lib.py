@@ -23,6 +23,10 @@ SIGNATURES = {
     "dq_quantize_act": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p, c_p, c_p, c_p]),
     "dq_quantize_q8_1_blocks": (c_int, [c_p, c_size, c_p, c_p]),
     "dq_gemv": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p, c_p, c_p, c_p]),
+    "dq_gemm_workspace_bytes": (c_int, [c_int, c_size, c_size, c_size, ctypes.POINTER(c_size)]),
+    "dq_gemm": (c_int, [c_int, c_p, c_size, c_size, c_p, c_size, c_p, c_p, c_size, c_p]),
+    "dq_quantize_act_f16": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p]),
+    "dq_gemm_f16act": (c_int, [c_int, c_p, c_size, c_size, c_p, c_size, c_p, c_p]),
 }
 
 _lib = None

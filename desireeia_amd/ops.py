@@ -141,3 +141,23 @@ def gemv(mat, act, out=None):
 def matmul(mat, x):
     """y = W x with the semantics of the reference's matmul_<fmt> (batch 1)."""
     return gemv(mat, quantize_act(x, act_kind_for(mat.fmt)))
+
+
+def gemm_workspace(mat, n_tok):
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    _lib.check(lib.dq_gemm_workspace_bytes(mat.fmt, mat.rows, mat.cols, n_tok, ctypes.byref(n)), "dq_gemm_workspace_bytes")
+    return torch.empty(max(n.value, 1), dtype=torch.uint8, device=mat.buf.device)
+
+
+def gemm(mat, x, out=None, work=None):
+    """Y[n_tok][rows] = X W^T with the semantics of matmul_<fmt>_batch (n_tok >= 4),
+    reference core/matmul.cpp:2090-2125."""
+    lib = _lib.load()
+    x = x.contiguous()
+    n_tok = x.shape[0]
+    y = out if out is not None else torch.empty(n_tok, mat.rows, dtype=torch.float32, device=x.device)
+    wk = work if work is not None else gemm_workspace(mat, n_tok)
+    _lib.check(lib.dq_gemm(mat.fmt, _ptr(mat.buf), mat.rows, mat.cols, _ptr(x), n_tok, _ptr(y), _ptr(wk),
+                           wk.numel(), _stream()), "dq_gemm")
+    return y

@@ -92,6 +92,24 @@ int dq_quantize_q8_1_blocks(const float* d_x, size_t n, void* d_blocks, void* st
 int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
             const float* d_xscale, const int32_t* d_xsum, float* d_y, void* stream);
 
+/* Prefill GEMM y[n_tok][rows] = x[n_tok][cols] W^T for Q4_K and Q6_K, with the
+ * semantics of matmul_q4_k_batch / matmul_q6_k_batch for n_tok >= 4 (the
+ * i8_gemm path, core/matmul.cpp:2090-2125 -> :806-845): per-32 activation
+ * quantization, exact float block sums for the Q4_K min term. Runs on fp16
+ * MFMA over pre-scaled operands (result within ~3e-4 relative of the
+ * reference). `d_work` (dq_gemm_workspace_bytes() bytes) holds the quantized
+ * activations and, for Q4_K, a per-call plane of the min terms. Other
+ * formats: -2. */
+int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t n_tok, size_t* bytes);
+int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,
+            float* d_y, void* d_work, size_t work_bytes, void* stream);
+/* The two halves of dq_gemm: the activation quantizer into the workspace
+ * layout, and the GEMM on an already quantized activation (several weight
+ * matrices reading the same x share one quantization). */
+int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_work, void* stream);
+int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work, size_t n_tok,
+                   float* d_y, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
