@@ -146,6 +146,22 @@ def kernel_stats(case, launches=400):
     return us, b / us / 1e3  # GB/s
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_up_14336x4096_traffic.md")
+
+
+def recorded_traffic():
+    """HBM bytes per launch of the dominant kernel, from the FETCH_SIZE and
+    WRITE_SIZE counter passes summarised in profiles/ (rocprofv3 cannot run
+    inside this process; the file gives the commands). None if absent."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline_q4k(budget_s=12.0):
     """The reference's matmul_q4_k (oracle/_ref) on the host cores, 14336x4096,
     distinct weight copies (DRAM regime), best of repeated passes."""
@@ -267,7 +283,8 @@ def main():
         log(f"{k}: {us:.2f} us  {gbs:.1f} GB/s  ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
     dom = extra["q4k_up"]
     roofline = {"bound": "hbm", "achieved": dom["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(dom["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(),
+                "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
                 "kernel": "gemv_kernel<Q4_K> 14336x4096",
                 "bytes_per_launch": gemv_kernel_bytes(synth.Q4_K, 14336, 4096)}
 
