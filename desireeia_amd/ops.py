@@ -161,3 +161,44 @@ def gemm(mat, x, out=None, work=None):
     _lib.check(lib.dq_gemm(mat.fmt, _ptr(mat.buf), mat.rows, mat.cols, _ptr(x), n_tok, _ptr(y), _ptr(wk),
                            wk.numel(), _stream()), "dq_gemm")
     return y
+
+
+class KVCache:
+    """Q8_0 K and V caches of one layer on the device, [n_ctx][n_head_kv][hd/32 x 34 B]
+    (models/dense_forward.cpp:2425, :4038-4043)."""
+
+    def __init__(self, n_ctx, n_head_kv, hd, device="cuda"):
+        self.n_ctx, self.n_head_kv, self.hd = n_ctx, n_head_kv, hd
+        self.pos_bytes = n_head_kv * hd // 32 * 34
+        self.k = torch.zeros(n_ctx * self.pos_bytes, dtype=torch.uint8, device=device)
+        self.v = torch.zeros(n_ctx * self.pos_bytes, dtype=torch.uint8, device=device)
+
+    def write(self, k, v, pos):
+        """Quantizes the rows k, v ([n_head_kv * hd] fp32) into position pos.
+        pos: int, or an int32 device tensor read when the kernel runs."""
+        lib = _lib.load()
+        dpos = pos if isinstance(pos, torch.Tensor) else None
+        _lib.check(lib.dq_kv_write(_ptr(k.contiguous()), _ptr(v.contiguous()), self.n_head_kv, self.hd,
+                                   _ptr(self.k), _ptr(self.v), 0 if dpos is not None else int(pos), _ptr(dpos),
+                                   self.n_ctx, _stream()), "dq_kv_write")
+
+
+def attn_workspace(n_head, n_head_kv, hd, n_ctx, device="cuda"):
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    _lib.check(lib.dq_attn_workspace_bytes(n_head, n_head_kv, hd, n_ctx, ctypes.byref(n)), "dq_attn_workspace_bytes")
+    return torch.empty(max(n.value, 1), dtype=torch.uint8, device=device)
+
+
+def attention_decode(q, cache, n_head, pos, cc_start=0, out=None, work=None):
+    """Decode attention of q [n_head * hd] over positions [cc_start, pos] of
+    the cache; pos an int or an int32 device tensor."""
+    lib = _lib.load()
+    hd = cache.hd
+    o = out if out is not None else torch.empty(n_head * hd, dtype=torch.float32, device=q.device)
+    wk = work if work is not None else attn_workspace(n_head, cache.n_head_kv, hd, cache.n_ctx, q.device)
+    dpos = pos if isinstance(pos, torch.Tensor) else None
+    _lib.check(lib.dq_attn_decode_q8(_ptr(q.contiguous()), _ptr(cache.k), _ptr(cache.v), n_head, cache.n_head_kv,
+                                     hd, cc_start, 0 if dpos is not None else int(pos), _ptr(dpos), cache.n_ctx,
+                                     _ptr(o), _ptr(wk), wk.numel(), _stream()), "dq_attn_decode_q8")
+    return o

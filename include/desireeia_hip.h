@@ -110,6 +110,29 @@ int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_t n_tok, vo
 int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work, size_t n_tok,
                    float* d_y, void* stream);
 
+/* Q8_0 KV cache of one layer, laid out [pos][kv_head][hd/32 blocks of 34 B]
+ * (models/dense_forward.cpp:2425, :4038-4043). dq_kv_write replaces
+ * write_kv_cache (:2552-2605): it quantizes the new K and V rows
+ * (n_head_kv * hd floats each, kv_quantize_row, kv/kv_quant.cpp:31-56,
+ * bit-exact) into position `pos`. With d_pos != NULL the position is read
+ * from device memory when the kernel runs (graph replay; clamped to
+ * [0, n_ctx)) and `pos` is ignored. */
+int dq_kv_write(const float* d_k, const float* d_v, uint32_t n_head_kv, uint32_t hd, void* d_kc, void* d_vc,
+                uint32_t pos, const int32_t* d_pos, uint32_t n_ctx, void* stream);
+
+/* Batch-1 decode attention over the Q8_0 cache (the quantized-KV branch of
+ * models/dense_forward.cpp:3956-4065; the GPU counterpart of cuda_attention_out,
+ * core/engine.h:806-811): q [n_head][hd] fp32 (after RoPE), keys/values at
+ * positions [cc_start, pos], query head h reads KV head h / (n_head /
+ * n_head_kv), scores scaled by 1/sqrt(hd), softmax, out [n_head][hd] fp32.
+ * hd = 128 and n_head / n_head_kv in {1, 2, 4, 8}; other shapes: -2.
+ * d_work holds dq_attn_workspace_bytes(n_ctx) bytes of split partials.
+ * d_pos as for dq_kv_write. */
+int dq_attn_workspace_bytes(uint32_t n_head, uint32_t n_head_kv, uint32_t hd, uint32_t n_ctx, size_t* bytes);
+int dq_attn_decode_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head, uint32_t n_head_kv,
+                      uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx,
+                      float* d_out, void* d_work, size_t work_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

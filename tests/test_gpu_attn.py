@@ -1,0 +1,134 @@
+"""Q8_0 KV cache writes and decode attention on the GPU against the oracle
+(reference kv/kv_quant.cpp and models/dense_forward.cpp:3956-4065).
+
+KV rows: bit-exact. Attention output: norm-wise relative error <= 1e-3 against
+the oracle's float path (the reference's own summation order) and against the
+fp64 evaluation over the same dequantized rows."""
+import numpy as np
+import pytest
+import torch
+
+from desireeia_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+HD = 128
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def host_cache(orc, n_pos, n_kv, seed):
+    rng = np.random.default_rng(seed)
+    k = rng.standard_normal((n_pos, n_kv, HD)).astype(np.float32)
+    v = rng.standard_normal((n_pos, n_kv, HD)).astype(np.float32)
+    return orc.kv_quantize_row(k.reshape(-1)), orc.kv_quantize_row(v.reshape(-1))
+
+
+def device_cache(gpu, kc, vc, n_ctx, n_kv):
+    c = ops.KVCache(n_ctx, n_kv, HD, device=gpu)
+    c.k[:kc.size] = torch.from_numpy(kc).to(gpu)
+    c.v[:vc.size] = torch.from_numpy(vc).to(gpu)
+    return c
+
+
+@pytest.mark.parametrize("n_kv,pos", [(8, 0), (8, 4096), (1, 77), (2, 1000)])
+def test_kv_write_bit_exact(gpu, orc, n_kv, pos):
+    print(f"kv_write n_kv={n_kv} pos={pos}", flush=True)
+    n_ctx = pos + 3
+    cache = ops.KVCache(n_ctx, n_kv, HD, device=gpu)
+    rng = np.random.default_rng(pos + n_kv)
+    k = (rng.standard_normal(n_kv * HD) * 3).astype(np.float32)
+    v = rng.standard_normal(n_kv * HD).astype(np.float32)
+    k[:32] = 0.0  # an all-zero block
+    cache.write(torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu), pos)
+    torch.cuda.synchronize()
+    pb = cache.pos_bytes
+    kc = cache.k.cpu().numpy()
+    vc = cache.v.cpu().numpy()
+    assert np.array_equal(kc[pos * pb:(pos + 1) * pb], orc.kv_quantize_row(k))
+    assert np.array_equal(vc[pos * pb:(pos + 1) * pb], orc.kv_quantize_row(v))
+    # nothing else written
+    assert not kc[:pos * pb].any() and not kc[(pos + 1) * pb:].any()
+    # device-side position
+    dpos = torch.tensor([pos + 1], dtype=torch.int32, device=gpu)
+    cache.write(torch.from_numpy(v).to(gpu), torch.from_numpy(k).to(gpu), dpos)
+    torch.cuda.synchronize()
+    assert np.array_equal(cache.k.cpu().numpy()[(pos + 1) * pb:(pos + 2) * pb], orc.kv_quantize_row(v))
+
+
+CASES = [
+    # n_head, n_kv, pos, cc_start
+    (32, 8, 4096, 0),    # config 4: 4097 keys, GQA 4
+    (32, 8, 0, 0),       # one key
+    (32, 8, 63, 0),      # exactly one tile
+    (32, 8, 64, 0),      # one tile + one
+    (32, 8, 1000, 900),  # sliding window start
+    (8, 8, 513, 0),      # MHA
+    (16, 8, 2000, 0),    # GQA 2
+    (64, 8, 3000, 0),    # GQA 8
+    (32, 8, 20000, 0),   # long context: several tiles per split
+]
+
+
+@pytest.mark.parametrize("n_head,n_kv,pos,cc_start", CASES)
+def test_attention_vs_oracle(gpu, orc, n_head, n_kv, pos, cc_start):
+    print(f"attn n_head={n_head} n_kv={n_kv} pos={pos} cc_start={cc_start}", flush=True)
+    kc, vc = host_cache(orc, pos + 1, n_kv, seed=pos + n_head)
+    q = np.random.default_rng(pos + 7).standard_normal(n_head * HD).astype(np.float32)
+    cache = device_cache(gpu, kc, vc, pos + 5, n_kv)
+    out = ops.attention_decode(torch.from_numpy(q).to(gpu), cache, n_head, pos, cc_start).cpu().numpy()
+    want = orc.attn_decode(q, kc, vc, n_head, n_kv, HD, cc_start, pos)
+    e = rel(out, want)
+    print(f"  rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    if pos <= 4096:
+        w64 = orc.attn_decode(q, kc, vc, n_head, n_kv, HD, cc_start, pos, f64=True)
+        assert rel(out, w64) <= TOL
+    # per head: no head may be wrong even if the norm hides it
+    for h in range(n_head):
+        assert rel(out[h * HD:(h + 1) * HD], want[h * HD:(h + 1) * HD]) <= 10 * TOL
+
+
+def test_attention_device_pos_graph(gpu, orc):
+    """Position in device memory, captured once in a HIP graph and replayed for
+    successive positions: every replay matches the eager call and the oracle."""
+    n_head, n_kv, n_ctx = 32, 8, 700
+    kc, vc = host_cache(orc, n_ctx, n_kv, seed=11)
+    cache = device_cache(gpu, kc, vc, n_ctx, n_kv)
+    q = torch.from_numpy(np.random.default_rng(12).standard_normal(n_head * HD).astype(np.float32)).to(gpu)
+    dpos = torch.zeros(1, dtype=torch.int32, device=gpu)
+    work = ops.attn_workspace(n_head, n_kv, HD, n_ctx, gpu)
+    out = torch.empty(n_head * HD, dtype=torch.float32, device=gpu)
+    ops.attention_decode(q, cache, n_head, dpos, out=out, work=work)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.attention_decode(q, cache, n_head, dpos, out=out, work=work)
+    qh = q.cpu().numpy()
+    for pos in (5, 64, 300, 699, 128):
+        dpos.fill_(pos)
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        eager = ops.attention_decode(q, cache, n_head, pos).cpu().numpy()
+        want = orc.attn_decode(qh, kc, vc, n_head, n_kv, HD, 0, pos)
+        print(f"  replay pos={pos}: rel err {rel(got, want):.3e}", flush=True)
+        assert rel(got, want) <= TOL
+        assert rel(got, eager) <= 1e-6
+
+
+def test_attention_unsupported(gpu):
+    n = ctypes_size()
+    lib = _lib.load()
+    assert lib.dq_attn_workspace_bytes(32, 8, 64, 100, n) == -2   # hd 64
+    assert lib.dq_attn_workspace_bytes(24, 8, 128, 100, n) == -2  # 3 heads per KV head
+    assert lib.dq_attn_workspace_bytes(30, 8, 128, 100, n) == -2  # not a multiple
+
+
+def ctypes_size():
+    import ctypes
+    return ctypes.byref(ctypes.c_size_t(0))
