@@ -289,7 +289,8 @@ __device__ __forceinline__ void load_group(typename Fmt<FMT>::W (&wr)[R][NIT], c
 template <int FMT, int R, int NIT, int KS>
 __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R][NIT], const XItem (&X)[NIT], int g,
                                               int rows, int i0, int i1, int lane, int ks, float (*part)[R][4],
-                                              int buf, float* __restrict__ y) {
+                                              int buf, float* __restrict__ y,
+                                              const float* __restrict__ res) {
     float acc[R];
 #pragma unroll
     for (int rr = 0; rr < R; ++rr) {
@@ -307,14 +308,17 @@ __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R
     if constexpr (KS == 1) {
         if ((lane & (GROUP - 1)) == 0) {
             const int r = g * R + lane / GROUP;
-            if (r < rows) y[r] = s;
+            if (r < rows) y[r] = res ? s + res[r] : s;
         }
     } else {
         if ((lane & (GROUP - 1)) == 0) part[buf][lane / GROUP][ks] = s;
         __syncthreads();
         if (ks == 0 && lane < R) {
             const int r = g * R + lane;
-            if (r < rows) y[r] = ((part[buf][lane][0] + part[buf][lane][1]) + part[buf][lane][2]) + part[buf][lane][3];
+            if (r < rows) {
+                const float v = ((part[buf][lane][0] + part[buf][lane][1]) + part[buf][lane][2]) + part[buf][lane][3];
+                y[r] = res ? v + res[r] : v;
+            }
         }
     }
 }
@@ -327,7 +331,8 @@ __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R
 template <int FMT, int R, int NIT, int KS>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w, DqLayout L, int rows, int items,
                                                    const int8_t* __restrict__ xq, const float* __restrict__ xs,
-                                                   const int32_t* __restrict__ xsum, float* __restrict__ y) {
+                                                   const int32_t* __restrict__ xsum, float* __restrict__ y,
+                                                   const float* __restrict__ res) {
     using W = typename Fmt<FMT>::W;
     __shared__ float part[2][R][4];
     const int lane = threadIdx.x & (DQ_WAVE - 1);
@@ -351,11 +356,11 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w
     // Two-deep pipeline, unrolled by two so the buffers never move.
     for (;;) {
         load_group<FMT, R, NIT>(b1, w, L, g + stride, ngroups, rows, i0, i1, lane, dummy);
-        compute_group<FMT, R, NIT, KS>(b0, X, g, rows, i0, i1, lane, ks, part, 0, y);
+        compute_group<FMT, R, NIT, KS>(b0, X, g, rows, i0, i1, lane, ks, part, 0, y, res);
         g += stride;
         if (g >= ngroups) break;
         load_group<FMT, R, NIT>(b0, w, L, g + stride, ngroups, rows, i0, i1, lane, dummy);
-        compute_group<FMT, R, NIT, KS>(b1, X, g, rows, i0, i1, lane, ks, part, 1, y);
+        compute_group<FMT, R, NIT, KS>(b1, X, g, rows, i0, i1, lane, ks, part, 1, y, res);
         g += stride;
         if (g >= ngroups) break;
     }
@@ -382,35 +387,35 @@ int env_int(const char* name, int dflt) {
 
 template <int FMT, int R, int NIT, int KS>
 int launch(const uint8_t* w, const DqLayout& L, int rows, int items, const int8_t* xq, const float* xs,
-           const int32_t* xsum, float* y, hipStream_t s) {
+           const int32_t* xsum, float* y, const float* res, hipStream_t s) {
     static const int wpc = env_int("DQ_GEMV_WPC", 8);  // persistent waves per CU
     const int ngroups = (rows + R - 1) / R;
     const int units = KS == 1 ? (ngroups + 3) / 4 : ngroups;
     const int max_wg = max(1, num_cus() * wpc / 4);
     const int iters = (units + max_wg - 1) / max_wg;  // balance: every workgroup walks `iters` units
     const unsigned grid = (unsigned)((units + iters - 1) / iters);
-    gemv_kernel<FMT, R, NIT, KS><<<grid, 256, 0, s>>>(w, L, rows, items, xq, xs, xsum, y);
+    gemv_kernel<FMT, R, NIT, KS><<<grid, 256, 0, s>>>(w, L, rows, items, xq, xs, xsum, y, res);
     return dq_launch_status();
 }
 
 template <int FMT, int R, int KS>
 int launch_nit(int nit, const uint8_t* w, const DqLayout& L, int rows, int items, const int8_t* xq,
-               const float* xs, const int32_t* xsum, float* y, hipStream_t s) {
+               const float* xs, const int32_t* xsum, float* y, const float* res, hipStream_t s) {
     switch (nit) {
-    case 1: return launch<FMT, R, 1, KS>(w, L, rows, items, xq, xs, xsum, y, s);
-    case 2: return launch<FMT, R, 2, KS>(w, L, rows, items, xq, xs, xsum, y, s);
-    case 3: return launch<FMT, R, 3, KS>(w, L, rows, items, xq, xs, xsum, y, s);
-    case 4: return launch<FMT, R, 4, KS>(w, L, rows, items, xq, xs, xsum, y, s);
+    case 1: return launch<FMT, R, 1, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
+    case 2: return launch<FMT, R, 2, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
+    case 3: return launch<FMT, R, 3, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
+    case 4: return launch<FMT, R, 4, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
     default:
-        if (nit <= 6) return launch<FMT, R, 6, KS>(w, L, rows, items, xq, xs, xsum, y, s);
-        if (nit <= 8) return launch<FMT, R, 8, KS>(w, L, rows, items, xq, xs, xsum, y, s);
+        if (nit <= 6) return launch<FMT, R, 6, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
+        if (nit <= 8) return launch<FMT, R, 8, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
         return DQ_ERR_NOT_SUPPORTED;
     }
 }
 
 template <int FMT>
 int launch_fmt(const uint8_t* w, const DqLayout& L, size_t rows, size_t cols, const int8_t* xq, const float* xs,
-               const int32_t* xsum, float* y, hipStream_t s) {
+               const int32_t* xsum, float* y, const float* res, hipStream_t s) {
     const int items = (int)(cols / 64);
     // K split: rows wider than 128 items are shared by the 4 waves of a workgroup
     int ks = env_int("DQ_GEMV_KS", 0);
@@ -424,19 +429,21 @@ int launch_fmt(const uint8_t* w, const DqLayout& L, size_t rows, size_t cols, co
     if (nit > 4 && r > 1) r = 1;
     const int R_ = r;
     if (ks == 1) {
-        if (R_ == 1) return launch_nit<FMT, 1, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
-        if (R_ == 2) return launch_nit<FMT, 2, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
-        return launch_nit<FMT, 4, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
+        if (R_ == 1) return launch_nit<FMT, 1, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
+        if (R_ == 2) return launch_nit<FMT, 2, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
+        return launch_nit<FMT, 4, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
     }
-    if (R_ == 1) return launch_nit<FMT, 1, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
-    if (R_ == 2) return launch_nit<FMT, 2, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
-    return launch_nit<FMT, 4, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, s);
+    if (R_ == 1) return launch_nit<FMT, 1, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
+    if (R_ == 2) return launch_nit<FMT, 2, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
+    return launch_nit<FMT, 4, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
 }
 
 }  // namespace
 
-extern "C" int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
-                       const float* d_xscale, const int32_t* d_xsum, float* d_y, void* stream) {
+namespace {
+
+int gemv_dispatch(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq, const float* d_xscale,
+                  const int32_t* d_xsum, const float* d_res, float* d_y, void* stream) {
     DqLayout L;
     if (!dq_layout(fmt, rows, cols, &L)) return DQ_ERR_NOT_SUPPORTED;
     if (rows == 0) return DQ_OK;
@@ -446,10 +453,24 @@ extern "C" int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const
     const uint8_t* w = (const uint8_t*)d_w;
     hipStream_t s = (hipStream_t)stream;
     switch (fmt) {
-    case DQ_FMT_Q8_0: return launch_fmt<DQ_FMT_Q8_0>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, s);
-    case DQ_FMT_Q4_0: return launch_fmt<DQ_FMT_Q4_0>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, s);
-    case DQ_FMT_Q4_K: return launch_fmt<DQ_FMT_Q4_K>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, s);
-    case DQ_FMT_Q6_K: return launch_fmt<DQ_FMT_Q6_K>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, s);
+    case DQ_FMT_Q8_0: return launch_fmt<DQ_FMT_Q8_0>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, d_res, s);
+    case DQ_FMT_Q4_0: return launch_fmt<DQ_FMT_Q4_0>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, d_res, s);
+    case DQ_FMT_Q4_K: return launch_fmt<DQ_FMT_Q4_K>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, d_res, s);
+    case DQ_FMT_Q6_K: return launch_fmt<DQ_FMT_Q6_K>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, d_res, s);
     }
     return DQ_ERR_NOT_SUPPORTED;
+}
+
+}  // namespace
+
+extern "C" int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
+                       const float* d_xscale, const int32_t* d_xsum, float* d_y, void* stream) {
+    return gemv_dispatch(fmt, d_w, rows, cols, d_xq, d_xscale, d_xsum, nullptr, d_y, stream);
+}
+
+extern "C" int dq_gemv_add(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
+                           const float* d_xscale, const int32_t* d_xsum, const float* d_res, float* d_y,
+                           void* stream) {
+    if (!d_res) return DQ_ERR_INVALID_ARG;
+    return gemv_dispatch(fmt, d_w, rows, cols, d_xq, d_xscale, d_xsum, d_res, d_y, stream);
 }

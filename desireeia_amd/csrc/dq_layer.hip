@@ -1,0 +1,380 @@
+// dq_layer.hip - one Llama-style decoder layer at batch 1 on the device
+// (the plain dense branch of models/dense_forward.cpp:3897-4257: RMSNorm,
+// Q/K/V, NeoX RoPE, Q8_0 KV write, GQA attention, output projection and
+// residual, RMSNorm, gated SiLU FFN and residual), plus the small fused
+// kernels it needs between the GEMVs:
+//
+//   norm_quant   (residual add +) RMSNorm + the per-256 activation quantizer
+//                of the K-quant GEMVs (core/matmul.cpp:1660-1778)
+//   rope_kv      NeoX RoPE of q and k from the caller's cos/sin table, and the
+//                Q8_0 rows of k and v written into the cache
+//   silu_quant   silu(gate) * up + the per-256 quantizer (input of ffn_down)
+//
+// Every float operation follows the reference's order and rounding, without
+// contraction (the file is built with -ffp-contract=off): the normalised
+// activations, rotated q/k and the cache bytes are those of the reference
+// given the same GEMV outputs.
+#include <math.h>
+
+#include "dq_common.h"
+
+
+namespace {
+
+// ------------------------------------------------------------ norm_quant --
+// h = a (+ b); y = h * (1/sqrtf(mean(h^2) + eps)) * w (models/dense_forward.cpp
+// :129-165: squares in float, summed in double); then per 256 values
+// amax, d = amax/127, id = 127/amax, q = rint(y*id) (core/matmul.cpp:1681-1700),
+// d replicated into the 8 per-32 slots, int32 sum of q per 32.
+// One workgroup of 256 threads; thread t owns chunks of 16 values.
+constexpr int NQ_T = 256;
+
+__global__ __launch_bounds__(NQ_T) void norm_quant_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                          float* __restrict__ h_out, const float* __restrict__ w,
+                                                          int n, float eps, int8_t* __restrict__ q,
+                                                          float* __restrict__ scale, int32_t* __restrict__ isum) {
+    __shared__ double wsum[NQ_T / 64];
+    __shared__ float s_scale;
+    const int t = threadIdx.x;
+    const int n_chunks = n / 16;
+    double acc = 0.0;
+    for (int c = t; c < n_chunks; c += NQ_T) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float4 x = reinterpret_cast<const float4*>(a + c * 16)[i];
+            if (b) {
+                const float4 y = reinterpret_cast<const float4*>(b + c * 16)[i];
+                x.x = x.x + y.x, x.y = x.y + y.y, x.z = x.z + y.z, x.w = x.w + y.w;
+                if (h_out) reinterpret_cast<float4*>(h_out + c * 16)[i] = x;
+            }
+            const float s0 = x.x * x.x, s1 = x.y * x.y, s2 = x.z * x.z, s3 = x.w * x.w;
+            acc += (double)s0;
+            acc += (double)s1;
+            acc += (double)s2;
+            acc += (double)s3;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, DQ_WAVE);
+    if ((t & 63) == 0) wsum[t >> 6] = acc;
+    __syncthreads();
+    if (t == 0) {
+        double s = 0.0;
+        for (int i = 0; i < NQ_T / 64; ++i) s += wsum[i];
+        s_scale = 1.0f / sqrtf((float)(s / (double)n) + eps);
+    }
+    __syncthreads();
+    const float sc = s_scale;
+    // 16 threads per 256-value block: chunks c = 16k .. 16k+15 belong to block k
+    for (int c0 = 0; c0 < n_chunks; c0 += NQ_T) {
+        const int c = c0 + t;
+        const bool live = c < n_chunks;
+        float y[16];
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float4 x = make_float4(0.f, 0.f, 0.f, 0.f), ww = x;
+            if (live) {
+                x = reinterpret_cast<const float4*>(a + c * 16)[i];
+                if (b) {
+                    const float4 yb = reinterpret_cast<const float4*>(b + c * 16)[i];
+                    x.x = x.x + yb.x, x.y = x.y + yb.y, x.z = x.z + yb.z, x.w = x.w + yb.w;
+                }
+                ww = reinterpret_cast<const float4*>(w + c * 16)[i];
+            }
+            y[4 * i + 0] = x.x * sc * ww.x;
+            y[4 * i + 1] = x.y * sc * ww.y;
+            y[4 * i + 2] = x.z * sc * ww.z;
+            y[4 * i + 3] = x.w * sc * ww.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(y[i]));
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, DQ_WAVE));
+        const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+        const float id = d > 0.0f ? 127.0f / amax : 0.0f;
+        int s = 0;
+        uint32_t pk[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                int iv = (int)rintf(y[4 * i + k] * id);
+                iv = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
+                s += iv;
+                word |= (uint32_t)(iv & 0xFF) << (8 * k);
+            }
+            pk[i] = word;
+        }
+        s += __shfl_xor(s, 1, DQ_WAVE);  // two chunks per 32-value block
+        if (live) {
+            *reinterpret_cast<dq_u32x4*>(q + c * 16) = dq_u32x4{pk[0], pk[1], pk[2], pk[3]};
+            if ((c & 1) == 0) {
+                scale[c / 2] = d;
+                isum[c / 2] = s;
+            }
+        }
+    }
+}
+
+// --------------------------------------------------------------- rope_kv --
+// Workgroup r < n_head: query head r; n_head <= r < n_head + n_kv: key head;
+// then value heads. 64 threads; thread j handles dims j and j + 64 of the
+// 128-dim head. RoPE (models/dense_forward.cpp:668-680) on the first n_rot
+// dims: pairs (j, j + n_rot/2), x0*c - x1*s and x0*s + x1*c with (c, s) =
+// table[2j], table[2j+1]. Keys and values are then quantized (kv_quantize_row).
+__global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q, const float* __restrict__ k,
+                                                     const float* __restrict__ v, const float* __restrict__ rope,
+                                                     int n_head, int n_kv, int n_rot, uint8_t* __restrict__ kc,
+                                                     uint8_t* __restrict__ vc, size_t pos_bytes, int pos_host,
+                                                     const int* __restrict__ pos_dev, int n_ctx) {
+    constexpr int HD = 128;
+    const int r = blockIdx.x, j = threadIdx.x;
+    const int kind = r < n_head ? 0 : (r < n_head + n_kv ? 1 : 2);
+    const int head = kind == 0 ? r : (kind == 1 ? r - n_head : r - n_head - n_kv);
+    const float* src = kind == 0 ? q + (size_t)head * HD : (kind == 1 ? k : v) + (size_t)head * HD;
+    float lo = src[j], hi = src[j + 64];
+    if (kind < 2 && rope) {
+        // n_rot = 128: pair (j, j+64); n_rot < 128: pairs inside [0, n_rot)
+        const int half = n_rot / 2;
+        if (n_rot == HD) {
+            const float c = rope[2 * j], s = rope[2 * j + 1];
+            const float x0 = lo, x1 = hi;
+            lo = x0 * c - x1 * s;
+            hi = x0 * s + x1 * c;
+        } else {
+            __shared__ float row[HD];
+            row[j] = lo;
+            row[j + 64] = hi;
+            __syncthreads();
+            if (j < half) {
+                const float c = rope[2 * j], s = rope[2 * j + 1];
+                const float x0 = row[j], x1 = row[j + half];
+                row[j] = x0 * c - x1 * s;
+                row[j + half] = x0 * s + x1 * c;
+            }
+            __syncthreads();
+            lo = row[j];
+            hi = row[j + 64];
+        }
+    }
+    if (kind == 0) {
+        q[(size_t)head * HD + j] = lo;
+        q[(size_t)head * HD + j + 64] = hi;
+        return;
+    }
+    // Q8_0 row: lanes 0-31 hold blocks 0 (lo) and 2 (hi), lanes 32-63 blocks 1 and 3
+    float alo = fabsf(lo), ahi = fabsf(hi);
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) {
+        alo = fmaxf(alo, __shfl_xor(alo, off, DQ_WAVE));
+        ahi = fmaxf(ahi, __shfl_xor(ahi, off, DQ_WAVE));
+    }
+    int p = pos_dev ? *pos_dev : pos_host;
+    p = p < 0 ? 0 : (p >= n_ctx ? n_ctx - 1 : p);
+    uint8_t* row = (kind == 1 ? kc : vc) + (size_t)p * pos_bytes + (size_t)head * (HD / 32) * DQ_SZ_Q8_0;
+    const int blo = j >> 5, bhi = blo + 2, i = j & 31;
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+        const float amax = part ? ahi : alo;
+        const float x = part ? hi : lo;
+        const int blk = part ? bhi : blo;
+        const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        int iv = (int)rintf(x * id);
+        iv = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
+        uint8_t* bp = row + blk * DQ_SZ_Q8_0;
+        bp[2 + i] = (uint8_t)(iv & 0xFF);
+        if (i == 0) *reinterpret_cast<uint16_t*>(bp) = dq_f2h(d);
+    }
+}
+
+// ------------------------------------------------------------ silu_quant --
+// h = silu(gate) * up, silu(x) = x / (1 + expf(-x)) (models/dense_forward.cpp
+// :53-55, :4230-4235); then the per-256 quantizer. One wave per 256 values,
+// 4 per lane.
+__global__ __launch_bounds__(256) void silu_quant_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                         int n, int8_t* __restrict__ q, float* __restrict__ scale,
+                                                         int32_t* __restrict__ isum) {
+    const int lane = threadIdx.x & 63;
+    const int blk = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk * 256 >= n) return;  // uniform per wave
+    const int e0 = blk * 256 + lane * 4;
+    const float4 g = *reinterpret_cast<const float4*>(gate + e0);
+    const float4 u = *reinterpret_cast<const float4*>(up + e0);
+    float hv[4] = {g.x, g.y, g.z, g.w};
+    const float uv[4] = {u.x, u.y, u.z, u.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float x = hv[i];
+        hv[i] = x / (1.0f + expf(-x)) * uv[i];
+        amax = fmaxf(amax, fabsf(hv[i]));
+    }
+    amax = dq_wave_max(amax);
+    const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+    const float id = d > 0.0f ? 127.0f / amax : 0.0f;
+    int s = 0;
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int iv = (int)rintf(hv[i] * id);
+        iv = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
+        s += iv;
+        word |= (uint32_t)(iv & 0xFF) << (8 * i);
+    }
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) s += __shfl_xor(s, off, DQ_WAVE);  // 8 lanes = 32 values
+    *reinterpret_cast<uint32_t*>(q + e0) = word;
+    if ((lane & 7) == 0) {
+        scale[e0 / 32] = d;
+        isum[e0 / 32] = s;
+    }
+}
+
+// ------------------------------------------------------------- workspace --
+struct LayerWs {
+    int8_t* aq;
+    float* as;
+    int32_t* ai;
+    float *q, *k, *v, *ao, *x2, *up, *gate;
+    void* attn;
+    size_t attn_bytes, total;
+};
+
+bool kquant(int fmt) { return fmt == DQ_FMT_Q4_K || fmt == DQ_FMT_Q6_K; }
+
+bool layer_ok(const dq_layer_t* L) {
+    if (!L || L->head_dim != 128 || L->n_head_kv == 0 || L->n_head % L->n_head_kv) return false;
+    if (L->n_embd == 0 || L->n_embd % 256 || L->n_ff == 0 || L->n_ff % 256 || (L->n_head * L->head_dim) % 256)
+        return false;
+    if (L->n_rot == 0 || L->n_rot > L->head_dim || L->n_rot % 2) return false;
+    const int f[7] = {L->fmt_q, L->fmt_k, L->fmt_v, L->fmt_o, L->fmt_gate, L->fmt_up, L->fmt_down};
+    for (int i = 0; i < 7; ++i)
+        if (!kquant(f[i])) return false;
+    return true;
+}
+
+LayerWs carve(const dq_layer_t* L, uint32_t n_ctx, uint8_t* base) {
+    const size_t E = L->n_embd, QD = (size_t)L->n_head * L->head_dim, KVD = (size_t)L->n_head_kv * L->head_dim;
+    const size_t F = L->n_ff;
+    const size_t AN = E > QD ? (E > F ? E : F) : (QD > F ? QD : F);
+    LayerWs w{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        uint8_t* p = base ? base + off : nullptr;
+        off += dq_align256(bytes);
+        return p;
+    };
+    w.aq = (int8_t*)take(AN);
+    w.as = (float*)take(AN / 32 * 4);
+    w.ai = (int32_t*)take(AN / 32 * 4);
+    w.q = (float*)take(QD * 4);
+    w.k = (float*)take(KVD * 4);
+    w.v = (float*)take(KVD * 4);
+    w.ao = (float*)take(QD * 4);
+    w.x2 = (float*)take(E * 4);
+    w.up = (float*)take(F * 4);
+    w.gate = (float*)take(F * 4);
+    size_t ab = 0;
+    dq_attn_workspace_bytes(L->n_head, L->n_head_kv, L->head_dim, n_ctx, &ab);
+    w.attn = take(ab);
+    w.attn_bytes = ab;
+    w.total = off;
+    return w;
+}
+
+#define DQ_TRY(x)                      \
+    do {                               \
+        const int rc_ = (x);           \
+        if (rc_ != DQ_OK) return rc_;  \
+    } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int dq_rope_cache(float* cache, uint32_t n_rot, uint32_t pos, float theta_base) {
+    // models/dense_forward.cpp:631-657 (rope_cache_init) without YaRN: theta_j =
+    // pos * theta_scale^j by repeated float products, theta_scale =
+    // powf(base, -2/n_rot). Host code: the same libm as the engine's.
+    if (!cache || n_rot == 0 || n_rot % 2) return DQ_ERR_INVALID_ARG;
+    const float theta_scale = powf(theta_base, -2.0f / (float)n_rot);
+    float theta = (float)pos;
+    for (uint32_t j = 0; j < n_rot / 2; ++j) {
+        cache[2 * j] = cosf(theta) * 1.0f;
+        cache[2 * j + 1] = sinf(theta) * 1.0f;
+        theta *= theta_scale;
+    }
+    return DQ_OK;
+}
+
+int dq_norm_quant(const float* d_a, const float* d_b, float* d_h, const float* d_w, size_t n, float eps,
+                  int8_t* d_q, float* d_scale, int32_t* d_isum, void* stream) {
+    if (!d_a || !d_w || !d_q || !d_scale || !d_isum || n == 0 || n % 256) return DQ_ERR_INVALID_ARG;
+    if (n > (1u << 26)) return DQ_ERR_NOT_SUPPORTED;
+    norm_quant_kernel<<<1, NQ_T, 0, (hipStream_t)stream>>>(d_a, d_b, d_h, d_w, (int)n, eps, d_q, d_scale, d_isum);
+    return dq_launch_status();
+}
+
+int dq_silu_quant(const float* d_gate, const float* d_up, size_t n, int8_t* d_q, float* d_scale, int32_t* d_isum,
+                  void* stream) {
+    if (!d_gate || !d_up || !d_q || !d_scale || !d_isum || n == 0 || n % 256) return DQ_ERR_INVALID_ARG;
+    const unsigned grid = (unsigned)((n / 256 + 3) / 4);
+    silu_quant_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(d_gate, d_up, (int)n, d_q, d_scale, d_isum);
+    return dq_launch_status();
+}
+
+int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float* d_rope, uint32_t n_head,
+                     uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
+                     const int32_t* d_pos, uint32_t n_ctx, void* stream) {
+    if (!d_q || !d_k || !d_v || !d_kc || !d_vc || n_ctx == 0) return DQ_ERR_INVALID_ARG;
+    if (hd != 128) return DQ_ERR_NOT_SUPPORTED;
+    if (d_rope && (n_rot == 0 || n_rot > hd || n_rot % 2)) return DQ_ERR_INVALID_ARG;
+    if (!d_pos && pos >= n_ctx) return DQ_ERR_INVALID_ARG;
+    const size_t pos_bytes = (size_t)n_head_kv * (hd / 32) * DQ_SZ_Q8_0;
+    rope_kv_kernel<<<n_head + 2 * n_head_kv, 64, 0, (hipStream_t)stream>>>(
+        d_q, d_k, d_v, d_rope, (int)n_head, (int)n_head_kv, (int)n_rot, (uint8_t*)d_kc, (uint8_t*)d_vc, pos_bytes,
+        (int)pos, d_pos, (int)n_ctx);
+    return dq_launch_status();
+}
+
+int dq_layer_workspace_bytes(const dq_layer_t* L, uint32_t n_ctx, size_t* bytes) {
+    if (!L || !bytes || n_ctx == 0) return DQ_ERR_INVALID_ARG;
+    if (!layer_ok(L)) return DQ_ERR_NOT_SUPPORTED;
+    *bytes = carve(L, n_ctx, nullptr).total;
+    return DQ_OK;
+}
+
+int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const float* d_rope, uint32_t pos,
+                    const int32_t* d_pos, uint32_t cc_start, void* d_kc, void* d_vc, uint32_t n_ctx, void* d_work,
+                    size_t work_bytes, void* stream) {
+    if (!L || !d_x || !d_x_out || !d_kc || !d_vc || !d_work || n_ctx == 0) return DQ_ERR_INVALID_ARG;
+    if (!layer_ok(L)) return DQ_ERR_NOT_SUPPORTED;
+    if (!d_pos && (pos >= n_ctx || cc_start > pos)) return DQ_ERR_INVALID_ARG;
+    const LayerWs w = carve(L, n_ctx, (uint8_t*)d_work);
+    if (work_bytes < w.total) return DQ_ERR_INVALID_ARG;
+    const size_t E = L->n_embd, QD = (size_t)L->n_head * L->head_dim, KVD = (size_t)L->n_head_kv * L->head_dim;
+    const size_t F = L->n_ff;
+    // attention block
+    DQ_TRY(dq_norm_quant(d_x, nullptr, nullptr, L->attn_norm, E, L->rms_eps, w.aq, w.as, w.ai, stream));
+    DQ_TRY(dq_gemv(L->fmt_q, L->wq, QD, E, w.aq, w.as, w.ai, w.q, stream));
+    DQ_TRY(dq_gemv(L->fmt_k, L->wk, KVD, E, w.aq, w.as, w.ai, w.k, stream));
+    DQ_TRY(dq_gemv(L->fmt_v, L->wv, KVD, E, w.aq, w.as, w.ai, w.v, stream));
+    DQ_TRY(dq_rope_kv_write(w.q, w.k, w.v, d_rope, L->n_head, L->n_head_kv, L->head_dim, L->n_rot, d_kc, d_vc, pos,
+                            d_pos, n_ctx, stream));
+    DQ_TRY(dq_attn_decode_q8(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos, n_ctx,
+                             w.ao, w.attn, w.attn_bytes, stream));
+    DQ_TRY(dq_quantize_act(DQ_ACT_Q8K_REP, w.ao, QD, 1, w.aq, w.as, w.ai, nullptr, stream));
+    DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.aq, w.as, w.ai, d_x, w.x2, stream));
+    // feed-forward block
+    DQ_TRY(dq_norm_quant(w.x2, nullptr, nullptr, L->ffn_norm, E, L->rms_eps, w.aq, w.as, w.ai, stream));
+    DQ_TRY(dq_gemv(L->fmt_up, L->wup, F, E, w.aq, w.as, w.ai, w.up, stream));
+    DQ_TRY(dq_gemv(L->fmt_gate, L->wgate, F, E, w.aq, w.as, w.ai, w.gate, stream));
+    DQ_TRY(dq_silu_quant(w.gate, w.up, F, w.aq, w.as, w.ai, stream));
+    DQ_TRY(dq_gemv_add(L->fmt_down, L->wdown, E, F, w.aq, w.as, w.ai, w.x2, d_x_out, stream));
+    return DQ_OK;
+}
+
+}  // extern "C"

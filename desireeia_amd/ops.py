@@ -202,3 +202,73 @@ def attention_decode(q, cache, n_head, pos, cc_start=0, out=None, work=None):
                                      hd, cc_start, 0 if dpos is not None else int(pos), _ptr(dpos), cache.n_ctx,
                                      _ptr(o), _ptr(wk), wk.numel(), _stream()), "dq_attn_decode_q8")
     return o
+
+
+class LayerDesc(ctypes.Structure):
+    """dq_layer_t of include/desireeia_hip.h."""
+    _fields_ = [("n_embd", ctypes.c_uint32), ("n_head", ctypes.c_uint32), ("n_head_kv", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("n_rot", ctypes.c_uint32), ("n_ff", ctypes.c_uint32),
+                ("rms_eps", ctypes.c_float),
+                ("fmt_q", ctypes.c_int), ("fmt_k", ctypes.c_int), ("fmt_v", ctypes.c_int), ("fmt_o", ctypes.c_int),
+                ("fmt_gate", ctypes.c_int), ("fmt_up", ctypes.c_int), ("fmt_down", ctypes.c_int),
+                ("wq", ctypes.c_void_p), ("wk", ctypes.c_void_p), ("wv", ctypes.c_void_p), ("wo", ctypes.c_void_p),
+                ("wgate", ctypes.c_void_p), ("wup", ctypes.c_void_p), ("wdown", ctypes.c_void_p),
+                ("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p)]
+
+
+def rope_cache(n_rot, pos, theta):
+    """Host cos/sin table of rope_cache_init (dq_rope_cache), as a CPU float tensor."""
+    lib = _lib.load()
+    out = torch.empty(n_rot, dtype=torch.float32)
+    _lib.check(lib.dq_rope_cache(ctypes.c_void_p(out.data_ptr()), n_rot, pos, theta), "dq_rope_cache")
+    return out
+
+
+class DecoderLayer:
+    """One decoder layer on the device (dq_layer_decode): packed weights,
+    norm weights and its Q8_0 KV cache. mats: dict name -> QuantMatrix for
+    q, k, v, o, gate, up, down."""
+
+    NAMES = ("q", "k", "v", "o", "gate", "up", "down")
+
+    def __init__(self, mats, attn_norm, ffn_norm, n_head, n_head_kv, head_dim, n_ctx, rms_eps=1e-5,
+                 rope_theta=500000.0, n_rot=None, device="cuda"):
+        self.mats = mats
+        self.attn_norm = attn_norm.to(device).float().contiguous()
+        self.ffn_norm = ffn_norm.to(device).float().contiguous()
+        self.n_embd = mats["q"].cols
+        self.n_head, self.n_head_kv, self.head_dim = n_head, n_head_kv, head_dim
+        self.n_ff = mats["up"].rows
+        self.n_rot = n_rot or head_dim
+        self.rope_theta = rope_theta
+        d = LayerDesc(self.n_embd, n_head, n_head_kv, head_dim, self.n_rot, self.n_ff, rms_eps)
+        for nm in self.NAMES:
+            setattr(d, "fmt_" + nm, mats[nm].fmt)
+            setattr(d, "w" + nm, mats[nm].buf.data_ptr())
+        d.attn_norm = self.attn_norm.data_ptr()
+        d.ffn_norm = self.ffn_norm.data_ptr()
+        self.desc = d
+        self.cache = KVCache(n_ctx, n_head_kv, head_dim, device)
+        lib = _lib.load()
+        n = ctypes.c_size_t(0)
+        _lib.check(lib.dq_layer_workspace_bytes(ctypes.byref(d), n_ctx, ctypes.byref(n)), "dq_layer_workspace_bytes")
+        self.work = torch.empty(max(n.value, 1), dtype=torch.uint8, device=device)
+        self.rope = torch.empty(self.n_rot, dtype=torch.float32, device=device)
+
+    def set_rope(self, pos):
+        self.rope.copy_(rope_cache(self.n_rot, pos, self.rope_theta))
+
+    def decode(self, x, pos, out=None, rope_ready=False, cc_start=0):
+        """x: device [n_embd]; pos: int (the RoPE table is rebuilt unless
+        rope_ready) or an int32 device tensor (then the caller keeps
+        self.rope in step with it)."""
+        lib = _lib.load()
+        y = out if out is not None else torch.empty_like(x)
+        dpos = pos if isinstance(pos, torch.Tensor) else None
+        if dpos is None and not rope_ready:
+            self.set_rope(int(pos))
+        _lib.check(lib.dq_layer_decode(ctypes.byref(self.desc), _ptr(x), _ptr(y), _ptr(self.rope),
+                                       0 if dpos is not None else int(pos), _ptr(dpos), cc_start,
+                                       _ptr(self.cache.k), _ptr(self.cache.v), self.cache.n_ctx, _ptr(self.work),
+                                       self.work.numel(), _stream()), "dq_layer_decode")
+        return y

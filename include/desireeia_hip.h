@@ -91,6 +91,11 @@ int dq_quantize_q8_1_blocks(const float* d_x, size_t n, void* d_blocks, void* st
  * d_xsum is required for Q4_0 and Q4_K. */
 int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
             const float* d_xscale, const int32_t* d_xsum, float* d_y, void* stream);
+/* The same GEMV with a residual: y = W x + res (res may alias y). The
+ * residual adds of the decoder layer (models/dense_forward.cpp, proj += x
+ * after the output projection, x_out = ffn_out + proj after ffn_down). */
+int dq_gemv_add(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
+                const float* d_xscale, const int32_t* d_xsum, const float* d_res, float* d_y, void* stream);
 
 /* Prefill GEMM y[n_tok][rows] = x[n_tok][cols] W^T for Q4_K and Q6_K, with the
  * semantics of matmul_q4_k_batch / matmul_q6_k_batch for n_tok >= 4 (the
@@ -132,6 +137,51 @@ int dq_attn_workspace_bytes(uint32_t n_head, uint32_t n_head_kv, uint32_t hd, ui
 int dq_attn_decode_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head, uint32_t n_head_kv,
                       uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx,
                       float* d_out, void* d_work, size_t work_bytes, void* stream);
+
+/* ------------------------------------------------------- decoder layer */
+
+/* rope_cache_init (models/dense_forward.cpp:631-657, no YaRN): host code,
+ * cache[2j] = cos(theta_j), cache[2j+1] = sin(theta_j), theta_j = pos *
+ * powf(base, -2/n_rot)^j by repeated float products. n_rot floats. */
+int dq_rope_cache(float* cache, uint32_t n_rot, uint32_t pos, float theta_base);
+
+/* Fused pieces of the layer (device pointers, stream-ordered):
+ * dq_norm_quant: h = a (+ b, written to d_h when both are given); rms_norm_vec
+ *   (models/dense_forward.cpp:129-165) with weight w, then the per-256
+ *   quantizer of the K-quant GEMVs (DQ_ACT_Q8K_REP). n % 256 == 0.
+ * dq_silu_quant: silu(gate) * up (:53-55), then the same quantizer.
+ * dq_rope_kv_write: NeoX RoPE (:668-680) of q (in place) and k with the
+ *   cos/sin table d_rope (dq_rope_cache; NULL = no RoPE), then the Q8_0 rows
+ *   of k and v into the caches at pos (as dq_kv_write). hd = 128. */
+int dq_norm_quant(const float* d_a, const float* d_b, float* d_h, const float* d_w, size_t n, float eps,
+                  int8_t* d_q, float* d_scale, int32_t* d_isum, void* stream);
+int dq_silu_quant(const float* d_gate, const float* d_up, size_t n, int8_t* d_q, float* d_scale, int32_t* d_isum,
+                  void* stream);
+int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float* d_rope, uint32_t n_head,
+                     uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
+                     const int32_t* d_pos, uint32_t n_ctx, void* stream);
+
+/* One Llama-style decoder layer at batch 1 on the device: the plain dense
+ * branch of models/dense_forward.cpp:3897-4257 (no biases, no QK-norm, no
+ * sandwich norms, gated SiLU FFN, Q8_0 KV cache) that cuda_layer_forward
+ * (core/engine.h:698-752) runs as one captured episode. Weights are packed
+ * device matrices (dq_weights_pack) of K-quant formats (Q4_K / Q6_K; others:
+ * -2), head_dim 128. x and x_out are device vectors of n_embd floats (they
+ * may not alias); d_rope is the device copy of dq_rope_cache(pos); the KV
+ * caches are those of dq_kv_write for this layer. d_pos as for dq_kv_write
+ * (graph replay). d_work: dq_layer_workspace_bytes(n_ctx) bytes. */
+typedef struct {
+    uint32_t n_embd, n_head, n_head_kv, head_dim, n_rot, n_ff;
+    float rms_eps;
+    int fmt_q, fmt_k, fmt_v, fmt_o, fmt_gate, fmt_up, fmt_down; /* DQ_FMT_* */
+    const void *wq, *wk, *wv, *wo, *wgate, *wup, *wdown;      /* packed device matrices */
+    const float *attn_norm, *ffn_norm;                        /* device, n_embd floats */
+} dq_layer_t;
+
+int dq_layer_workspace_bytes(const dq_layer_t* layer, uint32_t n_ctx, size_t* bytes);
+int dq_layer_decode(const dq_layer_t* layer, const float* d_x, float* d_x_out, const float* d_rope, uint32_t pos,
+                    const int32_t* d_pos, uint32_t cc_start, void* d_kc, void* d_vc, uint32_t n_ctx, void* d_work,
+                    size_t work_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -65,3 +65,23 @@ def test_gemv_unsupported_shapes(gpu):
     assert lib.dq_gemv(synth.FMT_Q8_0, None, 4, 96, None, None, None, None, None) == -2
     assert lib.dq_gemv(9, None, 4, 256, None, None, None, None, None) == -2
     assert lib.dq_gemv(synth.FMT_Q8_0, None, 0, 256, None, None, None, None, None) == 0
+
+
+def test_gemv_add_residual(gpu, orc):
+    """dq_gemv_add: y = W x + res, the residual adds of the decoder layer."""
+    for qtype, rows, cols in ((synth.Q4_K, 4096, 4096), (synth.Q6_K, 4096, 14336)):
+        w = synth.gen_weights(qtype, rows, cols, seed=rows + cols)
+        x = synth.gen_act(cols, seed=3)
+        res = np.random.default_rng(4).standard_normal(rows).astype(np.float32) * 100
+        m = ops.QuantMatrix.from_gguf(qtype, w, rows, cols)
+        act = ops.quantize_act(torch.from_numpy(x).to(gpu), ops.act_kind_for(m.fmt))
+        rd = torch.from_numpy(res).to(gpu)
+        y = torch.empty(rows, dtype=torch.float32, device=gpu)
+        lib = _lib.load()
+        _lib.check(lib.dq_gemv_add(m.fmt, ops._ptr(m.buf), rows, cols, ops._ptr(act.q), ops._ptr(act.scale),
+                                   ops._ptr(act.isum), ops._ptr(rd), ops._ptr(y), ops._stream()))
+        plain = ops.gemv(m, act)
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy(), plain.cpu().numpy() + res)
+        want = orc.matmul(qtype, w, rows, cols, x) + res
+        assert rel(y.cpu().numpy(), want) <= TOL

@@ -1,0 +1,175 @@
+"""One Llama-style decoder layer on the GPU (dq_layer_decode) against the
+oracle's composition of the reference layer (models/dense_forward.cpp
+:3897-4257): layer output within 1e-3 norm-wise, the KV rows written at pos
+within the Q8_0 step of the oracle's, and the fused pieces (norm+quantize,
+silu+quantize, RoPE+KV write) bit-exact against the oracle on the same
+inputs."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from desireeia_amd import _lib, ops, synth
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+Q4K, Q6K = synth.Q4_K, synth.Q6_K
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed):
+    from oracle.oracle import LayerArgs
+    hd = 128
+    qd, kvd = n_head * hd, n_kv * hd
+    # Q4_K_M mix: Q4_K everywhere but attn_v and ffn_down (Q6_K)
+    shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
+              "gate": (Q4K, F, E), "up": (Q4K, F, E), "down": (Q6K, E, F)}
+    gg = {nm: (qt, synth.gen_weights(qt, r, c, seed=seed + i)) for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
+    rng = np.random.default_rng(seed)
+    attn_norm = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+    ffn_norm = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+    mats = {nm: ops.QuantMatrix.from_gguf(qt, w, shapes[nm][1], shapes[nm][2], device=gpu)
+            for nm, (qt, w) in gg.items()}
+    layer = ops.DecoderLayer(mats, torch.from_numpy(attn_norm), torch.from_numpy(ffn_norm), n_head, n_kv, hd, n_ctx,
+                             device=gpu)
+    # prior cache: N(0,1) rows quantized (kv_quantize_row)
+    pb = layer.cache.pos_bytes
+    kc = np.zeros(n_ctx * pb, np.uint8)
+    vc = np.zeros(n_ctx * pb, np.uint8)
+    if n_prior:
+        kc[:n_prior * pb] = orc.kv_quantize_row(rng.standard_normal(n_prior * kvd).astype(np.float32))
+        vc[:n_prior * pb] = orc.kv_quantize_row(rng.standard_normal(n_prior * kvd).astype(np.float32))
+    layer.cache.k.copy_(torch.from_numpy(kc))
+    layer.cache.v.copy_(torch.from_numpy(vc))
+    args = LayerArgs(E, n_head, n_kv, hd, F, 1e-5, 500000.0, Q4K, Q4K, Q6K, Q4K, Q4K, Q4K, Q6K)
+    keep = {nm: np.ascontiguousarray(w) for nm, (qt, w) in gg.items()}
+    keep["attn_norm"], keep["ffn_norm"] = attn_norm, ffn_norm
+    for nm in ("q", "k", "v", "o", "gate", "up", "down"):
+        setattr(args, "w" + nm, keep[nm].ctypes.data)
+    args.attn_norm = attn_norm.ctypes.data
+    args.ffn_norm = ffn_norm.ctypes.data
+    return layer, args, keep, kc, vc
+
+
+def dequant_rows(orc, b, n):
+    return orc.dequantize_row(synth.Q8_0, np.ascontiguousarray(b), n)
+
+
+@pytest.mark.parametrize("E,n_head,n_kv,F,pos", [
+    (4096, 32, 8, 14336, 4096),   # config 4: Llama-3-8B layer, 4096 prior tokens
+    (512, 4, 2, 1024, 0),         # first token
+    (512, 8, 2, 1536, 70),        # GQA 4, two tiles
+])
+def test_layer_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos):
+    print(f"layer E={E} heads={n_head}/{n_kv} F={F} pos={pos}", flush=True)
+    n_ctx = pos + 2
+    layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos, seed=E + pos)
+    x = np.random.default_rng(pos + 1).standard_normal(E).astype(np.float32)
+    want, q, k, v, ao = orc.layer_decode(args, kc, vc, pos, x)
+    got = layer.decode(torch.from_numpy(x).to(gpu), pos).cpu().numpy()
+    e = rel(got, want)
+    print(f"  layer rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    # the K/V rows written at pos: the same Q8_0 rows up to GEMV rounding
+    pb = layer.cache.pos_bytes
+    kd = layer.cache.k.cpu().numpy()
+    vd = layer.cache.v.cpu().numpy()
+    kvd = n_kv * 128
+    for dev, host in ((kd, kc), (vd, vc)):
+        assert np.array_equal(dev[:pos * pb], host[:pos * pb])  # prior rows untouched
+        a = dequant_rows(orc, dev[pos * pb:(pos + 1) * pb], kvd)
+        b = dequant_rows(orc, host[pos * pb:(pos + 1) * pb], kvd)
+        assert rel(a, b) <= TOL
+
+
+def test_layer_graph_replay(gpu, orc):
+    """The layer captured once with a device-side position and replayed for
+    consecutive tokens (position and RoPE table updated between replays)
+    matches eager calls on an identical layer."""
+    E, n_head, n_kv, F, n_ctx = 512, 8, 2, 1024, 40
+    la, _, _, _, _ = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, 20, seed=9)
+    lb, _, _, _, _ = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, 20, seed=9)
+    dpos = torch.tensor([20], dtype=torch.int32, device=gpu)
+    x = torch.from_numpy(np.random.default_rng(3).standard_normal(E).astype(np.float32)).to(gpu)
+    y = torch.empty_like(x)
+    la.set_rope(20)
+    la.decode(x, dpos, out=y)  # warm-up (writes position 20, rewritten below)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        la.decode(x, dpos, out=y)
+    for pos in range(20, 26):
+        dpos.fill_(pos)
+        la.set_rope(pos)
+        g.replay()
+        want = lb.decode(x, pos)
+        torch.cuda.synchronize()
+        e = rel(y.cpu().numpy(), want.cpu().numpy())
+        print(f"  replay pos={pos}: rel {e:.3e}", flush=True)
+        assert e <= 1e-6
+    assert torch.equal(la.cache.k[:26 * la.cache.pos_bytes], lb.cache.k[:26 * lb.cache.pos_bytes])
+
+
+def test_norm_quant_bit_exact(gpu, orc):
+    lib = _lib.load()
+    rng = np.random.default_rng(4)
+    for n in (4096, 512, 14336):
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        w = (1 + 0.02 * rng.standard_normal(n)).astype(np.float32)
+        act = ops.empty_act((n,), ops.ACT_Q8K_REP, gpu)
+        xd, wd = torch.from_numpy(x).to(gpu), torch.from_numpy(w).to(gpu)
+        _lib.check(lib.dq_norm_quant(ops._ptr(xd), None, None, ops._ptr(wd), n, ctypes.c_float(1e-5),
+                                     ops._ptr(act.q), ops._ptr(act.scale), ops._ptr(act.isum), ops._stream()))
+        y = orc.rms_norm(x, w, 1e-5)
+        q, d, isum = orc.quantize_q8k_rep(y)
+        assert np.array_equal(act.q.cpu().numpy(), q)
+        assert np.array_equal(act.scale.cpu().numpy(), d)
+        assert np.array_equal(act.isum.cpu().numpy(), isum)
+
+
+def test_silu_quant_bit_exact(gpu, orc):
+    lib = _lib.load()
+    rng = np.random.default_rng(5)
+    n = 14336
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = (rng.standard_normal(n) * 4).astype(np.float32)
+    act = ops.empty_act((n,), ops.ACT_Q8K_REP, gpu)
+    gd, ud = torch.from_numpy(g).to(gpu), torch.from_numpy(u).to(gpu)  # kept alive until the kernel has run
+    _lib.check(lib.dq_silu_quant(ops._ptr(gd), ops._ptr(ud), n, ops._ptr(act.q), ops._ptr(act.scale),
+                                 ops._ptr(act.isum), ops._stream()))
+    torch.cuda.synchronize()
+    h = np.array([orc.L.dqo_silu(float(a)) for a in g], np.float32) * u
+    q, d, isum = orc.quantize_q8k_rep(h)
+    qg = act.q.cpu().numpy()
+    # expf may differ from the host's by one ulp: allow rare one-step flips
+    assert np.mean(qg != q) < 1e-3 and np.abs(qg.astype(int) - q).max() <= 1
+    assert np.allclose(act.scale.cpu().numpy(), d, rtol=1e-6)
+
+
+def test_rope_kv_write_bit_exact(gpu, orc):
+    n_head, n_kv, hd, pos, n_ctx = 32, 8, 128, 4096, 4097
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    k = rng.standard_normal(n_kv * hd).astype(np.float32)
+    v = rng.standard_normal(n_kv * hd).astype(np.float32)
+    cache = ops.KVCache(n_ctx, n_kv, hd, device=gpu)
+    rope = ops.rope_cache(hd, pos, 500000.0)
+    qd = torch.from_numpy(q).to(gpu)
+    kd, vd, rd = torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu), rope.to(gpu)
+    lib = _lib.load()
+    _lib.check(lib.dq_rope_kv_write(ops._ptr(qd), ops._ptr(kd), ops._ptr(vd), ops._ptr(rd), n_head, n_kv, hd, hd,
+                                    ops._ptr(cache.k), ops._ptr(cache.v), pos, None, n_ctx, ops._stream()))
+    torch.cuda.synchronize()
+    c = orc.rope_cache(hd, pos, 500000.0)
+    qr = np.concatenate([orc.rope_neox(q[h * hd:(h + 1) * hd], hd, c) for h in range(n_head)])
+    kr = np.concatenate([orc.rope_neox(k[h * hd:(h + 1) * hd], hd, c) for h in range(n_kv)])
+    assert np.array_equal(qd.cpu().numpy(), qr)
+    pb = cache.pos_bytes
+    assert np.array_equal(cache.k.cpu().numpy()[pos * pb:], orc.kv_quantize_row(kr))
+    assert np.array_equal(cache.v.cpu().numpy()[pos * pb:], orc.kv_quantize_row(v))
