@@ -31,6 +31,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0  # dense MFMA, MI355X
+INT8_PEAK_TOPS = 5000.0
 METRIC = "Q4_K/Q8_0 GEMV HBM GB/s (% of peak); prefill GEMM TFLOPS (% MFMA peak)"
 ROTATE_BYTES = 640 << 20  # >= 2x the 256 MB Infinity Cache
 
@@ -113,6 +115,88 @@ class GemmCase:
 
     def flops(self):
         return 2.0 * self.n_tok * self.rows * self.cols
+
+
+LAYER_WEIGHT_BYTES = 138903552   # config 4 Q4_K_M layer, GGUF bytes
+KV_READ_BYTES = 4097 * 8 * 136 * 2  # K and V rows of positions 0..4096
+
+
+class LayerCase:
+    """Config 4: Llama-style decoder layer (hidden 4096, 32/8 heads of 128,
+    FFN 14336, Q4_K_M mix) at position 4096 over a Q8_0 KV cache of 4096
+    prior N(0,1) tokens. n_layers distinct layers (weights copied, so every
+    byte comes from HBM) are chained like a model's layers; the position is a
+    device value, so the chain is one replayable graph."""
+
+    def __init__(self, dev, n_layers=4, pos=4096, seed=40):
+        import torch
+        from desireeia_amd import ops, synth
+        E, H, KV, HD, F = 4096, 32, 8, 128, 14336
+        shapes = {"q": (synth.Q4_K, H * HD, E), "k": (synth.Q4_K, KV * HD, E), "v": (synth.Q6_K, KV * HD, E),
+                  "o": (synth.Q4_K, E, H * HD), "gate": (synth.Q4_K, F, E), "up": (synth.Q4_K, F, E),
+                  "down": (synth.Q6_K, E, F)}
+        base = {nm: ops.QuantMatrix.from_gguf(qt, synth.gen_weights(qt, r, c, seed + i), r, c, device=dev)
+                for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
+        rng = np.random.default_rng(seed)
+        self.pos, self.n_ctx = pos, pos + 1
+        self.dpos = torch.tensor([pos], dtype=torch.int32, device=dev)
+        self.layers = []
+        for li in range(n_layers):
+            mats = base if li == 0 else {nm: m.clone() for nm, m in base.items()}
+            an = torch.from_numpy((1 + 0.02 * rng.standard_normal(E)).astype(np.float32))
+            fn = torch.from_numpy((1 + 0.02 * rng.standard_normal(E)).astype(np.float32))
+            L = ops.DecoderLayer(mats, an, fn, H, KV, HD, self.n_ctx, device=dev)
+            L.set_rope(pos)
+            kv = torch.randn(pos, 2, KV * HD, device=dev, generator=torch.Generator(device=dev).manual_seed(li))
+            for p in range(pos):
+                L.cache.write(kv[p, 0], kv[p, 1], p)
+            self.layers.append(L)
+        self.x = torch.from_numpy(synth.gen_act(E, seed + 99)).to(dev)
+        self.bufs = [torch.empty(E, dtype=torch.float32, device=dev) for _ in range(2)]
+        torch.cuda.synchronize()
+
+    def step(self):
+        x = self.x
+        for i, L in enumerate(self.layers):
+            y = self.bufs[i % 2]
+            L.decode(x, self.dpos, out=y)
+            x = y
+
+    def bytes_per_layer(self):
+        E, QD, F = 4096, 4096, 14336
+        # weights + KV rows read + the new KV row written + x in / out
+        return LAYER_WEIGHT_BYTES + KV_READ_BYTES + 2 * 1088 + 2 * E * 4
+
+
+class AttnCase:
+    """Decode attention alone at config 4's shape (32 query heads over 8 KV
+    heads of 128, positions 0..4096), caches rotated over >= 640 MB."""
+
+    def __init__(self, dev, pos=4096):
+        import torch
+        from desireeia_amd import ops
+        self.pos = pos
+        c0 = ops.KVCache(pos + 1, 8, 128, device=dev)
+        kv = torch.randn(pos + 1, 2, 1024, device=dev, generator=torch.Generator(device=dev).manual_seed(7))
+        for p in range(pos + 1):
+            c0.write(kv[p, 0], kv[p, 1], p)
+        ncopy = max(2, -(-ROTATE_BYTES // (2 * c0.k.numel())))
+        self.caches = [c0]
+        for _ in range(ncopy - 1):
+            c = ops.KVCache(pos + 1, 8, 128, device=dev)
+            c.k.copy_(c0.k)
+            c.v.copy_(c0.v)
+            self.caches.append(c)
+        self.q = torch.randn(32 * 128, device=dev)
+        self.out = torch.empty(32 * 128, device=dev)
+        self.work = ops.attn_workspace(32, 8, 128, pos + 1, dev)
+        self.i = 0
+
+    def kernel(self):
+        from desireeia_amd import ops
+        c = self.caches[self.i]
+        self.i = (self.i + 1) % len(self.caches)
+        ops.attention_decode(self.q, c, 32, self.pos, out=self.out, work=self.work)
 
 
 def graph_time(fn, calls_per_graph, reps, warmup_reps=2):
@@ -245,6 +329,16 @@ def main():
         log(f"{args.only}: gemm kernel {us:.1f} us = {g.flops() / us / 1e6:.1f} TFLOP/s; "
             f"quantize+gemm {us_step:.1f} us")
         return
+    if args.only == "layer":
+        lc = LayerCase(dev)
+        us = graph_time(lc.step, 1, max(1, args.steps // len(lc.layers))) / len(lc.layers)
+        log(f"layer: {us:.1f} us/layer, {lc.bytes_per_layer() / us / 1e3:.1f} GB/s")
+        return
+    if args.only == "attn":
+        ac = AttnCase(dev)
+        us = graph_time(ac.kernel, len(ac.caches), max(1, args.steps // len(ac.caches)))
+        log(f"attn: {us:.2f} us, {KV_READ_BYTES / us / 1e3:.1f} GB/s")
+        return
     if args.only:
         qt, r, c = shapes[args.only]
         case = GemvCase(qt, r, c, 11, dev)
@@ -281,6 +375,30 @@ def main():
         extra[k] = {"shape": f"{c.rows}x{c.cols}", "kernel_us": round(us, 3), "kernel_GBps": round(gbs, 1),
                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"{k}: {us:.2f} us  {gbs:.1f} GB/s  ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    # config 3: prefill GEMM (kernel alone; activations quantized beforehand)
+    for k, (qt, r, c, t) in gemm_shapes.items():
+        g = GemmCase(qt, r, c, t, 21, dev)
+        us = graph_time(g.kernel, 10, 5)
+        tf = g.flops() / us / 1e6
+        extra[k] = {"shape": f"{t}x{c} . {c}x{r}", "kernel_us": round(us, 2), "TFLOPs": round(tf, 1),
+                    "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4), "frac_int8_mfma": round(tf / INT8_PEAK_TOPS, 4)}
+        log(f"{k}: {us:.1f} us  {tf:.1f} TFLOP/s")
+        del g
+    # config 4: decode attention alone and the whole decoder layer
+    ac = AttnCase(dev)
+    us = graph_time(ac.kernel, len(ac.caches), 3)
+    extra["attn_decode_4097"] = {"kernel_us": round(us, 3), "GBps": round(KV_READ_BYTES / us / 1e3, 1),
+                                 "frac_hbm": round(KV_READ_BYTES / us / 1e3 / HBM_PEAK_GBS, 4)}
+    log(f"attention (32/8 heads, 4097 positions): {us:.2f} us")
+    del ac
+    lc = LayerCase(dev)
+    us = graph_time(lc.step, 1, 20) / len(lc.layers)
+    gbs = lc.bytes_per_layer() / us / 1e3
+    extra["layer_q4km_pos4096"] = {"us_per_layer": round(us, 2), "GBps": round(gbs, 1),
+                                   "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "layers_per_s": round(1e6 / us, 1),
+                                   "bytes_per_layer": lc.bytes_per_layer()}
+    log(f"decoder layer: {us:.1f} us/layer  {gbs:.1f} GB/s")
+    del lc
     dom = extra["q4k_up"]
     roofline = {"bound": "hbm", "achieved": dom["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(),

@@ -31,6 +31,8 @@ SIGNATURES = {
     "dq_attn_workspace_bytes": (c_int, [c_u32, c_u32, c_u32, c_u32, ctypes.POINTER(c_size)]),
     "dq_attn_decode_q8": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_u32, c_p, c_p, c_size,
                                   c_p]),
+    "dq_attn_decode_q8_act": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_u32, c_p, c_p, c_p,
+                                      c_p, c_p, c_size, c_p]),
     "dq_gemv_add": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p, c_p, c_p, c_p, c_p]),
     "dq_rope_cache": (c_int, [c_p, c_u32, c_u32, c_f]),
     "dq_norm_quant": (c_int, [c_p, c_p, c_p, c_p, c_size, c_f, c_p, c_p, c_p, c_p]),

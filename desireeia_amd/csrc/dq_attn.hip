@@ -10,7 +10,8 @@
 // split) walks tiles of 64 positions, tile j of a split s being s, s+S, ...,
 // and keeps a running max / sum / weighted V sum for the HPK query heads that
 // share the KV head (GQA), so each K/V byte is read once for all of them. A
-// second kernel merges the S partials of each head. The position may be read
+// second kernel merges the S partials of each head, and can also quantize the
+// merged output for the output projection. The position may be read
 // from device memory at run time, so the same launch can be replayed in a
 // graph for successive tokens.
 //
@@ -19,6 +20,8 @@
 // fp32; softmax; out = sum_p w_p * d_p * q_v. The sums run in fp32 in another
 // order than the reference's (the reference sums the softmax denominator in
 // double); results agree to ~1e-6 relative.
+#include <cstdlib>
+
 #include "dq_common.h"
 
 namespace {
@@ -133,6 +136,28 @@ __global__ __launch_bounds__(NT) void attn_part_kernel(const float* __restrict__
     const int n_tiles = (npos + TP - 1) / TP;
     if (s >= n_tiles) return;
 
+    // K/V rows of the first tile: issued before the query is staged
+    uint32_t kr[STAGE_IT], vr[STAGE_IT];
+    auto load_tile = [&](int t) {
+        const int p0 = c0 + t * TP;
+        const int nv = min(TP, pos + 1 - p0);
+        const uint8_t* kb = kc + (size_t)p0 * pos_bytes + (size_t)kvh * RB;
+        const uint8_t* vb = vc + (size_t)p0 * pos_bytes + (size_t)kvh * RB;
+#pragma unroll
+        for (int it = 0; it < STAGE_IT; ++it) {
+            const int i = tid + it * NT;
+            const int r = i / RBW, c = i % RBW;
+            if (r < nv) {
+                kr[it] = *reinterpret_cast<const uint32_t*>(kb + (size_t)r * pos_bytes + 4 * c);
+                vr[it] = *reinterpret_cast<const uint32_t*>(vb + (size_t)r * pos_bytes + 4 * c);
+            } else {
+                kr[it] = 0;
+                vr[it] = 0;
+            }
+        }
+    };
+    load_tile(s);
+
     // query of the HPK heads of this KV head
     for (int i = tid; i < HPK * HD; i += NT) qt[i % HD][i / HD] = q[(size_t)(kvh * HPK + i / HD) * HD + i % HD];
     __syncthreads();
@@ -155,34 +180,17 @@ __global__ __launch_bounds__(NT) void attn_part_kernel(const float* __restrict__
     for (int t = s; t < n_tiles; t += n_split) {
         const int p0 = c0 + t * TP;
         const int nv = min(TP, pos + 1 - p0);
-        // ---- stage the K and V rows of this head for the tile
         __syncthreads();  // previous tile's LDS reads are done
-        {
-            uint32_t kr[STAGE_IT], vr[STAGE_IT];
-            const uint8_t* kb = kc + (size_t)p0 * pos_bytes + (size_t)kvh * RB;
-            const uint8_t* vb = vc + (size_t)p0 * pos_bytes + (size_t)kvh * RB;
 #pragma unroll
-            for (int it = 0; it < STAGE_IT; ++it) {
-                const int i = tid + it * NT;
-                const int r = i / RBW, c = i % RBW;
-                if (r < nv) {
-                    kr[it] = *reinterpret_cast<const uint32_t*>(kb + (size_t)r * pos_bytes + 4 * c);
-                    vr[it] = *reinterpret_cast<const uint32_t*>(vb + (size_t)r * pos_bytes + 4 * c);
-                } else {
-                    kr[it] = 0;
-                    vr[it] = 0;
-                }
-            }
-#pragma unroll
-            for (int it = 0; it < STAGE_IT; ++it) {
-                const int i = tid + it * NT;
-                if (i < TP * RBW) {
-                    ks[i] = kr[it];
-                    vs[i] = vr[it];
-                }
+        for (int it = 0; it < STAGE_IT; ++it) {
+            const int i = tid + it * NT;
+            if (i < TP * RBW) {
+                ks[i] = kr[it];
+                vs[i] = vr[it];
             }
         }
         __syncthreads();
+        if (t + n_split < n_tiles) load_tile(t + n_split);  // prefetch the next tile
         // ---- partial scores: wave w takes blocks w, w+NW, ...; lane = position
         for (int b = wave; b < NB; b += NW) {
             const int p = lane;
@@ -296,59 +304,183 @@ __global__ __launch_bounds__(NT) void attn_part_kernel(const float* __restrict__
             rec[h * Part<HD>::FLOATS + HD + 1] = hh == 0 ? l_run : l_run2;
         }
     }
+
 }
 
-// Merge of the splits of one query head: out = sum_s e^(m_s-M) acc_s / sum_s e^(m_s-M) l_s.
+// Merge of the split partials: workgroup b owns outputs [256b, 256b + 256) of
+// the flattened [n_head][HD] output (two heads at HD = 128). out = sum_s
+// e^(m_s-M) acc_s / sum_s e^(m_s-M) l_s per head. 1024 threads: thread t sums
+// output t % 256 over the splits s = t / 256 (mod 4); up to 32 of its loads
+// are issued together with the (m, l) loads, so the merge costs about one
+// memory round trip. Optionally quantizes the 256 outputs (the per-256
+// activation of the output projection).
+constexpr int MT = 1024;
+constexpr int MG = MT / 256;  // split groups
+constexpr int MPRE = 32;      // acc loads per thread issued up front
+
 template <int HD, int HPK>
-__global__ __launch_bounds__(HD) void attn_merge_kernel(const float* __restrict__ part, int n_split, int cc_start,
+__global__ __launch_bounds__(MT) void attn_merge_kernel(const float* __restrict__ part, int n_split, int cc_start,
                                                         int pos_host, const int* __restrict__ pos_dev, int n_ctx,
-                                                        float* __restrict__ out) {
-    const int hq = blockIdx.x, kvh = hq / HPK, h = hq % HPK;
+                                                        float* __restrict__ out, int8_t* __restrict__ oq,
+                                                        float* __restrict__ oscale, int32_t* __restrict__ oisum) {
+    constexpr int HPB = 256 / HD;  // heads per block
+    static_assert(256 % HD == 0, "whole heads per block");
+    __shared__ float ml[HPB][2][MAX_SPLIT];
+    __shared__ float hsum[HPB];
+    __shared__ float red[MG][256];
+    __shared__ float wmax[MT / 64];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int pos = read_pos(pos_host, pos_dev, n_ctx);
     const int c0 = cc_start < pos ? cc_start : pos;
     const int n_tiles = (pos + 1 - c0 + TP - 1) / TP;
     const int n_used = min(n_split, n_tiles);
-    const float* base = part + (size_t)kvh * n_split * HPK * Part<HD>::FLOATS + (size_t)h * Part<HD>::FLOATS;
+    const int o0 = blockIdx.x * 256;          // first output of the block
+    const int d = t & 255, sg = t >> 8;
+    const int hq = (o0 + d) / HD, dd = (o0 + d) % HD;
+    const int kvh = hq / HPK, h = hq % HPK;
     const size_t stride = (size_t)HPK * Part<HD>::FLOATS;
-    float M = -INFINITY;
-    for (int s = 0; s < n_used; ++s) M = fmaxf(M, base[s * stride + HD]);
-    float L = 0.0f, o = 0.0f;
-    for (int s = 0; s < n_used; ++s) {
-        const float* r = base + s * stride;
-        const float f = __expf(r[HD] - M);
-        L = fmaf(f, r[HD + 1], L);
-        o = fmaf(f, r[threadIdx.x], o);
+    const float* base = part + (size_t)kvh * n_split * stride + (size_t)h * Part<HD>::FLOATS;
+    float pre[MPRE];
+#pragma unroll
+    for (int i = 0; i < MPRE; ++i) {
+        const int sidx = sg + MG * i;
+        pre[i] = sidx < n_used ? base[sidx * stride + dd] : 0.0f;
     }
-    out[(size_t)hq * HD + threadIdx.x] = o / L;
+    // (m, l) of the block's heads: thread t < n_used loads split t
+    if (t < HPB * MAX_SPLIT) {
+        const int j = t / MAX_SPLIT, sidx = t % MAX_SPLIT;
+        const int hqj = o0 / HD + j;
+        const float* bj = part + (size_t)(hqj / HPK) * n_split * stride + (size_t)(hqj % HPK) * Part<HD>::FLOATS;
+        ml[j][0][sidx] = sidx < n_used ? bj[sidx * stride + HD] : -INFINITY;
+        ml[j][1][sidx] = sidx < n_used ? bj[sidx * stride + HD + 1] : 0.0f;
+    }
+    __syncthreads();
+    // per head: M = max m_s, weights f_s = e^(m_s - M), L = sum f_s l_s
+    // (waves 0..3 handle head 0, waves 4..7 head 1: MAX_SPLIT = 256 splits)
+    if (wave < 4 * HPB) {
+        const int j = wave / 4, sidx = (wave % 4) * 64 + lane;
+        const float m = ml[j][0][sidx];
+        const float M0 = dq_wave_max(m);
+        if (lane == 0) wmax[wave] = M0;
+    }
+    __syncthreads();
+    if (wave < 4 * HPB) {
+        const int j = wave / 4, sidx = (wave % 4) * 64 + lane;
+        const float M = fmaxf(fmaxf(wmax[4 * j], wmax[4 * j + 1]), fmaxf(wmax[4 * j + 2], wmax[4 * j + 3]));
+        const float f = sidx < n_used ? __expf(ml[j][0][sidx] - M) : 0.0f;
+        const float lw = dq_wave_sum(f * ml[j][1][sidx]);
+        ml[j][0][sidx] = f;  // weights replace the maxima
+        if (lane == 0) red[0][wave] = lw;
+    }
+    __syncthreads();
+    if (t < HPB) hsum[t] = (red[0][4 * t] + red[0][4 * t + 1]) + (red[0][4 * t + 2] + red[0][4 * t + 3]);
+    __syncthreads();
+    const int j = d / HD;
+    float o = 0.0f;
+#pragma unroll
+    for (int i = 0; i < MPRE; ++i) {
+        const int sidx = sg + MG * i;
+        if (sidx < n_used) o = fmaf(ml[j][0][sidx], pre[i], o);
+    }
+    for (int sidx = sg + MG * MPRE; sidx < n_used; sidx += MG) o = fmaf(ml[j][0][sidx], base[sidx * stride + dd], o);
+    red[sg][d] = o;
+    __syncthreads();
+    float v = 0.0f;
+    if (sg == 0) {
+        v = ((red[0][d] + red[1][d]) + (red[2][d] + red[3][d])) / hsum[j];
+        out[o0 + d] = v;
+    }
+    if (!oq) return;  // uniform
+    // per-256 quantization (core/matmul.cpp:1660-1778) by waves 0..3
+    if (sg == 0) {
+        const float am = dq_wave_max(fabsf(v));
+        if (lane == 0) wmax[wave] = am;
+    }
+    __syncthreads();
+    if (sg != 0) return;
+    const float amax = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const float dsc = amax > 0.0f ? amax / 127.0f : 0.0f;
+    const float id = dsc > 0.0f ? 127.0f / amax : 0.0f;
+    int iv = (int)rintf(v * id);
+    iv = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
+    oq[o0 + d] = (int8_t)iv;
+    int sum = iv;
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) sum += __shfl_xor(sum, off, DQ_WAVE);
+    if ((d & 31) == 0) {
+        oscale[(o0 + d) / 32] = dsc;
+        oisum[(o0 + d) / 32] = sum;
+    }
+}
+
+int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    return e ? atoi(e) : dflt;
 }
 
 int split_count(int n_kv, int n_tiles_max) {
-    // about two workgroups per CU, a multiple of the 8 XCDs
-    int s = (2 * num_cus() + n_kv - 1) / n_kv;
-    s = s < n_tiles_max ? s : n_tiles_max;
+    // about `tpw` tiles per workgroup (the next tile's loads overlap the
+    // current tile's arithmetic), at most four workgroups per CU, a multiple
+    // of the 8 XCDs
+    static const int tpw = env_int("DQ_ATTN_TPW", 2) < 1 ? 1 : env_int("DQ_ATTN_TPW", 2);
+    int s = (4 * num_cus() + n_kv - 1) / n_kv;
+    const int want = (n_tiles_max + tpw - 1) / tpw;
+    s = s < want ? s : want;
     s = (s + 7) & ~7;
     return s < MAX_SPLIT ? s : MAX_SPLIT;
 }
 
-template <int HD, int HPK>
-int launch_attn(const float* q, const uint8_t* kc, const uint8_t* vc, int n_kv, int cc_start, int pos,
-                const int* pos_dev, int n_ctx, float* out, float* part, int n_split, hipStream_t st) {
-    const size_t pos_bytes = (size_t)n_kv * (HD / 32) * DQ_SZ_Q8_0;
-    const float scale = 1.0f / sqrtf((float)HD);
-    attn_part_kernel<HD, HPK><<<n_kv * n_split, NT, 0, st>>>(q, kc, vc, n_kv, pos_bytes, cc_start, pos, pos_dev,
-                                                              n_ctx, n_split, scale, part);
-    attn_merge_kernel<HD, HPK><<<n_kv * HPK, HD, 0, st>>>(part, n_split, cc_start, pos, pos_dev, n_ctx, out);
-    return dq_launch_status();
+// Workspace: the split partial records.
+size_t work_bytes_for(int n_head, int hd, int n_split) {
+    return dq_align256((size_t)n_head * n_split * (hd + 2) * sizeof(float));
 }
 
-size_t part_bytes(int n_head, int hd, int n_split) {
-    return dq_align256((size_t)n_head * n_split * (hd + 2) * sizeof(float));
+template <int HD, int HPK>
+int launch_attn(const float* q, const uint8_t* kc, const uint8_t* vc, int n_kv, int cc_start, int pos,
+                const int* pos_dev, int n_ctx, float* out, uint8_t* work, int n_split, int8_t* oq, float* os,
+                int32_t* oi, hipStream_t st) {
+    const size_t pos_bytes = (size_t)n_kv * (HD / 32) * DQ_SZ_Q8_0;
+    const float scale = 1.0f / sqrtf((float)HD);
+    float* part = reinterpret_cast<float*>(work);
+    attn_part_kernel<HD, HPK><<<n_kv * n_split, NT, 0, st>>>(q, kc, vc, n_kv, pos_bytes, cc_start, pos, pos_dev,
+                                                              n_ctx, n_split, scale, part);
+    attn_merge_kernel<HD, HPK><<<n_kv * HPK * HD / 256, MT, 0, st>>>(part, n_split, cc_start, pos, pos_dev, n_ctx,
+                                                                       out, oq, os, oi);
+    return dq_launch_status();
 }
 
 bool attn_shape_ok(uint32_t n_head, uint32_t n_head_kv, uint32_t hd) {
     if (n_head_kv == 0 || n_head % n_head_kv) return false;
     const uint32_t hpk = n_head / n_head_kv;
-    return hd == 128 && (hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8);
+    // the merge takes whole 256-output blocks
+    return hd == 128 && (hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8) && (n_head * hd) % 256 == 0;
+}
+
+int attn_run(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head, uint32_t n_head_kv, uint32_t hd,
+             uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx, float* d_out, void* d_work,
+             size_t work_bytes, int8_t* oq, float* os, int32_t* oi, void* stream) {
+    if (!d_q || !d_kc || !d_vc || !d_out || !d_work || n_ctx == 0) return DQ_ERR_INVALID_ARG;
+    if (!attn_shape_ok(n_head, n_head_kv, hd)) return DQ_ERR_NOT_SUPPORTED;
+    if (!d_pos && (pos >= n_ctx || cc_start > pos)) return DQ_ERR_INVALID_ARG;
+    const uint32_t hpk = n_head / n_head_kv;
+    if (oq && (!os || !oi)) return DQ_ERR_INVALID_ARG;
+    // with a host position the split count follows the live context; with a
+    // device position it is sized for the whole cache
+    const uint32_t span = d_pos ? n_ctx : pos + 1 - cc_start;
+    const int n_split = split_count((int)n_head_kv, (int)((span + TP - 1) / TP));
+    if (work_bytes < work_bytes_for((int)n_head, (int)hd, n_split)) return DQ_ERR_INVALID_ARG;
+    const hipStream_t st = (hipStream_t)stream;
+    const uint8_t* kc = (const uint8_t*)d_kc;
+    const uint8_t* vc = (const uint8_t*)d_vc;
+    uint8_t* w = (uint8_t*)d_work;
+    const int a = (int)cc_start, p = (int)pos, nk = (int)n_head_kv, nc = (int)n_ctx;
+    switch (hpk) {
+    case 1: return launch_attn<128, 1>(d_q, kc, vc, nk, a, p, d_pos, nc, d_out, w, n_split, oq, os, oi, st);
+    case 2: return launch_attn<128, 2>(d_q, kc, vc, nk, a, p, d_pos, nc, d_out, w, n_split, oq, os, oi, st);
+    case 4: return launch_attn<128, 4>(d_q, kc, vc, nk, a, p, d_pos, nc, d_out, w, n_split, oq, os, oi, st);
+    case 8: return launch_attn<128, 8>(d_q, kc, vc, nk, a, p, d_pos, nc, d_out, w, n_split, oq, os, oi, st);
+    }
+    return DQ_ERR_NOT_SUPPORTED;
 }
 
 }  // namespace
@@ -370,34 +502,24 @@ int dq_attn_workspace_bytes(uint32_t n_head, uint32_t n_head_kv, uint32_t hd, ui
     if (!bytes || n_ctx == 0) return DQ_ERR_INVALID_ARG;
     if (!attn_shape_ok(n_head, n_head_kv, hd)) return DQ_ERR_NOT_SUPPORTED;
     const int n_split = split_count((int)n_head_kv, (int)((n_ctx + TP - 1) / TP));
-    *bytes = part_bytes((int)n_head, (int)hd, n_split);
+    *bytes = work_bytes_for((int)n_head, (int)hd, n_split);
     return DQ_OK;
 }
 
 int dq_attn_decode_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head, uint32_t n_head_kv,
                       uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx,
                       float* d_out, void* d_work, size_t work_bytes, void* stream) {
-    if (!d_q || !d_kc || !d_vc || !d_out || !d_work || n_ctx == 0) return DQ_ERR_INVALID_ARG;
-    if (!attn_shape_ok(n_head, n_head_kv, hd)) return DQ_ERR_NOT_SUPPORTED;
-    if (!d_pos && (pos >= n_ctx || cc_start > pos)) return DQ_ERR_INVALID_ARG;
-    // with a host position the split count follows the live context; with a
-    // device position it is sized for the whole cache
-    const uint32_t span = d_pos ? n_ctx : pos + 1 - cc_start;
-    const int n_split = split_count((int)n_head_kv, (int)((span + TP - 1) / TP));
-    if (work_bytes < part_bytes((int)n_head, (int)hd, n_split)) return DQ_ERR_INVALID_ARG;
-    const hipStream_t st = (hipStream_t)stream;
-    const uint8_t* kc = (const uint8_t*)d_kc;
-    const uint8_t* vc = (const uint8_t*)d_vc;
-    float* part = (float*)d_work;
-    const int hpk = (int)(n_head / n_head_kv);
-    const int a = (int)cc_start, p = (int)pos, nk = (int)n_head_kv, nc = (int)n_ctx;
-    switch (hpk) {
-    case 1: return launch_attn<128, 1>(d_q, kc, vc, nk, a, p, d_pos, nc, d_out, part, n_split, st);
-    case 2: return launch_attn<128, 2>(d_q, kc, vc, nk, a, p, d_pos, nc, d_out, part, n_split, st);
-    case 4: return launch_attn<128, 4>(d_q, kc, vc, nk, a, p, d_pos, nc, d_out, part, n_split, st);
-    case 8: return launch_attn<128, 8>(d_q, kc, vc, nk, a, p, d_pos, nc, d_out, part, n_split, st);
-    }
-    return DQ_ERR_NOT_SUPPORTED;
+    return attn_run(d_q, d_kc, d_vc, n_head, n_head_kv, hd, cc_start, pos, d_pos, n_ctx, d_out, d_work, work_bytes,
+                    nullptr, nullptr, nullptr, stream);
+}
+
+int dq_attn_decode_q8_act(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head,
+                          uint32_t n_head_kv, uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos,
+                          uint32_t n_ctx, float* d_out, int8_t* d_oq, float* d_oscale, int32_t* d_oisum,
+                          void* d_work, size_t work_bytes, void* stream) {
+    if (!d_oq) return DQ_ERR_INVALID_ARG;
+    return attn_run(d_q, d_kc, d_vc, n_head, n_head_kv, hd, cc_start, pos, d_pos, n_ctx, d_out, d_work, work_bytes,
+                    d_oq, d_oscale, d_oisum, stream);
 }
 
 }  // extern "C"

@@ -364,9 +364,9 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
     DQ_TRY(dq_gemv(L->fmt_v, L->wv, KVD, E, w.aq, w.as, w.ai, w.v, stream));
     DQ_TRY(dq_rope_kv_write(w.q, w.k, w.v, d_rope, L->n_head, L->n_head_kv, L->head_dim, L->n_rot, d_kc, d_vc, pos,
                             d_pos, n_ctx, stream));
-    DQ_TRY(dq_attn_decode_q8(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos, n_ctx,
-                             w.ao, w.attn, w.attn_bytes, stream));
-    DQ_TRY(dq_quantize_act(DQ_ACT_Q8K_REP, w.ao, QD, 1, w.aq, w.as, w.ai, nullptr, stream));
+    // the attention's merge also quantizes its output for the projection
+    DQ_TRY(dq_attn_decode_q8_act(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos, n_ctx,
+                                 w.ao, w.aq, w.as, w.ai, w.attn, w.attn_bytes, stream));
     DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.aq, w.as, w.ai, d_x, w.x2, stream));
     // feed-forward block
     DQ_TRY(dq_norm_quant(w.x2, nullptr, nullptr, L->ffn_norm, E, L->rms_eps, w.aq, w.as, w.ai, stream));

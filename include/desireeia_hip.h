@@ -131,12 +131,19 @@ int dq_kv_write(const float* d_k, const float* d_v, uint32_t n_head_kv, uint32_t
  * positions [cc_start, pos], query head h reads KV head h / (n_head /
  * n_head_kv), scores scaled by 1/sqrt(hd), softmax, out [n_head][hd] fp32.
  * hd = 128 and n_head / n_head_kv in {1, 2, 4, 8}; other shapes: -2.
- * d_work holds dq_attn_workspace_bytes(n_ctx) bytes of split partials.
- * d_pos as for dq_kv_write. */
+ * d_work holds dq_attn_workspace_bytes(n_ctx) bytes of split partials
+ * (calls sharing a workspace must not overlap). d_pos as for dq_kv_write. */
 int dq_attn_workspace_bytes(uint32_t n_head, uint32_t n_head_kv, uint32_t hd, uint32_t n_ctx, size_t* bytes);
 int dq_attn_decode_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head, uint32_t n_head_kv,
                       uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx,
                       float* d_out, void* d_work, size_t work_bytes, void* stream);
+/* The same, also writing the output quantized per 256 values (DQ_ACT_Q8K_REP
+ * layout: int8 [n_head*hd], scale and int32 sum per 32), the activation of
+ * the output projection's GEMV. */
+int dq_attn_decode_q8_act(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head,
+                          uint32_t n_head_kv, uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos,
+                          uint32_t n_ctx, float* d_out, int8_t* d_oq, float* d_oscale, int32_t* d_oisum,
+                          void* d_work, size_t work_bytes, void* stream);
 
 /* ------------------------------------------------------- decoder layer */
 

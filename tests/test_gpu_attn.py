@@ -132,3 +132,31 @@ def test_attention_unsupported(gpu):
 def ctypes_size():
     import ctypes
     return ctypes.byref(ctypes.c_size_t(0))
+
+
+def test_attention_quantized_output(gpu, orc):
+    """dq_attn_decode_q8_act: the merged output quantized per 256 values is
+    bit-identical to the per-256 quantizer applied to the fp32 output, on
+    repeated calls sharing one workspace."""
+    import ctypes
+    n_head, n_kv, pos = 32, 8, 1500
+    kc, vc = host_cache(orc, pos + 1, n_kv, seed=21)
+    cache = device_cache(gpu, kc, vc, pos + 1, n_kv)
+    q = np.random.default_rng(22).standard_normal(n_head * HD).astype(np.float32)
+    qd = torch.from_numpy(q).to(gpu)
+    work = ops.attn_workspace(n_head, n_kv, HD, pos + 1, gpu)
+    lib = _lib.load()
+    for p in (pos, 100, pos):
+        out = torch.empty(n_head * HD, dtype=torch.float32, device=gpu)
+        act = ops.empty_act((n_head * HD,), ops.ACT_Q8K_REP, gpu)
+        _lib.check(lib.dq_attn_decode_q8_act(ops._ptr(qd), ops._ptr(cache.k), ops._ptr(cache.v), n_head, n_kv, HD, 0,
+                                             p, None, cache.n_ctx, ops._ptr(out), ops._ptr(act.q),
+                                             ops._ptr(act.scale), ops._ptr(act.isum), ops._ptr(work), work.numel(),
+                                             ops._stream()))
+        torch.cuda.synchronize()
+        o = out.cpu().numpy()
+        assert rel(o, orc.attn_decode(q, kc, vc, n_head, n_kv, HD, 0, p)) <= TOL
+        wq, wd, wi = orc.quantize_q8k_rep(o)
+        assert np.array_equal(act.q.cpu().numpy(), wq)
+        assert np.array_equal(act.scale.cpu().numpy(), wd)
+        assert np.array_equal(act.isum.cpu().numpy(), wi)
