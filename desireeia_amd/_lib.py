@@ -34,13 +34,91 @@ SIGNATURES = {
     "dq_attn_decode_q8_act": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_u32, c_p, c_p, c_p,
                                       c_p, c_p, c_size, c_p]),
     "dq_gemv_add": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p, c_p, c_p, c_p, c_p]),
+    "dq_gemv_group": (c_int, [c_p, c_size, c_size, c_p, c_p, c_p, c_p]),
     "dq_rope_cache": (c_int, [c_p, c_u32, c_u32, c_f]),
     "dq_norm_quant": (c_int, [c_p, c_p, c_p, c_p, c_size, c_f, c_p, c_p, c_p, c_p]),
     "dq_silu_quant": (c_int, [c_p, c_p, c_size, c_p, c_p, c_p, c_p]),
     "dq_rope_kv_write": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_p, c_p, c_u32, c_p, c_u32, c_p]),
     "dq_layer_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
     "dq_layer_decode": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_p, c_u32, c_p, c_p, c_u32, c_p, c_size, c_p]),
+    "dq_silu_mul": (c_int, [c_p, c_p, c_size, c_p, c_p]),
+    # engine layer (core/engine.h GPU block); struct arguments as void*
+    "cuda_gpu_count": (ctypes.c_int32, []),
+    "cuda_probe_gpu": (ctypes.c_bool, [ctypes.c_int32, c_p, c_size, c_p, c_p, c_p, c_p, c_p]),
+    "matmul_q8_0_cuda_upload_weights": (ctypes.c_bool, [c_p, c_size, c_size, c_p, c_p]),
+    "cuda_upload_weights": (ctypes.c_bool, [c_int, c_p, c_size, c_size, c_p, c_p]),
+    "cuda_free_device": (None, [c_p]),
+    "cuda_backend_shutdown": (None, []),
+    "matmul_kquant_cuda_resident": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p]),
+    "matmul_kquant_cuda_resident_same_x": (c_int, [c_p, c_size, c_size, c_p]),
+    "matmul_q8_0_cuda_resident": (c_int, [c_p, c_p, c_size, c_size, c_p, c_p]),
+    "matmul_q8_0_cuda_resident_group": (c_int, [c_p, c_size, c_size, c_p]),
+    "matmul_q8_0_cuda": (c_int, [c_p, c_size, c_size, c_p, c_p]),
+    "matmul_kquant_cuda_batch": (c_int, [c_int, c_p, c_size, c_size, c_p, c_size, c_p]),
+    "matmul_q8_0_cuda_ffn_gated": (c_int, [c_p, c_p, c_p, c_p, c_p, c_p, c_size, c_size, c_p, c_p, c_int]),
+    "cuda_kv_cache_reserve": (ctypes.c_bool, [c_size]),
+    "cuda_kv_cache_release": (None, []),
+    "cuda_kv_cache_upload": (ctypes.c_bool, [c_p, c_p, c_size]),
+    "cuda_kv_cache_download": (ctypes.c_bool, [c_p, c_p, c_size]),
+    "cuda_kv_cache_write": (ctypes.c_bool, [c_size, c_p, c_p, c_size]),
+    "cuda_kv_cache_read": (ctypes.c_bool, [c_size, c_p, c_p, c_size]),
+    "cuda_kv_cache_move": (ctypes.c_bool, [c_size, c_size, c_size]),
+    "cuda_set_attention_long": (None, [ctypes.c_bool]),
+    "cuda_drop_graphs": (None, []),
+    "cuda_attention_out": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_size, c_u32, c_u32, c_size, c_size,
+                                   c_p, c_int, c_size]),
+    "cuda_qkv_attention_out": (c_int, [c_p]),
+    "cuda_layer_forward": (c_int, [c_p]),
+    "cuda_attention_batch": (c_int, [c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_size, c_size, c_size, c_u32,
+                                     c_u32]),
+    "cuda_layer_forward_batch": (c_int, [c_p]),
+    "cuda_prefill_chunk_tokens": (c_int, []),
 }
+
+
+
+class CudaKQuantJob(ctypes.Structure):
+    """core/engine.h:536 (include/desireeia_hip.h)."""
+    _fields_ = [("format", c_int), ("d_w", c_p), ("rows", c_size), ("y", c_p)]
+
+
+class CudaQ80Job(ctypes.Structure):
+    """core/engine.h:598-603."""
+    _fields_ = [("d_qs", c_p), ("d_scale", c_p), ("rows", c_size), ("y", c_p)]
+
+
+class CudaQkvAttnArgs(ctypes.Structure):
+    """core/engine.h:675-691."""
+    _fields_ = ([(n, c_p) for n in ("wq_qs", "wq_scale", "wk_qs", "wk_scale", "wv_qs", "wv_scale", "wo_qs",
+                                    "wo_scale", "bq", "bk", "bv", "attn_in", "rope_cache", "proj", "host_k_row",
+                                    "host_v_row")]
+                + [("n_embd", c_size), ("q_dim", c_size), ("kv_dim", c_size)]
+                + [(n, c_u32) for n in ("n_head", "n_head_kv", "heads_per_kv", "head_dim", "n_rot")]
+                + [("kv_layer_off", c_size), ("cc_start", c_u32), ("pos", c_u32)])
+
+
+class CudaLayerArgs(ctypes.Structure):
+    """core/engine.h:698-751."""
+    _fields_ = ([(n, c_p) for n in ("wq_qs", "wq_scale", "wk_qs", "wk_scale", "wv_qs", "wv_scale", "wo_qs",
+                                    "wo_scale", "wgate_qs", "wgate_scale", "wup_qs", "wup_scale", "wdown_qs",
+                                    "wdown_scale", "wag_qs", "wag_scale", "bq", "bk", "bv", "attn_norm_w",
+                                    "ffn_norm_w", "q_norm_w", "k_norm_w", "post_attn_norm_w", "post_ffn_norm_w", "x",
+                                    "rope_cache", "x_out")]
+                + [(n, c_size) for n in ("n_embd", "q_dim", "kv_dim", "n_ff")]
+                + [(n, c_u32) for n in ("n_head", "n_head_kv", "heads_per_kv", "head_dim", "n_rot")]
+                + [("kv_layer_off", c_size), ("cc_start", c_u32), ("pos", c_u32), ("rms_eps", c_f),
+                   ("act_gelu", c_int)]
+                + [(n, c_int) for n in ("fmt_q", "fmt_k", "fmt_v", "fmt_o", "fmt_gate", "fmt_up", "fmt_down",
+                                        "fmt_ag", "upload_x", "download_x", "upload_dyn")]
+                + [("dyn_all", c_p), ("rope_all", c_p), ("n_slots", c_u32), ("rope_stride", c_u32),
+                   ("layer_slot", c_u32), ("x_from_token", c_int), ("embd_qs", c_p), ("embd_scale", c_p),
+                   ("embd_mul", c_f)])
+
+
+class GemvJob(ctypes.Structure):
+    """dq_gemv_job_t of include/desireeia_hip.h."""
+    _fields_ = [("fmt", c_int), ("d_w", c_p), ("rows", c_size), ("d_y", c_p), ("d_res", c_p)]
+
 
 _lib = None
 

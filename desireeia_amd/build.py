@@ -1,6 +1,6 @@
 """Builds the HIP library libdesireeia_hip.so for gfx950, in-tree.
 
-Every .hip file under csrc/ is compiled with hipcc (one process per file, in
+Every .hip and .cpp file under csrc/ is compiled with hipcc (one process per file, in
 parallel) and linked into desireeia_amd/libdesireeia_hip.so. Flags:
   -ffp-contract=off    no implicit multiply-add fusion: the dequantizers must be
                        bit-exact and the kernels use explicit fmaf where fusion
@@ -34,11 +34,11 @@ def hipcc():
 
 
 def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
 
 
 def _compile(src):
-    obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
+    obj = os.path.join(BUILD, os.path.splitext(os.path.basename(src))[0] + ".o")
     cmd = [hipcc()] + FLAGS + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # the host pass does not know the device-only feature flag: drop that line

@@ -220,6 +220,30 @@ struct Fmt<DQ_FMT_Q6_K> {
     }
 };
 
+// Up to DQ_GEMV_MAX_JOBS matrices that read the same activation (same cols,
+// same format) run in one grid: their row groups are concatenated, job j
+// owning groups [g0[j], g0[j+1]).
+#define DQ_GEMV_MAX_JOBS 4
+struct Jobs {
+    const uint8_t* w[DQ_GEMV_MAX_JOBS];
+    DqLayout L[DQ_GEMV_MAX_JOBS];
+    float* y[DQ_GEMV_MAX_JOBS];
+    const float* res[DQ_GEMV_MAX_JOBS];
+    int rows[DQ_GEMV_MAX_JOBS];
+    int g0[DQ_GEMV_MAX_JOBS + 1];
+    int n;
+};
+
+// Job of global group g (g < g0[n]) and the group's index inside it.
+__device__ __forceinline__ int job_of(const Jobs& J, int g, int* gl) {
+    int j = 0;
+#pragma unroll
+    for (int k = 1; k < DQ_GEMV_MAX_JOBS; ++k)
+        if (k < J.n && g >= J.g0[k]) j = k;
+    *gl = g - J.g0[j];
+    return j;
+}
+
 // Loads the weights of item i of row r (or, when `live` is false, reads a
 // cached dummy location instead: the pipeline's prefetch past the last group).
 template <int FMT>
@@ -269,16 +293,19 @@ __device__ __forceinline__ float reduce_rows(float (&acc)[R], int lane) {
 
 // Items of a wave: [i0, i1) of every row; lane owns i0 + lane + 64j.
 template <int FMT, int R, int NIT>
-__device__ __forceinline__ void load_group(typename Fmt<FMT>::W (&wr)[R][NIT], const uint8_t* base,
-                                           const DqLayout& L, int g, int ngroups, int rows, int i0, int i1, int lane,
-                                           const uint8_t* dummy) {
+__device__ __forceinline__ void load_group(typename Fmt<FMT>::W (&wr)[R][NIT], const Jobs& J, int g, int ngroups,
+                                           int i0, int i1, int lane, const uint8_t* dummy) {
     const bool live = g < ngroups;
+    int gl = 0;
+    const int j = live ? job_of(J, g, &gl) : 0;
+    const uint8_t* base = J.w[j];
+    const int rows = J.rows[j];
 #pragma unroll
     for (int rr = 0; rr < R; ++rr) {
-        const size_t r = (size_t)min(g * R + rr, rows - 1);
+        const size_t r = (size_t)min(gl * R + rr, rows - 1);
 #pragma unroll
-        for (int j = 0; j < NIT; ++j)
-            load_item<FMT>(wr[rr][j], base, L, r, min(i0 + lane + DQ_WAVE * j, i1 - 1), live, dummy);
+        for (int it = 0; it < NIT; ++it)
+            load_item<FMT>(wr[rr][it], base, J.L[j], r, min(i0 + lane + DQ_WAVE * it, i1 - 1), live, dummy);
     }
 }
 
@@ -287,34 +314,38 @@ __device__ __forceinline__ void load_group(typename Fmt<FMT>::W (&wr)[R][NIT], c
 // partial sums meet in LDS (double-buffered by `buf`, one barrier per group)
 // and wave 0 adds them in a fixed order.
 template <int FMT, int R, int NIT, int KS>
-__device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R][NIT], const XItem (&X)[NIT], int g,
-                                              int rows, int i0, int i1, int lane, int ks, float (*part)[R][4],
-                                              int buf, float* __restrict__ y,
-                                              const float* __restrict__ res) {
+__device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R][NIT], const XItem (&X)[NIT],
+                                              const Jobs& J, int g, int i0, int i1, int lane, int ks,
+                                              float (*part)[R][4], int buf) {
     float acc[R];
 #pragma unroll
     for (int rr = 0; rr < R; ++rr) {
         float a = 0.0f;
 #pragma unroll
-        for (int j = 0; j < NIT; ++j) {
-            const int i = i0 + lane + DQ_WAVE * j;
-            const float p = Fmt<FMT>::dot(wr[rr][j], X[j], i);
+        for (int it = 0; it < NIT; ++it) {
+            const int i = i0 + lane + DQ_WAVE * it;
+            const float p = Fmt<FMT>::dot(wr[rr][it], X[it], i);
             a += i < i1 ? p : 0.0f;
         }
         acc[rr] = a;
     }
     const float s = reduce_rows<R>(acc, lane);
     constexpr int GROUP = DQ_WAVE / R;
+    int gl = 0;
+    const int j = job_of(J, g, &gl);
+    float* __restrict__ y = J.y[j];
+    const float* __restrict__ res = J.res[j];
+    const int rows = J.rows[j];
     if constexpr (KS == 1) {
         if ((lane & (GROUP - 1)) == 0) {
-            const int r = g * R + lane / GROUP;
+            const int r = gl * R + lane / GROUP;
             if (r < rows) y[r] = res ? s + res[r] : s;
         }
     } else {
         if ((lane & (GROUP - 1)) == 0) part[buf][lane / GROUP][ks] = s;
         __syncthreads();
         if (ks == 0 && lane < R) {
-            const int r = g * R + lane;
+            const int r = gl * R + lane;
             if (r < rows) {
                 const float v = ((part[buf][lane][0] + part[buf][lane][1]) + part[buf][lane][2]) + part[buf][lane][3];
                 y[r] = res ? v + res[r] : v;
@@ -328,39 +359,38 @@ __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R
 // Grid: persistent 256-thread workgroups walking "units" u = blockIdx.x,
 // blockIdx.x + gridDim.x, ... KS == 1: unit u = groups 4u..4u+3, one per wave.
 // KS == 4: unit u = group u, shared by the 4 waves (K split in quarters).
+// Groups are global over the jobs of J.
 template <int FMT, int R, int NIT, int KS>
-__global__ __launch_bounds__(256) void gemv_kernel(const uint8_t* __restrict__ w, DqLayout L, int rows, int items,
-                                                   const int8_t* __restrict__ xq, const float* __restrict__ xs,
-                                                   const int32_t* __restrict__ xsum, float* __restrict__ y,
-                                                   const float* __restrict__ res) {
+__global__ __launch_bounds__(256) void gemv_kernel(Jobs J, int items, const int8_t* __restrict__ xq,
+                                                   const float* __restrict__ xs, const int32_t* __restrict__ xsum) {
     using W = typename Fmt<FMT>::W;
     __shared__ float part[2][R][4];
     const int lane = threadIdx.x & (DQ_WAVE - 1);
-    const int wv = (int)(threadIdx.x / DQ_WAVE);
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / DQ_WAVE));  // wave-uniform
     const int ks = KS == 1 ? 0 : wv;
     const int per = KS == 1 ? items : (items + 3) / 4;
     const int i0 = min(ks * per, items);
     const int i1 = min(i0 + per, items);
-    const int ngroups = (rows + R - 1) / R;
+    const int ngroups = J.g0[J.n];
     const int stride = KS == 1 ? 4 * (int)gridDim.x : (int)gridDim.x;
     int g = KS == 1 ? 4 * (int)blockIdx.x + wv : (int)blockIdx.x;
     if (g >= ngroups || i0 >= i1) return;  // uniform per wave (KS 1) / per workgroup (KS 4)
     const uint8_t* dummy = reinterpret_cast<const uint8_t*>(xq);
 
     W b0[R][NIT], b1[R][NIT];
-    load_group<FMT, R, NIT>(b0, w, L, g, ngroups, rows, i0, i1, lane, dummy);
+    load_group<FMT, R, NIT>(b0, J, g, ngroups, i0, i1, lane, dummy);
     XItem X[NIT];
 #pragma unroll
     for (int j = 0; j < NIT; ++j) Fmt<FMT>::load_x(X[j], min(i0 + lane + DQ_WAVE * j, i1 - 1), xq, xs, xsum);
 
     // Two-deep pipeline, unrolled by two so the buffers never move.
     for (;;) {
-        load_group<FMT, R, NIT>(b1, w, L, g + stride, ngroups, rows, i0, i1, lane, dummy);
-        compute_group<FMT, R, NIT, KS>(b0, X, g, rows, i0, i1, lane, ks, part, 0, y, res);
+        load_group<FMT, R, NIT>(b1, J, g + stride, ngroups, i0, i1, lane, dummy);
+        compute_group<FMT, R, NIT, KS>(b0, X, J, g, i0, i1, lane, ks, part, 0);
         g += stride;
         if (g >= ngroups) break;
-        load_group<FMT, R, NIT>(b0, w, L, g + stride, ngroups, rows, i0, i1, lane, dummy);
-        compute_group<FMT, R, NIT, KS>(b1, X, g, rows, i0, i1, lane, ks, part, 1, y, res);
+        load_group<FMT, R, NIT>(b0, J, g + stride, ngroups, i0, i1, lane, dummy);
+        compute_group<FMT, R, NIT, KS>(b1, X, J, g, i0, i1, lane, ks, part, 1);
         g += stride;
         if (g >= ngroups) break;
     }
@@ -385,37 +415,42 @@ int env_int(const char* name, int dflt) {
     return e ? atoi(e) : dflt;
 }
 
+// Fills the group prefix of J for R rows per group.
+void set_groups(Jobs& J, int R) {
+    J.g0[0] = 0;
+    for (int j = 0; j < J.n; ++j) J.g0[j + 1] = J.g0[j] + (J.rows[j] + R - 1) / R;
+}
+
 template <int FMT, int R, int NIT, int KS>
-int launch(const uint8_t* w, const DqLayout& L, int rows, int items, const int8_t* xq, const float* xs,
-           const int32_t* xsum, float* y, const float* res, hipStream_t s) {
+int launch(Jobs J, int items, const int8_t* xq, const float* xs, const int32_t* xsum, hipStream_t s) {
     static const int wpc = env_int("DQ_GEMV_WPC", 8);  // persistent waves per CU
-    const int ngroups = (rows + R - 1) / R;
+    set_groups(J, R);
+    const int ngroups = J.g0[J.n];
     const int units = KS == 1 ? (ngroups + 3) / 4 : ngroups;
     const int max_wg = max(1, num_cus() * wpc / 4);
     const int iters = (units + max_wg - 1) / max_wg;  // balance: every workgroup walks `iters` units
     const unsigned grid = (unsigned)((units + iters - 1) / iters);
-    gemv_kernel<FMT, R, NIT, KS><<<grid, 256, 0, s>>>(w, L, rows, items, xq, xs, xsum, y, res);
+    gemv_kernel<FMT, R, NIT, KS><<<grid, 256, 0, s>>>(J, items, xq, xs, xsum);
     return dq_launch_status();
 }
 
 template <int FMT, int R, int KS>
-int launch_nit(int nit, const uint8_t* w, const DqLayout& L, int rows, int items, const int8_t* xq,
-               const float* xs, const int32_t* xsum, float* y, const float* res, hipStream_t s) {
+int launch_nit(int nit, const Jobs& J, int items, const int8_t* xq, const float* xs, const int32_t* xsum,
+               hipStream_t s) {
     switch (nit) {
-    case 1: return launch<FMT, R, 1, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
-    case 2: return launch<FMT, R, 2, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
-    case 3: return launch<FMT, R, 3, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
-    case 4: return launch<FMT, R, 4, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
+    case 1: return launch<FMT, R, 1, KS>(J, items, xq, xs, xsum, s);
+    case 2: return launch<FMT, R, 2, KS>(J, items, xq, xs, xsum, s);
+    case 3: return launch<FMT, R, 3, KS>(J, items, xq, xs, xsum, s);
+    case 4: return launch<FMT, R, 4, KS>(J, items, xq, xs, xsum, s);
     default:
-        if (nit <= 6) return launch<FMT, R, 6, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
-        if (nit <= 8) return launch<FMT, R, 8, KS>(w, L, rows, items, xq, xs, xsum, y, res, s);
+        if (nit <= 6) return launch<FMT, R, 6, KS>(J, items, xq, xs, xsum, s);
+        if (nit <= 8) return launch<FMT, R, 8, KS>(J, items, xq, xs, xsum, s);
         return DQ_ERR_NOT_SUPPORTED;
     }
 }
 
 template <int FMT>
-int launch_fmt(const uint8_t* w, const DqLayout& L, size_t rows, size_t cols, const int8_t* xq, const float* xs,
-               const int32_t* xsum, float* y, const float* res, hipStream_t s) {
+int launch_fmt(const Jobs& J, size_t cols, const int8_t* xq, const float* xs, const int32_t* xsum, hipStream_t s) {
     const int items = (int)(cols / 64);
     // K split: rows wider than 128 items are shared by the 4 waves of a workgroup
     int ks = env_int("DQ_GEMV_KS", 0);
@@ -427,50 +462,97 @@ int launch_fmt(const uint8_t* w, const DqLayout& L, size_t rows, size_t cols, co
     int r = env_int("DQ_GEMV_R", 0);
     if (r != 1 && r != 2 && r != 4) r = nit == 1 ? 2 : 1;
     if (nit > 4 && r > 1) r = 1;
-    const int R_ = r;
     if (ks == 1) {
-        if (R_ == 1) return launch_nit<FMT, 1, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
-        if (R_ == 2) return launch_nit<FMT, 2, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
-        return launch_nit<FMT, 4, 1>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
+        if (r == 1) return launch_nit<FMT, 1, 1>(nit, J, items, xq, xs, xsum, s);
+        if (r == 2) return launch_nit<FMT, 2, 1>(nit, J, items, xq, xs, xsum, s);
+        return launch_nit<FMT, 4, 1>(nit, J, items, xq, xs, xsum, s);
     }
-    if (R_ == 1) return launch_nit<FMT, 1, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
-    if (R_ == 2) return launch_nit<FMT, 2, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
-    return launch_nit<FMT, 4, 4>(nit, w, L, (int)rows, items, xq, xs, xsum, y, res, s);
+    if (r == 1) return launch_nit<FMT, 1, 4>(nit, J, items, xq, xs, xsum, s);
+    if (r == 2) return launch_nit<FMT, 2, 4>(nit, J, items, xq, xs, xsum, s);
+    return launch_nit<FMT, 4, 4>(nit, J, items, xq, xs, xsum, s);
 }
 
-}  // namespace
-
-namespace {
-
-int gemv_dispatch(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq, const float* d_xscale,
-                  const int32_t* d_xsum, const float* d_res, float* d_y, void* stream) {
-    DqLayout L;
-    if (!dq_layout(fmt, rows, cols, &L)) return DQ_ERR_NOT_SUPPORTED;
-    if (rows == 0) return DQ_OK;
-    if (!d_w || !d_xq || !d_xscale || !d_y) return DQ_ERR_INVALID_ARG;
-    if ((fmt == DQ_FMT_Q4_0 || fmt == DQ_FMT_Q4_K) && !d_xsum) return DQ_ERR_INVALID_ARG;
-    if (rows > 0x3FFFFFFF) return DQ_ERR_NOT_SUPPORTED;
-    const uint8_t* w = (const uint8_t*)d_w;
-    hipStream_t s = (hipStream_t)stream;
+int launch_jobs(int fmt, const Jobs& J, size_t cols, const int8_t* xq, const float* xs, const int32_t* xsum,
+                hipStream_t s) {
     switch (fmt) {
-    case DQ_FMT_Q8_0: return launch_fmt<DQ_FMT_Q8_0>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, d_res, s);
-    case DQ_FMT_Q4_0: return launch_fmt<DQ_FMT_Q4_0>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, d_res, s);
-    case DQ_FMT_Q4_K: return launch_fmt<DQ_FMT_Q4_K>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, d_res, s);
-    case DQ_FMT_Q6_K: return launch_fmt<DQ_FMT_Q6_K>(w, L, rows, cols, d_xq, d_xscale, d_xsum, d_y, d_res, s);
+    case DQ_FMT_Q8_0: return launch_fmt<DQ_FMT_Q8_0>(J, cols, xq, xs, xsum, s);
+    case DQ_FMT_Q4_0: return launch_fmt<DQ_FMT_Q4_0>(J, cols, xq, xs, xsum, s);
+    case DQ_FMT_Q4_K: return launch_fmt<DQ_FMT_Q4_K>(J, cols, xq, xs, xsum, s);
+    case DQ_FMT_Q6_K: return launch_fmt<DQ_FMT_Q6_K>(J, cols, xq, xs, xsum, s);
     }
     return DQ_ERR_NOT_SUPPORTED;
+}
+
+bool per32_act(int fmt) { return fmt == DQ_FMT_Q8_0 || fmt == DQ_FMT_Q4_0; }
+bool needs_sum(int fmt) { return fmt == DQ_FMT_Q4_0 || fmt == DQ_FMT_Q4_K; }
+
+// Validates n jobs; writes the layouts. NOT_SUPPORTED for shapes/formats the
+// kernels do not cover and for groups that mix the per-32 (Q8_0, Q4_0) and
+// per-256 (Q4_K, Q6_K) activation kinds.
+int check_jobs(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* xq, const float* xs,
+               const int32_t* xsum, DqLayout* L) {
+    if (n == 0) return DQ_OK;
+    if (!jobs) return DQ_ERR_INVALID_ARG;
+    if (n > DQ_GEMV_MAX_JOBS) return DQ_ERR_NOT_SUPPORTED;
+    for (size_t j = 0; j < n; ++j) {
+        if (!dq_layout(jobs[j].fmt, jobs[j].rows, cols, &L[j])) return DQ_ERR_NOT_SUPPORTED;
+        if (jobs[j].rows > 0x3FFFFFFF) return DQ_ERR_NOT_SUPPORTED;
+        if (per32_act(jobs[j].fmt) != per32_act(jobs[0].fmt)) return DQ_ERR_NOT_SUPPORTED;
+    }
+    for (size_t j = 0; j < n; ++j) {
+        if (jobs[j].rows == 0) continue;  // nothing to do: no pointer is read
+        if (!jobs[j].d_w || !jobs[j].d_y || !xq || !xs) return DQ_ERR_INVALID_ARG;
+        if (needs_sum(jobs[j].fmt) && !xsum) return DQ_ERR_INVALID_ARG;
+    }
+    return DQ_OK;
+}
+
+// One launch per distinct format, in job order of first appearance.
+int run_jobs(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* xq, const float* xs,
+             const int32_t* xsum, hipStream_t s) {
+    DqLayout L[DQ_GEMV_MAX_JOBS];
+    const int rc = check_jobs(jobs, n, cols, xq, xs, xsum, L);
+    if (rc != DQ_OK || n == 0) return rc;
+    bool done[DQ_GEMV_MAX_JOBS] = {};
+    for (size_t a = 0; a < n; ++a) {
+        if (done[a]) continue;
+        Jobs J{};
+        const int fmt = jobs[a].fmt;
+        for (size_t j = a; j < n; ++j) {
+            if (done[j] || jobs[j].fmt != fmt) continue;
+            done[j] = true;
+            if (jobs[j].rows == 0) continue;
+            J.w[J.n] = (const uint8_t*)jobs[j].d_w;
+            J.L[J.n] = L[j];
+            J.y[J.n] = jobs[j].d_y;
+            J.res[J.n] = jobs[j].d_res;
+            J.rows[J.n] = (int)jobs[j].rows;
+            ++J.n;
+        }
+        if (J.n == 0) continue;
+        const int r = launch_jobs(fmt, J, cols, xq, xs, xsum, s);
+        if (r != DQ_OK) return r;
+    }
+    return DQ_OK;
 }
 
 }  // namespace
 
 extern "C" int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
                        const float* d_xscale, const int32_t* d_xsum, float* d_y, void* stream) {
-    return gemv_dispatch(fmt, d_w, rows, cols, d_xq, d_xscale, d_xsum, nullptr, d_y, stream);
+    const dq_gemv_job_t job = {fmt, d_w, rows, d_y, nullptr};
+    return run_jobs(&job, 1, cols, d_xq, d_xscale, d_xsum, (hipStream_t)stream);
 }
 
 extern "C" int dq_gemv_add(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
                            const float* d_xscale, const int32_t* d_xsum, const float* d_res, float* d_y,
                            void* stream) {
     if (!d_res) return DQ_ERR_INVALID_ARG;
-    return gemv_dispatch(fmt, d_w, rows, cols, d_xq, d_xscale, d_xsum, d_res, d_y, stream);
+    const dq_gemv_job_t job = {fmt, d_w, rows, d_y, d_res};
+    return run_jobs(&job, 1, cols, d_xq, d_xscale, d_xsum, (hipStream_t)stream);
+}
+
+extern "C" int dq_gemv_group(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* d_xq,
+                             const float* d_xscale, const int32_t* d_xsum, void* stream) {
+    return run_jobs(jobs, n, cols, d_xq, d_xscale, d_xsum, (hipStream_t)stream);
 }

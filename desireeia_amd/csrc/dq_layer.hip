@@ -32,7 +32,8 @@ constexpr int NQ_T = 256;
 __global__ __launch_bounds__(NQ_T) void norm_quant_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                           float* __restrict__ h_out, const float* __restrict__ w,
                                                           int n, float eps, int8_t* __restrict__ q,
-                                                          float* __restrict__ scale, int32_t* __restrict__ isum) {
+                                                          float* __restrict__ scale, int32_t* __restrict__ isum,
+                                                          float* __restrict__ y_out) {
     __shared__ double wsum[NQ_T / 64];
     __shared__ float s_scale;
     const int t = threadIdx.x;
@@ -86,6 +87,12 @@ __global__ __launch_bounds__(NQ_T) void norm_quant_kernel(const float* __restric
             y[4 * i + 1] = x.y * sc * ww.y;
             y[4 * i + 2] = x.z * sc * ww.z;
             y[4 * i + 3] = x.w * sc * ww.w;
+        }
+        if (y_out && live) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                reinterpret_cast<float4*>(y_out + c * 16)[i] =
+                    make_float4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(y[i]));
@@ -233,17 +240,33 @@ __global__ __launch_bounds__(256) void silu_quant_kernel(const float* __restrict
     }
 }
 
+// h = silu(gate) * up in float (the input of a Q8_0 / Q4_0 down projection,
+// which quantizes per 32 itself). One lane per value.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                       int n, float* __restrict__ h) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float x = gate[i];
+    h[i] = x / (1.0f + expf(-x)) * up[i];
+}
+
 // ------------------------------------------------------------- workspace --
 struct LayerWs {
-    int8_t* aq;
+    int8_t* aq;    // per-256 activation (K-quant matrices)
     float* as;
     int32_t* ai;
+    int8_t* bq;    // per-32 activation (Q8_0 / Q4_0 matrices)
+    float* bs;
+    int32_t* bi;
+    float* yn;     // float input of the per-32 quantizer
     float *q, *k, *v, *ao, *x2, *up, *gate;
     void* attn;
     size_t attn_bytes, total;
 };
 
 bool kquant(int fmt) { return fmt == DQ_FMT_Q4_K || fmt == DQ_FMT_Q6_K; }
+bool per32(int fmt) { return fmt == DQ_FMT_Q8_0 || fmt == DQ_FMT_Q4_0; }
+bool layer_fmt(int fmt) { return kquant(fmt) || per32(fmt); }
 
 bool layer_ok(const dq_layer_t* L) {
     if (!L || L->head_dim != 128 || L->n_head_kv == 0 || L->n_head % L->n_head_kv) return false;
@@ -252,7 +275,7 @@ bool layer_ok(const dq_layer_t* L) {
     if (L->n_rot == 0 || L->n_rot > L->head_dim || L->n_rot % 2) return false;
     const int f[7] = {L->fmt_q, L->fmt_k, L->fmt_v, L->fmt_o, L->fmt_gate, L->fmt_up, L->fmt_down};
     for (int i = 0; i < 7; ++i)
-        if (!kquant(f[i])) return false;
+        if (!layer_fmt(f[i])) return false;
     return true;
 }
 
@@ -270,6 +293,10 @@ LayerWs carve(const dq_layer_t* L, uint32_t n_ctx, uint8_t* base) {
     w.aq = (int8_t*)take(AN);
     w.as = (float*)take(AN / 32 * 4);
     w.ai = (int32_t*)take(AN / 32 * 4);
+    w.bq = (int8_t*)take(AN);
+    w.bs = (float*)take(AN / 32 * 4);
+    w.bi = (int32_t*)take(AN / 32 * 4);
+    w.yn = (float*)take(AN * 4);
     w.q = (float*)take(QD * 4);
     w.k = (float*)take(KVD * 4);
     w.v = (float*)take(KVD * 4);
@@ -314,7 +341,8 @@ int dq_norm_quant(const float* d_a, const float* d_b, float* d_h, const float* d
                   int8_t* d_q, float* d_scale, int32_t* d_isum, void* stream) {
     if (!d_a || !d_w || !d_q || !d_scale || !d_isum || n == 0 || n % 256) return DQ_ERR_INVALID_ARG;
     if (n > (1u << 26)) return DQ_ERR_NOT_SUPPORTED;
-    norm_quant_kernel<<<1, NQ_T, 0, (hipStream_t)stream>>>(d_a, d_b, d_h, d_w, (int)n, eps, d_q, d_scale, d_isum);
+    norm_quant_kernel<<<1, NQ_T, 0, (hipStream_t)stream>>>(d_a, d_b, d_h, d_w, (int)n, eps, d_q, d_scale, d_isum,
+                                                          nullptr);
     return dq_launch_status();
 }
 
@@ -323,6 +351,14 @@ int dq_silu_quant(const float* d_gate, const float* d_up, size_t n, int8_t* d_q,
     if (!d_gate || !d_up || !d_q || !d_scale || !d_isum || n == 0 || n % 256) return DQ_ERR_INVALID_ARG;
     const unsigned grid = (unsigned)((n / 256 + 3) / 4);
     silu_quant_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(d_gate, d_up, (int)n, d_q, d_scale, d_isum);
+    return dq_launch_status();
+}
+
+int dq_silu_mul(const float* d_gate, const float* d_up, size_t n, float* d_h, void* stream) {
+    if (!d_gate || !d_up || !d_h) return DQ_ERR_INVALID_ARG;
+    if (n == 0) return DQ_OK;
+    if (n > (1u << 30)) return DQ_ERR_NOT_SUPPORTED;
+    silu_mul_kernel<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(d_gate, d_up, (int)n, d_h);
     return dq_launch_status();
 }
 
@@ -355,25 +391,70 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
     if (!d_pos && (pos >= n_ctx || cc_start > pos)) return DQ_ERR_INVALID_ARG;
     const LayerWs w = carve(L, n_ctx, (uint8_t*)d_work);
     if (work_bytes < w.total) return DQ_ERR_INVALID_ARG;
+    const hipStream_t st = (hipStream_t)stream;
     const size_t E = L->n_embd, QD = (size_t)L->n_head * L->head_dim, KVD = (size_t)L->n_head_kv * L->head_dim;
     const size_t F = L->n_ff;
-    // attention block
-    DQ_TRY(dq_norm_quant(d_x, nullptr, nullptr, L->attn_norm, E, L->rms_eps, w.aq, w.as, w.ai, stream));
-    DQ_TRY(dq_gemv(L->fmt_q, L->wq, QD, E, w.aq, w.as, w.ai, w.q, stream));
-    DQ_TRY(dq_gemv(L->fmt_k, L->wk, KVD, E, w.aq, w.as, w.ai, w.k, stream));
-    DQ_TRY(dq_gemv(L->fmt_v, L->wv, KVD, E, w.aq, w.as, w.ai, w.v, stream));
+    // The matrices of a group read the normalised input quantized the way
+    // their format's reference GEMV does: per 256 for Q4_K / Q6_K
+    // (matmul_q4_k_pq / matmul_q6_k_pq on quantize_shared_q8k), per 32 for
+    // Q8_0 / Q4_0 (matmul_q8_0 / matmul_q4_0). The per-256 activation comes
+    // fused with the norm; the per-32 one, when some matrix needs it, from the
+    // normalised float vector.
+    auto norm_acts = [&](const float* x, const float* nw, bool need32) -> int {
+        norm_quant_kernel<<<1, NQ_T, 0, st>>>(x, nullptr, nullptr, nw, (int)E, L->rms_eps, w.aq, w.as, w.ai,
+                                               need32 ? w.yn : nullptr);
+        DQ_TRY(dq_launch_status());
+        if (need32) DQ_TRY(dq_quantize_act(DQ_ACT_Q8_0, w.yn, E, 1, w.bq, w.bs, w.bi, nullptr, stream));
+        return DQ_OK;
+    };
+    // Jobs of one group split by activation kind: one grouped launch each.
+    auto run_group = [&](const dq_gemv_job_t* jobs, int n, size_t cols) -> int {
+        dq_gemv_job_t k4[4], k32[4];
+        int nk = 0, n32 = 0;
+        for (int j = 0; j < n; ++j) {
+            if (per32(jobs[j].fmt)) k32[n32++] = jobs[j];
+            else k4[nk++] = jobs[j];
+        }
+        if (nk) DQ_TRY(dq_gemv_group(k4, nk, cols, w.aq, w.as, w.ai, stream));
+        if (n32) DQ_TRY(dq_gemv_group(k32, n32, cols, w.bq, w.bs, w.bi, stream));
+        return DQ_OK;
+    };
+    // ---- attention block
+    DQ_TRY(norm_acts(d_x, L->attn_norm, per32(L->fmt_q) || per32(L->fmt_k) || per32(L->fmt_v)));
+    {
+        const dq_gemv_job_t jobs[3] = {{L->fmt_q, L->wq, QD, w.q, nullptr},
+                                       {L->fmt_k, L->wk, KVD, w.k, nullptr},
+                                       {L->fmt_v, L->wv, KVD, w.v, nullptr}};
+        DQ_TRY(run_group(jobs, 3, E));
+    }
     DQ_TRY(dq_rope_kv_write(w.q, w.k, w.v, d_rope, L->n_head, L->n_head_kv, L->head_dim, L->n_rot, d_kc, d_vc, pos,
                             d_pos, n_ctx, stream));
-    // the attention's merge also quantizes its output for the projection
-    DQ_TRY(dq_attn_decode_q8_act(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos, n_ctx,
-                                 w.ao, w.aq, w.as, w.ai, w.attn, w.attn_bytes, stream));
-    DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.aq, w.as, w.ai, d_x, w.x2, stream));
-    // feed-forward block
-    DQ_TRY(dq_norm_quant(w.x2, nullptr, nullptr, L->ffn_norm, E, L->rms_eps, w.aq, w.as, w.ai, stream));
-    DQ_TRY(dq_gemv(L->fmt_up, L->wup, F, E, w.aq, w.as, w.ai, w.up, stream));
-    DQ_TRY(dq_gemv(L->fmt_gate, L->wgate, F, E, w.aq, w.as, w.ai, w.gate, stream));
-    DQ_TRY(dq_silu_quant(w.gate, w.up, F, w.aq, w.as, w.ai, stream));
-    DQ_TRY(dq_gemv_add(L->fmt_down, L->wdown, E, F, w.aq, w.as, w.ai, w.x2, d_x_out, stream));
+    if (kquant(L->fmt_o)) {
+        // the attention's merge also quantizes its output for the projection
+        DQ_TRY(dq_attn_decode_q8_act(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos,
+                                     n_ctx, w.ao, w.aq, w.as, w.ai, w.attn, w.attn_bytes, stream));
+        DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.aq, w.as, w.ai, d_x, w.x2, stream));
+    } else {
+        DQ_TRY(dq_attn_decode_q8(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos, n_ctx,
+                                 w.ao, w.attn, w.attn_bytes, stream));
+        DQ_TRY(dq_quantize_act(DQ_ACT_Q8_0, w.ao, QD, 1, w.bq, w.bs, w.bi, nullptr, stream));
+        DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.bq, w.bs, w.bi, d_x, w.x2, stream));
+    }
+    // ---- feed-forward block
+    DQ_TRY(norm_acts(w.x2, L->ffn_norm, per32(L->fmt_gate) || per32(L->fmt_up)));
+    {
+        const dq_gemv_job_t jobs[2] = {{L->fmt_gate, L->wgate, F, w.gate, nullptr},
+                                       {L->fmt_up, L->wup, F, w.up, nullptr}};
+        DQ_TRY(run_group(jobs, 2, E));
+    }
+    if (kquant(L->fmt_down)) {
+        DQ_TRY(dq_silu_quant(w.gate, w.up, F, w.aq, w.as, w.ai, stream));
+        DQ_TRY(dq_gemv_add(L->fmt_down, L->wdown, E, F, w.aq, w.as, w.ai, w.x2, d_x_out, stream));
+    } else {
+        DQ_TRY(dq_silu_mul(w.gate, w.up, F, w.yn, stream));
+        DQ_TRY(dq_quantize_act(DQ_ACT_Q8_0, w.yn, F, 1, w.bq, w.bs, w.bi, nullptr, stream));
+        DQ_TRY(dq_gemv_add(L->fmt_down, L->wdown, E, F, w.bq, w.bs, w.bi, w.x2, d_x_out, stream));
+    }
     return DQ_OK;
 }
 

@@ -138,6 +138,24 @@ def gemv(mat, act, out=None):
     return y
 
 
+def gemv_group(mats, act, outs=None, residuals=None):
+    """Several matrices with the same cols reading one activation
+    (matmul_fused_pq / matvec_shared_group): one launch per distinct format."""
+    lib = _lib.load()
+    n = len(mats)
+    ys = outs if outs is not None else [torch.empty(m.rows, dtype=torch.float32, device=m.buf.device) for m in mats]
+    res = residuals if residuals is not None else [None] * n
+    jobs = (_lib.GemvJob * max(n, 1))()
+    for j, m in enumerate(mats):
+        jobs[j].fmt, jobs[j].d_w, jobs[j].rows = m.fmt, m.buf.data_ptr(), m.rows
+        jobs[j].d_y = ys[j].data_ptr()
+        jobs[j].d_res = res[j].data_ptr() if res[j] is not None else None
+    cols = mats[0].cols if n else 0
+    _lib.check(lib.dq_gemv_group(jobs, n, cols, _ptr(act.q), _ptr(act.scale), _ptr(act.isum), _stream()),
+               "dq_gemv_group")
+    return ys
+
+
 def matmul(mat, x):
     """y = W x with the semantics of the reference's matmul_<fmt> (batch 1)."""
     return gemv(mat, quantize_act(x, act_kind_for(mat.fmt)))

@@ -18,6 +18,7 @@
 #ifndef DESIREEIA_HIP_H
 #define DESIREEIA_HIP_H
 
+#include <stdbool.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -97,6 +98,24 @@ int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_
 int dq_gemv_add(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
                 const float* d_xscale, const int32_t* d_xsum, const float* d_res, float* d_y, void* stream);
 
+/* Grouped GEMV: up to 4 matrices with the same cols reading the same
+ * activation, one launch per distinct format (matmul_fused_pq,
+ * core/matmul.cpp:2586-2639, reached through matvec_shared_group,
+ * models/dense_forward.cpp:554-601; the device counterpart of
+ * matmul_kquant_cuda_resident_same_x, core/engine.h:537-538). Each job's
+ * d_res may be NULL (no residual). Every job must use the activation kind of
+ * the first (Q8_0/Q4_0: DQ_ACT_Q8_0; Q4_K/Q6_K: DQ_ACT_Q8K_REP); mixing the
+ * two kinds or more than 4 jobs: -2, nothing launched. */
+typedef struct {
+    int fmt;
+    const void* d_w;
+    size_t rows;
+    float* d_y;
+    const float* d_res;
+} dq_gemv_job_t;
+int dq_gemv_group(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* d_xq, const float* d_xscale,
+                  const int32_t* d_xsum, void* stream);
+
 /* Prefill GEMM y[n_tok][rows] = x[n_tok][cols] W^T for Q4_K and Q6_K, with the
  * semantics of matmul_q4_k_batch / matmul_q6_k_batch for n_tok >= 4 (the
  * i8_gemm path, core/matmul.cpp:2090-2125 -> :806-845): per-32 activation
@@ -164,6 +183,9 @@ int dq_norm_quant(const float* d_a, const float* d_b, float* d_h, const float* d
                   int8_t* d_q, float* d_scale, int32_t* d_isum, void* stream);
 int dq_silu_quant(const float* d_gate, const float* d_up, size_t n, int8_t* d_q, float* d_scale, int32_t* d_isum,
                   void* stream);
+/* h = silu(gate) * up in fp32 (models/dense_forward.cpp:53-55), the input of a
+ * Q8_0 / Q4_0 down projection (which quantizes per 32 itself). */
+int dq_silu_mul(const float* d_gate, const float* d_up, size_t n, float* d_h, void* stream);
 int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float* d_rope, uint32_t n_head,
                      uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
                      const int32_t* d_pos, uint32_t n_ctx, void* stream);
@@ -172,8 +194,11 @@ int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float
  * branch of models/dense_forward.cpp:3897-4257 (no biases, no QK-norm, no
  * sandwich norms, gated SiLU FFN, Q8_0 KV cache) that cuda_layer_forward
  * (core/engine.h:698-752) runs as one captured episode. Weights are packed
- * device matrices (dq_weights_pack) of K-quant formats (Q4_K / Q6_K; others:
- * -2), head_dim 128. x and x_out are device vectors of n_embd floats (they
+ * device matrices (dq_weights_pack), each of any of the four formats (Q4_K /
+ * Q6_K read the per-256 activation, Q8_0 / Q4_0 the per-32 one, as the
+ * reference CPU GEMVs of those formats do); n_embd, n_ff and n_head*head_dim
+ * multiples of 256, head_dim 128; other shapes: -2. Q/K/V and gate/up each
+ * run as one grouped GEMV. x and x_out are device vectors of n_embd floats (they
  * may not alias); d_rope is the device copy of dq_rope_cache(pos); the KV
  * caches are those of dq_kv_write for this layer. d_pos as for dq_kv_write
  * (graph replay). d_work: dq_layer_workspace_bytes(n_ctx) bytes. */
@@ -189,6 +214,174 @@ int dq_layer_workspace_bytes(const dq_layer_t* layer, uint32_t n_ctx, size_t* by
 int dq_layer_decode(const dq_layer_t* layer, const float* d_x, float* d_x_out, const float* d_rope, uint32_t pos,
                     const int32_t* d_pos, uint32_t cc_start, void* d_kc, void* d_vc, uint32_t n_ctx, void* d_work,
                     size_t work_bytes, void* stream);
+
+
+/* ================================================================ engine layer
+ *
+ * The GPU operator entry points of the reference engine (core/engine.h
+ * :502-811, implemented there by cuda/backend_cuda.cu), with the same names,
+ * argument meaning and return conventions, so models/dense_forward.cpp can
+ * call them unchanged:
+ *   - int results are desireeia_error codes: DQ_OK; DQ_ERR_NOT_SUPPORTED
+ *     (shape, format or feature not covered: nothing was done, y untouched,
+ *     the caller recomputes on the CPU); DQ_ERR_IO (device failure);
+ *   - bool results: false = not done (upload: the matrix stays host-only);
+ *   - x / y / proj / x_out are HOST pointers; each call that returns host
+ *     data synchronises its stream once;
+ *   - one process-global stream, scratch that grows on demand and one device
+ *     KV cache; not thread-safe (as the reference backend).
+ * Where the reference passes a C++ reference (a struct or an out-parameter),
+ * the C ABI takes a pointer; INTEGRATION.md gives the one-line C++ overloads.
+ * Arithmetic follows the reference CPU functions the engine would otherwise
+ * run (matmul_q8_0 / q4_0 / q4_k / q6_k, their _batch forms, the dense
+ * layer); the format ids are those of the reference (0 = Q8_0, 1 = Q4_0,
+ * 5 = Q4_K, 7 = Q6_K). */
+
+/* core/engine.h:536 */
+typedef struct CudaKQuantJob {
+    int format;
+    const void* d_w;
+    size_t rows;
+    float* y; /* host */
+} CudaKQuantJob;
+
+/* core/engine.h:598-603 */
+typedef struct CudaQ80Job {
+    const void* d_qs;
+    const void* d_scale;
+    size_t rows;
+    float* y; /* host */
+} CudaQ80Job;
+
+/* core/engine.h:675-691 (field order kept) */
+typedef struct CudaQkvAttnArgs {
+    const void* wq_qs; const void* wq_scale;
+    const void* wk_qs; const void* wk_scale;
+    const void* wv_qs; const void* wv_scale;
+    const void* wo_qs; const void* wo_scale;
+    const float* bq; const float* bk; const float* bv;
+    const float* attn_in;
+    const float* rope_cache;
+    float* proj;
+    uint8_t* host_k_row;
+    uint8_t* host_v_row;
+    size_t n_embd; size_t q_dim; size_t kv_dim;
+    uint32_t n_head; uint32_t n_head_kv; uint32_t heads_per_kv;
+    uint32_t head_dim; uint32_t n_rot;
+    size_t kv_layer_off;
+    uint32_t cc_start; uint32_t pos;
+} CudaQkvAttnArgs;
+
+/* core/engine.h:698-751 (field order kept) */
+typedef struct CudaLayerArgs {
+    const void* wq_qs; const void* wq_scale;
+    const void* wk_qs; const void* wk_scale;
+    const void* wv_qs; const void* wv_scale;
+    const void* wo_qs; const void* wo_scale;
+    const void* wgate_qs; const void* wgate_scale;
+    const void* wup_qs; const void* wup_scale;
+    const void* wdown_qs; const void* wdown_scale;
+    const void* wag_qs; const void* wag_scale;
+    const float* bq; const float* bk; const float* bv;
+    const float* attn_norm_w; const float* ffn_norm_w;
+    const float* q_norm_w; const float* k_norm_w;
+    const float* post_attn_norm_w; const float* post_ffn_norm_w;
+    const float* x;
+    const float* rope_cache;
+    float* x_out;
+    size_t n_embd; size_t q_dim; size_t kv_dim; size_t n_ff;
+    uint32_t n_head; uint32_t n_head_kv; uint32_t heads_per_kv;
+    uint32_t head_dim; uint32_t n_rot;
+    size_t kv_layer_off;
+    uint32_t cc_start; uint32_t pos;
+    float rms_eps; int act_gelu;
+    int fmt_q; int fmt_k; int fmt_v; int fmt_o;
+    int fmt_gate; int fmt_up; int fmt_down; int fmt_ag;
+    int upload_x; int download_x;
+    int upload_dyn;
+    const uint32_t* dyn_all; const float* rope_all;
+    uint32_t n_slots; uint32_t rope_stride; uint32_t layer_slot;
+    int x_from_token;
+    const void* embd_qs; const void* embd_scale; float embd_mul;
+} CudaLayerArgs;
+
+/* The prefill-layer argument block (core/engine.h:764-796) is not read by
+ * this backend: opaque here. */
+struct CudaLayerBatchArgs;
+
+/* Devices: core/engine.h:627-629. */
+int32_t cuda_gpu_count(void);
+bool cuda_probe_gpu(int32_t index, char* name, size_t name_len, uint64_t* total, uint64_t* free_bytes,
+                    int32_t* cc_major, int32_t* cc_minor, int32_t* sms);
+
+/* Weight upload and lifetime: core/engine.h:516, :532, :556, :557. Q8_0
+ * returns the packed matrix in *out_d_qs and a pointer inside it in
+ * *out_d_scale (both may be passed to cuda_free_device; only the first frees);
+ * K-quants and Q4_0 leave *out_d_scale NULL. Other formats: false. */
+bool matmul_q8_0_cuda_upload_weights(const uint8_t* q8_data, size_t rows, size_t cols, void** out_d_qs,
+                                     void** out_d_scale);
+bool cuda_upload_weights(int format, const uint8_t* data, size_t rows, size_t cols, void** out_d_qs,
+                         void** out_d_scale);
+void cuda_free_device(void* p);
+void cuda_backend_shutdown(void);
+
+/* Decode GEMVs on resident weights: core/engine.h:534, :537-538, :587,
+ * :598-605, and the per-call-upload fallback :507. */
+int matmul_kquant_cuda_resident(int format, const void* d_w, size_t rows, size_t cols, const float* x, float* y);
+int matmul_kquant_cuda_resident_same_x(const CudaKQuantJob* jobs, size_t n, size_t cols, const float* x);
+int matmul_q8_0_cuda_resident(const void* d_qs, const void* d_scale, size_t rows, size_t cols, const float* x,
+                              float* y);
+int matmul_q8_0_cuda_resident_group(const CudaQ80Job* jobs, size_t n, size_t cols, const float* x);
+int matmul_q8_0_cuda(const uint8_t* q8_data, size_t rows, size_t cols, const float* x, float* y);
+
+/* Batched (prefill) product y[n_tok][rows] = x[n_tok][cols] W^T, core/engine.h
+ * :543: Q4_K / Q6_K with the semantics of matmul_q4_k_batch /
+ * matmul_q6_k_batch (i8_gemm for n_tok >= 4, per-token GEMVs below). Other
+ * formats: NOT_SUPPORTED. */
+int matmul_kquant_cuda_batch(int format, const void* d_w, size_t rows, size_t cols, const float* x, size_t n_tok,
+                             float* y);
+
+/* Gated FFN on Q8_0 weights (core/engine.h:612-617): up, gate, silu(gate)*up,
+ * down, one sync. act_gelu = 1 (GELU): NOT_SUPPORTED. */
+int matmul_q8_0_cuda_ffn_gated(const void* d_up_qs, const void* d_up_scale, const void* d_gate_qs,
+                               const void* d_gate_scale, const void* d_down_qs, const void* d_down_scale, size_t n_ff,
+                               size_t n_embd, const float* x, float* out, int act_gelu);
+
+/* Device KV cache, [layer][pos][kv_head][row] bytes as the host cache
+ * (core/engine.h:619-666). */
+bool cuda_kv_cache_reserve(size_t total_bytes);
+void cuda_kv_cache_release(void);
+bool cuda_kv_cache_upload(const void* k_host, const void* v_host, size_t total_bytes);
+bool cuda_kv_cache_download(void* k_host, void* v_host, size_t total_bytes);
+bool cuda_kv_cache_write(size_t byte_off, const void* k, const void* v, size_t bytes);
+bool cuda_kv_cache_read(size_t byte_off, void* k, void* v, size_t bytes);
+bool cuda_kv_cache_move(size_t dst_off, size_t src_off, size_t bytes);
+void cuda_set_attention_long(bool long_context);
+void cuda_drop_graphs(void);
+
+/* Attention episodes over the device Q8_0 KV cache (core/engine.h:806-811,
+ * :692, :752). cuda_attention_out: attention of q (host, q_dim floats) at
+ * [cc_start, pos] of the layer at layer_off, then proj = Wo * out (host).
+ * cuda_qkv_attention_out: Q/K/V (+ optional biases), RoPE, the new KV rows
+ * (device cache and host_k_row / host_v_row), attention and Wo.
+ * cuda_layer_forward: the whole dense layer; x stays on the device between
+ * layers (upload_x on the first, download_x on the last). Features outside
+ * the plain dense layer (attention gate, QK-norm, sandwich norms, GELU,
+ * per-layer RoPE/window slots, embedding from token) and head_dim != 128:
+ * NOT_SUPPORTED. */
+int cuda_attention_out(const void* d_wo_qs, const void* d_wo_scale, const float* q, uint32_t n_head,
+                       uint32_t heads_per_kv, uint32_t head_dim, uint32_t kv_dim, size_t layer_off, uint32_t cc_start,
+                       uint32_t pos, size_t n_embd, size_t q_dim, float* proj, int kv_quantized, size_t row_bytes);
+int cuda_qkv_attention_out(const CudaQkvAttnArgs* args);
+int cuda_layer_forward(const CudaLayerArgs* args);
+
+/* Prefill attention and the prefill layer (core/engine.h:550-555, :797-798)
+ * are outside this backend: NOT_SUPPORTED, and a chunk size of 0. */
+int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, uint32_t n_head,
+                         uint32_t heads_per_kv, uint32_t head_dim, uint32_t q_dim, size_t row_bytes, size_t pos_bytes,
+                         size_t layer_off, uint32_t col0, uint32_t n_swa);
+int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* args);
+int cuda_prefill_chunk_tokens(void);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,396 @@
+"""The engine-layer entry points (include/desireeia_hip.h, the GPU block of the
+reference's core/engine.h) on the GPU, called through the C ABI with host
+buffers as models/dense_forward.cpp calls them, against the oracle:
+GEMVs <= 1e-3, the batched product <= 4e-3 (n_tok >= 4, i8_gemm semantics),
+attention episodes and layers <= 1e-3, KV cache transfers bit-exact.
+NOT_SUPPORTED must leave the caller's outputs untouched."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from desireeia_amd import _lib, synth
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+OK, NOT_SUPPORTED = 0, -2
+Q8_0, Q4_0, Q4_K, Q6_K = synth.Q8_0, synth.Q4_0, synth.Q4_K, synth.Q6_K
+FMT = synth.FMT_OF_TYPE
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def P(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+@pytest.fixture(scope="module")
+def lib(gpu):
+    L = _lib.load()
+    yield L
+    L.cuda_backend_shutdown()
+
+
+class Mat:
+    """A matrix uploaded with the engine's upload entry point."""
+
+    def __init__(self, lib, qtype, rows, cols, seed):
+        self.lib, self.qtype, self.rows, self.cols = lib, qtype, rows, cols
+        self.fmt = FMT[qtype]
+        self.w = np.ascontiguousarray(synth.gen_weights(qtype, rows, cols, seed))
+        qs, sc = ctypes.c_void_p(), ctypes.c_void_p()
+        if qtype == Q8_0:
+            ok = lib.matmul_q8_0_cuda_upload_weights(P(self.w), rows, cols, ctypes.byref(qs), ctypes.byref(sc))
+            assert ok and qs.value and sc.value
+        else:
+            ok = lib.cuda_upload_weights(self.fmt, P(self.w), rows, cols, ctypes.byref(qs), ctypes.byref(sc))
+            assert ok and qs.value and sc.value is None
+        self.qs, self.sc = qs.value, sc.value
+
+    def free(self):
+        self.lib.cuda_free_device(self.sc)  # a Q8_0 scale view: frees nothing
+        self.lib.cuda_free_device(self.qs)
+
+
+def resident(lib, m, x):
+    y = np.full(m.rows, np.nan, np.float32)
+    if m.qtype == Q8_0:
+        rc = lib.matmul_q8_0_cuda_resident(m.qs, m.sc, m.rows, m.cols, P(x), P(y))
+    else:
+        rc = lib.matmul_kquant_cuda_resident(m.fmt, m.qs, m.rows, m.cols, P(x), P(y))
+    assert rc == OK
+    return y
+
+
+def test_probe(lib):
+    n = lib.cuda_gpu_count()
+    assert n >= 1
+    name = ctypes.create_string_buffer(256)
+    total, free = ctypes.c_uint64(), ctypes.c_uint64()
+    ma, mi, sms = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    assert lib.cuda_probe_gpu(0, name, 256, ctypes.byref(total), ctypes.byref(free), ctypes.byref(ma),
+                              ctypes.byref(mi), ctypes.byref(sms))
+    assert total.value > (100 << 30) and 0 < free.value <= total.value and sms.value > 0
+    assert not lib.cuda_probe_gpu(n, name, 256, ctypes.byref(total), ctypes.byref(free), ctypes.byref(ma),
+                                  ctypes.byref(mi), ctypes.byref(sms))
+
+
+@pytest.mark.parametrize("qtype,rows,cols", [(Q8_0, 4096, 4096), (Q4_0, 4096, 14336), (Q4_K, 14336, 4096),
+                                             (Q6_K, 4096, 14336), (Q4_K, 7, 256)])
+def test_resident_gemv(lib, orc, qtype, rows, cols):
+    print(f"resident gemv type={qtype} {rows}x{cols}", flush=True)
+    m = Mat(lib, qtype, rows, cols, seed=rows + cols)
+    x = synth.gen_act(cols, seed=cols)
+    y = resident(lib, m, x)
+    assert rel(y, orc.matmul(qtype, m.w, rows, cols, x)) <= TOL
+    # the same matrix twice in a row gives the same bits
+    assert np.array_equal(y, resident(lib, m, x))
+    m.free()
+
+
+def test_resident_not_supported_leaves_y(lib):
+    m = Mat(lib, Q4_K, 64, 512, seed=1)
+    x = synth.gen_act(512, seed=2)
+    y = np.full(64, 3.0, np.float32)
+    # Q8_0 is not a "kquant" format; a Q4_1 id is not covered; cols mismatch the layout
+    assert lib.matmul_kquant_cuda_resident(0, m.qs, 64, 512, P(x), P(y)) == NOT_SUPPORTED
+    assert lib.matmul_kquant_cuda_resident(2, m.qs, 64, 512, P(x), P(y)) == NOT_SUPPORTED
+    assert lib.matmul_kquant_cuda_resident(FMT[Q4_K], m.qs, 64, 500, P(x), P(y)) == NOT_SUPPORTED
+    assert np.all(y == 3.0)
+    # uploads of formats without a kernel stay host-only
+    qs, sc = ctypes.c_void_p(), ctypes.c_void_p()
+    assert not lib.cuda_upload_weights(6, P(m.w), 64, 512, ctypes.byref(qs), ctypes.byref(sc))
+    assert qs.value is None and sc.value is None
+    m.free()
+
+
+def test_same_x_and_q8_group(lib, orc):
+    cols = 4096
+    x = synth.gen_act(cols, seed=9)
+    ms = [Mat(lib, Q4_K, 4096, cols, 1), Mat(lib, Q4_K, 1024, cols, 2), Mat(lib, Q6_K, 1024, cols, 3),
+          Mat(lib, Q4_0, 512, cols, 4)]
+    jobs = (_lib.CudaKQuantJob * 4)()
+    ys = [np.full(m.rows, np.nan, np.float32) for m in ms]
+    for j, m in enumerate(ms):
+        jobs[j].format, jobs[j].d_w, jobs[j].rows, jobs[j].y = m.fmt, m.qs, m.rows, ys[j].ctypes.data
+    assert lib.matmul_kquant_cuda_resident_same_x(jobs, 4, cols, P(x)) == OK
+    for m, y in zip(ms, ys):
+        assert np.array_equal(y, resident(lib, m, x))
+        assert rel(y, orc.matmul(m.qtype, m.w, m.rows, cols, x)) <= TOL
+    q8 = [Mat(lib, Q8_0, r, cols, 10 + r) for r in (4096, 1024, 1024)]
+    qj = (_lib.CudaQ80Job * 3)()
+    qy = [np.full(m.rows, np.nan, np.float32) for m in q8]
+    for j, m in enumerate(q8):
+        qj[j].d_qs, qj[j].d_scale, qj[j].rows, qj[j].y = m.qs, m.sc, m.rows, qy[j].ctypes.data
+    assert lib.matmul_q8_0_cuda_resident_group(qj, 3, cols, P(x)) == OK
+    for m, y in zip(q8, qy):
+        assert np.array_equal(y, resident(lib, m, x))
+    # per-call upload: the same numbers as the resident matrix
+    y1 = np.empty(4096, np.float32)
+    assert lib.matmul_q8_0_cuda(P(q8[0].w), 4096, cols, P(x), P(y1)) == OK
+    assert np.array_equal(y1, qy[0])
+    for m in ms + q8:
+        m.free()
+
+
+@pytest.mark.parametrize("qtype,rows,cols,n_tok", [(Q4_K, 14336, 4096, 64), (Q6_K, 4096, 14336, 16),
+                                                   (Q4_K, 512, 1024, 3)])
+def test_batch(lib, orc, qtype, rows, cols, n_tok):
+    print(f"batch type={qtype} {rows}x{cols} n_tok={n_tok}", flush=True)
+    m = Mat(lib, qtype, rows, cols, seed=7)
+    x = synth.gen_act((n_tok, cols), seed=8)
+    y = np.full((n_tok, rows), np.nan, np.float32)
+    assert lib.matmul_kquant_cuda_batch(m.fmt, m.qs, rows, cols, P(x), n_tok, P(y)) == OK
+    if n_tok < 4:
+        # below the i8_gemm threshold: exactly the per-token GEMVs
+        for t in range(n_tok):
+            assert np.array_equal(y[t], resident(lib, m, np.ascontiguousarray(x[t])))
+    want = orc.gemm(qtype, m.w, rows, cols, x, n_tok)
+    assert rel(y, want) <= (4e-3 if n_tok >= 4 else TOL)
+    m.free()
+
+
+def test_batch_not_supported(lib):
+    m = Mat(lib, Q4_0, 64, 256, seed=1)
+    x = synth.gen_act((8, 256), seed=2)
+    y = np.full((8, 64), 5.0, np.float32)
+    assert lib.matmul_kquant_cuda_batch(m.fmt, m.qs, 64, 256, P(x), 8, P(y)) == NOT_SUPPORTED
+    assert np.all(y == 5.0)
+    m.free()
+
+
+def test_ffn_gated_q8_0(lib, orc):
+    E, F = 1024, 2816
+    up, gate, down = Mat(lib, Q8_0, F, E, 1), Mat(lib, Q8_0, F, E, 2), Mat(lib, Q8_0, E, F, 3)
+    x = synth.gen_act(E, seed=4)
+    out = np.full(E, np.nan, np.float32)
+    assert lib.matmul_q8_0_cuda_ffn_gated(up.qs, up.sc, gate.qs, gate.sc, down.qs, down.sc, F, E, P(x), P(out),
+                                          0) == OK
+    u = orc.matmul(Q8_0, up.w, F, E, x)
+    g = orc.matmul(Q8_0, gate.w, F, E, x)
+    h = np.array([orc.L.dqo_silu(float(a)) for a in g], np.float32) * u
+    want = orc.matmul(Q8_0, down.w, E, F, h.astype(np.float32))
+    assert rel(out, want) <= TOL
+    keep = out.copy()
+    assert lib.matmul_q8_0_cuda_ffn_gated(up.qs, up.sc, gate.qs, gate.sc, down.qs, down.sc, F, E, P(x), P(out),
+                                          1) == NOT_SUPPORTED
+    assert np.array_equal(out, keep)
+    for m in (up, gate, down):
+        m.free()
+
+
+def test_kv_cache_transfers(lib):
+    n = 1 << 20
+    rng = np.random.default_rng(0)
+    k = rng.integers(0, 256, n, dtype=np.uint8)
+    v = rng.integers(0, 256, n, dtype=np.uint8)
+    assert lib.cuda_kv_cache_reserve(n)
+    assert lib.cuda_kv_cache_upload(P(k), P(v), n)
+    k2, v2 = np.zeros(n, np.uint8), np.zeros(n, np.uint8)
+    assert lib.cuda_kv_cache_download(P(k2), P(v2), n)
+    assert np.array_equal(k, k2) and np.array_equal(v, v2)
+    # one range written, then read back
+    rk = rng.integers(0, 256, 1088, dtype=np.uint8)
+    rv = rng.integers(0, 256, 1088, dtype=np.uint8)
+    assert lib.cuda_kv_cache_write(5000, P(rk), P(rv), 1088)
+    k[5000:6088], v[5000:6088] = rk, rv
+    ok, ov = np.zeros(1088, np.uint8), np.zeros(1088, np.uint8)
+    assert lib.cuda_kv_cache_read(5000, P(ok), P(ov), 1088)
+    assert np.array_equal(ok, rk) and np.array_equal(ov, rv)
+    # overlapping move (memmove semantics), both directions
+    for dst, src, nb in ((1000, 0, 70000), (0, 3000, 90000)):
+        assert lib.cuda_kv_cache_move(dst, src, nb)
+        k[dst:dst + nb] = k[src:src + nb].copy()
+        v[dst:dst + nb] = v[src:src + nb].copy()
+    assert lib.cuda_kv_cache_download(P(k2), P(v2), n)
+    assert np.array_equal(k, k2) and np.array_equal(v, v2)
+    # out of range: refused
+    assert not lib.cuda_kv_cache_write(n - 10, P(rk), P(rv), 1088)
+    assert not lib.cuda_kv_cache_move(0, n - 10, 100)
+    lib.cuda_kv_cache_release()
+    assert not lib.cuda_kv_cache_download(P(k2), P(v2), n)
+
+
+def prior_cache(orc, n_layers, n_ctx, n_kv, hd, n_prior, seed):
+    """Host KV cache [layer][pos][kv_head][row] with n_prior N(0,1) rows per layer."""
+    rng = np.random.default_rng(seed)
+    pb = n_kv * hd // 32 * 34
+    kc = np.zeros(n_layers * n_ctx * pb, np.uint8)
+    vc = np.zeros_like(kc)
+    for l in range(n_layers):
+        o = l * n_ctx * pb
+        if n_prior:
+            kc[o:o + n_prior * pb] = orc.kv_quantize_row(rng.standard_normal(n_prior * n_kv * hd).astype(np.float32))
+            vc[o:o + n_prior * pb] = orc.kv_quantize_row(rng.standard_normal(n_prior * n_kv * hd).astype(np.float32))
+    return kc, vc, pb
+
+
+@pytest.mark.parametrize("wo_type", [Q8_0, Q4_K])
+def test_attention_out(lib, orc, wo_type):
+    n_head, n_kv, hd, E, n_ctx, pos = 32, 8, 128, 4096, 600, 517
+    kc, vc, pb = prior_cache(orc, 2, n_ctx, n_kv, hd, pos + 1, seed=3)
+    assert lib.cuda_kv_cache_reserve(kc.size)
+    assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+    wo = Mat(lib, wo_type, E, n_head * hd, 5)
+    q = synth.gen_act(n_head * hd, seed=6)
+    proj = np.full(E, np.nan, np.float32)
+    off = n_ctx * pb  # layer 1
+    sc = wo.sc if wo_type == Q8_0 else wo.qs  # the engine passes a non-null scale pointer
+    rc = lib.cuda_attention_out(wo.qs, sc, P(q), n_head, n_head // n_kv, hd, n_kv * hd, off, 3, pos, E,
+                                n_head * hd, P(proj), 1, hd // 32 * 34)
+    assert rc == OK
+    ao = orc.attn_decode(q, kc[off:], vc[off:], n_head, n_kv, hd, 3, pos)
+    want = orc.matmul(wo_type, wo.w, E, n_head * hd, ao)
+    assert rel(proj, want) <= TOL
+    # not covered: an unquantized cache
+    keep = proj.copy()
+    assert lib.cuda_attention_out(wo.qs, sc, P(q), n_head, n_head // n_kv, hd, n_kv * hd, off, 3, pos, E,
+                                  n_head * hd, P(proj), 0, hd * 4) == NOT_SUPPORTED
+    assert np.array_equal(proj, keep)
+    wo.free()
+    lib.cuda_kv_cache_release()
+
+
+def test_qkv_attention_out(lib, orc):
+    n_head, n_kv, hd, E, n_ctx, pos = 8, 2, 128, 1024, 200, 130
+    qd, kvd = n_head * hd, n_kv * hd
+    kc, vc, pb = prior_cache(orc, 1, n_ctx, n_kv, hd, pos, seed=4)
+    assert lib.cuda_kv_cache_reserve(kc.size)
+    assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+    wq, wk, wv, wo = Mat(lib, Q8_0, qd, E, 1), Mat(lib, Q8_0, kvd, E, 2), Mat(lib, Q8_0, kvd, E, 3), \
+        Mat(lib, Q8_0, E, qd, 4)
+    rng = np.random.default_rng(5)
+    bq, bk, bv = (rng.standard_normal(n).astype(np.float32) for n in (qd, kvd, kvd))
+    x = synth.gen_act(E, seed=6)
+    rope = orc.rope_cache(hd, pos, 500000.0)
+    proj = np.full(E, np.nan, np.float32)
+    hk, hv = np.zeros(pb, np.uint8), np.zeros(pb, np.uint8)
+    A = _lib.CudaQkvAttnArgs()
+    A.wq_qs, A.wq_scale, A.wk_qs, A.wk_scale = wq.qs, wq.sc, wk.qs, wk.sc
+    A.wv_qs, A.wv_scale, A.wo_qs, A.wo_scale = wv.qs, wv.sc, wo.qs, wo.sc
+    A.bq, A.bk, A.bv = bq.ctypes.data, bk.ctypes.data, bv.ctypes.data
+    A.attn_in, A.rope_cache, A.proj = x.ctypes.data, rope.ctypes.data, proj.ctypes.data
+    A.host_k_row, A.host_v_row = hk.ctypes.data, hv.ctypes.data
+    A.n_embd, A.q_dim, A.kv_dim = E, qd, kvd
+    A.n_head, A.n_head_kv, A.heads_per_kv, A.head_dim, A.n_rot = n_head, n_kv, n_head // n_kv, hd, hd
+    A.kv_layer_off, A.cc_start, A.pos = 0, 0, pos
+    assert lib.cuda_qkv_attention_out(ctypes.byref(A)) == OK
+    # oracle: biased Q/K/V, NeoX RoPE, the new rows, attention, Wo
+    q = orc.matmul(Q8_0, wq.w, qd, E, x) + bq
+    k = orc.matmul(Q8_0, wk.w, kvd, E, x) + bk
+    v = orc.matmul(Q8_0, wv.w, kvd, E, x) + bv
+    for h in range(n_head):
+        q[h * hd:(h + 1) * hd] = orc.rope_neox(q[h * hd:(h + 1) * hd].copy(), hd, rope)
+    for h in range(n_kv):
+        k[h * hd:(h + 1) * hd] = orc.rope_neox(k[h * hd:(h + 1) * hd].copy(), hd, rope)
+    krow, vrow = orc.kv_quantize_row(k.astype(np.float32)), orc.kv_quantize_row(v.astype(np.float32))
+    kc[pos * pb:(pos + 1) * pb], vc[pos * pb:(pos + 1) * pb] = krow, vrow
+    ao = orc.attn_decode(q.astype(np.float32), kc, vc, n_head, n_kv, hd, 0, pos)
+    want = orc.matmul(Q8_0, wo.w, E, qd, ao)
+    assert rel(proj, want) <= TOL
+    # the host slot received the device's row: the oracle's row up to GEMV rounding
+    assert rel(orc.dequantize_row(Q8_0, hk, kvd), orc.dequantize_row(Q8_0, krow, kvd)) <= 2e-2
+    assert rel(orc.dequantize_row(Q8_0, hv, kvd), orc.dequantize_row(Q8_0, vrow, kvd)) <= 2e-2
+    dk = np.zeros(pb, np.uint8)
+    dv = np.zeros(pb, np.uint8)
+    assert lib.cuda_kv_cache_read(pos * pb, P(dk), P(dv), pb)
+    assert np.array_equal(dk, hk) and np.array_equal(dv, hv)
+    for m in (wq, wk, wv, wo):
+        m.free()
+    lib.cuda_kv_cache_release()
+
+
+def make_layer(lib, orc, E, n_head, n_kv, F, types, seed):
+    from oracle.oracle import LayerArgs
+    hd = 128
+    qd, kvd = n_head * hd, n_kv * hd
+    names = ("q", "k", "v", "o", "gate", "up", "down")
+    shapes = {"q": (qd, E), "k": (kvd, E), "v": (kvd, E), "o": (E, qd), "gate": (F, E), "up": (F, E),
+              "down": (E, F)}
+    mats = {nm: Mat(lib, types[i], *shapes[nm], seed + i) for i, nm in enumerate(names)}
+    rng = np.random.default_rng(seed)
+    an = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+    fn = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+    oa = LayerArgs(E, n_head, n_kv, hd, F, 1e-5, 500000.0, *types)
+    for nm in names:
+        setattr(oa, "w" + nm, mats[nm].w.ctypes.data)
+    oa.attn_norm, oa.ffn_norm = an.ctypes.data, fn.ctypes.data
+    return mats, an, fn, oa
+
+
+def layer_args(mats, an, fn, E, n_head, n_kv, F, layer_off, pos, rope, x, x_out, upload_x, download_x, upload_dyn):
+    hd = 128
+    A = _lib.CudaLayerArgs()
+    for nm, key in (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo"), ("gate", "wgate"), ("up", "wup"),
+                    ("down", "wdown")):
+        setattr(A, key + "_qs", mats[nm].qs)
+        setattr(A, key + "_scale", mats[nm].sc)
+        setattr(A, "fmt_" + nm, mats[nm].fmt)
+    A.attn_norm_w, A.ffn_norm_w = an.ctypes.data, fn.ctypes.data
+    A.x = x.ctypes.data if x is not None else None
+    A.x_out = x_out.ctypes.data if x_out is not None else None
+    A.rope_cache = rope.ctypes.data
+    A.n_embd, A.q_dim, A.kv_dim, A.n_ff = E, n_head * hd, n_kv * hd, F
+    A.n_head, A.n_head_kv, A.heads_per_kv, A.head_dim, A.n_rot = n_head, n_kv, n_head // n_kv, hd, hd
+    A.kv_layer_off, A.cc_start, A.pos, A.rms_eps = layer_off, 0, pos, 1e-5
+    A.upload_x, A.download_x, A.upload_dyn = upload_x, download_x, upload_dyn
+    return A
+
+
+def test_layer_forward_chain(lib, orc):
+    """Two layers of one token (Q4_K_M mix, then an all-Q8_0 layer with a Q4_0
+    FFN), x kept on the device between them, against the oracle composition;
+    the device KV rows written at pos match the oracle's to GEMV rounding."""
+    E, n_head, n_kv, F, n_ctx, pos = 1024, 8, 2, 2816, 128, 77
+    kc, vc, pb = prior_cache(orc, 2, n_ctx, n_kv, 128, pos, seed=11)
+    assert lib.cuda_kv_cache_reserve(kc.size)
+    assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+    t0 = (Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K)
+    t1 = (Q8_0, Q8_0, Q8_0, Q8_0, Q4_0, Q4_0, Q8_0)
+    L0 = make_layer(lib, orc, E, n_head, n_kv, F, t0, 20)
+    L1 = make_layer(lib, orc, E, n_head, n_kv, F, t1, 40)
+    rope = orc.rope_cache(128, pos, 500000.0)
+    x = synth.gen_act(E, seed=12)
+    out = np.full(E, np.nan, np.float32)
+    A0 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos, rope, x, None, 1, 0, 1)
+    A1 = layer_args(*L1[:3], E, n_head, n_kv, F, n_ctx * pb, pos, rope, None, out, 0, 1, 0)
+    assert lib.cuda_layer_forward(ctypes.byref(A0)) == OK
+    assert lib.cuda_layer_forward(ctypes.byref(A1)) == OK
+    k0, v0 = kc[:n_ctx * pb].copy(), vc[:n_ctx * pb].copy()
+    k1, v1 = kc[n_ctx * pb:].copy(), vc[n_ctx * pb:].copy()
+    h = orc.layer_decode(L0[3], k0, v0, pos, x)[0]
+    want = orc.layer_decode(L1[3], k1, v1, pos, h)[0]
+    e = rel(out, want)
+    print(f"two-layer rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    dk, dv = np.zeros_like(kc), np.zeros_like(vc)
+    assert lib.cuda_kv_cache_download(P(dk), P(dv), kc.size)
+    kvd = n_kv * 128
+    for o, ref_k, ref_v in ((0, k0, v0), (n_ctx * pb, k1, v1)):
+        row = slice(o + pos * pb, o + (pos + 1) * pb)
+        rrow = slice(pos * pb, (pos + 1) * pb)
+        assert rel(orc.dequantize_row(Q8_0, dk[row], kvd), orc.dequantize_row(Q8_0, ref_k[rrow], kvd)) <= 2e-2
+        assert rel(orc.dequantize_row(Q8_0, dv[row], kvd), orc.dequantize_row(Q8_0, ref_v[rrow], kvd)) <= 2e-2
+        # the prior rows are untouched
+        assert np.array_equal(dk[o:o + pos * pb], kc[o:o + pos * pb])
+    # a feature outside the plain layer: NOT_SUPPORTED, output untouched
+    keep = out.copy()
+    bias = np.zeros(n_head * 128, np.float32)
+    A2 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos, rope, x, out, 1, 1, 1)
+    A2.bq = bias.ctypes.data
+    assert lib.cuda_layer_forward(ctypes.byref(A2)) == NOT_SUPPORTED
+    assert np.array_equal(out, keep)
+    for L in (L0, L1):
+        for m in L[0].values():
+            m.free()
+    lib.cuda_kv_cache_release()
+
+
+def test_out_of_scope_entries(lib):
+    assert lib.cuda_layer_forward_batch(None) == NOT_SUPPORTED
+    assert lib.cuda_attention_batch(None, None, 1, 1, 1, 128, 128, 136, 136, 0, 0, 0) == NOT_SUPPORTED
+    assert lib.cuda_prefill_chunk_tokens() == 0
