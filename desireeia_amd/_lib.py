@@ -42,6 +42,9 @@ SIGNATURES = {
     "dq_layer_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
     "dq_layer_decode": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_p, c_u32, c_p, c_p, c_u32, c_p, c_size, c_p]),
     "dq_silu_mul": (c_int, [c_p, c_p, c_size, c_p, c_p]),
+    "dq_moe_route": (c_int, [c_p, c_u32, c_u32, c_u32, c_int, c_f, c_p, c_p, c_p]),
+    "dq_moe_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
+    "dq_moe_ffn": (c_int, [c_p, c_p, c_p, c_u32, c_p, c_p, c_size, c_p]),
     # engine layer (core/engine.h GPU block); struct arguments as void*
     "cuda_gpu_count": (ctypes.c_int32, []),
     "cuda_probe_gpu": (ctypes.c_bool, [ctypes.c_int32, c_p, c_size, c_p, c_p, c_p, c_p, c_p]),
@@ -113,6 +116,12 @@ class CudaLayerArgs(ctypes.Structure):
                 + [("dyn_all", c_p), ("rope_all", c_p), ("n_slots", c_u32), ("rope_stride", c_u32),
                    ("layer_slot", c_u32), ("x_from_token", c_int), ("embd_qs", c_p), ("embd_scale", c_p),
                    ("embd_mul", c_f)])
+
+
+class MoeDesc(ctypes.Structure):
+    """dq_moe_t of include/desireeia_hip.h."""
+    _fields_ = [("n_expert", c_u32), ("n_expert_used", c_u32), ("n_embd", c_u32), ("n_ff", c_u32),
+                ("norm_w", c_int), ("w_scale", c_f), ("fmt", c_int), ("wgate", c_p), ("wup", c_p), ("wdown", c_p)]
 
 
 class GemvJob(ctypes.Structure):

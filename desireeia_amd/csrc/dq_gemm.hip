@@ -26,30 +26,12 @@
 // item order (both operands, see dq_quantize_act_f16), so a 64-column K step
 // is exactly one 64-weight item.
 #include "dq_common.h"
+#include "dq_f16.h"
 
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef float f16v __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BK = 64, NS = 3;  // tile rows (tokens), K per step, ring stages
-
-// Bytes 0/1 (sel 0x04010400) or 2/3 (sel 0x04030402) of v, each below 1024,
-// as the fp16 pair (1024 + v_lo, 1024 + v_hi): v_perm_b32 slots the byte under
-// the 0x64 exponent byte.
-__device__ __forceinline__ h2 magic_pair(uint32_t v, uint32_t sel) {
-    return __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, v, sel));
-}
-
-// 4 byte values (each < 1024 - bias) of word v -> 2 fp16 pairs (v - bias) * a.
-// The subtraction is exact; the product rounds once.
-__device__ __forceinline__ void bytes_to_h2(uint32_t v, h2 bias, h2 a, uint32_t* out) {
-    const h2 p0 = (magic_pair(v, 0x04010400u) - bias) * a;
-    const h2 p1 = (magic_pair(v, 0x04030402u) - bias) * a;
-    out[0] = __builtin_bit_cast(uint32_t, p0);
-    out[1] = __builtin_bit_cast(uint32_t, p1);
-}
 
 // ------------------------------------------------------------ LDS layout --
 // Ring of NS stages, each holding one K step of both operands:
@@ -183,19 +165,6 @@ __device__ __forceinline__ void issue_stage(const GemmArgs& g, uint8_t* ring, in
 }
 
 __device__ __forceinline__ const h8& lds_h8(const uint8_t* p) { return *reinterpret_cast<const h8*>(p); }
-
-// Q4_K 6-bit scale of sub-block j from header words w0 (scale bytes 0-3),
-// w1 (4-7), w2 (8-11) (quant/quant.cpp:22-29).
-__device__ __forceinline__ int q4k_scale(int j, uint32_t w0, uint32_t w1, uint32_t w2) {
-    if (j < 4) return (w0 >> (8 * j)) & 63;
-    const int sh = 8 * (j - 4);
-    return (int)(((w2 >> sh) & 0xF) | (((w0 >> sh) & 0xFF) >> 6 << 4));
-}
-__device__ __forceinline__ int q4k_min(int j, uint32_t w0, uint32_t w1, uint32_t w2) {
-    if (j < 4) return (w1 >> (8 * j)) & 63;
-    const int sh = 8 * (j - 4);
-    return (int)((((w2 >> sh) & 0xFF) >> 4) | (((w1 >> sh) & 0xFF) >> 6 << 4));
-}
 
 // B fragments of one ring stage for this lane: bf[kk][j], kk = 16-wide K
 // slice, j = 32-row n block. Lane l feeds row n = wn*64 + j*32 + l%32 with the

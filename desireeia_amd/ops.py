@@ -290,3 +290,52 @@ class DecoderLayer:
                                        _ptr(self.cache.k), _ptr(self.cache.v), self.cache.n_ctx, _ptr(self.work),
                                        self.work.numel(), _stream()), "dq_layer_decode")
         return y
+
+
+class MoeLayer:
+    """Expert FFN of one MoE layer on the device (dq_moe_ffn): stacked Q4_K
+    experts, gate/up [n_expert * n_ff][n_embd] and down [n_expert * n_embd][n_ff]
+    (models/dense_forward.cpp:1524-1560, combined as at :4160-4181)."""
+
+    def __init__(self, wgate, wup, wdown, n_expert, n_expert_used, norm_w=True, w_scale=1.0):
+        """wgate/wup/wdown: QuantMatrix (stacked experts)."""
+        self.mats = (wgate, wup, wdown)
+        self.n_embd, self.n_ff = wgate.cols, wdown.cols
+        d = _lib.MoeDesc(n_expert, n_expert_used, self.n_embd, self.n_ff, int(norm_w), w_scale, wgate.fmt,
+                         wgate.buf.data_ptr(), wup.buf.data_ptr(), wdown.buf.data_ptr())
+        self.desc = d
+        self._work = None
+
+    def workspace(self, n_tok, device):
+        lib = _lib.load()
+        n = ctypes.c_size_t(0)
+        _lib.check(lib.dq_moe_workspace_bytes(ctypes.byref(self.desc), n_tok, ctypes.byref(n)),
+                   "dq_moe_workspace_bytes")
+        if self._work is None or self._work.numel() < n.value:
+            self._work = torch.empty(max(n.value, 1), dtype=torch.uint8, device=device)
+        return self._work
+
+    def __call__(self, x, logits, out=None):
+        """x [n_tok][n_embd], logits [n_tok][n_expert] fp32 device tensors."""
+        lib = _lib.load()
+        x = x.contiguous()
+        logits = logits.contiguous()
+        n_tok = x.shape[0]
+        y = out if out is not None else torch.empty(n_tok, self.n_embd, dtype=torch.float32, device=x.device)
+        wk = self.workspace(n_tok, x.device)
+        _lib.check(lib.dq_moe_ffn(ctypes.byref(self.desc), _ptr(x), _ptr(logits), n_tok, _ptr(y), _ptr(wk),
+                                  wk.numel(), _stream()), "dq_moe_ffn")
+        return y
+
+
+def moe_route(logits, k, norm_w=True, w_scale=1.0):
+    """Router (moe_route_ex, softmax gating) of logits [n_tok][n_expert]:
+    ids int32 [n_tok][k], weights fp32 [n_tok][k]."""
+    lib = _lib.load()
+    logits = logits.contiguous()
+    n_tok, n_exp = logits.shape
+    ids = torch.empty(n_tok, k, dtype=torch.int32, device=logits.device)
+    wts = torch.empty(n_tok, k, dtype=torch.float32, device=logits.device)
+    _lib.check(lib.dq_moe_route(_ptr(logits), n_tok, n_exp, k, int(norm_w), w_scale, _ptr(ids), _ptr(wts), _stream()),
+               "dq_moe_route")
+    return ids, wts

@@ -216,6 +216,39 @@ int dq_layer_decode(const dq_layer_t* layer, const float* d_x, float* d_x_out, c
                     size_t work_bytes, void* stream);
 
 
+/* ------------------------------------------------------------------ MoE */
+
+/* Router of one MoE layer for n_tok tokens (moe_route_ex with softmax gating,
+ * models/moe_route.cpp:10-81): probabilities by softmax (float max, double
+ * sum), the k largest in descending order (ties: lower expert index),
+ * renormalised by their float sum when norm_w, then times w_scale (0 and 1
+ * mean no scaling). logits [n_tok][n_expert] -> ids, wts [n_tok][k].
+ * n_expert <= 64, k <= 8: otherwise -2. */
+int dq_moe_route(const float* d_logits, uint32_t n_tok, uint32_t n_expert, uint32_t k, int norm_w, float w_scale,
+                 int32_t* d_ids, float* d_wts, void* stream);
+
+/* Expert FFN of one MoE layer (models/dense_forward.cpp:1524-1560 expert_ffn,
+ * stacked experts, combined as at :4160-4181): for every token, its k routed
+ * experts' SwiGLU FFNs (matmul_q4_k semantics: activations quantized per
+ * 256) weighted and summed in slot order. Experts are stacked packed
+ * matrices (dq_weights_pack): gate and up [n_expert * n_ff][n_embd], down
+ * [n_expert * n_embd][n_ff], all Q4_K (other formats: -2); n_embd and n_ff
+ * multiples of 256; n_tok <= 65536. x [n_tok][n_embd], logits
+ * [n_tok][n_expert], out [n_tok][n_embd] (device). Each expert's weights are
+ * read once per call for all its tokens. Results within 4e-3 of the
+ * reference composition (fp16 MFMA operands). d_work:
+ * dq_moe_workspace_bytes(n_tok) bytes. */
+typedef struct {
+    uint32_t n_expert, n_expert_used, n_embd, n_ff;
+    int norm_w;
+    float w_scale;
+    int fmt; /* DQ_FMT_Q4_K */
+    const void *wgate, *wup, *wdown;
+} dq_moe_t;
+int dq_moe_workspace_bytes(const dq_moe_t* m, uint32_t n_tok, size_t* bytes);
+int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint32_t n_tok, float* d_out, void* d_work,
+               size_t work_bytes, void* stream);
+
 /* ================================================================ engine layer
  *
  * The GPU operator entry points of the reference engine (core/engine.h

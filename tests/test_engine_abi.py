@@ -11,8 +11,9 @@ import pytest
 from desireeia_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-STRUCTS = [_lib.CudaKQuantJob, _lib.CudaQ80Job, _lib.CudaQkvAttnArgs, _lib.CudaLayerArgs, _lib.GemvJob]
-C_NAME = {"GemvJob": "dq_gemv_job_t"}
+STRUCTS = [_lib.CudaKQuantJob, _lib.CudaQ80Job, _lib.CudaQkvAttnArgs, _lib.CudaLayerArgs, _lib.GemvJob,
+           _lib.MoeDesc]
+C_NAME = {"GemvJob": "dq_gemv_job_t", "MoeDesc": "dq_moe_t"}
 
 
 @pytest.fixture(scope="module")
