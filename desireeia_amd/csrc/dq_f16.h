@@ -38,3 +38,35 @@ __device__ __forceinline__ int q4k_min(int j, uint32_t w0, uint32_t w1, uint32_t
     return (int)((((w2 >> sh) & 0xFF) >> 4) | (((w1 >> sh) & 0xFF) >> 6 << 4));
 }
 
+
+namespace {
+
+// fp16 operands have a range of 65504, and a min column (a sum over a
+// 32-block) reaches 32 * max|v| of its activation row. Each activation row is
+// therefore multiplied by a power of two s that puts 32 * max|v| at or below
+// 2^15 (exact: only the exponent moves; small rows are scaled up, away from
+// the fp16 subnormals), and the GEMM multiplies its output row by 1/s.
+// row_scale_kernel: one 256-thread workgroup per row of `cols` floats
+// (cols % 4 == 0), s = 2^(15 - E) with 32 * max|v| = m * 2^E, m in [0.5, 1).
+__global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict__ src, int cols,
+                                                        float* __restrict__ scale) {
+    __shared__ float wmax[4];
+    const float* row = src + (size_t)blockIdx.x * cols;
+    float m = 0.0f;
+    for (int c = threadIdx.x * 4; c < cols; c += 1024) {
+        const float4 f = *reinterpret_cast<const float4*>(row + c);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
+    }
+    m = dq_wave_max(m);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float r = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+        int E = 0;
+        if (r > 0.0f && r <= 3.0e38f) frexpf(32.0f * r, &E);
+        E = E < -100 ? -100 : (E > 115 ? 115 : E);
+        scale[blockIdx.x] = ldexpf(1.0f, 15 - E);
+    }
+}
+
+}  // namespace

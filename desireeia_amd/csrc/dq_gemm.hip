@@ -89,6 +89,7 @@ struct GemmArgs {
     DqLayout L;
     const _Float16* A;      // activations [M][lda]
     const _Float16* mins;   // Q4_K min plane [N][ld_min] (fp16 -dmin*m), or null
+    const float* inv;       // per token: 1/s of its activation row
     int lda, ld_min, M, N, K;
     int m0, n0;
 };
@@ -350,8 +351,9 @@ __global__ __launch_bounds__(2 * BN) void gemm_kernel(GemmArgs g, float* __restr
                 const int m = g.m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
                 if (m < g.M) {
                     float* dst = y + (size_t)m * g.N + n;
-                    if (atomic_out) atomicAdd(dst, acc[i][j][r]);
-                    else *dst = acc[i][j][r];
+                    const float v = acc[i][j][r] * g.inv[m];  // a power of two: exact
+                    if (atomic_out) atomicAdd(dst, v);
+                    else *dst = v;
                 }
             }
         }
@@ -379,18 +381,22 @@ __global__ __launch_bounds__(256) void min_plane_kernel(const uint8_t* __restric
 }
 
 // Activation quantizer for the GEMM: per 32-block the reference integers and
-// scale (core/i8gemm_impl.h:50-82), written as fp16(q*d) in K order `perm`
-// (0 natural, 1 Q6_K item order), plus fp16(exact float block sum) in the
-// min columns [cols, cols + n_min) (zero past cols/32). One lane per block.
+// scale (core/i8gemm_impl.h:50-82), written as fp16(q*d*s) in K order `perm`
+// (0 natural, 1 Q6_K item order), plus fp16(exact float block sum * s) in the
+// min columns [cols, cols + n_min) (zero past cols/32), s the row's power-of-two
+// range scale (row_scale_kernel) and inv[t] = 1/s. One lane per block.
 __global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restrict__ x, int cols, int n_tok,
                                                            _Float16* __restrict__ out, int lda, int with_min,
-                                                           int n_min, int perm) {
+                                                           int n_min, int perm, const float* __restrict__ rscale,
+                                                           float* __restrict__ inv) {
     const int nb = cols / 32;
     const int gb = blockIdx.x * blockDim.x + threadIdx.x;
     const int stride = nb + (with_min ? n_min : 0);
     if (gb >= n_tok * stride) return;
     const int t = gb / stride, b = gb % stride;
     _Float16* o = out + (size_t)t * lda;
+    const float sc = rscale[t];
+    if (b == 0) inv[t] = 1.0f / sc;
     if (b >= nb) {  // min column b - nb
         const int mb = b - nb;
         if (mb >= nb) {
@@ -400,7 +406,7 @@ __global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restri
         const float* p = x + (size_t)t * cols + 32 * mb;
         float fs = 0.0f;
         for (int i = 0; i < 32; ++i) fs += p[i];
-        o[cols + mb] = (_Float16)fs;
+        o[cols + mb] = (_Float16)(fs * sc);
         return;
     }
     const float* p = x + (size_t)t * cols + 32 * b;
@@ -423,7 +429,7 @@ __global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restri
     for (int i = 0; i < 32; ++i) {
         int q = (int)rintf(v[i] * id);
         q = q > 127 ? 127 : (q < -127 ? -127 : q);
-        h[i] = (_Float16)((float)q * d);
+        h[i] = (_Float16)(((float)q * d) * sc);
     }
     if (perm == 0) {
         dq_u32x4* dst = reinterpret_cast<dq_u32x4*>(o + 32 * b);
@@ -464,7 +470,8 @@ int cus() {
 }  // namespace
 
 // Workspace of the GEMM: the activation [n_tok][lda] fp16 (lda = cols + the
-// min columns for Q4_K), then for Q4_K the min plane [rows][n_min] fp16.
+// min columns for Q4_K), the row scales s and 1/s [n_tok], then for Q4_K the
+// min plane [rows][n_min] fp16.
 static void gemm_act_shape(int fmt, size_t cols, int* lda, int* n_min) {
     *n_min = fmt == DQ_FMT_Q4_K ? (int)((cols / 32 + BK - 1) / BK * BK) : 0;
     *lda = (int)cols + *n_min;
@@ -476,13 +483,19 @@ static size_t act_bytes(int fmt, size_t cols, size_t n_tok) {
     return dq_align256(n_tok * (size_t)lda * 2);
 }
 
+static size_t scale_off(int fmt, size_t cols, size_t n_tok) { return act_bytes(fmt, cols, n_tok); }
+static size_t inv_off(int fmt, size_t cols, size_t n_tok) {
+    return scale_off(fmt, cols, n_tok) + dq_align256(n_tok * 4);
+}
+static size_t min_off(int fmt, size_t cols, size_t n_tok) { return inv_off(fmt, cols, n_tok) + dq_align256(n_tok * 4); }
+
 extern "C" int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t n_tok, size_t* bytes) {
     if (!bytes) return DQ_ERR_INVALID_ARG;
     if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K) return DQ_ERR_NOT_SUPPORTED;
     if (cols % 256) return DQ_ERR_NOT_SUPPORTED;
     int lda, n_min;
     gemm_act_shape(fmt, cols, &lda, &n_min);
-    *bytes = act_bytes(fmt, cols, n_tok) + dq_align256(rows * (size_t)n_min * 2);
+    *bytes = min_off(fmt, cols, n_tok) + dq_align256(rows * (size_t)n_min * 2);
     return DQ_OK;
 }
 
@@ -496,8 +509,12 @@ extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_
     gemm_act_shape(fmt, cols, &lda, &n_min);
     const int nb = (int)cols / 32;
     const size_t lanes = n_tok * (size_t)(nb + n_min);
+    uint8_t* base = (uint8_t*)d_out;
+    float* sc = (float*)(base + scale_off(fmt, cols, n_tok));
+    float* inv = (float*)(base + inv_off(fmt, cols, n_tok));
+    row_scale_kernel<<<(unsigned)n_tok, 256, 0, (hipStream_t)stream>>>(d_x, (int)cols, sc);
     quantize_f16_kernel<<<(unsigned)((lanes + 255) / 256), 256, 0, (hipStream_t)stream>>>(
-        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, lda, fmt == DQ_FMT_Q4_K, n_min, fmt == DQ_FMT_Q6_K);
+        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, lda, fmt == DQ_FMT_Q4_K, n_min, fmt == DQ_FMT_Q6_K, sc, inv);
     return dq_launch_status();
 }
 
@@ -536,13 +553,14 @@ extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols
     g.w = (const uint8_t*)d_w;
     g.L = L;
     g.A = (const _Float16*)d_work;
+    g.inv = (const float*)((const uint8_t*)d_work + inv_off(fmt, cols, n_tok));
     g.lda = lda;
     g.M = (int)n_tok;
     g.N = (int)rows;
     g.K = (int)cols;
     g.ld_min = n_min;
     if (fmt == DQ_FMT_Q4_K) {
-        _Float16* mins = (_Float16*)((uint8_t*)d_work + act_bytes(fmt, cols, n_tok));
+        _Float16* mins = (_Float16*)((uint8_t*)d_work + min_off(fmt, cols, n_tok));
         const size_t lanes = rows * (size_t)(n_min / 8);
         min_plane_kernel<<<(unsigned)((lanes + 255) / 256), 256, 0, s>>>(g.w, L, (int)rows, (int)cols / 32, n_min,
                                                                          mins);

@@ -133,32 +133,6 @@ __global__ __launch_bounds__(64) void moe_lists_kernel(const int32_t* __restrict
 }
 
 // ------------------------------------------------------- activation rows --
-// fp16 operands have a range of 65504; the min columns reach 32 * max|v|.
-// Each activation row is therefore multiplied by a power of two s that puts
-// 32 * max|v| at or below 2^15 (exact: only the exponent moves), and the GEMM
-// multiplies its output row by 1/s. row_scale_kernel: one workgroup per
-// source row, s = 2^(15 - E) with 32 * max|v| = m * 2^E, m in [0.5, 1).
-__global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict__ src, int cols,
-                                                        float* __restrict__ scale) {
-    __shared__ float wmax[4];
-    const float* row = src + (size_t)blockIdx.x * cols;
-    float m = 0.0f;
-    for (int c = threadIdx.x * 4; c < cols; c += 1024) {
-        const float4 f = *reinterpret_cast<const float4*>(row + c);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
-    }
-    m = dq_wave_max(m);
-    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const float r = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-        int E = 0;
-        if (r > 0.0f && r <= 3.0e38f) frexpf(32.0f * r, &E);
-        E = E < -100 ? -100 : (E > 115 ? 115 : E);
-        scale[blockIdx.x] = ldexpf(1.0f, 15 - E);
-    }
-}
-
 // Row p of A: the per-256 quantization of its source row (256 values per
 // wave, 4 per lane): d = amax/127, id = 127/amax, q = rint(v*id) (core/matmul.cpp
 // :1681-1700); columns [0, K) = fp16(q*d*s), min columns K + j =

@@ -121,9 +121,11 @@ int dq_gemv_group(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t
  * i8_gemm path, core/matmul.cpp:2090-2125 -> :806-845): per-32 activation
  * quantization, exact float block sums for the Q4_K min term. Runs on fp16
  * MFMA over pre-scaled operands (result within ~3e-4 relative of the
- * reference). `d_work` (dq_gemm_workspace_bytes() bytes) holds the quantized
- * activations and, for Q4_K, a per-call plane of the min terms. Other
- * formats: -2. */
+ * reference); each token's operand row carries a power-of-two range scale
+ * (undone exactly on the output), so any finite activation magnitude stays
+ * inside fp16. `d_work` (dq_gemm_workspace_bytes() bytes) holds the quantized
+ * activations, their row scales and, for Q4_K, a per-call plane of the min
+ * terms. Other formats: -2. */
 int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t n_tok, size_t* bytes);
 int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,
             float* d_y, void* d_work, size_t work_bytes, void* stream);

@@ -68,3 +68,21 @@ def test_gemm_unsupported(gpu):
     n = ctypes.c_size_t(0)
     assert lib.dq_gemm_workspace_bytes(synth.FMT_Q8_0, 64, 4096, 16, ctypes.byref(n)) == -2
     assert lib.dq_gemm_workspace_bytes(synth.FMT_Q4_K, 64, 100, 16, ctypes.byref(n)) == -2
+
+
+@pytest.mark.parametrize("scale", [3000.0, 1e-4])
+@pytest.mark.parametrize("qtype", [synth.Q4_K, synth.Q6_K])
+def test_gemm_activation_range(gpu, orc, qtype, scale):
+    """Activations far from N(0,1): the fp16 operands are range-scaled per token
+    by a power of two (block sums of 32 values of 3000 would overflow fp16;
+    1e-4 would fall into its subnormals). Rows mix both ranges."""
+    rows, cols, n_tok = 96, 1024, 12
+    w = synth.gen_weights(qtype, rows, cols, seed=31)
+    x = synth.gen_act((n_tok, cols), seed=32)
+    x[: n_tok // 2] *= scale
+    m = ops.QuantMatrix.from_gguf(qtype, w, rows, cols)
+    y = ops.gemm(m, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    want = orc.gemm(qtype, w, rows, cols, x, n_tok)
+    assert np.isfinite(y).all()
+    for t in range(n_tok):  # per token: each row's own magnitude
+        assert rel(y[t], want[t]) <= TOL, t
