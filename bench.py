@@ -3,12 +3,15 @@
 Headline: batch-1 decode GEMV at the FFN shapes,
 Q4_K 14336x4096 (up/gate) and 4096x14336 (down). One step = quantize the
 activation (per-256, as the reference's matmul_q4_k does) + GEMV, for both
-shapes, on weight copies rotated so that the working set (>= 512 MB) exceeds
-the 256 MB Infinity Cache and every weight byte comes from HBM. Inputs are
+shapes (one launch each: the GEMV quantizes its fp32 activation in-kernel),
+on weight copies rotated so that the working set (>= 512 MB) exceeds the
+256 MB Infinity Cache and every weight byte comes from HBM. Inputs are
 resident in HBM before timing. value = algorithmic bytes per step / step time.
 
 Also reported under "extra": the Q4_0 and Q8_0 GEMVs (configs 1-2), the Q6_K
-GEMV, each with its kernel-only bandwidth.
+GEMV, each with its kernel-only bandwidth; the prefill GEMMs (config 3); the
+decode attention and the decoder layer (config 4); the MoE expert FFN
+(config 5).
 
 `roofline` is the dominant kernel (Q4_K GEMV, up shape): algorithmic bytes per
 launch / average launch duration, from HIP events around back-to-back launches
@@ -71,10 +74,11 @@ class GemvCase:
         self.i = 0
 
     def step(self):
+        # quantize + GEMV: one launch, the activation quantized in-kernel
         from desireeia_amd import ops
         m = self.mats[self.i]
         self.i = (self.i + 1) % len(self.mats)
-        ops.gemv(m, ops.quantize_act(self.x, self.kind, out=self.act), out=self.y)
+        ops.matmul(m, self.x, out=self.y)
 
     def kernel(self):
         from desireeia_amd import ops
@@ -197,6 +201,37 @@ class AttnCase:
         c = self.caches[self.i]
         self.i = (self.i + 1) % len(self.caches)
         ops.attention_decode(self.q, c, 32, self.pos, out=self.out, work=self.work)
+
+
+MOE_WEIGHT_BYTES = 8 * 99090432  # config 5: 8 experts x (gate, up, down) Q4_K
+
+
+class MoeCase:
+    """Config 5: MoE expert FFN, 8 experts top-2 (renormalised softmax), hidden
+    4096, expert FFN 14336 (SwiGLU), Q4_K experts, 64 tokens of N(0,1); router
+    logits N(0,1). The 792 MB of expert weights are 3x the Infinity Cache, so
+    every call streams them from HBM."""
+
+    def __init__(self, dev, n_tok=64, seed=50):
+        import torch
+        from desireeia_amd import ops, synth
+        E, F, X = 4096, 14336, 8
+        mk = lambda r, c, sd: ops.QuantMatrix.from_gguf(synth.Q4_K, synth.gen_weights(synth.Q4_K, r, c, sd), r, c,
+                                                        device=dev)
+        self.mats = (mk(X * F, E, seed), mk(X * F, E, seed + 1), mk(X * E, F, seed + 2))
+        self.moe = ops.MoeLayer(*self.mats, n_expert=X, n_expert_used=2)
+        self.n_tok = n_tok
+        self.x = torch.from_numpy(synth.gen_act((n_tok, E), seed + 3)).to(dev)
+        self.lg = torch.from_numpy(synth.gen_act((n_tok, X), seed + 4)).to(dev)
+        self.out = torch.empty(n_tok, E, dtype=torch.float32, device=dev)
+        self.moe(self.x, self.lg, out=self.out)
+        torch.cuda.synchronize()
+
+    def step(self):
+        self.moe(self.x, self.lg, out=self.out)
+
+    def bytes(self):
+        return MOE_WEIGHT_BYTES + self.n_tok * 4096 * 4 * 2 + self.n_tok * 8 * 4
 
 
 def graph_time(fn, calls_per_graph, reps, warmup_reps=2):
@@ -334,6 +369,11 @@ def main():
         us = graph_time(lc.step, 1, max(1, args.steps // len(lc.layers))) / len(lc.layers)
         log(f"layer: {us:.1f} us/layer, {lc.bytes_per_layer() / us / 1e3:.1f} GB/s")
         return
+    if args.only == "moe":
+        mc = MoeCase(dev)
+        us = graph_time(mc.step, 4, max(1, args.steps // 4))
+        log(f"moe: {us:.1f} us/call, {mc.bytes() / us / 1e3:.1f} GB/s, {mc.n_tok / us * 1e6:.0f} tok/s")
+        return
     if args.only == "attn":
         ac = AttnCase(dev)
         us = graph_time(ac.kernel, len(ac.caches), max(1, args.steps // len(ac.caches)))
@@ -399,6 +439,13 @@ def main():
                                    "bytes_per_layer": lc.bytes_per_layer()}
     log(f"decoder layer: {us:.1f} us/layer  {gbs:.1f} GB/s")
     del lc
+    mc = MoeCase(dev)
+    us = graph_time(mc.step, 4, 5)
+    gbs = mc.bytes() / us / 1e3
+    extra["moe_8x2_64tok"] = {"us_per_call": round(us, 2), "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                              "tokens_per_s": round(mc.n_tok / us * 1e6, 1), "bytes_per_call": mc.bytes()}
+    log(f"MoE expert FFN (8 experts, top-2, 64 tokens): {us:.1f} us  {gbs:.1f} GB/s")
+    del mc
     dom = extra["q4k_up"]
     roofline = {"bound": "hbm", "achieved": dom["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(),
@@ -413,8 +460,8 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "config 2: Q4_K decode GEMV, up 14336x4096 + down 4096x14336, "
-                               "per-256 activation quantization + GEMV per matrix, weights rotated over "
-                               f">= {ROTATE_BYTES >> 20} MB",
+                               "per-256 activation quantization + GEMV per matrix (one launch each), "
+                               f"weights rotated over >= {ROTATE_BYTES >> 20} MB",
                    "bytes_per_step": bytes_step, "frac_hbm_step": round(value / HBM_PEAK_GBS, 4),
                    "wall_s": round(wall, 3)},
         "roofline": roofline, "cpu_baseline": cpu, "extra": extra,

@@ -33,8 +33,12 @@ SIGNATURES = {
                                   c_p]),
     "dq_attn_decode_q8_act": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_u32, c_p, c_p, c_p,
                                       c_p, c_p, c_size, c_p]),
+    "dq_attn_rope_kv_decode": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p,
+                                       c_u32, c_p, c_p, c_p, c_p, c_p, c_size, c_p]),
     "dq_gemv_add": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p, c_p, c_p, c_p, c_p]),
     "dq_gemv_group": (c_int, [c_p, c_size, c_size, c_p, c_p, c_p, c_p]),
+    "dq_gemv_f32": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p, c_p]),
+    "dq_gemv_group_f32": (c_int, [c_p, c_size, c_size, c_p, c_p]),
     "dq_rope_cache": (c_int, [c_p, c_u32, c_u32, c_f]),
     "dq_norm_quant": (c_int, [c_p, c_p, c_p, c_p, c_size, c_f, c_p, c_p, c_p, c_p]),
     "dq_silu_quant": (c_int, [c_p, c_p, c_size, c_p, c_p, c_p, c_p]),

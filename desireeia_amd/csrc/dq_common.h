@@ -128,6 +128,35 @@ __device__ __forceinline__ dq_u32x4 dq_ld16_stream(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const dq_u32x4*>(p));
 }
 
+// DPP move of a float (gfx9 dpp_ctrl encodings; all rows and banks enabled).
+template <int CTRL>
+__device__ __forceinline__ float dq_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum of v over each 16-lane row, in every lane of the row: quad_perm
+// [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror (VALU data
+// movement, no LDS round trip). Fixed order: deterministic.
+__device__ __forceinline__ float dq_row16_sum(float v) {
+    v += dq_dpp<0xB1>(v);
+    v += dq_dpp<0x4E>(v);
+    v += dq_dpp<0x141>(v);
+    v += dq_dpp<0x140>(v);
+    return v;
+}
+
+// Full-wave float sum as a wave-uniform value: the four row sums combined as
+// (row0 + row1) + (row2 + row3).
+__device__ __forceinline__ float dq_wave_sum_uniform(float v) {
+    v = dq_row16_sum(v);
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 // Full-wave float sum; every lane receives the total.
 __device__ __forceinline__ float dq_wave_sum(float v) {
 #pragma unroll
@@ -139,6 +168,43 @@ __device__ __forceinline__ float dq_wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, DQ_WAVE));
     return v;
+}
+
+// NeoX RoPE of the pair (x0, x1) = (dim j, dim j + n_rot/2) with (cos, sin) =
+// (rope[2j], rope[2j+1]) (models/dense_forward.cpp:668-680), unfused.
+__device__ __forceinline__ void dq_rope_pair(float& x0, float& x1, const float* rope, int j) {
+    const float c = rope[2 * j], s = rope[2 * j + 1];
+    const float a = x0, b = x1;
+    x0 = a * c - b * s;
+    x1 = a * s + b * c;
+}
+
+// kv_quantize_row (kv/kv_quant.cpp:31-56) of one 128-value row held by the 64
+// lanes of a wave as (lo, hi) = (value j, value j + 64): blocks 0 and 1 come
+// from the lo halves of lanes 0-31 / 32-63, blocks 2 and 3 from the hi
+// halves; each block is fp16 d followed by 32 int8. dst: 136 bytes, 2-byte
+// aligned (global or LDS).
+__device__ __forceinline__ void dq_q8_0_row128(float lo, float hi, int j, uint8_t* dst) {
+    float alo = fabsf(lo), ahi = fabsf(hi);
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) {
+        alo = fmaxf(alo, __shfl_xor(alo, off, DQ_WAVE));
+        ahi = fmaxf(ahi, __shfl_xor(ahi, off, DQ_WAVE));
+    }
+    const int blo = j >> 5, i = j & 31;
+#pragma unroll
+    for (int part = 0; part < 2; ++part) {
+        const float amax = part ? ahi : alo;
+        const float x = part ? hi : lo;
+        const int blk = part ? blo + 2 : blo;
+        const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        int iv = (int)rintf(x * id);
+        iv = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
+        uint8_t* bp = dst + blk * DQ_SZ_Q8_0;
+        bp[2 + i] = (uint8_t)(iv & 0xFF);
+        if (i == 0) *reinterpret_cast<uint16_t*>(bp) = dq_f2h(d);
+    }
 }
 
 // Host-side status from a HIP error.

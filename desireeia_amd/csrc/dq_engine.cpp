@@ -158,9 +158,10 @@ const WInfo* lookup(const void* p) {
 
 // ------------------------------------------------------------- GEMV core --
 
-// x (host, cols floats) -> device, quantized once per activation kind the
-// jobs need; then every job's GEMV into device y slices, then the host copies
-// and one synchronisation. jobs: (fmt, d_w, rows) with host y.
+// x (host, cols floats) -> device; every job's GEMV (the activation quantized
+// in-kernel, or once per activation kind for very wide rows) into device y
+// slices, then the host copies and one synchronisation. jobs: (fmt, d_w,
+// rows) with host y.
 struct HostJob {
     int fmt;
     const void* d_w;
@@ -186,13 +187,6 @@ int run_host_jobs(const HostJob* jobs, size_t n, size_t cols, const float* x) {
     const hipStream_t s = g.stream;
     float* dx = (float*)g.xbuf.p;
     if (hipMemcpyAsync(dx, x, cols * 4, hipMemcpyHostToDevice, s) != hipSuccess) return io_fail();
-    Act a[2] = {carve_act((uint8_t*)g.act.p, cols), carve_act((uint8_t*)g.act.p + act_bytes(cols), cols)};
-    for (int k = 0; k < 2; ++k)
-        if (need[k]) {
-            const int rc = dq_quantize_act(k, dx, cols, 1, a[k].q, a[k].s, a[k].i, nullptr, s);
-            if (rc != DQ_OK) return rc == DQ_ERR_IO ? io_fail() : rc;
-        }
-    // grouped launches of up to 4 jobs of one activation kind
     float* dy = (float*)g.ybuf.p;
     std::vector<float*> ys(n);
     size_t off = 0;
@@ -200,6 +194,28 @@ int run_host_jobs(const HostJob* jobs, size_t n, size_t cols, const float* x) {
         ys[j] = dy + off;
         off += jobs[j].rows;
     }
+    if (cols <= 49152) {
+        // the GEMVs quantize x in-kernel: grouped launches of up to 4 jobs
+        dq_gemv_job_t grp[4];
+        for (size_t j0 = 0; j0 < n; j0 += 4) {
+            const size_t m = n - j0 < 4 ? n - j0 : 4;
+            for (size_t j = 0; j < m; ++j)
+                grp[j] = {jobs[j0 + j].fmt, jobs[j0 + j].d_w, jobs[j0 + j].rows, ys[j0 + j], nullptr};
+            const int rc = dq_gemv_group_f32(grp, m, cols, dx, s);
+            if (rc != DQ_OK) return rc == DQ_ERR_IO ? io_fail() : rc;
+        }
+        for (size_t j = 0; j < n; ++j)
+            if (hipMemcpyAsync(jobs[j].y, ys[j], jobs[j].rows * 4, hipMemcpyDeviceToHost, s) != hipSuccess)
+                return io_fail();
+        return sync();
+    }
+    // wider rows: quantize once per activation kind, then grouped GEMVs
+    Act a[2] = {carve_act((uint8_t*)g.act.p, cols), carve_act((uint8_t*)g.act.p + act_bytes(cols), cols)};
+    for (int k = 0; k < 2; ++k)
+        if (need[k]) {
+            const int rc = dq_quantize_act(k, dx, cols, 1, a[k].q, a[k].s, a[k].i, nullptr, s);
+            if (rc != DQ_OK) return rc == DQ_ERR_IO ? io_fail() : rc;
+        }
     for (int k = 0; k < 2; ++k) {
         dq_gemv_job_t grp[4];
         int m = 0;

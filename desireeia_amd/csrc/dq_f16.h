@@ -48,6 +48,13 @@ namespace {
 // the fp16 subnormals), and the GEMM multiplies its output row by 1/s.
 // row_scale_kernel: one 256-thread workgroup per row of `cols` floats
 // (cols % 4 == 0), s = 2^(15 - E) with 32 * max|v| = m * 2^E, m in [0.5, 1).
+__device__ __forceinline__ float row_scale_of(float r) {
+    int E = 0;
+    if (r > 0.0f && r <= 3.0e38f) frexpf(32.0f * r, &E);
+    E = E < -100 ? -100 : (E > 115 ? 115 : E);
+    return ldexpf(1.0f, 15 - E);
+}
+
 __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict__ src, int cols,
                                                         float* __restrict__ scale) {
     __shared__ float wmax[4];
@@ -60,13 +67,7 @@ __global__ __launch_bounds__(256) void row_scale_kernel(const float* __restrict_
     m = dq_wave_max(m);
     if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const float r = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-        int E = 0;
-        if (r > 0.0f && r <= 3.0e38f) frexpf(32.0f * r, &E);
-        E = E < -100 ? -100 : (E > 115 ? 115 : E);
-        scale[blockIdx.x] = ldexpf(1.0f, 15 - E);
-    }
+    if (threadIdx.x == 0) scale[blockIdx.x] = row_scale_of(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
 }
 
 }  // namespace

@@ -14,14 +14,15 @@
 //    is redirected to a cached dummy address (no extra HBM traffic, and the
 //    compiler's in-order vmcnt accounting stays static).
 //  * Nibble/6-bit unpack and 6-bit scale decode in registers (one decode per
-//    64 weights), v_dot4_i32_i8 dots, and a butterfly reduce-scatter that
-//    finishes the R row sums of a group in log2(64) shuffle steps.
+//    64 weights), v_dot4_i32_i8 dots, and row sums over the wave by DPP row
+//    reductions and readlanes (no LDS round trips on the critical path).
 //
 // Semantics follow the reference CPU GEMVs (include/desireeia_hip.h): integer
 // partial sums are exact; only the float summation order differs.
 #include <cstdlib>
 
 #include "dq_common.h"
+#include "dq_quant.h"
 
 namespace {
 
@@ -260,37 +261,6 @@ __device__ __forceinline__ void load_item(typename Fmt<FMT>::W& w, const uint8_t
     }
 }
 
-// Butterfly reduce-scatter of R per-lane partial sums: returns, in every lane
-// of the group of 64/R lanes that holds row rr = lane / (64/R), the full sum of
-// row rr across the wave.
-template <int R>
-__device__ __forceinline__ float reduce_rows(float (&acc)[R], int lane) {
-    int n = R;
-    int off = 32;
-#pragma unroll
-    for (int step = 0; step < 3; ++step) {
-        if (n > 1) {
-            const bool upper = (lane & off) != 0;
-            const int h = n / 2;
-#pragma unroll
-            for (int k = 0; k < R / 2; ++k) {
-                if (k < h) {
-                    const float mine = upper ? acc[h + k] : acc[k];
-                    const float other = upper ? acc[k] : acc[h + k];
-                    acc[k] = mine + __shfl_xor(other, off, DQ_WAVE);
-                }
-            }
-            n = h;
-            off >>= 1;
-        }
-    }
-    float v = acc[0];
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1)
-        if (o <= off) v += __shfl_xor(v, o, DQ_WAVE);
-    return v;
-}
-
 // Items of a wave: [i0, i1) of every row; lane owns i0 + lane + 64j.
 template <int FMT, int R, int NIT>
 __device__ __forceinline__ void load_group(typename Fmt<FMT>::W (&wr)[R][NIT], const Jobs& J, int g, int ngroups,
@@ -329,20 +299,26 @@ __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R
         }
         acc[rr] = a;
     }
-    const float s = reduce_rows<R>(acc, lane);
-    constexpr int GROUP = DQ_WAVE / R;
+    // each row's sum over the wave: DPP row reductions + readlanes (uniform)
+    float tot[R];
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) tot[rr] = dq_wave_sum_uniform(acc[rr]);
     int gl = 0;
     const int j = job_of(J, g, &gl);
     float* __restrict__ y = J.y[j];
     const float* __restrict__ res = J.res[j];
     const int rows = J.rows[j];
+    // lane rr stores row rr (vector stores)
+    float mine = tot[0];
+#pragma unroll
+    for (int rr = 1; rr < R; ++rr) mine = lane == rr ? tot[rr] : mine;
     if constexpr (KS == 1) {
-        if ((lane & (GROUP - 1)) == 0) {
-            const int r = gl * R + lane / GROUP;
-            if (r < rows) y[r] = res ? s + res[r] : s;
+        if (lane < R) {
+            const int r = gl * R + lane;
+            if (r < rows) y[r] = res ? mine + res[r] : mine;
         }
     } else {
-        if ((lane & (GROUP - 1)) == 0) part[buf][lane / GROUP][ks] = s;
+        if (lane < R) part[buf][lane][ks] = mine;
         __syncthreads();
         if (ks == 0 && lane < R) {
             const int r = gl * R + lane;
@@ -356,14 +332,48 @@ __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R
 
 // ----------------------------------------------------------------- kernel --
 
+// Activation kind of a weight format's reference GEMV.
+template <int FMT>
+constexpr int act_kind_of() {
+    return (FMT == DQ_FMT_Q8_0 || FMT == DQ_FMT_Q4_0) ? DQ_ACT_Q8_0 : DQ_ACT_Q8K_REP;
+}
+
+// XQ: the workgroup quantizes the fp32 activation xf itself into LDS (int8
+// [cols], scale and int32 sum per 32, with the format's reference quantizer,
+// bit-exact as dq_quantize_act) while its first weight loads are in flight.
+template <int FMT>
+__device__ __forceinline__ void quantize_to_lds(const float* __restrict__ xf, int cols, uint8_t* xl) {
+    const int nblk = cols / 32;
+    int8_t* lq = reinterpret_cast<int8_t*>(xl);
+    float* ls = reinterpret_cast<float*>(xl + cols);
+    int32_t* li = reinterpret_cast<int32_t*>(xl + cols + 4 * nblk);
+    // per-256 groups of 8 lanes are aligned (nblk % 8 == 0 for the K-quants),
+    // so a group is wholly inside or outside [0, nblk)
+    for (int b = threadIdx.x; b < nblk; b += blockDim.x) {
+        float v[32];
+        dq_load32(xf + 32 * (size_t)b, v);
+        uint32_t packed[8];
+        float d, fs;
+        int sum;
+        dq_quant_block<act_kind_of<FMT>()>(v, packed, d, sum, fs);
+        dq_u32x4* qo = reinterpret_cast<dq_u32x4*>(lq + 32 * b);
+        qo[0] = dq_u32x4{packed[0], packed[1], packed[2], packed[3]};
+        qo[1] = dq_u32x4{packed[4], packed[5], packed[6], packed[7]};
+        ls[b] = d;
+        li[b] = sum;
+    }
+}
+
 // Grid: persistent 256-thread workgroups walking "units" u = blockIdx.x,
 // blockIdx.x + gridDim.x, ... KS == 1: unit u = groups 4u..4u+3, one per wave.
 // KS == 4: unit u = group u, shared by the 4 waves (K split in quarters).
 // Groups are global over the jobs of J.
-template <int FMT, int R, int NIT, int KS>
+template <int FMT, int R, int NIT, int KS, bool XQ>
 __global__ __launch_bounds__(256) void gemv_kernel(Jobs J, int items, const int8_t* __restrict__ xq,
-                                                   const float* __restrict__ xs, const int32_t* __restrict__ xsum) {
+                                                   const float* __restrict__ xs, const int32_t* __restrict__ xsum,
+                                                   const float* __restrict__ xf) {
     using W = typename Fmt<FMT>::W;
+    extern __shared__ __align__(16) uint8_t xl[];  // XQ: the quantized activation
     __shared__ float part[2][R][4];
     const int lane = threadIdx.x & (DQ_WAVE - 1);
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / DQ_WAVE));  // wave-uniform
@@ -374,11 +384,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(Jobs J, int items, const int8
     const int ngroups = J.g0[J.n];
     const int stride = KS == 1 ? 4 * (int)gridDim.x : (int)gridDim.x;
     int g = KS == 1 ? 4 * (int)blockIdx.x + wv : (int)blockIdx.x;
-    if (g >= ngroups || i0 >= i1) return;  // uniform per wave (KS 1) / per workgroup (KS 4)
-    const uint8_t* dummy = reinterpret_cast<const uint8_t*>(xq);
+    const bool active = g < ngroups && i0 < i1;  // uniform per wave (KS 1) / per workgroup (KS 4)
+    if (!XQ && !active) return;
+    const uint8_t* dummy = reinterpret_cast<const uint8_t*>(XQ ? (const void*)xf : (const void*)xq);
 
     W b0[R][NIT], b1[R][NIT];
-    load_group<FMT, R, NIT>(b0, J, g, ngroups, i0, i1, lane, dummy);
+    if (active) load_group<FMT, R, NIT>(b0, J, g, ngroups, i0, i1, lane, dummy);
+    if constexpr (XQ) {
+        const int cols = items * 64;
+        quantize_to_lds<FMT>(xf, cols, xl);
+        __syncthreads();
+        if (!active) return;
+        xq = reinterpret_cast<const int8_t*>(xl);
+        xs = reinterpret_cast<const float*>(xl + cols);
+        xsum = reinterpret_cast<const int32_t*>(xl + cols + 4 * (cols / 32));
+    }
     XItem X[NIT];
 #pragma unroll
     for (int j = 0; j < NIT; ++j) Fmt<FMT>::load_x(X[j], min(i0 + lane + DQ_WAVE * j, i1 - 1), xq, xs, xsum);
@@ -421,8 +441,12 @@ void set_groups(Jobs& J, int R) {
     for (int j = 0; j < J.n; ++j) J.g0[j + 1] = J.g0[j] + (J.rows[j] + R - 1) / R;
 }
 
+// Bytes of the in-kernel quantized activation (XQ) in LDS.
+size_t xq_lds_bytes(size_t cols) { return cols + 8 * (cols / 32); }
+
 template <int FMT, int R, int NIT, int KS>
-int launch(Jobs J, int items, const int8_t* xq, const float* xs, const int32_t* xsum, hipStream_t s) {
+int launch(Jobs J, int items, const int8_t* xq, const float* xs, const int32_t* xsum, const float* xf,
+           hipStream_t s) {
     static const int wpc = env_int("DQ_GEMV_WPC", 8);  // persistent waves per CU
     set_groups(J, R);
     const int ngroups = J.g0[J.n];
@@ -430,27 +454,32 @@ int launch(Jobs J, int items, const int8_t* xq, const float* xs, const int32_t* 
     const int max_wg = max(1, num_cus() * wpc / 4);
     const int iters = (units + max_wg - 1) / max_wg;  // balance: every workgroup walks `iters` units
     const unsigned grid = (unsigned)((units + iters - 1) / iters);
-    gemv_kernel<FMT, R, NIT, KS><<<grid, 256, 0, s>>>(J, items, xq, xs, xsum);
+    if (xf)
+        gemv_kernel<FMT, R, NIT, KS, true><<<grid, 256, xq_lds_bytes((size_t)items * 64), s>>>(J, items, xq, xs,
+                                                                                               xsum, xf);
+    else
+        gemv_kernel<FMT, R, NIT, KS, false><<<grid, 256, 0, s>>>(J, items, xq, xs, xsum, xf);
     return dq_launch_status();
 }
 
 template <int FMT, int R, int KS>
 int launch_nit(int nit, const Jobs& J, int items, const int8_t* xq, const float* xs, const int32_t* xsum,
-               hipStream_t s) {
+               const float* xf, hipStream_t s) {
     switch (nit) {
-    case 1: return launch<FMT, R, 1, KS>(J, items, xq, xs, xsum, s);
-    case 2: return launch<FMT, R, 2, KS>(J, items, xq, xs, xsum, s);
-    case 3: return launch<FMT, R, 3, KS>(J, items, xq, xs, xsum, s);
-    case 4: return launch<FMT, R, 4, KS>(J, items, xq, xs, xsum, s);
+    case 1: return launch<FMT, R, 1, KS>(J, items, xq, xs, xsum, xf, s);
+    case 2: return launch<FMT, R, 2, KS>(J, items, xq, xs, xsum, xf, s);
+    case 3: return launch<FMT, R, 3, KS>(J, items, xq, xs, xsum, xf, s);
+    case 4: return launch<FMT, R, 4, KS>(J, items, xq, xs, xsum, xf, s);
     default:
-        if (nit <= 6) return launch<FMT, R, 6, KS>(J, items, xq, xs, xsum, s);
-        if (nit <= 8) return launch<FMT, R, 8, KS>(J, items, xq, xs, xsum, s);
+        if (nit <= 6) return launch<FMT, R, 6, KS>(J, items, xq, xs, xsum, xf, s);
+        if (nit <= 8) return launch<FMT, R, 8, KS>(J, items, xq, xs, xsum, xf, s);
         return DQ_ERR_NOT_SUPPORTED;
     }
 }
 
 template <int FMT>
-int launch_fmt(const Jobs& J, size_t cols, const int8_t* xq, const float* xs, const int32_t* xsum, hipStream_t s) {
+int launch_fmt(const Jobs& J, size_t cols, const int8_t* xq, const float* xs, const int32_t* xsum, const float* xf,
+               hipStream_t s) {
     const int items = (int)(cols / 64);
     // K split: rows wider than 128 items are shared by the 4 waves of a workgroup
     int ks = env_int("DQ_GEMV_KS", 0);
@@ -463,45 +492,53 @@ int launch_fmt(const Jobs& J, size_t cols, const int8_t* xq, const float* xs, co
     if (r != 1 && r != 2 && r != 4) r = nit == 1 ? 2 : 1;
     if (nit > 4 && r > 1) r = 1;
     if (ks == 1) {
-        if (r == 1) return launch_nit<FMT, 1, 1>(nit, J, items, xq, xs, xsum, s);
-        if (r == 2) return launch_nit<FMT, 2, 1>(nit, J, items, xq, xs, xsum, s);
-        return launch_nit<FMT, 4, 1>(nit, J, items, xq, xs, xsum, s);
+        if (r == 1) return launch_nit<FMT, 1, 1>(nit, J, items, xq, xs, xsum, xf, s);
+        if (r == 2) return launch_nit<FMT, 2, 1>(nit, J, items, xq, xs, xsum, xf, s);
+        return launch_nit<FMT, 4, 1>(nit, J, items, xq, xs, xsum, xf, s);
     }
-    if (r == 1) return launch_nit<FMT, 1, 4>(nit, J, items, xq, xs, xsum, s);
-    if (r == 2) return launch_nit<FMT, 2, 4>(nit, J, items, xq, xs, xsum, s);
-    return launch_nit<FMT, 4, 4>(nit, J, items, xq, xs, xsum, s);
+    if (r == 1) return launch_nit<FMT, 1, 4>(nit, J, items, xq, xs, xsum, xf, s);
+    if (r == 2) return launch_nit<FMT, 2, 4>(nit, J, items, xq, xs, xsum, xf, s);
+    return launch_nit<FMT, 4, 4>(nit, J, items, xq, xs, xsum, xf, s);
 }
 
 int launch_jobs(int fmt, const Jobs& J, size_t cols, const int8_t* xq, const float* xs, const int32_t* xsum,
-                hipStream_t s) {
+                const float* xf, hipStream_t s) {
     switch (fmt) {
-    case DQ_FMT_Q8_0: return launch_fmt<DQ_FMT_Q8_0>(J, cols, xq, xs, xsum, s);
-    case DQ_FMT_Q4_0: return launch_fmt<DQ_FMT_Q4_0>(J, cols, xq, xs, xsum, s);
-    case DQ_FMT_Q4_K: return launch_fmt<DQ_FMT_Q4_K>(J, cols, xq, xs, xsum, s);
-    case DQ_FMT_Q6_K: return launch_fmt<DQ_FMT_Q6_K>(J, cols, xq, xs, xsum, s);
+    case DQ_FMT_Q8_0: return launch_fmt<DQ_FMT_Q8_0>(J, cols, xq, xs, xsum, xf, s);
+    case DQ_FMT_Q4_0: return launch_fmt<DQ_FMT_Q4_0>(J, cols, xq, xs, xsum, xf, s);
+    case DQ_FMT_Q4_K: return launch_fmt<DQ_FMT_Q4_K>(J, cols, xq, xs, xsum, xf, s);
+    case DQ_FMT_Q6_K: return launch_fmt<DQ_FMT_Q6_K>(J, cols, xq, xs, xsum, xf, s);
     }
     return DQ_ERR_NOT_SUPPORTED;
 }
 
 bool per32_act(int fmt) { return fmt == DQ_FMT_Q8_0 || fmt == DQ_FMT_Q4_0; }
+// LDS budget of the in-kernel quantized activation: within the 64 KB of
+// dynamic LDS a launch gets by default (cols <= 49152).
+constexpr size_t XQ_MAX_LDS = 60 * 1024;
 bool needs_sum(int fmt) { return fmt == DQ_FMT_Q4_0 || fmt == DQ_FMT_Q4_K; }
 
 // Validates n jobs; writes the layouts. NOT_SUPPORTED for shapes/formats the
 // kernels do not cover and for groups that mix the per-32 (Q8_0, Q4_0) and
 // per-256 (Q4_K, Q6_K) activation kinds.
 int check_jobs(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* xq, const float* xs,
-               const int32_t* xsum, DqLayout* L) {
+               const int32_t* xsum, const float* xf, DqLayout* L) {
     if (n == 0) return DQ_OK;
     if (!jobs) return DQ_ERR_INVALID_ARG;
     if (n > DQ_GEMV_MAX_JOBS) return DQ_ERR_NOT_SUPPORTED;
     for (size_t j = 0; j < n; ++j) {
         if (!dq_layout(jobs[j].fmt, jobs[j].rows, cols, &L[j])) return DQ_ERR_NOT_SUPPORTED;
         if (jobs[j].rows > 0x3FFFFFFF) return DQ_ERR_NOT_SUPPORTED;
-        if (per32_act(jobs[j].fmt) != per32_act(jobs[0].fmt)) return DQ_ERR_NOT_SUPPORTED;
+        // one shared pre-quantized activation serves one activation kind;
+        // with the fp32 activation every launch quantizes for its own format
+        if (!xf && per32_act(jobs[j].fmt) != per32_act(jobs[0].fmt)) return DQ_ERR_NOT_SUPPORTED;
     }
+    if (xf && xq_lds_bytes(cols) > XQ_MAX_LDS) return DQ_ERR_NOT_SUPPORTED;
     for (size_t j = 0; j < n; ++j) {
         if (jobs[j].rows == 0) continue;  // nothing to do: no pointer is read
-        if (!jobs[j].d_w || !jobs[j].d_y || !xq || !xs) return DQ_ERR_INVALID_ARG;
+        if (!jobs[j].d_w || !jobs[j].d_y) return DQ_ERR_INVALID_ARG;
+        if (xf) continue;
+        if (!xq || !xs) return DQ_ERR_INVALID_ARG;
         if (needs_sum(jobs[j].fmt) && !xsum) return DQ_ERR_INVALID_ARG;
     }
     return DQ_OK;
@@ -509,9 +546,9 @@ int check_jobs(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* x
 
 // One launch per distinct format, in job order of first appearance.
 int run_jobs(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* xq, const float* xs,
-             const int32_t* xsum, hipStream_t s) {
+             const int32_t* xsum, const float* xf, hipStream_t s) {
     DqLayout L[DQ_GEMV_MAX_JOBS];
-    const int rc = check_jobs(jobs, n, cols, xq, xs, xsum, L);
+    const int rc = check_jobs(jobs, n, cols, xq, xs, xsum, xf, L);
     if (rc != DQ_OK || n == 0) return rc;
     bool done[DQ_GEMV_MAX_JOBS] = {};
     for (size_t a = 0; a < n; ++a) {
@@ -530,7 +567,7 @@ int run_jobs(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* xq,
             ++J.n;
         }
         if (J.n == 0) continue;
-        const int r = launch_jobs(fmt, J, cols, xq, xs, xsum, s);
+        const int r = launch_jobs(fmt, J, cols, xq, xs, xsum, xf, s);
         if (r != DQ_OK) return r;
     }
     return DQ_OK;
@@ -541,7 +578,7 @@ int run_jobs(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* xq,
 extern "C" int dq_gemv(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
                        const float* d_xscale, const int32_t* d_xsum, float* d_y, void* stream) {
     const dq_gemv_job_t job = {fmt, d_w, rows, d_y, nullptr};
-    return run_jobs(&job, 1, cols, d_xq, d_xscale, d_xsum, (hipStream_t)stream);
+    return run_jobs(&job, 1, cols, d_xq, d_xscale, d_xsum, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int dq_gemv_add(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t* d_xq,
@@ -549,10 +586,25 @@ extern "C" int dq_gemv_add(int fmt, const void* d_w, size_t rows, size_t cols, c
                            void* stream) {
     if (!d_res) return DQ_ERR_INVALID_ARG;
     const dq_gemv_job_t job = {fmt, d_w, rows, d_y, d_res};
-    return run_jobs(&job, 1, cols, d_xq, d_xscale, d_xsum, (hipStream_t)stream);
+    return run_jobs(&job, 1, cols, d_xq, d_xscale, d_xsum, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int dq_gemv_group(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* d_xq,
                              const float* d_xscale, const int32_t* d_xsum, void* stream) {
-    return run_jobs(jobs, n, cols, d_xq, d_xscale, d_xsum, (hipStream_t)stream);
+    return run_jobs(jobs, n, cols, d_xq, d_xscale, d_xsum, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int dq_gemv_f32(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, float* d_y,
+                           void* stream) {
+    if (!d_x && rows) return DQ_ERR_INVALID_ARG;
+    const dq_gemv_job_t job = {fmt, d_w, rows, d_y, nullptr};
+    return run_jobs(&job, 1, cols, nullptr, nullptr, nullptr, d_x, (hipStream_t)stream);
+}
+
+extern "C" int dq_gemv_group_f32(const dq_gemv_job_t* jobs, size_t n, size_t cols, const float* d_x,
+                                 void* stream) {
+    bool any = false;
+    for (size_t j = 0; jobs && j < n; ++j) any = any || jobs[j].rows;
+    if (!d_x && any) return DQ_ERR_INVALID_ARG;
+    return run_jobs(jobs, n, cols, nullptr, nullptr, nullptr, d_x, (hipStream_t)stream);
 }

@@ -146,10 +146,7 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q, cons
         // n_rot = 128: pair (j, j+64); n_rot < 128: pairs inside [0, n_rot)
         const int half = n_rot / 2;
         if (n_rot == HD) {
-            const float c = rope[2 * j], s = rope[2 * j + 1];
-            const float x0 = lo, x1 = hi;
-            lo = x0 * c - x1 * s;
-            hi = x0 * s + x1 * c;
+            dq_rope_pair(lo, hi, rope, j);
         } else {
             __shared__ float row[HD];
             row[j] = lo;
@@ -171,30 +168,9 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q, cons
         q[(size_t)head * HD + j + 64] = hi;
         return;
     }
-    // Q8_0 row: lanes 0-31 hold blocks 0 (lo) and 2 (hi), lanes 32-63 blocks 1 and 3
-    float alo = fabsf(lo), ahi = fabsf(hi);
-#pragma unroll
-    for (int off = 1; off < 32; off <<= 1) {
-        alo = fmaxf(alo, __shfl_xor(alo, off, DQ_WAVE));
-        ahi = fmaxf(ahi, __shfl_xor(ahi, off, DQ_WAVE));
-    }
     int p = pos_dev ? *pos_dev : pos_host;
     p = p < 0 ? 0 : (p >= n_ctx ? n_ctx - 1 : p);
-    uint8_t* row = (kind == 1 ? kc : vc) + (size_t)p * pos_bytes + (size_t)head * (HD / 32) * DQ_SZ_Q8_0;
-    const int blo = j >> 5, bhi = blo + 2, i = j & 31;
-#pragma unroll
-    for (int part = 0; part < 2; ++part) {
-        const float amax = part ? ahi : alo;
-        const float x = part ? hi : lo;
-        const int blk = part ? bhi : blo;
-        const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
-        const float id = d > 0.0f ? 1.0f / d : 0.0f;
-        int iv = (int)rintf(x * id);
-        iv = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
-        uint8_t* bp = row + blk * DQ_SZ_Q8_0;
-        bp[2 + i] = (uint8_t)(iv & 0xFF);
-        if (i == 0) *reinterpret_cast<uint16_t*>(bp) = dq_f2h(d);
-    }
+    dq_q8_0_row128(lo, hi, j, (kind == 1 ? kc : vc) + (size_t)p * pos_bytes + (size_t)head * (HD / 32) * DQ_SZ_Q8_0);
 }
 
 // ------------------------------------------------------------ silu_quant --
@@ -427,16 +403,28 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
                                        {L->fmt_v, L->wv, KVD, w.v, nullptr}};
         DQ_TRY(run_group(jobs, 3, E));
     }
-    DQ_TRY(dq_rope_kv_write(w.q, w.k, w.v, d_rope, L->n_head, L->n_head_kv, L->head_dim, L->n_rot, d_kc, d_vc, pos,
-                            d_pos, n_ctx, stream));
-    if (kquant(L->fmt_o)) {
-        // the attention's merge also quantizes its output for the projection
+    // RoPE, the new K/V rows and attention in one launch when the rotation
+    // covers the whole head (else the separate RoPE + KV-write kernel first)
+    const bool fused = !d_rope || L->n_rot == L->head_dim;
+    if (!fused)
+        DQ_TRY(dq_rope_kv_write(w.q, w.k, w.v, d_rope, L->n_head, L->n_head_kv, L->head_dim, L->n_rot, d_kc, d_vc,
+                                pos, d_pos, n_ctx, stream));
+    // the attention also quantizes its output per 256 for a K-quant Wo
+    const bool q256 = kquant(L->fmt_o);
+    int8_t* oq = q256 ? w.aq : nullptr;
+    if (fused)
+        DQ_TRY(dq_attn_rope_kv_decode(w.q, w.k, w.v, d_rope, L->n_rot, d_kc, d_vc, L->n_head, L->n_head_kv,
+                                      L->head_dim, cc_start, pos, d_pos, n_ctx, w.ao, oq, w.as, w.ai, w.attn,
+                                      w.attn_bytes, stream));
+    else if (q256)
         DQ_TRY(dq_attn_decode_q8_act(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos,
                                      n_ctx, w.ao, w.aq, w.as, w.ai, w.attn, w.attn_bytes, stream));
-        DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.aq, w.as, w.ai, d_x, w.x2, stream));
-    } else {
+    else
         DQ_TRY(dq_attn_decode_q8(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos, n_ctx,
                                  w.ao, w.attn, w.attn_bytes, stream));
+    if (q256) {
+        DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.aq, w.as, w.ai, d_x, w.x2, stream));
+    } else {
         DQ_TRY(dq_quantize_act(DQ_ACT_Q8_0, w.ao, QD, 1, w.bq, w.bs, w.bi, nullptr, stream));
         DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.bq, w.bs, w.bi, d_x, w.x2, stream));
     }

@@ -20,10 +20,11 @@
 //    of the reference, entered into the MFMA as fp16(q * d), plus K/32 "min
 //    columns" fp16(d * isum_j) that carry the Q4_K min term (the weight side
 //    of those columns is fp16(-dmin * m_j));
-//  * expert GEMM: a wave owns 32 weight rows of one expert and streams their
-//    packed bytes once (prefetched one K step ahead), dequantizing each 64-K
-//    step to fp16 in registers (magic-number conversion, d*sc folded in) and
-//    applying it to up to 128 of the expert's tokens as 32x32x16 MFMA tiles.
+//  * expert GEMM: a workgroup owns 128 weight rows of one expert and streams
+//    their packed bytes once per 32 of the expert's tokens (a super-block per
+//    K step through a 2-stage LDS ring with the activation rows, 64 contiguous
+//    bytes per row and sub-plane per DMA), dequantizing to fp16 in registers
+//    (magic-number conversion, d*sc folded in) for 32x32x16 MFMA tiles.
 //    The fp16 roundings of the two operands move results by ~3e-4 relative.
 //    A K split (partials summed in a fixed order by the next kernel) gives
 //    the short down projection enough waves to stream HBM.
@@ -37,19 +38,40 @@ namespace {
 constexpr int MOE_MAX_EXPERT = 64;
 constexpr int MOE_MAX_K = 8;
 constexpr int TT = 32;         // tokens per MFMA tile
-constexpr int MAX_TILES = 4;   // token tiles per pass of a wave (128 pairs)
+constexpr int MAX_TILES = 1;   // token tiles per pass of a workgroup (32 pairs)
+constexpr int ACH = 32;        // 16-byte chunks of a token's activation per main step (256 halfs)
 constexpr int WAVES = 4;       // waves per workgroup, 32 weight rows each
-constexpr int MIN_BLK = 64;    // min columns are padded to a multiple of this
+constexpr int NSTAGE = 2;      // LDS ring stages (NSTAGE-1 steps in flight while one computes)
+constexpr int MIN_BLK = 8;     // min columns are padded to a multiple of this (16-byte rows)
+static_assert(NSTAGE == 2 || NSTAGE == 3, "the step wait counts NSTAGE-2 <= 1 later steps");
 
 // ---------------------------------------------------------------- routing --
 // One wave per token, lane e = expert e. The max is order-independent; the
 // double sum runs sequentially over the experts as the reference's loop does.
 __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int n_tok, int n_exp,
                                                         int k, int norm_w, float w_scale, int32_t* __restrict__ ids,
-                                                        float* __restrict__ wts) {
+                                                        float* __restrict__ wts, const float* __restrict__ x,
+                                                        int E, float* __restrict__ xscale) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= n_tok) return;  // uniform per wave
+    if (x) {
+        // the range scale of the token's activation row (row_scale_of)
+        float mx = 0.0f;
+        for (int c0 = 0; c0 < E; c0 += 16 * 256) {
+            // unconditional loads (clamped addresses) so all 16 are in flight at once
+            float4 f[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                f[j] = *reinterpret_cast<const float4*>(x + (size_t)t * E + min(c0 + 256 * j + 4 * lane, E - 4));
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (c0 + 256 * j + 4 * lane < E)
+                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f[j].x), fabsf(f[j].y)), fmaxf(fabsf(f[j].z), fabsf(f[j].w))));
+        }
+        mx = dq_wave_max(mx);
+        if (lane == 0) xscale[t] = row_scale_of(mx);
+    }
     const float* lg = logits + (size_t)t * n_exp;
     const float v = lane < n_exp ? lg[lane] : 0.0f;
     float m = lg[0];
@@ -96,63 +118,69 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
 }
 
 // Per-expert lists of the (token, slot) entries i = t*k + s, expert-major and
-// in ascending i; slot_pos[i] = the entry's position in that order. One thread
-// per expert, one workgroup.
-__global__ __launch_bounds__(64) void moe_lists_kernel(const int32_t* __restrict__ ids, int n_ent, int n_exp,
-                                                       int32_t* __restrict__ offsets, int32_t* __restrict__ pairs,
-                                                       int32_t* __restrict__ slot_pos) {
-    __shared__ int cnt[MOE_MAX_EXPERT + 1];
-    const int e = threadIdx.x;
-    if (e < n_exp) {
-        int c = 0;
-        for (int i = 0; i < n_ent; ++i) c += ids[i] == e;
-        cnt[e] = c;
-    }
-    __syncthreads();
-    if (e == 0) {
-        int o = 0;
-        for (int i = 0; i < n_exp; ++i) {
-            const int c = cnt[i];
-            cnt[i] = o;
-            o += c;
+// in ascending i; slot_pos[i] = the entry's position in that order. One
+// workgroup of 4 waves takes the entries 256 at a time (wave w: 64w..64w+63
+// of the round); per expert a ballot gives each wave's count and each lane's
+// rank among the earlier lanes of its wave. Pass 1 counts, pass 2 places.
+__global__ __launch_bounds__(256) void moe_lists_kernel(const int32_t* __restrict__ ids, int n_ent, int n_exp,
+                                                        int32_t* __restrict__ offsets, int32_t* __restrict__ pairs,
+                                                        int32_t* __restrict__ slot_pos) {
+    __shared__ int wcnt[4][MOE_MAX_EXPERT];
+    __shared__ int base[MOE_MAX_EXPERT + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;  // lanes below this one
+    // pass 1: per-expert totals, lane e of each wave accumulating expert e
+    int mine = 0;
+    for (int c0 = 0; c0 < n_ent; c0 += 256) {
+        const int i = c0 + tid;
+        const int id = i < n_ent ? ids[i] : -1;
+        for (int e = 0; e < n_exp; ++e) {
+            const int c = __popcll(__ballot(id == e));
+            if (lane == e) mine += c;
         }
-        cnt[n_exp] = o;
+    }
+    if (lane < n_exp) wcnt[wave][lane] = mine;
+    __syncthreads();
+    if (tid == 0) {
+        int o = 0;
+        for (int e = 0; e < n_exp; ++e) {
+            base[e] = o;
+            o += wcnt[0][e] + wcnt[1][e] + wcnt[2][e] + wcnt[3][e];
+        }
+        base[n_exp] = o;
     }
     __syncthreads();
-    if (e < n_exp) offsets[e] = cnt[e];
-    if (e == 0) offsets[n_exp] = cnt[n_exp];
-    if (e < n_exp) {
-        int o = cnt[e];
-        for (int i = 0; i < n_ent; ++i)
-            if (ids[i] == e) {
-                pairs[o] = i;
-                slot_pos[i] = o;
-                ++o;
-            }
+    if (tid <= n_exp) offsets[tid] = base[tid];
+    // pass 2: positions
+    for (int c0 = 0; c0 < n_ent; c0 += 256) {
+        const int i = c0 + tid;
+        const int id = i < n_ent ? ids[i] : -1;
+        int rank = 0;
+        for (int e = 0; e < n_exp; ++e) {
+            const uint64_t m = __ballot(id == e);
+            if (id == e) rank = __popcll(m & lt);
+            if (lane == e) wcnt[wave][e] = __popcll(m);
+        }
+        __syncthreads();
+        if (id >= 0) {
+            int pos = base[id] + rank;
+            for (int w = 0; w < wave; ++w) pos += wcnt[w][id];
+            pairs[pos] = i;
+            slot_pos[i] = pos;
+        }
+        __syncthreads();
+        if (tid < n_exp) base[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+        __syncthreads();
     }
 }
 
 // ------------------------------------------------------- activation rows --
-// Row p of A: the per-256 quantization of its source row (256 values per
-// wave, 4 per lane): d = amax/127, id = 127/amax, q = rint(v*id) (core/matmul.cpp
-// :1681-1700); columns [0, K) = fp16(q*d*s), min columns K + j =
-// fp16(d*isum_j*s) for the 32-blocks j, zero up to lda; inv[p] = 1/s.
-// The source row of p is pairs[p] / k (a token of x) when pairs is given,
-// else p.
-__global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ src,
-                                                      const float* __restrict__ rscale,
-                                                      const int32_t* __restrict__ pairs, int k, int n_rows, int K,
-                                                      int lda, _Float16* __restrict__ A, float* __restrict__ inv) {
-    const int lane = threadIdx.x & 63;
-    const int nblk = K / 256;
-    const long w = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (w >= (long)n_rows * nblk) return;  // uniform per wave
-    const int p = (int)(w / nblk), b = (int)(w % nblk);
-    const size_t srow = pairs ? (size_t)(pairs[p] / k) : (size_t)p;
-    const float sc = rscale[srow];
-    const int c0 = 256 * b + 4 * lane;
-    const float4 f = *reinterpret_cast<const float4*>(src + srow * K + c0);
-    const float v[4] = {f.x, f.y, f.z, f.w};
+// One 256-block b of an activation row (values v, 4 per lane): the per-256
+// quantization d = amax/127, id = 127/amax, q = rint(v*id) (core/matmul.cpp
+// :1681-1700), written as fp16(q*d*s) in columns 256b + 4 lane .. +3 and the
+// min columns K + 8b + j = fp16(d*isum_j*s), s the row's range scale.
+__device__ __forceinline__ void quant_256_block(const float (&v)[4], float sc, int lane, int b, int K,
+                                                _Float16* row) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     amax = dq_wave_max(amax);
     const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
@@ -166,31 +194,97 @@ __global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ 
         isum += q;
         hb[i] = __builtin_bit_cast(uint16_t, (_Float16)(((float)q * d) * sc));
     }
-    _Float16* row = A + (size_t)p * lda;
-    *reinterpret_cast<dq_u32x2*>(row + c0) = dq_u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+    *reinterpret_cast<dq_u32x2*>(row + 256 * b + 4 * lane) = dq_u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
     // 8 lanes hold one 32-block
 #pragma unroll
     for (int off = 1; off < 8; off <<= 1) isum += __shfl_xor(isum, off, DQ_WAVE);
     if ((lane & 7) == 0) row[K + 8 * b + (lane >> 3)] = (_Float16)((d * (float)isum) * sc);
+}
+
+// Row p of A from token pairs[p] / k of x: one wave per (pair, 256-block);
+// the row scales come from the route kernel; inv[p] = 1/s.
+__global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ x, const float* __restrict__ rscale,
+                                                      const int32_t* __restrict__ pairs, int k, int n_rows, int K,
+                                                      int lda, _Float16* __restrict__ A, float* __restrict__ inv) {
+    const int lane = threadIdx.x & 63;
+    const int nblk = K / 256;
+    const long w = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (w >= (long)n_rows * nblk) return;  // uniform per wave
+    const int p = (int)(w / nblk), b = (int)(w % nblk);
+    const size_t srow = (size_t)(pairs[p] / k);
+    const float sc = rscale[srow];
+    const float4 f = *reinterpret_cast<const float4*>(x + srow * K + 256 * b + 4 * lane);
+    const float v[4] = {f.x, f.y, f.z, f.w};
+    _Float16* row = A + (size_t)p * lda;
+    quant_256_block(v, sc, lane, b, K, row);
     if (b == 0) {  // zero padding of the min columns, and the output factor
         for (int c = K + K / 32 + lane; c < lda; c += DQ_WAVE) row[c] = (_Float16)0.0f;
         if (lane == 0) inv[p] = 1.0f / sc;
     }
 }
 
-// h[p] = silu(g) * u (models/dense_forward.cpp:53-55) with g, u the sums over
-// the K splits of the gate and up outputs of pair p (split order 0, 1, ...).
-__global__ __launch_bounds__(256) void moe_silu_kernel(const float* __restrict__ gate, const float* __restrict__ up,
-                                                       int nsplit, size_t split_stride, size_t n,
-                                                       float* __restrict__ h) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    float g = gate[i], u = up[i];
-    for (int s = 1; s < nsplit; ++s) {
-        g += gate[s * split_stride + i];
-        u += up[s * split_stride + i];
+// The down projection's activation row of pair p in one workgroup: h =
+// silu(g) * u (models/dense_forward.cpp:53-55) with g, u the sums over the K
+// splits of the gate and up outputs (split order 0, 1, ...), its range scale
+// (row_scale_of), and the per-256 quantization as moe_act_kernel writes it.
+// SILU_WAVES waves, wave w takes the 256-blocks w, w + SILU_WAVES, ...; h
+// stays in registers (F <= SILU_WAVES * SILU_J * 256).
+constexpr int SILU_WAVES = 16, SILU_J = 4;  // n_ff <= 16384
+__global__ __launch_bounds__(64 * SILU_WAVES) void moe_silu_act_kernel(const float* __restrict__ gate,
+                                                                       const float* __restrict__ up, int nsplit,
+                                                                       size_t split_stride, int F, int lda,
+                                                                       _Float16* __restrict__ A,
+                                                                       float* __restrict__ inv) {
+    __shared__ float wmax[SILU_WAVES];
+    const int p = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nblk = F / 256;
+    float4 g[SILU_J], u[SILU_J];
+    // every load of the row issued before the first use
+#pragma unroll
+    for (int j = 0; j < SILU_J; ++j) {
+        const int b = wave + SILU_WAVES * j;
+        const size_t o = (size_t)p * F + 256 * (size_t)min(b, nblk - 1) + 4 * lane;
+        g[j] = *reinterpret_cast<const float4*>(gate + o);
+        u[j] = *reinterpret_cast<const float4*>(up + o);
     }
-    h[i] = g / (1.0f + expf(-g)) * u;
+    for (int s = 1; s < nsplit; ++s) {
+#pragma unroll
+        for (int j = 0; j < SILU_J; ++j) {
+            const int b = wave + SILU_WAVES * j;
+            const size_t o = s * split_stride + (size_t)p * F + 256 * (size_t)min(b, nblk - 1) + 4 * lane;
+            const float4 g2 = *reinterpret_cast<const float4*>(gate + o);
+            const float4 u2 = *reinterpret_cast<const float4*>(up + o);
+            g[j].x += g2.x, g[j].y += g2.y, g[j].z += g2.z, g[j].w += g2.w;
+            u[j].x += u2.x, u[j].y += u2.y, u[j].z += u2.z, u[j].w += u2.w;
+        }
+    }
+    float h[SILU_J][4];
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < SILU_J; ++j) {
+        const float gv[4] = {g[j].x, g[j].y, g[j].z, g[j].w}, uv[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            h[j][i] = gv[i] / (1.0f + expf(-gv[i])) * uv[i];
+            if (wave + SILU_WAVES * j < nblk) mx = fmaxf(mx, fabsf(h[j][i]));
+        }
+    }
+    mx = dq_wave_max(mx);
+    if (lane == 0) wmax[wave] = mx;
+    __syncthreads();
+    float r = wmax[0];
+#pragma unroll
+    for (int w = 1; w < SILU_WAVES; ++w) r = fmaxf(r, wmax[w]);
+    const float sc = row_scale_of(r);
+    _Float16* row = A + (size_t)p * lda;
+#pragma unroll
+    for (int j = 0; j < SILU_J; ++j) {
+        const int b = wave + SILU_WAVES * j;
+        if (b < nblk) quant_256_block(h[j], sc, lane, b, F, row);
+    }
+    if (threadIdx.x == 0) inv[p] = 1.0f / sc;
+    for (int c = F + F / 32 + (int)threadIdx.x; c < lda; c += 64 * SILU_WAVES) row[c] = (_Float16)0.0f;
 }
 
 // ------------------------------------------------------------ expert GEMM --
@@ -201,142 +295,230 @@ struct MoeGemm {
     const _Float16* A;    // activation rows [n_pairs][lda]
     const float* inv;     // per pair: 1/s of its activation row
     const int32_t* offsets;
-    int rows, K, lda, n_pairs, nsplit, steps_per_split, main_steps, total_steps;
+    int rows, K, lda, n_pairs, nsplit, steps_per_split, main_steps;
 };
 
-// Weight bytes of one 64-K step (Q4_K item of 64 weights) for this lane's row:
-// qs bytes 8h..8h+7 of both sub-planes and the super-block header.
+// Weight bytes of one main step, a Q4_K super-block (K = 256, 4 items) of this
+// lane's row: the 4 16-byte items of quant sub-plane h and the super-block
+// header.
 struct WRaw {
-    dq_u32x2 p0, p1;
+    dq_u32x4 q[4];
     dq_u32x4 hd;
 };
 
-__device__ __forceinline__ void load_w(WRaw& r, const uint8_t* base, const DqLayout& L, size_t row, int st, int h,
-                                       bool live) {
-    if (live) {
-        const uint8_t* q = base + L.q_off + row * L.q_row + 16 * (size_t)st + 8 * h;
-        r.p0 = __builtin_nontemporal_load(reinterpret_cast<const dq_u32x2*>(q));
-        r.p1 = __builtin_nontemporal_load(reinterpret_cast<const dq_u32x2*>(q + L.p_stride));
-        r.hd = __builtin_nontemporal_load(
-            reinterpret_cast<const dq_u32x4*>(base + L.s_off + row * L.s_row + 16 * (size_t)(st >> 2)));
-    } else {
-        r.p0 = r.p1 = dq_u32x2{0, 0};
-        r.hd = dq_u32x4{0, 0, 0, 0};
-    }
-}
-
-// B fragments of a main step: kk 0: P0 low nibbles (sub-block 2g, first 16),
-// 1: P1 low (sub-block 2g, last 16), 2: P0 high (2g+1), 3: P1 high, times
-// a = d * sc of the sub-block (fp16), for this lane's 8 K values 8h..8h+7.
-__device__ __forceinline__ void b_main(const WRaw& r, int st, bool ok, h8 (&bf)[4]) {
-    const int g = st & 3;
+// B fragments of item t (= group g of the super-block) of a main step. Lane
+// half h holds quant sub-plane h of the item: bytes 0-15 of its 32 qs bytes
+// (h = 0) or 16-31 (h = 1), i.e. positions 16h..16h+15 of sub-block 2t (low
+// nibbles) and 2t+1 (high nibbles). Slice kk: kk/2 picks the sub-block,
+// kk%2 the 8 positions 16h + 8(kk%2) + 0..7; values (q) * d*sc in fp16. The
+// activation fragment of the same slice holds the same positions (see
+// a_offset).
+__device__ __forceinline__ void b_item(const WRaw& r, int t, bool ok, h8 (&bf)[4]) {
     const float d = dq_h2f((uint16_t)(r.hd.x & 0xFFFF));
-    const _Float16 a0 = (_Float16)(ok ? d * (float)q4k_scale(2 * g, r.hd.y, r.hd.z, r.hd.w) : 0.0f);
-    const _Float16 a1 = (_Float16)(ok ? d * (float)q4k_scale(2 * g + 1, r.hd.y, r.hd.z, r.hd.w) : 0.0f);
+    const _Float16 a0 = (_Float16)(ok ? d * (float)q4k_scale(2 * t, r.hd.y, r.hd.z, r.hd.w) : 0.0f);
+    const _Float16 a1 = (_Float16)(ok ? d * (float)q4k_scale(2 * t + 1, r.hd.y, r.hd.z, r.hd.w) : 0.0f);
     const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
     const h2 v0 = {a0, a0}, v1 = {a1, a1};
+    const dq_u32x4 w = r.q[t];
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-        const dq_u32x2 src = (kk & 1) ? r.p1 : r.p0;
-        const uint32_t m0 = kk < 2 ? (src.x & 0x0F0F0F0Fu) : ((src.x >> 4) & 0x0F0F0F0Fu);
-        const uint32_t m1 = kk < 2 ? (src.y & 0x0F0F0F0Fu) : ((src.y >> 4) & 0x0F0F0F0Fu);
-        uint32_t t[4];
-        bytes_to_h2(m0, bias, kk < 2 ? v0 : v1, &t[0]);
-        bytes_to_h2(m1, bias, kk < 2 ? v0 : v1, &t[2]);
-        bf[kk] = __builtin_bit_cast(h8, dq_u32x4{t[0], t[1], t[2], t[3]});
+        const uint32_t x0 = (kk & 1) ? w.z : w.x, x1 = (kk & 1) ? w.w : w.y;
+        const uint32_t m0 = kk < 2 ? (x0 & 0x0F0F0F0Fu) : ((x0 >> 4) & 0x0F0F0F0Fu);
+        const uint32_t m1 = kk < 2 ? (x1 & 0x0F0F0F0Fu) : ((x1 >> 4) & 0x0F0F0F0Fu);
+        uint32_t o[4];
+        bytes_to_h2(m0, bias, kk < 2 ? v0 : v1, &o[0]);
+        bytes_to_h2(m1, bias, kk < 2 ? v0 : v1, &o[2]);
+        bf[kk] = __builtin_bit_cast(h8, dq_u32x4{o[0], o[1], o[2], o[3]});
     }
 }
 
-// B fragments of min step e: column 64e + 16kk + 8h + i is 32-block j of the
-// row, i.e. sub-block i of super-block sb = 8e + 2kk + h: fp16(-dmin * m_i).
-__device__ __forceinline__ void b_min(const uint8_t* base, const DqLayout& L, size_t row, int e, int h, int nsb,
-                                      bool ok, h8 (&bf)[4]) {
+// Column (in halfs) of the activation fragment of lane half h for item t,
+// slice kk of main step st: sub-block 2t + kk/2, positions 16h + 8(kk%2)..+7.
+__device__ __forceinline__ int a_offset(int st, int t, int kk, int h) {
+    return 256 * st + 64 * t + 32 * (kk >> 1) + 16 * h + 8 * (kk & 1);
+}
+
+// Min term of the main step's super-block as one extra 16-wide MFMA slice:
+// lanes of half 0 carry its 8 sub-blocks (weight side fp16(-dmin * m_j) from
+// the header, activation side the min columns K + 8st + j), half 1 zeros.
+__device__ __forceinline__ h8 b_min8(const dq_u32x4& hd, bool ok) {
+    const float dmin = dq_h2f((uint16_t)(hd.x >> 16));
+    _Float16 v[8];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-        const int sb = 8 * e + 2 * kk + h;
-        _Float16 v[8];
-        if (ok && sb < nsb) {
-            const dq_u32x4 hd = *reinterpret_cast<const dq_u32x4*>(base + L.s_off + row * L.s_row + 16 * (size_t)sb);
-            const float dmin = dq_h2f((uint16_t)(hd.x >> 16));
+    for (int i = 0; i < 8; ++i) v[i] = (_Float16)(ok ? -(dmin * (float)q4k_min(i, hd.y, hd.z, hd.w)) : 0.0f);
+    return *reinterpret_cast<const h8*>(v);
+}
+
+#define DQ_LDS_PTR(p) reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(p))
+
+// s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt in bits
+// 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// DMA of the activation rows of main step st for the pass starting at pair c
+// into LDS stage `dst`: token m (0 .. 32*ntile-1) has 32 chunks of 16 bytes,
+// chunk k stored at slot m*32 + (k ^ (m & 31)) (an XOR swizzle: the 32 tokens
+// a fragment read spans fall into different bank groups). Slot s is written
+// by lane s % 64 of the instruction covering it (global_load_lds writes lane
+// i at base + 16 i), so each lane fetches the chunk that belongs there.
+constexpr int A_LOADS = MAX_TILES * TT * ACH / (64 * WAVES);  // DMAs per thread per step
+static_assert(A_LOADS >= 1, "activation DMA slots per thread");
+constexpr int A_MAIN_BYTES = MAX_TILES * TT * ACH * 16;
+constexpr int A_STAGE_BYTES = A_MAIN_BYTES + 64 * 16;  // + the min chunks (64 slots, 32 tokens twice)
+__device__ __forceinline__ void issue_a(const _Float16* A, int lda, int K, int c, int p_end, int st, uint8_t* dst,
+                                        int tid) {
+    {   // the step's 8 min columns of token lane % 32 (every wave loads the same slots)
+        const int p = min(c + (tid & 31), p_end - 1);
+        __builtin_amdgcn_global_load_lds(A + (size_t)p * lda + K + 8 * (size_t)st, DQ_LDS_PTR(dst + A_MAIN_BYTES), 16,
+                                         0, 0);
+    }
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = (_Float16)(-(dmin * (float)q4k_min(i, hd.y, hd.z, hd.w)));
-        } else {
+    for (int j = 0; j < A_LOADS; ++j) {
+        const int slot = j * 64 * WAVES + tid;
+        const int m = slot / ACH, kp = slot % ACH, k = kp ^ (m & 31);
+        const int p = min(c + m, p_end - 1);
+        const _Float16* src = A + (size_t)p * lda + 256 * (size_t)st + 8 * k;
+        uint8_t* base = dst + (size_t)(j * 64 * WAVES + (tid & ~63)) * 16;  // wave-uniform
+        __builtin_amdgcn_global_load_lds(src, DQ_LDS_PTR(base), 16, 0, 0);
+    }
+}
+
+// Weight tile of a main step in LDS: for the workgroup's 256 rows, the 64
+// bytes of sub-plane 0 and of sub-plane 1 (4 items of 16 bytes each) and the
+// 16-byte super-block header. The DMA reads each row-plane's 64 bytes with 4
+// consecutive lanes (whole 64-byte pieces of one line per row: the pattern
+// HBM streams at full rate; one lane per row, 16 bytes each, streams at less
+// than half of it). Item t of row r sits in chunk slot t ^ ((r >> 2) & 3), so
+// the fragment reads of 32 rows spread over the banks.
+constexpr int WROWS = 32 * WAVES;                  // rows per workgroup
+constexpr int WT_PLANE = WROWS * 64;               // bytes of one sub-plane tile
+constexpr int WT_BYTES = 2 * WT_PLANE + WROWS * 16;
+__device__ __forceinline__ void issue_w(const uint8_t* base, const DqLayout& L, size_t row0, int nrows, int st,
+                                        uint8_t* dst, int tid) {
+    const int wbase = tid & ~63;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = (_Float16)0.0f;
+    for (int pl = 0; pl < 2; ++pl) {
+#pragma unroll
+        for (int j = 0; j < WROWS * 4 / (64 * WAVES); ++j) {
+            const int slot = j * 64 * WAVES + tid;
+            const int r = slot >> 2, ts = slot & 3, t = ts ^ ((r >> 2) & 3);
+            const size_t row = row0 + (size_t)min(r, nrows - 1);
+            const uint8_t* src = base + L.q_off + (size_t)pl * L.p_stride + row * L.q_row + 64 * (size_t)st + 16 * t;
+            uint8_t* d = dst + pl * WT_PLANE + (size_t)(j * 64 * WAVES + wbase) * 16;
+            __builtin_amdgcn_global_load_lds(src, DQ_LDS_PTR(d), 16, 0, 0);
         }
-        bf[kk] = *reinterpret_cast<const h8*>(v);
     }
+    // headers: WROWS slots, so waves w and w + WAVES/2 load the same block
+    const int slot = tid % WROWS;
+    const size_t row = row0 + (size_t)min(slot, nrows - 1);
+    __builtin_amdgcn_global_load_lds(base + L.s_off + row * L.s_row + 16 * (size_t)st,
+                                     DQ_LDS_PTR(dst + 2 * WT_PLANE + (size_t)((tid & ~63) % WROWS) * 16), 16, 0, 0);
 }
+// DMAs per thread per step: activation (+ min chunk), the two sub-planes, the header
+constexpr int STEP_LOADS = A_LOADS + 1 + 2 * WROWS * 4 / (64 * WAVES) + 1;
+static_assert(WROWS * 4 % (64 * WAVES) == 0 && 64 * WAVES == 2 * WROWS, "DMA slots per thread");
 
-// Grid: x = 128-row tiles of one expert's rows, y = expert, z = matrix * nsplit
-// + split. Wave w of the workgroup owns rows 128x + 32w .. +31; lane l feeds
-// row l % 32 with K values 8(l/32)..+7 of each 16-wide slice.
+// Grid: x = 256-row tiles of one expert's rows, y = expert, z = matrix * nsplit
+// + split. Wave w of the workgroup owns rows 256x + 32w .. +31; lane l feeds
+// row l % 32 with K values 8(l/32)..+7 of each 16-wide slice. The expert's
+// pairs are taken 32 at a time (one 32-token MFMA tile). Per main step (one
+// super-block) the weight tile and the activation rows go through an
+// NSTAGE-stage LDS ring, the next NSTAGE-1 steps' DMAs in flight while this
+// one computes.
 __global__ __launch_bounds__(64 * WAVES) void moe_gemm_kernel(MoeGemm G) {
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    __shared__ __align__(16) uint8_t aring[NSTAGE][A_STAGE_BYTES];
+    __shared__ __align__(16) uint8_t wring[NSTAGE][WT_BYTES];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(tid >> 6));
     const int e = blockIdx.y;
     const int mat = blockIdx.z / G.nsplit, split = blockIdx.z % G.nsplit;
     const int p_begin = G.offsets[e], p_end = G.offsets[e + 1];
-    if (p_begin >= p_end) return;  // no token routed to this expert
+    if (p_begin >= p_end) return;  // no token routed to this expert (uniform)
     const int h = lane >> 5;
-    const int rloc = blockIdx.x * (32 * WAVES) + 32 * wave + (lane & 31);
+    const int r_wg = blockIdx.x * WROWS;                 // first row of the workgroup (in the expert)
+    const int nrows = min(WROWS, G.rows - r_wg);
+    const int rl = 32 * wave + (lane & 31);              // this lane's row in the tile
+    const int rloc = r_wg + rl;
     const bool row_ok = rloc < G.rows;
-    const size_t row = (size_t)e * G.rows + (size_t)min(rloc, G.rows - 1);
+    const size_t row0 = (size_t)e * G.rows + r_wg;
     const uint8_t* base = G.w[mat];
     const DqLayout L = G.L[mat];
     float* __restrict__ y = G.y[mat] + (size_t)split * G.n_pairs * G.rows;
     const int s0 = split * G.steps_per_split;
-    const int s1 = min(G.total_steps, s0 + G.steps_per_split);
-    if (s0 >= s1) return;
-    const int nsb = G.K / 256;
+    const int main_end = min(G.main_steps, s0 + G.steps_per_split);
+    if (s0 >= main_end) return;  // uniform
 
-    for (int c = p_begin; c < p_end; c += TT * MAX_TILES) {
-        const int ntile = min(MAX_TILES, (p_end - c + TT - 1) / TT);
-        f16v acc[MAX_TILES];
+    for (int c = p_begin; c < p_end; c += TT) {
+        f16v acc;
 #pragma unroll
-        for (int tt = 0; tt < MAX_TILES; ++tt)
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        {
+            // prologue: the first NSTAGE-1 steps in flight
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[tt][r] = 0.0f;
-        // activation row of this lane's token in each tile (clamped to the list)
-        const _Float16* arow[MAX_TILES];
-#pragma unroll
-        for (int tt = 0; tt < MAX_TILES; ++tt)
-            arow[tt] = G.A + (size_t)min(c + tt * TT + (lane & 31), p_end - 1) * G.lda + 8 * h;
-
-        WRaw cur, nxt;
-        load_w(cur, base, L, row, min(s0, G.main_steps - 1), h, s0 < G.main_steps);
-        for (int st = s0; st < s1; ++st) {
-            const bool main = st < G.main_steps;
-            // prefetch the next main step's weights while this one computes
-            load_w(nxt, base, L, row, min(st + 1, G.main_steps - 1), h, st + 1 < min(s1, G.main_steps));
-            h8 bf[4];
-            if (main) b_main(cur, st, row_ok, bf);
-            else b_min(base, L, row, st - G.main_steps, h, nsb, row_ok, bf);
-#pragma unroll
-            for (int tt = 0; tt < MAX_TILES; ++tt) {
-                if (tt < ntile) {
-                    const _Float16* ap = arow[tt] + 64 * (size_t)st;
-                    h8 af[4];
-#pragma unroll
-                    for (int kk = 0; kk < 4; ++kk) af[kk] = *reinterpret_cast<const h8*>(ap + 16 * kk);
-#pragma unroll
-                    for (int kk = 0; kk < 4; ++kk)
-                        acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk], bf[kk], acc[tt], 0, 0, 0);
+            for (int q = 0; q < NSTAGE - 1; ++q) {
+                if (s0 + q < main_end) {
+                    issue_a(G.A, G.lda, G.K, c, p_end, s0 + q, aring[q], tid);
+                    issue_w(base, L, row0, nrows, s0 + q, wring[q], tid);
                 }
             }
-            cur = nxt;
+            for (int st = s0; st < main_end; ++st) {
+                const int stage = (st - s0) % NSTAGE;
+                // this step's DMAs have landed once only the later steps'
+                // (issued after them, at most NSTAGE-2) can be outstanding
+                if constexpr (NSTAGE > 2) {
+                    if (st + 1 < main_end) wait_vm<STEP_LOADS * (NSTAGE - 2)>();
+                    else wait_vm<0>();
+                } else {
+                    wait_vm<0>();
+                }
+                __syncthreads();  // every wave's DMAs landed; stage st-1 is free
+                if (st + NSTAGE - 1 < main_end) {
+                    const int ns = (st - s0 + NSTAGE - 1) % NSTAGE;
+                    issue_a(G.A, G.lda, G.K, c, p_end, st + NSTAGE - 1, aring[ns], tid);
+                    issue_w(base, L, row0, nrows, st + NSTAGE - 1, wring[ns], tid);
+                }
+                const uint8_t* ab = aring[stage];
+                const uint8_t* wb = wring[stage];
+                WRaw wr;
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    wr.q[t] = *reinterpret_cast<const dq_u32x4*>(wb + h * WT_PLANE + rl * 64 +
+                                                                 16 * (t ^ ((rl >> 2) & 3)));
+                wr.hd = *reinterpret_cast<const dq_u32x4*>(wb + 2 * WT_PLANE + rl * 16);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    h8 bf[4];
+                    b_item(wr, t, row_ok, bf);
+                    const int m = lane & 31;
+                    h8 af[4];
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) {
+                        const int k = a_offset(0, t, kk, h) / 8;  // chunk of the slice
+                        af[kk] = *reinterpret_cast<const h8*>(ab + (size_t)(m * ACH + (k ^ (m & 31))) * 16);
+                    }
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk)
+                        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk], bf[kk], acc, 0, 0, 0);
+                }
+                {   // the super-block's min term
+                    const h8 zero = {};
+                    const h8 am = h == 0 ? *reinterpret_cast<const h8*>(ab + A_MAIN_BYTES + (lane & 31) * 16) : zero;
+                    const h8 bm = h == 0 ? b_min8(wr.hd, row_ok) : zero;
+                    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, acc, 0, 0, 0);
+                }
+            }
+            __syncthreads();  // the ring is reused by the next pass
         }
         // D of 32x32x16: lane l, register r -> weight row l % 32, token (r/4)*8 + (l/32)*4 + r%4
         if (row_ok) {
 #pragma unroll
-            for (int tt = 0; tt < MAX_TILES; ++tt) {
-                if (tt < ntile) {
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int p = c + tt * TT + (r >> 2) * 8 + h * 4 + (r & 3);
-                        if (p < p_end) y[(size_t)p * G.rows + rloc] = acc[tt][r] * G.inv[p];
-                    }
-                }
+            for (int r = 0; r < 16; ++r) {
+                const int p = c + (r >> 2) * 8 + h * 4 + (r & 3);
+                if (p < p_end) y[(size_t)p * G.rows + rloc] = acc[r] * G.inv[p];
             }
         }
     }
@@ -365,9 +547,9 @@ __global__ __launch_bounds__(256) void moe_scatter_kernel(const float* __restric
 // ------------------------------------------------------------- workspace --
 struct MoeWs {
     int32_t *ids, *offsets, *pairs, *slot_pos;
-    float *wts, *xscale, *hscale, *inv_in, *inv_h;
+    float *wts, *xscale, *inv_in, *inv_h;
     _Float16 *a_in, *a_h;
-    float *gate, *up, *h, *down;
+    float *gate, *up, *down;
     size_t total;
 };
 
@@ -386,11 +568,11 @@ int cus() {
 }
 
 // K splits: enough waves (>= 16 per CU) to stream the weights, a split
-// covering at least 16 K steps.
+// covering at least 4 K steps.
 int pick_split(int n_exp, int rows, int n_mat, int steps) {
     const long waves = (long)n_exp * ((rows + 31) / 32) * n_mat;
     int s = 1;
-    while (s < 8 && waves * s < 16L * cus() && steps / (2 * s) >= 16) s *= 2;
+    while (s < 8 && waves * s < 16L * cus() && steps / (2 * s) >= 4) s *= 2;
     return s;
 }
 
@@ -411,13 +593,11 @@ MoeWs carve(const dq_moe_t* m, uint32_t n_tok, int split_gu, int split_d, uint8_
     w.pairs = (int32_t*)take(n_ent * 4);
     w.slot_pos = (int32_t*)take(n_ent * 4);
     w.xscale = (float*)take((size_t)n_tok * 4);
-    w.hscale = (float*)take(n_ent * 4);
     w.inv_in = (float*)take(n_ent * 4);
     w.inv_h = (float*)take(n_ent * 4);
     w.a_in = (_Float16*)take(n_ent * lda_in * 2);
     w.gate = (float*)take((size_t)split_gu * n_ent * F * 4);
     w.up = (float*)take((size_t)split_gu * n_ent * F * 4);
-    w.h = (float*)take(n_ent * F * 4);
     w.a_h = (_Float16*)take(n_ent * lda_h * 2);
     w.down = (float*)take((size_t)split_d * n_ent * E * 4);
     w.total = off;
@@ -429,14 +609,14 @@ bool moe_ok(const dq_moe_t* m) {
     if (m->n_expert == 0 || m->n_expert > MOE_MAX_EXPERT) return false;
     if (m->n_expert_used == 0 || m->n_expert_used > MOE_MAX_K || m->n_expert_used > m->n_expert) return false;
     if (m->n_embd == 0 || m->n_embd % 256 || m->n_ff == 0 || m->n_ff % 256) return false;
-    if (m->n_embd > (1u << 20) || m->n_ff > (1u << 20)) return false;
+    if (m->n_embd > (1u << 20) || m->n_ff > 256u * SILU_WAVES * SILU_J) return false;
     if ((size_t)m->n_expert * m->n_ff > 0x3FFFFFFF || (size_t)m->n_expert * m->n_embd > 0x3FFFFFFF) return false;
     return true;
 }
 
 void splits(const dq_moe_t* m, int* sgu, int* sd) {
-    const int steps_gu = (int)m->n_embd / 64 + min_cols((int)m->n_embd) / 64;
-    const int steps_d = (int)m->n_ff / 64 + min_cols((int)m->n_ff) / 64;
+    const int steps_gu = (int)m->n_embd / 256;
+    const int steps_d = (int)m->n_ff / 256;
     *sgu = pick_split((int)m->n_expert, (int)m->n_ff, 2, steps_gu);
     *sd = pick_split((int)m->n_expert, (int)m->n_embd, 1, steps_d);
 }
@@ -459,9 +639,10 @@ int launch_gemm(const uint8_t* w0, const uint8_t* w1, int n_mat, int n_exp, int 
     G.lda = lda;
     G.n_pairs = n_pairs;
     G.nsplit = nsplit;
-    G.main_steps = K / 64;
-    G.total_steps = G.main_steps + min_cols(K) / 64;
-    G.steps_per_split = (G.total_steps + nsplit - 1) / nsplit;
+    G.main_steps = K / 256;  // a super-block per main step
+    G.steps_per_split = (G.main_steps + nsplit - 1) / nsplit;
+    // every split owns at least one step (its partial is always written)
+    if ((long)(nsplit - 1) * G.steps_per_split >= G.main_steps) return DQ_ERR_NOT_SUPPORTED;
     const dim3 grid((unsigned)((rows + 32 * WAVES - 1) / (32 * WAVES)), (unsigned)n_exp, (unsigned)(n_mat * nsplit));
     moe_gemm_kernel<<<grid, 64 * WAVES, 0, s>>>(G);
     return dq_launch_status();
@@ -485,7 +666,8 @@ int dq_moe_route(const float* d_logits, uint32_t n_tok, uint32_t n_expert, uint3
     if (!d_logits || !d_ids || !d_wts) return DQ_ERR_INVALID_ARG;
     if (n_tok > (1u << 24)) return DQ_ERR_NOT_SUPPORTED;
     moe_route_kernel<<<(n_tok + 3) / 4, 256, 0, (hipStream_t)stream>>>(d_logits, (int)n_tok, (int)n_expert, (int)k,
-                                                                       norm_w, w_scale, d_ids, d_wts);
+                                                                       norm_w, w_scale, d_ids, d_wts, nullptr, 0,
+                                                                       nullptr);
     return dq_launch_status();
 }
 
@@ -512,13 +694,13 @@ int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint3
     const int E = (int)m->n_embd, F = (int)m->n_ff;
     const int n_ent = (int)n_tok * k;
     const int lda_in = E + min_cols(E), lda_h = F + min_cols(F);
-    // routing and lists
-    DQ_TRY(dq_moe_route(d_logits, n_tok, m->n_expert, m->n_expert_used, m->norm_w, m->w_scale, w.ids, w.wts, stream));
-    moe_lists_kernel<<<1, 64, 0, s>>>(w.ids, n_ent, n_exp, w.offsets, w.pairs, w.slot_pos);
+    // routing (with the row scales of x) and the per-expert lists
+    moe_route_kernel<<<(n_tok + 3) / 4, 256, 0, s>>>(d_logits, (int)n_tok, n_exp, k, m->norm_w, m->w_scale, w.ids,
+                                                     w.wts, d_x, E, w.xscale);
     DQ_TRY(dq_launch_status());
-    // activation rows of the pairs (row scale per token)
-    row_scale_kernel<<<n_tok, 256, 0, s>>>(d_x, E, w.xscale);
+    moe_lists_kernel<<<1, 256, 0, s>>>(w.ids, n_ent, n_exp, w.offsets, w.pairs, w.slot_pos);
     DQ_TRY(dq_launch_status());
+    // activation rows of the pairs
     {
         const long waves = (long)n_ent * (E / 256);
         moe_act_kernel<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(d_x, w.xscale, w.pairs, k, n_ent, E, lda_in,
@@ -529,17 +711,8 @@ int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint3
     DQ_TRY(launch_gemm((const uint8_t*)m->wgate, (const uint8_t*)m->wup, 2, n_exp, F, E, w.a_in, w.inv_in, lda_in,
                        w.offsets, n_ent, sgu, w.gate, w.up, s));
     // h = silu(gate) * up, quantized for the down projection
-    {
-        const size_t n = (size_t)n_ent * F;
-        moe_silu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(w.gate, w.up, sgu, n, n, w.h);
-        DQ_TRY(dq_launch_status());
-        row_scale_kernel<<<n_ent, 256, 0, s>>>(w.h, F, w.hscale);
-        DQ_TRY(dq_launch_status());
-        const long waves = (long)n_ent * (F / 256);
-        moe_act_kernel<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(w.h, w.hscale, nullptr, k, n_ent, F, lda_h, w.a_h,
-                                                                   w.inv_h);
-        DQ_TRY(dq_launch_status());
-    }
+    moe_silu_act_kernel<<<n_ent, 64 * SILU_WAVES, 0, s>>>(w.gate, w.up, sgu, (size_t)n_ent * F, F, lda_h, w.a_h, w.inv_h);
+    DQ_TRY(dq_launch_status());
     DQ_TRY(launch_gemm((const uint8_t*)m->wdown, nullptr, 1, n_exp, E, F, w.a_h, w.inv_h, lda_h, w.offsets, n_ent,
                        sd, w.down, nullptr, s));
     {

@@ -1,13 +1,9 @@
-// dq_quant.hip - activation quantizers (per-32 and per-256-replicated) and the
-// GGUF block_q8_1 wire form. One lane per 32-value block: the lane loads its
-// 128 bytes as 8 dwordx4, so a wave covers 8 KB of contiguous input.
-//
-// Bit-exactness with the reference: amax is exact; d = amax/127 and the
-// reciprocal use IEEE division (hipcc's default correctly rounded fp32
-// divide); q = rint(x*id) is v_rndne_f32 (round to nearest even, the lrintf /
-// cvtps2dq rounding of the reference); the float sum is sequential. The file
-// is built with -ffp-contract=off so no multiply-add is fused.
+// dq_quant.hip - activation quantizers (per-32 and per-256-replicated, the
+// arithmetic in dq_quant.h) and the GGUF block_q8_1 wire form. One lane per
+// 32-value block: the lane loads its 128 bytes as 8 dwordx4, so a wave covers
+// 8 KB of contiguous input.
 #include "dq_common.h"
+#include "dq_quant.h"
 
 namespace {
 
@@ -21,54 +17,12 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restri
     const bool valid = b < n_blocks;
     const size_t bb = valid ? b : n_blocks - 1;
     float v[32];
-    const float4* p = reinterpret_cast<const float4*>(x + bb * 32);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 f = p[i];
-        v[4 * i + 0] = f.x;
-        v[4 * i + 1] = f.y;
-        v[4 * i + 2] = f.z;
-        v[4 * i + 3] = f.w;
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const float a = fabsf(v[i]);
-        amax = (amax < a) ? a : amax;
-    }
-    float d, id;
-    if (KIND == DQ_ACT_Q8_0) {
-        // core/quant.cpp:31-33
-        d = amax > 0.0f ? amax / 127.0f : 0.0f;
-        id = d > 0.0f ? 1.0f / d : 0.0f;
-    } else {
-        // core/matmul.cpp:1681-1683: one amax per 256 = 8 consecutive lanes
-#pragma unroll
-        for (int off = 1; off < 8; off <<= 1) {
-            const float o = __shfl_xor(amax, off, DQ_WAVE);
-            amax = (amax < o) ? o : amax;
-        }
-        d = amax > 0.0f ? amax / 127.0f : 0.0f;
-        id = d > 0.0f ? 127.0f / amax : 0.0f;
-    }
-    if (!valid) return;
-    int s = 0;
-    float fs = 0.0f;
+    dq_load32(x + bb * 32, v);
     uint32_t packed[8];
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            int iv = (int)rintf(v[4 * w + k] * id);
-            iv = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
-            s += iv;
-            word |= (uint32_t)(iv & 0xFF) << (8 * k);
-        }
-        packed[w] = word;
-    }
-#pragma unroll
-    for (int i = 0; i < 32; ++i) fs += v[i];
+    float d, fs;
+    int s;
+    dq_quant_block<KIND>(v, packed, d, s, fs);
+    if (!valid) return;
     dq_u32x4* qo = reinterpret_cast<dq_u32x4*>(q + b * 32);
     qo[0] = dq_u32x4{packed[0], packed[1], packed[2], packed[3]};
     qo[1] = dq_u32x4{packed[4], packed[5], packed[6], packed[7]};

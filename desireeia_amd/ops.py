@@ -156,9 +156,32 @@ def gemv_group(mats, act, outs=None, residuals=None):
     return ys
 
 
-def matmul(mat, x):
-    """y = W x with the semantics of the reference's matmul_<fmt> (batch 1)."""
-    return gemv(mat, quantize_act(x, act_kind_for(mat.fmt)))
+def matmul(mat, x, out=None):
+    """y = W x with the semantics of the reference's matmul_<fmt> (batch 1):
+    one launch, the activation quantized in-kernel (dq_gemv_f32)."""
+    lib = _lib.load()
+    x = x.contiguous()
+    y = out if out is not None else torch.empty(mat.rows, dtype=torch.float32, device=mat.buf.device)
+    _lib.check(lib.dq_gemv_f32(mat.fmt, _ptr(mat.buf), mat.rows, mat.cols, _ptr(x), _ptr(y), _stream()),
+               "dq_gemv_f32")
+    return y
+
+
+def matmul_group(mats, x, outs=None, residuals=None):
+    """Several matrices reading the fp32 activation x, any formats mixed
+    (dq_gemv_group_f32): one launch per distinct format."""
+    lib = _lib.load()
+    x = x.contiguous()
+    n = len(mats)
+    ys = outs if outs is not None else [torch.empty(m.rows, dtype=torch.float32, device=m.buf.device) for m in mats]
+    res = residuals if residuals is not None else [None] * n
+    jobs = (_lib.GemvJob * max(n, 1))()
+    for j, m in enumerate(mats):
+        jobs[j].fmt, jobs[j].d_w, jobs[j].rows = m.fmt, m.buf.data_ptr(), m.rows
+        jobs[j].d_y = ys[j].data_ptr()
+        jobs[j].d_res = res[j].data_ptr() if res[j] is not None else None
+    _lib.check(lib.dq_gemv_group_f32(jobs, n, mats[0].cols if n else 0, _ptr(x), _stream()), "dq_gemv_group_f32")
+    return ys
 
 
 def gemm_workspace(mat, n_tok):

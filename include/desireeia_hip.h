@@ -116,6 +116,14 @@ typedef struct {
 int dq_gemv_group(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* d_xq, const float* d_xscale,
                   const int32_t* d_xsum, void* stream);
 
+/* The same GEMVs on the fp32 activation d_x [cols]: every workgroup quantizes
+ * x in-kernel with the format's reference quantizer (the integers, scales and
+ * sums of dq_quantize_act, so the results are bit-identical to dq_quantize_act
+ * followed by dq_gemv / dq_gemv_group), saving the separate quantize launch.
+ * In the group form every format may be mixed. cols <= 49152; larger: -2. */
+int dq_gemv_f32(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, float* d_y, void* stream);
+int dq_gemv_group_f32(const dq_gemv_job_t* jobs, size_t n, size_t cols, const float* d_x, void* stream);
+
 /* Prefill GEMM y[n_tok][rows] = x[n_tok][cols] W^T for Q4_K and Q6_K, with the
  * semantics of matmul_q4_k_batch / matmul_q6_k_batch for n_tok >= 4 (the
  * i8_gemm path, core/matmul.cpp:2090-2125 -> :806-845): per-32 activation
@@ -152,7 +160,7 @@ int dq_kv_write(const float* d_k, const float* d_v, uint32_t n_head_kv, uint32_t
  * positions [cc_start, pos], query head h reads KV head h / (n_head /
  * n_head_kv), scores scaled by 1/sqrt(hd), softmax, out [n_head][hd] fp32.
  * hd = 128 and n_head / n_head_kv in {1, 2, 4, 8}; other shapes: -2.
- * d_work holds dq_attn_workspace_bytes(n_ctx) bytes of split partials
+ * d_work holds dq_attn_workspace_bytes(n_ctx) bytes of per-tile partials
  * (calls sharing a workspace must not overlap). d_pos as for dq_kv_write. */
 int dq_attn_workspace_bytes(uint32_t n_head, uint32_t n_head_kv, uint32_t hd, uint32_t n_ctx, size_t* bytes);
 int dq_attn_decode_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head, uint32_t n_head_kv,
@@ -165,6 +173,17 @@ int dq_attn_decode_q8_act(const float* d_q, const void* d_kc, const void* d_vc, 
                           uint32_t n_head_kv, uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos,
                           uint32_t n_ctx, float* d_out, int8_t* d_oq, float* d_oscale, int32_t* d_oisum,
                           void* d_work, size_t work_bytes, void* stream);
+/* The decode step of the layer in two launches (tiles, merge): NeoX
+ * RoPE (table d_rope, NULL = none; n_rot must equal hd, else -2) of the raw
+ * query q and key k, the Q8_0 rows of k and v written at `pos` (bit-exact
+ * kv_quantize_row of the rotated k and of v, as dq_rope_kv_write), then the
+ * attention as dq_attn_decode_q8; the output also quantized per 256 when
+ * d_oq != NULL. q, k, v: the Q/K/V projections of the new token. */
+int dq_attn_rope_kv_decode(const float* d_q, const float* d_k, const float* d_v, const float* d_rope,
+                           uint32_t n_rot, void* d_kc, void* d_vc, uint32_t n_head, uint32_t n_head_kv, uint32_t hd,
+                           uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx, float* d_out,
+                           int8_t* d_oq, float* d_oscale, int32_t* d_oisum, void* d_work, size_t work_bytes,
+                           void* stream);
 
 /* ------------------------------------------------------- decoder layer */
 

@@ -70,7 +70,7 @@ CASES = [
     (8, 8, 513, 0),      # MHA
     (16, 8, 2000, 0),    # GQA 2
     (64, 8, 3000, 0),    # GQA 8
-    (32, 8, 20000, 0),   # long context: several tiles per split
+    (32, 8, 20000, 0),   # long context: 313 tiles merged
 ]
 
 
@@ -156,6 +156,62 @@ def test_attention_quantized_output(gpu, orc):
         torch.cuda.synchronize()
         o = out.cpu().numpy()
         assert rel(o, orc.attn_decode(q, kc, vc, n_head, n_kv, HD, 0, p)) <= TOL
+        wq, wd, wi = orc.quantize_q8k_rep(o)
+        assert np.array_equal(act.q.cpu().numpy(), wq)
+        assert np.array_equal(act.scale.cpu().numpy(), wd)
+        assert np.array_equal(act.isum.cpu().numpy(), wi)
+
+
+@pytest.mark.parametrize("n_head,n_kv,pos,rope,quant", [
+    (32, 8, 4096, True, True),    # config 4's step
+    (32, 8, 0, True, True),       # the first token: the new row is the only key
+    (32, 8, 64, True, False),     # the new row starts a tile
+    (16, 16, 300, False, True),   # MHA, no RoPE: quantization falls back to a separate pass
+    (64, 8, 1000, True, True),    # GQA 8
+])
+def test_attention_rope_kv_fused(gpu, orc, n_head, n_kv, pos, rope, quant):
+    """dq_attn_rope_kv_decode: RoPE of the raw q and k, the new K/V rows at pos
+    (bit-exact: kv_quantize_row of the oracle's rotated k and of v), attention
+    over [0, pos] within 1e-3, the per-256 quantization of the output
+    bit-exact on the kernel's own float output; the prior rows untouched."""
+    print(f"fused attn n_head={n_head} n_kv={n_kv} pos={pos} rope={rope} quant={quant}", flush=True)
+    n_ctx = pos + 3
+    kc, vc = host_cache(orc, pos, n_kv, seed=pos + 3)
+    cache = device_cache(gpu, kc, vc, n_ctx, n_kv)
+    rng = np.random.default_rng(pos + 4)
+    q = rng.standard_normal(n_head * HD).astype(np.float32)
+    k = rng.standard_normal(n_kv * HD).astype(np.float32)
+    v = rng.standard_normal(n_kv * HD).astype(np.float32)
+    table = orc.rope_cache(HD, pos, 500000.0)
+    dq, dk, dv = (torch.from_numpy(a).to(gpu) for a in (q, k, v))
+    drope = torch.from_numpy(table).to(gpu) if rope else None
+    out = torch.empty(n_head * HD, dtype=torch.float32, device=gpu)
+    act = ops.empty_act((n_head * HD,), ops.ACT_Q8K_REP, gpu) if quant else None
+    work = ops.attn_workspace(n_head, n_kv, HD, n_ctx, gpu)
+    lib = _lib.load()
+    for _ in range(2):  # the same step twice on one workspace
+        _lib.check(lib.dq_attn_rope_kv_decode(ops._ptr(dq), ops._ptr(dk), ops._ptr(dv), ops._ptr(drope), HD,
+                                              ops._ptr(cache.k), ops._ptr(cache.v), n_head, n_kv, HD, 0, pos, None,
+                                              n_ctx, ops._ptr(out), ops._ptr(act.q) if quant else None,
+                                              ops._ptr(act.scale) if quant else None,
+                                              ops._ptr(act.isum) if quant else None, ops._ptr(work), work.numel(),
+                                              ops._stream()), "dq_attn_rope_kv_decode")
+    torch.cuda.synchronize()
+    qr, kr = q.copy(), k.copy()
+    if rope:
+        for h in range(n_head):
+            qr[h * HD:(h + 1) * HD] = orc.rope_neox(qr[h * HD:(h + 1) * HD], HD, table)
+        for h in range(n_kv):
+            kr[h * HD:(h + 1) * HD] = orc.rope_neox(kr[h * HD:(h + 1) * HD], HD, table)
+    pb = n_kv * HD // 32 * 34
+    gk, gv = cache.k.cpu().numpy(), cache.v.cpu().numpy()
+    assert np.array_equal(gk[pos * pb:(pos + 1) * pb], orc.kv_quantize_row(kr))
+    assert np.array_equal(gv[pos * pb:(pos + 1) * pb], orc.kv_quantize_row(v))
+    assert np.array_equal(gk[:pos * pb], kc) and np.array_equal(gv[:pos * pb], vc)
+    o = out.cpu().numpy()
+    want = orc.attn_decode(qr, gk, gv, n_head, n_kv, HD, 0, pos)
+    assert rel(o, want) <= TOL
+    if quant:
         wq, wd, wi = orc.quantize_q8k_rep(o)
         assert np.array_equal(act.q.cpu().numpy(), wq)
         assert np.array_equal(act.scale.cpu().numpy(), wd)

@@ -130,3 +130,34 @@ def test_gemv_group_residual_and_errors(gpu, orc):
     assert bool((sentinel == 7.0).all())
     with pytest.raises(_lib.DqError, match="NOT_SUPPORTED"):
         ops.gemv_group([a] * 5, act)
+
+
+@pytest.mark.parametrize("qtype,rows,cols", [(synth.Q4_K, 14336, 4096), (synth.Q4_K, 4096, 14336),
+                                             (synth.Q6_K, 4096, 14336), (synth.Q8_0, 4096, 4096),
+                                             (synth.Q4_0, 333, 4160), (synth.Q4_K, 5, 49152)])
+def test_gemv_f32_matches_quantize_then_gemv(gpu, qtype, rows, cols):
+    """dq_gemv_f32 (activation quantized in-kernel) is bit-identical to
+    dq_quantize_act + dq_gemv."""
+    print(f"gemv_f32 type={qtype} {rows}x{cols}", flush=True)
+    w = synth.gen_weights(qtype, rows, cols, seed=rows + cols + 1)
+    x = torch.from_numpy(synth.gen_act(cols, seed=cols + 2)).to(gpu)
+    m = ops.QuantMatrix.from_gguf(qtype, w, rows, cols)
+    fused = ops.matmul(m, x)
+    two = ops.gemv(m, ops.quantize_act(x, ops.act_kind_for(m.fmt)))
+    assert torch.equal(fused, two)
+
+
+def test_gemv_group_f32_mixed_kinds(gpu, orc):
+    """The fp32 group form mixes the per-32 and per-256 kinds (each launch
+    quantizes for its own format) and keeps residuals; too wide: -2."""
+    cols = 1024
+    x = torch.from_numpy(synth.gen_act(cols, seed=8)).to(gpu)
+    specs = [(synth.Q4_K, 300), (synth.Q8_0, 100), (synth.Q6_K, 64), (synth.Q4_0, 7)]
+    mats = [ops.QuantMatrix.from_gguf(qt, synth.gen_weights(qt, r, cols, seed=r), r, cols) for qt, r in specs]
+    res = [torch.randn(m.rows, device=gpu) for m in mats]
+    ys = ops.matmul_group(mats, x, residuals=res)
+    for m, y, r in zip(mats, ys, res):
+        assert torch.equal(y, ops.matmul(m, x) + r)
+    wide = ops.QuantMatrix.from_gguf(synth.Q4_K, synth.gen_weights(synth.Q4_K, 2, 65536, seed=1), 2, 65536)
+    with pytest.raises(_lib.DqError, match="NOT_SUPPORTED"):
+        ops.matmul(wide, torch.zeros(65536, device=gpu))
