@@ -149,28 +149,52 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
     // registers under FUSE
     const int n_load = (FUSE && tile == n_tiles - 1) ? nv - 1 : nv;
 
-    // ---- K / V rows of the tile: issued first, staged after the query
+    // ---- query values of this wave's heads (FUSE: wave w takes heads w,
+    // w+NW) and the new row's RoPE pair, loaded before the tile so that
+    // waiting for them leaves the tile's loads in flight
+    constexpr int HPW = (HPK + NW - 1) / NW;
+    float ql[HPW], qhv[HPW], rc = 1.0f, rs = 0.0f;
+    if constexpr (FUSE) {
+#pragma unroll
+        for (int t = 0; t < HPW; ++t) {
+            const int h = min(wave + NW * t, HPK - 1);
+            const float* qh = A.q + (size_t)(kvh * HPK + h) * HD;
+            ql[t] = qh[lane];
+            qhv[t] = qh[lane + 64];
+        }
+        if (A.rope) {
+            rc = A.rope[2 * lane];
+            rs = A.rope[2 * lane + 1];
+        }
+    }
+    // ---- K / V rows of the tile: issued next, staged after the query
     uint32_t kr[STAGE_IT], vr[STAGE_IT];
     {
         const uint8_t* kb = A.kc + (size_t)p0 * A.pos_bytes + (size_t)kvh * RB;
         const uint8_t* vb = A.vc + (size_t)p0 * A.pos_bytes + (size_t)kvh * RB;
+        // unconditional loads (addresses clamped into the tile's first rows,
+        // which exist: p0 <= pos < n_ctx) so that all of them are in flight
+        // together; the values of slots past the tile are never staged
+        const int rmax = n_load > 0 ? n_load - 1 : 0;
 #pragma unroll
         for (int it = 0; it < STAGE_IT; ++it) {
-            const int i = tid + it * NT;
-            const int r = i / RBW, c = i % RBW;
-            const bool ok = i < TP * RBW && r < n_load;
-            kr[it] = ok ? *reinterpret_cast<const uint32_t*>(kb + (size_t)r * A.pos_bytes + 4 * c) : 0u;
-            vr[it] = ok ? *reinterpret_cast<const uint32_t*>(vb + (size_t)r * A.pos_bytes + 4 * c) : 0u;
+            const int i = min(tid + it * NT, TP * RBW - 1);
+            const int r = min(i / RBW, rmax), c = i % RBW;
+            kr[it] = *reinterpret_cast<const uint32_t*>(kb + (size_t)r * A.pos_bytes + 4 * c);
+            vr[it] = *reinterpret_cast<const uint32_t*>(vb + (size_t)r * A.pos_bytes + 4 * c);
         }
     }
     // ---- query of the HPK heads (rotated under FUSE: wave w takes heads w, w+NW)
     if constexpr (FUSE) {
-        for (int h = wave; h < HPK; h += NW) {
-            const float* qh = A.q + (size_t)(kvh * HPK + h) * HD;
-            float lo = qh[lane], hi = qh[lane + 64];
-            if (A.rope) dq_rope_pair(lo, hi, A.rope, lane);
-            qt[lane][h] = lo;
-            qt[lane + 64][h] = hi;
+#pragma unroll
+        for (int t = 0; t < HPW; ++t) {
+            const int h = wave + NW * t;
+            if (h < HPK) {
+                // NeoX rotation of the pair (j, j + 64) (dq_rope_pair)
+                const float a = ql[t], b = qhv[t];
+                qt[lane][h] = A.rope ? a * rc - b * rs : a;
+                qt[lane + 64][h] = A.rope ? a * rs + b * rc : b;
+            }
         }
     } else {
         for (int i = tid; i < HPK * HD; i += NT) qt[i % HD][i / HD] = A.q[(size_t)(kvh * HPK + i / HD) * HD + i % HD];

@@ -129,6 +129,18 @@ __device__ __forceinline__ dq_u32x4 dq_ld16_stream(const void* p) {
 }
 
 // DPP move of a float (gfx9 dpp_ctrl encodings; all rows and banks enabled).
+// Workgroup barrier for LDS rings filled by global_load_lds: waits for this
+// wave's LDS reads (lgkmcnt 0; gfx9 s_waitcnt encoding, vmcnt and expcnt at
+// their maximum) and leaves the vector memory counter alone. __syncthreads
+// adds a fence that waits for every outstanding global load, which would
+// also wait for the DMAs of the ring stages still in flight; callers wait for
+// the DMAs they need with an explicit vmcnt before this barrier.
+__device__ __forceinline__ void dq_lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dq_dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));

@@ -38,6 +38,17 @@ __device__ __forceinline__ int q4k_min(int j, uint32_t w0, uint32_t w1, uint32_t
     return (int)((((w2 >> sh) & 0xFF) >> 4) | (((w1 >> sh) & 0xFF) >> 6 << 4));
 }
 
+// The 8 values fp16(-dmin * m_j) of a Q4_K super-block header hd (d and dmin
+// in hd.x, the 12 scale bytes in hd.y..hd.w): the weight side of the
+// super-block's min term as one 8-wide MFMA K slice. Zeros when !ok.
+__device__ __forceinline__ h8 q4k_neg_mins(const dq_u32x4& hd, bool ok) {
+    const float dmin = dq_h2f((uint16_t)(hd.x >> 16));
+    _Float16 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (_Float16)(ok ? -(dmin * (float)q4k_min(i, hd.y, hd.z, hd.w)) : 0.0f);
+    return *reinterpret_cast<const h8*>(v);
+}
+
 
 namespace {
 

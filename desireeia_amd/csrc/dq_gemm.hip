@@ -8,7 +8,9 @@
 // operands enter CDNA4's fp16 MFMA pre-scaled:
 //     A[t][k] = fp16(q_x * dx)            (the same integers and scale)
 //     B[k][r] = fp16(a_rb * q_w)          (a = d*sc; Q6_K: d*sc16, q-32)
-// and the Q4_K min term is K/32 extra columns A = fp16(sx), B = fp16(-m).
+// and the Q4_K min term is one extra 16-wide MFMA slice per super-block: the
+// 8 block sums A = fp16(sx) (a token-contiguous plane) against B =
+// fp16(-dmin*m_j) from the super-block header.
 // Accumulation is fp32. The only difference from the reference is the fp16
 // rounding of the two operands (2^-11 relative), which moves the result by
 // ~3e-4 relative - inside the 4e-3 tolerance.
@@ -18,41 +20,47 @@
 // which on CDNA4 (16 fp32 lanes/clk/SIMD vs ~1024 int8 MAC/clk/SIMD) caps the
 // int8 path below half its peak; pre-scaled fp16 operands need no epilogue.
 //
-// Tiling: 128 (tokens) x 128 (weight rows) x 64 (K) per 256-thread workgroup,
-// 4 waves of 64x64 (2x2 v_mfma_f32_32x32x16_f16 tiles), LDS double-buffered
-// with XOR-swizzled 16-byte chunks (no bank conflicts on fragment reads); the
-// weight tile is dequantized from the packed layout by the loader threads
-// while the MFMAs of the previous step run. Q6_K: K is permuted to the packed
-// item order (both operands, see dq_quantize_act_f16), so a 64-column K step
-// is exactly one 64-weight item.
+// Tiling: 128 (tokens) x BN (weight rows, 256 or 128) x 64 (K) per workgroup
+// of BN/32 waves, each 64x64 (2x2 v_mfma_f32_32x32x16_f16 tiles). A 3-stage
+// LDS ring filled by global_load_lds DMA holds per step the activation tile
+// (XOR-swizzled 16-byte chunks: no bank conflicts on fragment reads), the
+// super-block's block sums and the raw packed weight bytes; each wave turns
+// its rows' bytes into fp16 fragments in registers. Q6_K: K is permuted to the
+// packed item order (both operands, see dq_quantize_act_f16), so a 64-column
+// K step is exactly one 64-weight item.
 #include "dq_common.h"
 #include "dq_f16.h"
 
 namespace {
 
 
-constexpr int BM = 128, BK = 64, NS = 3;  // tile rows (tokens), K per step, ring stages
+constexpr int BM = 128, BK = 64;  // tile rows (tokens), K per step
+
+enum BKind { B_Q4K = 0, B_Q6K = 1 };
 
 // ------------------------------------------------------------ LDS layout --
 // Ring of NS stages, each holding one K step of both operands:
 //   A: BM rows x 8 chunks of 16 bytes (fp16), chunk c of row r at slot
 //      r*8 + (c ^ (r & 7)) - XOR swizzle: a wave's 16-byte fragment reads (32
 //      rows, one logical chunk) hit all banks.
+//   Q4_K only: the 8 min columns of the step's super-block (16 bytes per row).
 //   B: the raw bytes of the weight tile, format specific:
 //      Q4_K: P0[BN][16] P1[BN][16] H[BN][16]    (qs sub-planes, block header)
 //      Q6_K: QA[BN][16] QB[BN][16] QH[BN][16] S[BN][4] D[BN][4] (fp16 in the low half)
 // Every stage is filled by global_load_lds (direct global -> LDS DMA, 16, 4 or
 // 2 bytes per lane; lane i of a wave writes at base + i*16 for 16-byte loads and
-// at base + i*4 for the dword and sub-dword forms).
-template <int BN>
+// at base + i*4 for the dword and sub-dword forms). Three stages: two steps'
+// DMAs in flight while one is computed.
+template <int BN, int KIND>
 struct Ring {
+    static constexpr int NS = 3;
     static constexpr int A_BYTES = BM * BK * 2;
+    static constexpr int MIN_BYTES = KIND == B_Q4K ? BM * 16 : 0;
+    static constexpr int B_OFF = A_BYTES + MIN_BYTES;
     static constexpr int B_BYTES = BN * 64;
-    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int STAGE = B_OFF + B_BYTES;
     static constexpr int BYTES = NS * STAGE;
 };
-
-enum BKind { B_Q4K = 0, B_Q6K = 1 };
 
 #define DQ_LDS_PTR(p) reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(p))
 template <int SIZE>
@@ -72,25 +80,19 @@ __device__ __forceinline__ void lds_dma<2>(const void* g, uint8_t* b) {
 
 // s_waitcnt vmcnt(n), other counters untouched (gfx9 encoding: vmcnt in
 // bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
-__device__ __forceinline__ void wait_vm(int n) {
-#define DQ_WAIT_CASE(k) \
-    case k: __builtin_amdgcn_s_waitcnt(((k) & 15) | (((k) >> 4) << 14) | (7 << 4) | (15 << 8)); break;
-    switch (n) {
-        DQ_WAIT_CASE(0) DQ_WAIT_CASE(1) DQ_WAIT_CASE(2) DQ_WAIT_CASE(3) DQ_WAIT_CASE(4) DQ_WAIT_CASE(5)
-        DQ_WAIT_CASE(6) DQ_WAIT_CASE(7) DQ_WAIT_CASE(8) DQ_WAIT_CASE(9) DQ_WAIT_CASE(10) DQ_WAIT_CASE(11)
-        DQ_WAIT_CASE(12) DQ_WAIT_CASE(13) DQ_WAIT_CASE(14) DQ_WAIT_CASE(15)
-        default: __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); break;
-    }
-#undef DQ_WAIT_CASE
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
 struct GemmArgs {
     const uint8_t* w;       // packed weights
     DqLayout L;
     const _Float16* A;      // activations [M][lda]
-    const _Float16* mins;   // Q4_K min plane [N][ld_min] (fp16 -dmin*m), or null
+    const _Float16* minp;   // Q4_K: activation block sums, [K/256][M][8] (token-contiguous per super-block)
     const float* inv;       // per token: 1/s of its activation row
-    int lda, ld_min, M, N, K;
+    int lda, M, N, K;
     int m0, n0;
 };
 
@@ -98,20 +100,21 @@ struct GemmArgs {
 // `stage`. Every wave issues the same, compile-time number of load
 // instructions (stage_loads()), so one s_waitcnt vmcnt covers a stage: blocks
 // of 64 slots are dealt to the NW waves, and where a region has fewer blocks
-// than waves two waves load the same block (identical bytes to the same LDS
-// address).
+// than waves several waves load the same block (identical bytes to the same
+// LDS address).
 template <int BN, int KIND>
 constexpr int stage_loads() {
     constexpr int NW = BN / 32;
-    return BM * 8 / 64 / NW + (KIND == B_Q4K ? 2 : 3);
+    return BM * 8 / 64 / NW + (KIND == B_Q4K ? 3 : 3);
 }
 
 template <int BN, int KIND>
-__device__ __forceinline__ void issue_stage(const GemmArgs& g, uint8_t* ring, int stage, int st, int main_steps,
-                                            int wave, int lane) {
+__device__ __forceinline__ void issue_stage(const GemmArgs& g, uint8_t* ring, int stage, int st, int wave,
+                                            int lane) {
     constexpr int NW = BN / 32;      // waves per workgroup
     constexpr int HB = BN / 64;      // 64-slot blocks per [BN] region (= NW/2)
-    uint8_t* base = ring + stage * Ring<BN>::STAGE;
+    using R = Ring<BN, KIND>;
+    uint8_t* base = ring + stage * R::STAGE;
     // A: BM*8 slots of 16 bytes
     {
         const int kcol = st * BK;
@@ -124,8 +127,13 @@ __device__ __forceinline__ void issue_stage(const GemmArgs& g, uint8_t* ring, in
             lds_dma<16>(g.A + (size_t)m * g.lda + kcol + 8 * c, base + jj * 64 * 16);
         }
     }
-    uint8_t* bb = base + Ring<BN>::A_BYTES;
+    uint8_t* bb = base + R::B_OFF;
     if constexpr (KIND == B_Q4K) {
+        {   // block sums of super-block st/4 (16 contiguous bytes per token): 2
+            // blocks of 64 rows, block wave % 2
+            const int blk = wave & 1, m = min(g.m0 + blk * 64 + lane, g.M - 1);
+            lds_dma<16>(g.minp + ((size_t)(st >> 2) * g.M + m) * 8, base + R::A_BYTES + blk * 64 * 16);
+        }
         {   // P0/P1: 2*HB = NW blocks, one per wave
             const int region = wave / HB, n = (wave % HB) * 64 + lane;
             const size_t r = (size_t)min(g.n0 + n, g.N - 1);
@@ -167,54 +175,76 @@ __device__ __forceinline__ void issue_stage(const GemmArgs& g, uint8_t* ring, in
 
 __device__ __forceinline__ const h8& lds_h8(const uint8_t* p) { return *reinterpret_cast<const h8*>(p); }
 
-// B fragments of one ring stage for this lane: bf[kk][j], kk = 16-wide K
-// slice, j = 32-row n block. Lane l feeds row n = wn*64 + j*32 + l%32 with the
-// 8 K values kk*16 + 8*(l/32) .. +7.
+// Raw weight bytes of one ring stage that this lane's B fragments need: for
+// each of its two 32-row blocks j, lane half h's 8 bytes of the two quant
+// sub-planes (Q4_K: P0/P1; Q6_K: QA/QB plus QH) and the row's scales.
+struct BRaw {
+    dq_u32x2 q0[2], q1[2], q2[2];  // Q4_K: P0, P1 (q2 unused); Q6_K: QA, QB, QH
+    dq_u32x4 hd[2];                // Q4_K: super-block header; Q6_K: .x = 4 int8 scales, .y = d (low half)
+};
+
 template <int BN, int KIND>
-__device__ __forceinline__ void b_fragments(const uint8_t* bb, int st, int wn, int lane, int n_valid, h8 (&bf)[4][2]) {
+__device__ __forceinline__ void b_raw(const uint8_t* bb, int wn, int lane, BRaw& r) {
     const int h = lane >> 5;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int n = wn * 64 + j * 32 + (lane & 31);
-        const bool ok = n < n_valid;
+        r.q0[j] = *reinterpret_cast<const dq_u32x2*>(bb + n * 16 + 8 * h);
+        r.q1[j] = *reinterpret_cast<const dq_u32x2*>(bb + BN * 16 + n * 16 + 8 * h);
         if constexpr (KIND == B_Q4K) {
-            const dq_u32x2 p0 = *reinterpret_cast<const dq_u32x2*>(bb + n * 16 + 8 * h);
-            const dq_u32x2 p1 = *reinterpret_cast<const dq_u32x2*>(bb + BN * 16 + n * 16 + 8 * h);
-            const dq_u32x4 hd = *reinterpret_cast<const dq_u32x4*>(bb + 2 * BN * 16 + n * 16);
-            const int g = st & 3;
+            r.hd[j] = *reinterpret_cast<const dq_u32x4*>(bb + 2 * BN * 16 + n * 16);
+        } else {
+            r.q2[j] = *reinterpret_cast<const dq_u32x2*>(bb + 2 * BN * 16 + n * 16 + 8 * h);
+            r.hd[j].x = *reinterpret_cast<const uint32_t*>(bb + 3 * BN * 16 + n * 4);
+            r.hd[j].y = *reinterpret_cast<const uint32_t*>(bb + 3 * BN * 16 + BN * 4 + n * 4);
+        }
+    }
+}
+
+// B fragments of a step of phase G (= st % 4, the item of the super-block)
+// from the raw bytes: bf[kk][j], kk = 16-wide K slice, j = 32-row n block.
+// Lane l feeds row n = wn*64 + j*32 + l%32 with the 8 K values kk*16 +
+// 8*(l/32) .. +7. Rows past N hold the clamped last row's bytes (finite
+// values whose outputs are never stored). Q4_K, G == 3: bm[j] = the
+// super-block's min slice (q4k_neg_mins); the activation side is zero for
+// lane half 1.
+template <int KIND>
+__device__ __forceinline__ void b_dequant(const BRaw& r, int G, h8 (&bf)[4][2], h8 (&bm)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        if constexpr (KIND == B_Q4K) {
+            const dq_u32x4 hd = r.hd[j];
             const float d = dq_h2f((uint16_t)(hd.x & 0xFFFF));
-            const _Float16 a0 = (_Float16)(ok ? d * (float)q4k_scale(2 * g, hd.y, hd.z, hd.w) : 0.0f);
-            const _Float16 a1 = (_Float16)(ok ? d * (float)q4k_scale(2 * g + 1, hd.y, hd.z, hd.w) : 0.0f);
+            const _Float16 a0 = (_Float16)(d * (float)q4k_scale(2 * G, hd.y, hd.z, hd.w));
+            const _Float16 a1 = (_Float16)(d * (float)q4k_scale(2 * G + 1, hd.y, hd.z, hd.w));
             const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
             const h2 v0 = {a0, a0}, v1 = {a1, a1};
             uint32_t t[4];
             // kk 0: P0 low nibbles, 1: P1 low, 2: P0 high, 3: P1 high
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                const dq_u32x2 src = (kk & 1) ? p1 : p0;
+                const dq_u32x2 src = (kk & 1) ? r.q1[j] : r.q0[j];
                 const uint32_t m0 = kk < 2 ? (src.x & 0x0F0F0F0Fu) : ((src.x >> 4) & 0x0F0F0F0Fu);
                 const uint32_t m1 = kk < 2 ? (src.y & 0x0F0F0F0Fu) : ((src.y >> 4) & 0x0F0F0F0Fu);
                 bytes_to_h2(m0, bias, kk < 2 ? v0 : v1, &t[0]);
                 bytes_to_h2(m1, bias, kk < 2 ? v0 : v1, &t[2]);
                 bf[kk][j] = __builtin_bit_cast(h8, dq_u32x4{t[0], t[1], t[2], t[3]});
             }
+            if (G == 3) bm[j] = q4k_neg_mins(hd, true);
         } else {
-            const dq_u32x2 qa = *reinterpret_cast<const dq_u32x2*>(bb + n * 16 + 8 * h);
-            const dq_u32x2 qb = *reinterpret_cast<const dq_u32x2*>(bb + BN * 16 + n * 16 + 8 * h);
-            const dq_u32x2 qh = *reinterpret_cast<const dq_u32x2*>(bb + 2 * BN * 16 + n * 16 + 8 * h);
-            const uint32_t sc = *reinterpret_cast<const uint32_t*>(bb + 3 * BN * 16 + n * 4);
-            const float d = dq_h2f(*reinterpret_cast<const uint16_t*>(bb + 3 * BN * 16 + BN * 4 + n * 4));
+            const uint32_t sc = r.hd[j].x;
+            const float d = dq_h2f((uint16_t)(r.hd[j].y & 0xFFFF));
             const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};  // 1024 + 32
             uint32_t t[4];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
-                const _Float16 a = (_Float16)(ok ? d * (float)(int8_t)((sc >> (8 * kk)) & 0xFF) : 0.0f);
+                const _Float16 a = (_Float16)(d * (float)(int8_t)((sc >> (8 * kk)) & 0xFF));
                 const h2 va = {a, a};
-                const dq_u32x2 lo = (kk & 1) ? qb : qa;
+                const dq_u32x2 lo = (kk & 1) ? r.q1[j] : r.q0[j];
 #pragma unroll
                 for (int wd = 0; wd < 2; ++wd) {
                     const uint32_t l4 = kk < 2 ? (lo[wd] & 0x0F0F0F0Fu) : ((lo[wd] >> 4) & 0x0F0F0F0Fu);
-                    const uint32_t v6 = l4 | (((qh[wd] >> (2 * kk)) & 0x03030303u) << 4);
+                    const uint32_t v6 = l4 | (((r.q2[j][wd] >> (2 * kk)) & 0x03030303u) << 4);
                     bytes_to_h2(v6, bias, va, &t[2 * wd]);
                 }
                 bf[kk][j] = __builtin_bit_cast(h8, dq_u32x4{t[0], t[1], t[2], t[3]});
@@ -223,79 +253,77 @@ __device__ __forceinline__ void b_fragments(const uint8_t* bb, int st, int wn, i
     }
 }
 
-// K steps [s0, s1): fill NS-1 stages, then per step: wait for the oldest
-// stage, barrier, issue the DMA NS-1 steps ahead (steps past the end re-issue
-// the last one, so every wave issues the same count per stage), run the MFMAs
-// of the current stage.
+// One K step st (phase G = st % 4, the item of the super-block) in ring
+// stage `stage`: wait until the stage has landed (NS-2 later stages may
+// still be in flight), barrier (every wave's DMAs visible, step st-1
+// retired), DMA of step st+NS-1 into the stage of st-1 (past the end: the
+// last step again, so every wave issues the same count per stage), then the
+// weight fragments (LDS bytes -> fp16 in registers) and the MFMAs; at the
+// last item of a super-block (Q4_K) also its min term.
 template <int BN, int KIND>
-__device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* ring, int s0, int s1, int main_steps,
+__device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* ring, int st, int stage, int s1,
                                           f16v (&acc)[2][2], int wave, int lane) {
-    if (s0 >= s1) return;
+    const int G = st & 3;
+    using R = Ring<BN, KIND>;
+    constexpr int NS = R::NS;
     constexpr int PER = stage_loads<BN, KIND>();
     const int wm = wave & 1, wn = wave >> 1;
-    const int n_valid = g.N - g.n0;
+    wait_vm<(NS - 2) * PER>();
+    dq_lds_barrier();
+    issue_stage<BN, KIND>(g, ring, stage == 0 ? NS - 1 : stage - 1, min(st + NS - 1, s1 - 1), wave, lane);
+    const uint8_t* base = ring + stage * R::STAGE;
+    BRaw raw;
+    b_raw<BN, KIND>(base + R::B_OFF, wn, lane, raw);
+    h8 bf[4][2], bm[2];
+    b_dequant<KIND>(raw, G, bf, bm);
 #pragma unroll
-    for (int p = 0; p < NS - 1; ++p) issue_stage<BN, KIND>(g, ring, p, min(s0 + p, s1 - 1), main_steps, wave, lane);
-    for (int st = s0; st < s1; ++st) {
-        const int stage = (st - s0) % NS;
-        // this wave's DMAs of `stage` are done (NS-2 stages still in flight);
-        // the barrier makes every wave's DMAs visible and retires step st-1
-        wait_vm((NS - 2) * PER);
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        issue_stage<BN, KIND>(g, ring, (st - s0 + NS - 1) % NS, min(st + NS - 1, s1 - 1), main_steps, wave, lane);
-        const uint8_t* base = ring + stage * Ring<BN>::STAGE;
-        h8 bf[4][2];
-        b_fragments<BN, KIND>(base + Ring<BN>::A_BYTES, st, wn, lane, n_valid, bf);
+    for (int kk = 0; kk < 4; ++kk) {
+        h8 af[2];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            h8 af[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int r = wm * 64 + i * 32 + (lane & 31);
-                af[i] = lds_h8(base + (r * 8 + ((2 * kk + (lane >> 5)) ^ (r & 7))) * 16);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[kk][j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < 2; ++i) {
+            const int r = wm * 64 + i * 32 + (lane & 31);
+            af[i] = lds_h8(base + (r * 8 + ((2 * kk + (lane >> 5)) ^ (r & 7))) * 16);
         }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[kk][j], acc[i][j], 0, 0, 0);
     }
-    wait_vm(0);  // drain the DMAs issued past the end
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    if (KIND == B_Q4K && G == 3) {  // the super-block's min term
+        const h8 zero = {};
+        h8 am[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const h8 v = lds_h8(base + R::A_BYTES + (wm * 64 + i * 32 + (lane & 31)) * 16);
+            am[i] = (lane >> 5) == 0 ? v : zero;
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[i], bm[j], acc[i][j], 0, 0, 0);
+    }
 }
 
-// Q4_K min term, steps [s0, s1) of the min columns: A = fp16 block sums
-// (activation columns K + ...), B = fp16(-dmin*m) from the min plane. Small
-// (K/32 columns), so fragments come straight from global memory.
-__device__ __forceinline__ void min_steps(const GemmArgs& g, int s0, int s1, f16v (&acc)[2][2], int wave, int lane) {
-    const int wm = wave & 1, wn = wave >> 1, h = lane >> 5;
-    for (int e = s0; e < s1; ++e) {
-        const int col = e * BK;
-        h8 af[4][2], bf[4][2];
+// K steps [s0, s1), s0 and s1 multiples of 4 (whole super-blocks, so every
+// super-block's min term falls in one split): NS-1 stages in flight before
+// the first step, then one step at a time.
+template <int BN, int KIND>
+__device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* ring, int s0, int s1, f16v (&acc)[2][2],
+                                          int wave, int lane) {
+    using R = Ring<BN, KIND>;
+    constexpr int NS = R::NS;
+    if (s0 >= s1) return;
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int m = min(g.m0 + wm * 64 + i * 32 + (lane & 31), g.M - 1);
-                af[kk][i] = *reinterpret_cast<const h8*>(g.A + (size_t)m * g.lda + g.K + col + kk * 16 + 8 * h);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int n = min(g.n0 + wn * 64 + j * 32 + (lane & 31), g.N - 1);
-                bf[kk][j] = *reinterpret_cast<const h8*>(g.mins + (size_t)n * g.ld_min + col + kk * 16 + 8 * h);
-            }
-        }
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk][i], bf[kk][j], acc[i][j], 0, 0, 0);
+    for (int p = 0; p < NS - 1; ++p) issue_stage<BN, KIND>(g, ring, p, min(s0 + p, s1 - 1), wave, lane);
+    int stage = 0;
+    for (int st = s0; st < s1; ++st) {
+        gemm_step<BN, KIND>(g, ring, st, stage, s1, acc, wave, lane);
+        stage = stage + 1 == NS ? 0 : stage + 1;
     }
+    wait_vm<0>();  // drain the DMAs issued past the end
+    dq_lds_barrier();
 }
 
 // Tile index -> (m block, n block): tiles are ordered m-major and handed to
@@ -309,10 +337,13 @@ __device__ __forceinline__ void tile_of(int id, int mb, int nb, int* m_blk, int*
     *n_blk = t % nb;
 }
 
+// Register budget of two waves per SIMD (256 per lane): the wide tile runs
+// one 8-wave workgroup per CU; the narrow one (4 waves) one or two.
 template <int FMT, int BN>
-__global__ __launch_bounds__(2 * BN) void gemm_kernel(GemmArgs g, float* __restrict__ y, int main_steps,
-                                                      int total_steps, int steps_per_split, int atomic_out) {
-    __shared__ __align__(16) uint8_t ring[Ring<BN>::BYTES];
+__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(GemmArgs g, float* __restrict__ y, int steps,
+                                                      int steps_per_split, int atomic_out) {
+    constexpr int KIND = FMT == DQ_FMT_Q4_K ? B_Q4K : B_Q6K;
+    __shared__ __align__(16) uint8_t ring[Ring<BN, KIND>::BYTES];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -322,7 +353,7 @@ __global__ __launch_bounds__(2 * BN) void gemm_kernel(GemmArgs g, float* __restr
     g.n0 = n_blk * BN;
     g.m0 = m_blk * BM;
     const int s0 = blockIdx.z * steps_per_split;
-    const int s1 = min(total_steps, s0 + steps_per_split);
+    const int s1 = min(steps, s0 + steps_per_split);
 
     f16v acc[2][2];
 #pragma unroll
@@ -332,14 +363,18 @@ __global__ __launch_bounds__(2 * BN) void gemm_kernel(GemmArgs g, float* __restr
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    if constexpr (FMT == DQ_FMT_Q4_K) {
-        run_steps<BN, B_Q4K>(g, ring, s0, min(s1, main_steps), main_steps, acc, wave, lane);
-        min_steps(g, max(s0, main_steps) - main_steps, s1 - main_steps, acc, wave, lane);
-    } else {
-        run_steps<BN, B_Q6K>(g, ring, s0, s1, main_steps, acc, wave, lane);
-    }
+    run_steps<BN, KIND>(g, ring, s0, s1, acc, wave, lane);
 
-    // D layout of 32x32x16: lane l, register r -> n = l%32, m = (r/4)*8 + (l/32)*4 + r%4
+    // D layout of 32x32x16: lane l, register r -> n = l%32, m = (r/4)*8 + (l/32)*4 + r%4.
+    // The row factors 1/s are loaded together up front (unconditional loads
+    // of clamped rows; a load inside the store's branch would be waited for
+    // one at a time).
+    float inv[2][16];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            inv[i][r] = g.inv[min(g.m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), g.M - 1)];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -351,7 +386,7 @@ __global__ __launch_bounds__(2 * BN) void gemm_kernel(GemmArgs g, float* __restr
                 const int m = g.m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
                 if (m < g.M) {
                     float* dst = y + (size_t)m * g.N + n;
-                    const float v = acc[i][j][r] * g.inv[m];  // a power of two: exact
+                    const float v = acc[i][j][r] * inv[i][r];  // a power of two: exact
                     if (atomic_out) atomicAdd(dst, v);
                     else *dst = v;
                 }
@@ -359,54 +394,30 @@ __global__ __launch_bounds__(2 * BN) void gemm_kernel(GemmArgs g, float* __restr
         }
 }
 
-// Q4_K min plane for the min columns: mins[n][b] = fp16(-dmin*m_b) of row n,
-// zero for b >= cols/32 (rows padded to ld_min columns).
-__global__ __launch_bounds__(256) void min_plane_kernel(const uint8_t* __restrict__ w, DqLayout L, int N, int nblk,
-                                                        int ld_min, _Float16* __restrict__ out) {
-    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;  // one lane per (row, super-block slot)
-    const int per_row = ld_min / 8;
-    if (t >= (size_t)N * per_row) return;
-    const int n = (int)(t / per_row), s = (int)(t % per_row);
-    _Float16 v[8];
-    if (s * 8 < nblk) {
-        const dq_u32x4 hd = dq_ld16(w + L.s_off + (size_t)n * L.s_row + 16 * (size_t)s);
-        const float dmin = dq_h2f((uint16_t)(hd.x >> 16));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (_Float16)(-(dmin * (float)q4k_min(j, hd.y, hd.z, hd.w)));
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (_Float16)0.0f;
-    }
-    *reinterpret_cast<h8*>(out + (size_t)n * ld_min + 8 * s) = *reinterpret_cast<const h8*>(v);
-}
-
 // Activation quantizer for the GEMM: per 32-block the reference integers and
 // scale (core/i8gemm_impl.h:50-82), written as fp16(q*d*s) in K order `perm`
-// (0 natural, 1 Q6_K item order), plus fp16(exact float block sum * s) in the
-// min columns [cols, cols + n_min) (zero past cols/32), s the row's power-of-two
-// range scale (row_scale_kernel) and inv[t] = 1/s. One lane per block.
+// (0 natural, 1 Q6_K item order); with a min plane (Q4_K), fp16(exact float
+// block sum * s) of block b at minp[b/8][t][b%8]; s the row's power-of-two
+// range scale (row_scale_kernel) and inv[t] = 1/s. One lane per block (and,
+// with a min plane, one per block sum).
 __global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restrict__ x, int cols, int n_tok,
-                                                           _Float16* __restrict__ out, int lda, int with_min,
-                                                           int n_min, int perm, const float* __restrict__ rscale,
-                                                           float* __restrict__ inv) {
+                                                           _Float16* __restrict__ out, int lda,
+                                                           _Float16* __restrict__ minp, int perm,
+                                                           const float* __restrict__ rscale, float* __restrict__ inv) {
     const int nb = cols / 32;
     const int gb = blockIdx.x * blockDim.x + threadIdx.x;
-    const int stride = nb + (with_min ? n_min : 0);
+    const int stride = minp ? 2 * nb : nb;
     if (gb >= n_tok * stride) return;
     const int t = gb / stride, b = gb % stride;
     _Float16* o = out + (size_t)t * lda;
     const float sc = rscale[t];
     if (b == 0) inv[t] = 1.0f / sc;
-    if (b >= nb) {  // min column b - nb
+    if (b >= nb) {  // block sum of block b - nb
         const int mb = b - nb;
-        if (mb >= nb) {
-            o[cols + mb] = (_Float16)0.0f;
-            return;
-        }
         const float* p = x + (size_t)t * cols + 32 * mb;
         float fs = 0.0f;
         for (int i = 0; i < 32; ++i) fs += p[i];
-        o[cols + mb] = (_Float16)(fs * sc);
+        minp[((size_t)(mb / 8) * n_tok + t) * 8 + (mb % 8)] = (_Float16)(fs * sc);
         return;
     }
     const float* p = x + (size_t)t * cols + 32 * b;
@@ -469,33 +480,26 @@ int cus() {
 
 }  // namespace
 
-// Workspace of the GEMM: the activation [n_tok][lda] fp16 (lda = cols + the
-// min columns for Q4_K), the row scales s and 1/s [n_tok], then for Q4_K the
-// min plane [rows][n_min] fp16.
-static void gemm_act_shape(int fmt, size_t cols, int* lda, int* n_min) {
-    *n_min = fmt == DQ_FMT_Q4_K ? (int)((cols / 32 + BK - 1) / BK * BK) : 0;
-    *lda = (int)cols + *n_min;
+// Workspace of the GEMM: the activation [n_tok][cols] fp16, for Q4_K the
+// block sums [cols/256][n_tok][8] fp16, then the row scales s and 1/s [n_tok].
+static size_t act_bytes(size_t cols, size_t n_tok) { return dq_align256(n_tok * cols * 2); }
+static size_t min_bytes(int fmt, size_t cols, size_t n_tok) {
+    return fmt == DQ_FMT_Q4_K ? dq_align256(n_tok * (cols / 32) * 2) : 0;
 }
-
-static size_t act_bytes(int fmt, size_t cols, size_t n_tok) {
-    int lda, n_min;
-    gemm_act_shape(fmt, cols, &lda, &n_min);
-    return dq_align256(n_tok * (size_t)lda * 2);
+static size_t min_off(size_t cols, size_t n_tok) { return act_bytes(cols, n_tok); }
+static size_t scale_off(int fmt, size_t cols, size_t n_tok) {
+    return min_off(cols, n_tok) + min_bytes(fmt, cols, n_tok);
 }
-
-static size_t scale_off(int fmt, size_t cols, size_t n_tok) { return act_bytes(fmt, cols, n_tok); }
 static size_t inv_off(int fmt, size_t cols, size_t n_tok) {
     return scale_off(fmt, cols, n_tok) + dq_align256(n_tok * 4);
 }
-static size_t min_off(int fmt, size_t cols, size_t n_tok) { return inv_off(fmt, cols, n_tok) + dq_align256(n_tok * 4); }
 
 extern "C" int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t n_tok, size_t* bytes) {
+    (void)rows;
     if (!bytes) return DQ_ERR_INVALID_ARG;
     if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K) return DQ_ERR_NOT_SUPPORTED;
     if (cols % 256) return DQ_ERR_NOT_SUPPORTED;
-    int lda, n_min;
-    gemm_act_shape(fmt, cols, &lda, &n_min);
-    *bytes = min_off(fmt, cols, n_tok) + dq_align256(rows * (size_t)n_min * 2);
+    *bytes = inv_off(fmt, cols, n_tok) + dq_align256(n_tok * 4);
     return DQ_OK;
 }
 
@@ -505,39 +509,36 @@ extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_
     if (cols % 256 || cols > (1u << 24) || n_tok > (1u << 20)) return DQ_ERR_NOT_SUPPORTED;
     if (!d_x || !d_out) return DQ_ERR_INVALID_ARG;
     if (n_tok == 0) return DQ_OK;
-    int lda, n_min;
-    gemm_act_shape(fmt, cols, &lda, &n_min);
     const int nb = (int)cols / 32;
-    const size_t lanes = n_tok * (size_t)(nb + n_min);
+    const bool with_min = fmt == DQ_FMT_Q4_K;
+    const size_t lanes = n_tok * (size_t)(with_min ? 2 * nb : nb);
     uint8_t* base = (uint8_t*)d_out;
+    _Float16* minp = with_min ? (_Float16*)(base + min_off(cols, n_tok)) : nullptr;
     float* sc = (float*)(base + scale_off(fmt, cols, n_tok));
     float* inv = (float*)(base + inv_off(fmt, cols, n_tok));
     row_scale_kernel<<<(unsigned)n_tok, 256, 0, (hipStream_t)stream>>>(d_x, (int)cols, sc);
     quantize_f16_kernel<<<(unsigned)((lanes + 255) / 256), 256, 0, (hipStream_t)stream>>>(
-        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, lda, fmt == DQ_FMT_Q4_K, n_min, fmt == DQ_FMT_Q6_K, sc, inv);
+        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)cols, minp, fmt == DQ_FMT_Q6_K, sc, inv);
     return dq_launch_status();
 }
 
 template <int FMT, int BN>
-static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int main_steps, int total, float* d_y,
-                       hipStream_t s) {
+static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int steps, float* d_y, hipStream_t s) {
     const int mb = (int)((n_tok + BM - 1) / BM), nb = (int)((rows + BN - 1) / BN);
     // split K in two when the tile grid leaves CUs idle (two partials added
     // atomically into zeroed y: a+b == b+a, so the result is deterministic)
-    const int split = ((size_t)mb * nb * 2 <= (size_t)cus() && total >= 8) ? 2 : 1;
-    const int per = (total + split - 1) / split;
+    const int split = ((size_t)mb * nb * 2 <= (size_t)cus() && steps >= 8) ? 2 : 1;
+    const int per = (steps / 4 + split - 1) / split * 4;  // whole super-blocks per split
     if (split > 1) {
         const size_t n = rows * n_tok;
         zero_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(d_y, n);
     }
     const dim3 grid((unsigned)(mb * nb), 1, split);
-    gemm_kernel<FMT, BN><<<grid, 2 * BN, 0, s>>>(g, d_y, main_steps, total, per, split > 1);
+    gemm_kernel<FMT, BN><<<grid, 2 * BN, 0, s>>>(g, d_y, steps, per, split > 1);
     return dq_launch_status();
 }
 
-// GEMM on the workspace written by dq_quantize_act_f16 (its first part); for
-// Q4_K the min plane (second part of the workspace) is rebuilt from the
-// weights on every call.
+// GEMM on the workspace written by dq_quantize_act_f16.
 extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work,
                               size_t n_tok, float* d_y, void* stream) {
     DqLayout L;
@@ -546,36 +547,26 @@ extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols
     if (rows > (1u << 30) || n_tok > (1u << 20)) return DQ_ERR_NOT_SUPPORTED;
     if (rows == 0 || n_tok == 0) return DQ_OK;
     if (!d_w || !d_work || !d_y) return DQ_ERR_INVALID_ARG;
-    int lda, n_min;
-    gemm_act_shape(fmt, cols, &lda, &n_min);
     hipStream_t s = (hipStream_t)stream;
     GemmArgs g{};
     g.w = (const uint8_t*)d_w;
     g.L = L;
     g.A = (const _Float16*)d_work;
+    g.minp = (const _Float16*)((const uint8_t*)d_work + min_off(cols, n_tok));
     g.inv = (const float*)((const uint8_t*)d_work + inv_off(fmt, cols, n_tok));
-    g.lda = lda;
+    g.lda = (int)cols;
     g.M = (int)n_tok;
     g.N = (int)rows;
     g.K = (int)cols;
-    g.ld_min = n_min;
-    if (fmt == DQ_FMT_Q4_K) {
-        _Float16* mins = (_Float16*)((uint8_t*)d_work + min_off(fmt, cols, n_tok));
-        const size_t lanes = rows * (size_t)(n_min / 8);
-        min_plane_kernel<<<(unsigned)((lanes + 255) / 256), 256, 0, s>>>(g.w, L, (int)rows, (int)cols / 32, n_min,
-                                                                         mins);
-        g.mins = mins;
-    }
-    const int main_steps = (int)cols / BK;
-    const int total = main_steps + n_min / BK;
+    const int steps = (int)cols / BK;
     // wide tiles (less activation re-reading) when they still fill the CUs
     const size_t mb = (n_tok + BM - 1) / BM;
     const bool wide = mb * ((rows + 255) / 256) * 8 >= (size_t)cus() * 7;
     if (fmt == DQ_FMT_Q4_K)
-        return wide ? launch_gemm<DQ_FMT_Q4_K, 256>(g, rows, n_tok, main_steps, total, d_y, s)
-                    : launch_gemm<DQ_FMT_Q4_K, 128>(g, rows, n_tok, main_steps, total, d_y, s);
-    return wide ? launch_gemm<DQ_FMT_Q6_K, 256>(g, rows, n_tok, main_steps, total, d_y, s)
-                : launch_gemm<DQ_FMT_Q6_K, 128>(g, rows, n_tok, main_steps, total, d_y, s);
+        return wide ? launch_gemm<DQ_FMT_Q4_K, 256>(g, rows, n_tok, steps, d_y, s)
+                    : launch_gemm<DQ_FMT_Q4_K, 128>(g, rows, n_tok, steps, d_y, s);
+    return wide ? launch_gemm<DQ_FMT_Q6_K, 256>(g, rows, n_tok, steps, d_y, s)
+                : launch_gemm<DQ_FMT_Q6_K, 128>(g, rows, n_tok, steps, d_y, s);
 }
 
 extern "C" int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,

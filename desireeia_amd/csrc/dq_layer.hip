@@ -29,6 +29,22 @@ namespace {
 // One workgroup of 256 threads; thread t owns chunks of 16 values.
 constexpr int NQ_T = 256;
 
+// x = a (+ b) of chunk c: every load issued before the adds (a load whose
+// use sits in the same branch would be waited for on its own).
+__device__ __forceinline__ void nq_chunk(const float* __restrict__ a, const float* __restrict__ b, int c,
+                                         float4 (&x)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = reinterpret_cast<const float4*>(a + c * 16)[i];
+    if (b) {
+        float4 y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[i] = reinterpret_cast<const float4*>(b + c * 16)[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i].x = x[i].x + y[i].x, x[i].y = x[i].y + y[i].y, x[i].z = x[i].z + y[i].z,
+                                    x[i].w = x[i].w + y[i].w;
+    }
+}
+
 __global__ __launch_bounds__(NQ_T) void norm_quant_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                           float* __restrict__ h_out, const float* __restrict__ w,
                                                           int n, float eps, int8_t* __restrict__ q,
@@ -39,22 +55,32 @@ __global__ __launch_bounds__(NQ_T) void norm_quant_kernel(const float* __restric
     const int t = threadIdx.x;
     const int n_chunks = n / 16;
     double acc = 0.0;
-    for (int c = t; c < n_chunks; c += NQ_T) {
+    float4 x0[4];  // the first pass's chunk, kept for the quantization
+    for (int c0 = 0; c0 < n_chunks; c0 += NQ_T) {
+        const bool live = c0 + t < n_chunks;
+        const int c = min(c0 + t, n_chunks - 1);
+        float4 x[4];
+        nq_chunk(a, b, c, x);
+        if (c0 == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float4 x = reinterpret_cast<const float4*>(a + c * 16)[i];
-            if (b) {
-                const float4 y = reinterpret_cast<const float4*>(b + c * 16)[i];
-                x.x = x.x + y.x, x.y = x.y + y.y, x.z = x.z + y.z, x.w = x.w + y.w;
-                if (h_out) reinterpret_cast<float4*>(h_out + c * 16)[i] = x;
+            for (int i = 0; i < 4; ++i) x0[i] = x[i];
+        }
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if (b && h_out) reinterpret_cast<float4*>(h_out + c * 16)[i] = x[i];
+                const float s0 = x[i].x * x[i].x, s1 = x[i].y * x[i].y, s2 = x[i].z * x[i].z, s3 = x[i].w * x[i].w;
+                acc += (double)s0;
+                acc += (double)s1;
+                acc += (double)s2;
+                acc += (double)s3;
             }
-            const float s0 = x.x * x.x, s1 = x.y * x.y, s2 = x.z * x.z, s3 = x.w * x.w;
-            acc += (double)s0;
-            acc += (double)s1;
-            acc += (double)s2;
-            acc += (double)s3;
         }
     }
+    // the weights of the first chunk, in flight during the reduction
+    float4 w0[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w0[i] = reinterpret_cast<const float4*>(w + min(t, n_chunks - 1) * 16)[i];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, DQ_WAVE);
     if ((t & 63) == 0) wsum[t >> 6] = acc;
@@ -68,25 +94,25 @@ __global__ __launch_bounds__(NQ_T) void norm_quant_kernel(const float* __restric
     const float sc = s_scale;
     // 16 threads per 256-value block: chunks c = 16k .. 16k+15 belong to block k
     for (int c0 = 0; c0 < n_chunks; c0 += NQ_T) {
-        const int c = c0 + t;
-        const bool live = c < n_chunks;
+        const bool live = c0 + t < n_chunks;
+        const int c = min(c0 + t, n_chunks - 1);
+        float4 x[4], ww[4];
+        if (c0 == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = x0[i], ww[i] = w0[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ww[i] = reinterpret_cast<const float4*>(w + c * 16)[i];
+            nq_chunk(a, b, c, x);
+        }
         float y[16];
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            float4 x = make_float4(0.f, 0.f, 0.f, 0.f), ww = x;
-            if (live) {
-                x = reinterpret_cast<const float4*>(a + c * 16)[i];
-                if (b) {
-                    const float4 yb = reinterpret_cast<const float4*>(b + c * 16)[i];
-                    x.x = x.x + yb.x, x.y = x.y + yb.y, x.z = x.z + yb.z, x.w = x.w + yb.w;
-                }
-                ww = reinterpret_cast<const float4*>(w + c * 16)[i];
-            }
-            y[4 * i + 0] = x.x * sc * ww.x;
-            y[4 * i + 1] = x.y * sc * ww.y;
-            y[4 * i + 2] = x.z * sc * ww.z;
-            y[4 * i + 3] = x.w * sc * ww.w;
+            y[4 * i + 0] = x[i].x * sc * ww[i].x;
+            y[4 * i + 1] = x[i].y * sc * ww[i].y;
+            y[4 * i + 2] = x[i].z * sc * ww[i].z;
+            y[4 * i + 3] = x[i].w * sc * ww[i].w;
         }
         if (y_out && live) {
 #pragma unroll

@@ -14,20 +14,26 @@
 // Design: the reference CPU path re-streams every expert's weights once per
 // token. Here the tokens routed to an expert are gathered into one list, and
 // each weight byte is read from HBM once for all of them:
-//  * routing: one wave per token, lane = expert;
-//  * lists: expert-major, ascending token order (deterministic);
+//  * routing: one wave per token, lane = expert (the token's activation range
+//    scale computed alongside);
+//  * lists: expert-major, ascending (token, slot) order (deterministic), by
+//    wave ballots in one workgroup;
 //  * activation rows per (token, expert) pair: the per-256 integers and scale
-//    of the reference, entered into the MFMA as fp16(q * d), plus K/32 "min
-//    columns" fp16(d * isum_j) that carry the Q4_K min term (the weight side
-//    of those columns is fp16(-dmin * m_j));
+//    of the reference, entered into the MFMA as fp16(q * d * s) (s a
+//    power-of-two range scale undone on the output), plus the 8 block sums
+//    fp16(d * isum_j * s) per super-block in a plane with the pairs
+//    contiguous, which carry the Q4_K min term as one extra 16-wide MFMA
+//    slice per super-block against fp16(-dmin * m_j);
 //  * expert GEMM: a workgroup owns 128 weight rows of one expert and streams
-//    their packed bytes once per 32 of the expert's tokens (a super-block per
-//    K step through a 2-stage LDS ring with the activation rows, 64 contiguous
-//    bytes per row and sub-plane per DMA), dequantizing to fp16 in registers
-//    (magic-number conversion, d*sc folded in) for 32x32x16 MFMA tiles.
-//    The fp16 roundings of the two operands move results by ~3e-4 relative.
-//    A K split (partials summed in a fixed order by the next kernel) gives
-//    the short down projection enough waves to stream HBM.
+//    their packed bytes once per 32 of the expert's tokens, a super-block per
+//    K step through a 2-stage LDS ring with the activation rows (64
+//    contiguous bytes per row and sub-plane per DMA), dequantizing to fp16 in
+//    registers (magic-number conversion, d*sc folded in) for 32x32x16 MFMA
+//    tiles. The fp16 roundings of the two operands move results by ~3e-4
+//    relative. A K split (partials summed in a fixed order by the next
+//    kernel) gives the short down projection enough waves to stream HBM;
+//  * SiLU(gate) * up, its range scale and quantization in one kernel per
+//    pair; the weighted scatter back to the tokens in slot order.
 #include <math.h>
 
 #include "dq_common.h"
@@ -42,7 +48,6 @@ constexpr int MAX_TILES = 1;   // token tiles per pass of a workgroup (32 pairs)
 constexpr int ACH = 32;        // 16-byte chunks of a token's activation per main step (256 halfs)
 constexpr int WAVES = 4;       // waves per workgroup, 32 weight rows each
 constexpr int NSTAGE = 2;      // LDS ring stages (NSTAGE-1 steps in flight while one computes)
-constexpr int MIN_BLK = 8;     // min columns are padded to a multiple of this (16-byte rows)
 static_assert(NSTAGE == 2 || NSTAGE == 3, "the step wait counts NSTAGE-2 <= 1 later steps");
 
 // ---------------------------------------------------------------- routing --
@@ -175,12 +180,13 @@ __global__ __launch_bounds__(256) void moe_lists_kernel(const int32_t* __restric
 }
 
 // ------------------------------------------------------- activation rows --
-// One 256-block b of an activation row (values v, 4 per lane): the per-256
+// One 256-block b of activation row p (values v, 4 per lane): the per-256
 // quantization d = amax/127, id = 127/amax, q = rint(v*id) (core/matmul.cpp
-// :1681-1700), written as fp16(q*d*s) in columns 256b + 4 lane .. +3 and the
-// min columns K + 8b + j = fp16(d*isum_j*s), s the row's range scale.
-__device__ __forceinline__ void quant_256_block(const float (&v)[4], float sc, int lane, int b, int K,
-                                                _Float16* row) {
+// :1681-1700), written as fp16(q*d*s) in columns 256b + 4 lane .. +3 of the
+// row, and the block sums fp16(d*isum_j*s), j = 0..7, at minp[b][p][j] (a
+// plane with the pairs contiguous per super-block); s the row's range scale.
+__device__ __forceinline__ void quant_256_block(const float (&v)[4], float sc, int lane, int b, int p, int n_rows,
+                                                _Float16* row, _Float16* minp) {
     float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     amax = dq_wave_max(amax);
     const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
@@ -198,14 +204,15 @@ __device__ __forceinline__ void quant_256_block(const float (&v)[4], float sc, i
     // 8 lanes hold one 32-block
 #pragma unroll
     for (int off = 1; off < 8; off <<= 1) isum += __shfl_xor(isum, off, DQ_WAVE);
-    if ((lane & 7) == 0) row[K + 8 * b + (lane >> 3)] = (_Float16)((d * (float)isum) * sc);
+    if ((lane & 7) == 0) minp[((size_t)b * n_rows + p) * 8 + (lane >> 3)] = (_Float16)((d * (float)isum) * sc);
 }
 
 // Row p of A from token pairs[p] / k of x: one wave per (pair, 256-block);
 // the row scales come from the route kernel; inv[p] = 1/s.
 __global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ x, const float* __restrict__ rscale,
                                                       const int32_t* __restrict__ pairs, int k, int n_rows, int K,
-                                                      int lda, _Float16* __restrict__ A, float* __restrict__ inv) {
+                                                      _Float16* __restrict__ A, _Float16* __restrict__ minp,
+                                                      float* __restrict__ inv) {
     const int lane = threadIdx.x & 63;
     const int nblk = K / 256;
     const long w = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -215,12 +222,8 @@ __global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ 
     const float sc = rscale[srow];
     const float4 f = *reinterpret_cast<const float4*>(x + srow * K + 256 * b + 4 * lane);
     const float v[4] = {f.x, f.y, f.z, f.w};
-    _Float16* row = A + (size_t)p * lda;
-    quant_256_block(v, sc, lane, b, K, row);
-    if (b == 0) {  // zero padding of the min columns, and the output factor
-        for (int c = K + K / 32 + lane; c < lda; c += DQ_WAVE) row[c] = (_Float16)0.0f;
-        if (lane == 0) inv[p] = 1.0f / sc;
-    }
+    quant_256_block(v, sc, lane, b, p, n_rows, A + (size_t)p * K, minp);
+    if (b == 0 && lane == 0) inv[p] = 1.0f / sc;  // the output factor
 }
 
 // The down projection's activation row of pair p in one workgroup: h =
@@ -232,8 +235,9 @@ __global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ 
 constexpr int SILU_WAVES = 16, SILU_J = 4;  // n_ff <= 16384
 __global__ __launch_bounds__(64 * SILU_WAVES) void moe_silu_act_kernel(const float* __restrict__ gate,
                                                                        const float* __restrict__ up, int nsplit,
-                                                                       size_t split_stride, int F, int lda,
+                                                                       size_t split_stride, int F, int n_rows,
                                                                        _Float16* __restrict__ A,
+                                                                       _Float16* __restrict__ minp,
                                                                        float* __restrict__ inv) {
     __shared__ float wmax[SILU_WAVES];
     const int p = blockIdx.x;
@@ -277,14 +281,13 @@ __global__ __launch_bounds__(64 * SILU_WAVES) void moe_silu_act_kernel(const flo
 #pragma unroll
     for (int w = 1; w < SILU_WAVES; ++w) r = fmaxf(r, wmax[w]);
     const float sc = row_scale_of(r);
-    _Float16* row = A + (size_t)p * lda;
+    _Float16* row = A + (size_t)p * F;
 #pragma unroll
     for (int j = 0; j < SILU_J; ++j) {
         const int b = wave + SILU_WAVES * j;
-        if (b < nblk) quant_256_block(h[j], sc, lane, b, F, row);
+        if (b < nblk) quant_256_block(h[j], sc, lane, b, p, n_rows, row, minp);
     }
     if (threadIdx.x == 0) inv[p] = 1.0f / sc;
-    for (int c = F + F / 32 + (int)threadIdx.x; c < lda; c += 64 * SILU_WAVES) row[c] = (_Float16)0.0f;
 }
 
 // ------------------------------------------------------------ expert GEMM --
@@ -292,10 +295,11 @@ struct MoeGemm {
     const uint8_t* w[2];  // packed stacked matrices ([n_exp * rows][K])
     DqLayout L[2];
     float* y[2];          // outputs [nsplit][n_pairs][rows]
-    const _Float16* A;    // activation rows [n_pairs][lda]
+    const _Float16* A;    // activation rows [n_pairs][K]
+    const _Float16* minp; // their block sums [K/256][n_pairs][8]
     const float* inv;     // per pair: 1/s of its activation row
     const int32_t* offsets;
-    int rows, K, lda, n_pairs, nsplit, steps_per_split, main_steps;
+    int rows, K, n_pairs, nsplit, steps_per_split, main_steps;
 };
 
 // Weight bytes of one main step, a Q4_K super-block (K = 256, 4 items) of this
@@ -338,17 +342,6 @@ __device__ __forceinline__ int a_offset(int st, int t, int kk, int h) {
     return 256 * st + 64 * t + 32 * (kk >> 1) + 16 * h + 8 * (kk & 1);
 }
 
-// Min term of the main step's super-block as one extra 16-wide MFMA slice:
-// lanes of half 0 carry its 8 sub-blocks (weight side fp16(-dmin * m_j) from
-// the header, activation side the min columns K + 8st + j), half 1 zeros.
-__device__ __forceinline__ h8 b_min8(const dq_u32x4& hd, bool ok) {
-    const float dmin = dq_h2f((uint16_t)(hd.x >> 16));
-    _Float16 v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (_Float16)(ok ? -(dmin * (float)q4k_min(i, hd.y, hd.z, hd.w)) : 0.0f);
-    return *reinterpret_cast<const h8*>(v);
-}
-
 #define DQ_LDS_PTR(p) reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(p))
 
 // s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt in bits
@@ -368,11 +361,13 @@ constexpr int A_LOADS = MAX_TILES * TT * ACH / (64 * WAVES);  // DMAs per thread
 static_assert(A_LOADS >= 1, "activation DMA slots per thread");
 constexpr int A_MAIN_BYTES = MAX_TILES * TT * ACH * 16;
 constexpr int A_STAGE_BYTES = A_MAIN_BYTES + 64 * 16;  // + the min chunks (64 slots, 32 tokens twice)
-__device__ __forceinline__ void issue_a(const _Float16* A, int lda, int K, int c, int p_end, int st, uint8_t* dst,
-                                        int tid) {
-    {   // the step's 8 min columns of token lane % 32 (every wave loads the same slots)
+__device__ __forceinline__ void issue_a(const _Float16* A, const _Float16* minp, int K, int n_pairs, int c,
+                                        int p_end, int st, uint8_t* dst, int tid) {
+    const int lda = K;
+    {   // the step's 8 block sums of pair lane % 32 (contiguous over the pairs;
+        // every wave loads the same slots)
         const int p = min(c + (tid & 31), p_end - 1);
-        __builtin_amdgcn_global_load_lds(A + (size_t)p * lda + K + 8 * (size_t)st, DQ_LDS_PTR(dst + A_MAIN_BYTES), 16,
+        __builtin_amdgcn_global_load_lds(minp + ((size_t)st * n_pairs + p) * 8, DQ_LDS_PTR(dst + A_MAIN_BYTES), 16,
                                          0, 0);
     }
 #pragma unroll
@@ -461,7 +456,7 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_kernel(MoeGemm G) {
 #pragma unroll
             for (int q = 0; q < NSTAGE - 1; ++q) {
                 if (s0 + q < main_end) {
-                    issue_a(G.A, G.lda, G.K, c, p_end, s0 + q, aring[q], tid);
+                    issue_a(G.A, G.minp, G.K, G.n_pairs, c, p_end, s0 + q, aring[q], tid);
                     issue_w(base, L, row0, nrows, s0 + q, wring[q], tid);
                 }
             }
@@ -475,10 +470,10 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_kernel(MoeGemm G) {
                 } else {
                     wait_vm<0>();
                 }
-                __syncthreads();  // every wave's DMAs landed; stage st-1 is free
+                dq_lds_barrier();  // every wave's DMAs of this step landed; stage st-1 is free
                 if (st + NSTAGE - 1 < main_end) {
                     const int ns = (st - s0 + NSTAGE - 1) % NSTAGE;
-                    issue_a(G.A, G.lda, G.K, c, p_end, st + NSTAGE - 1, aring[ns], tid);
+                    issue_a(G.A, G.minp, G.K, G.n_pairs, c, p_end, st + NSTAGE - 1, aring[ns], tid);
                     issue_w(base, L, row0, nrows, st + NSTAGE - 1, wring[ns], tid);
                 }
                 const uint8_t* ab = aring[stage];
@@ -504,21 +499,28 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_kernel(MoeGemm G) {
                     for (int kk = 0; kk < 4; ++kk)
                         acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk], bf[kk], acc, 0, 0, 0);
                 }
-                {   // the super-block's min term
+                {   // the super-block's min term: one 16-wide slice, lanes of half 0
+                    // carry its 8 sub-blocks (the min columns K + 8st + j
+                    // against fp16(-dmin * m_j)), half 1 zeros
                     const h8 zero = {};
                     const h8 am = h == 0 ? *reinterpret_cast<const h8*>(ab + A_MAIN_BYTES + (lane & 31) * 16) : zero;
-                    const h8 bm = h == 0 ? b_min8(wr.hd, row_ok) : zero;
+                    const h8 bm = h == 0 ? q4k_neg_mins(wr.hd, row_ok) : zero;
                     acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, acc, 0, 0, 0);
                 }
             }
             __syncthreads();  // the ring is reused by the next pass
         }
-        // D of 32x32x16: lane l, register r -> weight row l % 32, token (r/4)*8 + (l/32)*4 + r%4
+        // D of 32x32x16: lane l, register r -> weight row l % 32, token (r/4)*8 + (l/32)*4 + r%4.
+        // The pairs' factors 1/s are loaded together first (clamped pairs: a
+        // load inside the store's branch would be waited for one at a time).
+        float inv[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) inv[r] = G.inv[min(c + (r >> 2) * 8 + h * 4 + (r & 3), p_end - 1)];
         if (row_ok) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int p = c + (r >> 2) * 8 + h * 4 + (r & 3);
-                if (p < p_end) y[(size_t)p * G.rows + rloc] = acc[r] * G.inv[p];
+                if (p < p_end) y[(size_t)p * G.rows + rloc] = acc[r] * inv[r];
             }
         }
     }
@@ -548,12 +550,11 @@ __global__ __launch_bounds__(256) void moe_scatter_kernel(const float* __restric
 struct MoeWs {
     int32_t *ids, *offsets, *pairs, *slot_pos;
     float *wts, *xscale, *inv_in, *inv_h;
-    _Float16 *a_in, *a_h;
+    _Float16 *a_in, *a_h, *min_in, *min_h;
     float *gate, *up, *down;
     size_t total;
 };
 
-int min_cols(int K) { return (K / 32 + MIN_BLK - 1) / MIN_BLK * MIN_BLK; }
 
 int cus() {
     static int n = 0;
@@ -579,7 +580,6 @@ int pick_split(int n_exp, int rows, int n_mat, int steps) {
 MoeWs carve(const dq_moe_t* m, uint32_t n_tok, int split_gu, int split_d, uint8_t* base) {
     const size_t n_ent = (size_t)n_tok * m->n_expert_used;
     const size_t E = m->n_embd, F = m->n_ff;
-    const size_t lda_in = E + min_cols((int)E), lda_h = F + min_cols((int)F);
     MoeWs w{};
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -595,10 +595,12 @@ MoeWs carve(const dq_moe_t* m, uint32_t n_tok, int split_gu, int split_d, uint8_
     w.xscale = (float*)take((size_t)n_tok * 4);
     w.inv_in = (float*)take(n_ent * 4);
     w.inv_h = (float*)take(n_ent * 4);
-    w.a_in = (_Float16*)take(n_ent * lda_in * 2);
+    w.a_in = (_Float16*)take(n_ent * E * 2);
+    w.min_in = (_Float16*)take(n_ent * (E / 32) * 2);
     w.gate = (float*)take((size_t)split_gu * n_ent * F * 4);
     w.up = (float*)take((size_t)split_gu * n_ent * F * 4);
-    w.a_h = (_Float16*)take(n_ent * lda_h * 2);
+    w.a_h = (_Float16*)take(n_ent * F * 2);
+    w.min_h = (_Float16*)take(n_ent * (F / 32) * 2);
     w.down = (float*)take((size_t)split_d * n_ent * E * 4);
     w.total = off;
     return w;
@@ -622,8 +624,8 @@ void splits(const dq_moe_t* m, int* sgu, int* sd) {
 }
 
 int launch_gemm(const uint8_t* w0, const uint8_t* w1, int n_mat, int n_exp, int rows, int K, const _Float16* A,
-                const float* inv, int lda, const int32_t* offsets, int n_pairs, int nsplit, float* y0, float* y1,
-                hipStream_t s) {
+                const _Float16* minp, const float* inv, const int32_t* offsets, int n_pairs, int nsplit, float* y0,
+                float* y1, hipStream_t s) {
     MoeGemm G{};
     G.w[0] = w0;
     G.w[1] = w1 ? w1 : w0;
@@ -632,11 +634,11 @@ int launch_gemm(const uint8_t* w0, const uint8_t* w1, int n_mat, int n_exp, int 
     G.y[0] = y0;
     G.y[1] = y1 ? y1 : y0;
     G.A = A;
+    G.minp = minp;
     G.inv = inv;
     G.offsets = offsets;
     G.rows = rows;
     G.K = K;
-    G.lda = lda;
     G.n_pairs = n_pairs;
     G.nsplit = nsplit;
     G.main_steps = K / 256;  // a super-block per main step
@@ -693,7 +695,6 @@ int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint3
     const int k = (int)m->n_expert_used, n_exp = (int)m->n_expert;
     const int E = (int)m->n_embd, F = (int)m->n_ff;
     const int n_ent = (int)n_tok * k;
-    const int lda_in = E + min_cols(E), lda_h = F + min_cols(F);
     // routing (with the row scales of x) and the per-expert lists
     moe_route_kernel<<<(n_tok + 3) / 4, 256, 0, s>>>(d_logits, (int)n_tok, n_exp, k, m->norm_w, m->w_scale, w.ids,
                                                      w.wts, d_x, E, w.xscale);
@@ -703,17 +704,18 @@ int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint3
     // activation rows of the pairs
     {
         const long waves = (long)n_ent * (E / 256);
-        moe_act_kernel<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(d_x, w.xscale, w.pairs, k, n_ent, E, lda_in,
-                                                                   w.a_in, w.inv_in);
+        moe_act_kernel<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(d_x, w.xscale, w.pairs, k, n_ent, E, w.a_in,
+                                                                   w.min_in, w.inv_in);
         DQ_TRY(dq_launch_status());
     }
     // gate and up of every pair (one launch, two matrices)
-    DQ_TRY(launch_gemm((const uint8_t*)m->wgate, (const uint8_t*)m->wup, 2, n_exp, F, E, w.a_in, w.inv_in, lda_in,
+    DQ_TRY(launch_gemm((const uint8_t*)m->wgate, (const uint8_t*)m->wup, 2, n_exp, F, E, w.a_in, w.min_in, w.inv_in,
                        w.offsets, n_ent, sgu, w.gate, w.up, s));
     // h = silu(gate) * up, quantized for the down projection
-    moe_silu_act_kernel<<<n_ent, 64 * SILU_WAVES, 0, s>>>(w.gate, w.up, sgu, (size_t)n_ent * F, F, lda_h, w.a_h, w.inv_h);
+    moe_silu_act_kernel<<<n_ent, 64 * SILU_WAVES, 0, s>>>(w.gate, w.up, sgu, (size_t)n_ent * F, F, n_ent, w.a_h,
+                                                          w.min_h, w.inv_h);
     DQ_TRY(dq_launch_status());
-    DQ_TRY(launch_gemm((const uint8_t*)m->wdown, nullptr, 1, n_exp, E, F, w.a_h, w.inv_h, lda_h, w.offsets, n_ent,
+    DQ_TRY(launch_gemm((const uint8_t*)m->wdown, nullptr, 1, n_exp, E, F, w.a_h, w.min_h, w.inv_h, w.offsets, n_ent,
                        sd, w.down, nullptr, s));
     {
         const size_t n = (size_t)n_tok * E;
