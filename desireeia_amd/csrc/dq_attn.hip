@@ -30,7 +30,6 @@ namespace {
 constexpr int TP = 64;         // positions per tile
 constexpr int NT = 256;        // threads per workgroup
 constexpr int MCH = 256;       // tiles per merge chunk
-constexpr int NW_M = NT / 64;  // waves of the merge kernel
 
 __device__ __forceinline__ int read_pos(int pos_host, const int* pos_dev, int n_ctx) {
     int p = pos_dev ? *pos_dev : pos_host;
@@ -330,49 +329,65 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
 }
 
 // Merge of the tile records: workgroup b owns outputs [256b, 256b + 256) of
-// the flattened [n_head][HD] output (HD = 128: two heads, waves 0-1 and 2-3).
-// Per head: M = max over tiles of m_t (lanes over tiles); then in chunks of
-// MCH tiles the weights w_t = e^(m_t - M) go to LDS, L = sum w_t l_t and
-// out = sum w_t acc_t / L, with the acc loads of a chunk batched. Optionally
-// quantizes the 256 outputs per 256 (core/matmul.cpp:1660-1778).
+// the flattened [n_head][HD] output (HD = 128: two heads). Per head: M = max
+// over tiles of m_t; then in chunks of MCH tiles the weights w_t = e^(m_t -
+// M) go to LDS, L = sum w_t l_t and out = sum w_t acc_t / L. The MG thread
+// groups of the workgroup take every MG-th tile, each issuing its record
+// loads in batches of 16 (one round trip per batch instead of one per tile);
+// the MG partial sums are added in group order. Optionally quantizes the 256
+// outputs per 256 (core/matmul.cpp:1660-1778).
+constexpr int MG = 4;                 // tile groups of the merge
+constexpr int MNO = 256;              // outputs per merge workgroup
+constexpr int MNT = MG * MNO;         // its threads
+constexpr int MB = 16;                // record loads per batch
 template <int HD, int HPK>
-__global__ __launch_bounds__(NT) void attn_merge_kernel(AttnArgs A) {
+__global__ __launch_bounds__(MNT) void attn_merge_kernel(AttnArgs A) {
     constexpr int REC = HD + 2;
-    constexpr int HPB = NT / HD;  // heads per block
-    static_assert(NT % HD == 0, "whole heads per block");
+    constexpr int HPB = MNO / HD;        // heads per block
+    constexpr int NWV = MNT / 64;        // waves
+    static_assert(MNO % HD == 0 && MNO == NT, "whole heads per block");
     __shared__ float mtot[HPB];
-    __shared__ float wred[NT / 64];
+    __shared__ float wred[NWV];
     __shared__ float mw[HPB][MCH];
     __shared__ float ml[HPB][MCH];
+    __shared__ float pacc[MG][MNO];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int WPH = NW_M / HPB;  // waves per head
+    const int g = tid / MNO, ol = tid % MNO;     // tile group, output in the block
     const int pos = read_pos(A.pos_host, A.pos_dev, A.n_ctx);
     const int c0 = A.cc_start < pos ? A.cc_start : pos;
     const int n_tiles = min((pos + 1 - c0 + TP - 1) / TP, A.max_tiles);
-    const int o = blockIdx.x * NT + tid;          // flattened output
-    const int hb = tid / HD;                      // head within the block
+    const int o = blockIdx.x * MNO + ol;          // flattened output
+    const int hb = ol / HD;                       // head within the block
     const int hq = blockIdx.x * HPB + hb;         // query head
     const int kvh = hq / HPK, h = hq % HPK, dd = o % HD;
     const float* recs = A.part + (size_t)kvh * A.max_tiles * HPK * REC;
-    // per-head max: the WPH waves of the head split the tiles
+    // per-head max: the waves of a head (every (g, 64-output) wave whose
+    // outputs lie in it) split the tiles
     {
+        constexpr int WPH = NWV / HPB;  // waves per head
+        const int wi = g * (HD / 64) + (ol % HD) / 64;  // this wave's index among its head's waves
         float M = -INFINITY;
-        for (int t = (wave % WPH) * 64 + lane; t < n_tiles; t += 64 * WPH)
-            M = fmaxf(M, recs[(t * HPK + h) * REC + HD]);
+        for (int t0 = wi * 64; t0 < n_tiles; t0 += 64 * WPH) {
+            const int t = t0 + lane;
+            const float m = recs[(min(t, n_tiles - 1) * HPK + h) * REC + HD];
+            if (t < n_tiles) M = fmaxf(M, m);
+        }
         M = dq_wave_max(M);
         if (lane == 0) wred[wave] = M;
         __syncthreads();
         if (tid < HPB) {
-            float m = wred[tid * WPH];
-            for (int w = 1; w < WPH; ++w) m = fmaxf(m, wred[tid * WPH + w]);
+            // waves of head j: those whose outputs (wave % (MNO/64)) fall in head j
+            float m = -INFINITY;
+            for (int w = 0; w < NWV; ++w)
+                if (((w % (MNO / 64)) * 64) / HD == tid) m = fmaxf(m, wred[w]);
             mtot[tid] = m;
         }
     }
-    float a = 0.0f, L = 0.0f;
+    float a = 0.0f;
     for (int t0 = 0; t0 < n_tiles; t0 += MCH) {
         const int nt = min(MCH, n_tiles - t0);
         __syncthreads();  // mtot ready / the previous chunk consumed
-        for (int i = tid; i < HPB * nt; i += NT) {
+        for (int i = tid; i < HPB * nt; i += MNT) {
             const int j = i / nt, t = t0 + i % nt;
             const int hj = (blockIdx.x * HPB + j) % HPK, kj = (blockIdx.x * HPB + j) / HPK;
             const float* r = A.part + ((size_t)kj * A.max_tiles * HPK + (size_t)t * HPK + hj) * REC;
@@ -382,23 +397,49 @@ __global__ __launch_bounds__(NT) void attn_merge_kernel(AttnArgs A) {
         }
         __syncthreads();
         const float* base = recs + ((size_t)t0 * HPK + h) * REC + dd;
-#pragma unroll 8
-        for (int t = 0; t < nt; ++t) {
-            a = fmaf(mw[hb][t], base[(size_t)t * HPK * REC], a);
-            L += ml[hb][t];
+        for (int tb = g; tb < nt; tb += MG * MB) {
+            float v[MB];
+#pragma unroll
+            for (int k = 0; k < MB; ++k) v[k] = base[(size_t)min(tb + MG * k, nt - 1) * HPK * REC];
+#pragma unroll
+            for (int k = 0; k < MB; ++k)
+                if (tb + MG * k < nt) a = fmaf(mw[hb][tb + MG * k], v[k], a);
         }
     }
-    const float v = a / L;
-    A.out[o] = v;
+    pacc[g][ol] = a;
+    __syncthreads();
+    // group 0 (waves 0 .. MNO/64-1) finishes; the others stay for the barriers
+    float v = 0.0f;
+    if (g == 0) {
+        float L = 0.0f;
+        for (int t0 = 0; t0 < n_tiles; t0 += MCH) {
+            // the last chunk's l weights are still in LDS; earlier chunks'
+            // are recomputed from the records
+            const int nt = min(MCH, n_tiles - t0);
+            if (t0 + MCH >= n_tiles) {
+                for (int t = 0; t < nt; ++t) L += ml[hb][t];
+            } else {
+                for (int t = 0; t < nt; ++t) {
+                    const float* r = recs + ((size_t)(t0 + t) * HPK + h) * REC;
+                    L += __expf(r[HD] - mtot[hb]) * r[HD + 1];
+                }
+            }
+        }
+        float acc = pacc[0][ol];
+#pragma unroll
+        for (int q = 1; q < MG; ++q) acc += pacc[q][ol];
+        v = acc / L;
+        A.out[o] = v;
+    }
     if (!A.oq) return;  // uniform
     // per-256 quantization of the block's 256 outputs
-    __syncthreads();
     const float am = dq_wave_max(fabsf(v));
     if (lane == 0) wred[wave] = am;
     __syncthreads();
+    if (g != 0) return;
     float amax = wred[0];
 #pragma unroll
-    for (int w = 1; w < NW_M; ++w) amax = fmaxf(amax, wred[w]);
+    for (int w = 1; w < MNO / 64; ++w) amax = fmaxf(amax, wred[w]);
     const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
     const float id = d > 0.0f ? 127.0f / amax : 0.0f;
     int iv = (int)rintf(v * id);
@@ -413,11 +454,6 @@ __global__ __launch_bounds__(NT) void attn_merge_kernel(AttnArgs A) {
     }
 }
 
-int env_int(const char* name, int dflt) {
-    const char* e = getenv(name);
-    return e ? atoi(e) : dflt;
-}
-
 // Workspace: the tile records.
 int max_tiles_for(uint32_t n_ctx) { return (int)((n_ctx + TP - 1) / TP); }
 size_t work_bytes_for(int n_head, int hd, int max_tiles) {
@@ -428,7 +464,7 @@ template <int HD, int HPK, bool FUSE>
 int launch_attn(const AttnArgs& a, int n_head, hipStream_t st) {
     const int slots = a.n_kv * ((a.max_tiles + 7) / 8);  // per XCD
     attn_tile_kernel<HD, HPK, FUSE><<<8 * slots, NT, 0, st>>>(a);
-    attn_merge_kernel<HD, HPK><<<n_head * HD / NT, NT, 0, st>>>(a);
+    attn_merge_kernel<HD, HPK><<<n_head * HD / MNO, MNT, 0, st>>>(a);
     return dq_launch_status();
 }
 

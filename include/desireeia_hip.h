@@ -132,8 +132,8 @@ int dq_gemv_group_f32(const dq_gemv_job_t* jobs, size_t n, size_t cols, const fl
  * reference); each token's operand row carries a power-of-two range scale
  * (undone exactly on the output), so any finite activation magnitude stays
  * inside fp16. `d_work` (dq_gemm_workspace_bytes() bytes) holds the quantized
- * activations, their row scales and, for Q4_K, a per-call plane of the min
- * terms. Other formats: -2. */
+ * activations, for Q4_K their per-32 block sums (the min-term input, tokens
+ * contiguous per super-block), and their row scales. Other formats: -2. */
 int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t n_tok, size_t* bytes);
 int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,
             float* d_y, void* d_work, size_t work_bytes, void* stream);
