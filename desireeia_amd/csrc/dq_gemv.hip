@@ -7,12 +7,16 @@
 //  * The activation bytes of a lane's items (x int8, scale, sums) are loaded
 //    into registers once per wave and reused for every row the wave visits;
 //    only weights stream from HBM.
-//  * Waves are persistent (a few per SIMD) and walk row groups of R rows with
-//    a two-deep software pipeline: the loads of group k+1 are issued before
-//    group k is computed, so dot products and scale decoding overlap the HBM
-//    stream instead of piling up after it. Past the last group the prefetch
-//    is redirected to a cached dummy address (no extra HBM traffic, and the
-//    compiler's in-order vmcnt accounting stays static).
+//  * Flat grid (the default where it fits): one wave, or one workgroup for a
+//    K-split row, per group of R rows, sized so every wave of the launch is
+//    resident at once (about 16 per CU). The activation registers are loaded
+//    first, then every weight load of the group, so the whole matrix's loads
+//    are in flight from the start and each row's arithmetic runs as soon as
+//    its own weights land (rows are kept in order by scheduling barriers).
+//  * Persistent grid (larger shapes): waves walk row groups with a two-deep
+//    software pipeline, the loads of group k+1 issued before group k is
+//    computed; past the last group the prefetch reads a cached dummy address
+//    (no extra HBM traffic, static vmcnt accounting).
 //  * Nibble/6-bit unpack and 6-bit scale decode in registers (one decode per
 //    64 weights), v_dot4_i32_i8 dots, and row sums over the wave by DPP row
 //    reductions and readlanes (no LDS round trips on the critical path).
@@ -147,27 +151,20 @@ struct Fmt<DQ_FMT_Q4_K> {
         const int da = dot16(nib_lo(w.qb), X.x[1], dot16(nib_lo(w.qa), X.x[0], 0));
         const int db = dot16(nib_hi(w.qb), X.x[3], dot16(nib_hi(w.qa), X.x[2], 0));
         // 6-bit scale/min of sub-blocks j = 2g, 2g+1 (quant/quant.cpp:22-29);
-        // scale bytes q[0..11] are header words h.y, h.z, h.w.
+        // scale bytes q[0..11] are header words h.y, h.z, h.w. Branch-free
+        // (g differs between lanes): bytes 2(g&1), 2(g&1)+1 of each word, then
+        //   j < 4:  sc = q[j] & 63,                     m = q[j+4] & 63
+        //   j >= 4: sc = (q[j+4]&15) | ((q[j-4]>>6)<<4), m = (q[j+4]>>4) | ((q[j]>>6)<<4)
         const int g = i & 3;
-        const uint32_t w0 = w.h.y, w1 = w.h.z, w2 = w.h.w;
-        int sca, mna, scb, mnb;
-        if (g < 2) {
-            const int sh = 16 * g;  // j < 4: sc = q[j] & 63, m = q[j+4] & 63
-            sca = (w0 >> sh) & 63;
-            scb = (w0 >> (sh + 8)) & 63;
-            mna = (w1 >> sh) & 63;
-            mnb = (w1 >> (sh + 8)) & 63;
-        } else {
-            // j >= 4: sc = (q[j+4]&15) | ((q[j-4]>>6)<<4), m = (q[j+4]>>4) | ((q[j]>>6)<<4)
-            const int sh = 16 * (g - 2);
-            const uint32_t qa8 = (w2 >> sh) & 0xFF, qb8 = (w2 >> (sh + 8)) & 0xFF;
-            const uint32_t la = (w0 >> sh) & 0xFF, lb = (w0 >> (sh + 8)) & 0xFF;
-            const uint32_t ma = (w1 >> sh) & 0xFF, mb = (w1 >> (sh + 8)) & 0xFF;
-            sca = (int)((qa8 & 0xF) | ((la >> 6) << 4));
-            scb = (int)((qb8 & 0xF) | ((lb >> 6) << 4));
-            mna = (int)((qa8 >> 4) | ((ma >> 6) << 4));
-            mnb = (int)((qb8 >> 4) | ((mb >> 6) << 4));
-        }
+        const int sh = 16 * (g & 1);
+        const bool hi = g >= 2;
+        const uint32_t b0a = (w.h.y >> sh) & 0xFF, b0b = (w.h.y >> (sh + 8)) & 0xFF;
+        const uint32_t b1a = (w.h.z >> sh) & 0xFF, b1b = (w.h.z >> (sh + 8)) & 0xFF;
+        const uint32_t b2a = (w.h.w >> sh) & 0xFF, b2b = (w.h.w >> (sh + 8)) & 0xFF;
+        const int sca = (int)(hi ? ((b2a & 15) | ((b0a >> 6) << 4)) : (b0a & 63));
+        const int scb = (int)(hi ? ((b2b & 15) | ((b0b >> 6) << 4)) : (b0b & 63));
+        const int mna = (int)(hi ? ((b2a >> 4) | ((b1a >> 6) << 4)) : (b1a & 63));
+        const int mnb = (int)(hi ? ((b2b >> 4) | ((b1b >> 6) << 4)) : (b1b & 63));
         const float d = dq_h2f((uint16_t)(w.h.x & 0xFFFF));
         const float dmin = dq_h2f((uint16_t)(w.h.x >> 16));
         const int isum = sca * da + scb * db;
@@ -298,6 +295,9 @@ __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R
             a += i < i1 ? p : 0.0f;
         }
         acc[rr] = a;
+        // row by row: the scheduler would otherwise sink every row's dot
+        // products below the wait for the last row's weights
+        __builtin_amdgcn_sched_barrier(0);
     }
     // each row's sum over the wave: DPP row reductions + readlanes (uniform)
     float tot[R];
@@ -416,6 +416,154 @@ __global__ __launch_bounds__(256) void gemv_kernel(Jobs J, int items, const int8
     }
 }
 
+// In-kernel activation quantization of the flat grid, in two phases so that
+// it overlaps the weight stream: xstage_load issues the fp32 loads BEFORE the
+// weight loads (vector memory returns are counted in issue order, so loads
+// issued after the weights could not be used before every weight byte had
+// arrived); xstage_quant then quantizes into LDS while the weights are in
+// flight. Loads are coalesced: round r of wave w (of nw) covers the 256
+// columns c0 + 256*(w + r*nw) + [0, 256), lane l holding the 4 at +4l (one
+// contiguous kilobyte per load instruction). A 32-block is 8 lanes and a
+// 256-block the whole wave, so block maxima and integer sums are lane
+// reductions (DPP within rows, shuffles across rows); max and integer sums
+// do not depend on order, so the integers and scales are bit-exact with the
+// per-block quantizer (dq_quant_block). Columns past c1 load the last four
+// (valid address) and are not stored; c0, c1 are multiples of 64 (whole
+// 32-blocks of 8 lanes) and, for the per-256 quantizer, of 256.
+template <int ROUNDS>
+struct XStage {
+    float4 v[ROUNDS];
+};
+
+template <int ROUNDS>
+__device__ __forceinline__ void xstage_load(XStage<ROUNDS>& st, const float* __restrict__ xf, int c0, int c1, int w,
+                                            int nw, int lane) {
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) {
+        const int c = min(c0 + 256 * (w + r * nw) + 4 * lane, c1 - 4);
+        st.v[r] = *reinterpret_cast<const float4*>(xf + c);
+    }
+}
+
+__device__ __forceinline__ float max8_lanes(float v) {  // max over the 8 lanes of an aligned group
+    v = fmaxf(v, dq_dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dq_dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+    return fmaxf(v, dq_dpp<0x141>(v));  // row_half_mirror: the other quad of the 8
+}
+__device__ __forceinline__ int sum8_lanes(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    return v + __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+}
+
+// LDS image of columns [c0, c1): int8 q at xl + (c - c0), fp32 scale and
+// int32 sum of 32-block k at xl + 32*nblk + 4k and xl + 36*nblk + 4k (nblk =
+// the region's block capacity).
+template <int FMT, int ROUNDS>
+__device__ __forceinline__ void xstage_quant(const XStage<ROUNDS>& st, int c0, int c1, int w, int nw, int lane,
+                                             int nblk, uint8_t* xl) {
+    constexpr bool PER256 = act_kind_of<FMT>() == DQ_ACT_Q8K_REP;
+    float* ls = reinterpret_cast<float*>(xl + 32 * (size_t)nblk);
+    int32_t* li = reinterpret_cast<int32_t*>(xl + 36 * (size_t)nblk);
+#pragma unroll
+    for (int r = 0; r < ROUNDS; ++r) {
+        const int c = c0 + 256 * (w + r * nw) + 4 * lane;
+        const float4 v = st.v[r];
+        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        amax = max8_lanes(amax);
+        if constexpr (PER256) {
+            amax = fmaxf(amax, dq_dpp<0x140>(amax));  // row_mirror: the 16-lane row
+            amax = fmaxf(amax, __shfl_xor(amax, 16, DQ_WAVE));
+            amax = fmaxf(amax, __shfl_xor(amax, 32, DQ_WAVE));
+        }
+        const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+        float id;
+        if constexpr (PER256) id = d > 0.0f ? 127.0f / amax : 0.0f;  // core/matmul.cpp:1681-1700
+        else id = d > 0.0f ? 1.0f / d : 0.0f;                          // core/quant.cpp:15-50
+        int q[4];
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int iv = (int)rintf(vv[k] * id);
+            q[k] = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
+        }
+        const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
+                                ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
+        const int isum = sum8_lanes(q[0] + q[1] + q[2] + q[3]);
+        if (c < c1) {
+            const int o = c - c0;
+            *reinterpret_cast<uint32_t*>(xl + o) = packed;
+            if ((lane & 7) == 0) {
+                ls[o >> 5] = d;
+                li[o >> 5] = isum;
+            }
+        }
+    }
+}
+
+// Flat grid: one wave (KS == 1) or one workgroup (KS == 4, K split in
+// quarters) per group of R rows, and every weight load of the group issued
+// before any is used. No loop and no prefetch past the end: the grid holds
+// all groups at once (about 16 waves per CU), which keeps the whole matrix's
+// loads in flight from the start and ends every wave right after its only
+// group. Groups are global over the jobs of J. One item per lane (NIT 1).
+template <int FMT, int R, int KS, bool XQ>
+__global__ __launch_bounds__(256) void gemv_flat_kernel(Jobs J, int items, int per, const int8_t* __restrict__ xq,
+                                                        const float* __restrict__ xs,
+                                                        const int32_t* __restrict__ xsum,
+                                                        const float* __restrict__ xf) {
+    using W = typename Fmt<FMT>::W;
+    extern __shared__ __align__(16) uint8_t xl[];
+    __shared__ float part[2][R][4];
+    const int lane = threadIdx.x & (DQ_WAVE - 1);
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / DQ_WAVE));
+    const int ks = KS == 1 ? 0 : wv;
+    const int i0 = min(ks * per, items);
+    const int i1 = min(i0 + per, items);
+    const int ngroups = J.g0[J.n];
+    const int g = KS == 1 ? 4 * (int)blockIdx.x + wv : (int)blockIdx.x;
+    const bool live = g < ngroups;  // uniform per wave (KS 1) / per workgroup (KS 4)
+    // KS 1 with XQ: every wave takes part in the shared quantization first
+    if ((KS == 4 || !XQ) && !live) return;
+
+    // A wave of a K split whose item range is empty (i0 == i1 == items) still
+    // loads (clamped, valid) addresses; its terms are masked in compute_group.
+    // XQ rounds: KS 1 - the 4 waves share the whole activation (cols <= 8192,
+    // <= 8 rounds each); KS 4 - each wave its own K quarter (<= 4096 columns).
+    constexpr int XR = KS == 1 ? 8 : 16;
+    const int xc0 = KS == 1 ? 0 : 64 * i0, xc1 = KS == 1 ? 64 * items : 64 * i1;
+    const int xw = KS == 1 ? wv : 0, xnw = KS == 1 ? 4 : 1;
+    XStage<XR> xst;
+    if constexpr (XQ) xstage_load<XR>(xst, xf, xc0, xc1, xw, xnw, lane);  // xc1 >= 64: loads stay in x
+    int xi = min(i0 + lane, i1 - 1);  // this lane's activation item (clamped)
+    XItem X[1];
+    // pre-quantized activation: its registers are loaded before the weights,
+    // so each row's arithmetic can start when that row's weights land
+    if constexpr (!XQ) Fmt<FMT>::load_x(X[0], xi, xq, xs, xsum);
+    __builtin_amdgcn_sched_barrier(0);
+    W w[R][1];
+    load_group<FMT, R, 1>(w, J, min(g, ngroups - 1), ngroups, i0, i1, lane, nullptr);
+    // keep the quantization's arithmetic below the weight loads: hoisted above
+    // them, it would wait for its activation loads before the weights are issued
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XQ) {
+        const int nblk = KS == 1 ? 2 * items : 2 * per;
+        // wave region (KS 4): 80 bytes per item (64 int8, 2 scales, 2 sums)
+        uint8_t* reg = KS == 1 ? xl : xl + (size_t)ks * 80 * per;
+        xstage_quant<FMT, XR>(xst, xc0, xc1, xw, xnw, lane, nblk, reg);
+        if constexpr (KS == 1) {
+            __syncthreads();
+            if (!live) return;
+        }
+        xq = reinterpret_cast<const int8_t*>(reg);
+        xs = reinterpret_cast<const float*>(reg + 32 * nblk);
+        xsum = reinterpret_cast<const int32_t*>(reg + 36 * nblk);
+        if constexpr (KS == 4) xi = max(0, min(lane, i1 - i0 - 1));  // relative to i0 (a multiple of 4 items)
+        Fmt<FMT>::load_x(X[0], xi, xq, xs, xsum);
+    }
+    compute_group<FMT, R, 1, KS>(w, X, J, g, i0, i1, lane, ks, part, 0);
+}
+
 int g_num_cus = 0;
 
 int num_cus() {
@@ -441,6 +589,10 @@ void set_groups(Jobs& J, int R) {
     for (int j = 0; j < J.n; ++j) J.g0[j + 1] = J.g0[j] + (J.rows[j] + R - 1) / R;
 }
 
+// LDS budget of the in-kernel quantized activation: within the 64 KB of
+// dynamic LDS a launch gets by default (cols <= 49152).
+constexpr size_t XQ_MAX_LDS = 60 * 1024;
+
 // Bytes of the in-kernel quantized activation (XQ) in LDS.
 size_t xq_lds_bytes(size_t cols) { return cols + 8 * (cols / 32); }
 
@@ -463,18 +615,94 @@ int launch(Jobs J, int items, const int8_t* xq, const float* xs, const int32_t* 
 }
 
 template <int FMT, int R, int KS>
+int launch_flat_r(Jobs J, int items, int per, const int8_t* xq, const float* xs, const int32_t* xsum,
+                  const float* xf, hipStream_t s) {
+    set_groups(J, R);
+    const int ngroups = J.g0[J.n];
+    const unsigned grid = (unsigned)(KS == 1 ? (ngroups + 3) / 4 : ngroups);
+    if (xf) {
+        const size_t lds = KS == 1 ? (size_t)80 * items : (size_t)4 * 80 * per;
+        gemv_flat_kernel<FMT, R, KS, true><<<grid, 256, lds, s>>>(J, items, per, xq, xs, xsum, xf);
+    } else {
+        gemv_flat_kernel<FMT, R, KS, false><<<grid, 256, 0, s>>>(J, items, per, xq, xs, xsum, xf);
+    }
+    return dq_launch_status();
+}
+
+// Returned by launch_flat when the flat grid does not apply (no launch).
+constexpr int NO_FLAT = 1;
+
+// Waves of gemv_flat_kernel<FMT, R, KS, XQ> that one CU holds at once (its
+// register and LDS needs; cached per instantiation).
+template <int FMT, int R, int KS>
+int flat_resident_waves(bool xq, size_t lds) {
+    static int cached[2] = {0, 0};
+    int& c = cached[xq ? 1 : 0];
+    if (c == 0) {
+        int nb = 0;
+        const void* k = xq ? reinterpret_cast<const void*>(&gemv_flat_kernel<FMT, R, KS, true>)
+                           : reinterpret_cast<const void*>(&gemv_flat_kernel<FMT, R, KS, false>);
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, lds) != hipSuccess || nb <= 0) nb = 1;
+        c = 4 * nb;
+    }
+    return c;
+}
+
+// Groups of R rows over the jobs of J.
+int count_groups(const Jobs& J, int R) {
+    int n = 0;
+    for (int j = 0; j < J.n; ++j) n += (J.rows[j] + R - 1) / R;
+    return n;
+}
+
+// The flat grid with the fewest rows per group (1, 2, 4 or 8) whose waves all
+// fit on the CUs at once, at most `wpc` per CU; NO_FLAT when one item per
+// lane does not cover a wave's K range or no R fits (then the persistent grid
+// runs).
+template <int FMT, int KS>
+int launch_flat(const Jobs& J, int items, int per, int nit, const int8_t* xq, const float* xs, const int32_t* xsum,
+                const float* xf, hipStream_t s) {
+    static const int on = env_int("DQ_GEMV_FLAT", 1);
+    static const int wpc = env_int("DQ_GEMV_FWPC", 16);
+    if (!on || nit != 1) return NO_FLAT;
+    // fp32 activation with the per-256 quantizer: every workgroup would repeat
+    // its cross-row reductions and divisions per 256 columns; the persistent
+    // grid (fewer workgroups) quantizes less often
+    if (xf && act_kind_of<FMT>() == DQ_ACT_Q8K_REP) return NO_FLAT;
+    const size_t lds = !xf ? 0 : KS == 1 ? (size_t)80 * items : (size_t)4 * 80 * per;
+    if (lds > XQ_MAX_LDS) return NO_FLAT;
+    const int gw = KS == 1 ? 1 : 4;  // waves per group
+    const long cus = num_cus();
+    const bool q = xf != nullptr;
+    auto fits = [&](int r, int resident) { return (long)count_groups(J, r) * gw <= cus * min(wpc, resident); };
+    constexpr int WB = (int)sizeof(typename Fmt<FMT>::W);  // weight bytes per row per lane
+    if (fits(1, flat_resident_waves<FMT, 1, KS>(q, lds)))
+        return launch_flat_r<FMT, 1, KS>(J, items, per, xq, xs, xsum, xf, s);
+    if (fits(2, flat_resident_waves<FMT, 2, KS>(q, lds)))
+        return launch_flat_r<FMT, 2, KS>(J, items, per, xq, xs, xsum, xf, s);
+    if (fits(4, flat_resident_waves<FMT, 4, KS>(q, lds)))
+        return launch_flat_r<FMT, 4, KS>(J, items, per, xq, xs, xsum, xf, s);
+    if (8 * WB <= 400 && fits(8, flat_resident_waves<FMT, 8, KS>(q, lds)))
+        return launch_flat_r<FMT, 8, KS>(J, items, per, xq, xs, xsum, xf, s);
+    return NO_FLAT;
+}
+
+// Persistent grid: two rows per group when one item per lane covers the K
+// range, else one row with NIT items per lane. KS 1 has items <= 128 (NIT <= 2).
+template <int FMT, int KS>
 int launch_nit(int nit, const Jobs& J, int items, const int8_t* xq, const float* xs, const int32_t* xsum,
                const float* xf, hipStream_t s) {
     switch (nit) {
-    case 1: return launch<FMT, R, 1, KS>(J, items, xq, xs, xsum, xf, s);
-    case 2: return launch<FMT, R, 2, KS>(J, items, xq, xs, xsum, xf, s);
-    case 3: return launch<FMT, R, 3, KS>(J, items, xq, xs, xsum, xf, s);
-    case 4: return launch<FMT, R, 4, KS>(J, items, xq, xs, xsum, xf, s);
-    default:
-        if (nit <= 6) return launch<FMT, R, 6, KS>(J, items, xq, xs, xsum, xf, s);
-        if (nit <= 8) return launch<FMT, R, 8, KS>(J, items, xq, xs, xsum, xf, s);
-        return DQ_ERR_NOT_SUPPORTED;
+    case 1: return launch<FMT, 2, 1, KS>(J, items, xq, xs, xsum, xf, s);
+    case 2: return launch<FMT, 1, 2, KS>(J, items, xq, xs, xsum, xf, s);
     }
+    if constexpr (KS == 4) {
+        if (nit == 3) return launch<FMT, 1, 3, KS>(J, items, xq, xs, xsum, xf, s);
+        if (nit == 4) return launch<FMT, 1, 4, KS>(J, items, xq, xs, xsum, xf, s);
+        if (nit <= 6) return launch<FMT, 1, 6, KS>(J, items, xq, xs, xsum, xf, s);
+        if (nit <= 8) return launch<FMT, 1, 8, KS>(J, items, xq, xs, xsum, xf, s);
+    }
+    return DQ_ERR_NOT_SUPPORTED;
 }
 
 template <int FMT>
@@ -482,23 +710,19 @@ int launch_fmt(const Jobs& J, size_t cols, const int8_t* xq, const float* xs, co
                hipStream_t s) {
     const int items = (int)(cols / 64);
     // K split: rows wider than 128 items are shared by the 4 waves of a workgroup
-    int ks = env_int("DQ_GEMV_KS", 0);
-    if (ks != 1 && ks != 4) ks = items > 2 * DQ_WAVE ? 4 : 1;
+    const int ks = items > 2 * DQ_WAVE ? 4 : 1;
     const int per = ks == 1 ? items : (items + 3) / 4;
     const int nit = (per + DQ_WAVE - 1) / DQ_WAVE;
     if (nit > 8) return DQ_ERR_NOT_SUPPORTED;
-    // rows per group: enough loads in flight per wave, bounded registers
-    int r = env_int("DQ_GEMV_R", 0);
-    if (r != 1 && r != 2 && r != 4) r = nit == 1 ? 2 : 1;
-    if (nit > 4 && r > 1) r = 1;
-    if (ks == 1) {
-        if (r == 1) return launch_nit<FMT, 1, 1>(nit, J, items, xq, xs, xsum, xf, s);
-        if (r == 2) return launch_nit<FMT, 2, 1>(nit, J, items, xq, xs, xsum, xf, s);
-        return launch_nit<FMT, 4, 1>(nit, J, items, xq, xs, xsum, xf, s);
+    {   // flat grid first; a wave's K quarter holds whole 256-blocks (per-256 quantizer)
+        const int fper = ks == 1 ? items : (act_kind_of<FMT>() == DQ_ACT_Q8K_REP ? (items + 15) / 16 * 4 : per);
+        const int fnit = (fper + DQ_WAVE - 1) / DQ_WAVE;
+        const int rc = ks == 1 ? launch_flat<FMT, 1>(J, items, fper, fnit, xq, xs, xsum, xf, s)
+                               : launch_flat<FMT, 4>(J, items, fper, fnit, xq, xs, xsum, xf, s);
+        if (rc != NO_FLAT) return rc;
     }
-    if (r == 1) return launch_nit<FMT, 1, 4>(nit, J, items, xq, xs, xsum, xf, s);
-    if (r == 2) return launch_nit<FMT, 2, 4>(nit, J, items, xq, xs, xsum, xf, s);
-    return launch_nit<FMT, 4, 4>(nit, J, items, xq, xs, xsum, xf, s);
+    return ks == 1 ? launch_nit<FMT, 1>(nit, J, items, xq, xs, xsum, xf, s)
+                   : launch_nit<FMT, 4>(nit, J, items, xq, xs, xsum, xf, s);
 }
 
 int launch_jobs(int fmt, const Jobs& J, size_t cols, const int8_t* xq, const float* xs, const int32_t* xsum,
@@ -513,9 +737,6 @@ int launch_jobs(int fmt, const Jobs& J, size_t cols, const int8_t* xq, const flo
 }
 
 bool per32_act(int fmt) { return fmt == DQ_FMT_Q8_0 || fmt == DQ_FMT_Q4_0; }
-// LDS budget of the in-kernel quantized activation: within the 64 KB of
-// dynamic LDS a launch gets by default (cols <= 49152).
-constexpr size_t XQ_MAX_LDS = 60 * 1024;
 bool needs_sum(int fmt) { return fmt == DQ_FMT_Q4_0 || fmt == DQ_FMT_Q4_K; }
 
 // Validates n jobs; writes the layouts. NOT_SUPPORTED for shapes/formats the

@@ -147,6 +147,47 @@ def test_gemv_f32_matches_quantize_then_gemv(gpu, qtype, rows, cols):
     assert torch.equal(fused, two)
 
 
+def _edge_activation(cols, seed):
+    """Per 256-column chunk: all zeros; amax 127 with exact .5 ties (id = 1,
+    so rint must round half to even); magnitudes near 1e30 and 1e-30; one
+    lone nonzero; otherwise N(0,1)."""
+    x = synth.gen_act(cols, seed=seed).astype(np.float32)
+    ties = np.arange(-60, 60, dtype=np.float32) + 0.5
+    for c in range(cols // 256):
+        sl = slice(256 * c, 256 * c + 256)
+        kind = c % 5
+        if kind == 0:
+            x[sl] = 0.0
+        elif kind == 1:
+            v = np.resize(ties, 256)
+            v[::32] = 127.0  # every 32-block has amax 127
+            x[sl] = v
+        elif kind == 2:
+            x[sl] *= np.float32(1e30)
+        elif kind == 3:
+            x[sl] *= np.float32(1e-30)
+        else:
+            x[sl] = 0.0
+            x[256 * c + 77] = -3.25
+    return x
+
+
+@pytest.mark.parametrize("qtype,rows,cols", [(synth.Q4_K, 1000, 4096), (synth.Q4_K, 256, 14336),
+                                             (synth.Q8_0, 700, 4096), (synth.Q4_0, 300, 14336),
+                                             (synth.Q6_K, 513, 14336)])
+def test_gemv_f32_quantizer_edges(gpu, qtype, rows, cols):
+    """The in-kernel quantizer of dq_gemv_f32 gives the same integers and
+    scales as dq_quantize_act on zero blocks, .5 ties, extreme magnitudes and
+    sparse blocks (bit-identical GEMV outputs)."""
+    print(f"gemv_f32 edges type={qtype} {rows}x{cols}", flush=True)
+    w = synth.gen_weights(qtype, rows, cols, seed=rows + 7)
+    x = torch.from_numpy(_edge_activation(cols, seed=cols)).to(gpu)
+    m = ops.QuantMatrix.from_gguf(qtype, w, rows, cols)
+    fused = ops.matmul(m, x)
+    two = ops.gemv(m, ops.quantize_act(x, ops.act_kind_for(m.fmt)))
+    assert torch.equal(fused, two)
+
+
 def test_gemv_group_f32_mixed_kinds(gpu, orc):
     """The fp32 group form mixes the per-32 and per-256 kinds (each launch
     quantizes for its own format) and keeps residuals; too wide: -2."""
