@@ -283,7 +283,7 @@ __device__ __forceinline__ void load_group(typename Fmt<FMT>::W (&wr)[R][NIT], c
 template <int FMT, int R, int NIT, int KS>
 __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R][NIT], const XItem (&X)[NIT],
                                               const Jobs& J, int g, int i0, int i1, int lane, int ks,
-                                              float (*part)[R][4], int buf) {
+                                              float (*part)[R][4], int buf, bool store = true) {
     float acc[R];
 #pragma unroll
     for (int rr = 0; rr < R; ++rr) {
@@ -313,14 +313,14 @@ __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R
 #pragma unroll
     for (int rr = 1; rr < R; ++rr) mine = lane == rr ? tot[rr] : mine;
     if constexpr (KS == 1) {
-        if (lane < R) {
+        if (store && lane < R) {
             const int r = gl * R + lane;
             if (r < rows) y[r] = res ? mine + res[r] : mine;
         }
     } else {
         if (lane < R) part[buf][lane][ks] = mine;
         __syncthreads();
-        if (ks == 0 && lane < R) {
+        if (store && ks == 0 && lane < R) {
             const int r = gl * R + lane;
             if (r < rows) {
                 const float v = ((part[buf][lane][0] + part[buf][lane][1]) + part[buf][lane][2]) + part[buf][lane][3];
@@ -467,14 +467,18 @@ __device__ __forceinline__ void xstage_quant(const XStage<ROUNDS>& st, int c0, i
     int32_t* li = reinterpret_cast<int32_t*>(xl + 36 * (size_t)nblk);
 #pragma unroll
     for (int r = 0; r < ROUNDS; ++r) {
+        if (c0 + 256 * (w + r * nw) >= c1) continue;  // wave-uniform: a round wholly past the end
         const int c = c0 + 256 * (w + r * nw) + 4 * lane;
         const float4 v = st.v[r];
         float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
         amax = max8_lanes(amax);
         if constexpr (PER256) {
             amax = fmaxf(amax, dq_dpp<0x140>(amax));  // row_mirror: the 16-lane row
-            amax = fmaxf(amax, __shfl_xor(amax, 16, DQ_WAVE));
-            amax = fmaxf(amax, __shfl_xor(amax, 32, DQ_WAVE));
+            const int b = __builtin_bit_cast(int, amax);  // the 4 row maxima, wave-uniform
+            amax = fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
+                               __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
+                         fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
+                               __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
         }
         const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
         float id;
@@ -564,6 +568,47 @@ __global__ __launch_bounds__(256) void gemv_flat_kernel(Jobs J, int items, int p
     compute_group<FMT, R, 1, KS>(w, X, J, g, i0, i1, lane, ks, part, 0);
 }
 
+// Flat grid for the fp32 activation with the per-256 quantizer: 16-wave
+// (1024-thread) workgroups, so one quantization of the activation serves 16
+// waves (4x fewer repeats over the grid than 4-wave workgroups). KS 1: 16
+// groups per workgroup, one per wave; KS 4: 4 groups of 4 waves (K quarters).
+// The activation is quantized whole into LDS (round r of wave w: 256-column
+// chunk w + 16r, at most 4 rounds: cols <= 16384), its loads issued before
+// the weights. No wave leaves before the last barrier; a group past the end
+// computes the clamped last group and stores nothing.
+template <int FMT, int R, int KS>
+__global__ __launch_bounds__(1024) void gemv_flat16_kernel(Jobs J, int items, int per, const float* __restrict__ xf) {
+    using W = typename Fmt<FMT>::W;
+    constexpr int GPW = KS == 1 ? 16 : 4;  // groups per workgroup
+    extern __shared__ __align__(16) uint8_t xl[];
+    __shared__ float part[GPW][R][4];
+    const int lane = threadIdx.x & (DQ_WAVE - 1);
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / DQ_WAVE));
+    const int ks = KS == 1 ? 0 : (wv & 3);
+    const int gi = KS == 1 ? wv : (wv >> 2);
+    const int i0 = min(ks * per, items);
+    const int i1 = min(i0 + per, items);
+    const int ngroups = J.g0[J.n];
+    const int g = GPW * (int)blockIdx.x + gi;
+    const bool live = g < ngroups;
+    const int cols = 64 * items;
+
+    XStage<4> xst;
+    xstage_load<4>(xst, xf, 0, cols, wv, 16, lane);
+    W w[R][1];
+    load_group<FMT, R, 1>(w, J, min(g, ngroups - 1), ngroups, i0, i1, lane, nullptr);
+    __builtin_amdgcn_sched_barrier(0);
+    const int nblk = 2 * items;
+    xstage_quant<FMT, 4>(xst, 0, cols, wv, 16, lane, nblk, xl);
+    __syncthreads();
+    if (KS == 1 && !live) return;  // KS 1 has no barrier after this one
+    XItem X[1];
+    Fmt<FMT>::load_x(X[0], min(i0 + lane, i1 - 1), reinterpret_cast<const int8_t*>(xl),
+                     reinterpret_cast<const float*>(xl + 32 * nblk), reinterpret_cast<const int32_t*>(xl + 36 * nblk));
+    compute_group<FMT, R, 1, KS>(w, X, J, min(g, ngroups - 1), i0, i1, lane, ks,
+                                 reinterpret_cast<float(*)[R][4]>(&part[gi][0][0]), 0, live);
+}
+
 int g_num_cus = 0;
 
 int num_cus() {
@@ -632,6 +677,51 @@ int launch_flat_r(Jobs J, int items, int per, const int8_t* xq, const float* xs,
 // Returned by launch_flat when the flat grid does not apply (no launch).
 constexpr int NO_FLAT = 1;
 
+// Groups of R rows over the jobs of J.
+int count_groups(const Jobs& J, int R) {
+    int n = 0;
+    for (int j = 0; j < J.n; ++j) n += (J.rows[j] + R - 1) / R;
+    return n;
+}
+
+template <int FMT, int R, int KS>
+int launch_flat16_r(Jobs J, int items, int per, const float* xf, hipStream_t s) {
+    set_groups(J, R);
+    constexpr int GPW = KS == 1 ? 16 : 4;
+    const unsigned grid = (unsigned)((J.g0[J.n] + GPW - 1) / GPW);
+    gemv_flat16_kernel<FMT, R, KS><<<grid, 1024, (size_t)80 * items, s>>>(J, items, per, xf);
+    return dq_launch_status();
+}
+
+// Workgroups of gemv_flat16_kernel<FMT, R, KS> one CU holds at once (cached).
+template <int FMT, int R, int KS>
+int flat16_resident(size_t lds) {
+    static int c = -1;
+    if (c < 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(&gemv_flat16_kernel<FMT, R, KS>),
+                                                         1024, lds) != hipSuccess)
+            nb = 0;
+        c = nb;
+    }
+    return c;
+}
+
+// 16-wave flat grid with the fewest rows per group (1, 2, 4) whose
+// workgroups are all resident at once; NO_FLAT otherwise.
+template <int FMT, int KS>
+int launch_flat16(const Jobs& J, int items, int per, const float* xf, hipStream_t s) {
+    const size_t lds = (size_t)80 * items;
+    if (lds > XQ_MAX_LDS || items * 64 > 16384) return NO_FLAT;
+    constexpr int GPW = KS == 1 ? 16 : 4;
+    const long cus = num_cus();
+    auto fits = [&](int r, int resident) { return resident > 0 && (count_groups(J, r) + GPW - 1) / GPW <= cus * resident; };
+    if (fits(1, flat16_resident<FMT, 1, KS>(lds))) return launch_flat16_r<FMT, 1, KS>(J, items, per, xf, s);
+    if (fits(2, flat16_resident<FMT, 2, KS>(lds))) return launch_flat16_r<FMT, 2, KS>(J, items, per, xf, s);
+    if (fits(4, flat16_resident<FMT, 4, KS>(lds))) return launch_flat16_r<FMT, 4, KS>(J, items, per, xf, s);
+    return NO_FLAT;
+}
+
 // Waves of gemv_flat_kernel<FMT, R, KS, XQ> that one CU holds at once (its
 // register and LDS needs; cached per instantiation).
 template <int FMT, int R, int KS>
@@ -648,12 +738,6 @@ int flat_resident_waves(bool xq, size_t lds) {
     return c;
 }
 
-// Groups of R rows over the jobs of J.
-int count_groups(const Jobs& J, int R) {
-    int n = 0;
-    for (int j = 0; j < J.n; ++j) n += (J.rows[j] + R - 1) / R;
-    return n;
-}
 
 // The flat grid with the fewest rows per group (1, 2, 4 or 8) whose waves all
 // fit on the CUs at once, at most `wpc` per CU; NO_FLAT when one item per
@@ -665,10 +749,11 @@ int launch_flat(const Jobs& J, int items, int per, int nit, const int8_t* xq, co
     static const int on = env_int("DQ_GEMV_FLAT", 1);
     static const int wpc = env_int("DQ_GEMV_FWPC", 16);
     if (!on || nit != 1) return NO_FLAT;
-    // fp32 activation with the per-256 quantizer: every workgroup would repeat
-    // its cross-row reductions and divisions per 256 columns; the persistent
-    // grid (fewer workgroups) quantizes less often
-    if (xf && act_kind_of<FMT>() == DQ_ACT_Q8K_REP) return NO_FLAT;
+    // fp32 activation with the per-256 quantizer (cross-row reductions and
+    // two divisions per 256 columns, repeated by every workgroup): 16-wave
+    // workgroups
+    if constexpr (act_kind_of<FMT>() == DQ_ACT_Q8K_REP)
+        if (xf) return launch_flat16<FMT, KS>(J, items, per, xf, s);
     const size_t lds = !xf ? 0 : KS == 1 ? (size_t)80 * items : (size_t)4 * 80 * per;
     if (lds > XQ_MAX_LDS) return NO_FLAT;
     const int gw = KS == 1 ? 1 : 4;  // waves per group
