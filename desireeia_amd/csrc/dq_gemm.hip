@@ -28,13 +28,20 @@
 // its rows' bytes into fp16 fragments in registers. Q6_K: K is permuted to the
 // packed item order (both operands, see dq_quantize_act_f16), so a 64-column
 // K step is exactly one 64-weight item.
+#include <cstdlib>
+#include <utility>
+
 #include "dq_common.h"
 #include "dq_f16.h"
 
 namespace {
 
 
-constexpr int BM = 128, BK = 64;  // tile rows (tokens), K per step
+constexpr int BK = 64;  // K per step
+
+// Tile rows (tokens) of a workgroup: 2 waves along M, each WM 32-token blocks.
+template <int WM>
+constexpr int bm_of() { return 64 * WM; }
 
 enum BKind { B_Q4K = 0, B_Q6K = 1 };
 
@@ -51,13 +58,14 @@ enum BKind { B_Q4K = 0, B_Q6K = 1 };
 // 2 bytes per lane; lane i of a wave writes at base + i*16 for 16-byte loads and
 // at base + i*4 for the dword and sub-dword forms). Three stages: two steps'
 // DMAs in flight while one is computed.
-template <int BN, int KIND>
+template <int BN, int KIND, int WM>
 struct Ring {
+    static constexpr int BM = bm_of<WM>();
     static constexpr int NS = 3;
     static constexpr int A_BYTES = BM * BK * 2;
     static constexpr int MIN_BYTES = KIND == B_Q4K ? BM * 16 : 0;
     static constexpr int B_OFF = A_BYTES + MIN_BYTES;
-    static constexpr int B_BYTES = BN * 64;
+    static constexpr int B_BYTES = BN * 56;  // Q4_K 48 bytes per row, Q6_K 56
     static constexpr int STAGE = B_OFF + B_BYTES;
     static constexpr int BYTES = NS * STAGE;
 };
@@ -102,18 +110,20 @@ struct GemmArgs {
 // of 64 slots are dealt to the NW waves, and where a region has fewer blocks
 // than waves several waves load the same block (identical bytes to the same
 // LDS address).
-template <int BN, int KIND>
+template <int BN, int KIND, int WM>
 constexpr int stage_loads() {
     constexpr int NW = BN / 32;
-    return BM * 8 / 64 / NW + (KIND == B_Q4K ? 3 : 3);
+    return bm_of<WM>() * 8 / 64 / NW + 3;  // A, then Q4_K: sums, P0/P1, H; Q6_K: QA/QB, QH or S, D
 }
 
-template <int BN, int KIND>
+template <int BN, int KIND, int WM>
 __device__ __forceinline__ void issue_stage(const GemmArgs& g, uint8_t* ring, int stage, int st, int wave,
                                             int lane) {
     constexpr int NW = BN / 32;      // waves per workgroup
     constexpr int HB = BN / 64;      // 64-slot blocks per [BN] region (= NW/2)
-    using R = Ring<BN, KIND>;
+    using R = Ring<BN, KIND, WM>;
+    constexpr int BM = R::BM;
+    static_assert(BM / 64 <= NW, "one block-sum block per wave at most");
     uint8_t* base = ring + stage * R::STAGE;
     // A: BM*8 slots of 16 bytes
     {
@@ -129,9 +139,9 @@ __device__ __forceinline__ void issue_stage(const GemmArgs& g, uint8_t* ring, in
     }
     uint8_t* bb = base + R::B_OFF;
     if constexpr (KIND == B_Q4K) {
-        {   // block sums of super-block st/4 (16 contiguous bytes per token): 2
-            // blocks of 64 rows, block wave % 2
-            const int blk = wave & 1, m = min(g.m0 + blk * 64 + lane, g.M - 1);
+        {   // block sums of super-block st/4 (16 contiguous bytes per token):
+            // BM/64 blocks of 64 rows, block wave % (BM/64)
+            const int blk = wave % (BM / 64), m = min(g.m0 + blk * 64 + lane, g.M - 1);
             lds_dma<16>(g.minp + ((size_t)(st >> 2) * g.M + m) * 8, base + R::A_BYTES + blk * 64 * 16);
         }
         {   // P0/P1: 2*HB = NW blocks, one per wave
@@ -202,14 +212,19 @@ __device__ __forceinline__ void b_raw(const uint8_t* bb, int wn, int lane, BRaw&
 }
 
 // B fragments of a step of phase G (= st % 4, the item of the super-block)
-// from the raw bytes: bf[kk][j], kk = 16-wide K slice, j = 32-row n block.
-// Lane l feeds row n = wn*64 + j*32 + l%32 with the 8 K values kk*16 +
+// from the raw bytes, one 16-wide K slice KK at a time (so a slice can be
+// built while the previous slice's MFMAs run): bf[j], j = 32-row n block.
+// Lane l feeds row n = wn*64 + j*32 + l%32 with the 8 K values KK*16 +
 // 8*(l/32) .. +7. Rows past N hold the clamped last row's bytes (finite
-// values whose outputs are never stored). Q4_K, G == 3: bm[j] = the
-// super-block's min slice (q4k_neg_mins); the activation side is zero for
-// lane half 1.
+// values whose outputs are never stored). b_scales holds the fp16 scale pair
+// of every (j, KK): Q4_K a = d*sc of sub-block 2G (KK 0, 1: low nibbles) or
+// 2G+1 (KK 2, 3: high nibbles); Q6_K a = d*sc of the KK-th 16-block.
+struct BScale {
+    h2 s[2][4];
+};
+
 template <int KIND>
-__device__ __forceinline__ void b_dequant(const BRaw& r, int G, h8 (&bf)[4][2], h8 (&bm)[2]) {
+__device__ __forceinline__ void b_scales(const BRaw& r, int G, BScale& S) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         if constexpr (KIND == B_Q4K) {
@@ -217,39 +232,55 @@ __device__ __forceinline__ void b_dequant(const BRaw& r, int G, h8 (&bf)[4][2], 
             const float d = dq_h2f((uint16_t)(hd.x & 0xFFFF));
             const _Float16 a0 = (_Float16)(d * (float)q4k_scale(2 * G, hd.y, hd.z, hd.w));
             const _Float16 a1 = (_Float16)(d * (float)q4k_scale(2 * G + 1, hd.y, hd.z, hd.w));
-            const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
-            const h2 v0 = {a0, a0}, v1 = {a1, a1};
-            uint32_t t[4];
-            // kk 0: P0 low nibbles, 1: P1 low, 2: P0 high, 3: P1 high
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                const dq_u32x2 src = (kk & 1) ? r.q1[j] : r.q0[j];
-                const uint32_t m0 = kk < 2 ? (src.x & 0x0F0F0F0Fu) : ((src.x >> 4) & 0x0F0F0F0Fu);
-                const uint32_t m1 = kk < 2 ? (src.y & 0x0F0F0F0Fu) : ((src.y >> 4) & 0x0F0F0F0Fu);
-                bytes_to_h2(m0, bias, kk < 2 ? v0 : v1, &t[0]);
-                bytes_to_h2(m1, bias, kk < 2 ? v0 : v1, &t[2]);
-                bf[kk][j] = __builtin_bit_cast(h8, dq_u32x4{t[0], t[1], t[2], t[3]});
-            }
-            if (G == 3) bm[j] = q4k_neg_mins(hd, true);
+            S.s[j][0] = S.s[j][1] = h2{a0, a0};
+            S.s[j][2] = S.s[j][3] = h2{a1, a1};
         } else {
             const uint32_t sc = r.hd[j].x;
             const float d = dq_h2f((uint16_t)(r.hd[j].y & 0xFFFF));
-            const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};  // 1024 + 32
-            uint32_t t[4];
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 const _Float16 a = (_Float16)(d * (float)(int8_t)((sc >> (8 * kk)) & 0xFF));
-                const h2 va = {a, a};
-                const dq_u32x2 lo = (kk & 1) ? r.q1[j] : r.q0[j];
-#pragma unroll
-                for (int wd = 0; wd < 2; ++wd) {
-                    const uint32_t l4 = kk < 2 ? (lo[wd] & 0x0F0F0F0Fu) : ((lo[wd] >> 4) & 0x0F0F0F0Fu);
-                    const uint32_t v6 = l4 | (((r.q2[j][wd] >> (2 * kk)) & 0x03030303u) << 4);
-                    bytes_to_h2(v6, bias, va, &t[2 * wd]);
-                }
-                bf[kk][j] = __builtin_bit_cast(h8, dq_u32x4{t[0], t[1], t[2], t[3]});
+                S.s[j][kk] = h2{a, a};
             }
         }
+    }
+}
+
+template <int KIND, int KK>
+__device__ __forceinline__ void b_frag(const BRaw& r, const BScale& S, h8 (&bf)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint32_t t[4];
+        if constexpr (KIND == B_Q4K) {
+            // KK 0: P0 low nibbles, 1: P1 low, 2: P0 high, 3: P1 high
+            const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
+            const dq_u32x2 src = (KK & 1) ? r.q1[j] : r.q0[j];
+            const uint32_t m0 = KK < 2 ? (src.x & 0x0F0F0F0Fu) : ((src.x >> 4) & 0x0F0F0F0Fu);
+            const uint32_t m1 = KK < 2 ? (src.y & 0x0F0F0F0Fu) : ((src.y >> 4) & 0x0F0F0F0Fu);
+            bytes_to_h2(m0, bias, S.s[j][KK], &t[0]);
+            bytes_to_h2(m1, bias, S.s[j][KK], &t[2]);
+        } else {
+            const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};  // 1024 + 32
+            const dq_u32x2 lo = (KK & 1) ? r.q1[j] : r.q0[j];
+#pragma unroll
+            for (int wd = 0; wd < 2; ++wd) {
+                const uint32_t l4 = KK < 2 ? (lo[wd] & 0x0F0F0F0Fu) : ((lo[wd] >> 4) & 0x0F0F0F0Fu);
+                const uint32_t v6 = l4 | (((r.q2[j][wd] >> (2 * KK)) & 0x03030303u) << 4);
+                bytes_to_h2(v6, bias, S.s[j][KK], &t[2 * wd]);
+            }
+        }
+        bf[j] = __builtin_bit_cast(h8, dq_u32x4{t[0], t[1], t[2], t[3]});
+    }
+}
+
+// A fragments of K slice kk for the wave's WM 32-token blocks (XOR-swizzled
+// 16-byte chunks of the stage's activation tile).
+template <int WM>
+__device__ __forceinline__ void a_frags(const uint8_t* base, int wm, int kk, int lane, h8 (&af)[WM]) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+        const int r = wm * 32 * WM + i * 32 + (lane & 31);
+        af[i] = lds_h8(base + (r * 8 + ((2 * kk + (lane >> 5)) ^ (r & 7))) * 16);
     }
 }
 
@@ -260,46 +291,51 @@ __device__ __forceinline__ void b_dequant(const BRaw& r, int G, h8 (&bf)[4][2], 
 // last step again, so every wave issues the same count per stage), then the
 // weight fragments (LDS bytes -> fp16 in registers) and the MFMAs; at the
 // last item of a super-block (Q4_K) also its min term.
-template <int BN, int KIND>
+template <int BN, int KIND, int WM>
 __device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* ring, int st, int stage, int s1,
-                                          f16v (&acc)[2][2], int wave, int lane) {
+                                          f16v (&acc)[WM][2], int wave, int lane) {
     const int G = st & 3;
-    using R = Ring<BN, KIND>;
+    using R = Ring<BN, KIND, WM>;
     constexpr int NS = R::NS;
-    constexpr int PER = stage_loads<BN, KIND>();
+    constexpr int PER = stage_loads<BN, KIND, WM>();
     const int wm = wave & 1, wn = wave >> 1;
     wait_vm<(NS - 2) * PER>();
     dq_lds_barrier();
-    issue_stage<BN, KIND>(g, ring, stage == 0 ? NS - 1 : stage - 1, min(st + NS - 1, s1 - 1), wave, lane);
+    issue_stage<BN, KIND, WM>(g, ring, stage == 0 ? NS - 1 : stage - 1, min(st + NS - 1, s1 - 1), wave, lane);
     const uint8_t* base = ring + stage * R::STAGE;
     BRaw raw;
     b_raw<BN, KIND>(base + R::B_OFF, wn, lane, raw);
-    h8 bf[4][2], bm[2];
-    b_dequant<KIND>(raw, G, bf, bm);
+    BScale S;
+    b_scales<KIND>(raw, G, S);
+    // The four K slices in order, slice kk+1's activation fragments (LDS)
+    // and weight fragments (VALU) written after slice kk's MFMAs so the
+    // scheduler can overlap them.
+    h8 af[4][WM], bf[4][2];
+    a_frags<WM>(base, wm, 0, lane, af[0]);
+    b_frag<KIND, 0>(raw, S, bf[0]);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-        h8 af[2];
+        if (kk == 0) { a_frags<WM>(base, wm, 1, lane, af[1]); b_frag<KIND, 1>(raw, S, bf[1]); }
+        if (kk == 1) { a_frags<WM>(base, wm, 2, lane, af[2]); b_frag<KIND, 2>(raw, S, bf[2]); }
+        if (kk == 2) { a_frags<WM>(base, wm, 3, lane, af[3]); b_frag<KIND, 3>(raw, S, bf[3]); }
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int r = wm * 64 + i * 32 + (lane & 31);
-            af[i] = lds_h8(base + (r * 8 + ((2 * kk + (lane >> 5)) ^ (r & 7))) * 16);
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[kk][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk][i], bf[kk][j], acc[i][j], 0, 0, 0);
     }
+    h8 bm[2];
+    if (KIND == B_Q4K && G == 3) bm[0] = q4k_neg_mins(raw.hd[0], true), bm[1] = q4k_neg_mins(raw.hd[1], true);
     if (KIND == B_Q4K && G == 3) {  // the super-block's min term
         const h8 zero = {};
-        h8 am[2];
+        h8 am[WM];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const h8 v = lds_h8(base + R::A_BYTES + (wm * 64 + i * 32 + (lane & 31)) * 16);
+        for (int i = 0; i < WM; ++i) {
+            const h8 v = lds_h8(base + R::A_BYTES + (wm * 32 * WM + i * 32 + (lane & 31)) * 16);
             am[i] = (lane >> 5) == 0 ? v : zero;
         }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[i], bm[j], acc[i][j], 0, 0, 0);
@@ -309,17 +345,17 @@ __device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* ring, int 
 // K steps [s0, s1), s0 and s1 multiples of 4 (whole super-blocks, so every
 // super-block's min term falls in one split): NS-1 stages in flight before
 // the first step, then one step at a time.
-template <int BN, int KIND>
-__device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* ring, int s0, int s1, f16v (&acc)[2][2],
+template <int BN, int KIND, int WM>
+__device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* ring, int s0, int s1, f16v (&acc)[WM][2],
                                           int wave, int lane) {
-    using R = Ring<BN, KIND>;
+    using R = Ring<BN, KIND, WM>;
     constexpr int NS = R::NS;
     if (s0 >= s1) return;
 #pragma unroll
-    for (int p = 0; p < NS - 1; ++p) issue_stage<BN, KIND>(g, ring, p, min(s0 + p, s1 - 1), wave, lane);
+    for (int p = 0; p < NS - 1; ++p) issue_stage<BN, KIND, WM>(g, ring, p, min(s0 + p, s1 - 1), wave, lane);
     int stage = 0;
     for (int st = s0; st < s1; ++st) {
-        gemm_step<BN, KIND>(g, ring, st, stage, s1, acc, wave, lane);
+        gemm_step<BN, KIND, WM>(g, ring, st, stage, s1, acc, wave, lane);
         stage = stage + 1 == NS ? 0 : stage + 1;
     }
     wait_vm<0>();  // drain the DMAs issued past the end
@@ -337,17 +373,20 @@ __device__ __forceinline__ void tile_of(int id, int mb, int nb, int* m_blk, int*
     *n_blk = t % nb;
 }
 
-// Register budget of two waves per SIMD (256 per lane): the wide tile runs
-// one 8-wave workgroup per CU; the narrow one (4 waves) one or two.
-template <int FMT, int BN>
-__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(GemmArgs g, float* __restrict__ y, int steps,
-                                                      int steps_per_split, int atomic_out) {
+// Register budget of two waves per SIMD (256 per lane): an 8-wave (BN 256)
+// workgroup per CU, or one or two 4-wave (BN 128) ones. Wave (wm, wn) owns
+// tokens wm*32*WM .. +32*WM and rows wn*64 .. +64 of the tile: WM 32x32
+// blocks by 2, so each dequantized weight fragment feeds WM MFMAs.
+template <int FMT, int BN, int WM>
+__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(
+    GemmArgs g, float* __restrict__ y, int steps, int steps_per_split, int atomic_out) {
     constexpr int KIND = FMT == DQ_FMT_Q4_K ? B_Q4K : B_Q6K;
-    __shared__ __align__(16) uint8_t ring[Ring<BN, KIND>::BYTES];
+    constexpr int BM = bm_of<WM>();
+    __shared__ __align__(16) uint8_t ring[Ring<BN, KIND, WM>::BYTES];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1, wn = wave >> 1;  // 2 x (BN/64) waves of 64x64
+    const int wm = wave & 1, wn = wave >> 1;  // 2 x (BN/64) waves of (32*WM) x 64
     int m_blk, n_blk;
     tile_of(blockIdx.x, (g.M + BM - 1) / BM, (g.N + BN - 1) / BN, &m_blk, &n_blk);
     g.n0 = n_blk * BN;
@@ -355,43 +394,42 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     const int s0 = blockIdx.z * steps_per_split;
     const int s1 = min(steps, s0 + steps_per_split);
 
-    f16v acc[2][2];
+    f16v acc[WM][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    run_steps<BN, KIND>(g, ring, s0, s1, acc, wave, lane);
+    run_steps<BN, KIND, WM>(g, ring, s0, s1, acc, wave, lane);
 
     // D layout of 32x32x16: lane l, register r -> n = l%32, m = (r/4)*8 + (l/32)*4 + r%4.
-    // The row factors 1/s are loaded together up front (unconditional loads
-    // of clamped rows; a load inside the store's branch would be waited for
-    // one at a time).
-    float inv[2][16];
+    // The row factors 1/s of a 32-token block are loaded together before its
+    // stores (unconditional loads of clamped rows; a load inside the store's
+    // branch would be waited for one at a time).
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < WM; ++i) {
+        const int mb0 = g.m0 + wm * 32 * WM + i * 32 + (lane >> 5) * 4;
+        float inv[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            inv[i][r] = g.inv[min(g.m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3), g.M - 1)];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int r = 0; r < 16; ++r) inv[r] = g.inv[min(mb0 + (r >> 2) * 8 + (r & 3), g.M - 1)];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int n = g.n0 + wn * 64 + j * 32 + (lane & 31);
             if (n >= g.N) continue;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = g.m0 + wm * 64 + i * 32 + (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3);
+                const int m = mb0 + (r >> 2) * 8 + (r & 3);
                 if (m < g.M) {
                     float* dst = y + (size_t)m * g.N + n;
-                    const float v = acc[i][j][r] * inv[i][r];  // a power of two: exact
+                    const float v = acc[i][j][r] * inv[r];  // a power of two: exact
                     if (atomic_out) atomicAdd(dst, v);
                     else *dst = v;
                 }
             }
         }
+    }
 }
 
 // Activation quantizer for the GEMM: per 32-block the reference integers and
@@ -482,7 +520,11 @@ int cus() {
 
 // Workspace of the GEMM: the activation [n_tok][cols] fp16, for Q4_K the
 // block sums [cols/256][n_tok][8] fp16, then the row scales s and 1/s [n_tok].
-static size_t act_bytes(size_t cols, size_t n_tok) { return dq_align256(n_tok * cols * 2); }
+// Row stride of the fp16 activation: cols plus 64 halves (128 bytes), so the
+// rows a K step reads (same column, consecutive tokens) fall on different L2
+// channels; at a power-of-two stride they would all queue on one channel.
+static size_t act_lda(size_t cols) { return cols + 64; }
+static size_t act_bytes(size_t cols, size_t n_tok) { return dq_align256(n_tok * act_lda(cols) * 2); }
 static size_t min_bytes(int fmt, size_t cols, size_t n_tok) {
     return fmt == DQ_FMT_Q4_K ? dq_align256(n_tok * (cols / 32) * 2) : 0;
 }
@@ -518,24 +560,52 @@ extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_
     float* inv = (float*)(base + inv_off(fmt, cols, n_tok));
     row_scale_kernel<<<(unsigned)n_tok, 256, 0, (hipStream_t)stream>>>(d_x, (int)cols, sc);
     quantize_f16_kernel<<<(unsigned)((lanes + 255) / 256), 256, 0, (hipStream_t)stream>>>(
-        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)cols, minp, fmt == DQ_FMT_Q6_K, sc, inv);
+        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)act_lda(cols), minp, fmt == DQ_FMT_Q6_K, sc, inv);
     return dq_launch_status();
 }
 
-template <int FMT, int BN>
-static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int steps, float* d_y, hipStream_t s) {
+template <int FMT, int BN, int WM>
+static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int steps, int split, float* d_y, hipStream_t s) {
+    constexpr int BM = bm_of<WM>();
     const int mb = (int)((n_tok + BM - 1) / BM), nb = (int)((rows + BN - 1) / BN);
-    // split K in two when the tile grid leaves CUs idle (two partials added
-    // atomically into zeroed y: a+b == b+a, so the result is deterministic)
-    const int split = ((size_t)mb * nb * 2 <= (size_t)cus() && steps >= 8) ? 2 : 1;
     const int per = (steps / 4 + split - 1) / split * 4;  // whole super-blocks per split
     if (split > 1) {
         const size_t n = rows * n_tok;
         zero_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(d_y, n);
     }
     const dim3 grid((unsigned)(mb * nb), 1, split);
-    gemm_kernel<FMT, BN><<<grid, 2 * BN, 0, s>>>(g, d_y, steps, per, split > 1);
+    gemm_kernel<FMT, BN, WM><<<grid, 2 * BN, 0, s>>>(g, d_y, steps, per, split > 1);
     return dq_launch_status();
+}
+
+// Tile shape and K split. The K split is 2 when the tile grid leaves at
+// least half the CUs idle (two partials added atomically into zeroed y:
+// a+b == b+a, so the result is deterministic). Default: 128x256 tiles (8
+// waves of 64x64) when their grid, split included, covers 7/8 of the CUs,
+// else 128x128. The 256x256 tile (waves of 128x64, each weight fragment
+// feeding 4 MFMAs) is selectable with DQ_GEMM_WM=4 for tuning; it measured
+// slower at M = 512 (fewer, longer steps; the step is bound by its VALU and
+// LDS issue, not by the MFMA count).
+struct GemmPlan {
+    int bn, wm, split;
+};
+static size_t bm_of_rt(int wm) { return (size_t)64 * wm; }
+static GemmPlan plan_gemm(size_t rows, size_t n_tok, int steps) {
+    const size_t c = (size_t)cus();
+    auto make = [&](int bn, int wm) {
+        const size_t tiles = ((n_tok + bm_of_rt(wm) - 1) / bm_of_rt(wm)) * ((rows + bn - 1) / bn);
+        const int split = (tiles * 2 <= c && steps >= 8) ? 2 : 1;
+        return std::pair<GemmPlan, size_t>{GemmPlan{bn, wm, split}, tiles * split};
+    };
+    const char* fw = getenv("DQ_GEMM_WM");  // tuning overrides: tile shape and K split
+    const char* fs = getenv("DQ_GEMM_SPLIT");
+    GemmPlan pl;
+    const auto wide = make(256, 2);
+    if (fw) pl = atoi(fw) == 4 ? make(256, 4).first : atoi(fw) == 2 ? wide.first : make(128, 2).first;
+    else if (wide.second * 8 >= c * 7) pl = wide.first;
+    else pl = make(128, 2).first;
+    if (fs && (atoi(fs) == 1 || atoi(fs) == 2)) pl.split = atoi(fs);
+    return pl;
 }
 
 // GEMM on the workspace written by dq_quantize_act_f16.
@@ -554,19 +624,20 @@ extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols
     g.A = (const _Float16*)d_work;
     g.minp = (const _Float16*)((const uint8_t*)d_work + min_off(cols, n_tok));
     g.inv = (const float*)((const uint8_t*)d_work + inv_off(fmt, cols, n_tok));
-    g.lda = (int)cols;
+    g.lda = (int)act_lda(cols);
     g.M = (int)n_tok;
     g.N = (int)rows;
     g.K = (int)cols;
     const int steps = (int)cols / BK;
-    // wide tiles (less activation re-reading) when they still fill the CUs
-    const size_t mb = (n_tok + BM - 1) / BM;
-    const bool wide = mb * ((rows + 255) / 256) * 8 >= (size_t)cus() * 7;
-    if (fmt == DQ_FMT_Q4_K)
-        return wide ? launch_gemm<DQ_FMT_Q4_K, 256>(g, rows, n_tok, steps, d_y, s)
-                    : launch_gemm<DQ_FMT_Q4_K, 128>(g, rows, n_tok, steps, d_y, s);
-    return wide ? launch_gemm<DQ_FMT_Q6_K, 256>(g, rows, n_tok, steps, d_y, s)
-                : launch_gemm<DQ_FMT_Q6_K, 128>(g, rows, n_tok, steps, d_y, s);
+    const GemmPlan pl = plan_gemm(rows, n_tok, steps);
+    if (fmt == DQ_FMT_Q4_K) {
+        if (pl.wm == 4) return launch_gemm<DQ_FMT_Q4_K, 256, 4>(g, rows, n_tok, steps, pl.split, d_y, s);
+        if (pl.bn == 256) return launch_gemm<DQ_FMT_Q4_K, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
+        return launch_gemm<DQ_FMT_Q4_K, 128, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
+    }
+    if (pl.wm == 4) return launch_gemm<DQ_FMT_Q6_K, 256, 4>(g, rows, n_tok, steps, pl.split, d_y, s);
+    if (pl.bn == 256) return launch_gemm<DQ_FMT_Q6_K, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
+    return launch_gemm<DQ_FMT_Q6_K, 128, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
 }
 
 extern "C" int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,
