@@ -29,7 +29,6 @@ namespace {
 
 constexpr int TP = 64;         // positions per tile
 constexpr int NT = 256;        // threads per workgroup
-constexpr int MCH = 256;       // tiles per merge chunk
 
 __device__ __forceinline__ int read_pos(int pos_host, const int* pos_dev, int n_ctx) {
     int p = pos_dev ? *pos_dev : pos_host;
@@ -329,27 +328,25 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
 }
 
 // Merge of the tile records: workgroup b owns outputs [256b, 256b + 256) of
-// the flattened [n_head][HD] output (HD = 128: two heads). Per head: M = max
-// over tiles of m_t; then in chunks of MCH tiles the weights w_t = e^(m_t -
-// M) go to LDS, L = sum w_t l_t and out = sum w_t acc_t / L. The MG thread
-// groups of the workgroup take every MG-th tile, each issuing its record
-// loads in batches of 16 (one round trip per batch instead of one per tile);
-// the MG partial sums are added in group order. Optionally quantizes the 256
-// outputs per 256 (core/matmul.cpp:1660-1778).
+// the flattened [n_head][HD] output (HD = 128: two heads). Thread (g, o)
+// takes tiles g, g+MG, ... of its head in batches of MB (all of a batch's
+// record loads in flight at once: one memory round trip for up to MG*MB
+// tiles) and keeps an online softmax state (running max M, sum L of
+// e^(m_t - M) l_t, and acc of e^(m_t - M) acc_t); the MG group states are then
+// combined in group order, each rescaled to the common max. Optionally
+// quantizes the 256 outputs per 256 (core/matmul.cpp:1660-1778).
 constexpr int MG = 4;                 // tile groups of the merge
 constexpr int MNO = 256;              // outputs per merge workgroup
 constexpr int MNT = MG * MNO;         // its threads
-constexpr int MB = 16;                // record loads per batch
+constexpr int MB = 20;                // tiles per batch and thread
 template <int HD, int HPK>
 __global__ __launch_bounds__(MNT) void attn_merge_kernel(AttnArgs A) {
     constexpr int REC = HD + 2;
     constexpr int HPB = MNO / HD;        // heads per block
     constexpr int NWV = MNT / 64;        // waves
     static_assert(MNO % HD == 0 && MNO == NT, "whole heads per block");
-    __shared__ float mtot[HPB];
     __shared__ float wred[NWV];
-    __shared__ float mw[HPB][MCH];
-    __shared__ float ml[HPB][MCH];
+    __shared__ float gm[MG][HPB], gl[MG][HPB];
     __shared__ float pacc[MG][MNO];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = tid / MNO, ol = tid % MNO;     // tile group, output in the block
@@ -360,75 +357,53 @@ __global__ __launch_bounds__(MNT) void attn_merge_kernel(AttnArgs A) {
     const int hb = ol / HD;                       // head within the block
     const int hq = blockIdx.x * HPB + hb;         // query head
     const int kvh = hq / HPK, h = hq % HPK, dd = o % HD;
-    const float* recs = A.part + (size_t)kvh * A.max_tiles * HPK * REC;
-    // per-head max: the waves of a head (every (g, 64-output) wave whose
-    // outputs lie in it) split the tiles
-    {
-        constexpr int WPH = NWV / HPB;  // waves per head
-        const int wi = g * (HD / 64) + (ol % HD) / 64;  // this wave's index among its head's waves
-        float M = -INFINITY;
-        for (int t0 = wi * 64; t0 < n_tiles; t0 += 64 * WPH) {
-            const int t = t0 + lane;
-            const float m = recs[(min(t, n_tiles - 1) * HPK + h) * REC + HD];
-            if (t < n_tiles) M = fmaxf(M, m);
-        }
-        M = dq_wave_max(M);
-        if (lane == 0) wred[wave] = M;
-        __syncthreads();
-        if (tid < HPB) {
-            // waves of head j: those whose outputs (wave % (MNO/64)) fall in head j
-            float m = -INFINITY;
-            for (int w = 0; w < NWV; ++w)
-                if (((w % (MNO / 64)) * 64) / HD == tid) m = fmaxf(m, wred[w]);
-            mtot[tid] = m;
-        }
-    }
-    float a = 0.0f;
-    for (int t0 = 0; t0 < n_tiles; t0 += MCH) {
-        const int nt = min(MCH, n_tiles - t0);
-        __syncthreads();  // mtot ready / the previous chunk consumed
-        for (int i = tid; i < HPB * nt; i += MNT) {
-            const int j = i / nt, t = t0 + i % nt;
-            const int hj = (blockIdx.x * HPB + j) % HPK, kj = (blockIdx.x * HPB + j) / HPK;
-            const float* r = A.part + ((size_t)kj * A.max_tiles * HPK + (size_t)t * HPK + hj) * REC;
-            const float w = __expf(r[HD] - mtot[j]);
-            mw[j][i % nt] = w;
-            ml[j][i % nt] = w * r[HD + 1];
-        }
-        __syncthreads();
-        const float* base = recs + ((size_t)t0 * HPK + h) * REC + dd;
-        for (int tb = g; tb < nt; tb += MG * MB) {
-            float v[MB];
+    const float* recs = A.part + ((size_t)kvh * A.max_tiles * HPK + h) * REC;  // tile t at + t*HPK*REC
+    float M = -INFINITY, L = 0.0f, a = 0.0f;
+    for (int tb = g; tb < n_tiles; tb += MG * MB) {
+        float v[MB], mm[MB], ll[MB];
 #pragma unroll
-            for (int k = 0; k < MB; ++k) v[k] = base[(size_t)min(tb + MG * k, nt - 1) * HPK * REC];
-#pragma unroll
-            for (int k = 0; k < MB; ++k)
-                if (tb + MG * k < nt) a = fmaf(mw[hb][tb + MG * k], v[k], a);
+        for (int k = 0; k < MB; ++k) {
+            const float* r = recs + (size_t)min(tb + MG * k, n_tiles - 1) * HPK * REC;
+            v[k] = r[dd];
+            mm[k] = r[HD];
+            ll[k] = r[HD + 1];
         }
+        float bm = M;
+#pragma unroll
+        for (int k = 0; k < MB; ++k)
+            if (tb + MG * k < n_tiles) bm = fmaxf(bm, mm[k]);
+        const float sc = __expf(M - bm);  // M = -inf on the first batch: 0
+        a *= sc;
+        L *= sc;
+#pragma unroll
+        for (int k = 0; k < MB; ++k)
+            if (tb + MG * k < n_tiles) {
+                const float w = __expf(mm[k] - bm);
+                a = fmaf(w, v[k], a);
+                L = fmaf(w, ll[k], L);
+            }
+        M = bm;
     }
     pacc[g][ol] = a;
+    if (dd == 0) {
+        gm[g][hb] = M;
+        gl[g][hb] = L;
+    }
     __syncthreads();
     // group 0 (waves 0 .. MNO/64-1) finishes; the others stay for the barriers
     float v = 0.0f;
     if (g == 0) {
-        float L = 0.0f;
-        for (int t0 = 0; t0 < n_tiles; t0 += MCH) {
-            // the last chunk's l weights are still in LDS; earlier chunks'
-            // are recomputed from the records
-            const int nt = min(MCH, n_tiles - t0);
-            if (t0 + MCH >= n_tiles) {
-                for (int t = 0; t < nt; ++t) L += ml[hb][t];
-            } else {
-                for (int t = 0; t < nt; ++t) {
-                    const float* r = recs + ((size_t)(t0 + t) * HPK + h) * REC;
-                    L += __expf(r[HD] - mtot[hb]) * r[HD + 1];
-                }
-            }
-        }
-        float acc = pacc[0][ol];
+        float Mt = gm[0][hb];
 #pragma unroll
-        for (int q = 1; q < MG; ++q) acc += pacc[q][ol];
-        v = acc / L;
+        for (int q = 1; q < MG; ++q) Mt = fmaxf(Mt, gm[q][hb]);
+        float acc = 0.0f, Lt = 0.0f;
+#pragma unroll
+        for (int q = 0; q < MG; ++q) {
+            const float w = __expf(gm[q][hb] - Mt);  // a group with no tile: e^-inf = 0
+            acc = fmaf(w, pacc[q][ol], acc);
+            Lt = fmaf(w, gl[q][hb], Lt);
+        }
+        v = acc / Lt;
         A.out[o] = v;
     }
     if (!A.oq) return;  // uniform
