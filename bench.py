@@ -450,7 +450,7 @@ def main():
     roofline = {"bound": "hbm", "achieved": dom["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(),
                 "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
-                "kernel": "gemv_kernel<Q4_K> 14336x4096",
+                "kernel": "gemv_flat_kernel<Q4_K> 14336x4096 (dq_gemv)",
                 "bytes_per_launch": gemv_kernel_bytes(synth.Q4_K, 14336, 4096)}
 
     cpu = None if args.no_cpu else cpu_baseline_q4k()
