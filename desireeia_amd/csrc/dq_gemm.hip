@@ -102,6 +102,7 @@ struct GemmArgs {
     const float* inv;       // per token: 1/s of its activation row
     int lda, M, N, K;
     int m0, n0;
+    uint32_t magic;         // 0x54005400 (kept in a register: see run_steps)
 };
 
 // Issues the DMA of K step `st` (weights and activations) into ring stage
@@ -220,7 +221,8 @@ __device__ __forceinline__ void b_raw(const uint8_t* bb, int wn, int lane, BRaw&
 // of every (j, KK): Q4_K a = d*sc of sub-block 2G (KK 0, 1: low nibbles) or
 // 2G+1 (KK 2, 3: high nibbles); Q6_K a = d*sc of the KK-th 16-block.
 struct BScale {
-    h2 s[2][4];
+    h2 s[2][4];  // Q6_K: scale pair per (j, KK); Q4_K: low-nibble a, high-nibble a, -64a of each
+    uint32_t magic;
 };
 
 template <int KIND>
@@ -232,8 +234,11 @@ __device__ __forceinline__ void b_scales(const BRaw& r, int G, BScale& S) {
             const float d = dq_h2f((uint16_t)(hd.x & 0xFFFF));
             const _Float16 a0 = (_Float16)(d * (float)q4k_scale(2 * G, hd.y, hd.z, hd.w));
             const _Float16 a1 = (_Float16)(d * (float)q4k_scale(2 * G + 1, hd.y, hd.z, hd.w));
-            S.s[j][0] = S.s[j][1] = h2{a0, a0};
-            S.s[j][2] = S.s[j][3] = h2{a1, a1};
+            S.s[j][0] = h2{a0, a0};
+            S.s[j][1] = h2{a1, a1};
+            // -64a is exact while |a| < 1024 (64*a stays below the fp16 maximum)
+            S.s[j][2] = h2{(_Float16)(-64.0f) * a0, (_Float16)(-64.0f) * a0};
+            S.s[j][3] = h2{(_Float16)(-64.0f) * a1, (_Float16)(-64.0f) * a1};
         } else {
             const uint32_t sc = r.hd[j].x;
             const float d = dq_h2f((uint16_t)(r.hd[j].y & 0xFFFF));
@@ -252,13 +257,25 @@ __device__ __forceinline__ void b_frag(const BRaw& r, const BScale& S, h8 (&bf)[
     for (int j = 0; j < 2; ++j) {
         uint32_t t[4];
         if constexpr (KIND == B_Q4K) {
-            // KK 0: P0 low nibbles, 1: P1 low, 2: P0 high, 3: P1 high
-            const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
-            const dq_u32x2 src = (KK & 1) ? r.q1[j] : r.q0[j];
-            const uint32_t m0 = KK < 2 ? (src.x & 0x0F0F0F0Fu) : ((src.x >> 4) & 0x0F0F0F0Fu);
-            const uint32_t m1 = KK < 2 ? (src.y & 0x0F0F0F0Fu) : ((src.y >> 4) & 0x0F0F0F0Fu);
-            bytes_to_h2(m0, bias, S.s[j][KK], &t[0]);
-            bytes_to_h2(m1, bias, S.s[j][KK], &t[2]);
+            // KK 0, 1: P0 bytes 8h..8h+3, 8h+4..8h+7; KK 2, 3: the same of P1.
+            // From the dword's bytes B0..B3, a nibble ORed into mantissa bits
+            // 7:4 under the exponent of 64 (0x5400) is the fp16 64 + q exactly,
+            // two per v_and_or; fma(64 + q, a, -64a) = q*a rounded once (as
+            // (q)*a would be). Fragment order (the activation tile is permuted
+            // to match, dq_quantize_act_f16): lo B0, lo B2, hi B0, hi B2, lo B1,
+            // lo B3, hi B1, hi B3; lo = sub-block 2G (scale a0), hi = 2G+1 (a1).
+            const dq_u32x2 src = KK < 2 ? r.q0[j] : r.q1[j];
+            const uint32_t w = (KK & 1) ? src.y : src.x;
+            // the exponent pattern comes from a register (S.magic): with both
+            // operands literal the compiler splits each v_and_or into two
+            const uint32_t e0 = ((w << 4) & 0x00F000F0u) | S.magic;
+            const uint32_t e1 = (w & 0x00F000F0u) | S.magic;
+            const uint32_t e2 = ((w >> 4) & 0x00F000F0u) | S.magic;
+            const uint32_t e3 = ((w >> 8) & 0x00F000F0u) | S.magic;
+            t[0] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, e0), S.s[j][0], S.s[j][2]));
+            t[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, e1), S.s[j][1], S.s[j][3]));
+            t[2] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, e2), S.s[j][0], S.s[j][2]));
+            t[3] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, e3), S.s[j][1], S.s[j][3]));
         } else {
             const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};  // 1024 + 32
             const dq_u32x2 lo = (KK & 1) ? r.q1[j] : r.q0[j];
@@ -293,7 +310,7 @@ __device__ __forceinline__ void a_frags(const uint8_t* base, int wm, int kk, int
 // last item of a super-block (Q4_K) also its min term.
 template <int BN, int KIND, int WM>
 __device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* ring, int st, int stage, int s1,
-                                          f16v (&acc)[WM][2], int wave, int lane) {
+                                          f16v (&acc)[WM][2], int wave, int lane, uint32_t magic) {
     const int G = st & 3;
     using R = Ring<BN, KIND, WM>;
     constexpr int NS = R::NS;
@@ -306,6 +323,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* ring, int 
     BRaw raw;
     b_raw<BN, KIND>(base + R::B_OFF, wn, lane, raw);
     BScale S;
+    S.magic = magic;
     b_scales<KIND>(raw, G, S);
     // The four K slices in order, slice kk+1's activation fragments (LDS)
     // and weight fragments (VALU) written after slice kk's MFMAs so the
@@ -353,9 +371,14 @@ __device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* ring, int 
     if (s0 >= s1) return;
 #pragma unroll
     for (int p = 0; p < NS - 1; ++p) issue_stage<BN, KIND, WM>(g, ring, p, min(s0 + p, s1 - 1), wave, lane);
+    // the fp16 exponent pattern of the Q4_K nibble conversion in a VGPR (an
+    // identity DPP move the compiler cannot fold), so each nibble pair is one
+    // v_and_or_b32 (literal mask, register pattern) instead of an and + or
+    const uint32_t magic =
+        (uint32_t)__builtin_amdgcn_update_dpp((int)g.magic, (int)g.magic, 0xE4, 0xF, 0xF, false);
     int stage = 0;
     for (int st = s0; st < s1; ++st) {
-        gemm_step<BN, KIND, WM>(g, ring, st, stage, s1, acc, wave, lane);
+        gemm_step<BN, KIND, WM>(g, ring, st, stage, s1, acc, wave, lane, magic);
         stage = stage + 1 == NS ? 0 : stage + 1;
     }
     wait_vm<0>();  // drain the DMAs issued past the end
@@ -484,6 +507,19 @@ __global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restri
         dq_u32x4* dst = reinterpret_cast<dq_u32x4*>(o + 32 * b);
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = __builtin_bit_cast(dq_u32x4, *reinterpret_cast<const h8*>(&h[8 * i]));
+    } else if (perm == 2) {
+        // Q4_K fragment order (gemm b_frag): block b is half hi = b % 2 (the
+        // high nibbles) of item g = (b % 8) / 2; its element e is byte j = e of
+        // the item's 32 qs bytes, in sub-plane j / 16, lane half (j % 16) / 8,
+        // slice KK = 2 * plane + (j % 8) / 4, fragment slot f = 4 * (bo & 1) +
+        // (bo >> 1) + 2 * hi with bo = j % 4; column 16 KK + 8 half + f.
+        const int hi = b & 1;
+        _Float16* item = o + 64 * (size_t)(b / 2);
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const int pl = e / 16, hf = (e % 16) / 8, kk = 2 * pl + (e % 8) / 4, bo = e % 4;
+            item[16 * kk + 8 * hf + 4 * (bo & 1) + (bo >> 1) + 2 * hi] = h[e];
+        }
     } else {
         // Q6_K item order: position pos in the 256-block -> column
         // s*256 + (2n+k)*64 + qq*16 + e, with pos = 128n + 32qq + 16k + e.
@@ -560,7 +596,7 @@ extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_
     float* inv = (float*)(base + inv_off(fmt, cols, n_tok));
     row_scale_kernel<<<(unsigned)n_tok, 256, 0, (hipStream_t)stream>>>(d_x, (int)cols, sc);
     quantize_f16_kernel<<<(unsigned)((lanes + 255) / 256), 256, 0, (hipStream_t)stream>>>(
-        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)act_lda(cols), minp, fmt == DQ_FMT_Q6_K, sc, inv);
+        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)act_lda(cols), minp, fmt == DQ_FMT_Q6_K ? 1 : 2, sc, inv);
     return dq_launch_status();
 }
 
@@ -625,6 +661,7 @@ extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols
     g.minp = (const _Float16*)((const uint8_t*)d_work + min_off(cols, n_tok));
     g.inv = (const float*)((const uint8_t*)d_work + inv_off(fmt, cols, n_tok));
     g.lda = (int)act_lda(cols);
+    g.magic = 0x54005400u;
     g.M = (int)n_tok;
     g.N = (int)rows;
     g.K = (int)cols;
