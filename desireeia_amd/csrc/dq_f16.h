@@ -28,16 +28,19 @@ __device__ __forceinline__ void bytes_to_h2(uint32_t v, h2 bias, h2 a, uint32_t*
 // Q4_K 6-bit scale of sub-block j from header words w0 (scale bytes 0-3),
 // w1 (4-7), w2 (8-11) (quant/quant.cpp:22-29).
 // Branch-free (j may be a run-time value): both forms are computed from the
-// byte at position j & 3 and one is selected.
+// byte at position j & 3 and one is kept by a bit mask (a ?: on a uniform j
+// is compiled into branches).
 __device__ __forceinline__ int q4k_scale(int j, uint32_t w0, uint32_t w1, uint32_t w2) {
     const int sh = 8 * (j & 3);
     const uint32_t b0 = (w0 >> sh) & 0xFF, b2 = (w2 >> sh) & 0xFF;
-    return (int)(j < 4 ? (b0 & 63) : ((b2 & 0xF) | ((b0 >> 6) << 4)));
+    const uint32_t hi = 0u - (uint32_t)(j >> 2);  // all ones for j >= 4
+    return (int)(((b0 & 63) & ~hi) | (((b2 & 0xF) | ((b0 >> 6) << 4)) & hi));
 }
 __device__ __forceinline__ int q4k_min(int j, uint32_t w0, uint32_t w1, uint32_t w2) {
     const int sh = 8 * (j & 3);
     const uint32_t b1 = (w1 >> sh) & 0xFF, b2 = (w2 >> sh) & 0xFF;
-    return (int)(j < 4 ? (b1 & 63) : ((b2 >> 4) | ((b1 >> 6) << 4)));
+    const uint32_t hi = 0u - (uint32_t)(j >> 2);
+    return (int)(((b1 & 63) & ~hi) | (((b2 >> 4) | ((b1 >> 6) << 4)) & hi));
 }
 
 // The 8 values fp16(-dmin * m_j) of a Q4_K super-block header hd (d and dmin

@@ -294,15 +294,15 @@ __device__ __forceinline__ void compute_group(const typename Fmt<FMT>::W (&wr)[R
             const float p = Fmt<FMT>::dot(wr[rr][it], X[it], i);
             a += i < i1 ? p : 0.0f;
         }
-        acc[rr] = a;
+        // each row's sum over the wave (DPP row reductions + readlanes,
+        // uniform) right after its dot products, so that only the last row's
+        // reduction is left once the last weights land
+        acc[rr] = dq_wave_sum_uniform(a);
         // row by row: the scheduler would otherwise sink every row's dot
         // products below the wait for the last row's weights
         __builtin_amdgcn_sched_barrier(0);
     }
-    // each row's sum over the wave: DPP row reductions + readlanes (uniform)
-    float tot[R];
-#pragma unroll
-    for (int rr = 0; rr < R; ++rr) tot[rr] = dq_wave_sum_uniform(acc[rr]);
+    const float (&tot)[R] = acc;
     int gl = 0;
     const int j = job_of(J, g, &gl);
     float* __restrict__ y = J.y[j];
