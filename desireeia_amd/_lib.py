@@ -49,6 +49,28 @@ SIGNATURES = {
     "dq_moe_route": (c_int, [c_p, c_u32, c_u32, c_u32, c_int, c_f, c_p, c_p, c_p]),
     "dq_moe_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
     "dq_moe_ffn": (c_int, [c_p, c_p, c_p, c_u32, c_p, c_p, c_size, c_p]),
+    # GGUF files (host)
+    "dq_row_size": (c_size, [c_int, c_i64]),
+    "dq_fmt_of_gguf_type": (c_int, [c_int]),
+    "dq_gguf_open": (c_int, [ctypes.c_char_p, c_p]),
+    "dq_gguf_close": (None, [c_p]),
+    "dq_gguf_version": (c_int, [c_p]),
+    "dq_gguf_data_offset": (ctypes.c_uint64, [c_p]),
+    "dq_gguf_kv_count": (c_i64, [c_p]),
+    "dq_gguf_kv_key": (ctypes.c_char_p, [c_p, c_i64]),
+    "dq_gguf_kv_type": (c_int, [c_p, ctypes.c_char_p]),
+    "dq_gguf_get_int": (c_int, [c_p, ctypes.c_char_p, ctypes.POINTER(c_i64)]),
+    "dq_gguf_get_float": (c_int, [c_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "dq_gguf_get_str": (c_int, [c_p, ctypes.c_char_p, ctypes.POINTER(c_p), ctypes.POINTER(ctypes.c_uint64)]),
+    "dq_gguf_get_array": (c_int, [c_p, ctypes.c_char_p, ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_uint64),
+                                  ctypes.POINTER(c_p)]),
+    "dq_gguf_n_tensors": (c_i64, [c_p]),
+    "dq_gguf_find_tensor": (c_i64, [c_p, ctypes.c_char_p]),
+    "dq_gguf_tensor_info": (c_int, [c_p, c_i64, c_p]),
+    "dq_gguf_read_tensor_raw": (c_int, [c_p, ctypes.c_char_p, c_p, c_size, ctypes.POINTER(c_int),
+                                        ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "dq_gguf_upload": (c_int, [c_p, ctypes.c_char_p, ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_uint64),
+                               ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(c_p), ctypes.POINTER(c_p)]),
     # engine layer (core/engine.h GPU block); struct arguments as void*
     "cuda_gpu_count": (ctypes.c_int32, []),
     "cuda_probe_gpu": (ctypes.c_bool, [ctypes.c_int32, c_p, c_size, c_p, c_p, c_p, c_p, c_p]),
@@ -82,6 +104,12 @@ SIGNATURES = {
     "cuda_prefill_chunk_tokens": (c_int, []),
 }
 
+
+
+class GgufTensor(ctypes.Structure):
+    """dq_gguf_tensor_t"""
+    _fields_ = [("name", ctypes.c_char_p), ("type", c_int), ("n_dims", c_int), ("dims", ctypes.c_uint64 * 4),
+                ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64), ("data", c_p)]
 
 
 class CudaKQuantJob(ctypes.Structure):

@@ -437,6 +437,69 @@ int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, 
 int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* args);
 int cuda_prefill_chunk_tokens(void);
 
+/* ------------------------------------------------------------------------
+ * GGUF model files (host): the engine's GgufReader (src/gguf/gguf_reader.cpp
+ * :100-305, ModelReader::open / read_tensor_raw) over a read-only memory map,
+ * and the upload its caller load_matrix (models/dense_forward.cpp:1628-1720)
+ * does through cuda_upload_weights. Header, metadata and tensor directory are
+ * parsed and bounds-checked at open; for version >= 2 tensor offsets are
+ * relative to the data section (end of the tensor infos rounded up to
+ * general.alignment, default 32), for version < 2 they are absolute, as the
+ * engine reads them. Errors: DQ_ERR_IO (cannot open or map the file),
+ * DQ_ERR_INVALID_ARG (not GGUF, truncated or malformed; a null argument),
+ * DQ_ERR_NOT_SUPPORTED (no such key / tensor, or a type without a known row
+ * size). Pointers returned (names, strings, array and tensor data) point into
+ * the map and stay valid until dq_gguf_close. Not thread-safe per handle.
+ * ---------------------------------------------------------------------- */
+typedef struct dq_gguf dq_gguf;
+
+typedef struct {
+    const char* name;
+    int type;           /* GGUF tensor type id (quant/quant.h:439-476) */
+    int n_dims;
+    uint64_t dims[4];   /* ne0 (columns) first; unused dims are 1 */
+    uint64_t offset;    /* absolute file offset of the tensor's bytes */
+    uint64_t nbytes;    /* row_size(type, ne0) * rows; 0 for an unknown type */
+    const void* data;   /* the bytes in the map (NULL when nbytes is 0) */
+} dq_gguf_tensor_t;
+
+/* desireeia_row_size (quant/quant.cpp:905-910): bytes of ne0 values of a
+ * tensor type; 0 for an unknown type. */
+size_t dq_row_size(int type, int64_t ne0);
+/* GGUF type -> backend format id (DQ_FMT_*), -1 where the device path has no kernels. */
+int dq_fmt_of_gguf_type(int type);
+
+int dq_gguf_open(const char* path, dq_gguf** out);
+void dq_gguf_close(dq_gguf* g);
+int dq_gguf_version(const dq_gguf* g);
+uint64_t dq_gguf_data_offset(const dq_gguf* g);
+int64_t dq_gguf_kv_count(const dq_gguf* g);
+const char* dq_gguf_kv_key(const dq_gguf* g, int64_t i);
+/* value type of a key (0-12 as in the file), -1 if absent */
+int dq_gguf_kv_type(const dq_gguf* g, const char* key);
+/* integer kinds (U8..I32, BOOL, U64, I64) */
+int dq_gguf_get_int(const dq_gguf* g, const char* key, int64_t* v);
+/* any numeric kind */
+int dq_gguf_get_float(const dq_gguf* g, const char* key, double* v);
+int dq_gguf_get_str(const dq_gguf* g, const char* key, const char** s, uint64_t* len);
+/* arrays: element type, count and the raw elements (scalar elements packed;
+ * string elements as u64 length + bytes each) */
+int dq_gguf_get_array(const dq_gguf* g, const char* key, int* elem_type, uint64_t* n, const void** data);
+int64_t dq_gguf_n_tensors(const dq_gguf* g);
+/* index of a tensor by name, -1 if absent */
+int64_t dq_gguf_find_tensor(const dq_gguf* g, const char* name);
+int dq_gguf_tensor_info(const dq_gguf* g, int64_t i, dq_gguf_tensor_t* out);
+/* ModelReader::read_tensor_raw (gguf_reader.cpp:288-305): copies the tensor's
+ * bytes to dst (cap bytes available; dst NULL: sizes only) and reports its
+ * type, ne0 and rows = prod(dims[1..]). */
+int dq_gguf_read_tensor_raw(const dq_gguf* g, const char* name, void* dst, size_t cap, int* type, uint64_t* ne0,
+                            uint64_t* rows);
+/* Uploads a Q8_0 / Q4_0 / Q4_K / Q6_K matrix into the device layout with
+ * cuda_upload_weights (release with cuda_free_device), straight from the map:
+ * fmt, rows, cols and the engine's (d_qs, d_scale) pair. */
+int dq_gguf_upload(const dq_gguf* g, const char* name, int* fmt, uint64_t* rows, uint64_t* cols, void** d_qs,
+                   void** d_scale);
+
 #ifdef __cplusplus
 }
 #endif

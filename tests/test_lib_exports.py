@@ -25,7 +25,7 @@ def declared_functions():
             line = text[text.rfind("\n", 0, m.start()) + 1:m.start()]
             if line.lstrip().startswith("#"):
                 continue
-            if re.search(r"(int|void|float|size_t|uint32_t|int32_t|bool|char)\s*\**\s*$", line):
+            if re.search(r"(int|void|float|size_t|uint32_t|int32_t|int64_t|uint64_t|bool|char)\s*\**\s*$", line):
                 names.add(name)
     return names
 
