@@ -1,0 +1,464 @@
+// dq_prefill.hip - the prompt (prefill) side of the Q8_0 KV cache: the K/V
+// rows of a run of tokens written in one launch, optionally with their RoPE,
+// and causal attention of every token of the run over the cache.
+//
+// Cache layout as in dq_attn.hip: [pos][kv_head][hd/32 Q8_0 blocks of 34 B].
+//
+// Attention (reference core/attn_cpu.cpp:128-390, the CPU definition of
+// record; the GPU kernels it replaces are attention_prefill_*,
+// cuda/backend_cuda.cu:7080-8290): row (token t, head h) at position
+// pos0 + t attends to keys [lo, pos0 + t] of KV head h / hpk, lo = 0 or the
+// sliding-window start; scores q.k / sqrt(hd), softmax, sum p v.
+//
+// Work split: a workgroup takes one KV head and 128 consecutive rows
+// (row = token * hpk + head-in-group, so the query heads sharing a KV head
+// share every K/V tile), four waves of 32 rows. Keys go in tiles of 32: the
+// tile's raw Q8_0 rows are staged through LDS once per workgroup and turned
+// into fp16 operands there; each wave then runs
+//   S^T = K Q^T      (v_mfma_f32_32x32x16_f16, M = keys, N = its 32 rows)
+//   online softmax   (one row per lane pair: lanes l and l + 32)
+//   O^T += V^T P^T   (M = head dims, N = rows)
+// so that a row's scores, running max/sum and output all sit in the two
+// lanes of that row and no transpose is needed between the two products.
+//
+// Precision: every operand is split into fp16 hi + lo parts and each product
+// runs as hi*hi + lo*hi + hi*lo (the lo*lo term is below 2^-22 relative), so
+// the scores and the weighted sums carry ~22 bits. K and V values d*q (fp16
+// d times an int8, at most 18 significant bits) split exactly. The query is
+// scaled by 1/sqrt(hd) * log2(e) in fp32 first, so the softmax uses exp2.
+// Range: the cached values and the scaled query must lie inside fp16
+// (|x| < 65504), which Q8_0 rows of activations satisfy.
+#include <cstdlib>
+
+#include "dq_common.h"
+#include "dq_f16.h"
+
+namespace {
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+constexpr int KT = 32;    // keys per tile
+constexpr int NT = 256;   // threads per workgroup
+constexpr int RPW = 32;   // rows per wave
+constexpr int RPB = 128;  // rows per workgroup
+
+struct PrefillArgs {
+    const float* q;       // [n_tok][q_dim]
+    float* out;           // [n_tok][q_dim]
+    const uint8_t* kc;    // cache of the layer
+    const uint8_t* vc;
+    size_t pos_bytes;
+    int q_dim, n_tok, hpk, n_kv, pos0, n_swa, n_qblk;
+    float qscale;         // 1/sqrt(hd) * log2(e)
+};
+
+__device__ __forceinline__ int win_lo(int pos, int n_swa) {
+    return (n_swa > 0 && pos + 1 > n_swa) ? pos + 1 - n_swa : 0;
+}
+
+__device__ __forceinline__ void split8(const float (&x)[8], h8& hi, h8& lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const _Float16 h = (_Float16)x[i];
+        hi[i] = h;
+        lo[i] = (_Float16)(x[i] - (float)h);
+    }
+}
+
+// Column of actual key a (0..31) in the transposed V tile: the key order in
+// which a lane's scores (S^T layout: keys 8*(r/4) + 4*(l/32) + r%4 of
+// register r) are the B operand of the V product in register order, i.e.
+// bits 2 and 3 of the key swapped.
+__device__ __forceinline__ int vcol_group(int g) {  // g = a / 4
+    return (g & 4) | ((g & 1) << 1) | ((g >> 1) & 1);
+}
+
+template <int HD>
+__global__ __launch_bounds__(NT) void attn_prefill_kernel(PrefillArgs A) {
+    constexpr int NB = HD / 32;          // Q8_0 blocks per row
+    constexpr int RB = NB * DQ_SZ_Q8_0;  // row bytes
+    constexpr int RBW = RB / 4;          // row dwords
+    constexpr int NS = HD / 16;          // K steps of the score product
+    constexpr int KROW = HD + 8;         // fp16 per K row in LDS (16-byte pad)
+    constexpr int VROW = KT + 8;         // fp16 per transposed V row
+    constexpr int PER = (KT * RBW + NT - 1) / NT;
+    constexpr int UNITS = 2 * HD;        // conversion units of K (and of V) per tile
+    static_assert(RB % 4 == 0, "rows must be whole dwords");
+
+    __shared__ uint32_t rawk[KT * RBW], rawv[KT * RBW];
+    __shared__ __attribute__((aligned(16))) _Float16 kh[KT * KROW], kl[KT * KROW];
+    __shared__ __attribute__((aligned(16))) _Float16 vh[HD * VROW], vl[HD * VROW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+    const int hkv = blockIdx.x % A.n_kv;
+    const int qb = A.n_qblk - 1 - (int)(blockIdx.x / A.n_kv);  // longest rows first
+    const int hpk = A.hpk;
+    const int n_rows = A.n_tok * hpk;
+    const int R0 = qb * RPB;
+    const int p_first = A.pos0 + R0 / hpk;
+    const int p_last = A.pos0 + min(R0 + RPB - 1, n_rows - 1) / hpk;
+    const int k_begin = win_lo(p_first, A.n_swa);
+
+    // this wave's rows and this lane's row (rows past the end are computed
+    // on a clamped copy and not stored)
+    const int wr0 = R0 + RPW * wave;
+    const bool wave_live = wr0 < n_rows;
+    const int w_pmax = A.pos0 + min(wr0 + RPW - 1, n_rows - 1) / hpk;
+    const int w_lomin = win_lo(A.pos0 + min(wr0, n_rows - 1) / hpk, A.n_swa);
+    const int row = wr0 + (lane & 31);
+    const bool row_ok = row < n_rows;
+    const int rc = min(row, n_rows - 1);
+    const int t = rc / hpk, head = hkv * hpk + rc % hpk;
+    const int pos = A.pos0 + t;
+    const int lo = win_lo(pos, A.n_swa);
+
+    // K/V rows of a tile into registers (positions clamped into
+    // [k_begin, p_last]: rows outside are never read, in-tile keys past them
+    // are masked)
+    uint32_t rk[PER], rv[PER];
+    auto load_tile = [&](int k0) {
+#pragma unroll
+        for (int it = 0; it < PER; ++it) {
+            const int i = min(tid + it * NT, KT * RBW - 1);
+            const int key = i / RBW, c = i - key * RBW;
+            const int p = max(min(k0 + key, p_last), k_begin);
+            const size_t off = (size_t)p * A.pos_bytes + (size_t)hkv * RB + 4 * c;
+            rk[it] = *reinterpret_cast<const uint32_t*>(A.kc + off);
+            rv[it] = *reinterpret_cast<const uint32_t*>(A.vc + off);
+        }
+    };
+    const int kt0 = k_begin & ~(KT - 1);
+    load_tile(kt0);
+
+    // query fragments (B operand of S^T = K Q^T): dims 16s + 8*half + i
+    h8 qh[NS], ql[NS];
+    {
+        const float* qp = A.q + (size_t)t * A.q_dim + (size_t)head * HD + 8 * half;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const float4 a = *reinterpret_cast<const float4*>(qp + 16 * s);
+            const float4 b = *reinterpret_cast<const float4*>(qp + 16 * s + 4);
+            const float x[8] = {a.x * A.qscale, a.y * A.qscale, a.z * A.qscale, a.w * A.qscale,
+                                b.x * A.qscale, b.y * A.qscale, b.z * A.qscale, b.w * A.qscale};
+            split8(x, qh[s], ql[s]);
+        }
+    }
+
+    f16v o[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[b][r] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+
+    const uint8_t* rkb = reinterpret_cast<const uint8_t*>(rawk);
+    const uint8_t* rvb = reinterpret_cast<const uint8_t*>(rawv);
+    for (int k0 = kt0; k0 <= p_last; k0 += KT) {
+#pragma unroll
+        for (int it = 0; it < PER; ++it) {
+            const int i = tid + it * NT;
+            if (i < KT * RBW) {
+                rawk[i] = rk[it];
+                rawv[i] = rv[it];
+            }
+        }
+        __syncthreads();
+        // ---- raw Q8_0 -> fp16 hi/lo operands
+        for (int u = tid; u < UNITS; u += NT) {
+            {   // K: (key, 16 dims) -> kh/kl[key][dims]
+                const int key = u / (HD / 16), part = u % (HD / 16);
+                const int b = part >> 1, hf = part & 1;
+                const uint8_t* bp = rkb + key * RB + b * DQ_SZ_Q8_0;
+                const float d = dq_h2f(*reinterpret_cast<const uint16_t*>(bp));
+                float x[16];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const uint16_t w = *reinterpret_cast<const uint16_t*>(bp + 2 + 16 * hf + 2 * j);
+                    x[2 * j] = d * (float)(int8_t)(w & 0xFF);
+                    x[2 * j + 1] = d * (float)(int8_t)(w >> 8);
+                }
+                h8 a0, a1, b0, b1;
+                split8(reinterpret_cast<const float(&)[8]>(x[0]), a0, b0);
+                split8(reinterpret_cast<const float(&)[8]>(x[8]), a1, b1);
+                _Float16* dh = kh + key * KROW + 32 * b + 16 * hf;
+                _Float16* dl = kl + key * KROW + 32 * b + 16 * hf;
+                *reinterpret_cast<h8*>(dh) = a0;
+                *reinterpret_cast<h8*>(dh + 8) = a1;
+                *reinterpret_cast<h8*>(dl) = b0;
+                *reinterpret_cast<h8*>(dl + 8) = b1;
+            }
+            {   // V: (4 keys, 4 dims) -> vh/vl[dim][permuted keys]
+                const int g = u & 7, c = u >> 3;
+                const int b = c >> 3, off = 4 * (c & 7);
+                float x[4][4];  // [key][dim]
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const uint8_t* bp = rvb + (4 * g + kk) * RB + b * DQ_SZ_Q8_0;
+                    const float d = dq_h2f(*reinterpret_cast<const uint16_t*>(bp));
+                    const uint16_t w0 = *reinterpret_cast<const uint16_t*>(bp + 2 + off);
+                    const uint16_t w1 = *reinterpret_cast<const uint16_t*>(bp + 4 + off);
+                    x[kk][0] = d * (float)(int8_t)(w0 & 0xFF);
+                    x[kk][1] = d * (float)(int8_t)(w0 >> 8);
+                    x[kk][2] = d * (float)(int8_t)(w1 & 0xFF);
+                    x[kk][3] = d * (float)(int8_t)(w1 >> 8);
+                }
+                const int col = 4 * vcol_group(g);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    h4 hv, lv;
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) {
+                        const _Float16 h = (_Float16)x[kk][j];
+                        hv[kk] = h;
+                        lv[kk] = (_Float16)(x[kk][j] - (float)h);
+                    }
+                    *reinterpret_cast<h4*>(vh + (4 * c + j) * VROW + col) = hv;
+                    *reinterpret_cast<h4*>(vl + (4 * c + j) * VROW + col) = lv;
+                }
+            }
+        }
+        if (k0 + KT <= p_last) load_tile(k0 + KT);
+        __syncthreads();
+        if (!wave_live || k0 > w_pmax || k0 + KT - 1 < w_lomin) continue;  // uniform per wave
+
+        // ---- scores S^T (lane: row lane%32, keys 8*(r/4) + 4*half + r%4)
+        f16v st;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) st[r] = 0.0f;
+        {
+            const _Float16* krh = kh + (lane & 31) * KROW + 8 * half;
+            const _Float16* krl = kl + (lane & 31) * KROW + 8 * half;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const h8 ah = *reinterpret_cast<const h8*>(krh + 16 * s);
+                const h8 al = *reinterpret_cast<const h8*>(krl + 16 * s);
+                st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, qh[s], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, qh[s], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ql[s], st, 0, 0, 0);
+            }
+        }
+        // ---- causal / window mask, online softmax
+        float mt = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+            const bool ok = key <= pos && key >= lo;
+            st[r] = ok ? st[r] : -INFINITY;
+            mt = fmaxf(mt, st[r]);
+        }
+        mt = fmaxf(mt, __shfl_xor(mt, 32, DQ_WAVE));
+        const float mn = fmaxf(m, mt);
+        const float corr = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+        float ps = 0.0f;
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            p[r] = st[r] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(st[r] - mn);
+            ps += p[r];
+        }
+        l = l * corr + ps;
+        m = mn;
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[b][r] *= corr;
+        h8 ph[2], pl[2];
+        split8(reinterpret_cast<const float(&)[8]>(p[0]), ph[0], pl[0]);
+        split8(reinterpret_cast<const float(&)[8]>(p[8]), ph[1], pl[1]);
+        // ---- O^T += V^T P^T (lane: row lane%32, dims 32b + 8*(r/4) + 4*half + r%4)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const _Float16* vrh = vh + (32 * b + (lane & 31)) * VROW + 8 * half;
+            const _Float16* vrl = vl + (32 * b + (lane & 31)) * VROW + 8 * half;
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const h8 ah = *reinterpret_cast<const h8*>(vrh + 16 * s);
+                const h8 al = *reinterpret_cast<const h8*>(vrl + 16 * s);
+                o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, ph[s], o[b], 0, 0, 0);
+                o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, ph[s], o[b], 0, 0, 0);
+                o[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, pl[s], o[b], 0, 0, 0);
+            }
+        }
+    }
+    if (!wave_live) return;
+    const float lt = l + __shfl_xor(l, 32, DQ_WAVE);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    if (!row_ok) return;
+    float* dst = A.out + (size_t)t * A.q_dim + (size_t)head * HD + 4 * half;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<float4*>(dst + 32 * b + 8 * g) =
+                make_float4(o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv);
+}
+
+// ------------------------------------------------------------ row writes --
+// kv_quantize_batch_kernel (cuda/backend_cuda.cu:7028-7058) / write_kv_cache
+// per position: kv_quantize_row (kv/kv_quant.cpp:31-56) of every token's K
+// and V rows into positions pos0 + t. One lane per 32-value block: per block
+// amax, d = amax/127, q = clamp(rint(x/d), -127, 127).
+__device__ __forceinline__ void kv_block_store(const float* x, uint8_t* dst) {
+    float xv[32];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 f = reinterpret_cast<const float4*>(x)[i];
+        xv[4 * i] = f.x, xv[4 * i + 1] = f.y, xv[4 * i + 2] = f.z, xv[4 * i + 3] = f.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(xv[i]));
+    const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+    const float id = d > 0.0f ? 1.0f / d : 0.0f;
+    uint16_t* o = reinterpret_cast<uint16_t*>(dst);  // 34-byte blocks: 2-byte aligned
+    o[0] = dq_f2h(d);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        int a = (int)rintf(xv[2 * i] * id), c = (int)rintf(xv[2 * i + 1] * id);
+        a = a > 127 ? 127 : (a < -127 ? -127 : a);
+        c = c > 127 ? 127 : (c < -127 ? -127 : c);
+        o[1 + i] = (uint16_t)((a & 0xFF) | ((c & 0xFF) << 8));
+    }
+}
+
+__global__ __launch_bounds__(256) void kv_write_batch_kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                            size_t ld, int n_tok, int blocks_per_row,
+                                                            uint8_t* __restrict__ kc, uint8_t* __restrict__ vc,
+                                                            size_t pos_bytes, int pos0) {
+    const int per_tok = 2 * blocks_per_row;
+    const long gb = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gb >= (long)n_tok * per_tok) return;
+    const int t = (int)(gb / per_tok), b = (int)(gb % per_tok);
+    const bool is_v = b >= blocks_per_row;
+    const int bb = is_v ? b - blocks_per_row : b;
+    const float* x = (is_v ? v : k) + (size_t)t * ld + (size_t)bb * 32;
+    uint8_t* dst = (is_v ? vc : kc) + (size_t)(pos0 + t) * pos_bytes + (size_t)bb * DQ_SZ_Q8_0;
+    kv_block_store(x, dst);
+}
+
+// RoPE of a run of tokens (models/dense_forward.cpp:668-680 per token, table
+// row t = dq_rope_cache(pos0 + t)) on the query heads, in place, and on the
+// key heads, whose rotated rows then go into the cache with the value rows
+// (kv_quantize_row). 128-dim heads; grid (n_head + 2 n_kv, n_tok), 64 threads,
+// thread j holds dims j and j + 64.
+__global__ __launch_bounds__(64) void rope_kv_batch_kernel(float* __restrict__ q, const float* __restrict__ k,
+                                                           const float* __restrict__ v, size_t q_ld, size_t kv_ld,
+                                                           const float* __restrict__ rope, int n_rot, int n_head,
+                                                           int n_kv, uint8_t* __restrict__ kc,
+                                                           uint8_t* __restrict__ vc, size_t pos_bytes, int pos0) {
+    constexpr int HD = 128;
+    const int r = blockIdx.x, t = blockIdx.y, j = threadIdx.x;
+    const int kind = r < n_head ? 0 : (r < n_head + n_kv ? 1 : 2);
+    const int hh = kind == 0 ? r : (kind == 1 ? r - n_head : r - n_head - n_kv);
+    float* qrow = q + (size_t)t * q_ld + (size_t)hh * HD;
+    const float* src = kind == 0 ? qrow : (kind == 1 ? k : v) + (size_t)t * kv_ld + (size_t)hh * HD;
+    float x0 = src[j], x1 = src[j + 64];
+    if (kind < 2 && rope) {
+        const float* tab = rope + (size_t)t * n_rot;
+        if (n_rot == HD) {
+            dq_rope_pair(x0, x1, tab, j);
+        } else {
+            __shared__ float rowb[HD];
+            rowb[j] = x0;
+            rowb[j + 64] = x1;
+            __syncthreads();
+            const int hn = n_rot / 2;
+            if (j < hn) {
+                const float c = tab[2 * j], s = tab[2 * j + 1];
+                const float a = rowb[j], b = rowb[j + hn];
+                rowb[j] = a * c - b * s;
+                rowb[j + hn] = a * s + b * c;
+            }
+            __syncthreads();
+            x0 = rowb[j];
+            x1 = rowb[j + 64];
+        }
+    }
+    if (kind == 0) {
+        qrow[j] = x0;
+        qrow[j + 64] = x1;
+        return;
+    }
+    dq_q8_0_row128(x0, x1, j, (kind == 1 ? kc : vc) + (size_t)(pos0 + t) * pos_bytes + (size_t)hh * (HD / 32) * DQ_SZ_Q8_0);
+}
+
+template <int HD>
+int launch_prefill(const PrefillArgs& a, int grid, hipStream_t s) {
+    attn_prefill_kernel<HD><<<grid, NT, 0, s>>>(a);
+    return dq_launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+int dq_kv_write_batch(const float* d_k, const float* d_v, size_t ld, uint32_t n_tok, uint32_t n_head_kv, uint32_t hd,
+                      void* d_kc, void* d_vc, uint32_t pos0, uint32_t n_ctx, void* stream) {
+    if (!d_k || !d_v || !d_kc || !d_vc) return DQ_ERR_INVALID_ARG;
+    if (hd == 0 || hd % 32 || n_head_kv == 0) return DQ_ERR_NOT_SUPPORTED;
+    if (ld < (size_t)n_head_kv * hd || ld % 4) return DQ_ERR_INVALID_ARG;
+    if (n_tok == 0) return DQ_OK;
+    if ((uint64_t)pos0 + n_tok > n_ctx) return DQ_ERR_INVALID_ARG;
+    const int bpr = (int)(n_head_kv * hd / 32);
+    const uint64_t total = (uint64_t)n_tok * 2 * bpr;
+    if (total > (1ull << 31)) return DQ_ERR_NOT_SUPPORTED;
+    const size_t pos_bytes = (size_t)bpr * DQ_SZ_Q8_0;
+    kv_write_batch_kernel<<<(unsigned)((total + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+        d_k, d_v, ld, (int)n_tok, bpr, (uint8_t*)d_kc, (uint8_t*)d_vc, pos_bytes, (int)pos0);
+    return dq_launch_status();
+}
+
+int dq_rope_kv_write_batch(float* d_q, const float* d_k, const float* d_v, size_t q_ld, size_t kv_ld,
+                           const float* d_rope, uint32_t n_rot, uint32_t n_tok, uint32_t n_head, uint32_t n_head_kv,
+                           uint32_t hd, void* d_kc, void* d_vc, uint32_t pos0, uint32_t n_ctx, void* stream) {
+    if (!d_q || !d_k || !d_v || !d_kc || !d_vc) return DQ_ERR_INVALID_ARG;
+    if (hd != 128 || n_head_kv == 0) return DQ_ERR_NOT_SUPPORTED;
+    if (d_rope && (n_rot == 0 || n_rot > hd || n_rot % 2)) return DQ_ERR_INVALID_ARG;
+    if (q_ld < (size_t)n_head * hd || kv_ld < (size_t)n_head_kv * hd) return DQ_ERR_INVALID_ARG;
+    if (n_tok == 0) return DQ_OK;
+    if ((uint64_t)pos0 + n_tok > n_ctx || n_tok > 65535) return DQ_ERR_INVALID_ARG;
+    const size_t pos_bytes = (size_t)n_head_kv * (hd / 32) * DQ_SZ_Q8_0;
+    rope_kv_batch_kernel<<<dim3(n_head + 2 * n_head_kv, n_tok), 64, 0, (hipStream_t)stream>>>(
+        d_q, d_k, d_v, q_ld, kv_ld, d_rope, (int)n_rot, (int)n_head, (int)n_head_kv, (uint8_t*)d_kc, (uint8_t*)d_vc,
+        pos_bytes, (int)pos0);
+    return dq_launch_status();
+}
+
+int dq_attn_prefill_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_tok, uint32_t n_head,
+                       uint32_t n_head_kv, uint32_t hd, uint32_t q_dim, uint32_t pos0, uint32_t n_swa,
+                       uint32_t n_ctx, float* d_out, void* stream) {
+    if (!d_q || !d_kc || !d_vc || !d_out) return DQ_ERR_INVALID_ARG;
+    if (n_head_kv == 0 || n_head % n_head_kv) return DQ_ERR_NOT_SUPPORTED;
+    if (hd != 64 && hd != 128 && hd != 256) return DQ_ERR_NOT_SUPPORTED;
+    if (q_dim < n_head * hd || q_dim % 4) return DQ_ERR_INVALID_ARG;
+    if (((uintptr_t)d_kc | (uintptr_t)d_vc) & 3) return DQ_ERR_NOT_SUPPORTED;
+    if (n_tok == 0) return DQ_OK;
+    if ((uint64_t)pos0 + n_tok > n_ctx) return DQ_ERR_INVALID_ARG;
+    const uint32_t hpk = n_head / n_head_kv;
+    const uint64_t n_rows = (uint64_t)n_tok * hpk;
+    const uint64_t n_qblk = (n_rows + RPB - 1) / RPB;
+    if (n_qblk * n_head_kv > 0x7FFFFFFFull || n_rows > 0x7FFFFFFFull) return DQ_ERR_NOT_SUPPORTED;
+    PrefillArgs a;
+    a.q = d_q;
+    a.out = d_out;
+    a.kc = (const uint8_t*)d_kc;
+    a.vc = (const uint8_t*)d_vc;
+    a.pos_bytes = (size_t)n_head_kv * (hd / 32) * DQ_SZ_Q8_0;
+    a.q_dim = (int)q_dim;
+    a.n_tok = (int)n_tok;
+    a.hpk = (int)hpk;
+    a.n_kv = (int)n_head_kv;
+    a.pos0 = (int)pos0;
+    a.n_swa = (int)n_swa;
+    a.n_qblk = (int)n_qblk;
+    a.qscale = (1.0f / sqrtf((float)hd)) * 1.4426950408889634f;
+    const int grid = (int)(n_qblk * n_head_kv);
+    const hipStream_t s = (hipStream_t)stream;
+    switch (hd) {
+    case 64: return launch_prefill<64>(a, grid, s);
+    case 128: return launch_prefill<128>(a, grid, s);
+    default: return launch_prefill<256>(a, grid, s);
+    }
+}
+
+}  // extern "C"

@@ -224,6 +224,41 @@ class KVCache:
                                    self.n_ctx, _stream()), "dq_kv_write")
 
 
+    def write_batch(self, k, v, pos0):
+        """Quantizes the rows of k, v ([n_tok][n_head_kv * hd] fp32) into
+        positions [pos0, pos0 + n_tok)."""
+        lib = _lib.load()
+        k, v = k.contiguous(), v.contiguous()
+        _lib.check(lib.dq_kv_write_batch(_ptr(k), _ptr(v), k.shape[-1], k.shape[0], self.n_head_kv, self.hd,
+                                         _ptr(self.k), _ptr(self.v), int(pos0), self.n_ctx, _stream()),
+                   "dq_kv_write_batch")
+
+    def rope_write_batch(self, q, k, v, rope, n_rot, pos0):
+        """RoPE of q (in place, [n_tok][q_ld]) and k with the per-token table
+        rope ([n_tok][n_rot] device floats, or None), then the K/V rows of the
+        tokens into positions [pos0, pos0 + n_tok)."""
+        lib = _lib.load()
+        k, v = k.contiguous(), v.contiguous()
+        n_head = q.shape[-1] // self.hd
+        _lib.check(lib.dq_rope_kv_write_batch(_ptr(q), _ptr(k), _ptr(v), q.shape[-1], k.shape[-1], _ptr(rope),
+                                              n_rot, q.shape[0], n_head, self.n_head_kv, self.hd, _ptr(self.k),
+                                              _ptr(self.v), int(pos0), self.n_ctx, _stream()),
+                   "dq_rope_kv_write_batch")
+
+
+def attention_prefill(q, cache, n_head, pos0, n_swa=0, out=None):
+    """Prefill attention of q [n_tok][q_dim] (token t at position pos0 + t)
+    over the cache, causal (n_swa 0) or over a sliding window of n_swa."""
+    lib = _lib.load()
+    q = q.contiguous()
+    n_tok, q_dim = q.shape
+    o = out if out is not None else torch.zeros(n_tok, q_dim, dtype=torch.float32, device=q.device)
+    _lib.check(lib.dq_attn_prefill_q8(_ptr(q), _ptr(cache.k), _ptr(cache.v), n_tok, n_head, cache.n_head_kv,
+                                      cache.hd, q_dim, int(pos0), int(n_swa), cache.n_ctx, _ptr(o), _stream()),
+               "dq_attn_prefill_q8")
+    return o
+
+
 def attn_workspace(n_head, n_head_kv, hd, n_ctx, device="cuda"):
     lib = _lib.load()
     n = ctypes.c_size_t(0)

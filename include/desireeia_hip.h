@@ -185,6 +185,37 @@ int dq_attn_rope_kv_decode(const float* d_q, const float* d_k, const float* d_v,
                            int8_t* d_oq, float* d_oscale, int32_t* d_oisum, void* d_work, size_t work_bytes,
                            void* stream);
 
+/* ------------------------------------------------------------- prefill */
+
+/* K/V rows of n_tok consecutive tokens into positions [pos0, pos0 + n_tok)
+ * (kv_quantize_batch_kernel, cuda/backend_cuda.cu:7028-7058; per position
+ * write_kv_cache, models/dense_forward.cpp:2552-2605, with kv_quantize_row,
+ * kv/kv_quant.cpp:31-56, bit-exact). d_k, d_v: [n_tok][ld] floats, the first
+ * n_head_kv * hd of a row are stored. hd % 32 == 0. */
+int dq_kv_write_batch(const float* d_k, const float* d_v, size_t ld, uint32_t n_tok, uint32_t n_head_kv, uint32_t hd,
+                      void* d_kc, void* d_vc, uint32_t pos0, uint32_t n_ctx, void* stream);
+/* The RoPE step of the prefill for n_tok tokens (models/dense_forward.cpp
+ * :3347-3362 per token): NeoX RoPE of every query head in place and of every
+ * key head with the table row d_rope + t * n_rot (dq_rope_cache(pos0 + t);
+ * NULL = no RoPE), then the Q8_0 rows of the rotated k and of v at pos0 + t
+ * (as dq_kv_write_batch). q: [n_tok][q_ld], k, v: [n_tok][kv_ld]. hd = 128. */
+int dq_rope_kv_write_batch(float* d_q, const float* d_k, const float* d_v, size_t q_ld, size_t kv_ld,
+                           const float* d_rope, uint32_t n_rot, uint32_t n_tok, uint32_t n_head, uint32_t n_head_kv,
+                           uint32_t hd, void* d_kc, void* d_vc, uint32_t pos0, uint32_t n_ctx, void* stream);
+/* Prefill attention over the Q8_0 cache: the device counterpart of
+ * attention_prefill_cpu_q8 (core/attn_cpu.cpp:128-390, core/engine.h:470-477)
+ * and of cuda_attention_batch's kernels (cuda/backend_cuda.cu:3799-3870,
+ * 7080-8290). q, out: [n_tok][q_dim] fp32; token t at position pos0 + t
+ * attends to keys [lo, pos0 + t] of KV head h / (n_head / n_head_kv), lo = 0
+ * or pos0 + t + 1 - n_swa (n_swa > 0: sliding window); scores scaled by
+ * 1/sqrt(hd). Columns of q_dim past n_head * hd are left untouched. The K/V
+ * rows of every position read must already be in the cache. hd in {64, 128,
+ * 256}; other hd: -2. Operands run on fp16 MFMA split into hi + lo parts
+ * (~2^-22 relative); cached values and queries must lie inside fp16. */
+int dq_attn_prefill_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_tok, uint32_t n_head,
+                       uint32_t n_head_kv, uint32_t hd, uint32_t q_dim, uint32_t pos0, uint32_t n_swa,
+                       uint32_t n_ctx, float* d_out, void* stream);
+
 /* ------------------------------------------------------- decoder layer */
 
 /* rope_cache_init (models/dense_forward.cpp:631-657, no YaRN): host code,

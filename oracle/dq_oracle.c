@@ -759,6 +759,65 @@ void dqo_attn_decode_q8(const float* q, const uint8_t* kc, const uint8_t* vc,
     free(scores);
 }
 
+/* core/attn_cpu.cpp:128-390 (attention_prefill_cpu_q8), one row at a time:
+ * row (token t, head h) sits at position pos0 + t and attends to the keys
+ * [lo, pos] of KV head h / hpk, lo = pos + 1 - n_swa when n_swa > 0 and
+ * pos + 1 > n_swa, else 0 (:165, :310-311). The query is multiplied by inv_d
+ * first (:157); K and V rows are dequantized to float d * q (:96-104); the
+ * scores are float dot products, the softmax subtracts the row maximum, and
+ * the output is sum(p * v) * (1 / sum(p)) (:380-384). The reference tiles the
+ * keys with an online maximum and a polynomial exp; results agree to float
+ * rounding. Rows of other heads' columns of q_dim are left untouched. */
+static void deq_kv_row(const uint8_t* row, uint32_t hd, float* out) {
+    for (uint32_t b = 0; b < hd / 32; ++b) {
+        const uint8_t* blk = row + (size_t)b * SZ_Q8_0;
+        const float d = dqo_fp16_to_fp32(rd16(blk));
+        for (int j = 0; j < 32; ++j) out[b * 32 + j] = d * (float)(int8_t)blk[2 + j];
+    }
+}
+
+int dqo_attn_prefill_q8(const float* q_all, float* out, uint32_t n_tok, uint32_t n_head, uint32_t hpk,
+                        uint32_t hd, uint32_t q_dim, const uint8_t* kbase, const uint8_t* vbase,
+                        size_t row_bytes, size_t pos_bytes, uint32_t pos0, uint32_t n_swa, float inv_d) {
+    if (hd == 0 || hd % 32 || hpk == 0 || n_head % hpk) return DQO_ERR_NOT_SUPPORTED;
+    float* qs = (float*)malloc(hd * sizeof(float));
+    float* row = (float*)malloc(hd * sizeof(float));
+    float* o = (float*)malloc(hd * sizeof(float));
+    float* s = (float*)malloc(((size_t)pos0 + n_tok) * sizeof(float));
+    for (uint32_t t = 0; t < n_tok; ++t) {
+        const uint32_t pos = pos0 + t;
+        const uint32_t lo = (n_swa > 0 && pos + 1 > n_swa) ? pos + 1 - n_swa : 0;
+        for (uint32_t h = 0; h < n_head; ++h) {
+            const uint32_t hkv = h / hpk;
+            const float* qh = q_all + (size_t)t * q_dim + (size_t)h * hd;
+            for (uint32_t d = 0; d < hd; ++d) qs[d] = qh[d] * inv_d;
+            float m = -INFINITY;
+            for (uint32_t k = lo; k <= pos; ++k) {
+                deq_kv_row(kbase + (size_t)k * pos_bytes + (size_t)hkv * row_bytes, hd, row);
+                float a = 0.0f;
+                for (uint32_t d = 0; d < hd; ++d) a += qs[d] * row[d];
+                s[k] = a;
+                m = a > m ? a : m;
+            }
+            float l = 0.0f;
+            for (uint32_t k = lo; k <= pos; ++k) {
+                s[k] = expf(s[k] - m);
+                l += s[k];
+            }
+            for (uint32_t d = 0; d < hd; ++d) o[d] = 0.0f;
+            for (uint32_t k = lo; k <= pos; ++k) {
+                deq_kv_row(vbase + (size_t)k * pos_bytes + (size_t)hkv * row_bytes, hd, row);
+                for (uint32_t d = 0; d < hd; ++d) o[d] += s[k] * row[d];
+            }
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            float* dst = out + (size_t)t * q_dim + (size_t)h * hd;
+            for (uint32_t d = 0; d < hd; ++d) dst[d] = o[d] * inv;
+        }
+    }
+    free(qs); free(row); free(o); free(s);
+    return DQO_OK;
+}
+
 /* fp64 softmax attention over the dequantized K/V rows. */
 void dqo_attn_decode_q8_f64(const float* q, const uint8_t* kc, const uint8_t* vc,
                             uint32_t n_head, uint32_t n_head_kv, uint32_t hd,

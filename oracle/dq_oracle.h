@@ -106,6 +106,13 @@ void dqo_rope_cache(float* cache, size_t n_rot, uint32_t pos, float theta_base);
 void dqo_rope_neox(float* v, size_t n_rot, const float* cache);
 float dqo_silu(float v);
 void dqo_softmax(float* s, size_t n);
+/* Prefill attention over a Q8_0 KV cache (core/attn_cpu.cpp:128-390):
+ * q_all/out [n_tok][q_dim]; K/V row of (pos, kv head) at base + pos*pos_bytes
+ * + kv_head*row_bytes; token t at position pos0 + t; n_swa 0 = causal. */
+int dqo_attn_prefill_q8(const float* q_all, float* out, uint32_t n_tok, uint32_t n_head, uint32_t hpk,
+                        uint32_t hd, uint32_t q_dim, const uint8_t* kbase, const uint8_t* vbase,
+                        size_t row_bytes, size_t pos_bytes, uint32_t pos0, uint32_t n_swa, float inv_d);
+
 
 /* One Llama-style decode layer (models/dense_forward.cpp:3897-4257) with
  * Q4_K/Q6_K weights and a Q8_0 KV cache of one layer. The new K/V rows are

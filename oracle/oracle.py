@@ -72,6 +72,8 @@ class Oracle:
         L.dqo_kv_axpy_q8_0.argtypes = [c_p, c_p, c_size, c_f]
         L.dqo_attn_decode_q8.argtypes = [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p]
         L.dqo_attn_decode_q8_f64.argtypes = [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p]
+        L.dqo_attn_prefill_q8.argtypes = [c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_p, c_size, c_size,
+                                          c_u32, c_u32, c_f]
         L.dqo_moe_route.restype = c_u32
         L.dqo_moe_route.argtypes = [c_p, c_u32, c_u32, c_int, c_f, c_p, c_p]
         L.dqo_rms_norm.argtypes = [c_p, c_p, c_p, c_size, c_f]
@@ -185,6 +187,10 @@ class Oracle:
            n_head, n_head_kv, hd, cc_start, pos, _p(out))
         return out
 
+    def attn_prefill(self, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0, n_swa=0, q_dim=None, out=None):
+        return _attn_prefill(self.L.dqo_attn_prefill_q8, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0, n_swa,
+                             q_dim, out)
+
     def moe_route(self, logits, k, norm_w=True, w_scale=1.0):
         logits = np.ascontiguousarray(logits, np.float32)
         ids = np.zeros(max(k, 1), np.uint32)
@@ -265,6 +271,8 @@ class Ref:
         L.dqr_kv_axpy_q8_0.argtypes = [c_p, c_p, c_size, c_f]
         L.dqr_moe_route.restype = c_u32
         L.dqr_moe_route.argtypes = [c_p, c_u32, c_u32, c_int, c_f, c_p, c_p]
+        L.dqr_attention_prefill_q8.argtypes = [c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_p, c_size, c_size,
+                                               c_u32, c_u32, c_f]
 
     @staticmethod
     def available():
@@ -345,6 +353,26 @@ class Ref:
         wts = np.zeros(max(k, 1, logits.size), np.float32)
         n = self.L.dqr_moe_route(_p(logits), logits.size, k, int(norm_w), w_scale, _p(ids), _p(wts))
         return ids[:n].copy(), wts[:n].copy()
+
+
+    def attn_prefill(self, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0, n_swa=0, q_dim=None, out=None):
+        return _attn_prefill(self.L.dqr_attention_prefill_q8, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0,
+                             n_swa, q_dim, out)
+
+
+def _attn_prefill(fn, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0, n_swa, q_dim, out):
+    """q_all [n_tok][q_dim] -> out [n_tok][q_dim]; caches of one layer laid out
+    [pos][kv head][hd/32 Q8_0 blocks]."""
+    q_dim = q_dim or n_head * hd
+    q_all = np.ascontiguousarray(q_all, np.float32).reshape(-1)
+    out = np.zeros(n_tok * q_dim, np.float32) if out is None else np.ascontiguousarray(out, np.float32).copy()
+    row_bytes = hd // 32 * 34
+    rc = fn(_p(q_all), _p(out), n_tok, n_head, n_head // n_head_kv, hd, q_dim, _p(np.ascontiguousarray(kc, np.uint8)),
+            _p(np.ascontiguousarray(vc, np.uint8)), row_bytes, n_head_kv * row_bytes, pos0, n_swa,
+            float(np.float32(1.0) / np.sqrt(np.float32(hd))))
+    if rc != 0:
+        raise ValueError(f"attn_prefill rc={rc}")
+    return out
 
 
 _oracle = None

@@ -14,6 +14,7 @@
 //   matmul_*_batch ................ core/matmul.cpp:2090-2125, :848-860
 //   kv_quantize_row/dot/axpy ...... kv/kv_quant.cpp:31,58,102
 //   moe_route ..................... models/moe_route.cpp:77
+//   attention_prefill_cpu_q8 ...... core/attn_cpu.cpp:128
 //   ThreadPool::set_thread_override core/thread_pool.cpp:36
 #include "core/engine.h"
 #include "core/i8gemm.h"
@@ -93,6 +94,13 @@ uint32_t dqr_moe_route(const float* logits, uint32_t n, uint32_t k, int norm_w, 
         wts[i] = sel[i].second;
     }
     return (uint32_t)sel.size();
+}
+
+int dqr_attention_prefill_q8(const float* q_all, float* out, uint32_t n_tok, uint32_t n_head, uint32_t hpk,
+                             uint32_t hd, uint32_t q_dim, const uint8_t* kbase, const uint8_t* vbase,
+                             size_t row_bytes, size_t pos_bytes, uint32_t pos0, uint32_t n_swa, float inv_d) {
+    return attention_prefill_cpu_q8(q_all, out, n_tok, n_head, hpk, hd, q_dim, kbase, vbase, row_bytes, pos_bytes,
+                                    pos0, n_swa, inv_d);
 }
 
 }  // extern "C"

@@ -128,6 +128,59 @@ def test_attention_closed_forms(orc):
         assert np.allclose(out[h], V[:, h // 2].mean(axis=0), rtol=1e-5, atol=1e-6)
 
 
+# ------------------------------------------------------- prefill attention
+
+PREFILL_CASES = [
+    # n_head, n_kv, hd, pos0, n_tok, n_swa
+    (8, 2, 128, 0, 40, 0), (8, 2, 128, 100, 50, 0), (6, 2, 64, 30, 33, 16), (4, 4, 256, 5, 12, 0),
+    (6, 2, 128, 64, 70, 100),
+]
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,pos0,n_tok,n_swa", PREFILL_CASES)
+def test_attn_prefill_vs_numpy_and_decode(orc, n_head, n_kv, hd, pos0, n_tok, n_swa):
+    """core/attn_cpu.cpp restated: every row against an fp64 numpy softmax over
+    the dequantized rows, and against the decode oracle (dense_forward.cpp
+    :3956-4065) at the row's position with the window start as cc_start."""
+    kc, vc = make_cache(orc, pos0 + n_tok, n_kv, hd, seed=pos0 + n_tok)
+    q = np.random.default_rng(n_tok).standard_normal((n_tok, n_head * hd)).astype(np.float32)
+    got = orc.attn_prefill(q, kc, vc, n_tok, n_head, n_kv, hd, pos0, n_swa).reshape(n_tok, n_head * hd)
+    for t in (0, n_tok // 3, n_tok - 1):
+        pos = pos0 + t
+        lo = pos + 1 - n_swa if n_swa and pos + 1 > n_swa else 0
+        want = attn_numpy(orc, q[t], kc, vc, n_head, n_kv, hd, lo, pos)
+        assert np.linalg.norm(got[t] - want) / np.linalg.norm(want) < 1e-5
+        dec = orc.attn_decode(q[t], kc, vc, n_head, n_kv, hd, lo, pos)
+        assert np.linalg.norm(got[t] - dec) / np.linalg.norm(dec) < 1e-5
+
+
+def test_attn_prefill_first_token_is_v_row(orc):
+    # token 0 at position 0 sees one key: its output is that position's V row
+    n_head, n_kv, hd = 4, 2, 128
+    kc, vc = make_cache(orc, 3, n_kv, hd, seed=9)
+    q = np.random.default_rng(2).standard_normal((3, n_head * hd)).astype(np.float32)
+    out = orc.attn_prefill(q, kc, vc, 3, n_head, n_kv, hd, 0).reshape(3, n_head, hd)
+    V = dequant_q8_rows(orc, vc, 3 * n_kv * hd).reshape(3, n_kv, hd)
+    for h in range(n_head):
+        assert np.array_equal(out[0, h], V[0, h // 2])
+    # a window of 1: every token sees only its own position
+    out = orc.attn_prefill(q, kc, vc, 3, n_head, n_kv, hd, 0, n_swa=1).reshape(3, n_head, hd)
+    for t in range(3):
+        for h in range(n_head):
+            assert np.array_equal(out[t, h], V[t, h // 2])
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,pos0,n_tok,n_swa", PREFILL_CASES)
+def test_attn_prefill_vs_reference(orc, ref, n_head, n_kv, hd, pos0, n_tok, n_swa):
+    """The compiled reference attention_prefill_cpu_q8 (oracle/_ref)."""
+    kc, vc = make_cache(orc, pos0 + n_tok, n_kv, hd, seed=pos0 + 2 * n_tok)
+    q = np.random.default_rng(n_tok + 1).standard_normal((n_tok, n_head * hd)).astype(np.float32)
+    got = orc.attn_prefill(q, kc, vc, n_tok, n_head, n_kv, hd, pos0, n_swa)
+    want = ref.attn_prefill(q, kc, vc, n_tok, n_head, n_kv, hd, pos0, n_swa)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) < 2e-6
+    assert np.abs(got - want).max() < 1e-5
+
+
 def test_softmax(orc):
     s = np.random.default_rng(1).standard_normal(1000).astype(np.float32) * 5
     p = orc.softmax(s)
