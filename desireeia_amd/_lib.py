@@ -49,6 +49,8 @@ SIGNATURES = {
     "dq_attn_prefill_q8": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_u32, c_u32, c_u32, c_p,
                                    c_p]),
     "dq_layer_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
+    "dq_layer_prefill_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
+    "dq_layer_prefill": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_u32, c_u32, c_p, c_p, c_u32, c_p, c_size, c_p]),
     "dq_layer_decode": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_p, c_u32, c_p, c_p, c_u32, c_p, c_size, c_p]),
     "dq_silu_mul": (c_int, [c_p, c_p, c_size, c_p, c_p]),
     "dq_moe_route": (c_int, [c_p, c_u32, c_u32, c_u32, c_int, c_f, c_p, c_p, c_p]),

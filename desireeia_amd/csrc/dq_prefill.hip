@@ -382,6 +382,124 @@ __global__ __launch_bounds__(64) void rope_kv_batch_kernel(float* __restrict__ q
     dq_q8_0_row128(x0, x1, j, (kind == 1 ? kc : vc) + (size_t)(pos0 + t) * pos_bytes + (size_t)hh * (HD / 32) * DQ_SZ_Q8_0);
 }
 
+// rms_norm_vec (models/dense_forward.cpp:129-165) of every row of a
+// [n_tok][n] array: squares in float summed in double, scale =
+// 1/sqrtf(mean + eps), y = x * scale * w. With b: x = a + b first (the
+// attention residual, :3549-3557), written to h. One workgroup per row.
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                           float* __restrict__ h, const float* __restrict__ w, int n,
+                                                           float eps, float* __restrict__ y) {
+    __shared__ double part[4];
+    const size_t row = (size_t)blockIdx.x * n;
+    const int t = threadIdx.x;
+    double acc = 0.0;
+    for (int i = 4 * t; i < n; i += 1024) {
+        float4 x = *reinterpret_cast<const float4*>(a + row + i);
+        if (b) {
+            const float4 c = *reinterpret_cast<const float4*>(b + row + i);
+            x = make_float4(x.x + c.x, x.y + c.y, x.z + c.z, x.w + c.w);
+            if (h) *reinterpret_cast<float4*>(h + row + i) = x;
+        }
+        const float s0 = x.x * x.x, s1 = x.y * x.y, s2 = x.z * x.z, s3 = x.w * x.w;
+        acc += (double)s0;
+        acc += (double)s1;
+        acc += (double)s2;
+        acc += (double)s3;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, DQ_WAVE);
+    if ((t & 63) == 0) part[t >> 6] = acc;
+    __syncthreads();
+    const double sum = (part[0] + part[1]) + (part[2] + part[3]);
+    const float sc = 1.0f / sqrtf((float)(sum / (double)n) + eps);
+    for (int i = 4 * t; i < n; i += 1024) {
+        float4 x = *reinterpret_cast<const float4*>(a + row + i);
+        if (b) {
+            const float4 c = *reinterpret_cast<const float4*>(b + row + i);
+            x = make_float4(x.x + c.x, x.y + c.y, x.z + c.z, x.w + c.w);
+        }
+        const float4 ww = *reinterpret_cast<const float4*>(w + i);
+        *reinterpret_cast<float4*>(y + row + i) =
+            make_float4(x.x * sc * ww.x, x.y * sc * ww.y, x.z * sc * ww.z, x.w * sc * ww.w);
+    }
+}
+
+// out = a + b (the FFN residual, models/dense_forward.cpp:3616-3624), 4 per lane.
+__global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a, const float* __restrict__ b, size_t n4,
+                                                 float* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const float4 x = reinterpret_cast<const float4*>(a)[i];
+    const float4 y = reinterpret_cast<const float4*>(b)[i];
+    reinterpret_cast<float4*>(out)[i] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+}
+
+// h = silu(gate) * up, silu(x) = x / (1 + expf(-x)) (models/dense_forward.cpp
+// :53-55, :3606-3611), in place into up, 4 per lane.
+__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float* __restrict__ gate, float* __restrict__ up,
+                                                           size_t n4) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const float4 g = reinterpret_cast<const float4*>(gate)[i];
+    const float4 u = reinterpret_cast<const float4*>(up)[i];
+    reinterpret_cast<float4*>(up)[i] = make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
+                                                   g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
+}
+
+// ---------------------------------------------------------- layer prefill --
+// Workspace of dq_layer_prefill: fp32 activations of the chunk, then one
+// GEMM activation workspace per K-quant format (sized for the widest input).
+struct PrefillWs {
+    float *xn, *q, *k, *v, *attn, *h, *gate, *up, *down;
+    uint8_t* gw[2];  // Q4_K, Q6_K
+    size_t gw_bytes, total;
+};
+
+bool prefill_layer_ok(const dq_layer_t* L) {
+    const int f[7] = {L->fmt_q, L->fmt_k, L->fmt_v, L->fmt_o, L->fmt_gate, L->fmt_up, L->fmt_down};
+    for (int i = 0; i < 7; ++i)
+        if (f[i] != DQ_FMT_Q4_K && f[i] != DQ_FMT_Q6_K) return false;
+    if (L->head_dim != 128 || L->n_head_kv == 0 || L->n_head % L->n_head_kv) return false;
+    if (L->n_embd % 256 || L->n_ff % 256 || ((size_t)L->n_head * L->head_dim) % 256) return false;
+    if (L->n_rot == 0 || L->n_rot > L->head_dim || L->n_rot % 2) return false;
+    return true;
+}
+
+PrefillWs prefill_carve(const dq_layer_t* L, uint32_t n_tok, uint8_t* base) {
+    PrefillWs w{};
+    const size_t E = L->n_embd, QD = (size_t)L->n_head * L->head_dim, KVD = (size_t)L->n_head_kv * L->head_dim;
+    const size_t F = L->n_ff, T = n_tok;
+    size_t off = 0;
+    auto take = [&](size_t floats) {
+        float* p = base ? reinterpret_cast<float*>(base + off) : nullptr;
+        off += dq_align256(floats * 4);
+        return p;
+    };
+    w.xn = take(T * E);
+    w.q = take(T * QD);
+    w.k = take(T * KVD);
+    w.v = take(T * KVD);
+    w.attn = take(T * QD);
+    w.h = take(T * E);
+    w.gate = take(T * F);
+    w.up = take(T * F);
+    w.down = take(T * E);
+    size_t gb = 0;
+    const size_t cols[3] = {E, QD, F};
+    for (int f = 0; f < 2; ++f)
+        for (size_t c : cols) {
+            size_t b = 0;
+            if (dq_gemm_workspace_bytes(f == 0 ? DQ_FMT_Q4_K : DQ_FMT_Q6_K, 1, c, T, &b) == DQ_OK && b > gb) gb = b;
+        }
+    w.gw_bytes = dq_align256(gb);
+    for (int f = 0; f < 2; ++f) {
+        w.gw[f] = base ? base + off : nullptr;
+        off += w.gw_bytes;
+    }
+    w.total = off;
+    return w;
+}
+
 template <int HD>
 int launch_prefill(const PrefillArgs& a, int grid, hipStream_t s) {
     attn_prefill_kernel<HD><<<grid, NT, 0, s>>>(a);
@@ -459,6 +577,93 @@ int dq_attn_prefill_q8(const float* d_q, const void* d_kc, const void* d_vc, uin
     case 128: return launch_prefill<128>(a, grid, s);
     default: return launch_prefill<256>(a, grid, s);
     }
+}
+
+int dq_layer_prefill_workspace_bytes(const dq_layer_t* L, uint32_t n_tok, size_t* bytes) {
+    if (!L || !bytes) return DQ_ERR_INVALID_ARG;
+    if (!prefill_layer_ok(L)) return DQ_ERR_NOT_SUPPORTED;
+    *bytes = prefill_carve(L, n_tok, nullptr).total;
+    return DQ_OK;
+}
+
+#define DQP_TRY(x)                     \
+    do {                               \
+        const int rc_ = (x);           \
+        if (rc_ != DQ_OK) return rc_;  \
+    } while (0)
+
+int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, const float* d_rope, uint32_t pos0,
+                     uint32_t n_tok, uint32_t n_swa, void* d_kc, void* d_vc, uint32_t n_ctx, void* d_work,
+                     size_t work_bytes, void* stream) {
+    if (!L || !d_x || !d_x_out || !d_kc || !d_vc) return DQ_ERR_INVALID_ARG;
+    if (!prefill_layer_ok(L)) return DQ_ERR_NOT_SUPPORTED;
+    if (n_tok == 0) return DQ_OK;
+    if ((uint64_t)pos0 + n_tok > n_ctx || n_tok > 65535) return DQ_ERR_INVALID_ARG;
+    const PrefillWs w = prefill_carve(L, n_tok, (uint8_t*)d_work);
+    if (!d_work || work_bytes < w.total) return DQ_ERR_INVALID_ARG;
+    const hipStream_t s = (hipStream_t)stream;
+    const size_t E = L->n_embd, QD = (size_t)L->n_head * L->head_dim, KVD = (size_t)L->n_head_kv * L->head_dim;
+    const size_t F = L->n_ff, T = n_tok;
+    auto gw = [&](int fmt) { return w.gw[fmt == DQ_FMT_Q4_K ? 0 : 1]; };
+    // products of one input x [T][cols] with up to three matrices: one
+    // activation quantization per distinct format
+    auto products = [&](const float* x, size_t cols, int n, const int* fmt, const void* const* wm, const size_t* rows,
+                        float* const* y) -> int {
+        bool done[2] = {false, false};
+        for (int j = 0; j < n; ++j) {
+            const int fi = fmt[j] == DQ_FMT_Q4_K ? 0 : 1;
+            if (!done[fi]) {
+                DQP_TRY(dq_quantize_act_f16(fmt[j], x, cols, T, gw(fmt[j]), stream));
+                done[fi] = true;
+            }
+            DQP_TRY(dq_gemm_f16act(fmt[j], wm[j], rows[j], cols, gw(fmt[j]), T, y[j], stream));
+        }
+        return DQ_OK;
+    };
+    // attention block (models/dense_forward.cpp:3264-3290, 3300-3362, 3430-3460)
+    rms_norm_rows_kernel<<<n_tok, 256, 0, s>>>(d_x, nullptr, nullptr, L->attn_norm, (int)E, L->rms_eps, w.xn);
+    DQP_TRY(dq_launch_status());
+    {
+        const int f[3] = {L->fmt_q, L->fmt_k, L->fmt_v};
+        const void* m[3] = {L->wq, L->wk, L->wv};
+        const size_t r[3] = {QD, KVD, KVD};
+        float* const y[3] = {w.q, w.k, w.v};
+        DQP_TRY(products(w.xn, E, 3, f, m, r, y));
+    }
+    DQP_TRY(dq_rope_kv_write_batch(w.q, w.k, w.v, QD, KVD, d_rope, L->n_rot, n_tok, L->n_head, L->n_head_kv,
+                                   L->head_dim, d_kc, d_vc, pos0, n_ctx, stream));
+    DQP_TRY(dq_attn_prefill_q8(w.q, d_kc, d_vc, n_tok, L->n_head, L->n_head_kv, L->head_dim, (uint32_t)QD, pos0,
+                               n_swa, n_ctx, w.attn, stream));
+    {
+        const int f[1] = {L->fmt_o};
+        const void* m[1] = {L->wo};
+        const size_t r[1] = {E};
+        float* const y[1] = {w.down};
+        DQP_TRY(products(w.attn, QD, 1, f, m, r, y));
+    }
+    // residual + FFN norm (:3539-3560), gated FFN (:3600-3624)
+    rms_norm_rows_kernel<<<n_tok, 256, 0, s>>>(w.down, d_x, w.h, L->ffn_norm, (int)E, L->rms_eps, w.xn);
+    DQP_TRY(dq_launch_status());
+    {
+        const int f[2] = {L->fmt_up, L->fmt_gate};
+        const void* m[2] = {L->wup, L->wgate};
+        const size_t r[2] = {F, F};
+        float* const y[2] = {w.up, w.gate};
+        DQP_TRY(products(w.xn, E, 2, f, m, r, y));
+    }
+    const size_t nf4 = T * F / 4;
+    silu_mul_rows_kernel<<<(unsigned)((nf4 + 255) / 256), 256, 0, s>>>(w.gate, w.up, nf4);
+    DQP_TRY(dq_launch_status());
+    {
+        const int f[1] = {L->fmt_down};
+        const void* m[1] = {L->wdown};
+        const size_t r[1] = {E};
+        float* const y[1] = {w.down};
+        DQP_TRY(products(w.up, F, 1, f, m, r, y));
+    }
+    const size_t ne4 = T * E / 4;
+    add_kernel<<<(unsigned)((ne4 + 255) / 256), 256, 0, s>>>(w.down, w.h, ne4, d_x_out);
+    return dq_launch_status();
 }
 
 }  // extern "C"

@@ -350,6 +350,28 @@ class DecoderLayer:
         return y
 
 
+    def prefill_workspace(self, n_tok):
+        lib = _lib.load()
+        n = ctypes.c_size_t(0)
+        _lib.check(lib.dq_layer_prefill_workspace_bytes(ctypes.byref(self.desc), n_tok, ctypes.byref(n)),
+                   "dq_layer_prefill_workspace_bytes")
+        return torch.empty(max(n.value, 1), dtype=torch.uint8, device=self.attn_norm.device)
+
+    def prefill(self, x, pos0, out=None, n_swa=0, work=None, rope=None):
+        """x: device [n_tok][n_embd], the chunk's tokens at positions pos0..;
+        the RoPE tables of the chunk are built here unless given ([n_tok][n_rot])."""
+        lib = _lib.load()
+        n_tok = x.shape[0]
+        y = out if out is not None else torch.empty_like(x)
+        if rope is None:
+            rope = torch.stack([rope_cache(self.n_rot, pos0 + t, self.rope_theta) for t in range(n_tok)]).to(x.device)
+        wk = work if work is not None else self.prefill_workspace(n_tok)
+        _lib.check(lib.dq_layer_prefill(ctypes.byref(self.desc), _ptr(x), _ptr(y), _ptr(rope), int(pos0), n_tok,
+                                        int(n_swa), _ptr(self.cache.k), _ptr(self.cache.v), self.cache.n_ctx,
+                                        _ptr(wk), wk.numel(), _stream()), "dq_layer_prefill")
+        return y
+
+
 class MoeLayer:
     """Expert FFN of one MoE layer on the device (dq_moe_ffn): stacked Q4_K
     experts, gate/up [n_expert * n_ff][n_embd] and down [n_expert * n_embd][n_ff]

@@ -267,6 +267,25 @@ int dq_layer_decode(const dq_layer_t* layer, const float* d_x, float* d_x_out, c
                     const int32_t* d_pos, uint32_t cc_start, void* d_kc, void* d_vc, uint32_t n_ctx, void* d_work,
                     size_t work_bytes, void* stream);
 
+/* The same layer for a prompt chunk of n_tok consecutive tokens at positions
+ * [pos0, pos0 + n_tok): the CPU batch branch of models/dense_forward.cpp
+ * (:3260-3290 norm and Q/K/V through matvec_batch, :3300-3362 RoPE and KV
+ * rows per token, :3430-3460 attention_prefill_cpu_q8, :3539-3560 output
+ * projection, residual and FFN norm, :3600-3624 gated SiLU FFN and residual)
+ * that cuda_layer_forward_batch (core/engine.h:754-797, backend_cuda.cu:8466)
+ * runs on the GPU. Every product is the prefill GEMM (dq_gemm: the i8 GEMM
+ * semantics of matmul_q4_k_batch / matmul_q6_k_batch), so all seven matrices
+ * must be Q4_K or Q6_K; attention is dq_attn_prefill_q8 (n_swa > 0: sliding
+ * window). d_x, d_x_out: [n_tok][n_embd] device rows (may alias); d_rope:
+ * [n_tok][n_rot] cos/sin tables (dq_rope_cache(pos0 + t)) or NULL. The K/V
+ * rows of the chunk are written into the caches. Shapes as dq_layer_decode
+ * plus: n_rot even and <= head_dim; n_tok <= 65535. d_work:
+ * dq_layer_prefill_workspace_bytes(n_tok) bytes. */
+int dq_layer_prefill_workspace_bytes(const dq_layer_t* layer, uint32_t n_tok, size_t* bytes);
+int dq_layer_prefill(const dq_layer_t* layer, const float* d_x, float* d_x_out, const float* d_rope, uint32_t pos0,
+                     uint32_t n_tok, uint32_t n_swa, void* d_kc, void* d_vc, uint32_t n_ctx, void* d_work,
+                     size_t work_bytes, void* stream);
+
 
 /* ------------------------------------------------------------------ MoE */
 

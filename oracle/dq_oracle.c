@@ -1003,6 +1003,58 @@ int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t po
     return rc ? DQO_ERR_NOT_SUPPORTED : DQO_OK;
 }
 
+/* The CPU batch branch of models/dense_forward.cpp for a prompt chunk of
+ * n_tok tokens at positions pos0..: per token rms_norm (:3264-3273), Q/K/V
+ * through matvec_batch (:3286-3290, matmul_q4_k_batch / matmul_q6_k_batch:
+ * dqo_gemm), per token RoPE and KV rows (:3347-3362), attention over the
+ * cache (:3449-3460, attention_prefill_cpu_q8), output projection, residual
+ * and FFN norm (:3539-3560), up/gate, silu(gate) * up, down, residual
+ * (:3600-3624). RoPE over the whole head (n_rot = head_dim). */
+int dqo_layer_prefill(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t pos0, uint32_t n_tok,
+                      uint32_t n_swa, const float* x, float* x_out) {
+    const size_t E = L->n_embd, hd = L->head_dim, T = n_tok;
+    const size_t qd = (size_t)L->n_head * hd, kvd = (size_t)L->n_head_kv * hd, F = L->n_ff;
+    float* xn = (float*)malloc(T * E * sizeof(float));
+    float* q = (float*)malloc(T * qd * sizeof(float));
+    float* k = (float*)malloc(T * kvd * sizeof(float));
+    float* v = (float*)malloc(T * kvd * sizeof(float));
+    float* ao = (float*)malloc(T * qd * sizeof(float));
+    float* proj = (float*)malloc(T * E * sizeof(float));
+    float* up = (float*)malloc(T * F * sizeof(float));
+    float* gate = (float*)malloc(T * F * sizeof(float));
+    float* fout = (float*)malloc(T * E * sizeof(float));
+    float* rope = (float*)malloc(hd * sizeof(float));
+    int rc = DQO_OK;
+    for (size_t t = 0; t < T; ++t) dqo_rms_norm(x + t * E, L->attn_norm, xn + t * E, E, L->rms_eps);
+    rc |= dqo_gemm(L->fmt_q, L->wq, qd, E, xn, T, q, 0, 0, 0, 0);
+    rc |= dqo_gemm(L->fmt_k, L->wk, kvd, E, xn, T, k, 0, 0, 0, 0);
+    rc |= dqo_gemm(L->fmt_v, L->wv, kvd, E, xn, T, v, 0, 0, 0, 0);
+    const size_t row_bytes = hd / 32 * SZ_Q8_0;
+    const size_t pos_bytes = (size_t)L->n_head_kv * row_bytes;
+    for (size_t t = 0; t < T; ++t) {
+        const uint32_t pos = pos0 + (uint32_t)t;
+        dqo_rope_cache(rope, hd, pos, L->rope_theta);
+        for (uint32_t h = 0; h < L->n_head; ++h) dqo_rope_neox(q + t * qd + h * hd, hd, rope);
+        for (uint32_t h = 0; h < L->n_head_kv; ++h) {
+            dqo_rope_neox(k + t * kvd + h * hd, hd, rope);
+            dqo_kv_quantize_row(k + t * kvd + h * hd, hd, kc + (size_t)pos * pos_bytes + h * row_bytes);
+            dqo_kv_quantize_row(v + t * kvd + h * hd, hd, vc + (size_t)pos * pos_bytes + h * row_bytes);
+        }
+    }
+    rc |= dqo_attn_prefill_q8(q, ao, n_tok, L->n_head, L->n_head / L->n_head_kv, (uint32_t)hd, (uint32_t)qd, kc, vc,
+                              row_bytes, pos_bytes, pos0, n_swa, 1.0f / sqrtf((float)hd));
+    rc |= dqo_gemm(L->fmt_o, L->wo, E, qd, ao, T, proj, 0, 0, 0, 0);
+    for (size_t i = 0; i < T * E; ++i) proj[i] += x[i];
+    for (size_t t = 0; t < T; ++t) dqo_rms_norm(proj + t * E, L->ffn_norm, xn + t * E, E, L->rms_eps);
+    rc |= dqo_gemm(L->fmt_up, L->wup, F, E, xn, T, up, 0, 0, 0, 0);
+    rc |= dqo_gemm(L->fmt_gate, L->wgate, F, E, xn, T, gate, 0, 0, 0, 0);
+    for (size_t i = 0; i < T * F; ++i) up[i] = dqo_silu(gate[i]) * up[i];
+    rc |= dqo_gemm(L->fmt_down, L->wdown, E, F, up, T, fout, 0, 0, 0, 0);
+    for (size_t i = 0; i < T * E; ++i) x_out[i] = fout[i] + proj[i];
+    free(xn); free(q); free(k); free(v); free(ao); free(proj); free(up); free(gate); free(fout); free(rope);
+    return rc ? DQO_ERR_NOT_SUPPORTED : DQO_OK;
+}
+
 /* models/dense_forward.cpp:1524-1560 expert_ffn (stacked experts, matvec_raw
  * -> matmul_q4_k per token) and the combine at :4160-4181. */
 int dqo_moe_ffn(int fmt, const uint8_t* wgate, const uint8_t* wup, const uint8_t* wdown,

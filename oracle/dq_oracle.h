@@ -129,6 +129,12 @@ int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t po
                      const float* x, float* x_out, float* q_out, float* k_out,
                      float* v_out, float* attn_out);
 
+/* The same layer for a prompt chunk of n_tok tokens at positions pos0..
+ * (the batch branch of models/dense_forward.cpp:3260-3624): x/x_out
+ * [n_tok][n_embd]; the chunk's K/V rows are written into kc/vc. */
+int dqo_layer_prefill(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t pos0, uint32_t n_tok,
+                      uint32_t n_swa, const float* x, float* x_out);
+
 /* MoE expert FFN for n_tok tokens (dense_forward.cpp:1524-1560, combine at
  * :4160-4181). Experts stacked: gate/up [n_expert*n_ff][n_embd] rows,
  * down [n_expert*n_embd][n_ff] rows, all of format fmt. */

@@ -83,6 +83,7 @@ class Oracle:
         L.dqo_silu.argtypes = [c_f]
         L.dqo_softmax.argtypes = [c_p, c_size]
         L.dqo_layer_decode.argtypes = [ctypes.POINTER(LayerArgs), c_p, c_p, c_u32, c_p, c_p, c_p, c_p, c_p, c_p]
+        L.dqo_layer_prefill.argtypes = [ctypes.POINTER(LayerArgs), c_p, c_p, c_u32, c_u32, c_u32, c_p, c_p]
         L.dqo_moe_ffn.argtypes = [c_int, c_p, c_p, c_p, c_u32, c_u32, c_u32, c_p, c_p, c_u32, c_u32, c_int, c_p,
                                   c_u32, c_u32]
 
@@ -218,6 +219,15 @@ class Oracle:
         s = np.ascontiguousarray(s, np.float32).copy()
         self.L.dqo_softmax(_p(s), s.size)
         return s
+
+    def layer_prefill(self, args, kc, vc, pos0, x, n_swa=0):
+        """x: [n_tok][n_embd]; kc/vc: writable uint8 numpy arrays (one layer)."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty_like(x)
+        rc = self.L.dqo_layer_prefill(ctypes.byref(args), _p(kc), _p(vc), pos0, x.shape[0], n_swa, _p(x), _p(out))
+        if rc != 0:
+            raise ValueError(f"layer_prefill rc={rc}")
+        return out
 
     def layer_decode(self, args, kc, vc, pos, x):
         """args: LayerArgs; kc/vc: writable uint8 numpy arrays (one layer)."""

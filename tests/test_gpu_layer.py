@@ -23,7 +23,7 @@ def rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed):
+def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0)):
     from oracle.oracle import LayerArgs
     hd = 128
     qd, kvd = n_head * hd, n_kv * hd
@@ -32,8 +32,8 @@ def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed):
               "gate": (Q4K, F, E), "up": (Q4K, F, E), "down": (Q6K, E, F)}
     gg = {nm: (qt, synth.gen_weights(qt, r, c, seed=seed + i)) for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
     rng = np.random.default_rng(seed)
-    attn_norm = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32)
-    ffn_norm = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+    attn_norm = (norm_scale[0] * (1 + 0.02 * rng.standard_normal(E))).astype(np.float32)
+    ffn_norm = (norm_scale[1] * (1 + 0.02 * rng.standard_normal(E))).astype(np.float32)
     mats = {nm: ops.QuantMatrix.from_gguf(qt, w, shapes[nm][1], shapes[nm][2], device=gpu)
             for nm, (qt, w) in gg.items()}
     layer = ops.DecoderLayer(mats, torch.from_numpy(attn_norm), torch.from_numpy(ffn_norm), n_head, n_kv, hd, n_ctx,

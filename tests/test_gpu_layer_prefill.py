@@ -1,0 +1,201 @@
+"""One Llama-style decoder layer over a prompt chunk on the GPU
+(dq_layer_prefill) against the oracle's composition of the reference's CPU
+batch branch (models/dense_forward.cpp:3260-3624).
+
+What is pinned, and to what bound:
+  * every stage on the oracle's own inputs: the seven products within the
+    prefill GEMM's 4e-3 (they measure ~4e-4), attention within 1e-3, norms,
+    RoPE and K/V rows bit-exact;
+  * the fused layer is bit-identical to the chain of those tested entry
+    points (host norm / RoPE / SiLU, which match the GPU bit for bit);
+  * the oracle's layer equals a composition of its pieces done here in
+    numpy (1e-6);
+  * end to end, layer output within 3e-2 norm-wise of the oracle.
+The end-to-end bound is loose by construction: the layer re-quantizes its
+intermediates five times (the K/V rows and the per-32 int8 inputs of four
+GEMMs). A product difference e flips ~127 e / (amax / rms) of those roundings
+by one step (1/50 of the rms each), ~8x per stage, and the synthetic Q4_K
+weights (entry mean 1.4 against rms 2.2) make some tokens' products nearly
+cancel, amplifying relative differences further: tokens measure 2e-3 to 6e-2.
+The layers use RMSNorm weights of 0.25 / sqrt(E) and 0.3 / sqrt(E) so that
+scores and FFN activations are O(1) (with unit norms a 4096-wide layer's
+softmax is an argmax); the chunking test, GPU against GPU, keeps unit norms.
+Splitting a prompt into chunks leaves the result unchanged, and decode after
+a prefill continues from its cache."""
+import numpy as np
+import pytest
+import torch
+
+from desireeia_amd import _lib, ops, synth
+
+from test_gpu_layer import dequant_rows, make_layer, rel
+
+pytestmark = pytest.mark.gpu
+TOL_GEMM = 4e-3
+TOL_ATTN = 1e-3
+TOL_LAYER = 3e-2
+HD = 128
+
+
+def conditioned(E):
+    return (0.25 / np.sqrt(E), 0.3 / np.sqrt(E))
+
+
+def chain(layer, keep, orc, x, pos0, gemm, attention):
+    """The layer as a chain of stages with the given product and attention
+    functions (norms, RoPE, K/V rows, SiLU on the host with the oracle's
+    arithmetic)."""
+    T = x.shape[0]
+    nh, nkv = layer.n_head, layer.n_head_kv
+    xn = np.stack([orc.rms_norm(x[t], keep["attn_norm"], 1e-5) for t in range(T)])
+    q, k, v = gemm("q", xn), gemm("k", xn), gemm("v", xn)
+    for t in range(T):
+        tab = orc.rope_cache(HD, pos0 + t, 500000.0)
+        for h in range(nh):
+            q[t, h * HD:(h + 1) * HD] = orc.rope_neox(q[t, h * HD:(h + 1) * HD], HD, tab)
+        for h in range(nkv):
+            k[t, h * HD:(h + 1) * HD] = orc.rope_neox(k[t, h * HD:(h + 1) * HD], HD, tab)
+    kr, vr = orc.kv_quantize_row(k.reshape(-1)), orc.kv_quantize_row(v.reshape(-1))
+    attn = attention(q, kr, vr)
+    proj = gemm("o", attn)
+    h = proj + x
+    xn2 = np.stack([orc.rms_norm(h[t], keep["ffn_norm"], 1e-5) for t in range(T)])
+    up, gate = gemm("up", xn2), gemm("gate", xn2)
+    act = (gate / (np.float32(1) + np.exp(-gate))) * up
+    return dict(xn=xn, q=q, k=k, v=v, kr=kr, vr=vr, attn=attn, h=h, xn2=xn2, act=act, out=gemm("down", act) + h)
+
+
+def oracle_fns(layer, keep, orc, kc, vc, pos0, T):
+    pb = layer.cache.pos_bytes
+
+    def gemm(nm, inp):
+        m = layer.mats[nm]
+        return np.asarray(orc.gemm(synth.TYPE_OF_FMT[m.fmt], keep[nm], m.rows, m.cols, inp, inp.shape[0])).reshape(
+            inp.shape[0], -1)
+
+    def attention(q, kr, vr):
+        kk, vv = kc[:(pos0 + T) * pb].copy(), vc[:(pos0 + T) * pb].copy()
+        kk[pos0 * pb:], vv[pos0 * pb:] = kr, vr
+        return orc.attn_prefill(q, kk, vv, T, layer.n_head, layer.n_head_kv, HD, pos0).reshape(T, -1)
+    return gemm, attention
+
+
+def gpu_fns(gpu, layer, kc, vc, pos0, T):
+    pb = layer.cache.pos_bytes
+
+    def gemm(nm, inp):
+        return ops.gemm(layer.mats[nm], torch.from_numpy(np.ascontiguousarray(inp, np.float32)).to(gpu)).cpu().numpy()
+
+    def attention(q, kr, vr):
+        c = ops.KVCache(pos0 + T, layer.n_head_kv, HD, device=gpu)
+        c.k[:pos0 * pb] = torch.from_numpy(kc[:pos0 * pb]).to(gpu)
+        c.v[:pos0 * pb] = torch.from_numpy(vc[:pos0 * pb]).to(gpu)
+        c.k[pos0 * pb:] = torch.from_numpy(kr).to(gpu)
+        c.v[pos0 * pb:] = torch.from_numpy(vr).to(gpu)
+        return ops.attention_prefill(torch.from_numpy(np.ascontiguousarray(q)).to(gpu), c, layer.n_head,
+                                     pos0).cpu().numpy()
+    return gemm, attention
+
+
+@pytest.mark.parametrize("E,n_head,n_kv,F,pos0,n_tok", [
+    (4096, 32, 8, 14336, 1000, 16),  # config-4 layer shape after 1000 cached tokens
+    (512, 8, 2, 1536, 0, 40),        # prompt from position 0
+    (512, 4, 2, 1024, 70, 130),      # two attention query blocks, GEMM M tail
+])
+def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok):
+    print(f"layer_prefill E={E} heads={n_head}/{n_kv} F={F} pos0={pos0} n_tok={n_tok}", flush=True)
+    n_ctx = pos0 + n_tok + 2
+    layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos0, seed=E + pos0 + n_tok,
+                                           norm_scale=conditioned(E))
+    x = np.random.default_rng(n_tok).standard_normal((n_tok, E)).astype(np.float32)
+    og, oa = oracle_fns(layer, keep, orc, kc, vc, pos0, n_tok)
+    gg, ga = gpu_fns(gpu, layer, kc, vc, pos0, n_tok)
+    O = chain(layer, keep, orc, x, pos0, og, oa)
+    # every GPU stage on the oracle's inputs
+    for nm, inp in (("q", O["xn"]), ("k", O["xn"]), ("v", O["xn"]), ("o", O["attn"]), ("up", O["xn2"]),
+                    ("gate", O["xn2"]), ("down", O["act"])):
+        e = rel(gg(nm, inp), og(nm, inp))
+        print(f"  gemm {nm}: {e:.2e}", flush=True)
+        assert e <= TOL_GEMM
+    e = rel(ga(O["q"], O["kr"], O["vr"]), O["attn"])
+    print(f"  attention: {e:.2e}", flush=True)
+    assert e <= TOL_ATTN
+    # the oracle's layer is the composition of its pieces
+    kc1, vc1 = kc.copy(), vc.copy()
+    want = orc.layer_prefill(args, kc1, vc1, pos0, x)
+    assert rel(want, O["out"]) <= 1e-6
+    # the fused layer is the chain of the tested GPU entry points
+    got = layer.prefill(torch.from_numpy(x).to(gpu), pos0).cpu().numpy()
+    G = chain(layer, keep, orc, x, pos0, gg, ga)
+    e = rel(got, G["out"])
+    print(f"  fused vs chain of entry points: {e:.2e}", flush=True)
+    assert e <= 1e-6
+    e = rel(got, want)
+    print(f"  layer vs oracle: {e:.2e} (tokens {min(rel(got[t], want[t]) for t in range(n_tok)):.1e} .. "
+          f"{max(rel(got[t], want[t]) for t in range(n_tok)):.1e})", flush=True)
+    assert e <= TOL_LAYER
+    # the chunk's K/V rows: the GPU chain's rows exactly, the oracle's within its quantization step
+    pb = layer.cache.pos_bytes
+    kd, vd = layer.cache.k.cpu().numpy(), layer.cache.v.cpu().numpy()
+    assert np.array_equal(kd[:pos0 * pb], kc[:pos0 * pb]) and np.array_equal(vd[:pos0 * pb], vc[:pos0 * pb])
+    assert np.array_equal(kd[pos0 * pb:(pos0 + n_tok) * pb], G["kr"])
+    assert np.array_equal(vd[pos0 * pb:(pos0 + n_tok) * pb], G["vr"])
+    kvd = n_kv * HD
+    for dev, host in ((kd, kc1), (vd, vc1)):
+        a = dequant_rows(orc, dev[pos0 * pb:(pos0 + n_tok) * pb], n_tok * kvd)
+        b = dequant_rows(orc, host[pos0 * pb:(pos0 + n_tok) * pb], n_tok * kvd)
+        assert rel(a, b) <= 1e-2
+    assert not kd[(pos0 + n_tok) * pb:].any()
+
+
+def test_layer_prefill_chunks(gpu, orc):
+    """The engine runs a long prompt chunk by chunk (cuda_layer_forward_batch,
+    x_row0 / pos0): 100 tokens in one chunk or as 37 + 63 give the same layer
+    output and the same cache (the oracle: bit-identical)."""
+    E, n_head, n_kv, F, n_ctx = 512, 8, 2, 1024, 110
+    la, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, 5, seed=21)
+    lb, _, _, _, _ = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, 5, seed=21)
+    x = np.random.default_rng(22).standard_normal((100, E)).astype(np.float32)
+    dx = torch.from_numpy(x).to(gpu)
+    ya = la.prefill(dx, 5).cpu().numpy()
+    yb = np.concatenate([lb.prefill(dx[:37], 5).cpu().numpy(), lb.prefill(dx[37:], 42).cpu().numpy()])
+    e = rel(yb, ya)
+    print(f"  one chunk vs two: rel {e:.3e}", flush=True)
+    assert e <= 1e-5
+    assert torch.equal(la.cache.k, lb.cache.k) and torch.equal(la.cache.v, lb.cache.v)
+    # the oracle's chunking is exact
+    kc1, vc1, kc2, vc2 = kc.copy(), vc.copy(), kc.copy(), vc.copy()
+    w1 = orc.layer_prefill(args, kc1, vc1, 5, x)
+    w2 = np.concatenate([orc.layer_prefill(args, kc2, vc2, 5, x[:37]), orc.layer_prefill(args, kc2, vc2, 42, x[37:])])
+    assert np.array_equal(w1, w2) and np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
+
+
+def test_decode_after_prefill(gpu, orc):
+    """A 48-token prompt through dq_layer_prefill, then one decode step
+    (dq_layer_decode) on the cache it left: the oracle's decode step on that
+    same cache (decode-layer tolerance 1e-3)."""
+    E, n_head, n_kv, F, n_ctx = 512, 8, 2, 1024, 60
+    layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, 0, seed=31, norm_scale=conditioned(E))
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((48, E)).astype(np.float32)
+    xt = rng.standard_normal(E).astype(np.float32)
+    layer.prefill(torch.from_numpy(x).to(gpu), 0)
+    kc = layer.cache.k.cpu().numpy().copy()
+    vc = layer.cache.v.cpu().numpy().copy()
+    got = layer.decode(torch.from_numpy(xt).to(gpu), 48).cpu().numpy()
+    want = orc.layer_decode(args, kc, vc, 48, xt)[0]
+    e = rel(got, want)
+    print(f"  decode after prefill: rel {e:.3e}", flush=True)
+    assert e <= 1e-3
+
+
+def test_layer_prefill_window_and_errors(gpu, orc):
+    E, n_head, n_kv, F, n_ctx = 512, 4, 2, 1024, 80
+    layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, 10, seed=41,
+                                           norm_scale=conditioned(E))
+    x = np.random.default_rng(42).standard_normal((50, E)).astype(np.float32)
+    got = layer.prefill(torch.from_numpy(x).to(gpu), 10, n_swa=16).cpu().numpy()
+    want = orc.layer_prefill(args, kc, vc, 10, x, n_swa=16)
+    assert rel(got, want) <= TOL_LAYER
+    with pytest.raises(_lib.DqError):
+        layer.prefill(torch.from_numpy(x).to(gpu), 40)  # 40 + 50 > n_ctx
