@@ -157,6 +157,24 @@ class CudaLayerArgs(ctypes.Structure):
                    ("embd_mul", c_f)])
 
 
+class CudaLayerBatchArgs(ctypes.Structure):
+    """core/engine.h:764-796."""
+    _fields_ = ([(n, c_p) for n in ("wq_qs", "wq_scale", "wk_qs", "wk_scale", "wv_qs", "wv_scale", "wo_qs",
+                                    "wo_scale", "wgate_qs", "wgate_scale", "wup_qs", "wup_scale", "wdown_qs",
+                                    "wdown_scale", "wag_qs", "wag_scale", "bq", "bk", "bv", "attn_norm_w",
+                                    "ffn_norm_w", "q_norm_w", "k_norm_w", "post_attn_norm_w", "post_ffn_norm_w", "x",
+                                    "x_out")]
+                + [("x_out_row0", c_u32), ("rope_caches", c_p), ("host_kcache", c_p), ("host_vcache", c_p)]
+                + [(n, c_size) for n in ("n_embd", "q_dim", "kv_dim", "n_ff")]
+                + [(n, c_u32) for n in ("n_head", "n_head_kv", "heads_per_kv", "head_dim", "n_rot")]
+                + [("kv_layer_off", c_size)]
+                + [(n, c_u32) for n in ("pos0", "n_tok", "n_swa", "x_row0", "n_total")]
+                + [("rms_eps", c_f), ("act_gelu", c_int)]
+                + [(n, c_int) for n in ("fmt_q", "fmt_k", "fmt_v", "fmt_o", "fmt_gate", "fmt_up", "fmt_down",
+                                        "fmt_ag", "upload_x", "download_x", "upload_rope", "prepare_weights",
+                                        "rope_slot")])
+
+
 class MoeDesc(ctypes.Structure):
     """dq_moe_t of include/desireeia_hip.h."""
     _fields_ = [("n_expert", c_u32), ("n_expert_used", c_u32), ("n_embd", c_u32), ("n_ff", c_u32),

@@ -60,6 +60,16 @@ struct Engine {
     size_t kv_bytes = 0;
     std::unordered_map<const void*, WInfo> reg;
     std::unordered_map<const void*, LayerGraph> graphs;  // keyed by wq
+    // prefill: the prompt's activations, RoPE table slots, the layer
+    // workspace and norm weights, and the K/V rows still to be mirrored to
+    // the host cache (copied with the prompt's one synchronisation)
+    DevBuf px, prope[4], pwork, pnorm, pio;
+    struct Mirror {
+        uint8_t* k;
+        uint8_t* v;
+        size_t off, bytes;
+    };
+    std::vector<Mirror> mirror;
 };
 
 Engine g;
@@ -379,7 +389,10 @@ void cuda_free_device(void* p) {
 void cuda_backend_shutdown(void) {
     if (g.stream) (void)hipStreamSynchronize(g.stream);
     drop_graphs();
-    for (DevBuf* b : {&g.xbuf, &g.ybuf, &g.act, &g.work, &g.stage, &g.lx[0], &g.lx[1], &g.rope}) release(*b);
+    for (DevBuf* b : {&g.xbuf, &g.ybuf, &g.act, &g.work, &g.stage, &g.lx[0], &g.lx[1], &g.rope, &g.px, &g.prope[0],
+                      &g.prope[1], &g.prope[2], &g.prope[3], &g.pwork, &g.pnorm, &g.pio})
+        release(*b);
+    g.mirror.clear();
     cuda_kv_cache_release();
     if (g.stream) (void)hipStreamDestroy(g.stream);
     g.stream = nullptr;
@@ -802,16 +815,136 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
 int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, uint32_t n_head,
                          uint32_t heads_per_kv, uint32_t head_dim, uint32_t q_dim, size_t row_bytes, size_t pos_bytes,
                          size_t layer_off, uint32_t col0, uint32_t n_swa) {
-    (void)q_all, (void)out_all, (void)n_tokens, (void)n_head, (void)heads_per_kv, (void)head_dim, (void)q_dim;
-    (void)row_bytes, (void)pos_bytes, (void)layer_off, (void)col0, (void)n_swa;
-    return DQ_ERR_NOT_SUPPORTED;
+    if (!g.kc || n_tokens == 0 || n_head == 0 || heads_per_kv == 0 || n_head % heads_per_kv)
+        return DQ_ERR_NOT_SUPPORTED;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) return DQ_ERR_NOT_SUPPORTED;
+    const uint32_t n_kv = n_head / heads_per_kv;
+    if (row_bytes != (size_t)(head_dim / 32) * DQ_SZ_Q8_0 || pos_bytes != kv_pos_bytes(n_kv, head_dim))
+        return DQ_ERR_NOT_SUPPORTED;
+    if ((size_t)q_dim < (size_t)n_head * head_dim || q_dim % 4 || layer_off % 4) return DQ_ERR_NOT_SUPPORTED;
+    const uint32_t n_ctx = kv_positions(layer_off, pos_bytes);
+    if ((uint64_t)col0 + n_tokens > n_ctx) return DQ_ERR_NOT_SUPPORTED;
+    if (!q_all || !out_all) return DQ_ERR_INVALID_ARG;
+    if (!stream()) return DQ_ERR_IO;
+    const size_t n = (size_t)n_tokens * q_dim;
+    if (!reserve(g.pio, 2 * n * 4)) return DQ_ERR_IO;
+    const hipStream_t s = g.stream;
+    float* dq = (float*)g.pio.p;
+    float* dout = dq + n;
+    if (hipMemcpyAsync(dq, q_all, n * 4, hipMemcpyHostToDevice, s) != hipSuccess) return io_fail();
+    // columns past the heads keep the caller's values
+    if ((size_t)q_dim > (size_t)n_head * head_dim &&
+        hipMemcpyAsync(dout, out_all, n * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+        return io_fail();
+    if (dq_attn_prefill_q8(dq, g.kc + layer_off, g.vc + layer_off, n_tokens, n_head, n_kv, head_dim, q_dim, col0,
+                           n_swa, n_ctx, dout, s) != DQ_OK)
+        return io_fail();
+    if (hipMemcpyAsync(out_all, dout, n * 4, hipMemcpyDeviceToHost, s) != hipSuccess) return io_fail();
+    return sync();
 }
 
-int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* args) {
-    (void)args;
-    return DQ_ERR_NOT_SUPPORTED;
+int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
+    if (!A || !g.kc || A->n_tok == 0 || A->n_total == 0) return DQ_ERR_NOT_SUPPORTED;
+    // features outside the plain dense layer: the engine's CPU path runs them
+    if (A->wag_qs || A->bq || A->bk || A->bv || A->q_norm_w || A->k_norm_w || A->post_attn_norm_w ||
+        A->post_ffn_norm_w || A->act_gelu)
+        return DQ_ERR_NOT_SUPPORTED;
+    if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
+    if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
+        A->heads_per_kv != A->n_head / A->n_head_kv)
+        return DQ_ERR_NOT_SUPPORTED;
+    if (A->q_dim != (size_t)A->n_head * A->head_dim || A->kv_dim != (size_t)A->n_head_kv * A->head_dim)
+        return DQ_ERR_NOT_SUPPORTED;
+    if (A->n_embd > 0xFFFFFFFFu || A->n_ff > 0xFFFFFFFFu) return DQ_ERR_NOT_SUPPORTED;
+    if ((uint64_t)A->x_row0 + A->n_tok > A->n_total || A->n_tok > 65535) return DQ_ERR_NOT_SUPPORTED;
+    if (A->rope_caches && (A->n_rot == 0 || A->n_rot > A->head_dim || A->n_rot % 2 || A->rope_slot < 0 ||
+                           A->rope_slot > 3))
+        return DQ_ERR_NOT_SUPPORTED;
+    dq_layer_t L{};
+    L.n_embd = (uint32_t)A->n_embd;
+    L.n_head = A->n_head;
+    L.n_head_kv = A->n_head_kv;
+    L.head_dim = A->head_dim;
+    L.n_rot = A->rope_caches ? A->n_rot : A->head_dim;
+    L.n_ff = (uint32_t)A->n_ff;
+    L.rms_eps = A->rms_eps;
+    L.fmt_q = A->fmt_q, L.fmt_k = A->fmt_k, L.fmt_v = A->fmt_v, L.fmt_o = A->fmt_o;
+    L.fmt_gate = A->fmt_gate, L.fmt_up = A->fmt_up, L.fmt_down = A->fmt_down;
+    L.wq = A->wq_qs, L.wk = A->wk_qs, L.wv = A->wv_qs, L.wo = A->wo_qs;
+    L.wgate = A->wgate_qs, L.wup = A->wup_qs, L.wdown = A->wdown_qs;
+    const void* w[7] = {L.wq, L.wk, L.wv, L.wo, L.wgate, L.wup, L.wdown};
+    const int f[7] = {L.fmt_q, L.fmt_k, L.fmt_v, L.fmt_o, L.fmt_gate, L.fmt_up, L.fmt_down};
+    const size_t r[7] = {A->q_dim, A->kv_dim, A->kv_dim, A->n_embd, A->n_ff, A->n_ff, A->n_embd};
+    const size_t c[7] = {A->n_embd, A->n_embd, A->n_embd, A->q_dim, A->n_embd, A->n_embd, A->n_ff};
+    for (int j = 0; j < 7; ++j) {
+        const WInfo* wi = lookup(w[j]);
+        if (!wi || wi->base != w[j] || wi->fmt != f[j] || wi->rows != r[j] || wi->cols != c[j])
+            return DQ_ERR_NOT_SUPPORTED;
+    }
+    size_t wbytes = 0;
+    if (dq_layer_prefill_workspace_bytes(&L, A->n_tok, &wbytes) != DQ_OK) return DQ_ERR_NOT_SUPPORTED;
+    const size_t pb = kv_pos_bytes(A->n_head_kv, A->head_dim);
+    const uint32_t n_ctx = kv_positions(A->kv_layer_off, pb);
+    if ((uint64_t)A->pos0 + A->n_tok > n_ctx) return DQ_ERR_NOT_SUPPORTED;
+    if (A->upload_x && !A->x) return DQ_ERR_INVALID_ARG;
+    if (A->download_x && !A->x_out) return DQ_ERR_INVALID_ARG;
+    if (A->rope_caches && A->upload_rope == 0 && !g.prope[A->rope_slot].p) return DQ_ERR_INVALID_ARG;
+    if (!stream()) return DQ_ERR_IO;
+    const size_t E = A->n_embd, NT = A->n_total;
+    const int slot = A->rope_caches ? A->rope_slot : 0;
+    if (!reserve(g.px, NT * E * 4) || !reserve(g.pwork, wbytes) || !reserve(g.pnorm, 2 * dq_align256(E * 4)) ||
+        (A->rope_caches && !reserve(g.prope[slot], NT * A->n_rot * 4)))
+        return DQ_ERR_IO;
+    const hipStream_t s = g.stream;
+    if (A->upload_x) {
+        g.mirror.clear();  // left over by a prompt that stopped midway
+        if (hipMemcpyAsync(g.px.p, A->x, NT * E * 4, hipMemcpyHostToDevice, s) != hipSuccess) return io_fail();
+    }
+    if (A->rope_caches && A->upload_rope &&
+        hipMemcpyAsync(g.prope[slot].p, A->rope_caches, NT * A->n_rot * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+        return io_fail();
+    float* an = (float*)g.pnorm.p;
+    float* fn = (float*)((uint8_t*)g.pnorm.p + dq_align256(E * 4));
+    if (hipMemcpyAsync(an, A->attn_norm_w, E * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(fn, A->ffn_norm_w, E * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+        return io_fail();
+    L.attn_norm = an;
+    L.ffn_norm = fn;
+    float* xc = (float*)g.px.p + (size_t)A->x_row0 * E;  // this chunk's rows, updated in place
+    const float* rope = A->rope_caches ? (const float*)g.prope[slot].p + (size_t)A->x_row0 * A->n_rot : nullptr;
+    const int rc = dq_layer_prefill(&L, xc, xc, rope, A->pos0, A->n_tok, A->n_swa, g.kc + A->kv_layer_off,
+                                    g.vc + A->kv_layer_off, n_ctx, g.pwork.p, g.pwork.cap, s);
+    if (rc != DQ_OK) return rc == DQ_ERR_IO ? io_fail() : rc;
+    // the host cache follows the device rows (copied at the prompt's end)
+    if (A->host_kcache && A->host_vcache) {
+        const size_t off = A->kv_layer_off + (size_t)A->pos0 * pb;
+        g.mirror.push_back({(uint8_t*)A->host_kcache + off, (uint8_t*)A->host_vcache + off, off, (size_t)A->n_tok * pb});
+    }
+    if (!A->download_x) return DQ_OK;
+    for (const Engine::Mirror& m : g.mirror) {
+        if (hipMemcpyAsync(m.k, g.kc + m.off, m.bytes, hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipMemcpyAsync(m.v, g.vc + m.off, m.bytes, hipMemcpyDeviceToHost, s) != hipSuccess)
+            return io_fail();
+    }
+    g.mirror.clear();
+    const size_t r0 = A->x_out_row0 < A->n_total ? A->x_out_row0 : 0;
+    if (hipMemcpyAsync(A->x_out + r0 * E, (float*)g.px.p + r0 * E, (NT - r0) * E * 4, hipMemcpyDeviceToHost, s) !=
+        hipSuccess)
+        return io_fail();
+    return sync();
 }
 
-int cuda_prefill_chunk_tokens(void) { return 0; }
+// Tokens per prefill chunk: 8 per CU (2048 on 256 CUs: the chunk's GEMMs
+// fill the GPU with 128 x 256 tiles), within [1024, 4096].
+int cuda_prefill_chunk_tokens(void) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    const int n = 8 * cus;
+    return n < 1024 ? 1024 : (n > 4096 ? 4096 : n);
+}
 
 }  // extern "C"

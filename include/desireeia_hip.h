@@ -409,9 +409,40 @@ typedef struct CudaLayerArgs {
     const void* embd_qs; const void* embd_scale; float embd_mul;
 } CudaLayerArgs;
 
-/* The prefill-layer argument block (core/engine.h:764-796) is not read by
- * this backend: opaque here. */
-struct CudaLayerBatchArgs;
+/* The prefill-layer argument block, core/engine.h:764-796 (same fields,
+ * same order). x / x_out / rope_caches are host arrays of the whole prompt
+ * ([n_total][n_embd], [n_total][n_rot]); the call covers rows
+ * [x_row0, x_row0 + n_tok) at positions [pos0, pos0 + n_tok). */
+typedef struct CudaLayerBatchArgs {
+    const void* wq_qs; const void* wq_scale;
+    const void* wk_qs; const void* wk_scale;
+    const void* wv_qs; const void* wv_scale;
+    const void* wo_qs; const void* wo_scale;
+    const void* wgate_qs; const void* wgate_scale;
+    const void* wup_qs; const void* wup_scale;
+    const void* wdown_qs; const void* wdown_scale;
+    const void* wag_qs; const void* wag_scale;
+    const float* bq; const float* bk; const float* bv;
+    const float* attn_norm_w; const float* ffn_norm_w;
+    const float* q_norm_w; const float* k_norm_w;
+    const float* post_attn_norm_w; const float* post_ffn_norm_w;
+    const float* x;
+    float* x_out;
+    uint32_t x_out_row0;
+    const float* rope_caches;
+    void* host_kcache; void* host_vcache;
+    size_t n_embd; size_t q_dim; size_t kv_dim; size_t n_ff;
+    uint32_t n_head; uint32_t n_head_kv; uint32_t heads_per_kv;
+    uint32_t head_dim; uint32_t n_rot;
+    size_t kv_layer_off;
+    uint32_t pos0; uint32_t n_tok; uint32_t n_swa;
+    uint32_t x_row0; uint32_t n_total;
+    float rms_eps; int act_gelu;
+    int fmt_q; int fmt_k; int fmt_v; int fmt_o;
+    int fmt_gate; int fmt_up; int fmt_down; int fmt_ag;
+    int upload_x; int download_x; int upload_rope; int prepare_weights;
+    int rope_slot;
+} CudaLayerBatchArgs;
 
 /* Devices: core/engine.h:627-629. */
 int32_t cuda_gpu_count(void);
@@ -479,8 +510,23 @@ int cuda_attention_out(const void* d_wo_qs, const void* d_wo_scale, const float*
 int cuda_qkv_attention_out(const CudaQkvAttnArgs* args);
 int cuda_layer_forward(const CudaLayerArgs* args);
 
-/* Prefill attention and the prefill layer (core/engine.h:550-555, :797-798)
- * are outside this backend: NOT_SUPPORTED, and a chunk size of 0. */
+/* Prefill (core/engine.h:550-555, :797-798; backend_cuda.cu:3799-3870,
+ * :8457-8860).
+ * cuda_attention_batch: attention of n_tokens queries (host q_all, [n][q_dim])
+ *   at positions col0.. over the device KV cache of the layer at layer_off
+ *   (dq_attn_prefill_q8); out_all (host) receives [n][q_dim] (columns past
+ *   n_head * head_dim keep their values). head_dim 64/128/256 with the
+ *   cache's row_bytes / pos_bytes; otherwise NOT_SUPPORTED.
+ * cuda_layer_forward_batch: the dense layer over a prompt chunk
+ *   (dq_layer_prefill). The prompt's activations stay on the device
+ *   between layers and chunks: upload_x on the first call, download_x on the
+ *   last (rows from x_out_row0 on), which also copies every K/V row the
+ *   prompt wrote into host_kcache / host_vcache and synchronises once. RoPE
+ *   tables: rope_caches uploaded when upload_rope into slot rope_slot (0-3);
+ *   NULL = no RoPE. Matrices must be Q4_K / Q6_K uploads; biases, QK-norm,
+ *   sandwich norms, the attention gate, GELU and head_dim != 128:
+ *   NOT_SUPPORTED, before any device work.
+ * cuda_prefill_chunk_tokens: tokens per chunk, 8 per CU within [1024, 4096]. */
 int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, uint32_t n_head,
                          uint32_t heads_per_kv, uint32_t head_dim, uint32_t q_dim, size_t row_bytes, size_t pos_bytes,
                          size_t layer_off, uint32_t col0, uint32_t n_swa);

@@ -1,5 +1,6 @@
 """The engine-layer argument structs of include/desireeia_hip.h have the
-reference's field order (core/engine.h:536, :598-603, :675-691, :698-751), and
+reference's field order (core/engine.h:536, :598-603, :675-691, :698-751,
+:764-796), and
 the ctypes mirrors used by the tests agree with the C compiler's layout
 (no GPU needed: a C program prints sizeof/offsetof)."""
 import os
@@ -11,8 +12,8 @@ import pytest
 from desireeia_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-STRUCTS = [_lib.CudaKQuantJob, _lib.CudaQ80Job, _lib.CudaQkvAttnArgs, _lib.CudaLayerArgs, _lib.GemvJob,
-           _lib.MoeDesc]
+STRUCTS = [_lib.CudaKQuantJob, _lib.CudaQ80Job, _lib.CudaQkvAttnArgs, _lib.CudaLayerArgs,
+           _lib.CudaLayerBatchArgs, _lib.GemvJob, _lib.MoeDesc]
 C_NAME = {"GemvJob": "dq_gemv_job_t", "MoeDesc": "dq_moe_t"}
 
 
@@ -55,3 +56,11 @@ def test_reference_field_order():
     assert i("x") < i("rope_cache") < i("x_out") < i("n_embd") < i("rms_eps") < i("fmt_q") < i("upload_x")
     assert lay[-4:] == ["x_from_token", "embd_qs", "embd_scale", "embd_mul"]
     assert len(lay) == 62
+    bat = [f for f, _ in _lib.CudaLayerBatchArgs._fields_]
+    j = bat.index
+    # core/engine.h:764-796
+    assert bat[:2] == ["wq_qs", "wq_scale"] and bat[25:27] == ["x", "x_out"]
+    assert j("x_out") < j("x_out_row0") < j("rope_caches") < j("host_kcache") < j("n_embd") < j("kv_layer_off")
+    assert j("kv_layer_off") < j("pos0") < j("n_tok") < j("n_swa") < j("x_row0") < j("n_total") < j("rms_eps")
+    assert bat[-5:] == ["upload_x", "download_x", "upload_rope", "prepare_weights", "rope_slot"]
+    assert len(bat) == 61

@@ -390,7 +390,150 @@ def test_layer_forward_chain(lib, orc):
     lib.cuda_kv_cache_release()
 
 
-def test_out_of_scope_entries(lib):
+def test_prefill_chunk_tokens(lib):
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert lib.cuda_prefill_chunk_tokens() == min(4096, max(1024, 8 * cus))
+
+
+def test_attention_batch(lib, orc):
+    """cuda_attention_batch over the second layer of a two-layer device cache
+    (host q in, host out back): the oracle's prefill attention; padding
+    columns of q_dim keep the caller's values; unsupported shapes leave out."""
+    n_head, n_kv, hd, n_ctx, col0, n_tok = 16, 4, 128, 400, 250, 90
+    kc, vc, pb = prior_cache(orc, 2, n_ctx, n_kv, hd, col0 + n_tok, seed=7)
+    assert lib.cuda_kv_cache_reserve(kc.size)
+    assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+    q_dim = n_head * hd + 32
+    q = np.random.default_rng(8).standard_normal((n_tok, q_dim)).astype(np.float32)
+    out = np.full((n_tok, q_dim), 5.0, np.float32)
+    off = n_ctx * pb
+    rc = lib.cuda_attention_batch(P(q), P(out), n_tok, n_head, n_head // n_kv, hd, q_dim, hd // 32 * 34, pb, off,
+                                  col0, 0)
+    assert rc == OK
+    want = orc.attn_prefill(q, kc[off:], vc[off:], n_tok, n_head, n_kv, hd, col0, q_dim=q_dim,
+                            out=np.full(n_tok * q_dim, 5.0, np.float32)).reshape(n_tok, q_dim)
+    e = rel(out, want)
+    print(f"attention batch rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    assert np.all(out[:, n_head * hd:] == 5.0)
+    # sliding window
+    out2 = np.zeros((n_tok, q_dim), np.float32)
+    assert lib.cuda_attention_batch(P(q), P(out2), n_tok, n_head, n_head // n_kv, hd, q_dim, hd // 32 * 34, pb, off,
+                                    col0, 64) == OK
+    want2 = orc.attn_prefill(q, kc[off:], vc[off:], n_tok, n_head, n_kv, hd, col0, 64, q_dim=q_dim).reshape(n_tok, -1)
+    assert rel(out2, want2) <= TOL
+    keep = out.copy()
+    for args in ((n_tok, n_head, n_head // n_kv, 96, q_dim, 3 * 34, n_kv * 3 * 34, off, col0, 0),  # hd 96
+                 (n_tok, n_head, n_head // n_kv, hd, q_dim, hd // 32 * 34, pb, off, n_ctx - 10, 0),  # past the end
+                 (n_tok, n_head, n_head // n_kv, hd, q_dim, 100, pb, off, col0, 0)):  # foreign row size
+        assert lib.cuda_attention_batch(P(q), P(out), *args) == NOT_SUPPORTED
+    assert np.array_equal(out, keep)
+    lib.cuda_kv_cache_release()
+
+
+def batch_args(mats, an, fn, E, n_head, n_kv, F, layer_off, pos0, n_tok, x_row0, n_total, rope, x, x_out, hk, hv,
+               upload_x, download_x, upload_rope):
+    hd = 128
+    A = _lib.CudaLayerBatchArgs()
+    for nm, key in (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo"), ("gate", "wgate"), ("up", "wup"),
+                    ("down", "wdown")):
+        setattr(A, key + "_qs", mats[nm].qs)
+        setattr(A, key + "_scale", mats[nm].sc)
+        setattr(A, "fmt_" + nm, mats[nm].fmt)
+    A.attn_norm_w, A.ffn_norm_w = an.ctypes.data, fn.ctypes.data
+    A.x = x.ctypes.data if x is not None else None
+    A.x_out = x_out.ctypes.data if x_out is not None else None
+    A.rope_caches = rope.ctypes.data if rope is not None else None
+    A.host_kcache = hk.ctypes.data if hk is not None else None
+    A.host_vcache = hv.ctypes.data if hv is not None else None
+    A.n_embd, A.q_dim, A.kv_dim, A.n_ff = E, n_head * hd, n_kv * hd, F
+    A.n_head, A.n_head_kv, A.heads_per_kv, A.head_dim, A.n_rot = n_head, n_kv, n_head // n_kv, hd, hd
+    A.kv_layer_off, A.pos0, A.n_tok, A.n_swa, A.x_row0, A.n_total = layer_off, pos0, n_tok, 0, x_row0, n_total
+    A.rms_eps = 1e-5
+    A.upload_x, A.download_x, A.upload_rope, A.rope_slot = upload_x, download_x, upload_rope, 0
+    return A
+
+
+def test_layer_forward_batch(lib, orc):
+    """A 100-token prompt after 20 cached positions through two layers, layer
+    by layer, in chunks of 60 + 40 (cuda_layer_forward_batch with host x in
+    and out): the same result as dq_layer_prefill over whole-prompt chunks on
+    an identical device cache (bit-identical: the layer is row-independent),
+    the host cache mirror equal to the device rows, and the oracle's two
+    layers within the layer tolerance."""
+    import torch
+    from desireeia_amd import ops
+    E, n_head, n_kv, F, n_ctx, prior, T = 512, 8, 2, 1024, 128, 20, 100
+    hd = 128
+    kc, vc, pb = prior_cache(orc, 2, n_ctx, n_kv, hd, prior, seed=51)
+    assert lib.cuda_kv_cache_reserve(kc.size)
+    assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+    t = (Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K)
+    layers = [make_layer(lib, orc, E, n_head, n_kv, F, t, s) for s in (60, 80)]
+    for mats, an, fn, oa in layers:  # O(1) scores and FFN activations
+        an *= 0.25 / np.sqrt(E)
+        fn *= 0.3 / np.sqrt(E)
+    x = np.random.default_rng(52).standard_normal((T, E)).astype(np.float32)
+    rope = np.stack([orc.rope_cache(hd, prior + i, 500000.0) for i in range(T)])
+    out = np.full((T, E), np.nan, np.float32)
+    hk, hv = kc.copy(), vc.copy()
+    chunks = ((0, 60), (60, 40))
+    for li, (mats, an, fn, _) in enumerate(layers):
+        for ci, (r0, n) in enumerate(chunks):
+            first, last = li == 0 and ci == 0, li == 1 and ci == 1
+            A = batch_args(mats, an, fn, E, n_head, n_kv, F, li * n_ctx * pb, prior + r0, n, r0, T, rope, x, out, hk,
+                           hv, int(first), int(last), int(first))
+            assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == OK
+    dk, dv = np.zeros_like(kc), np.zeros_like(vc)
+    assert lib.cuda_kv_cache_download(P(dk), P(dv), kc.size)
+    assert np.array_equal(hk, dk) and np.array_equal(hv, dv)
+    # the same two layers through dq_layer_prefill on the packed matrices
+    dev = torch.device("cuda:0")
+    y = torch.from_numpy(x).to(dev)
+    drope = torch.from_numpy(rope).to(dev)
+    for li, (mats, an, fn, _) in enumerate(layers):
+        d = ops.LayerDesc(E, n_head, n_kv, hd, hd, F, 1e-5)
+        for nm in ("q", "k", "v", "o", "gate", "up", "down"):
+            setattr(d, "fmt_" + nm, mats[nm].fmt)
+            setattr(d, "w" + nm, mats[nm].qs)
+        dan, dfn = torch.from_numpy(an).to(dev), torch.from_numpy(fn).to(dev)
+        d.attn_norm, d.ffn_norm = dan.data_ptr(), dfn.data_ptr()
+        cache = ops.KVCache(n_ctx, n_kv, hd, device=dev)
+        cache.k.copy_(torch.from_numpy(kc[li * n_ctx * pb:(li + 1) * n_ctx * pb]))
+        cache.v.copy_(torch.from_numpy(vc[li * n_ctx * pb:(li + 1) * n_ctx * pb]))
+        n = ctypes.c_size_t(0)
+        assert lib.dq_layer_prefill_workspace_bytes(ctypes.byref(d), T, ctypes.byref(n)) == OK
+        wk = torch.empty(n.value, dtype=torch.uint8, device=dev)
+        assert lib.dq_layer_prefill(ctypes.byref(d), ops._ptr(y), ops._ptr(y), ops._ptr(drope), prior, T, 0,
+                                    ops._ptr(cache.k), ops._ptr(cache.v), n_ctx, ops._ptr(wk), wk.numel(),
+                                    ops._stream()) == OK
+        torch.cuda.synchronize()
+        assert np.array_equal(cache.k.cpu().numpy(), dk[li * n_ctx * pb:(li + 1) * n_ctx * pb])
+    e = rel(out, y.cpu().numpy())
+    print(f"engine chunks vs one dq_layer_prefill per layer: {e:.3e}", flush=True)
+    assert e <= 1e-6
+    # the oracle's two layers
+    k0, v0 = kc[:n_ctx * pb].copy(), vc[:n_ctx * pb].copy()
+    k1, v1 = kc[n_ctx * pb:].copy(), vc[n_ctx * pb:].copy()
+    h = orc.layer_prefill(layers[0][3], k0, v0, prior, x)
+    want = orc.layer_prefill(layers[1][3], k1, v1, prior, h)
+    e = rel(out, want)
+    print(f"engine two layers vs oracle: {e:.3e}", flush=True)
+    assert e <= 3e-2
+    # features outside the plain layer, or Q8_0 matrices: NOT_SUPPORTED, out untouched
+    keep = out.copy()
+    mats, an, fn, _ = layers[0]
+    bias = np.zeros(n_head * hd, np.float32)
+    A = batch_args(mats, an, fn, E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, None, None, 1, 1, 1)
+    A.bq = bias.ctypes.data
+    assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == NOT_SUPPORTED
+    q8 = make_layer(lib, orc, E, n_head, n_kv, F, (Q8_0,) * 7, 90)
+    A = batch_args(*q8[:3], E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, None, None, 1, 1, 1)
+    assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == NOT_SUPPORTED
     assert lib.cuda_layer_forward_batch(None) == NOT_SUPPORTED
-    assert lib.cuda_attention_batch(None, None, 1, 1, 1, 128, 128, 136, 136, 0, 0, 0) == NOT_SUPPORTED
-    assert lib.cuda_prefill_chunk_tokens() == 0
+    assert np.array_equal(out, keep)
+    for L in layers + [q8]:
+        for m in L[0].values():
+            m.free()
+    lib.cuda_kv_cache_release()
