@@ -11,7 +11,8 @@ resident in HBM before timing. value = algorithmic bytes per step / step time.
 Also reported under "extra": the Q4_0 and Q8_0 GEMVs (configs 1-2), the Q6_K
 GEMV, each with its kernel-only bandwidth; the prefill GEMMs (config 3); the
 decode attention and the decoder layer (config 4); the MoE expert FFN
-(config 5).
+(config 5); the prefill attention and the decoder layer over a 512-token
+prompt chunk (config 4's layer, the prefill path).
 
 `roofline` is the dominant kernel (Q4_K GEMV, up shape): algorithmic bytes per
 launch / average launch duration, from HIP events around back-to-back launches
@@ -234,6 +235,72 @@ class MoeCase:
         return MOE_WEIGHT_BYTES + self.n_tok * 4096 * 4 * 2 + self.n_tok * 8 * 4
 
 
+class AttnPrefillCase:
+    """Prefill attention at config 4's head shape (32 query heads over 8 KV
+    heads of 128): n_tok prompt tokens after pos0 cached positions, every
+    token attending causally to all earlier positions. Algorithmic work: the
+    two products, 4 * hd flops per (row, key) pair."""
+
+    def __init__(self, dev, pos0=3584, n_tok=512):
+        import torch
+        from desireeia_amd import ops
+        self.pos0, self.n_tok = pos0, n_tok
+        g = torch.Generator(device=dev).manual_seed(9)
+        self.cache = ops.KVCache(pos0 + n_tok, 8, 128, device=dev)
+        self.cache.write_batch(torch.randn(pos0 + n_tok, 1024, device=dev, generator=g),
+                               torch.randn(pos0 + n_tok, 1024, device=dev, generator=g), 0)
+        self.q = torch.randn(n_tok, 32 * 128, device=dev, generator=g)
+        self.out = torch.empty_like(self.q)
+        torch.cuda.synchronize()
+
+    def kernel(self):
+        from desireeia_amd import ops
+        ops.attention_prefill(self.q, self.cache, 32, self.pos0, out=self.out)
+
+    def flops(self):
+        keys = self.n_tok * (self.pos0 + 1) + self.n_tok * (self.n_tok - 1) // 2
+        return 4.0 * 128 * 32 * keys
+
+
+class LayerPrefillCase:
+    """Config 4's decoder layer (hidden 4096, 32/8 heads of 128, FFN 14336,
+    Q4_K_M mix) over a prompt chunk of n_tok tokens at positions pos0..
+    (dq_layer_prefill: seven prefill GEMMs, batched RoPE + KV rows, prefill
+    attention, norms, SiLU, residuals). RMSNorm weights 0.25 / sqrt(4096) and
+    0.3 / sqrt(4096) keep the synthetic activations O(1)."""
+
+    def __init__(self, dev, pos0=0, n_tok=512, seed=60):
+        import torch
+        from desireeia_amd import ops, synth
+        E, H, KV, HD, F = 4096, 32, 8, 128, 14336
+        shapes = {"q": (synth.Q4_K, H * HD, E), "k": (synth.Q4_K, KV * HD, E), "v": (synth.Q6_K, KV * HD, E),
+                  "o": (synth.Q4_K, E, H * HD), "gate": (synth.Q4_K, F, E), "up": (synth.Q4_K, F, E),
+                  "down": (synth.Q6_K, E, F)}
+        mats = {nm: ops.QuantMatrix.from_gguf(qt, synth.gen_weights(qt, r, c, seed + i), r, c, device=dev)
+                for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
+        an, fn = torch.full((E,), 0.25 / 64), torch.full((E,), 0.3 / 64)
+        self.layer = ops.DecoderLayer(mats, an, fn, H, KV, HD, pos0 + n_tok, device=dev)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        if pos0:
+            self.layer.cache.write_batch(torch.randn(pos0, KV * HD, device=dev, generator=g),
+                                         torch.randn(pos0, KV * HD, device=dev, generator=g), 0)
+        self.pos0, self.n_tok = pos0, n_tok
+        self.x = torch.randn(n_tok, E, device=dev, generator=g)
+        self.out = torch.empty_like(self.x)
+        self.rope = torch.stack([ops.rope_cache(HD, pos0 + t, 500000.0) for t in range(n_tok)]).to(dev)
+        self.work = self.layer.prefill_workspace(n_tok)
+        torch.cuda.synchronize()
+
+    def step(self):
+        self.layer.prefill(self.x, self.pos0, out=self.out, work=self.work, rope=self.rope)
+
+    def flops(self):
+        E, QD, KVD, F = 4096, 4096, 1024, 14336
+        gemm = 2.0 * self.n_tok * (QD * E + 2 * KVD * E + E * QD + 3 * F * E)
+        keys = self.n_tok * (self.pos0 + 1) + self.n_tok * (self.n_tok - 1) // 2
+        return gemm + 4.0 * 128 * 32 * keys
+
+
 def graph_time(fn, calls_per_graph, reps, warmup_reps=2):
     """Captures calls_per_graph calls of fn into one HIP graph and times `reps`
     replays with HIP events on the capturing stream. Returns us per call."""
@@ -379,6 +446,16 @@ def main():
         us = graph_time(ac.kernel, len(ac.caches), max(1, args.steps // len(ac.caches)))
         log(f"attn: {us:.2f} us, {KV_READ_BYTES / us / 1e3:.1f} GB/s")
         return
+    if args.only == "attn_prefill":
+        pc = AttnPrefillCase(dev)
+        us = graph_time(pc.kernel, 4, max(1, args.steps // 4))
+        log(f"attn_prefill: {us:.1f} us, {pc.flops() / us / 1e6:.1f} TFLOP/s (algorithmic)")
+        return
+    if args.only == "layer_prefill":
+        lp = LayerPrefillCase(dev)
+        us = graph_time(lp.step, 1, max(1, args.steps))
+        log(f"layer_prefill: {us:.1f} us/layer, {lp.n_tok / us * 1e6:.0f} tok/s, {lp.flops() / us / 1e6:.1f} TFLOP/s")
+        return
     if args.only:
         qt, r, c = shapes[args.only]
         case = GemvCase(qt, r, c, 11, dev)
@@ -446,6 +523,22 @@ def main():
                               "tokens_per_s": round(mc.n_tok / us * 1e6, 1), "bytes_per_call": mc.bytes()}
     log(f"MoE expert FFN (8 experts, top-2, 64 tokens): {us:.1f} us  {gbs:.1f} GB/s")
     del mc
+    # prefill (the layer path over a prompt chunk): attention alone and the layer
+    pc = AttnPrefillCase(dev)
+    us = graph_time(pc.kernel, 4, 3)
+    tf = pc.flops() / us / 1e6
+    extra["attn_prefill_512_after_3584"] = {
+        "kernel_us": round(us, 2), "TFLOPs_alg": round(tf, 1), "frac_fp16_mfma_alg": round(tf / FP16_PEAK_TFLOPS, 4),
+        "frac_fp16_mfma_issued": round(3 * tf / FP16_PEAK_TFLOPS, 4)}
+    log(f"prefill attention (512 tokens after 3584): {us:.1f} us  {tf:.1f} TFLOP/s algorithmic")
+    del pc
+    lp = LayerPrefillCase(dev)
+    us = graph_time(lp.step, 1, 5)
+    tf = lp.flops() / us / 1e6
+    extra["layer_prefill_q4km_512tok"] = {"us_per_layer": round(us, 1), "tokens_per_s": round(lp.n_tok / us * 1e6, 1),
+                                          "TFLOPs_alg": round(tf, 1), "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4)}
+    log(f"decoder layer prefill (512 tokens): {us:.1f} us/layer  {lp.n_tok / us * 1e6:.0f} tok/s  {tf:.1f} TFLOP/s")
+    del lp
     dom = extra["q4k_up"]
     roofline = {"bound": "hbm", "achieved": dom["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(),
