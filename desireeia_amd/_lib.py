@@ -50,6 +50,20 @@ SIGNATURES = {
                                    c_p]),
     "dq_layer_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
     "dq_layer_prefill_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
+    "dq_rms_norm_rows": (c_int, [c_p, c_p, c_p, c_p, c_size, c_size, c_f, c_p, c_p]),
+    "dq_head_workspace_bytes": (c_int, [c_int, c_size, c_size, ctypes.POINTER(c_size)]),
+    "dq_head_logits": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p, c_f, c_p, c_p, c_size, c_p]),
+    "dq_topk_workspace_bytes": (c_int, [c_u32, c_u32, ctypes.POINTER(c_size)]),
+    "dq_topk": (c_int, [c_p, c_u32, c_u32, c_p, c_p, c_p, c_size, c_p]),
+    "dq_sample_reset": (c_int, [c_p, c_p, c_size, c_p]),
+    "dq_sample_candidates": (c_int, [c_p, c_p, c_u32, c_p, c_p, c_p]),
+    "dq_embed_q8_0": (c_int, [c_p, c_size, c_size, c_p, c_f, c_p, c_p]),
+    "cuda_head_forward": (c_int, [c_int, c_p, c_p, c_p, c_size, c_f, c_size, c_p]),
+    "cuda_head_forward_topk": (c_int, [c_int, c_p, c_p, c_p, c_size, c_f, c_size, c_u32, c_p, c_p]),
+    "cuda_head_forward_sample": (c_int, [c_int, c_p, c_p, c_p, c_size, c_f, c_size, c_p]),
+    "cuda_sample_wait": (c_int, [c_u32, c_p]),
+    "cuda_sample_history": (c_int, [c_p, c_size]),
+    "cuda_fetch_x": (c_int, [c_p, c_size]),
     "dq_layer_prefill": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_u32, c_u32, c_p, c_p, c_u32, c_p, c_size, c_p]),
     "dq_layer_decode": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_p, c_u32, c_p, c_p, c_u32, c_p, c_size, c_p]),
     "dq_silu_mul": (c_int, [c_p, c_p, c_size, c_p, c_p]),
@@ -173,6 +187,19 @@ class CudaLayerBatchArgs(ctypes.Structure):
                 + [(n, c_int) for n in ("fmt_q", "fmt_k", "fmt_v", "fmt_o", "fmt_gate", "fmt_up", "fmt_down",
                                         "fmt_ag", "upload_x", "download_x", "upload_rope", "prepare_weights",
                                         "rope_slot")])
+
+
+class CudaSampleArgs(ctypes.Structure):
+    """core/engine.h:570-579."""
+    _fields_ = [("temperature", c_f), ("top_k", ctypes.c_int32), ("top_p", c_f), ("penalty_repeat", c_f),
+                ("penalty_freq", c_f), ("penalty_present", c_f), ("penalty_last_n", ctypes.c_int32), ("kk", c_u32),
+                ("logit_scale", c_f), ("u", c_f), ("append_input", c_int), ("slot", c_u32)]
+
+
+class SampleState(ctypes.Structure):
+    """dq_sample_state_t."""
+    _fields_ = [("tok", ctypes.c_int32), ("len", c_u32), ("wpos", c_u32), ("ring", ctypes.c_int32 * 4),
+                ("hist", ctypes.c_int32 * 256)]
 
 
 class MoeDesc(ctypes.Structure):

@@ -70,6 +70,15 @@ struct Engine {
         size_t off, bytes;
     };
     std::vector<Mirror> mirror;
+    // output head and the pipelined draw: logits, top-k, the model's output
+    // norm (device copy, re-sent when its content changes), the draw state,
+    // pinned readback slots with an event each and the readback stream
+    DevBuf hlog, hwork, htk, hnorm, hcand;
+    std::vector<float> hnorm_host;
+    dq_sample_state_t* sst = nullptr;
+    int32_t* tok_pinned = nullptr;
+    hipEvent_t tok_ev[4] = {}, drawn_ev[4] = {};
+    hipStream_t tok_stream = nullptr;
 };
 
 Engine g;
@@ -390,9 +399,23 @@ void cuda_backend_shutdown(void) {
     if (g.stream) (void)hipStreamSynchronize(g.stream);
     drop_graphs();
     for (DevBuf* b : {&g.xbuf, &g.ybuf, &g.act, &g.work, &g.stage, &g.lx[0], &g.lx[1], &g.rope, &g.px, &g.prope[0],
-                      &g.prope[1], &g.prope[2], &g.prope[3], &g.pwork, &g.pnorm, &g.pio})
+                      &g.prope[1], &g.prope[2], &g.prope[3], &g.pwork, &g.pnorm, &g.pio, &g.hlog, &g.hwork, &g.htk,
+                      &g.hnorm, &g.hcand})
         release(*b);
     g.mirror.clear();
+    g.hnorm_host.clear();
+    if (g.tok_stream) (void)hipStreamSynchronize(g.tok_stream);
+    for (int i = 0; i < 4; ++i) {
+        if (g.tok_ev[i]) (void)hipEventDestroy(g.tok_ev[i]);
+        if (g.drawn_ev[i]) (void)hipEventDestroy(g.drawn_ev[i]);
+        g.tok_ev[i] = g.drawn_ev[i] = nullptr;
+    }
+    if (g.tok_stream) (void)hipStreamDestroy(g.tok_stream);
+    g.tok_stream = nullptr;
+    if (g.sst) (void)hipFree(g.sst);
+    g.sst = nullptr;
+    if (g.tok_pinned) (void)hipHostFree(g.tok_pinned);
+    g.tok_pinned = nullptr;
     cuda_kv_cache_release();
     if (g.stream) (void)hipStreamDestroy(g.stream);
     g.stream = nullptr;
@@ -735,7 +758,7 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     if (!A || !g.kc) return DQ_ERR_NOT_SUPPORTED;
     // features outside the plain dense layer: the engine's CPU path runs them
     if (A->wag_qs || A->bq || A->bk || A->bv || A->q_norm_w || A->k_norm_w || A->post_attn_norm_w ||
-        A->post_ffn_norm_w || A->act_gelu || A->dyn_all || A->rope_all || A->x_from_token)
+        A->post_ffn_norm_w || A->act_gelu || A->dyn_all || A->rope_all)
         return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
     if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
@@ -774,7 +797,16 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     if (A->pos >= n_ctx || A->cc_start > A->pos) return DQ_ERR_NOT_SUPPORTED;
     size_t wbytes = 0;
     if (dq_layer_workspace_bytes(&L, n_ctx, &wbytes) != DQ_OK) return DQ_ERR_NOT_SUPPORTED;
-    if (A->upload_x && !A->x) return DQ_ERR_INVALID_ARG;
+    // x_from_token: x is the Q8_0 embedding row of the token the previous
+    // step drew on the device (pipelined decode)
+    const WInfo* emb = nullptr;
+    if (A->x_from_token) {
+        emb = lookup(A->embd_qs);
+        if (!A->upload_x || !emb || emb->base != A->embd_qs || emb->fmt != DQ_FMT_Q8_0 || emb->cols != A->n_embd ||
+            !g.sst)
+            return DQ_ERR_NOT_SUPPORTED;
+    }
+    if (A->upload_x && !A->x && !A->x_from_token) return DQ_ERR_INVALID_ARG;
     if (A->download_x && !A->x_out) return DQ_ERR_INVALID_ARG;
     if (!stream()) return DQ_ERR_IO;
     const size_t E = A->n_embd;
@@ -796,7 +828,12 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     }
     if (A->upload_x) {
         g.cur = 0;
-        if (hipMemcpyAsync(g.lx[0].p, A->x, E * 4, hipMemcpyHostToDevice, s) != hipSuccess) return io_fail();
+        if (A->x_from_token) {
+            if (dq_embed_q8_0(A->embd_qs, emb->rows, E, &g.sst->tok, A->embd_mul, (float*)g.lx[0].p, s) != DQ_OK)
+                return io_fail();
+        } else if (hipMemcpyAsync(g.lx[0].p, A->x, E * 4, hipMemcpyHostToDevice, s) != hipSuccess) {
+            return io_fail();
+        }
     }
     float* xin = (float*)g.lx[g.cur].p;
     float* xout = (float*)g.lx[g.cur ^ 1].p;
@@ -945,6 +982,150 @@ int cuda_prefill_chunk_tokens(void) {
     }
     const int n = 8 * cus;
     return n < 1024 ? 1024 : (n > 4096 ? 4096 : n);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------- head --
+
+namespace {
+
+bool sample_state_ready() {
+    if (g.sst) return true;
+    if (!stream()) return false;
+    dq_sample_state_t* st = nullptr;
+    if (hipMalloc((void**)&st, sizeof(dq_sample_state_t)) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (hipHostMalloc((void**)&g.tok_pinned, 4 * sizeof(int32_t), hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(st);
+        g.tok_pinned = nullptr;
+        return false;
+    }
+    bool ok = hipStreamCreateWithFlags(&g.tok_stream, hipStreamNonBlocking) == hipSuccess;
+    for (int i = 0; ok && i < 4; ++i)
+        ok = hipEventCreateWithFlags(&g.tok_ev[i], hipEventDisableTiming) == hipSuccess &&
+             hipEventCreateWithFlags(&g.drawn_ev[i], hipEventDisableTiming) == hipSuccess;
+    g.sst = st;
+    if (!ok || dq_sample_reset(st, nullptr, 0, g.stream) != DQ_OK) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return true;
+}
+
+// Final norm and head product of the token the layer chain left on the
+// device, into g.hlog (backend_cuda.cu:3383-3436).
+int head_launch(int format, const void* d_qs, const void* d_scale, const float* norm_w, size_t n_embd, float eps,
+                size_t rows) {
+    const WInfo* w = lookup(d_qs);
+    if (!w || w->base != d_qs || w->fmt != format || w->rows != rows || w->cols != n_embd || !norm_w)
+        return DQ_ERR_NOT_SUPPORTED;
+    if (format == DQ_FMT_Q8_0 && (!d_scale || !lookup(d_scale) || lookup(d_scale)->base != d_qs))
+        return DQ_ERR_NOT_SUPPORTED;
+    if (!g.lx[g.cur].p || g.lx[g.cur].cap < n_embd * 4) return DQ_ERR_NOT_SUPPORTED;  // no device x
+    if (n_embd % 4 || n_embd > 49152) return DQ_ERR_NOT_SUPPORTED;
+    size_t wb = 0;
+    if (dq_head_workspace_bytes(format, rows, n_embd, &wb) != DQ_OK) return DQ_ERR_NOT_SUPPORTED;
+    if (!stream()) return DQ_ERR_IO;
+    if (!reserve(g.hlog, rows * 4) || !reserve(g.hwork, wb) || !reserve(g.hnorm, n_embd * 4)) return DQ_ERR_IO;
+    const hipStream_t s = g.stream;
+    // the model's output norm, sent once; re-sent when its content changes
+    // (a later model may reuse the host allocation)
+    if (g.hnorm_host.size() != n_embd || memcmp(g.hnorm_host.data(), norm_w, n_embd * 4) != 0) {
+        g.hnorm_host.assign(norm_w, norm_w + n_embd);
+        if (hipMemcpyAsync(g.hnorm.p, g.hnorm_host.data(), n_embd * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+            return io_fail();
+    }
+    if (dq_head_logits(format, d_qs, rows, n_embd, (const float*)g.lx[g.cur].p, (const float*)g.hnorm.p, eps,
+                       (float*)g.hlog.p, g.hwork.p, g.hwork.cap, s) != DQ_OK)
+        return io_fail();
+    return DQ_OK;
+}
+
+// The kk largest logits into g.hcand (ids then values).
+int head_topk(size_t rows, uint32_t kk) {
+    size_t tb = 0;
+    if (rows > 0xFFFFFFFFu || dq_topk_workspace_bytes((uint32_t)rows, kk, &tb) != DQ_OK) return DQ_ERR_NOT_SUPPORTED;
+    if (!reserve(g.htk, tb) || !reserve(g.hcand, 2 * 256 * 4)) return DQ_ERR_IO;
+    int32_t* ids = (int32_t*)g.hcand.p;
+    float* vals = (float*)g.hcand.p + 256;
+    if (dq_topk((const float*)g.hlog.p, (uint32_t)rows, kk, ids, vals, g.htk.p, g.htk.cap, g.stream) != DQ_OK)
+        return io_fail();
+    return DQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int cuda_head_forward(int format, const void* d_qs, const void* d_scale, const float* norm_w, size_t n_embd,
+                      float eps, size_t rows, float* y) {
+    if (!y) return DQ_ERR_INVALID_ARG;
+    const int rc = head_launch(format, d_qs, d_scale, norm_w, n_embd, eps, rows);
+    if (rc != DQ_OK) return rc;
+    if (hipMemcpyAsync(y, g.hlog.p, rows * 4, hipMemcpyDeviceToHost, g.stream) != hipSuccess) return io_fail();
+    return sync();
+}
+
+int cuda_head_forward_topk(int format, const void* d_qs, const void* d_scale, const float* norm_w, size_t n_embd,
+                           float eps, size_t rows, uint32_t kk, int32_t* ids, float* vals) {
+    if (kk == 0 || kk > 256 || rows < kk) return DQ_ERR_NOT_SUPPORTED;
+    if (!ids || !vals) return DQ_ERR_INVALID_ARG;
+    int rc = head_launch(format, d_qs, d_scale, norm_w, n_embd, eps, rows);
+    if (rc == DQ_OK) rc = head_topk(rows, kk);
+    if (rc != DQ_OK) return rc;
+    const hipStream_t s = g.stream;
+    if (hipMemcpyAsync(ids, g.hcand.p, kk * 4, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipMemcpyAsync(vals, (float*)g.hcand.p + 256, kk * 4, hipMemcpyDeviceToHost, s) != hipSuccess)
+        return io_fail();
+    return sync();
+}
+
+int cuda_head_forward_sample(int format, const void* d_qs, const void* d_scale, const float* norm_w, size_t n_embd,
+                             float eps, size_t rows, const CudaSampleArgs* a) {
+    if (!a || a->kk == 0 || a->kk > 256 || rows < a->kk || a->slot > 3) return DQ_ERR_NOT_SUPPORTED;
+    if (a->temperature > 0.0f && a->top_k <= 0) return DQ_ERR_NOT_SUPPORTED;
+    if (a->penalty_last_n > DQ_SAMPLE_HIST) return DQ_ERR_NOT_SUPPORTED;
+    if (!sample_state_ready()) return DQ_ERR_NOT_SUPPORTED;
+    int rc = head_launch(format, d_qs, d_scale, norm_w, n_embd, eps, rows);
+    if (rc == DQ_OK) rc = head_topk(rows, a->kk);
+    if (rc != DQ_OK) return rc;
+    const hipStream_t s = g.stream;
+    if (dq_sample_candidates((const float*)g.hcand.p + 256, (const int32_t*)g.hcand.p, a->kk, a, g.sst, s) != DQ_OK)
+        return io_fail();
+    // the drawn token goes back on its own stream, so that the next step's
+    // work on the decode stream does not wait for the copy
+    const int slot = (int)a->slot;
+    if (hipEventRecord(g.drawn_ev[slot], s) != hipSuccess ||
+        hipStreamWaitEvent(g.tok_stream, g.drawn_ev[slot], 0) != hipSuccess ||
+        hipMemcpyAsync(g.tok_pinned + slot, &g.sst->ring[slot], 4, hipMemcpyDeviceToHost, g.tok_stream) !=
+            hipSuccess ||
+        hipEventRecord(g.tok_ev[slot], g.tok_stream) != hipSuccess)
+        return io_fail();
+    return DQ_OK;
+}
+
+int cuda_sample_wait(uint32_t slot, int32_t* token) {
+    if (slot > 3 || !token || !g.sst || !g.tok_ev[slot]) return DQ_ERR_IO;
+    if (hipEventSynchronize(g.tok_ev[slot]) != hipSuccess) return io_fail();
+    *token = g.tok_pinned[slot];
+    return DQ_OK;
+}
+
+int cuda_sample_history(const int32_t* hist, size_t n) {
+    if (!sample_state_ready()) return DQ_ERR_NOT_SUPPORTED;
+    if (n && !hist) return DQ_ERR_INVALID_ARG;
+    return dq_sample_reset(g.sst, hist, n, g.stream) == DQ_OK ? DQ_OK : io_fail();
+}
+
+int cuda_fetch_x(float* dst, size_t n) {
+    if (!dst) return DQ_ERR_INVALID_ARG;
+    if (!g.lx[g.cur].p || g.lx[g.cur].cap < n * 4 || !g.stream) return DQ_ERR_NOT_SUPPORTED;
+    if (hipMemcpyAsync(dst, g.lx[g.cur].p, n * 4, hipMemcpyDeviceToHost, g.stream) != hipSuccess) return io_fail();
+    return sync();
 }
 
 }  // extern "C"

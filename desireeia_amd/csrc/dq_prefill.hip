@@ -579,6 +579,15 @@ int dq_attn_prefill_q8(const float* d_q, const void* d_kc, const void* d_vc, uin
     }
 }
 
+int dq_rms_norm_rows(const float* d_a, const float* d_b, float* d_h, const float* d_w, size_t n, size_t rows,
+                     float eps, float* d_y, void* stream) {
+    if (!d_a || !d_w || !d_y) return DQ_ERR_INVALID_ARG;
+    if (n == 0 || n % 4 || n > (1u << 30) || rows > 0x7FFFFFFF) return DQ_ERR_NOT_SUPPORTED;
+    if (rows == 0) return DQ_OK;
+    rms_norm_rows_kernel<<<(unsigned)rows, 256, 0, (hipStream_t)stream>>>(d_a, d_b, d_h, d_w, (int)n, eps, d_y);
+    return dq_launch_status();
+}
+
 int dq_layer_prefill_workspace_bytes(const dq_layer_t* L, uint32_t n_tok, size_t* bytes) {
     if (!L || !bytes) return DQ_ERR_INVALID_ARG;
     if (!prefill_layer_ok(L)) return DQ_ERR_NOT_SUPPORTED;

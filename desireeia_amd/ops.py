@@ -259,6 +259,65 @@ def attention_prefill(q, cache, n_head, pos0, n_swa=0, out=None):
     return o
 
 
+def head_logits(mat, x, norm_w, eps=1e-5, out=None):
+    """Final RMSNorm of x [cols] (weight norm_w) and the head product: logits [rows]."""
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    _lib.check(lib.dq_head_workspace_bytes(mat.fmt, mat.rows, mat.cols, ctypes.byref(n)), "dq_head_workspace_bytes")
+    wk = torch.empty(n.value, dtype=torch.uint8, device=x.device)
+    y = out if out is not None else torch.empty(mat.rows, dtype=torch.float32, device=x.device)
+    _lib.check(lib.dq_head_logits(mat.fmt, _ptr(mat.buf), mat.rows, mat.cols, _ptr(x.contiguous()),
+                                  _ptr(norm_w.contiguous()), ctypes.c_float(eps), _ptr(y), _ptr(wk), wk.numel(),
+                                  _stream()), "dq_head_logits")
+    return y
+
+
+def topk(v, kk):
+    """(ids int32 [kk], values [kk]): the kk largest of v, largest first, lower index on ties."""
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    _lib.check(lib.dq_topk_workspace_bytes(v.numel(), kk, ctypes.byref(n)), "dq_topk_workspace_bytes")
+    wk = torch.empty(n.value, dtype=torch.uint8, device=v.device)
+    ids = torch.empty(kk, dtype=torch.int32, device=v.device)
+    vals = torch.empty(kk, dtype=torch.float32, device=v.device)
+    _lib.check(lib.dq_topk(_ptr(v.contiguous()), v.numel(), kk, _ptr(ids), _ptr(vals), _ptr(wk), wk.numel(),
+                           _stream()), "dq_topk")
+    return ids, vals
+
+
+class DeviceSampler:
+    """The draw of the pipelined decode on the device (dq_sample_candidates)
+    with its state: last token, 256-token history ring, readback slots."""
+
+    def __init__(self, device="cuda", hist=()):
+        self.state = torch.zeros(ctypes.sizeof(_lib.SampleState), dtype=torch.uint8, device=device)
+        self.reset(hist)
+
+    def reset(self, hist):
+        lib = _lib.load()
+        h = (ctypes.c_int32 * max(len(hist), 1))(*hist)
+        _lib.check(lib.dq_sample_reset(_ptr(self.state), h if len(hist) else None, len(hist), _stream()),
+                   "dq_sample_reset")
+
+    def sample(self, ids, vals, args):
+        lib = _lib.load()
+        _lib.check(lib.dq_sample_candidates(_ptr(vals.contiguous()), _ptr(ids.contiguous()), ids.numel(),
+                                            ctypes.byref(args), _ptr(self.state), _stream()), "dq_sample_candidates")
+
+    def read(self):
+        st = _lib.SampleState.from_buffer_copy(bytes(self.state.cpu().numpy()))
+        return st
+
+
+def embed_q8_0(mat, tok, mul=0.0, out=None):
+    """Row tok (int32 device tensor of one element) of a packed Q8_0 matrix, times mul when non-zero."""
+    lib = _lib.load()
+    y = out if out is not None else torch.empty(mat.cols, dtype=torch.float32, device=tok.device)
+    _lib.check(lib.dq_embed_q8_0(_ptr(mat.buf), mat.rows, mat.cols, _ptr(tok), ctypes.c_float(mul), _ptr(y),
+                                 _stream()), "dq_embed_q8_0")
+    return y
+
+
 def attn_workspace(n_head, n_head_kv, hd, n_ctx, device="cuda"):
     lib = _lib.load()
     n = ctypes.c_size_t(0)

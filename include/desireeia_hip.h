@@ -287,6 +287,70 @@ int dq_layer_prefill(const dq_layer_t* layer, const float* d_x, float* d_x_out, 
                      size_t work_bytes, void* stream);
 
 
+/* rms_norm_vec (models/dense_forward.cpp:129-165) of each of `rows` rows of
+ * n floats: x = a (+ b, stored to d_h when given), y = x / sqrt(mean(x^2) +
+ * eps) * w, the squares summed in double. n % 4 == 0. */
+int dq_rms_norm_rows(const float* d_a, const float* d_b, float* d_h, const float* d_w, size_t n, size_t rows,
+                     float eps, float* d_y, void* stream);
+
+/* ------------------------------------------------------------ output head */
+
+/* Logits of the output head for one token: the final RMSNorm (weight d_norm)
+ * of x [cols], then the head product [rows] with the activation quantized
+ * per the matrix format as the engine's CPU head does (models/dense_forward.cpp
+ * final norm + matvec; backend_cuda.cu:3383-3436 head_forward_launch).
+ * d_work: dq_head_workspace_bytes() bytes. */
+int dq_head_workspace_bytes(int fmt, size_t rows, size_t cols, size_t* bytes);
+int dq_head_logits(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, const float* d_norm,
+                   float eps, float* d_logits, void* d_work, size_t work_bytes, void* stream);
+/* The kk (1..256, <= n) largest of n values, largest first, lower index first
+ * on equal values (+0 and -0 equal): ids and/or values (device arrays of kk).
+ * cuda_head_forward_topk's selection (backend_cuda.cu:3438-3497, 3642-3689).
+ * d_work: dq_topk_workspace_bytes() bytes. */
+int dq_topk_workspace_bytes(uint32_t n, uint32_t kk, size_t* bytes);
+int dq_topk(const float* d_v, uint32_t n, uint32_t kk, int32_t* d_ids, float* d_vals, void* d_work,
+            size_t work_bytes, void* stream);
+
+/* Sampling arguments of the pipelined decode, core/engine.h:570-579. */
+typedef struct CudaSampleArgs {
+    float temperature; int32_t top_k; float top_p;
+    float penalty_repeat; float penalty_freq; float penalty_present; int32_t penalty_last_n;
+    uint32_t kk;
+    float logit_scale;
+    float u;
+    int append_input;
+    uint32_t slot;
+} CudaSampleArgs;
+
+/* Device state of the draw: the last drawn token, the recent history the
+ * penalties read (a ring of DQ_SAMPLE_HIST tokens, `len` tokens seen, next
+ * write at `wpos`), and the token of each readback slot. */
+#define DQ_SAMPLE_HIST 256
+typedef struct {
+    int32_t tok;
+    uint32_t len, wpos;
+    int32_t ring[4];
+    int32_t hist[DQ_SAMPLE_HIST];
+} dq_sample_state_t;
+/* Resets the state to the last min(n, 256) tokens of hist (host), the last
+ * of them as the current token (cuda_sample_history, backend_cuda.cu:3745-3752).
+ * Synchronises. */
+int dq_sample_reset(void* d_state, const int32_t* hist, size_t n, void* stream);
+/* Sampler::sample_candidates (core/sampler.cpp:298-322, finish_ :202-253) on
+ * n <= 256 candidates (values, ids): append the current token to the history
+ * if args->append_input, penalties over the last penalty_last_n (<= 256)
+ * tokens, order by (value desc, id asc), greedy when temperature <= 0, else
+ * top-k (> 0), temperature softmax, top-p, and the draw r = u * cum. The
+ * token goes to state->tok and state->ring[slot]. */
+int dq_sample_candidates(const float* d_vals, const int32_t* d_ids, uint32_t n, const CudaSampleArgs* args,
+                         void* d_state, void* stream);
+/* x [cols] = the row *d_tok of a packed Q8_0 matrix (d * q, times mul when
+ * mul != 0): the embedding of the pipelined decode's next token
+ * (backend_cuda.cu:3555-3566). A token outside [0, rows) reads the nearest
+ * row. */
+int dq_embed_q8_0(const void* d_w, size_t rows, size_t cols, const int32_t* d_tok, float mul, float* d_x,
+                  void* stream);
+
 /* ------------------------------------------------------------------ MoE */
 
 /* Router of one MoE layer for n_tok tokens (moe_route_ex with softmax gating,
@@ -532,6 +596,27 @@ int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, 
                          size_t layer_off, uint32_t col0, uint32_t n_swa);
 int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* args);
 int cuda_prefill_chunk_tokens(void);
+
+/* Output head and the pipelined draw (core/engine.h:558-591,
+ * backend_cuda.cu:3383-3780): on the x the last cuda_layer_forward left on
+ * the device. cuda_head_forward: logits to host y [rows]. cuda_head_forward_topk:
+ * the kk (<= 256) largest, largest first, lower id on ties. cuda_head_forward_sample:
+ * head + top-kk + the draw (dq_sample_candidates), queued without a
+ * synchronisation; cuda_sample_wait returns the token of a slot.
+ * cuda_sample_history replaces the device history with the last tokens of
+ * hist. cuda_fetch_x copies the device x to the host. The head matrix must be
+ * an upload of this library with format / rows / n_embd as given: otherwise
+ * NOT_SUPPORTED. With x_from_token (CudaLayerArgs), cuda_layer_forward builds
+ * x from the drawn token and a Q8_0 embedding upload (embd_qs, embd_mul). */
+int cuda_head_forward(int format, const void* d_qs, const void* d_scale, const float* norm_w, size_t n_embd,
+                      float eps, size_t rows, float* y);
+int cuda_head_forward_topk(int format, const void* d_qs, const void* d_scale, const float* norm_w, size_t n_embd,
+                           float eps, size_t rows, uint32_t kk, int32_t* ids, float* vals);
+int cuda_head_forward_sample(int format, const void* d_qs, const void* d_scale, const float* norm_w, size_t n_embd,
+                             float eps, size_t rows, const CudaSampleArgs* args);
+int cuda_sample_wait(uint32_t slot, int32_t* token);
+int cuda_sample_history(const int32_t* hist, size_t n);
+int cuda_fetch_x(float* dst, size_t n);
 
 /* ------------------------------------------------------------------------
  * GGUF model files (host): the engine's GgufReader (src/gguf/gguf_reader.cpp

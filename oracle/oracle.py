@@ -281,6 +281,9 @@ class Ref:
         L.dqr_kv_axpy_q8_0.argtypes = [c_p, c_p, c_size, c_f]
         L.dqr_moe_route.restype = c_u32
         L.dqr_moe_route.argtypes = [c_p, c_u32, c_u32, c_int, c_f, c_p, c_p]
+        L.dqr_sample_candidates.restype = ctypes.c_int32
+        L.dqr_sample_candidates.argtypes = [c_f, ctypes.c_int32, c_f, c_f, c_f, c_f, ctypes.c_int32, c_u32, c_u32, c_p,
+                                            c_p, c_size, c_p, c_size, c_p]
         L.dqr_attention_prefill_q8.argtypes = [c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_p, c_size, c_size,
                                                c_u32, c_u32, c_f]
 
@@ -365,9 +368,27 @@ class Ref:
         return ids[:n].copy(), wts[:n].copy()
 
 
+    def sample_candidates(self, ids, vals, hist, temperature=0.0, top_k=40, top_p=0.95, repeat=1.0, freq=0.0,
+                          present=0.0, last_n=64, seed=1, skip=0):
+        """The reference's Sampler::sample_candidates with a seeded generator:
+        (token, u) where u is the uniform number the device draw is given."""
+        return _ref_sample(self.L, ids, vals, list(hist), temperature, top_k, top_p, repeat, freq, present, last_n,
+                           seed, skip)
+
     def attn_prefill(self, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0, n_swa=0, q_dim=None, out=None):
         return _attn_prefill(self.L.dqr_attention_prefill_q8, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0,
                              n_swa, q_dim, out)
+
+
+def _ref_sample(L, ids, vals, hist, temperature, top_k, top_p, repeat, freq, present, last_n, seed, skip):
+    ids = np.ascontiguousarray(ids, np.int32)
+    vals = np.ascontiguousarray(vals, np.float32)
+    nh = len(hist)
+    h = np.ascontiguousarray(hist if nh else [0], np.int32)
+    u = ctypes.c_float()
+    tok = L.dqr_sample_candidates(temperature, top_k, top_p, repeat, freq, present, last_n, seed, skip, _p(ids),
+                                  _p(vals), ids.size, _p(h), nh, ctypes.byref(u))
+    return tok, u.value
 
 
 def _attn_prefill(fn, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0, n_swa, q_dim, out):

@@ -15,12 +15,14 @@
 //   kv_quantize_row/dot/axpy ...... kv/kv_quant.cpp:31,58,102
 //   moe_route ..................... models/moe_route.cpp:77
 //   attention_prefill_cpu_q8 ...... core/attn_cpu.cpp:128
+//   Sampler::sample_candidates .... core/sampler.cpp:298 (draw_uniform :131)
 //   ThreadPool::set_thread_override core/thread_pool.cpp:36
 #include "core/engine.h"
 #include "core/i8gemm.h"
 #include "core/thread_pool.h"
 #include "kv/kv_quant.h"
 #include "models/moe_route.h"
+#include "core/sampler.h"
 #include "quant/quant.h"
 
 #include <cstring>
@@ -101,6 +103,35 @@ int dqr_attention_prefill_q8(const float* q_all, float* out, uint32_t n_tok, uin
                              size_t row_bytes, size_t pos_bytes, uint32_t pos0, uint32_t n_swa, float inv_d) {
     return attention_prefill_cpu_q8(q_all, out, n_tok, n_head, hpk, hd, q_dim, kbase, vbase, row_bytes, pos_bytes,
                                     pos0, n_swa, inv_d);
+}
+
+// The host draw over candidates, and the uniform number the device path is
+// given for the same generator state (draw_uniform on a saved state, which is
+// then restored): the device pick for that u must be this pick. `skip` draws
+// advance the generator first.
+int32_t dqr_sample_candidates(float temperature, int32_t top_k, float top_p, float pen_repeat, float pen_freq,
+                              float pen_present, int32_t pen_last_n, uint32_t seed, uint32_t skip,
+                              const int32_t* ids, const float* vals, size_t n, const int32_t* hist, size_t nh,
+                              float* u_out) {
+    SamplerParams p;
+    p.temperature = temperature;
+    p.top_k = top_k;
+    p.top_p = top_p;
+    p.penalty_repeat = pen_repeat;
+    p.penalty_freq = pen_freq;
+    p.penalty_present = pen_present;
+    p.penalty_last_n = pen_last_n;
+    p.seed = seed;
+    Sampler s;
+    s.configure(p);
+    for (uint32_t i = 0; i < skip; ++i) (void)s.draw_uniform();
+    const std::mt19937 st = s.rng_state();
+    *u_out = s.draw_uniform();
+    s.set_rng_state(st);
+    std::vector<int32_t> vi(ids, ids + n);
+    std::vector<float> vv(vals, vals + n);
+    std::vector<int32_t> h(hist, hist + nh);
+    return s.sample_candidates(vi, vv, h);
 }
 
 }  // extern "C"

@@ -13,8 +13,8 @@ from desireeia_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 STRUCTS = [_lib.CudaKQuantJob, _lib.CudaQ80Job, _lib.CudaQkvAttnArgs, _lib.CudaLayerArgs,
-           _lib.CudaLayerBatchArgs, _lib.GemvJob, _lib.MoeDesc]
-C_NAME = {"GemvJob": "dq_gemv_job_t", "MoeDesc": "dq_moe_t"}
+           _lib.CudaLayerBatchArgs, _lib.CudaSampleArgs, _lib.SampleState, _lib.GemvJob, _lib.MoeDesc]
+C_NAME = {"GemvJob": "dq_gemv_job_t", "MoeDesc": "dq_moe_t", "SampleState": "dq_sample_state_t"}
 
 
 @pytest.fixture(scope="module")

@@ -537,3 +537,63 @@ def test_layer_forward_batch(lib, orc):
         for m in L[0].values():
             m.free()
     lib.cuda_kv_cache_release()
+
+
+def test_head_and_pipelined_decode(lib, orc):
+    """One decode step through cuda_layer_forward with x left on the device,
+    then the head entry points on it: logits (final norm + head GEMV), top-40,
+    and a greedy draw queued on the device; the next step builds x from the
+    drawn token's Q8_0 embedding row (x_from_token)."""
+    from oracle import sampler_oracle as so
+    E, n_head, n_kv, F, n_ctx, pos, V = 1024, 8, 2, 2816, 64, 20, 5000
+    kc, vc, pb = prior_cache(orc, 1, n_ctx, n_kv, 128, pos, seed=71)
+    assert lib.cuda_kv_cache_reserve(kc.size)
+    assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+    L0 = make_layer(lib, orc, E, n_head, n_kv, F, (Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K), 72)
+    head = Mat(lib, Q6_K, V, E, 73)
+    emb = Mat(lib, Q8_0, V, E, 74)
+    rng = np.random.default_rng(75)
+    norm = (1 + 0.05 * rng.standard_normal(E)).astype(np.float32)
+    x = synth.gen_act(E, seed=76)
+    A = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos, orc.rope_cache(128, pos, 500000.0), x, None, 1, 0, 1)
+    assert lib.cuda_layer_forward(ctypes.byref(A)) == OK
+    xd = np.empty(E, np.float32)
+    assert lib.cuda_fetch_x(P(xd), E) == OK
+    k0, v0 = kc.copy(), vc.copy()
+    assert rel(xd, orc.layer_decode(L0[3], k0, v0, pos, x)[0]) <= TOL
+    y = np.empty(V, np.float32)
+    assert lib.cuda_head_forward(head.fmt, head.qs, head.sc, P(norm), E, ctypes.c_float(1e-5), V, P(y)) == OK
+    want = orc.matmul(Q6_K, head.w, V, E, orc.rms_norm(xd, norm, 1e-5))
+    assert rel(y, want) <= TOL
+    ids, vals = np.empty(40, np.int32), np.empty(40, np.float32)
+    assert lib.cuda_head_forward_topk(head.fmt, head.qs, head.sc, P(norm), E, ctypes.c_float(1e-5), V, 40, P(ids),
+                                      P(vals)) == OK
+    assert np.array_equal(ids, so.top_k_select(y, 40)) and np.array_equal(vals, y[ids])
+    hist = np.array([1, 2, 3], np.int32)
+    assert lib.cuda_sample_history(P(hist), 3) == OK
+    a = _lib.CudaSampleArgs()
+    a.temperature, a.top_k, a.top_p, a.penalty_repeat, a.kk, a.slot = 0.0, 40, 1.0, 1.0, 1, 2
+    assert lib.cuda_head_forward_sample(head.fmt, head.qs, head.sc, P(norm), E, ctypes.c_float(1e-5), V,
+                                        ctypes.byref(a)) == OK
+    tok = ctypes.c_int32(-1)
+    assert lib.cuda_sample_wait(2, ctypes.byref(tok)) == OK
+    assert tok.value == int(so.top_k_select(y, 1)[0])
+    # next step: x is the drawn token's embedding row, built on the device
+    out = np.full(E, np.nan, np.float32)
+    A2 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos + 1, orc.rope_cache(128, pos + 1, 500000.0), None, out, 1, 1,
+                    1)
+    A2.x_from_token, A2.embd_qs, A2.embd_scale, A2.embd_mul = 1, emb.qs, emb.sc, 0.0
+    assert lib.cuda_layer_forward(ctypes.byref(A2)) == OK
+    xe = orc.dequantize_row(Q8_0, np.ascontiguousarray(emb.w[tok.value]), E)
+    dk, dv = np.zeros_like(kc), np.zeros_like(vc)
+    assert lib.cuda_kv_cache_download(P(dk), P(dv), kc.size)
+    want2 = orc.layer_decode(L0[3], dk.copy(), dv.copy(), pos + 1, xe)[0]
+    assert rel(out, want2) <= TOL
+    # a head matrix the library did not upload: NOT_SUPPORTED, y untouched
+    keep = y.copy()
+    assert lib.cuda_head_forward(head.fmt, head.qs + 256, None, P(norm), E, ctypes.c_float(1e-5), V, P(y)) == \
+        NOT_SUPPORTED
+    assert np.array_equal(y, keep)
+    for m in list(L0[0].values()) + [head, emb]:
+        m.free()
+    lib.cuda_kv_cache_release()
