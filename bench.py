@@ -12,7 +12,8 @@ Also reported under "extra": the Q4_0 and Q8_0 GEMVs (configs 1-2), the Q6_K
 GEMV, each with its kernel-only bandwidth; the prefill GEMMs (config 3); the
 decode attention and the decoder layer (config 4); the MoE expert FFN
 (config 5); the prefill attention and the decoder layer over a 512-token
-prompt chunk (config 4's layer, the prefill path).
+prompt chunk (config 4's layer, the prefill path); the output head of a
+128256-token vocabulary with the device top-k and draw.
 
 `roofline` is the dominant kernel (Q4_K GEMV, up shape): algorithmic bytes per
 launch / average launch duration, from HIP events around back-to-back launches
@@ -301,6 +302,44 @@ class LayerPrefillCase:
         return gemm + 4.0 * 128 * 32 * keys
 
 
+class HeadCase:
+    """Output head of a 128256-token vocabulary over hidden 4096 (Q6_K, as
+    Llama-3 GGUF heads are commonly stored): final RMSNorm + head GEMV for one
+    decoded token, then the top-40 and the draw (temperature 0.8, top-k 40,
+    top-p 0.95, repeat penalty over 64 tokens) on the device."""
+
+    def __init__(self, dev, rows=128256, cols=4096, seed=70):
+        import torch
+        from desireeia_amd import _lib, ops, synth
+        self.rows, self.cols = rows, cols
+        self.mat = ops.QuantMatrix.from_gguf(synth.Q6_K, synth.gen_weights(synth.Q6_K, rows, cols, seed), rows, cols,
+                                             device=dev)
+        self.x = torch.from_numpy(synth.gen_act(cols, seed + 1)).to(dev)
+        self.norm = torch.ones(cols, device=dev)
+        self.logits = torch.empty(rows, device=dev)
+        self.sampler = ops.DeviceSampler(dev, hist=list(range(64)))
+        a = _lib.CudaSampleArgs()
+        a.temperature, a.top_k, a.top_p, a.penalty_repeat, a.penalty_last_n = 0.8, 40, 0.95, 1.1, 64
+        a.kk, a.u = 104, 0.5
+        self.args = a
+        torch.cuda.synchronize()
+
+    def logits_step(self):
+        from desireeia_amd import ops
+        ops.head_logits(self.mat, self.x, self.norm, out=self.logits)
+
+    def select_step(self):
+        from desireeia_amd import ops
+        ids, vals = ops.topk(self.logits, 104)
+        self.sampler.sample(ids, vals, self.args)
+
+    def bytes(self):
+        from desireeia_amd import synth
+        # the weights (431 MB: more than the Infinity Cache, streamed each
+        # call), x, the norm weights and the logits
+        return gemv_kernel_bytes(synth.Q6_K, self.rows, self.cols) + 2 * self.cols * 4
+
+
 def graph_time(fn, calls_per_graph, reps, warmup_reps=2):
     """Captures calls_per_graph calls of fn into one HIP graph and times `reps`
     replays with HIP events on the capturing stream. Returns us per call."""
@@ -446,6 +485,12 @@ def main():
         us = graph_time(ac.kernel, len(ac.caches), max(1, args.steps // len(ac.caches)))
         log(f"attn: {us:.2f} us, {KV_READ_BYTES / us / 1e3:.1f} GB/s")
         return
+    if args.only == "head":
+        hc = HeadCase(dev)
+        us = graph_time(hc.logits_step, 4, max(1, args.steps // 4))
+        us_sel = graph_time(hc.select_step, 4, max(1, args.steps // 4))
+        log(f"head: logits {us:.1f} us ({hc.bytes() / us / 1e3:.1f} GB/s), top-104 + draw {us_sel:.1f} us")
+        return
     if args.only == "attn_prefill":
         pc = AttnPrefillCase(dev)
         us = graph_time(pc.kernel, 4, max(1, args.steps // 4))
@@ -539,6 +584,14 @@ def main():
                                           "TFLOPs_alg": round(tf, 1), "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4)}
     log(f"decoder layer prefill (512 tokens): {us:.1f} us/layer  {lp.n_tok / us * 1e6:.0f} tok/s  {tf:.1f} TFLOP/s")
     del lp
+    hc = HeadCase(dev)
+    us = graph_time(hc.logits_step, 4, 5)
+    us_sel = graph_time(hc.select_step, 4, 5)
+    gbs = hc.bytes() / us / 1e3
+    extra["head_q6k_128256x4096"] = {"logits_us": round(us, 2), "GBps": round(gbs, 1),
+                                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "topk104_draw_us": round(us_sel, 2)}
+    log(f"output head 128256x4096 Q6_K: {us:.1f} us  {gbs:.1f} GB/s; top-104 + draw {us_sel:.1f} us")
+    del hc
     dom = extra["q4k_up"]
     roofline = {"bound": "hbm", "achieved": dom["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(),

@@ -13,9 +13,9 @@
 // in the sampler's order - larger value first, lower id on ties - so the
 // selection is a plain sort of integers: the high word is the float's bits
 // made order-preserving and inverted (+0 and -0 made equal), the low word the
-// id. Pass 1 sorts chunks of 4096 keys in LDS (bitonic) and keeps each
-// chunk's kk smallest; later passes do the same on the survivors until one
-// chunk remains. kk = 1 is a min-reduction instead.
+// id. Each pass selects the kk smallest keys of every chunk of 4096 by a
+// radix select over LDS histograms; passes repeat on the survivors until one
+// chunk remains, whose kk keys are sorted. kk = 1 is a min-reduction instead.
 //
 // Sampling (sample_kernel): penalties on the candidates that carry them
 // (counts over the last penalty_last_n tokens of a 256-token device ring),
@@ -45,11 +45,13 @@ __device__ __forceinline__ float key_value(uint64_t k) {
     return __builtin_bit_cast(float, u);
 }
 
-// Sorts TK_CHUNK keys of LDS ascending (bitonic network).
-__device__ void bitonic_sort(uint64_t* s) {
-    for (int size = 2; size <= TK_CHUNK; size <<= 1) {
+constexpr int TK_PER = TK_CHUNK / TK_T;  // keys per thread
+
+// Sorts the first P (a power of two <= TK_CHUNK) keys of LDS ascending.
+__device__ void bitonic_sort(uint64_t* s, int P) {
+    for (int size = 2; size <= P; size <<= 1) {
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int t = threadIdx.x; t < TK_CHUNK / 2; t += TK_T) {
+            for (int t = threadIdx.x; t < P / 2; t += TK_T) {
                 const int i = 2 * t - (t & (stride - 1)), j = i + stride;
                 const bool asc = (i & size) == 0;
                 const uint64_t a = s[i], b = s[j];
@@ -63,26 +65,117 @@ __device__ void bitonic_sort(uint64_t* s) {
     }
 }
 
-// One selection pass: chunk blockIdx.x of the input (float logits with their
-// index as id on the first pass, keys afterwards) -> its kk smallest keys.
+// One selection pass over chunk blockIdx.x (float logits with their index as
+// id on the first pass, keys afterwards): the kk smallest keys of the chunk.
+// Radix select: eight rounds of an 8-bit LDS histogram over the keys that
+// share the prefix fixed so far find the kk-th smallest key K exactly (keys
+// are distinct: the id is in them); the keys <= K are then gathered, and on
+// the final pass (one chunk) sorted.
 __global__ __launch_bounds__(TK_T) void topk_pass_kernel(const float* __restrict__ v, const uint64_t* __restrict__ kin,
-                                                         uint32_t n, uint32_t kk, uint64_t* __restrict__ kout) {
-    __shared__ uint64_t s[TK_CHUNK];
+                                                         uint32_t n, uint32_t kk, int sorted,
+                                                         uint64_t* __restrict__ kout, int32_t* __restrict__ ids,
+                                                         float* __restrict__ vals) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint64_t list[256];
+    __shared__ uint64_t s_prefix, s_key;
+    __shared__ uint32_t s_rank, s_cnt, s_bin;
+    const int t = threadIdx.x;
     const size_t base = (size_t)blockIdx.x * TK_CHUNK;
-    for (int j = threadIdx.x; j < TK_CHUNK; j += TK_T) {
-        const size_t g = base + j;
+    uint64_t key[TK_PER];
+#pragma unroll
+    for (int j = 0; j < TK_PER; ++j) {
+        const size_t g = base + (size_t)j * TK_T + t;  // coalesced
         uint64_t k = ~0ull;
         if (g < n) k = kin ? kin[g] : order_key(v[g], (uint32_t)g);
-        s[j] = k;
+        key[j] = k;
+    }
+    const size_t m = n - base < (size_t)TK_CHUNK ? n - base : (size_t)TK_CHUNK;  // keys in this chunk
+    const uint32_t want = (uint32_t)(kk < m ? kk : m);
+    uint64_t prefix = 0;
+    uint32_t rank = want;  // 1-based rank of K among the keys with this prefix
+    for (int r = 0; r < 8; ++r) {
+        const int shift = 56 - 8 * r;
+        hist[t] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < TK_PER; ++j) {
+            const bool match = r == 0 || (key[j] >> (shift + 8)) == prefix;
+            if (match) atomicAdd(&hist[(key[j] >> shift) & 255], 1u);
+        }
+        __syncthreads();
+        if (t < 64) {  // one wave scans the 256 bins, 4 per lane
+            const uint32_t h0 = hist[4 * t], h1 = hist[4 * t + 1], h2 = hist[4 * t + 2], h3 = hist[4 * t + 3];
+            const uint32_t tot = h0 + h1 + h2 + h3;
+            uint32_t incl = tot;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint32_t o = __shfl_up(incl, off, DQ_WAVE);
+                if (t >= off) incl += o;
+            }
+            const uint32_t excl = incl - tot;
+            if (excl < rank && rank <= incl) {  // exactly one lane
+                uint32_t c = excl, d = 4 * t;
+                const uint32_t hv[4] = {h0, h1, h2, h3};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (c + hv[q] >= rank) {
+                        d = 4 * t + q;
+                        break;
+                    }
+                    c += hv[q];
+                }
+                s_prefix = (prefix << 8) | d;
+                s_rank = rank - c;
+                s_bin = hist[d];
+            }
+        }
+        __syncthreads();
+        prefix = s_prefix;
+        rank = s_rank;
+        if (s_bin == 1) {  // one key has this prefix: it is K (uniform branch)
+#pragma unroll
+            for (int j = 0; j < TK_PER; ++j)
+                if ((key[j] >> shift) == prefix) s_key = key[j];
+            __syncthreads();
+            prefix = s_key;
+            break;
+        }
+    }
+    // prefix is now K, the want-th smallest key. Real keys are distinct, so
+    // exactly `want` keys are <= K - unless K is the padding key ~0 (a later
+    // pass over a chunk holding fewer than kk real keys): then only the keys
+    // below it are taken and the rest of the output is padding again.
+    if (t == 0) s_cnt = 0;
+    __syncthreads();
+    const bool real = prefix != ~0ull;
+#pragma unroll
+    for (int j = 0; j < TK_PER; ++j) {
+        if (key[j] < prefix || (real && key[j] == prefix)) {
+            const uint32_t pos = atomicAdd(&s_cnt, 1u);
+            if (pos < 256) list[pos] = key[j];
+        }
     }
     __syncthreads();
-    bitonic_sort(s);
-    for (uint32_t j = threadIdx.x; j < kk; j += TK_T) kout[(size_t)blockIdx.x * kk + j] = s[j];
+    const uint32_t got = s_cnt < want ? s_cnt : want;
+    int P = 1;
+    while (P < (int)kk) P <<= 1;
+    for (int j = got + t; j < P; j += TK_T) list[j] = ~0ull;
+    __syncthreads();
+    if (sorted) {  // the final pass: ids and values, best first
+        bitonic_sort(list, P);
+        for (uint32_t j = t; j < kk; j += TK_T) {
+            if (ids) ids[j] = (int32_t)(uint32_t)list[j];
+            if (vals) vals[j] = key_value(list[j]);
+        }
+        return;
+    }
+    for (uint32_t j = t; j < kk; j += TK_T) kout[(size_t)blockIdx.x * kk + j] = list[j];
 }
 
 // kk = 1: the smallest key of each chunk.
 __global__ __launch_bounds__(TK_T) void argmin_pass_kernel(const float* __restrict__ v, const uint64_t* __restrict__ kin,
-                                                           uint32_t n, uint64_t* __restrict__ kout) {
+                                                           uint32_t n, int final, uint64_t* __restrict__ kout,
+                                                           int32_t* __restrict__ ids, float* __restrict__ vals) {
     __shared__ uint64_t part[TK_T / 64];
     const size_t base = (size_t)blockIdx.x * TK_CHUNK;
     uint64_t best = ~0ull;
@@ -102,17 +195,13 @@ __global__ __launch_bounds__(TK_T) void argmin_pass_kernel(const float* __restri
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < TK_T / 64; ++w) best = part[w] < best ? part[w] : best;
-        kout[blockIdx.x] = best;
+        if (final) {
+            if (ids) ids[0] = (int32_t)(uint32_t)best;
+            if (vals) vals[0] = key_value(best);
+        } else {
+            kout[blockIdx.x] = best;
+        }
     }
-}
-
-__global__ void topk_unpack_kernel(const uint64_t* __restrict__ k, uint32_t kk, int32_t* __restrict__ ids,
-                                   float* __restrict__ vals) {
-    const uint32_t j = blockIdx.x * blockDim.x + threadIdx.x;
-    if (j >= kk) return;
-    const uint64_t key = k[j];
-    if (ids) ids[j] = (int32_t)(uint32_t)key;
-    if (vals) vals[j] = key_value(key);
 }
 
 // Sampler::sample_candidates (core/sampler.cpp:298-322) with finish_
@@ -121,17 +210,28 @@ __global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ v
                                                      uint32_t n, CudaSampleArgs a, dq_sample_state_t* st) {
     __shared__ uint64_t s[256];
     __shared__ float probs[256];
+    __shared__ int32_t hist[DQ_SAMPLE_HIST];
     const int t = threadIdx.x;
-    if (a.append_input && t == 0) {  // the step's input token enters the history
-        const uint32_t pos = st->wpos;
-        st->hist[pos] = st->tok;
-        st->wpos = (pos + 1) % DQ_SAMPLE_HIST;
-        st->len = st->len + 1;
-    }
+    // the history ring into LDS (one entry per thread), then the step's input
+    // token appended to both copies
+    const uint32_t len0 = st->len, wpos0 = st->wpos;
+    hist[t] = st->hist[t];
     __syncthreads();
+    uint32_t len = len0, wpos = wpos0;
+    if (a.append_input) {
+        if (t == 0) {
+            const int32_t tok = st->tok;
+            hist[wpos0] = tok;
+            st->hist[wpos0] = tok;
+            st->wpos = (wpos0 + 1) % DQ_SAMPLE_HIST;
+            st->len = len0 + 1;
+        }
+        wpos = (wpos0 + 1) % DQ_SAMPLE_HIST;
+        len = len0 + 1;
+        __syncthreads();
+    }
     const bool pen = a.penalty_last_n > 0 &&
                      (a.penalty_repeat != 1.0f || a.penalty_freq != 0.0f || a.penalty_present != 0.0f);
-    const uint32_t len = st->len, wpos = st->wpos;
     const uint32_t look = min((uint32_t)a.penalty_last_n, min(len, (uint32_t)DQ_SAMPLE_HIST));
     uint64_t key = ~0ull;
     if (t < (int)n) {
@@ -141,7 +241,7 @@ __global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ v
         if (pen) {
             int32_t cnt = 0;
             for (uint32_t j = 0; j < look; ++j)
-                cnt += st->hist[(wpos + DQ_SAMPLE_HIST - 1 - j) % DQ_SAMPLE_HIST] == id;
+                cnt += hist[(wpos + DQ_SAMPLE_HIST - 1 - j) % DQ_SAMPLE_HIST] == id;
             if (cnt > 0) {
                 if (lg <= 0.0f) lg *= a.penalty_repeat;
                 else lg /= a.penalty_repeat;
@@ -296,14 +396,14 @@ int dq_topk(const float* d_v, uint32_t n, uint32_t kk, int32_t* d_ids, float* d_
     int cur = 0;
     for (;;) {
         const unsigned blocks = (unsigned)((m + TK_CHUNK - 1) / TK_CHUNK);
-        if (kk == 1) argmin_pass_kernel<<<blocks, TK_T, 0, s>>>(d_v, kin, (uint32_t)m, buf[cur]);
-        else topk_pass_kernel<<<blocks, TK_T, 0, s>>>(d_v, kin, (uint32_t)m, kk, buf[cur]);
+        const int final = blocks == 1;
+        if (kk == 1) argmin_pass_kernel<<<blocks, TK_T, 0, s>>>(d_v, kin, (uint32_t)m, final, buf[cur], d_ids, d_vals);
+        else topk_pass_kernel<<<blocks, TK_T, 0, s>>>(d_v, kin, (uint32_t)m, kk, final, buf[cur], d_ids, d_vals);
         kin = buf[cur];
         m = (size_t)blocks * kk;
         cur ^= 1;
         if (blocks == 1) break;
     }
-    topk_unpack_kernel<<<(kk + 255) / 256, 256, 0, s>>>(kin, kk, d_ids, d_vals);
     return dq_launch_status();
 }
 
