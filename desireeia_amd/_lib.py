@@ -46,8 +46,9 @@ SIGNATURES = {
     "dq_kv_write_batch": (c_int, [c_p, c_p, c_size, c_u32, c_u32, c_u32, c_p, c_p, c_u32, c_u32, c_p]),
     "dq_rope_kv_write_batch": (c_int, [c_p, c_p, c_p, c_size, c_size, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p,
                                        c_p, c_u32, c_u32, c_p]),
+    "dq_attn_prefill_workspace_bytes": (c_int, [c_u32, c_u32, c_u32, c_u32, ctypes.POINTER(c_size)]),
     "dq_attn_prefill_q8": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_u32, c_u32, c_u32, c_p,
-                                   c_p]),
+                                   c_p, c_size, c_p]),
     "dq_layer_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
     "dq_layer_prefill_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
     "dq_rms_norm_rows": (c_int, [c_p, c_p, c_p, c_p, c_size, c_size, c_f, c_p, c_p]),

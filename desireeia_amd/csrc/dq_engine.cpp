@@ -864,17 +864,20 @@ int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, 
     if (!q_all || !out_all) return DQ_ERR_INVALID_ARG;
     if (!stream()) return DQ_ERR_IO;
     const size_t n = (size_t)n_tokens * q_dim;
-    if (!reserve(g.pio, 2 * n * 4)) return DQ_ERR_IO;
+    size_t ab = 0;
+    if (dq_attn_prefill_workspace_bytes(n_tokens, n_head, n_kv, head_dim, &ab) != DQ_OK) return DQ_ERR_NOT_SUPPORTED;
+    if (!reserve(g.pio, 2 * dq_align256(n * 4) + ab)) return DQ_ERR_IO;
     const hipStream_t s = g.stream;
     float* dq = (float*)g.pio.p;
-    float* dout = dq + n;
+    float* dout = (float*)((uint8_t*)g.pio.p + dq_align256(n * 4));
+    void* dwork = (uint8_t*)g.pio.p + 2 * dq_align256(n * 4);
     if (hipMemcpyAsync(dq, q_all, n * 4, hipMemcpyHostToDevice, s) != hipSuccess) return io_fail();
     // columns past the heads keep the caller's values
     if ((size_t)q_dim > (size_t)n_head * head_dim &&
         hipMemcpyAsync(dout, out_all, n * 4, hipMemcpyHostToDevice, s) != hipSuccess)
         return io_fail();
     if (dq_attn_prefill_q8(dq, g.kc + layer_off, g.vc + layer_off, n_tokens, n_head, n_kv, head_dim, q_dim, col0,
-                           n_swa, n_ctx, dout, s) != DQ_OK)
+                           n_swa, n_ctx, dout, dwork, ab, s) != DQ_OK)
         return io_fail();
     if (hipMemcpyAsync(out_all, dout, n * 4, hipMemcpyDeviceToHost, s) != hipSuccess) return io_fail();
     return sync();

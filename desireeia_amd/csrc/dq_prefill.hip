@@ -50,6 +50,8 @@ struct PrefillArgs {
     size_t pos_bytes;
     int q_dim, n_tok, hpk, n_kv, pos0, n_swa, n_qblk;
     float qscale;         // 1/sqrt(hd) * log2(e)
+    int split;            // key splits per (KV head, row block); > 1: partial records
+    float* part;          // [n_kv][n_rows][split][HD + 4]: O (unnormalised), max (log2 units), sum, pad
 };
 
 __device__ __forceinline__ int win_lo(int pos, int n_swa) {
@@ -73,7 +75,7 @@ __device__ __forceinline__ int vcol_group(int g) {  // g = a / 4
     return (g & 4) | ((g & 1) << 1) | ((g >> 1) & 1);
 }
 
-template <int HD>
+template <int HD, bool SPLIT>
 __global__ __launch_bounds__(NT) void attn_prefill_kernel(PrefillArgs A) {
     constexpr int NB = HD / 32;          // Q8_0 blocks per row
     constexpr int RB = NB * DQ_SZ_Q8_0;  // row bytes
@@ -91,7 +93,8 @@ __global__ __launch_bounds__(NT) void attn_prefill_kernel(PrefillArgs A) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
     const int hkv = blockIdx.x % A.n_kv;
-    const int qb = A.n_qblk - 1 - (int)(blockIdx.x / A.n_kv);  // longest rows first
+    const int sp = SPLIT ? (int)(blockIdx.x / A.n_kv) % A.split : 0;
+    const int qb = A.n_qblk - 1 - (int)(blockIdx.x / A.n_kv / (SPLIT ? A.split : 1));  // longest rows first
     const int hpk = A.hpk;
     const int n_rows = A.n_tok * hpk;
     const int R0 = qb * RPB;
@@ -127,7 +130,16 @@ __global__ __launch_bounds__(NT) void attn_prefill_kernel(PrefillArgs A) {
             rv[it] = *reinterpret_cast<const uint32_t*>(A.vc + off);
         }
     };
-    const int kt0 = k_begin & ~(KT - 1);
+    int kt0 = k_begin & ~(KT - 1);
+    int k_end = p_last;  // last key of this workgroup's range
+    if constexpr (SPLIT) {
+        // this split's contiguous share of the key tiles
+        const int n_tiles = (p_last - kt0) / KT + 1;
+        const int per = (n_tiles + A.split - 1) / A.split;
+        const int first = kt0 + sp * per * KT;
+        k_end = min(p_last, first + per * KT - 1);
+        kt0 = first;
+    }
     load_tile(kt0);
 
     // query fragments (B operand of S^T = K Q^T): dims 16s + 8*half + i
@@ -153,7 +165,7 @@ __global__ __launch_bounds__(NT) void attn_prefill_kernel(PrefillArgs A) {
 
     const uint8_t* rkb = reinterpret_cast<const uint8_t*>(rawk);
     const uint8_t* rvb = reinterpret_cast<const uint8_t*>(rawv);
-    for (int k0 = kt0; k0 <= p_last; k0 += KT) {
+    for (int k0 = kt0; k0 <= k_end; k0 += KT) {
 #pragma unroll
         for (int it = 0; it < PER; ++it) {
             const int i = tid + it * NT;
@@ -217,7 +229,7 @@ __global__ __launch_bounds__(NT) void attn_prefill_kernel(PrefillArgs A) {
                 }
             }
         }
-        if (k0 + KT <= p_last) load_tile(k0 + KT);
+        if (k0 + KT <= k_end) load_tile(k0 + KT);
         __syncthreads();
         if (!wave_live || k0 > w_pmax || k0 + KT - 1 < w_lomin) continue;  // uniform per wave
 
@@ -282,6 +294,23 @@ __global__ __launch_bounds__(NT) void attn_prefill_kernel(PrefillArgs A) {
     }
     if (!wave_live) return;
     const float lt = l + __shfl_xor(l, 32, DQ_WAVE);
+    if constexpr (SPLIT) {
+        // partial record of this row and split: O, max, sum (a split with no
+        // visible key leaves max = -inf, sum = 0)
+        if (!row_ok) return;
+        float* rec = A.part + (((size_t)hkv * n_rows + row) * A.split + sp) * (HD + 4);  // 16-byte aligned
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<float4*>(rec + 32 * b + 8 * g + 4 * half) =
+                    make_float4(o[b][4 * g], o[b][4 * g + 1], o[b][4 * g + 2], o[b][4 * g + 3]);
+        if (half == 0) {
+            rec[HD] = m;
+            rec[HD + 1] = lt;
+        }
+        return;
+    }
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     if (!row_ok) return;
     float* dst = A.out + (size_t)t * A.q_dim + (size_t)head * HD + 4 * half;
@@ -291,6 +320,38 @@ __global__ __launch_bounds__(NT) void attn_prefill_kernel(PrefillArgs A) {
         for (int g = 0; g < 4; ++g)
             *reinterpret_cast<float4*>(dst + 32 * b + 8 * g) =
                 make_float4(o[b][4 * g] * inv, o[b][4 * g + 1] * inv, o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv);
+}
+
+// Merge of the key splits: one wave per row combines its split records
+// (max M = max m_s, O = sum O_s 2^(m_s - M) / sum l_s 2^(m_s - M)) and writes
+// the row's output.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_merge_kernel(PrefillArgs A) {
+    constexpr int PER = HD / 64;  // dims per lane
+    const int n_rows = A.n_tok * A.hpk;
+    const int w = (int)(blockIdx.x * 4 + (threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63;
+    if (w >= n_rows * A.n_kv) return;  // uniform per wave
+    const int hkv = w / n_rows, row = w % n_rows;
+    const int t = row / A.hpk, head = hkv * A.hpk + row % A.hpk;
+    const float* rec = A.part + ((size_t)hkv * n_rows + row) * A.split * (HD + 4);
+    float M = -INFINITY;
+    for (int s = 0; s < A.split; ++s) M = fmaxf(M, rec[s * (HD + 4) + HD]);
+    float L = 0.0f, o[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) o[i] = 0.0f;
+    for (int s = 0; s < A.split; ++s) {
+        const float* r = rec + s * (HD + 4);
+        const float ms = r[HD];
+        const float f = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+        L += r[HD + 1] * f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) o[i] += r[lane + 64 * i] * f;
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    float* dst = A.out + (size_t)t * A.q_dim + (size_t)head * HD;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) dst[lane + 64 * i] = o[i] * inv;
 }
 
 // ------------------------------------------------------------ row writes --
@@ -452,7 +513,8 @@ __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float* __restr
 struct PrefillWs {
     float *xn, *q, *k, *v, *attn, *h, *gate, *up, *down;
     uint8_t* gw[2];  // Q4_K, Q6_K
-    size_t gw_bytes, total;
+    uint8_t* aw;     // attention key-split records
+    size_t gw_bytes, aw_bytes, total;
 };
 
 bool prefill_layer_ok(const dq_layer_t* L) {
@@ -496,14 +558,46 @@ PrefillWs prefill_carve(const dq_layer_t* L, uint32_t n_tok, uint8_t* base) {
         w.gw[f] = base ? base + off : nullptr;
         off += w.gw_bytes;
     }
+    size_t ab = 0;
+    (void)dq_attn_prefill_workspace_bytes(n_tok, L->n_head, L->n_head_kv, L->head_dim, &ab);
+    w.aw = base ? base + off : nullptr;
+    w.aw_bytes = ab;
+    off += ab;
     w.total = off;
     return w;
 }
 
 template <int HD>
 int launch_prefill(const PrefillArgs& a, int grid, hipStream_t s) {
-    attn_prefill_kernel<HD><<<grid, NT, 0, s>>>(a);
+    if (a.split > 1) {
+        attn_prefill_kernel<HD, true><<<grid * a.split, NT, 0, s>>>(a);
+        const int rows = a.n_tok * a.hpk * a.n_kv;
+        attn_prefill_merge_kernel<HD><<<(rows + 3) / 4, 256, 0, s>>>(a);
+    } else {
+        attn_prefill_kernel<HD, false><<<grid, NT, 0, s>>>(a);
+    }
     return dq_launch_status();
+}
+
+// Key splits for a grid of `blocks` workgroups over `tiles` key tiles of the
+// longest rows: enough workgroups for two per CU, each split keeping at least
+// 4 tiles (128 keys); at most 16.
+int prefill_split(int blocks, int tiles, int cus) {
+    int sp = 1;
+    while (sp < 16 && blocks * sp < 2 * cus && tiles / (2 * sp) >= 4) sp *= 2;
+    return sp;
+}
+
+int prefill_cus() {
+    static int c = 0;
+    if (!c) {
+        int dev = 0, n = 0;
+        c = (hipGetDevice(&dev) == hipSuccess &&
+             hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+                ? n
+                : 256;
+    }
+    return c;
 }
 
 }  // namespace
@@ -542,9 +636,29 @@ int dq_rope_kv_write_batch(float* d_q, const float* d_k, const float* d_v, size_
     return dq_launch_status();
 }
 
+// Key splits the grid of (n_tok, n_head, n_head_kv) could use at most, and
+// the bytes of their partial records.
+static int prefill_split_max(uint32_t n_tok, uint32_t n_head, uint32_t n_head_kv) {
+    const uint64_t n_qblk = ((uint64_t)n_tok * (n_head / n_head_kv) + RPB - 1) / RPB;
+    return prefill_split((int)(n_qblk * n_head_kv), 1 << 30, prefill_cus());
+}
+
+static size_t prefill_part_bytes(uint32_t n_tok, uint32_t n_head, uint32_t hd, int split) {
+    return split > 1 ? dq_align256((size_t)n_tok * n_head * split * (hd + 4) * 4) : 0;
+}
+
+int dq_attn_prefill_workspace_bytes(uint32_t n_tok, uint32_t n_head, uint32_t n_head_kv, uint32_t hd,
+                                    size_t* bytes) {
+    if (!bytes) return DQ_ERR_INVALID_ARG;
+    if (n_head_kv == 0 || n_head % n_head_kv) return DQ_ERR_NOT_SUPPORTED;
+    if (hd != 64 && hd != 128 && hd != 256) return DQ_ERR_NOT_SUPPORTED;
+    *bytes = prefill_part_bytes(n_tok, n_head, hd, prefill_split_max(n_tok, n_head, n_head_kv));
+    return DQ_OK;
+}
+
 int dq_attn_prefill_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_tok, uint32_t n_head,
                        uint32_t n_head_kv, uint32_t hd, uint32_t q_dim, uint32_t pos0, uint32_t n_swa,
-                       uint32_t n_ctx, float* d_out, void* stream) {
+                       uint32_t n_ctx, float* d_out, void* d_work, size_t work_bytes, void* stream) {
     if (!d_q || !d_kc || !d_vc || !d_out) return DQ_ERR_INVALID_ARG;
     if (n_head_kv == 0 || n_head % n_head_kv) return DQ_ERR_NOT_SUPPORTED;
     if (hd != 64 && hd != 128 && hd != 256) return DQ_ERR_NOT_SUPPORTED;
@@ -555,7 +669,7 @@ int dq_attn_prefill_q8(const float* d_q, const void* d_kc, const void* d_vc, uin
     const uint32_t hpk = n_head / n_head_kv;
     const uint64_t n_rows = (uint64_t)n_tok * hpk;
     const uint64_t n_qblk = (n_rows + RPB - 1) / RPB;
-    if (n_qblk * n_head_kv > 0x7FFFFFFFull || n_rows > 0x7FFFFFFFull) return DQ_ERR_NOT_SUPPORTED;
+    if (n_qblk * n_head_kv * 16 > 0x7FFFFFFFull || n_rows > 0x7FFFFFFFull) return DQ_ERR_NOT_SUPPORTED;
     PrefillArgs a;
     a.q = d_q;
     a.out = d_out;
@@ -571,6 +685,16 @@ int dq_attn_prefill_q8(const float* d_q, const void* d_kc, const void* d_vc, uin
     a.n_qblk = (int)n_qblk;
     a.qscale = (1.0f / sqrtf((float)hd)) * 1.4426950408889634f;
     const int grid = (int)(n_qblk * n_head_kv);
+    // key tiles of the longest rows (the last row block): the split is sized
+    // so that a grid too small for the GPU spreads their keys over more
+    // workgroups; it needs room for the partial records
+    const uint32_t p_last = pos0 + n_tok - 1;
+    const uint32_t p_first = pos0 + (uint32_t)(((n_qblk - 1) * RPB) / hpk);
+    const uint32_t kb = (n_swa > 0 && p_first + 1 > n_swa) ? p_first + 1 - n_swa : 0;
+    int split = prefill_split(grid, (int)((p_last - (kb & ~(uint32_t)(KT - 1))) / KT + 1), prefill_cus());
+    while (split > 1 && (!d_work || work_bytes < prefill_part_bytes(n_tok, n_head, hd, split))) split /= 2;
+    a.split = split;
+    a.part = (float*)d_work;
     const hipStream_t s = (hipStream_t)stream;
     switch (hd) {
     case 64: return launch_prefill<64>(a, grid, s);
@@ -642,7 +766,7 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
     DQP_TRY(dq_rope_kv_write_batch(w.q, w.k, w.v, QD, KVD, d_rope, L->n_rot, n_tok, L->n_head, L->n_head_kv,
                                    L->head_dim, d_kc, d_vc, pos0, n_ctx, stream));
     DQP_TRY(dq_attn_prefill_q8(w.q, d_kc, d_vc, n_tok, L->n_head, L->n_head_kv, L->head_dim, (uint32_t)QD, pos0,
-                               n_swa, n_ctx, w.attn, stream));
+                               n_swa, n_ctx, w.attn, w.aw, w.aw_bytes, stream));
     {
         const int f[1] = {L->fmt_o};
         const void* m[1] = {L->wo};

@@ -246,16 +246,27 @@ class KVCache:
                    "dq_rope_kv_write_batch")
 
 
-def attention_prefill(q, cache, n_head, pos0, n_swa=0, out=None):
+def attn_prefill_workspace(n_tok, n_head, n_head_kv, hd, device="cuda"):
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    _lib.check(lib.dq_attn_prefill_workspace_bytes(n_tok, n_head, n_head_kv, hd, ctypes.byref(n)),
+               "dq_attn_prefill_workspace_bytes")
+    return torch.empty(max(n.value, 1), dtype=torch.uint8, device=device)
+
+
+def attention_prefill(q, cache, n_head, pos0, n_swa=0, out=None, work=None, split=True):
     """Prefill attention of q [n_tok][q_dim] (token t at position pos0 + t)
-    over the cache, causal (n_swa 0) or over a sliding window of n_swa."""
+    over the cache, causal (n_swa 0) or over a sliding window of n_swa.
+    split=False runs without a workspace (no key split)."""
     lib = _lib.load()
     q = q.contiguous()
     n_tok, q_dim = q.shape
     o = out if out is not None else torch.zeros(n_tok, q_dim, dtype=torch.float32, device=q.device)
+    wk = work if work is not None or not split else attn_prefill_workspace(n_tok, n_head, cache.n_head_kv, cache.hd,
+                                                                             q.device)
     _lib.check(lib.dq_attn_prefill_q8(_ptr(q), _ptr(cache.k), _ptr(cache.v), n_tok, n_head, cache.n_head_kv,
-                                      cache.hd, q_dim, int(pos0), int(n_swa), cache.n_ctx, _ptr(o), _stream()),
-               "dq_attn_prefill_q8")
+                                      cache.hd, q_dim, int(pos0), int(n_swa), cache.n_ctx, _ptr(o), _ptr(wk),
+                                      wk.numel() if wk is not None else 0, _stream()), "dq_attn_prefill_q8")
     return o
 
 

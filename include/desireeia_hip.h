@@ -211,10 +211,17 @@ int dq_rope_kv_write_batch(float* d_q, const float* d_k, const float* d_v, size_
  * 1/sqrt(hd). Columns of q_dim past n_head * hd are left untouched. The K/V
  * rows of every position read must already be in the cache. hd in {64, 128,
  * 256}; other hd: -2. Operands run on fp16 MFMA split into hi + lo parts
- * (~2^-22 relative); cached values and queries must lie inside fp16. */
+ * (~2^-22 relative); cached values and queries must lie inside fp16. When the
+ * (row block x KV head) grid is too small for the GPU, each block's keys are
+ * split over several workgroups whose partial softmax records a second kernel
+ * merges; that needs d_work of dq_attn_prefill_workspace_bytes() bytes (NULL
+ * or smaller: fewer or no splits, same result to float rounding). Calls
+ * sharing a workspace must not overlap. */
+int dq_attn_prefill_workspace_bytes(uint32_t n_tok, uint32_t n_head, uint32_t n_head_kv, uint32_t hd,
+                                    size_t* bytes);
 int dq_attn_prefill_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_tok, uint32_t n_head,
                        uint32_t n_head_kv, uint32_t hd, uint32_t q_dim, uint32_t pos0, uint32_t n_swa,
-                       uint32_t n_ctx, float* d_out, void* stream);
+                       uint32_t n_ctx, float* d_out, void* d_work, size_t work_bytes, void* stream);
 
 /* ------------------------------------------------------- decoder layer */
 

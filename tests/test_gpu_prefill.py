@@ -168,3 +168,29 @@ def test_attention_prefill_unsupported(gpu):
     q = torch.zeros(4, 4 * 128, device=gpu)
     with pytest.raises(_lib.DqError):
         ops.attention_prefill(q, cache, 4, 13)  # positions past the cache
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,pos0,n_tok,n_swa", [
+    (32, 8, 128, 4000, 100, 0),    # a follow-up prompt after a long context: 32 workgroups, 16 key splits
+    (32, 8, 128, 3000, 50, 1024),  # the same over a sliding window
+    (8, 2, 64, 2000, 30, 0),       # hd 64
+    (8, 2, 256, 1500, 20, 0),      # hd 256
+    (4, 4, 128, 700, 3, 0),        # three tokens
+])
+def test_attention_prefill_key_split(gpu, orc, n_head, n_kv, hd, pos0, n_tok, n_swa):
+    """Key splits (small grids): the merged result equals the unsplit kernel's
+    to float rounding, and the oracle within the attention tolerance."""
+    print(f"attn_prefill split n_head={n_head} n_kv={n_kv} hd={hd} pos0={pos0} n_tok={n_tok} n_swa={n_swa}",
+          flush=True)
+    kc, vc = host_cache(orc, pos0 + n_tok, n_kv, hd, seed=pos0 + n_tok)
+    q = np.random.default_rng(n_tok).standard_normal((n_tok, n_head * hd)).astype(np.float32)
+    cache = device_cache(gpu, kc, vc, pos0 + n_tok, n_kv, hd)
+    dq = torch.from_numpy(q).to(gpu)
+    split = ops.attention_prefill(dq, cache, n_head, pos0, n_swa).cpu().numpy()
+    whole = ops.attention_prefill(dq, cache, n_head, pos0, n_swa, split=False).cpu().numpy()
+    e = rel(split, whole)
+    print(f"  split vs unsplit: {e:.2e}", flush=True)
+    assert e <= 1e-6
+    for t in (0, n_tok - 1):
+        want = orc.attn_prefill(q[t:t + 1], kc, vc, 1, n_head, n_kv, hd, pos0 + t, n_swa)
+        assert rel(split[t], want) <= TOL
