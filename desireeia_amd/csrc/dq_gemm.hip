@@ -459,20 +459,13 @@ __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 // scale (core/i8gemm_impl.h:50-82), written as fp16(q*d*s) in K order `perm`
 // (0 natural, 1 Q6_K item order); with a min plane (Q4_K), fp16(exact float
 // block sum * s) of block b at minp[b/8][t][b%8]; s the row's power-of-two
-// range scale (row_scale_kernel) and inv[t] = 1/s. One lane per block (and,
-// with a min plane, one per block sum).
-__global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restrict__ x, int cols, int n_tok,
-                                                           _Float16* __restrict__ out, int lda,
-                                                           _Float16* __restrict__ minp, int perm,
-                                                           const float* __restrict__ rscale, float* __restrict__ inv) {
+// range scale. One block (or one block sum) per call; the row kernel below
+// runs them for its token.
+__device__ __forceinline__ void quantize_f16_block(const float* __restrict__ x, int cols, int n_tok,
+                                                   _Float16* __restrict__ out, int lda, _Float16* __restrict__ minp,
+                                                   int perm, int t, int b, float sc) {
     const int nb = cols / 32;
-    const int gb = blockIdx.x * blockDim.x + threadIdx.x;
-    const int stride = minp ? 2 * nb : nb;
-    if (gb >= n_tok * stride) return;
-    const int t = gb / stride, b = gb % stride;
     _Float16* o = out + (size_t)t * lda;
-    const float sc = rscale[t];
-    if (b == 0) inv[t] = 1.0f / sc;
     if (b >= nb) {  // block sum of block b - nb
         const int mb = b - nb;
         const float* p = x + (size_t)t * cols + 32 * mb;
@@ -535,6 +528,34 @@ __global__ __launch_bounds__(256) void quantize_f16_kernel(const float* __restri
     }
 }
 
+// One workgroup per token row: the row's power-of-two range scale (as
+// row_scale_kernel) and then every block of the row (quantize_f16_block);
+// inv[t] = 1/s.
+__global__ __launch_bounds__(256) void quantize_f16_rows_kernel(const float* __restrict__ x, int cols, int n_tok,
+                                                                _Float16* __restrict__ out, int lda,
+                                                                _Float16* __restrict__ minp, int perm,
+                                                                float* __restrict__ rscale, float* __restrict__ inv) {
+    __shared__ float wmax[4];
+    const int t = blockIdx.x;
+    const float* row = x + (size_t)t * cols;
+    float m = 0.0f;
+    for (int c = threadIdx.x * 4; c < cols; c += 1024) {
+        const float4 f = *reinterpret_cast<const float4*>(row + c);
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
+    }
+    m = dq_wave_max(m);
+    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    __syncthreads();
+    const float sc = row_scale_of(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+    if (threadIdx.x == 0) {
+        rscale[t] = sc;
+        inv[t] = 1.0f / sc;
+    }
+    const int nb = cols / 32;
+    const int stride = minp ? 2 * nb : nb;
+    for (int b = threadIdx.x; b < stride; b += 256) quantize_f16_block(x, cols, n_tok, out, lda, minp, perm, t, b, sc);
+}
+
 __global__ void zero_kernel(float* __restrict__ y, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) y[i] = 0.0f;
@@ -594,8 +615,8 @@ extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_
     _Float16* minp = with_min ? (_Float16*)(base + min_off(cols, n_tok)) : nullptr;
     float* sc = (float*)(base + scale_off(fmt, cols, n_tok));
     float* inv = (float*)(base + inv_off(fmt, cols, n_tok));
-    row_scale_kernel<<<(unsigned)n_tok, 256, 0, (hipStream_t)stream>>>(d_x, (int)cols, sc);
-    quantize_f16_kernel<<<(unsigned)((lanes + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+    (void)lanes;
+    quantize_f16_rows_kernel<<<(unsigned)n_tok, 256, 0, (hipStream_t)stream>>>(
         d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)act_lda(cols), minp, fmt == DQ_FMT_Q6_K ? 1 : 2, sc, inv);
     return dq_launch_status();
 }
