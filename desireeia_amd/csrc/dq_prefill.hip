@@ -75,8 +75,12 @@ __device__ __forceinline__ int vcol_group(int g) {  // g = a / 4
     return (g & 4) | ((g & 1) << 1) | ((g >> 1) & 1);
 }
 
+// Two waves per SIMD for HD <= 128 (the register budget fits without spills:
+// the conversion and softmax VALU work of one workgroup overlaps the other's
+// MFMAs); HD = 256 needs one.
 template <int HD, bool SPLIT>
-__global__ __launch_bounds__(NT) void attn_prefill_kernel(PrefillArgs A) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(HD <= 128 ? 2 : 1, 2))) void attn_prefill_kernel(
+    PrefillArgs A) {
     constexpr int NB = HD / 32;          // Q8_0 blocks per row
     constexpr int RB = NB * DQ_SZ_Q8_0;  // row bytes
     constexpr int RBW = RB / 4;          // row dwords
