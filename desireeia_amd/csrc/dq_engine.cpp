@@ -474,14 +474,16 @@ int matmul_q8_0_cuda(const uint8_t* q8_data, size_t rows, size_t cols, const flo
 
 int matmul_kquant_cuda_batch(int format, const void* d_w, size_t rows, size_t cols, const float* x, size_t n_tok,
                              float* y) {
-    if (format != DQ_FMT_Q4_K && format != DQ_FMT_Q6_K) return DQ_ERR_NOT_SUPPORTED;
+    if (format != DQ_FMT_Q4_K && format != DQ_FMT_Q6_K && format != DQ_FMT_Q8_0 && format != DQ_FMT_Q4_0)
+        return DQ_ERR_NOT_SUPPORTED;
     if (!d_w || rows == 0 || n_tok == 0 || cols == 0 || cols % 256 || !gemv_shape_ok(format, rows, cols))
         return DQ_ERR_NOT_SUPPORTED;
     if (rows > (1u << 30) || n_tok > (1u << 20)) return DQ_ERR_NOT_SUPPORTED;
     if (!x || !y) return DQ_ERR_INVALID_ARG;
-    if (n_tok < 4) {
-        // matmul_q4_k_batch / matmul_q6_k_batch below the i8_gemm threshold
-        // (core/matmul.cpp:2090-2125): the single-column GEMV per token
+    // matmul_<fmt>_batch take the i8_gemm path from 4 tokens (Q8_0: from 2,
+    // core/matmul.cpp:848-860, 2090-2125)
+    if (n_tok < (format == DQ_FMT_Q8_0 ? 2u : 4u)) {
+        // below the i8_gemm threshold: the single-column GEMV per token
         for (size_t t = 0; t < n_tok; ++t) {
             const HostJob j = {format, d_w, rows, y + t * rows};
             const int rc = run_host_jobs(&j, 1, cols, x + t * cols);

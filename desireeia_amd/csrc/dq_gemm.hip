@@ -43,7 +43,12 @@ constexpr int BK = 64;  // K per step
 template <int WM>
 constexpr int bm_of() { return 64 * WM; }
 
-enum BKind { B_Q4K = 0, B_Q6K = 1 };
+enum BKind { B_Q4K = 0, B_Q6K = 1, B_Q80 = 2, B_Q40 = 3 };
+
+template <int FMT>
+constexpr int kind_of() {
+    return FMT == DQ_FMT_Q4_K ? B_Q4K : FMT == DQ_FMT_Q6_K ? B_Q6K : FMT == DQ_FMT_Q8_0 ? B_Q80 : B_Q40;
+}
 
 // ------------------------------------------------------------ LDS layout --
 // Ring of NS stages, each holding one K step of both operands:
@@ -54,6 +59,8 @@ enum BKind { B_Q4K = 0, B_Q6K = 1 };
 //   B: the raw bytes of the weight tile, format specific:
 //      Q4_K: P0[BN][16] P1[BN][16] H[BN][16]    (qs sub-planes, block header)
 //      Q6_K: QA[BN][16] QB[BN][16] QH[BN][16] S[BN][4] D[BN][4] (fp16 in the low half)
+//      Q8_0: P0..P3[BN][16] D[BN][4] (the item's two fp16 block scales)
+//      Q4_0: P0 P1[BN][16] D[BN][4]
 // Every stage is filled by global_load_lds (direct global -> LDS DMA, 16, 4 or
 // 2 bytes per lane; lane i of a wave writes at base + i*16 for 16-byte loads and
 // at base + i*4 for the dword and sub-dword forms). Three stages: two steps'
@@ -65,7 +72,7 @@ struct Ring {
     static constexpr int A_BYTES = BM * BK * 2;
     static constexpr int MIN_BYTES = KIND == B_Q4K ? BM * 16 : 0;
     static constexpr int B_OFF = A_BYTES + MIN_BYTES;
-    static constexpr int B_BYTES = BN * 56;  // Q4_K 48 bytes per row, Q6_K 56
+    static constexpr int B_BYTES = BN * (KIND == B_Q80 ? 68 : 56);  // Q4_K 48, Q6_K 56, Q8_0 68, Q4_0 36 per row
     static constexpr int STAGE = B_OFF + B_BYTES;
     static constexpr int BYTES = NS * STAGE;
 };
@@ -114,7 +121,8 @@ struct GemmArgs {
 template <int BN, int KIND, int WM>
 constexpr int stage_loads() {
     constexpr int NW = BN / 32;
-    return bm_of<WM>() * 8 / 64 / NW + 3;  // A, then Q4_K: sums, P0/P1, H; Q6_K: QA/QB, QH or S, D
+    // A, then Q4_K: sums, P0/P1, H; Q6_K: QA/QB, QH or S, D; Q8_0: two plane blocks, D; Q4_0: P0/P1, D
+    return bm_of<WM>() * 8 / 64 / NW + (KIND == B_Q40 ? 2 : 3);
 }
 
 template <int BN, int KIND, int WM>
@@ -181,6 +189,21 @@ __device__ __forceinline__ void issue_stage(const GemmArgs& g, uint8_t* ring, in
             lds_dma<2>(g.w + g.L.d_off + r * g.L.d_row + 2 * (size_t)(st >> 2),
                        bb + 3 * BN * 16 + BN * 4 + blk * 64 * 4);
         }
+    } else {  // Q8_0 (4 sub-planes) and Q4_0 (2): one item per row and step
+        constexpr int NP = KIND == B_Q80 ? 4 : 2;
+#pragma unroll
+        for (int q = 0; q < NP / 2; ++q) {  // NP * HB plane blocks = NP/2 per wave
+            const int blk = wave + q * NW;
+            const int region = blk / HB, n = (blk % HB) * 64 + lane;
+            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
+            lds_dma<16>(g.w + g.L.q_off + (size_t)region * g.L.p_stride + r * g.L.q_row + 16 * (size_t)st,
+                        bb + blk * 64 * 16);
+        }
+        {   // D: the item's two fp16 scales, HB blocks of dwords (waves w and w + HB: block w % HB)
+            const int blk = wave % HB, n = blk * 64 + lane;
+            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
+            lds_dma<4>(g.w + g.L.d_off + r * g.L.d_row + 4 * (size_t)st, bb + NP * BN * 16 + blk * 64 * 4);
+        }
     }
 }
 
@@ -190,8 +213,8 @@ __device__ __forceinline__ const h8& lds_h8(const uint8_t* p) { return *reinterp
 // each of its two 32-row blocks j, lane half h's 8 bytes of the two quant
 // sub-planes (Q4_K: P0/P1; Q6_K: QA/QB plus QH) and the row's scales.
 struct BRaw {
-    dq_u32x2 q0[2], q1[2], q2[2];  // Q4_K: P0, P1 (q2 unused); Q6_K: QA, QB, QH
-    dq_u32x4 hd[2];                // Q4_K: super-block header; Q6_K: .x = 4 int8 scales, .y = d (low half)
+    dq_u32x2 q0[2], q1[2], q2[2], q3[2];  // Q4_K: P0, P1; Q6_K: QA, QB, QH; Q8_0: P0..P3; Q4_0: P0, P1
+    dq_u32x4 hd[2];  // Q4_K: super-block header; Q6_K: .x = 4 int8 scales, .y = d (low half); Q8_0/Q4_0: .x = 2 d
 };
 
 template <int BN, int KIND>
@@ -204,6 +227,12 @@ __device__ __forceinline__ void b_raw(const uint8_t* bb, int wn, int lane, BRaw&
         r.q1[j] = *reinterpret_cast<const dq_u32x2*>(bb + BN * 16 + n * 16 + 8 * h);
         if constexpr (KIND == B_Q4K) {
             r.hd[j] = *reinterpret_cast<const dq_u32x4*>(bb + 2 * BN * 16 + n * 16);
+        } else if constexpr (KIND == B_Q80) {
+            r.q2[j] = *reinterpret_cast<const dq_u32x2*>(bb + 2 * BN * 16 + n * 16 + 8 * h);
+            r.q3[j] = *reinterpret_cast<const dq_u32x2*>(bb + 3 * BN * 16 + n * 16 + 8 * h);
+            r.hd[j].x = *reinterpret_cast<const uint32_t*>(bb + 4 * BN * 16 + n * 4);
+        } else if constexpr (KIND == B_Q40) {
+            r.hd[j].x = *reinterpret_cast<const uint32_t*>(bb + 2 * BN * 16 + n * 4);
         } else {
             r.q2[j] = *reinterpret_cast<const dq_u32x2*>(bb + 2 * BN * 16 + n * 16 + 8 * h);
             r.hd[j].x = *reinterpret_cast<const uint32_t*>(bb + 3 * BN * 16 + n * 4);
@@ -239,6 +268,13 @@ __device__ __forceinline__ void b_scales(const BRaw& r, int G, BScale& S) {
             // -64a is exact while |a| < 1024 (64*a stays below the fp16 maximum)
             S.s[j][2] = h2{(_Float16)(-64.0f) * a0, (_Float16)(-64.0f) * a0};
             S.s[j][3] = h2{(_Float16)(-64.0f) * a1, (_Float16)(-64.0f) * a1};
+        } else if constexpr (KIND == B_Q80 || KIND == B_Q40) {
+            // K slices 0, 1: the item's first block (scale d0), 2, 3: the second
+            const uint32_t dd = r.hd[j].x;
+            const _Float16 d0 = __builtin_bit_cast(_Float16, (uint16_t)(dd & 0xFFFF));
+            const _Float16 d1 = __builtin_bit_cast(_Float16, (uint16_t)(dd >> 16));
+            S.s[j][0] = S.s[j][1] = h2{d0, d0};
+            S.s[j][2] = S.s[j][3] = h2{d1, d1};
         } else {
             const uint32_t sc = r.hd[j].x;
             const float d = dq_h2f((uint16_t)(r.hd[j].y & 0xFFFF));
@@ -276,6 +312,21 @@ __device__ __forceinline__ void b_frag(const BRaw& r, const BScale& S, h8 (&bf)[
             t[1] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, e1), S.s[j][1], S.s[j][3]));
             t[2] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, e2), S.s[j][0], S.s[j][2]));
             t[3] = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(h2, e3), S.s[j][1], S.s[j][3]));
+        } else if constexpr (KIND == B_Q80) {
+            // slice KK = sub-plane KK, bytes 8h..8h+7: q ^ 0x80 = q + 128 under
+            // the exponent of 1024, minus 1152 = q exactly, times d (one rounding)
+            const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+            const dq_u32x2 src = KK == 0 ? r.q0[j] : KK == 1 ? r.q1[j] : KK == 2 ? r.q2[j] : r.q3[j];
+            bytes_to_h2(src.x ^ 0x80808080u, bias, S.s[j][KK], &t[0]);
+            bytes_to_h2(src.y ^ 0x80808080u, bias, S.s[j][KK], &t[2]);
+        } else if constexpr (KIND == B_Q40) {
+            // slices 0, 1: sub-plane 0 (block 2i) low, high nibbles; 2, 3: sub-plane 1;
+            // the nibble q under the exponent of 1024, minus 1032 = q - 8, times d
+            const h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+            const dq_u32x2 src = KK < 2 ? r.q0[j] : r.q1[j];
+            const int sh = (KK & 1) ? 4 : 0;
+            bytes_to_h2((src.x >> sh) & 0x0F0F0F0Fu, bias, S.s[j][KK], &t[0]);
+            bytes_to_h2((src.y >> sh) & 0x0F0F0F0Fu, bias, S.s[j][KK], &t[2]);
         } else {
             const h2 bias = {(_Float16)1056.0f, (_Float16)1056.0f};  // 1024 + 32
             const dq_u32x2 lo = (KK & 1) ? r.q1[j] : r.q0[j];
@@ -403,7 +454,7 @@ __device__ __forceinline__ void tile_of(int id, int mb, int nb, int* m_blk, int*
 template <int FMT, int BN, int WM>
 __global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(
     GemmArgs g, float* __restrict__ y, int steps, int steps_per_split, int atomic_out) {
-    constexpr int KIND = FMT == DQ_FMT_Q4_K ? B_Q4K : B_Q6K;
+    constexpr int KIND = kind_of<FMT>();
     constexpr int BM = bm_of<WM>();
     __shared__ __align__(16) uint8_t ring[Ring<BN, KIND, WM>::BYTES];
     const int tid = threadIdx.x;
@@ -596,7 +647,8 @@ static size_t inv_off(int fmt, size_t cols, size_t n_tok) {
 extern "C" int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t n_tok, size_t* bytes) {
     (void)rows;
     if (!bytes) return DQ_ERR_INVALID_ARG;
-    if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K) return DQ_ERR_NOT_SUPPORTED;
+    if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K && fmt != DQ_FMT_Q8_0 && fmt != DQ_FMT_Q4_0)
+        return DQ_ERR_NOT_SUPPORTED;
     if (cols % 256) return DQ_ERR_NOT_SUPPORTED;
     *bytes = inv_off(fmt, cols, n_tok) + dq_align256(n_tok * 4);
     return DQ_OK;
@@ -604,7 +656,8 @@ extern "C" int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t
 
 extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_out,
                                    void* stream) {
-    if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K) return DQ_ERR_NOT_SUPPORTED;
+    if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K && fmt != DQ_FMT_Q8_0 && fmt != DQ_FMT_Q4_0)
+        return DQ_ERR_NOT_SUPPORTED;
     if (cols % 256 || cols > (1u << 24) || n_tok > (1u << 20)) return DQ_ERR_NOT_SUPPORTED;
     if (!d_x || !d_out) return DQ_ERR_INVALID_ARG;
     if (n_tok == 0) return DQ_OK;
@@ -617,7 +670,8 @@ extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_
     float* inv = (float*)(base + inv_off(fmt, cols, n_tok));
     (void)lanes;
     quantize_f16_rows_kernel<<<(unsigned)n_tok, 256, 0, (hipStream_t)stream>>>(
-        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)act_lda(cols), minp, fmt == DQ_FMT_Q6_K ? 1 : 2, sc, inv);
+        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)act_lda(cols), minp,
+        fmt == DQ_FMT_Q6_K ? 1 : (fmt == DQ_FMT_Q4_K ? 2 : 0), sc, inv);
     return dq_launch_status();
 }
 
@@ -669,8 +723,9 @@ static GemmPlan plan_gemm(size_t rows, size_t n_tok, int steps) {
 extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work,
                               size_t n_tok, float* d_y, void* stream) {
     DqLayout L;
-    if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K) return DQ_ERR_NOT_SUPPORTED;
-    if (!dq_layout(fmt, rows, cols, &L)) return DQ_ERR_NOT_SUPPORTED;
+    if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K && fmt != DQ_FMT_Q8_0 && fmt != DQ_FMT_Q4_0)
+        return DQ_ERR_NOT_SUPPORTED;
+    if (!dq_layout(fmt, rows, cols, &L) || cols % 256) return DQ_ERR_NOT_SUPPORTED;
     if (rows > (1u << 30) || n_tok > (1u << 20)) return DQ_ERR_NOT_SUPPORTED;
     if (rows == 0 || n_tok == 0) return DQ_OK;
     if (!d_w || !d_work || !d_y) return DQ_ERR_INVALID_ARG;
@@ -692,6 +747,14 @@ extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols
         if (pl.wm == 4) return launch_gemm<DQ_FMT_Q4_K, 256, 4>(g, rows, n_tok, steps, pl.split, d_y, s);
         if (pl.bn == 256) return launch_gemm<DQ_FMT_Q4_K, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
         return launch_gemm<DQ_FMT_Q4_K, 128, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
+    }
+    if (fmt == DQ_FMT_Q8_0) {
+        if (pl.bn == 256) return launch_gemm<DQ_FMT_Q8_0, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
+        return launch_gemm<DQ_FMT_Q8_0, 128, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
+    }
+    if (fmt == DQ_FMT_Q4_0) {
+        if (pl.bn == 256) return launch_gemm<DQ_FMT_Q4_0, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
+        return launch_gemm<DQ_FMT_Q4_0, 128, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
     }
     if (pl.wm == 4) return launch_gemm<DQ_FMT_Q6_K, 256, 4>(g, rows, n_tok, steps, pl.split, d_y, s);
     if (pl.bn == 256) return launch_gemm<DQ_FMT_Q6_K, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);

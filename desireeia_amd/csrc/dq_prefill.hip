@@ -516,7 +516,7 @@ __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float* __restr
 // GEMM activation workspace per K-quant format (sized for the widest input).
 struct PrefillWs {
     float *xn, *q, *k, *v, *attn, *h, *gate, *up, *down;
-    uint8_t* gw[2];  // Q4_K, Q6_K
+    uint8_t* gw[3];  // activation layouts: Q4_K, Q6_K, natural order (Q8_0 / Q4_0)
     uint8_t* aw;     // attention key-split records
     size_t gw_bytes, aw_bytes, total;
 };
@@ -524,7 +524,7 @@ struct PrefillWs {
 bool prefill_layer_ok(const dq_layer_t* L) {
     const int f[7] = {L->fmt_q, L->fmt_k, L->fmt_v, L->fmt_o, L->fmt_gate, L->fmt_up, L->fmt_down};
     for (int i = 0; i < 7; ++i)
-        if (f[i] != DQ_FMT_Q4_K && f[i] != DQ_FMT_Q6_K) return false;
+        if (f[i] != DQ_FMT_Q4_K && f[i] != DQ_FMT_Q6_K && f[i] != DQ_FMT_Q8_0 && f[i] != DQ_FMT_Q4_0) return false;
     if (L->head_dim != 128 || L->n_head_kv == 0 || L->n_head % L->n_head_kv) return false;
     if (L->n_embd % 256 || L->n_ff % 256 || ((size_t)L->n_head * L->head_dim) % 256) return false;
     if (L->n_rot == 0 || L->n_rot > L->head_dim || L->n_rot % 2) return false;
@@ -552,13 +552,14 @@ PrefillWs prefill_carve(const dq_layer_t* L, uint32_t n_tok, uint8_t* base) {
     w.down = take(T * E);
     size_t gb = 0;
     const size_t cols[3] = {E, QD, F};
-    for (int f = 0; f < 2; ++f)
+    const int fmts[3] = {DQ_FMT_Q4_K, DQ_FMT_Q6_K, DQ_FMT_Q8_0};
+    for (int f = 0; f < 3; ++f)
         for (size_t c : cols) {
             size_t b = 0;
-            if (dq_gemm_workspace_bytes(f == 0 ? DQ_FMT_Q4_K : DQ_FMT_Q6_K, 1, c, T, &b) == DQ_OK && b > gb) gb = b;
+            if (dq_gemm_workspace_bytes(fmts[f], 1, c, T, &b) == DQ_OK && b > gb) gb = b;
         }
     w.gw_bytes = dq_align256(gb);
-    for (int f = 0; f < 2; ++f) {
+    for (int f = 0; f < 3; ++f) {
         w.gw[f] = base ? base + off : nullptr;
         off += w.gw_bytes;
     }
@@ -741,14 +742,17 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
     const hipStream_t s = (hipStream_t)stream;
     const size_t E = L->n_embd, QD = (size_t)L->n_head * L->head_dim, KVD = (size_t)L->n_head_kv * L->head_dim;
     const size_t F = L->n_ff, T = n_tok;
-    auto gw = [&](int fmt) { return w.gw[fmt == DQ_FMT_Q4_K ? 0 : 1]; };
+    // the activation layout a format's GEMM reads: Q4_K and Q6_K their own,
+    // Q8_0 and Q4_0 the same natural order
+    auto cls = [](int fmt) { return fmt == DQ_FMT_Q4_K ? 0 : (fmt == DQ_FMT_Q6_K ? 1 : 2); };
+    auto gw = [&](int fmt) { return w.gw[cls(fmt)]; };
     // products of one input x [T][cols] with up to three matrices: one
     // activation quantization per distinct format
     auto products = [&](const float* x, size_t cols, int n, const int* fmt, const void* const* wm, const size_t* rows,
                         float* const* y) -> int {
-        bool done[2] = {false, false};
+        bool done[3] = {false, false, false};
         for (int j = 0; j < n; ++j) {
-            const int fi = fmt[j] == DQ_FMT_Q4_K ? 0 : 1;
+            const int fi = cls(fmt[j]);
             if (!done[fi]) {
                 DQP_TRY(dq_quantize_act_f16(fmt[j], x, cols, T, gw(fmt[j]), stream));
                 done[fi] = true;

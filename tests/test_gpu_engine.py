@@ -138,27 +138,30 @@ def test_same_x_and_q8_group(lib, orc):
 
 
 @pytest.mark.parametrize("qtype,rows,cols,n_tok", [(Q4_K, 14336, 4096, 64), (Q6_K, 4096, 14336, 16),
-                                                   (Q4_K, 512, 1024, 3)])
+                                                   (Q4_K, 512, 1024, 3), (Q8_0, 4096, 4096, 32), (Q8_0, 512, 1024, 2),
+                                                   (Q4_0, 4096, 14336, 8), (Q4_0, 512, 1024, 3)])
 def test_batch(lib, orc, qtype, rows, cols, n_tok):
     print(f"batch type={qtype} {rows}x{cols} n_tok={n_tok}", flush=True)
     m = Mat(lib, qtype, rows, cols, seed=7)
     x = synth.gen_act((n_tok, cols), seed=8)
     y = np.full((n_tok, rows), np.nan, np.float32)
     assert lib.matmul_kquant_cuda_batch(m.fmt, m.qs, rows, cols, P(x), n_tok, P(y)) == OK
-    if n_tok < 4:
+    gemm_from = 2 if qtype == Q8_0 else 4  # matmul_q8_0_batch takes i8_gemm from 2 tokens
+    if n_tok < gemm_from:
         # below the i8_gemm threshold: exactly the per-token GEMVs
         for t in range(n_tok):
             assert np.array_equal(y[t], resident(lib, m, np.ascontiguousarray(x[t])))
     want = orc.gemm(qtype, m.w, rows, cols, x, n_tok)
-    assert rel(y, want) <= (4e-3 if n_tok >= 4 else TOL)
+    assert rel(y, want) <= (4e-3 if n_tok >= gemm_from else TOL)
     m.free()
 
 
 def test_batch_not_supported(lib):
-    m = Mat(lib, Q4_0, 64, 256, seed=1)
-    x = synth.gen_act((8, 256), seed=2)
+    # K not a multiple of 256 (the prefill GEMM's step): NOT_SUPPORTED, y untouched
+    m = Mat(lib, Q4_0, 64, 320, seed=1)
+    x = synth.gen_act((8, 320), seed=2)
     y = np.full((8, 64), 5.0, np.float32)
-    assert lib.matmul_kquant_cuda_batch(m.fmt, m.qs, 64, 256, P(x), 8, P(y)) == NOT_SUPPORTED
+    assert lib.matmul_kquant_cuda_batch(m.fmt, m.qs, 64, 320, P(x), 8, P(y)) == NOT_SUPPORTED
     assert np.all(y == 5.0)
     m.free()
 
@@ -521,7 +524,7 @@ def test_layer_forward_batch(lib, orc):
     e = rel(out, want)
     print(f"engine two layers vs oracle: {e:.3e}", flush=True)
     assert e <= 3e-2
-    # features outside the plain layer, or Q8_0 matrices: NOT_SUPPORTED, out untouched
+    # features outside the plain layer: NOT_SUPPORTED, out untouched
     keep = out.copy()
     mats, an, fn, _ = layers[0]
     bias = np.zeros(n_head * hd, np.float32)
@@ -530,6 +533,7 @@ def test_layer_forward_batch(lib, orc):
     assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == NOT_SUPPORTED
     q8 = make_layer(lib, orc, E, n_head, n_kv, F, (Q8_0,) * 7, 90)
     A = batch_args(*q8[:3], E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, None, None, 1, 1, 1)
+    A.act_gelu = 1  # a GELU FFN
     assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == NOT_SUPPORTED
     assert lib.cuda_layer_forward_batch(None) == NOT_SUPPORTED
     assert np.array_equal(out, keep)

@@ -19,6 +19,8 @@ def rel(a, b):
 @pytest.mark.parametrize("qtype,rows,cols,n_tok", [
     (synth.Q4_K, 14336, 4096, 512),   # config 3 up/gate
     (synth.Q6_K, 4096, 14336, 512),   # config 3 down
+    (synth.Q8_0, 14336, 4096, 512),   # the same shape in the formats of Q8_0 / Q4_0 models
+    (synth.Q4_0, 4096, 14336, 512),
 ])
 def test_gemm_config3(gpu, orc, qtype, rows, cols, n_tok):
     print(f"gemm type={qtype} rows={rows} cols={cols} n_tok={n_tok}", flush=True)
@@ -40,6 +42,10 @@ def test_gemm_config3(gpu, orc, qtype, rows, cols, n_tok):
     (synth.Q6_K, 100, 768, 7),        # a single partial M tile
     (synth.Q4_K, 64, 256, 4),         # K = one super-block, min columns padded
     (synth.Q6_K, 300, 2048, 33),
+    (synth.Q8_0, 300, 1024, 33),      # Q8_0: per-32 scales, four sub-planes
+    (synth.Q8_0, 129, 512, 2),        # Q8_0 takes the i8_gemm path from 2 tokens
+    (synth.Q4_0, 129, 512, 130),      # Q4_0: nibbles - 8
+    (synth.Q4_0, 64, 256, 4),
 ])
 def test_gemm_ragged(gpu, orc, qtype, rows, cols, n_tok):
     print(f"gemm ragged type={qtype} rows={rows} cols={cols} n_tok={n_tok}", flush=True)
@@ -66,8 +72,9 @@ def test_gemm_unsupported(gpu):
     lib = _lib.load()
     import ctypes
     n = ctypes.c_size_t(0)
-    assert lib.dq_gemm_workspace_bytes(synth.FMT_Q8_0, 64, 4096, 16, ctypes.byref(n)) == -2
+    assert lib.dq_gemm_workspace_bytes(synth.FMT_Q8_0, 64, 320, 16, ctypes.byref(n)) == -2  # K % 256
     assert lib.dq_gemm_workspace_bytes(synth.FMT_Q4_K, 64, 100, 16, ctypes.byref(n)) == -2
+    assert lib.dq_gemm_workspace_bytes(99, 64, 4096, 16, ctypes.byref(n)) == -2  # unknown format
 
 
 @pytest.mark.parametrize("scale", [3000.0, 1e-4])

@@ -23,13 +23,15 @@ def rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0)):
+def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None):
     from oracle.oracle import LayerArgs
     hd = 128
     qd, kvd = n_head * hd, n_kv * hd
     # Q4_K_M mix: Q4_K everywhere but attn_v and ffn_down (Q6_K)
     shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
               "gate": (Q4K, F, E), "up": (Q4K, F, E), "down": (Q6K, E, F)}
+    for nm, qt in (types or {}).items():
+        shapes[nm] = (qt,) + shapes[nm][1:]
     gg = {nm: (qt, synth.gen_weights(qt, r, c, seed=seed + i)) for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
     rng = np.random.default_rng(seed)
     attn_norm = (norm_scale[0] * (1 + 0.02 * rng.standard_normal(E))).astype(np.float32)
@@ -47,7 +49,8 @@ def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1
         vc[:n_prior * pb] = orc.kv_quantize_row(rng.standard_normal(n_prior * kvd).astype(np.float32))
     layer.cache.k.copy_(torch.from_numpy(kc))
     layer.cache.v.copy_(torch.from_numpy(vc))
-    args = LayerArgs(E, n_head, n_kv, hd, F, 1e-5, 500000.0, Q4K, Q4K, Q6K, Q4K, Q4K, Q4K, Q6K)
+    args = LayerArgs(E, n_head, n_kv, hd, F, 1e-5, 500000.0,
+                     *[shapes[nm][0] for nm in ("q", "k", "v", "o", "gate", "up", "down")])
     keep = {nm: np.ascontiguousarray(w) for nm, (qt, w) in gg.items()}
     keep["attn_norm"], keep["ffn_norm"] = attn_norm, ffn_norm
     for nm in ("q", "k", "v", "o", "gate", "up", "down"):

@@ -97,16 +97,22 @@ def gpu_fns(gpu, layer, kc, vc, pos0, T):
     return gemm, attention
 
 
-@pytest.mark.parametrize("E,n_head,n_kv,F,pos0,n_tok", [
-    (4096, 32, 8, 14336, 1000, 16),  # config-4 layer shape after 1000 cached tokens
-    (512, 8, 2, 1536, 0, 40),        # prompt from position 0
-    (512, 4, 2, 1024, 70, 130),      # two attention query blocks, GEMM M tail
+Q80_ALL = {nm: synth.Q8_0 for nm in ("q", "k", "v", "o", "gate", "up", "down")}
+Q40_FFN = {"gate": synth.Q4_0, "up": synth.Q4_0, "v": synth.Q8_0}
+
+
+@pytest.mark.parametrize("E,n_head,n_kv,F,pos0,n_tok,types", [
+    (4096, 32, 8, 14336, 1000, 16, None),  # config-4 layer shape after 1000 cached tokens
+    (512, 8, 2, 1536, 0, 40, None),        # prompt from position 0
+    (512, 4, 2, 1024, 70, 130, None),      # two attention query blocks, GEMM M tail
+    (512, 8, 2, 1536, 30, 48, Q80_ALL),    # a Q8_0 model
+    (512, 8, 2, 1536, 10, 40, Q40_FFN),    # Q4_0 FFN, Q8_0 V, Q4_K/Q6_K elsewhere
 ])
-def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok):
-    print(f"layer_prefill E={E} heads={n_head}/{n_kv} F={F} pos0={pos0} n_tok={n_tok}", flush=True)
+def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, types):
+    print(f"layer_prefill E={E} heads={n_head}/{n_kv} F={F} pos0={pos0} n_tok={n_tok} types={types}", flush=True)
     n_ctx = pos0 + n_tok + 2
     layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos0, seed=E + pos0 + n_tok,
-                                           norm_scale=conditioned(E))
+                                           norm_scale=conditioned(E), types=types)
     x = np.random.default_rng(n_tok).standard_normal((n_tok, E)).astype(np.float32)
     og, oa = oracle_fns(layer, keep, orc, kc, vc, pos0, n_tok)
     gg, ga = gpu_fns(gpu, layer, kc, vc, pos0, n_tok)
