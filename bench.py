@@ -461,7 +461,8 @@ def main():
         torch.cuda.synchronize()
         log(f"copy: {args.steps} x {src.numel()} bytes")
         return
-    gemm_shapes = {"gemm_q4k": (synth.Q4_K, 14336, 4096, 512), "gemm_q6k": (synth.Q6_K, 4096, 14336, 512)}
+    gemm_shapes = {"gemm_q4k": (synth.Q4_K, 14336, 4096, 512), "gemm_q6k": (synth.Q6_K, 4096, 14336, 512),
+                   "gemm_q80": (synth.Q8_0, 14336, 4096, 512)}
     if args.only in gemm_shapes:
         qt, r, c, t = gemm_shapes[args.only]
         g = GemmCase(qt, r, c, t, 21, dev)

@@ -124,16 +124,18 @@ int dq_gemv_group(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t
 int dq_gemv_f32(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, float* d_y, void* stream);
 int dq_gemv_group_f32(const dq_gemv_job_t* jobs, size_t n, size_t cols, const float* d_x, void* stream);
 
-/* Prefill GEMM y[n_tok][rows] = x[n_tok][cols] W^T for Q4_K and Q6_K, with the
- * semantics of matmul_q4_k_batch / matmul_q6_k_batch for n_tok >= 4 (the
- * i8_gemm path, core/matmul.cpp:2090-2125 -> :806-845): per-32 activation
- * quantization, exact float block sums for the Q4_K min term. Runs on fp16
+/* Prefill GEMM y[n_tok][rows] = x[n_tok][cols] W^T for Q4_K, Q6_K, Q8_0 and
+ * Q4_0 (cols % 256 == 0), with the semantics of matmul_<fmt>_batch on the
+ * i8_gemm path (Q4_K/Q6_K/Q4_0 from 4 tokens, Q8_0 from 2; core/matmul.cpp
+ * :848-860, 2090-2125 -> :806-845): per-32 activation quantization, exact
+ * float block sums for the Q4_K min term. Runs on fp16
  * MFMA over pre-scaled operands (result within ~3e-4 relative of the
  * reference); each token's operand row carries a power-of-two range scale
  * (undone exactly on the output), so any finite activation magnitude stays
  * inside fp16. `d_work` (dq_gemm_workspace_bytes() bytes) holds the quantized
  * activations, for Q4_K their per-32 block sums (the min-term input, tokens
- * contiguous per super-block), and their row scales. Other formats: -2. */
+ * contiguous per super-block), and their row scales. Other formats and
+ * cols % 256 != 0: -2. */
 int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t n_tok, size_t* bytes);
 int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,
             float* d_y, void* d_work, size_t work_bytes, void* stream);
@@ -281,8 +283,8 @@ int dq_layer_decode(const dq_layer_t* layer, const float* d_x, float* d_x_out, c
  * projection, residual and FFN norm, :3600-3624 gated SiLU FFN and residual)
  * that cuda_layer_forward_batch (core/engine.h:754-797, backend_cuda.cu:8466)
  * runs on the GPU. Every product is the prefill GEMM (dq_gemm: the i8 GEMM
- * semantics of matmul_q4_k_batch / matmul_q6_k_batch), so all seven matrices
- * must be Q4_K or Q6_K; attention is dq_attn_prefill_q8 (n_swa > 0: sliding
+ * semantics of matmul_<fmt>_batch), each matrix any of Q4_K, Q6_K, Q8_0 and
+ * Q4_0; attention is dq_attn_prefill_q8 (n_swa > 0: sliding
  * window). d_x, d_x_out: [n_tok][n_embd] device rows (may alias); d_rope:
  * [n_tok][n_rot] cos/sin tables (dq_rope_cache(pos0 + t)) or NULL. The K/V
  * rows of the chunk are written into the caches. Shapes as dq_layer_decode
@@ -541,9 +543,9 @@ int matmul_q8_0_cuda_resident_group(const CudaQ80Job* jobs, size_t n, size_t col
 int matmul_q8_0_cuda(const uint8_t* q8_data, size_t rows, size_t cols, const float* x, float* y);
 
 /* Batched (prefill) product y[n_tok][rows] = x[n_tok][cols] W^T, core/engine.h
- * :543: Q4_K / Q6_K with the semantics of matmul_q4_k_batch /
- * matmul_q6_k_batch (i8_gemm for n_tok >= 4, per-token GEMVs below). Other
- * formats: NOT_SUPPORTED. */
+ * :543: Q4_K / Q6_K / Q8_0 / Q4_0 with the semantics of matmul_<fmt>_batch
+ * (i8_gemm from 4 tokens, Q8_0 from 2; per-token GEMVs below). cols % 256 != 0
+ * or other formats: NOT_SUPPORTED. */
 int matmul_kquant_cuda_batch(int format, const void* d_w, size_t rows, size_t cols, const float* x, size_t n_tok,
                              float* y);
 
@@ -594,7 +596,7 @@ int cuda_layer_forward(const CudaLayerArgs* args);
  *   last (rows from x_out_row0 on), which also copies every K/V row the
  *   prompt wrote into host_kcache / host_vcache and synchronises once. RoPE
  *   tables: rope_caches uploaded when upload_rope into slot rope_slot (0-3);
- *   NULL = no RoPE. Matrices must be Q4_K / Q6_K uploads; biases, QK-norm,
+ *   NULL = no RoPE. Matrices: uploads of this library; biases, QK-norm,
  *   sandwich norms, the attention gate, GELU and head_dim != 128:
  *   NOT_SUPPORTED, before any device work.
  * cuda_prefill_chunk_tokens: tokens per chunk, 8 per CU within [1024, 4096]. */
