@@ -421,10 +421,63 @@ def cpu_baseline_q4k(budget_s=12.0):
         best = min(best, dt)
         total += dt
         calls += 1
-    return {"value": round(nbytes / best / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
-            "sample": f"Q4_K GEMV 14336x4096 (matmul_q4_k incl. its per-256 activation quantization), "
-                      f"8 distinct weight copies (264 MB), best of {calls} calls over {budget_s:.0f} s"
-                      + ("" if kind == "reference" else "; rows 0..511 timed and scaled to 14336")}
+    out = {"value": round(nbytes / best / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
+           "sample": f"Q4_K GEMV 14336x4096 (matmul_q4_k incl. its per-256 activation quantization), "
+                     f"8 distinct weight copies (264 MB), best of {calls} calls over {budget_s:.0f} s"
+                     + ("" if kind == "reference" else "; rows 0..511 timed and scaled to 14336")}
+    if kind == "reference":
+        out["rows"] = cpu_rows(r)
+    return out
+
+
+def _best_of(fn, budget_s, min_calls=2):
+    t_end = time.time() + budget_s
+    best, calls = 1e30, 0
+    while time.time() < t_end or calls < min_calls:
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+        calls += 1
+    return best, calls
+
+
+def cpu_rows(r, budget_s=3.0):
+    """The reference's CPU path for the other measured rows, on the same
+    shapes as their GPU lines: prefill GEMM (matmul_batch, Q4_K 14336x4096,
+    512 tokens), prefill attention (attention_prefill_q8, 512 tokens after
+    3584 cached positions, 32/8 heads of 128) and the output-head GEMV
+    (matmul_q6_k 128256x4096). Best of repeated calls over budget_s each."""
+    from desireeia_amd import synth
+    from oracle import oracle as orc
+    rows = {}
+    R, C, T = 14336, 4096, 512
+    w = synth.gen_weights(synth.Q4_K, R, C, seed=21)
+    x = synth.gen_act((T, C), 22)
+    best, calls = _best_of(lambda: r.matmul_batch(synth.Q4_K, w, R, C, x, T), budget_s)
+    rows["gemm_q4k"] = {"TFLOPs": round(2.0 * T * R * C / best / 1e12, 4), "ms": round(best * 1e3, 2),
+                        "sample": f"matmul_batch Q4_K {T}x{C} . {C}x{R}, best of {calls}"}
+    del w, x
+    hd, nkv, nh, pos0, T = 128, 8, 32, 3584, 512
+    rng = np.random.default_rng(9)
+    o = orc.oracle()
+    kc = o.kv_quantize_row(rng.standard_normal((pos0 + T) * nkv * hd).astype(np.float32))
+    vc = o.kv_quantize_row(rng.standard_normal((pos0 + T) * nkv * hd).astype(np.float32))
+    q = rng.standard_normal((T, nh * hd)).astype(np.float32)
+    best, calls = _best_of(lambda: r.attn_prefill(q, kc, vc, T, nh, nkv, hd, pos0), budget_s)
+    keys = T * (pos0 + 1) + T * (T - 1) // 2
+    rows["attn_prefill_512_after_3584"] = {"TFLOPs_alg": round(4.0 * hd * nh * keys / best / 1e12, 4),
+                                           "ms": round(best * 1e3, 2),
+                                           "sample": f"attention_prefill_q8, best of {calls}"}
+    del kc, vc, q
+    R, C = 128256, 4096
+    w = synth.gen_weights(synth.Q6_K, R, C, seed=70)
+    xv = synth.gen_act(C, 71)
+    best, calls = _best_of(lambda: r.matmul(synth.Q6_K, w, R, C, xv), budget_s)
+    rows["head_q6k_128256x4096"] = {"GBps": round(R * synth.row_bytes(synth.Q6_K, C) / best / 1e9, 2),
+                                    "ms": round(best * 1e3, 2), "sample": f"matmul_q6_k, best of {calls}"}
+    for k, v in rows.items():
+        log(f"cpu reference {k}: {v}")
+    return rows
 
 
 def main():

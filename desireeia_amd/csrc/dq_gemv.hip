@@ -24,6 +24,7 @@
 // Semantics follow the reference CPU GEMVs (include/desireeia_hip.h): integer
 // partial sums are exact; only the float summation order differs.
 #include <cstdlib>
+#include <type_traits>
 
 #include "dq_common.h"
 #include "dq_quant.h"
@@ -423,13 +424,13 @@ __global__ __launch_bounds__(256) void gemv_kernel(Jobs J, int items, const int8
 // arrived); xstage_quant then quantizes into LDS while the weights are in
 // flight. Loads are coalesced: round r of wave w (of nw) covers the 256
 // columns c0 + 256*(w + r*nw) + [0, 256), lane l holding the 4 at +4l (one
-// contiguous kilobyte per load instruction). A 32-block is 8 lanes and a
-// 256-block the whole wave, so block maxima and integer sums are lane
-// reductions (DPP within rows, shuffles across rows); max and integer sums
-// do not depend on order, so the integers and scales are bit-exact with the
+// contiguous kilobyte per load instruction). A 32-block is 8 lanes, so block
+// maxima and integer sums are DPP lane reductions; max and integer sums do
+// not depend on order, so the integers and scales are bit-exact with the
 // per-block quantizer (dq_quant_block). Columns past c1 load the last four
 // (valid address) and are not stored; c0, c1 are multiples of 64 (whole
-// 32-blocks of 8 lanes) and, for the per-256 quantizer, of 256.
+// 32-blocks of 8 lanes). Per-32 kind only (Q8_0, Q4_0); the per-256 kind
+// takes xrow_quant.
 template <int ROUNDS>
 struct XStage {
     float4 v[ROUNDS];
@@ -445,10 +446,17 @@ __device__ __forceinline__ void xstage_load(XStage<ROUNDS>& st, const float* __r
     }
 }
 
-__device__ __forceinline__ float max8_lanes(float v) {  // max over the 8 lanes of an aligned group
-    v = fmaxf(v, dq_dpp<0xB1>(v));   // quad_perm [1,0,3,2]
-    v = fmaxf(v, dq_dpp<0x4E>(v));   // quad_perm [2,3,0,1]
-    return fmaxf(v, dq_dpp<0x141>(v));  // row_half_mirror: the other quad of the 8
+// Maxima of |x| are taken on the bit patterns: non-negative floats order as
+// their bits, so an unsigned max equals fmaxf on them (and needs no NaN
+// canonicalization between DPP steps).
+template <int CTRL>
+__device__ __forceinline__ uint32_t umax_dpp(uint32_t v) {
+    return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t max8_lanes(uint32_t v) {  // over the 8 lanes of an aligned group
+    v = umax_dpp<0xB1>(v);          // quad_perm [1,0,3,2]
+    v = umax_dpp<0x4E>(v);          // quad_perm [2,3,0,1]
+    return umax_dpp<0x141>(v);      // row_half_mirror: the other quad of the 8
 }
 __device__ __forceinline__ int sum8_lanes(int v) {
     v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
@@ -456,44 +464,65 @@ __device__ __forceinline__ int sum8_lanes(int v) {
     return v + __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
 }
 
+// amax / 127 rounded to float, as the IEEE single division: the product in
+// double is within 2^-52 (relative) of amax/127, and amax/127 is never within
+// 2^-32 of a float rounding midpoint (a midpoint times 127 needs more than 24
+// significant bits), so the final rounding is the division's. Checked
+// exhaustively against amax / 127.0f over every positive float.
+__device__ __forceinline__ float div127(float amax) {
+    return (float)((double)amax * (1.0 / 127.0));
+}
+
+// Signed byte rint(p) for |p| <= 127.5 (round half to even): p + 1.5*2^23
+// rounds p to an integer in the low mantissa bits (the sum's ulp is 1), whose
+// low byte is rint(p) in two's complement. Checked exhaustively against
+// rintf over every float of magnitude <= 128.
+__device__ __forceinline__ uint32_t rint_bits(float p) {
+    return __builtin_bit_cast(uint32_t, p + 12582912.0f);
+}
+
 // LDS image of columns [c0, c1): int8 q at xl + (c - c0), fp32 scale and
 // int32 sum of 32-block k at xl + 32*nblk + 4k and xl + 36*nblk + 4k (nblk =
-// the region's block capacity).
+// the region's block capacity). Quantized values need no clamp: |x*id| <=
+// 127 * (1 + 2^-23) by construction of id (1/d here, 127/amax per 256), so
+// rint <= 127, except where id overflows to inf (handled on its own).
 template <int FMT, int ROUNDS>
 __device__ __forceinline__ void xstage_quant(const XStage<ROUNDS>& st, int c0, int c1, int w, int nw, int lane,
                                              int nblk, uint8_t* xl) {
-    constexpr bool PER256 = act_kind_of<FMT>() == DQ_ACT_Q8K_REP;
+    static_assert(act_kind_of<FMT>() != DQ_ACT_Q8K_REP, "per-256 activations use xrow_quant");
     float* ls = reinterpret_cast<float*>(xl + 32 * (size_t)nblk);
     int32_t* li = reinterpret_cast<int32_t*>(xl + 36 * (size_t)nblk);
+    // A round wholly past the end is computed on its clamped loads and stores
+    // nothing (c >= c1 in every lane). It is not skipped by a branch: the
+    // compiler would sink that round's load into the branch, below the weight
+    // loads, and its wait would then be for every weight byte.
 #pragma unroll
     for (int r = 0; r < ROUNDS; ++r) {
-        if (c0 + 256 * (w + r * nw) >= c1) continue;  // wave-uniform: a round wholly past the end
         const int c = c0 + 256 * (w + r * nw) + 4 * lane;
         const float4 v = st.v[r];
-        float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        amax = max8_lanes(amax);
-        if constexpr (PER256) {
-            amax = fmaxf(amax, dq_dpp<0x140>(amax));  // row_mirror: the 16-lane row
-            const int b = __builtin_bit_cast(int, amax);  // the 4 row maxima, wave-uniform
-            amax = fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)),
-                               __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))),
-                         fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)),
-                               __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48))));
-        }
-        const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
-        float id;
-        if constexpr (PER256) id = d > 0.0f ? 127.0f / amax : 0.0f;  // core/matmul.cpp:1681-1700
-        else id = d > 0.0f ? 1.0f / d : 0.0f;                          // core/quant.cpp:15-50
-        int q[4];
-        const float vv[4] = {v.x, v.y, v.z, v.w};
+        const float m4 = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        const uint32_t am = max8_lanes(__builtin_bit_cast(uint32_t, m4));  // the 32-block's maximum
+        const float amax = __builtin_bit_cast(float, am);
+        const float d = amax > 0.0f ? div127(amax) : 0.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;  // core/quant.cpp:15-50
+        // bytes rint(x * id) of the 4 columns, packed little-endian
+        const uint32_t t0 = rint_bits(v.x * id), t1 = rint_bits(v.y * id);
+        const uint32_t t2 = rint_bits(v.z * id), t3 = rint_bits(v.w * id);
+        const uint32_t lo = __builtin_amdgcn_perm(t1, t0, 0x0C0C0400u);  // [t0.b0, t1.b0, 0, 0]
+        const uint32_t hi = __builtin_amdgcn_perm(t3, t2, 0x0C0C0400u);  // [t2.b0, t3.b0, 0, 0]
+        uint32_t packed = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        if (__builtin_expect(!(id <= 3.40282347e38f), 0)) {
+            // id = inf (d below 1 / FLT_MAX): x * id is +-inf or
+            // NaN, converted with saturation and clamped as in dq_quant_block
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            packed = 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int iv = (int)rintf(vv[k] * id);
-            q[k] = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
+            for (int k = 0; k < 4; ++k) {
+                const int iv = (int)rintf(vv[k] * id);
+                packed |= (uint32_t)((iv > 127 ? 127 : (iv < -127 ? -127 : iv)) & 0xFF) << (8 * k);
+            }
         }
-        const uint32_t packed = (uint32_t)(q[0] & 0xFF) | ((uint32_t)(q[1] & 0xFF) << 8) |
-                                ((uint32_t)(q[2] & 0xFF) << 16) | ((uint32_t)(q[3] & 0xFF) << 24);
-        const int isum = sum8_lanes(q[0] + q[1] + q[2] + q[3]);
+        const int isum = sum8_lanes(dq_sdot4((int)packed, 0x01010101, 0));
         if (c < c1) {
             const int o = c - c0;
             *reinterpret_cast<uint32_t*>(xl + o) = packed;
@@ -511,7 +540,9 @@ __device__ __forceinline__ void xstage_quant(const XStage<ROUNDS>& st, int c0, i
 // all groups at once (about 16 waves per CU), which keeps the whole matrix's
 // loads in flight from the start and ends every wave right after its only
 // group. Groups are global over the jobs of J. One item per lane (NIT 1).
-template <int FMT, int R, int KS, bool XQ>
+// XQ: XR quantization rounds per wave, enough for the activation (the host
+// picks the smallest of its instantiations that covers it).
+template <int FMT, int R, int KS, bool XQ, int XR>
 __global__ __launch_bounds__(256) void gemv_flat_kernel(Jobs J, int items, int per, const int8_t* __restrict__ xq,
                                                         const float* __restrict__ xs,
                                                         const int32_t* __restrict__ xsum,
@@ -534,7 +565,6 @@ __global__ __launch_bounds__(256) void gemv_flat_kernel(Jobs J, int items, int p
     // loads (clamped, valid) addresses; its terms are masked in compute_group.
     // XQ rounds: KS 1 - the 4 waves share the whole activation (cols <= 8192,
     // <= 8 rounds each); KS 4 - each wave its own K quarter (<= 4096 columns).
-    constexpr int XR = KS == 1 ? 8 : 16;
     const int xc0 = KS == 1 ? 0 : 64 * i0, xc1 = KS == 1 ? 64 * items : 64 * i1;
     const int xw = KS == 1 ? wv : 0, xnw = KS == 1 ? 4 : 1;
     XStage<XR> xst;
@@ -568,14 +598,89 @@ __global__ __launch_bounds__(256) void gemv_flat_kernel(Jobs J, int items, int p
     compute_group<FMT, R, 1, KS>(w, X, J, g, i0, i1, lane, ks, part, 0);
 }
 
+// Per-256 quantization of the 16-wave flat grid, one 256-column block per
+// 16-lane row: lane j of row q of wave w holds columns 1024w + 256q + 64k +
+// 4j + [0, 4), k = 0..3 (each load instruction reads four contiguous 256-byte
+// runs). A block's maximum is a 4-step DPP reduction within the row, and one
+// scale and one reciprocal serve the lane's 16 values, so a wave quantizes
+// 1024 columns per pass (16 waves: cols <= 16384 in one pass). Same
+// integers, scales and sums as dq_quant_block; same LDS image as
+// xstage_quant.
+struct XRow {
+    float4 v[4];
+};
+
+__device__ __forceinline__ void xrow_load(XRow& st, const float* __restrict__ xf, int cols, int w, int lane) {
+    const int base = 1024 * w + 256 * (lane >> 4) + 4 * (lane & 15);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) st.v[k] = *reinterpret_cast<const float4*>(xf + min(base + 64 * k, cols - 4));
+}
+
+__device__ __forceinline__ void xrow_quant(const XRow& st, int cols, int w, int lane, int nblk, uint8_t* xl) {
+    float* ls = reinterpret_cast<float*>(xl + 32 * (size_t)nblk);
+    int32_t* li = reinterpret_cast<int32_t*>(xl + 36 * (size_t)nblk);
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(st.v[k].x), fabsf(st.v[k].y)), fmaxf(fabsf(st.v[k].z), fabsf(st.v[k].w))));
+    uint32_t am = __builtin_bit_cast(uint32_t, m);
+    am = umax_dpp<0xB1>(am);   // quad_perm [1,0,3,2]
+    am = umax_dpp<0x4E>(am);   // quad_perm [2,3,0,1]
+    am = umax_dpp<0x141>(am);  // row_half_mirror
+    am = umax_dpp<0x140>(am);  // row_mirror: the block's maximum in all 16 lanes
+    const float amax = __builtin_bit_cast(float, am);
+    const float d = amax > 0.0f ? div127(amax) : 0.0f;
+    const float id = d > 0.0f ? 127.0f / amax : 0.0f;  // core/matmul.cpp:1681-1700
+    uint32_t packed[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 v = st.v[k];
+        const uint32_t lo = __builtin_amdgcn_perm(rint_bits(v.y * id), rint_bits(v.x * id), 0x0C0C0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(rint_bits(v.w * id), rint_bits(v.z * id), 0x0C0C0400u);
+        packed[k] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    }
+    if (__builtin_expect(!(id <= 3.40282347e38f), 0)) {
+        // id = inf (block maximum below 127 / FLT_MAX): saturating conversion
+        // and clamp, as dq_quant_block
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float vv[4] = {st.v[k].x, st.v[k].y, st.v[k].z, st.v[k].w};
+            packed[k] = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int iv = (int)rintf(vv[e] * id);
+                packed[k] |= (uint32_t)((iv > 127 ? 127 : (iv < -127 ? -127 : iv)) & 0xFF) << (8 * e);
+            }
+        }
+    }
+    int isum[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) isum[k] = sum8_lanes(dq_sdot4((int)packed[k], 0x01010101, 0));
+    const int o = 1024 * w + 256 * (lane >> 4) + 4 * (lane & 15);
+    if (1024 * w + 256 * (lane >> 4) < cols) {  // the row's block lies inside the activation
+#pragma unroll
+        for (int k = 0; k < 4; ++k) *reinterpret_cast<uint32_t*>(xl + o + 64 * k) = packed[k];
+        if ((lane & 7) == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                ls[(o + 64 * k) >> 5] = d;
+                li[(o + 64 * k) >> 5] = isum[k];
+            }
+        }
+    }
+}
+
 // Flat grid for the fp32 activation with the per-256 quantizer: 16-wave
 // (1024-thread) workgroups, so one quantization of the activation serves 16
 // waves (4x fewer repeats over the grid than 4-wave workgroups). KS 1: 16
 // groups per workgroup, one per wave; KS 4: 4 groups of 4 waves (K quarters).
-// The activation is quantized whole into LDS (round r of wave w: 256-column
-// chunk w + 16r, at most 4 rounds: cols <= 16384), its loads issued before
-// the weights. No wave leaves before the last barrier; a group past the end
-// computes the clamped last group and stores nothing.
+// The activation is quantized whole into LDS (xrow_quant: wave w takes
+// columns [1024w, 1024w + 1024), cols <= 16384), its loads issued before the
+// weights. A wave with no columns skips the arithmetic but still consumes
+// its loads, so the compiler keeps them above the weight loads (a load used
+// only inside the branch would be sunk into it, and its wait would then be
+// for every weight byte). No wave leaves before the last barrier; a group
+// past the end computes the clamped last group and stores nothing.
 template <int FMT, int R, int KS>
 __global__ __launch_bounds__(1024) void gemv_flat16_kernel(Jobs J, int items, int per, const float* __restrict__ xf) {
     using W = typename Fmt<FMT>::W;
@@ -593,13 +698,16 @@ __global__ __launch_bounds__(1024) void gemv_flat16_kernel(Jobs J, int items, in
     const bool live = g < ngroups;
     const int cols = 64 * items;
 
-    XStage<4> xst;
-    xstage_load<4>(xst, xf, 0, cols, wv, 16, lane);
+    XRow xst;
+    xrow_load(xst, xf, cols, wv, lane);
     W w[R][1];
     load_group<FMT, R, 1>(w, J, min(g, ngroups - 1), ngroups, i0, i1, lane, nullptr);
     __builtin_amdgcn_sched_barrier(0);
     const int nblk = 2 * items;
-    xstage_quant<FMT, 4>(xst, 0, cols, wv, 16, lane, nblk, xl);
+    if (1024 * wv < cols)
+        xrow_quant(xst, cols, wv, lane, nblk, xl);
+    else
+        asm volatile("" ::"v"(xst.v[0].x), "v"(xst.v[1].x), "v"(xst.v[2].x), "v"(xst.v[3].x));
     __syncthreads();
     if (KS == 1 && !live) return;  // KS 1 has no barrier after this one
     XItem X[1];
@@ -659,6 +767,33 @@ int launch(Jobs J, int items, const int8_t* xq, const float* xs, const int32_t* 
     return dq_launch_status();
 }
 
+// Quantization rounds per wave of the 4-wave flat grid: KS 1 - the 4 waves
+// share the activation's 256-column chunks (2, 4 or 8 rounds: cols <= 8192);
+// KS 4 - each wave its own K quarter (per <= 64 items: 16 rounds).
+template <int KS>
+int flat_xr(int items, int per) {
+    if (KS == 4) return 16;
+    const int rounds = ((items + 3) / 4 + 3) / 4;
+    return rounds <= 2 ? 2 : rounds <= 4 ? 4 : 8;
+}
+
+// Calls f(std::integral_constant<int, XR>) for the 4-wave flat grid's XR.
+template <int KS, class F>
+auto with_flat_xr(int xr, F&& f) {
+    if constexpr (KS == 4) {
+        return f(std::integral_constant<int, 16>{});
+    } else {
+        if (xr == 2) return f(std::integral_constant<int, 2>{});
+        if (xr == 4) return f(std::integral_constant<int, 4>{});
+        return f(std::integral_constant<int, 8>{});
+    }
+}
+
+// The in-kernel quantized (XQ) instantiations exist for the per-32 formats
+// only: the per-256 formats take gemv_flat16_kernel with the fp32 activation.
+template <int FMT>
+constexpr bool flat_xq() { return act_kind_of<FMT>() != DQ_ACT_Q8K_REP; }
+
 template <int FMT, int R, int KS>
 int launch_flat_r(Jobs J, int items, int per, const int8_t* xq, const float* xs, const int32_t* xsum,
                   const float* xf, hipStream_t s) {
@@ -666,10 +801,18 @@ int launch_flat_r(Jobs J, int items, int per, const int8_t* xq, const float* xs,
     const int ngroups = J.g0[J.n];
     const unsigned grid = (unsigned)(KS == 1 ? (ngroups + 3) / 4 : ngroups);
     if (xf) {
-        const size_t lds = KS == 1 ? (size_t)80 * items : (size_t)4 * 80 * per;
-        gemv_flat_kernel<FMT, R, KS, true><<<grid, 256, lds, s>>>(J, items, per, xq, xs, xsum, xf);
+        if constexpr (flat_xq<FMT>()) {
+            const size_t lds = KS == 1 ? (size_t)80 * items : (size_t)4 * 80 * per;
+            with_flat_xr<KS>(flat_xr<KS>(items, per), [&](auto xr) {
+                gemv_flat_kernel<FMT, R, KS, true, decltype(xr)::value>
+                    <<<grid, 256, lds, s>>>(J, items, per, xq, xs, xsum, xf);
+                return 0;
+            });
+        } else {
+            return DQ_ERR_NOT_SUPPORTED;
+        }
     } else {
-        gemv_flat_kernel<FMT, R, KS, false><<<grid, 256, 0, s>>>(J, items, per, xq, xs, xsum, xf);
+        gemv_flat_kernel<FMT, R, KS, false, 1><<<grid, 256, 0, s>>>(J, items, per, xq, xs, xsum, xf);
     }
     return dq_launch_status();
 }
@@ -699,39 +842,63 @@ int flat16_resident(size_t lds) {
     static int c = -1;
     if (c < 0) {
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(&gemv_flat16_kernel<FMT, R, KS>),
-                                                         1024, lds) != hipSuccess)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &nb, reinterpret_cast<const void*>(&gemv_flat16_kernel<FMT, R, KS>), 1024, lds) != hipSuccess)
             nb = 0;
         c = nb;
     }
     return c;
 }
 
-// 16-wave flat grid with the fewest rows per group (1, 2, 4) whose
-// workgroups are all resident at once; NO_FLAT otherwise.
 template <int FMT, int KS>
-int launch_flat16(const Jobs& J, int items, int per, const float* xf, hipStream_t s) {
+int launch_flat16_fit(const Jobs& J, int items, int per, const float* xf, hipStream_t s) {
     const size_t lds = (size_t)80 * items;
-    if (lds > XQ_MAX_LDS || items * 64 > 16384) return NO_FLAT;
     constexpr int GPW = KS == 1 ? 16 : 4;
+    static const int rmin = env_int("DQ_GEMV_F16_RMIN", 1);  // smallest rows per group tried
     const long cus = num_cus();
-    auto fits = [&](int r, int resident) { return resident > 0 && (count_groups(J, r) + GPW - 1) / GPW <= cus * resident; };
+    auto fits = [&](int r, int resident) {
+        return r >= rmin && resident > 0 && (count_groups(J, r) + GPW - 1) / GPW <= cus * resident;
+    };
+    // K split (wide rows: every workgroup quantizes >= 32 KB of activation):
+    // the most rows per group whose grid still covers every CU, so the fewest
+    // workgroups repeat the quantization
+    if constexpr (KS == 4) {
+        auto covers = [&](int r) { return (count_groups(J, r) + GPW - 1) / GPW >= cus; };
+        if (covers(4) && fits(4, flat16_resident<FMT, 4, KS>(lds)))
+            return launch_flat16_r<FMT, 4, KS>(J, items, per, xf, s);
+        if (covers(2) && fits(2, flat16_resident<FMT, 2, KS>(lds)))
+            return launch_flat16_r<FMT, 2, KS>(J, items, per, xf, s);
+    }
     if (fits(1, flat16_resident<FMT, 1, KS>(lds))) return launch_flat16_r<FMT, 1, KS>(J, items, per, xf, s);
     if (fits(2, flat16_resident<FMT, 2, KS>(lds))) return launch_flat16_r<FMT, 2, KS>(J, items, per, xf, s);
     if (fits(4, flat16_resident<FMT, 4, KS>(lds))) return launch_flat16_r<FMT, 4, KS>(J, items, per, xf, s);
     return NO_FLAT;
 }
 
-// Waves of gemv_flat_kernel<FMT, R, KS, XQ> that one CU holds at once (its
-// register and LDS needs; cached per instantiation).
+// 16-wave flat grid with the fewest rows per group (1, 2, 4) whose
+// workgroups are all resident at once (K split: see launch_flat16_fit);
+// NO_FLAT otherwise.
+template <int FMT, int KS>
+int launch_flat16(const Jobs& J, int items, int per, const float* xf, hipStream_t s) {
+    if ((size_t)80 * items > XQ_MAX_LDS || items * 64 > 16384) return NO_FLAT;
+    return launch_flat16_fit<FMT, KS>(J, items, per, xf, s);
+}
+
+// Waves of gemv_flat_kernel<FMT, R, KS, XQ, XR> that one CU holds at once
+// (its register and LDS needs; cached per instantiation; XR as flat_xr).
 template <int FMT, int R, int KS>
-int flat_resident_waves(bool xq, size_t lds) {
-    static int cached[2] = {0, 0};
-    int& c = cached[xq ? 1 : 0];
+int flat_resident_waves(bool xq, int xr, size_t lds) {
+    static int cached[4] = {0, 0, 0, 0};
+    const int slot = !xq ? 0 : xr == 2 ? 1 : xr == 4 ? 2 : 3;
+    int& c = cached[slot];
     if (c == 0) {
+        const void* k = reinterpret_cast<const void*>(&gemv_flat_kernel<FMT, R, KS, false, 1>);
+        if constexpr (flat_xq<FMT>())
+            if (xq)
+                k = with_flat_xr<KS>(xr, [&](auto x) {
+                    return reinterpret_cast<const void*>(&gemv_flat_kernel<FMT, R, KS, true, decltype(x)::value>);
+                });
         int nb = 0;
-        const void* k = xq ? reinterpret_cast<const void*>(&gemv_flat_kernel<FMT, R, KS, true>)
-                           : reinterpret_cast<const void*>(&gemv_flat_kernel<FMT, R, KS, false>);
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k, 256, lds) != hipSuccess || nb <= 0) nb = 1;
         c = 4 * nb;
     }
@@ -759,15 +926,16 @@ int launch_flat(const Jobs& J, int items, int per, int nit, const int8_t* xq, co
     const int gw = KS == 1 ? 1 : 4;  // waves per group
     const long cus = num_cus();
     const bool q = xf != nullptr;
+    const int xr = flat_xr<KS>(items, per);
     auto fits = [&](int r, int resident) { return (long)count_groups(J, r) * gw <= cus * min(wpc, resident); };
     constexpr int WB = (int)sizeof(typename Fmt<FMT>::W);  // weight bytes per row per lane
-    if (fits(1, flat_resident_waves<FMT, 1, KS>(q, lds)))
+    if (fits(1, flat_resident_waves<FMT, 1, KS>(q, xr, lds)))
         return launch_flat_r<FMT, 1, KS>(J, items, per, xq, xs, xsum, xf, s);
-    if (fits(2, flat_resident_waves<FMT, 2, KS>(q, lds)))
+    if (fits(2, flat_resident_waves<FMT, 2, KS>(q, xr, lds)))
         return launch_flat_r<FMT, 2, KS>(J, items, per, xq, xs, xsum, xf, s);
-    if (fits(4, flat_resident_waves<FMT, 4, KS>(q, lds)))
+    if (fits(4, flat_resident_waves<FMT, 4, KS>(q, xr, lds)))
         return launch_flat_r<FMT, 4, KS>(J, items, per, xq, xs, xsum, xf, s);
-    if (8 * WB <= 400 && fits(8, flat_resident_waves<FMT, 8, KS>(q, lds)))
+    if (8 * WB <= 400 && fits(8, flat_resident_waves<FMT, 8, KS>(q, xr, lds)))
         return launch_flat_r<FMT, 8, KS>(J, items, per, xq, xs, xsum, xf, s);
     return NO_FLAT;
 }
