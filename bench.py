@@ -555,6 +555,17 @@ def main():
         us = graph_time(lp.step, 1, max(1, args.steps))
         log(f"layer_prefill: {us:.1f} us/layer, {lp.n_tok / us * 1e6:.0f} tok/s, {lp.flops() / us / 1e6:.1f} TFLOP/s")
         return
+    if args.only == "step":  # the headline step: fp32 activation, quantize + GEMV in one launch, up then down
+        up = GemvCase(synth.Q4_K, 14336, 4096, 11, dev)
+        down = GemvCase(synth.Q4_K, 4096, 14336, 12, dev)
+
+        def fused():
+            up.step()
+            down.step()
+        per = max(len(up.mats), len(down.mats))
+        us = graph_time(fused, per, max(1, args.steps // per))
+        log(f"step: {us:.2f} us, {(step_bytes(synth.Q4_K, 14336, 4096) + step_bytes(synth.Q4_K, 4096, 14336)) / us / 1e3:.1f} GB/s")
+        return
     if args.only:
         qt, r, c = shapes[args.only]
         case = GemvCase(qt, r, c, 11, dev)

@@ -670,21 +670,22 @@ __device__ __forceinline__ void xrow_quant(const XRow& st, int cols, int w, int 
     }
 }
 
-// Flat grid for the fp32 activation with the per-256 quantizer: 16-wave
-// (1024-thread) workgroups, so one quantization of the activation serves 16
-// waves (4x fewer repeats over the grid than 4-wave workgroups). KS 1: 16
-// groups per workgroup, one per wave; KS 4: 4 groups of 4 waves (K quarters).
-// The activation is quantized whole into LDS (xrow_quant: wave w takes
-// columns [1024w, 1024w + 1024), cols <= 16384), its loads issued before the
+// Flat grid for the fp32 activation with the per-256 quantizer: NW-wave
+// workgroups, one quantization of the activation per workgroup. KS 1: NW
+// (4 or 8) groups per workgroup, one per wave; KS 4: 16 waves, 4 groups of
+// 4 waves (K quarters), so one quantization serves 16 waves. The
+// activation is quantized whole into LDS (xrow_quant: wave w takes columns
+// [1024w, 1024w + 1024), cols <= 1024 NW), its loads issued before the
 // weights. A wave with no columns skips the arithmetic but still consumes
 // its loads, so the compiler keeps them above the weight loads (a load used
 // only inside the branch would be sunk into it, and its wait would then be
 // for every weight byte). No wave leaves before the last barrier; a group
 // past the end computes the clamped last group and stores nothing.
-template <int FMT, int R, int KS>
-__global__ __launch_bounds__(1024) void gemv_flat16_kernel(Jobs J, int items, int per, const float* __restrict__ xf) {
+template <int FMT, int R, int KS, int NW = 16>
+__global__ __launch_bounds__(NW * 64) void gemv_flat16_kernel(Jobs J, int items, int per, const float* __restrict__ xf) {
+    static_assert(NW == 16 || ((NW == 8 || NW == 4) && KS == 1), "fewer waves: one pass of NW * 1024 columns");
     using W = typename Fmt<FMT>::W;
-    constexpr int GPW = KS == 1 ? 16 : 4;  // groups per workgroup
+    constexpr int GPW = KS == 1 ? NW : NW / 4;  // groups per workgroup
     extern __shared__ __align__(16) uint8_t xl[];
     __shared__ float part[GPW][R][4];
     const int lane = threadIdx.x & (DQ_WAVE - 1);
@@ -827,33 +828,33 @@ int count_groups(const Jobs& J, int R) {
     return n;
 }
 
-template <int FMT, int R, int KS>
+template <int FMT, int R, int KS, int NW>
 int launch_flat16_r(Jobs J, int items, int per, const float* xf, hipStream_t s) {
     set_groups(J, R);
-    constexpr int GPW = KS == 1 ? 16 : 4;
+    constexpr int GPW = KS == 1 ? NW : NW / 4;
     const unsigned grid = (unsigned)((J.g0[J.n] + GPW - 1) / GPW);
-    gemv_flat16_kernel<FMT, R, KS><<<grid, 1024, (size_t)80 * items, s>>>(J, items, per, xf);
+    gemv_flat16_kernel<FMT, R, KS, NW><<<grid, NW * 64, (size_t)80 * items, s>>>(J, items, per, xf);
     return dq_launch_status();
 }
 
-// Workgroups of gemv_flat16_kernel<FMT, R, KS> one CU holds at once (cached).
-template <int FMT, int R, int KS>
+// Workgroups of gemv_flat16_kernel<FMT, R, KS, NW> one CU holds at once (cached).
+template <int FMT, int R, int KS, int NW>
 int flat16_resident(size_t lds) {
     static int c = -1;
     if (c < 0) {
         int nb = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, reinterpret_cast<const void*>(&gemv_flat16_kernel<FMT, R, KS>), 1024, lds) != hipSuccess)
+                &nb, reinterpret_cast<const void*>(&gemv_flat16_kernel<FMT, R, KS, NW>), NW * 64, lds) != hipSuccess)
             nb = 0;
         c = nb;
     }
     return c;
 }
 
-template <int FMT, int KS>
+template <int FMT, int KS, int NW>
 int launch_flat16_fit(const Jobs& J, int items, int per, const float* xf, hipStream_t s) {
     const size_t lds = (size_t)80 * items;
-    constexpr int GPW = KS == 1 ? 16 : 4;
+    constexpr int GPW = KS == 1 ? NW : NW / 4;
     static const int rmin = env_int("DQ_GEMV_F16_RMIN", 1);  // smallest rows per group tried
     const long cus = num_cus();
     auto fits = [&](int r, int resident) {
@@ -864,14 +865,14 @@ int launch_flat16_fit(const Jobs& J, int items, int per, const float* xf, hipStr
     // workgroups repeat the quantization
     if constexpr (KS == 4) {
         auto covers = [&](int r) { return (count_groups(J, r) + GPW - 1) / GPW >= cus; };
-        if (covers(4) && fits(4, flat16_resident<FMT, 4, KS>(lds)))
-            return launch_flat16_r<FMT, 4, KS>(J, items, per, xf, s);
-        if (covers(2) && fits(2, flat16_resident<FMT, 2, KS>(lds)))
-            return launch_flat16_r<FMT, 2, KS>(J, items, per, xf, s);
+        if (covers(4) && fits(4, flat16_resident<FMT, 4, KS, NW>(lds)))
+            return launch_flat16_r<FMT, 4, KS, NW>(J, items, per, xf, s);
+        if (covers(2) && fits(2, flat16_resident<FMT, 2, KS, NW>(lds)))
+            return launch_flat16_r<FMT, 2, KS, NW>(J, items, per, xf, s);
     }
-    if (fits(1, flat16_resident<FMT, 1, KS>(lds))) return launch_flat16_r<FMT, 1, KS>(J, items, per, xf, s);
-    if (fits(2, flat16_resident<FMT, 2, KS>(lds))) return launch_flat16_r<FMT, 2, KS>(J, items, per, xf, s);
-    if (fits(4, flat16_resident<FMT, 4, KS>(lds))) return launch_flat16_r<FMT, 4, KS>(J, items, per, xf, s);
+    if (fits(1, flat16_resident<FMT, 1, KS, NW>(lds))) return launch_flat16_r<FMT, 1, KS, NW>(J, items, per, xf, s);
+    if (fits(2, flat16_resident<FMT, 2, KS, NW>(lds))) return launch_flat16_r<FMT, 2, KS, NW>(J, items, per, xf, s);
+    if (fits(4, flat16_resident<FMT, 4, KS, NW>(lds))) return launch_flat16_r<FMT, 4, KS, NW>(J, items, per, xf, s);
     return NO_FLAT;
 }
 
@@ -881,7 +882,19 @@ int launch_flat16_fit(const Jobs& J, int items, int per, const float* xf, hipStr
 template <int FMT, int KS>
 int launch_flat16(const Jobs& J, int items, int per, const float* xf, hipStream_t s) {
     if ((size_t)80 * items > XQ_MAX_LDS || items * 64 > 16384) return NO_FLAT;
-    return launch_flat16_fit<FMT, KS>(J, items, per, xf, s);
+    // Without a K split: the fewest waves whose one pass covers the columns
+    // (4 waves: cols <= 4096; 8 waves: cols <= 8192). The barrier after the
+    // quantization waits for the workgroup's slowest wave to issue its loads
+    // under memory back-pressure, so smaller workgroups start their dot
+    // products sooner; the quantization they repeat costs ~100 instructions
+    // per wave pass (Q4_K 14336x4096 fp32 step: 16 waves 8.66 us, 8 waves
+    // 8.16 us, 4 waves 7.96 us; pre-quantized GEMV 7.61 us).
+    static const int nw = env_int("DQ_GEMV_F16_NW", 4);  // smallest waves per workgroup tried
+    if constexpr (KS == 1) {
+        if (nw <= 4 && items * 64 <= 4096) return launch_flat16_fit<FMT, KS, 4>(J, items, per, xf, s);
+        if (nw <= 8) return launch_flat16_fit<FMT, KS, 8>(J, items, per, xf, s);
+    }
+    return launch_flat16_fit<FMT, KS, 16>(J, items, per, xf, s);
 }
 
 // Waves of gemv_flat_kernel<FMT, R, KS, XQ, XR> that one CU holds at once
