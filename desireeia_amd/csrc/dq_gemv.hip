@@ -672,18 +672,18 @@ __device__ __forceinline__ void xrow_quant(const XRow& st, int cols, int w, int 
 
 // Flat grid for the fp32 activation with the per-256 quantizer: NW-wave
 // workgroups, one quantization of the activation per workgroup. KS 1: NW
-// (4 or 8) groups per workgroup, one per wave; KS 4: 16 waves, 4 groups of
-// 4 waves (K quarters), so one quantization serves 16 waves. The
-// activation is quantized whole into LDS (xrow_quant: wave w takes columns
-// [1024w, 1024w + 1024), cols <= 1024 NW), its loads issued before the
-// weights. A wave with no columns skips the arithmetic but still consumes
+// (4 or 8) groups per workgroup, one per wave; KS 4: NW / 4 groups of 4
+// waves (K quarters). The activation is quantized whole into LDS
+// (xrow_quant: pass p of wave w takes columns [1024(w + NW p), +1024), XP
+// passes, cols <= 1024 NW XP), its loads issued before the weights. A wave with no columns skips the arithmetic but still consumes
 // its loads, so the compiler keeps them above the weight loads (a load used
 // only inside the branch would be sunk into it, and its wait would then be
 // for every weight byte). No wave leaves before the last barrier; a group
 // past the end computes the clamped last group and stores nothing.
 template <int FMT, int R, int KS, int NW = 16>
 __global__ __launch_bounds__(NW * 64) void gemv_flat16_kernel(Jobs J, int items, int per, const float* __restrict__ xf) {
-    static_assert(NW == 16 || ((NW == 8 || NW == 4) && KS == 1), "fewer waves: one pass of NW * 1024 columns");
+    static_assert(NW == 16 || NW == 8 || (NW == 4 && KS == 1), "waves per workgroup");
+    constexpr int XP = (KS == 4 && NW == 8) ? 2 : 1;  // quantization passes per wave (cols <= 1024 NW XP)
     using W = typename Fmt<FMT>::W;
     constexpr int GPW = KS == 1 ? NW : NW / 4;  // groups per workgroup
     extern __shared__ __align__(16) uint8_t xl[];
@@ -699,16 +699,20 @@ __global__ __launch_bounds__(NW * 64) void gemv_flat16_kernel(Jobs J, int items,
     const bool live = g < ngroups;
     const int cols = 64 * items;
 
-    XRow xst;
-    xrow_load(xst, xf, cols, wv, lane);
+    XRow xst[XP];
+#pragma unroll
+    for (int p = 0; p < XP; ++p) xrow_load(xst[p], xf, cols, wv + NW * p, lane);
     W w[R][1];
     load_group<FMT, R, 1>(w, J, min(g, ngroups - 1), ngroups, i0, i1, lane, nullptr);
     __builtin_amdgcn_sched_barrier(0);
     const int nblk = 2 * items;
-    if (1024 * wv < cols)
-        xrow_quant(xst, cols, wv, lane, nblk, xl);
-    else
-        asm volatile("" ::"v"(xst.v[0].x), "v"(xst.v[1].x), "v"(xst.v[2].x), "v"(xst.v[3].x));
+#pragma unroll
+    for (int p = 0; p < XP; ++p) {
+        if (1024 * (wv + NW * p) < cols)
+            xrow_quant(xst[p], cols, wv + NW * p, lane, nblk, xl);
+        else
+            asm volatile("" ::"v"(xst[p].v[0].x), "v"(xst[p].v[1].x), "v"(xst[p].v[2].x), "v"(xst[p].v[3].x));
+    }
     __syncthreads();
     if (KS == 1 && !live) return;  // KS 1 has no barrier after this one
     XItem X[1];
@@ -893,6 +897,12 @@ int launch_flat16(const Jobs& J, int items, int per, const float* xf, hipStream_
     if constexpr (KS == 1) {
         if (nw <= 4 && items * 64 <= 4096) return launch_flat16_fit<FMT, KS, 4>(J, items, per, xf, s);
         if (nw <= 8) return launch_flat16_fit<FMT, KS, 8>(J, items, per, xf, s);
+    } else {
+        // K split: 8 waves (2 groups of 4 K quarters, two quantization
+        // passes per wave) rather than 16 (Q4_K 4096x14336 fp32 step 9.48 ->
+        // 8.96 us, Q6_K 12.58 -> 11.78 us)
+        static const int nw4 = env_int("DQ_GEMV_F16_NW4", 8);
+        if (nw4 == 8) return launch_flat16_fit<FMT, KS, 8>(J, items, per, xf, s);
     }
     return launch_flat16_fit<FMT, KS, 16>(J, items, per, xf, s);
 }
