@@ -20,9 +20,15 @@ launch / average launch duration, from HIP events around back-to-back launches
 on the stream the kernels run on, captured in a HIP graph so host launch
 overhead is not counted. `cpu_baseline` times the reference engine's
 own matmul_q4_k (oracle/_ref, compiled from the reference sources) on the
-host, over a bounded sample.
+host, over a bounded sample; `cpu_baseline.rows` times its matmul_batch,
+attention_prefill_q8 and matmul_q6_k on the prefill GEMM, prefill attention
+and output-head shapes.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--only NAME] [--no-cpu]
+
+--only runs one line N times for a profiler: a GEMV shape (q4k_up, ...),
+step (the headline step), copy, gemm_*, layer, moe, attn, head,
+attn_prefill, layer_prefill.
 """
 import argparse
 import json
