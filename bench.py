@@ -349,6 +349,14 @@ class HeadCase:
 def graph_time(fn, calls_per_graph, reps, warmup_reps=2):
     """Captures calls_per_graph calls of fn into one HIP graph and times `reps`
     replays with HIP events on the capturing stream. Returns us per call."""
+    ts = replay_times(fn, calls_per_graph, reps, warmup_reps)
+    return sum(ts) / len(ts)
+
+
+def replay_times(fn, calls_per_graph, reps, warmup_reps=2):
+    """Captures calls_per_graph calls of fn into one HIP graph and times each
+    of `reps` replays on its own (HIP events on the capturing stream, the
+    stream the kernels run on). Returns us per call, one figure per replay."""
     import torch
     fn()
     torch.cuda.synchronize()
@@ -359,25 +367,28 @@ def graph_time(fn, calls_per_graph, reps, warmup_reps=2):
     for _ in range(warmup_reps):
         g.replay()
     torch.cuda.synchronize()
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    ev[0].record()
+    for i in range(reps):
         g.replay()
-    e.record()
+        ev[i + 1].record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / (reps * calls_per_graph) * 1e3
+    return [ev[i].elapsed_time(ev[i + 1]) / calls_per_graph * 1e3 for i in range(reps)]
 
 
-def kernel_stats(case, launches=400):
-    """Average GEMV launch duration (us): graph of back-to-back launches over
-    the rotated weight copies."""
+def kernel_stats(case, launches=400, fp32=False):
+    """Average GEMV launch duration (us) over a graph of back-to-back launches
+    on the rotated weight copies: the pre-quantized GEMV (dq_gemv), or with
+    fp32=True the launch the benchmark step runs (dq_gemv_f32: the
+    activation quantized in-kernel). Returns (us, GB/s of that launch's
+    algorithmic bytes)."""
     per = 2 * len(case.mats)
-    us = graph_time(case.kernel, per, max(1, launches // per))
-    b = gemv_kernel_bytes(case.qtype, case.rows, case.cols)
-    return us, b / us / 1e3  # GB/s
+    us = graph_time(case.step if fp32 else case.kernel, per, max(1, launches // per))
+    b = (step_bytes if fp32 else gemv_kernel_bytes)(case.qtype, case.rows, case.cols)
+    return us, b / us / 1e3
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_up_14336x4096_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_down_4096x14336_fp32_traffic.md")
 
 
 def recorded_traffic():
@@ -393,47 +404,85 @@ def recorded_traffic():
     return None
 
 
-def cpu_baseline_q4k(budget_s=12.0):
-    """The reference's matmul_q4_k (oracle/_ref) on the host cores, 14336x4096,
-    distinct weight copies (DRAM regime), best of repeated passes."""
-    from desireeia_amd import synth
-    from oracle import oracle as orc
-    r = orc.ref()
-    kind = "reference"
-    cores = min(16, len(os.sched_getaffinity(0)))
-    if r is None:
-        r = orc.oracle()
-        kind = "port"
-        cores = 1
-    else:
-        r.set_threads(cores)
-    rows, cols = 14336, 4096
-    w0 = synth.gen_weights(synth.Q4_K, rows, cols, seed=99)
-    copies = [w0] + [np.roll(w0, k, axis=0) for k in range(1, 8)]  # 8 x 33 MB
-    x = synth.gen_act(cols, 100)
-    nbytes = rows * synth.row_bytes(synth.Q4_K, cols)
-    t_end = time.time() + budget_s
-    best, calls, total = 1e30, 0, 0.0
-    while time.time() < t_end or calls < 2:
-        w = copies[calls % len(copies)]
-        t0 = time.perf_counter()
-        if kind == "reference":
-            r.matmul(synth.Q4_K, w, rows, cols, x)
-        else:
-            r.matmul(synth.Q4_K, w, rows, cols, x, 0, 512)
-        dt = time.perf_counter() - t0
-        if kind == "port":
-            dt *= rows / 512.0
-        best = min(best, dt)
-        total += dt
-        calls += 1
-    out = {"value": round(nbytes / best / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": kind,
-           "sample": f"Q4_K GEMV 14336x4096 (matmul_q4_k incl. its per-256 activation quantization), "
-                     f"8 distinct weight copies (264 MB), best of {calls} calls over {budget_s:.0f} s"
-                     + ("" if kind == "reference" else "; rows 0..511 timed and scaled to 14336")}
-    if kind == "reference":
-        out["rows"] = cpu_rows(r)
-    return out
+def stream_read_ceiling(dev, nbytes, reps=20):
+    """The device's streaming-read rate at one GEMV's size: dq_stream_read of
+    nbytes over buffers rotated across >= 640 MB (every byte from HBM), one
+    launch per call in a graph, at 8, 12, 16 and 24 waves per CU. Returns
+    {waves_per_cu: GB/s} and the best."""
+    import torch
+    from desireeia_amd import _lib, ops
+    lib = _lib.load()
+    nbytes = -(-nbytes // 4096) * 4096
+    ncopy = max(2, -(-ROTATE_BYTES // nbytes))
+    bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev) for _ in range(ncopy)]
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = {}
+    for wpc in (8, 12, 16, 24):
+        i = [0]
+
+        def call():
+            b = bufs[i[0]]
+            i[0] = (i[0] + 1) % len(bufs)
+            _lib.check(lib.dq_stream_read(ops._ptr(b), nbytes, wpc, ops._ptr(sink), 0x9E3779B9, ops._stream()),
+                       "dq_stream_read")
+        us = graph_time(call, ncopy, reps)
+        out[wpc] = round(nbytes / us / 1e3, 1)
+    del bufs
+    return out, max(out.values())
+
+
+# ------------------------------------------------------------------ CPU side
+
+def host_description():
+    """The host CPU as lscpu reports it (model, sockets, cores per socket,
+    threads per core, total L3), and the threads this process may use."""
+    import subprocess
+    d = {}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, env=dict(os.environ, LC_ALL="C"),
+                             timeout=20).stdout
+        for line in txt.splitlines():
+            k, _, v = line.partition(":")
+            d[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    sockets = int(d.get("Socket(s)", "1") or 1)
+    cps = int(d.get("Core(s) per socket", "0") or 0)
+    tpc = int(d.get("Thread(s) per core", "1") or 1)
+    # sysfs sums the distinct L3 instances; lscpu's "L3" line (newer
+    # util-linux) is already that total
+    l3_total = _sysfs_l3() or _parse_size(d.get("L3", ""))
+    share = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        share = min(share, int(os.environ["OMP_NUM_THREADS"]))
+    phys = sockets * cps if cps else share
+    return {"model": d.get("Model name", "?"), "sockets": sockets, "cores_per_socket": cps,
+            "threads_per_core": tpc, "physical_cores": phys, "l3_bytes": l3_total,
+            "cpu_share": share, "threads_used": max(1, min(phys, share))}
+
+
+def _parse_size(txt):
+    import re
+    m = re.match(r"\s*([0-9.]+)\s*([KMG])i?B?", txt)
+    if not m:
+        return None
+    return int(float(m.group(1)) * {"K": 1 << 10, "M": 1 << 20, "G": 1 << 30}[m.group(2)])
+
+
+def _sysfs_l3():
+    try:
+        ids, total = set(), 0
+        base = "/sys/devices/system/cpu"
+        for c in os.listdir(base):
+            p = os.path.join(base, c, "cache", "index3")
+            if c.startswith("cpu") and os.path.isdir(p):
+                sid = open(os.path.join(p, "shared_cpu_list")).read().strip()
+                if sid not in ids:
+                    ids.add(sid)
+                    total += _parse_size(open(os.path.join(p, "size")).read().strip()) or 0
+        return total or None
+    except OSError:
+        return None
 
 
 def _best_of(fn, budget_s, min_calls=2):
@@ -447,12 +496,171 @@ def _best_of(fn, budget_s, min_calls=2):
     return best, calls
 
 
+def _dram_copies(w0, rot_bytes):
+    """Distinct copies of a weight matrix totalling >= rot_bytes, so that
+    calls rotating over them read DRAM, not the host's last-level cache
+    (bench/kernel_bench.cpp:112-132)."""
+    n = max(2, -(-rot_bytes // w0.nbytes))
+    return [w0] + [np.roll(w0, k, axis=0) for k in range(1, n)]
+
+
+def cpu_gemv(r, qtype, rows, cols, rot_bytes, budget_s, seed):
+    from desireeia_amd import synth
+    copies = _dram_copies(synth.gen_weights(qtype, rows, cols, seed), rot_bytes)
+    x = synth.gen_act(cols, seed + 1)
+    i = [0]
+
+    def call():
+        r.matmul(qtype, copies[i[0] % len(copies)], rows, cols, x)
+        i[0] += 1
+    best, calls = _best_of(call, budget_s)
+    nbytes = rows * synth.row_bytes(qtype, cols)
+    return nbytes / best / 1e9, best, calls, len(copies), len(copies) * copies[0].nbytes
+
+
+def cpu_layer(r, budget_s=5.0):
+    """Config 4's decode step on the CPU from the reference's own operators:
+    matmul_q4_k / matmul_q6_k for the seven products (each quantizing its
+    input per 256, as matvec does), kv_quantize_row for the new K/V rows,
+    decode attention over 4097 positions from kv_dot_q8_0 / kv_axpy_q8_0 on
+    the reference's thread pool, and RMSNorm / RoPE / SiLU / residuals in
+    numpy (dense_forward.cpp:3897-4257 order). Four distinct layers (556 MB
+    of weights) rotate so that weights come from DRAM."""
+    from desireeia_amd import synth
+    E, H, KV, HD, F, pos = 4096, 32, 8, 128, 14336, 4096
+    shapes = {"q": (synth.Q4_K, H * HD, E), "k": (synth.Q4_K, KV * HD, E), "v": (synth.Q6_K, KV * HD, E),
+              "o": (synth.Q4_K, E, H * HD), "gate": (synth.Q4_K, F, E), "up": (synth.Q4_K, F, E),
+              "down": (synth.Q6_K, E, F)}
+    base = {nm: synth.gen_weights(qt, rr, c, 40 + i) for i, (nm, (qt, rr, c)) in enumerate(shapes.items())}
+    layers = [base] + [{nm: np.roll(w, k, axis=0) for nm, w in base.items()} for k in range(1, 4)]
+    rng = np.random.default_rng(41)
+    pb = KV * HD // 32 * 34
+    kc = np.zeros((pos + 1) * pb, np.uint8)
+    vc = np.zeros((pos + 1) * pb, np.uint8)
+    kc[:pos * pb] = r.kv_quantize_row(rng.standard_normal(pos * KV * HD).astype(np.float32))
+    vc[:pos * pb] = r.kv_quantize_row(rng.standard_normal(pos * KV * HD).astype(np.float32))
+    an = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+    fn = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32)
+    ts = np.float32(500000.0) ** np.float32(-2.0 / HD)
+    th = np.float32(pos) * ts ** np.arange(HD // 2, dtype=np.float32)
+    cs, sn = np.cos(th).astype(np.float32), np.sin(th).astype(np.float32)
+    x0 = synth.gen_act(E, 42)
+    state = {"i": 0}
+
+    def norm(v, w):
+        return v * (np.float32(1) / np.sqrt(np.float32(np.dot(v.astype(np.float64), v) / v.size) + np.float32(1e-5))) * w
+
+    def rope(v, n):
+        v = v.reshape(n, HD)
+        a, b = v[:, :HD // 2].copy(), v[:, HD // 2:].copy()
+        v[:, :HD // 2], v[:, HD // 2:] = a * cs - b * sn, a * sn + b * cs
+        return v.reshape(-1)
+
+    def step():
+        w = layers[state["i"] % len(layers)]
+        state["i"] += 1
+        mm = lambda nm, v: r.matmul(shapes[nm][0], w[nm], shapes[nm][1], shapes[nm][2], v)
+        xn = norm(x0, an)
+        q, k, v = rope(mm("q", xn), H), rope(mm("k", xn), KV), mm("v", xn)
+        kc[pos * pb:] = r.kv_quantize_row(k)
+        vc[pos * pb:] = r.kv_quantize_row(v)
+        ao = r.attn_decode(q, kc, vc, H, KV, HD, 0, pos)
+        h = mm("o", ao) + x0
+        xn2 = norm(h, fn)
+        g, u = mm("gate", xn2), mm("up", xn2)
+        with np.errstate(over="ignore"):
+            act = (g / (np.float32(1) + np.exp(-g))) * u
+        return mm("down", act) + h
+    best, calls = _best_of(step, budget_s)
+    return best, calls
+
+
+def cpu_moe(r, budget_s=5.0):
+    """Config 5 on the CPU as the reference's expert_ffn runs it
+    (dense_forward.cpp:1524-1560, combine :4160-4181): per token, moe_route
+    (top-2, renormalised) and, per selected expert, matmul_q4_k for up and
+    gate, SiLU(gate) * up, matmul_q4_k for down, weighted sum. 64 tokens,
+    8 experts of 14336 x 4096 Q4_K (792 MB of weights)."""
+    from desireeia_amd import synth
+    E, F, X, T = 4096, 14336, 8, 64
+    wg = synth.gen_weights(synth.Q4_K, X * F, E, 50)
+    wu = synth.gen_weights(synth.Q4_K, X * F, E, 51)
+    wd = synth.gen_weights(synth.Q4_K, X * E, F, 52)
+    x = synth.gen_act((T, E), 53)
+    lg = synth.gen_act((T, X), 54)
+
+    def call():
+        out = np.zeros((T, E), np.float32)
+        for t in range(T):
+            ids, wts = r.moe_route(lg[t], 2, True)
+            for e, wt in zip(ids, wts):
+                e = int(e)
+                u = r.matmul(synth.Q4_K, wu[e * F:(e + 1) * F], F, E, x[t])
+                g = r.matmul(synth.Q4_K, wg[e * F:(e + 1) * F], F, E, x[t])
+                with np.errstate(over="ignore"):
+                    h = (g / (np.float32(1) + np.exp(-g))) * u
+                out[t] += np.float32(wt) * r.matmul(synth.Q4_K, wd[e * E:(e + 1) * E], E, F, h)
+        return out
+    best, calls = _best_of(call, budget_s, min_calls=1)
+    return best, calls
+
+
+def cpu_baseline(budget_s=12.0):
+    """The reference's own CPU operators (oracle/_ref, compiled from its
+    sources) timed on this host: `value` is matmul_q4_k at the headline's up
+    shape; `rows` cover the other configurations. Threads = the host's
+    physical cores, capped at this process's CPU share; the GEMV rows rotate
+    distinct weight copies totalling >= 4x the host's L3 (DRAM regime), best
+    of repeated calls (bench/kernel_bench.cpp:40-53, 112-132)."""
+    from desireeia_amd import synth
+    from oracle import oracle as orc
+    host = host_description()
+    r = orc.ref()
+    if r is None:
+        # the compiled reference is absent: time the oracle's scalar port on a sample
+        o = orc.oracle()
+        rows, cols = 14336, 4096
+        w = synth.gen_weights(synth.Q4_K, rows, cols, seed=99)
+        x = synth.gen_act(cols, 100)
+        best, calls = _best_of(lambda: o.matmul(synth.Q4_K, w, rows, cols, x, 0, 512), budget_s)
+        nbytes = rows * synth.row_bytes(synth.Q4_K, cols)
+        return {"value": round(nbytes / (best * rows / 512.0) / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"Q4_K GEMV 14336x4096, rows 0..511 timed and scaled, best of {calls}", "host": host}
+    threads = host["threads_used"]
+    r.set_threads(threads)
+    rot = max(4 * (host["l3_bytes"] or (64 << 20)), 264 << 20)
+    gbs, best, calls, ncopy, wset = cpu_gemv(r, synth.Q4_K, 14336, 4096, rot, budget_s, 99)
+    out = {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "reference",
+           "sample": f"Q4_K GEMV 14336x4096 (matmul_q4_k incl. its per-256 activation quantization), "
+                     f"{ncopy} distinct weight copies ({wset >> 20} MB, >= 4x L3), best of {calls} calls over "
+                     f"{budget_s:.0f} s, {threads} threads",
+           "host": host}
+    rows = {}
+    gbs, best, calls, ncopy, wset = cpu_gemv(r, synth.Q8_0, 4096, 4096, rot, 3.0, 31)
+    rows["gemv_q80_4096x4096"] = {"GBps": round(gbs, 2), "us": round(best * 1e6, 1),
+                                  "sample": f"matmul_q8_0 (config 1), {ncopy} copies ({wset >> 20} MB), best of {calls}"}
+    log(f"cpu reference gemv_q80: {rows['gemv_q80_4096x4096']}")
+    rows.update(cpu_rows(r))
+    best, calls = cpu_layer(r)
+    rows["layer_q4km_pos4096"] = {"ms_per_layer": round(best * 1e3, 3), "layers_per_s": round(1.0 / best, 1),
+                                  "GBps": round((LAYER_WEIGHT_BYTES + KV_READ_BYTES) / best / 1e9, 1),
+                                  "sample": f"config 4 decode step from the reference's matmul_q4_k/q6_k, "
+                                            f"kv_quantize_row, kv_dot/kv_axpy attention; numpy glue; best of {calls}"}
+    log(f"cpu reference layer: {rows['layer_q4km_pos4096']}")
+    best, calls = cpu_moe(r)
+    rows["moe_8x2_64tok"] = {"ms_per_call": round(best * 1e3, 1), "tokens_per_s": round(64 / best, 1),
+                             "sample": f"config 5 as expert_ffn: moe_route + matmul_q4_k per token and expert, "
+                                       f"best of {calls}"}
+    log(f"cpu reference moe: {rows['moe_8x2_64tok']}")
+    out["rows"] = rows
+    return out
+
+
 def cpu_rows(r, budget_s=3.0):
-    """The reference's CPU path for the other measured rows, on the same
-    shapes as their GPU lines: prefill GEMM (matmul_batch, Q4_K 14336x4096,
-    512 tokens), prefill attention (attention_prefill_q8, 512 tokens after
-    3584 cached positions, 32/8 heads of 128) and the output-head GEMV
-    (matmul_q6_k 128256x4096). Best of repeated calls over budget_s each."""
+    """The reference's CPU path for the prefill GEMM (matmul_batch, Q4_K
+    14336x4096, 512 tokens), prefill attention (attention_prefill_q8, 512
+    tokens after 3584 cached positions, 32/8 heads of 128) and the output-head
+    GEMV (matmul_q6_k 128256x4096). Best of repeated calls over budget_s each."""
     from desireeia_amd import synth
     from oracle import oracle as orc
     rows = {}
@@ -520,6 +728,11 @@ def main():
         torch.cuda.synchronize()
         log(f"copy: {args.steps} x {src.numel()} bytes")
         return
+    if args.only == "ceiling":
+        for nb in (33103872, 17858560):
+            per, best = stream_read_ceiling(dev, nb)
+            log(f"stream read {nb} B: {per} GB/s by waves per CU; best {best} GB/s ({best / HBM_PEAK_GBS:.3f})")
+        return
     gemm_shapes = {"gemm_q4k": (synth.Q4_K, 14336, 4096, 512), "gemm_q6k": (synth.Q6_K, 4096, 14336, 512),
                    "gemm_q80": (synth.Q8_0, 14336, 4096, 512)}
     if args.only in gemm_shapes:
@@ -572,6 +785,12 @@ def main():
         us = graph_time(fused, per, max(1, args.steps // per))
         log(f"step: {us:.2f} us, {(step_bytes(synth.Q4_K, 14336, 4096) + step_bytes(synth.Q4_K, 4096, 14336)) / us / 1e3:.1f} GB/s")
         return
+    if args.only and args.only.endswith("_f32") and args.only[:-4] in shapes:
+        qt, r, c = shapes[args.only[:-4]]
+        case = GemvCase(qt, r, c, 11, dev)
+        us, gbs = kernel_stats(case, launches=args.steps, fp32=True)
+        log(f"{args.only}: {us:.2f} us/launch, {gbs:.1f} GB/s")
+        return
     if args.only:
         qt, r, c = shapes[args.only]
         case = GemvCase(qt, r, c, 11, dev)
@@ -581,25 +800,32 @@ def main():
 
     cases = {k: GemvCase(qt, r, c, 11 + i, dev) for i, (k, (qt, r, c)) in enumerate(shapes.items())}
 
-    # ---- headline: Q4_K decode FFN GEMVs (up 14336x4096 + down 4096x14336), quantize + GEMV each
+    # ---- headline: Q4_K decode FFN GEMVs (up 14336x4096 + down 4096x14336), quantize + GEMV each.
+    # One graph holds exactly --steps steps (each on the next weight copy); it is
+    # replayed REPLAYS times, each replay timed on its own, bracketed by
+    # synchronisations; ms_per_step is the median replay.
     up, down = cases["q4k_up"], cases["q4k_down"]
 
     def step():
         up.step()
         down.step()
 
-    per_graph = max(len(up.mats), len(down.mats))
-    reps = max(1, args.steps // per_graph)
-    n_steps = reps * per_graph
+    REPLAYS = 10
+    n_steps = max(1, args.steps)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    us_step = graph_time(step, per_graph, reps, warmup_reps=1)
+    per_replay = replay_times(step, n_steps, REPLAYS, warmup_reps=1)
     wall = time.perf_counter() - t0
-    ms_per_step = us_step / 1e3
+    srt = sorted(per_replay)
+    us_med = 0.5 * (srt[(REPLAYS - 1) // 2] + srt[REPLAYS // 2])
+    us_best = srt[0]
+    ms_per_step = us_med / 1e3
     bytes_step = step_bytes(synth.Q4_K, 14336, 4096) + step_bytes(synth.Q4_K, 4096, 14336)
     value = bytes_step / (ms_per_step * 1e-3) / 1e9
+    distinct = min(n_steps, len(up.mats)) * up.mats[0].buf.numel() + min(n_steps, len(down.mats)) * down.mats[0].buf.numel()
+    log(f"headline step: median {us_med:.2f} us, best {us_best:.2f} us over {REPLAYS} replays of {n_steps} steps")
 
     # ---- per-kernel figures
     extra = {}
@@ -608,18 +834,39 @@ def main():
         extra[k] = {"shape": f"{c.rows}x{c.cols}", "kernel_us": round(us, 3), "kernel_GBps": round(gbs, 1),
                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
         log(f"{k}: {us:.2f} us  {gbs:.1f} GB/s  ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
-    # config 3: prefill GEMM (kernel alone; activations quantized beforehand)
+    # the two launches of the headline step, each alone (fp32 activation, quantized in-kernel)
+    for k in ("q4k_up", "q4k_down"):
+        c = cases[k]
+        us, gbs = kernel_stats(c, fp32=True)
+        extra[k + "_f32"] = {"shape": f"{c.rows}x{c.cols}", "kernel_us": round(us, 3), "kernel_GBps": round(gbs, 1),
+                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                             "bytes_per_launch": step_bytes(c.qtype, c.rows, c.cols)}
+        log(f"{k} fp32 activation: {us:.2f} us  {gbs:.1f} GB/s  ({100 * gbs / HBM_PEAK_GBS:.1f}% of HBM peak)")
+    # what a plain streaming read of the same size achieves on this device
+    ceil = {}
+    for nm, nb in (("33MB", bytes_step // 2), ("17.8MB", 17858560)):
+        per, best = stream_read_ceiling(dev, nb)
+        ceil[nm] = {"bytes": nb, "GBps_by_waves_per_cu": per, "best_GBps": best,
+                    "frac_hbm": round(best / HBM_PEAK_GBS, 4)}
+        log(f"stream-read ceiling {nm}: {best} GB/s ({per})")
+    extra["stream_read_ceiling"] = ceil
+    # config 3: prefill GEMM, kernel alone and with the activation quantization
     for k, (qt, r, c, t) in gemm_shapes.items():
         g = GemmCase(qt, r, c, t, 21, dev)
-        us = graph_time(g.kernel, 10, 5)
+        kt = replay_times(g.kernel, 10, 10)
+        us = sorted(kt)[len(kt) // 2]
+        us_q = sorted(replay_times(g.step, 10, 10))[5]
         tf = g.flops() / us / 1e6
-        extra[k] = {"shape": f"{t}x{c} . {c}x{r}", "kernel_us": round(us, 2), "TFLOPs": round(tf, 1),
-                    "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4), "frac_int8_mfma": round(tf / INT8_PEAK_TOPS, 4)}
-        log(f"{k}: {us:.1f} us  {tf:.1f} TFLOP/s")
+        extra[k] = {"shape": f"{t}x{c} . {c}x{r}", "kernel_us": round(us, 2), "kernel_us_best": round(min(kt), 2),
+                    "TFLOPs": round(tf, 1), "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4),
+                    "frac_int8_mfma": round(tf / INT8_PEAK_TOPS, 4),
+                    "quantize_plus_gemm_us": round(us_q, 2),
+                    "quantize_plus_gemm_TFLOPs": round(g.flops() / us_q / 1e6, 1)}
+        log(f"{k}: {us:.1f} us  {tf:.1f} TFLOP/s; with the activation quantization {us_q:.1f} us")
         del g
     # config 4: decode attention alone and the whole decoder layer
     ac = AttnCase(dev)
-    us = graph_time(ac.kernel, len(ac.caches), 3)
+    us = graph_time(ac.kernel, len(ac.caches), 10)
     extra["attn_decode_4097"] = {"kernel_us": round(us, 3), "GBps": round(KV_READ_BYTES / us / 1e3, 1),
                                  "frac_hbm": round(KV_READ_BYTES / us / 1e3 / HBM_PEAK_GBS, 4)}
     log(f"attention (32/8 heads, 4097 positions): {us:.2f} us")
@@ -633,7 +880,7 @@ def main():
     log(f"decoder layer: {us:.1f} us/layer  {gbs:.1f} GB/s")
     del lc
     mc = MoeCase(dev)
-    us = graph_time(mc.step, 4, 5)
+    us = graph_time(mc.step, 4, 10)
     gbs = mc.bytes() / us / 1e3
     extra["moe_8x2_64tok"] = {"us_per_call": round(us, 2), "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                               "tokens_per_s": round(mc.n_tok / us * 1e6, 1), "bytes_per_call": mc.bytes()}
@@ -641,7 +888,7 @@ def main():
     del mc
     # prefill (the layer path over a prompt chunk): attention alone and the layer
     pc = AttnPrefillCase(dev)
-    us = graph_time(pc.kernel, 4, 3)
+    us = graph_time(pc.kernel, 4, 5)
     tf = pc.flops() / us / 1e6
     extra["attn_prefill_512_after_3584"] = {
         "kernel_us": round(us, 2), "TFLOPs_alg": round(tf, 1), "frac_fp16_mfma_alg": round(tf / FP16_PEAK_TFLOPS, 4),
@@ -663,24 +910,30 @@ def main():
                                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "topk104_draw_us": round(us_sel, 2)}
     log(f"output head 128256x4096 Q6_K: {us:.1f} us  {gbs:.1f} GB/s; top-104 + draw {us_sel:.1f} us")
     del hc
-    dom = extra["q4k_up"]
+    # the dominant kernel of the timed step: the down launch (4096x14336, the
+    # longer of the two), fp32 activation quantized in-kernel
+    dom = extra["q4k_down_f32"]
     roofline = {"bound": "hbm", "achieved": dom["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["kernel_GBps"] / HBM_PEAK_GBS, 4), "traffic": recorded_traffic(),
                 "traffic_source": os.path.relpath(TRAFFIC_FILE, ROOT),
-                "kernel": "gemv_flat_kernel<Q4_K> 14336x4096 (dq_gemv)",
-                "bytes_per_launch": gemv_kernel_bytes(synth.Q4_K, 14336, 4096)}
+                "kernel": "gemv_flat16_kernel (dq_gemv_f32, Q4_K 4096x14336: per-256 activation quantization "
+                          "in-kernel + GEMV), the down launch of the headline step",
+                "launch_us": dom["kernel_us"], "bytes_per_launch": dom["bytes_per_launch"],
+                "ceiling_same_size_GBps": ceil["33MB"]["best_GBps"]}
 
-    cpu = None if args.no_cpu else cpu_baseline_q4k()
+    cpu = None if args.no_cpu else cpu_baseline()
 
     out = {
         "metric": METRIC, "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": n_steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "config 2: Q4_K decode GEMV, up 14336x4096 + down 4096x14336, "
-                               "per-256 activation quantization + GEMV per matrix (one launch each), "
-                               f"weights rotated over >= {ROTATE_BYTES >> 20} MB",
+                               "per-256 activation quantization + GEMV per matrix (one launch each)",
                    "bytes_per_step": bytes_step, "frac_hbm_step": round(value / HBM_PEAK_GBS, 4),
-                   "wall_s": round(wall, 3)},
+                   "replays": REPLAYS, "steps_per_replay": n_steps,
+                   "us_per_step_median": round(us_med, 3), "us_per_step_best": round(us_best, 3),
+                   "us_per_step_replays": [round(t, 3) for t in per_replay],
+                   "distinct_weight_bytes": int(distinct), "wall_s": round(wall, 3)},
         "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
     }
     print(json.dumps(out))

@@ -1,4 +1,7 @@
-// dq_runtime.hip - library version and device query.
+// dq_runtime.hip - library version, device query, and the streaming-read
+// probe the benchmark uses to measure the device's read ceiling at a GEMV's
+// size (a read of N bytes with no arithmetic: what a bandwidth-bound kernel
+// of that size can at best approach on this device).
 #include "dq_common.h"
 
 extern "C" int dq_version(void) { return 1; }
@@ -7,4 +10,47 @@ extern "C" int dq_device_count(void) {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess) return 0;
     return n;
+}
+
+namespace {
+
+constexpr int PROBE_LOADS = 4;  // 16-byte loads per lane in flight: 4 KB per wave
+
+// Wave w of the grid reads the 4 KB chunks w, w + n_waves, ...: every load
+// instruction of a wave covers one contiguous kilobyte. The loaded words are
+// folded into one value per lane, stored only if it equals a value the
+// caller chose never to occur, so no load can be removed.
+__global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restrict__ src, size_t n_chunks,
+                                                          uint32_t* __restrict__ sink, uint32_t never) {
+    const int lane = threadIdx.x & 63;
+    const size_t wave = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const size_t n_waves = ((size_t)gridDim.x * blockDim.x) >> 6;
+    uint32_t acc = 0;
+    for (size_t c = wave; c < n_chunks; c += n_waves) {
+        const uint4* p = src + c * (64 * PROBE_LOADS) + lane;
+        uint4 v[PROBE_LOADS];
+#pragma unroll
+        for (int i = 0; i < PROBE_LOADS; ++i) v[i] = p[64 * i];
+#pragma unroll
+        for (int i = 0; i < PROBE_LOADS; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    }
+    if (acc == never) sink[0] = acc;
+}
+
+}  // namespace
+
+extern "C" int dq_stream_read(const void* d_src, size_t bytes, uint32_t waves_per_cu, uint32_t* d_sink,
+                              uint32_t never, void* stream) {
+    if (!d_src || !d_sink || waves_per_cu == 0 || waves_per_cu > 32) return DQ_ERR_INVALID_ARG;
+    constexpr size_t CHUNK = 64 * 16 * PROBE_LOADS;
+    if (bytes % CHUNK || reinterpret_cast<uintptr_t>(d_src) % 16) return DQ_ERR_NOT_SUPPORTED;
+    if (bytes == 0) return DQ_OK;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return DQ_ERR_IO;
+    const unsigned grid = (unsigned)((size_t)cus * waves_per_cu / 4);  // 4 waves per workgroup
+    stream_read_kernel<<<grid > 0 ? grid : 1, 256, 0, (hipStream_t)stream>>>(
+        static_cast<const uint4*>(d_src), bytes / CHUNK, d_sink, never);
+    return dq_launch_status();
 }

@@ -207,6 +207,21 @@ int dqo_dequantize_row(int type, const void* src, float* dst, int64_t n) {
 /* Activation quantizers                                                    */
 /* ------------------------------------------------------------------------ */
 
+/* x * id rounded to nearest-even and clamped to +-127. For every block
+ * whose maximum |x| is at least 127 / FLT_MAX (about 3.7e-37) x * id is
+ * finite and this is the reference's clamp(lrintf(x * id)). Below that
+ * (and above the point where d rounds to 0) id overflows to inf and the
+ * reference's conversion of +-inf / NaN is not defined by its source: its
+ * AVX2 build packs the integer-indefinite value into -128 for every element
+ * and its scalar path is undefined behaviour. Here, as on the GPU, the
+ * conversion saturates: +-inf -> +-127, NaN (x = 0) -> 0. */
+static inline long rint_sat127(float v) {
+    if (v != v) return 0;
+    if (v >= 127.0f) return 127;
+    if (v <= -127.0f) return -127;
+    return lrintf(v);
+}
+
 /* Per-32 recipe, core/quant.cpp:15-50 (quantize_q8_0): amax, d = amax/127,
  * id = 1/d, q = clamp(lrintf(x*id), +-127). */
 void dqo_quantize_q8_0(const float* x, size_t n, int8_t* q, float* dout) {
@@ -221,10 +236,7 @@ void dqo_quantize_q8_0(const float* x, size_t n, int8_t* q, float* dout) {
         const float id = d > 0.0f ? 1.0f / d : 0.0f;
         dout[b] = d;
         for (int i = 0; i < QK; ++i) {
-            long v = lrintf(p[i] * id);
-            if (v > 127) v = 127;
-            if (v < -127) v = -127;
-            q[b * QK + i] = (int8_t)v;
+            q[b * QK + i] = (int8_t)rint_sat127(p[i] * id);
         }
     }
 }
@@ -262,10 +274,7 @@ void dqo_quantize_q8k_rep(const float* x, size_t n, int8_t* q, float* d32, int32
         const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
         const float id = d > 0.0f ? 127.0f / amax : 0.0f;
         for (int j = 0; j < QKK; ++j) {
-            long v = lrintf(xs[j] * id);
-            if (v > 127) v = 127;
-            if (v < -127) v = -127;
-            q[s * QKK + j] = (int8_t)v;
+            q[s * QKK + j] = (int8_t)rint_sat127(xs[j] * id);
         }
         for (int sb = 0; sb < 8; ++sb) {
             int32_t acc = 0;
@@ -294,11 +303,7 @@ void dqo_kv_quantize_row(const float* x, size_t dim, uint8_t* out) {
         blk[1] = (uint8_t)(h >> 8);
         for (size_t i = 0; i < 32; ++i) {
             long v = 0;
-            if (i < len) {
-                v = lrintf(x[start + i] * id);
-                if (v > 127) v = 127;
-                if (v < -127) v = -127;
-            }
+            if (i < len) v = rint_sat127(x[start + i] * id);
             blk[2 + i] = (uint8_t)(int8_t)v;
         }
     }
@@ -1088,4 +1093,47 @@ int dqo_moe_ffn(int fmt, const uint8_t* wgate, const uint8_t* wup, const uint8_t
     free(gate);
     free(fo);
     return rc ? DQO_ERR_NOT_SUPPORTED : DQO_OK;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Exhaustive identity checks (see dq_oracle.h)                             */
+/* ------------------------------------------------------------------------ */
+uint64_t dqo_check_div127(uint32_t lo, uint32_t hi) {
+    uint64_t bad = 0;
+    for (uint64_t u = lo; u < hi; ++u) {
+        const float a = u2f((uint32_t)u);
+        if (a != a || isinf(a)) continue;
+        const float x = (float)((double)a * (1.0 / 127.0));
+        const float y = a / 127.0f;
+        bad += f2u(x) != f2u(y);
+    }
+    return bad;
+}
+
+uint64_t dqo_check_rint_byte(uint32_t lo, uint32_t hi) {
+    uint64_t bad = 0;
+    for (uint64_t u = lo; u < hi; ++u) {
+        const float p = u2f((uint32_t)u);
+        if (p != p || !(fabsf(p) <= 128.0f)) continue;
+        const uint8_t got = (uint8_t)(f2u(p + 12582912.0f) & 0xFF);
+        const uint8_t want = (uint8_t)(int8_t)(int)rintf(p);
+        bad += got != want;
+    }
+    return bad;
+}
+
+uint64_t dqo_check_id_bound(uint32_t lo, uint32_t hi) {
+    uint64_t bad = 0;
+    for (uint64_t u = lo; u < hi; ++u) {
+        const float a = u2f((uint32_t)u);
+        if (a != a || isinf(a) || !(a > 0.0f)) continue;
+        const float d = a / 127.0f;
+        if (d > 0.0f) {
+            const float id32 = 1.0f / d;
+            if (!isinf(id32)) bad += rintf(a * id32) > 127.0f;
+        }
+        const float id256 = 127.0f / a;
+        if (!isinf(id256)) bad += rintf(a * id256) > 127.0f;
+    }
+    return bad;
 }

@@ -143,6 +143,19 @@ int dqo_moe_ffn(int fmt, const uint8_t* wgate, const uint8_t* wup, const uint8_t
                 const float* x, const float* logits, uint32_t n_tok, uint32_t k_used,
                 int norm_w, float* out, uint32_t t0, uint32_t t1);
 
+/* Exhaustive checks, over a range [lo, hi) of float bit patterns, of the
+ * float identities the GPU quantizers rely on instead of a division and a
+ * clamped conversion. Each returns the number of inputs where the identity
+ * fails (NaN and inf inputs are skipped).
+ *   div127:    (float)((double)a * (1.0 / 127.0)) == a / 127.0f
+ *   rint_byte: low byte of bits(p + 1.5 * 2^23) == (int8_t)rintf(p), |p| <= 128
+ *   id_bound:  for a > 0 with finite id, rint(a * id) <= 127 for both
+ *              id = 1 / (a / 127) (per-32) and id = 127 / a (per-256), so
+ *              |x * id| never needs the clamp when |x| <= a. */
+uint64_t dqo_check_div127(uint32_t lo, uint32_t hi);
+uint64_t dqo_check_rint_byte(uint32_t lo, uint32_t hi);
+uint64_t dqo_check_id_bound(uint32_t lo, uint32_t hi);
+
 #ifdef __cplusplus
 }
 #endif

@@ -284,6 +284,7 @@ class Ref:
         L.dqr_sample_candidates.restype = ctypes.c_int32
         L.dqr_sample_candidates.argtypes = [c_f, ctypes.c_int32, c_f, c_f, c_f, c_f, ctypes.c_int32, c_u32, c_u32, c_p,
                                             c_p, c_size, c_p, c_size, c_p]
+        L.dqr_attn_decode_q8.argtypes = [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p]
         L.dqr_attention_prefill_q8.argtypes = [c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_p, c_size, c_size,
                                                c_u32, c_u32, c_f]
 
@@ -374,6 +375,14 @@ class Ref:
         (token, u) where u is the uniform number the device draw is given."""
         return _ref_sample(self.L, ids, vals, list(hist), temperature, top_k, top_p, repeat, freq, present, last_n,
                            seed, skip)
+
+    def attn_decode(self, q, kc, vc, n_head, n_head_kv, hd, cc_start, pos):
+        """Decode attention composed from the reference's kv_dot_q8_0 /
+        kv_axpy_q8_0 over heads on its thread pool (dense_forward.cpp:4014-4066)."""
+        out = np.zeros(n_head * hd, np.float32)
+        self.L.dqr_attn_decode_q8(_p(np.ascontiguousarray(q, np.float32)), _p(np.ascontiguousarray(kc, np.uint8)),
+                                  _p(np.ascontiguousarray(vc, np.uint8)), n_head, n_head_kv, hd, cc_start, pos, _p(out))
+        return out
 
     def attn_prefill(self, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0, n_swa=0, q_dim=None, out=None):
         return _attn_prefill(self.L.dqr_attention_prefill_q8, q_all, kc, vc, n_tok, n_head, n_head_kv, hd, pos0,

@@ -15,6 +15,11 @@
 //   kv_quantize_row/dot/axpy ...... kv/kv_quant.cpp:31,58,102
 //   moe_route ..................... models/moe_route.cpp:77
 //   attention_prefill_cpu_q8 ...... core/attn_cpu.cpp:128
+//   decode attention .............. models/dense_forward.cpp:4014-4066: per
+//                                   query head (parallel_units over heads)
+//                                   kv_dot_q8_0 scores, softmax_inplace
+//                                   (:805-821, restated: float max, double
+//                                   sum), kv_axpy_q8_0 accumulation
 //   Sampler::sample_candidates .... core/sampler.cpp:298 (draw_uniform :131)
 //   ThreadPool::set_thread_override core/thread_pool.cpp:36
 #include "core/engine.h"
@@ -25,6 +30,8 @@
 #include "core/sampler.h"
 #include "quant/quant.h"
 
+#include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <vector>
 
@@ -103,6 +110,38 @@ int dqr_attention_prefill_q8(const float* q_all, float* out, uint32_t n_tok, uin
                              size_t row_bytes, size_t pos_bytes, uint32_t pos0, uint32_t n_swa, float inv_d) {
     return attention_prefill_cpu_q8(q_all, out, n_tok, n_head, hpk, hd, q_dim, kbase, vbase, row_bytes, pos_bytes,
                                     pos0, n_swa, inv_d);
+}
+
+// Decode attention of one token over positions [cc_start, pos] of a Q8_0
+// cache laid out [pos][kv head][hd/32 blocks], as the engine's CPU decode
+// step runs it (quantized-KV branch, no ALiBi, no window).
+void dqr_attn_decode_q8(const float* q, const uint8_t* kc, const uint8_t* vc, uint32_t n_head, uint32_t n_head_kv,
+                        uint32_t hd, uint32_t cc_start, uint32_t pos, float* out) {
+    const size_t row_bytes = (size_t)hd / 32 * sizeof(block_q8_0);
+    const size_t pos_bytes = (size_t)n_head_kv * row_bytes;
+    const uint32_t hpk = n_head / n_head_kv;
+    const float inv_d = 1.0f / std::sqrt((float)hd);
+    std::vector<float> scores((size_t)n_head * (pos + 1));
+    parallel_units(n_head, [&](size_t h0, size_t h1) {
+        for (uint32_t h = (uint32_t)h0; h < (uint32_t)h1; ++h) {
+            float* s = scores.data() + (size_t)h * (pos + 1);
+            const float* qh = q + (size_t)h * hd;
+            const uint8_t* kb = kc + (size_t)(h / hpk) * row_bytes;
+            const uint8_t* vb = vc + (size_t)(h / hpk) * row_bytes;
+            for (uint32_t cc = cc_start; cc <= pos; ++cc) s[cc] = kv_dot_q8_0(qh, kb + cc * pos_bytes, hd) * inv_d;
+            float m = -INFINITY;
+            for (uint32_t cc = cc_start; cc <= pos; ++cc) m = std::max(m, s[cc]);
+            double sum = 0.0;
+            for (uint32_t cc = cc_start; cc <= pos; ++cc) {
+                s[cc] = expf(s[cc] - m);
+                sum += s[cc];
+            }
+            for (uint32_t cc = cc_start; cc <= pos; ++cc) s[cc] /= (float)sum;
+            float* oh = out + (size_t)h * hd;
+            for (uint32_t d = 0; d < hd; ++d) oh[d] = 0.0f;
+            for (uint32_t cc = cc_start; cc <= pos; ++cc) kv_axpy_q8_0(oh, vb + cc * pos_bytes, hd, s[cc]);
+        }
+    });
 }
 
 // The host draw over candidates, and the uniform number the device path is

@@ -90,3 +90,16 @@ def test_quantize_q8_1_blocks(gpu, orc):
     # its dequantization is the q8_0 one
     y = orc.dequantize_row(synth.Q8_1, blk.reshape(-1), 4096)
     assert np.allclose(y, x, atol=np.abs(x).max() / 127)
+
+
+@pytest.mark.parametrize("kind", [ops.ACT_Q8_0, ops.ACT_Q8K_REP])
+def test_quantize_act_tiny_blocks(gpu, orc, kind):
+    """Blocks whose maximum is near or below 127/FLT_MAX (id overflows to
+    inf), subnormal and flushed-to-zero scales: the oracle's saturating
+    conversion, bit for bit."""
+    rng = np.random.default_rng(12)
+    scales = [1e-30, 1e-36, 3e-37, 1e-38, 1e-40, 1e-44, 1.0, 1e-39]
+    x = np.concatenate([(rng.standard_normal(256) * s).astype(np.float32) for s in scales])
+    x[5::256] = 0.0
+    a = ops.quantize_act(torch.from_numpy(x).to(gpu), kind)
+    _check_act(orc, x, kind, a)

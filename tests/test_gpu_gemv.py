@@ -132,9 +132,13 @@ def test_gemv_group_residual_and_errors(gpu, orc):
         ops.gemv_group([a] * 5, act)
 
 
+# 5120 and 8192 columns: the per-256 kind without a K split in 8-wave
+# workgroups (4096 < cols <= 8192), e.g. hidden sizes 5120 and 8192
 @pytest.mark.parametrize("qtype,rows,cols", [(synth.Q4_K, 14336, 4096), (synth.Q4_K, 4096, 14336),
                                              (synth.Q6_K, 4096, 14336), (synth.Q8_0, 4096, 4096),
-                                             (synth.Q4_0, 333, 4160), (synth.Q4_K, 5, 49152)])
+                                             (synth.Q4_0, 333, 4160), (synth.Q4_K, 5, 49152),
+                                             (synth.Q4_K, 1000, 5120), (synth.Q6_K, 513, 8192),
+                                             (synth.Q8_0, 700, 5120), (synth.Q4_0, 300, 8192)])
 def test_gemv_f32_matches_quantize_then_gemv(gpu, qtype, rows, cols):
     """dq_gemv_f32 (activation quantized in-kernel) is bit-identical to
     dq_quantize_act + dq_gemv."""
@@ -150,12 +154,15 @@ def test_gemv_f32_matches_quantize_then_gemv(gpu, qtype, rows, cols):
 def _edge_activation(cols, seed):
     """Per 256-column chunk: all zeros; amax 127 with exact .5 ties (id = 1,
     so rint must round half to even); magnitudes near 1e30 and 1e-30; one
-    lone nonzero; otherwise N(0,1)."""
+    lone nonzero; magnitudes near 1e-38 (id overflows to inf: the saturating
+    branch); subnormals of mixed sign with exact zeros (subnormal maximum);
+    otherwise N(0,1)."""
     x = synth.gen_act(cols, seed=seed).astype(np.float32)
     ties = np.arange(-60, 60, dtype=np.float32) + 0.5
+    tiny = np.random.default_rng(seed + 1).integers(-4000, 4001, 256).astype(np.int32)
     for c in range(cols // 256):
         sl = slice(256 * c, 256 * c + 256)
-        kind = c % 5
+        kind = c % 7
         if kind == 0:
             x[sl] = 0.0
         elif kind == 1:
@@ -166,15 +173,21 @@ def _edge_activation(cols, seed):
             x[sl] *= np.float32(1e30)
         elif kind == 3:
             x[sl] *= np.float32(1e-30)
-        else:
+        elif kind == 4:
             x[sl] = 0.0
             x[256 * c + 77] = -3.25
+        elif kind == 5:
+            x[sl] *= np.float32(1e-38)
+        else:
+            # k * 2^-149: subnormals (|k| <= 4000), some exactly zero
+            x[sl] = (tiny.astype(np.float64) * 2.0 ** -149).astype(np.float32)
     return x
 
 
 @pytest.mark.parametrize("qtype,rows,cols", [(synth.Q4_K, 1000, 4096), (synth.Q4_K, 256, 14336),
                                              (synth.Q8_0, 700, 4096), (synth.Q4_0, 300, 14336),
-                                             (synth.Q6_K, 513, 14336)])
+                                             (synth.Q6_K, 513, 14336), (synth.Q4_K, 1000, 5120),
+                                             (synth.Q6_K, 513, 8192)])
 def test_gemv_f32_quantizer_edges(gpu, qtype, rows, cols):
     """The in-kernel quantizer of dq_gemv_f32 gives the same integers and
     scales as dq_quantize_act on zero blocks, .5 ties, extreme magnitudes and
@@ -202,3 +215,19 @@ def test_gemv_group_f32_mixed_kinds(gpu, orc):
     wide = ops.QuantMatrix.from_gguf(synth.Q4_K, synth.gen_weights(synth.Q4_K, 2, 65536, seed=1), 2, 65536)
     with pytest.raises(_lib.DqError, match="NOT_SUPPORTED"):
         ops.matmul(wide, torch.zeros(65536, device=gpu))
+
+
+@pytest.mark.parametrize("cols", [5120, 8192])
+def test_gemv_group_f32_wide_matches_quantize_then_group(gpu, cols):
+    """The grouped fp32 form at 4096 < cols <= 8192 (8-wave workgroups, no K
+    split, one quantization pass): bit-identical to dq_quantize_act +
+    dq_gemv_group on normal and edge activations."""
+    print(f"gemv_group_f32 cols={cols}", flush=True)
+    specs = [(synth.Q4_K, 1024), (synth.Q4_K, 256), (synth.Q6_K, 300)]
+    mats = [ops.QuantMatrix.from_gguf(qt, synth.gen_weights(qt, r, cols, seed=r + cols), r, cols) for qt, r in specs]
+    for x in (synth.gen_act(cols, seed=cols), _edge_activation(cols, seed=cols + 1)):
+        xd = torch.from_numpy(x).to(gpu)
+        fused = ops.matmul_group(mats, xd)
+        two = ops.gemv_group(mats, ops.quantize_act(xd, ops.ACT_Q8K_REP))
+        for a, b in zip(fused, two):
+            assert torch.equal(a, b)

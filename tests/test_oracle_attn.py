@@ -257,3 +257,17 @@ def test_rope_neox(orc):
 def test_silu(orc):
     for v in (-20.0, -1.0, 0.0, 0.5, 3.0, 30.0):
         assert abs(orc.L.dqo_silu(v) - v / (1 + np.exp(-v))) <= 1e-6 * max(1.0, abs(v))
+
+
+def test_decode_attention_vs_reference_operators(orc, ref):
+    """The oracle's decode attention against the same loop over the compiled
+    reference's kv_dot_q8_0 / kv_axpy_q8_0 (the timed CPU baseline of the
+    attention row), GQA 32/8 heads over 300 positions from cc_start 7."""
+    rng = np.random.default_rng(3)
+    n_head, n_kv, hd, pos = 32, 8, 128, 299
+    kc = orc.kv_quantize_row(rng.standard_normal((pos + 1) * n_kv * hd).astype(np.float32))
+    vc = orc.kv_quantize_row(rng.standard_normal((pos + 1) * n_kv * hd).astype(np.float32))
+    q = (0.3 * rng.standard_normal(n_head * hd)).astype(np.float32)
+    a = orc.attn_decode(q, kc, vc, n_head, n_kv, hd, 7, pos)
+    b = ref.attn_decode(q, kc, vc, n_head, n_kv, hd, 7, pos)
+    assert np.linalg.norm(a - b) / np.linalg.norm(b) <= 1e-6

@@ -1,6 +1,8 @@
 """Activation quantizers of the oracle (reference core/quant.cpp:15-50,
 core/matmul.cpp:1660-1778, kv/kv_quant.cpp:31-56): closed-form known answers
 and bit-exact agreement with the compiled reference."""
+import os
+
 import numpy as np
 
 from desireeia_amd import synth
@@ -89,3 +91,80 @@ def test_kv_quantize_bitexact_vs_reference_and_roundtrip(orc, ref):
     # LE/tests/selftest.cpp:1931-1960: round trip rel-RMS < 1% at dim 512
     y = orc.dequantize_row(synth.Q8_0, a, 512)
     assert np.sqrt(np.mean((y - x) ** 2)) / np.sqrt(np.mean(x ** 2)) < 0.01
+
+
+def _tiny_block_input():
+    """Blocks whose maximum spans the range where id = 1/d or 127/amax
+    overflows: 1e-30 (finite id), 1e-36, 3e-37 (just above 127/FLT_MAX),
+    1e-38, 1e-40 (subnormal maximum), 1e-44 (d rounds to 0), mixed signs and
+    an exact zero in each block."""
+    rng = np.random.default_rng(11)
+    scales = [1e-30, 1e-36, 3e-37, 1e-38, 1e-40, 1e-44, 1.0, 1e-39]
+    x = np.concatenate([(rng.standard_normal(256) * s).astype(np.float32) for s in scales])
+    x[5::256] = 0.0
+    return x, scales
+
+
+def test_tiny_blocks_saturate(orc, ref):
+    """Where the block maximum is at least 127/FLT_MAX the oracle is the
+    reference bit for bit. Below it id overflows to inf and the reference's
+    conversion of +-inf/NaN is not defined by its source: compiled here, its
+    per-256 AVX2 quantizer writes -128 in every slot and its per-32 ones 0
+    (lrintf's overflow value truncated to int32). The oracle, like the GPU
+    kernels, saturates instead: sign(x) * 127, 0 for x = 0, with d = amax / 127
+    kept."""
+    x, scales = _tiny_block_input()
+    for kind in ("q8k", "q8_0", "kv"):
+        for b, s in enumerate(scales):
+            xb = x[256 * b:256 * (b + 1)]
+            if kind == "q8k":
+                q, d, isum = orc.quantize_q8k_rep(xb)
+                rq, rd, _ = ref.quantize_q8k_rep(xb)
+            elif kind == "q8_0":
+                q, d, isum, _ = orc.quantize_q8_1(xb)
+                rq, rd = ref.quantize_q8_0(xb)
+            else:
+                q = orc.kv_quantize_row(xb).reshape(-1, 34)[:, 2:].view(np.int8).reshape(-1)
+                rq = ref.kv_quantize_row(xb).reshape(-1, 34)[:, 2:].view(np.int8).reshape(-1)
+            if kind != "kv":
+                assert np.array_equal(d.view(np.uint32), rd.view(np.uint32))
+            blk = 256 if kind == "q8k" else 32
+            for j in range(0, 256, blk):
+                xs, qs, rqs = xb[j:j + blk], q[j:j + blk], rq[j:j + blk]
+                amax = np.float32(np.abs(xs).max())
+                dd = np.float32(amax / np.float32(127))
+                with np.errstate(over="ignore", divide="ignore"):
+                    idv = np.float32(127) / amax if kind == "q8k" else np.float32(1) / dd
+                if dd == 0:
+                    assert not qs.any() and not rqs.any()
+                elif np.isfinite(idv):
+                    assert np.array_equal(qs, rqs)
+                else:
+                    assert np.array_equal(qs, (np.sign(xs) * 127).astype(np.int8))
+                    assert (rqs == (-128 if kind == "q8k" else 0)).all()  # the reference's overflow
+
+
+def _run_chunks(fn, lo, hi, n=16):
+    """fn over [lo, hi) in n chunks on threads (ctypes releases the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+    edges = np.linspace(lo, hi, n + 1).astype(np.uint64)
+    with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:
+        return sum(ex.map(lambda i: int(fn(int(edges[i]), int(edges[i + 1]))), range(n)))
+
+
+def test_quantizer_identities_exhaustive(orc):
+    """The float identities the GPU quantizers use in place of a division and
+    a clamped conversion hold for every input (oracle dqo_check_*):
+    amax / 127 as a double product, rint as the low byte of p + 1.5 * 2^23,
+    and |x * id| <= 127 without a clamp wherever id is finite."""
+    import ctypes
+    L = orc.L
+    for nm in ("dqo_check_div127", "dqo_check_rint_byte", "dqo_check_id_bound"):
+        getattr(L, nm).restype = ctypes.c_uint64
+        getattr(L, nm).argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+    pos_end = 0x7F800000  # +inf: every finite non-negative float below it
+    assert _run_chunks(L.dqo_check_div127, 0, pos_end) == 0
+    assert _run_chunks(L.dqo_check_id_bound, 1, pos_end) == 0
+    m128 = 0x43000001  # bits of 128.0f, plus one
+    assert _run_chunks(L.dqo_check_rint_byte, 0, m128) == 0
+    assert _run_chunks(L.dqo_check_rint_byte, 0x80000000, 0x80000000 + m128) == 0
