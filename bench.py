@@ -406,27 +406,29 @@ def recorded_traffic():
 
 def stream_read_ceiling(dev, nbytes, reps=20):
     """The device's streaming-read rate at one GEMV's size: dq_stream_read of
-    nbytes over buffers rotated across >= 640 MB (every byte from HBM), one
-    launch per call in a graph, at 8, 12, 16 and 24 waves per CU. Returns
-    {waves_per_cu: GB/s} and the best."""
+    nbytes (rounded up to 16 KB) over buffers rotated across >= 640 MB (every
+    byte from HBM), one launch per call in a graph, over 4, 8 and 16 KB in
+    flight per wave and 4, 8 and 16 waves per CU. Returns {"waves/CU x KB":
+    GB/s} and the best."""
     import torch
     from desireeia_amd import _lib, ops
     lib = _lib.load()
-    nbytes = -(-nbytes // 4096) * 4096
+    nbytes = -(-nbytes // 16384) * 16384
     ncopy = max(2, -(-ROTATE_BYTES // nbytes))
     bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev) for _ in range(ncopy)]
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
     out = {}
-    for wpc in (8, 12, 16, 24):
-        i = [0]
+    for depth in (4, 8, 16):
+        for wpc in (4, 8, 16):
+            i = [0]
 
-        def call():
-            b = bufs[i[0]]
-            i[0] = (i[0] + 1) % len(bufs)
-            _lib.check(lib.dq_stream_read(ops._ptr(b), nbytes, wpc, ops._ptr(sink), 0x9E3779B9, ops._stream()),
-                       "dq_stream_read")
-        us = graph_time(call, ncopy, reps)
-        out[wpc] = round(nbytes / us / 1e3, 1)
+            def call():
+                b = bufs[i[0]]
+                i[0] = (i[0] + 1) % len(bufs)
+                _lib.check(lib.dq_stream_read(ops._ptr(b), nbytes, wpc, depth, ops._ptr(sink), 0x9E3779B9,
+                                              ops._stream()), "dq_stream_read")
+            us = graph_time(call, ncopy, reps)
+            out[f"{wpc}x{depth}KB"] = round(nbytes / us / 1e3, 1)
     del bufs
     return out, max(out.values())
 
@@ -846,7 +848,7 @@ def main():
     ceil = {}
     for nm, nb in (("33MB", bytes_step // 2), ("17.8MB", 17858560)):
         per, best = stream_read_ceiling(dev, nb)
-        ceil[nm] = {"bytes": nb, "GBps_by_waves_per_cu": per, "best_GBps": best,
+        ceil[nm] = {"bytes": nb, "GBps_by_shape": per, "best_GBps": best,
                     "frac_hbm": round(best / HBM_PEAK_GBS, 4)}
         log(f"stream-read ceiling {nm}: {best} GB/s ({per})")
     extra["stream_read_ceiling"] = ceil

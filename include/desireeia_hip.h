@@ -57,12 +57,13 @@ int dq_version(void);
 int dq_device_count(void);
 
 /* Streaming-read probe (no counterpart in the reference: it measures this
- * device's read ceiling for the benchmark). Reads `bytes` (a multiple of 4096,
- * 16-byte aligned) once with waves_per_cu (1..32) waves per compute unit,
- * each wave reading 4 KB per step as 64 lanes x 4 x 16 contiguous bytes.
- * Writes d_sink[0] only if the XOR of the words equals `never`. */
-int dq_stream_read(const void* d_src, size_t bytes, uint32_t waves_per_cu, uint32_t* d_sink, uint32_t never,
-                   void* stream);
+ * device's read ceiling for the benchmark). Reads `bytes` (a multiple of
+ * depth_kb KiB, 16-byte aligned) once with waves_per_cu (1..32) waves per
+ * compute unit; each wave reads depth_kb (4, 8 or 16) KiB per step, all loads
+ * of a step in flight together, 64 lanes x 16 contiguous bytes per load
+ * instruction. Writes d_sink[0] only if the XOR of the words equals `never`. */
+int dq_stream_read(const void* d_src, size_t bytes, uint32_t waves_per_cu, uint32_t depth_kb, uint32_t* d_sink,
+                   uint32_t never, void* stream);
 
 /* Replaces desireeia_dequantize_row (quant/quant.cpp:912-984) for the on-path
  * types Q4_0, Q8_0, Q8_1, Q4_K, Q6_K: GGUF blocks in, n fp32 values out,
