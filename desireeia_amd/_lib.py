@@ -32,6 +32,7 @@ SIGNATURES = {
     "dq_attn_workspace_bytes": (c_int, [c_u32, c_u32, c_u32, c_u32, ctypes.POINTER(c_size)]),
     "dq_attn_decode_q8": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_u32, c_p, c_p, c_size,
                                   c_p]),
+    "dq_attn_decode_q8_noalloc": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_u32, c_p, c_p]),
     "dq_attn_decode_q8_act": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_u32, c_p, c_p, c_p,
                                       c_p, c_p, c_size, c_p]),
     "dq_attn_rope_kv_decode": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p,

@@ -22,6 +22,7 @@
 // order than the reference's (the reference sums the softmax denominator in
 // double); results agree to ~1e-6 relative.
 #include <cstdlib>
+#include <mutex>
 
 #include "dq_common.h"
 
@@ -500,6 +501,32 @@ int attn_run(const float* d_q, const float* d_k, const float* d_v, const float* 
     return rc;
 }
 
+// Scratch of the allocation-free entry point: the tile records in a
+// file-scope device array, one per device the library runs on, held until the
+// process ends. Host code never names the array in a kernel argument or a
+// copy: its host-side name is not a device address. The device address comes
+// from hipGetSymbolAddress, looked up once per device with that device
+// current, and is what the kernels are given.
+constexpr size_t NOALLOC_SCRATCH_BYTES = 16u << 20;
+__device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES];
+
+// The device address of this device's scratch array (NULL on failure).
+void* scratch_ptr() {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
 }  // namespace
 
 extern "C" {
@@ -527,6 +554,19 @@ int dq_attn_decode_q8(const float* d_q, const void* d_kc, const void* d_vc, uint
                       float* d_out, void* d_work, size_t work_bytes, void* stream) {
     return attn_run(d_q, nullptr, nullptr, nullptr, d_kc, d_vc, n_head, n_head_kv, hd, cc_start, pos, d_pos, n_ctx,
                     d_out, d_work, work_bytes, nullptr, nullptr, nullptr, stream);
+}
+
+int dq_attn_decode_q8_noalloc(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head,
+                              uint32_t n_head_kv, uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos,
+                              uint32_t n_ctx, float* d_out, void* stream) {
+    if (!d_q || !d_kc || !d_vc || !d_out || n_ctx == 0) return DQ_ERR_INVALID_ARG;
+    if (!attn_shape_ok(n_head, n_head_kv, hd)) return DQ_ERR_NOT_SUPPORTED;
+    const size_t need = work_bytes_for((int)n_head, (int)hd, max_tiles_for(n_ctx));
+    if (need > NOALLOC_SCRATCH_BYTES) return DQ_ERR_NOT_SUPPORTED;  // beyond the static scratch
+    void* work = scratch_ptr();
+    if (!work) return DQ_ERR_IO;
+    return attn_run(d_q, nullptr, nullptr, nullptr, d_kc, d_vc, n_head, n_head_kv, hd, cc_start, pos, d_pos, n_ctx,
+                    d_out, work, NOALLOC_SCRATCH_BYTES, nullptr, nullptr, nullptr, stream);
 }
 
 int dq_attn_decode_q8_act(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head,

@@ -177,6 +177,21 @@ int dq_attn_workspace_bytes(uint32_t n_head, uint32_t n_head_kv, uint32_t hd, ui
 int dq_attn_decode_q8(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head, uint32_t n_head_kv,
                       uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx,
                       float* d_out, void* d_work, size_t work_bytes, void* stream);
+
+/* Allocation-free form of dq_attn_decode_q8 (no counterpart in the reference:
+ * for callers that cannot allocate device memory, e.g. code under HIP graph
+ * capture or a serving loop that forbids hipMalloc). Same arguments and
+ * results without d_work: the tile records live in a static 16 MiB device
+ * array of the library, one per GPU, held until the process ends. Shapes whose
+ * dq_attn_workspace_bytes exceeds 16 MiB (n_head * ceil(n_ctx / 64) * 520
+ * bytes at hd = 128: 32 heads up to n_ctx = 64512) return
+ * DQ_ERR_NOT_SUPPORTED and do nothing. Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (other streams, other threads) race. It
+ * calls no hipMalloc/hipFree; its first call on a device looks the array's
+ * address up (hipGetSymbolAddress) and must not itself be under capture. */
+int dq_attn_decode_q8_noalloc(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head,
+                              uint32_t n_head_kv, uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos,
+                              uint32_t n_ctx, float* d_out, void* stream);
 /* The same, also writing the output quantized per 256 values (DQ_ACT_Q8K_REP
  * layout: int8 [n_head*hd], scale and int32 sum per 32), the activation of
  * the output projection's GEMV. */
