@@ -21,10 +21,11 @@
 // Every on-device weight layout is split into 256-byte-aligned planes inside
 // one allocation. A row is cut into items of 64 weights (cols/64 per row);
 // the quant bytes of an item are split over NP "sub-planes" of 16 bytes per
-// item, each sub-plane item-major ([rows][items][16 B]). A wave whose lane l
-// reads item 64j+l of a sub-plane thus issues one contiguous kilobyte per
-// global_load_dwordx4. Byte counts per row equal the GGUF row size, so the HBM
-// traffic of a kernel is the GGUF size of the matrix.
+// item, each sub-plane item-major ([rows][items][16 B], rows q_row bytes
+// apart). A wave whose lane l reads item 64j+l of a sub-plane thus issues one
+// contiguous kilobyte per global_load_dwordx4. Byte counts per row equal the
+// GGUF row size, so the HBM traffic of a kernel is the GGUF size of the
+// matrix.
 //
 //   Q8_0 (NP 4): sub-plane k of item i = int8 weights 64i+16k..+16
 //         D = fp16 [rows][cols/32] (item i: the scales of blocks 2i, 2i+1)

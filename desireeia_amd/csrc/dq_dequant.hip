@@ -94,7 +94,13 @@ __global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t* __rest
 }
 
 // ---------------------------------------------------------------- packing --
-// Layouts: see dq_common.h. `ps` is the distance between quant sub-planes.
+// Layouts: see dq_common.h. `ps` is the distance between quant sub-planes;
+// PlaneRows maps a matrix-wide item index to its byte offset in a sub-plane
+// (rows q_row bytes apart, ipr items per row).
+struct PlaneRows {
+    size_t ipr, q_row;
+    __device__ size_t off(size_t item) const { return (item / ipr) * q_row + 16 * (item % ipr); }
+};
 
 __device__ __forceinline__ dq_u32x4 ld16_bytes(const uint8_t* src) {
     uint32_t w[4];
@@ -106,28 +112,28 @@ __device__ __forceinline__ dq_u32x4 ld16_bytes(const uint8_t* src) {
 }
 
 __global__ __launch_bounds__(256) void pack_q8_0_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
-                                                        size_t ps, uint16_t* __restrict__ dp, size_t nb) {
+                                                        size_t ps, PlaneRows pr, uint16_t* __restrict__ dp, size_t nb) {
     // one lane per block b: its halves go to sub-planes 2(b%2), 2(b%2)+1 of item b/2
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nb) return;
     const uint8_t* blk = x + b * DQ_SZ_Q8_0;
-    const size_t o = 16 * (b / 2), k = 2 * (b % 2);
+    const size_t o = pr.off(b / 2), k = 2 * (b % 2);
     *reinterpret_cast<dq_u32x4*>(qp + k * ps + o) = ld16_bytes(blk + 2);
     *reinterpret_cast<dq_u32x4*>(qp + (k + 1) * ps + o) = ld16_bytes(blk + 18);
     dp[b] = rd16(blk);
 }
 
 __global__ __launch_bounds__(256) void pack_q4_0_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
-                                                        size_t ps, uint16_t* __restrict__ dp, size_t nb) {
+                                                        size_t ps, PlaneRows pr, uint16_t* __restrict__ dp, size_t nb) {
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nb) return;
     const uint8_t* blk = x + b * DQ_SZ_Q4_0;
-    *reinterpret_cast<dq_u32x4*>(qp + (b % 2) * ps + 16 * (b / 2)) = ld16_bytes(blk + 2);
+    *reinterpret_cast<dq_u32x4*>(qp + (b % 2) * ps + pr.off(b / 2)) = ld16_bytes(blk + 2);
     dp[b] = rd16(blk);
 }
 
 __global__ __launch_bounds__(256) void pack_q4_k_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
-                                                        size_t ps, uint8_t* __restrict__ hp, size_t ns) {
+                                                        size_t ps, PlaneRows pr, uint8_t* __restrict__ hp, size_t ns) {
     // one lane per 16-byte piece: 9 pieces per block (header + 8 qs pieces)
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= ns * 9) return;
@@ -138,12 +144,12 @@ __global__ __launch_bounds__(256) void pack_q4_k_kernel(const uint8_t* __restric
         *reinterpret_cast<dq_u32x4*>(hp + s * 16) = v;
     } else {
         const int q = p - 1, g = q / 2, k = q % 2;
-        *reinterpret_cast<dq_u32x4*>(qp + (size_t)k * ps + 64 * s + 16 * g) = v;
+        *reinterpret_cast<dq_u32x4*>(qp + (size_t)k * ps + pr.off(4 * s + g)) = v;
     }
 }
 
 __global__ __launch_bounds__(256) void pack_q6_k_kernel(const uint8_t* __restrict__ x, uint8_t* __restrict__ qp,
-                                                        size_t ps, uint8_t* __restrict__ sp,
+                                                        size_t ps, PlaneRows pr, uint8_t* __restrict__ sp,
                                                         uint16_t* __restrict__ dp, size_t ns) {
     // one lane per item t = 4s + it, it = 2n + k
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -151,21 +157,22 @@ __global__ __launch_bounds__(256) void pack_q6_k_kernel(const uint8_t* __restric
     const size_t s = t / 4;
     const int it = (int)(t % 4), n = it / 2, k = it % 2;
     const uint8_t* blk = x + s * DQ_SZ_Q6_K;
-    *reinterpret_cast<dq_u32x4*>(qp + 16 * t) = ld16_bytes(blk + 64 * n + 16 * k);
-    *reinterpret_cast<dq_u32x4*>(qp + ps + 16 * t) = ld16_bytes(blk + 64 * n + 32 + 16 * k);
-    *reinterpret_cast<dq_u32x4*>(qp + 2 * ps + 16 * t) = ld16_bytes(blk + 128 + 32 * n + 16 * k);
+    const size_t o = pr.off(t);
+    *reinterpret_cast<dq_u32x4*>(qp + o) = ld16_bytes(blk + 64 * n + 16 * k);
+    *reinterpret_cast<dq_u32x4*>(qp + ps + o) = ld16_bytes(blk + 64 * n + 32 + 16 * k);
+    *reinterpret_cast<dq_u32x4*>(qp + 2 * ps + o) = ld16_bytes(blk + 128 + 32 * n + 16 * k);
     for (int qq = 0; qq < 4; ++qq) sp[t * 4 + qq] = blk[192 + 8 * n + k + 2 * qq];
     if (it == 0) dp[s] = rd16(blk + 208);
 }
 
 // Dequantization from the device layout (same values as from GGUF blocks).
 __global__ __launch_bounds__(256) void dequant_dev_q8_0_kernel(const uint8_t* __restrict__ qp, size_t ps,
-                                                               const uint16_t* __restrict__ dp,
+                                                               PlaneRows pr, const uint16_t* __restrict__ dp,
                                                                float* __restrict__ y, size_t nb) {
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nb) return;
     const float d = dq_h2f(dp[b]);
-    const size_t o = 16 * (b / 2), k = 2 * (b % 2);
+    const size_t o = pr.off(b / 2), k = 2 * (b % 2);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         y[b * 32 + j] = (float)(int8_t)qp[k * ps + o + j] * d;
@@ -174,12 +181,12 @@ __global__ __launch_bounds__(256) void dequant_dev_q8_0_kernel(const uint8_t* __
 }
 
 __global__ __launch_bounds__(256) void dequant_dev_q4_0_kernel(const uint8_t* __restrict__ qp, size_t ps,
-                                                               const uint16_t* __restrict__ dp,
+                                                               PlaneRows pr, const uint16_t* __restrict__ dp,
                                                                float* __restrict__ y, size_t nb) {
     const size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nb) return;
     const float d = dq_h2f(dp[b]);
-    const uint8_t* q = qp + (b % 2) * ps + 16 * (b / 2);
+    const uint8_t* q = qp + (b % 2) * ps + pr.off(b / 2);
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
         const uint8_t v = q[j];
@@ -189,7 +196,7 @@ __global__ __launch_bounds__(256) void dequant_dev_q4_0_kernel(const uint8_t* __
 }
 
 __global__ __launch_bounds__(256) void dequant_dev_q4_k_kernel(const uint8_t* __restrict__ qp, size_t ps,
-                                                               const uint8_t* __restrict__ hp,
+                                                               PlaneRows pr, const uint8_t* __restrict__ hp,
                                                                float* __restrict__ y, size_t n_sub) {
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n_sub) return;
@@ -206,13 +213,13 @@ __global__ __launch_bounds__(256) void dequant_dev_q4_k_kernel(const uint8_t* __
     float* o = y + t * 32;
 #pragma unroll
     for (int l = 0; l < 32; ++l) {
-        const uint8_t v = qp[(size_t)(l / 16) * ps + 64 * s + 16 * g + (l % 16)];
+        const uint8_t v = qp[(size_t)(l / 16) * ps + pr.off(4 * s + g) + (l % 16)];
         o[l] = d1 * (float)((v >> sh) & 0xF) - m1;
     }
 }
 
 __global__ __launch_bounds__(256) void dequant_dev_q6_k_kernel(const uint8_t* __restrict__ qp, size_t ps,
-                                                               const int8_t* __restrict__ sp,
+                                                               PlaneRows pr, const int8_t* __restrict__ sp,
                                                                const uint16_t* __restrict__ dp,
                                                                float* __restrict__ y, size_t n_items) {
     // one lane per item (n,k): 64 outputs at 128n + 16k + {0..15} + 32*quarter
@@ -223,8 +230,9 @@ __global__ __launch_bounds__(256) void dequant_dev_q6_k_kernel(const uint8_t* __
     const int8_t* sc = sp + t * 4;
     const float d = dq_h2f(dp[s]);
     float* o = y + s * 256 + 128 * n + 16 * k;
+    const size_t qo = pr.off(t);
     for (int tt = 0; tt < 16; ++tt) {
-        const uint8_t a = qp[16 * t + tt], b = qp[ps + 16 * t + tt], h = qp[2 * ps + 16 * t + tt];
+        const uint8_t a = qp[qo + tt], b = qp[ps + qo + tt], h = qp[2 * ps + qo + tt];
         const int q1 = (int)((a & 0xF) | (((h >> 0) & 3) << 4)) - 32;
         const int q2 = (int)((b & 0xF) | (((h >> 2) & 3) << 4)) - 32;
         const int q3 = (int)((a >> 4) | (((h >> 4) & 3) << 4)) - 32;
@@ -289,25 +297,26 @@ extern "C" int dq_weights_pack(int fmt, const void* d_gguf, size_t rows, size_t 
     hipStream_t s = (hipStream_t)stream;
     const uint8_t* x = (const uint8_t*)d_gguf;
     uint8_t* base = (uint8_t*)d_dev;
+    const PlaneRows pr{cols / 64, L.q_row};
     switch (fmt) {
     case DQ_FMT_Q8_0: {
         const size_t nb = rows * cols / 32;
-        pack_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, L.p_stride, (uint16_t*)(base + L.d_off), nb);
+        pack_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, L.p_stride, pr, (uint16_t*)(base + L.d_off), nb);
         break;
     }
     case DQ_FMT_Q4_0: {
         const size_t nb = rows * cols / 32;
-        pack_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, L.p_stride, (uint16_t*)(base + L.d_off), nb);
+        pack_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(x, base + L.q_off, L.p_stride, pr, (uint16_t*)(base + L.d_off), nb);
         break;
     }
     case DQ_FMT_Q4_K: {
         const size_t ns = rows * cols / 256;
-        pack_q4_k_kernel<<<grid_for(ns * 9), 256, 0, s>>>(x, base + L.q_off, L.p_stride, base + L.s_off, ns);
+        pack_q4_k_kernel<<<grid_for(ns * 9), 256, 0, s>>>(x, base + L.q_off, L.p_stride, pr, base + L.s_off, ns);
         break;
     }
     case DQ_FMT_Q6_K: {
         const size_t ns = rows * cols / 256;
-        pack_q6_k_kernel<<<grid_for(ns * 4), 256, 0, s>>>(x, base + L.q_off, L.p_stride, base + L.s_off,
+        pack_q6_k_kernel<<<grid_for(ns * 4), 256, 0, s>>>(x, base + L.q_off, L.p_stride, pr, base + L.s_off,
                                                           (uint16_t*)(base + L.d_off), ns);
         break;
     }
@@ -323,28 +332,29 @@ extern "C" int dq_weights_dequantize(int fmt, const void* d_dev, size_t rows, si
     if (rows == 0) return DQ_OK;
     hipStream_t s = (hipStream_t)stream;
     const uint8_t* base = (const uint8_t*)d_dev;
+    const PlaneRows pr{cols / 64, L.q_row};
     switch (fmt) {
     case DQ_FMT_Q8_0: {
         const size_t nb = rows * cols / 32;
-        dequant_dev_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, L.p_stride,
+        dequant_dev_q8_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, L.p_stride, pr,
                                                              (const uint16_t*)(base + L.d_off), d_out, nb);
         break;
     }
     case DQ_FMT_Q4_0: {
         const size_t nb = rows * cols / 32;
-        dequant_dev_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, L.p_stride,
+        dequant_dev_q4_0_kernel<<<grid_for(nb), 256, 0, s>>>(base + L.q_off, L.p_stride, pr,
                                                              (const uint16_t*)(base + L.d_off), d_out, nb);
         break;
     }
     case DQ_FMT_Q4_K: {
         const size_t nsub = rows * cols / 32;
-        dequant_dev_q4_k_kernel<<<grid_for(nsub), 256, 0, s>>>(base + L.q_off, L.p_stride, base + L.s_off, d_out,
+        dequant_dev_q4_k_kernel<<<grid_for(nsub), 256, 0, s>>>(base + L.q_off, L.p_stride, pr, base + L.s_off, d_out,
                                                                nsub);
         break;
     }
     case DQ_FMT_Q6_K: {
         const size_t ni = rows * cols / 64;
-        dequant_dev_q6_k_kernel<<<grid_for(ni), 256, 0, s>>>(base + L.q_off, L.p_stride,
+        dequant_dev_q6_k_kernel<<<grid_for(ni), 256, 0, s>>>(base + L.q_off, L.p_stride, pr,
                                                              (const int8_t*)(base + L.s_off),
                                                              (const uint16_t*)(base + L.d_off), d_out, ni);
         break;

@@ -20,12 +20,16 @@
 // which on CDNA4 (16 fp32 lanes/clk/SIMD vs ~1024 int8 MAC/clk/SIMD) caps the
 // int8 path below half its peak; pre-scaled fp16 operands need no epilogue.
 //
-// Tiling: 128 (tokens) x BN (weight rows, 256 or 128) x 64 (K) per workgroup
-// of BN/32 waves, each 64x64 (2x2 v_mfma_f32_32x32x16_f16 tiles). A 3-stage
-// LDS ring filled by global_load_lds DMA holds per step the activation tile
-// (XOR-swizzled 16-byte chunks: no bank conflicts on fragment reads), the
-// super-block's block sums and the raw packed weight bytes; each wave turns
-// its rows' bytes into fp16 fragments in registers. Q6_K: K is permuted to the
+// Tiling: a workgroup of 4 waves computes 128 tokens x 64*NWN weight rows;
+// the waves are NWN (64-row blocks) x KSW (K groups). Wave (wn, kg) owns all
+// 128 tokens of its 64 rows over the kg-th share of the workgroup's K steps:
+// 4 x 2 v_mfma_f32_32x32x16_f16 tiles, so each weight fragment it turns into
+// fp16 feeds 4 MFMAs, and no other wave converts the same bytes. Each K group
+// has a 3-stage LDS ring filled by global_load_lds DMA holding per K step (64
+// columns, one packed weight item) the activation tile (XOR-swizzled 16-byte
+// chunks: no bank conflicts on fragment reads), the super-block's block sums
+// and the raw packed weight bytes of the group's rows. KSW = 2 partials are
+// added through LDS at the end in a fixed order. Q6_K: K is permuted to the
 // packed item order (both operands, see dq_quantize_act_f16), so a 64-column
 // K step is exactly one 64-weight item.
 #include <cstdlib>
@@ -39,9 +43,7 @@ namespace {
 
 constexpr int BK = 64;  // K per step
 
-// Tile rows (tokens) of a workgroup: 2 waves along M, each WM 32-token blocks.
-template <int WM>
-constexpr int bm_of() { return 64 * WM; }
+constexpr int BM = 128;  // tokens per workgroup (and per wave)
 
 enum BKind { B_Q4K = 0, B_Q6K = 1, B_Q80 = 2, B_Q40 = 3 };
 
@@ -51,31 +53,52 @@ constexpr int kind_of() {
 }
 
 // ------------------------------------------------------------ LDS layout --
-// Ring of NS stages, each holding one K step of both operands:
-//   A: BM rows x 8 chunks of 16 bytes (fp16), chunk c of row r at slot
-//      r*8 + (c ^ (r & 7)) - XOR swizzle: a wave's 16-byte fragment reads (32
-//      rows, one logical chunk) hit all banks.
-//   Q4_K only: the 8 min columns of the step's super-block (16 bytes per row).
-//   B: the raw bytes of the weight tile, format specific:
-//      Q4_K: P0[BN][16] P1[BN][16] H[BN][16]    (qs sub-planes, block header)
-//      Q6_K: QA[BN][16] QB[BN][16] QH[BN][16] S[BN][4] D[BN][4] (fp16 in the low half)
-//      Q8_0: P0..P3[BN][16] D[BN][4] (the item's two fp16 block scales)
-//      Q4_0: P0 P1[BN][16] D[BN][4]
-// Every stage is filled by global_load_lds (direct global -> LDS DMA, 16, 4 or
-// 2 bytes per lane; lane i of a wave writes at base + i*16 for 16-byte loads and
-// at base + i*4 for the dword and sub-dword forms). Three stages: two steps'
-// DMAs in flight while one is computed.
-template <int BN, int KIND, int WM>
+// Per K group: an A ring of NS stages, one K step each - the activation tile
+// as fp16, BM rows x 8 chunks of 16 bytes, chunk c of row r at slot
+// r*8 + (c ^ aswz(r)) - and a B ring of NB super-stages, each
+// holding SB consecutive weight items (K steps) of the group's BN rows:
+//   Q4_K (SB 4): P0[BN][4][16] P1[BN][4][16] H[BN][16] MIN[BM][16]
+//   Q4_0 (SB 4): P0[BN][4][16] P1[BN][4][16] D[4][BN][4]
+//   Q6_K (SB 2): QA[BN][2][16] QB[BN][2][16] QH[BN][2][16] S[2][BN][4] D[BN][4]
+//   Q8_0 (SB 2): P0..P3[BN][2][16] D[2][BN][4]
+// (H: the super-block header; MIN: the super-block's 8 activation block sums
+// per token; S: an item's four int8 scales; D: fp16 scales, Q6_K's in the low
+// half of a dword slot.) Item t of row n of a [BN][SB][16] plane sits in
+// chunk slot t ^ swz(n). The swizzles make the 16-byte fragment reads (one
+// chunk of 16 consecutive rows per half-wave) conflict-free whether the LDS
+// serves 8 lanes over 32 banks or 16 lanes over 64 banks per cycle: over any
+// 8 aligned rows the chunk slots are distinct, and over 16 rows so are the
+// pairs (row parity, slot) (A) or (row % 4, slot) (SB 4) or (row % 8, slot)
+// (SB 2). Every
+// region is filled by global_load_lds (direct global -> LDS DMA: lane i of a
+// wave writes base + 16i, or base + 4i for the dword and sub-dword forms);
+// the plane DMA reads a row's SB*16 contiguous bytes with SB consecutive
+// lanes (whole cache-line pieces, not one 16-byte item of a different row
+// per lane).
+template <int KIND>
+constexpr int sb_of() { return (KIND == B_Q6K || KIND == B_Q80) ? 2 : 4; }
+template <int KIND>
+constexpr int planes_of() { return KIND == B_Q80 ? 4 : KIND == B_Q6K ? 3 : 2; }
+template <int KIND>
+constexpr int aux_row_of() { return KIND == B_Q6K ? 12 : KIND == B_Q80 ? 8 : 16; }
+
+template <int NWN, int KIND>
 struct Ring {
-    static constexpr int BM = bm_of<WM>();
-    static constexpr int NS = 3;
-    static constexpr int A_BYTES = BM * BK * 2;
-    static constexpr int MIN_BYTES = KIND == B_Q4K ? BM * 16 : 0;
-    static constexpr int B_OFF = A_BYTES + MIN_BYTES;
-    static constexpr int B_BYTES = BN * (KIND == B_Q80 ? 68 : 56);  // Q4_K 48, Q6_K 56, Q8_0 68, Q4_0 36 per row
-    static constexpr int STAGE = B_OFF + B_BYTES;
-    static constexpr int BYTES = NS * STAGE;
+    static constexpr int BN = 64 * NWN;
+    static constexpr int SB = sb_of<KIND>();
+    static constexpr int NB = SB == 4 ? 2 : 3;       // B super-stages in the ring
+    static constexpr int A_STAGE = BM * BK * 2;
+    static constexpr int PLANE = BN * SB * 16;
+    static constexpr int AUX = planes_of<KIND>() * PLANE;
+    static constexpr int MIN = AUX + BN * aux_row_of<KIND>();
+    static constexpr int B_STAGE = MIN + (KIND == B_Q4K ? BM * 16 : 0);
+    template <int NS>
+    static constexpr int group_bytes() { return NS * A_STAGE + NB * B_STAGE; }
 };
+
+template <int SB>
+__device__ __forceinline__ int swz(int n) { return SB == 4 ? ((n >> 1) ^ (n >> 3)) & 3 : ((n >> 2) ^ (n >> 3)) & 1; }
+__device__ __forceinline__ int aswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 #define DQ_LDS_PTR(p) reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(p))
 template <int SIZE>
@@ -112,133 +135,121 @@ struct GemmArgs {
     uint32_t magic;         // 0x54005400 (kept in a register: see run_steps)
 };
 
-// Issues the DMA of K step `st` (weights and activations) into ring stage
-// `stage`. Every wave issues the same, compile-time number of load
-// instructions (stage_loads()), so one s_waitcnt vmcnt covers a stage: blocks
-// of 64 slots are dealt to the NW waves, and where a region has fewer blocks
-// than waves several waves load the same block (identical bytes to the same
-// LDS address).
-template <int BN, int KIND, int WM>
-constexpr int stage_loads() {
-    constexpr int NW = BN / 32;
-    // A, then Q4_K: sums, P0/P1, H; Q6_K: QA/QB, QH or S, D; Q8_0: two plane blocks, D; Q4_0: P0/P1, D
-    return bm_of<WM>() * 8 / 64 / NW + (KIND == B_Q40 ? 2 : 3);
+// DMA issue. Every wave issues the same, compile-time number of load
+// instructions per call (a_loads(), b_loads()), so s_waitcnt vmcnt counts
+// cover whole stages. A: the NWN waves of a K group deal the activation
+// tile's 64-slot blocks among them. B: wave wn loads its own 64 weight rows
+// only (so the B side of a step needs no barrier, only the wave's own vmcnt),
+// plus one of the two 64-token blocks of Q4_K block sums (waves wn % 2;
+// identical bytes to the same LDS address where NWN > 2).
+template <int NWN>
+constexpr int a_loads() { return BM * 8 / 64 / NWN; }
+template <int KIND>
+constexpr int b_loads() {
+    constexpr int SB = sb_of<KIND>();
+    // planes: 64 rows x SB x 16 bytes = SB kilobytes each; then the aux region
+    return planes_of<KIND>() * SB + (KIND == B_Q4K ? 2 : KIND == B_Q40 ? 4 : KIND == B_Q6K ? 3 : 2);
 }
 
-template <int BN, int KIND, int WM>
-__device__ __forceinline__ void issue_stage(const GemmArgs& g, uint8_t* ring, int stage, int st, int wave,
-                                            int lane) {
-    constexpr int NW = BN / 32;      // waves per workgroup
-    constexpr int HB = BN / 64;      // 64-slot blocks per [BN] region (= NW/2)
-    using R = Ring<BN, KIND, WM>;
-    constexpr int BM = R::BM;
-    static_assert(BM / 64 <= NW, "one block-sum block per wave at most");
-    uint8_t* base = ring + stage * R::STAGE;
-    // A: BM*8 slots of 16 bytes
-    {
-        const int kcol = st * BK;
+template <int NWN, int KIND>
+__device__ __forceinline__ void issue_a(const GemmArgs& g, uint8_t* stage_base, int st, int wn, int lane) {
+    const int kcol = st * BK;
 #pragma unroll
-        for (int j = 0; j < BM * 8 / 64 / NW; ++j) {
-            const int jj = j * NW + wave;
-            const int slot = jj * 64 + lane;
-            const int r = slot >> 3, c = (slot & 7) ^ (r & 7);
-            const int m = min(g.m0 + r, g.M - 1);
-            lds_dma<16>(g.A + (size_t)m * g.lda + kcol + 8 * c, base + jj * 64 * 16);
+    for (int j = 0; j < a_loads<NWN>(); ++j) {
+        const int jj = j * NWN + wn;
+        const int slot = jj * 64 + lane;
+        const int r = slot >> 3, c = (slot & 7) ^ aswz(r);
+        const int m = min(g.m0 + r, g.M - 1);
+        lds_dma<16>(g.A + (size_t)m * g.lda + kcol + 8 * c, stage_base + jj * 64 * 16);
+    }
+}
+
+template <int NWN, int KIND>
+__device__ __forceinline__ void issue_b(const GemmArgs& g, uint8_t* bb, int sb, int wn, int lane) {
+    using R = Ring<NWN, KIND>;
+    constexpr int SB = R::SB, BN = R::BN;
+    const int item0 = SB * sb;
+    // planes: instruction k covers own rows 64 SB^-1 ... : slot s = 64k + lane
+#pragma unroll
+    for (int p = 0; p < planes_of<KIND>(); ++p) {
+#pragma unroll
+        for (int k = 0; k < SB; ++k) {
+            const int s = 64 * k + lane;
+            const int n = 64 * wn + s / SB;                 // row in the tile
+            const int t = (s % SB) ^ swz<SB>(n);            // the item this LDS slot holds
+            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
+            const uint8_t* src = g.w + g.L.q_off + p * g.L.p_stride + r * g.L.q_row + 16 * (size_t)(item0 + t);
+            lds_dma<16>(src, bb + p * R::PLANE + (64 * wn * SB + 64 * k) * 16);
         }
     }
-    uint8_t* bb = base + R::B_OFF;
+    const int n = 64 * wn + lane;
+    const size_t r = (size_t)min(g.n0 + n, g.N - 1);
+    uint8_t* aux = bb + R::AUX;
     if constexpr (KIND == B_Q4K) {
-        {   // block sums of super-block st/4 (16 contiguous bytes per token):
-            // BM/64 blocks of 64 rows, block wave % (BM/64)
-            const int blk = wave % (BM / 64), m = min(g.m0 + blk * 64 + lane, g.M - 1);
-            lds_dma<16>(g.minp + ((size_t)(st >> 2) * g.M + m) * 8, base + R::A_BYTES + blk * 64 * 16);
-        }
-        {   // P0/P1: 2*HB = NW blocks, one per wave
-            const int region = wave / HB, n = (wave % HB) * 64 + lane;
-            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
-            lds_dma<16>(g.w + g.L.q_off + (size_t)region * g.L.p_stride + r * g.L.q_row + 16 * (size_t)st,
-                        bb + wave * 64 * 16);
-        }
-        {   // H: HB blocks, waves w and w + HB load block w % HB
-            const int blk = wave % HB, n = blk * 64 + lane;
-            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
-            lds_dma<16>(g.w + g.L.s_off + r * g.L.s_row + 16 * (size_t)(st >> 2), bb + 2 * BN * 16 + blk * 64 * 16);
-        }
+        lds_dma<16>(g.w + g.L.s_off + r * g.L.s_row + 16 * (size_t)sb, aux + 64 * wn * 16);
+        const int blk = wn & 1, m = min(g.m0 + blk * 64 + lane, g.M - 1);
+        lds_dma<16>(g.minp + ((size_t)sb * g.M + m) * 8, bb + R::MIN + blk * 64 * 16);
     } else if constexpr (KIND == B_Q6K) {
-        {   // QA/QB/QH blocks 0..NW-1: one per wave
-            const int region = wave / HB, n = (wave % HB) * 64 + lane;
-            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
-            lds_dma<16>(g.w + g.L.q_off + (size_t)region * g.L.p_stride + r * g.L.q_row + 16 * (size_t)st,
-                        bb + wave * 64 * 16);
-        }
-        if (wave < HB) {  // QH blocks (the last HB plane blocks)
-            const int n = wave * 64 + lane;
-            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
-            lds_dma<16>(g.w + g.L.q_off + 2 * g.L.p_stride + r * g.L.q_row + 16 * (size_t)st,
-                        bb + (NW + wave) * 64 * 16);
-        } else {          // S: HB blocks of dwords
-            const int n = (wave - HB) * 64 + lane;
-            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
-            lds_dma<4>(g.w + g.L.s_off + r * g.L.s_row + 4 * (size_t)st, bb + 3 * BN * 16 + (wave - HB) * 64 * 4);
-        }
-        {   // D: HB blocks of ushorts, waves w and w + HB load block w % HB. A
-            // sub-dword LDS DMA still advances 4 bytes per lane: d sits in the
-            // low half of a dword slot.
-            const int blk = wave % HB, n = blk * 64 + lane;
-            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
-            lds_dma<2>(g.w + g.L.d_off + r * g.L.d_row + 2 * (size_t)(st >> 2),
-                       bb + 3 * BN * 16 + BN * 4 + blk * 64 * 4);
-        }
-    } else {  // Q8_0 (4 sub-planes) and Q4_0 (2): one item per row and step
-        constexpr int NP = KIND == B_Q80 ? 4 : 2;
 #pragma unroll
-        for (int q = 0; q < NP / 2; ++q) {  // NP * HB plane blocks = NP/2 per wave
-            const int blk = wave + q * NW;
-            const int region = blk / HB, n = (blk % HB) * 64 + lane;
-            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
-            lds_dma<16>(g.w + g.L.q_off + (size_t)region * g.L.p_stride + r * g.L.q_row + 16 * (size_t)st,
-                        bb + blk * 64 * 16);
-        }
-        {   // D: the item's two fp16 scales, HB blocks of dwords (waves w and w + HB: block w % HB)
-            const int blk = wave % HB, n = blk * 64 + lane;
-            const size_t r = (size_t)min(g.n0 + n, g.N - 1);
-            lds_dma<4>(g.w + g.L.d_off + r * g.L.d_row + 4 * (size_t)st, bb + NP * BN * 16 + blk * 64 * 4);
-        }
+        for (int c = 0; c < 2; ++c)
+            lds_dma<4>(g.w + g.L.s_off + r * g.L.s_row + 4 * (size_t)(item0 + c), aux + c * BN * 4 + 64 * wn * 4);
+        // a sub-dword LDS DMA still advances 4 bytes per lane: d sits in the
+        // low half of a dword slot
+        lds_dma<2>(g.w + g.L.d_off + r * g.L.d_row + 2 * (size_t)(item0 >> 2), aux + 2 * BN * 4 + 64 * wn * 4);
+    } else {
+        constexpr int ND = KIND == B_Q80 ? 2 : 4;  // one dword (two fp16 block scales) per item
+#pragma unroll
+        for (int c = 0; c < ND; ++c)
+            lds_dma<4>(g.w + g.L.d_off + r * g.L.d_row + 4 * (size_t)(item0 + c), aux + c * BN * 4 + 64 * wn * 4);
     }
 }
 
 __device__ __forceinline__ const h8& lds_h8(const uint8_t* p) { return *reinterpret_cast<const h8*>(p); }
+__device__ __forceinline__ dq_u32x4 lds_u4(const uint8_t* p) { return *reinterpret_cast<const dq_u32x4*>(p); }
+__device__ __forceinline__ uint32_t lds_u1(const uint8_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
 
-// Raw weight bytes of one ring stage that this lane's B fragments need: for
-// each of its two 32-row blocks j, lane half h's 8 bytes of the two quant
-// sub-planes (Q4_K: P0/P1; Q6_K: QA/QB plus QH) and the row's scales.
+// Raw weight bytes of item t of a B super-stage that this lane's B fragments
+// need: for each of its two 32-row blocks j, 8 bytes of each quant sub-plane
+// (Q4_K: all 16 bytes of sub-plane h = lane/32, see b_frag; the other
+// formats: bytes 8h..8h+7 of each sub-plane, a 16-byte read and a select, so
+// the reads stay conflict-free) and the row's scales.
 struct BRaw {
-    dq_u32x2 q0[2], q1[2], q2[2], q3[2];  // Q4_K: P0, P1; Q6_K: QA, QB, QH; Q8_0: P0..P3; Q4_0: P0, P1
+    dq_u32x2 q0[2], q1[2], q2[2], q3[2];  // Q4_K: words 0-1 / 2-3 of sub-plane h; Q6_K: QA, QB, QH; Q8_0: P0..P3; Q4_0: P0, P1
     dq_u32x4 hd[2];  // Q4_K: super-block header; Q6_K: .x = 4 int8 scales, .y = d (low half); Q8_0/Q4_0: .x = 2 d
 };
 
-template <int BN, int KIND>
-__device__ __forceinline__ void b_raw(const uint8_t* bb, int wn, int lane, BRaw& r) {
+__device__ __forceinline__ dq_u32x2 half_of(const dq_u32x4& v, bool h) {
+    return dq_u32x2{h ? v.z : v.x, h ? v.w : v.y};
+}
+
+template <int NWN, int KIND>
+__device__ __forceinline__ void b_raw_j(const uint8_t* bb, int t, int wn, int lane, BRaw& r, int j) {
+    using R = Ring<NWN, KIND>;
+    constexpr int SB = R::SB, BN = R::BN;
     const int h = lane >> 5;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    {
         const int n = wn * 64 + j * 32 + (lane & 31);
-        r.q0[j] = *reinterpret_cast<const dq_u32x2*>(bb + n * 16 + 8 * h);
-        r.q1[j] = *reinterpret_cast<const dq_u32x2*>(bb + BN * 16 + n * 16 + 8 * h);
+        const int off = n * SB * 16 + 16 * (t ^ swz<SB>(n));
         if constexpr (KIND == B_Q4K) {
-            r.hd[j] = *reinterpret_cast<const dq_u32x4*>(bb + 2 * BN * 16 + n * 16);
-        } else if constexpr (KIND == B_Q80) {
-            r.q2[j] = *reinterpret_cast<const dq_u32x2*>(bb + 2 * BN * 16 + n * 16 + 8 * h);
-            r.q3[j] = *reinterpret_cast<const dq_u32x2*>(bb + 3 * BN * 16 + n * 16 + 8 * h);
-            r.hd[j].x = *reinterpret_cast<const uint32_t*>(bb + 4 * BN * 16 + n * 4);
-        } else if constexpr (KIND == B_Q40) {
-            r.hd[j].x = *reinterpret_cast<const uint32_t*>(bb + 2 * BN * 16 + n * 4);
+            const dq_u32x4 v = lds_u4(bb + h * R::PLANE + off);
+            r.q0[j] = dq_u32x2{v.x, v.y};
+            r.q1[j] = dq_u32x2{v.z, v.w};
+            r.hd[j] = lds_u4(bb + R::AUX + n * 16);
         } else {
-            r.q2[j] = *reinterpret_cast<const dq_u32x2*>(bb + 2 * BN * 16 + n * 16 + 8 * h);
-            r.hd[j].x = *reinterpret_cast<const uint32_t*>(bb + 3 * BN * 16 + n * 4);
-            r.hd[j].y = *reinterpret_cast<const uint32_t*>(bb + 3 * BN * 16 + BN * 4 + n * 4);
+            r.q0[j] = half_of(lds_u4(bb + off), h);
+            r.q1[j] = half_of(lds_u4(bb + R::PLANE + off), h);
+            if constexpr (KIND == B_Q6K || KIND == B_Q80) r.q2[j] = half_of(lds_u4(bb + 2 * R::PLANE + off), h);
+            if constexpr (KIND == B_Q80) r.q3[j] = half_of(lds_u4(bb + 3 * R::PLANE + off), h);
+            r.hd[j].x = lds_u1(bb + R::AUX + t * BN * 4 + n * 4);
+            if constexpr (KIND == B_Q6K) r.hd[j].y = lds_u1(bb + R::AUX + 2 * BN * 4 + n * 4);
         }
     }
+}
+
+template <int NWN, int KIND>
+__device__ __forceinline__ void b_raw(const uint8_t* bb, int t, int wn, int lane, BRaw& r) {
+    b_raw_j<NWN, KIND>(bb, t, wn, lane, r, 0);
+    b_raw_j<NWN, KIND>(bb, t, wn, lane, r, 1);
 }
 
 // B fragments of a step of phase G (= st % 4, the item of the super-block)
@@ -247,17 +258,17 @@ __device__ __forceinline__ void b_raw(const uint8_t* bb, int wn, int lane, BRaw&
 // Lane l feeds row n = wn*64 + j*32 + l%32 with the 8 K values KK*16 +
 // 8*(l/32) .. +7. Rows past N hold the clamped last row's bytes (finite
 // values whose outputs are never stored). b_scales holds the fp16 scale pair
-// of every (j, KK): Q4_K a = d*sc of sub-block 2G (KK 0, 1: low nibbles) or
-// 2G+1 (KK 2, 3: high nibbles); Q6_K a = d*sc of the KK-th 16-block.
+// of every (j, KK): Q4_K (the same for every slice) a0 = d*sc of sub-block 2G
+// (the low nibbles), a1 = d*sc of 2G+1 (the high nibbles), -64 a0, -64 a1;
+// Q6_K a = d*sc of the KK-th 16-block.
 struct BScale {
     h2 s[2][4];  // Q6_K: scale pair per (j, KK); Q4_K: low-nibble a, high-nibble a, -64a of each
     uint32_t magic;
 };
 
 template <int KIND>
-__device__ __forceinline__ void b_scales(const BRaw& r, int G, BScale& S) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
+__device__ __forceinline__ void b_scales_j(const BRaw& r, int G, BScale& S, int j) {
+    {
         if constexpr (KIND == B_Q4K) {
             const dq_u32x4 hd = r.hd[j];
             const float d = dq_h2f((uint16_t)(hd.x & 0xFFFF));
@@ -287,14 +298,19 @@ __device__ __forceinline__ void b_scales(const BRaw& r, int G, BScale& S) {
     }
 }
 
+template <int KIND>
+__device__ __forceinline__ void b_scales(const BRaw& r, int G, BScale& S) {
+    b_scales_j<KIND>(r, G, S, 0);
+    b_scales_j<KIND>(r, G, S, 1);
+}
+
 template <int KIND, int KK>
-__device__ __forceinline__ void b_frag(const BRaw& r, const BScale& S, h8 (&bf)[2]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
+__device__ __forceinline__ h8 b_frag_j(const BRaw& r, const BScale& S, int j) {
+    {
         uint32_t t[4];
         if constexpr (KIND == B_Q4K) {
-            // KK 0, 1: P0 bytes 8h..8h+3, 8h+4..8h+7; KK 2, 3: the same of P1.
-            // From the dword's bytes B0..B3, a nibble ORed into mantissa bits
+            // Slice KK: word KK of sub-plane h (lane half h holds all 16 bytes
+            // of sub-plane h). From the dword's bytes B0..B3, a nibble ORed into mantissa bits
             // 7:4 under the exponent of 64 (0x5400) is the fp16 64 + q exactly,
             // two per v_and_or; fma(64 + q, a, -64a) = q*a rounded once (as
             // (q)*a would be). Fragment order (the activation tile is permuted
@@ -337,100 +353,218 @@ __device__ __forceinline__ void b_frag(const BRaw& r, const BScale& S, h8 (&bf)[
                 bytes_to_h2(v6, bias, S.s[j][KK], &t[2 * wd]);
             }
         }
-        bf[j] = __builtin_bit_cast(h8, dq_u32x4{t[0], t[1], t[2], t[3]});
+        return __builtin_bit_cast(h8, dq_u32x4{t[0], t[1], t[2], t[3]});
     }
 }
 
-// A fragments of K slice kk for the wave's WM 32-token blocks (XOR-swizzled
-// 16-byte chunks of the stage's activation tile).
-template <int WM>
-__device__ __forceinline__ void a_frags(const uint8_t* base, int wm, int kk, int lane, h8 (&af)[WM]) {
+template <int KIND, int KK>
+__device__ __forceinline__ void b_frag(const BRaw& r, const BScale& S, h8 (&bf)[2]) {
+    bf[0] = b_frag_j<KIND, KK>(r, S, 0);
+    bf[1] = b_frag_j<KIND, KK>(r, S, 1);
+}
+
+// A fragments of K slice kk for the wave's 4 32-token blocks (XOR-swizzled
+// 16-byte chunks of a stage's activation tile).
+__device__ __forceinline__ void a_frags(const uint8_t* base, int kk, int lane, h8 (&af)[4]) {
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
-        const int r = wm * 32 * WM + i * 32 + (lane & 31);
-        af[i] = lds_h8(base + (r * 8 + ((2 * kk + (lane >> 5)) ^ (r & 7))) * 16);
+    for (int i = 0; i < 4; ++i) {
+        const int r = i * 32 + (lane & 31);
+        af[i] = lds_h8(base + (r * 8 + ((2 * kk + (lane >> 5)) ^ aswz(r))) * 16);
     }
 }
 
-// One K step st (phase G = st % 4, the item of the super-block) in ring
-// stage `stage`: wait until the stage has landed (NS-2 later stages may
-// still be in flight), barrier (every wave's DMAs visible, step st-1
-// retired), DMA of step st+NS-1 into the stage of st-1 (past the end: the
-// last step again, so every wave issues the same count per stage), then the
-// weight fragments (LDS bytes -> fp16 in registers) and the MFMAs; at the
-// last item of a super-block (Q4_K) also its min term.
-template <int BN, int KIND, int WM>
-__device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* ring, int st, int stage, int s1,
-                                          f16v (&acc)[WM][2], int wave, int lane, uint32_t magic) {
-    const int G = st & 3;
-    using R = Ring<BN, KIND, WM>;
-    constexpr int NS = R::NS;
-    constexpr int PER = stage_loads<BN, KIND, WM>();
-    const int wm = wave & 1, wn = wave >> 1;
-    wait_vm<(NS - 2) * PER>();
-    dq_lds_barrier();
-    issue_stage<BN, KIND, WM>(g, ring, stage == 0 ? NS - 1 : stage - 1, min(st + NS - 1, s1 - 1), wave, lane);
-    const uint8_t* base = ring + stage * R::STAGE;
+// What a wave holds for its next step before that step starts: the slice-0
+// activation fragments and the B side (raw bytes, scales, slice-0 weight
+// fragments); Q4_K: the super-block's min-term weight fragments, built during
+// the super-block's second step.
+struct Pre {
+    h8 af[4];
     BRaw raw;
-    b_raw<BN, KIND>(base + R::B_OFF, wn, lane, raw);
     BScale S;
-    S.magic = magic;
-    b_scales<KIND>(raw, G, S);
-    // The four K slices in order, slice kk+1's activation fragments (LDS)
-    // and weight fragments (VALU) written after slice kk's MFMAs so the
-    // scheduler can overlap them.
-    h8 af[4][WM], bf[4][2];
-    a_frags<WM>(base, wm, 0, lane, af[0]);
-    b_frag<KIND, 0>(raw, S, bf[0]);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-        if (kk == 0) { a_frags<WM>(base, wm, 1, lane, af[1]); b_frag<KIND, 1>(raw, S, bf[1]); }
-        if (kk == 1) { a_frags<WM>(base, wm, 2, lane, af[2]); b_frag<KIND, 2>(raw, S, bf[2]); }
-        if (kk == 2) { a_frags<WM>(base, wm, 3, lane, af[3]); b_frag<KIND, 3>(raw, S, bf[3]); }
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk][i], bf[kk][j], acc[i][j], 0, 0, 0);
-    }
+    h8 bf[2];
     h8 bm[2];
-    if (KIND == B_Q4K && G == 3) bm[0] = q4k_neg_mins(raw.hd[0], true), bm[1] = q4k_neg_mins(raw.hd[1], true);
-    if (KIND == B_Q4K && G == 3) {  // the super-block's min term
-        const h8 zero = {};
-        h8 am[WM];
-#pragma unroll
-        for (int i = 0; i < WM; ++i) {
-            const h8 v = lds_h8(base + R::A_BYTES + (wm * 32 * WM + i * 32 + (lane & 31)) * 16);
-            am[i] = (lane >> 5) == 0 ? v : zero;
-        }
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[i], bm[j], acc[i][j], 0, 0, 0);
+};
+
+// s_waitcnt vmcnt at the middle of a step of phase T: the A stage of the next
+// step must have landed (and, at the last phase, this wave's part of the next
+// B super-stage). DMAs are issued in the middle of each step - A(st + NS),
+// then at phase 0 the B super-stage NB-1 ahead - so the count of DMA
+// instructions issued after the needed one depends only on the phase.
+template <int NWN, int KIND, int NS, int T>
+constexpr int mid_wait() {
+    constexpr int SB = sb_of<KIND>(), PA = a_loads<NWN>(), PB = b_loads<KIND>();
+    // A(st+1) was issued NS-1 steps back; B issues in between at phase 0
+    int w = 0;
+    for (int back = NS - 1; back >= 1; --back) {
+        // issues of step st - back, after A(st+1) itself (which is issued by step st+1-NS)
+        const int ph = ((T - back) % SB + SB) % SB;
+        if (back < NS - 1) w += PA;          // A issued by a later step
+        if (ph == 0) w += PB;                 // that step's B issue (after its A)
     }
+    return w;
 }
 
-// K steps [s0, s1), s0 and s1 multiples of 4 (whole super-blocks, so every
-// super-block's min term falls in one split): NS-1 stages in flight before
-// the first step, then one step at a time.
-template <int BN, int KIND, int WM>
-__device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* ring, int s0, int s1, f16v (&acc)[WM][2],
-                                          int wave, int lane) {
-    using R = Ring<BN, KIND, WM>;
-    constexpr int NS = R::NS;
-    if (s0 >= s1) return;
+__device__ __forceinline__ h8 a_frag(const uint8_t* base, int kk, int i, int lane) {
+    const int r = i * 32 + (lane & 31);
+    return lds_h8(base + (r * 8 + ((2 * kk + (lane >> 5)) ^ aswz(r))) * 16);
+}
+
+// MFMA q of a slice (32x32 block i = q/2 of the tokens, j = q%2 of the rows),
+// and the pin that keeps the companion work written after it in place: a
+// wave issues in order and an MFMA waits for the matrix pipe, so the LDS
+// reads and conversions of the next slice are placed one or two per MFMA
+// rather than in runs the scheduler would build (a run of MFMAs holds back
+// every instruction behind it).
+#define DQ_MF(AF, BF, Q) \
+    acc[(Q) >> 1][(Q)&1] = __builtin_amdgcn_mfma_f32_32x32x16_f16((AF)[(Q) >> 1], (BF)[(Q)&1], acc[(Q) >> 1][(Q)&1], 0, 0, 0)
+#define DQ_PIN() __builtin_amdgcn_sched_barrier(0)
+
+// One K step st (phase T of super-stage sb) of a wave whose registers P hold
+// the step's slice-0 fragments. Slices 0-2: each MFMA is followed by a piece
+// of the next slice's work (its four activation fragments, LDS; its weight
+// fragments, VALU) and, within a super-stage, of the next step's B side (this
+// wave's own rows: raw bytes, scales, slice-0 fragments). Then, once every A
+// read of the step is issued: the wait for the next step's stage, the
+// workgroup barrier (this stage free, the next one visible), the DMAs into
+// the freed stage (and at phase 0 the B super-stage NB-1 ahead), and slice
+// 3 with the next step's slice-0 activation fragments; at the last phase the
+// next super-stage's B side (landed by the wait), overlapped with the Q4_K
+// min-term slice. Q4_K builds the min-term weight fragments in phase 1.
+template <int NWN, int KIND, int NS, int T>
+__device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* aring, uint8_t* bring, int& astage, int sb,
+                                          int a_next, int b_next, Pre& P, f16v (&acc)[4][2], int wn, int lane) {
+    using R = Ring<NWN, KIND>;
+    constexpr int SB = R::SB, NB = R::NB;
+    constexpr bool LAST = T + 1 == SB;
+    constexpr int T1 = LAST ? 0 : T + 1;
+    constexpr bool MINT = KIND == B_Q4K && T == 3;  // min-term slice
+    const uint8_t* abase = aring + astage * R::A_STAGE;
+    const uint8_t* bbase = bring + (sb % NB) * R::B_STAGE;
+    const int next_stage = astage + 1 == NS ? 0 : astage + 1;
+    const uint8_t* anext = aring + next_stage * R::A_STAGE;
+    const uint8_t* bnext = bring + ((sb + 1) % NB) * R::B_STAGE;
+    h8 af1[4], af2[4], af3[4], bf1[2], bf2[2], bf3[2], bn[2], am[4];
+    BRaw rn;
+    BScale sn;
+    sn.magic = P.S.magic;
+    // slice 0
+    DQ_MF(P.af, P.bf, 0); af1[0] = a_frag(abase, 1, 0, lane); DQ_PIN();
+    DQ_MF(P.af, P.bf, 1); af1[1] = a_frag(abase, 1, 1, lane); DQ_PIN();
+    DQ_MF(P.af, P.bf, 2); af1[2] = a_frag(abase, 1, 2, lane); DQ_PIN();
+    DQ_MF(P.af, P.bf, 3); af1[3] = a_frag(abase, 1, 3, lane); DQ_PIN();
+    DQ_MF(P.af, P.bf, 4); bf1[0] = b_frag_j<KIND, 1>(P.raw, P.S, 0); DQ_PIN();
+    DQ_MF(P.af, P.bf, 5); if constexpr (!LAST) b_raw_j<NWN, KIND>(bbase, T1, wn, lane, rn, 0); DQ_PIN();
+    DQ_MF(P.af, P.bf, 6); bf1[1] = b_frag_j<KIND, 1>(P.raw, P.S, 1); DQ_PIN();
+    DQ_MF(P.af, P.bf, 7); if constexpr (!LAST) b_raw_j<NWN, KIND>(bbase, T1, wn, lane, rn, 1); DQ_PIN();
+    // slice 1
+    DQ_MF(af1, bf1, 0); af2[0] = a_frag(abase, 2, 0, lane); DQ_PIN();
+    DQ_MF(af1, bf1, 1); if constexpr (KIND == B_Q4K && T == 1) P.bm[0] = q4k_neg_mins(P.raw.hd[0], true); DQ_PIN();
+    DQ_MF(af1, bf1, 2); af2[1] = a_frag(abase, 2, 1, lane); af2[2] = a_frag(abase, 2, 2, lane); DQ_PIN();
+    DQ_MF(af1, bf1, 3); if constexpr (KIND == B_Q4K && T == 1) P.bm[1] = q4k_neg_mins(P.raw.hd[1], true); DQ_PIN();
+    DQ_MF(af1, bf1, 4); af2[3] = a_frag(abase, 2, 3, lane); bf2[0] = b_frag_j<KIND, 2>(P.raw, P.S, 0); DQ_PIN();
+    DQ_MF(af1, bf1, 5); if constexpr (!LAST) b_scales_j<KIND>(rn, T1, sn, 0); DQ_PIN();
+    DQ_MF(af1, bf1, 6); bf2[1] = b_frag_j<KIND, 2>(P.raw, P.S, 1); DQ_PIN();
+    DQ_MF(af1, bf1, 7); if constexpr (!LAST) b_scales_j<KIND>(rn, T1, sn, 1); DQ_PIN();
+    // slice 2
+    DQ_MF(af2, bf2, 0); af3[0] = a_frag(abase, 3, 0, lane); DQ_PIN();
+    DQ_MF(af2, bf2, 1); af3[1] = a_frag(abase, 3, 1, lane); DQ_PIN();
+    DQ_MF(af2, bf2, 2); af3[2] = a_frag(abase, 3, 2, lane); DQ_PIN();
+    DQ_MF(af2, bf2, 3); af3[3] = a_frag(abase, 3, 3, lane); DQ_PIN();
+    DQ_MF(af2, bf2, 4); bf3[0] = b_frag_j<KIND, 3>(P.raw, P.S, 0); DQ_PIN();
+    DQ_MF(af2, bf2, 5); if constexpr (!LAST) bn[0] = b_frag_j<KIND, 0>(rn, sn, 0); DQ_PIN();
+    DQ_MF(af2, bf2, 6); bf3[1] = b_frag_j<KIND, 3>(P.raw, P.S, 1); DQ_PIN();
+    DQ_MF(af2, bf2, 7); if constexpr (!LAST) bn[1] = b_frag_j<KIND, 0>(rn, sn, 1); DQ_PIN();
+    // the next step's stage, the barrier, the DMAs into this step's stage
+    wait_vm<mid_wait<NWN, KIND, NS, T>()>();
+    dq_lds_barrier();
+    issue_a<NWN, KIND>(g, aring + astage * R::A_STAGE, a_next, wn, lane);
+    if constexpr (T == 0) issue_b<NWN, KIND>(g, bring + (b_next % NB) * R::B_STAGE, b_next, wn, lane);
+    DQ_PIN();
+    // slice 3
+    DQ_MF(af3, bf3, 0); P.af[0] = a_frag(anext, 0, 0, lane); DQ_PIN();
+    DQ_MF(af3, bf3, 1); P.af[1] = a_frag(anext, 0, 1, lane); DQ_PIN();
+    DQ_MF(af3, bf3, 2); P.af[2] = a_frag(anext, 0, 2, lane); DQ_PIN();
+    DQ_MF(af3, bf3, 3); P.af[3] = a_frag(anext, 0, 3, lane); DQ_PIN();
+    DQ_MF(af3, bf3, 4); if constexpr (LAST) b_raw_j<NWN, KIND>(bnext, 0, wn, lane, P.raw, 0); DQ_PIN();
+    DQ_MF(af3, bf3, 5); if constexpr (LAST) b_raw_j<NWN, KIND>(bnext, 0, wn, lane, P.raw, 1); DQ_PIN();
+    DQ_MF(af3, bf3, 6);
+    if constexpr (MINT) {
+        am[0] = lds_h8(bbase + R::MIN + (0 * 32 + (lane & 31)) * 16);
+        am[1] = lds_h8(bbase + R::MIN + (1 * 32 + (lane & 31)) * 16);
+    }
+    DQ_PIN();
+    DQ_MF(af3, bf3, 7);
+    if constexpr (MINT) {
+        am[2] = lds_h8(bbase + R::MIN + (2 * 32 + (lane & 31)) * 16);
+        am[3] = lds_h8(bbase + R::MIN + (3 * 32 + (lane & 31)) * 16);
+    }
+    DQ_PIN();
+    if constexpr (MINT) {
+        // the super-block's min term: the block sums (lanes 0-31: the 8 K
+        // values; lanes 32-63 zero) against -dmin*m; the next super-stage's
+        // B side is converted behind it
+        const h8 zero = {};
 #pragma unroll
-    for (int p = 0; p < NS - 1; ++p) issue_stage<BN, KIND, WM>(g, ring, p, min(s0 + p, s1 - 1), wave, lane);
-    // the fp16 exponent pattern of the Q4_K nibble conversion in a VGPR (an
-    // identity DPP move the compiler cannot fold), so each nibble pair is one
-    // v_and_or_b32 (literal mask, register pattern) instead of an and + or
-    const uint32_t magic =
-        (uint32_t)__builtin_amdgcn_update_dpp((int)g.magic, (int)g.magic, 0xE4, 0xF, 0xF, false);
-    int stage = 0;
-    for (int st = s0; st < s1; ++st) {
-        gemm_step<BN, KIND, WM>(g, ring, st, stage, s1, acc, wave, lane, magic);
-        stage = stage + 1 == NS ? 0 : stage + 1;
+        for (int i = 0; i < 4; ++i) am[i] = (lane >> 5) == 0 ? am[i] : zero;
+        DQ_MF(am, P.bm, 0); b_scales_j<KIND>(P.raw, 0, P.S, 0); DQ_PIN();
+        DQ_MF(am, P.bm, 1); DQ_PIN();
+        DQ_MF(am, P.bm, 2); b_scales_j<KIND>(P.raw, 0, P.S, 1); DQ_PIN();
+        DQ_MF(am, P.bm, 3); DQ_PIN();
+        DQ_MF(am, P.bm, 4); P.bf[0] = b_frag_j<KIND, 0>(P.raw, P.S, 0); DQ_PIN();
+        DQ_MF(am, P.bm, 5); DQ_PIN();
+        DQ_MF(am, P.bm, 6); P.bf[1] = b_frag_j<KIND, 0>(P.raw, P.S, 1); DQ_PIN();
+        DQ_MF(am, P.bm, 7); DQ_PIN();
+    } else if constexpr (LAST) {
+        b_scales<KIND>(P.raw, 0, P.S);
+        b_frag<KIND, 0>(P.raw, P.S, P.bf);
+    } else {
+        P.raw = rn;
+        P.S = sn;
+        P.bf[0] = bn[0];
+        P.bf[1] = bn[1];
+    }
+    astage = next_stage;
+}
+#undef DQ_MF
+#undef DQ_PIN
+
+// The K group's super-stages [sb0, sb1) (whole super-blocks): the prologue
+// puts the first B super-stage(s) and NS A stages in flight in the order the
+// steady state would have issued them, waits for the first step's, and
+// prefetches it; then SB steps per iteration. DMAs past the range re-read the
+// group's last step / super-stage (valid addresses, never consumed).
+template <int NWN, int KIND, int NS>
+__device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* aring, uint8_t* bring, int sb0, int sb1,
+                                          f16v (&acc)[4][2], int wn, int lane) {
+    using R = Ring<NWN, KIND>;
+    constexpr int SB = R::SB, NB = R::NB, PA = a_loads<NWN>(), PB = b_loads<KIND>();
+    if (sb0 >= sb1) return;  // uniform over the workgroup (the planner gives every K group the same count)
+    const int s0 = SB * sb0, s_last = SB * sb1 - 1, sb_last = sb1 - 1;
+    issue_b<NWN, KIND>(g, bring + (sb0 % NB) * R::B_STAGE, sb0, wn, lane);
+    issue_a<NWN, KIND>(g, aring, s0, wn, lane);
+    issue_a<NWN, KIND>(g, aring + R::A_STAGE, min(s0 + 1, s_last), wn, lane);
+    if constexpr (NB == 3)
+        issue_b<NWN, KIND>(g, bring + ((sb0 + 1) % NB) * R::B_STAGE, min(sb0 + 1, sb_last), wn, lane);
+    if constexpr (NS == 3) issue_a<NWN, KIND>(g, aring + 2 * R::A_STAGE, min(s0 + 2, s_last), wn, lane);
+    // wait for B(sb0) and A(s0): the loads issued after A(s0) may stay in flight
+    wait_vm<(NS - 1) * PA + (NB == 3 ? PB : 0)>();
+    dq_lds_barrier();
+    Pre P;
+    P.S.magic = (uint32_t)__builtin_amdgcn_update_dpp((int)g.magic, (int)g.magic, 0xE4, 0xF, 0xF, false);
+    a_frags(aring, 0, lane, P.af);
+    b_raw<NWN, KIND>(bring + (sb0 % NB) * R::B_STAGE, 0, wn, lane, P.raw);
+    b_scales<KIND>(P.raw, 0, P.S);
+    b_frag<KIND, 0>(P.raw, P.S, P.bf);
+    int astage = 0;
+    for (int sb = sb0; sb < sb1; ++sb) {
+        const int st = SB * sb;
+        const int bn = min(sb + NB - 1, sb_last);
+        gemm_step<NWN, KIND, NS, 0>(g, aring, bring, astage, sb, min(st + NS, s_last), bn, P, acc, wn, lane);
+        gemm_step<NWN, KIND, NS, 1>(g, aring, bring, astage, sb, min(st + 1 + NS, s_last), bn, P, acc, wn, lane);
+        if constexpr (SB == 4) {
+            gemm_step<NWN, KIND, NS, 2>(g, aring, bring, astage, sb, min(st + 2 + NS, s_last), bn, P, acc, wn, lane);
+            gemm_step<NWN, KIND, NS, 3>(g, aring, bring, astage, sb, min(st + 3 + NS, s_last), bn, P, acc, wn, lane);
+        }
     }
     wait_vm<0>();  // drain the DMAs issued past the end
     dq_lds_barrier();
@@ -447,44 +581,79 @@ __device__ __forceinline__ void tile_of(int id, int mb, int nb, int* m_blk, int*
     *n_blk = t % nb;
 }
 
-// Register budget of two waves per SIMD (256 per lane): an 8-wave (BN 256)
-// workgroup per CU, or one or two 4-wave (BN 128) ones. Wave (wm, wn) owns
-// tokens wm*32*WM .. +32*WM and rows wn*64 .. +64 of the tile: WM 32x32
-// blocks by 2, so each dequantized weight fragment feeds WM MFMAs.
-template <int FMT, int BN, int WM>
-__global__ __launch_bounds__(2 * BN) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_kernel(
-    GemmArgs g, float* __restrict__ y, int steps, int steps_per_split, int atomic_out) {
+// Workgroup of NWN x KSW = 4 waves, one per SIMD, one workgroup per CU (its
+// LDS rings). The accumulators (128 per lane) live in AGPRs. blockIdx.z
+// selects a K split (atomic_out: partials added into zeroed y, at most 2 so
+// the sum is order-independent). KSW = 2: the K groups' partials are added
+// through LDS in group order.
+template <int FMT, int NWN, int KSW, int NS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void gemm_kernel(GemmArgs g, float* __restrict__ y, int nsb, int sb_per_split, int atomic_out) {
+    static_assert(NWN * KSW == 4, "4 waves per workgroup");
     constexpr int KIND = kind_of<FMT>();
-    constexpr int BM = bm_of<WM>();
-    __shared__ __align__(16) uint8_t ring[Ring<BN, KIND, WM>::BYTES];
+    using R = Ring<NWN, KIND>;
+    constexpr int SB = R::SB, GROUP = R::template group_bytes<NS>();
+    static_assert(KSW * GROUP <= 160 * 1024, "LDS");
+    __shared__ __align__(16) uint8_t ring[KSW * GROUP];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave & 1, wn = wave >> 1;  // 2 x (BN/64) waves of (32*WM) x 64
+    const int wn = wave % NWN, kg = wave / NWN;
     int m_blk, n_blk;
-    tile_of(blockIdx.x, (g.M + BM - 1) / BM, (g.N + BN - 1) / BN, &m_blk, &n_blk);
-    g.n0 = n_blk * BN;
+    tile_of(blockIdx.x, (g.M + BM - 1) / BM, (g.N + R::BN - 1) / R::BN, &m_blk, &n_blk);
+    g.n0 = n_blk * R::BN;
     g.m0 = m_blk * BM;
-    const int s0 = blockIdx.z * steps_per_split;
-    const int s1 = min(steps, s0 + steps_per_split);
+    // this split's super-blocks, then this K group's half (equal counts: the
+    // planner only splits even ranges), in super-stages of SB items
+    const int b0 = min(nsb, (int)blockIdx.z * sb_per_split);
+    const int b1 = min(nsb, b0 + sb_per_split);
+    const int half = (b1 - b0) / KSW;
+    const int per = 4 / SB;  // super-stages per super-block
+    const int sb0 = per * (b0 + kg * half), sb1 = per * (KSW == 1 ? b1 : b0 + (kg + 1) * half);
 
-    f16v acc[WM][2];
+    f16v acc[4][2];
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    run_steps<BN, KIND, WM>(g, ring, s0, s1, acc, wave, lane);
+    uint8_t* gr = ring + kg * GROUP;
+    run_steps<NWN, KIND, NS>(g, gr, gr + NS * R::A_STAGE, sb0, sb1, acc, wn, lane);
+
+    // K group 1 hands its partial to group 0 through the (drained) ring, one
+    // half of the tile (j) at a time: acc0 + acc1 in that order
+    if constexpr (KSW > 1) {
+        float* red = reinterpret_cast<float*>(ring) + (size_t)wn * 4 * 16 * 64;
+        static_assert(NWN * 4 * 16 * 64 * 4 <= KSW * GROUP, "reduction fits the ring");
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (kg == 1) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) red[(i * 16 + r) * 64 + lane] = acc[i][j][r];
+            }
+            __syncthreads();
+            if (kg == 0) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] += red[(i * 16 + r) * 64 + lane];
+            }
+            __syncthreads();
+        }
+        if (kg != 0) return;
+    }
 
     // D layout of 32x32x16: lane l, register r -> n = l%32, m = (r/4)*8 + (l/32)*4 + r%4.
     // The row factors 1/s of a 32-token block are loaded together before its
     // stores (unconditional loads of clamped rows; a load inside the store's
     // branch would be waited for one at a time).
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
-        const int mb0 = g.m0 + wm * 32 * WM + i * 32 + (lane >> 5) * 4;
+    for (int i = 0; i < 4; ++i) {
+        const int mb0 = g.m0 + i * 32 + (lane >> 5) * 4;
         float inv[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) inv[r] = g.inv[min(mb0 + (r >> 2) * 8 + (r & 3), g.M - 1)];
@@ -552,16 +721,17 @@ __device__ __forceinline__ void quantize_f16_block(const float* __restrict__ x, 
 #pragma unroll
         for (int i = 0; i < 4; ++i) dst[i] = __builtin_bit_cast(dq_u32x4, *reinterpret_cast<const h8*>(&h[8 * i]));
     } else if (perm == 2) {
-        // Q4_K fragment order (gemm b_frag): block b is half hi = b % 2 (the
-        // high nibbles) of item g = (b % 8) / 2; its element e is byte j = e of
-        // the item's 32 qs bytes, in sub-plane j / 16, lane half (j % 16) / 8,
-        // slice KK = 2 * plane + (j % 8) / 4, fragment slot f = 4 * (bo & 1) +
-        // (bo >> 1) + 2 * hi with bo = j % 4; column 16 KK + 8 half + f.
+        // Q4_K fragment order (gemm b_raw / b_frag): block b is half hi = b % 2
+        // (the high nibbles) of item g = (b % 8) / 2; its element e is byte
+        // j = e of the item's 32 qs bytes, in sub-plane j / 16 = the lane half
+        // that reads it, word (slice) KK = (j % 16) / 4 of that sub-plane's 16
+        // bytes, fragment slot f = 4 * (bo & 1) + (bo >> 1) + 2 * hi with
+        // bo = j % 4; column 16 KK + 8 half + f.
         const int hi = b & 1;
         _Float16* item = o + 64 * (size_t)(b / 2);
 #pragma unroll
         for (int e = 0; e < 32; ++e) {
-            const int pl = e / 16, hf = (e % 16) / 8, kk = 2 * pl + (e % 8) / 4, bo = e % 4;
+            const int hf = e / 16, kk = (e % 16) / 4, bo = e % 4;
             item[16 * kk + 8 * hf + 4 * (bo & 1) + (bo >> 1) + 2 * hi] = h[e];
         }
     } else {
@@ -675,48 +845,72 @@ extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_
     return dq_launch_status();
 }
 
-template <int FMT, int BN, int WM>
-static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int steps, int split, float* d_y, hipStream_t s) {
-    constexpr int BM = bm_of<WM>();
-    const int mb = (int)((n_tok + BM - 1) / BM), nb = (int)((rows + BN - 1) / BN);
-    const int per = (steps / 4 + split - 1) / split * 4;  // whole super-blocks per split
+template <int FMT, int NWN, int KSW, int NS>
+static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, int split, float* d_y, hipStream_t s) {
+    const int mb = (int)((n_tok + BM - 1) / BM), nb = (int)((rows + 64 * NWN - 1) / (64 * NWN));
+    const int per = (nsb + split - 1) / split;  // super-blocks per split
+    // both K groups of a workgroup must run the same number of steps (they
+    // meet at every barrier): every split's range divides evenly
+    if (KSW > 1 && (nsb % (split * KSW) != 0)) return DQ_ERR_NOT_SUPPORTED;
     if (split > 1) {
         const size_t n = rows * n_tok;
         zero_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(d_y, n);
     }
     const dim3 grid((unsigned)(mb * nb), 1, split);
-    gemm_kernel<FMT, BN, WM><<<grid, 2 * BN, 0, s>>>(g, d_y, steps, per, split > 1);
+    gemm_kernel<FMT, NWN, KSW, NS><<<grid, 256, 0, s>>>(g, d_y, nsb, per, split > 1);
     return dq_launch_status();
 }
 
-// Tile shape and K split. The K split is 2 when the tile grid leaves at
-// least half the CUs idle (two partials added atomically into zeroed y:
-// a+b == b+a, so the result is deterministic). Default: 128x256 tiles (8
-// waves of 64x64) when their grid, split included, covers 7/8 of the CUs,
-// else 128x128. The 256x256 tile (waves of 128x64, each weight fragment
-// feeding 4 MFMAs) is selectable with DQ_GEMM_WM=4 for tuning; it measured
-// slower at M = 512 (fewer, longer steps; the step is bound by its VALU and
-// LDS issue, not by the MFMA count).
+// Workgroup shapes: 4x1 (128 tokens x 256 rows, one K group, 3 A stages) or
+// 2x2 (128 x 128, the K steps split between two wave pairs, 2 A stages; not
+// for Q8_0, whose B super-stages leave no room for a second ring), optionally
+// with a 2-way K split over workgroups (two partials added atomically into
+// zeroed y: a+b == b+a, so the result is deterministic). One workgroup per
+// CU; the plan with the fewest super-blocks on the busiest CU wins (rounds of
+// the grid times super-blocks per K group), ties going to no split and then
+// to 4x1. DQ_GEMM_SHAPE (41 or 22) and DQ_GEMM_SPLIT (1 or 2) override it for
+// tuning where the override is valid.
 struct GemmPlan {
-    int bn, wm, split;
+    int nwn, split;
 };
-static size_t bm_of_rt(int wm) { return (size_t)64 * wm; }
-static GemmPlan plan_gemm(size_t rows, size_t n_tok, int steps) {
+static bool plan_ok(int fmt, int nwn, int split, int nsb) {
+    if (split == 2 && nsb < 2) return false;
+    if (nwn == 2) return fmt != DQ_FMT_Q8_0 && nsb % (2 * split) == 0;
+    return true;
+}
+static GemmPlan plan_gemm(int fmt, size_t rows, size_t n_tok, int nsb) {
     const size_t c = (size_t)cus();
-    auto make = [&](int bn, int wm) {
-        const size_t tiles = ((n_tok + bm_of_rt(wm) - 1) / bm_of_rt(wm)) * ((rows + bn - 1) / bn);
-        const int split = (tiles * 2 <= c && steps >= 8) ? 2 : 1;
-        return std::pair<GemmPlan, size_t>{GemmPlan{bn, wm, split}, tiles * split};
-    };
-    const char* fw = getenv("DQ_GEMM_WM");  // tuning overrides: tile shape and K split
+    const size_t mb = (n_tok + BM - 1) / BM;
+    GemmPlan best{4, 1};
+    size_t best_cost = ~(size_t)0;
+    for (int split = 1; split <= 2; ++split) {
+        for (int nwn = 4; nwn >= 2; nwn -= 2) {
+            if (!plan_ok(fmt, nwn, split, nsb)) continue;
+            const int ksw = 4 / nwn;
+            const size_t wgs = mb * ((rows + 64 * nwn - 1) / (64 * nwn)) * split;
+            const int per_split = (nsb + split - 1) / split;
+            const size_t cost = ((wgs + c - 1) / c) * (size_t)((per_split + ksw - 1) / ksw);
+            if (cost < best_cost) {
+                best_cost = cost;
+                best = GemmPlan{nwn, split};
+            }
+        }
+    }
+    const char* fw = getenv("DQ_GEMM_SHAPE");
     const char* fs = getenv("DQ_GEMM_SPLIT");
-    GemmPlan pl;
-    const auto wide = make(256, 2);
-    if (fw) pl = atoi(fw) == 4 ? make(256, 4).first : atoi(fw) == 2 ? wide.first : make(128, 2).first;
-    else if (wide.second * 8 >= c * 7) pl = wide.first;
-    else pl = make(128, 2).first;
-    if (fs && (atoi(fs) == 1 || atoi(fs) == 2)) pl.split = atoi(fs);
-    return pl;
+    GemmPlan o = best;
+    if (fw && (atoi(fw) == 41 || atoi(fw) == 22)) o.nwn = atoi(fw) / 10;
+    if (fs && (atoi(fs) == 1 || atoi(fs) == 2)) o.split = atoi(fs);
+    return plan_ok(fmt, o.nwn, o.split, nsb) ? o : best;
+}
+
+template <int FMT>
+static int launch_plan(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, float* d_y, hipStream_t s) {
+    const GemmPlan p = plan_gemm(FMT, rows, n_tok, nsb);
+    if constexpr (FMT != DQ_FMT_Q8_0) {
+        if (p.nwn == 2) return launch_gemm<FMT, 2, 2, 2>(g, rows, n_tok, nsb, p.split, d_y, s);
+    }
+    return launch_gemm<FMT, 4, 1, 3>(g, rows, n_tok, nsb, p.split, d_y, s);
 }
 
 // GEMM on the workspace written by dq_quantize_act_f16.
@@ -741,25 +935,15 @@ extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols
     g.M = (int)n_tok;
     g.N = (int)rows;
     g.K = (int)cols;
-    const int steps = (int)cols / BK;
-    const GemmPlan pl = plan_gemm(rows, n_tok, steps);
-    if (fmt == DQ_FMT_Q4_K) {
-        if (pl.wm == 4) return launch_gemm<DQ_FMT_Q4_K, 256, 4>(g, rows, n_tok, steps, pl.split, d_y, s);
-        if (pl.bn == 256) return launch_gemm<DQ_FMT_Q4_K, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
-        return launch_gemm<DQ_FMT_Q4_K, 128, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
+    const int nsb = (int)cols / 256;  // super-blocks (cols % 256 == 0)
+    switch (fmt) {
+    case DQ_FMT_Q4_K: return launch_plan<DQ_FMT_Q4_K>(g, rows, n_tok, nsb, d_y, s);
+    case DQ_FMT_Q8_0: return launch_plan<DQ_FMT_Q8_0>(g, rows, n_tok, nsb, d_y, s);
+    case DQ_FMT_Q4_0: return launch_plan<DQ_FMT_Q4_0>(g, rows, n_tok, nsb, d_y, s);
+    default: return launch_plan<DQ_FMT_Q6_K>(g, rows, n_tok, nsb, d_y, s);
     }
-    if (fmt == DQ_FMT_Q8_0) {
-        if (pl.bn == 256) return launch_gemm<DQ_FMT_Q8_0, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
-        return launch_gemm<DQ_FMT_Q8_0, 128, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
-    }
-    if (fmt == DQ_FMT_Q4_0) {
-        if (pl.bn == 256) return launch_gemm<DQ_FMT_Q4_0, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
-        return launch_gemm<DQ_FMT_Q4_0, 128, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
-    }
-    if (pl.wm == 4) return launch_gemm<DQ_FMT_Q6_K, 256, 4>(g, rows, n_tok, steps, pl.split, d_y, s);
-    if (pl.bn == 256) return launch_gemm<DQ_FMT_Q6_K, 256, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
-    return launch_gemm<DQ_FMT_Q6_K, 128, 2>(g, rows, n_tok, steps, pl.split, d_y, s);
 }
+
 
 extern "C" int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,
                        float* d_y, void* d_work, size_t work_bytes, void* stream) {

@@ -316,9 +316,10 @@ __global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ v
 
 // x = row *tok of a packed Q8_0 matrix, d * q in float, times mul when
 // non-zero (the embedding of the pipelined decode's next token,
-// backend_cuda.cu:3555-3566). Packed layout: block B's 32 values are bytes
-// [16 (B/2), +16) of sub-planes 2 (B%2) and 2 (B%2) + 1.
-__global__ __launch_bounds__(256) void embed_q8_0_kernel(const uint8_t* __restrict__ qp, size_t ps,
+// backend_cuda.cu:3555-3566). Packed layout: block b of row t holds its 32
+// values in bytes [t q_row + 16 (b/2), +16) of sub-planes 2 (b%2) and
+// 2 (b%2) + 1.
+__global__ __launch_bounds__(256) void embed_q8_0_kernel(const uint8_t* __restrict__ qp, size_t ps, size_t q_row,
                                                          const uint16_t* __restrict__ dp, const int32_t* __restrict__ tok,
                                                          uint32_t rows, uint32_t cols, float mul, float* __restrict__ x) {
     int32_t t = *tok;
@@ -327,7 +328,7 @@ __global__ __launch_bounds__(256) void embed_q8_0_kernel(const uint8_t* __restri
         const size_t B = (size_t)t * (cols / 32) + i / 32;
         const uint32_t w = i % 32;
         const size_t plane = 2 * (B % 2) + (w >= 16 ? 1 : 0);
-        const int8_t q = (int8_t)qp[plane * ps + 16 * (B / 2) + (w & 15)];
+        const int8_t q = (int8_t)qp[plane * ps + (size_t)t * q_row + 16 * (i / 64) + (w & 15)];
         float val = dq_h2f(dp[B]) * (float)q;
         if (mul != 0.0f) val *= mul;
         x[i] = val;
@@ -440,7 +441,7 @@ int dq_embed_q8_0(const void* d_w, size_t rows, size_t cols, const int32_t* d_to
     if (rows > 0x7FFFFFFF || cols > 0xFFFFFFFFu) return DQ_ERR_NOT_SUPPORTED;
     const uint8_t* base = (const uint8_t*)d_w;
     const unsigned grid = (unsigned)((cols + 255) / 256 < 64 ? (cols + 255) / 256 : 64);
-    embed_q8_0_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(base + L.q_off, L.p_stride,
+    embed_q8_0_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(base + L.q_off, L.p_stride, L.q_row,
                                                              (const uint16_t*)(base + L.d_off), d_tok, (uint32_t)rows,
                                                              (uint32_t)cols, mul, d_x);
     return dq_launch_status();
