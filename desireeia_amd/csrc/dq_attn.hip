@@ -105,7 +105,7 @@ struct AttnArgs {
     int n_kv, cc_start, pos_host, n_ctx, max_tiles;
     const int* pos_dev;
     float scale;
-    float* part;          // [n_kv][max_tiles][HPK][HD + 2]
+    float* part;          // [n_kv][max_tiles][HPK][HD + 4]
     float* out;           // [n_head][HD]
     int8_t* oq;           // fused per-256 quantization (or NULL)
     float* oscale;
@@ -121,12 +121,15 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
     constexpr int DP = HD / 2;           // dim pairs (V phase)
     constexpr int PG = NT / DP;          // position groups (V phase)
     constexpr int PPG = TP / PG;         // positions per group
-    constexpr int STAGE_IT = (TP * RBW + NT - 1) / NT;
-    constexpr int REC = HD + 2;
-    static_assert(HD == 128 && RB % 4 == 0 && NT % DP == 0 && TP % PG == 0, "shape");
+    constexpr int RBQ = RB / 8;          // row 8-byte words (rows are 8-byte aligned)
+    constexpr int STAGE_IT = (TP * RBQ + NT - 1) / NT;
+    constexpr int REC = HD + 4;     // acc[HD], max, sum, 2 pad (16-byte records)
+    static_assert(HD == 128 && RB % 8 == 0 && NT % DP == 0 && TP % PG == 0, "shape");
 
-    __shared__ uint32_t ks[TP * RBW];
-    __shared__ uint32_t vs[TP * RBW];
+    __shared__ uint64_t ks8[TP * RBQ];
+    __shared__ uint64_t vs8[TP * RBQ];
+    uint32_t* ks = reinterpret_cast<uint32_t*>(ks8);
+    uint32_t* vs = reinterpret_cast<uint32_t*>(vs8);
     __shared__ float qt[HD][HPK];        // query, transposed
     __shared__ float qsum[NB][HPK];      // per-block sums of the query
     __shared__ float sp[NB][HPK][TP];    // per-block partial scores
@@ -166,8 +169,8 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
             rs = A.rope[2 * lane + 1];
         }
     }
-    // ---- K / V rows of the tile: issued next, staged after the query
-    uint32_t kr[STAGE_IT], vr[STAGE_IT];
+    // ---- K / V rows of the tile (8 bytes per load): issued next, staged after the query
+    uint64_t kr[STAGE_IT], vr[STAGE_IT];
     {
         const uint8_t* kb = A.kc + (size_t)p0 * A.pos_bytes + (size_t)kvh * RB;
         const uint8_t* vb = A.vc + (size_t)p0 * A.pos_bytes + (size_t)kvh * RB;
@@ -177,10 +180,10 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
         const int rmax = n_load > 0 ? n_load - 1 : 0;
 #pragma unroll
         for (int it = 0; it < STAGE_IT; ++it) {
-            const int i = min(tid + it * NT, TP * RBW - 1);
-            const int r = min(i / RBW, rmax), c = i % RBW;
-            kr[it] = *reinterpret_cast<const uint32_t*>(kb + (size_t)r * A.pos_bytes + 4 * c);
-            vr[it] = *reinterpret_cast<const uint32_t*>(vb + (size_t)r * A.pos_bytes + 4 * c);
+            const int i = min(tid + it * NT, TP * RBQ - 1);
+            const int r = min(i / RBQ, rmax), c = i % RBQ;
+            kr[it] = *reinterpret_cast<const uint64_t*>(kb + (size_t)r * A.pos_bytes + 8 * c);
+            vr[it] = *reinterpret_cast<const uint64_t*>(vb + (size_t)r * A.pos_bytes + 8 * c);
         }
     }
     // ---- query of the HPK heads (rotated under FUSE: wave w takes heads w, w+NW)
@@ -204,9 +207,9 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
 #pragma unroll
     for (int it = 0; it < STAGE_IT; ++it) {
         const int i = tid + it * NT;
-        if (i < TP * RBW && i / RBW < n_load) {
-            ks[i] = kr[it];
-            vs[i] = vr[it];
+        if (i < TP * RBQ && i / RBQ < n_load) {
+            ks8[i] = kr[it];
+            vs8[i] = vr[it];
         }
     }
     if constexpr (FUSE) {
@@ -329,71 +332,80 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
 }
 
 // Merge of the tile records: workgroup b owns outputs [256b, 256b + 256) of
-// the flattened [n_head][HD] output (HD = 128: two heads). Thread (g, o)
-// takes tiles g, g+MG, ... of its head in batches of MB (all of a batch's
-// record loads in flight at once: one memory round trip for up to MG*MB
-// tiles) and keeps an online softmax state (running max M, sum L of
-// e^(m_t - M) l_t, and acc of e^(m_t - M) acc_t); the MG group states are then
-// combined in group order, each rescaled to the common max. Optionally
-// quantizes the 256 outputs per 256 (core/matmul.cpp:1660-1778).
-constexpr int MG = 4;                 // tile groups of the merge
+// the flattened [n_head][HD] output (HD = 128: two heads). Thread (g, q)
+// takes output quad q (4 consecutive outputs, one 16-byte record load per
+// tile) and tiles g, g+MG, ... in batches of MB (all of a batch's record
+// loads in flight at once: one memory round trip for up to MG*MB tiles),
+// keeping an online softmax state (running max M, sum L of e^(m_t - M) l_t,
+// and acc of e^(m_t - M) acc_t); the MG group states are then combined in
+// group order, each rescaled to the common max. Optionally quantizes the 256
+// outputs per 256 (core/matmul.cpp:1660-1778).
 constexpr int MNO = 256;              // outputs per merge workgroup
-constexpr int MNT = MG * MNO;         // its threads
-constexpr int MB = 20;                // tiles per batch and thread
+constexpr int MQ = MNO / 4;           // output quads
+constexpr int MG = 16;                // tile groups of the merge
+constexpr int MNT = MG * MQ;          // its threads
+constexpr int MB = 6;                 // tiles per batch and thread
 template <int HD, int HPK>
 __global__ __launch_bounds__(MNT) void attn_merge_kernel(AttnArgs A) {
-    constexpr int REC = HD + 2;
+    constexpr int REC = HD + 4;
     constexpr int HPB = MNO / HD;        // heads per block
-    constexpr int NWV = MNT / 64;        // waves
-    static_assert(MNO % HD == 0 && MNO == NT, "whole heads per block");
-    __shared__ float wred[NWV];
+    constexpr int NWO = MNO / 64;        // waves holding the final outputs
+    static_assert(MNO % HD == 0 && MNO == NT && HD % 4 == 0, "whole heads per block");
+    __shared__ float wred[NWO];
     __shared__ float gm[MG][HPB], gl[MG][HPB];
-    __shared__ float pacc[MG][MNO];
+    __shared__ float4 pacc[MG][MQ];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int g = tid / MNO, ol = tid % MNO;     // tile group, output in the block
+    const int g = tid / MQ, qd = tid % MQ;        // tile group, output quad
     const int pos = read_pos(A.pos_host, A.pos_dev, A.n_ctx);
     const int c0 = A.cc_start < pos ? A.cc_start : pos;
     const int n_tiles = min((pos + 1 - c0 + TP - 1) / TP, A.max_tiles);
-    const int o = blockIdx.x * MNO + ol;          // flattened output
-    const int hb = ol / HD;                       // head within the block
-    const int hq = blockIdx.x * HPB + hb;         // query head
-    const int kvh = hq / HPK, h = hq % HPK, dd = o % HD;
-    const float* recs = A.part + ((size_t)kvh * A.max_tiles * HPK + h) * REC;  // tile t at + t*HPK*REC
-    float M = -INFINITY, L = 0.0f, a = 0.0f;
-    for (int tb = g; tb < n_tiles; tb += MG * MB) {
-        float v[MB], mm[MB], ll[MB];
+    {
+        const int ol = 4 * qd;                    // first output of the quad in the block
+        const int hb = ol / HD;                   // head within the block
+        const int hq = blockIdx.x * HPB + hb;     // query head
+        const int kvh = hq / HPK, h = hq % HPK, dd = ol % HD;
+        const float* recs = A.part + ((size_t)kvh * A.max_tiles * HPK + h) * REC;  // tile t at + t*HPK*REC
+        float M = -INFINITY, L = 0.0f;
+        float4 a = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int tb = g; tb < n_tiles; tb += MG * MB) {
+            float4 v[MB];
+            float2 ml[MB];
 #pragma unroll
-        for (int k = 0; k < MB; ++k) {
-            const float* r = recs + (size_t)min(tb + MG * k, n_tiles - 1) * HPK * REC;
-            v[k] = r[dd];
-            mm[k] = r[HD];
-            ll[k] = r[HD + 1];
-        }
-        float bm = M;
-#pragma unroll
-        for (int k = 0; k < MB; ++k)
-            if (tb + MG * k < n_tiles) bm = fmaxf(bm, mm[k]);
-        const float sc = __expf(M - bm);  // M = -inf on the first batch: 0
-        a *= sc;
-        L *= sc;
-#pragma unroll
-        for (int k = 0; k < MB; ++k)
-            if (tb + MG * k < n_tiles) {
-                const float w = __expf(mm[k] - bm);
-                a = fmaf(w, v[k], a);
-                L = fmaf(w, ll[k], L);
+            for (int k = 0; k < MB; ++k) {
+                const float* r = recs + (size_t)min(tb + MG * k, n_tiles - 1) * HPK * REC;
+                v[k] = *reinterpret_cast<const float4*>(r + dd);
+                ml[k] = *reinterpret_cast<const float2*>(r + HD);
             }
-        M = bm;
-    }
-    pacc[g][ol] = a;
-    if (dd == 0) {
-        gm[g][hb] = M;
-        gl[g][hb] = L;
+            float bm = M;
+#pragma unroll
+            for (int k = 0; k < MB; ++k)
+                if (tb + MG * k < n_tiles) bm = fmaxf(bm, ml[k].x);
+            const float sc = __expf(M - bm);  // M = -inf on the first batch: 0
+            a.x *= sc, a.y *= sc, a.z *= sc, a.w *= sc;
+            L *= sc;
+#pragma unroll
+            for (int k = 0; k < MB; ++k)
+                if (tb + MG * k < n_tiles) {
+                    const float w = __expf(ml[k].x - bm);
+                    a.x = fmaf(w, v[k].x, a.x);
+                    a.y = fmaf(w, v[k].y, a.y);
+                    a.z = fmaf(w, v[k].z, a.z);
+                    a.w = fmaf(w, v[k].w, a.w);
+                    L = fmaf(w, ml[k].y, L);
+                }
+            M = bm;
+        }
+        pacc[g][qd] = a;
+        if (dd == 0) {
+            gm[g][hb] = M;
+            gl[g][hb] = L;
+        }
     }
     __syncthreads();
-    // group 0 (waves 0 .. MNO/64-1) finishes; the others stay for the barriers
+    // the first MNO threads finish output o = tid; the others stay for the barriers
     float v = 0.0f;
-    if (g == 0) {
+    if (tid < MNO) {
+        const int hb = tid / HD;
         float Mt = gm[0][hb];
 #pragma unroll
         for (int q = 1; q < MG; ++q) Mt = fmaxf(Mt, gm[q][hb]);
@@ -401,25 +413,26 @@ __global__ __launch_bounds__(MNT) void attn_merge_kernel(AttnArgs A) {
 #pragma unroll
         for (int q = 0; q < MG; ++q) {
             const float w = __expf(gm[q][hb] - Mt);  // a group with no tile: e^-inf = 0
-            acc = fmaf(w, pacc[q][ol], acc);
+            acc = fmaf(w, pacc[q][tid / 4][tid % 4], acc);
             Lt = fmaf(w, gl[q][hb], Lt);
         }
         v = acc / Lt;
-        A.out[o] = v;
+        A.out[(size_t)blockIdx.x * MNO + tid] = v;
     }
     if (!A.oq) return;  // uniform
     // per-256 quantization of the block's 256 outputs
     const float am = dq_wave_max(fabsf(v));
-    if (lane == 0) wred[wave] = am;
+    if (lane == 0 && wave < NWO) wred[wave] = am;
     __syncthreads();
-    if (g != 0) return;
+    if (tid >= MNO) return;
     float amax = wred[0];
 #pragma unroll
-    for (int w = 1; w < MNO / 64; ++w) amax = fmaxf(amax, wred[w]);
+    for (int w = 1; w < NWO; ++w) amax = fmaxf(amax, wred[w]);
     const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
     const float id = d > 0.0f ? 127.0f / amax : 0.0f;
     int iv = (int)rintf(v * id);
     iv = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
+    const int o = blockIdx.x * MNO + tid;
     A.oq[o] = (int8_t)iv;
     int sum = iv;
 #pragma unroll
@@ -433,7 +446,7 @@ __global__ __launch_bounds__(MNT) void attn_merge_kernel(AttnArgs A) {
 // Workspace: the tile records.
 int max_tiles_for(uint32_t n_ctx) { return (int)((n_ctx + TP - 1) / TP); }
 size_t work_bytes_for(int n_head, int hd, int max_tiles) {
-    return dq_align256((size_t)n_head * max_tiles * (hd + 2) * sizeof(float));
+    return dq_align256((size_t)n_head * max_tiles * (hd + 4) * sizeof(float));
 }
 
 template <int HD, int HPK, bool FUSE>

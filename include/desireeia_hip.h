@@ -183,8 +183,8 @@ int dq_attn_decode_q8(const float* d_q, const void* d_kc, const void* d_vc, uint
  * capture or a serving loop that forbids hipMalloc). Same arguments and
  * results without d_work: the tile records live in a static 16 MiB device
  * array of the library, one per GPU, held until the process ends. Shapes whose
- * dq_attn_workspace_bytes exceeds 16 MiB (n_head * ceil(n_ctx / 64) * 520
- * bytes at hd = 128: 32 heads up to n_ctx = 64512) return
+ * dq_attn_workspace_bytes exceeds 16 MiB (n_head * ceil(n_ctx / 64) * 528
+ * bytes at hd = 128: 32 heads up to n_ctx = 63488) return
  * DQ_ERR_NOT_SUPPORTED and do nothing. Every call on a GPU shares that GPU's
  * array: calls that overlap on one GPU (other streams, other threads) race. It
  * calls no hipMalloc/hipFree; its first call on a device looks the array's

@@ -216,3 +216,22 @@ def test_attention_rope_kv_fused(gpu, orc, n_head, n_kv, pos, rope, quant):
         assert np.array_equal(act.q.cpu().numpy(), wq)
         assert np.array_equal(act.scale.cpu().numpy(), wd)
         assert np.array_equal(act.isum.cpu().numpy(), wi)
+
+
+def test_attention_workspace_reuse(gpu, orc):
+    """One workspace through calls of every size class (one tile, a partial
+    last tile, tile boundaries, a long context, back to short): each output
+    matches the oracle, so no call reads another call's records."""
+    n_head, n_kv, n_ctx = 32, 8, 5000
+    kc, vc = host_cache(orc, n_ctx, n_kv, seed=41)
+    cache = device_cache(gpu, kc, vc, n_ctx, n_kv)
+    work = ops.attn_workspace(n_head, n_kv, HD, n_ctx, gpu)
+    out = torch.empty(n_head * HD, dtype=torch.float32, device=gpu)
+    rng = np.random.default_rng(42)
+    for pos in (4999, 0, 127, 128, 4095, 255, 1, 4999):
+        q = rng.standard_normal(n_head * HD).astype(np.float32)
+        ops.attention_decode(torch.from_numpy(q).to(gpu), cache, n_head, pos, out=out, work=work)
+        torch.cuda.synchronize()
+        e = rel(out.cpu().numpy(), orc.attn_decode(q, kc, vc, n_head, n_kv, HD, 0, pos))
+        print(f"  pos={pos}: rel err {e:.3e}", flush=True)
+        assert e <= TOL

@@ -52,18 +52,18 @@ def test_noalloc_matches_allocating_entry_point(gpu, orc):
 
 
 def test_noalloc_rejects_oversized_shape(gpu):
-    """32 heads of 128 need 520 bytes per head and 64-position tile: the
-    16 MiB scratch covers 64512 positions; one more is refused, nothing runs."""
+    """32 heads of 128 need 528 bytes per head and 64-position tile: the
+    16 MiB scratch covers 63488 positions; one more is refused, nothing runs."""
     lib = _lib.load()
     n = ctypes.c_size_t(0)
-    _lib.check(lib.dq_attn_workspace_bytes(32, 8, HD, 64512, ctypes.byref(n)), "dq_attn_workspace_bytes")
+    _lib.check(lib.dq_attn_workspace_bytes(32, 8, HD, 63488, ctypes.byref(n)), "dq_attn_workspace_bytes")
     assert n.value <= 16 << 20
-    _lib.check(lib.dq_attn_workspace_bytes(32, 8, HD, 64513, ctypes.byref(n)), "dq_attn_workspace_bytes")
+    _lib.check(lib.dq_attn_workspace_bytes(32, 8, HD, 63489, ctypes.byref(n)), "dq_attn_workspace_bytes")
     assert n.value > 16 << 20
     q = torch.zeros(32 * HD, device=gpu)
     kc = torch.zeros(8 * 136, dtype=torch.uint8, device=gpu)  # position 0's rows, were anything to run
     out = torch.full((32 * HD,), 7.0, device=gpu)
-    rc = lib.dq_attn_decode_q8_noalloc(ops._ptr(q), ops._ptr(kc), ops._ptr(kc), 32, 8, HD, 0, 0, None, 64513,
+    rc = lib.dq_attn_decode_q8_noalloc(ops._ptr(q), ops._ptr(kc), ops._ptr(kc), 32, 8, HD, 0, 0, None, 63489,
                                        ops._ptr(out), ops._stream())
     assert rc == -2  # DQ_ERR_NOT_SUPPORTED
     torch.cuda.synchronize()
