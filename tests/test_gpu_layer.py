@@ -23,41 +23,56 @@ def rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
+class HostLayer:
+    """The host side of a synthetic layer: weights, norms, the prior cache and
+    the oracle's arguments, with the shape attributes the stage chains read
+    (n_head, n_head_kv, mats[nm].fmt/rows/cols, cache.pos_bytes)."""
+
+    def __init__(self, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None):
+        from types import SimpleNamespace as NS
+
+        from oracle.oracle import LayerArgs
+        hd = 128
+        qd, kvd = n_head * hd, n_kv * hd
+        # Q4_K_M mix: Q4_K everywhere but attn_v and ffn_down (Q6_K)
+        shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
+                  "gate": (Q4K, F, E), "up": (Q4K, F, E), "down": (Q6K, E, F)}
+        for nm, qt in (types or {}).items():
+            shapes[nm] = (qt,) + shapes[nm][1:]
+        self.shapes = shapes
+        gg = {nm: (qt, synth.gen_weights(qt, r, c, seed=seed + i)) for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
+        rng = np.random.default_rng(seed)
+        self.attn_norm = (norm_scale[0] * (1 + 0.02 * rng.standard_normal(E))).astype(np.float32)
+        self.ffn_norm = (norm_scale[1] * (1 + 0.02 * rng.standard_normal(E))).astype(np.float32)
+        self.n_head, self.n_head_kv = n_head, n_kv
+        self.mats = {nm: NS(fmt=synth.FMT_OF_TYPE[qt], rows=r, cols=c) for nm, (qt, r, c) in shapes.items()}
+        pb = n_kv * hd // 32 * 34
+        self.cache = NS(pos_bytes=pb)
+        # prior cache: N(0,1) rows quantized (kv_quantize_row)
+        self.kc = np.zeros(n_ctx * pb, np.uint8)
+        self.vc = np.zeros(n_ctx * pb, np.uint8)
+        if n_prior:
+            self.kc[:n_prior * pb] = orc.kv_quantize_row(rng.standard_normal(n_prior * kvd).astype(np.float32))
+            self.vc[:n_prior * pb] = orc.kv_quantize_row(rng.standard_normal(n_prior * kvd).astype(np.float32))
+        self.args = LayerArgs(E, n_head, n_kv, hd, F, 1e-5, 500000.0,
+                              *[shapes[nm][0] for nm in ("q", "k", "v", "o", "gate", "up", "down")])
+        self.keep = {nm: np.ascontiguousarray(w) for nm, (qt, w) in gg.items()}
+        self.keep["attn_norm"], self.keep["ffn_norm"] = self.attn_norm, self.ffn_norm
+        for nm in ("q", "k", "v", "o", "gate", "up", "down"):
+            setattr(self.args, "w" + nm, self.keep[nm].ctypes.data)
+        self.args.attn_norm = self.attn_norm.ctypes.data
+        self.args.ffn_norm = self.ffn_norm.ctypes.data
+
+
 def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None):
-    from oracle.oracle import LayerArgs
-    hd = 128
-    qd, kvd = n_head * hd, n_kv * hd
-    # Q4_K_M mix: Q4_K everywhere but attn_v and ffn_down (Q6_K)
-    shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
-              "gate": (Q4K, F, E), "up": (Q4K, F, E), "down": (Q6K, E, F)}
-    for nm, qt in (types or {}).items():
-        shapes[nm] = (qt,) + shapes[nm][1:]
-    gg = {nm: (qt, synth.gen_weights(qt, r, c, seed=seed + i)) for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
-    rng = np.random.default_rng(seed)
-    attn_norm = (norm_scale[0] * (1 + 0.02 * rng.standard_normal(E))).astype(np.float32)
-    ffn_norm = (norm_scale[1] * (1 + 0.02 * rng.standard_normal(E))).astype(np.float32)
-    mats = {nm: ops.QuantMatrix.from_gguf(qt, w, shapes[nm][1], shapes[nm][2], device=gpu)
-            for nm, (qt, w) in gg.items()}
-    layer = ops.DecoderLayer(mats, torch.from_numpy(attn_norm), torch.from_numpy(ffn_norm), n_head, n_kv, hd, n_ctx,
-                             device=gpu)
-    # prior cache: N(0,1) rows quantized (kv_quantize_row)
-    pb = layer.cache.pos_bytes
-    kc = np.zeros(n_ctx * pb, np.uint8)
-    vc = np.zeros(n_ctx * pb, np.uint8)
-    if n_prior:
-        kc[:n_prior * pb] = orc.kv_quantize_row(rng.standard_normal(n_prior * kvd).astype(np.float32))
-        vc[:n_prior * pb] = orc.kv_quantize_row(rng.standard_normal(n_prior * kvd).astype(np.float32))
-    layer.cache.k.copy_(torch.from_numpy(kc))
-    layer.cache.v.copy_(torch.from_numpy(vc))
-    args = LayerArgs(E, n_head, n_kv, hd, F, 1e-5, 500000.0,
-                     *[shapes[nm][0] for nm in ("q", "k", "v", "o", "gate", "up", "down")])
-    keep = {nm: np.ascontiguousarray(w) for nm, (qt, w) in gg.items()}
-    keep["attn_norm"], keep["ffn_norm"] = attn_norm, ffn_norm
-    for nm in ("q", "k", "v", "o", "gate", "up", "down"):
-        setattr(args, "w" + nm, keep[nm].ctypes.data)
-    args.attn_norm = attn_norm.ctypes.data
-    args.ffn_norm = ffn_norm.ctypes.data
-    return layer, args, keep, kc, vc
+    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types)
+    mats = {nm: ops.QuantMatrix.from_gguf(qt, h.keep[nm], r, c, device=gpu) for nm, (qt, r, c) in h.shapes.items()}
+    layer = ops.DecoderLayer(mats, torch.from_numpy(h.attn_norm), torch.from_numpy(h.ffn_norm), n_head, n_kv, 128,
+                             n_ctx, device=gpu)
+    assert layer.cache.pos_bytes == h.cache.pos_bytes
+    layer.cache.k.copy_(torch.from_numpy(h.kc))
+    layer.cache.v.copy_(torch.from_numpy(h.vc))
+    return layer, h.args, h.keep, h.kc, h.vc
 
 
 def dequant_rows(orc, b, n):

@@ -10,13 +10,15 @@ What is pinned, and to what bound:
     points (host norm / RoPE / SiLU, which match the GPU bit for bit);
   * the oracle's layer equals a composition of its pieces done here in
     numpy (1e-6);
-  * end to end, layer output within 3e-2 norm-wise of the oracle.
-The end-to-end bound is loose by construction: the layer re-quantizes its
-intermediates five times (the K/V rows and the per-32 int8 inputs of four
-GEMMs). A product difference e flips ~127 e / (amax / rms) of those roundings
-by one step (1/50 of the rms each), ~8x per stage, and the synthetic Q4_K
-weights (entry mean 1.4 against rms 2.2) make some tokens' products nearly
-cancel, amplifying relative differences further: tokens measure 2e-3 to 6e-2.
+  * end to end, layer output within 1.5e-2 norm-wise of the oracle.
+The end-to-end bound is what the products' own rounding explains: the layer
+re-quantizes its intermediates five times (the K/V rows and the per-32 int8
+inputs of four GEMMs), and the synthetic Q4_K weights (entry mean 1.4 against
+rms 2.2) make some tokens' products nearly cancel, so a product error is
+amplified on the way out. test_oracle_sensitivity.py perturbs the oracle's
+own products by the 4e-4 the GPU's measure and finds the layer moving by up
+to ~9e-3 (single tokens up to ~0.35); the GPU measures 1.6e-5 .. 6.7e-3 on
+these cases (tokens 2e-3 to 0.26).
 The layers use RMSNorm weights of 0.25 / sqrt(E) and 0.3 / sqrt(E) so that
 scores and FFN activations are O(1) (with unit norms a 4096-wide layer's
 softmax is an argmax); the chunking test, GPU against GPU, keeps unit norms.
@@ -33,7 +35,7 @@ from test_gpu_layer import dequant_rows, make_layer, rel
 pytestmark = pytest.mark.gpu
 TOL_GEMM = 4e-3
 TOL_ATTN = 1e-3
-TOL_LAYER = 3e-2
+TOL_LAYER = 1.5e-2  # 1.5x the oracle's own move under 4e-4 product errors (test_oracle_sensitivity.py)
 HD = 128
 
 
@@ -202,6 +204,8 @@ def test_layer_prefill_window_and_errors(gpu, orc):
     x = np.random.default_rng(42).standard_normal((50, E)).astype(np.float32)
     got = layer.prefill(torch.from_numpy(x).to(gpu), 10, n_swa=16).cpu().numpy()
     want = orc.layer_prefill(args, kc, vc, 10, x, n_swa=16)
-    assert rel(got, want) <= TOL_LAYER
+    e = rel(got, want)
+    print(f"  window 16: layer vs oracle {e:.2e}", flush=True)
+    assert e <= TOL_LAYER
     with pytest.raises(_lib.DqError):
         layer.prefill(torch.from_numpy(x).to(gpu), 40)  # 40 + 50 > n_ctx

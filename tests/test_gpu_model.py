@@ -17,7 +17,7 @@ import gguf_writer as gw
 
 pytestmark = pytest.mark.gpu
 E, H, KV, HD, F, V, NL = 512, 8, 2, 128, 1024, 3000, 2
-TOL_LOGITS = 3e-2
+TOL_LOGITS = 3e-2  # the oracle's own logits move ~2e-2 under 4e-4 product errors (test_oracle_sensitivity.py)
 
 
 def rel(a, b):
