@@ -573,12 +573,18 @@ __device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* aring, uin
 // Tile index -> (m block, n block): tiles are ordered m-major and handed to
 // the 8 XCDs in contiguous ranges (workgroup id % 8 is its XCD), so the
 // workgroups of one XCD share their activation rows in that XCD's L2.
+// Tile of workgroup `id`. Workgroups are dealt to the 8 XCDs round-robin (id
+// % 8), each XCD with its own L2: XCD x takes the x-th eighth of the tiles,
+// ordered M-block fastest, so the M blocks sharing a weight tile run at the
+// same time on one XCD and the weight bytes come from HBM once per XCD
+// instead of once per M block (Q8_0 142 -> 113 us, Q6_K 142 -> 122 us at
+// M = 512).
 __device__ __forceinline__ void tile_of(int id, int mb, int nb, int* m_blk, int* n_blk) {
     const int total = mb * nb;
     int t = id;
     if (total % 8 == 0) t = (id % 8) * (total / 8) + id / 8;
-    *m_blk = t / nb;
-    *n_blk = t % nb;
+    *m_blk = t % mb;
+    *n_blk = t / mb;
 }
 
 // Workgroup of NWN x KSW = 4 waves, one per SIMD, one workgroup per CU (its
