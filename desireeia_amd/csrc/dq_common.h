@@ -223,3 +223,23 @@ __device__ __forceinline__ void dq_q8_0_row128(float lo, float hi, int j, uint8_
 // Host-side status from a HIP error.
 static inline int dq_status(hipError_t e) { return e == hipSuccess ? DQ_OK : DQ_ERR_IO; }
 static inline int dq_launch_status() { return dq_status(hipGetLastError()); }
+
+// Float ranges an activation quantizer launch clears on the side (the
+// outputs of the K-split GEMMs that read its result next); counts are
+// multiples of 4, pointers 16-byte aligned, unused slots null.
+struct DqZeroSpans {
+    static constexpr int N = 3;
+    float* p[N] = {nullptr, nullptr, nullptr};
+    size_t n[N] = {0, 0, 0};
+};
+// Library-internal parts of the prefill GEMM (dq_gemm.hip): the quantizer
+// with spans to clear, whether a product's plan adds K-split partials into y
+// (so y must start at zero), and the GEMM on a y already cleared.
+int dq_quantize_act_f16_zero(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_out,
+                             const DqZeroSpans& z, void* stream);
+bool dq_gemm_adds_into_y(int fmt, size_t rows, size_t cols, size_t n_tok);
+int dq_gemm_f16act_zeroed(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work, size_t n_tok,
+                          float* d_y, bool y_zeroed, void* stream);
+static inline bool dq_zero_span_ok(const float* p, size_t n) {
+    return p && n % 4 == 0 && reinterpret_cast<uintptr_t>(p) % 16 == 0;
+}

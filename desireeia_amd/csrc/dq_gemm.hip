@@ -757,13 +757,24 @@ __device__ __forceinline__ void quantize_f16_block(const float* __restrict__ x, 
 
 // One workgroup per token row: the row's power-of-two range scale (as
 // row_scale_kernel) and then every block of the row (quantize_f16_block);
-// inv[t] = 1/s.
+// inv[t] = 1/s. The workgroups also clear the outputs of the K-split GEMMs
+// that read this activation next (z: their float counts, multiples of 4,
+// split evenly over the workgroups), which saves those GEMMs a fill launch.
 __global__ __launch_bounds__(256) void quantize_f16_rows_kernel(const float* __restrict__ x, int cols, int n_tok,
                                                                 _Float16* __restrict__ out, int lda,
                                                                 _Float16* __restrict__ minp, int perm,
-                                                                float* __restrict__ rscale, float* __restrict__ inv) {
+                                                                float* __restrict__ rscale, float* __restrict__ inv,
+                                                                DqZeroSpans z) {
     __shared__ float wmax[4];
     const int t = blockIdx.x;
+#pragma unroll
+    for (int k = 0; k < DqZeroSpans::N; ++k) {
+        if (!z.p[k]) continue;
+        const size_t n4 = z.n[k] / 4, per = (n4 + gridDim.x - 1) / gridDim.x;
+        const size_t e = min(n4, per * (t + 1));
+        for (size_t i = per * t + threadIdx.x; i < e; i += 256)
+            reinterpret_cast<float4*>(z.p[k])[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     const float* row = x + (size_t)t * cols;
     float m = 0.0f;
     for (int c = threadIdx.x * 4; c < cols; c += 1024) {
@@ -830,8 +841,8 @@ extern "C" int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t
     return DQ_OK;
 }
 
-extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_out,
-                                   void* stream) {
+int dq_quantize_act_f16_zero(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_out,
+                             const DqZeroSpans& z, void* stream) {
     if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K && fmt != DQ_FMT_Q8_0 && fmt != DQ_FMT_Q4_0)
         return DQ_ERR_NOT_SUPPORTED;
     if (cols % 256 || cols > (1u << 24) || n_tok > (1u << 20)) return DQ_ERR_NOT_SUPPORTED;
@@ -847,18 +858,24 @@ extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_
     (void)lanes;
     quantize_f16_rows_kernel<<<(unsigned)n_tok, 256, 0, (hipStream_t)stream>>>(
         d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)act_lda(cols), minp,
-        fmt == DQ_FMT_Q6_K ? 1 : (fmt == DQ_FMT_Q4_K ? 2 : 0), sc, inv);
+        fmt == DQ_FMT_Q6_K ? 1 : (fmt == DQ_FMT_Q4_K ? 2 : 0), sc, inv, z);
     return dq_launch_status();
 }
 
+extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_out,
+                                   void* stream) {
+    return dq_quantize_act_f16_zero(fmt, d_x, cols, n_tok, d_out, DqZeroSpans{}, stream);
+}
+
 template <int FMT, int NWN, int KSW, int NS>
-static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, int split, float* d_y, hipStream_t s) {
+static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, int split, float* d_y, bool y_zeroed,
+                       hipStream_t s) {
     const int mb = (int)((n_tok + BM - 1) / BM), nb = (int)((rows + 64 * NWN - 1) / (64 * NWN));
     const int per = (nsb + split - 1) / split;  // super-blocks per split
     // both K groups of a workgroup must run the same number of steps (they
     // meet at every barrier): every split's range divides evenly
     if (KSW > 1 && (nsb % (split * KSW) != 0)) return DQ_ERR_NOT_SUPPORTED;
-    if (split > 1) {
+    if (split > 1 && !y_zeroed) {
         const size_t n = rows * n_tok;
         zero_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(d_y, n);
     }
@@ -911,17 +928,28 @@ static GemmPlan plan_gemm(int fmt, size_t rows, size_t n_tok, int nsb) {
 }
 
 template <int FMT>
-static int launch_plan(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, float* d_y, hipStream_t s) {
+static int launch_plan(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, float* d_y, bool y_zeroed,
+                       hipStream_t s) {
     const GemmPlan p = plan_gemm(FMT, rows, n_tok, nsb);
     if constexpr (FMT != DQ_FMT_Q8_0) {
-        if (p.nwn == 2) return launch_gemm<FMT, 2, 2, 2>(g, rows, n_tok, nsb, p.split, d_y, s);
+        if (p.nwn == 2) return launch_gemm<FMT, 2, 2, 2>(g, rows, n_tok, nsb, p.split, d_y, y_zeroed, s);
     }
-    return launch_gemm<FMT, 4, 1, 3>(g, rows, n_tok, nsb, p.split, d_y, s);
+    return launch_gemm<FMT, 4, 1, 3>(g, rows, n_tok, nsb, p.split, d_y, y_zeroed, s);
+}
+
+bool dq_gemm_adds_into_y(int fmt, size_t rows, size_t cols, size_t n_tok) {
+    if (cols % 256 || rows == 0 || n_tok == 0) return false;
+    return plan_gemm(fmt, rows, n_tok, (int)(cols / 256)).split > 1;
 }
 
 // GEMM on the workspace written by dq_quantize_act_f16.
 extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work,
                               size_t n_tok, float* d_y, void* stream) {
+    return dq_gemm_f16act_zeroed(fmt, d_w, rows, cols, d_work, n_tok, d_y, false, stream);
+}
+
+int dq_gemm_f16act_zeroed(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work, size_t n_tok,
+                          float* d_y, bool y_zeroed, void* stream) {
     DqLayout L;
     if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K && fmt != DQ_FMT_Q8_0 && fmt != DQ_FMT_Q4_0)
         return DQ_ERR_NOT_SUPPORTED;
@@ -943,10 +971,10 @@ extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols
     g.K = (int)cols;
     const int nsb = (int)cols / 256;  // super-blocks (cols % 256 == 0)
     switch (fmt) {
-    case DQ_FMT_Q4_K: return launch_plan<DQ_FMT_Q4_K>(g, rows, n_tok, nsb, d_y, s);
-    case DQ_FMT_Q8_0: return launch_plan<DQ_FMT_Q8_0>(g, rows, n_tok, nsb, d_y, s);
-    case DQ_FMT_Q4_0: return launch_plan<DQ_FMT_Q4_0>(g, rows, n_tok, nsb, d_y, s);
-    default: return launch_plan<DQ_FMT_Q6_K>(g, rows, n_tok, nsb, d_y, s);
+    case DQ_FMT_Q4_K: return launch_plan<DQ_FMT_Q4_K>(g, rows, n_tok, nsb, d_y, y_zeroed, s);
+    case DQ_FMT_Q8_0: return launch_plan<DQ_FMT_Q8_0>(g, rows, n_tok, nsb, d_y, y_zeroed, s);
+    case DQ_FMT_Q4_0: return launch_plan<DQ_FMT_Q4_0>(g, rows, n_tok, nsb, d_y, y_zeroed, s);
+    default: return launch_plan<DQ_FMT_Q6_K>(g, rows, n_tok, nsb, d_y, y_zeroed, s);
     }
 }
 
@@ -957,7 +985,14 @@ extern "C" int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const
     const int rc = dq_gemm_workspace_bytes(fmt, rows, cols, n_tok, &need);
     if (rc != DQ_OK) return rc;
     if (work_bytes < need || (need && !d_work)) return DQ_ERR_INVALID_ARG;
-    const int r1 = dq_quantize_act_f16(fmt, d_x, cols, n_tok, d_work, stream);
+    // the K-split plans add their partials into y: the quantizer clears it
+    DqZeroSpans z{};
+    const bool zero = dq_zero_span_ok(d_y, rows * n_tok) && rows <= (1u << 30) && dq_gemm_adds_into_y(fmt, rows, cols, n_tok);
+    if (zero) {
+        z.p[0] = d_y;
+        z.n[0] = rows * n_tok;
+    }
+    const int r1 = dq_quantize_act_f16_zero(fmt, d_x, cols, n_tok, d_work, z, stream);
     if (r1 != DQ_OK) return r1;
-    return dq_gemm_f16act(fmt, d_w, rows, cols, d_work, n_tok, d_y, stream);
+    return dq_gemm_f16act_zeroed(fmt, d_w, rows, cols, d_work, n_tok, d_y, zero, stream);
 }

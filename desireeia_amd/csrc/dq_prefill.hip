@@ -750,14 +750,26 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
     // activation quantization per distinct format
     auto products = [&](const float* x, size_t cols, int n, const int* fmt, const void* const* wm, const size_t* rows,
                         float* const* y) -> int {
-        bool done[3] = {false, false, false};
+        // the quantizer of a format class also clears the outputs its
+        // K-split products add their partials into
+        bool done[3] = {false, false, false}, zeroed[3] = {false, false, false};
         for (int j = 0; j < n; ++j) {
             const int fi = cls(fmt[j]);
             if (!done[fi]) {
-                DQP_TRY(dq_quantize_act_f16(fmt[j], x, cols, T, gw(fmt[j]), stream));
+                DqZeroSpans z{};
+                int k = 0;
+                for (int i = j; i < n; ++i) {
+                    if (cls(fmt[i]) != fi || !dq_gemm_adds_into_y(fmt[i], rows[i], cols, T) ||
+                        !dq_zero_span_ok(y[i], rows[i] * T))
+                        continue;
+                    z.p[k] = y[i];
+                    z.n[k++] = rows[i] * T;
+                    zeroed[i] = true;
+                }
+                DQP_TRY(dq_quantize_act_f16_zero(fmt[j], x, cols, T, gw(fmt[j]), z, stream));
                 done[fi] = true;
             }
-            DQP_TRY(dq_gemm_f16act(fmt[j], wm[j], rows[j], cols, gw(fmt[j]), T, y[j], stream));
+            DQP_TRY(dq_gemm_f16act_zeroed(fmt[j], wm[j], rows[j], cols, gw(fmt[j]), T, y[j], zeroed[j], stream));
         }
         return DQ_OK;
     };
