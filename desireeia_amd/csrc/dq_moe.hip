@@ -300,6 +300,7 @@ struct MoeGemm {
     const float* inv;     // per pair: 1/s of its activation row
     const int32_t* offsets;
     int rows, K, n_pairs, nsplit, steps_per_split, main_steps;
+    int n_exp, n_tiles;
 };
 
 // Weight bytes of one main step, a Q4_K super-block (K = 256, 4 items) of this
@@ -416,25 +417,32 @@ __device__ __forceinline__ void issue_w(const uint8_t* base, const DqLayout& L, 
 constexpr int STEP_LOADS = A_LOADS + 1 + 2 * WROWS * 4 / (64 * WAVES) + 1;
 static_assert(WROWS * 4 % (64 * WAVES) == 0 && 64 * WAVES == 2 * WROWS, "DMA slots per thread");
 
-// Grid: x = 256-row tiles of one expert's rows, y = expert, z = matrix * nsplit
-// + split. Wave w of the workgroup owns rows 256x + 32w .. +31; lane l feeds
+// Grid (one dimension): workgroup id -> expert id % n_exp, then the row tile,
+// then the K split, then the matrix. Workgroups are dealt to the 8 XCDs
+// round-robin, so with 8 (or a multiple of 8) experts each XCD serves whole
+// experts: the activation rows an expert's tiles re-read every K step stay
+// in that XCD's L2. Wave w of the workgroup owns rows 128x + 32w .. +31 of
+// row tile x; lane l feeds
 // row l % 32 with K values 8(l/32)..+7 of each 16-wide slice. The expert's
 // pairs are taken 32 at a time (one 32-token MFMA tile). Per main step (one
 // super-block) the weight tile and the activation rows go through an
 // NSTAGE-stage LDS ring, the next NSTAGE-1 steps' DMAs in flight while this
 // one computes.
-__global__ __launch_bounds__(64 * WAVES) void moe_gemm_kernel(MoeGemm G) {
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void moe_gemm_kernel(MoeGemm G) {
     __shared__ __align__(16) uint8_t aring[NSTAGE][A_STAGE_BYTES];
     __shared__ __align__(16) uint8_t wring[NSTAGE][WT_BYTES];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(tid >> 6));
-    const int e = blockIdx.y;
-    const int mat = blockIdx.z / G.nsplit, split = blockIdx.z % G.nsplit;
+    const int e = (int)(blockIdx.x % (unsigned)G.n_exp);
+    int rest = (int)(blockIdx.x / (unsigned)G.n_exp);
+    const int tile = rest % G.n_tiles;
+    rest /= G.n_tiles;
+    const int split = rest % G.nsplit, mat = rest / G.nsplit;
     const int p_begin = G.offsets[e], p_end = G.offsets[e + 1];
     if (p_begin >= p_end) return;  // no token routed to this expert (uniform)
     const int h = lane >> 5;
-    const int r_wg = blockIdx.x * WROWS;                 // first row of the workgroup (in the expert)
+    const int r_wg = tile * WROWS;                       // first row of the workgroup (in the expert)
     const int nrows = min(WROWS, G.rows - r_wg);
     const int rl = 32 * wave + (lane & 31);              // this lane's row in the tile
     const int rloc = r_wg + rl;
@@ -448,9 +456,9 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_kernel(MoeGemm G) {
     if (s0 >= main_end) return;  // uniform
 
     for (int c = p_begin; c < p_end; c += TT) {
-        f16v acc;
+        f16v acc, acc1;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[r] = acc1[r] = 0.0f;
         {
             // prologue: the first NSTAGE-1 steps in flight
 #pragma unroll
@@ -478,38 +486,47 @@ __global__ __launch_bounds__(64 * WAVES) void moe_gemm_kernel(MoeGemm G) {
                 }
                 const uint8_t* ab = aring[stage];
                 const uint8_t* wb = wring[stage];
+                // every LDS read of the step first (one wait for all of them),
+                // then the dequantization and the MFMAs, items alternating
+                // between two accumulators (two independent MFMA chains)
                 WRaw wr;
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
                     wr.q[t] = *reinterpret_cast<const dq_u32x4*>(wb + h * WT_PLANE + rl * 64 +
                                                                  16 * (t ^ ((rl >> 2) & 3)));
                 wr.hd = *reinterpret_cast<const dq_u32x4*>(wb + 2 * WT_PLANE + rl * 16);
+                const int m = lane & 31;
+                h8 af[4][4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) {
+                        const int k = a_offset(0, t, kk, h) / 8;  // chunk of the slice
+                        af[t][kk] = *reinterpret_cast<const h8*>(ab + (size_t)(m * ACH + (k ^ (m & 31))) * 16);
+                    }
+                const h8 zero = {};
+                const h8 am = h == 0 ? *reinterpret_cast<const h8*>(ab + A_MAIN_BYTES + m * 16) : zero;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     h8 bf[4];
                     b_item(wr, t, row_ok, bf);
-                    const int m = lane & 31;
-                    h8 af[4];
 #pragma unroll
                     for (int kk = 0; kk < 4; ++kk) {
-                        const int k = a_offset(0, t, kk, h) / 8;  // chunk of the slice
-                        af[kk] = *reinterpret_cast<const h8*>(ab + (size_t)(m * ACH + (k ^ (m & 31))) * 16);
+                        if (t & 1) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[t][kk], bf[kk], acc1, 0, 0, 0);
+                        else acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[t][kk], bf[kk], acc, 0, 0, 0);
                     }
-#pragma unroll
-                    for (int kk = 0; kk < 4; ++kk)
-                        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[kk], bf[kk], acc, 0, 0, 0);
                 }
                 {   // the super-block's min term: one 16-wide slice, lanes of half 0
                     // carry its 8 sub-blocks (the min columns K + 8st + j
                     // against fp16(-dmin * m_j)), half 1 zeros
-                    const h8 zero = {};
-                    const h8 am = h == 0 ? *reinterpret_cast<const h8*>(ab + A_MAIN_BYTES + (lane & 31) * 16) : zero;
                     const h8 bm = h == 0 ? q4k_neg_mins(wr.hd, row_ok) : zero;
-                    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, acc, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, acc1, 0, 0, 0);
                 }
             }
             __syncthreads();  // the ring is reused by the next pass
         }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] += acc1[r];
         // D of 32x32x16: lane l, register r -> weight row l % 32, token (r/4)*8 + (l/32)*4 + r%4.
         // The pairs' factors 1/s are loaded together first (clamped pairs: a
         // load inside the store's branch would be waited for one at a time).
@@ -645,8 +662,11 @@ int launch_gemm(const uint8_t* w0, const uint8_t* w1, int n_mat, int n_exp, int 
     G.steps_per_split = (G.main_steps + nsplit - 1) / nsplit;
     // every split owns at least one step (its partial is always written)
     if ((long)(nsplit - 1) * G.steps_per_split >= G.main_steps) return DQ_ERR_NOT_SUPPORTED;
-    const dim3 grid((unsigned)((rows + 32 * WAVES - 1) / (32 * WAVES)), (unsigned)n_exp, (unsigned)(n_mat * nsplit));
-    moe_gemm_kernel<<<grid, 64 * WAVES, 0, s>>>(G);
+    G.n_exp = n_exp;
+    G.n_tiles = (rows + WROWS - 1) / WROWS;
+    const long wgs = (long)G.n_tiles * n_exp * n_mat * nsplit;
+    if (wgs > 0x7FFFFFFF) return DQ_ERR_NOT_SUPPORTED;
+    moe_gemm_kernel<<<(unsigned)wgs, 64 * WAVES, 0, s>>>(G);
     return dq_launch_status();
 }
 
