@@ -25,10 +25,11 @@
 // 128 tokens of its 64 rows over the kg-th share of the workgroup's K steps:
 // 4 x 2 v_mfma_f32_32x32x16_f16 tiles, so each weight fragment it turns into
 // fp16 feeds 4 MFMAs, and no other wave converts the same bytes. Each K group
-// has a 3-stage LDS ring filled by global_load_lds DMA holding per K step (64
-// columns, one packed weight item) the activation tile (XOR-swizzled 16-byte
-// chunks: no bank conflicts on fragment reads), the super-block's block sums
-// and the raw packed weight bytes of the group's rows. KSW = 2 partials are
+// has LDS rings filled by global_load_lds DMA: NS (2 or 3) activation stages
+// of one K step (64 columns; XOR-swizzled 16-byte chunks, no bank conflicts
+// on fragment reads) and NB super-stages of SB packed weight items of the
+// group's rows (with the super-block header and, for Q4_K, the block sums
+// of the min term; see Ring). KSW = 2 partials are
 // added through LDS at the end in a fixed order. Q6_K: K is permuted to the
 // packed item order (both operands, see dq_quantize_act_f16), so a 64-column
 // K step is exactly one 64-weight item.
