@@ -110,6 +110,7 @@ struct AttnArgs {
     int8_t* oq;           // fused per-256 quantization (or NULL)
     float* oscale;
     int32_t* oisum;
+    DqQkvPost post;       // FUSE: optional biases and QK-norm before RoPE
 };
 
 template <int HD, int HPK, bool FUSE>
@@ -191,9 +192,10 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
 #pragma unroll
         for (int t = 0; t < HPW; ++t) {
             const int h = wave + NW * t;
-            if (h < HPK) {
+            if (h < HPK) {  // wave-uniform
+                float a = ql[t], b = qhv[t];
+                dq_qkv_post(a, b, 0, kvh * HPK + h, lane, A.post);
                 // NeoX rotation of the pair (j, j + 64) (dq_rope_pair)
-                const float a = ql[t], b = qhv[t];
                 qt[lane][h] = A.rope ? a * rc - b * rs : a;
                 qt[lane + 64][h] = A.rope ? a * rs + b * rc : b;
             }
@@ -217,6 +219,7 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
             // the new row of this KV head: wave 0 = K (rotated), wave 1 = V
             const float* src = (wave == 0 ? A.k : A.v) + (size_t)kvh * HD;
             float lo = src[lane], hi = src[lane + 64];
+            dq_qkv_post(lo, hi, wave == 0 ? 1 : 2, kvh, lane, A.post);
             if (wave == 0 && A.rope) dq_rope_pair(lo, hi, A.rope, lane);
             uint8_t* lrow = reinterpret_cast<uint8_t*>(wave == 0 ? ks : vs) + (nv - 1) * RB;
             dq_q8_0_row128(lo, hi, lane, lrow);
@@ -467,7 +470,7 @@ bool attn_shape_ok(uint32_t n_head, uint32_t n_head_kv, uint32_t hd) {
 int attn_run(const float* d_q, const float* d_k, const float* d_v, const float* d_rope, const void* d_kc,
              const void* d_vc, uint32_t n_head, uint32_t n_head_kv, uint32_t hd, uint32_t cc_start, uint32_t pos,
              const int32_t* d_pos, uint32_t n_ctx, float* d_out, void* d_work, size_t work_bytes, int8_t* oq,
-             float* os, int32_t* oi, void* stream) {
+             float* os, int32_t* oi, void* stream, const DqQkvPost& post = DqQkvPost{}) {
     if (!d_q || !d_kc || !d_vc || !d_out || !d_work || n_ctx == 0) return DQ_ERR_INVALID_ARG;
     if (!attn_shape_ok(n_head, n_head_kv, hd)) return DQ_ERR_NOT_SUPPORTED;
     if (!d_pos && (pos >= n_ctx || cc_start > pos)) return DQ_ERR_INVALID_ARG;
@@ -498,6 +501,7 @@ int attn_run(const float* d_q, const float* d_k, const float* d_v, const float* 
     a.oq = oq;
     a.oscale = os;
     a.oisum = oi;
+    a.post = post;
     const int nh = (int)n_head;
     int rc = DQ_ERR_NOT_SUPPORTED;
 #define DQ_ATTN_CASE(H)                                                                              \
@@ -596,10 +600,20 @@ int dq_attn_rope_kv_decode(const float* d_q, const float* d_k, const float* d_v,
                            uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx, float* d_out,
                            int8_t* d_oq, float* d_oscale, int32_t* d_oisum, void* d_work, size_t work_bytes,
                            void* stream) {
-    if (!d_k || !d_v) return DQ_ERR_INVALID_ARG;
-    if (d_rope && n_rot != hd) return DQ_ERR_NOT_SUPPORTED;  // partial rotation: dq_rope_kv_write
-    return attn_run(d_q, d_k, d_v, d_rope, d_kc, d_vc, n_head, n_head_kv, hd, cc_start, pos, d_pos, n_ctx, d_out,
-                    d_work, work_bytes, d_oq, d_oscale, d_oisum, stream);
+    return dq_attn_rope_kv_decode_post(d_q, d_k, d_v, d_rope, n_rot, d_kc, d_vc, n_head, n_head_kv, hd, cc_start, pos,
+                                       d_pos, n_ctx, d_out, d_oq, d_oscale, d_oisum, d_work, work_bytes, DqQkvPost{},
+                                       stream);
 }
 
 }  // extern "C"
+
+int dq_attn_rope_kv_decode_post(const float* d_q, const float* d_k, const float* d_v, const float* d_rope,
+                                uint32_t n_rot, void* d_kc, void* d_vc, uint32_t n_head, uint32_t n_head_kv,
+                                uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx,
+                                float* d_out, int8_t* d_oq, float* d_oscale, int32_t* d_oisum, void* d_work,
+                                size_t work_bytes, const DqQkvPost& post, void* stream) {
+    if (!d_k || !d_v) return DQ_ERR_INVALID_ARG;
+    if (d_rope && n_rot != hd) return DQ_ERR_NOT_SUPPORTED;  // partial rotation: dq_rope_kv_write
+    return attn_run(d_q, d_k, d_v, d_rope, d_kc, d_vc, n_head, n_head_kv, hd, cc_start, pos, d_pos, n_ctx, d_out,
+                    d_work, work_bytes, d_oq, d_oscale, d_oisum, stream, post);
+}

@@ -177,6 +177,43 @@ __device__ __forceinline__ float dq_wave_sum(float v) {
     return v;
 }
 
+__device__ __forceinline__ double dq_wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, DQ_WAVE);
+    return v;
+}
+
+// rms_norm_vec (models/dense_forward.cpp:129-165) of one 128-value head held
+// by a wave as (lo, hi) = values (lane, lane + 64): squares in float summed
+// in double, scale = 1/sqrtf((float)(sum/128) + eps), y = x * scale * w. The
+// per-head QK-norm of :3915-3931.
+__device__ __forceinline__ void dq_head_rms_norm(float& lo, float& hi, const float* __restrict__ w, int lane,
+                                                 float eps) {
+    const float a = lo * lo, b = hi * hi;
+    const double s = dq_wave_sum_f64((double)a + (double)b);
+    const float scale = 1.0f / sqrtf((float)(s / 128.0) + eps);
+    lo = lo * scale * w[lane];
+    hi = hi * scale * w[lane + 64];
+}
+
+// Q/K/V post-processing of one head held by a wave as (lo, hi) (lane, lane
+// + 64), between the projections and RoPE: the bias (add_bias, y += b;
+// :3904-3908) and the per-head RMSNorm (:3915-3931). All optional.
+struct DqQkvPost {
+    const float *bq, *bk, *bv, *q_norm, *k_norm;
+    float eps;
+};
+// kind 0: query head, 1: key head, 2: value head
+__device__ __forceinline__ void dq_qkv_post(float& lo, float& hi, int kind, int head, int lane, const DqQkvPost& P) {
+    const float* b = kind == 0 ? P.bq : (kind == 1 ? P.bk : P.bv);
+    if (b) {
+        lo += b[(size_t)head * 128 + lane];
+        hi += b[(size_t)head * 128 + lane + 64];
+    }
+    const float* nw = kind == 0 ? P.q_norm : (kind == 1 ? P.k_norm : nullptr);
+    if (nw) dq_head_rms_norm(lo, hi, nw, lane, P.eps);
+}
+
 __device__ __forceinline__ float dq_wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, DQ_WAVE));
@@ -242,4 +279,23 @@ int dq_gemm_f16act_zeroed(int fmt, const void* d_w, size_t rows, size_t cols, co
                           float* d_y, bool y_zeroed, void* stream);
 static inline bool dq_zero_span_ok(const float* p, size_t n) {
     return p && n % 4 == 0 && reinterpret_cast<uintptr_t>(p) % 16 == 0;
+}
+// Library-internal forms of the fused decode attention, the RoPE + K/V-row
+// write of one token and of a prompt chunk, with the optional Q/K/V biases
+// and per-head QK-norm applied first (the public entry points pass none).
+int dq_attn_rope_kv_decode_post(const float* d_q, const float* d_k, const float* d_v, const float* d_rope,
+                                uint32_t n_rot, void* d_kc, void* d_vc, uint32_t n_head, uint32_t n_head_kv,
+                                uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx,
+                                float* d_out, int8_t* d_oq, float* d_oscale, int32_t* d_oisum, void* d_work,
+                                size_t work_bytes, const DqQkvPost& post, void* stream);
+int dq_rope_kv_write_post(float* d_q, const float* d_k, const float* d_v, const float* d_rope, uint32_t n_head,
+                          uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
+                          const int32_t* d_pos, uint32_t n_ctx, const DqQkvPost& post, void* stream);
+int dq_rope_kv_write_batch_post(float* d_q, const float* d_k, const float* d_v, size_t q_ld, size_t kv_ld,
+                                const float* d_rope, uint32_t n_rot, uint32_t n_tok, uint32_t n_head,
+                                uint32_t n_head_kv, uint32_t hd, void* d_kc, void* d_vc, uint32_t pos0,
+                                uint32_t n_ctx, const DqQkvPost& post, void* stream);
+// The layer's post-processing from its descriptor.
+static inline DqQkvPost dq_layer_post(const dq_layer_t* L) {
+    return DqQkvPost{L->bq, L->bk, L->bv, L->q_norm, L->k_norm, L->rms_eps};
 }

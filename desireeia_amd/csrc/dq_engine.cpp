@@ -756,11 +756,40 @@ int cuda_qkv_attention_out(const CudaQkvAttnArgs* A) {
 
 // ------------------------------------------------------------------ layer --
 
+// The optional per-layer vectors of a Qwen-style layer (Q/K/V biases,
+// QK-norm weights): host pointers (NULL = absent) and float counts.
+struct LayerExtras {
+    const float* h[5];
+    size_t n[5];
+    size_t bytes() const {
+        size_t b = 0;
+        for (int i = 0; i < 5; ++i)
+            if (h[i]) b += dq_align256(n[i] * 4);
+        return b;
+    }
+    // device copies at dst (each 256-byte aligned), pointers into the layer
+    bool upload(dq_layer_t& L, uint8_t* dst, hipStream_t s) const {
+        const float** d[5] = {&L.bq, &L.bk, &L.bv, &L.q_norm, &L.k_norm};
+        for (int i = 0; i < 5; ++i) {
+            *d[i] = nullptr;
+            if (!h[i]) continue;
+            if (hipMemcpyAsync(dst, h[i], n[i] * 4, hipMemcpyHostToDevice, s) != hipSuccess) return false;
+            *d[i] = (const float*)dst;
+            dst += dq_align256(n[i] * 4);
+        }
+        return true;
+    }
+};
+static LayerExtras extras_of(const float* bq, const float* bk, const float* bv, const float* qn, const float* kn,
+                             size_t q_dim, size_t kv_dim, size_t hd) {
+    return LayerExtras{{bq, bk, bv, qn, kn}, {q_dim, kv_dim, kv_dim, hd, hd}};
+}
+
 int cuda_layer_forward(const CudaLayerArgs* A) {
     if (!A || !g.kc) return DQ_ERR_NOT_SUPPORTED;
-    // features outside the plain dense layer: the engine's CPU path runs them
-    if (A->wag_qs || A->bq || A->bk || A->bv || A->q_norm_w || A->k_norm_w || A->post_attn_norm_w ||
-        A->post_ffn_norm_w || A->act_gelu || A->dyn_all || A->rope_all)
+    // features outside the dense layer with optional Q/K/V biases and per-head
+    // QK-norm: the engine's CPU path runs them
+    if (A->wag_qs || A->post_attn_norm_w || A->post_ffn_norm_w || A->act_gelu || A->dyn_all || A->rope_all)
         return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
     if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
@@ -812,15 +841,20 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     if (A->download_x && !A->x_out) return DQ_ERR_INVALID_ARG;
     if (!stream()) return DQ_ERR_IO;
     const size_t E = A->n_embd;
-    // norm weights: device copies in the tail of the workspace
+    // norm weights and the optional biases / QK-norm weights: device copies in
+    // the tail of the workspace
+    const LayerExtras ex =
+        extras_of(A->bq, A->bk, A->bv, A->q_norm_w, A->k_norm_w, A->q_dim, A->kv_dim, A->head_dim);
     const size_t norm_off = dq_align256(wbytes);
-    if (!reserve(g.work, norm_off + 2 * dq_align256(E * 4)) || !reserve(g.lx[0], E * 4) || !reserve(g.lx[1], E * 4))
+    if (!reserve(g.work, norm_off + 2 * dq_align256(E * 4) + ex.bytes()) || !reserve(g.lx[0], E * 4) ||
+        !reserve(g.lx[1], E * 4))
         return DQ_ERR_IO;
     const hipStream_t s = g.stream;
     float* an = (float*)((uint8_t*)g.work.p + norm_off);
     float* fn = (float*)((uint8_t*)g.work.p + norm_off + dq_align256(E * 4));
     if (hipMemcpyAsync(an, A->attn_norm_w, E * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipMemcpyAsync(fn, A->ffn_norm_w, E * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+        hipMemcpyAsync(fn, A->ffn_norm_w, E * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+        !ex.upload(L, (uint8_t*)g.work.p + norm_off + 2 * dq_align256(E * 4), s))
         return io_fail();
     L.attn_norm = an;
     L.ffn_norm = fn;
@@ -887,10 +921,9 @@ int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, 
 
 int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     if (!A || !g.kc || A->n_tok == 0 || A->n_total == 0) return DQ_ERR_NOT_SUPPORTED;
-    // features outside the plain dense layer: the engine's CPU path runs them
-    if (A->wag_qs || A->bq || A->bk || A->bv || A->q_norm_w || A->k_norm_w || A->post_attn_norm_w ||
-        A->post_ffn_norm_w || A->act_gelu)
-        return DQ_ERR_NOT_SUPPORTED;
+    // features outside the dense layer with optional Q/K/V biases and per-head
+    // QK-norm: the engine's CPU path runs them
+    if (A->wag_qs || A->post_attn_norm_w || A->post_ffn_norm_w || A->act_gelu) return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
     if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
         A->heads_per_kv != A->n_head / A->n_head_kv)
@@ -934,7 +967,10 @@ int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     if (!stream()) return DQ_ERR_IO;
     const size_t E = A->n_embd, NT = A->n_total;
     const int slot = A->rope_caches ? A->rope_slot : 0;
-    if (!reserve(g.px, NT * E * 4) || !reserve(g.pwork, wbytes) || !reserve(g.pnorm, 2 * dq_align256(E * 4)) ||
+    const LayerExtras ex =
+        extras_of(A->bq, A->bk, A->bv, A->q_norm_w, A->k_norm_w, A->q_dim, A->kv_dim, A->head_dim);
+    if (!reserve(g.px, NT * E * 4) || !reserve(g.pwork, wbytes) ||
+        !reserve(g.pnorm, 2 * dq_align256(E * 4) + ex.bytes()) ||
         (A->rope_caches && !reserve(g.prope[slot], NT * A->n_rot * 4)))
         return DQ_ERR_IO;
     const hipStream_t s = g.stream;
@@ -948,7 +984,8 @@ int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     float* an = (float*)g.pnorm.p;
     float* fn = (float*)((uint8_t*)g.pnorm.p + dq_align256(E * 4));
     if (hipMemcpyAsync(an, A->attn_norm_w, E * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipMemcpyAsync(fn, A->ffn_norm_w, E * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+        hipMemcpyAsync(fn, A->ffn_norm_w, E * 4, hipMemcpyHostToDevice, s) != hipSuccess ||
+        !ex.upload(L, (uint8_t*)g.pnorm.p + 2 * dq_align256(E * 4), s))
         return io_fail();
     L.attn_norm = an;
     L.ffn_norm = fn;

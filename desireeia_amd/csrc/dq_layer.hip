@@ -161,13 +161,14 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q, cons
                                                      const float* __restrict__ v, const float* __restrict__ rope,
                                                      int n_head, int n_kv, int n_rot, uint8_t* __restrict__ kc,
                                                      uint8_t* __restrict__ vc, size_t pos_bytes, int pos_host,
-                                                     const int* __restrict__ pos_dev, int n_ctx) {
+                                                     const int* __restrict__ pos_dev, int n_ctx, DqQkvPost post) {
     constexpr int HD = 128;
     const int r = blockIdx.x, j = threadIdx.x;
     const int kind = r < n_head ? 0 : (r < n_head + n_kv ? 1 : 2);
     const int head = kind == 0 ? r : (kind == 1 ? r - n_head : r - n_head - n_kv);
     const float* src = kind == 0 ? q + (size_t)head * HD : (kind == 1 ? k : v) + (size_t)head * HD;
     float lo = src[j], hi = src[j + 64];
+    dq_qkv_post(lo, hi, kind, head, j, post);
     if (kind < 2 && rope) {
         // n_rot = 128: pair (j, j+64); n_rot < 128: pairs inside [0, n_rot)
         const int half = n_rot / 2;
@@ -367,6 +368,15 @@ int dq_silu_mul(const float* d_gate, const float* d_up, size_t n, float* d_h, vo
 int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float* d_rope, uint32_t n_head,
                      uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
                      const int32_t* d_pos, uint32_t n_ctx, void* stream) {
+    return dq_rope_kv_write_post(d_q, d_k, d_v, d_rope, n_head, n_head_kv, hd, n_rot, d_kc, d_vc, pos, d_pos, n_ctx,
+                                 DqQkvPost{}, stream);
+}
+
+}  // extern "C"
+
+int dq_rope_kv_write_post(float* d_q, const float* d_k, const float* d_v, const float* d_rope, uint32_t n_head,
+                          uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
+                          const int32_t* d_pos, uint32_t n_ctx, const DqQkvPost& post, void* stream) {
     if (!d_q || !d_k || !d_v || !d_kc || !d_vc || n_ctx == 0) return DQ_ERR_INVALID_ARG;
     if (hd != 128) return DQ_ERR_NOT_SUPPORTED;
     if (d_rope && (n_rot == 0 || n_rot > hd || n_rot % 2)) return DQ_ERR_INVALID_ARG;
@@ -374,9 +384,11 @@ int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float
     const size_t pos_bytes = (size_t)n_head_kv * (hd / 32) * DQ_SZ_Q8_0;
     rope_kv_kernel<<<n_head + 2 * n_head_kv, 64, 0, (hipStream_t)stream>>>(
         d_q, d_k, d_v, d_rope, (int)n_head, (int)n_head_kv, (int)n_rot, (uint8_t*)d_kc, (uint8_t*)d_vc, pos_bytes,
-        (int)pos, d_pos, (int)n_ctx);
+        (int)pos, d_pos, (int)n_ctx, post);
     return dq_launch_status();
 }
+
+extern "C" {
 
 int dq_layer_workspace_bytes(const dq_layer_t* L, uint32_t n_ctx, size_t* bytes) {
     if (!L || !bytes || n_ctx == 0) return DQ_ERR_INVALID_ARG;
@@ -429,19 +441,21 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
                                        {L->fmt_v, L->wv, KVD, w.v, nullptr}};
         DQ_TRY(run_group(jobs, 3, E));
     }
-    // RoPE, the new K/V rows and attention in one launch when the rotation
-    // covers the whole head (else the separate RoPE + KV-write kernel first)
+    // the optional biases and QK-norm, RoPE, the new K/V rows and attention in
+    // one launch when the rotation covers the whole head (else the separate
+    // post + RoPE + KV-write kernel first)
+    const DqQkvPost post = dq_layer_post(L);
     const bool fused = !d_rope || L->n_rot == L->head_dim;
     if (!fused)
-        DQ_TRY(dq_rope_kv_write(w.q, w.k, w.v, d_rope, L->n_head, L->n_head_kv, L->head_dim, L->n_rot, d_kc, d_vc,
-                                pos, d_pos, n_ctx, stream));
+        DQ_TRY(dq_rope_kv_write_post(w.q, w.k, w.v, d_rope, L->n_head, L->n_head_kv, L->head_dim, L->n_rot, d_kc,
+                                     d_vc, pos, d_pos, n_ctx, post, stream));
     // the attention also quantizes its output per 256 for a K-quant Wo
     const bool q256 = kquant(L->fmt_o);
     int8_t* oq = q256 ? w.aq : nullptr;
     if (fused)
-        DQ_TRY(dq_attn_rope_kv_decode(w.q, w.k, w.v, d_rope, L->n_rot, d_kc, d_vc, L->n_head, L->n_head_kv,
-                                      L->head_dim, cc_start, pos, d_pos, n_ctx, w.ao, oq, w.as, w.ai, w.attn,
-                                      w.attn_bytes, stream));
+        DQ_TRY(dq_attn_rope_kv_decode_post(w.q, w.k, w.v, d_rope, L->n_rot, d_kc, d_vc, L->n_head, L->n_head_kv,
+                                           L->head_dim, cc_start, pos, d_pos, n_ctx, w.ao, oq, w.as, w.ai, w.attn,
+                                           w.attn_bytes, post, stream));
     else if (q256)
         DQ_TRY(dq_attn_decode_q8_act(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos,
                                      n_ctx, w.ao, w.aq, w.as, w.ai, w.attn, w.attn_bytes, stream));

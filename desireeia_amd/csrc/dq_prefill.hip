@@ -401,8 +401,9 @@ __global__ __launch_bounds__(256) void kv_write_batch_kernel(const float* __rest
     kv_block_store(x, dst);
 }
 
-// RoPE of a run of tokens (models/dense_forward.cpp:668-680 per token, table
-// row t = dq_rope_cache(pos0 + t)) on the query heads, in place, and on the
+// The optional Q/K/V biases and per-head QK-norm, then RoPE of a run of tokens
+// (models/dense_forward.cpp:668-680 per token, table row t =
+// dq_rope_cache(pos0 + t)) on the query heads, in place, and on the
 // key heads, whose rotated rows then go into the cache with the value rows
 // (kv_quantize_row). 128-dim heads; grid (n_head + 2 n_kv, n_tok), 64 threads,
 // thread j holds dims j and j + 64.
@@ -410,7 +411,8 @@ __global__ __launch_bounds__(64) void rope_kv_batch_kernel(float* __restrict__ q
                                                            const float* __restrict__ v, size_t q_ld, size_t kv_ld,
                                                            const float* __restrict__ rope, int n_rot, int n_head,
                                                            int n_kv, uint8_t* __restrict__ kc,
-                                                           uint8_t* __restrict__ vc, size_t pos_bytes, int pos0) {
+                                                           uint8_t* __restrict__ vc, size_t pos_bytes, int pos0,
+                                                           DqQkvPost post) {
     constexpr int HD = 128;
     const int r = blockIdx.x, t = blockIdx.y, j = threadIdx.x;
     const int kind = r < n_head ? 0 : (r < n_head + n_kv ? 1 : 2);
@@ -418,6 +420,7 @@ __global__ __launch_bounds__(64) void rope_kv_batch_kernel(float* __restrict__ q
     float* qrow = q + (size_t)t * q_ld + (size_t)hh * HD;
     const float* src = kind == 0 ? qrow : (kind == 1 ? k : v) + (size_t)t * kv_ld + (size_t)hh * HD;
     float x0 = src[j], x1 = src[j + 64];
+    dq_qkv_post(x0, x1, kind, hh, j, post);  // optional biases and QK-norm (:3318-3342)
     if (kind < 2 && rope) {
         const float* tab = rope + (size_t)t * n_rot;
         if (n_rot == HD) {
@@ -628,6 +631,16 @@ int dq_kv_write_batch(const float* d_k, const float* d_v, size_t ld, uint32_t n_
 int dq_rope_kv_write_batch(float* d_q, const float* d_k, const float* d_v, size_t q_ld, size_t kv_ld,
                            const float* d_rope, uint32_t n_rot, uint32_t n_tok, uint32_t n_head, uint32_t n_head_kv,
                            uint32_t hd, void* d_kc, void* d_vc, uint32_t pos0, uint32_t n_ctx, void* stream) {
+    return dq_rope_kv_write_batch_post(d_q, d_k, d_v, q_ld, kv_ld, d_rope, n_rot, n_tok, n_head, n_head_kv, hd, d_kc,
+                                       d_vc, pos0, n_ctx, DqQkvPost{}, stream);
+}
+
+}  // extern "C"
+
+int dq_rope_kv_write_batch_post(float* d_q, const float* d_k, const float* d_v, size_t q_ld, size_t kv_ld,
+                                const float* d_rope, uint32_t n_rot, uint32_t n_tok, uint32_t n_head,
+                                uint32_t n_head_kv, uint32_t hd, void* d_kc, void* d_vc, uint32_t pos0,
+                                uint32_t n_ctx, const DqQkvPost& post, void* stream) {
     if (!d_q || !d_k || !d_v || !d_kc || !d_vc) return DQ_ERR_INVALID_ARG;
     if (hd != 128 || n_head_kv == 0) return DQ_ERR_NOT_SUPPORTED;
     if (d_rope && (n_rot == 0 || n_rot > hd || n_rot % 2)) return DQ_ERR_INVALID_ARG;
@@ -637,9 +650,11 @@ int dq_rope_kv_write_batch(float* d_q, const float* d_k, const float* d_v, size_
     const size_t pos_bytes = (size_t)n_head_kv * (hd / 32) * DQ_SZ_Q8_0;
     rope_kv_batch_kernel<<<dim3(n_head + 2 * n_head_kv, n_tok), 64, 0, (hipStream_t)stream>>>(
         d_q, d_k, d_v, q_ld, kv_ld, d_rope, (int)n_rot, (int)n_head, (int)n_head_kv, (uint8_t*)d_kc, (uint8_t*)d_vc,
-        pos_bytes, (int)pos0);
+        pos_bytes, (int)pos0, post);
     return dq_launch_status();
 }
+
+extern "C" {
 
 // Key splits the grid of (n_tok, n_head, n_head_kv) could use at most, and
 // the bytes of their partial records.
@@ -783,8 +798,8 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         float* const y[3] = {w.q, w.k, w.v};
         DQP_TRY(products(w.xn, E, 3, f, m, r, y));
     }
-    DQP_TRY(dq_rope_kv_write_batch(w.q, w.k, w.v, QD, KVD, d_rope, L->n_rot, n_tok, L->n_head, L->n_head_kv,
-                                   L->head_dim, d_kc, d_vc, pos0, n_ctx, stream));
+    DQP_TRY(dq_rope_kv_write_batch_post(w.q, w.k, w.v, QD, KVD, d_rope, L->n_rot, n_tok, L->n_head, L->n_head_kv,
+                                        L->head_dim, d_kc, d_vc, pos0, n_ctx, dq_layer_post(L), stream));
     DQP_TRY(dq_attn_prefill_q8(w.q, d_kc, d_vc, n_tok, L->n_head, L->n_head_kv, L->head_dim, (uint32_t)QD, pos0,
                                n_swa, n_ctx, w.attn, w.aw, w.aw_bytes, stream));
     {

@@ -359,7 +359,9 @@ class LayerDesc(ctypes.Structure):
                 ("fmt_gate", ctypes.c_int), ("fmt_up", ctypes.c_int), ("fmt_down", ctypes.c_int),
                 ("wq", ctypes.c_void_p), ("wk", ctypes.c_void_p), ("wv", ctypes.c_void_p), ("wo", ctypes.c_void_p),
                 ("wgate", ctypes.c_void_p), ("wup", ctypes.c_void_p), ("wdown", ctypes.c_void_p),
-                ("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p)]
+                ("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p),
+                ("bq", ctypes.c_void_p), ("bk", ctypes.c_void_p), ("bv", ctypes.c_void_p),
+                ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p)]
 
 
 def rope_cache(n_rot, pos, theta):
@@ -378,7 +380,9 @@ class DecoderLayer:
     NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
     def __init__(self, mats, attn_norm, ffn_norm, n_head, n_head_kv, head_dim, n_ctx, rms_eps=1e-5,
-                 rope_theta=500000.0, n_rot=None, device="cuda"):
+                 rope_theta=500000.0, n_rot=None, device="cuda", bias=None, qk_norm=None):
+        """bias: optional (bq, bk, bv) float tensors; qk_norm: optional
+        (q_norm, k_norm) [head_dim] weights (Qwen-style layers)."""
         self.mats = mats
         self.attn_norm = attn_norm.to(device).float().contiguous()
         self.ffn_norm = ffn_norm.to(device).float().contiguous()
@@ -393,6 +397,12 @@ class DecoderLayer:
             setattr(d, "w" + nm, mats[nm].buf.data_ptr())
         d.attn_norm = self.attn_norm.data_ptr()
         d.ffn_norm = self.ffn_norm.data_ptr()
+        self.extras = {}
+        for names, vals in ((("bq", "bk", "bv"), bias), (("q_norm", "k_norm"), qk_norm)):
+            for nm, t in zip(names, vals or ()):
+                if t is not None:
+                    self.extras[nm] = t.to(device).float().contiguous()
+                    setattr(d, nm, self.extras[nm].data_ptr())
         self.desc = d
         self.cache = KVCache(n_ctx, n_head_kv, head_dim, device)
         lib = _lib.load()

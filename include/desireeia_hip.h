@@ -275,10 +275,14 @@ int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float
                      uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
                      const int32_t* d_pos, uint32_t n_ctx, void* stream);
 
-/* One Llama-style decoder layer at batch 1 on the device: the plain dense
- * branch of models/dense_forward.cpp:3897-4257 (no biases, no QK-norm, no
- * sandwich norms, gated SiLU FFN, Q8_0 KV cache) that cuda_layer_forward
- * (core/engine.h:698-752) runs as one captured episode. Weights are packed
+/* One Llama-style decoder layer at batch 1 on the device: the dense branch
+ * of models/dense_forward.cpp:3897-4257 with optional Q/K/V biases and
+ * per-head QK-norm (Qwen-style layers; no sandwich norms, gated SiLU FFN,
+ * Q8_0 KV cache) that cuda_layer_forward (core/engine.h:698-752) runs as one
+ * captured episode. The biases (bq [n_head*head_dim], bk, bv
+ * [n_head_kv*head_dim]) are added to the projections (add_bias,
+ * :3904-3908); q_norm / k_norm [head_dim] then normalise every q and k head
+ * (rms_norm_vec per head, :3915-3931), before RoPE. Each may be NULL. Weights are packed
  * device matrices (dq_weights_pack), each of any of the four formats (Q4_K /
  * Q6_K read the per-256 activation, Q8_0 / Q4_0 the per-32 one, as the
  * reference CPU GEMVs of those formats do); n_embd, n_ff and n_head*head_dim
@@ -293,6 +297,7 @@ typedef struct {
     int fmt_q, fmt_k, fmt_v, fmt_o, fmt_gate, fmt_up, fmt_down; /* DQ_FMT_* */
     const void *wq, *wk, *wv, *wo, *wgate, *wup, *wdown;      /* packed device matrices */
     const float *attn_norm, *ffn_norm;                        /* device, n_embd floats */
+    const float *bq, *bk, *bv, *q_norm, *k_norm;              /* device, optional (NULL) */
 } dq_layer_t;
 
 int dq_layer_workspace_bytes(const dq_layer_t* layer, uint32_t n_ctx, size_t* bytes);

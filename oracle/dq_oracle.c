@@ -953,10 +953,26 @@ float dqo_silu(float v) { return v / (1.0f + expf(-v)); }
 
 static size_t rb_of(int fmt, size_t cols) { return dqo_row_size(fmt, (int64_t)cols); }
 
-/* models/dense_forward.cpp:3897-4257, the plain Llama branch: no biases,
- * no QK-norm, no sandwich norms, gated SiLU FFN, Q8_0 KV. The K-quant
- * matvecs quantize their input per 256 (matvec -> matmul_q4_k/q6_k, and
- * quantize_shared_q8k for the shared Q/K/V and gate/up inputs). */
+/* After the Q/K/V products of one token (models/dense_forward.cpp
+ * :3904-3931 decode, :3318-3342 batch): the optional biases (add_bias: y +=
+ * b), then the optional per-head QK-norm (rms_norm_vec of each head of q and
+ * of k with the head_dim weights q_norm / k_norm). */
+static void qkv_post(const dqo_layer_t* L, float* q, float* k, float* v) {
+    const size_t hd = L->head_dim, qd = (size_t)L->n_head * hd, kvd = (size_t)L->n_head_kv * hd;
+    if (L->bq) for (size_t i = 0; i < qd; ++i) q[i] += L->bq[i];
+    if (L->bk) for (size_t i = 0; i < kvd; ++i) k[i] += L->bk[i];
+    if (L->bv) for (size_t i = 0; i < kvd; ++i) v[i] += L->bv[i];
+    if (L->q_norm)
+        for (uint32_t h = 0; h < L->n_head; ++h) dqo_rms_norm(q + h * hd, L->q_norm, q + h * hd, hd, L->rms_eps);
+    if (L->k_norm)
+        for (uint32_t h = 0; h < L->n_head_kv; ++h) dqo_rms_norm(k + h * hd, L->k_norm, k + h * hd, hd, L->rms_eps);
+}
+
+/* models/dense_forward.cpp:3897-4257, the Llama branch with the optional
+ * Q/K/V biases and per-head QK-norm (Qwen-style layers); no sandwich norms,
+ * gated SiLU FFN, Q8_0 KV. The K-quant matvecs quantize their input per 256
+ * (matvec -> matmul_q4_k/q6_k, and quantize_shared_q8k for the shared Q/K/V
+ * and gate/up inputs). */
 int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t pos,
                      const float* x, float* x_out, float* q_out, float* k_out,
                      float* v_out, float* attn_out_opt) {
@@ -979,6 +995,7 @@ int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t po
     rc |= dqo_matmul(L->fmt_q, L->wq, qd, E, attn_in, q, 0, 0);
     rc |= dqo_matmul(L->fmt_k, L->wk, kvd, E, attn_in, k, 0, 0);
     rc |= dqo_matmul(L->fmt_v, L->wv, kvd, E, attn_in, v, 0, 0);
+    qkv_post(L, q, k, v);
     dqo_rope_cache(rope, hd, pos, L->rope_theta);
     for (uint32_t h = 0; h < L->n_head; ++h) dqo_rope_neox(q + h * hd, hd, rope);
     for (uint32_t h = 0; h < L->n_head_kv; ++h) dqo_rope_neox(k + h * hd, hd, rope);
@@ -1011,7 +1028,8 @@ int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t po
 /* The CPU batch branch of models/dense_forward.cpp for a prompt chunk of
  * n_tok tokens at positions pos0..: per token rms_norm (:3264-3273), Q/K/V
  * through matvec_batch (:3286-3290, matmul_q4_k_batch / matmul_q6_k_batch:
- * dqo_gemm), per token RoPE and KV rows (:3347-3362), attention over the
+ * dqo_gemm), per token the optional biases and QK-norm (:3318-3342), RoPE
+ * and KV rows (:3347-3362), attention over the
  * cache (:3449-3460, attention_prefill_cpu_q8), output projection, residual
  * and FFN norm (:3539-3560), up/gate, silu(gate) * up, down, residual
  * (:3600-3624). RoPE over the whole head (n_rot = head_dim). */
@@ -1038,6 +1056,7 @@ int dqo_layer_prefill(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t p
     const size_t pos_bytes = (size_t)L->n_head_kv * row_bytes;
     for (size_t t = 0; t < T; ++t) {
         const uint32_t pos = pos0 + (uint32_t)t;
+        qkv_post(L, q + t * qd, k + t * kvd, v + t * kvd);
         dqo_rope_cache(rope, hd, pos, L->rope_theta);
         for (uint32_t h = 0; h < L->n_head; ++h) dqo_rope_neox(q + t * qd + h * hd, hd, rope);
         for (uint32_t h = 0; h < L->n_head_kv; ++h) {

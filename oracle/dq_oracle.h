@@ -123,6 +123,10 @@ typedef struct {
     int fmt_q, fmt_k, fmt_v, fmt_o, fmt_gate, fmt_up, fmt_down; /* GGUF ids */
     const uint8_t *wq, *wk, *wv, *wo, *wgate, *wup, *wdown;
     const float *attn_norm, *ffn_norm;
+    /* optional (NULL = absent): Q/K/V biases added to the projections
+     * (add_bias, :3904-3908), then the per-head QK-norm (rms_norm_vec over
+     * each head with a head_dim weight, :3915-3931), both before RoPE */
+    const float *bq, *bk, *bv, *q_norm, *k_norm;
 } dqo_layer_t;
 
 int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t pos,

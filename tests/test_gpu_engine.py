@@ -325,6 +325,25 @@ def make_layer(lib, orc, E, n_head, n_kv, F, types, seed):
     return mats, an, fn, oa
 
 
+def qwen_extras(oa, n_head, n_kv, seed):
+    """Q/K/V biases and per-head QK-norm weights (Qwen-style layer), set on the
+    oracle's arguments; returned for the engine's arguments."""
+    rng = np.random.default_rng(seed)
+    ex = {"bq": rng.standard_normal(n_head * 128).astype(np.float32),
+          "bk": rng.standard_normal(n_kv * 128).astype(np.float32),
+          "bv": (0.5 * rng.standard_normal(n_kv * 128)).astype(np.float32),
+          "q_norm": (1 + 0.1 * rng.standard_normal(128)).astype(np.float32),
+          "k_norm": (0.5 + 0.1 * rng.standard_normal(128)).astype(np.float32)}
+    for nm, v in ex.items():
+        setattr(oa, nm, v.ctypes.data)
+    return ex
+
+
+def set_extras(A, ex):
+    A.bq, A.bk, A.bv = ex["bq"].ctypes.data, ex["bk"].ctypes.data, ex["bv"].ctypes.data
+    A.q_norm_w, A.k_norm_w = ex["q_norm"].ctypes.data, ex["k_norm"].ctypes.data
+
+
 def layer_args(mats, an, fn, E, n_head, n_kv, F, layer_off, pos, rope, x, x_out, upload_x, download_x, upload_dyn):
     hd = 128
     A = _lib.CudaLayerArgs()
@@ -380,11 +399,28 @@ def test_layer_forward_chain(lib, orc):
         assert rel(orc.dequantize_row(Q8_0, dv[row], kvd), orc.dequantize_row(Q8_0, ref_v[rrow], kvd)) <= 2e-2
         # the prior rows are untouched
         assert np.array_equal(dk[o:o + pos * pb], kc[o:o + pos * pb])
-    # a feature outside the plain layer: NOT_SUPPORTED, output untouched
+    # a Qwen-style layer (Q/K/V biases, per-head QK-norm) on the first layer's
+    # cache slot at pos + 1, against the oracle with the same extras
+    ex = qwen_extras(L0[3], n_head, n_kv, 13)
+    rope1 = orc.rope_cache(128, pos + 1, 500000.0)
+    out_q = np.full(E, np.nan, np.float32)
+    A3 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos + 1, rope1, x, out_q, 1, 1, 1)
+    set_extras(A3, ex)
+    assert lib.cuda_layer_forward(ctypes.byref(A3)) == OK
+    k0q, v0q = k0.copy(), v0.copy()
+    want_q = orc.layer_decode(L0[3], k0q, v0q, pos + 1, x)[0]
+    e = rel(out_q, want_q)
+    print(f"qwen-style layer rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    # features still outside the layer (sandwich norms, a GELU FFN):
+    # NOT_SUPPORTED, output untouched
     keep = out.copy()
-    bias = np.zeros(n_head * 128, np.float32)
+    post = np.ones(E, np.float32)
     A2 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos, rope, x, out, 1, 1, 1)
-    A2.bq = bias.ctypes.data
+    A2.post_attn_norm_w = post.ctypes.data
+    assert lib.cuda_layer_forward(ctypes.byref(A2)) == NOT_SUPPORTED
+    A2 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos, rope, x, out, 1, 1, 1)
+    A2.act_gelu = 1
     assert lib.cuda_layer_forward(ctypes.byref(A2)) == NOT_SUPPORTED
     assert np.array_equal(out, keep)
     for L in (L0, L1):
@@ -524,12 +560,12 @@ def test_layer_forward_batch(lib, orc):
     e = rel(out, want)
     print(f"engine two layers vs oracle: {e:.3e}", flush=True)
     assert e <= 3e-2  # two layers: twice the one-layer bound of test_gpu_layer_prefill.py
-    # features outside the plain layer: NOT_SUPPORTED, out untouched
+    # features outside the layer (sandwich norms, a GELU FFN): NOT_SUPPORTED, out untouched
     keep = out.copy()
     mats, an, fn, _ = layers[0]
-    bias = np.zeros(n_head * hd, np.float32)
+    post = np.ones(E, np.float32)
     A = batch_args(mats, an, fn, E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, None, None, 1, 1, 1)
-    A.bq = bias.ctypes.data
+    A.post_ffn_norm_w = post.ctypes.data
     assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == NOT_SUPPORTED
     q8 = make_layer(lib, orc, E, n_head, n_kv, F, (Q8_0,) * 7, 90)
     A = batch_args(*q8[:3], E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, None, None, 1, 1, 1)
@@ -540,6 +576,45 @@ def test_layer_forward_batch(lib, orc):
     for L in layers + [q8]:
         for m in L[0].values():
             m.free()
+    lib.cuda_kv_cache_release()
+
+
+def test_layer_forward_batch_qwen(lib, orc):
+    """A Qwen-style layer (Q/K/V biases, per-head QK-norm) over a 40-token
+    chunk after 20 cached positions through cuda_layer_forward_batch, against
+    the oracle's layer prefill with the same extras (the prefill-layer bound,
+    1.5e-2) and its K/V rows within the Q8_0 step."""
+    E, n_head, n_kv, F, n_ctx, prior, T = 512, 8, 2, 1024, 64, 20, 40
+    hd = 128
+    kc, vc, pb = prior_cache(orc, 1, n_ctx, n_kv, hd, prior, seed=91)
+    assert lib.cuda_kv_cache_reserve(kc.size)
+    assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+    mats, an, fn, oa = make_layer(lib, orc, E, n_head, n_kv, F, (Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K), 92)
+    an *= 0.25 / np.sqrt(E)  # O(1) scores and FFN activations
+    fn *= 0.3 / np.sqrt(E)
+    ex = qwen_extras(oa, n_head, n_kv, 93)
+    x = np.random.default_rng(94).standard_normal((T, E)).astype(np.float32)
+    rope = np.stack([orc.rope_cache(hd, prior + i, 500000.0) for i in range(T)])
+    out = np.full((T, E), np.nan, np.float32)
+    A = batch_args(mats, an, fn, E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, None, None, 1, 1, 1)
+    set_extras(A, ex)
+    assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == OK
+    k1, v1 = kc.copy(), vc.copy()
+    want = orc.layer_prefill(oa, k1, v1, prior, x)
+    e = rel(out, want)
+    print(f"qwen-style layer prefill vs oracle: {e:.3e}", flush=True)
+    assert e <= 1.5e-2
+    dk, dv = np.zeros_like(kc), np.zeros_like(vc)
+    assert lib.cuda_kv_cache_download(P(dk), P(dv), kc.size)
+    kvd = n_kv * hd
+    rows = slice(prior * pb, (prior + T) * pb)
+    for d, h, c0 in ((dk, k1, kc), (dv, v1, vc)):
+        assert np.array_equal(d[:prior * pb], c0[:prior * pb])
+        a_ = orc.dequantize_row(Q8_0, d[rows], T * kvd)
+        b_ = orc.dequantize_row(Q8_0, h[rows], T * kvd)
+        assert rel(a_, b_) <= 2e-2
+    for m in mats.values():
+        m.free()
     lib.cuda_kv_cache_release()
 
 

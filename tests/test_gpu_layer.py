@@ -28,7 +28,8 @@ class HostLayer:
     the oracle's arguments, with the shape attributes the stage chains read
     (n_head, n_head_kv, mats[nm].fmt/rows/cols, cache.pos_bytes)."""
 
-    def __init__(self, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None):
+    def __init__(self, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None,
+                 qwen=False):
         from types import SimpleNamespace as NS
 
         from oracle.oracle import LayerArgs
@@ -62,13 +63,28 @@ class HostLayer:
             setattr(self.args, "w" + nm, self.keep[nm].ctypes.data)
         self.args.attn_norm = self.attn_norm.ctypes.data
         self.args.ffn_norm = self.ffn_norm.ctypes.data
+        # Qwen-style extras: Q/K/V biases and per-head QK-norm weights
+        self.extras = {}
+        if qwen:
+            r2 = np.random.default_rng(seed + 7)
+            self.extras = {"bq": r2.standard_normal(qd).astype(np.float32),
+                           "bk": r2.standard_normal(kvd).astype(np.float32),
+                           "bv": (0.5 * r2.standard_normal(kvd)).astype(np.float32),
+                           "q_norm": (1 + 0.1 * r2.standard_normal(hd)).astype(np.float32),
+                           "k_norm": (0.5 + 0.1 * r2.standard_normal(hd)).astype(np.float32)}
+            for nm, v in self.extras.items():
+                setattr(self.args, nm, v.ctypes.data)
+                self.keep[nm] = v
 
 
-def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None):
-    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types)
+def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None, qwen=False):
+    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types, qwen)
     mats = {nm: ops.QuantMatrix.from_gguf(qt, h.keep[nm], r, c, device=gpu) for nm, (qt, r, c) in h.shapes.items()}
+    ex = {nm: torch.from_numpy(v) for nm, v in h.extras.items()}
     layer = ops.DecoderLayer(mats, torch.from_numpy(h.attn_norm), torch.from_numpy(h.ffn_norm), n_head, n_kv, 128,
-                             n_ctx, device=gpu)
+                             n_ctx, device=gpu,
+                             bias=(ex["bq"], ex["bk"], ex["bv"]) if ex else None,
+                             qk_norm=(ex["q_norm"], ex["k_norm"]) if ex else None)
     assert layer.cache.pos_bytes == h.cache.pos_bytes
     layer.cache.k.copy_(torch.from_numpy(h.kc))
     layer.cache.v.copy_(torch.from_numpy(h.vc))
@@ -79,15 +95,17 @@ def dequant_rows(orc, b, n):
     return orc.dequantize_row(synth.Q8_0, np.ascontiguousarray(b), n)
 
 
-@pytest.mark.parametrize("E,n_head,n_kv,F,pos", [
-    (4096, 32, 8, 14336, 4096),   # config 4: Llama-3-8B layer, 4096 prior tokens
-    (512, 4, 2, 1024, 0),         # first token
-    (512, 8, 2, 1536, 70),        # GQA 4, two tiles
+@pytest.mark.parametrize("E,n_head,n_kv,F,pos,qwen", [
+    (4096, 32, 8, 14336, 4096, False),   # config 4: Llama-3-8B layer, 4096 prior tokens
+    (512, 4, 2, 1024, 0, False),         # first token
+    (512, 8, 2, 1536, 70, False),        # GQA 4, two tiles
+    (512, 8, 2, 1536, 70, True),         # Qwen-style: Q/K/V biases, per-head QK-norm
+    (4096, 32, 8, 14336, 4096, True),
 ])
-def test_layer_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos):
-    print(f"layer E={E} heads={n_head}/{n_kv} F={F} pos={pos}", flush=True)
+def test_layer_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos, qwen):
+    print(f"layer E={E} heads={n_head}/{n_kv} F={F} pos={pos} qwen={qwen}", flush=True)
     n_ctx = pos + 2
-    layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos, seed=E + pos)
+    layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos, seed=E + pos, qwen=qwen)
     x = np.random.default_rng(pos + 1).standard_normal(E).astype(np.float32)
     want, q, k, v, ao = orc.layer_decode(args, kc, vc, pos, x)
     got = layer.decode(torch.from_numpy(x).to(gpu), pos).cpu().numpy()

@@ -51,6 +51,13 @@ def chain(layer, keep, orc, x, pos0, gemm, attention):
     nh, nkv = layer.n_head, layer.n_head_kv
     xn = np.stack([orc.rms_norm(x[t], keep["attn_norm"], 1e-5) for t in range(T)])
     q, k, v = gemm("q", xn), gemm("k", xn), gemm("v", xn)
+    if "bq" in keep:  # Qwen-style: biases, then per-head QK-norm, before RoPE
+        q, k, v = q + keep["bq"], k + keep["bk"], v + keep["bv"]
+        for t in range(T):
+            for h in range(nh):
+                q[t, h * HD:(h + 1) * HD] = orc.rms_norm(q[t, h * HD:(h + 1) * HD], keep["q_norm"], 1e-5)
+            for h in range(nkv):
+                k[t, h * HD:(h + 1) * HD] = orc.rms_norm(k[t, h * HD:(h + 1) * HD], keep["k_norm"], 1e-5)
     for t in range(T):
         tab = orc.rope_cache(HD, pos0 + t, 500000.0)
         for h in range(nh):
@@ -103,18 +110,20 @@ Q80_ALL = {nm: synth.Q8_0 for nm in ("q", "k", "v", "o", "gate", "up", "down")}
 Q40_FFN = {"gate": synth.Q4_0, "up": synth.Q4_0, "v": synth.Q8_0}
 
 
-@pytest.mark.parametrize("E,n_head,n_kv,F,pos0,n_tok,types", [
-    (4096, 32, 8, 14336, 1000, 16, None),  # config-4 layer shape after 1000 cached tokens
-    (512, 8, 2, 1536, 0, 40, None),        # prompt from position 0
-    (512, 4, 2, 1024, 70, 130, None),      # two attention query blocks, GEMM M tail
-    (512, 8, 2, 1536, 30, 48, Q80_ALL),    # a Q8_0 model
-    (512, 8, 2, 1536, 10, 40, Q40_FFN),    # Q4_0 FFN, Q8_0 V, Q4_K/Q6_K elsewhere
+@pytest.mark.parametrize("E,n_head,n_kv,F,pos0,n_tok,types,qwen", [
+    (4096, 32, 8, 14336, 1000, 16, None, False),  # config-4 layer shape after 1000 cached tokens
+    (512, 8, 2, 1536, 0, 40, None, False),        # prompt from position 0
+    (512, 4, 2, 1024, 70, 130, None, False),      # two attention query blocks, GEMM M tail
+    (512, 8, 2, 1536, 30, 48, Q80_ALL, False),    # a Q8_0 model
+    (512, 8, 2, 1536, 10, 40, Q40_FFN, False),    # Q4_0 FFN, Q8_0 V, Q4_K/Q6_K elsewhere
+    (512, 8, 2, 1536, 20, 40, None, True),        # Qwen-style: Q/K/V biases, per-head QK-norm
 ])
-def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, types):
-    print(f"layer_prefill E={E} heads={n_head}/{n_kv} F={F} pos0={pos0} n_tok={n_tok} types={types}", flush=True)
+def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, types, qwen):
+    print(f"layer_prefill E={E} heads={n_head}/{n_kv} F={F} pos0={pos0} n_tok={n_tok} types={types} qwen={qwen}",
+          flush=True)
     n_ctx = pos0 + n_tok + 2
     layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos0, seed=E + pos0 + n_tok,
-                                           norm_scale=conditioned(E), types=types)
+                                           norm_scale=conditioned(E), types=types, qwen=qwen)
     x = np.random.default_rng(n_tok).standard_normal((n_tok, E)).astype(np.float32)
     og, oa = oracle_fns(layer, keep, orc, kc, vc, pos0, n_tok)
     gg, ga = gpu_fns(gpu, layer, kc, vc, pos0, n_tok)

@@ -6,6 +6,10 @@ it, in the reference's order:
   -> attention over [0, pos] -> Wo + residual -> norm (ffn_norm) -> up, gate
   -> silu(gate) * up -> down + residual.
 
+With Q/K/V biases and per-head QK-norm (Qwen-style layers) the chain adds
+q,k,v += b (:3904-3908) and rms_norm of each q and k head (:3915-3931)
+between the products and RoPE.
+
 1. The same chain from the oracle's individually pinned pieces (matmul,
    rms_norm, rope_cache/rope_neox, kv_quantize_row, attn_decode, silu):
    equal to the layer (1e-6 norm-wise; it is the same float arithmetic).
@@ -18,7 +22,8 @@ it, in the reference's order:
    O(1) scores at config 4's shape that measures 1.5e-4, elsewhere <= 1e-7.
 3. Planted mistakes in chain 1 (gate and up swapped, a residual dropped, the
    two norm weights swapped, RoPE on adjacent pairs instead of NeoX halves,
-   the new K/V row not written, V read from the K cache) each move the result
+   the new K/V row not written, V read from the K cache, the biases
+   dropped, QK-norm after RoPE, q_norm and k_norm swapped) each move the result
    by far more than the bound, so the comparison would catch them.
 4. dqo_layer_prefill on one token at the same position (the CPU batch branch,
    whose products fall back to per-token GEMV semantics below 4 tokens) equals
@@ -41,7 +46,7 @@ def rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0)):
+def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False):
     from oracle.oracle import LayerArgs
     qd, kvd = n_head * HD, n_kv * HD
     shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
@@ -62,6 +67,16 @@ def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0)):
         setattr(args, "w" + nm, w[nm].ctypes.data)
     args.attn_norm = w["attn_norm"].ctypes.data
     args.ffn_norm = w["ffn_norm"].ctypes.data
+    if qwen:
+        # Q/K/V biases and per-head QK-norm weights (distinct scales, so that
+        # swapping the two norms matters)
+        w["bq"] = rng.standard_normal(qd).astype(np.float32)
+        w["bk"] = rng.standard_normal(kvd).astype(np.float32)
+        w["bv"] = (0.5 * rng.standard_normal(kvd)).astype(np.float32)
+        w["q_norm"] = (1.0 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+        w["k_norm"] = (0.5 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+        for nm in ("bq", "bk", "bv", "q_norm", "k_norm"):
+            setattr(args, nm, w[nm].ctypes.data)
     x = np.random.default_rng(seed + 100).standard_normal(E).astype(np.float32)
     return dict(E=E, n_head=n_head, n_kv=n_kv, F=F, pos=pos, shapes=shapes, w=w, kc=kc, vc=vc, pb=pb, args=args, x=x)
 
@@ -180,12 +195,26 @@ def chain(L, P, mistake=None):
     n1, n2 = ("ffn_norm", "attn_norm") if mistake == "norms_swapped" else ("attn_norm", "ffn_norm")
     xn = P.rms_norm(x, w[n1])
     q, k, v = mm("q", xn), mm("k", xn), mm("v", xn)
+    if "bq" in w and mistake != "no_bias":  # add_bias (:3904-3908)
+        q, k, v = q + w["bq"], k + w["bk"], v + w["bv"]
+    qn, kn = ("k_norm", "q_norm") if mistake == "qk_norms_swapped" else ("q_norm", "k_norm")
+
+    def qk_norm(q, k):  # per-head rms_norm_vec (:3915-3931)
+        for h in range(nh):
+            q[h * HD:(h + 1) * HD] = P.rms_norm(q[h * HD:(h + 1) * HD], w[qn])
+        for h in range(nkv):
+            k[h * HD:(h + 1) * HD] = P.rms_norm(k[h * HD:(h + 1) * HD], w[kn])
+
+    if "q_norm" in w and mistake != "qk_norm_after_rope":
+        qk_norm(q, k)
     tab = P.rope_table(pos)
     neox = mistake != "rope_adjacent"
     for h in range(nh):
         q[h * HD:(h + 1) * HD] = P.rope(q[h * HD:(h + 1) * HD], tab, neox)
     for h in range(nkv):
         k[h * HD:(h + 1) * HD] = P.rope(k[h * HD:(h + 1) * HD], tab, neox)
+    if "q_norm" in w and mistake == "qk_norm_after_rope":
+        qk_norm(q, k)
     pb = L["pb"]
     if mistake != "no_kv_write":
         kc[pos * pb:(pos + 1) * pb] = P.kv_row(k)
@@ -212,17 +241,20 @@ def layer(orc, L):
 
 
 SHAPES = [
-    pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), id="E512-pos70"),
-    pytest.param(4096, 32, 8, 14336, 4096, (1.0, 1.0), id="config4-pos4096"),
+    pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), False, id="E512-pos70"),
+    pytest.param(4096, 32, 8, 14336, 4096, (1.0, 1.0), False, id="config4-pos4096"),
     # unit norm weights make a 4096-wide layer's softmax nearly an argmax;
     # these scales keep scores and FFN activations O(1)
-    pytest.param(4096, 32, 8, 14336, 4096, (0.25 / 64, 0.3 / 64), id="config4-pos4096-conditioned"),
+    pytest.param(4096, 32, 8, 14336, 4096, (0.25 / 64, 0.3 / 64), False, id="config4-pos4096-conditioned"),
+    # Qwen-style: Q/K/V biases and per-head QK-norm
+    pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), True, id="E512-pos70-qwen"),
+    pytest.param(4096, 32, 8, 14336, 4096, (0.25 / 64, 0.3 / 64), True, id="config4-pos4096-qwen"),
 ]
 
 
-@pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns", SHAPES)
-def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos, norm_scale=ns)
+@pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
+def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns, qwen):
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos, norm_scale=ns, qwen=qwen)
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, OraclePieces(orc))
     e = rel(got, want)
@@ -232,9 +264,9 @@ def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns):
     assert not np.array_equal(gkc, L["kc"])  # the step wrote its row
 
 
-@pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns", SHAPES)
-def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv, F, pos, ns):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 1, norm_scale=ns)
+@pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
+def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv, F, pos, ns, qwen):
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 1, norm_scale=ns, qwen=qwen)
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, IndependentPieces(ref))
     e = rel(got, want)
@@ -250,15 +282,16 @@ def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv,
 
 
 MISTAKES = ["gate_up_swapped", "no_attn_residual", "no_ffn_residual", "norms_swapped", "rope_adjacent",
-            "no_kv_write", "v_from_k"]
+            "no_kv_write", "v_from_k", "no_bias", "qk_norm_after_rope", "qk_norms_swapped"]
 
 
 @pytest.mark.parametrize("mistake", MISTAKES)
 def test_planted_mistakes_fail(orc, mistake):
     """Each planted mistake moves the chain far outside the 1e-6 bound that
     the correct chain meets (norm weights 1 +- 0.02 for the swap are replaced
-    by distinct scales so that swapping them matters)."""
-    L = make(orc, 512, 8, 2, 1536, 70, seed=77, norm_scale=(0.25 / np.sqrt(512), 0.6 / np.sqrt(512)))
+    by distinct scales so that swapping them matters). The layer carries
+    Q/K/V biases and QK-norm, so the mistakes in those are covered too."""
+    L = make(orc, 512, 8, 2, 1536, 70, seed=77, norm_scale=(0.25 / np.sqrt(512), 0.6 / np.sqrt(512)), qwen=True)
     got = layer(orc, L)[0]
     ok = chain(L, OraclePieces(orc))[0]
     assert rel(got, ok) <= 1e-6
@@ -268,9 +301,9 @@ def test_planted_mistakes_fail(orc, mistake):
     assert e > 1e-3
 
 
-@pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns", SHAPES)
-def test_prefill_one_token_equals_decode(orc, E, n_head, n_kv, F, pos, ns):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 2, norm_scale=ns)
+@pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
+def test_prefill_one_token_equals_decode(orc, E, n_head, n_kv, F, pos, ns, qwen):
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 2, norm_scale=ns, qwen=qwen)
     dec, dkc, dvc = layer(orc, L)
     kc, vc = L["kc"].copy(), L["vc"].copy()
     pre = orc.layer_prefill(L["args"], kc, vc, pos, L["x"][None, :])[0]
