@@ -196,6 +196,43 @@ __device__ __forceinline__ void dq_head_rms_norm(float& lo, float& hi, const flo
     hi = hi * scale * w[lane + 64];
 }
 
+// The gated FFN activations of the reference (act(gate) * up):
+//  * silu(x) = x / (1 + expf(-x)) (models/dense_forward.cpp:53-55);
+//  * the decode branch's GELU, geglu_inplace (:107-126, its 8-wide path):
+//    g / (1 + exp(-2u)), u = (0.7978845608 g)(1 + 0.044715 g^2), with exp by
+//    exp_ps_avx2 (:69-94): clamp to [-87, 87], t = x log2(e), k = nearest
+//    integer (ties to even), r = t - k, 2^r by the degree-5 Horner
+//    polynomial (separate multiplies and adds), times 2^k from the exponent
+//    bits;
+//  * the batch branch's GELU, gelu_tanh (:49-51, :3608-3609).
+__device__ __forceinline__ float dq_exp_avx2(float x) {
+    x = x > -87.0f ? x : -87.0f;  // _mm256_max_ps(x, -87): NaN -> -87
+    x = x < 87.0f ? x : 87.0f;
+    const float t = x * 1.44269504088896341f;
+    const float k = rintf(t);
+    const float r = t - k;
+    float p = 1.3327544e-3f;
+    p = p * r + 9.6181292e-3f;
+    p = p * r + 5.5504109e-2f;
+    p = p * r + 2.4022651e-1f;
+    p = p * r + 6.9314718e-1f;
+    p = p * r + 1.0f;
+    return p * __builtin_bit_cast(float, ((int)k + 127) << 23);
+}
+enum DqFfnAct { DQ_ACT_SILU = 0, DQ_ACT_GEGLU = 1, DQ_ACT_GELU_TANH = 2 };
+template <int ACT>
+__device__ __forceinline__ float dq_ffn_act(float g) {
+    if constexpr (ACT == DQ_ACT_SILU) {
+        return g / (1.0f + expf(-g));
+    } else if constexpr (ACT == DQ_ACT_GEGLU) {
+        const float xx = g * g;
+        const float u = (0.7978845608028654f * g) * (1.0f + 0.044715f * xx);
+        return g / (1.0f + dq_exp_avx2(-2.0f * u));
+    } else {
+        return 0.5f * g * (1.0f + tanhf(0.7978845608028654f * g * (1.0f + 0.044715f * g * g)));
+    }
+}
+
 // Q/K/V post-processing of one head held by a wave as (lo, hi) (lane, lane
 // + 64), between the projections and RoPE: the bias (add_bias, y += b;
 // :3904-3908) and the per-head RMSNorm (:3915-3931). All optional.
@@ -299,3 +336,8 @@ int dq_rope_kv_write_batch_post(float* d_q, const float* d_k, const float* d_v, 
 static inline DqQkvPost dq_layer_post(const dq_layer_t* L) {
     return DqQkvPost{L->bq, L->bk, L->bv, L->q_norm, L->k_norm, L->rms_eps};
 }
+// act(gate) * up of the decode layer (gelu 1: geglu_inplace, else silu), then
+// the per-256 quantizer (dq_act_quant) or in float (dq_act_mul).
+int dq_act_quant(const float* d_gate, const float* d_up, size_t n, int gelu, int8_t* d_q, float* d_scale,
+                 int32_t* d_isum, void* stream);
+int dq_act_mul(const float* d_gate, const float* d_up, size_t n, int gelu, float* d_h, void* stream);

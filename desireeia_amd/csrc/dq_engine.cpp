@@ -507,7 +507,6 @@ int matmul_kquant_cuda_batch(int format, const void* d_w, size_t rows, size_t co
 int matmul_q8_0_cuda_ffn_gated(const void* d_up_qs, const void* d_up_scale, const void* d_gate_qs,
                                const void* d_gate_scale, const void* d_down_qs, const void* d_down_scale, size_t n_ff,
                                size_t n_embd, const float* x, float* out, int act_gelu) {
-    if (act_gelu != 0) return DQ_ERR_NOT_SUPPORTED;
     if (!d_up_qs || !d_up_scale || !d_gate_qs || !d_gate_scale || !d_down_qs || !d_down_scale)
         return DQ_ERR_NOT_SUPPORTED;
     if (!gemv_shape_ok(DQ_FMT_Q8_0, n_ff, n_embd) || !gemv_shape_ok(DQ_FMT_Q8_0, n_embd, n_ff))
@@ -526,10 +525,11 @@ int matmul_q8_0_cuda_ffn_gated(const void* d_up_qs, const void* d_up_scale, cons
     const Act a = carve_act((uint8_t*)g.act.p, mx);
     if (hipMemcpyAsync(dx, x, n_embd * 4, hipMemcpyHostToDevice, s) != hipSuccess) return io_fail();
     // matvec(up), matvec(gate) (matmul_q8_0: per-32 quantization of x),
-    // silu(gate) * up, matvec(down) (per-32 quantization of h)
+    // silu(gate) * up or geglu (the decode branch, dense_forward.cpp
+    // :4212-4219), matvec(down) (per-32 quantization of h)
     const dq_gemv_job_t jobs[2] = {{DQ_FMT_Q8_0, d_up_qs, n_ff, up, nullptr}, {DQ_FMT_Q8_0, d_gate_qs, n_ff, gate, nullptr}};
     if (dq_quantize_act(DQ_ACT_Q8_0, dx, n_embd, 1, a.q, a.s, a.i, nullptr, s) != DQ_OK ||
-        dq_gemv_group(jobs, 2, n_embd, a.q, a.s, a.i, s) != DQ_OK || dq_silu_mul(gate, up, n_ff, h, s) != DQ_OK ||
+        dq_gemv_group(jobs, 2, n_embd, a.q, a.s, a.i, s) != DQ_OK || dq_act_mul(gate, up, n_ff, act_gelu ? 1 : 0, h, s) != DQ_OK ||
         dq_quantize_act(DQ_ACT_Q8_0, h, n_ff, 1, a.q, a.s, a.i, nullptr, s) != DQ_OK ||
         dq_gemv(DQ_FMT_Q8_0, d_down_qs, n_embd, n_ff, a.q, a.s, a.i, dout, s) != DQ_OK)
         return io_fail();
@@ -787,9 +787,9 @@ static LayerExtras extras_of(const float* bq, const float* bk, const float* bv, 
 
 int cuda_layer_forward(const CudaLayerArgs* A) {
     if (!A || !g.kc) return DQ_ERR_NOT_SUPPORTED;
-    // features outside the dense layer with optional Q/K/V biases and per-head
-    // QK-norm: the engine's CPU path runs them
-    if (A->wag_qs || A->post_attn_norm_w || A->post_ffn_norm_w || A->act_gelu || A->dyn_all || A->rope_all)
+    // features outside the dense layer with optional Q/K/V biases, per-head
+    // QK-norm and a SiLU or GELU gated FFN: the engine's CPU path runs them
+    if (A->wag_qs || A->post_attn_norm_w || A->post_ffn_norm_w || A->dyn_all || A->rope_all)
         return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
     if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
@@ -807,6 +807,7 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     L.n_rot = A->rope_cache ? A->n_rot : A->head_dim;
     L.n_ff = (uint32_t)A->n_ff;
     L.rms_eps = A->rms_eps;
+    L.act_gelu = A->act_gelu ? 1 : 0;
     L.fmt_q = A->fmt_q, L.fmt_k = A->fmt_k, L.fmt_v = A->fmt_v, L.fmt_o = A->fmt_o;
     L.fmt_gate = A->fmt_gate, L.fmt_up = A->fmt_up, L.fmt_down = A->fmt_down;
     L.wq = A->wq_qs, L.wk = A->wk_qs, L.wv = A->wv_qs, L.wo = A->wo_qs;
@@ -921,9 +922,9 @@ int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, 
 
 int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     if (!A || !g.kc || A->n_tok == 0 || A->n_total == 0) return DQ_ERR_NOT_SUPPORTED;
-    // features outside the dense layer with optional Q/K/V biases and per-head
-    // QK-norm: the engine's CPU path runs them
-    if (A->wag_qs || A->post_attn_norm_w || A->post_ffn_norm_w || A->act_gelu) return DQ_ERR_NOT_SUPPORTED;
+    // features outside the dense layer with optional Q/K/V biases, per-head
+    // QK-norm and a SiLU or GELU gated FFN: the engine's CPU path runs them
+    if (A->wag_qs || A->post_attn_norm_w || A->post_ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
     if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
         A->heads_per_kv != A->n_head / A->n_head_kv)
@@ -943,6 +944,7 @@ int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     L.n_rot = A->rope_caches ? A->n_rot : A->head_dim;
     L.n_ff = (uint32_t)A->n_ff;
     L.rms_eps = A->rms_eps;
+    L.act_gelu = A->act_gelu ? 1 : 0;
     L.fmt_q = A->fmt_q, L.fmt_k = A->fmt_k, L.fmt_v = A->fmt_v, L.fmt_o = A->fmt_o;
     L.fmt_gate = A->fmt_gate, L.fmt_up = A->fmt_up, L.fmt_down = A->fmt_down;
     L.wq = A->wq_qs, L.wk = A->wk_qs, L.wv = A->wv_qs, L.wo = A->wo_qs;

@@ -204,6 +204,7 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q, cons
 // h = silu(gate) * up, silu(x) = x / (1 + expf(-x)) (models/dense_forward.cpp
 // :53-55, :4230-4235); then the per-256 quantizer. One wave per 256 values,
 // 4 per lane.
+template <int ACT>
 __global__ __launch_bounds__(256) void silu_quant_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                          int n, int8_t* __restrict__ q, float* __restrict__ scale,
                                                          int32_t* __restrict__ isum) {
@@ -218,8 +219,7 @@ __global__ __launch_bounds__(256) void silu_quant_kernel(const float* __restrict
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float x = hv[i];
-        hv[i] = x / (1.0f + expf(-x)) * uv[i];
+        hv[i] = dq_ffn_act<ACT>(hv[i]) * uv[i];
         amax = fmaxf(amax, fabsf(hv[i]));
     }
     amax = dq_wave_max(amax);
@@ -245,12 +245,12 @@ __global__ __launch_bounds__(256) void silu_quant_kernel(const float* __restrict
 
 // h = silu(gate) * up in float (the input of a Q8_0 / Q4_0 down projection,
 // which quantizes per 32 itself). One lane per value.
+template <int ACT>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                        int n, float* __restrict__ h) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
-    const float x = gate[i];
-    h[i] = x / (1.0f + expf(-x)) * up[i];
+    h[i] = dq_ffn_act<ACT>(gate[i]) * up[i];
 }
 
 // ------------------------------------------------------------- workspace --
@@ -351,19 +351,41 @@ int dq_norm_quant(const float* d_a, const float* d_b, float* d_h, const float* d
 
 int dq_silu_quant(const float* d_gate, const float* d_up, size_t n, int8_t* d_q, float* d_scale, int32_t* d_isum,
                   void* stream) {
-    if (!d_gate || !d_up || !d_q || !d_scale || !d_isum || n == 0 || n % 256) return DQ_ERR_INVALID_ARG;
-    const unsigned grid = (unsigned)((n / 256 + 3) / 4);
-    silu_quant_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(d_gate, d_up, (int)n, d_q, d_scale, d_isum);
-    return dq_launch_status();
+    return dq_act_quant(d_gate, d_up, n, 0, d_q, d_scale, d_isum, stream);
 }
 
 int dq_silu_mul(const float* d_gate, const float* d_up, size_t n, float* d_h, void* stream) {
+    return dq_act_mul(d_gate, d_up, n, 0, d_h, stream);
+}
+
+}  // extern "C"
+
+// act(gate) * up with the decode branch's activation (gelu: geglu_inplace),
+// then the per-256 quantizer / in float.
+int dq_act_quant(const float* d_gate, const float* d_up, size_t n, int gelu, int8_t* d_q, float* d_scale,
+                 int32_t* d_isum, void* stream) {
+    if (!d_gate || !d_up || !d_q || !d_scale || !d_isum || n == 0 || n % 256) return DQ_ERR_INVALID_ARG;
+    const unsigned grid = (unsigned)((n / 256 + 3) / 4);
+    if (gelu)
+        silu_quant_kernel<DQ_ACT_GEGLU><<<grid, 256, 0, (hipStream_t)stream>>>(d_gate, d_up, (int)n, d_q, d_scale, d_isum);
+    else
+        silu_quant_kernel<DQ_ACT_SILU><<<grid, 256, 0, (hipStream_t)stream>>>(d_gate, d_up, (int)n, d_q, d_scale, d_isum);
+    return dq_launch_status();
+}
+
+int dq_act_mul(const float* d_gate, const float* d_up, size_t n, int gelu, float* d_h, void* stream) {
     if (!d_gate || !d_up || !d_h) return DQ_ERR_INVALID_ARG;
     if (n == 0) return DQ_OK;
     if (n > (1u << 30)) return DQ_ERR_NOT_SUPPORTED;
-    silu_mul_kernel<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(d_gate, d_up, (int)n, d_h);
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    if (gelu)
+        silu_mul_kernel<DQ_ACT_GEGLU><<<grid, 256, 0, (hipStream_t)stream>>>(d_gate, d_up, (int)n, d_h);
+    else
+        silu_mul_kernel<DQ_ACT_SILU><<<grid, 256, 0, (hipStream_t)stream>>>(d_gate, d_up, (int)n, d_h);
     return dq_launch_status();
 }
+
+extern "C" {
 
 int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float* d_rope, uint32_t n_head,
                      uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
@@ -476,10 +498,10 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
         DQ_TRY(run_group(jobs, 2, E));
     }
     if (kquant(L->fmt_down)) {
-        DQ_TRY(dq_silu_quant(w.gate, w.up, F, w.aq, w.as, w.ai, stream));
+        DQ_TRY(dq_act_quant(w.gate, w.up, F, L->act_gelu, w.aq, w.as, w.ai, stream));
         DQ_TRY(dq_gemv_add(L->fmt_down, L->wdown, E, F, w.aq, w.as, w.ai, w.x2, d_x_out, stream));
     } else {
-        DQ_TRY(dq_silu_mul(w.gate, w.up, F, w.yn, stream));
+        DQ_TRY(dq_act_mul(w.gate, w.up, F, L->act_gelu, w.yn, stream));
         DQ_TRY(dq_quantize_act(DQ_ACT_Q8_0, w.yn, F, 1, w.bq, w.bs, w.bi, nullptr, stream));
         DQ_TRY(dq_gemv_add(L->fmt_down, L->wdown, E, F, w.bq, w.bs, w.bi, w.x2, d_x_out, stream));
     }

@@ -502,16 +502,17 @@ __global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a, c
     reinterpret_cast<float4*>(out)[i] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
 }
 
-// h = silu(gate) * up, silu(x) = x / (1 + expf(-x)) (models/dense_forward.cpp
+// h = act(gate) * up: silu(x) = x / (1 + expf(-x)) or gelu_tanh (models/dense_forward.cpp
 // :53-55, :3606-3611), in place into up, 4 per lane.
+template <int ACT>
 __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float* __restrict__ gate, float* __restrict__ up,
                                                            size_t n4) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n4) return;
     const float4 g = reinterpret_cast<const float4*>(gate)[i];
     const float4 u = reinterpret_cast<const float4*>(up)[i];
-    reinterpret_cast<float4*>(up)[i] = make_float4(g.x / (1.0f + expf(-g.x)) * u.x, g.y / (1.0f + expf(-g.y)) * u.y,
-                                                   g.z / (1.0f + expf(-g.z)) * u.z, g.w / (1.0f + expf(-g.w)) * u.w);
+    reinterpret_cast<float4*>(up)[i] = make_float4(dq_ffn_act<ACT>(g.x) * u.x, dq_ffn_act<ACT>(g.y) * u.y,
+                                                   dq_ffn_act<ACT>(g.z) * u.z, dq_ffn_act<ACT>(g.w) * u.w);
 }
 
 // ---------------------------------------------------------- layer prefill --
@@ -820,7 +821,11 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         DQP_TRY(products(w.xn, E, 2, f, m, r, y));
     }
     const size_t nf4 = T * F / 4;
-    silu_mul_rows_kernel<<<(unsigned)((nf4 + 255) / 256), 256, 0, s>>>(w.gate, w.up, nf4);
+    // the batch branch's activation: silu, or gelu_tanh per element (:3608-3609)
+    if (L->act_gelu)
+        silu_mul_rows_kernel<DQ_ACT_GELU_TANH><<<(unsigned)((nf4 + 255) / 256), 256, 0, s>>>(w.gate, w.up, nf4);
+    else
+        silu_mul_rows_kernel<DQ_ACT_SILU><<<(unsigned)((nf4 + 255) / 256), 256, 0, s>>>(w.gate, w.up, nf4);
     DQP_TRY(dq_launch_status());
     {
         const int f[1] = {L->fmt_down};

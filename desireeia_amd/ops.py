@@ -361,7 +361,7 @@ class LayerDesc(ctypes.Structure):
                 ("wgate", ctypes.c_void_p), ("wup", ctypes.c_void_p), ("wdown", ctypes.c_void_p),
                 ("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p),
                 ("bq", ctypes.c_void_p), ("bk", ctypes.c_void_p), ("bv", ctypes.c_void_p),
-                ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p)]
+                ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p), ("act_gelu", ctypes.c_int)]
 
 
 def rope_cache(n_rot, pos, theta):
@@ -380,9 +380,10 @@ class DecoderLayer:
     NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
     def __init__(self, mats, attn_norm, ffn_norm, n_head, n_head_kv, head_dim, n_ctx, rms_eps=1e-5,
-                 rope_theta=500000.0, n_rot=None, device="cuda", bias=None, qk_norm=None):
+                 rope_theta=500000.0, n_rot=None, device="cuda", bias=None, qk_norm=None, act_gelu=False):
         """bias: optional (bq, bk, bv) float tensors; qk_norm: optional
-        (q_norm, k_norm) [head_dim] weights (Qwen-style layers)."""
+        (q_norm, k_norm) [head_dim] weights (Qwen-style layers); act_gelu: a
+        gated GELU FFN."""
         self.mats = mats
         self.attn_norm = attn_norm.to(device).float().contiguous()
         self.ffn_norm = ffn_norm.to(device).float().contiguous()
@@ -397,6 +398,7 @@ class DecoderLayer:
             setattr(d, "w" + nm, mats[nm].buf.data_ptr())
         d.attn_norm = self.attn_norm.data_ptr()
         d.ffn_norm = self.ffn_norm.data_ptr()
+        d.act_gelu = int(act_gelu)
         self.extras = {}
         for names, vals in ((("bq", "bk", "bv"), bias), (("q_norm", "k_norm"), qk_norm)):
             for nm, t in zip(names, vals or ()):

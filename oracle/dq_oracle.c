@@ -951,6 +951,45 @@ void dqo_rope_neox(float* v, size_t n_rot, const float* cache) {
 /* models/dense_forward.cpp:53-55 */
 float dqo_silu(float v) { return v / (1.0f + expf(-v)); }
 
+/* models/dense_forward.cpp:49-51 gelu_tanh (the batch branch's gated GELU,
+ * :3608-3609, and the CPU fallback's scalar tail). */
+float dqo_gelu_tanh(float v) {
+    return 0.5f * v * (1.0f + tanhf(0.7978845608028654f * v * (1.0f + 0.044715f * v * v)));
+}
+
+/* :69-94 exp_ps_avx2, one lane: clamp to [-87, 87], t = x log2(e), k =
+ * nearest integer of t (ties to even), r = t - k, 2^r by the degree-5
+ * Horner polynomial (a multiply then an add per step), times 2^k built in
+ * the exponent field. Separate multiplies and adds throughout (the
+ * intrinsics are not contracted). */
+float dqo_exp_avx2(float x) {
+    x = x > -87.0f ? x : -87.0f; /* _mm256_max_ps(x, -87): NaN -> -87 */
+    x = x < 87.0f ? x : 87.0f;
+    const float t = x * 1.44269504088896341f;
+    const float k = rintf(t);
+    const float r = t - k;
+    float p = 1.3327544e-3f;
+    p = p * r + 9.6181292e-3f;
+    p = p * r + 5.5504109e-2f;
+    p = p * r + 2.4022651e-1f;
+    p = p * r + 6.9314718e-1f;
+    p = p * r + 1.0f;
+    const int32_t bits = ((int32_t)k + 127) << 23;
+    float pow2k;
+    memcpy(&pow2k, &bits, 4);
+    return p * pow2k;
+}
+
+/* :107-126 geglu_inplace, its 8-wide path (every n_ff here is a multiple of
+ * 8): gelu(g) = g / (1 + exp(-2u)), u = (0.7978845608 g)(1 + 0.044715 g^2),
+ * then times up. The decode branch's gated GELU (:4212-4213). */
+float dqo_geglu(float g) {
+    const float xx = g * g;
+    const float u = (0.7978845608028654f * g) * (1.0f + 0.044715f * xx);
+    const float e = dqo_exp_avx2(-2.0f * u);
+    return g / (1.0f + e);
+}
+
 static size_t rb_of(int fmt, size_t cols) { return dqo_row_size(fmt, (int64_t)cols); }
 
 /* After the Q/K/V products of one token (models/dense_forward.cpp
@@ -1012,7 +1051,7 @@ int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t po
     dqo_rms_norm(proj, L->ffn_norm, xnp, E, L->rms_eps);
     rc |= dqo_matmul(L->fmt_up, L->wup, F, E, xnp, up, 0, 0);
     rc |= dqo_matmul(L->fmt_gate, L->wgate, F, E, xnp, gate, 0, 0);
-    for (size_t i = 0; i < F; ++i) up[i] = dqo_silu(gate[i]) * up[i];
+    for (size_t i = 0; i < F; ++i) up[i] = (L->act_gelu ? dqo_geglu(gate[i]) : dqo_silu(gate[i])) * up[i];
     rc |= dqo_matmul(L->fmt_down, L->wdown, E, F, up, fout, 0, 0);
     for (size_t i = 0; i < E; ++i) x_out[i] = fout[i] + proj[i];
 
@@ -1072,7 +1111,7 @@ int dqo_layer_prefill(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t p
     for (size_t t = 0; t < T; ++t) dqo_rms_norm(proj + t * E, L->ffn_norm, xn + t * E, E, L->rms_eps);
     rc |= dqo_gemm(L->fmt_up, L->wup, F, E, xn, T, up, 0, 0, 0, 0);
     rc |= dqo_gemm(L->fmt_gate, L->wgate, F, E, xn, T, gate, 0, 0, 0, 0);
-    for (size_t i = 0; i < T * F; ++i) up[i] = dqo_silu(gate[i]) * up[i];
+    for (size_t i = 0; i < T * F; ++i) up[i] = (L->act_gelu ? dqo_gelu_tanh(gate[i]) : dqo_silu(gate[i])) * up[i];
     rc |= dqo_gemm(L->fmt_down, L->wdown, E, F, up, T, fout, 0, 0, 0, 0);
     for (size_t i = 0; i < T * E; ++i) x_out[i] = fout[i] + proj[i];
     free(xn); free(q); free(k); free(v); free(ao); free(proj); free(up); free(gate); free(fout); free(rope);

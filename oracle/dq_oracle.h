@@ -105,6 +105,9 @@ void dqo_rms_norm(const float* x, const float* w, float* y, size_t n, float eps)
 void dqo_rope_cache(float* cache, size_t n_rot, uint32_t pos, float theta_base);
 void dqo_rope_neox(float* v, size_t n_rot, const float* cache);
 float dqo_silu(float v);
+float dqo_gelu_tanh(float v);
+float dqo_exp_avx2(float x);
+float dqo_geglu(float g);
 void dqo_softmax(float* s, size_t n);
 /* Prefill attention over a Q8_0 KV cache (core/attn_cpu.cpp:128-390):
  * q_all/out [n_tok][q_dim]; K/V row of (pos, kv head) at base + pos*pos_bytes
@@ -127,6 +130,9 @@ typedef struct {
      * (add_bias, :3904-3908), then the per-head QK-norm (rms_norm_vec over
      * each head with a head_dim weight, :3915-3931), both before RoPE */
     const float *bq, *bk, *bv, *q_norm, *k_norm;
+    /* 1: gated GELU instead of SiLU (decode: geglu_inplace, :4212-4213;
+     * batch: gelu_tanh per element, :3608-3609) */
+    int act_gelu;
 } dqo_layer_t;
 
 int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t pos,

@@ -43,7 +43,7 @@ class LayerArgs(ctypes.Structure):
                 ("fmt_up", c_int), ("fmt_down", c_int),
                 ("wq", c_p), ("wk", c_p), ("wv", c_p), ("wo", c_p), ("wgate", c_p), ("wup", c_p), ("wdown", c_p),
                 ("attn_norm", c_p), ("ffn_norm", c_p),
-                ("bq", c_p), ("bk", c_p), ("bv", c_p), ("q_norm", c_p), ("k_norm", c_p)]
+                ("bq", c_p), ("bk", c_p), ("bv", c_p), ("q_norm", c_p), ("k_norm", c_p), ("act_gelu", c_int)]
 
 
 class Oracle:
@@ -82,6 +82,9 @@ class Oracle:
         L.dqo_rope_neox.argtypes = [c_p, c_size, c_p]
         L.dqo_silu.restype = c_f
         L.dqo_silu.argtypes = [c_f]
+        for fn in ("dqo_gelu_tanh", "dqo_exp_avx2", "dqo_geglu"):
+            getattr(L, fn).restype = c_f
+            getattr(L, fn).argtypes = [c_f]
         L.dqo_softmax.argtypes = [c_p, c_size]
         L.dqo_layer_decode.argtypes = [ctypes.POINTER(LayerArgs), c_p, c_p, c_u32, c_p, c_p, c_p, c_p, c_p, c_p]
         L.dqo_layer_prefill.argtypes = [ctypes.POINTER(LayerArgs), c_p, c_p, c_u32, c_u32, c_u32, c_p, c_p]

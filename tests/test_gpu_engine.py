@@ -178,10 +178,14 @@ def test_ffn_gated_q8_0(lib, orc):
     h = np.array([orc.L.dqo_silu(float(a)) for a in g], np.float32) * u
     want = orc.matmul(Q8_0, down.w, E, F, h.astype(np.float32))
     assert rel(out, want) <= TOL
-    keep = out.copy()
+    # act_gelu = 1: the decode branch's gated GELU (geglu_inplace)
     assert lib.matmul_q8_0_cuda_ffn_gated(up.qs, up.sc, gate.qs, gate.sc, down.qs, down.sc, F, E, P(x), P(out),
-                                          1) == NOT_SUPPORTED
-    assert np.array_equal(out, keep)
+                                          1) == OK
+    h = np.array([orc.L.dqo_geglu(float(a)) for a in g], np.float32) * u
+    want = orc.matmul(Q8_0, down.w, E, F, h.astype(np.float32))
+    e = rel(out, want)
+    print(f"ffn_gated gelu rel err {e:.3e}", flush=True)
+    assert e <= TOL
     for m in (up, gate, down):
         m.free()
 
@@ -412,7 +416,19 @@ def test_layer_forward_chain(lib, orc):
     e = rel(out_q, want_q)
     print(f"qwen-style layer rel err {e:.3e}", flush=True)
     assert e <= TOL
-    # features still outside the layer (sandwich norms, a GELU FFN):
+    # a gated-GELU layer (act_gelu) at pos + 2 against the oracle's decode GELU
+    L0[3].bq = L0[3].bk = L0[3].bv = L0[3].q_norm = L0[3].k_norm = None
+    L0[3].act_gelu = 1
+    rope2 = orc.rope_cache(128, pos + 2, 500000.0)
+    out_g = np.full(E, np.nan, np.float32)
+    A4 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos + 2, rope2, x, out_g, 1, 1, 1)
+    A4.act_gelu = 1
+    assert lib.cuda_layer_forward(ctypes.byref(A4)) == OK
+    want_g = orc.layer_decode(L0[3], k0q, v0q, pos + 2, x)[0]
+    e = rel(out_g, want_g)
+    print(f"gelu layer rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    # features still outside the layer (sandwich norms, an attention gate):
     # NOT_SUPPORTED, output untouched
     keep = out.copy()
     post = np.ones(E, np.float32)
@@ -420,7 +436,7 @@ def test_layer_forward_chain(lib, orc):
     A2.post_attn_norm_w = post.ctypes.data
     assert lib.cuda_layer_forward(ctypes.byref(A2)) == NOT_SUPPORTED
     A2 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos, rope, x, out, 1, 1, 1)
-    A2.act_gelu = 1
+    A2.wag_qs = L0[0]["q"].qs
     assert lib.cuda_layer_forward(ctypes.byref(A2)) == NOT_SUPPORTED
     assert np.array_equal(out, keep)
     for L in (L0, L1):
@@ -569,7 +585,7 @@ def test_layer_forward_batch(lib, orc):
     assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == NOT_SUPPORTED
     q8 = make_layer(lib, orc, E, n_head, n_kv, F, (Q8_0,) * 7, 90)
     A = batch_args(*q8[:3], E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, None, None, 1, 1, 1)
-    A.act_gelu = 1  # a GELU FFN
+    A.wag_qs = q8[0]["q"].qs  # an attention gate
     assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == NOT_SUPPORTED
     assert lib.cuda_layer_forward_batch(None) == NOT_SUPPORTED
     assert np.array_equal(out, keep)
@@ -579,7 +595,8 @@ def test_layer_forward_batch(lib, orc):
     lib.cuda_kv_cache_release()
 
 
-def test_layer_forward_batch_qwen(lib, orc):
+@pytest.mark.parametrize("gelu", [False, True])
+def test_layer_forward_batch_qwen(lib, orc, gelu):
     """A Qwen-style layer (Q/K/V biases, per-head QK-norm) over a 40-token
     chunk after 20 cached positions through cuda_layer_forward_batch, against
     the oracle's layer prefill with the same extras (the prefill-layer bound,
@@ -593,11 +610,13 @@ def test_layer_forward_batch_qwen(lib, orc):
     an *= 0.25 / np.sqrt(E)  # O(1) scores and FFN activations
     fn *= 0.3 / np.sqrt(E)
     ex = qwen_extras(oa, n_head, n_kv, 93)
+    oa.act_gelu = int(gelu)  # the batch branch's gated GELU (gelu_tanh)
     x = np.random.default_rng(94).standard_normal((T, E)).astype(np.float32)
     rope = np.stack([orc.rope_cache(hd, prior + i, 500000.0) for i in range(T)])
     out = np.full((T, E), np.nan, np.float32)
     A = batch_args(mats, an, fn, E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, None, None, 1, 1, 1)
     set_extras(A, ex)
+    A.act_gelu = int(gelu)
     assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == OK
     k1, v1 = kc.copy(), vc.copy()
     want = orc.layer_prefill(oa, k1, v1, prior, x)

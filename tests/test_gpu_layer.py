@@ -29,7 +29,7 @@ class HostLayer:
     (n_head, n_head_kv, mats[nm].fmt/rows/cols, cache.pos_bytes)."""
 
     def __init__(self, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None,
-                 qwen=False):
+                 qwen=False, gelu=False):
         from types import SimpleNamespace as NS
 
         from oracle.oracle import LayerArgs
@@ -63,6 +63,8 @@ class HostLayer:
             setattr(self.args, "w" + nm, self.keep[nm].ctypes.data)
         self.args.attn_norm = self.attn_norm.ctypes.data
         self.args.ffn_norm = self.ffn_norm.ctypes.data
+        self.gelu = gelu
+        self.args.act_gelu = int(gelu)
         # Qwen-style extras: Q/K/V biases and per-head QK-norm weights
         self.extras = {}
         if qwen:
@@ -77,14 +79,15 @@ class HostLayer:
                 self.keep[nm] = v
 
 
-def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None, qwen=False):
-    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types, qwen)
+def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None, qwen=False,
+               gelu=False):
+    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types, qwen, gelu)
     mats = {nm: ops.QuantMatrix.from_gguf(qt, h.keep[nm], r, c, device=gpu) for nm, (qt, r, c) in h.shapes.items()}
     ex = {nm: torch.from_numpy(v) for nm, v in h.extras.items()}
     layer = ops.DecoderLayer(mats, torch.from_numpy(h.attn_norm), torch.from_numpy(h.ffn_norm), n_head, n_kv, 128,
                              n_ctx, device=gpu,
                              bias=(ex["bq"], ex["bk"], ex["bv"]) if ex else None,
-                             qk_norm=(ex["q_norm"], ex["k_norm"]) if ex else None)
+                             qk_norm=(ex["q_norm"], ex["k_norm"]) if ex else None, act_gelu=gelu)
     assert layer.cache.pos_bytes == h.cache.pos_bytes
     layer.cache.k.copy_(torch.from_numpy(h.kc))
     layer.cache.v.copy_(torch.from_numpy(h.vc))
@@ -101,11 +104,16 @@ def dequant_rows(orc, b, n):
     (512, 8, 2, 1536, 70, False),        # GQA 4, two tiles
     (512, 8, 2, 1536, 70, True),         # Qwen-style: Q/K/V biases, per-head QK-norm
     (4096, 32, 8, 14336, 4096, True),
+    (512, 8, 2, 1536, 70, "gelu"),       # gated GELU FFN (geglu_inplace)
+    (512, 8, 2, 1536, 70, "gelu32"),     # gated GELU with a Q8_0 down projection (the float form)
 ])
 def test_layer_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos, qwen):
     print(f"layer E={E} heads={n_head}/{n_kv} F={F} pos={pos} qwen={qwen}", flush=True)
     n_ctx = pos + 2
-    layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos, seed=E + pos, qwen=qwen)
+    gelu = qwen in ("gelu", "gelu32")
+    types = {"down": synth.Q8_0} if qwen == "gelu32" else None
+    layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos, seed=E + pos, qwen=qwen is True,
+                                           gelu=gelu, types=types)
     x = np.random.default_rng(pos + 1).standard_normal(E).astype(np.float32)
     want, q, k, v, ao = orc.layer_decode(args, kc, vc, pos, x)
     got = layer.decode(torch.from_numpy(x).to(gpu), pos).cpu().numpy()

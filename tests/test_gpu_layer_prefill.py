@@ -70,7 +70,10 @@ def chain(layer, keep, orc, x, pos0, gemm, attention):
     h = proj + x
     xn2 = np.stack([orc.rms_norm(h[t], keep["ffn_norm"], 1e-5) for t in range(T)])
     up, gate = gemm("up", xn2), gemm("gate", xn2)
-    act = (gate / (np.float32(1) + np.exp(-gate))) * up
+    if getattr(layer, "gelu", False):  # the batch branch's gelu_tanh
+        act = np.vectorize(orc.L.dqo_gelu_tanh, otypes=[np.float32])(gate) * up
+    else:
+        act = (gate / (np.float32(1) + np.exp(-gate))) * up
     return dict(xn=xn, q=q, k=k, v=v, kr=kr, vr=vr, attn=attn, h=h, xn2=xn2, act=act, out=gemm("down", act) + h)
 
 
@@ -117,13 +120,16 @@ Q40_FFN = {"gate": synth.Q4_0, "up": synth.Q4_0, "v": synth.Q8_0}
     (512, 8, 2, 1536, 30, 48, Q80_ALL, False),    # a Q8_0 model
     (512, 8, 2, 1536, 10, 40, Q40_FFN, False),    # Q4_0 FFN, Q8_0 V, Q4_K/Q6_K elsewhere
     (512, 8, 2, 1536, 20, 40, None, True),        # Qwen-style: Q/K/V biases, per-head QK-norm
+    (512, 8, 2, 1536, 20, 40, None, "gelu"),      # gated GELU FFN (gelu_tanh)
 ])
 def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, types, qwen):
     print(f"layer_prefill E={E} heads={n_head}/{n_kv} F={F} pos0={pos0} n_tok={n_tok} types={types} qwen={qwen}",
           flush=True)
     n_ctx = pos0 + n_tok + 2
     layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos0, seed=E + pos0 + n_tok,
-                                           norm_scale=conditioned(E), types=types, qwen=qwen)
+                                           norm_scale=conditioned(E), types=types, qwen=qwen is True,
+                                           gelu=qwen == "gelu")
+    layer.gelu = qwen == "gelu"
     x = np.random.default_rng(n_tok).standard_normal((n_tok, E)).astype(np.float32)
     og, oa = oracle_fns(layer, keep, orc, kc, vc, pos0, n_tok)
     gg, ga = gpu_fns(gpu, layer, kc, vc, pos0, n_tok)

@@ -46,7 +46,7 @@ def rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False):
+def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, gelu=False):
     from oracle.oracle import LayerArgs
     qd, kvd = n_head * HD, n_kv * HD
     shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
@@ -77,8 +77,10 @@ def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False):
         w["k_norm"] = (0.5 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
         for nm in ("bq", "bk", "bv", "q_norm", "k_norm"):
             setattr(args, nm, w[nm].ctypes.data)
+    args.act_gelu = int(gelu)
     x = np.random.default_rng(seed + 100).standard_normal(E).astype(np.float32)
-    return dict(E=E, n_head=n_head, n_kv=n_kv, F=F, pos=pos, shapes=shapes, w=w, kc=kc, vc=vc, pb=pb, args=args, x=x)
+    return dict(E=E, n_head=n_head, n_kv=n_kv, F=F, pos=pos, shapes=shapes, w=w, kc=kc, vc=vc, pb=pb, args=args, x=x,
+                gelu=gelu)
 
 
 class OraclePieces:
@@ -109,6 +111,10 @@ class OraclePieces:
 
     def silu_mul(self, gate, up):
         s = np.array([self.o.L.dqo_silu(float(g)) for g in gate], np.float32)
+        return s * up
+
+    def gelu_mul(self, gate, up):
+        s = np.array([self.o.L.dqo_geglu(float(g)) for g in gate], np.float32)
         return s * up
 
 
@@ -180,6 +186,10 @@ class IndependentPieces:
         with np.errstate(over="ignore"):  # exp(-g) = inf gives silu = -0, as expf does
             return (g / (np.float32(1) + np.exp(-g))) * up
 
+    def gelu_mul(self, gate, up):
+        g = gate.astype(np.float64)  # the tanh form (:49-51) in fp64
+        return (0.5 * g * (1 + np.tanh(0.7978845608028654 * g * (1 + 0.044715 * g * g)))).astype(np.float32) * up
+
 
 def chain(L, P, mistake=None):
     """The decode layer as a chain of pieces P, in the reference's order.
@@ -227,7 +237,8 @@ def chain(L, P, mistake=None):
     up, gate = mm("up", xn2), mm("gate", xn2)
     if mistake == "gate_up_swapped":
         up, gate = gate, up
-    h = P.silu_mul(gate, up)
+    gelu = L["gelu"] != (mistake == "silu_for_gelu")
+    h = P.gelu_mul(gate, up) if gelu else P.silu_mul(gate, up)
     out = mm("down", h)
     if mistake != "no_ffn_residual":
         out = out + proj
@@ -249,12 +260,14 @@ SHAPES = [
     # Qwen-style: Q/K/V biases and per-head QK-norm
     pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), True, id="E512-pos70-qwen"),
     pytest.param(4096, 32, 8, 14336, 4096, (0.25 / 64, 0.3 / 64), True, id="config4-pos4096-qwen"),
+    # gated GELU FFN (geglu_inplace / gelu_tanh)
+    pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), "gelu", id="E512-pos70-gelu"),
 ]
 
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns, qwen):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos, norm_scale=ns, qwen=qwen)
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos, norm_scale=ns, qwen=qwen is True, gelu=qwen == "gelu")
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, OraclePieces(orc))
     e = rel(got, want)
@@ -266,7 +279,7 @@ def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns, qwen):
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv, F, pos, ns, qwen):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 1, norm_scale=ns, qwen=qwen)
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 1, norm_scale=ns, qwen=qwen is True, gelu=qwen == "gelu")
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, IndependentPieces(ref))
     e = rel(got, want)
@@ -282,7 +295,7 @@ def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv,
 
 
 MISTAKES = ["gate_up_swapped", "no_attn_residual", "no_ffn_residual", "norms_swapped", "rope_adjacent",
-            "no_kv_write", "v_from_k", "no_bias", "qk_norm_after_rope", "qk_norms_swapped"]
+            "no_kv_write", "v_from_k", "no_bias", "qk_norm_after_rope", "qk_norms_swapped", "silu_for_gelu"]
 
 
 @pytest.mark.parametrize("mistake", MISTAKES)
@@ -291,7 +304,8 @@ def test_planted_mistakes_fail(orc, mistake):
     the correct chain meets (norm weights 1 +- 0.02 for the swap are replaced
     by distinct scales so that swapping them matters). The layer carries
     Q/K/V biases and QK-norm, so the mistakes in those are covered too."""
-    L = make(orc, 512, 8, 2, 1536, 70, seed=77, norm_scale=(0.25 / np.sqrt(512), 0.6 / np.sqrt(512)), qwen=True)
+    L = make(orc, 512, 8, 2, 1536, 70, seed=77, norm_scale=(0.25 / np.sqrt(512), 0.6 / np.sqrt(512)), qwen=True,
+             gelu=mistake == "silu_for_gelu")
     got = layer(orc, L)[0]
     ok = chain(L, OraclePieces(orc))[0]
     assert rel(got, ok) <= 1e-6
@@ -303,7 +317,7 @@ def test_planted_mistakes_fail(orc, mistake):
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_prefill_one_token_equals_decode(orc, E, n_head, n_kv, F, pos, ns, qwen):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 2, norm_scale=ns, qwen=qwen)
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 2, norm_scale=ns, qwen=qwen is True, gelu=qwen == "gelu")
     dec, dkc, dvc = layer(orc, L)
     kc, vc = L["kc"].copy(), L["vc"].copy()
     pre = orc.layer_prefill(L["args"], kc, vc, pos, L["x"][None, :])[0]
@@ -311,3 +325,26 @@ def test_prefill_one_token_equals_decode(orc, E, n_head, n_kv, F, pos, ns, qwen)
     print(f"  prefill(n_tok=1) vs decode: {e:.2e}")
     assert e <= 1e-5
     assert np.array_equal(kc, dkc) and np.array_equal(vc, dvc)
+
+
+def test_gelu_pieces(orc):
+    """The gated-GELU pieces against mathematics: exp_avx2 within its degree-5
+    polynomial's error of exp over its whole range (measured 6.6e-6; a
+    dropped r^5 term alone moves it by ~4e-5, any other term or sign far
+    more), its clamp at -87 / 87 (and NaN -> exp(-87), as _mm256_max_ps
+    returns its second operand); geglu (the exp form) and gelu_tanh (the
+    tanh form) within 1e-5 of 0.5 g (1 + tanh(u)) in fp64 (relative, or
+    absolute 5e-7 where 1 + tanh(u) cancels)."""
+    L = orc.L
+    xs = np.concatenate([np.linspace(-87, 87, 20001), np.linspace(-1, 1, 2001)]).astype(np.float32)
+    e = np.array([L.dqo_exp_avx2(float(x)) for x in xs], np.float64)
+    want = np.exp(xs.astype(np.float64))
+    assert np.max(np.abs(e / want - 1)) <= 1e-5
+    lim = np.exp(np.float64(np.float32(-87.0)))
+    assert abs(L.dqo_exp_avx2(-100.0) / lim - 1) <= 1e-5 and abs(L.dqo_exp_avx2(float("nan")) / lim - 1) <= 1e-5
+    assert abs(L.dqo_exp_avx2(100.0) / np.exp(87.0) - 1) <= 1e-5
+    g = np.linspace(-12, 12, 4801).astype(np.float32)
+    exact = 0.5 * g.astype(np.float64) * (1 + np.tanh(0.7978845608028654 * g * (1 + 0.044715 * g.astype(np.float64) ** 2)))
+    for fn in (L.dqo_geglu, L.dqo_gelu_tanh):
+        got = np.array([fn(float(v)) for v in g], np.float64)
+        assert np.all(np.abs(got - exact) <= 1e-5 * np.maximum(np.abs(exact), 0.05))
