@@ -341,3 +341,7 @@ static inline DqQkvPost dq_layer_post(const dq_layer_t* L) {
 int dq_act_quant(const float* d_gate, const float* d_up, size_t n, int gelu, int8_t* d_q, float* d_scale,
                  int32_t* d_isum, void* stream);
 int dq_act_mul(const float* d_gate, const float* d_up, size_t n, int gelu, float* d_h, void* stream);
+// out = rms_norm_vec(a, w) + b for each of `rows` rows of n floats (the
+// sandwich norm before a residual); out may alias b.
+int dq_post_norm_add(const float* d_a, const float* d_w, const float* d_b, float* d_out, size_t n, uint32_t rows,
+                     float eps, void* stream);

@@ -756,21 +756,22 @@ int cuda_qkv_attention_out(const CudaQkvAttnArgs* A) {
 
 // ------------------------------------------------------------------ layer --
 
-// The optional per-layer vectors of a Qwen-style layer (Q/K/V biases,
-// QK-norm weights): host pointers (NULL = absent) and float counts.
+// The optional per-layer vectors (Q/K/V biases, QK-norm weights, sandwich
+// norms): host pointers (NULL = absent) and float counts.
 struct LayerExtras {
-    const float* h[5];
-    size_t n[5];
+    static constexpr int N = 7;
+    const float* h[N];
+    size_t n[N];
     size_t bytes() const {
         size_t b = 0;
-        for (int i = 0; i < 5; ++i)
+        for (int i = 0; i < N; ++i)
             if (h[i]) b += dq_align256(n[i] * 4);
         return b;
     }
     // device copies at dst (each 256-byte aligned), pointers into the layer
     bool upload(dq_layer_t& L, uint8_t* dst, hipStream_t s) const {
-        const float** d[5] = {&L.bq, &L.bk, &L.bv, &L.q_norm, &L.k_norm};
-        for (int i = 0; i < 5; ++i) {
+        const float** d[N] = {&L.bq, &L.bk, &L.bv, &L.q_norm, &L.k_norm, &L.post_attn_norm, &L.post_ffn_norm};
+        for (int i = 0; i < N; ++i) {
             *d[i] = nullptr;
             if (!h[i]) continue;
             if (hipMemcpyAsync(dst, h[i], n[i] * 4, hipMemcpyHostToDevice, s) != hipSuccess) return false;
@@ -781,16 +782,16 @@ struct LayerExtras {
     }
 };
 static LayerExtras extras_of(const float* bq, const float* bk, const float* bv, const float* qn, const float* kn,
-                             size_t q_dim, size_t kv_dim, size_t hd) {
-    return LayerExtras{{bq, bk, bv, qn, kn}, {q_dim, kv_dim, kv_dim, hd, hd}};
+                             const float* pa, const float* pf, size_t q_dim, size_t kv_dim, size_t hd, size_t E) {
+    return LayerExtras{{bq, bk, bv, qn, kn, pa, pf}, {q_dim, kv_dim, kv_dim, hd, hd, E, E}};
 }
 
 int cuda_layer_forward(const CudaLayerArgs* A) {
     if (!A || !g.kc) return DQ_ERR_NOT_SUPPORTED;
     // features outside the dense layer with optional Q/K/V biases, per-head
-    // QK-norm and a SiLU or GELU gated FFN: the engine's CPU path runs them
-    if (A->wag_qs || A->post_attn_norm_w || A->post_ffn_norm_w || A->dyn_all || A->rope_all)
-        return DQ_ERR_NOT_SUPPORTED;
+    // QK-norm, a SiLU or GELU gated FFN and sandwich norms (an attention
+    // gate, per-layer slots): the engine's CPU path runs them
+    if (A->wag_qs || A->dyn_all || A->rope_all) return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
     if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
         A->heads_per_kv != A->n_head / A->n_head_kv)
@@ -814,6 +815,8 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     L.wgate = A->wgate_qs, L.wup = A->wup_qs, L.wdown = A->wdown_qs;
     L.attn_norm = A->attn_norm_w;  // host pointers here; device copies below
     L.ffn_norm = A->ffn_norm_w;
+    L.post_attn_norm = A->post_attn_norm_w;  // (their presence sizes the workspace)
+    L.post_ffn_norm = A->post_ffn_norm_w;
     // every matrix must be one of ours, of the declared format and shape
     const void* w[7] = {L.wq, L.wk, L.wv, L.wo, L.wgate, L.wup, L.wdown};
     const int f[7] = {L.fmt_q, L.fmt_k, L.fmt_v, L.fmt_o, L.fmt_gate, L.fmt_up, L.fmt_down};
@@ -845,7 +848,8 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     // norm weights and the optional biases / QK-norm weights: device copies in
     // the tail of the workspace
     const LayerExtras ex =
-        extras_of(A->bq, A->bk, A->bv, A->q_norm_w, A->k_norm_w, A->q_dim, A->kv_dim, A->head_dim);
+        extras_of(A->bq, A->bk, A->bv, A->q_norm_w, A->k_norm_w, A->post_attn_norm_w, A->post_ffn_norm_w, A->q_dim,
+                  A->kv_dim, A->head_dim, A->n_embd);
     const size_t norm_off = dq_align256(wbytes);
     if (!reserve(g.work, norm_off + 2 * dq_align256(E * 4) + ex.bytes()) || !reserve(g.lx[0], E * 4) ||
         !reserve(g.lx[1], E * 4))
@@ -923,8 +927,9 @@ int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, 
 int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     if (!A || !g.kc || A->n_tok == 0 || A->n_total == 0) return DQ_ERR_NOT_SUPPORTED;
     // features outside the dense layer with optional Q/K/V biases, per-head
-    // QK-norm and a SiLU or GELU gated FFN: the engine's CPU path runs them
-    if (A->wag_qs || A->post_attn_norm_w || A->post_ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
+    // QK-norm, a SiLU or GELU gated FFN and sandwich norms (an attention
+    // gate, per-layer slots): the engine's CPU path runs them
+    if (A->wag_qs) return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
     if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
         A->heads_per_kv != A->n_head / A->n_head_kv)
@@ -970,7 +975,8 @@ int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     const size_t E = A->n_embd, NT = A->n_total;
     const int slot = A->rope_caches ? A->rope_slot : 0;
     const LayerExtras ex =
-        extras_of(A->bq, A->bk, A->bv, A->q_norm_w, A->k_norm_w, A->q_dim, A->kv_dim, A->head_dim);
+        extras_of(A->bq, A->bk, A->bv, A->q_norm_w, A->k_norm_w, A->post_attn_norm_w, A->post_ffn_norm_w, A->q_dim,
+                  A->kv_dim, A->head_dim, A->n_embd);
     if (!reserve(g.px, NT * E * 4) || !reserve(g.pwork, wbytes) ||
         !reserve(g.pnorm, 2 * dq_align256(E * 4) + ex.bytes()) ||
         (A->rope_caches && !reserve(g.prope[slot], NT * A->n_rot * 4)))

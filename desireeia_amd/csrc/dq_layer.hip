@@ -263,6 +263,7 @@ struct LayerWs {
     int32_t* bi;
     float* yn;     // float input of the per-32 quantizer
     float *q, *k, *v, *ao, *x2, *up, *gate;
+    float* tmp;  // sandwich norms: a projection before its norm
     void* attn;
     size_t attn_bytes, total;
 };
@@ -307,6 +308,7 @@ LayerWs carve(const dq_layer_t* L, uint32_t n_ctx, uint8_t* base) {
     w.x2 = (float*)take(E * 4);
     w.up = (float*)take(F * 4);
     w.gate = (float*)take(F * 4);
+    w.tmp = (float*)take(L->post_attn_norm || L->post_ffn_norm ? E * 4 : 0);
     size_t ab = 0;
     dq_attn_workspace_bytes(L->n_head, L->n_head_kv, L->head_dim, n_ctx, &ab);
     w.attn = take(ab);
@@ -484,11 +486,19 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
     else
         DQ_TRY(dq_attn_decode_q8(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos, n_ctx,
                                  w.ao, w.attn, w.attn_bytes, stream));
+    // the output projection plus the residual (x2 = x + Wo a), or with a
+    // sandwich norm x2 = x + rms_norm(Wo a, post_attn_norm) (:4140-4147)
+    auto residual = [&](int fmt, const void* wm, size_t rows, size_t cols, const int8_t* xq, const float* xs,
+                        const int32_t* xi, const float* res, const float* post, float* out) -> int {
+        if (!post) return dq_gemv_add(fmt, wm, rows, cols, xq, xs, xi, res, out, stream);
+        DQ_TRY(dq_gemv(fmt, wm, rows, cols, xq, xs, xi, w.tmp, stream));
+        return dq_post_norm_add(w.tmp, post, res, out, rows, 1, L->rms_eps, stream);
+    };
     if (q256) {
-        DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.aq, w.as, w.ai, d_x, w.x2, stream));
+        DQ_TRY(residual(L->fmt_o, L->wo, E, QD, w.aq, w.as, w.ai, d_x, L->post_attn_norm, w.x2));
     } else {
         DQ_TRY(dq_quantize_act(DQ_ACT_Q8_0, w.ao, QD, 1, w.bq, w.bs, w.bi, nullptr, stream));
-        DQ_TRY(dq_gemv_add(L->fmt_o, L->wo, E, QD, w.bq, w.bs, w.bi, d_x, w.x2, stream));
+        DQ_TRY(residual(L->fmt_o, L->wo, E, QD, w.bq, w.bs, w.bi, d_x, L->post_attn_norm, w.x2));
     }
     // ---- feed-forward block
     DQ_TRY(norm_acts(w.x2, L->ffn_norm, per32(L->fmt_gate) || per32(L->fmt_up)));
@@ -499,11 +509,11 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
     }
     if (kquant(L->fmt_down)) {
         DQ_TRY(dq_act_quant(w.gate, w.up, F, L->act_gelu, w.aq, w.as, w.ai, stream));
-        DQ_TRY(dq_gemv_add(L->fmt_down, L->wdown, E, F, w.aq, w.as, w.ai, w.x2, d_x_out, stream));
+        DQ_TRY(residual(L->fmt_down, L->wdown, E, F, w.aq, w.as, w.ai, w.x2, L->post_ffn_norm, d_x_out));
     } else {
         DQ_TRY(dq_act_mul(w.gate, w.up, F, L->act_gelu, w.yn, stream));
         DQ_TRY(dq_quantize_act(DQ_ACT_Q8_0, w.yn, F, 1, w.bq, w.bs, w.bi, nullptr, stream));
-        DQ_TRY(dq_gemv_add(L->fmt_down, L->wdown, E, F, w.bq, w.bs, w.bi, w.x2, d_x_out, stream));
+        DQ_TRY(residual(L->fmt_down, L->wdown, E, F, w.bq, w.bs, w.bi, w.x2, L->post_ffn_norm, d_x_out));
     }
     return DQ_OK;
 }

@@ -450,6 +450,40 @@ __global__ __launch_bounds__(64) void rope_kv_batch_kernel(float* __restrict__ q
     dq_q8_0_row128(x0, x1, j, (kind == 1 ? kc : vc) + (size_t)(pos0 + t) * pos_bytes + (size_t)hh * (HD / 32) * DQ_SZ_Q8_0);
 }
 
+// Sandwich norm and residual of every row (models/dense_forward.cpp
+// :4140-4147 and :4245-4255; batch :3546-3550, :3618-3626): out =
+// rms_norm_vec(a, w) + b, the norm with squares in float summed in double,
+// scale = 1/sqrtf(mean + eps), a * scale * w. One workgroup per row; out may
+// alias b.
+__global__ __launch_bounds__(256) void post_norm_add_kernel(const float* __restrict__ a, const float* __restrict__ w,
+                                                           const float* b, int n, float eps, float* out) {
+    __shared__ double part[4];
+    const size_t row = (size_t)blockIdx.x * n;
+    const int t = threadIdx.x;
+    double acc = 0.0;
+    for (int i = 4 * t; i < n; i += 1024) {
+        const float4 x = *reinterpret_cast<const float4*>(a + row + i);
+        const float s0 = x.x * x.x, s1 = x.y * x.y, s2 = x.z * x.z, s3 = x.w * x.w;
+        acc += (double)s0;
+        acc += (double)s1;
+        acc += (double)s2;
+        acc += (double)s3;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, DQ_WAVE);
+    if ((t & 63) == 0) part[t >> 6] = acc;
+    __syncthreads();
+    const double sum = (part[0] + part[1]) + (part[2] + part[3]);
+    const float sc = 1.0f / sqrtf((float)(sum / (double)n) + eps);
+    for (int i = 4 * t; i < n; i += 1024) {
+        const float4 x = *reinterpret_cast<const float4*>(a + row + i);
+        const float4 ww = *reinterpret_cast<const float4*>(w + i);
+        const float4 c = *reinterpret_cast<const float4*>(b + row + i);
+        *reinterpret_cast<float4*>(out + row + i) = make_float4(x.x * sc * ww.x + c.x, x.y * sc * ww.y + c.y,
+                                                                x.z * sc * ww.z + c.z, x.w * sc * ww.w + c.w);
+    }
+}
+
 // rms_norm_vec (models/dense_forward.cpp:129-165) of every row of a
 // [n_tok][n] array: squares in float summed in double, scale =
 // 1/sqrtf(mean + eps), y = x * scale * w. With b: x = a + b first (the
@@ -811,7 +845,12 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         DQP_TRY(products(w.attn, QD, 1, f, m, r, y));
     }
     // residual + FFN norm (:3539-3560), gated FFN (:3600-3624)
-    rms_norm_rows_kernel<<<n_tok, 256, 0, s>>>(w.down, d_x, w.h, L->ffn_norm, (int)E, L->rms_eps, w.xn);
+    if (L->post_attn_norm) {  // sandwich norm of the projection before the residual
+        DQP_TRY(dq_post_norm_add(w.down, L->post_attn_norm, d_x, w.h, E, n_tok, L->rms_eps, stream));
+        rms_norm_rows_kernel<<<n_tok, 256, 0, s>>>(w.h, nullptr, nullptr, L->ffn_norm, (int)E, L->rms_eps, w.xn);
+    } else {
+        rms_norm_rows_kernel<<<n_tok, 256, 0, s>>>(w.down, d_x, w.h, L->ffn_norm, (int)E, L->rms_eps, w.xn);
+    }
     DQP_TRY(dq_launch_status());
     {
         const int f[2] = {L->fmt_up, L->fmt_gate};
@@ -835,8 +874,19 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         DQP_TRY(products(w.up, F, 1, f, m, r, y));
     }
     const size_t ne4 = T * E / 4;
+    if (L->post_ffn_norm)  // sandwich norm of the FFN output before the residual
+        return dq_post_norm_add(w.down, L->post_ffn_norm, w.h, d_x_out, E, n_tok, L->rms_eps, stream);
     add_kernel<<<(unsigned)((ne4 + 255) / 256), 256, 0, s>>>(w.down, w.h, ne4, d_x_out);
     return dq_launch_status();
 }
 
 }  // extern "C"
+
+int dq_post_norm_add(const float* d_a, const float* d_w, const float* d_b, float* d_out, size_t n, uint32_t rows,
+                     float eps, void* stream) {
+    if (!d_a || !d_w || !d_b || !d_out || n == 0 || n % 4) return DQ_ERR_INVALID_ARG;
+    if (rows == 0) return DQ_OK;
+    if (n > (1u << 26)) return DQ_ERR_NOT_SUPPORTED;
+    post_norm_add_kernel<<<rows, 256, 0, (hipStream_t)stream>>>(d_a, d_w, d_b, (int)n, eps, d_out);
+    return dq_launch_status();
+}

@@ -361,7 +361,8 @@ class LayerDesc(ctypes.Structure):
                 ("wgate", ctypes.c_void_p), ("wup", ctypes.c_void_p), ("wdown", ctypes.c_void_p),
                 ("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p),
                 ("bq", ctypes.c_void_p), ("bk", ctypes.c_void_p), ("bv", ctypes.c_void_p),
-                ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p), ("act_gelu", ctypes.c_int)]
+                ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p), ("act_gelu", ctypes.c_int),
+                ("post_attn_norm", ctypes.c_void_p), ("post_ffn_norm", ctypes.c_void_p)]
 
 
 def rope_cache(n_rot, pos, theta):
@@ -380,10 +381,12 @@ class DecoderLayer:
     NAMES = ("q", "k", "v", "o", "gate", "up", "down")
 
     def __init__(self, mats, attn_norm, ffn_norm, n_head, n_head_kv, head_dim, n_ctx, rms_eps=1e-5,
-                 rope_theta=500000.0, n_rot=None, device="cuda", bias=None, qk_norm=None, act_gelu=False):
+                 rope_theta=500000.0, n_rot=None, device="cuda", bias=None, qk_norm=None, act_gelu=False,
+                 post_norms=None):
         """bias: optional (bq, bk, bv) float tensors; qk_norm: optional
         (q_norm, k_norm) [head_dim] weights (Qwen-style layers); act_gelu: a
-        gated GELU FFN."""
+        gated GELU FFN; post_norms: optional (post_attn_norm, post_ffn_norm)
+        [n_embd] sandwich-norm weights."""
         self.mats = mats
         self.attn_norm = attn_norm.to(device).float().contiguous()
         self.ffn_norm = ffn_norm.to(device).float().contiguous()
@@ -400,7 +403,8 @@ class DecoderLayer:
         d.ffn_norm = self.ffn_norm.data_ptr()
         d.act_gelu = int(act_gelu)
         self.extras = {}
-        for names, vals in ((("bq", "bk", "bv"), bias), (("q_norm", "k_norm"), qk_norm)):
+        for names, vals in ((("bq", "bk", "bv"), bias), (("q_norm", "k_norm"), qk_norm),
+                            (("post_attn_norm", "post_ffn_norm"), post_norms)):
             for nm, t in zip(names, vals or ()):
                 if t is not None:
                     self.extras[nm] = t.to(device).float().contiguous()

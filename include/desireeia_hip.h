@@ -285,7 +285,10 @@ int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float
  * (rms_norm_vec per head, :3915-3931), before RoPE. Each may be NULL.
  * act_gelu selects the gated GELU FFN of GELU architectures: the decode
  * layer uses geglu_inplace (:107-126, :4212-4213), the prefill layer the
- * per-element gelu_tanh of the batch branch (:49-51, :3608-3609). Weights are packed
+ * per-element gelu_tanh of the batch branch (:49-51, :3608-3609).
+ * post_attn_norm / post_ffn_norm (Gemma-style sandwich norms) normalise the
+ * output projection and the FFN output before their residuals (rms_norm_vec,
+ * :4140-4142, :4245-4247). Weights are packed
  * device matrices (dq_weights_pack), each of any of the four formats (Q4_K /
  * Q6_K read the per-256 activation, Q8_0 / Q4_0 the per-32 one, as the
  * reference CPU GEMVs of those formats do); n_embd, n_ff and n_head*head_dim
@@ -302,6 +305,7 @@ typedef struct {
     const float *attn_norm, *ffn_norm;                        /* device, n_embd floats */
     const float *bq, *bk, *bv, *q_norm, *k_norm;              /* device, optional (NULL) */
     int act_gelu; /* 1: gated GELU FFN (decode: geglu_inplace; prefill: gelu_tanh) */
+    const float *post_attn_norm, *post_ffn_norm; /* device [n_embd], optional (NULL): sandwich norms */
 } dq_layer_t;
 
 int dq_layer_workspace_bytes(const dq_layer_t* layer, uint32_t n_ctx, size_t* bytes);

@@ -1047,12 +1047,14 @@ int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t po
     }
     dqo_attn_decode_q8(q, kc, vc, L->n_head, L->n_head_kv, (uint32_t)hd, 0, pos, ao);
     rc |= dqo_matmul(L->fmt_o, L->wo, E, qd, ao, proj, 0, 0);
+    if (L->post_attn_norm) dqo_rms_norm(proj, L->post_attn_norm, proj, E, L->rms_eps); /* :4140-4142 */
     for (size_t i = 0; i < E; ++i) proj[i] += x[i];
     dqo_rms_norm(proj, L->ffn_norm, xnp, E, L->rms_eps);
     rc |= dqo_matmul(L->fmt_up, L->wup, F, E, xnp, up, 0, 0);
     rc |= dqo_matmul(L->fmt_gate, L->wgate, F, E, xnp, gate, 0, 0);
     for (size_t i = 0; i < F; ++i) up[i] = (L->act_gelu ? dqo_geglu(gate[i]) : dqo_silu(gate[i])) * up[i];
     rc |= dqo_matmul(L->fmt_down, L->wdown, E, F, up, fout, 0, 0);
+    if (L->post_ffn_norm) dqo_rms_norm(fout, L->post_ffn_norm, fout, E, L->rms_eps); /* :4245-4247 */
     for (size_t i = 0; i < E; ++i) x_out[i] = fout[i] + proj[i];
 
     if (q_out) memcpy(q_out, q, qd * sizeof(float));
@@ -1107,12 +1109,16 @@ int dqo_layer_prefill(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t p
     rc |= dqo_attn_prefill_q8(q, ao, n_tok, L->n_head, L->n_head / L->n_head_kv, (uint32_t)hd, (uint32_t)qd, kc, vc,
                               row_bytes, pos_bytes, pos0, n_swa, 1.0f / sqrtf((float)hd));
     rc |= dqo_gemm(L->fmt_o, L->wo, E, qd, ao, T, proj, 0, 0, 0, 0);
+    if (L->post_attn_norm) /* :3546-3548 */
+        for (size_t t = 0; t < T; ++t) dqo_rms_norm(proj + t * E, L->post_attn_norm, proj + t * E, E, L->rms_eps);
     for (size_t i = 0; i < T * E; ++i) proj[i] += x[i];
     for (size_t t = 0; t < T; ++t) dqo_rms_norm(proj + t * E, L->ffn_norm, xn + t * E, E, L->rms_eps);
     rc |= dqo_gemm(L->fmt_up, L->wup, F, E, xn, T, up, 0, 0, 0, 0);
     rc |= dqo_gemm(L->fmt_gate, L->wgate, F, E, xn, T, gate, 0, 0, 0, 0);
     for (size_t i = 0; i < T * F; ++i) up[i] = (L->act_gelu ? dqo_gelu_tanh(gate[i]) : dqo_silu(gate[i])) * up[i];
     rc |= dqo_gemm(L->fmt_down, L->wdown, E, F, up, T, fout, 0, 0, 0, 0);
+    if (L->post_ffn_norm) /* :3618-3620 */
+        for (size_t t = 0; t < T; ++t) dqo_rms_norm(fout + t * E, L->post_ffn_norm, fout + t * E, E, L->rms_eps);
     for (size_t i = 0; i < T * E; ++i) x_out[i] = fout[i] + proj[i];
     free(xn); free(q); free(k); free(v); free(ao); free(proj); free(up); free(gate); free(fout); free(rope);
     return rc ? DQO_ERR_NOT_SUPPORTED : DQO_OK;

@@ -133,6 +133,10 @@ typedef struct {
     /* 1: gated GELU instead of SiLU (decode: geglu_inplace, :4212-4213;
      * batch: gelu_tanh per element, :3608-3609) */
     int act_gelu;
+    /* optional sandwich norms (NULL = absent): rms_norm_vec of the output
+     * projection and of the FFN output, each before its residual
+     * (:4140-4142, :4245-4247; batch :3546-3548, :3618-3620) */
+    const float *post_attn_norm, *post_ffn_norm;
 } dqo_layer_t;
 
 int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t pos,

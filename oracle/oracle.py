@@ -43,7 +43,8 @@ class LayerArgs(ctypes.Structure):
                 ("fmt_up", c_int), ("fmt_down", c_int),
                 ("wq", c_p), ("wk", c_p), ("wv", c_p), ("wo", c_p), ("wgate", c_p), ("wup", c_p), ("wdown", c_p),
                 ("attn_norm", c_p), ("ffn_norm", c_p),
-                ("bq", c_p), ("bk", c_p), ("bv", c_p), ("q_norm", c_p), ("k_norm", c_p), ("act_gelu", c_int)]
+                ("bq", c_p), ("bk", c_p), ("bv", c_p), ("q_norm", c_p), ("k_norm", c_p), ("act_gelu", c_int),
+                ("post_attn_norm", c_p), ("post_ffn_norm", c_p)]
 
 
 class Oracle:

@@ -29,7 +29,7 @@ class HostLayer:
     (n_head, n_head_kv, mats[nm].fmt/rows/cols, cache.pos_bytes)."""
 
     def __init__(self, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None,
-                 qwen=False, gelu=False):
+                 qwen=False, gelu=False, sandwich=False):
         from types import SimpleNamespace as NS
 
         from oracle.oracle import LayerArgs
@@ -65,6 +65,14 @@ class HostLayer:
         self.args.ffn_norm = self.ffn_norm.ctypes.data
         self.gelu = gelu
         self.args.act_gelu = int(gelu)
+        self.post = {}
+        if sandwich:  # Gemma-style post-norms of the attention and FFN outputs
+            r3 = np.random.default_rng(seed + 9)
+            self.post = {"post_attn_norm": (0.5 + 0.05 * r3.standard_normal(E)).astype(np.float32),
+                         "post_ffn_norm": (0.8 + 0.05 * r3.standard_normal(E)).astype(np.float32)}
+            for nm, v in self.post.items():
+                setattr(self.args, nm, v.ctypes.data)
+                self.keep[nm] = v
         # Qwen-style extras: Q/K/V biases and per-head QK-norm weights
         self.extras = {}
         if qwen:
@@ -80,14 +88,16 @@ class HostLayer:
 
 
 def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None, qwen=False,
-               gelu=False):
-    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types, qwen, gelu)
+               gelu=False, sandwich=False):
+    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types, qwen, gelu, sandwich)
     mats = {nm: ops.QuantMatrix.from_gguf(qt, h.keep[nm], r, c, device=gpu) for nm, (qt, r, c) in h.shapes.items()}
     ex = {nm: torch.from_numpy(v) for nm, v in h.extras.items()}
     layer = ops.DecoderLayer(mats, torch.from_numpy(h.attn_norm), torch.from_numpy(h.ffn_norm), n_head, n_kv, 128,
                              n_ctx, device=gpu,
                              bias=(ex["bq"], ex["bk"], ex["bv"]) if ex else None,
-                             qk_norm=(ex["q_norm"], ex["k_norm"]) if ex else None, act_gelu=gelu)
+                             qk_norm=(ex["q_norm"], ex["k_norm"]) if ex else None, act_gelu=gelu,
+                             post_norms=(torch.from_numpy(h.post["post_attn_norm"]),
+                                         torch.from_numpy(h.post["post_ffn_norm"])) if h.post else None)
     assert layer.cache.pos_bytes == h.cache.pos_bytes
     layer.cache.k.copy_(torch.from_numpy(h.kc))
     layer.cache.v.copy_(torch.from_numpy(h.vc))
@@ -106,14 +116,16 @@ def dequant_rows(orc, b, n):
     (4096, 32, 8, 14336, 4096, True),
     (512, 8, 2, 1536, 70, "gelu"),       # gated GELU FFN (geglu_inplace)
     (512, 8, 2, 1536, 70, "gelu32"),     # gated GELU with a Q8_0 down projection (the float form)
+    (512, 8, 2, 1536, 70, "gemma"),      # Gemma-style: gated GELU and sandwich norms
+    (4096, 32, 8, 14336, 4096, "gemma"),
 ])
 def test_layer_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos, qwen):
     print(f"layer E={E} heads={n_head}/{n_kv} F={F} pos={pos} qwen={qwen}", flush=True)
     n_ctx = pos + 2
-    gelu = qwen in ("gelu", "gelu32")
+    gelu = qwen in ("gelu", "gelu32", "gemma")
     types = {"down": synth.Q8_0} if qwen == "gelu32" else None
     layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos, seed=E + pos, qwen=qwen is True,
-                                           gelu=gelu, types=types)
+                                           gelu=gelu, types=types, sandwich=qwen == "gemma")
     x = np.random.default_rng(pos + 1).standard_normal(E).astype(np.float32)
     want, q, k, v, ao = orc.layer_decode(args, kc, vc, pos, x)
     got = layer.decode(torch.from_numpy(x).to(gpu), pos).cpu().numpy()

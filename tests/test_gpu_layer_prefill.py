@@ -36,6 +36,9 @@ pytestmark = pytest.mark.gpu
 TOL_GEMM = 4e-3
 TOL_ATTN = 1e-3
 TOL_LAYER = 1.5e-2  # 1.5x the oracle's own move under 4e-4 product errors (test_oracle_sensitivity.py)
+# sandwich norms re-normalise the projection and FFN outputs, which amplifies
+# a product error further (the oracle moves up to 1.24e-2): 1.5x that
+TOL_LAYER_SANDWICH = 2e-2
 HD = 128
 
 
@@ -67,6 +70,8 @@ def chain(layer, keep, orc, x, pos0, gemm, attention):
     kr, vr = orc.kv_quantize_row(k.reshape(-1)), orc.kv_quantize_row(v.reshape(-1))
     attn = attention(q, kr, vr)
     proj = gemm("o", attn)
+    if "post_attn_norm" in keep:  # sandwich norm (:3546-3548)
+        proj = np.stack([orc.rms_norm(proj[t], keep["post_attn_norm"], 1e-5) for t in range(T)])
     h = proj + x
     xn2 = np.stack([orc.rms_norm(h[t], keep["ffn_norm"], 1e-5) for t in range(T)])
     up, gate = gemm("up", xn2), gemm("gate", xn2)
@@ -74,7 +79,10 @@ def chain(layer, keep, orc, x, pos0, gemm, attention):
         act = np.vectorize(orc.L.dqo_gelu_tanh, otypes=[np.float32])(gate) * up
     else:
         act = (gate / (np.float32(1) + np.exp(-gate))) * up
-    return dict(xn=xn, q=q, k=k, v=v, kr=kr, vr=vr, attn=attn, h=h, xn2=xn2, act=act, out=gemm("down", act) + h)
+    down = gemm("down", act)
+    if "post_ffn_norm" in keep:  # sandwich norm (:3618-3620)
+        down = np.stack([orc.rms_norm(down[t], keep["post_ffn_norm"], 1e-5) for t in range(T)])
+    return dict(xn=xn, q=q, k=k, v=v, kr=kr, vr=vr, attn=attn, h=h, xn2=xn2, act=act, out=down + h)
 
 
 def oracle_fns(layer, keep, orc, kc, vc, pos0, T):
@@ -121,6 +129,7 @@ Q40_FFN = {"gate": synth.Q4_0, "up": synth.Q4_0, "v": synth.Q8_0}
     (512, 8, 2, 1536, 10, 40, Q40_FFN, False),    # Q4_0 FFN, Q8_0 V, Q4_K/Q6_K elsewhere
     (512, 8, 2, 1536, 20, 40, None, True),        # Qwen-style: Q/K/V biases, per-head QK-norm
     (512, 8, 2, 1536, 20, 40, None, "gelu"),      # gated GELU FFN (gelu_tanh)
+    (512, 8, 2, 1536, 20, 40, None, "gemma"),     # gated GELU and sandwich norms
 ])
 def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, types, qwen):
     print(f"layer_prefill E={E} heads={n_head}/{n_kv} F={F} pos0={pos0} n_tok={n_tok} types={types} qwen={qwen}",
@@ -128,8 +137,8 @@ def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, type
     n_ctx = pos0 + n_tok + 2
     layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos0, seed=E + pos0 + n_tok,
                                            norm_scale=conditioned(E), types=types, qwen=qwen is True,
-                                           gelu=qwen == "gelu")
-    layer.gelu = qwen == "gelu"
+                                           gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma")
+    layer.gelu = qwen in ("gelu", "gemma")
     x = np.random.default_rng(n_tok).standard_normal((n_tok, E)).astype(np.float32)
     og, oa = oracle_fns(layer, keep, orc, kc, vc, pos0, n_tok)
     gg, ga = gpu_fns(gpu, layer, kc, vc, pos0, n_tok)
@@ -156,7 +165,7 @@ def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, type
     e = rel(got, want)
     print(f"  layer vs oracle: {e:.2e} (tokens {min(rel(got[t], want[t]) for t in range(n_tok)):.1e} .. "
           f"{max(rel(got[t], want[t]) for t in range(n_tok)):.1e})", flush=True)
-    assert e <= TOL_LAYER
+    assert e <= (TOL_LAYER_SANDWICH if qwen == "gemma" else TOL_LAYER)
     # the chunk's K/V rows: the GPU chain's rows exactly, the oracle's within its quantization step
     pb = layer.cache.pos_bytes
     kd, vd = layer.cache.k.cpu().numpy(), layer.cache.v.cpu().numpy()

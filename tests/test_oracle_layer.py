@@ -23,7 +23,8 @@ between the products and RoPE.
 3. Planted mistakes in chain 1 (gate and up swapped, a residual dropped, the
    two norm weights swapped, RoPE on adjacent pairs instead of NeoX halves,
    the new K/V row not written, V read from the K cache, the biases
-   dropped, QK-norm after RoPE, q_norm and k_norm swapped) each move the result
+   dropped, QK-norm after RoPE, q_norm and k_norm swapped, SiLU for GELU,
+   the sandwich norms dropped or swapped) each move the result
    by far more than the bound, so the comparison would catch them.
 4. dqo_layer_prefill on one token at the same position (the CPU batch branch,
    whose products fall back to per-token GEMV semantics below 4 tokens) equals
@@ -46,7 +47,7 @@ def rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, gelu=False):
+def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, gelu=False, sandwich=False):
     from oracle.oracle import LayerArgs
     qd, kvd = n_head * HD, n_kv * HD
     shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
@@ -78,6 +79,12 @@ def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, 
         for nm in ("bq", "bk", "bv", "q_norm", "k_norm"):
             setattr(args, nm, w[nm].ctypes.data)
     args.act_gelu = int(gelu)
+    if sandwich:  # Gemma-style post-norms of the attention and FFN outputs
+        r2 = np.random.default_rng(seed + 200)
+        w["post_attn_norm"] = (0.5 + 0.05 * r2.standard_normal(E)).astype(np.float32)
+        w["post_ffn_norm"] = (0.8 + 0.05 * r2.standard_normal(E)).astype(np.float32)
+        args.post_attn_norm = w["post_attn_norm"].ctypes.data
+        args.post_ffn_norm = w["post_ffn_norm"].ctypes.data
     x = np.random.default_rng(seed + 100).standard_normal(E).astype(np.float32)
     return dict(E=E, n_head=n_head, n_kv=n_kv, F=F, pos=pos, shapes=shapes, w=w, kc=kc, vc=vc, pb=pb, args=args, x=x,
                 gelu=gelu)
@@ -231,6 +238,10 @@ def chain(L, P, mistake=None):
         vc[pos * pb:(pos + 1) * pb] = P.kv_row(v)
     ao = P.attention(q, kc, kc if mistake == "v_from_k" else vc, nh, nkv, pos)
     proj = mm("o", ao)
+    pa, pf = ("post_ffn_norm", "post_attn_norm") if mistake == "post_norms_swapped" else ("post_attn_norm",
+                                                                                          "post_ffn_norm")
+    if "post_attn_norm" in w and mistake != "no_post_norms":  # sandwich norm (:4140-4142)
+        proj = P.rms_norm(proj, w[pa])
     if mistake != "no_attn_residual":
         proj = proj + x
     xn2 = P.rms_norm(proj, w[n2])
@@ -240,6 +251,8 @@ def chain(L, P, mistake=None):
     gelu = L["gelu"] != (mistake == "silu_for_gelu")
     h = P.gelu_mul(gate, up) if gelu else P.silu_mul(gate, up)
     out = mm("down", h)
+    if "post_ffn_norm" in w and mistake != "no_post_norms":  # sandwich norm (:4245-4247)
+        out = P.rms_norm(out, w[pf])
     if mistake != "no_ffn_residual":
         out = out + proj
     return out, kc, vc
@@ -262,12 +275,15 @@ SHAPES = [
     pytest.param(4096, 32, 8, 14336, 4096, (0.25 / 64, 0.3 / 64), True, id="config4-pos4096-qwen"),
     # gated GELU FFN (geglu_inplace / gelu_tanh)
     pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), "gelu", id="E512-pos70-gelu"),
+    # Gemma-style: gated GELU and sandwich norms
+    pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), "gemma", id="E512-pos70-gemma"),
 ]
 
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns, qwen):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos, norm_scale=ns, qwen=qwen is True, gelu=qwen == "gelu")
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos, norm_scale=ns, qwen=qwen is True,
+             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma")
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, OraclePieces(orc))
     e = rel(got, want)
@@ -279,7 +295,8 @@ def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns, qwen):
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv, F, pos, ns, qwen):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 1, norm_scale=ns, qwen=qwen is True, gelu=qwen == "gelu")
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 1, norm_scale=ns, qwen=qwen is True,
+             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma")
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, IndependentPieces(ref))
     e = rel(got, want)
@@ -295,7 +312,8 @@ def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv,
 
 
 MISTAKES = ["gate_up_swapped", "no_attn_residual", "no_ffn_residual", "norms_swapped", "rope_adjacent",
-            "no_kv_write", "v_from_k", "no_bias", "qk_norm_after_rope", "qk_norms_swapped", "silu_for_gelu"]
+            "no_kv_write", "v_from_k", "no_bias", "qk_norm_after_rope", "qk_norms_swapped", "silu_for_gelu",
+            "no_post_norms", "post_norms_swapped"]
 
 
 @pytest.mark.parametrize("mistake", MISTAKES)
@@ -305,7 +323,7 @@ def test_planted_mistakes_fail(orc, mistake):
     by distinct scales so that swapping them matters). The layer carries
     Q/K/V biases and QK-norm, so the mistakes in those are covered too."""
     L = make(orc, 512, 8, 2, 1536, 70, seed=77, norm_scale=(0.25 / np.sqrt(512), 0.6 / np.sqrt(512)), qwen=True,
-             gelu=mistake == "silu_for_gelu")
+             gelu=mistake == "silu_for_gelu", sandwich=mistake in ("no_post_norms", "post_norms_swapped"))
     got = layer(orc, L)[0]
     ok = chain(L, OraclePieces(orc))[0]
     assert rel(got, ok) <= 1e-6
@@ -317,7 +335,8 @@ def test_planted_mistakes_fail(orc, mistake):
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_prefill_one_token_equals_decode(orc, E, n_head, n_kv, F, pos, ns, qwen):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 2, norm_scale=ns, qwen=qwen is True, gelu=qwen == "gelu")
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 2, norm_scale=ns, qwen=qwen is True,
+             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma")
     dec, dkc, dvc = layer(orc, L)
     kc, vc = L["kc"].copy(), L["vc"].copy()
     pre = orc.layer_prefill(L["args"], kc, vc, pos, L["x"][None, :])[0]

@@ -18,6 +18,11 @@ must exceed the worst perturbed deviation by a margin:
     norm-wise, single tokens up to ~0.35; TOL_LAYER = 1.5e-2 covers the worst
     of the trials 1.5x over (the GPU measures 1.6e-5 .. 6.7e-3 on the same
     cases);
+  * Qwen-style (biases, QK-norm) and gated-GELU layers move like the plain
+    one; with sandwich norms up to ~1.2e-2: TOL_LAYER_SANDWICH = 2e-2;
+  * the engine test's Qwen-style layer (test_layer_forward_batch_qwen) moves
+    up to ~1.0e-2, with GELU and sandwich norms ~1.5e-2: TOL_QWEN_BATCH =
+    2.5e-2;
   * two-layer model: prefill of 24 tokens, head, two decode steps: the logits
     move by up to ~2e-2, so TOL_LOGITS = 3e-2 stays (the GPU measures ~1e-2:
     its up/gate products are 10x closer than 4e-4)."""
@@ -51,20 +56,24 @@ def perturbed(gemm, delta, rng):
     return pg
 
 
-LAYER_CASES = [  # test_layer_prefill_vs_oracle's cases and the number of noise draws
-    ((4096, 32, 8, 14336, 1000, 16, None), 1),
-    ((512, 8, 2, 1536, 0, 40, None), 3),
-    ((512, 4, 2, 1024, 70, 130, None), 3),
-    ((512, 8, 2, 1536, 30, 48, tlp.Q80_ALL), 3),
-    ((512, 8, 2, 1536, 10, 40, tlp.Q40_FFN), 3),
+LAYER_CASES = [  # test_layer_prefill_vs_oracle's cases, the number of noise draws, the variant
+    ((4096, 32, 8, 14336, 1000, 16, None), 1, None),
+    ((512, 8, 2, 1536, 0, 40, None), 3, None),
+    ((512, 4, 2, 1024, 70, 130, None), 3, None),
+    ((512, 8, 2, 1536, 30, 48, tlp.Q80_ALL), 3, None),
+    ((512, 8, 2, 1536, 10, 40, tlp.Q40_FFN), 3, None),
+    ((512, 8, 2, 1536, 20, 40, None), 3, "qwen"),
+    ((512, 8, 2, 1536, 20, 40, None), 3, "gelu"),
+    ((512, 8, 2, 1536, 20, 40, None), 4, "gemma"),
 ]
 
 
-@pytest.mark.parametrize("case,draws", LAYER_CASES)
-def test_layer_prefill_product_sensitivity(orc, case, draws):
+@pytest.mark.parametrize("case,draws,kind", LAYER_CASES)
+def test_layer_prefill_product_sensitivity(orc, case, draws, kind):
     E, n_head, n_kv, F, pos0, n_tok, types_ = case
     h = tl.HostLayer(orc, E, n_head, n_kv, F, pos0 + n_tok + 2, pos0, seed=E + pos0 + n_tok,
-                     norm_scale=tlp.conditioned(E), types=types_)
+                     norm_scale=tlp.conditioned(E), types=types_, qwen=kind == "qwen",
+                     gelu=kind in ("gelu", "gemma"), sandwich=kind == "gemma")
     x = np.random.default_rng(n_tok).standard_normal((n_tok, E)).astype(np.float32)
     og, oa = tlp.oracle_fns(h, h.keep, orc, h.kc, h.vc, pos0, n_tok)
     want = orc.layer_prefill(h.args, h.kc.copy(), h.vc.copy(), pos0, x)
@@ -77,7 +86,52 @@ def test_layer_prefill_product_sensitivity(orc, case, draws):
         print(f"  products +{DELTA:.0e}: layer moves {e:.2e} (x{e / DELTA:.1f}), tokens {min(tok):.1e} .. "
               f"{max(tok):.1e}", flush=True)
         worst = max(worst, e)
-    assert 1.5 * worst <= tlp.TOL_LAYER
+    assert 1.5 * worst <= (tlp.TOL_LAYER_SANDWICH if kind == "gemma" else tlp.TOL_LAYER)
+
+
+@pytest.mark.parametrize("gelu,sandwich", [(False, False), (True, False), (True, True)])
+def test_engine_batch_layer_product_sensitivity(orc, gelu, sandwich):
+    """test_gpu_engine.py::test_layer_forward_batch_qwen's layer rebuilt on the
+    host from the same seeds (Q4_K_M weights, Q/K/V biases and QK-norm,
+    optionally GELU and sandwich norms; 40 tokens after 20 cached positions):
+    the oracle's move under 4e-4 product errors, which TOL_QWEN_BATCH covers
+    1.5x over."""
+    from oracle.oracle import LayerArgs
+    import test_gpu_engine as te
+    E, n_head, n_kv, F, n_ctx, prior, T, hd = 512, 8, 2, 1024, 64, 20, 40, 128
+    kc, vc, pb = te.prior_cache(orc, 1, n_ctx, n_kv, hd, prior, seed=91)
+    tys = (synth.Q4_K, synth.Q4_K, synth.Q6_K, synth.Q4_K, synth.Q4_K, synth.Q4_K, synth.Q6_K)
+    names = ("q", "k", "v", "o", "gate", "up", "down")
+    qd, kvd = n_head * hd, n_kv * hd
+    shapes = {"q": (qd, E), "k": (kvd, E), "v": (kvd, E), "o": (E, qd), "gate": (F, E), "up": (F, E), "down": (E, F)}
+    keep = {nm: np.ascontiguousarray(synth.gen_weights(tys[i], *shapes[nm], 92 + i)) for i, nm in enumerate(names)}
+    rng = np.random.default_rng(92)
+    keep["attn_norm"] = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32) * np.float32(0.25 / np.sqrt(E))
+    keep["ffn_norm"] = (1 + 0.02 * rng.standard_normal(E)).astype(np.float32) * np.float32(0.3 / np.sqrt(E))
+    oa = LayerArgs(E, n_head, n_kv, hd, F, 1e-5, 500000.0, *tys)
+    for nm in names:
+        setattr(oa, "w" + nm, keep[nm].ctypes.data)
+    oa.attn_norm, oa.ffn_norm = keep["attn_norm"].ctypes.data, keep["ffn_norm"].ctypes.data
+    keep.update(te.qwen_extras(oa, n_head, n_kv, 93))
+    oa.act_gelu = int(gelu)
+    if sandwich:
+        keep["post_attn_norm"] = (0.5 + 0.05 * np.random.default_rng(95).standard_normal(E)).astype(np.float32)
+        keep["post_ffn_norm"] = (0.8 + 0.05 * np.random.default_rng(96).standard_normal(E)).astype(np.float32)
+        oa.post_attn_norm, oa.post_ffn_norm = keep["post_attn_norm"].ctypes.data, keep["post_ffn_norm"].ctypes.data
+    x = np.random.default_rng(94).standard_normal((T, E)).astype(np.float32)
+    spec = types.SimpleNamespace(n_head=n_head, n_head_kv=n_kv, gelu=gelu, cache=types.SimpleNamespace(pos_bytes=pb),
+                                 mats={nm: types.SimpleNamespace(fmt=synth.FMT_OF_TYPE[tys[i]], rows=shapes[nm][0],
+                                                                 cols=shapes[nm][1]) for i, nm in enumerate(names)})
+    want = orc.layer_prefill(oa, kc.copy(), vc.copy(), prior, x)
+    og, oattn = tlp.oracle_fns(spec, keep, orc, kc, vc, prior, T)
+    assert rel(tlp.chain(spec, keep, orc, x, prior, og, oattn)["out"], want) <= 1e-6
+    worst = 0.0
+    for d in range(3):
+        e = rel(tlp.chain(spec, keep, orc, x, prior, perturbed(og, DELTA, np.random.default_rng(100 + d)), oattn)["out"],
+                want)
+        print(f"  products +{DELTA:.0e}: layer moves {e:.2e}", flush=True)
+        worst = max(worst, e)
+    assert 1.5 * worst <= te.TOL_QWEN_BATCH
 
 
 def test_model_logits_product_sensitivity(orc):
