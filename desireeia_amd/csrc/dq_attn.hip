@@ -18,18 +18,23 @@
 //
 // Arithmetic (reference models/dense_forward.cpp:3956-4065, kv/kv_quant.cpp):
 // score = (sum over blocks of d * sum(q_k * q)) / sqrt(hd) with the query in
-// fp32; softmax; out = sum_p w_p * d_p * q_v. The sums run in fp32 in another
-// order than the reference's (the reference sums the softmax denominator in
-// double); results agree to ~1e-6 relative.
+// fp32; softmax; out = sum_p w_p * d_p * q_v. Both products run on the matrix
+// cores with the fp32 factors split into fp16 hi + lo parts (~22 significant
+// bits; the int8 factors are exact) and fp32 sums in another order than the
+// reference's (which sums the softmax denominator in double); results agree
+// to ~1e-6 relative over any range of K / V scales.
 #include <cstdlib>
 #include <mutex>
 
 #include "dq_common.h"
+#include "dq_f16.h"
 
 namespace {
 
 constexpr int TP = 64;         // positions per tile
 constexpr int NT = 256;        // threads per workgroup
+
+typedef float f4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int read_pos(int pos_host, const int* pos_dev, int n_ctx) {
     int p = pos_dev ? *pos_dev : pos_host;
@@ -79,17 +84,33 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const float* __restrict__
 }
 
 // ------------------------------------------------------------ attention --
-// One workgroup per (KV head, tile of TP positions): it stages the tile's K
-// and V rows through LDS, computes the scores of the HPK query heads that
-// share the KV head (GQA: each KV byte is read once for all of them), the
-// tile softmax and weighted V sum, and writes a partial record (acc[HD],
-// tile max, tile sum) for attn_merge_kernel.
+// One workgroup per (KV head, tile of TP positions): the tile's K and V rows
+// go straight into LDS (dword DMA), and the HPK query heads that share the KV
+// head (GQA: each KV byte is read once for all of them) are scored, the tile
+// softmax taken and the weighted V sum formed on the matrix cores; the
+// workgroup writes a partial record (acc[HD], tile max, tile sum) per head
+// for attn_merge_kernel.
+//
+// Both products run as v_mfma_f32_16x16x32_f16 with exact operands:
+//  * scores, per (16 positions, Q8_0 block b): A = the query's 32 values of
+//    block b (rows = heads), B = the 32 K bytes of each position (int8 values
+//    are exact in fp16); the fp32 result is scaled by the position's block
+//    scale dk and summed over the blocks, as the reference's
+//    sum_b dk * sum(q * k8);
+//  * weighted sum, per (32 positions, 16 dims of block b): A = the weight
+//    w[h][p] * dv[p][b] (rows = heads), B = the V bytes, read position-major.
+// The fp32 A operands are split into fp16 hi + lo parts (hi*B + lo*B: ~22
+// significant bits), after scaling by a power of two that puts the largest
+// value of the head (query) or block (weights) in [2^13, 2^14): no fp16
+// overflow, full precision for the values that matter, and the scaling is
+// undone exactly afterwards.
 //
 // FUSE: q, k, v are the raw projections of the new token: every workgroup
-// applies RoPE to its query heads, and the workgroup of the last tile (the
-// one holding `pos`) also rotates k, quantizes the new K and V rows of its KV
-// head (kv_quantize_row), writes them into the cache and uses them directly.
-// This replaces the separate RoPE + KV-write kernel of the decoder layer.
+// applies the optional bias / QK-norm and RoPE to its query heads, and the
+// workgroup of the last tile (the one holding `pos`) also processes k and v,
+// quantizes the new K and V rows of its KV head (kv_quantize_row), writes
+// them into the cache and uses them directly. This replaces the separate
+// RoPE + KV-write kernel of the decoder layer.
 //
 // XCD-aware placement: consecutive workgroups go to different XCDs; the KV
 // heads of one tile share an XCD, so the 1088-byte position rows they split
@@ -113,31 +134,71 @@ struct AttnArgs {
     DqQkvPost post;       // FUSE: optional biases and QK-norm before RoPE
 };
 
+// 8 int8 values (two dwords) -> 8 fp16, exactly: the fp16 of bits
+// 0x64 | (b ^ 0x80) is 1024 + b + 128.
+__device__ __forceinline__ h8 i8x8_to_h8(uint32_t w0, uint32_t w1) {
+    const h2 c = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t t0 = w0 ^ 0x80808080u, t1 = w1 ^ 0x80808080u;
+    const h2 r0 = magic_pair(t0, 0x04010400u) - c, r1 = magic_pair(t0, 0x04030402u) - c;
+    const h2 r2 = magic_pair(t1, 0x04010400u) - c, r3 = magic_pair(t1, 0x04030402u) - c;
+    const dq_u32x4 w = {__builtin_bit_cast(uint32_t, r0), __builtin_bit_cast(uint32_t, r1),
+                        __builtin_bit_cast(uint32_t, r2), __builtin_bit_cast(uint32_t, r3)};
+    return __builtin_bit_cast(h8, w);
+}
+
+// 8 int8 values held as bytes (zero-extended, one per word) -> 8 fp16.
+__device__ __forceinline__ h8 i8_bytes_to_h8(const uint32_t (&u)[8]) {
+    const h2 c = {(_Float16)1152.0f, (_Float16)1152.0f};
+    dq_u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w[i] = __builtin_bit_cast(uint32_t,
+                                  __builtin_bit_cast(h2, (u[2 * i] | (u[2 * i + 1] << 16)) ^ 0x64806480u) - c);
+    return __builtin_bit_cast(h8, w);
+}
+
+__device__ __forceinline__ void split_hl(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
+// Exponent shift that brings a largest magnitude m into [2^13, 2^14) (0 for
+// m == 0 or not finite).
+__device__ __forceinline__ int pow2_shift(float m, int cap) {
+    if (!(m > 0.0f) || !(m <= 3.0e38f)) return 0;
+    int e = 0;
+    (void)frexpf(m, &e);
+    return min(14 - e, cap);
+}
+
 template <int HD, int HPK, bool FUSE>
 __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
-    constexpr int NB = HD / 32;          // Q8_0 blocks per row
-    constexpr int RB = NB * DQ_SZ_Q8_0;  // row bytes
-    constexpr int RBW = RB / 4;          // row dwords
+    constexpr int NB = HD / 32;            // Q8_0 blocks per row
+    constexpr int RB = NB * DQ_SZ_Q8_0;    // row bytes
     constexpr int NW = NT / 64;
-    constexpr int DP = HD / 2;           // dim pairs (V phase)
-    constexpr int PG = NT / DP;          // position groups (V phase)
-    constexpr int PPG = TP / PG;         // positions per group
-    constexpr int RBQ = RB / 8;          // row 8-byte words (rows are 8-byte aligned)
-    constexpr int STAGE_IT = (TP * RBQ + NT - 1) / NT;
-    constexpr int REC = HD + 4;     // acc[HD], max, sum, 2 pad (16-byte records)
-    static_assert(HD == 128 && RB % 8 == 0 && NT % DP == 0 && TP % PG == 0, "shape");
+    constexpr int GPW = TP / 16 / NW;      // 16-position groups per wave
+    constexpr int KS = TP / 32;            // 32-position steps of the V product
+    constexpr int RBW = RB / 4;            // row dwords
+    constexpr int NDMA = TP * RBW / 64;    // dword-DMA instructions per tensor
+    constexpr int DPW = (NDMA + NW - 1) / NW;
+    constexpr int QROW = HD + 8;           // fp16 row of the query operands (padded)
+    constexpr int REC = HD + 4;            // acc[HD], max, sum, 2 pad (16-byte records)
+    constexpr int HPW = (HPK + NW - 1) / NW;
+    static_assert(HD == 128 && NB == NW && HPK <= 8 && TP % 64 == 0 && RB == 136, "shape");
 
-    __shared__ uint64_t ks8[TP * RBQ];
-    __shared__ uint64_t vs8[TP * RBQ];
-    uint32_t* ks = reinterpret_cast<uint32_t*>(ks8);
-    uint32_t* vs = reinterpret_cast<uint32_t*>(vs8);
-    __shared__ float qt[HD][HPK];        // query, transposed
-    __shared__ float qsum[NB][HPK];      // per-block sums of the query
-    __shared__ float sp[NB][HPK][TP];    // per-block partial scores
-    __shared__ float pw[TP][HPK];        // tile weights exp(s - m)
-    __shared__ float red[PG][HPK][HD];   // V-phase cross-group reduction
+    __shared__ __align__(16) uint32_t kt[TP * RBW];     // K rows of the tile (136 bytes each)
+    __shared__ __align__(16) uint32_t vt[TP * RBW];     // V rows
+    __shared__ __align__(16) _Float16 qhs[16 * QROW];   // scaled query, fp16 hi (rows >= HPK zero)
+    __shared__ __align__(16) _Float16 qls[16 * QROW];   // and lo
+    __shared__ __align__(16) float dvf[NB][TP];         // V block scales times dvs (0 past the tile)
+    __shared__ __align__(16) float ew[16][TP];          // tile weights exp(s - m) (rows >= HPK zero)
+    __shared__ uint32_t nrow[2][RB / 4];                // FUSE: the new K and V rows
+    __shared__ float qsc[HPK];                          // per head: 1/sqrt(hd) / query scale
+    __shared__ float dvs[NB];                           // per block: weight operand scale
+    __shared__ float wmx[NW][HPK], wsm[NW][HPK];        // per-wave maxima and sums
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n16 = lane & 15, g4 = lane >> 4;
     const int n_xcd = 8;
     const int xcd = blockIdx.x % n_xcd, slot = blockIdx.x / n_xcd;
     const int kvh = slot % A.n_kv;
@@ -150,187 +211,299 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
     const int nv = min(TP, pos + 1 - p0);
     // the new row (position pos, the last row of the last tile) comes from
     // registers under FUSE
-    const int n_load = (FUSE && tile == n_tiles - 1) ? nv - 1 : nv;
+    const bool new_row = FUSE && tile == n_tiles - 1;
+    const int n_load = new_row ? nv - 1 : nv;
 
-    // ---- query values of this wave's heads (FUSE: wave w takes heads w,
-    // w+NW) and the new row's RoPE pair, loaded before the tile so that
-    // waiting for them leaves the tile's loads in flight
-    constexpr int HPW = (HPK + NW - 1) / NW;
-    float ql[HPW], qhv[HPW], rc = 1.0f, rs = 0.0f;
-    if constexpr (FUSE) {
+    // ---- raw inputs of this wave's query heads (wave w takes heads w, w+NW)
+    // and, under FUSE, their bias, QK-norm weights and RoPE pair, and the new
+    // K (wave 0) / V (wave 1) row: loaded before the tile, so that waiting
+    // for them leaves the tile's loads in flight
+    float qa[HPW], qb[HPW], ba[HPW], bb[HPW];
+    float rc = 1.0f, rs = 0.0f, na = 0.0f, nb = 0.0f;
+    float xa = 0.0f, xb = 0.0f, xba = 0.0f, xbb = 0.0f, xna = 0.0f, xnb = 0.0f;
 #pragma unroll
-        for (int t = 0; t < HPW; ++t) {
-            const int h = min(wave + NW * t, HPK - 1);
-            const float* qh = A.q + (size_t)(kvh * HPK + h) * HD;
-            ql[t] = qh[lane];
-            qhv[t] = qh[lane + 64];
+    for (int t = 0; t < HPW; ++t) {
+        const size_t hq = (size_t)kvh * HPK + min(wave + NW * t, HPK - 1);
+        qa[t] = A.q[hq * HD + lane];
+        qb[t] = A.q[hq * HD + lane + 64];
+        ba[t] = bb[t] = 0.0f;
+        if constexpr (FUSE) {
+            if (A.post.bq) {
+                ba[t] = A.post.bq[hq * HD + lane];
+                bb[t] = A.post.bq[hq * HD + lane + 64];
+            }
         }
+    }
+    if constexpr (FUSE) {
         if (A.rope) {
             rc = A.rope[2 * lane];
             rs = A.rope[2 * lane + 1];
         }
+        if (A.post.q_norm) {
+            na = A.post.q_norm[lane];
+            nb = A.post.q_norm[lane + 64];
+        }
+        if (new_row && wave < 2) {  // wave-uniform
+            const size_t o = (size_t)kvh * HD + lane;
+            xa = (wave == 0 ? A.k : A.v)[o];
+            xb = (wave == 0 ? A.k : A.v)[o + 64];
+            const float* bias = wave == 0 ? A.post.bk : A.post.bv;
+            if (bias) {
+                xba = bias[o];
+                xbb = bias[o + 64];
+            }
+            if (wave == 0 && A.post.k_norm) {
+                xna = A.post.k_norm[lane];
+                xnb = A.post.k_norm[lane + 64];
+            }
+        }
     }
-    // ---- K / V rows of the tile (8 bytes per load): issued next, staged after the query
-    uint64_t kr[STAGE_IT], vr[STAGE_IT];
+    // ---- the tile's K and V rows, straight into LDS (lane i of a dword DMA
+    // writes dword i of the instruction's 64-dword span, row r of the tile at
+    // byte 136 r: each instruction reads two rows' worth of consecutive
+    // dwords). Every wave issues the same count (spare slots repeat the last
+    // span), and rows at or past n_load read a row of the tile instead: rows
+    // >= nv are never used, and the new row is written over afterwards.
     {
         const uint8_t* kb = A.kc + (size_t)p0 * A.pos_bytes + (size_t)kvh * RB;
         const uint8_t* vb = A.vc + (size_t)p0 * A.pos_bytes + (size_t)kvh * RB;
-        // unconditional loads (addresses clamped into the tile's first rows,
-        // which exist: p0 <= pos < n_ctx) so that all of them are in flight
-        // together; the values of slots past the tile are never staged
         const int rmax = n_load > 0 ? n_load - 1 : 0;
 #pragma unroll
-        for (int it = 0; it < STAGE_IT; ++it) {
-            const int i = min(tid + it * NT, TP * RBQ - 1);
-            const int r = min(i / RBQ, rmax), c = i % RBQ;
-            kr[it] = *reinterpret_cast<const uint64_t*>(kb + (size_t)r * A.pos_bytes + 8 * c);
-            vr[it] = *reinterpret_cast<const uint64_t*>(vb + (size_t)r * A.pos_bytes + 8 * c);
+        for (int i = 0; i < DPW; ++i) {
+            const int j = min(wave + NW * i, NDMA - 1);
+            const int d = 64 * j + lane;
+            const int r = d / RBW, c = d - r * RBW;
+            const uint32_t go = (uint32_t)min(r, rmax) * (uint32_t)A.pos_bytes + 4u * (uint32_t)c;
+            __builtin_amdgcn_global_load_lds(kb + go, DQ_LDS_PTR(kt + 64 * j), 4, 0, 0);
+            __builtin_amdgcn_global_load_lds(vb + go, DQ_LDS_PTR(vt + 64 * j), 4, 0, 0);
         }
     }
-    // ---- query of the HPK heads (rotated under FUSE: wave w takes heads w, w+NW)
-    if constexpr (FUSE) {
-#pragma unroll
-        for (int t = 0; t < HPW; ++t) {
-            const int h = wave + NW * t;
-            if (h < HPK) {  // wave-uniform
-                float a = ql[t], b = qhv[t];
-                dq_qkv_post(a, b, 0, kvh * HPK + h, lane, A.post);
-                // NeoX rotation of the pair (j, j + 64) (dq_rope_pair)
-                qt[lane][h] = A.rope ? a * rc - b * rs : a;
-                qt[lane + 64][h] = A.rope ? a * rs + b * rc : b;
-            }
-        }
-    } else {
-        for (int i = tid; i < HPK * HD; i += NT) qt[i % HD][i / HD] = A.q[(size_t)(kvh * HPK + i / HD) * HD + i % HD];
-    }
-    // rows >= n_load are not staged: the new row (FUSE) is written there by
-    // waves 0 and 1 below, and rows >= nv are never read (their scores are
-    // masked, the V sum stops at nv)
-#pragma unroll
-    for (int it = 0; it < STAGE_IT; ++it) {
-        const int i = tid + it * NT;
-        if (i < TP * RBQ && i / RBQ < n_load) {
-            ks8[i] = kr[it];
-            vs8[i] = vr[it];
-        }
-    }
-    if constexpr (FUSE) {
-        if (tile == n_tiles - 1 && wave < 2) {
-            // the new row of this KV head: wave 0 = K (rotated), wave 1 = V
-            const float* src = (wave == 0 ? A.k : A.v) + (size_t)kvh * HD;
-            float lo = src[lane], hi = src[lane + 64];
-            dq_qkv_post(lo, hi, wave == 0 ? 1 : 2, kvh, lane, A.post);
-            if (wave == 0 && A.rope) dq_rope_pair(lo, hi, A.rope, lane);
-            uint8_t* lrow = reinterpret_cast<uint8_t*>(wave == 0 ? ks : vs) + (nv - 1) * RB;
-            dq_q8_0_row128(lo, hi, lane, lrow);
-            uint8_t* grow = (wave == 0 ? A.kc : A.vc) + (size_t)pos * A.pos_bytes + (size_t)kvh * RB;
-            dq_q8_0_row128(lo, hi, lane, grow);
-        }
-    }
-    __syncthreads();
-    if (tid < NB * HPK) {
-        const int b = tid / HPK, h = tid % HPK;
-        float a = 0.0f;
-        for (int i = 0; i < 32; ++i) a += qt[32 * b + i][h];
-        qsum[b][h] = a;
-    }
-    __syncthreads();
-    // ---- partial scores: wave w takes blocks w, w+NW, ...; lane = position
-    for (int b = wave; b < NB; b += NW) {
-        const int p = lane;
-        const uint32_t* row = ks + p * RBW;
-        const int o = b * DQ_SZ_Q8_0;  // byte offset of the block in the row
-        const int w0 = o >> 2;
-        uint32_t dw[9];
-#pragma unroll
-        for (int i = 0; i < 9; ++i) dw[i] = row[w0 + i];
-        float dk;
-        uint32_t qw[8];
-        if ((o & 3) == 0) {
-            dk = dq_h2f((uint16_t)(dw[0] & 0xFFFF));
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qw[i] = __builtin_amdgcn_alignbyte(dw[i + 1], dw[i], 2);
-        } else {
-            dk = dq_h2f((uint16_t)(dw[0] >> 16));
-#pragma unroll
-            for (int i = 0; i < 8; ++i) qw[i] = dw[i + 1];
-        }
-        // bytes biased to unsigned (q + 128): one conversion per value, the
-        // bias removed with the query's block sum
-        float a[HPK];
-#pragma unroll
-        for (int h = 0; h < HPK; ++h) a[h] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t u = qw[i] ^ 0x80808080u;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float fv = (float)((u >> (8 * k)) & 0xFF);
-                const int dim = 32 * b + 4 * i + k;
-#pragma unroll
-                for (int h = 0; h < HPK; ++h) a[h] = fmaf(fv, qt[dim][h], a[h]);
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < HPK; ++h) sp[b][h][p] = dk * fmaf(-128.0f, qsum[b][h], a[h]);
-    }
-    __syncthreads();
-    // ---- tile softmax: wave w takes heads w, w+NW; lane = position
-    float* rec = A.part + ((size_t)kvh * A.max_tiles + tile) * HPK * REC;
-    for (int h = wave; h < HPK; h += NW) {
-        const int p = lane;
-        float sc = -INFINITY;
-        if (p < nv) {
-            float a = 0.0f;
-#pragma unroll
-            for (int b = 0; b < NB; ++b) a += sp[b][h][p];
-            sc = a * A.scale;
-        }
-        const float m = dq_wave_max(sc);
-        const float e = p < nv ? __expf(sc - m) : 0.0f;
-        const float l = dq_wave_sum(e);
-        pw[p][h] = e;
-        if (lane == 0) {
-            rec[h * REC + HD] = m;
-            rec[h * REC + HD + 1] = l;
-        }
-    }
-    __syncthreads();
-    // ---- weighted V sum: thread = (dim pair, position group)
+    // ---- zero rows HPK..15 of the query and weight operands (the MFMA rows
+    // that no head fills)
     {
-        const int dp = tid % DP, pg = tid / DP;
-        const int vblk = (2 * dp) / 32;
-        const int voff = vblk * DQ_SZ_Q8_0 + 2 + 2 * (dp % 16);
-        float acc[HPK][2];
-#pragma unroll
-        for (int h = 0; h < HPK; ++h) acc[h][0] = acc[h][1] = 0.0f;
-        const uint8_t* vbytes = reinterpret_cast<const uint8_t*>(vs);
-        const int pend = min(nv, (pg + 1) * PPG);
-        for (int p = pg * PPG; p < pend; ++p) {
-            const uint8_t* row = vbytes + p * RB;
-            const uint16_t vv = *reinterpret_cast<const uint16_t*>(row + voff);
-            const float dv = dq_h2f(*reinterpret_cast<const uint16_t*>(row + vblk * DQ_SZ_Q8_0));
-            const float f0 = (float)(int8_t)(vv & 0xFF), f1 = (float)(int8_t)(vv >> 8);
-#pragma unroll
-            for (int h = 0; h < HPK; ++h) {
-                const float wd = pw[p][h] * dv;
-                acc[h][0] = fmaf(wd, f0, acc[h][0]);
-                acc[h][1] = fmaf(wd, f1, acc[h][1]);
-            }
+        constexpr int QZ = (16 - HPK) * QROW * 2 / 16, EZ = (16 - HPK) * TP * 4 / 16;
+        const uint4 z = {0u, 0u, 0u, 0u};
+        for (int i = tid; i < QZ; i += NT) {
+            reinterpret_cast<uint4*>(qhs + HPK * QROW)[i] = z;
+            reinterpret_cast<uint4*>(qls + HPK * QROW)[i] = z;
         }
+        for (int i = tid; i < EZ; i += NT) reinterpret_cast<uint4*>(&ew[HPK][0])[i] = z;
+    }
+    // ---- query operands: bias, QK-norm, RoPE (FUSE), then the head's
+    // power-of-two scale and the fp16 hi / lo split
 #pragma unroll
-        for (int h = 0; h < HPK; ++h) {
-            red[pg][h][2 * dp] = acc[h][0];
-            red[pg][h][2 * dp + 1] = acc[h][1];
+    for (int t = 0; t < HPW; ++t) {
+        const int h = wave + NW * t;
+        if (h < HPK) {  // wave-uniform
+            float a = qa[t], b = qb[t];
+            if constexpr (FUSE) {
+                if (A.post.bq) {
+                    a += ba[t];
+                    b += bb[t];
+                }
+                if (A.post.q_norm) dq_head_rms_norm_w(a, b, na, nb, A.post.eps);
+                if (A.rope) {  // NeoX rotation of the pair (j, j + 64) (dq_rope_pair)
+                    const float x = a, y = b;
+                    a = x * rc - y * rs;
+                    b = x * rs + y * rc;
+                }
+            }
+            const int sh = pow2_shift(dq_wave_max_uniform(fmaxf(fabsf(a), fabsf(b))), 100);
+            const float s = ldexpf(1.0f, sh);
+            split_hl(a * s, qhs[h * QROW + lane], qls[h * QROW + lane]);
+            split_hl(b * s, qhs[h * QROW + lane + 64], qls[h * QROW + lane + 64]);
+            if (lane == 0) qsc[h] = A.scale * ldexpf(1.0f, -sh);
+        }
+    }
+    // ---- new K / V row (FUSE, last tile): bias, K-norm and RoPE of k,
+    // kv_quantize_row into the cache and into nrow (copied into the tile once
+    // the DMAs have landed)
+    if constexpr (FUSE) {
+        if (new_row && wave < 2) {
+            const float* bias = wave == 0 ? A.post.bk : A.post.bv;
+            if (bias) {
+                xa += xba;
+                xb += xbb;
+            }
+            if (wave == 0 && A.post.k_norm) dq_head_rms_norm_w(xa, xb, xna, xnb, A.post.eps);
+            if (wave == 0 && A.rope) {
+                const float x = xa, y = xb;
+                xa = x * rc - y * rs;
+                xb = x * rs + y * rc;
+            }
+            uint8_t* grow = (wave == 0 ? A.kc : A.vc) + (size_t)pos * A.pos_bytes + (size_t)kvh * RB;
+            dq_q8_0_row128(xa, xb, lane, grow);
+            dq_q8_0_row128(xa, xb, lane, reinterpret_cast<uint8_t*>(nrow[wave]));
+        }
+    }
+    __syncthreads();  // every wave's DMAs have landed; query operands in LDS
+    if constexpr (FUSE) {
+        if (new_row) {  // workgroup-uniform
+            if (wave < 2 && lane < RBW) (wave == 0 ? kt : vt)[(nv - 1) * RBW + lane] = nrow[wave][lane];
+            __syncthreads();
+        }
+    }
+    const uint8_t* kb8 = reinterpret_cast<const uint8_t*>(kt);
+    const uint8_t* vb8 = reinterpret_cast<const uint8_t*>(vt);
+
+    // ---- scores: lane (n16, g4) of group gi holds rows 4*g4 + r (heads) of
+    // column n16 (position 16*(wave + NW*gi) + n16)
+    float sc[GPW][4];
+    {
+        h8 qah[NB], qal[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            qah[b] = *reinterpret_cast<const h8*>(qhs + n16 * QROW + 32 * b + 8 * g4);
+            qal[b] = *reinterpret_cast<const h8*>(qls + n16 * QROW + 32 * b + 8 * g4);
+        }
+        float hs[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) hs[r] = 4 * g4 + r < HPK ? qsc[4 * g4 + r] : 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
+            const int p = 16 * (wave + NW * gi) + n16;
+            // the row's dwords from 2*g4 on (+ the block's first dword)
+            const uint32_t* kl = kt + p * RBW + 2 * g4;
+            const uint8_t* kr = kb8 + p * RB;
+            float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                // quants of block b at row bytes 34b + 2 + 8 g4 ...: dword
+                // aligned for odd b, two bytes in for even b
+                const int cb = (DQ_SZ_Q8_0 * b + 2) >> 2;
+                uint32_t w0, w1;
+                if (b & 1) {
+                    w0 = kl[cb];
+                    w1 = kl[cb + 1];
+                } else {
+                    const uint32_t d0 = kl[cb], d1 = kl[cb + 1], d2 = kl[cb + 2];
+                    w0 = __builtin_amdgcn_alignbyte(d1, d0, 2);
+                    w1 = __builtin_amdgcn_alignbyte(d2, d1, 2);
+                }
+                const h8 kv = i8x8_to_h8(w0, w1);
+                f4v c = {0.0f, 0.0f, 0.0f, 0.0f};
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qah[b], kv, c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_f16(qal[b], kv, c, 0, 0, 0);
+                // the block scale: row bytes 34b, 34b + 1
+                const float dk = dq_h2f(*reinterpret_cast<const uint16_t*>(kr + DQ_SZ_Q8_0 * b));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s4[r] = fmaf(dk, c[r], s4[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[gi][r] = (4 * g4 + r < HPK && p < nv) ? s4[r] * hs[r] : -INFINITY;
+        }
+    }
+    // V block scales of block `wave` and their power-of-two operand scale
+    {
+        const int b = wave;
+        float dv[TP / 64];
+        float m = 0.0f;
+#pragma unroll
+        for (int i = 0; i < TP / 64; ++i) {
+            const int p = lane + 64 * i;
+            dv[i] = p < nv ? dq_h2f(*reinterpret_cast<const uint16_t*>(vb8 + p * RB + DQ_SZ_Q8_0 * b)) : 0.0f;
+            m = fmaxf(m, fabsf(dv[i]));
+        }
+        // dvf holds dv * s (a power of two: exact); the records divide by s
+        const float s = ldexpf(1.0f, pow2_shift(dq_wave_max_uniform(m), 100));
+#pragma unroll
+        for (int i = 0; i < TP / 64; ++i) dvf[b][lane + 64 * i] = dv[i] * s;
+        if (lane == 0) dvs[b] = s;
+    }
+    // ---- tile softmax: per-wave maxima, then the tile's
+    {
+        float mx[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            mx[r] = sc[0][r];
+#pragma unroll
+            for (int gi = 1; gi < GPW; ++gi) mx[r] = fmaxf(mx[r], sc[gi][r]);
+            mx[r] = dq_row16_max(mx[r]);
+            if (n16 == 0 && 4 * g4 + r < HPK) wmx[wave][4 * g4 + r] = mx[r];
         }
     }
     __syncthreads();
-    for (int i = tid; i < HPK * HD; i += NT) {
-        const int h = i / HD, dd = i % HD;
-        float a = 0.0f;
+    float ls[4];
 #pragma unroll
-        for (int g = 0; g < PG; ++g) a += red[g][h][dd];
-        rec[h * REC + dd] = a;
+    for (int r = 0; r < 4; ++r) {
+        const int h = 4 * g4 + r;
+        float m = -INFINITY;
+        if (h < HPK) {
+#pragma unroll
+            for (int w = 0; w < NW; ++w) m = fmaxf(m, wmx[w][h]);
+        }
+        ls[r] = 0.0f;
+#pragma unroll
+        for (int gi = 0; gi < GPW; ++gi) {
+            const int p = 16 * (wave + NW * gi) + n16;
+            const float e = (h < HPK && p < nv) ? __expf(sc[gi][r] - m) : 0.0f;
+            ls[r] += e;
+            if (h < HPK) ew[h][p] = e;
+        }
+        ls[r] = dq_row16_sum(ls[r]);
+        if (n16 == 0 && h < HPK) wsm[wave][h] = ls[r];
+    }
+    __syncthreads();
+    // ---- weighted V sum: wave w takes block w (dims 32w + 16t + n16, t = 0,
+    // 1); lane (n16, g4) of a step takes positions 32 ks + 8 g4 + j
+    float* rec = A.part + ((size_t)kvh * A.max_tiles + tile) * HPK * REC;
+    {
+        const int b = wave;
+        // the lane's V byte (dims 32b + n16 (+16 t)) of position 8 g4 (+ j + 32 ks)
+        const uint8_t* vl = vb8 + 8 * g4 * RB + DQ_SZ_Q8_0 * b + 2 + n16;
+        f4v o0 = {0.0f, 0.0f, 0.0f, 0.0f}, o1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            // A: the weights W[h][p] = ew[h][p] * dv[p][b] (times the block's
+            // power of two, in dvf) split into fp16 hi / lo (rows >= HPK: zero)
+            h8 ah, al;
+            {
+                const int p = 32 * ks + 8 * g4;
+                const float4 e0 = *reinterpret_cast<const float4*>(&ew[n16][p]);
+                const float4 e1 = *reinterpret_cast<const float4*>(&ew[n16][p + 4]);
+                const float4 d0 = *reinterpret_cast<const float4*>(&dvf[b][p]);
+                const float4 d1 = *reinterpret_cast<const float4*>(&dvf[b][p + 4]);
+                const float e[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+                const float d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    _Float16 x, y;
+                    split_hl(e[j] * d[j], x, y);
+                    ah[j] = x;
+                    al[j] = y;
+                }
+            }
+            const uint8_t* col = vl + 32 * ks * RB;
+            uint32_t u0[8], u1[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                u0[j] = col[j * RB];
+                u1[j] = col[j * RB + 16];
+            }
+            const h8 bv0 = i8_bytes_to_h8(u0), bv1 = i8_bytes_to_h8(u1);
+            o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv0, o0, 0, 0, 0);
+            o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv0, o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv1, o1, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv1, o1, 0, 0, 0);
+        }
+        const float inv = 1.0f / dvs[b];  // a power of two: exact
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int h = 4 * g4 + r;
+            if (h < HPK) {
+                rec[h * REC + 32 * b + n16] = o0[r] * inv;
+                rec[h * REC + 32 * b + 16 + n16] = o1[r] * inv;
+            }
+        }
+    }
+    if (tid < HPK) {
+        float m = wmx[0][tid], l = wsm[0][tid];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) m = fmaxf(m, wmx[w][tid]);
+#pragma unroll
+        for (int w = 1; w < NW; ++w) l += wsm[w][tid];
+        rec[tid * REC + HD] = m;
+        rec[tid * REC + HD + 1] = l;
     }
 }
 

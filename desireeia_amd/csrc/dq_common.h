@@ -129,6 +129,10 @@ __device__ __forceinline__ dq_u32x4 dq_ld16_stream(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const dq_u32x4*>(p));
 }
 
+// The LDS address of a pointer into a __shared__ array, as the LDS operand of
+// __builtin_amdgcn_global_load_lds (direct global -> LDS DMA).
+#define DQ_LDS_PTR(p) reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(p))
+
 // DPP move of a float (gfx9 dpp_ctrl encodings; all rows and banks enabled).
 // Workgroup barrier for LDS rings filled by global_load_lds: waits for this
 // wave's LDS reads (lgkmcnt 0; gfx9 s_waitcnt encoding, vmcnt and expcnt at
@@ -158,6 +162,16 @@ __device__ __forceinline__ float dq_row16_sum(float v) {
     return v;
 }
 
+// Maximum of v over each 16-lane row, in every lane of the row (the same
+// DPP steps as dq_row16_sum).
+__device__ __forceinline__ float dq_row16_max(float v) {
+    v = fmaxf(v, dq_dpp<0xB1>(v));
+    v = fmaxf(v, dq_dpp<0x4E>(v));
+    v = fmaxf(v, dq_dpp<0x141>(v));
+    v = fmaxf(v, dq_dpp<0x140>(v));
+    return v;
+}
+
 // Full-wave float sum as a wave-uniform value: the four row sums combined as
 // (row0 + row1) + (row2 + row3).
 __device__ __forceinline__ float dq_wave_sum_uniform(float v) {
@@ -168,6 +182,18 @@ __device__ __forceinline__ float dq_wave_sum_uniform(float v) {
     const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
     const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
     return (r0 + r1) + (r2 + r3);
+}
+
+// Full-wave float maximum as a wave-uniform value (DPP row maxima, then the
+// four rows' by readlane: no LDS round trips).
+__device__ __forceinline__ float dq_wave_max_uniform(float v) {
+    v = dq_row16_max(v);
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 // Full-wave float sum; every lane receives the total.
@@ -187,13 +213,17 @@ __device__ __forceinline__ double dq_wave_sum_f64(double v) {
 // by a wave as (lo, hi) = values (lane, lane + 64): squares in float summed
 // in double, scale = 1/sqrtf((float)(sum/128) + eps), y = x * scale * w. The
 // per-head QK-norm of :3915-3931.
-__device__ __forceinline__ void dq_head_rms_norm(float& lo, float& hi, const float* __restrict__ w, int lane,
-                                                 float eps) {
+// The weights (w_lo, w_hi) = (w[lane], w[lane + 64]) already in registers.
+__device__ __forceinline__ void dq_head_rms_norm_w(float& lo, float& hi, float w_lo, float w_hi, float eps) {
     const float a = lo * lo, b = hi * hi;
     const double s = dq_wave_sum_f64((double)a + (double)b);
     const float scale = 1.0f / sqrtf((float)(s / 128.0) + eps);
-    lo = lo * scale * w[lane];
-    hi = hi * scale * w[lane + 64];
+    lo = lo * scale * w_lo;
+    hi = hi * scale * w_hi;
+}
+__device__ __forceinline__ void dq_head_rms_norm(float& lo, float& hi, const float* __restrict__ w, int lane,
+                                                 float eps) {
+    dq_head_rms_norm_w(lo, hi, w[lane], w[lane + 64], eps);
 }
 
 // The gated FFN activations of the reference (act(gate) * up):

@@ -101,7 +101,6 @@ template <int SB>
 __device__ __forceinline__ int swz(int n) { return SB == 4 ? ((n >> 1) ^ (n >> 3)) & 3 : ((n >> 2) ^ (n >> 3)) & 1; }
 __device__ __forceinline__ int aswz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-#define DQ_LDS_PTR(p) reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(p))
 template <int SIZE>
 __device__ __forceinline__ void lds_dma(const void* g, uint8_t* lds_wave_base);
 template <>

@@ -343,7 +343,6 @@ __device__ __forceinline__ int a_offset(int st, int t, int kk, int h) {
     return 256 * st + 64 * t + 32 * (kk >> 1) + 16 * h + 8 * (kk & 1);
 }
 
-#define DQ_LDS_PTR(p) reinterpret_cast<__attribute__((address_space(3))) void*>(reinterpret_cast<uintptr_t>(p))
 
 // s_waitcnt vmcnt(N), other counters untouched (gfx9 encoding: vmcnt in bits
 // 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).

@@ -218,6 +218,42 @@ def test_attention_rope_kv_fused(gpu, orc, n_head, n_kv, pos, rope, quant):
         assert np.array_equal(act.isum.cpu().numpy(), wi)
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_attention_wide_value_range(gpu, orc, fused):
+    """Large query, key and value magnitudes (scores in the tens of thousands,
+    one dominant position; the new row's V block scale ~1000x the others):
+    the weight operand scale is the maximum over every row of the tile, so no
+    fp16 operand overflows. Output finite and within 1e-3 of the oracle."""
+    n_head, n_kv, pos = 8, 2, 70
+    print(f"wide range fused={fused}", flush=True)
+    n_ctx = pos + 2
+    rng = np.random.default_rng(pos)
+    kc, vc = (orc.kv_quantize_row(rng.standard_normal(pos * n_kv * HD).astype(np.float32)) for _ in range(2))
+    cache = device_cache(gpu, kc, vc, n_ctx, n_kv)
+    q = (300 * rng.standard_normal(n_head * HD)).astype(np.float32)
+    k = (200 * rng.standard_normal(n_kv * HD)).astype(np.float32)
+    v = (1000 * rng.standard_normal(n_kv * HD)).astype(np.float32)
+    dq, dk, dv = (torch.from_numpy(a).to(gpu) for a in (q, k, v))
+    out = torch.empty(n_head * HD, dtype=torch.float32, device=gpu)
+    work = ops.attn_workspace(n_head, n_kv, HD, n_ctx, gpu)
+    if fused:
+        lib = _lib.load()
+        _lib.check(lib.dq_attn_rope_kv_decode(ops._ptr(dq), ops._ptr(dk), ops._ptr(dv), None, HD, ops._ptr(cache.k),
+                                              ops._ptr(cache.v), n_head, n_kv, HD, 0, pos, None, n_ctx, ops._ptr(out),
+                                              None, None, None, ops._ptr(work), work.numel(), ops._stream()),
+                   "dq_attn_rope_kv_decode")
+    else:
+        cache.write(dk, dv, pos)
+        ops.attention_decode(dq, cache, n_head, pos, out=out, work=work)
+    torch.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.isfinite(o).all()
+    want = orc.attn_decode(q, cache.k.cpu().numpy(), cache.v.cpu().numpy(), n_head, n_kv, HD, 0, pos)
+    e = rel(o, want)
+    print(f"  rel err {e:.3e}", flush=True)
+    assert e <= TOL
+
+
 def test_attention_workspace_reuse(gpu, orc):
     """One workspace through calls of every size class (one tile, a partial
     last tile, tile boundaries, a long context, back to short): each output
