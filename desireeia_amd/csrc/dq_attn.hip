@@ -593,6 +593,10 @@ __global__ __launch_bounds__(MNT) void attn_merge_kernel(AttnArgs A) {
             Lt = fmaf(w, gl[q][hb], Lt);
         }
         v = acc / Lt;
+        if (A.post.gate) {  // per-head output gate (dense_forward.cpp:4102-4114)
+            const float g = 1.0f / (1.0f + expf(-A.post.gate[blockIdx.x * HPB + hb]));
+            v *= g;
+        }
         A.out[(size_t)blockIdx.x * MNO + tid] = v;
     }
     if (!A.oq) return;  // uniform
@@ -779,6 +783,15 @@ int dq_attn_rope_kv_decode(const float* d_q, const float* d_k, const float* d_v,
 }
 
 }  // extern "C"
+
+int dq_attn_decode_q8_post(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head,
+                           uint32_t n_head_kv, uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos,
+                           uint32_t n_ctx, float* d_out, int8_t* d_oq, float* d_oscale, int32_t* d_oisum,
+                           void* d_work, size_t work_bytes, const DqQkvPost& post, void* stream) {
+    if (d_oq && (!d_oscale || !d_oisum)) return DQ_ERR_INVALID_ARG;
+    return attn_run(d_q, nullptr, nullptr, nullptr, d_kc, d_vc, n_head, n_head_kv, hd, cc_start, pos, d_pos, n_ctx,
+                    d_out, d_work, work_bytes, d_oq, d_oscale, d_oisum, stream, post);
+}
 
 int dq_attn_rope_kv_decode_post(const float* d_q, const float* d_k, const float* d_v, const float* d_rope,
                                 uint32_t n_rot, void* d_kc, void* d_vc, uint32_t n_head, uint32_t n_head_kv,

@@ -269,6 +269,10 @@ __device__ __forceinline__ float dq_ffn_act(float g) {
 struct DqQkvPost {
     const float *bq, *bk, *bv, *q_norm, *k_norm;
     float eps;
+    // optional per-head output gate values g_h (device, one per query head):
+    // the attention output of head h is scaled by 1 / (1 + exp(-g_h))
+    // (dense_forward.cpp:4102-4114)
+    const float* gate;
 };
 // kind 0: query head, 1: key head, 2: value head
 __device__ __forceinline__ void dq_qkv_post(float& lo, float& hi, int kind, int head, int lane, const DqQkvPost& P) {
@@ -349,12 +353,18 @@ static inline bool dq_zero_span_ok(const float* p, size_t n) {
 }
 // Library-internal forms of the fused decode attention, the RoPE + K/V-row
 // write of one token and of a prompt chunk, with the optional Q/K/V biases
-// and per-head QK-norm applied first (the public entry points pass none).
+// and per-head QK-norm applied first and the optional per-head output gate
+// applied to the attention output (the public entry points pass none); and
+// of the plain decode attention with the output gate.
 int dq_attn_rope_kv_decode_post(const float* d_q, const float* d_k, const float* d_v, const float* d_rope,
                                 uint32_t n_rot, void* d_kc, void* d_vc, uint32_t n_head, uint32_t n_head_kv,
                                 uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos, uint32_t n_ctx,
                                 float* d_out, int8_t* d_oq, float* d_oscale, int32_t* d_oisum, void* d_work,
                                 size_t work_bytes, const DqQkvPost& post, void* stream);
+int dq_attn_decode_q8_post(const float* d_q, const void* d_kc, const void* d_vc, uint32_t n_head,
+                           uint32_t n_head_kv, uint32_t hd, uint32_t cc_start, uint32_t pos, const int32_t* d_pos,
+                           uint32_t n_ctx, float* d_out, int8_t* d_oq, float* d_oscale, int32_t* d_oisum,
+                           void* d_work, size_t work_bytes, const DqQkvPost& post, void* stream);
 int dq_rope_kv_write_post(float* d_q, const float* d_k, const float* d_v, const float* d_rope, uint32_t n_head,
                           uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
                           const int32_t* d_pos, uint32_t n_ctx, const DqQkvPost& post, void* stream);
@@ -364,7 +374,7 @@ int dq_rope_kv_write_batch_post(float* d_q, const float* d_k, const float* d_v, 
                                 uint32_t n_ctx, const DqQkvPost& post, void* stream);
 // The layer's post-processing from its descriptor.
 static inline DqQkvPost dq_layer_post(const dq_layer_t* L) {
-    return DqQkvPost{L->bq, L->bk, L->bv, L->q_norm, L->k_norm, L->rms_eps};
+    return DqQkvPost{L->bq, L->bk, L->bv, L->q_norm, L->k_norm, L->rms_eps, nullptr};
 }
 // act(gate) * up of the decode layer (gelu 1: geglu_inplace, else silu), then
 // the per-256 quantizer (dq_act_quant) or in float (dq_act_mul).

@@ -54,6 +54,8 @@ struct Engine {
     DevBuf lx[2];        // layer chain x ping-pong
     int cur = 0;         // lx[cur] holds the current x
     DevBuf rope;         // RoPE table of the current token
+    DevBuf rope_all;     // per-layer slots: the RoPE tables of every layer
+    size_t rope_all_n = 0;  // floats of rope_all uploaded (0: none)
     bool rope_on = false;
     uint8_t* kc = nullptr;
     uint8_t* vc = nullptr;
@@ -398,10 +400,11 @@ void cuda_free_device(void* p) {
 void cuda_backend_shutdown(void) {
     if (g.stream) (void)hipStreamSynchronize(g.stream);
     drop_graphs();
-    for (DevBuf* b : {&g.xbuf, &g.ybuf, &g.act, &g.work, &g.stage, &g.lx[0], &g.lx[1], &g.rope, &g.px, &g.prope[0],
-                      &g.prope[1], &g.prope[2], &g.prope[3], &g.pwork, &g.pnorm, &g.pio, &g.hlog, &g.hwork, &g.htk,
-                      &g.hnorm, &g.hcand})
+    for (DevBuf* b : {&g.xbuf, &g.ybuf, &g.act, &g.work, &g.stage, &g.lx[0], &g.lx[1], &g.rope, &g.rope_all, &g.px,
+                      &g.prope[0], &g.prope[1], &g.prope[2], &g.prope[3], &g.pwork, &g.pnorm, &g.pio, &g.hlog,
+                      &g.hwork, &g.htk, &g.hnorm, &g.hcand})
         release(*b);
+    g.rope_all_n = 0;
     g.mirror.clear();
     g.hnorm_host.clear();
     if (g.tok_stream) (void)hipStreamSynchronize(g.tok_stream);
@@ -788,11 +791,17 @@ static LayerExtras extras_of(const float* bq, const float* bk, const float* bv, 
 
 int cuda_layer_forward(const CudaLayerArgs* A) {
     if (!A || !g.kc) return DQ_ERR_NOT_SUPPORTED;
-    // features outside the dense layer with optional Q/K/V biases, per-head
-    // QK-norm, a SiLU or GELU gated FFN and sandwich norms (an attention
-    // gate, per-layer slots): the engine's CPU path runs them
-    if (A->wag_qs || A->dyn_all || A->rope_all) return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
+    // per-layer slots (models whose layers differ in window or RoPE base,
+    // dense_forward.cpp:3760-3788): the (pos, cc_start) pairs [n_slots][2]
+    // and RoPE tables [n_slots][rope_stride] of every layer; this layer reads
+    // slot layer_slot (backend_cuda.cu:4330-4366). The tables go to the
+    // device with the first layer of a token (upload_x); the pair is read
+    // from the host array every layer passes.
+    const bool slots = A->dyn_all && A->layer_slot < A->n_slots;
+    if (slots && A->rope_cache && (!A->rope_all || A->rope_stride < A->n_rot)) return DQ_ERR_INVALID_ARG;
+    const uint32_t pos = slots ? A->dyn_all[2 * (size_t)A->layer_slot] : A->pos;
+    const uint32_t cc_start = slots ? A->dyn_all[2 * (size_t)A->layer_slot + 1] : A->cc_start;
     if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
         A->heads_per_kv != A->n_head / A->n_head_kv)
         return DQ_ERR_NOT_SUPPORTED;
@@ -817,19 +826,20 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     L.ffn_norm = A->ffn_norm_w;
     L.post_attn_norm = A->post_attn_norm_w;  // (their presence sizes the workspace)
     L.post_ffn_norm = A->post_ffn_norm_w;
+    L.wag = A->wag_qs, L.fmt_ag = A->fmt_ag;  // optional per-head attention output gate
     // every matrix must be one of ours, of the declared format and shape
-    const void* w[7] = {L.wq, L.wk, L.wv, L.wo, L.wgate, L.wup, L.wdown};
-    const int f[7] = {L.fmt_q, L.fmt_k, L.fmt_v, L.fmt_o, L.fmt_gate, L.fmt_up, L.fmt_down};
-    const size_t r[7] = {A->q_dim, A->kv_dim, A->kv_dim, A->n_embd, A->n_ff, A->n_ff, A->n_embd};
-    const size_t c[7] = {A->n_embd, A->n_embd, A->n_embd, A->q_dim, A->n_embd, A->n_embd, A->n_ff};
-    for (int j = 0; j < 7; ++j) {
+    const void* w[8] = {L.wq, L.wk, L.wv, L.wo, L.wgate, L.wup, L.wdown, L.wag};
+    const int f[8] = {L.fmt_q, L.fmt_k, L.fmt_v, L.fmt_o, L.fmt_gate, L.fmt_up, L.fmt_down, L.fmt_ag};
+    const size_t r[8] = {A->q_dim, A->kv_dim, A->kv_dim, A->n_embd, A->n_ff, A->n_ff, A->n_embd, A->n_head};
+    const size_t c[8] = {A->n_embd, A->n_embd, A->n_embd, A->q_dim, A->n_embd, A->n_embd, A->n_ff, A->n_embd};
+    for (int j = 0; j < (L.wag ? 8 : 7); ++j) {
         const WInfo* wi = lookup(w[j]);
         if (!wi || wi->base != w[j] || wi->fmt != f[j] || wi->rows != r[j] || wi->cols != c[j])
             return DQ_ERR_NOT_SUPPORTED;
     }
     const size_t pb = kv_pos_bytes(A->n_head_kv, A->head_dim);
     const uint32_t n_ctx = kv_positions(A->kv_layer_off, pb);
-    if (A->pos >= n_ctx || A->cc_start > A->pos) return DQ_ERR_NOT_SUPPORTED;
+    if (pos >= n_ctx || cc_start > pos) return DQ_ERR_NOT_SUPPORTED;
     size_t wbytes = 0;
     if (dq_layer_workspace_bytes(&L, n_ctx, &wbytes) != DQ_OK) return DQ_ERR_NOT_SUPPORTED;
     // x_from_token: x is the Q8_0 embedding row of the token the previous
@@ -863,9 +873,25 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
         return io_fail();
     L.attn_norm = an;
     L.ffn_norm = fn;
-    if (A->upload_dyn || !g.rope.p) {
-        const int rc = upload_rope(A->rope_cache, A->n_rot);
-        if (rc != DQ_OK) return rc;
+    const float* d_rope = nullptr;
+    if (slots) {
+        if (A->rope_cache) {
+            const size_t nr = (size_t)A->n_slots * A->rope_stride;
+            if (A->upload_x || g.rope_all_n != nr) {
+                g.rope_all_n = 0;
+                if (!reserve(g.rope_all, nr * 4)) return DQ_ERR_IO;
+                if (hipMemcpyAsync(g.rope_all.p, A->rope_all, nr * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+                    return io_fail();
+                g.rope_all_n = nr;
+            }
+            d_rope = (const float*)g.rope_all.p + (size_t)A->layer_slot * A->rope_stride;
+        }
+    } else {
+        if (A->upload_dyn || !g.rope.p) {
+            const int rc = upload_rope(A->rope_cache, A->n_rot);
+            if (rc != DQ_OK) return rc;
+        }
+        d_rope = g.rope_on ? (const float*)g.rope.p : nullptr;
     }
     if (A->upload_x) {
         g.cur = 0;
@@ -878,9 +904,8 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     }
     float* xin = (float*)g.lx[g.cur].p;
     float* xout = (float*)g.lx[g.cur ^ 1].p;
-    const int rc = dq_layer_decode(&L, xin, xout, g.rope_on ? (const float*)g.rope.p : nullptr, A->pos, nullptr,
-                                   A->cc_start, g.kc + A->kv_layer_off, g.vc + A->kv_layer_off, n_ctx, g.work.p,
-                                   norm_off, s);
+    const int rc = dq_layer_decode(&L, xin, xout, d_rope, pos, nullptr, cc_start, g.kc + A->kv_layer_off,
+                                   g.vc + A->kv_layer_off, n_ctx, g.work.p, norm_off, s);
     if (rc != DQ_OK) return rc == DQ_ERR_IO ? io_fail() : rc;
     g.cur ^= 1;
     if (A->download_x) {
@@ -926,10 +951,6 @@ int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, 
 
 int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     if (!A || !g.kc || A->n_tok == 0 || A->n_total == 0) return DQ_ERR_NOT_SUPPORTED;
-    // features outside the dense layer with optional Q/K/V biases, per-head
-    // QK-norm, a SiLU or GELU gated FFN and sandwich norms (an attention
-    // gate, per-layer slots): the engine's CPU path runs them
-    if (A->wag_qs) return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
     if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
         A->heads_per_kv != A->n_head / A->n_head_kv)
@@ -954,11 +975,12 @@ int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     L.fmt_gate = A->fmt_gate, L.fmt_up = A->fmt_up, L.fmt_down = A->fmt_down;
     L.wq = A->wq_qs, L.wk = A->wk_qs, L.wv = A->wv_qs, L.wo = A->wo_qs;
     L.wgate = A->wgate_qs, L.wup = A->wup_qs, L.wdown = A->wdown_qs;
-    const void* w[7] = {L.wq, L.wk, L.wv, L.wo, L.wgate, L.wup, L.wdown};
-    const int f[7] = {L.fmt_q, L.fmt_k, L.fmt_v, L.fmt_o, L.fmt_gate, L.fmt_up, L.fmt_down};
-    const size_t r[7] = {A->q_dim, A->kv_dim, A->kv_dim, A->n_embd, A->n_ff, A->n_ff, A->n_embd};
-    const size_t c[7] = {A->n_embd, A->n_embd, A->n_embd, A->q_dim, A->n_embd, A->n_embd, A->n_ff};
-    for (int j = 0; j < 7; ++j) {
+    L.wag = A->wag_qs, L.fmt_ag = A->fmt_ag;  // optional per-head attention output gate
+    const void* w[8] = {L.wq, L.wk, L.wv, L.wo, L.wgate, L.wup, L.wdown, L.wag};
+    const int f[8] = {L.fmt_q, L.fmt_k, L.fmt_v, L.fmt_o, L.fmt_gate, L.fmt_up, L.fmt_down, L.fmt_ag};
+    const size_t r[8] = {A->q_dim, A->kv_dim, A->kv_dim, A->n_embd, A->n_ff, A->n_ff, A->n_embd, A->n_head};
+    const size_t c[8] = {A->n_embd, A->n_embd, A->n_embd, A->q_dim, A->n_embd, A->n_embd, A->n_ff, A->n_embd};
+    for (int j = 0; j < (L.wag ? 8 : 7); ++j) {
         const WInfo* wi = lookup(w[j]);
         if (!wi || wi->base != w[j] || wi->fmt != f[j] || wi->rows != r[j] || wi->cols != c[j])
             return DQ_ERR_NOT_SUPPORTED;

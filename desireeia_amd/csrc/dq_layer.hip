@@ -264,6 +264,7 @@ struct LayerWs {
     float* yn;     // float input of the per-32 quantizer
     float *q, *k, *v, *ao, *x2, *up, *gate;
     float* tmp;  // sandwich norms: a projection before its norm
+    float* ag;   // attention gate: the per-head gate values
     void* attn;
     size_t attn_bytes, total;
 };
@@ -280,7 +281,7 @@ bool layer_ok(const dq_layer_t* L) {
     const int f[7] = {L->fmt_q, L->fmt_k, L->fmt_v, L->fmt_o, L->fmt_gate, L->fmt_up, L->fmt_down};
     for (int i = 0; i < 7; ++i)
         if (!layer_fmt(f[i])) return false;
-    return true;
+    return !L->wag || layer_fmt(L->fmt_ag);
 }
 
 LayerWs carve(const dq_layer_t* L, uint32_t n_ctx, uint8_t* base) {
@@ -309,6 +310,7 @@ LayerWs carve(const dq_layer_t* L, uint32_t n_ctx, uint8_t* base) {
     w.up = (float*)take(F * 4);
     w.gate = (float*)take(F * 4);
     w.tmp = (float*)take(L->post_attn_norm || L->post_ffn_norm ? E * 4 : 0);
+    w.ag = (float*)take(L->wag ? (size_t)L->n_head * 4 : 0);
     size_t ab = 0;
     dq_attn_workspace_bytes(L->n_head, L->n_head_kv, L->head_dim, n_ctx, &ab);
     w.attn = take(ab);
@@ -458,17 +460,21 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
         return DQ_OK;
     };
     // ---- attention block
-    DQ_TRY(norm_acts(d_x, L->attn_norm, per32(L->fmt_q) || per32(L->fmt_k) || per32(L->fmt_v)));
+    DQ_TRY(norm_acts(d_x, L->attn_norm,
+                     per32(L->fmt_q) || per32(L->fmt_k) || per32(L->fmt_v) || (L->wag && per32(L->fmt_ag))));
     {
-        const dq_gemv_job_t jobs[3] = {{L->fmt_q, L->wq, QD, w.q, nullptr},
+        // the attention gate's matrix reads the same normalised input (:4108)
+        const dq_gemv_job_t jobs[4] = {{L->fmt_q, L->wq, QD, w.q, nullptr},
                                        {L->fmt_k, L->wk, KVD, w.k, nullptr},
-                                       {L->fmt_v, L->wv, KVD, w.v, nullptr}};
-        DQ_TRY(run_group(jobs, 3, E));
+                                       {L->fmt_v, L->wv, KVD, w.v, nullptr},
+                                       {L->fmt_ag, L->wag, L->n_head, w.ag, nullptr}};
+        DQ_TRY(run_group(jobs, L->wag ? 4 : 3, E));
     }
     // the optional biases and QK-norm, RoPE, the new K/V rows and attention in
     // one launch when the rotation covers the whole head (else the separate
     // post + RoPE + KV-write kernel first)
-    const DqQkvPost post = dq_layer_post(L);
+    DqQkvPost post = dq_layer_post(L);
+    post.gate = L->wag ? w.ag : nullptr;
     const bool fused = !d_rope || L->n_rot == L->head_dim;
     if (!fused)
         DQ_TRY(dq_rope_kv_write_post(w.q, w.k, w.v, d_rope, L->n_head, L->n_head_kv, L->head_dim, L->n_rot, d_kc,
@@ -480,12 +486,9 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
         DQ_TRY(dq_attn_rope_kv_decode_post(w.q, w.k, w.v, d_rope, L->n_rot, d_kc, d_vc, L->n_head, L->n_head_kv,
                                            L->head_dim, cc_start, pos, d_pos, n_ctx, w.ao, oq, w.as, w.ai, w.attn,
                                            w.attn_bytes, post, stream));
-    else if (q256)
-        DQ_TRY(dq_attn_decode_q8_act(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos,
-                                     n_ctx, w.ao, w.aq, w.as, w.ai, w.attn, w.attn_bytes, stream));
     else
-        DQ_TRY(dq_attn_decode_q8(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos, n_ctx,
-                                 w.ao, w.attn, w.attn_bytes, stream));
+        DQ_TRY(dq_attn_decode_q8_post(w.q, d_kc, d_vc, L->n_head, L->n_head_kv, L->head_dim, cc_start, pos, d_pos,
+                                      n_ctx, w.ao, oq, w.as, w.ai, w.attn, w.attn_bytes, post, stream));
     // the output projection plus the residual (x2 = x + Wo a), or with a
     // sandwich norm x2 = x + rms_norm(Wo a, post_attn_norm) (:4140-4147)
     auto residual = [&](int fmt, const void* wm, size_t rows, size_t cols, const int8_t* xq, const float* xs,

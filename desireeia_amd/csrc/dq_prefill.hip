@@ -527,6 +527,22 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
 }
 
 // out = a + b (the FFN residual, models/dense_forward.cpp:3616-3624), 4 per lane.
+// The per-head attention output gate of a prompt chunk (DenseQuirks::attn_gate,
+// models/dense_forward.cpp:3527-3536): row t, head h of the attention output
+// [n_tok][q_dim] times 1 / (1 + exp(-g[t][h])). One workgroup per (token,
+// head), a float4 of the head per thread.
+__global__ __launch_bounds__(64) void attn_gate_rows_kernel(float* __restrict__ a, const float* __restrict__ g,
+                                                             int n_head, int hd, size_t q_dim) {
+    const int t = blockIdx.x / n_head, h = blockIdx.x % n_head;
+    const float gv = 1.0f / (1.0f + expf(-g[(size_t)t * n_head + h]));
+    float* row = a + (size_t)t * q_dim + (size_t)h * hd;
+    for (int i = 4 * threadIdx.x; i < hd; i += 256) {
+        float4 v = *reinterpret_cast<float4*>(row + i);
+        v.x *= gv, v.y *= gv, v.z *= gv, v.w *= gv;
+        *reinterpret_cast<float4*>(row + i) = v;
+    }
+}
+
 __global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a, const float* __restrict__ b, size_t n4,
                                                  float* __restrict__ out) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -554,6 +570,7 @@ __global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float* __restr
 // GEMM activation workspace per K-quant format (sized for the widest input).
 struct PrefillWs {
     float *xn, *q, *k, *v, *attn, *h, *gate, *up, *down;
+    float* ag;       // attention gate values [n_tok][n_head]
     uint8_t* gw[3];  // activation layouts: Q4_K, Q6_K, natural order (Q8_0 / Q4_0)
     uint8_t* aw;     // attention key-split records
     size_t gw_bytes, aw_bytes, total;
@@ -566,6 +583,9 @@ bool prefill_layer_ok(const dq_layer_t* L) {
     if (L->head_dim != 128 || L->n_head_kv == 0 || L->n_head % L->n_head_kv) return false;
     if (L->n_embd % 256 || L->n_ff % 256 || ((size_t)L->n_head * L->head_dim) % 256) return false;
     if (L->n_rot == 0 || L->n_rot > L->head_dim || L->n_rot % 2) return false;
+    if (L->wag && L->fmt_ag != DQ_FMT_Q4_K && L->fmt_ag != DQ_FMT_Q6_K && L->fmt_ag != DQ_FMT_Q8_0 &&
+        L->fmt_ag != DQ_FMT_Q4_0)
+        return false;
     return true;
 }
 
@@ -588,6 +608,7 @@ PrefillWs prefill_carve(const dq_layer_t* L, uint32_t n_tok, uint8_t* base) {
     w.gate = take(T * F);
     w.up = take(T * F);
     w.down = take(T * E);
+    w.ag = take(L->wag ? T * L->n_head : 0);
     size_t gb = 0;
     const size_t cols[3] = {E, QD, F};
     const int fmts[3] = {DQ_FMT_Q4_K, DQ_FMT_Q6_K, DQ_FMT_Q8_0};
@@ -796,20 +817,20 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
     // Q8_0 and Q4_0 the same natural order
     auto cls = [](int fmt) { return fmt == DQ_FMT_Q4_K ? 0 : (fmt == DQ_FMT_Q6_K ? 1 : 2); };
     auto gw = [&](int fmt) { return w.gw[cls(fmt)]; };
-    // products of one input x [T][cols] with up to three matrices: one
+    // products of one input x [T][cols] with up to four matrices: one
     // activation quantization per distinct format
     auto products = [&](const float* x, size_t cols, int n, const int* fmt, const void* const* wm, const size_t* rows,
                         float* const* y) -> int {
         // the quantizer of a format class also clears the outputs its
         // K-split products add their partials into
-        bool done[3] = {false, false, false}, zeroed[3] = {false, false, false};
+        bool done[3] = {false, false, false}, zeroed[4] = {false, false, false, false};
         for (int j = 0; j < n; ++j) {
             const int fi = cls(fmt[j]);
             if (!done[fi]) {
                 DqZeroSpans z{};
                 int k = 0;
                 for (int i = j; i < n; ++i) {
-                    if (cls(fmt[i]) != fi || !dq_gemm_adds_into_y(fmt[i], rows[i], cols, T) ||
+                    if (k == DqZeroSpans::N || cls(fmt[i]) != fi || !dq_gemm_adds_into_y(fmt[i], rows[i], cols, T) ||
                         !dq_zero_span_ok(y[i], rows[i] * T))
                         continue;
                     z.p[k] = y[i];
@@ -827,16 +848,22 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
     rms_norm_rows_kernel<<<n_tok, 256, 0, s>>>(d_x, nullptr, nullptr, L->attn_norm, (int)E, L->rms_eps, w.xn);
     DQP_TRY(dq_launch_status());
     {
-        const int f[3] = {L->fmt_q, L->fmt_k, L->fmt_v};
-        const void* m[3] = {L->wq, L->wk, L->wv};
-        const size_t r[3] = {QD, KVD, KVD};
-        float* const y[3] = {w.q, w.k, w.v};
-        DQP_TRY(products(w.xn, E, 3, f, m, r, y));
+        // with the attention gate's matrix, which reads the same normalised
+        // input (:3525-3526)
+        const int f[4] = {L->fmt_q, L->fmt_k, L->fmt_v, L->fmt_ag};
+        const void* m[4] = {L->wq, L->wk, L->wv, L->wag};
+        const size_t r[4] = {QD, KVD, KVD, L->n_head};
+        float* const y[4] = {w.q, w.k, w.v, w.ag};
+        DQP_TRY(products(w.xn, E, L->wag ? 4 : 3, f, m, r, y));
     }
     DQP_TRY(dq_rope_kv_write_batch_post(w.q, w.k, w.v, QD, KVD, d_rope, L->n_rot, n_tok, L->n_head, L->n_head_kv,
                                         L->head_dim, d_kc, d_vc, pos0, n_ctx, dq_layer_post(L), stream));
     DQP_TRY(dq_attn_prefill_q8(w.q, d_kc, d_vc, n_tok, L->n_head, L->n_head_kv, L->head_dim, (uint32_t)QD, pos0,
                                n_swa, n_ctx, w.attn, w.aw, w.aw_bytes, stream));
+    if (L->wag) {  // the per-head output gate before the output projection
+        attn_gate_rows_kernel<<<n_tok * L->n_head, 64, 0, s>>>(w.attn, w.ag, (int)L->n_head, (int)L->head_dim, QD);
+        DQP_TRY(dq_launch_status());
+    }
     {
         const int f[1] = {L->fmt_o};
         const void* m[1] = {L->wo};

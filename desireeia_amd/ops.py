@@ -362,7 +362,8 @@ class LayerDesc(ctypes.Structure):
                 ("attn_norm", ctypes.c_void_p), ("ffn_norm", ctypes.c_void_p),
                 ("bq", ctypes.c_void_p), ("bk", ctypes.c_void_p), ("bv", ctypes.c_void_p),
                 ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p), ("act_gelu", ctypes.c_int),
-                ("post_attn_norm", ctypes.c_void_p), ("post_ffn_norm", ctypes.c_void_p)]
+                ("post_attn_norm", ctypes.c_void_p), ("post_ffn_norm", ctypes.c_void_p),
+                ("wag", ctypes.c_void_p), ("fmt_ag", ctypes.c_int)]
 
 
 def rope_cache(n_rot, pos, theta):
@@ -382,11 +383,12 @@ class DecoderLayer:
 
     def __init__(self, mats, attn_norm, ffn_norm, n_head, n_head_kv, head_dim, n_ctx, rms_eps=1e-5,
                  rope_theta=500000.0, n_rot=None, device="cuda", bias=None, qk_norm=None, act_gelu=False,
-                 post_norms=None):
+                 post_norms=None, attn_gate=None):
         """bias: optional (bq, bk, bv) float tensors; qk_norm: optional
         (q_norm, k_norm) [head_dim] weights (Qwen-style layers); act_gelu: a
         gated GELU FFN; post_norms: optional (post_attn_norm, post_ffn_norm)
-        [n_embd] sandwich-norm weights."""
+        [n_embd] sandwich-norm weights; attn_gate: optional QuantMatrix
+        [n_head][n_embd], the per-head attention output gate."""
         self.mats = mats
         self.attn_norm = attn_norm.to(device).float().contiguous()
         self.ffn_norm = ffn_norm.to(device).float().contiguous()
@@ -402,6 +404,9 @@ class DecoderLayer:
         d.attn_norm = self.attn_norm.data_ptr()
         d.ffn_norm = self.ffn_norm.data_ptr()
         d.act_gelu = int(act_gelu)
+        self.attn_gate = attn_gate
+        if attn_gate is not None:
+            d.wag, d.fmt_ag = attn_gate.buf.data_ptr(), attn_gate.fmt
         self.extras = {}
         for names, vals in ((("bq", "bk", "bv"), bias), (("q_norm", "k_norm"), qk_norm),
                             (("post_attn_norm", "post_ffn_norm"), post_norms)):

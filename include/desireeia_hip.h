@@ -277,8 +277,9 @@ int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float
 
 /* One Llama-style decoder layer at batch 1 on the device: the dense branch
  * of models/dense_forward.cpp:3897-4257 with optional Q/K/V biases and
- * per-head QK-norm (Qwen-style layers; no sandwich norms, gated SiLU FFN,
- * Q8_0 KV cache) that cuda_layer_forward (core/engine.h:698-752) runs as one
+ * per-head QK-norm (Qwen-style layers), a gated SiLU or GELU FFN, optional
+ * sandwich norms and attention gate, and a Q8_0 KV cache, that
+ * cuda_layer_forward (core/engine.h:698-752) runs as one
  * captured episode. The biases (bq [n_head*head_dim], bk, bv
  * [n_head_kv*head_dim]) are added to the projections (add_bias,
  * :3904-3908); q_norm / k_norm [head_dim] then normalise every q and k head
@@ -288,7 +289,10 @@ int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float
  * per-element gelu_tanh of the batch branch (:49-51, :3608-3609).
  * post_attn_norm / post_ffn_norm (Gemma-style sandwich norms) normalise the
  * output projection and the FFN output before their residuals (rms_norm_vec,
- * :4140-4142, :4245-4247). Weights are packed
+ * :4140-4142, :4245-4247). wag (DenseQuirks::attn_gate) is a per-head output
+ * gate: its n_head rows times the same normalised input as Q/K/V give g_h,
+ * and head h of the attention output is scaled by 1 / (1 + exp(-g_h)) before
+ * the output projection (:4102-4114; batch :3522-3537). Weights are packed
  * device matrices (dq_weights_pack), each of any of the four formats (Q4_K /
  * Q6_K read the per-256 activation, Q8_0 / Q4_0 the per-32 one, as the
  * reference CPU GEMVs of those formats do); n_embd, n_ff and n_head*head_dim
@@ -306,6 +310,8 @@ typedef struct {
     const float *bq, *bk, *bv, *q_norm, *k_norm;              /* device, optional (NULL) */
     int act_gelu; /* 1: gated GELU FFN (decode: geglu_inplace; prefill: gelu_tanh) */
     const float *post_attn_norm, *post_ffn_norm; /* device [n_embd], optional (NULL): sandwich norms */
+    const void* wag; /* optional (NULL) per-head attention output gate [n_head][n_embd], packed, format fmt_ag */
+    int fmt_ag;
 } dq_layer_t;
 
 int dq_layer_workspace_bytes(const dq_layer_t* layer, uint32_t n_ctx, size_t* bytes);

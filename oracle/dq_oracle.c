@@ -1012,6 +1012,16 @@ static void qkv_post(const dqo_layer_t* L, float* q, float* k, float* v) {
  * gated SiLU FFN, Q8_0 KV. The K-quant matvecs quantize their input per 256
  * (matvec -> matmul_q4_k/q6_k, and quantize_shared_q8k for the shared Q/K/V
  * and gate/up inputs). */
+/* The per-head output gate of one token (DenseQuirks::attn_gate,
+ * models/dense_forward.cpp:4102-4114 and :3527-3536): g = 1 / (1 + exp(-x))
+ * of the head's gate value, times every value of the head's output. */
+void dqo_attn_gate_apply(float* ao, const float* gate, uint32_t n_head, size_t hd) {
+    for (uint32_t h = 0; h < n_head; ++h) {
+        const float g = 1.0f / (1.0f + expf(-gate[h]));
+        for (size_t d = 0; d < hd; ++d) ao[h * hd + d] *= g;
+    }
+}
+
 int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t pos,
                      const float* x, float* x_out, float* q_out, float* k_out,
                      float* v_out, float* attn_out_opt) {
@@ -1046,6 +1056,12 @@ int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t po
         dqo_kv_quantize_row(v + h * hd, hd, vc + (size_t)pos * pos_bytes + h * row_bytes);
     }
     dqo_attn_decode_q8(q, kc, vc, L->n_head, L->n_head_kv, (uint32_t)hd, 0, pos, ao);
+    if (L->wag) { /* :4102-4114: matvec of the same normalized input */
+        float* gv = (float*)malloc(L->n_head * sizeof(float));
+        rc |= dqo_matmul(L->fmt_ag, L->wag, L->n_head, E, attn_in, gv, 0, 0);
+        dqo_attn_gate_apply(ao, gv, L->n_head, hd);
+        free(gv);
+    }
     rc |= dqo_matmul(L->fmt_o, L->wo, E, qd, ao, proj, 0, 0);
     if (L->post_attn_norm) dqo_rms_norm(proj, L->post_attn_norm, proj, E, L->rms_eps); /* :4140-4142 */
     for (size_t i = 0; i < E; ++i) proj[i] += x[i];
@@ -1108,6 +1124,12 @@ int dqo_layer_prefill(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t p
     }
     rc |= dqo_attn_prefill_q8(q, ao, n_tok, L->n_head, L->n_head / L->n_head_kv, (uint32_t)hd, (uint32_t)qd, kc, vc,
                               row_bytes, pos_bytes, pos0, n_swa, 1.0f / sqrtf((float)hd));
+    if (L->wag) { /* :3522-3537: matvec_batch of the normalized inputs, per token */
+        float* gv = (float*)malloc(T * L->n_head * sizeof(float));
+        rc |= dqo_gemm(L->fmt_ag, L->wag, L->n_head, E, xn, T, gv, 0, 0, 0, 0);
+        for (size_t t = 0; t < T; ++t) dqo_attn_gate_apply(ao + t * qd, gv + t * L->n_head, L->n_head, hd);
+        free(gv);
+    }
     rc |= dqo_gemm(L->fmt_o, L->wo, E, qd, ao, T, proj, 0, 0, 0, 0);
     if (L->post_attn_norm) /* :3546-3548 */
         for (size_t t = 0; t < T; ++t) dqo_rms_norm(proj + t * E, L->post_attn_norm, proj + t * E, E, L->rms_eps);

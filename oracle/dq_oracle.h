@@ -137,7 +137,18 @@ typedef struct {
      * projection and of the FFN output, each before its residual
      * (:4140-4142, :4245-4247; batch :3546-3548, :3618-3620) */
     const float *post_attn_norm, *post_ffn_norm;
+    /* optional per-head output gate (NULL = absent; DenseQuirks::attn_gate):
+     * [n_head][n_embd] of format fmt_ag, multiplied with the same normalized
+     * input as Q/K/V; head h of the attention output is scaled by
+     * 1 / (1 + exp(-gate_h)) before the output projection (decode :4102-4114,
+     * batch :3522-3537) */
+    const uint8_t* wag;
+    int fmt_ag;
 } dqo_layer_t;
+
+/* The per-head output gate of one token: head h of ao ([n_head][hd]) times
+ * 1 / (1 + exp(-gate[h])) (dense_forward.cpp:4102-4114). */
+void dqo_attn_gate_apply(float* ao, const float* gate, uint32_t n_head, size_t hd);
 
 int dqo_layer_decode(const dqo_layer_t* L, uint8_t* kc, uint8_t* vc, uint32_t pos,
                      const float* x, float* x_out, float* q_out, float* k_out,

@@ -44,7 +44,7 @@ class LayerArgs(ctypes.Structure):
                 ("wq", c_p), ("wk", c_p), ("wv", c_p), ("wo", c_p), ("wgate", c_p), ("wup", c_p), ("wdown", c_p),
                 ("attn_norm", c_p), ("ffn_norm", c_p),
                 ("bq", c_p), ("bk", c_p), ("bv", c_p), ("q_norm", c_p), ("k_norm", c_p), ("act_gelu", c_int),
-                ("post_attn_norm", c_p), ("post_ffn_norm", c_p)]
+                ("post_attn_norm", c_p), ("post_ffn_norm", c_p), ("wag", c_p), ("fmt_ag", c_int)]
 
 
 class Oracle:
@@ -64,6 +64,7 @@ class Oracle:
         L.dqo_quantize_q8_1.argtypes = [c_p, c_size, c_p, c_p, c_p, c_p]
         L.dqo_quantize_q8k_rep.argtypes = [c_p, c_size, c_p, c_p, c_p]
         L.dqo_kv_quantize_row.argtypes = [c_p, c_size, c_p]
+        L.dqo_attn_gate_apply.argtypes = [c_p, c_p, c_u32, c_size]
         L.dqo_matmul.argtypes = [c_int, c_p, c_size, c_size, c_p, c_p, c_size, c_size]
         L.dqo_matmul_f64.argtypes = [c_int, c_p, c_size, c_size, c_p, c_p, c_size, c_size]
         L.dqo_matmul_pq.argtypes = [c_int, c_p, c_size, c_size, c_p, c_p, c_p, c_p, c_size, c_size]
@@ -147,6 +148,13 @@ class Oracle:
         return out
 
     # -- GEMV / GEMM
+
+    def attn_gate_apply(self, ao, gate, n_head, hd):
+        """Head h of ao times 1 / (1 + expf(-gate[h])) (dqo_attn_gate_apply)."""
+        ao = np.ascontiguousarray(ao, np.float32).copy()
+        gate = np.ascontiguousarray(gate, np.float32)
+        self.L.dqo_attn_gate_apply(ao.ctypes.data, gate.ctypes.data, n_head, hd)
+        return ao
     def matmul(self, qtype, w, rows, cols, x, row0=0, row1=0):
         w = np.ascontiguousarray(w, np.uint8)
         x = np.ascontiguousarray(x, np.float32)

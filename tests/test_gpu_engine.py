@@ -447,13 +447,50 @@ def test_layer_forward_chain(lib, orc):
     e = rel(out_s, want_s)
     print(f"gemma-style layer rel err {e:.3e}", flush=True)
     assert e <= TOL
-    # a feature still outside the layer (an attention gate): NOT_SUPPORTED,
-    # output untouched
+    # a per-head attention output gate (Q8_0 [n_head][n_embd]) at pos + 4
+    L0[3].post_attn_norm = L0[3].post_ffn_norm = None
+    L0[3].act_gelu = 0
+    gm = Mat(lib, Q8_0, n_head, E, 97)
+    L0[3].wag, L0[3].fmt_ag = gm.w.ctypes.data, Q8_0
+    rope4 = orc.rope_cache(128, pos + 4, 500000.0)
+    out_a = np.full(E, np.nan, np.float32)
+    A6 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos + 4, rope4, x, out_a, 1, 1, 1)
+    A6.wag_qs, A6.wag_scale, A6.fmt_ag = gm.qs, gm.sc, gm.fmt
+    assert lib.cuda_layer_forward(ctypes.byref(A6)) == OK
+    want_a = orc.layer_decode(L0[3], k0q, v0q, pos + 4, x)[0]
+    e = rel(out_a, want_a)
+    print(f"gated-attention layer rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    L0[3].wag = None
+    # per-layer slots (dyn_all / rope_all): this layer's (pos, cc_start) and
+    # RoPE table from slot 1 of two; the same output as the plain call with
+    # those values, bit for bit (both write the row at pos + 5)
+    rope_b = orc.rope_cache(128, pos + 5, 10000.0)
+    out_p = np.full(E, np.nan, np.float32)
+    A7 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos + 5, rope_b, x, out_p, 1, 1, 1)
+    A7.cc_start = 40
+    assert lib.cuda_layer_forward(ctypes.byref(A7)) == OK
+    dyn = np.array([pos + 5, 0, pos + 5, 40], np.uint32)
+    rope_all = np.ascontiguousarray(np.stack([orc.rope_cache(128, pos + 5, 500000.0), rope_b]))
+    out_s = np.full(E, np.nan, np.float32)
+    A8 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, 0, rope_b, x, out_s, 1, 1, 0)
+    A8.dyn_all, A8.rope_all, A8.n_slots, A8.rope_stride, A8.layer_slot = dyn.ctypes.data, rope_all.ctypes.data, 2, 128, 1
+    assert lib.cuda_layer_forward(ctypes.byref(A8)) == OK
+    assert np.array_equal(out_s, out_p)
+    # a slot past n_slots: the plain pos / cc_start and RoPE table apply
+    out_n = np.full(E, np.nan, np.float32)
+    A9 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos + 5, rope_b, x, out_n, 1, 1, 1)
+    A9.cc_start = 40
+    A9.dyn_all, A9.rope_all, A9.n_slots, A9.rope_stride, A9.layer_slot = dyn.ctypes.data, rope_all.ctypes.data, 2, 128, 2
+    assert lib.cuda_layer_forward(ctypes.byref(A9)) == OK
+    assert np.array_equal(out_n, out_p)
+    # an attention gate of the wrong shape: NOT_SUPPORTED, output untouched
     keep = out.copy()
     A2 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos, rope, x, out, 1, 1, 1)
-    A2.wag_qs = L0[0]["q"].qs
+    A2.wag_qs, A2.fmt_ag = L0[0]["q"].qs, L0[0]["q"].fmt
     assert lib.cuda_layer_forward(ctypes.byref(A2)) == NOT_SUPPORTED
     assert np.array_equal(out, keep)
+    gm.free()
     for L in (L0, L1):
         for m in L[0].values():
             m.free()
@@ -595,7 +632,7 @@ def test_layer_forward_batch(lib, orc):
     keep = out.copy()
     q8 = make_layer(lib, orc, E, n_head, n_kv, F, (Q8_0,) * 7, 90)
     A = batch_args(*q8[:3], E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, None, None, 1, 1, 1)
-    A.wag_qs = q8[0]["q"].qs  # an attention gate
+    A.wag_qs = q8[0]["q"].qs  # an attention gate of the wrong shape ([q_dim] rows, not [n_head])
     assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == NOT_SUPPORTED
     assert lib.cuda_layer_forward_batch(None) == NOT_SUPPORTED
     assert np.array_equal(out, keep)
@@ -605,8 +642,9 @@ def test_layer_forward_batch(lib, orc):
     lib.cuda_kv_cache_release()
 
 
-@pytest.mark.parametrize("gelu,sandwich", [(False, False), (True, False), (True, True)])
-def test_layer_forward_batch_qwen(lib, orc, gelu, sandwich):
+@pytest.mark.parametrize("gelu,sandwich,gate", [(False, False, False), (True, False, False), (True, True, False),
+                                               (False, False, True)])
+def test_layer_forward_batch_qwen(lib, orc, gelu, sandwich, gate):
     """A Qwen-style layer (Q/K/V biases, per-head QK-norm) over a 40-token
     chunk after 20 cached positions through cuda_layer_forward_batch, against
     the oracle's layer prefill with the same extras (within TOL_QWEN_BATCH,
@@ -626,6 +664,9 @@ def test_layer_forward_batch_qwen(lib, orc, gelu, sandwich):
     pf = (0.8 + 0.05 * np.random.default_rng(96).standard_normal(E)).astype(np.float32)
     if sandwich:
         oa.post_attn_norm, oa.post_ffn_norm = pa.ctypes.data, pf.ctypes.data
+    gm = Mat(lib, Q8_0, n_head, E, 98) if gate else None  # per-head attention output gate
+    if gate:
+        oa.wag, oa.fmt_ag = gm.w.ctypes.data, Q8_0
     x = np.random.default_rng(94).standard_normal((T, E)).astype(np.float32)
     rope = np.stack([orc.rope_cache(hd, prior + i, 500000.0) for i in range(T)])
     out = np.full((T, E), np.nan, np.float32)
@@ -634,6 +675,8 @@ def test_layer_forward_batch_qwen(lib, orc, gelu, sandwich):
     A.act_gelu = int(gelu)
     if sandwich:
         A.post_attn_norm_w, A.post_ffn_norm_w = pa.ctypes.data, pf.ctypes.data
+    if gate:
+        A.wag_qs, A.wag_scale, A.fmt_ag = gm.qs, gm.sc, gm.fmt
     assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == OK
     k1, v1 = kc.copy(), vc.copy()
     want = orc.layer_prefill(oa, k1, v1, prior, x)
@@ -649,7 +692,7 @@ def test_layer_forward_batch_qwen(lib, orc, gelu, sandwich):
         a_ = orc.dequantize_row(Q8_0, d[rows], T * kvd)
         b_ = orc.dequantize_row(Q8_0, h[rows], T * kvd)
         assert rel(a_, b_) <= 2e-2
-    for m in mats.values():
+    for m in list(mats.values()) + ([gm] if gm else []):
         m.free()
     lib.cuda_kv_cache_release()
 

@@ -29,7 +29,7 @@ class HostLayer:
     (n_head, n_head_kv, mats[nm].fmt/rows/cols, cache.pos_bytes)."""
 
     def __init__(self, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None,
-                 qwen=False, gelu=False, sandwich=False):
+                 qwen=False, gelu=False, sandwich=False, attn_gate=False):
         from types import SimpleNamespace as NS
 
         from oracle.oracle import LayerArgs
@@ -40,6 +40,8 @@ class HostLayer:
                   "gate": (Q4K, F, E), "up": (Q4K, F, E), "down": (Q6K, E, F)}
         for nm, qt in (types or {}).items():
             shapes[nm] = (qt,) + shapes[nm][1:]
+        if attn_gate:  # per-head attention output gate [n_head][n_embd], Q8_0
+            shapes["ag"] = (synth.Q8_0, n_head, E)
         self.shapes = shapes
         gg = {nm: (qt, synth.gen_weights(qt, r, c, seed=seed + i)) for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
         rng = np.random.default_rng(seed)
@@ -63,6 +65,8 @@ class HostLayer:
             setattr(self.args, "w" + nm, self.keep[nm].ctypes.data)
         self.args.attn_norm = self.attn_norm.ctypes.data
         self.args.ffn_norm = self.ffn_norm.ctypes.data
+        if attn_gate:
+            self.args.wag, self.args.fmt_ag = self.keep["ag"].ctypes.data, synth.Q8_0
         self.gelu = gelu
         self.args.act_gelu = int(gelu)
         self.post = {}
@@ -88,8 +92,8 @@ class HostLayer:
 
 
 def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None, qwen=False,
-               gelu=False, sandwich=False):
-    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types, qwen, gelu, sandwich)
+               gelu=False, sandwich=False, attn_gate=False):
+    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types, qwen, gelu, sandwich, attn_gate)
     mats = {nm: ops.QuantMatrix.from_gguf(qt, h.keep[nm], r, c, device=gpu) for nm, (qt, r, c) in h.shapes.items()}
     ex = {nm: torch.from_numpy(v) for nm, v in h.extras.items()}
     layer = ops.DecoderLayer(mats, torch.from_numpy(h.attn_norm), torch.from_numpy(h.ffn_norm), n_head, n_kv, 128,
@@ -97,7 +101,8 @@ def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1
                              bias=(ex["bq"], ex["bk"], ex["bv"]) if ex else None,
                              qk_norm=(ex["q_norm"], ex["k_norm"]) if ex else None, act_gelu=gelu,
                              post_norms=(torch.from_numpy(h.post["post_attn_norm"]),
-                                         torch.from_numpy(h.post["post_ffn_norm"])) if h.post else None)
+                                         torch.from_numpy(h.post["post_ffn_norm"])) if h.post else None,
+                             attn_gate=mats.get("ag"))
     assert layer.cache.pos_bytes == h.cache.pos_bytes
     layer.cache.k.copy_(torch.from_numpy(h.kc))
     layer.cache.v.copy_(torch.from_numpy(h.vc))
@@ -118,6 +123,8 @@ def dequant_rows(orc, b, n):
     (512, 8, 2, 1536, 70, "gelu32"),     # gated GELU with a Q8_0 down projection (the float form)
     (512, 8, 2, 1536, 70, "gemma"),      # Gemma-style: gated GELU and sandwich norms
     (4096, 32, 8, 14336, 4096, "gemma"),
+    (512, 8, 2, 1536, 70, "gate"),       # per-head attention output gate
+    (4096, 32, 8, 14336, 4096, "gate"),
 ])
 def test_layer_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos, qwen):
     print(f"layer E={E} heads={n_head}/{n_kv} F={F} pos={pos} qwen={qwen}", flush=True)
@@ -125,7 +132,7 @@ def test_layer_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos, qwen):
     gelu = qwen in ("gelu", "gelu32", "gemma")
     types = {"down": synth.Q8_0} if qwen == "gelu32" else None
     layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos, seed=E + pos, qwen=qwen is True,
-                                           gelu=gelu, types=types, sandwich=qwen == "gemma")
+                                           gelu=gelu, types=types, sandwich=qwen == "gemma", attn_gate=qwen == "gate")
     x = np.random.default_rng(pos + 1).standard_normal(E).astype(np.float32)
     want, q, k, v, ao = orc.layer_decode(args, kc, vc, pos, x)
     got = layer.decode(torch.from_numpy(x).to(gpu), pos).cpu().numpy()

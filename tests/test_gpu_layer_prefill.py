@@ -68,7 +68,10 @@ def chain(layer, keep, orc, x, pos0, gemm, attention):
         for h in range(nkv):
             k[t, h * HD:(h + 1) * HD] = orc.rope_neox(k[t, h * HD:(h + 1) * HD], HD, tab)
     kr, vr = orc.kv_quantize_row(k.reshape(-1)), orc.kv_quantize_row(v.reshape(-1))
-    attn = attention(q, kr, vr)
+    attn = attn_raw = attention(q, kr, vr)
+    if "ag" in keep:  # per-head output gate from the normalised input (:3522-3537)
+        gv = gemm("ag", xn)
+        attn = np.stack([orc.attn_gate_apply(attn[t], gv[t], nh, HD) for t in range(T)])
     proj = gemm("o", attn)
     if "post_attn_norm" in keep:  # sandwich norm (:3546-3548)
         proj = np.stack([orc.rms_norm(proj[t], keep["post_attn_norm"], 1e-5) for t in range(T)])
@@ -82,7 +85,7 @@ def chain(layer, keep, orc, x, pos0, gemm, attention):
     down = gemm("down", act)
     if "post_ffn_norm" in keep:  # sandwich norm (:3618-3620)
         down = np.stack([orc.rms_norm(down[t], keep["post_ffn_norm"], 1e-5) for t in range(T)])
-    return dict(xn=xn, q=q, k=k, v=v, kr=kr, vr=vr, attn=attn, h=h, xn2=xn2, act=act, out=down + h)
+    return dict(xn=xn, q=q, k=k, v=v, kr=kr, vr=vr, attn_raw=attn_raw, attn=attn, h=h, xn2=xn2, act=act, out=down + h)
 
 
 def oracle_fns(layer, keep, orc, kc, vc, pos0, T):
@@ -130,6 +133,7 @@ Q40_FFN = {"gate": synth.Q4_0, "up": synth.Q4_0, "v": synth.Q8_0}
     (512, 8, 2, 1536, 20, 40, None, True),        # Qwen-style: Q/K/V biases, per-head QK-norm
     (512, 8, 2, 1536, 20, 40, None, "gelu"),      # gated GELU FFN (gelu_tanh)
     (512, 8, 2, 1536, 20, 40, None, "gemma"),     # gated GELU and sandwich norms
+    (512, 8, 2, 1536, 20, 40, None, "gate"),      # per-head attention output gate
 ])
 def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, types, qwen):
     print(f"layer_prefill E={E} heads={n_head}/{n_kv} F={F} pos0={pos0} n_tok={n_tok} types={types} qwen={qwen}",
@@ -137,7 +141,8 @@ def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, type
     n_ctx = pos0 + n_tok + 2
     layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos0, seed=E + pos0 + n_tok,
                                            norm_scale=conditioned(E), types=types, qwen=qwen is True,
-                                           gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma")
+                                           gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma",
+                                           attn_gate=qwen == "gate")
     layer.gelu = qwen in ("gelu", "gemma")
     x = np.random.default_rng(n_tok).standard_normal((n_tok, E)).astype(np.float32)
     og, oa = oracle_fns(layer, keep, orc, kc, vc, pos0, n_tok)
@@ -145,11 +150,11 @@ def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, type
     O = chain(layer, keep, orc, x, pos0, og, oa)
     # every GPU stage on the oracle's inputs
     for nm, inp in (("q", O["xn"]), ("k", O["xn"]), ("v", O["xn"]), ("o", O["attn"]), ("up", O["xn2"]),
-                    ("gate", O["xn2"]), ("down", O["act"])):
+                    ("gate", O["xn2"]), ("down", O["act"])) + ((("ag", O["xn"]),) if "ag" in keep else ()):
         e = rel(gg(nm, inp), og(nm, inp))
         print(f"  gemm {nm}: {e:.2e}", flush=True)
         assert e <= TOL_GEMM
-    e = rel(ga(O["q"], O["kr"], O["vr"]), O["attn"])
+    e = rel(ga(O["q"], O["kr"], O["vr"]), O["attn_raw"])
     print(f"  attention: {e:.2e}", flush=True)
     assert e <= TOL_ATTN
     # the oracle's layer is the composition of its pieces
@@ -161,7 +166,10 @@ def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, type
     G = chain(layer, keep, orc, x, pos0, gg, ga)
     e = rel(got, G["out"])
     print(f"  fused vs chain of entry points: {e:.2e}", flush=True)
-    assert e <= 1e-6
+    # the gate's logistic: the device expf in the fused layer, the host's in
+    # the chain (each within 1 ulp); a 1-ulp gate moves a few of the output
+    # projection's activation roundings
+    assert e <= (1e-4 if qwen == "gate" else 1e-6)
     e = rel(got, want)
     print(f"  layer vs oracle: {e:.2e} (tokens {min(rel(got[t], want[t]) for t in range(n_tok)):.1e} .. "
           f"{max(rel(got[t], want[t]) for t in range(n_tok)):.1e})", flush=True)

@@ -47,7 +47,8 @@ def rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, gelu=False, sandwich=False):
+def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, gelu=False, sandwich=False,
+         attn_gate=False):
     from oracle.oracle import LayerArgs
     qd, kvd = n_head * HD, n_kv * HD
     shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
@@ -85,6 +86,11 @@ def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, 
         w["post_ffn_norm"] = (0.8 + 0.05 * r2.standard_normal(E)).astype(np.float32)
         args.post_attn_norm = w["post_attn_norm"].ctypes.data
         args.post_ffn_norm = w["post_ffn_norm"].ctypes.data
+    if attn_gate:  # per-head output gate: [n_head][n_embd] Q8_0 (the device form of the reference's)
+        shapes["ag"] = (synth.Q8_0, n_head, E)
+        w["ag"] = synth.gen_weights(synth.Q8_0, n_head, E, seed=seed + 300)
+        args.wag = w["ag"].ctypes.data
+        args.fmt_ag = synth.Q8_0
     x = np.random.default_rng(seed + 100).standard_normal(E).astype(np.float32)
     return dict(E=E, n_head=n_head, n_kv=n_kv, F=F, pos=pos, shapes=shapes, w=w, kc=kc, vc=vc, pb=pb, args=args, x=x,
                 gelu=gelu)
@@ -123,6 +129,9 @@ class OraclePieces:
     def gelu_mul(self, gate, up):
         s = np.array([self.o.L.dqo_geglu(float(g)) for g in gate], np.float32)
         return s * up
+
+    def attn_gate(self, ao, gv, n_head):
+        return self.o.attn_gate_apply(ao, gv, n_head, HD)
 
 
 def rope_adjacent(v, tab):
@@ -197,6 +206,10 @@ class IndependentPieces:
         g = gate.astype(np.float64)  # the tanh form (:49-51) in fp64
         return (0.5 * g * (1 + np.tanh(0.7978845608028654 * g * (1 + 0.044715 * g * g)))).astype(np.float32) * up
 
+    def attn_gate(self, ao, gv, n_head):  # 1 / (1 + exp(-g)) in fp64 (:4102-4114)
+        g = 1.0 / (1.0 + np.exp(-gv.astype(np.float64)))
+        return (ao.reshape(n_head, HD) * g[:, None]).reshape(-1).astype(np.float32)
+
 
 def chain(L, P, mistake=None):
     """The decode layer as a chain of pieces P, in the reference's order.
@@ -237,6 +250,12 @@ def chain(L, P, mistake=None):
         kc[pos * pb:(pos + 1) * pb] = P.kv_row(k)
         vc[pos * pb:(pos + 1) * pb] = P.kv_row(v)
     ao = P.attention(q, kc, kc if mistake == "v_from_k" else vc, nh, nkv, pos)
+    if "ag" in w and mistake != "no_attn_gate":  # per-head output gate (:4102-4114)
+        gv = mm("ag", x if mistake == "attn_gate_from_x" else xn)
+        if mistake == "attn_gate_no_sigmoid":
+            ao = (ao.reshape(nh, HD) * gv[:, None]).reshape(-1).astype(np.float32)
+        else:
+            ao = P.attn_gate(ao, gv, nh)
     proj = mm("o", ao)
     pa, pf = ("post_ffn_norm", "post_attn_norm") if mistake == "post_norms_swapped" else ("post_attn_norm",
                                                                                           "post_ffn_norm")
@@ -277,13 +296,16 @@ SHAPES = [
     pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), "gelu", id="E512-pos70-gelu"),
     # Gemma-style: gated GELU and sandwich norms
     pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), "gemma", id="E512-pos70-gemma"),
+    # per-head attention output gate (DenseQuirks::attn_gate)
+    pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), "gate", id="E512-pos70-gate"),
+    pytest.param(4096, 32, 8, 14336, 4096, (0.25 / 64, 0.3 / 64), "gate", id="config4-pos4096-gate"),
 ]
 
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns, qwen):
     L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos, norm_scale=ns, qwen=qwen is True,
-             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma")
+             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma", attn_gate=qwen == "gate")
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, OraclePieces(orc))
     e = rel(got, want)
@@ -296,7 +318,7 @@ def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns, qwen):
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv, F, pos, ns, qwen):
     L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 1, norm_scale=ns, qwen=qwen is True,
-             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma")
+             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma", attn_gate=qwen == "gate")
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, IndependentPieces(ref))
     e = rel(got, want)
@@ -313,7 +335,7 @@ def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv,
 
 MISTAKES = ["gate_up_swapped", "no_attn_residual", "no_ffn_residual", "norms_swapped", "rope_adjacent",
             "no_kv_write", "v_from_k", "no_bias", "qk_norm_after_rope", "qk_norms_swapped", "silu_for_gelu",
-            "no_post_norms", "post_norms_swapped"]
+            "no_post_norms", "post_norms_swapped", "no_attn_gate", "attn_gate_no_sigmoid", "attn_gate_from_x"]
 
 
 @pytest.mark.parametrize("mistake", MISTAKES)
@@ -323,7 +345,8 @@ def test_planted_mistakes_fail(orc, mistake):
     by distinct scales so that swapping them matters). The layer carries
     Q/K/V biases and QK-norm, so the mistakes in those are covered too."""
     L = make(orc, 512, 8, 2, 1536, 70, seed=77, norm_scale=(0.25 / np.sqrt(512), 0.6 / np.sqrt(512)), qwen=True,
-             gelu=mistake == "silu_for_gelu", sandwich=mistake in ("no_post_norms", "post_norms_swapped"))
+             gelu=mistake == "silu_for_gelu", sandwich=mistake in ("no_post_norms", "post_norms_swapped"),
+             attn_gate=mistake.startswith(("no_attn_gate", "attn_gate")))
     got = layer(orc, L)[0]
     ok = chain(L, OraclePieces(orc))[0]
     assert rel(got, ok) <= 1e-6
@@ -336,7 +359,7 @@ def test_planted_mistakes_fail(orc, mistake):
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_prefill_one_token_equals_decode(orc, E, n_head, n_kv, F, pos, ns, qwen):
     L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 2, norm_scale=ns, qwen=qwen is True,
-             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma")
+             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma", attn_gate=qwen == "gate")
     dec, dkc, dvc = layer(orc, L)
     kc, vc = L["kc"].copy(), L["vc"].copy()
     pre = orc.layer_prefill(L["args"], kc, vc, pos, L["x"][None, :])[0]
@@ -367,3 +390,17 @@ def test_gelu_pieces(orc):
     for fn in (L.dqo_geglu, L.dqo_gelu_tanh):
         got = np.array([fn(float(v)) for v in g], np.float64)
         assert np.all(np.abs(got - exact) <= 1e-5 * np.maximum(np.abs(exact), 0.05))
+
+
+def test_attn_gate_piece(orc):
+    """The oracle's per-head output gate against mathematics: every value of
+    head h times 1 / (1 + exp(-g_h)), with the logistic in fp64, over gate
+    values from deep saturation to zero (both tails, exact 0)."""
+    n_head = 64
+    g = np.concatenate([np.linspace(-40, 40, n_head - 2), [0.0, -0.0]]).astype(np.float32)
+    ao = np.random.default_rng(5).standard_normal(n_head * HD).astype(np.float32)
+    got = orc.attn_gate_apply(ao, g, n_head, HD).reshape(n_head, HD)
+    want = ao.reshape(n_head, HD).astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64)))[:, None]
+    err = np.abs(got - want) / np.maximum(np.abs(want), 1e-300)
+    assert float(err.max()) <= 4e-7
+    assert np.array_equal(got[-1], ao.reshape(n_head, HD)[-1] * np.float32(0.5))
