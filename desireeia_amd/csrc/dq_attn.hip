@@ -4,7 +4,7 @@
 // Cache layout (one layer), as the reference keeps it (models/dense_forward.cpp
 // :2425, :4038-4043): [pos][kv_head][hd/32 Q8_0 blocks of 34 bytes], i.e. a
 // row of 136 bytes per (pos, kv head) at hd = 128 and 8 * 136 = 1088 bytes per
-// position at 8 KV heads.
+// position at 8 KV heads. Head dims 64, 128 and 256 are supported.
 //
 // Attention is split over positions (flash-decoding): a workgroup per (KV
 // head, tile of 64 positions) keeps the tile's max / sum / weighted V sum for
@@ -25,6 +25,7 @@
 // to ~1e-6 relative over any range of K / V scales.
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 
 #include "dq_common.h"
 #include "dq_f16.h"
@@ -184,15 +185,18 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
     constexpr int QROW = HD + 8;           // fp16 row of the query operands (padded)
     constexpr int REC = HD + 4;            // acc[HD], max, sum, 2 pad (16-byte records)
     constexpr int HPW = (HPK + NW - 1) / NW;
-    static_assert(HD == 128 && NB == NW && HPK <= 8 && TP % 64 == 0 && RB == 136, "shape");
+    constexpr int QV = HD / 64;            // values of a head per lane (value lane + 64 i)
+    constexpr int CTW = HD / 16 / NW;      // 16-dim output column tiles per wave
+    constexpr int RP = HD == 64 ? 1 : QV / 2;  // RoPE pairs per lane
+    static_assert(dq_head_dim_ok<HD>() && HPK <= 8 && TP % 64 == 0 && RB % 4 == 0 && CTW >= 1, "shape");
 
-    __shared__ __align__(16) uint32_t kt[TP * RBW];     // K rows of the tile (136 bytes each)
+    __shared__ __align__(16) uint32_t kt[TP * RBW];     // K rows of the tile (RB bytes each)
     __shared__ __align__(16) uint32_t vt[TP * RBW];     // V rows
     __shared__ __align__(16) _Float16 qhs[16 * QROW];   // scaled query, fp16 hi (rows >= HPK zero)
     __shared__ __align__(16) _Float16 qls[16 * QROW];   // and lo
     __shared__ __align__(16) float dvf[NB][TP];         // V block scales times dvs (0 past the tile)
     __shared__ __align__(16) float ew[16][TP];          // tile weights exp(s - m) (rows >= HPK zero)
-    __shared__ uint32_t nrow[2][RB / 4];                // FUSE: the new K and V rows
+    __shared__ uint32_t nrow[2][RBW];                   // FUSE: the new K and V rows
     __shared__ float qsc[HPK];                          // per head: 1/sqrt(hd) / query scale
     __shared__ float dvs[NB];                           // per block: weight operand scale
     __shared__ float wmx[NW][HPK], wsm[NW][HPK];        // per-wave maxima and sums
@@ -215,55 +219,64 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
     const int n_load = new_row ? nv - 1 : nv;
 
     // ---- raw inputs of this wave's query heads (wave w takes heads w, w+NW)
-    // and, under FUSE, their bias, QK-norm weights and RoPE pair, and the new
+    // and, under FUSE, their bias, QK-norm weights and RoPE pairs, and the new
     // K (wave 0) / V (wave 1) row: loaded before the tile, so that waiting
     // for them leaves the tile's loads in flight
-    float qa[HPW], qb[HPW], ba[HPW], bb[HPW];
-    float rc = 1.0f, rs = 0.0f, na = 0.0f, nb = 0.0f;
-    float xa = 0.0f, xb = 0.0f, xba = 0.0f, xbb = 0.0f, xna = 0.0f, xnb = 0.0f;
+    float qx[HPW][QV], qb[HPW][QV];
+    float rc[RP], rs[RP], nq[QV], xr[QV], xbias[QV], xn[QV];
 #pragma unroll
     for (int t = 0; t < HPW; ++t) {
         const size_t hq = (size_t)kvh * HPK + min(wave + NW * t, HPK - 1);
-        qa[t] = A.q[hq * HD + lane];
-        qb[t] = A.q[hq * HD + lane + 64];
-        ba[t] = bb[t] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < QV; ++i) {
+            qx[t][i] = A.q[hq * HD + lane + 64 * i];
+            qb[t][i] = 0.0f;
+        }
         if constexpr (FUSE) {
             if (A.post.bq) {
-                ba[t] = A.post.bq[hq * HD + lane];
-                bb[t] = A.post.bq[hq * HD + lane + 64];
+#pragma unroll
+                for (int i = 0; i < QV; ++i) qb[t][i] = A.post.bq[hq * HD + lane + 64 * i];
             }
         }
     }
+#pragma unroll
+    for (int i = 0; i < RP; ++i) {
+        rc[i] = 1.0f;
+        rs[i] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < QV; ++i) nq[i] = xr[i] = xbias[i] = xn[i] = 0.0f;
     if constexpr (FUSE) {
         if (A.rope) {
-            rc = A.rope[2 * lane];
-            rs = A.rope[2 * lane + 1];
+#pragma unroll
+            for (int i = 0; i < RP; ++i) {
+                const int j = HD == 64 ? (lane & 31) : lane + 64 * i;
+                rc[i] = A.rope[2 * j];
+                rs[i] = A.rope[2 * j + 1];
+            }
         }
         if (A.post.q_norm) {
-            na = A.post.q_norm[lane];
-            nb = A.post.q_norm[lane + 64];
+#pragma unroll
+            for (int i = 0; i < QV; ++i) nq[i] = A.post.q_norm[lane + 64 * i];
         }
         if (new_row && wave < 2) {  // wave-uniform
-            const size_t o = (size_t)kvh * HD + lane;
-            xa = (wave == 0 ? A.k : A.v)[o];
-            xb = (wave == 0 ? A.k : A.v)[o + 64];
+            const float* src = wave == 0 ? A.k : A.v;
             const float* bias = wave == 0 ? A.post.bk : A.post.bv;
-            if (bias) {
-                xba = bias[o];
-                xbb = bias[o + 64];
-            }
-            if (wave == 0 && A.post.k_norm) {
-                xna = A.post.k_norm[lane];
-                xnb = A.post.k_norm[lane + 64];
+#pragma unroll
+            for (int i = 0; i < QV; ++i) {
+                const size_t o = (size_t)kvh * HD + lane + 64 * i;
+                xr[i] = src[o];
+                if (bias) xbias[i] = bias[o];
+                if (wave == 0 && A.post.k_norm) xn[i] = A.post.k_norm[lane + 64 * i];
             }
         }
     }
     // ---- the tile's K and V rows, straight into LDS (lane i of a dword DMA
     // writes dword i of the instruction's 64-dword span, row r of the tile at
-    // byte 136 r: each instruction reads two rows' worth of consecutive
-    // dwords). Every wave issues the same count (spare slots repeat the last
-    // span), and rows at or past n_load read a row of the tile instead: rows
-    // >= nv are never used, and the new row is written over afterwards.
+    // byte RB r: each instruction reads 256 consecutive bytes of rows). Every
+    // wave issues the same count (spare slots repeat the last span), and rows
+    // at or past n_load read a row of the tile instead: rows >= nv are never
+    // used, and the new row is written over afterwards.
     {
         const uint8_t* kb = A.kc + (size_t)p0 * A.pos_bytes + (size_t)kvh * RB;
         const uint8_t* vb = A.vc + (size_t)p0 * A.pos_bytes + (size_t)kvh * RB;
@@ -289,29 +302,45 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
         }
         for (int i = tid; i < EZ; i += NT) reinterpret_cast<uint4*>(&ew[HPK][0])[i] = z;
     }
+    // NeoX RoPE of a head held as x[i] = value lane + 64 i with the lane's
+    // pairs' (cos, sin) in registers (dq_rope_head with the table preloaded)
+    auto rope = [&](float(&x)[QV]) {
+        if constexpr (HD == 64) {
+            const float y = __shfl_xor(x[0], 32, DQ_WAVE);
+            x[0] = lane < 32 ? x[0] * rc[0] - y * rs[0] : y * rs[0] + x[0] * rc[0];
+        } else {
+#pragma unroll
+            for (int i = 0; i < RP; ++i) {
+                const float a = x[i], b = x[i + RP];
+                x[i] = a * rc[i] - b * rs[i];
+                x[i + RP] = a * rs[i] + b * rc[i];
+            }
+        }
+    };
     // ---- query operands: bias, QK-norm, RoPE (FUSE), then the head's
     // power-of-two scale and the fp16 hi / lo split
 #pragma unroll
     for (int t = 0; t < HPW; ++t) {
         const int h = wave + NW * t;
         if (h < HPK) {  // wave-uniform
-            float a = qa[t], b = qb[t];
+            float x[QV];
+#pragma unroll
+            for (int i = 0; i < QV; ++i) x[i] = qx[t][i];
             if constexpr (FUSE) {
                 if (A.post.bq) {
-                    a += ba[t];
-                    b += bb[t];
+#pragma unroll
+                    for (int i = 0; i < QV; ++i) x[i] += qb[t][i];
                 }
-                if (A.post.q_norm) dq_head_rms_norm_w(a, b, na, nb, A.post.eps);
-                if (A.rope) {  // NeoX rotation of the pair (j, j + 64) (dq_rope_pair)
-                    const float x = a, y = b;
-                    a = x * rc - y * rs;
-                    b = x * rs + y * rc;
-                }
+                if (A.post.q_norm) dq_head_rms_norm_w<HD>(x, nq, A.post.eps);
+                if (A.rope) rope(x);
             }
-            const int sh = pow2_shift(dq_wave_max_uniform(fmaxf(fabsf(a), fabsf(b))), 100);
-            const float s = ldexpf(1.0f, sh);
-            split_hl(a * s, qhs[h * QROW + lane], qls[h * QROW + lane]);
-            split_hl(b * s, qhs[h * QROW + lane + 64], qls[h * QROW + lane + 64]);
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < QV; ++i) m = fmaxf(m, fabsf(x[i]));
+            const int sh = pow2_shift(dq_wave_max_uniform(m), 100);
+            const float sc = ldexpf(1.0f, sh);
+#pragma unroll
+            for (int i = 0; i < QV; ++i) split_hl(x[i] * sc, qhs[h * QROW + lane + 64 * i], qls[h * QROW + lane + 64 * i]);
             if (lane == 0) qsc[h] = A.scale * ldexpf(1.0f, -sh);
         }
     }
@@ -322,24 +351,22 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
         if (new_row && wave < 2) {
             const float* bias = wave == 0 ? A.post.bk : A.post.bv;
             if (bias) {
-                xa += xba;
-                xb += xbb;
+#pragma unroll
+                for (int i = 0; i < QV; ++i) xr[i] += xbias[i];
             }
-            if (wave == 0 && A.post.k_norm) dq_head_rms_norm_w(xa, xb, xna, xnb, A.post.eps);
-            if (wave == 0 && A.rope) {
-                const float x = xa, y = xb;
-                xa = x * rc - y * rs;
-                xb = x * rs + y * rc;
-            }
+            if (wave == 0 && A.post.k_norm) dq_head_rms_norm_w<HD>(xr, xn, A.post.eps);
+            if (wave == 0 && A.rope) rope(xr);
             uint8_t* grow = (wave == 0 ? A.kc : A.vc) + (size_t)pos * A.pos_bytes + (size_t)kvh * RB;
-            dq_q8_0_row128(xa, xb, lane, grow);
-            dq_q8_0_row128(xa, xb, lane, reinterpret_cast<uint8_t*>(nrow[wave]));
+            dq_q8_0_row<HD>(xr, lane, grow);
+            dq_q8_0_row<HD>(xr, lane, reinterpret_cast<uint8_t*>(nrow[wave]));
         }
     }
     __syncthreads();  // every wave's DMAs have landed; query operands in LDS
     if constexpr (FUSE) {
         if (new_row) {  // workgroup-uniform
-            if (wave < 2 && lane < RBW) (wave == 0 ? kt : vt)[(nv - 1) * RBW + lane] = nrow[wave][lane];
+            if (wave < 2) {
+                for (int l = lane; l < RBW; l += 64) (wave == 0 ? kt : vt)[(nv - 1) * RBW + l] = nrow[wave][l];
+            }
             __syncthreads();
         }
     }
@@ -369,7 +396,8 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 // quants of block b at row bytes 34b + 2 + 8 g4 ...: dword
-                // aligned for odd b, two bytes in for even b
+                // aligned for odd b, two bytes in for even b (RB is a
+                // multiple of 4)
                 const int cb = (DQ_SZ_Q8_0 * b + 2) >> 2;
                 uint32_t w0, w1;
                 if (b & 1) {
@@ -393,9 +421,9 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
             for (int r = 0; r < 4; ++r) sc[gi][r] = (4 * g4 + r < HPK && p < nv) ? s4[r] * hs[r] : -INFINITY;
         }
     }
-    // V block scales of block `wave` and their power-of-two operand scale
-    {
-        const int b = wave;
+    // V block scales (wave w: blocks w, w + NW, ...) and their power-of-two
+    // operand scale
+    for (int b = wave; b < NB; b += NW) {  // wave-uniform
         float dv[TP / 64];
         float m = 0.0f;
 #pragma unroll
@@ -444,55 +472,57 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
         if (n16 == 0 && h < HPK) wsm[wave][h] = ls[r];
     }
     __syncthreads();
-    // ---- weighted V sum: wave w takes block w (dims 32w + 16t + n16, t = 0,
-    // 1); lane (n16, g4) of a step takes positions 32 ks + 8 g4 + j
+    // ---- weighted V sum: wave w takes the output column tiles ct = CTW w +
+    // c (dims 16 ct + n16 of block ct / 2); lane (n16, g4) of a step takes
+    // positions 32 ks + 8 g4 + j
     float* rec = A.part + ((size_t)kvh * A.max_tiles + tile) * HPK * REC;
     {
-        const int b = wave;
-        // the lane's V byte (dims 32b + n16 (+16 t)) of position 8 g4 (+ j + 32 ks)
-        const uint8_t* vl = vb8 + 8 * g4 * RB + DQ_SZ_Q8_0 * b + 2 + n16;
-        f4v o0 = {0.0f, 0.0f, 0.0f, 0.0f}, o1 = {0.0f, 0.0f, 0.0f, 0.0f};
+        f4v o[CTW];
+#pragma unroll
+        for (int c = 0; c < CTW; ++c) o[c] = f4v{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) {
-            // A: the weights W[h][p] = ew[h][p] * dv[p][b] (times the block's
-            // power of two, in dvf) split into fp16 hi / lo (rows >= HPK: zero)
             h8 ah, al;
-            {
-                const int p = 32 * ks + 8 * g4;
-                const float4 e0 = *reinterpret_cast<const float4*>(&ew[n16][p]);
-                const float4 e1 = *reinterpret_cast<const float4*>(&ew[n16][p + 4]);
-                const float4 d0 = *reinterpret_cast<const float4*>(&dvf[b][p]);
-                const float4 d1 = *reinterpret_cast<const float4*>(&dvf[b][p + 4]);
-                const float e[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-                const float d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    _Float16 x, y;
-                    split_hl(e[j] * d[j], x, y);
-                    ah[j] = x;
-                    al[j] = y;
+            for (int c = 0; c < CTW; ++c) {
+                const int ct = CTW * wave + c, b = ct >> 1, t = ct & 1;
+                if (c == 0 || t == 0) {
+                    // A: the weights W[h][p] = ew[h][p] * dv[p][b] (times the
+                    // block's power of two, in dvf) split into fp16 hi / lo
+                    // (rows >= HPK: zero)
+                    const int p = 32 * ks + 8 * g4;
+                    const float4 e0 = *reinterpret_cast<const float4*>(&ew[n16][p]);
+                    const float4 e1 = *reinterpret_cast<const float4*>(&ew[n16][p + 4]);
+                    const float4 d0 = *reinterpret_cast<const float4*>(&dvf[b][p]);
+                    const float4 d1 = *reinterpret_cast<const float4*>(&dvf[b][p + 4]);
+                    const float e[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+                    const float d[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        _Float16 x, y;
+                        split_hl(e[j] * d[j], x, y);
+                        ah[j] = x;
+                        al[j] = y;
+                    }
                 }
-            }
-            const uint8_t* col = vl + 32 * ks * RB;
-            uint32_t u0[8], u1[8];
+                // the lane's V byte (dim 16 ct + n16) of positions 32 ks + 8 g4 + j
+                const uint8_t* col = vb8 + (32 * ks + 8 * g4) * RB + DQ_SZ_Q8_0 * b + 2 + 16 * t + n16;
+                uint32_t u[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                u0[j] = col[j * RB];
-                u1[j] = col[j * RB + 16];
+                for (int j = 0; j < 8; ++j) u[j] = col[j * RB];
+                const h8 bv = i8_bytes_to_h8(u);
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv, o[c], 0, 0, 0);
+                o[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv, o[c], 0, 0, 0);
             }
-            const h8 bv0 = i8_bytes_to_h8(u0), bv1 = i8_bytes_to_h8(u1);
-            o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv0, o0, 0, 0, 0);
-            o0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv0, o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv1, o1, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv1, o1, 0, 0, 0);
         }
-        const float inv = 1.0f / dvs[b];  // a power of two: exact
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int h = 4 * g4 + r;
-            if (h < HPK) {
-                rec[h * REC + 32 * b + n16] = o0[r] * inv;
-                rec[h * REC + 32 * b + 16 + n16] = o1[r] * inv;
+        for (int c = 0; c < CTW; ++c) {
+            const int ct = CTW * wave + c;
+            const float inv = 1.0f / dvs[ct >> 1];  // a power of two: exact
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int h = 4 * g4 + r;
+                if (h < HPK) rec[h * REC + 16 * ct + n16] = o[c][r] * inv;
             }
         }
     }
@@ -641,7 +671,7 @@ bool attn_shape_ok(uint32_t n_head, uint32_t n_head_kv, uint32_t hd) {
     if (n_head_kv == 0 || n_head % n_head_kv || n_head_kv > 4096) return false;
     const uint32_t hpk = n_head / n_head_kv;
     // the merge takes whole 256-output blocks
-    return hd == 128 && (hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8) && (n_head * hd) % 256 == 0;
+    return dq_head_dim_supported(hd) && (hpk == 1 || hpk == 2 || hpk == 4 || hpk == 8) && (n_head * hd) % 256 == 0;
 }
 
 int attn_run(const float* d_q, const float* d_k, const float* d_v, const float* d_rope, const void* d_kc,
@@ -681,17 +711,26 @@ int attn_run(const float* d_q, const float* d_k, const float* d_v, const float* 
     a.post = post;
     const int nh = (int)n_head;
     int rc = DQ_ERR_NOT_SUPPORTED;
-#define DQ_ATTN_CASE(H)                                                                              \
-    case H:                                                                                          \
-        rc = fuse ? launch_attn<128, H, true>(a, nh, st) : launch_attn<128, H, false>(a, nh, st);    \
+    auto by_hpk = [&](auto hdc) {
+        constexpr int HD = decltype(hdc)::value;
+#define DQ_ATTN_CASE(H)                                                                          \
+    case H:                                                                                      \
+        rc = fuse ? launch_attn<HD, H, true>(a, nh, st) : launch_attn<HD, H, false>(a, nh, st);  \
         break;
-    switch (hpk) {
-        DQ_ATTN_CASE(1)
-        DQ_ATTN_CASE(2)
-        DQ_ATTN_CASE(4)
-        DQ_ATTN_CASE(8)
-    }
+        switch (hpk) {
+            DQ_ATTN_CASE(1)
+            DQ_ATTN_CASE(2)
+            DQ_ATTN_CASE(4)
+            DQ_ATTN_CASE(8)
+        }
 #undef DQ_ATTN_CASE
+    };
+    if (hd == 64)
+        by_hpk(std::integral_constant<int, 64>{});
+    else if (hd == 128)
+        by_hpk(std::integral_constant<int, 128>{});
+    else
+        by_hpk(std::integral_constant<int, 256>{});
     return rc;
 }
 

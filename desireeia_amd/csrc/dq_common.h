@@ -209,21 +209,35 @@ __device__ __forceinline__ double dq_wave_sum_f64(double v) {
     return v;
 }
 
-// rms_norm_vec (models/dense_forward.cpp:129-165) of one 128-value head held
-// by a wave as (lo, hi) = values (lane, lane + 64): squares in float summed
-// in double, scale = 1/sqrtf((float)(sum/128) + eps), y = x * scale * w. The
-// per-head QK-norm of :3915-3931.
-// The weights (w_lo, w_hi) = (w[lane], w[lane + 64]) already in registers.
-__device__ __forceinline__ void dq_head_rms_norm_w(float& lo, float& hi, float w_lo, float w_hi, float eps) {
-    const float a = lo * lo, b = hi * hi;
-    const double s = dq_wave_sum_f64((double)a + (double)b);
-    const float scale = 1.0f / sqrtf((float)(s / 128.0) + eps);
-    lo = lo * scale * w_lo;
-    hi = hi * scale * w_hi;
+// A head of HD values (HD = 64, 128 or 256) held by the 64 lanes of a wave:
+// x[i] = value lane + 64 i, HD / 64 values per lane.
+template <int HD>
+constexpr bool dq_head_dim_ok() {
+    return HD == 64 || HD == 128 || HD == 256;
 }
-__device__ __forceinline__ void dq_head_rms_norm(float& lo, float& hi, const float* __restrict__ w, int lane,
+inline bool dq_head_dim_supported(uint32_t hd) { return hd == 64 || hd == 128 || hd == 256; }
+
+// rms_norm_vec (models/dense_forward.cpp:129-165) of one head held by a wave:
+// squares in float summed in double, scale = 1/sqrtf((float)(sum/HD) + eps),
+// y = x * scale * w. The per-head QK-norm of :3915-3931. w[i] = weight of
+// value lane + 64 i, already in registers.
+template <int HD>
+__device__ __forceinline__ void dq_head_rms_norm_w(float (&x)[HD / 64], const float (&w)[HD / 64], float eps) {
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < HD / 64; ++i) s += (double)(x[i] * x[i]);
+    s = dq_wave_sum_f64(s);
+    const float scale = 1.0f / sqrtf((float)(s / (double)HD) + eps);
+#pragma unroll
+    for (int i = 0; i < HD / 64; ++i) x[i] = x[i] * scale * w[i];
+}
+template <int HD>
+__device__ __forceinline__ void dq_head_rms_norm(float (&x)[HD / 64], const float* __restrict__ w, int lane,
                                                  float eps) {
-    dq_head_rms_norm_w(lo, hi, w[lane], w[lane + 64], eps);
+    float wr[HD / 64];
+#pragma unroll
+    for (int i = 0; i < HD / 64; ++i) wr[i] = w[lane + 64 * i];
+    dq_head_rms_norm_w<HD>(x, wr, eps);
 }
 
 // The gated FFN activations of the reference (act(gate) * up):
@@ -263,8 +277,8 @@ __device__ __forceinline__ float dq_ffn_act(float g) {
     }
 }
 
-// Q/K/V post-processing of one head held by a wave as (lo, hi) (lane, lane
-// + 64), between the projections and RoPE: the bias (add_bias, y += b;
+// Q/K/V post-processing of one head held by a wave (x[i] = value lane +
+// 64 i), between the projections and RoPE: the bias (add_bias, y += b;
 // :3904-3908) and the per-head RMSNorm (:3915-3931). All optional.
 struct DqQkvPost {
     const float *bq, *bk, *bv, *q_norm, *k_norm;
@@ -275,14 +289,15 @@ struct DqQkvPost {
     const float* gate;
 };
 // kind 0: query head, 1: key head, 2: value head
-__device__ __forceinline__ void dq_qkv_post(float& lo, float& hi, int kind, int head, int lane, const DqQkvPost& P) {
+template <int HD>
+__device__ __forceinline__ void dq_qkv_post(float (&x)[HD / 64], int kind, int head, int lane, const DqQkvPost& P) {
     const float* b = kind == 0 ? P.bq : (kind == 1 ? P.bk : P.bv);
     if (b) {
-        lo += b[(size_t)head * 128 + lane];
-        hi += b[(size_t)head * 128 + lane + 64];
+#pragma unroll
+        for (int i = 0; i < HD / 64; ++i) x[i] += b[(size_t)head * HD + lane + 64 * i];
     }
     const float* nw = kind == 0 ? P.q_norm : (kind == 1 ? P.k_norm : nullptr);
-    if (nw) dq_head_rms_norm(lo, hi, nw, lane, P.eps);
+    if (nw) dq_head_rms_norm<HD>(x, nw, lane, P.eps);
 }
 
 __device__ __forceinline__ float dq_wave_max(float v) {
@@ -300,31 +315,49 @@ __device__ __forceinline__ void dq_rope_pair(float& x0, float& x1, const float* 
     x1 = a * s + b * c;
 }
 
-// kv_quantize_row (kv/kv_quant.cpp:31-56) of one 128-value row held by the 64
-// lanes of a wave as (lo, hi) = (value j, value j + 64): blocks 0 and 1 come
-// from the lo halves of lanes 0-31 / 32-63, blocks 2 and 3 from the hi
-// halves; each block is fp16 d followed by 32 int8. dst: 136 bytes, 2-byte
-// aligned (global or LDS).
-__device__ __forceinline__ void dq_q8_0_row128(float lo, float hi, int j, uint8_t* dst) {
-    float alo = fabsf(lo), ahi = fabsf(hi);
+// NeoX RoPE of a whole head held by a wave (n_rot = HD): pairs (j, j + HD/2)
+// with (cos, sin) = (rope[2j], rope[2j+1]) (models/dense_forward.cpp:668-680).
+// HD >= 128: both values of a pair sit in one lane (x[i], x[i + HD/128]);
+// HD = 64: in lanes j and j + 32.
+template <int HD>
+__device__ __forceinline__ void dq_rope_head(float (&x)[HD / 64], const float* __restrict__ rope, int lane) {
+    if constexpr (HD == 64) {
+        const float y = __shfl_xor(x[0], 32, DQ_WAVE);  // the pair's other value
+        const int j = lane & 31;
+        const float c = rope[2 * j], s = rope[2 * j + 1];
+        x[0] = lane < 32 ? x[0] * c - y * s : y * s + x[0] * c;
+    } else {
+#pragma unroll
+        for (int i = 0; i < HD / 128; ++i) dq_rope_pair(x[i], x[i + HD / 128], rope, lane + 64 * i);
+    }
+}
+
+// kv_quantize_row (kv/kv_quant.cpp:31-56) of one HD-value row held by a wave
+// (x[i] = value lane + 64 i): value lane + 64 i is element lane % 32 of block
+// 2 i + lane / 32; a block's maximum is a reduction over its 32 lanes. Each
+// block is fp16 d followed by 32 int8. dst: HD / 32 * 34 bytes, 2-byte aligned
+// (global or LDS).
+template <int HD>
+__device__ __forceinline__ void dq_q8_0_row(const float (&x)[HD / 64], int lane, uint8_t* dst) {
+    float am[HD / 64];
+#pragma unroll
+    for (int i = 0; i < HD / 64; ++i) am[i] = fabsf(x[i]);
 #pragma unroll
     for (int off = 1; off < 32; off <<= 1) {
-        alo = fmaxf(alo, __shfl_xor(alo, off, DQ_WAVE));
-        ahi = fmaxf(ahi, __shfl_xor(ahi, off, DQ_WAVE));
-    }
-    const int blo = j >> 5, i = j & 31;
 #pragma unroll
-    for (int part = 0; part < 2; ++part) {
-        const float amax = part ? ahi : alo;
-        const float x = part ? hi : lo;
-        const int blk = part ? blo + 2 : blo;
+        for (int i = 0; i < HD / 64; ++i) am[i] = fmaxf(am[i], __shfl_xor(am[i], off, DQ_WAVE));
+    }
+    const int hb = lane >> 5, e = lane & 31;
+#pragma unroll
+    for (int i = 0; i < HD / 64; ++i) {
+        const float amax = am[i];
         const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
         const float id = d > 0.0f ? 1.0f / d : 0.0f;
-        int iv = (int)rintf(x * id);
+        int iv = (int)rintf(x[i] * id);
         iv = iv > 127 ? 127 : (iv < -127 ? -127 : iv);
-        uint8_t* bp = dst + blk * DQ_SZ_Q8_0;
-        bp[2 + i] = (uint8_t)(iv & 0xFF);
-        if (i == 0) *reinterpret_cast<uint16_t*>(bp) = dq_f2h(d);
+        uint8_t* bp = dst + (2 * i + hb) * DQ_SZ_Q8_0;
+        bp[2 + e] = (uint8_t)(iv & 0xFF);
+        if (e == 0) *reinterpret_cast<uint16_t*>(bp) = dq_f2h(d);
     }
 }
 

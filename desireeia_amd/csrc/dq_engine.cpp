@@ -647,7 +647,7 @@ int cuda_attention_out(const void* d_wo_qs, const void* d_wo_scale, const float*
     if (!g.kc || !d_wo_qs || !d_wo_scale || !kv_quantized) return DQ_ERR_NOT_SUPPORTED;
     const WInfo* wo = lookup(d_wo_qs);
     if (!wo || wo->rows != n_embd || wo->cols != q_dim) return DQ_ERR_NOT_SUPPORTED;
-    if (heads_per_kv == 0 || n_head % heads_per_kv || head_dim != 128) return DQ_ERR_NOT_SUPPORTED;
+    if (heads_per_kv == 0 || n_head % heads_per_kv || !dq_head_dim_supported(head_dim)) return DQ_ERR_NOT_SUPPORTED;
     const uint32_t n_kv = n_head / heads_per_kv;
     if ((size_t)n_head * head_dim != q_dim || (size_t)n_kv * head_dim != kv_dim) return DQ_ERR_NOT_SUPPORTED;
     if (row_bytes != (size_t)(head_dim / 32) * DQ_SZ_Q8_0) return DQ_ERR_NOT_SUPPORTED;
@@ -681,7 +681,7 @@ int cuda_qkv_attention_out(const CudaQkvAttnArgs* A) {
     const WInfo* m[4] = {lookup(A->wq_qs), lookup(A->wk_qs), lookup(A->wv_qs), lookup(A->wo_qs)};
     for (const WInfo* w : m)
         if (!w) return DQ_ERR_NOT_SUPPORTED;
-    if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv) return DQ_ERR_NOT_SUPPORTED;
+    if (!dq_head_dim_supported(A->head_dim) || A->n_head_kv == 0 || A->n_head % A->n_head_kv) return DQ_ERR_NOT_SUPPORTED;
     if (A->heads_per_kv != A->n_head / A->n_head_kv) return DQ_ERR_NOT_SUPPORTED;
     const size_t E = A->n_embd, QD = A->q_dim, KVD = A->kv_dim;
     if (QD != (size_t)A->n_head * A->head_dim || KVD != (size_t)A->n_head_kv * A->head_dim) return DQ_ERR_NOT_SUPPORTED;
@@ -802,7 +802,7 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     if (slots && A->rope_cache && (!A->rope_all || A->rope_stride < A->n_rot)) return DQ_ERR_INVALID_ARG;
     const uint32_t pos = slots ? A->dyn_all[2 * (size_t)A->layer_slot] : A->pos;
     const uint32_t cc_start = slots ? A->dyn_all[2 * (size_t)A->layer_slot + 1] : A->cc_start;
-    if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
+    if (!dq_head_dim_supported(A->head_dim) || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
         A->heads_per_kv != A->n_head / A->n_head_kv)
         return DQ_ERR_NOT_SUPPORTED;
     if (A->q_dim != (size_t)A->n_head * A->head_dim || A->kv_dim != (size_t)A->n_head_kv * A->head_dim)
@@ -952,7 +952,7 @@ int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, 
 int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     if (!A || !g.kc || A->n_tok == 0 || A->n_total == 0) return DQ_ERR_NOT_SUPPORTED;
     if (!A->attn_norm_w || !A->ffn_norm_w) return DQ_ERR_NOT_SUPPORTED;
-    if (A->head_dim != 128 || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
+    if (!dq_head_dim_supported(A->head_dim) || A->n_head_kv == 0 || A->n_head % A->n_head_kv ||
         A->heads_per_kv != A->n_head / A->n_head_kv)
         return DQ_ERR_NOT_SUPPORTED;
     if (A->q_dim != (size_t)A->n_head * A->head_dim || A->kv_dim != (size_t)A->n_head_kv * A->head_dim)

@@ -153,51 +153,53 @@ __global__ __launch_bounds__(NQ_T) void norm_quant_kernel(const float* __restric
 
 // --------------------------------------------------------------- rope_kv --
 // Workgroup r < n_head: query head r; n_head <= r < n_head + n_kv: key head;
-// then value heads. 64 threads; thread j handles dims j and j + 64 of the
-// 128-dim head. RoPE (models/dense_forward.cpp:668-680) on the first n_rot
-// dims: pairs (j, j + n_rot/2), x0*c - x1*s and x0*s + x1*c with (c, s) =
-// table[2j], table[2j+1]. Keys and values are then quantized (kv_quantize_row).
+// then value heads. 64 threads; thread j holds dims j + 64 i of the HD-dim
+// head. RoPE (models/dense_forward.cpp:668-680) on the first n_rot dims: pairs
+// (j, j + n_rot/2), x0*c - x1*s and x0*s + x1*c with (c, s) = table[2j],
+// table[2j+1]. Keys and values are then quantized (kv_quantize_row).
+template <int HD>
 __global__ __launch_bounds__(64) void rope_kv_kernel(float* __restrict__ q, const float* __restrict__ k,
                                                      const float* __restrict__ v, const float* __restrict__ rope,
                                                      int n_head, int n_kv, int n_rot, uint8_t* __restrict__ kc,
                                                      uint8_t* __restrict__ vc, size_t pos_bytes, int pos_host,
                                                      const int* __restrict__ pos_dev, int n_ctx, DqQkvPost post) {
-    constexpr int HD = 128;
+    constexpr int QV = HD / 64;
     const int r = blockIdx.x, j = threadIdx.x;
     const int kind = r < n_head ? 0 : (r < n_head + n_kv ? 1 : 2);
     const int head = kind == 0 ? r : (kind == 1 ? r - n_head : r - n_head - n_kv);
     const float* src = kind == 0 ? q + (size_t)head * HD : (kind == 1 ? k : v) + (size_t)head * HD;
-    float lo = src[j], hi = src[j + 64];
-    dq_qkv_post(lo, hi, kind, head, j, post);
+    float x[QV];
+#pragma unroll
+    for (int i = 0; i < QV; ++i) x[i] = src[j + 64 * i];
+    dq_qkv_post<HD>(x, kind, head, j, post);
     if (kind < 2 && rope) {
-        // n_rot = 128: pair (j, j+64); n_rot < 128: pairs inside [0, n_rot)
-        const int half = n_rot / 2;
         if (n_rot == HD) {
-            dq_rope_pair(lo, hi, rope, j);
-        } else {
+            dq_rope_head<HD>(x, rope, j);
+        } else {  // pairs inside [0, n_rot)
             __shared__ float row[HD];
-            row[j] = lo;
-            row[j + 64] = hi;
+#pragma unroll
+            for (int i = 0; i < QV; ++i) row[j + 64 * i] = x[i];
             __syncthreads();
-            if (j < half) {
-                const float c = rope[2 * j], s = rope[2 * j + 1];
-                const float x0 = row[j], x1 = row[j + half];
-                row[j] = x0 * c - x1 * s;
-                row[j + half] = x0 * s + x1 * c;
+            const int half = n_rot / 2;
+            for (int jj = j; jj < half; jj += 64) {
+                const float c = rope[2 * jj], s = rope[2 * jj + 1];
+                const float x0 = row[jj], x1 = row[jj + half];
+                row[jj] = x0 * c - x1 * s;
+                row[jj + half] = x0 * s + x1 * c;
             }
             __syncthreads();
-            lo = row[j];
-            hi = row[j + 64];
+#pragma unroll
+            for (int i = 0; i < QV; ++i) x[i] = row[j + 64 * i];
         }
     }
     if (kind == 0) {
-        q[(size_t)head * HD + j] = lo;
-        q[(size_t)head * HD + j + 64] = hi;
+#pragma unroll
+        for (int i = 0; i < QV; ++i) q[(size_t)head * HD + j + 64 * i] = x[i];
         return;
     }
     int p = pos_dev ? *pos_dev : pos_host;
     p = p < 0 ? 0 : (p >= n_ctx ? n_ctx - 1 : p);
-    dq_q8_0_row128(lo, hi, j, (kind == 1 ? kc : vc) + (size_t)p * pos_bytes + (size_t)head * (HD / 32) * DQ_SZ_Q8_0);
+    dq_q8_0_row<HD>(x, j, (kind == 1 ? kc : vc) + (size_t)p * pos_bytes + (size_t)head * (HD / 32) * DQ_SZ_Q8_0);
 }
 
 // ------------------------------------------------------------ silu_quant --
@@ -274,7 +276,7 @@ bool per32(int fmt) { return fmt == DQ_FMT_Q8_0 || fmt == DQ_FMT_Q4_0; }
 bool layer_fmt(int fmt) { return kquant(fmt) || per32(fmt); }
 
 bool layer_ok(const dq_layer_t* L) {
-    if (!L || L->head_dim != 128 || L->n_head_kv == 0 || L->n_head % L->n_head_kv) return false;
+    if (!L || !dq_head_dim_supported(L->head_dim) || L->n_head_kv == 0 || L->n_head % L->n_head_kv) return false;
     if (L->n_embd == 0 || L->n_embd % 256 || L->n_ff == 0 || L->n_ff % 256 || (L->n_head * L->head_dim) % 256)
         return false;
     if (L->n_rot == 0 || L->n_rot > L->head_dim || L->n_rot % 2) return false;
@@ -404,13 +406,22 @@ int dq_rope_kv_write_post(float* d_q, const float* d_k, const float* d_v, const 
                           uint32_t n_head_kv, uint32_t hd, uint32_t n_rot, void* d_kc, void* d_vc, uint32_t pos,
                           const int32_t* d_pos, uint32_t n_ctx, const DqQkvPost& post, void* stream) {
     if (!d_q || !d_k || !d_v || !d_kc || !d_vc || n_ctx == 0) return DQ_ERR_INVALID_ARG;
-    if (hd != 128) return DQ_ERR_NOT_SUPPORTED;
+    if (!dq_head_dim_supported(hd)) return DQ_ERR_NOT_SUPPORTED;
     if (d_rope && (n_rot == 0 || n_rot > hd || n_rot % 2)) return DQ_ERR_INVALID_ARG;
     if (!d_pos && pos >= n_ctx) return DQ_ERR_INVALID_ARG;
     const size_t pos_bytes = (size_t)n_head_kv * (hd / 32) * DQ_SZ_Q8_0;
-    rope_kv_kernel<<<n_head + 2 * n_head_kv, 64, 0, (hipStream_t)stream>>>(
-        d_q, d_k, d_v, d_rope, (int)n_head, (int)n_head_kv, (int)n_rot, (uint8_t*)d_kc, (uint8_t*)d_vc, pos_bytes,
-        (int)pos, d_pos, (int)n_ctx, post);
+    auto go = [&](auto kern) {
+        kern<<<n_head + 2 * n_head_kv, 64, 0, (hipStream_t)stream>>>(d_q, d_k, d_v, d_rope, (int)n_head,
+                                                                      (int)n_head_kv, (int)n_rot, (uint8_t*)d_kc,
+                                                                      (uint8_t*)d_vc, pos_bytes, (int)pos, d_pos,
+                                                                      (int)n_ctx, post);
+    };
+    if (hd == 64)
+        go(rope_kv_kernel<64>);
+    else if (hd == 128)
+        go(rope_kv_kernel<128>);
+    else
+        go(rope_kv_kernel<256>);
     return dq_launch_status();
 }
 

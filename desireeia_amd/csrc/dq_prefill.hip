@@ -405,49 +405,52 @@ __global__ __launch_bounds__(256) void kv_write_batch_kernel(const float* __rest
 // (models/dense_forward.cpp:668-680 per token, table row t =
 // dq_rope_cache(pos0 + t)) on the query heads, in place, and on the
 // key heads, whose rotated rows then go into the cache with the value rows
-// (kv_quantize_row). 128-dim heads; grid (n_head + 2 n_kv, n_tok), 64 threads,
-// thread j holds dims j and j + 64.
+// (kv_quantize_row). HD-dim heads (64, 128, 256); grid (n_head + 2 n_kv,
+// n_tok), 64 threads, thread j holds dims j + 64 i.
+template <int HD>
 __global__ __launch_bounds__(64) void rope_kv_batch_kernel(float* __restrict__ q, const float* __restrict__ k,
                                                            const float* __restrict__ v, size_t q_ld, size_t kv_ld,
                                                            const float* __restrict__ rope, int n_rot, int n_head,
                                                            int n_kv, uint8_t* __restrict__ kc,
                                                            uint8_t* __restrict__ vc, size_t pos_bytes, int pos0,
                                                            DqQkvPost post) {
-    constexpr int HD = 128;
+    constexpr int QV = HD / 64;
     const int r = blockIdx.x, t = blockIdx.y, j = threadIdx.x;
     const int kind = r < n_head ? 0 : (r < n_head + n_kv ? 1 : 2);
     const int hh = kind == 0 ? r : (kind == 1 ? r - n_head : r - n_head - n_kv);
     float* qrow = q + (size_t)t * q_ld + (size_t)hh * HD;
     const float* src = kind == 0 ? qrow : (kind == 1 ? k : v) + (size_t)t * kv_ld + (size_t)hh * HD;
-    float x0 = src[j], x1 = src[j + 64];
-    dq_qkv_post(x0, x1, kind, hh, j, post);  // optional biases and QK-norm (:3318-3342)
+    float x[QV];
+#pragma unroll
+    for (int i = 0; i < QV; ++i) x[i] = src[j + 64 * i];
+    dq_qkv_post<HD>(x, kind, hh, j, post);  // optional biases and QK-norm (:3318-3342)
     if (kind < 2 && rope) {
         const float* tab = rope + (size_t)t * n_rot;
         if (n_rot == HD) {
-            dq_rope_pair(x0, x1, tab, j);
+            dq_rope_head<HD>(x, tab, j);
         } else {
             __shared__ float rowb[HD];
-            rowb[j] = x0;
-            rowb[j + 64] = x1;
+#pragma unroll
+            for (int i = 0; i < QV; ++i) rowb[j + 64 * i] = x[i];
             __syncthreads();
             const int hn = n_rot / 2;
-            if (j < hn) {
-                const float c = tab[2 * j], s = tab[2 * j + 1];
-                const float a = rowb[j], b = rowb[j + hn];
-                rowb[j] = a * c - b * s;
-                rowb[j + hn] = a * s + b * c;
+            for (int jj = j; jj < hn; jj += 64) {
+                const float c = tab[2 * jj], s = tab[2 * jj + 1];
+                const float a = rowb[jj], b = rowb[jj + hn];
+                rowb[jj] = a * c - b * s;
+                rowb[jj + hn] = a * s + b * c;
             }
             __syncthreads();
-            x0 = rowb[j];
-            x1 = rowb[j + 64];
+#pragma unroll
+            for (int i = 0; i < QV; ++i) x[i] = rowb[j + 64 * i];
         }
     }
     if (kind == 0) {
-        qrow[j] = x0;
-        qrow[j + 64] = x1;
+#pragma unroll
+        for (int i = 0; i < QV; ++i) qrow[j + 64 * i] = x[i];
         return;
     }
-    dq_q8_0_row128(x0, x1, j, (kind == 1 ? kc : vc) + (size_t)(pos0 + t) * pos_bytes + (size_t)hh * (HD / 32) * DQ_SZ_Q8_0);
+    dq_q8_0_row<HD>(x, j, (kind == 1 ? kc : vc) + (size_t)(pos0 + t) * pos_bytes + (size_t)hh * (HD / 32) * DQ_SZ_Q8_0);
 }
 
 // Sandwich norm and residual of every row (models/dense_forward.cpp
@@ -580,7 +583,7 @@ bool prefill_layer_ok(const dq_layer_t* L) {
     const int f[7] = {L->fmt_q, L->fmt_k, L->fmt_v, L->fmt_o, L->fmt_gate, L->fmt_up, L->fmt_down};
     for (int i = 0; i < 7; ++i)
         if (f[i] != DQ_FMT_Q4_K && f[i] != DQ_FMT_Q6_K && f[i] != DQ_FMT_Q8_0 && f[i] != DQ_FMT_Q4_0) return false;
-    if (L->head_dim != 128 || L->n_head_kv == 0 || L->n_head % L->n_head_kv) return false;
+    if (!dq_head_dim_supported(L->head_dim) || L->n_head_kv == 0 || L->n_head % L->n_head_kv) return false;
     if (L->n_embd % 256 || L->n_ff % 256 || ((size_t)L->n_head * L->head_dim) % 256) return false;
     if (L->n_rot == 0 || L->n_rot > L->head_dim || L->n_rot % 2) return false;
     if (L->wag && L->fmt_ag != DQ_FMT_Q4_K && L->fmt_ag != DQ_FMT_Q6_K && L->fmt_ag != DQ_FMT_Q8_0 &&
@@ -698,15 +701,23 @@ int dq_rope_kv_write_batch_post(float* d_q, const float* d_k, const float* d_v, 
                                 uint32_t n_head_kv, uint32_t hd, void* d_kc, void* d_vc, uint32_t pos0,
                                 uint32_t n_ctx, const DqQkvPost& post, void* stream) {
     if (!d_q || !d_k || !d_v || !d_kc || !d_vc) return DQ_ERR_INVALID_ARG;
-    if (hd != 128 || n_head_kv == 0) return DQ_ERR_NOT_SUPPORTED;
+    if (!dq_head_dim_supported(hd) || n_head_kv == 0) return DQ_ERR_NOT_SUPPORTED;
     if (d_rope && (n_rot == 0 || n_rot > hd || n_rot % 2)) return DQ_ERR_INVALID_ARG;
     if (q_ld < (size_t)n_head * hd || kv_ld < (size_t)n_head_kv * hd) return DQ_ERR_INVALID_ARG;
     if (n_tok == 0) return DQ_OK;
     if ((uint64_t)pos0 + n_tok > n_ctx || n_tok > 65535) return DQ_ERR_INVALID_ARG;
     const size_t pos_bytes = (size_t)n_head_kv * (hd / 32) * DQ_SZ_Q8_0;
-    rope_kv_batch_kernel<<<dim3(n_head + 2 * n_head_kv, n_tok), 64, 0, (hipStream_t)stream>>>(
-        d_q, d_k, d_v, q_ld, kv_ld, d_rope, (int)n_rot, (int)n_head, (int)n_head_kv, (uint8_t*)d_kc, (uint8_t*)d_vc,
-        pos_bytes, (int)pos0, post);
+    auto go = [&](auto kern) {
+        kern<<<dim3(n_head + 2 * n_head_kv, n_tok), 64, 0, (hipStream_t)stream>>>(
+            d_q, d_k, d_v, q_ld, kv_ld, d_rope, (int)n_rot, (int)n_head, (int)n_head_kv, (uint8_t*)d_kc,
+            (uint8_t*)d_vc, pos_bytes, (int)pos0, post);
+    };
+    if (hd == 64)
+        go(rope_kv_batch_kernel<64>);
+    else if (hd == 128)
+        go(rope_kv_batch_kernel<128>);
+    else
+        go(rope_kv_batch_kernel<256>);
     return dq_launch_status();
 }
 

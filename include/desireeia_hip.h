@@ -170,7 +170,8 @@ int dq_kv_write(const float* d_k, const float* d_v, uint32_t n_head_kv, uint32_t
  * core/engine.h:806-811): q [n_head][hd] fp32 (after RoPE), keys/values at
  * positions [cc_start, pos], query head h reads KV head h / (n_head /
  * n_head_kv), scores scaled by 1/sqrt(hd), softmax, out [n_head][hd] fp32.
- * hd = 128 and n_head / n_head_kv in {1, 2, 4, 8}; other shapes: -2.
+ * hd in {64, 128, 256}, n_head / n_head_kv in {1, 2, 4, 8} and n_head * hd a
+ * multiple of 256; other shapes: -2.
  * d_work holds dq_attn_workspace_bytes(n_ctx) bytes of per-tile partials
  * (calls sharing a workspace must not overlap). d_pos as for dq_kv_write. */
 int dq_attn_workspace_bytes(uint32_t n_head, uint32_t n_head_kv, uint32_t hd, uint32_t n_ctx, size_t* bytes);
@@ -224,7 +225,8 @@ int dq_kv_write_batch(const float* d_k, const float* d_v, size_t ld, uint32_t n_
  * :3347-3362 per token): NeoX RoPE of every query head in place and of every
  * key head with the table row d_rope + t * n_rot (dq_rope_cache(pos0 + t);
  * NULL = no RoPE), then the Q8_0 rows of the rotated k and of v at pos0 + t
- * (as dq_kv_write_batch). q: [n_tok][q_ld], k, v: [n_tok][kv_ld]. hd = 128. */
+ * (as dq_kv_write_batch). q: [n_tok][q_ld], k, v: [n_tok][kv_ld]. hd in {64,
+ * 128, 256}. */
 int dq_rope_kv_write_batch(float* d_q, const float* d_k, const float* d_v, size_t q_ld, size_t kv_ld,
                            const float* d_rope, uint32_t n_rot, uint32_t n_tok, uint32_t n_head, uint32_t n_head_kv,
                            uint32_t hd, void* d_kc, void* d_vc, uint32_t pos0, uint32_t n_ctx, void* stream);
@@ -263,7 +265,7 @@ int dq_rope_cache(float* cache, uint32_t n_rot, uint32_t pos, float theta_base);
  * dq_silu_quant: silu(gate) * up (:53-55), then the same quantizer.
  * dq_rope_kv_write: NeoX RoPE (:668-680) of q (in place) and k with the
  *   cos/sin table d_rope (dq_rope_cache; NULL = no RoPE), then the Q8_0 rows
- *   of k and v into the caches at pos (as dq_kv_write). hd = 128. */
+ *   of k and v into the caches at pos (as dq_kv_write). hd in {64, 128, 256}. */
 int dq_norm_quant(const float* d_a, const float* d_b, float* d_h, const float* d_w, size_t n, float eps,
                   int8_t* d_q, float* d_scale, int32_t* d_isum, void* stream);
 int dq_silu_quant(const float* d_gate, const float* d_up, size_t n, int8_t* d_q, float* d_scale, int32_t* d_isum,
@@ -296,7 +298,7 @@ int dq_rope_kv_write(float* d_q, const float* d_k, const float* d_v, const float
  * device matrices (dq_weights_pack), each of any of the four formats (Q4_K /
  * Q6_K read the per-256 activation, Q8_0 / Q4_0 the per-32 one, as the
  * reference CPU GEMVs of those formats do); n_embd, n_ff and n_head*head_dim
- * multiples of 256, head_dim 128; other shapes: -2. Q/K/V and gate/up each
+ * multiples of 256, head_dim 64, 128 or 256; other shapes: -2. Q/K/V and gate/up each
  * run as one grouped GEMV. x and x_out are device vectors of n_embd floats (they
  * may not alias); d_rope is the device copy of dq_rope_cache(pos); the KV
  * caches are those of dq_kv_write for this layer. d_pos as for dq_kv_write
@@ -616,10 +618,10 @@ void cuda_drop_graphs(void);
  * cuda_qkv_attention_out: Q/K/V (+ optional biases), RoPE, the new KV rows
  * (device cache and host_k_row / host_v_row), attention and Wo.
  * cuda_layer_forward: the whole dense layer; x stays on the device between
- * layers (upload_x on the first, download_x on the last). Features outside
- * the plain dense layer (attention gate, QK-norm, sandwich norms, GELU,
- * per-layer RoPE/window slots, embedding from token) and head_dim != 128:
- * NOT_SUPPORTED. */
+ * layers (upload_x on the first, download_x on the last). Q/K/V biases,
+ * per-head QK-norm, sandwich norms, gated GELU, the attention output gate,
+ * per-layer slots (dyn_all / rope_all) and the embedding from the drawn token
+ * are taken; head_dim other than 64, 128 or 256: NOT_SUPPORTED. */
 int cuda_attention_out(const void* d_wo_qs, const void* d_wo_scale, const float* q, uint32_t n_head,
                        uint32_t heads_per_kv, uint32_t head_dim, uint32_t kv_dim, size_t layer_off, uint32_t cc_start,
                        uint32_t pos, size_t n_embd, size_t q_dim, float* proj, int kv_quantized, size_t row_bytes);
@@ -639,9 +641,10 @@ int cuda_layer_forward(const CudaLayerArgs* args);
  *   last (rows from x_out_row0 on), which also copies every K/V row the
  *   prompt wrote into host_kcache / host_vcache and synchronises once. RoPE
  *   tables: rope_caches uploaded when upload_rope into slot rope_slot (0-3);
- *   NULL = no RoPE. Matrices: uploads of this library; biases, QK-norm,
- *   sandwich norms, the attention gate, GELU and head_dim != 128:
- *   NOT_SUPPORTED, before any device work.
+ *   NULL = no RoPE. Matrices: uploads of this library; biases, per-head
+ *   QK-norm, sandwich norms, the attention gate and gated GELU are taken;
+ *   head_dim other than 64, 128 or 256: NOT_SUPPORTED, before any device
+ *   work.
  * cuda_prefill_chunk_tokens: tokens per chunk, 8 per CU within [1024, 4096]. */
 int cuda_attention_batch(const float* q_all, float* out_all, uint32_t n_tokens, uint32_t n_head,
                          uint32_t heads_per_kv, uint32_t head_dim, uint32_t q_dim, size_t row_bytes, size_t pos_bytes,

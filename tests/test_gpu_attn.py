@@ -21,15 +21,15 @@ def rel(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-def host_cache(orc, n_pos, n_kv, seed):
+def host_cache(orc, n_pos, n_kv, seed, hd=HD):
     rng = np.random.default_rng(seed)
-    k = rng.standard_normal((n_pos, n_kv, HD)).astype(np.float32)
-    v = rng.standard_normal((n_pos, n_kv, HD)).astype(np.float32)
+    k = rng.standard_normal((n_pos, n_kv, hd)).astype(np.float32)
+    v = rng.standard_normal((n_pos, n_kv, hd)).astype(np.float32)
     return orc.kv_quantize_row(k.reshape(-1)), orc.kv_quantize_row(v.reshape(-1))
 
 
-def device_cache(gpu, kc, vc, n_ctx, n_kv):
-    c = ops.KVCache(n_ctx, n_kv, HD, device=gpu)
+def device_cache(gpu, kc, vc, n_ctx, n_kv, hd=HD):
+    c = ops.KVCache(n_ctx, n_kv, hd, device=gpu)
     c.k[:kc.size] = torch.from_numpy(kc).to(gpu)
     c.v[:vc.size] = torch.from_numpy(vc).to(gpu)
     return c
@@ -93,6 +93,38 @@ def test_attention_vs_oracle(gpu, orc, n_head, n_kv, pos, cc_start):
         assert rel(out[h * HD:(h + 1) * HD], want[h * HD:(h + 1) * HD]) <= 10 * TOL
 
 
+HD_CASES = [
+    # hd, n_head, n_kv, pos, cc_start
+    (64, 16, 4, 1000, 0),     # GQA 4, 16 tiles
+    (64, 32, 4, 4096, 0),     # GQA 8, 65 tiles
+    (64, 8, 8, 70, 0),        # MHA, a partial second tile
+    (64, 8, 1, 0, 0),         # one key, 8 heads on one KV head
+    (256, 8, 2, 1000, 0),     # GQA 4
+    (256, 16, 2, 4096, 100),  # GQA 8, window start
+    (256, 4, 4, 63, 0),       # MHA, exactly one tile
+    (256, 2, 1, 20000, 0),    # GQA 2, long context
+]
+
+
+@pytest.mark.parametrize("hd,n_head,n_kv,pos,cc_start", HD_CASES)
+def test_attention_head_dims(gpu, orc, hd, n_head, n_kv, pos, cc_start):
+    """Heads of 64 and 256 values (rows of 2 and 8 Q8_0 blocks): the same
+    bound against the oracle and its fp64 evaluation, head by head."""
+    print(f"attn hd={hd} n_head={n_head} n_kv={n_kv} pos={pos} cc_start={cc_start}", flush=True)
+    kc, vc = host_cache(orc, pos + 1, n_kv, seed=pos + n_head + hd, hd=hd)
+    q = np.random.default_rng(pos + hd).standard_normal(n_head * hd).astype(np.float32)
+    cache = device_cache(gpu, kc, vc, pos + 5, n_kv, hd=hd)
+    out = ops.attention_decode(torch.from_numpy(q).to(gpu), cache, n_head, pos, cc_start).cpu().numpy()
+    want = orc.attn_decode(q, kc, vc, n_head, n_kv, hd, cc_start, pos)
+    e = rel(out, want)
+    print(f"  rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    if pos <= 4096:
+        assert rel(out, orc.attn_decode(q, kc, vc, n_head, n_kv, hd, cc_start, pos, f64=True)) <= TOL
+    for h in range(n_head):
+        assert rel(out[h * hd:(h + 1) * hd], want[h * hd:(h + 1) * hd]) <= 10 * TOL
+
+
 def test_attention_device_pos_graph(gpu, orc):
     """Position in device memory, captured once in a HIP graph and replayed for
     successive positions: every replay matches the eager call and the oracle."""
@@ -124,7 +156,9 @@ def test_attention_device_pos_graph(gpu, orc):
 def test_attention_unsupported(gpu):
     n = ctypes_size()
     lib = _lib.load()
-    assert lib.dq_attn_workspace_bytes(32, 8, 64, 100, n) == -2   # hd 64
+    assert lib.dq_attn_workspace_bytes(32, 8, 96, 100, n) == -2   # hd 96
+    assert lib.dq_attn_workspace_bytes(32, 8, 32, 100, n) == -2   # hd 32
+    assert lib.dq_attn_workspace_bytes(6, 2, 64, 100, n) == -2    # 384 outputs: not whole 256-blocks
     assert lib.dq_attn_workspace_bytes(24, 8, 128, 100, n) == -2  # 3 heads per KV head
     assert lib.dq_attn_workspace_bytes(30, 8, 128, 100, n) == -2  # not a multiple
 
@@ -162,22 +196,26 @@ def test_attention_quantized_output(gpu, orc):
         assert np.array_equal(act.isum.cpu().numpy(), wi)
 
 
-@pytest.mark.parametrize("n_head,n_kv,pos,rope,quant", [
-    (32, 8, 4096, True, True),    # config 4's step
-    (32, 8, 0, True, True),       # the first token: the new row is the only key
-    (32, 8, 64, True, False),     # the new row starts a tile
-    (16, 16, 300, False, True),   # MHA, no RoPE: quantization falls back to a separate pass
-    (64, 8, 1000, True, True),    # GQA 8
+@pytest.mark.parametrize("HD,n_head,n_kv,pos,rope,quant", [
+    (128, 32, 8, 4096, True, True),    # config 4's step
+    (128, 32, 8, 0, True, True),       # the first token: the new row is the only key
+    (128, 32, 8, 64, True, False),     # the new row starts a tile
+    (128, 16, 16, 300, False, True),   # MHA, no RoPE: quantization falls back to a separate pass
+    (128, 64, 8, 1000, True, True),    # GQA 8
+    (64, 16, 4, 500, True, True),      # 64-value heads: RoPE pairs in lanes j and j + 32
+    (64, 8, 8, 0, True, False),
+    (256, 8, 2, 129, True, True),      # 256-value heads: two RoPE pairs per lane
+    (256, 16, 2, 64, True, True),
 ])
-def test_attention_rope_kv_fused(gpu, orc, n_head, n_kv, pos, rope, quant):
+def test_attention_rope_kv_fused(gpu, orc, HD, n_head, n_kv, pos, rope, quant):
     """dq_attn_rope_kv_decode: RoPE of the raw q and k, the new K/V rows at pos
     (bit-exact: kv_quantize_row of the oracle's rotated k and of v), attention
     over [0, pos] within 1e-3, the per-256 quantization of the output
     bit-exact on the kernel's own float output; the prior rows untouched."""
-    print(f"fused attn n_head={n_head} n_kv={n_kv} pos={pos} rope={rope} quant={quant}", flush=True)
+    print(f"fused attn hd={HD} n_head={n_head} n_kv={n_kv} pos={pos} rope={rope} quant={quant}", flush=True)
     n_ctx = pos + 3
-    kc, vc = host_cache(orc, pos, n_kv, seed=pos + 3)
-    cache = device_cache(gpu, kc, vc, n_ctx, n_kv)
+    kc, vc = host_cache(orc, pos, n_kv, seed=pos + 3, hd=HD)
+    cache = device_cache(gpu, kc, vc, n_ctx, n_kv, hd=HD)
     rng = np.random.default_rng(pos + 4)
     q = rng.standard_normal(n_head * HD).astype(np.float32)
     k = rng.standard_normal(n_kv * HD).astype(np.float32)
@@ -218,18 +256,18 @@ def test_attention_rope_kv_fused(gpu, orc, n_head, n_kv, pos, rope, quant):
         assert np.array_equal(act.isum.cpu().numpy(), wi)
 
 
-@pytest.mark.parametrize("fused", [True, False])
-def test_attention_wide_value_range(gpu, orc, fused):
+@pytest.mark.parametrize("fused,HD", [(True, 128), (False, 128), (True, 64), (True, 256)])
+def test_attention_wide_value_range(gpu, orc, fused, HD):
     """Large query, key and value magnitudes (scores in the tens of thousands,
     one dominant position; the new row's V block scale ~1000x the others):
     the weight operand scale is the maximum over every row of the tile, so no
     fp16 operand overflows. Output finite and within 1e-3 of the oracle."""
     n_head, n_kv, pos = 8, 2, 70
-    print(f"wide range fused={fused}", flush=True)
+    print(f"wide range fused={fused} hd={HD}", flush=True)
     n_ctx = pos + 2
     rng = np.random.default_rng(pos)
     kc, vc = (orc.kv_quantize_row(rng.standard_normal(pos * n_kv * HD).astype(np.float32)) for _ in range(2))
-    cache = device_cache(gpu, kc, vc, n_ctx, n_kv)
+    cache = device_cache(gpu, kc, vc, n_ctx, n_kv, hd=HD)
     q = (300 * rng.standard_normal(n_head * HD)).astype(np.float32)
     k = (200 * rng.standard_normal(n_kv * HD)).astype(np.float32)
     v = (1000 * rng.standard_normal(n_kv * HD)).astype(np.float32)

@@ -315,9 +315,8 @@ def test_qkv_attention_out(lib, orc):
     lib.cuda_kv_cache_release()
 
 
-def make_layer(lib, orc, E, n_head, n_kv, F, types, seed):
+def make_layer(lib, orc, E, n_head, n_kv, F, types, seed, hd=128):
     from oracle.oracle import LayerArgs
-    hd = 128
     qd, kvd = n_head * hd, n_kv * hd
     names = ("q", "k", "v", "o", "gate", "up", "down")
     shapes = {"q": (qd, E), "k": (kvd, E), "v": (kvd, E), "o": (E, qd), "gate": (F, E), "up": (F, E),
@@ -333,15 +332,15 @@ def make_layer(lib, orc, E, n_head, n_kv, F, types, seed):
     return mats, an, fn, oa
 
 
-def qwen_extras(oa, n_head, n_kv, seed):
+def qwen_extras(oa, n_head, n_kv, seed, hd=128):
     """Q/K/V biases and per-head QK-norm weights (Qwen-style layer), set on the
     oracle's arguments; returned for the engine's arguments."""
     rng = np.random.default_rng(seed)
-    ex = {"bq": rng.standard_normal(n_head * 128).astype(np.float32),
-          "bk": rng.standard_normal(n_kv * 128).astype(np.float32),
-          "bv": (0.5 * rng.standard_normal(n_kv * 128)).astype(np.float32),
-          "q_norm": (1 + 0.1 * rng.standard_normal(128)).astype(np.float32),
-          "k_norm": (0.5 + 0.1 * rng.standard_normal(128)).astype(np.float32)}
+    ex = {"bq": rng.standard_normal(n_head * hd).astype(np.float32),
+          "bk": rng.standard_normal(n_kv * hd).astype(np.float32),
+          "bv": (0.5 * rng.standard_normal(n_kv * hd)).astype(np.float32),
+          "q_norm": (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32),
+          "k_norm": (0.5 + 0.1 * rng.standard_normal(hd)).astype(np.float32)}
     for nm, v in ex.items():
         setattr(oa, nm, v.ctypes.data)
     return ex
@@ -352,8 +351,8 @@ def set_extras(A, ex):
     A.q_norm_w, A.k_norm_w = ex["q_norm"].ctypes.data, ex["k_norm"].ctypes.data
 
 
-def layer_args(mats, an, fn, E, n_head, n_kv, F, layer_off, pos, rope, x, x_out, upload_x, download_x, upload_dyn):
-    hd = 128
+def layer_args(mats, an, fn, E, n_head, n_kv, F, layer_off, pos, rope, x, x_out, upload_x, download_x, upload_dyn,
+               hd=128):
     A = _lib.CudaLayerArgs()
     for nm, key in (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo"), ("gate", "wgate"), ("up", "wup"),
                     ("down", "wdown")):
@@ -497,6 +496,52 @@ def test_layer_forward_chain(lib, orc):
     lib.cuda_kv_cache_release()
 
 
+@pytest.mark.parametrize("hd,n_head,n_kv,qwen", [(64, 16, 4, False), (64, 16, 4, True), (256, 8, 2, False),
+                                                (256, 8, 2, True)])
+def test_layer_forward_head_dims(lib, orc, hd, n_head, n_kv, qwen):
+    """cuda_layer_forward (one token) and cuda_layer_forward_batch (a 24-token
+    chunk) with heads of 64 and 256 values, optionally Qwen-style, against
+    the oracle's decode and prefill layers."""
+    print(f"engine layer hd={hd} heads={n_head}/{n_kv} qwen={qwen}", flush=True)
+    E, F, n_ctx, pos, T = 1024, 2048, 96, 40, 24
+    kc, vc, pb = prior_cache(orc, 1, n_ctx, n_kv, hd, pos, seed=hd + 1)
+    assert lib.cuda_kv_cache_reserve(kc.size)
+    assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+    mats, an, fn, oa = make_layer(lib, orc, E, n_head, n_kv, F, (Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K), hd + 2,
+                                  hd=hd)
+    an *= 0.25 / np.sqrt(E)  # O(1) scores and FFN activations
+    fn *= 0.3 / np.sqrt(E)
+    ex = qwen_extras(oa, n_head, n_kv, hd + 3, hd=hd) if qwen else None
+    # one token at pos
+    x = synth.gen_act(E, seed=hd + 4)
+    out = np.full(E, np.nan, np.float32)
+    rope1 = orc.rope_cache(hd, pos, 500000.0)  # kept alive: the arguments hold its address
+    A = layer_args(mats, an, fn, E, n_head, n_kv, F, 0, pos, rope1, x, out, 1, 1, 1, hd=hd)
+    if ex:
+        set_extras(A, ex)
+    assert lib.cuda_layer_forward(ctypes.byref(A)) == OK
+    k0, v0 = kc.copy(), vc.copy()
+    want = orc.layer_decode(oa, k0, v0, pos, x)[0]
+    e = rel(out, want)
+    print(f"  decode rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    # a chunk of T tokens after it (positions pos + 1 ...)
+    xs = np.random.default_rng(hd + 5).standard_normal((T, E)).astype(np.float32)
+    rope = np.stack([orc.rope_cache(hd, pos + 1 + i, 500000.0) for i in range(T)])
+    outs = np.full((T, E), np.nan, np.float32)
+    B = batch_args(mats, an, fn, E, n_head, n_kv, F, 0, pos + 1, T, 0, T, rope, xs, outs, None, None, 1, 1, 1, hd=hd)
+    if ex:
+        set_extras(B, ex)
+    assert lib.cuda_layer_forward_batch(ctypes.byref(B)) == OK
+    wantb = orc.layer_prefill(oa, k0, v0, pos + 1, xs)
+    e = rel(outs, wantb)
+    print(f"  batch rel err {e:.3e}", flush=True)
+    assert e <= TOL_QWEN_BATCH
+    for m in mats.values():
+        m.free()
+    lib.cuda_kv_cache_release()
+
+
 def test_prefill_chunk_tokens(lib):
     import torch
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -540,8 +585,7 @@ def test_attention_batch(lib, orc):
 
 
 def batch_args(mats, an, fn, E, n_head, n_kv, F, layer_off, pos0, n_tok, x_row0, n_total, rope, x, x_out, hk, hv,
-               upload_x, download_x, upload_rope):
-    hd = 128
+               upload_x, download_x, upload_rope, hd=128):
     A = _lib.CudaLayerBatchArgs()
     for nm, key in (("q", "wq"), ("k", "wk"), ("v", "wv"), ("o", "wo"), ("gate", "wgate"), ("up", "wup"),
                     ("down", "wdown")):
@@ -713,7 +757,8 @@ def test_head_and_pipelined_decode(lib, orc):
     rng = np.random.default_rng(75)
     norm = (1 + 0.05 * rng.standard_normal(E)).astype(np.float32)
     x = synth.gen_act(E, seed=76)
-    A = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos, orc.rope_cache(128, pos, 500000.0), x, None, 1, 0, 1)
+    rope0 = orc.rope_cache(128, pos, 500000.0)  # kept alive: the arguments hold its address
+    A = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos, rope0, x, None, 1, 0, 1)
     assert lib.cuda_layer_forward(ctypes.byref(A)) == OK
     xd = np.empty(E, np.float32)
     assert lib.cuda_fetch_x(P(xd), E) == OK
@@ -738,8 +783,8 @@ def test_head_and_pipelined_decode(lib, orc):
     assert tok.value == int(so.top_k_select(y, 1)[0])
     # next step: x is the drawn token's embedding row, built on the device
     out = np.full(E, np.nan, np.float32)
-    A2 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos + 1, orc.rope_cache(128, pos + 1, 500000.0), None, out, 1, 1,
-                    1)
+    rope1 = orc.rope_cache(128, pos + 1, 500000.0)
+    A2 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, pos + 1, rope1, None, out, 1, 1, 1)
     A2.x_from_token, A2.embd_qs, A2.embd_scale, A2.embd_mul = 1, emb.qs, emb.sc, 0.0
     assert lib.cuda_layer_forward(ctypes.byref(A2)) == OK
     xe = orc.dequantize_row(Q8_0, np.ascontiguousarray(emb.w[tok.value]), E)

@@ -29,11 +29,11 @@ class HostLayer:
     (n_head, n_head_kv, mats[nm].fmt/rows/cols, cache.pos_bytes)."""
 
     def __init__(self, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None,
-                 qwen=False, gelu=False, sandwich=False, attn_gate=False):
+                 qwen=False, gelu=False, sandwich=False, attn_gate=False, hd=128):
         from types import SimpleNamespace as NS
 
         from oracle.oracle import LayerArgs
-        hd = 128
+        self.hd = self.head_dim = hd
         qd, kvd = n_head * hd, n_kv * hd
         # Q4_K_M mix: Q4_K everywhere but attn_v and ffn_down (Q6_K)
         shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
@@ -92,11 +92,11 @@ class HostLayer:
 
 
 def make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale=(1.0, 1.0), types=None, qwen=False,
-               gelu=False, sandwich=False, attn_gate=False):
-    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types, qwen, gelu, sandwich, attn_gate)
+               gelu=False, sandwich=False, attn_gate=False, hd=128):
+    h = HostLayer(orc, E, n_head, n_kv, F, n_ctx, n_prior, seed, norm_scale, types, qwen, gelu, sandwich, attn_gate, hd)
     mats = {nm: ops.QuantMatrix.from_gguf(qt, h.keep[nm], r, c, device=gpu) for nm, (qt, r, c) in h.shapes.items()}
     ex = {nm: torch.from_numpy(v) for nm, v in h.extras.items()}
-    layer = ops.DecoderLayer(mats, torch.from_numpy(h.attn_norm), torch.from_numpy(h.ffn_norm), n_head, n_kv, 128,
+    layer = ops.DecoderLayer(mats, torch.from_numpy(h.attn_norm), torch.from_numpy(h.ffn_norm), n_head, n_kv, hd,
                              n_ctx, device=gpu,
                              bias=(ex["bq"], ex["bk"], ex["bv"]) if ex else None,
                              qk_norm=(ex["q_norm"], ex["k_norm"]) if ex else None, act_gelu=gelu,
@@ -148,6 +148,38 @@ def test_layer_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos, qwen):
         assert np.array_equal(dev[:pos * pb], host[:pos * pb])  # prior rows untouched
         a = dequant_rows(orc, dev[pos * pb:(pos + 1) * pb], kvd)
         b = dequant_rows(orc, host[pos * pb:(pos + 1) * pb], kvd)
+        assert rel(a, b) <= TOL
+
+
+@pytest.mark.parametrize("hd,E,n_head,n_kv,F,pos,kind", [
+    (64, 1024, 16, 4, 2048, 300, None),     # 64-value heads, GQA 4
+    (64, 1024, 16, 4, 2048, 300, "qwen"),   # with Q/K/V biases and per-head QK-norm of 64 values
+    (64, 512, 8, 8, 1024, 0, None),         # MHA, first token
+    (256, 1024, 8, 2, 2048, 300, None),     # 256-value heads, GQA 4
+    (256, 1024, 8, 2, 2048, 300, "gemma"),  # with gated GELU and sandwich norms
+    (256, 2048, 8, 4, 4096, 1000, "qwen"),
+])
+def test_layer_head_dims(gpu, orc, hd, E, n_head, n_kv, F, pos, kind):
+    """Decoder layers with 64- and 256-value heads (the fused RoPE / K/V write
+    / attention kernel at rows of 2 and 8 Q8_0 blocks, QK-norm over the head's
+    values, RoPE pairs across lanes at 64) against the oracle's layer, which
+    takes the head size as a parameter."""
+    print(f"layer hd={hd} E={E} heads={n_head}/{n_kv} F={F} pos={pos} kind={kind}", flush=True)
+    n_ctx = pos + 2
+    layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos, seed=E + pos + hd,
+                                           qwen=kind == "qwen", gelu=kind == "gemma", sandwich=kind == "gemma",
+                                           hd=hd)
+    x = np.random.default_rng(pos + 2).standard_normal(E).astype(np.float32)
+    want = orc.layer_decode(args, kc, vc, pos, x)[0]
+    got = layer.decode(torch.from_numpy(x).to(gpu), pos).cpu().numpy()
+    e = rel(got, want)
+    print(f"  layer rel err {e:.3e}", flush=True)
+    assert e <= TOL
+    pb = layer.cache.pos_bytes
+    for dev, host in ((layer.cache.k.cpu().numpy(), kc), (layer.cache.v.cpu().numpy(), vc)):
+        assert np.array_equal(dev[:pos * pb], host[:pos * pb])
+        a = dequant_rows(orc, dev[pos * pb:(pos + 1) * pb], n_kv * hd)
+        b = dequant_rows(orc, host[pos * pb:(pos + 1) * pb], n_kv * hd)
         assert rel(a, b) <= TOL
 
 
@@ -215,23 +247,27 @@ def test_silu_quant_bit_exact(gpu, orc):
     assert np.allclose(act.scale.cpu().numpy(), d, rtol=1e-6)
 
 
-def test_rope_kv_write_bit_exact(gpu, orc):
-    n_head, n_kv, hd, pos, n_ctx = 32, 8, 128, 4096, 4097
+@pytest.mark.parametrize("hd,n_rot", [(128, 128), (128, 64), (64, 64), (64, 32), (256, 256), (256, 64)])
+def test_rope_kv_write_bit_exact(gpu, orc, hd, n_rot):
+    """RoPE of q and k (full or partial rotation) and the new K/V rows,
+    bit-exact against the oracle, at 64-, 128- and 256-value heads."""
+    print(f"rope_kv_write hd={hd} n_rot={n_rot}", flush=True)
+    n_head, n_kv, pos, n_ctx = 32, 8, 4096, 4097
     rng = np.random.default_rng(6)
     q = rng.standard_normal(n_head * hd).astype(np.float32)
     k = rng.standard_normal(n_kv * hd).astype(np.float32)
     v = rng.standard_normal(n_kv * hd).astype(np.float32)
     cache = ops.KVCache(n_ctx, n_kv, hd, device=gpu)
-    rope = ops.rope_cache(hd, pos, 500000.0)
+    rope = ops.rope_cache(n_rot, pos, 500000.0)
     qd = torch.from_numpy(q).to(gpu)
     kd, vd, rd = torch.from_numpy(k).to(gpu), torch.from_numpy(v).to(gpu), rope.to(gpu)
     lib = _lib.load()
-    _lib.check(lib.dq_rope_kv_write(ops._ptr(qd), ops._ptr(kd), ops._ptr(vd), ops._ptr(rd), n_head, n_kv, hd, hd,
+    _lib.check(lib.dq_rope_kv_write(ops._ptr(qd), ops._ptr(kd), ops._ptr(vd), ops._ptr(rd), n_head, n_kv, hd, n_rot,
                                     ops._ptr(cache.k), ops._ptr(cache.v), pos, None, n_ctx, ops._stream()))
     torch.cuda.synchronize()
-    c = orc.rope_cache(hd, pos, 500000.0)
-    qr = np.concatenate([orc.rope_neox(q[h * hd:(h + 1) * hd], hd, c) for h in range(n_head)])
-    kr = np.concatenate([orc.rope_neox(k[h * hd:(h + 1) * hd], hd, c) for h in range(n_kv)])
+    c = orc.rope_cache(n_rot, pos, 500000.0)
+    qr = np.concatenate([orc.rope_neox(q[h * hd:(h + 1) * hd], n_rot, c) for h in range(n_head)])
+    kr = np.concatenate([orc.rope_neox(k[h * hd:(h + 1) * hd], n_rot, c) for h in range(n_kv)])
     assert np.array_equal(qd.cpu().numpy(), qr)
     pb = cache.pos_bytes
     assert np.array_equal(cache.k.cpu().numpy()[pos * pb:], orc.kv_quantize_row(kr))

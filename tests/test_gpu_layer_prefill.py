@@ -51,7 +51,7 @@ def chain(layer, keep, orc, x, pos0, gemm, attention):
     functions (norms, RoPE, K/V rows, SiLU on the host with the oracle's
     arithmetic)."""
     T = x.shape[0]
-    nh, nkv = layer.n_head, layer.n_head_kv
+    nh, nkv, HD = layer.n_head, layer.n_head_kv, layer.head_dim
     xn = np.stack([orc.rms_norm(x[t], keep["attn_norm"], 1e-5) for t in range(T)])
     q, k, v = gemm("q", xn), gemm("k", xn), gemm("v", xn)
     if "bq" in keep:  # Qwen-style: biases, then per-head QK-norm, before RoPE
@@ -99,7 +99,7 @@ def oracle_fns(layer, keep, orc, kc, vc, pos0, T):
     def attention(q, kr, vr):
         kk, vv = kc[:(pos0 + T) * pb].copy(), vc[:(pos0 + T) * pb].copy()
         kk[pos0 * pb:], vv[pos0 * pb:] = kr, vr
-        return orc.attn_prefill(q, kk, vv, T, layer.n_head, layer.n_head_kv, HD, pos0).reshape(T, -1)
+        return orc.attn_prefill(q, kk, vv, T, layer.n_head, layer.n_head_kv, layer.head_dim, pos0).reshape(T, -1)
     return gemm, attention
 
 
@@ -110,7 +110,7 @@ def gpu_fns(gpu, layer, kc, vc, pos0, T):
         return ops.gemm(layer.mats[nm], torch.from_numpy(np.ascontiguousarray(inp, np.float32)).to(gpu)).cpu().numpy()
 
     def attention(q, kr, vr):
-        c = ops.KVCache(pos0 + T, layer.n_head_kv, HD, device=gpu)
+        c = ops.KVCache(pos0 + T, layer.n_head_kv, layer.head_dim, device=gpu)
         c.k[:pos0 * pb] = torch.from_numpy(kc[:pos0 * pb]).to(gpu)
         c.v[:pos0 * pb] = torch.from_numpy(vc[:pos0 * pb]).to(gpu)
         c.k[pos0 * pb:] = torch.from_numpy(kr).to(gpu)
@@ -134,15 +134,19 @@ Q40_FFN = {"gate": synth.Q4_0, "up": synth.Q4_0, "v": synth.Q8_0}
     (512, 8, 2, 1536, 20, 40, None, "gelu"),      # gated GELU FFN (gelu_tanh)
     (512, 8, 2, 1536, 20, 40, None, "gemma"),     # gated GELU and sandwich norms
     (512, 8, 2, 1536, 20, 40, None, "gate"),      # per-head attention output gate
+    (1024, 16, 4, 2048, 20, 40, None, "hd64"),    # 64-value heads
+    (1024, 16, 4, 2048, 20, 40, None, "hd64q"),   # 64-value heads, biases and QK-norm
+    (1024, 8, 2, 2048, 20, 40, None, "hd256"),    # 256-value heads
 ])
 def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, types, qwen):
     print(f"layer_prefill E={E} heads={n_head}/{n_kv} F={F} pos0={pos0} n_tok={n_tok} types={types} qwen={qwen}",
           flush=True)
     n_ctx = pos0 + n_tok + 2
+    hd = {"hd64": 64, "hd64q": 64, "hd256": 256}.get(qwen, 128)
     layer, args, keep, kc, vc = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos0, seed=E + pos0 + n_tok,
-                                           norm_scale=conditioned(E), types=types, qwen=qwen is True,
+                                           norm_scale=conditioned(E), types=types, qwen=qwen is True or qwen == "hd64q",
                                            gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma",
-                                           attn_gate=qwen == "gate")
+                                           attn_gate=qwen == "gate", hd=hd)
     layer.gelu = qwen in ("gelu", "gemma")
     x = np.random.default_rng(n_tok).standard_normal((n_tok, E)).astype(np.float32)
     og, oa = oracle_fns(layer, keep, orc, kc, vc, pos0, n_tok)
@@ -180,7 +184,7 @@ def test_layer_prefill_vs_oracle(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, type
     assert np.array_equal(kd[:pos0 * pb], kc[:pos0 * pb]) and np.array_equal(vd[:pos0 * pb], vc[:pos0 * pb])
     assert np.array_equal(kd[pos0 * pb:(pos0 + n_tok) * pb], G["kr"])
     assert np.array_equal(vd[pos0 * pb:(pos0 + n_tok) * pb], G["vr"])
-    kvd = n_kv * HD
+    kvd = n_kv * hd
     for dev, host in ((kd, kc1), (vd, vc1)):
         a = dequant_rows(orc, dev[pos0 * pb:(pos0 + n_tok) * pb], n_tok * kvd)
         b = dequant_rows(orc, host[pos0 * pb:(pos0 + n_tok) * pb], n_tok * kvd)

@@ -48,23 +48,23 @@ def rel(a, b):
 
 
 def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, gelu=False, sandwich=False,
-         attn_gate=False):
+         attn_gate=False, hd=HD):
     from oracle.oracle import LayerArgs
-    qd, kvd = n_head * HD, n_kv * HD
+    qd, kvd = n_head * hd, n_kv * hd
     shapes = {"q": (Q4K, qd, E), "k": (Q4K, kvd, E), "v": (Q6K, kvd, E), "o": (Q4K, E, qd),
               "gate": (Q4K, F, E), "up": (Q4K, F, E), "down": (Q6K, E, F)}
     w = {nm: synth.gen_weights(qt, r, c, seed=seed + i) for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
     rng = np.random.default_rng(seed)
     w["attn_norm"] = (norm_scale[0] * (1 + 0.02 * rng.standard_normal(E))).astype(np.float32)
     w["ffn_norm"] = (norm_scale[1] * (1 + 0.02 * rng.standard_normal(E))).astype(np.float32)
-    pb = n_kv * (HD // 32) * 34
+    pb = n_kv * (hd // 32) * 34
     n_ctx = pos + 1
     kc = np.zeros(n_ctx * pb, np.uint8)
     vc = np.zeros(n_ctx * pb, np.uint8)
     if pos:
         kc[:pos * pb] = orc.kv_quantize_row(rng.standard_normal(pos * kvd).astype(np.float32))
         vc[:pos * pb] = orc.kv_quantize_row(rng.standard_normal(pos * kvd).astype(np.float32))
-    args = LayerArgs(E, n_head, n_kv, HD, F, 1e-5, 500000.0, *[shapes[nm][0] for nm in NAMES])
+    args = LayerArgs(E, n_head, n_kv, hd, F, 1e-5, 500000.0, *[shapes[nm][0] for nm in NAMES])
     for nm in NAMES:
         setattr(args, "w" + nm, w[nm].ctypes.data)
     args.attn_norm = w["attn_norm"].ctypes.data
@@ -75,8 +75,8 @@ def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, 
         w["bq"] = rng.standard_normal(qd).astype(np.float32)
         w["bk"] = rng.standard_normal(kvd).astype(np.float32)
         w["bv"] = (0.5 * rng.standard_normal(kvd)).astype(np.float32)
-        w["q_norm"] = (1.0 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
-        w["k_norm"] = (0.5 + 0.1 * rng.standard_normal(HD)).astype(np.float32)
+        w["q_norm"] = (1.0 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
+        w["k_norm"] = (0.5 + 0.1 * rng.standard_normal(hd)).astype(np.float32)
         for nm in ("bq", "bk", "bv", "q_norm", "k_norm"):
             setattr(args, nm, w[nm].ctypes.data)
     args.act_gelu = int(gelu)
@@ -93,11 +93,13 @@ def make(orc, E, n_head, n_kv, F, pos, seed, norm_scale=(1.0, 1.0), qwen=False, 
         args.fmt_ag = synth.Q8_0
     x = np.random.default_rng(seed + 100).standard_normal(E).astype(np.float32)
     return dict(E=E, n_head=n_head, n_kv=n_kv, F=F, pos=pos, shapes=shapes, w=w, kc=kc, vc=vc, pb=pb, args=args, x=x,
-                gelu=gelu)
+                gelu=gelu, hd=hd)
 
 
 class OraclePieces:
-    """The oracle's individually pinned functions."""
+    """The oracle's individually pinned functions (hd: the head size, set by
+    chain from the layer)."""
+    hd = HD
 
     def __init__(self, orc):
         self.o = orc
@@ -109,18 +111,18 @@ class OraclePieces:
         return self.o.rms_norm(x, w, 1e-5)
 
     def rope_table(self, pos):
-        return self.o.rope_cache(HD, pos, 500000.0)
+        return self.o.rope_cache(self.hd, pos, 500000.0)
 
     def rope(self, v, tab, neox=True):
         if neox:
-            return self.o.rope_neox(v, HD, tab)
+            return self.o.rope_neox(v, self.hd, tab)
         return rope_adjacent(v, tab)
 
     def kv_row(self, x):
         return self.o.kv_quantize_row(x)
 
     def attention(self, q, kc, vc, n_head, n_kv, pos):
-        return self.o.attn_decode(q, kc, vc, n_head, n_kv, HD, 0, pos)
+        return self.o.attn_decode(q, kc, vc, n_head, n_kv, self.hd, 0, pos)
 
     def silu_mul(self, gate, up):
         s = np.array([self.o.L.dqo_silu(float(g)) for g in gate], np.float32)
@@ -131,7 +133,7 @@ class OraclePieces:
         return s * up
 
     def attn_gate(self, ao, gv, n_head):
-        return self.o.attn_gate_apply(ao, gv, n_head, HD)
+        return self.o.attn_gate_apply(ao, gv, n_head, self.hd)
 
 
 def rope_adjacent(v, tab):
@@ -150,7 +152,8 @@ class IndependentPieces:
     of the dense_forward.cpp glue: RMSNorm with a double sum of float squares
     (:129-165), the RoPE table by repeated float products (:631-657) with NeoX
     pairs (:668-680), SiLU (:53-55), and softmax attention in fp64 over the
-    dequantized K/V rows (:3956-4065)."""
+    dequantized K/V rows (:3956-4065). hd: the head size, set by chain."""
+    hd = HD
 
     def __init__(self, ref):
         self.r = ref
@@ -165,36 +168,38 @@ class IndependentPieces:
         return (x * scale) * w
 
     def rope_table(self, pos):
-        ts = np.power(np.float32(500000.0), np.float32(-2.0 / HD), dtype=np.float32)
+        # powf(theta_base, -2 / n_rot), correctly rounded (numpy's float32 power is not)
+        ts = np.float32(np.float64(500000.0) ** np.float64(np.float32(-2.0 / self.hd)))
         th = np.float32(pos)
-        tab = np.empty(HD, np.float32)
-        for j in range(HD // 2):
-            tab[2 * j], tab[2 * j + 1] = np.cos(th), np.sin(th)
+        tab = np.empty(self.hd, np.float32)
+        for j in range(self.hd // 2):
+            # cosf / sinf of the float angle, correctly rounded (numpy's float32 cos is not)
+            tab[2 * j], tab[2 * j + 1] = np.cos(np.float64(th)), np.sin(np.float64(th))
             th = np.float32(th * ts)
         return tab
 
     def rope(self, v, tab, neox=True):
         v = v.astype(np.float32).copy()
         c, s = tab[0::2], tab[1::2]
-        a, b = v[:HD // 2].copy(), v[HD // 2:].copy()
-        v[:HD // 2] = a * c - b * s
-        v[HD // 2:] = a * s + b * c
+        a, b = v[:self.hd // 2].copy(), v[self.hd // 2:].copy()
+        v[:self.hd // 2] = a * c - b * s
+        v[self.hd // 2:] = a * s + b * c
         return v
 
     def kv_row(self, x):
         return self.r.kv_quantize_row(x)
 
     def attention(self, q, kc, vc, n_head, n_kv, pos):
-        pb = n_kv * (HD // 32) * 34
-        K = self.r.dequantize_row(synth.Q8_0, kc[:(pos + 1) * pb], (pos + 1) * n_kv * HD).reshape(pos + 1, n_kv, HD)
-        V = self.r.dequantize_row(synth.Q8_0, vc[:(pos + 1) * pb], (pos + 1) * n_kv * HD).reshape(pos + 1, n_kv, HD)
+        pb = n_kv * (self.hd // 32) * 34
+        K = self.r.dequantize_row(synth.Q8_0, kc[:(pos + 1) * pb], (pos + 1) * n_kv * self.hd).reshape(pos + 1, n_kv, self.hd)
+        V = self.r.dequantize_row(synth.Q8_0, vc[:(pos + 1) * pb], (pos + 1) * n_kv * self.hd).reshape(pos + 1, n_kv, self.hd)
         hpk = n_head // n_kv
-        out = np.empty(n_head * HD, np.float64)
+        out = np.empty(n_head * self.hd, np.float64)
         for h in range(n_head):
             k, v = K[:, h // hpk].astype(np.float64), V[:, h // hpk].astype(np.float64)
-            s = k @ q[h * HD:(h + 1) * HD].astype(np.float64) / np.sqrt(HD)
+            s = k @ q[h * self.hd:(h + 1) * self.hd].astype(np.float64) / np.sqrt(self.hd)
             p = np.exp(s - s.max())
-            out[h * HD:(h + 1) * HD] = (p / p.sum()) @ v
+            out[h * self.hd:(h + 1) * self.hd] = (p / p.sum()) @ v
         return out.astype(np.float32)
 
     def silu_mul(self, gate, up):
@@ -208,13 +213,14 @@ class IndependentPieces:
 
     def attn_gate(self, ao, gv, n_head):  # 1 / (1 + exp(-g)) in fp64 (:4102-4114)
         g = 1.0 / (1.0 + np.exp(-gv.astype(np.float64)))
-        return (ao.reshape(n_head, HD) * g[:, None]).reshape(-1).astype(np.float32)
+        return (ao.reshape(n_head, self.hd) * g[:, None]).reshape(-1).astype(np.float32)
 
 
 def chain(L, P, mistake=None):
     """The decode layer as a chain of pieces P, in the reference's order.
     Returns (x_out, kc, vc) with the caches as the step leaves them."""
     E, nh, nkv, F, pos, sh, w = L["E"], L["n_head"], L["n_kv"], L["F"], L["pos"], L["shapes"], L["w"]
+    HD = P.hd = L["hd"]
     kc, vc = L["kc"].copy(), L["vc"].copy()
     x = L["x"]
 
@@ -283,6 +289,16 @@ def layer(orc, L):
     return out, kc, vc
 
 
+def kind(qwen):
+    """make() flags of a SHAPES kind: True (Qwen-style), "gelu", "gemma",
+    "gate", or "hd<n>[-qwen|-gemma]" (heads of n values)."""
+    hd, q = HD, qwen
+    if isinstance(qwen, str) and qwen.startswith("hd"):
+        h, _, q = qwen.partition("-")
+        hd, q = int(h[2:]), {"qwen": True, "": False}.get(q, q)
+    return dict(qwen=q is True, gelu=q in ("gelu", "gemma"), sandwich=q == "gemma", attn_gate=q == "gate", hd=hd)
+
+
 SHAPES = [
     pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), False, id="E512-pos70"),
     pytest.param(4096, 32, 8, 14336, 4096, (1.0, 1.0), False, id="config4-pos4096"),
@@ -299,13 +315,17 @@ SHAPES = [
     # per-head attention output gate (DenseQuirks::attn_gate)
     pytest.param(512, 8, 2, 1536, 70, (0.25 / np.sqrt(512), 0.3 / np.sqrt(512)), "gate", id="E512-pos70-gate"),
     pytest.param(4096, 32, 8, 14336, 4096, (0.25 / 64, 0.3 / 64), "gate", id="config4-pos4096-gate"),
+    # heads of 64 and 256 values
+    pytest.param(1024, 16, 4, 2048, 300, (0.25 / 32, 0.3 / 32), "hd64", id="E1024-hd64"),
+    pytest.param(1024, 16, 4, 2048, 300, (0.25 / 32, 0.3 / 32), "hd64-qwen", id="E1024-hd64-qwen"),
+    pytest.param(1024, 8, 2, 2048, 300, (0.25 / 32, 0.3 / 32), "hd256", id="E1024-hd256"),
+    pytest.param(1024, 8, 2, 2048, 300, (0.25 / 32, 0.3 / 32), "hd256-gemma", id="E1024-hd256-gemma"),
 ]
 
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns, qwen):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos, norm_scale=ns, qwen=qwen is True,
-             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma", attn_gate=qwen == "gate")
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos, norm_scale=ns, **kind(qwen))
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, OraclePieces(orc))
     e = rel(got, want)
@@ -317,15 +337,14 @@ def test_layer_decode_vs_oracle_pieces(orc, E, n_head, n_kv, F, pos, ns, qwen):
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_layer_decode_vs_compiled_reference_operators(orc, ref, E, n_head, n_kv, F, pos, ns, qwen):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 1, norm_scale=ns, qwen=qwen is True,
-             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma", attn_gate=qwen == "gate")
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 1, norm_scale=ns, **kind(qwen))
     got, gkc, gvc = layer(orc, L)
     want, wkc, wvc = chain(L, IndependentPieces(ref))
     e = rel(got, want)
     print(f"  layer vs reference operators + numpy glue: {e:.2e}")
     assert e <= 1e-3
     # the written K/V rows: equal up to a rounding flip of the projections
-    pb, kvd, pos = L["pb"], n_kv * HD, L["pos"]
+    pb, kvd, pos = L["pb"], n_kv * L["hd"], L["pos"]
     for a, b in ((gkc, wkc), (gvc, wvc)):
         assert np.array_equal(a[:pos * pb], b[:pos * pb])
         da = orc.dequantize_row(synth.Q8_0, a[pos * pb:], kvd)
@@ -358,8 +377,7 @@ def test_planted_mistakes_fail(orc, mistake):
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos,ns,qwen", SHAPES)
 def test_prefill_one_token_equals_decode(orc, E, n_head, n_kv, F, pos, ns, qwen):
-    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 2, norm_scale=ns, qwen=qwen is True,
-             gelu=qwen in ("gelu", "gemma"), sandwich=qwen == "gemma", attn_gate=qwen == "gate")
+    L = make(orc, E, n_head, n_kv, F, pos, seed=E + pos + 2, norm_scale=ns, **kind(qwen))
     dec, dkc, dvc = layer(orc, L)
     kc, vc = L["kc"].copy(), L["vc"].copy()
     pre = orc.layer_prefill(L["args"], kc, vc, pos, L["x"][None, :])[0]

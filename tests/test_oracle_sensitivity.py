@@ -119,7 +119,7 @@ def test_engine_batch_layer_product_sensitivity(orc, gelu, sandwich):
         keep["post_ffn_norm"] = (0.8 + 0.05 * np.random.default_rng(96).standard_normal(E)).astype(np.float32)
         oa.post_attn_norm, oa.post_ffn_norm = keep["post_attn_norm"].ctypes.data, keep["post_ffn_norm"].ctypes.data
     x = np.random.default_rng(94).standard_normal((T, E)).astype(np.float32)
-    spec = types.SimpleNamespace(n_head=n_head, n_head_kv=n_kv, gelu=gelu, cache=types.SimpleNamespace(pos_bytes=pb),
+    spec = types.SimpleNamespace(n_head=n_head, n_head_kv=n_kv, head_dim=128, gelu=gelu, cache=types.SimpleNamespace(pos_bytes=pb),
                                  mats={nm: types.SimpleNamespace(fmt=synth.FMT_OF_TYPE[tys[i]], rows=shapes[nm][0],
                                                                  cols=shapes[nm][1]) for i, nm in enumerate(names)})
     want = orc.layer_prefill(oa, kc.copy(), vc.copy(), prior, x)
@@ -152,7 +152,7 @@ def test_model_logits_product_sensitivity(orc):
     pb = KV * HD // 32 * 34
     from oracle.oracle import LayerArgs
     oargs, keeps = [], []
-    spec = types.SimpleNamespace(n_head=H, n_head_kv=KV, cache=types.SimpleNamespace(pos_bytes=pb),
+    spec = types.SimpleNamespace(n_head=H, n_head_kv=KV, head_dim=128, cache=types.SimpleNamespace(pos_bytes=pb),
                                  mats={nm: types.SimpleNamespace(fmt=synth.FMT_OF_TYPE[qt], rows=r, cols=c)
                                        for nm, (qt, r, c) in shapes.items()})
     for l in range(NL):
