@@ -353,10 +353,15 @@ def graph_time(fn, calls_per_graph, reps, warmup_reps=2):
     return sum(ts) / len(ts)
 
 
+WARMUP_MS = 25.0  # untimed graph replays before every timed set: the first few ms of a
+                  # workload after set-up run up to 15% slower than its steady state
+
+
 def replay_times(fn, calls_per_graph, reps, warmup_reps=2):
     """Captures calls_per_graph calls of fn into one HIP graph and times each
     of `reps` replays on its own (HIP events on the capturing stream, the
-    stream the kernels run on). Returns us per call, one figure per replay."""
+    stream the kernels run on), after warmup_reps untimed replays and at least
+    WARMUP_MS of them. Returns us per call, one figure per replay."""
     import torch
     fn()
     torch.cuda.synchronize()
@@ -364,8 +369,13 @@ def replay_times(fn, calls_per_graph, reps, warmup_reps=2):
     with torch.cuda.graph(g):
         for _ in range(calls_per_graph):
             fn()
-    for _ in range(warmup_reps):
+    t0 = time.perf_counter()
+    n = 0
+    while n < warmup_reps or (time.perf_counter() - t0) * 1e3 < WARMUP_MS:
         g.replay()
+        n += 1
+        if n % 4 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
     ev[0].record()
