@@ -755,6 +755,59 @@ __device__ __forceinline__ void quantize_f16_block(const float* __restrict__ x, 
     }
 }
 
+// Q4_K order, one item (blocks 2i and 2i+1, 64 values) per call: the two
+// blocks' integers, scales and exact float sums as quantize_f16_block, their
+// 64 fp16 values stored as 8 contiguous 16-byte chunks (chunk (kk, hf) at
+// column 16 kk + 8 hf of the item holds elements e = 16 hf + 4 kk + bo of the
+// low block (hi = 0) and of the high block (hi = 1) at slot
+// 4 (bo & 1) + (bo >> 1) + 2 hi), and the two block sums as one 4-byte store.
+__device__ __forceinline__ void quantize_f16_item_q4k(const float* __restrict__ x, int cols, int n_tok,
+                                                      _Float16* __restrict__ out, int lda,
+                                                      _Float16* __restrict__ minp, int t, int i, float sc) {
+    const float* p = x + (size_t)t * cols + 64 * i;
+    float v[64];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float4 f = reinterpret_cast<const float4*>(p)[k];
+        v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+    }
+    _Float16 h[64];
+    _Float16 fsum[2];
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi) {
+        const float* vb = v + 32 * hi;
+        float amax = 0.0f, fs = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            const float a = fabsf(vb[e]);
+            amax = (amax < a) ? a : amax;
+            fs += vb[e];
+        }
+        const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) {
+            int q = (int)rintf(vb[e] * id);
+            q = q > 127 ? 127 : (q < -127 ? -127 : q);
+            h[32 * hi + e] = (_Float16)(((float)q * d) * sc);
+        }
+        fsum[hi] = (_Float16)(fs * sc);
+    }
+    _Float16* o = out + (size_t)t * lda + 64 * (size_t)i;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+            const int e0 = 16 * hf + 4 * kk;
+            const h8 c = {h[e0], h[e0 + 2], h[32 + e0], h[32 + e0 + 2], h[e0 + 1], h[e0 + 3], h[32 + e0 + 1],
+                          h[32 + e0 + 3]};
+            *reinterpret_cast<h8*>(o + 16 * kk + 8 * hf) = c;
+        }
+    const int mb = 2 * i;
+    const h2 sums = {fsum[0], fsum[1]};
+    *reinterpret_cast<h2*>(minp + ((size_t)(mb / 8) * n_tok + t) * 8 + (mb % 8)) = sums;
+}
+
 // One workgroup per token row: the row's power-of-two range scale (as
 // row_scale_kernel) and then every block of the row (quantize_f16_block);
 // inv[t] = 1/s. The workgroups also clear the outputs of the K-split GEMMs
@@ -790,6 +843,10 @@ __global__ __launch_bounds__(256) void quantize_f16_rows_kernel(const float* __r
         inv[t] = 1.0f / sc;
     }
     const int nb = cols / 32;
+    if (perm == 2) {  // Q4_K: whole items (contiguous stores), block sums alongside
+        for (int i = threadIdx.x; i < nb / 2; i += 256) quantize_f16_item_q4k(x, cols, n_tok, out, lda, minp, t, i, sc);
+        return;
+    }
     const int stride = minp ? 2 * nb : nb;
     for (int b = threadIdx.x; b < stride; b += 256) quantize_f16_block(x, cols, n_tok, out, lda, minp, perm, t, b, sc);
 }

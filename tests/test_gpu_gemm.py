@@ -2,6 +2,8 @@
 core/matmul.cpp:806-845, core/i8gemm_impl.h:326-419): norm-wise relative error
 <= 4e-3 (the MFMA GEMM tolerance). The full config-3 shapes are checked on
 row/token sub-blocks that cover the first, middle and last tiles."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -93,3 +95,84 @@ def test_gemm_activation_range(gpu, orc, qtype, scale):
     assert np.isfinite(y).all()
     for t in range(n_tok):  # per token: each row's own magnitude
         assert rel(y[t], want[t]) <= TOL, t
+
+
+def _f16_act_ref(fmt, x):
+    """The GEMM's activation workspace rebuilt in numpy from its definition:
+    per token the power-of-two range scale s = 2^(15 - E) with 32 max|x| =
+    m 2^E (frexp), per 32-block the reference quantizer (d = amax/127, id =
+    1/d, q = rint(x id) clamped to +-127) written as fp16((q d) s) in the
+    format's K order, and for Q4_K the sequential float block sums as
+    fp16(sum s) in [cols/256][n_tok][8]. Returns (act [n_tok][cols], minp, s)."""
+    n_tok, cols = x.shape
+    f32 = np.float32
+    r = np.abs(x).max(axis=1)
+    s = np.empty(n_tok, f32)
+    for t in range(n_tok):
+        E = int(np.frexp(f32(32.0) * r[t])[1]) if r[t] > 0 else 0
+        s[t] = np.ldexp(f32(1.0), 15 - min(max(E, -100), 115))
+    blk = x.reshape(n_tok, cols // 32, 32)
+    amax = np.abs(blk).max(axis=2)
+    d = np.divide(amax, f32(127.0), out=np.zeros_like(amax), where=amax > 0).astype(f32)
+    idv = np.divide(f32(1.0), d, out=np.zeros_like(d), where=d > 0).astype(f32)
+    # through int32, as the kernel does: a negative value that rounds to zero gives +0
+    q = np.clip(np.rint(blk * idv[..., None]), -127, 127).astype(np.int32).astype(f32)
+    h = ((q * d[..., None]) * s[:, None, None]).astype(np.float16)  # [n_tok][nb][32]
+    nb = cols // 32
+    col = np.empty((nb, 32), np.int64)
+    for b in range(nb):
+        for e in range(32):
+            if fmt == synth.Q4_K:
+                kk, hf, bo, hi = (e % 16) // 4, e // 16, e % 4, b % 2
+                col[b, e] = 64 * (b // 2) + 16 * kk + 8 * hf + 4 * (bo & 1) + (bo >> 1) + 2 * hi
+            elif fmt == synth.Q6_K:
+                sb, pos0 = b // 8, 32 * (b % 8)
+                n, qq, k = pos0 // 128, (pos0 % 128) // 32, e // 16
+                col[b, e] = sb * 256 + (2 * n + k) * 64 + qq * 16 + e % 16
+            else:
+                col[b, e] = 32 * b + e
+    act = np.zeros((n_tok, cols), np.float16)
+    act[:, col.reshape(-1)] = h.reshape(n_tok, -1)
+    minp = None
+    if fmt == synth.Q4_K:
+        fs = np.cumsum(blk, axis=2, dtype=f32)[..., -1]  # sequential float sums
+        minp = (fs * s[:, None]).astype(np.float16).reshape(n_tok, cols // 256, 8).transpose(1, 0, 2)
+    return act, minp, s
+
+
+@pytest.mark.parametrize("qtype,cols,n_tok", [(synth.Q4_K, 4096, 512), (synth.Q4_K, 256, 3), (synth.Q4_K, 14336, 7),
+                                              (synth.Q6_K, 14336, 5), (synth.Q8_0, 4096, 9), (synth.Q4_0, 512, 2)])
+def test_gemm_activation_layout(gpu, qtype, cols, n_tok):
+    """dq_quantize_act_f16 writes exactly the fp16 activation, block sums and
+    row scales of its definition (bit-exact), including zero blocks, a zero
+    row and rows far from N(0,1)."""
+    print(f"gemm act layout type={qtype} cols={cols} n_tok={n_tok}", flush=True)
+    lib = _lib.load()
+    x = synth.gen_act((n_tok, cols), seed=cols + n_tok).astype(np.float32)
+    x[0, 32:96] = 0.0                        # two zero blocks
+    if n_tok > 2:
+        x[1] *= np.float32(3e4)
+        x[2] = 0.0                           # a zero row
+    m = ops.QuantMatrix.from_gguf(qtype, synth.gen_weights(qtype, 1, cols, seed=1), 1, cols)
+    n = ctypes.c_size_t()
+    _lib.check(lib.dq_gemm_workspace_bytes(m.fmt, 1, cols, n_tok, ctypes.byref(n)), "dq_gemm_workspace_bytes")
+    work = torch.zeros(n.value, dtype=torch.uint8, device=gpu)
+    xd = torch.from_numpy(x).to(gpu)
+    _lib.check(lib.dq_quantize_act_f16(m.fmt, ops._ptr(xd), cols, n_tok, ops._ptr(work), ops._stream()),
+               "dq_quantize_act_f16")
+    w = work.cpu().numpy()
+    lda = cols + 64
+    a256 = lambda b: (b + 255) // 256 * 256
+    act_b = a256(n_tok * lda * 2)
+    got = w[:n_tok * lda * 2].view(np.float16).reshape(n_tok, lda)[:, :cols]
+    want, minp, s = _f16_act_ref(qtype, x)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    off = act_b
+    if minp is not None:
+        gm = w[off:off + minp.size * 2].view(np.float16).reshape(minp.shape)
+        assert np.array_equal(gm.view(np.uint16), minp.view(np.uint16))
+        off += a256(n_tok * (cols // 32) * 2)
+    gs = w[off:off + 4 * n_tok].view(np.float32)
+    assert np.array_equal(gs, s)
+    gi = w[off + a256(4 * n_tok):off + a256(4 * n_tok) + 4 * n_tok].view(np.float32)
+    assert np.array_equal(gi, (np.float32(1.0) / s).astype(np.float32))
