@@ -225,6 +225,7 @@ struct Fmt<DQ_FMT_Q6_K> {
 #define DQ_GEMV_MAX_JOBS 4
 struct Jobs {
     const uint8_t* w[DQ_GEMV_MAX_JOBS];
+    int fmt[DQ_GEMV_MAX_JOBS];  // the mixed-format launch picks each group's format by its job
     DqLayout L[DQ_GEMV_MAX_JOBS];
     float* y[DQ_GEMV_MAX_JOBS];
     const float* res[DQ_GEMV_MAX_JOBS];
@@ -598,6 +599,41 @@ __global__ __launch_bounds__(256) void gemv_flat_kernel(Jobs J, int items, int p
     compute_group<FMT, R, 1, KS>(w, X, J, g, i0, i1, lane, ks, part, 0);
 }
 
+// Flat grid over jobs of two per-256 formats reading one pre-quantized
+// activation (the decoder layer's Q/K in Q4_K and V in Q6_K): one launch for
+// the whole group. A wave's group belongs to one job, so each wave runs the
+// single-format body (activation registers, every weight load of the group,
+// the rows' dot products) of its job's format; the arithmetic is that of the
+// single-format flat kernel. One item per lane (no K split).
+template <int FA, int FB, int R>
+__global__ __launch_bounds__(256) void gemv_flat_mixed_kernel(Jobs J, int items, const int8_t* __restrict__ xq,
+                                                              const float* __restrict__ xs,
+                                                              const int32_t* __restrict__ xsum) {
+    const int lane = threadIdx.x & (DQ_WAVE - 1);
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / DQ_WAVE));
+    const int ngroups = J.g0[J.n];
+    const int g = 4 * (int)blockIdx.x + wv;
+    if (g >= ngroups) return;  // uniform per wave
+    int gl = 0;
+    const int j = job_of(J, g, &gl);
+    const int xi = min(lane, items - 1);
+    auto body = [&](auto fc) {
+        constexpr int F = decltype(fc)::value;
+        using W = typename Fmt<F>::W;
+        XItem X[1];
+        Fmt<F>::load_x(X[0], xi, xq, xs, xsum);
+        __builtin_amdgcn_sched_barrier(0);
+        W w[R][1];
+        load_group<F, R, 1>(w, J, g, ngroups, 0, items, lane, nullptr);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_group<F, R, 1, 1>(w, X, J, g, 0, items, lane, 0, nullptr, 0);
+    };
+    if (J.fmt[j] == FB)  // uniform per wave
+        body(std::integral_constant<int, FB>{});
+    else
+        body(std::integral_constant<int, FA>{});
+}
+
 // Per-256 quantization of the 16-wave flat grid, one 256-column block per
 // 16-lane row: lane j of row q of wave w holds columns 1024w + 256q + 64k +
 // 4j + [0, 4), k = 0..3 (each load instruction reads four contiguous 256-byte
@@ -832,6 +868,45 @@ int count_groups(const Jobs& J, int R) {
     return n;
 }
 
+// Waves of gemv_flat_mixed_kernel<FA, FB, R> one CU holds at once (cached).
+template <int FA, int FB, int R>
+int mixed_resident_waves() {
+    static int c = 0;
+    if (c == 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &nb, reinterpret_cast<const void*>(&gemv_flat_mixed_kernel<FA, FB, R>), 256, 0) != hipSuccess ||
+            nb <= 0)
+            nb = 1;
+        c = 4 * nb;
+    }
+    return c;
+}
+
+template <int FA, int FB, int R>
+int launch_mixed_r(Jobs J, int items, const int8_t* xq, const float* xs, const int32_t* xsum, hipStream_t s) {
+    set_groups(J, R);
+    const unsigned grid = (unsigned)((J.g0[J.n] + 3) / 4);
+    gemv_flat_mixed_kernel<FA, FB, R><<<grid, 256, 0, s>>>(J, items, xq, xs, xsum);
+    return dq_launch_status();
+}
+
+// One launch for a group of Q4_K and Q6_K jobs on a pre-quantized per-256
+// activation (cols <= 4096: one item per lane), with the fewest rows per
+// group (1, 2, 4) whose waves are all resident at once; NO_FLAT otherwise.
+int launch_mixed(const Jobs& J, int items, const int8_t* xq, const float* xs, const int32_t* xsum, hipStream_t s) {
+    static const int on = env_int("DQ_GEMV_MIXED", 1);
+    if (!on || items > DQ_WAVE) return NO_FLAT;
+    const long cus = num_cus();
+    static const int wpc = env_int("DQ_GEMV_FWPC", 16);
+    auto fits = [&](int r, int resident) { return (long)count_groups(J, r) <= cus * min(wpc, resident); };
+    constexpr int A = DQ_FMT_Q4_K, B = DQ_FMT_Q6_K;
+    if (fits(1, mixed_resident_waves<A, B, 1>())) return launch_mixed_r<A, B, 1>(J, items, xq, xs, xsum, s);
+    if (fits(2, mixed_resident_waves<A, B, 2>())) return launch_mixed_r<A, B, 2>(J, items, xq, xs, xsum, s);
+    if (fits(4, mixed_resident_waves<A, B, 4>())) return launch_mixed_r<A, B, 4>(J, items, xq, xs, xsum, s);
+    return NO_FLAT;
+}
+
 template <int FMT, int R, int KS, int NW>
 int launch_flat16_r(Jobs J, int items, int per, const float* xf, hipStream_t s) {
     set_groups(J, R);
@@ -1047,6 +1122,30 @@ int run_jobs(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* xq,
     DqLayout L[DQ_GEMV_MAX_JOBS];
     const int rc = check_jobs(jobs, n, cols, xq, xs, xsum, xf, L);
     if (rc != DQ_OK || n == 0) return rc;
+    {   // Q4_K and Q6_K jobs together on a pre-quantized activation: one launch
+        bool q4 = false, q6 = false, other = false;
+        for (size_t j = 0; j < n; ++j) {
+            if (jobs[j].rows == 0) continue;
+            q4 = q4 || jobs[j].fmt == DQ_FMT_Q4_K;
+            q6 = q6 || jobs[j].fmt == DQ_FMT_Q6_K;
+            other = other || (jobs[j].fmt != DQ_FMT_Q4_K && jobs[j].fmt != DQ_FMT_Q6_K);
+        }
+        if (!xf && q4 && q6 && !other) {
+            Jobs J{};
+            for (size_t j = 0; j < n; ++j) {
+                if (jobs[j].rows == 0) continue;
+                J.w[J.n] = (const uint8_t*)jobs[j].d_w;
+                J.fmt[J.n] = jobs[j].fmt;
+                J.L[J.n] = L[j];
+                J.y[J.n] = jobs[j].d_y;
+                J.res[J.n] = jobs[j].d_res;
+                J.rows[J.n] = (int)jobs[j].rows;
+                ++J.n;
+            }
+            const int r = launch_mixed(J, (int)(cols / 64), xq, xs, xsum, s);
+            if (r != NO_FLAT) return r;
+        }
+    }
     bool done[DQ_GEMV_MAX_JOBS] = {};
     for (size_t a = 0; a < n; ++a) {
         if (done[a]) continue;
@@ -1057,6 +1156,7 @@ int run_jobs(const dq_gemv_job_t* jobs, size_t n, size_t cols, const int8_t* xq,
             done[j] = true;
             if (jobs[j].rows == 0) continue;
             J.w[J.n] = (const uint8_t*)jobs[j].d_w;
+            J.fmt[J.n] = fmt;
             J.L[J.n] = L[j];
             J.y[J.n] = jobs[j].d_y;
             J.res[J.n] = jobs[j].d_res;

@@ -92,6 +92,9 @@ def test_gemv_add_residual(gpu, orc):
     ((synth.Q4_K, synth.Q4_K), (14336, 14336), 4096),                    # config 4 gate/up
     ((synth.Q8_0, synth.Q4_0, synth.Q8_0, synth.Q4_0), (5, 64, 129, 3), 256),  # ragged, per-32 kind
     ((synth.Q6_K,), (7,), 768),
+    ((synth.Q6_K, synth.Q4_K, synth.Q6_K, synth.Q4_K), (7, 33, 130, 5), 256),  # mixed per-256 kinds, one launch
+    ((synth.Q4_K, synth.Q6_K), (1000, 77), 2048),
+    ((synth.Q6_K, synth.Q4_K), (300, 2000), 8192),      # beyond one item per lane: a launch per format
 ])
 def test_gemv_group_matches_single(gpu, orc, fmts, rows, cols):
     """The grouped GEMV (matmul_fused_pq semantics) gives every matrix exactly
