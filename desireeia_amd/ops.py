@@ -140,7 +140,8 @@ def gemv(mat, act, out=None):
 
 def gemv_group(mats, act, outs=None, residuals=None):
     """Several matrices with the same cols reading one activation
-    (matmul_fused_pq / matvec_shared_group): one launch per distinct format."""
+    (matmul_fused_pq / matvec_shared_group): one launch per distinct format,
+    Q4_K and Q6_K together in one where cols <= 4096."""
     lib = _lib.load()
     n = len(mats)
     ys = outs if outs is not None else [torch.empty(m.rows, dtype=torch.float32, device=m.buf.device) for m in mats]

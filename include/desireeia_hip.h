@@ -108,7 +108,8 @@ int dq_gemv_add(int fmt, const void* d_w, size_t rows, size_t cols, const int8_t
                 const float* d_xscale, const int32_t* d_xsum, const float* d_res, float* d_y, void* stream);
 
 /* Grouped GEMV: up to 4 matrices with the same cols reading the same
- * activation, one launch per distinct format (matmul_fused_pq,
+ * activation, one launch per distinct format, except that Q4_K and Q6_K
+ * matrices share one launch where cols <= 4096 (matmul_fused_pq,
  * core/matmul.cpp:2586-2639, reached through matvec_shared_group,
  * models/dense_forward.cpp:554-601; the device counterpart of
  * matmul_kquant_cuda_resident_same_x, core/engine.h:537-538). Each job's
