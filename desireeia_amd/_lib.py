@@ -71,6 +71,8 @@ SIGNATURES = {
     "dq_layer_decode": (c_int, [c_p, c_p, c_p, c_p, c_u32, c_p, c_u32, c_p, c_p, c_u32, c_p, c_size, c_p]),
     "dq_silu_mul": (c_int, [c_p, c_p, c_size, c_p, c_p]),
     "dq_moe_route": (c_int, [c_p, c_u32, c_u32, c_u32, c_int, c_f, c_p, c_p, c_p]),
+    "dq_moe_tiles_bytes": (c_int, [c_u32, c_size, c_size, ctypes.POINTER(c_size)]),
+    "dq_moe_tiles_pack": (c_int, [c_p, c_u32, c_size, c_size, c_p, c_p]),
     "dq_moe_workspace_bytes": (c_int, [c_p, c_u32, ctypes.POINTER(c_size)]),
     "dq_moe_ffn": (c_int, [c_p, c_p, c_p, c_u32, c_p, c_p, c_size, c_p]),
     # GGUF files (host)

@@ -292,7 +292,7 @@ __global__ __launch_bounds__(64 * SILU_WAVES) void moe_silu_act_kernel(const flo
 
 // ------------------------------------------------------------ expert GEMM --
 struct MoeGemm {
-    const uint8_t* w[2];  // packed stacked matrices ([n_exp * rows][K])
+    const uint8_t* w[2];  // stacked matrices ([n_exp * rows][K]): packed rows, or expert tiles (TILED)
     DqLayout L[2];
     float* y[2];          // outputs [nsplit][n_pairs][rows]
     const _Float16* A;    // activation rows [n_pairs][K]
@@ -416,6 +416,58 @@ __device__ __forceinline__ void issue_w(const uint8_t* base, const DqLayout& L, 
 constexpr int STEP_LOADS = A_LOADS + 1 + 2 * WROWS * 4 / (64 * WAVES) + 1;
 static_assert(WROWS * 4 % (64 * WAVES) == 0 && 64 * WAVES == 2 * WROWS, "DMA slots per thread");
 
+// Expert-tile layout (DQ_FMT_Q4_K_TILES): the weight tile of one main step
+// stored as the LDS stage image, so the step's DMA reads one contiguous
+// run (64 lanes x 16 consecutive bytes per instruction) instead of 4 lanes
+// per 64-byte row piece. Chunk (e, x, sb) of expert e, row tile x (rows
+// 128x .. +127, the last row repeated past the expert's end) and super-block
+// sb sits at ((e * n_tiles + x) * nsb + sb) * WT_BYTES: the two sub-plane
+// tiles [128 rows][4 slots][16 B] (slot t ^ ((r >> 2) & 3) holding item t)
+// and the headers [128 rows][16 B].
+constexpr int WT_SLOTS = WT_BYTES / 16;
+constexpr int WT_TILE_LOADS = (WT_SLOTS + 64 * WAVES - 1) / (64 * WAVES);  // DMAs per thread per step
+static_assert(WT_TILE_LOADS == 2 * WROWS * 4 / (64 * WAVES) + 1, "the same DMA count as the row layout");
+__device__ __forceinline__ void issue_w_tiles(const uint8_t* chunk, uint8_t* dst, int tid) {
+    const int wv = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int j = 0; j < WT_TILE_LOADS; ++j) {
+        // a wave past the last full span repeats the last 64 slots (same bytes)
+        const int ws = min(j * 64 * WAVES + 64 * wv, WT_SLOTS - 64);  // wave-uniform
+        __builtin_amdgcn_global_load_lds(chunk + 16 * (size_t)(ws + lane), DQ_LDS_PTR(dst + 16 * (size_t)ws), 16, 0,
+                                         0);
+    }
+}
+
+// One thread per 16-byte slot of the tile layout, copied from the packed
+// rows (dq_weights_pack of the stacked matrix).
+__global__ __launch_bounds__(256) void moe_tiles_pack_kernel(const uint8_t* __restrict__ src, DqLayout L, int rows,
+                                                             int n_tiles, int nsb, size_t n_slots,
+                                                             uint8_t* __restrict__ dst) {
+    const size_t g = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (g >= n_slots) return;
+    const size_t chunk = g / WT_SLOTS;
+    const int c = (int)(g % WT_SLOTS);
+    const int sb = (int)(chunk % nsb);
+    const size_t et = chunk / nsb;
+    const int x = (int)(et % n_tiles);
+    const size_t e = et / n_tiles;
+    const uint8_t* p;
+    if (c < 2 * WROWS * 4) {
+        const int pl = c / (WROWS * 4), rs = c % (WROWS * 4), r = rs / 4, t = (rs % 4) ^ ((r >> 2) & 3);
+        const size_t row = e * rows + (size_t)min(WROWS * x + r, rows - 1);
+        p = src + L.q_off + (size_t)pl * L.p_stride + row * L.q_row + 16 * (size_t)(4 * sb + t);
+    } else {
+        const int r = c - 2 * WROWS * 4;
+        const size_t row = e * rows + (size_t)min(WROWS * x + r, rows - 1);
+        p = src + L.s_off + row * L.s_row + 16 * (size_t)sb;
+    }
+    *reinterpret_cast<dq_u32x4*>(dst + 16 * g) = *reinterpret_cast<const dq_u32x4*>(p);
+}
+
+size_t tiles_bytes(size_t n_exp, size_t rows, size_t cols) {
+    return n_exp * ((rows + WROWS - 1) / WROWS) * (cols / 256) * (size_t)WT_BYTES;
+}
+
 // Grid (one dimension): workgroup id -> expert id % n_exp, then the row tile,
 // then the K split, then the matrix. Workgroups are dealt to the 8 XCDs
 // round-robin, so with 8 (or a multiple of 8) experts each XCD serves whole
@@ -427,6 +479,7 @@ static_assert(WROWS * 4 % (64 * WAVES) == 0 && 64 * WAVES == 2 * WROWS, "DMA slo
 // super-block) the weight tile and the activation rows go through an
 // NSTAGE-stage LDS ring, the next NSTAGE-1 steps' DMAs in flight while this
 // one computes.
+template <bool TILED>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void moe_gemm_kernel(MoeGemm G) {
     __shared__ __align__(16) uint8_t aring[NSTAGE][A_STAGE_BYTES];
     __shared__ __align__(16) uint8_t wring[NSTAGE][WT_BYTES];
@@ -447,6 +500,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     const int rloc = r_wg + rl;
     const bool row_ok = rloc < G.rows;
     const size_t row0 = (size_t)e * G.rows + r_wg;
+    // TILED: the expert tile's first chunk (one per main step after it)
+    const size_t chunk0 = ((size_t)e * G.n_tiles + tile) * (size_t)G.main_steps;
     const uint8_t* base = G.w[mat];
     const DqLayout L = G.L[mat];
     float* __restrict__ y = G.y[mat] + (size_t)split * G.n_pairs * G.rows;
@@ -464,7 +519,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
             for (int q = 0; q < NSTAGE - 1; ++q) {
                 if (s0 + q < main_end) {
                     issue_a(G.A, G.minp, G.K, G.n_pairs, c, p_end, s0 + q, aring[q], tid);
-                    issue_w(base, L, row0, nrows, s0 + q, wring[q], tid);
+                    if constexpr (TILED) issue_w_tiles(base + (chunk0 + s0 + q) * WT_BYTES, wring[q], tid);
+                    else issue_w(base, L, row0, nrows, s0 + q, wring[q], tid);
                 }
             }
             for (int st = s0; st < main_end; ++st) {
@@ -481,7 +537,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
                 if (st + NSTAGE - 1 < main_end) {
                     const int ns = (st - s0 + NSTAGE - 1) % NSTAGE;
                     issue_a(G.A, G.minp, G.K, G.n_pairs, c, p_end, st + NSTAGE - 1, aring[ns], tid);
-                    issue_w(base, L, row0, nrows, st + NSTAGE - 1, wring[ns], tid);
+                    if constexpr (TILED) issue_w_tiles(base + (chunk0 + st + NSTAGE - 1) * WT_BYTES, wring[ns], tid);
+                    else issue_w(base, L, row0, nrows, st + NSTAGE - 1, wring[ns], tid);
                 }
                 const uint8_t* ab = aring[stage];
                 const uint8_t* wb = wring[stage];
@@ -623,7 +680,7 @@ MoeWs carve(const dq_moe_t* m, uint32_t n_tok, int split_gu, int split_d, uint8_
 }
 
 bool moe_ok(const dq_moe_t* m) {
-    if (!m || m->fmt != DQ_FMT_Q4_K) return false;
+    if (!m || (m->fmt != DQ_FMT_Q4_K && m->fmt != DQ_FMT_Q4_K_TILES)) return false;
     if (m->n_expert == 0 || m->n_expert > MOE_MAX_EXPERT) return false;
     if (m->n_expert_used == 0 || m->n_expert_used > MOE_MAX_K || m->n_expert_used > m->n_expert) return false;
     if (m->n_embd == 0 || m->n_embd % 256 || m->n_ff == 0 || m->n_ff % 256) return false;
@@ -639,9 +696,9 @@ void splits(const dq_moe_t* m, int* sgu, int* sd) {
     *sd = pick_split((int)m->n_expert, (int)m->n_embd, 1, steps_d);
 }
 
-int launch_gemm(const uint8_t* w0, const uint8_t* w1, int n_mat, int n_exp, int rows, int K, const _Float16* A,
-                const _Float16* minp, const float* inv, const int32_t* offsets, int n_pairs, int nsplit, float* y0,
-                float* y1, hipStream_t s) {
+int launch_gemm(bool tiled, const uint8_t* w0, const uint8_t* w1, int n_mat, int n_exp, int rows, int K,
+                const _Float16* A, const _Float16* minp, const float* inv, const int32_t* offsets, int n_pairs,
+                int nsplit, float* y0, float* y1, hipStream_t s) {
     MoeGemm G{};
     G.w[0] = w0;
     G.w[1] = w1 ? w1 : w0;
@@ -665,7 +722,10 @@ int launch_gemm(const uint8_t* w0, const uint8_t* w1, int n_mat, int n_exp, int 
     G.n_tiles = (rows + WROWS - 1) / WROWS;
     const long wgs = (long)G.n_tiles * n_exp * n_mat * nsplit;
     if (wgs > 0x7FFFFFFF) return DQ_ERR_NOT_SUPPORTED;
-    moe_gemm_kernel<<<(unsigned)wgs, 64 * WAVES, 0, s>>>(G);
+    if (tiled)
+        moe_gemm_kernel<true><<<(unsigned)wgs, 64 * WAVES, 0, s>>>(G);
+    else
+        moe_gemm_kernel<false><<<(unsigned)wgs, 64 * WAVES, 0, s>>>(G);
     return dq_launch_status();
 }
 
@@ -689,6 +749,28 @@ int dq_moe_route(const float* d_logits, uint32_t n_tok, uint32_t n_expert, uint3
     moe_route_kernel<<<(n_tok + 3) / 4, 256, 0, (hipStream_t)stream>>>(d_logits, (int)n_tok, (int)n_expert, (int)k,
                                                                        norm_w, w_scale, d_ids, d_wts, nullptr, 0,
                                                                        nullptr);
+    return dq_launch_status();
+}
+
+int dq_moe_tiles_bytes(uint32_t n_expert, size_t rows, size_t cols, size_t* bytes) {
+    if (!bytes) return DQ_ERR_INVALID_ARG;
+    if (n_expert == 0 || rows == 0 || cols == 0 || cols % 256 || (size_t)n_expert * rows > 0x3FFFFFFF)
+        return DQ_ERR_NOT_SUPPORTED;
+    *bytes = tiles_bytes(n_expert, rows, cols);
+    return DQ_OK;
+}
+
+int dq_moe_tiles_pack(const void* d_packed, uint32_t n_expert, size_t rows, size_t cols, void* d_tiles,
+                      void* stream) {
+    size_t bytes = 0;
+    DQ_TRY(dq_moe_tiles_bytes(n_expert, rows, cols, &bytes));
+    if (!d_packed || !d_tiles) return DQ_ERR_INVALID_ARG;
+    DqLayout L;
+    if (!dq_layout(DQ_FMT_Q4_K, (size_t)n_expert * rows, cols, &L)) return DQ_ERR_NOT_SUPPORTED;
+    const size_t n_slots = bytes / 16;
+    moe_tiles_pack_kernel<<<(unsigned)((n_slots + 255) / 256), 256, 0, (hipStream_t)stream>>>(
+        (const uint8_t*)d_packed, L, (int)rows, (int)((rows + WROWS - 1) / WROWS), (int)(cols / 256), n_slots,
+        (uint8_t*)d_tiles);
     return dq_launch_status();
 }
 
@@ -728,13 +810,16 @@ int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint3
         DQ_TRY(dq_launch_status());
     }
     // gate and up of every pair (one launch, two matrices)
-    DQ_TRY(launch_gemm((const uint8_t*)m->wgate, (const uint8_t*)m->wup, 2, n_exp, F, E, w.a_in, w.min_in, w.inv_in,
+    const bool tiled = m->fmt == DQ_FMT_Q4_K_TILES;
+    DQ_TRY(launch_gemm(tiled, (const uint8_t*)m->wgate, (const uint8_t*)m->wup, 2, n_exp, F, E, w.a_in, w.min_in,
+                       w.inv_in,
                        w.offsets, n_ent, sgu, w.gate, w.up, s));
     // h = silu(gate) * up, quantized for the down projection
     moe_silu_act_kernel<<<n_ent, 64 * SILU_WAVES, 0, s>>>(w.gate, w.up, sgu, (size_t)n_ent * F, F, n_ent, w.a_h,
                                                           w.min_h, w.inv_h);
     DQ_TRY(dq_launch_status());
-    DQ_TRY(launch_gemm((const uint8_t*)m->wdown, nullptr, 1, n_exp, E, F, w.a_h, w.min_h, w.inv_h, w.offsets, n_ent,
+    DQ_TRY(launch_gemm(tiled, (const uint8_t*)m->wdown, nullptr, 1, n_exp, E, F, w.a_h, w.min_h, w.inv_h, w.offsets,
+                       n_ent,
                        sd, w.down, nullptr, s));
     {
         const size_t n = (size_t)n_tok * E;

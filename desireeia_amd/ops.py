@@ -469,12 +469,29 @@ class MoeLayer:
     experts, gate/up [n_expert * n_ff][n_embd] and down [n_expert * n_embd][n_ff]
     (models/dense_forward.cpp:1524-1560, combined as at :4160-4181)."""
 
-    def __init__(self, wgate, wup, wdown, n_expert, n_expert_used, norm_w=True, w_scale=1.0):
-        """wgate/wup/wdown: QuantMatrix (stacked experts)."""
+    FMT_Q4_K_TILES = 0x105
+
+    def __init__(self, wgate, wup, wdown, n_expert, n_expert_used, norm_w=True, w_scale=1.0, tiled=True):
+        """wgate/wup/wdown: QuantMatrix (stacked experts). tiled: the expert
+        GEMMs read the expert-tile copies of the matrices (dq_moe_tiles_pack,
+        contiguous weight DMA); False: the packed rows themselves."""
         self.mats = (wgate, wup, wdown)
         self.n_embd, self.n_ff = wgate.cols, wdown.cols
-        d = _lib.MoeDesc(n_expert, n_expert_used, self.n_embd, self.n_ff, int(norm_w), w_scale, wgate.fmt,
-                         wgate.buf.data_ptr(), wup.buf.data_ptr(), wdown.buf.data_ptr())
+        bufs, fmt = [m.buf for m in self.mats], wgate.fmt
+        if tiled:
+            lib = _lib.load()
+            bufs = []
+            for m, rows in ((wgate, self.n_ff), (wup, self.n_ff), (wdown, self.n_embd)):
+                n = ctypes.c_size_t(0)
+                _lib.check(lib.dq_moe_tiles_bytes(n_expert, rows, m.cols, ctypes.byref(n)), "dq_moe_tiles_bytes")
+                t = torch.empty(n.value, dtype=torch.uint8, device=m.buf.device)
+                _lib.check(lib.dq_moe_tiles_pack(_ptr(m.buf), n_expert, rows, m.cols, _ptr(t), _stream()),
+                           "dq_moe_tiles_pack")
+                bufs.append(t)
+            fmt = self.FMT_Q4_K_TILES
+        self.bufs = bufs
+        d = _lib.MoeDesc(n_expert, n_expert_used, self.n_embd, self.n_ff, int(norm_w), w_scale, fmt,
+                         bufs[0].data_ptr(), bufs[1].data_ptr(), bufs[2].data_ptr())
         self.desc = d
         self._work = None
 

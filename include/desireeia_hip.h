@@ -38,6 +38,8 @@ extern "C" {
 #define DQ_FMT_Q4_0 1
 #define DQ_FMT_Q4_K 5
 #define DQ_FMT_Q6_K 7
+/* Q4_K experts in the expert-tile layout of dq_moe_tiles_pack (dq_moe_t only). */
+#define DQ_FMT_Q4_K_TILES 0x105
 
 /* GGUF type ids for dq_dequantize_row (quant/quant.h:439-476). */
 #define DQ_TYPE_Q4_0 2
@@ -432,10 +434,23 @@ typedef struct {
     uint32_t n_expert, n_expert_used, n_embd, n_ff;
     int norm_w;
     float w_scale;
-    int fmt; /* DQ_FMT_Q4_K */
+    int fmt; /* DQ_FMT_Q4_K (packed rows) or DQ_FMT_Q4_K_TILES (expert tiles) */
     const void *wgate, *wup, *wdown;
 } dq_moe_t;
 int dq_moe_workspace_bytes(const dq_moe_t* m, uint32_t n_tok, size_t* bytes);
+/* The expert-tile layout of a stacked Q4_K expert matrix (n_expert experts
+ * of rows x cols, cols % 256 == 0), for dq_moe_t with fmt DQ_FMT_Q4_K_TILES:
+ * per expert, tile of 128 rows and super-block, the tile's packed bytes as
+ * one contiguous run in the order the expert GEMM stages them, so its weight
+ * DMA reads contiguous kilobytes. It is the device layout of the expert
+ * tensors (the reference keeps them as stacked GGUF rows, loaded by
+ * models/dense_forward.cpp:1628-1720 load_matrix; cuda_upload_weights owns the
+ * device form, backend_cuda.cu:2910-2923): d_packed is the dq_weights_pack
+ * form of the stacked matrix, d_tiles receives dq_moe_tiles_bytes() bytes
+ * (the same bytes when rows % 128 == 0). Results of dq_moe_ffn are
+ * bit-identical with either layout. */
+int dq_moe_tiles_bytes(uint32_t n_expert, size_t rows, size_t cols, size_t* bytes);
+int dq_moe_tiles_pack(const void* d_packed, uint32_t n_expert, size_t rows, size_t cols, void* d_tiles, void* stream);
 int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint32_t n_tok, float* d_out, void* d_work,
                size_t work_bytes, void* stream);
 

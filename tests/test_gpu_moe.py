@@ -99,3 +99,28 @@ def test_moe_activation_range(gpu, orc, scale):
     errs = [rel(got[t], want[t]) for t in range(n_tok)]
     print("  per-token rel errs", ["%.2e" % e for e in errs], flush=True)
     assert max(errs) <= 1e-2
+
+
+@pytest.mark.parametrize("n_tok,n_exp,k,E,F", [(64, 8, 2, 4096, 14336), (300, 4, 2, 256, 512), (5, 8, 2, 512, 768),
+                                             (9, 3, 2, 512, 256)])
+def test_moe_tiles_match_rows(gpu, n_tok, n_exp, k, E, F):
+    """The expert-tile layout (dq_moe_tiles_pack, contiguous weight DMA) and
+    the packed rows give bit-identical outputs."""
+    print(f"moe tiles n_tok={n_tok} E={E} F={F}", flush=True)
+    _, mats = make_moe(gpu, n_exp, E, F, seed=E + 3 * F)
+    x = torch.from_numpy(synth.gen_act((n_tok, E), seed=11)).to(gpu)
+    lg = torch.from_numpy(synth.gen_act((n_tok, n_exp), seed=12)).to(gpu)
+    rows = ops.MoeLayer(*mats, n_expert=n_exp, n_expert_used=k, tiled=False)(x, lg)
+    tiles = ops.MoeLayer(*mats, n_expert=n_exp, n_expert_used=k, tiled=True)(x, lg)
+    assert torch.equal(rows, tiles)
+
+
+def test_moe_tiles_errors(gpu):
+    lib = _lib.load()
+    import ctypes
+    n = ctypes.c_size_t(0)
+    assert lib.dq_moe_tiles_bytes(8, 14336, 4096, ctypes.byref(n)) == 0
+    assert n.value == 8 * 112 * 16 * (2 * 128 * 64 + 128 * 16)
+    assert lib.dq_moe_tiles_bytes(8, 14336, 4000, ctypes.byref(n)) == -2   # cols % 256
+    assert lib.dq_moe_tiles_bytes(0, 14336, 4096, ctypes.byref(n)) == -2
+    assert lib.dq_moe_tiles_pack(None, 2, 256, 256, None, None) == -1
