@@ -226,8 +226,9 @@ class MoeCase:
         E, F, X = 4096, 14336, 8
         mk = lambda r, c, sd: ops.QuantMatrix.from_gguf(synth.Q4_K, synth.gen_weights(synth.Q4_K, r, c, sd), r, c,
                                                         device=dev)
-        self.mats = (mk(X * F, E, seed), mk(X * F, E, seed + 1), mk(X * E, F, seed + 2))
-        self.moe = ops.MoeLayer(*self.mats, n_expert=X, n_expert_used=2)
+        # the layer keeps the expert-tile copies only; the packed rows are freed here
+        self.moe = ops.MoeLayer(mk(X * F, E, seed), mk(X * F, E, seed + 1), mk(X * E, F, seed + 2), n_expert=X,
+                                n_expert_used=2)
         self.n_tok = n_tok
         self.x = torch.from_numpy(synth.gen_act((n_tok, E), seed + 3)).to(dev)
         self.lg = torch.from_numpy(synth.gen_act((n_tok, X), seed + 4)).to(dev)

@@ -875,17 +875,19 @@ int cuda_layer_forward(const CudaLayerArgs* A) {
     L.ffn_norm = fn;
     const float* d_rope = nullptr;
     if (slots) {
-        if (A->rope_cache) {
-            const size_t nr = (size_t)A->n_slots * A->rope_stride;
-            if (A->upload_x || g.rope_all_n != nr) {
-                g.rope_all_n = 0;
-                if (!reserve(g.rope_all, nr * 4)) return DQ_ERR_IO;
-                if (hipMemcpyAsync(g.rope_all.p, A->rope_all, nr * 4, hipMemcpyHostToDevice, s) != hipSuccess)
-                    return io_fail();
-                g.rope_all_n = nr;
-            }
-            d_rope = (const float*)g.rope_all.p + (size_t)A->layer_slot * A->rope_stride;
+        // Every slot's table goes to the device with the token's first layer
+        // (upload_x), whether or not that layer rotates: a first layer without
+        // RoPE must not leave the later layers on the previous token's tables
+        // (backend_cuda.cu:4331-4345).
+        const size_t nr = (size_t)A->n_slots * A->rope_stride;
+        if (A->rope_all && nr && (A->upload_x || g.rope_all_n != nr)) {
+            g.rope_all_n = 0;
+            if (!reserve(g.rope_all, nr * 4)) return DQ_ERR_IO;
+            if (hipMemcpyAsync(g.rope_all.p, A->rope_all, nr * 4, hipMemcpyHostToDevice, s) != hipSuccess)
+                return io_fail();
+            g.rope_all_n = nr;
         }
+        if (A->rope_cache) d_rope = (const float*)g.rope_all.p + (size_t)A->layer_slot * A->rope_stride;
     } else {
         if (A->upload_dyn || !g.rope.p) {
             const int rc = upload_rope(A->rope_cache, A->n_rot);

@@ -1042,9 +1042,14 @@ extern "C" int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const
     const int rc = dq_gemm_workspace_bytes(fmt, rows, cols, n_tok, &need);
     if (rc != DQ_OK) return rc;
     if (work_bytes < need || (need && !d_work)) return DQ_ERR_INVALID_ARG;
-    // the K-split plans add their partials into y: the quantizer clears it
+    // the K-split plans add their partials into y: the quantizer clears it,
+    // unless y overlaps x (the quantizer is still reading x), in which case
+    // the GEMM launch clears y itself after the quantizer has finished
+    const uintptr_t xb = reinterpret_cast<uintptr_t>(d_x), yb = reinterpret_cast<uintptr_t>(d_y);
+    const bool overlap = xb < yb + rows * n_tok * sizeof(float) && yb < xb + n_tok * cols * sizeof(float);
     DqZeroSpans z{};
-    const bool zero = dq_zero_span_ok(d_y, rows * n_tok) && rows <= (1u << 30) && dq_gemm_adds_into_y(fmt, rows, cols, n_tok);
+    const bool zero = !overlap && dq_zero_span_ok(d_y, rows * n_tok) && rows <= (1u << 30) &&
+                      dq_gemm_adds_into_y(fmt, rows, cols, n_tok);
     if (zero) {
         z.p[0] = d_y;
         z.n[0] = rows * n_tok;

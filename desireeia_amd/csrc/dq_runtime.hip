@@ -42,6 +42,7 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
 extern "C" int dq_stream_read(const void* d_src, size_t bytes, uint32_t waves_per_cu, uint32_t depth_kb,
                               uint32_t* d_sink, uint32_t never, void* stream) {
     if (!d_src || !d_sink || waves_per_cu == 0 || waves_per_cu > 32) return DQ_ERR_INVALID_ARG;
+    if (waves_per_cu > 4 && waves_per_cu % 4) return DQ_ERR_NOT_SUPPORTED;  // whole 4-wave workgroups per CU
     if (depth_kb != 4 && depth_kb != 8 && depth_kb != 16) return DQ_ERR_NOT_SUPPORTED;
     const size_t chunk = (size_t)depth_kb * 1024;
     if (bytes % chunk || reinterpret_cast<uintptr_t>(d_src) % 16) return DQ_ERR_NOT_SUPPORTED;
@@ -50,12 +51,16 @@ extern "C" int dq_stream_read(const void* d_src, size_t bytes, uint32_t waves_pe
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
         return DQ_ERR_IO;
-    const unsigned grid = (unsigned)((size_t)cus * waves_per_cu / 4);  // 4 waves per workgroup
+    // waves_per_cu waves on every CU: workgroups of 4 waves, or one workgroup
+    // of waves_per_cu waves per CU below 4
+    const unsigned wg_waves = waves_per_cu >= 4 ? 4u : waves_per_cu;
+    const unsigned grid = (unsigned)((size_t)cus * waves_per_cu / wg_waves);
+    const unsigned threads = 64u * wg_waves;
     const auto* src = static_cast<const uint4*>(d_src);
     const hipStream_t st = (hipStream_t)stream;
     const size_t n = bytes / chunk;
-    if (depth_kb == 4) stream_read_kernel<4><<<grid > 0 ? grid : 1, 256, 0, st>>>(src, n, d_sink, never);
-    else if (depth_kb == 8) stream_read_kernel<8><<<grid > 0 ? grid : 1, 256, 0, st>>>(src, n, d_sink, never);
-    else stream_read_kernel<16><<<grid > 0 ? grid : 1, 256, 0, st>>>(src, n, d_sink, never);
+    if (depth_kb == 4) stream_read_kernel<4><<<grid, threads, 0, st>>>(src, n, d_sink, never);
+    else if (depth_kb == 8) stream_read_kernel<8><<<grid, threads, 0, st>>>(src, n, d_sink, never);
+    else stream_read_kernel<16><<<grid, threads, 0, st>>>(src, n, d_sink, never);
     return dq_launch_status();
 }

@@ -474,10 +474,11 @@ class MoeLayer:
     def __init__(self, wgate, wup, wdown, n_expert, n_expert_used, norm_w=True, w_scale=1.0, tiled=True):
         """wgate/wup/wdown: QuantMatrix (stacked experts). tiled: the expert
         GEMMs read the expert-tile copies of the matrices (dq_moe_tiles_pack,
-        contiguous weight DMA); False: the packed rows themselves."""
-        self.mats = (wgate, wup, wdown)
+        contiguous weight DMA), and the layer keeps only those (the packed rows
+        are freed once the caller drops its own references: keeping both would
+        hold the experts' bytes twice); False: the packed rows themselves."""
         self.n_embd, self.n_ff = wgate.cols, wdown.cols
-        bufs, fmt = [m.buf for m in self.mats], wgate.fmt
+        bufs, fmt = [m.buf for m in (wgate, wup, wdown)], wgate.fmt
         if tiled:
             lib = _lib.load()
             bufs = []

@@ -60,8 +60,8 @@ int dq_device_count(void);
 
 /* Streaming-read probe (no counterpart in the reference: it measures this
  * device's read ceiling for the benchmark). Reads `bytes` (a multiple of
- * depth_kb KiB, 16-byte aligned) once with waves_per_cu (1..32) waves per
- * compute unit; each wave reads depth_kb (4, 8 or 16) KiB per step, all loads
+ * depth_kb KiB, 16-byte aligned) once with waves_per_cu waves per compute
+ * unit (1..4, or a multiple of 4 up to 32; others -2); each wave reads depth_kb (4, 8 or 16) KiB per step, all loads
  * of a step in flight together, 64 lanes x 16 contiguous bytes per load
  * instruction. Writes d_sink[0] only if the XOR of the words equals `never`. */
 int dq_stream_read(const void* d_src, size_t bytes, uint32_t waves_per_cu, uint32_t depth_kb, uint32_t* d_sink,
@@ -146,8 +146,9 @@ int dq_gemv_group_f32(const dq_gemv_job_t* jobs, size_t n, size_t cols, const fl
  * (undone exactly on the output), so any finite activation magnitude stays
  * inside fp16. `d_work` (dq_gemm_workspace_bytes() bytes) holds the quantized
  * activations, for Q4_K their per-32 block sums (the min-term input, tokens
- * contiguous per super-block), and their row scales. Other formats and
- * cols % 256 != 0: -2. */
+ * contiguous per super-block), and their row scales. d_y may overlap d_x
+ * (the K-split plans then clear y after the quantizer, in a launch of their
+ * own, instead of inside it). Other formats and cols % 256 != 0: -2. */
 int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t n_tok, size_t* bytes);
 int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,
             float* d_y, void* d_work, size_t work_bytes, void* stream);

@@ -496,6 +496,56 @@ def test_layer_forward_chain(lib, orc):
     lib.cuda_kv_cache_release()
 
 
+def test_layer_slots_first_layer_without_rope(lib, orc):
+    """Per-layer slots over two tokens where the token's first layer has no
+    RoPE (rope_cache NULL) and the second takes its table from slot 1: the
+    tables of every slot go to the device with the first layer (upload_x), so
+    the second token's second layer rotates with its own position's table.
+    Bit-identical to plain calls given each layer's table directly."""
+    E, n_head, n_kv, F, n_ctx, pos = 1024, 8, 2, 2816, 128, 50
+    kc, vc, pb = prior_cache(orc, 2, n_ctx, n_kv, 128, pos, seed=21)
+    types = (Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K)
+    L0 = make_layer(lib, orc, E, n_head, n_kv, F, types, 60)
+    L1 = make_layer(lib, orc, E, n_head, n_kv, F, types, 70)
+    xs = [synth.gen_act(E, seed=30 + t) for t in range(2)]
+    no_rope = np.zeros(128, np.float32)  # placeholder for layer_args; cleared below
+
+    def run(slots):
+        assert lib.cuda_kv_cache_reserve(kc.size)
+        assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+        outs, keep = [], []
+        for t in range(2):
+            p = pos + t
+            rope_t = orc.rope_cache(128, p, 10000.0)
+            rope_all = np.ascontiguousarray(np.stack([np.zeros(128, np.float32), rope_t]))
+            dyn = np.array([p, 0, p, 0], np.uint32)
+            out = np.full(E, np.nan, np.float32)
+            A0 = layer_args(*L0[:3], E, n_head, n_kv, F, 0, p, no_rope, xs[t], None, 1, 0, 1)
+            A0.rope_cache = None
+            A1 = layer_args(*L1[:3], E, n_head, n_kv, F, n_ctx * pb, p, rope_t, None, out, 0, 1, 1)
+            if slots:
+                for A, s in ((A0, 0), (A1, 1)):
+                    A.dyn_all, A.rope_all, A.n_slots, A.rope_stride, A.layer_slot = (
+                        dyn.ctypes.data, rope_all.ctypes.data, 2, 128, s)
+                    A.pos, A.upload_dyn = 0, 0
+            assert lib.cuda_layer_forward(ctypes.byref(A0)) == OK
+            assert lib.cuda_layer_forward(ctypes.byref(A1)) == OK
+            keep.append((rope_t, rope_all, dyn))
+            outs.append(out)
+        lib.cuda_kv_cache_release()
+        return outs
+
+    plain, slotted = run(False), run(True)
+    for t in range(2):
+        assert np.isfinite(plain[t]).all()
+        assert np.array_equal(slotted[t], plain[t]), f"token {t}"
+    # and the rotation matters: the second token's output differs from the first's table
+    assert not np.array_equal(plain[0], plain[1])
+    for L in (L0, L1):
+        for m in L[0].values():
+            m.free()
+
+
 @pytest.mark.parametrize("hd,n_head,n_kv,qwen", [(64, 16, 4, False), (64, 16, 4, True), (256, 8, 2, False),
                                                 (256, 8, 2, True)])
 def test_layer_forward_head_dims(lib, orc, hd, n_head, n_kv, qwen):

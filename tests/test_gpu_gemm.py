@@ -176,3 +176,27 @@ def test_gemm_activation_layout(gpu, qtype, cols, n_tok):
     assert np.array_equal(gs, s)
     gi = w[off + a256(4 * n_tok):off + a256(4 * n_tok) + 4 * n_tok].view(np.float32)
     assert np.array_equal(gi, (np.float32(1.0) / s).astype(np.float32))
+
+
+@pytest.mark.parametrize("qtype,n,n_tok", [(synth.Q4_K, 4096, 512), (synth.Q6_K, 4096, 512),
+                                           (synth.Q8_0, 2048, 64), (synth.Q6_K, 4096, 16)])
+def test_gemm_in_place(gpu, qtype, n, n_tok):
+    """y may overlap x: an in-place product (y written over x) and one whose y
+    starts inside x equal the out-of-place product bit for bit, whichever plan
+    (K split or not) the shape takes."""
+    print(f"gemm in place type={qtype} n={n} n_tok={n_tok}", flush=True)
+    w = synth.gen_weights(qtype, n, n, seed=n + n_tok)
+    x = torch.from_numpy(synth.gen_act((n_tok, n), seed=n_tok + 3)).to(gpu)
+    m = ops.QuantMatrix.from_gguf(qtype, w, n, n)
+    want = ops.gemm(m, x.clone())
+    buf = x.clone()
+    got = ops.gemm(m, buf, out=buf)
+    assert got.data_ptr() == buf.data_ptr()
+    assert torch.equal(got, want)
+    # y begins half a row into x
+    big = torch.zeros(n_tok * n + n // 2, dtype=torch.float32, device=gpu)
+    big[:n_tok * n] = x.reshape(-1)
+    xv = big[:n_tok * n].view(n_tok, n)
+    yv = big[n // 2:].view(n_tok, n)
+    ops.gemm(m, xv, out=yv)
+    assert torch.equal(yv, want)
