@@ -200,6 +200,8 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
     __shared__ float qsc[HPK];                          // per head: 1/sqrt(hd) / query scale
     __shared__ float dvs[NB];                           // per block: weight operand scale
     __shared__ float wmx[NW][HPK], wsm[NW][HPK];        // per-wave maxima and sums
+    constexpr int NSTG = FUSE ? (2 * HPW + 5) * HD : HPW * HD;
+    __shared__ __align__(16) float stg[NW][NSTG];       // per wave: raw inputs staged by DMA
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n16 = lane & 15, g4 = lane >> 4;
@@ -219,57 +221,35 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
     const int n_load = new_row ? nv - 1 : nv;
 
     // ---- raw inputs of this wave's query heads (wave w takes heads w, w+NW)
-    // and, under FUSE, their bias, QK-norm weights and RoPE pairs, and the new
-    // K (wave 0) / V (wave 1) row: loaded before the tile, so that waiting
-    // for them leaves the tile's loads in flight
-    float qx[HPW][QV], qb[HPW][QV];
-    float rc[RP], rs[RP], nq[QV], xr[QV], xbias[QV], xn[QV];
+    // and, under FUSE, their biases, the RoPE table, the QK-norm weights and
+    // the new K (wave 0) / V (wave 1) row with its bias: staged into the
+    // wave's LDS area by DMA ahead of the tile's K and V rows, and read after
+    // a wait counted to cover exactly these (absent inputs stage q and are
+    // ignored). The compiler waits for every outstanding load at the first
+    // use of a plain load issued next to LDS DMAs, which held the query work
+    // behind the whole tile transfer (and, under FUSE, the tile's DMAs behind
+    // the query loads).
+    const float* const dmy = A.q;
+    auto stage = [&](const float* src, int off) {
+#pragma unroll
+        for (int i = 0; i < HD / 64; ++i)
+            __builtin_amdgcn_global_load_lds(src + 64 * i + lane, DQ_LDS_PTR(&stg[wave][off + 64 * i]), 4, 0, 0);
+    };
 #pragma unroll
     for (int t = 0; t < HPW; ++t) {
         const size_t hq = (size_t)kvh * HPK + min(wave + NW * t, HPK - 1);
-#pragma unroll
-        for (int i = 0; i < QV; ++i) {
-            qx[t][i] = A.q[hq * HD + lane + 64 * i];
-            qb[t][i] = 0.0f;
-        }
-        if constexpr (FUSE) {
-            if (A.post.bq) {
-#pragma unroll
-                for (int i = 0; i < QV; ++i) qb[t][i] = A.post.bq[hq * HD + lane + 64 * i];
-            }
-        }
+        stage(A.q + hq * HD, t * HD);
+        if constexpr (FUSE) stage(A.post.bq ? A.post.bq + hq * HD : dmy, (HPW + t) * HD);
     }
-#pragma unroll
-    for (int i = 0; i < RP; ++i) {
-        rc[i] = 1.0f;
-        rs[i] = 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < QV; ++i) nq[i] = xr[i] = xbias[i] = xn[i] = 0.0f;
     if constexpr (FUSE) {
-        if (A.rope) {
-#pragma unroll
-            for (int i = 0; i < RP; ++i) {
-                const int j = HD == 64 ? (lane & 31) : lane + 64 * i;
-                rc[i] = A.rope[2 * j];
-                rs[i] = A.rope[2 * j + 1];
-            }
-        }
-        if (A.post.q_norm) {
-#pragma unroll
-            for (int i = 0; i < QV; ++i) nq[i] = A.post.q_norm[lane + 64 * i];
-        }
-        if (new_row && wave < 2) {  // wave-uniform
-            const float* src = wave == 0 ? A.k : A.v;
-            const float* bias = wave == 0 ? A.post.bk : A.post.bv;
-#pragma unroll
-            for (int i = 0; i < QV; ++i) {
-                const size_t o = (size_t)kvh * HD + lane + 64 * i;
-                xr[i] = src[o];
-                if (bias) xbias[i] = bias[o];
-                if (wave == 0 && A.post.k_norm) xn[i] = A.post.k_norm[lane + 64 * i];
-            }
-        }
+        stage(A.rope ? A.rope : dmy, (2 * HPW) * HD);
+        stage(A.post.q_norm ? A.post.q_norm : dmy, (2 * HPW + 1) * HD);
+        const size_t o = (size_t)kvh * HD;
+        const float* src = wave == 0 ? A.k : A.v;
+        const float* bias = wave == 0 ? A.post.bk : A.post.bv;
+        stage(src + o, (2 * HPW + 2) * HD);
+        stage(bias ? bias + o : dmy, (2 * HPW + 3) * HD);
+        stage(A.post.k_norm ? A.post.k_norm : dmy, (2 * HPW + 4) * HD);
     }
     // ---- the tile's K and V rows, straight into LDS (lane i of a dword DMA
     // writes dword i of the instruction's 64-dword span, row r of the tile at
@@ -289,6 +269,39 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
             const uint32_t go = (uint32_t)min(r, rmax) * (uint32_t)A.pos_bytes + 4u * (uint32_t)c;
             __builtin_amdgcn_global_load_lds(kb + go, DQ_LDS_PTR(kt + 64 * j), 4, 0, 0);
             __builtin_amdgcn_global_load_lds(vb + go, DQ_LDS_PTR(vt + 64 * j), 4, 0, 0);
+        }
+    }
+    // the staged inputs have landed (the tile's DMAs, issued after them, may
+    // not); a wave's LDS operations run in issue order, so only the compiler
+    // is kept from moving the reads above the wait
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * DPW < 63 ? 2 * DPW : 63) : "memory");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float qx[HPW][QV], qb[HPW][QV];
+    float rc[RP], rs[RP], nq[QV], xr[QV], xbias[QV], xn[QV];
+    {
+        const float* sg = stg[wave];
+#pragma unroll
+        for (int t = 0; t < HPW; ++t)
+#pragma unroll
+            for (int i = 0; i < QV; ++i) {
+                qx[t][i] = sg[t * HD + lane + 64 * i];
+                qb[t][i] = FUSE ? sg[(HPW + t) * HD + lane + 64 * i] : 0.0f;
+            }
+#pragma unroll
+        for (int i = 0; i < RP; ++i) {
+            const int j = HD == 64 ? (lane & 31) : lane + 64 * i;
+            rc[i] = FUSE ? sg[2 * HPW * HD + 2 * j] : 1.0f;
+            rs[i] = FUSE ? sg[2 * HPW * HD + 2 * j + 1] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < QV; ++i) {
+            const int c = lane + 64 * i;
+            nq[i] = FUSE ? sg[(2 * HPW + 1) * HD + c] : 0.0f;
+            xr[i] = FUSE ? sg[(2 * HPW + 2) * HD + c] : 0.0f;
+            xbias[i] = FUSE ? sg[(2 * HPW + 3) * HD + c] : 0.0f;
+            xn[i] = FUSE ? sg[(2 * HPW + 4) * HD + c] : 0.0f;
         }
     }
     // ---- zero rows HPK..15 of the query and weight operands (the MFMA rows

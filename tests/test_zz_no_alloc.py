@@ -52,18 +52,28 @@ def test_noalloc_matches_allocating_entry_point(gpu, orc):
 
 
 def test_noalloc_rejects_oversized_shape(gpu):
-    """32 heads of 128 need 528 bytes per head and 64-position tile: the
-    16 MiB scratch covers 63488 positions; one more is refused, nothing runs."""
+    """The 16 MiB scratch covers the contexts whose records
+    (dq_attn_workspace_bytes) fit in it, for 32 heads of 128; the first
+    context past them is refused and nothing runs."""
     lib = _lib.load()
-    n = ctypes.c_size_t(0)
-    _lib.check(lib.dq_attn_workspace_bytes(32, 8, HD, 63488, ctypes.byref(n)), "dq_attn_workspace_bytes")
-    assert n.value <= 16 << 20
-    _lib.check(lib.dq_attn_workspace_bytes(32, 8, HD, 63489, ctypes.byref(n)), "dq_attn_workspace_bytes")
-    assert n.value > 16 << 20
+
+    def need(n_ctx):
+        n = ctypes.c_size_t(0)
+        _lib.check(lib.dq_attn_workspace_bytes(32, 8, HD, n_ctx, ctypes.byref(n)), "dq_attn_workspace_bytes")
+        return n.value
+
+    lo, hi = 1, 1 << 22  # need(lo) fits, need(hi) does not
+    assert need(lo) <= 16 << 20 < need(hi)
+    while hi - lo > 1:
+        mid = (lo + hi) // 2
+        lo, hi = (mid, hi) if need(mid) <= 16 << 20 else (lo, mid)
+    big = hi
+    print(f"noalloc: contexts up to {lo} positions fit the scratch", flush=True)
+    assert lo >= 60000  # config 4's heads cover long contexts
     q = torch.zeros(32 * HD, device=gpu)
     kc = torch.zeros(8 * 136, dtype=torch.uint8, device=gpu)  # position 0's rows, were anything to run
     out = torch.full((32 * HD,), 7.0, device=gpu)
-    rc = lib.dq_attn_decode_q8_noalloc(ops._ptr(q), ops._ptr(kc), ops._ptr(kc), 32, 8, HD, 0, 0, None, 63489,
+    rc = lib.dq_attn_decode_q8_noalloc(ops._ptr(q), ops._ptr(kc), ops._ptr(kc), 32, 8, HD, 0, 0, None, big,
                                        ops._ptr(out), ops._stream())
     assert rc == -2  # DQ_ERR_NOT_SUPPORTED
     torch.cuda.synchronize()
