@@ -976,11 +976,12 @@ static GemmPlan plan_gemm(int fmt, size_t rows, size_t n_tok, int nsb) {
             }
         }
     }
-    const char* fw = getenv("DQ_GEMM_SHAPE");
-    const char* fs = getenv("DQ_GEMM_SPLIT");
+    // tuning overrides, read once per process
+    static const int force_shape = [] { const char* e = getenv("DQ_GEMM_SHAPE"); return e ? atoi(e) : 0; }();
+    static const int force_split = [] { const char* e = getenv("DQ_GEMM_SPLIT"); return e ? atoi(e) : 0; }();
     GemmPlan o = best;
-    if (fw && (atoi(fw) == 41 || atoi(fw) == 22)) o.nwn = atoi(fw) / 10;
-    if (fs && (atoi(fs) == 1 || atoi(fs) == 2)) o.split = atoi(fs);
+    if (force_shape == 41 || force_shape == 22) o.nwn = force_shape / 10;
+    if (force_split == 1 || force_split == 2) o.split = force_split;
     return plan_ok(fmt, o.nwn, o.split, nsb) ? o : best;
 }
 

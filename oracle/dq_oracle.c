@@ -683,6 +683,28 @@ static int gemm_impl(int type, const uint8_t* w, size_t rows, size_t cols, const
     return DQO_OK;
 }
 
+/* The weight side of the i8_gemm semantics above, as unpack_row gives it
+ * (core/matmul.cpp:505-638): per row, the integer weights q[cols], the scale
+ * a of each 16 columns and the Q4_K offset m of each 16 (0 for the other
+ * types). With the per-32 activation integers and scales and the exact block
+ * sums of dqo_quantize_q8_1, the product is
+ *   y[t][r] = sum_k (a q)[r][k] (dx q_x)[t][k] - sum_b m[r][b] sx[t][b],
+ * which a test can form in fp64 for every output of a full-size product. */
+int dqo_gemm_operands(int type, const uint8_t* w, size_t rows, size_t cols, int8_t* q, float* a, float* m) {
+    if (!gemv_cols_ok(type, cols) || type == DQO_Q8_1) return DQO_ERR_NOT_SUPPORTED;
+    const size_t nb = cols / QK;
+    const size_t row_bytes = dqo_row_size(type, (int64_t)cols);
+    unpacked_row u;
+    for (size_t r = 0; r < rows; ++r) {
+        u.q = q + r * cols;
+        u.a = a + r * 2 * nb;
+        u.m = m + r * 2 * nb;
+        memset(u.m, 0, 2 * nb * sizeof(float));
+        unpack_row(type, w + r * row_bytes, cols, &u);
+    }
+    return DQO_OK;
+}
+
 int dqo_gemm(int type, const uint8_t* w, size_t rows, size_t cols, const float* x,
              size_t n_tok, float* y, size_t row0, size_t row1, size_t t0, size_t t1) {
     return gemm_impl(type, w, rows, cols, x, n_tok, y, NULL, row0, row1, t0, t1);

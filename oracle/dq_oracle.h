@@ -83,6 +83,9 @@ int dqo_gemm(int type, const uint8_t* w, size_t rows, size_t cols,
 int dqo_gemm_f64(int type, const uint8_t* w, size_t rows, size_t cols,
                  const float* x, size_t n_tok, double* y,
                  size_t row0, size_t row1, size_t t0, size_t t1);
+/* unpack_row's integer weights, per-16 scales and per-16 Q4_K offsets of every
+ * row (the weight operands of the prefill GEMM semantics). */
+int dqo_gemm_operands(int type, const uint8_t* w, size_t rows, size_t cols, int8_t* q, float* a, float* m);
 
 /* Q8_0 KV rows (kv/kv_quant.cpp). */
 float dqo_kv_dot_q8_0(const float* q, const uint8_t* row, size_t dim);

@@ -70,6 +70,7 @@ class Oracle:
         L.dqo_matmul_pq.argtypes = [c_int, c_p, c_size, c_size, c_p, c_p, c_p, c_p, c_size, c_size]
         L.dqo_gemm.argtypes = [c_int, c_p, c_size, c_size, c_p, c_size, c_p, c_size, c_size, c_size, c_size]
         L.dqo_gemm_f64.argtypes = [c_int, c_p, c_size, c_size, c_p, c_size, c_p, c_size, c_size, c_size, c_size]
+        L.dqo_gemm_operands.argtypes = [c_int, c_p, c_size, c_size, c_p, c_p, c_p]
         L.dqo_kv_dot_q8_0.restype = c_f
         L.dqo_kv_dot_q8_0.argtypes = [c_p, c_p, c_size]
         L.dqo_kv_axpy_q8_0.argtypes = [c_p, c_p, c_size, c_f]
@@ -184,6 +185,18 @@ class Oracle:
         return y
 
     # -- attention / router / glue
+    def gemm_operands(self, qtype, w, rows, cols):
+        """unpack_row of every row: int8 weights [rows][cols], scale and Q4_K
+        offset of each 16 columns [rows][cols/16] (the prefill GEMM's weight
+        operands; y = (a q) (dx q_x)^T - m sx^T)."""
+        q = np.empty((rows, cols), np.int8)
+        a = np.empty((rows, cols // 16), np.float32)
+        m = np.empty((rows, cols // 16), np.float32)
+        rc = self.L.dqo_gemm_operands(qtype, _p(np.ascontiguousarray(w)), rows, cols, _p(q), _p(a), _p(m))
+        if rc != 0:
+            raise ValueError(f"gemm_operands rc={rc}")
+        return q, a, m
+
     def kv_dot(self, q, row, dim):
         return self.L.dqo_kv_dot_q8_0(_p(np.ascontiguousarray(q, np.float32)),
                                       _p(np.ascontiguousarray(row, np.uint8)), dim)

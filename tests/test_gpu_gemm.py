@@ -1,7 +1,9 @@
 """Prefill GEMM on the GPU against the oracle's i8_gemm semantics (reference
 core/matmul.cpp:806-845, core/i8gemm_impl.h:326-419): norm-wise relative error
 <= 4e-3 (the MFMA GEMM tolerance). The full config-3 shapes are checked on
-row/token sub-blocks that cover the first, middle and last tiles."""
+row/token sub-blocks against the oracle's GEMM itself, and in every output
+(overall and per workgroup tile) against the fp64 product of the oracle's
+operands."""
 import ctypes
 
 import numpy as np
@@ -37,6 +39,59 @@ def test_gemm_config3(gpu, orc, qtype, rows, cols, n_tok):
         errs.append(e)
         assert e <= TOL, (r0, t0, e)
     print("  rel errs", ["%.2e" % e for e in errs])
+
+
+def f64_product(orc, qtype, w, rows, cols, x, dev):
+    """Every output of the prefill product in fp64 on the device, from the
+    oracle's operands: y = (a q)(dx q_x)^T - m sx^T, with the weight integers,
+    per-16 scales and Q4_K offsets of unpack_row and the per-32 activation
+    integers, scales and exact block sums of the oracle's quantizer
+    (test_oracle_gemm.py pins this form against the oracle's fp64 GEMM and the
+    bit-exact dequantizer). Returns [n_tok][rows] float64 on the device."""
+    q, a, m = orc.gemm_operands(qtype, w, rows, cols)
+    n_tok = x.shape[0]
+    xq = np.empty((n_tok, cols), np.int8)
+    dx = np.empty((n_tok, cols // 32), np.float32)
+    sx = np.empty((n_tok, cols // 32), np.float32)
+    for t in range(n_tok):
+        xq[t], dx[t], _, sx[t] = orc.quantize_q8_1(x[t])
+    f64 = torch.float64
+    wa = torch.from_numpy(q).to(dev, f64) * torch.from_numpy(a).to(dev, f64).repeat_interleave(16, dim=1)
+    xqt = (torch.from_numpy(xq).to(dev, f64) * torch.from_numpy(dx).to(dev, f64).repeat_interleave(32, dim=1)).t()
+    yt = torch.mm(wa, xqt.contiguous())  # [rows][n_tok]
+    del wa
+    if qtype == synth.Q4_K:
+        mt = torch.from_numpy(np.ascontiguousarray(m[:, ::2])).to(dev, f64)
+        yt -= torch.mm(mt, torch.from_numpy(sx).to(dev, f64).t().contiguous())
+    return yt.t()
+
+
+@pytest.mark.parametrize("qtype,rows,cols", [
+    (synth.Q4_K, 14336, 4096),   # config 3 up/gate
+    (synth.Q6_K, 4096, 14336),   # config 3 down
+    (synth.Q8_0, 14336, 4096),
+    (synth.Q4_0, 4096, 14336),
+])
+def test_gemm_config3_every_output(gpu, orc, qtype, rows, cols):
+    """All n_tok x rows outputs of the config-3 products against the fp64
+    product of the oracle's operands: norm-wise within the GEMM bound overall
+    and within every 128-token x 256-row tile (a misplaced or skipped
+    workgroup tile fails on its own)."""
+    n_tok = 512
+    print(f"gemm every output type={qtype} {n_tok}x{cols} . {cols}x{rows}", flush=True)
+    w = synth.gen_weights(qtype, rows, cols, seed=rows + 11)
+    x = synth.gen_act((n_tok, cols), seed=cols + 13)
+    m = ops.QuantMatrix.from_gguf(qtype, w, rows, cols)
+    y = ops.gemm(m, torch.from_numpy(x).to(gpu)).double()
+    want = f64_product(orc, qtype, w, rows, cols, x, gpu)
+    assert torch.isfinite(y).all()
+    e = float(torch.linalg.norm(y - want) / torch.linalg.norm(want))
+    tiles = (y - want).reshape(n_tok // 128, 128, rows // 256, 256).square().sum(dim=(1, 3)).sqrt() / \
+        want.reshape(n_tok // 128, 128, rows // 256, 256).square().sum(dim=(1, 3)).sqrt()
+    worst = float(tiles.max())
+    print(f"  rel err {e:.2e}, worst 128x256 tile {worst:.2e} of {tiles.numel()}", flush=True)
+    assert e <= TOL
+    assert worst <= TOL
 
 
 @pytest.mark.parametrize("qtype,rows,cols,n_tok", [

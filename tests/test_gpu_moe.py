@@ -12,6 +12,7 @@ from desireeia_amd import _lib, ops, synth
 pytestmark = pytest.mark.gpu
 Q4K = synth.Q4_K
 TOL = 4e-3
+TOL_TOKEN = 1e-2  # per-token structural check (test_moe_ffn)
 
 
 def rel(a, b):
@@ -46,6 +47,20 @@ def make_moe(gpu, n_exp, E, F, seed):
     return (wg, wu, wd), mats
 
 
+def moe_oracle_all(orc, ws, n_exp, E, F, x, lg, n_tok, k, threads=8):
+    """The oracle's expert FFN for every token, token ranges on host threads
+    (the C oracle releases the interpreter lock)."""
+    from concurrent.futures import ThreadPoolExecutor
+    step = -(-n_tok // threads)
+    ranges = [(t0, min(n_tok, t0 + step)) for t0 in range(0, n_tok, step)]
+    with ThreadPoolExecutor(len(ranges)) as ex:
+        parts = list(ex.map(lambda r: orc.moe_ffn(Q4K, *ws, n_exp, E, F, x, lg, n_tok, k, t0=r[0], t1=r[1]), ranges))
+    out = np.zeros((n_tok, E), np.float32)
+    for (t0, t1), p in zip(ranges, parts):
+        out[t0:t1] = p[t0:t1]
+    return out
+
+
 @pytest.mark.parametrize("n_tok,n_exp,k,E,F,skew", [
     (64, 8, 2, 4096, 14336, False),   # config 5
     (5, 8, 2, 512, 768, False),       # most experts get no token
@@ -61,13 +76,18 @@ def test_moe_ffn(gpu, orc, n_tok, n_exp, k, E, F, skew):
         lg[:, 0] += 4.0  # expert 0 in nearly every token's top-k
     moe = ops.MoeLayer(*mats, n_expert=n_exp, n_expert_used=k)
     got = moe(torch.from_numpy(x).to(gpu), torch.from_numpy(lg).to(gpu)).cpu().numpy()
-    # the CPU oracle checks a prefix of the tokens at the full shape (it
-    # re-streams 2 experts' 177 MB per token); every token elsewhere
-    n_chk = 16 if E >= 4096 else n_tok
-    want = orc.moe_ffn(Q4K, *ws, n_exp, E, F, x, lg, n_tok, k, t0=0, t1=n_chk)
-    e = rel(got[:n_chk], want[:n_chk])
-    print(f"  rel err {e:.3e}", flush=True)
+    # every token against the CPU oracle (token ranges on host threads: the
+    # oracle re-streams two experts' 177 MB per token at the full shape)
+    want = moe_oracle_all(orc, ws, n_exp, E, F, x, lg, n_tok, k)
+    e = rel(got, want)
+    per_tok = [rel(got[t], want[t]) for t in range(n_tok)]
+    print(f"  rel err {e:.3e}, per token median {np.median(per_tok):.2e} worst {max(per_tok):.2e}", flush=True)
     assert e <= TOL
+    # each token on its own within TOL_TOKEN: a per-256 rounding tie of the
+    # FFN intermediate that falls differently on the GPU and the CPU moves one
+    # token by up to ~6e-3 (see test_moe_activation_range); a token sent to a
+    # wrong expert, or a misplaced expert tile, is off by O(1)
+    assert max(per_tok) <= TOL_TOKEN
     # a second call on the same workspace gives the same bits
     again = moe(torch.from_numpy(x).to(gpu), torch.from_numpy(lg).to(gpu)).cpu().numpy()
     assert np.array_equal(got, again)

@@ -61,3 +61,39 @@ def test_sub_ranges(orc):
     full = orc.gemm(synth.Q6_K, w, rows, cols, x, n_tok)
     part = orc.gemm(synth.Q6_K, w, rows, cols, x, n_tok, 4, 12, 2, 6)
     assert np.array_equal(part[2:6, 4:12], full[2:6, 4:12])
+
+
+@pytest.mark.parametrize("qtype", FMTS)
+def test_gemm_operands_rebuild_dequant(orc, qtype):
+    """The GEMM weight operands (unpack_row: integers, scale and Q4_K offset
+    per 16) rebuild the bit-exact dequantizer's weights as fl(fl(a q) - m),
+    the dequantizer's own two roundings (quant/quant.cpp:255-273, 517-543)."""
+    rows, cols = 24, 1024
+    w = synth.gen_weights(qtype, rows, cols, seed=71)
+    q, a, m = orc.gemm_operands(qtype, w, rows, cols)
+    deq = np.stack([orc.dequantize_row(qtype, w[r], cols) for r in range(rows)])
+    rebuilt = (q.astype(np.float32) * np.repeat(a, 16, axis=1)).astype(np.float32) - np.repeat(m, 16, axis=1)
+    assert np.array_equal(rebuilt.view(np.uint32), deq.astype(np.float32).view(np.uint32))
+    if qtype != synth.Q4_K:
+        assert not m.any()
+
+
+@pytest.mark.parametrize("qtype", FMTS)
+def test_gemm_operands_product_is_f64_twin(orc, qtype):
+    """The fp64 matrix form the GPU whole-output test uses,
+    y = (a q)(dx q_x)^T - m sx^T over the oracle's operands and per-32
+    activations, equals the oracle's row-by-row fp64 GEMM."""
+    rows, cols, n_tok = 40, 768, 9
+    w = synth.gen_weights(qtype, rows, cols, seed=81)
+    x = synth.gen_act((n_tok, cols), seed=82)
+    q, a, m = orc.gemm_operands(qtype, w, rows, cols)
+    Wa = q.astype(np.float64) * np.repeat(a, 16, axis=1).astype(np.float64)
+    Xq = np.empty((n_tok, cols), np.float64)
+    Sx = np.empty((n_tok, cols // 32), np.float64)
+    for t in range(n_tok):
+        xq, dx, _, fs = orc.quantize_q8_1(x[t])
+        Xq[t] = xq.astype(np.float64) * np.repeat(dx, 32).astype(np.float64)
+        Sx[t] = fs
+    y = Xq @ Wa.T - Sx @ m[:, ::2].astype(np.float64).T
+    want = orc.gemm(qtype, w, rows, cols, x, n_tok, f64=True)
+    assert np.max(np.abs(y - want)) <= 1e-12 * np.max(np.abs(want))
