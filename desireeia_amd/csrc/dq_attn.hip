@@ -195,7 +195,11 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
     __shared__ __align__(16) _Float16 qhs[16 * QROW];   // scaled query, fp16 hi (rows >= HPK zero)
     __shared__ __align__(16) _Float16 qls[16 * QROW];   // and lo
     __shared__ __align__(16) float dvf[NB][TP];         // V block scales times dvs (0 past the tile)
-    __shared__ __align__(16) float ew[16][TP];          // tile weights exp(s - m) (rows >= HPK zero)
+    // tile weights exp(s - m) (rows >= HPK zero), rows padded by 4 floats: the
+    // weighted V sum reads one column of 16 rows per instruction, which at a
+    // 256-byte row stride would fall in one bank
+    constexpr int EWS = TP + 4;
+    __shared__ __align__(16) float ew[16][EWS];
     __shared__ uint32_t nrow[2][RBW];                   // FUSE: the new K and V rows
     __shared__ float qsc[HPK];                          // per head: 1/sqrt(hd) / query scale
     __shared__ float dvs[NB];                           // per block: weight operand scale
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(NT) void attn_tile_kernel(AttnArgs A) {
     // ---- zero rows HPK..15 of the query and weight operands (the MFMA rows
     // that no head fills)
     {
-        constexpr int QZ = (16 - HPK) * QROW * 2 / 16, EZ = (16 - HPK) * TP * 4 / 16;
+        constexpr int QZ = (16 - HPK) * QROW * 2 / 16, EZ = (16 - HPK) * EWS * 4 / 16;
         const uint4 z = {0u, 0u, 0u, 0u};
         for (int i = tid; i < QZ; i += NT) {
             reinterpret_cast<uint4*>(qhs + HPK * QROW)[i] = z;
