@@ -43,15 +43,64 @@ __device__ __forceinline__ int q4k_min(int j, uint32_t w0, uint32_t w1, uint32_t
     return (int)(((b1 & 63) & ~hi) | (((b2 >> 4) | ((b1 >> 6) << 4)) & hi));
 }
 
-// The 8 values fp16(-dmin * m_j) of a Q4_K super-block header hd (d and dmin
-// in hd.x, the 12 scale bytes in hd.y..hd.w): the weight side of the
-// super-block's min term as one 8-wide MFMA K slice. Zeros when !ok.
+// The 8 6-bit scales (sc_bytes) or mins (m_bytes) of a Q4_K super-block
+// header hd (d and dmin in hd.x, the 12 scale bytes in hd.y..hd.w) as bytes:
+// j = 0..3 in lo, 4..7 in hi (the packing of quant/quant.cpp:22-29, four at
+// a time: sc_j = b0_j & 63, sc_{j+4} = (b2_j & 15) | (b0_j >> 6) << 4, and
+// the mins alike from b1 and the high nibbles of b2).
+__device__ __forceinline__ void q4k_sc_bytes(const dq_u32x4& hd, uint32_t& lo, uint32_t& hi) {
+    lo = hd.y & 0x3F3F3F3Fu;
+    hi = (hd.w & 0x0F0F0F0Fu) | ((hd.y >> 2) & 0x30303030u);
+}
+__device__ __forceinline__ void q4k_m_bytes(const dq_u32x4& hd, uint32_t& lo, uint32_t& hi) {
+    lo = hd.z & 0x3F3F3F3Fu;
+    hi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+}
+
+// Pairs p[i] = (b_2i * f, b_2i+1 * f) in fp16 of the 8 bytes of lo, hi (each
+// below 1024): the byte is exact in fp16 and the product rounds once, as the
+// float product fp16((float)f * b) does.
+__device__ __forceinline__ void bytes8_times(uint32_t lo, uint32_t hi, _Float16 f, h2 (&p)[4]) {
+    const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f}, ff = {f, f};
+    p[0] = (magic_pair(lo, 0x04010400u) - bias) * ff;
+    p[1] = (magic_pair(lo, 0x04030402u) - bias) * ff;
+    p[2] = (magic_pair(hi, 0x04010400u) - bias) * ff;
+    p[3] = (magic_pair(hi, 0x04030402u) - bias) * ff;
+}
+
+// The 8 values fp16(-dmin * m_j) of a Q4_K super-block header hd: the weight
+// side of the super-block's min term as one 8-wide MFMA K slice. Zeros when
+// !ok.
 __device__ __forceinline__ h8 q4k_neg_mins(const dq_u32x4& hd, bool ok) {
-    const float dmin = dq_h2f((uint16_t)(hd.x >> 16));
-    _Float16 v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (_Float16)(ok ? -(dmin * (float)q4k_min(i, hd.y, hd.z, hd.w)) : 0.0f);
-    return *reinterpret_cast<const h8*>(v);
+    uint32_t lo, hi;
+    q4k_m_bytes(hd, lo, hi);
+    const _Float16 f = ok ? __builtin_bit_cast(_Float16, (uint16_t)((hd.x >> 16) ^ 0x8000u)) : (_Float16)0.0f;
+    h2 p[4];
+    bytes8_times(lo, hi, f, p);
+    return __builtin_bit_cast(h8, dq_u32x4{__builtin_bit_cast(uint32_t, p[0]), __builtin_bit_cast(uint32_t, p[1]),
+                                           __builtin_bit_cast(uint32_t, p[2]), __builtin_bit_cast(uint32_t, p[3])});
+}
+
+// Nibble pairs to scaled fp16 pairs with one v_and_or and one fma: two 4-bit
+// values q_a, q_b at bits 6-9 and 22-25 of v (the caller shifts them there)
+// are slotted under the exponent of 16.0 (0x4C00, mantissa step 2^-6), so
+// each half is 16 + q exactly, and fma(16 + q, s, c) with c = -16 s is
+// q * s exactly before its single rounding: the same fp16 as (q) * s.
+// Needs 16 |s| finite in fp16: |s| <= 4094. The mask and the exponent word
+// come in registers (NibConst): gfx9 VOP3 instructions take no literal.
+struct NibConst {
+    uint32_t mask;  // 0x03C003C0, in an SGPR
+    uint32_t expo;  // 0x4C004C00, in a VGPR
+};
+__device__ __forceinline__ NibConst nib_const() {
+    NibConst k{0x03C003C0u, 0x4C004C00u};
+    asm volatile("" : "+s"(k.mask));
+    asm volatile("" : "+v"(k.expo));
+    return k;
+}
+__device__ __forceinline__ uint32_t nib_pair_fma(uint32_t v, NibConst k, h2 s, h2 c) {
+    const h2 m = __builtin_bit_cast(h2, (v & k.mask) | k.expo);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(m, s, c));
 }
 
 

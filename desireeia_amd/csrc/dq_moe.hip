@@ -36,6 +36,8 @@
 //    pair; the weighted scatter back to the tokens in slot order.
 #include <math.h>
 
+#include <type_traits>
+
 #include "dq_common.h"
 #include "dq_f16.h"
 
@@ -47,8 +49,7 @@ constexpr int TT = 32;         // tokens per MFMA tile
 constexpr int MAX_TILES = 1;   // token tiles per pass of a workgroup (32 pairs)
 constexpr int ACH = 32;        // 16-byte chunks of a token's activation per main step (256 halfs)
 constexpr int WAVES = 4;       // waves per workgroup, 32 weight rows each
-constexpr int NSTAGE = 2;      // LDS ring stages (NSTAGE-1 steps in flight while one computes)
-static_assert(NSTAGE == 2 || NSTAGE == 3, "the step wait counts NSTAGE-2 <= 1 later steps");
+constexpr int NSTAGE = 2;      // LDS ring stages (one step in flight while one computes)
 
 // ---------------------------------------------------------------- routing --
 // One wave per token, lane e = expert e. The max is order-independent; the
@@ -183,7 +184,7 @@ __global__ __launch_bounds__(256) void moe_lists_kernel(const int32_t* __restric
 // One 256-block b of activation row p (values v, 4 per lane): the per-256
 // quantization d = amax/127, id = 127/amax, q = rint(v*id) (core/matmul.cpp
 // :1681-1700), written as fp16(q*d*s) in columns 256b + 4 lane .. +3 of the
-// row, and the block sums fp16(d*isum_j*s), j = 0..7, at minp[b][p][j] (a
+// row (stored in the order 0, 2, 1, 3), and the block sums fp16(d*isum_j*s), j = 0..7, at minp[b][p][j] (a
 // plane with the pairs contiguous per super-block); s the row's range scale.
 __device__ __forceinline__ void quant_256_block(const float (&v)[4], float sc, int lane, int b, int p, int n_rows,
                                                 _Float16* row, _Float16* minp) {
@@ -200,7 +201,9 @@ __device__ __forceinline__ void quant_256_block(const float (&v)[4], float sc, i
         isum += q;
         hb[i] = __builtin_bit_cast(uint16_t, (_Float16)(((float)q * d) * sc));
     }
-    *reinterpret_cast<dq_u32x2*>(row + 256 * b + 4 * lane) = dq_u32x2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+    // columns in the order 0, 2, 1, 3 of each group of 4 (the expert GEMM's
+    // order of a word's 4 weight bytes)
+    *reinterpret_cast<dq_u32x2*>(row + 256 * b + 4 * lane) = dq_u32x2{hb[0] | (hb[2] << 16), hb[1] | (hb[3] << 16)};
     // 8 lanes hold one 32-block
 #pragma unroll
     for (int off = 1; off < 8; off <<= 1) isum += __shfl_xor(isum, off, DQ_WAVE);
@@ -311,28 +314,47 @@ struct WRaw {
     dq_u32x4 hd;
 };
 
+// The 8 sub-block scales fp16(d * sc_j) of a main step's super-block header
+// as pairs (sub-blocks 2t, 2t + 1 in pair t); zeros when !ok.
+__device__ __forceinline__ void step_scales(const dq_u32x4& hd, bool ok, h2 (&a)[4]) {
+    uint32_t lo, hi;
+    q4k_sc_bytes(hd, lo, hi);
+    const _Float16 d = ok ? __builtin_bit_cast(_Float16, (uint16_t)(hd.x & 0xFFFFu)) : (_Float16)0.0f;
+    bytes8_times(lo, hi, d, a);
+}
+
 // B fragments of item t (= group g of the super-block) of a main step. Lane
-// half h holds quant sub-plane h of the item: bytes 0-15 of its 32 qs bytes
+// half h holds quant sub-plane h of the item w: bytes 0-15 of its 32 qs bytes
 // (h = 0) or 16-31 (h = 1), i.e. positions 16h..16h+15 of sub-block 2t (low
 // nibbles) and 2t+1 (high nibbles). Slice kk: kk/2 picks the sub-block,
-// kk%2 the 8 positions 16h + 8(kk%2) + 0..7; values (q) * d*sc in fp16. The
-// activation fragment of the same slice holds the same positions (see
-// a_offset).
-__device__ __forceinline__ void b_item(const WRaw& r, int t, bool ok, h8 (&bf)[4]) {
-    const float d = dq_h2f((uint16_t)(r.hd.x & 0xFFFF));
-    const _Float16 a0 = (_Float16)(ok ? d * (float)q4k_scale(2 * t, r.hd.y, r.hd.z, r.hd.w) : 0.0f);
-    const _Float16 a1 = (_Float16)(ok ? d * (float)q4k_scale(2 * t + 1, r.hd.y, r.hd.z, r.hd.w) : 0.0f);
-    const h2 bias = {(_Float16)1024.0f, (_Float16)1024.0f};
-    const h2 v0 = {a0, a0}, v1 = {a1, a1};
-    const dq_u32x4 w = r.q[t];
+// kk%2 the 8 positions 16h + 8(kk%2) + 0..7, taken from each word in the
+// byte order 0, 2, 1, 3 (two nibbles per instruction); values q * (d*sc) in
+// fp16, sc = (a.x, a.y) for the two sub-blocks. The activation fragment of
+// the same slice holds the same positions in the same order (a_offset, and
+// quant_256_block's column order).
+// Per pair one shift, one v_and_or and one fma (nib_pair_fma, c = -16 a):
+// needs |d * sc| <= 4094 (weights up to 61,410 in magnitude; the fp16 operand
+// caps them at 65,504 in any form).
+__device__ __forceinline__ void b_item(const dq_u32x4& w, h2 a, NibConst k, h8 (&bf)[4]) {
+    const h2 m16 = {(_Float16)-16.0f, (_Float16)-16.0f};
+    const h2 c = a * m16;  // exact: a power of two
+    const h2 a0 = {a.x, a.x}, a1 = {a.y, a.y}, c0 = {c.x, c.x}, c1 = {c.y, c.y};
+    const uint32_t x[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-        const uint32_t x0 = (kk & 1) ? w.z : w.x, x1 = (kk & 1) ? w.w : w.y;
-        const uint32_t m0 = kk < 2 ? (x0 & 0x0F0F0F0Fu) : ((x0 >> 4) & 0x0F0F0F0Fu);
-        const uint32_t m1 = kk < 2 ? (x1 & 0x0F0F0F0Fu) : ((x1 >> 4) & 0x0F0F0F0Fu);
+        const uint32_t u = x[2 * (kk & 1)], v = x[2 * (kk & 1) + 1];
         uint32_t o[4];
-        bytes_to_h2(m0, bias, kk < 2 ? v0 : v1, &o[0]);
-        bytes_to_h2(m1, bias, kk < 2 ? v0 : v1, &o[2]);
+        if (kk < 2) {  // low nibbles: bytes 0, 2 of a word at bits 6-9, 22-25 after << 6, bytes 1, 3 after >> 2
+            o[0] = nib_pair_fma(u << 6, k, a0, c0);
+            o[1] = nib_pair_fma(u >> 2, k, a0, c0);
+            o[2] = nib_pair_fma(v << 6, k, a0, c0);
+            o[3] = nib_pair_fma(v >> 2, k, a0, c0);
+        } else {       // high nibbles: bytes 0, 2 after << 2, bytes 1, 3 after >> 6
+            o[0] = nib_pair_fma(u << 2, k, a1, c1);
+            o[1] = nib_pair_fma(u >> 6, k, a1, c1);
+            o[2] = nib_pair_fma(v << 2, k, a1, c1);
+            o[3] = nib_pair_fma(v >> 6, k, a1, c1);
+        }
         bf[kk] = __builtin_bit_cast(h8, dq_u32x4{o[0], o[1], o[2], o[3]});
     }
 }
@@ -361,23 +383,33 @@ constexpr int A_LOADS = MAX_TILES * TT * ACH / (64 * WAVES);  // DMAs per thread
 static_assert(A_LOADS >= 1, "activation DMA slots per thread");
 constexpr int A_MAIN_BYTES = MAX_TILES * TT * ACH * 16;
 constexpr int A_STAGE_BYTES = A_MAIN_BYTES + 64 * 16;  // + the min chunks (64 slots, 32 tokens twice)
-__device__ __forceinline__ void issue_a(const _Float16* A, const _Float16* minp, int K, int n_pairs, int c,
-                                        int p_end, int st, uint8_t* dst, int tid) {
-    const int lda = K;
-    {   // the step's 8 block sums of pair lane % 32 (contiguous over the pairs;
-        // every wave loads the same slots)
-        const int p = min(c + (tid & 31), p_end - 1);
-        __builtin_amdgcn_global_load_lds(minp + ((size_t)st * n_pairs + p) * 8, DQ_LDS_PTR(dst + A_MAIN_BYTES), 16,
-                                         0, 0);
-    }
+// Per-thread sources of a pass's activation DMAs at main step 0 (a main step
+// adds 256 halfs to each, and n_pairs * 8 halfs to the block-sum source),
+// computed once per pass.
+struct ASrc {
+    const _Float16* a[A_LOADS];
+    const _Float16* m;
+};
+__device__ __forceinline__ ASrc a_sources(const _Float16* A, const _Float16* minp, int K, int c, int p_end, int tid) {
+    ASrc s;
+    // the block sums of pair lane % 32 (contiguous over the pairs; every wave
+    // loads the same slots)
+    s.m = minp + (size_t)min(c + (tid & 31), p_end - 1) * 8;
 #pragma unroll
     for (int j = 0; j < A_LOADS; ++j) {
         const int slot = j * 64 * WAVES + tid;
         const int m = slot / ACH, kp = slot % ACH, k = kp ^ (m & 31);
         const int p = min(c + m, p_end - 1);
-        const _Float16* src = A + (size_t)p * lda + 256 * (size_t)st + 8 * k;
+        s.a[j] = A + (size_t)p * K + 8 * k;
+    }
+    return s;
+}
+__device__ __forceinline__ void issue_a(const ASrc& s, int n_pairs, int st, uint8_t* dst, int tid) {
+    __builtin_amdgcn_global_load_lds(s.m + (size_t)st * n_pairs * 8, DQ_LDS_PTR(dst + A_MAIN_BYTES), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < A_LOADS; ++j) {
         uint8_t* base = dst + (size_t)(j * 64 * WAVES + (tid & ~63)) * 16;  // wave-uniform
-        __builtin_amdgcn_global_load_lds(src, DQ_LDS_PTR(base), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(s.a[j] + 256 * (size_t)st, DQ_LDS_PTR(base), 16, 0, 0);
     }
 }
 
@@ -412,8 +444,6 @@ __device__ __forceinline__ void issue_w(const uint8_t* base, const DqLayout& L, 
     __builtin_amdgcn_global_load_lds(base + L.s_off + row * L.s_row + 16 * (size_t)st,
                                      DQ_LDS_PTR(dst + 2 * WT_PLANE + (size_t)((tid & ~63) % WROWS) * 16), 16, 0, 0);
 }
-// DMAs per thread per step: activation (+ min chunk), the two sub-planes, the header
-constexpr int STEP_LOADS = A_LOADS + 1 + 2 * WROWS * 4 / (64 * WAVES) + 1;
 static_assert(WROWS * 4 % (64 * WAVES) == 0 && 64 * WAVES == 2 * WROWS, "DMA slots per thread");
 
 // Expert-tile layout (DQ_FMT_Q4_K_TILES): the weight tile of one main step
@@ -468,17 +498,35 @@ size_t tiles_bytes(size_t n_exp, size_t rows, size_t cols) {
     return n_exp * ((rows + WROWS - 1) / WROWS) * (cols / 256) * (size_t)WT_BYTES;
 }
 
+// The 16 MFMAs of a main step's 4 items, items alternating between two
+// accumulators (two independent MFMA chains).
+__device__ __forceinline__ void item_mfmas(const WRaw& wr, const h2 (&sa)[4], NibConst k, const h8 (&af)[4][4],
+                                           f16v& acc, f16v& acc1) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        h8 bf[4];
+        b_item(wr.q[t], sa[t], k, bf);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            if (t & 1) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[t][kk], bf[kk], acc1, 0, 0, 0);
+            else acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[t][kk], bf[kk], acc, 0, 0, 0);
+        }
+    }
+}
+
 // Grid (one dimension): workgroup id -> expert id % n_exp, then the row tile,
 // then the K split, then the matrix. Workgroups are dealt to the 8 XCDs
 // round-robin, so with 8 (or a multiple of 8) experts each XCD serves whole
 // experts: the activation rows an expert's tiles re-read every K step stay
 // in that XCD's L2. Wave w of the workgroup owns rows 128x + 32w .. +31 of
-// row tile x; lane l feeds
-// row l % 32 with K values 8(l/32)..+7 of each 16-wide slice. The expert's
-// pairs are taken 32 at a time (one 32-token MFMA tile). Per main step (one
-// super-block) the weight tile and the activation rows go through an
-// NSTAGE-stage LDS ring, the next NSTAGE-1 steps' DMAs in flight while this
-// one computes.
+// row tile x; lane l feeds row l % 32 with K values 8(l/32)..+7 of each
+// 16-wide slice. The expert's pairs are taken 32 at a time (one 32-token MFMA
+// tile). Per main step (one super-block) the weight tile and the activation
+// rows go through a 2-stage LDS ring, the next step's DMAs in flight while
+// this one computes. The kernel is bound by its VALU work (the weight
+// conversion: one shift, one v_and_or and one fma per pair of weights), so
+// the step body keeps everything else off the VALU: scales decoded four at a
+// time, LDS addresses as immediates.
 template <bool TILED>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void moe_gemm_kernel(MoeGemm G) {
     __shared__ __align__(16) uint8_t aring[NSTAGE][A_STAGE_BYTES];
@@ -509,42 +557,33 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     const int main_end = min(G.main_steps, s0 + G.steps_per_split);
     if (s0 >= main_end) return;  // uniform
 
+    const NibConst nk = nib_const();
     for (int c = p_begin; c < p_end; c += TT) {
         f16v acc, acc1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = acc1[r] = 0.0f;
         {
-            // prologue: the first NSTAGE-1 steps in flight
-#pragma unroll
-            for (int q = 0; q < NSTAGE - 1; ++q) {
-                if (s0 + q < main_end) {
-                    issue_a(G.A, G.minp, G.K, G.n_pairs, c, p_end, s0 + q, aring[q], tid);
-                    if constexpr (TILED) issue_w_tiles(base + (chunk0 + s0 + q) * WT_BYTES, wring[q], tid);
-                    else issue_w(base, L, row0, nrows, s0 + q, wring[q], tid);
+            const ASrc as = a_sources(G.A, G.minp, G.K, c, p_end, tid);
+            // prologue: the first step in flight
+            issue_a(as, G.n_pairs, s0, aring[0], tid);
+            if constexpr (TILED) issue_w_tiles(base + (chunk0 + s0) * WT_BYTES, wring[0], tid);
+            else issue_w(base, L, row0, nrows, s0, wring[0], tid);
+            // one main step from ring stage S = (st - s0) % 2, a constant in
+            // each of the two copies of the body (every LDS address is then a
+            // register plus an immediate)
+            auto step = [&](int st, auto stage_c) {
+                constexpr int S = decltype(stage_c)::value;
+                wait_vm<0>();      // this step's DMAs, the only ones outstanding, have landed
+                dq_lds_barrier();  // ... in every wave; stage 1 - S is free
+                if (st + 1 < main_end) {
+                    issue_a(as, G.n_pairs, st + 1, aring[1 - S], tid);
+                    if constexpr (TILED) issue_w_tiles(base + (chunk0 + st + 1) * WT_BYTES, wring[1 - S], tid);
+                    else issue_w(base, L, row0, nrows, st + 1, wring[1 - S], tid);
                 }
-            }
-            for (int st = s0; st < main_end; ++st) {
-                const int stage = (st - s0) % NSTAGE;
-                // this step's DMAs have landed once only the later steps'
-                // (issued after them, at most NSTAGE-2) can be outstanding
-                if constexpr (NSTAGE > 2) {
-                    if (st + 1 < main_end) wait_vm<STEP_LOADS * (NSTAGE - 2)>();
-                    else wait_vm<0>();
-                } else {
-                    wait_vm<0>();
-                }
-                dq_lds_barrier();  // every wave's DMAs of this step landed; stage st-1 is free
-                if (st + NSTAGE - 1 < main_end) {
-                    const int ns = (st - s0 + NSTAGE - 1) % NSTAGE;
-                    issue_a(G.A, G.minp, G.K, G.n_pairs, c, p_end, st + NSTAGE - 1, aring[ns], tid);
-                    if constexpr (TILED) issue_w_tiles(base + (chunk0 + st + NSTAGE - 1) * WT_BYTES, wring[ns], tid);
-                    else issue_w(base, L, row0, nrows, st + NSTAGE - 1, wring[ns], tid);
-                }
-                const uint8_t* ab = aring[stage];
-                const uint8_t* wb = wring[stage];
+                const uint8_t* ab = aring[S];
+                const uint8_t* wb = wring[S];
                 // every LDS read of the step first (one wait for all of them),
-                // then the dequantization and the MFMAs, items alternating
-                // between two accumulators (two independent MFMA chains)
+                // then the dequantization and the MFMAs
                 WRaw wr;
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
@@ -562,22 +601,19 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
                     }
                 const h8 zero = {};
                 const h8 am = h == 0 ? *reinterpret_cast<const h8*>(ab + A_MAIN_BYTES + m * 16) : zero;
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    h8 bf[4];
-                    b_item(wr, t, row_ok, bf);
-#pragma unroll
-                    for (int kk = 0; kk < 4; ++kk) {
-                        if (t & 1) acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[t][kk], bf[kk], acc1, 0, 0, 0);
-                        else acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[t][kk], bf[kk], acc, 0, 0, 0);
-                    }
-                }
+                h2 sa[4];
+                step_scales(wr.hd, row_ok, sa);
+                item_mfmas(wr, sa, nk, af, acc, acc1);
                 {   // the super-block's min term: one 16-wide slice, lanes of half 0
                     // carry its 8 sub-blocks (the min columns K + 8st + j
                     // against fp16(-dmin * m_j)), half 1 zeros
                     const h8 bm = h == 0 ? q4k_neg_mins(wr.hd, row_ok) : zero;
                     acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, acc1, 0, 0, 0);
                 }
+            };
+            for (int st = s0; st < main_end; st += 2) {
+                step(st, std::integral_constant<int, 0>{});
+                if (st + 1 < main_end) step(st + 1, std::integral_constant<int, 1>{});
             }
             __syncthreads();  // the ring is reused by the next pass
         }
