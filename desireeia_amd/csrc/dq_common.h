@@ -369,18 +369,31 @@ static inline int dq_launch_status() { return dq_status(hipGetLastError()); }
 // outputs of the K-split GEMMs that read its result next); counts are
 // multiples of 4, pointers 16-byte aligned, unused slots null.
 struct DqZeroSpans {
-    static constexpr int N = 3;
-    float* p[N] = {nullptr, nullptr, nullptr};
-    size_t n[N] = {0, 0, 0};
+    static constexpr int N = 4;
+    float* p[N] = {nullptr, nullptr, nullptr, nullptr};
+    size_t n[N] = {0, 0, 0, 0};
 };
 // Library-internal parts of the prefill GEMM (dq_gemm.hip): the quantizer
-// with spans to clear, whether a product's plan adds K-split partials into y
-// (so y must start at zero), and the GEMM on a y already cleared.
+// with spans to clear (with d_gate, of the gated FFN product act(gate) * x,
+// act a DqFfnAct: SiLU or gelu_tanh), whether a product's plan adds K-split partials into y
+// (so y must start at zero), the plan's workgroup count, and the GEMM on a y
+// already cleared. cu_budget > 0 plans the product for that many CUs (a
+// product that runs beside others); 0 plans it for the whole GPU.
 int dq_quantize_act_f16_zero(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_out,
-                             const DqZeroSpans& z, void* stream);
-bool dq_gemm_adds_into_y(int fmt, size_t rows, size_t cols, size_t n_tok);
+                             const DqZeroSpans& z, void* stream, const float* d_gate = nullptr, int act = 0);
+bool dq_gemm_adds_into_y(int fmt, size_t rows, size_t cols, size_t n_tok, int cu_budget = 0);
+size_t dq_gemm_workgroups(int fmt, size_t rows, size_t cols, size_t n_tok, int cu_budget = 0);
 int dq_gemm_f16act_zeroed(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work, size_t n_tok,
-                          float* d_y, bool y_zeroed, void* stream);
+                          float* d_y, bool y_zeroed, void* stream, int cu_budget = 0);
+int dq_gemm_cus();
+// The RMSNorm of rows of a (+ b, the residual, kept in h when given) with
+// weight w (to y when given; rms_norm_rows_kernel's arithmetic) fused with
+// the activation quantization of the normalised rows for n_fmt (1 or 2)
+// formats of different classes into their workspaces outs[k]; spans z are
+// cleared on the side.
+int dq_norm_quant_f16(const float* d_a, const float* d_b, float* d_h, const float* d_w, size_t cols, size_t n_tok,
+                      float eps, float* d_y, int n_fmt, const int* fmts, void* const* outs, const DqZeroSpans& z,
+                      void* stream);
 static inline bool dq_zero_span_ok(const float* p, size_t n) {
     return p && n % 4 == 0 && reinterpret_cast<uintptr_t>(p) % 16 == 0;
 }

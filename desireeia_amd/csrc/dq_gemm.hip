@@ -683,172 +683,246 @@ void gemm_kernel(GemmArgs g, float* __restrict__ y, int nsb, int sb_per_split, i
 
 // Activation quantizer for the GEMM: per 32-block the reference integers and
 // scale (core/i8gemm_impl.h:50-82), written as fp16(q*d*s) in K order `perm`
-// (0 natural, 1 Q6_K item order); with a min plane (Q4_K), fp16(exact float
-// block sum * s) of block b at minp[b/8][t][b%8]; s the row's power-of-two
-// range scale. One block (or one block sum) per call; the row kernel below
-// runs them for its token.
-__device__ __forceinline__ void quantize_f16_block(const float* __restrict__ x, int cols, int n_tok,
-                                                   _Float16* __restrict__ out, int lda, _Float16* __restrict__ minp,
-                                                   int perm, int t, int b, float sc) {
-    const int nb = cols / 32;
-    _Float16* o = out + (size_t)t * lda;
-    if (b >= nb) {  // block sum of block b - nb
-        const int mb = b - nb;
-        const float* p = x + (size_t)t * cols + 32 * mb;
-        float fs = 0.0f;
-        for (int i = 0; i < 32; ++i) fs += p[i];
-        minp[((size_t)(mb / 8) * n_tok + t) * 8 + (mb % 8)] = (_Float16)(fs * sc);
-        return;
-    }
-    const float* p = x + (size_t)t * cols + 32 * b;
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 f = reinterpret_cast<const float4*>(p)[i];
-        v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const float a = fabsf(v[i]);
-        amax = (amax < a) ? a : amax;
-    }
-    const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
-    const float id = d > 0.0f ? 1.0f / d : 0.0f;
-    _Float16 h[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        int q = (int)rintf(v[i] * id);
-        q = q > 127 ? 127 : (q < -127 ? -127 : q);
-        h[i] = (_Float16)(((float)q * d) * sc);
-    }
-    if (perm == 0) {
-        dq_u32x4* dst = reinterpret_cast<dq_u32x4*>(o + 32 * b);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[i] = __builtin_bit_cast(dq_u32x4, *reinterpret_cast<const h8*>(&h[8 * i]));
-    } else if (perm == 2) {
-        // Q4_K fragment order (gemm b_raw / b_frag): block b is half hi = b % 2
-        // (the high nibbles) of item g = (b % 8) / 2; its element e is byte
-        // j = e of the item's 32 qs bytes, in sub-plane j / 16 = the lane half
-        // that reads it, word (slice) KK = (j % 16) / 4 of that sub-plane's 16
-        // bytes, fragment slot f = 4 * (bo & 1) + (bo >> 1) + 2 * hi with
-        // bo = j % 4; column 16 KK + 8 half + f.
-        const int hi = b & 1;
-        _Float16* item = o + 64 * (size_t)(b / 2);
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const int hf = e / 16, kk = (e % 16) / 4, bo = e % 4;
-            item[16 * kk + 8 * hf + 4 * (bo & 1) + (bo >> 1) + 2 * hi] = h[e];
-        }
-    } else {
-        // Q6_K item order: position pos in the 256-block -> column
-        // s*256 + (2n+k)*64 + qq*16 + e, with pos = 128n + 32qq + 16k + e.
-        const int s = b / 8, pos0 = 32 * (b % 8);
-        const int n = pos0 / 128, qq = (pos0 % 128) / 32;
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const int col = s * 256 + (2 * n + k) * 64 + qq * 16;
-            dq_u32x4* dst = reinterpret_cast<dq_u32x4*>(o + col);
-            dst[0] = __builtin_bit_cast(dq_u32x4, *reinterpret_cast<const h8*>(&h[16 * k]));
-            dst[1] = __builtin_bit_cast(dq_u32x4, *reinterpret_cast<const h8*>(&h[16 * k + 8]));
-        }
-    }
-}
+// (0 natural, 1 Q6_K item order, 2 Q4_K fragment order with a min plane:
+// fp16(exact float block sum * s) of block b at minp[b/8][t][b%8]); s the
+// row's power-of-two range scale.
 
-// Q4_K order, one item (blocks 2i and 2i+1, 64 values) per call: the two
-// blocks' integers, scales and exact float sums as quantize_f16_block, their
-// 64 fp16 values stored as 8 contiguous 16-byte chunks (chunk (kk, hf) at
-// column 16 kk + 8 hf of the item holds elements e = 16 hf + 4 kk + bo of the
-// low block (hi = 0) and of the high block (hi = 1) at slot
-// 4 (bo & 1) + (bo >> 1) + 2 hi), and the two block sums as one 4-byte store.
-__device__ __forceinline__ void quantize_f16_item_q4k(const float* __restrict__ x, int cols, int n_tok,
-                                                      _Float16* __restrict__ out, int lda,
-                                                      _Float16* __restrict__ minp, int t, int i, float sc) {
-    const float* p = x + (size_t)t * cols + 64 * i;
-    float v[64];
+// The quantizer's row kernel: one workgroup per token row, thread j taking
+// the 8-value groups j, j + TPR, ... of the row (up to G of them, kept in
+// registers between the passes); a 32-block is 4 consecutive lanes, a Q4_K
+// item (blocks 2i and 2i+1) 8. Per row: the power-of-two range scale s from
+// the maximum over the row, then per block the reference integers and scale
+// (amax over the 4 lanes) and, for the Q4_K min plane, the exact float sum
+// of the block in element order (a running sum handed lane to lane), stored
+// for up to two format classes (the block arithmetic does not depend on the
+// layout). The input per SRC: the row x itself, the gated FFN product
+// act(g) * x (the expression of the FFN's activation pass, so the same
+// bits), or the RMSNorm of a (+ b, the residual, kept in h) with weight w,
+// written to y when given (float squares summed in double, then
+// (x * (1 / sqrt(mean + eps))) * w, rms_norm_rows_kernel's arithmetic). The
+// workgroups also clear the outputs of the K-split GEMMs that read this
+// activation next (z: float counts, multiples of 4, split evenly over the
+// workgroups), which saves those GEMMs a fill launch.
+struct QuantDst {
+    _Float16* out;
+    _Float16* minp;  // Q4_K block sums (perm 2), else unused
+    float* rscale;
+    float* inv;
+    int perm;        // 2 Q4_K fragment order, 1 Q6_K item order, 0 natural
+};
+enum QuantSrcKind { Q_PLAIN = 0, Q_SILU = 1, Q_GELU = 2, Q_NORM = 3 };
+struct QuantSrc {
+    const float* x;  // the row input (Q_NORM: a)
+    const float* g;  // gated: the gate; Q_NORM: the residual b (or null)
+    const float* w;  // Q_NORM: the norm weight
+    float* h;        // Q_NORM: a + b (when b and h are given)
+    float* y;        // Q_NORM: the normalised row (when given)
+    float eps;
+};
+
+// Group c (columns 8c .. 8c+7) of row `row`: the raw input (Q_NORM: a + b),
+// or for the other kinds the quantizer's input itself.
+template <int SRC>
+__device__ __forceinline__ void group_in(const QuantSrc& S, size_t row, int c, float (&v)[8]) {
+    const size_t o = row + 8 * (size_t)c;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const float4 f = reinterpret_cast<const float4*>(p)[k];
+    for (int k = 0; k < 2; ++k) {
+        float4 f = *reinterpret_cast<const float4*>(S.x + o + 4 * k);
+        if constexpr (SRC == Q_SILU || SRC == Q_GELU) {
+            constexpr int A = SRC == Q_SILU ? DQ_ACT_SILU : DQ_ACT_GELU_TANH;
+            const float4 gg = *reinterpret_cast<const float4*>(S.g + o + 4 * k);
+            f = make_float4(dq_ffn_act<A>(gg.x) * f.x, dq_ffn_act<A>(gg.y) * f.y, dq_ffn_act<A>(gg.z) * f.z,
+                            dq_ffn_act<A>(gg.w) * f.w);
+        } else if constexpr (SRC == Q_NORM) {
+            if (S.g) {
+                const float4 c4 = *reinterpret_cast<const float4*>(S.g + o + 4 * k);
+                f = make_float4(f.x + c4.x, f.y + c4.y, f.z + c4.z, f.w + c4.w);
+            }
+        }
         v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
     }
-    _Float16 h[64];
-    _Float16 fsum[2];
-#pragma unroll
-    for (int hi = 0; hi < 2; ++hi) {
-        const float* vb = v + 32 * hi;
-        float amax = 0.0f, fs = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            const float a = fabsf(vb[e]);
-            amax = (amax < a) ? a : amax;
-            fs += vb[e];
-        }
-        const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
-        const float id = d > 0.0f ? 1.0f / d : 0.0f;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) {
-            int q = (int)rintf(vb[e] * id);
-            q = q > 127 ? 127 : (q < -127 ? -127 : q);
-            h[32 * hi + e] = (_Float16)(((float)q * d) * sc);
-        }
-        fsum[hi] = (_Float16)(fs * sc);
-    }
-    _Float16* o = out + (size_t)t * lda + 64 * (size_t)i;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            const int e0 = 16 * hf + 4 * kk;
-            const h8 c = {h[e0], h[e0 + 2], h[32 + e0], h[32 + e0 + 2], h[e0 + 1], h[e0 + 3], h[32 + e0 + 1],
-                          h[32 + e0 + 3]};
-            *reinterpret_cast<h8*>(o + 16 * kk + 8 * hf) = c;
-        }
-    const int mb = 2 * i;
-    const h2 sums = {fsum[0], fsum[1]};
-    *reinterpret_cast<h2*>(minp + ((size_t)(mb / 8) * n_tok + t) * 8 + (mb % 8)) = sums;
 }
 
-// One workgroup per token row: the row's power-of-two range scale (as
-// row_scale_kernel) and then every block of the row (quantize_f16_block);
-// inv[t] = 1/s. The workgroups also clear the outputs of the K-split GEMMs
-// that read this activation next (z: their float counts, multiples of 4,
-// split evenly over the workgroups), which saves those GEMMs a fill launch.
-__global__ __launch_bounds__(256) void quantize_f16_rows_kernel(const float* __restrict__ x, int cols, int n_tok,
-                                                                _Float16* __restrict__ out, int lda,
-                                                                _Float16* __restrict__ minp, int perm,
-                                                                float* __restrict__ rscale, float* __restrict__ inv,
-                                                                DqZeroSpans z) {
-    __shared__ float wmax[4];
+// The 8 fp16 values h of group c (lane c % 4 of its block, c % 8 of its
+// Q4_K item) into layout d of row t; for Q4_K the lane also receives its
+// item partner's values (lanes 4 apart) and the last lane of a block writes
+// the block sum fs.
+__device__ __forceinline__ void store_group(const QuantDst& d, int lda, int n_tok, int t, int c, const h8& hv,
+                                            float fs_scaled, bool sum_lane, bool ok) {
+    _Float16* o = d.out + (size_t)t * lda;
+    const int b = c / 4, q = c % 4;  // block, group in the block
+    if (d.perm == 0) {
+        if (ok) *reinterpret_cast<h8*>(o + 8 * (size_t)c) = hv;
+    } else if (d.perm == 1) {
+        // Q6_K item order: position pos of the 256-block -> column s*256 +
+        // (2n+k)*64 + qq*16 + e, pos = 128n + 32qq + 16k + e
+        const int sb = b / 8, pos0 = 32 * (b % 8);
+        const int n = pos0 / 128, qq = (pos0 % 128) / 32, k = q / 2;
+        if (ok) *reinterpret_cast<h8*>(o + sb * 256 + (2 * n + k) * 64 + qq * 16 + 8 * (q % 2)) = hv;
+    } else {
+        // Q4_K fragment order: chunk (kk, hf) at column 16 kk + 8 hf of item i
+        // holds elements e0..e0+3 (e0 = 16 hf + 4 kk) of the low block and of
+        // the high block as {lo e0, lo e0+2, hi e0, hi e0+2, lo e0+1, lo e0+3,
+        // hi e0+1, hi e0+3}. Group q of the low block (elements 8q..8q+7)
+        // writes chunk kk = 2 (q % 2), hf = q / 2 with the partner's first
+        // four; the high block's group q the chunk kk + 1 with the low
+        // group's last four.
+        const bool hi = (c / 4) & 1;
+        const dq_u32x4 mine = __builtin_bit_cast(dq_u32x4, hv);
+        // low lanes send their last four values, high lanes their first four
+        const uint32_t s0 = hi ? mine.x : mine.z, s1 = hi ? mine.y : mine.w;
+        const uint32_t r0 = __shfl_xor(s0, 4, DQ_WAVE), r1 = __shfl_xor(s1, 4, DQ_WAVE);
+        h8 lo4, hi4;  // elements e0..e0+3 of the two blocks (in their first four slots)
+        if (!hi) {
+            lo4 = hv;
+            hi4 = __builtin_bit_cast(h8, dq_u32x4{r0, r1, 0u, 0u});
+        } else {
+            lo4 = __builtin_bit_cast(h8, dq_u32x4{r0, r1, 0u, 0u});
+            hi4 = __builtin_bit_cast(h8, dq_u32x4{mine.z, mine.w, 0u, 0u});
+        }
+        const int kk = 2 * (q % 2) + (hi ? 1 : 0), hf = q / 2;
+        const h8 ch = {lo4[0], lo4[2], hi4[0], hi4[2], lo4[1], lo4[3], hi4[1], hi4[3]};
+        if (!ok) return;
+        *reinterpret_cast<h8*>(o + 64 * (size_t)(b / 2) + 16 * kk + 8 * hf) = ch;
+        if (sum_lane) d.minp[((size_t)(b / 8) * n_tok + t) * 8 + (b % 8)] = (_Float16)fs_scaled;
+    }
+}
+
+template <int SRC, int G>
+__global__ __launch_bounds__(1024) void quant_rows_kernel(QuantSrc S, int cols, int n_tok, int lda, QuantDst d0,
+                                                          QuantDst d1, int n_dst, DqZeroSpans z) {
+    __shared__ double dpart[16];
+    __shared__ float fpart[16];
+    const int tid = threadIdx.x, lane = tid & 63, TPR = blockDim.x, nw = TPR / 64;
     const int t = blockIdx.x;
 #pragma unroll
     for (int k = 0; k < DqZeroSpans::N; ++k) {
         if (!z.p[k]) continue;
         const size_t n4 = z.n[k] / 4, per = (n4 + gridDim.x - 1) / gridDim.x;
         const size_t e = min(n4, per * (t + 1));
-        for (size_t i = per * t + threadIdx.x; i < e; i += 256)
+        for (size_t i = per * t + tid; i < e; i += TPR)
             reinterpret_cast<float4*>(z.p[k])[i] = float4{0.0f, 0.0f, 0.0f, 0.0f};
     }
-    const float* row = x + (size_t)t * cols;
+    const size_t row = (size_t)t * cols;
+    const int ng = cols / 8;  // groups of the row (a multiple of 32)
+    float v[G][8];
+    // ng is a multiple of 32 and TPR of 64: a wave's groups are all
+    // present, all absent, or present in its first half (whole blocks and
+    // items either way)
+#pragma unroll
+    for (int it = 0; it < G; ++it) {
+        const int c = tid + it * TPR;
+        if (c < ng) group_in<SRC>(S, row, c, v[it]);
+    }
+    float nsc = 1.0f;
+    if constexpr (SRC == Q_NORM) {
+        double acc = 0.0;
+#pragma unroll
+        for (int it = 0; it < G; ++it) {
+            const int c = tid + it * TPR;
+            if (c >= ng) continue;
+            if (S.g && S.h) {
+                float* hp = S.h + row + 8 * (size_t)c;
+                *reinterpret_cast<float4*>(hp) = make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
+                *reinterpret_cast<float4*>(hp + 4) = make_float4(v[it][4], v[it][5], v[it][6], v[it][7]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float sq = v[it][e] * v[it][e];
+                acc += (double)sq;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, DQ_WAVE);
+        if (lane == 0) dpart[tid >> 6] = acc;
+        __syncthreads();
+        acc = 0.0;
+        for (int w = 0; w < nw; ++w) acc += dpart[w];
+        nsc = 1.0f / sqrtf((float)(acc / (double)cols) + S.eps);
+#pragma unroll
+        for (int it = 0; it < G; ++it) {
+            const int c = tid + it * TPR;
+            if (c >= ng) continue;
+            const float4 w0 = *reinterpret_cast<const float4*>(S.w + 8 * (size_t)c);
+            const float4 w1 = *reinterpret_cast<const float4*>(S.w + 8 * (size_t)c + 4);
+            const float ww[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[it][e] = v[it][e] * nsc * ww[e];
+            if (S.y) {
+                float* yp = S.y + row + 8 * (size_t)c;
+                *reinterpret_cast<float4*>(yp) = make_float4(v[it][0], v[it][1], v[it][2], v[it][3]);
+                *reinterpret_cast<float4*>(yp + 4) = make_float4(v[it][4], v[it][5], v[it][6], v[it][7]);
+            }
+        }
+    }
     float m = 0.0f;
-    for (int c = threadIdx.x * 4; c < cols; c += 1024) {
-        const float4 f = *reinterpret_cast<const float4*>(row + c);
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
-    }
+#pragma unroll
+    for (int it = 0; it < G; ++it)
+        if (tid + it * TPR < ng)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[it][e]));
     m = dq_wave_max(m);
-    if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+    if (lane == 0) fpart[tid >> 6] = m;
     __syncthreads();
-    const float sc = row_scale_of(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
-    if (threadIdx.x == 0) {
-        rscale[t] = sc;
-        inv[t] = 1.0f / sc;
+    m = fpart[0];
+    for (int w = 1; w < nw; ++w) m = fmaxf(m, fpart[w]);
+    const float sc = row_scale_of(m);
+    if (tid == 0) {
+        d0.rscale[t] = sc;
+        d0.inv[t] = 1.0f / sc;
+        if (n_dst > 1) {
+            d1.rscale[t] = sc;
+            d1.inv[t] = 1.0f / sc;
+        }
     }
-    const int nb = cols / 32;
-    if (perm == 2) {  // Q4_K: whole items (contiguous stores), block sums alongside
-        for (int i = threadIdx.x; i < nb / 2; i += 256) quantize_f16_item_q4k(x, cols, n_tok, out, lda, minp, t, i, sc);
-        return;
+    const bool sums = d0.perm == 2 || (n_dst > 1 && d1.perm == 2);
+#pragma unroll
+    for (int it = 0; it < G; ++it) {
+        const int c = tid + it * TPR;
+        if (it * TPR + (tid & ~63) >= ng) break;  // wave-uniform: the wave's groups are absent
+        // the block's maximum over its 4 lanes
+        float amax = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float a = fabsf(v[it][e]);
+            amax = (amax < a) ? a : amax;
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 1, DQ_WAVE));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, DQ_WAVE));
+        const float d = amax > 0.0f ? amax / 127.0f : 0.0f;
+        const float id = d > 0.0f ? 1.0f / d : 0.0f;
+        h8 hv;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            int q = (int)rintf(v[it][e] * id);
+            q = q > 127 ? 127 : (q < -127 ? -127 : q);
+            hv[e] = (_Float16)(((float)q * d) * sc);
+        }
+        // the block's exact float sum in element order: lane q of the block
+        // continues the running sum of lane q - 1
+        float fs = 0.0f;
+        if (sums) {
+            const int q = lane & 3;
+            if (q == 0)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) fs += v[it][e];
+#pragma unroll
+            for (int k = 1; k < 4; ++k) {
+                const float p = __shfl_up(fs, 1, DQ_WAVE);
+                if (q == k) {
+                    fs = p;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) fs += v[it][e];
+                }
+            }
+        }
+        // lanes past the row (in a wave the row half covers) compute on
+        // unset values but take part in the shuffles, which stay within
+        // blocks and items, all present or all absent; they store nothing
+        const bool sum_lane = (lane & 3) == 3, ok = c < ng;
+        store_group(d0, lda, n_tok, t, c, hv, fs * sc, sum_lane, ok);
+        if (n_dst > 1) store_group(d1, lda, n_tok, t, c, hv, fs * sc, sum_lane, ok);
     }
-    const int stride = minp ? 2 * nb : nb;
-    for (int b = threadIdx.x; b < stride; b += 256) quantize_f16_block(x, cols, n_tok, out, lda, minp, perm, t, b, sc);
 }
 
 __global__ void zero_kernel(float* __restrict__ y, size_t n) {
@@ -869,6 +943,8 @@ int cus() {
 }
 
 }  // namespace
+
+int dq_gemm_cus() { return cus(); }
 
 // Workspace of the GEMM: the activation [n_tok][cols] fp16, for Q4_K the
 // block sums [cols/256][n_tok][8] fp16, then the row scales s and 1/s [n_tok].
@@ -898,25 +974,77 @@ extern "C" int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t
     return DQ_OK;
 }
 
+static bool quant_fmt_ok(int fmt) {
+    return fmt == DQ_FMT_Q4_K || fmt == DQ_FMT_Q6_K || fmt == DQ_FMT_Q8_0 || fmt == DQ_FMT_Q4_0;
+}
+static QuantDst quant_dst(int fmt, size_t cols, size_t n_tok, void* out) {
+    uint8_t* base = (uint8_t*)out;
+    QuantDst d{};
+    d.out = (_Float16*)base;
+    d.minp = fmt == DQ_FMT_Q4_K ? (_Float16*)(base + min_off(cols, n_tok)) : nullptr;
+    d.rscale = (float*)(base + scale_off(fmt, cols, n_tok));
+    d.inv = (float*)(base + inv_off(fmt, cols, n_tok));
+    d.perm = fmt == DQ_FMT_Q6_K ? 1 : (fmt == DQ_FMT_Q4_K ? 2 : 0);
+    return d;
+}
+// One workgroup per row of 64 (threads per row, up to 1024) times up to 8
+// groups of 8 columns per thread: rows of up to 65536 columns.
+constexpr size_t QUANT_MAX_COLS = 65536;
+template <int SRC>
+static int launch_quant_rows(const QuantSrc& S, size_t cols, size_t n_tok, const QuantDst (&d)[2], int n_dst,
+                             const DqZeroSpans& z, hipStream_t s) {
+    const int lda = (int)act_lda(cols);
+    const size_t ng = cols / 8;
+    int G = 1;
+    while ((ng + G - 1) / G > 1024) G *= 2;
+    const unsigned tpr = (unsigned)(((ng + G - 1) / G + 63) / 64 * 64);
+    const unsigned grid = (unsigned)n_tok;
+    switch (G) {
+    case 1: quant_rows_kernel<SRC, 1><<<grid, tpr, 0, s>>>(S, (int)cols, (int)n_tok, lda, d[0], d[1], n_dst, z); break;
+    case 2: quant_rows_kernel<SRC, 2><<<grid, tpr, 0, s>>>(S, (int)cols, (int)n_tok, lda, d[0], d[1], n_dst, z); break;
+    case 4: quant_rows_kernel<SRC, 4><<<grid, tpr, 0, s>>>(S, (int)cols, (int)n_tok, lda, d[0], d[1], n_dst, z); break;
+    default: quant_rows_kernel<SRC, 8><<<grid, tpr, 0, s>>>(S, (int)cols, (int)n_tok, lda, d[0], d[1], n_dst, z);
+    }
+    return dq_launch_status();
+}
+
 int dq_quantize_act_f16_zero(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_out,
-                             const DqZeroSpans& z, void* stream) {
-    if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K && fmt != DQ_FMT_Q8_0 && fmt != DQ_FMT_Q4_0)
-        return DQ_ERR_NOT_SUPPORTED;
-    if (cols % 256 || cols > (1u << 24) || n_tok > (1u << 20)) return DQ_ERR_NOT_SUPPORTED;
+                             const DqZeroSpans& z, void* stream, const float* d_gate, int act) {
+    if (!quant_fmt_ok(fmt)) return DQ_ERR_NOT_SUPPORTED;
+    if (cols % 256 || cols > QUANT_MAX_COLS || n_tok > (1u << 20)) return DQ_ERR_NOT_SUPPORTED;
     if (!d_x || !d_out) return DQ_ERR_INVALID_ARG;
     if (n_tok == 0) return DQ_OK;
-    const int nb = (int)cols / 32;
-    const bool with_min = fmt == DQ_FMT_Q4_K;
-    const size_t lanes = n_tok * (size_t)(with_min ? 2 * nb : nb);
-    uint8_t* base = (uint8_t*)d_out;
-    _Float16* minp = with_min ? (_Float16*)(base + min_off(cols, n_tok)) : nullptr;
-    float* sc = (float*)(base + scale_off(fmt, cols, n_tok));
-    float* inv = (float*)(base + inv_off(fmt, cols, n_tok));
-    (void)lanes;
-    quantize_f16_rows_kernel<<<(unsigned)n_tok, 256, 0, (hipStream_t)stream>>>(
-        d_x, (int)cols, (int)n_tok, (_Float16*)d_out, (int)act_lda(cols), minp,
-        fmt == DQ_FMT_Q6_K ? 1 : (fmt == DQ_FMT_Q4_K ? 2 : 0), sc, inv, z);
-    return dq_launch_status();
+    const QuantDst d[2] = {quant_dst(fmt, cols, n_tok, d_out), QuantDst{}};
+    QuantSrc S{};
+    S.x = d_x;
+    S.g = d_gate;
+    const hipStream_t s = (hipStream_t)stream;
+    if (!d_gate) return launch_quant_rows<Q_PLAIN>(S, cols, n_tok, d, 1, z, s);
+    if (act == DQ_ACT_SILU) return launch_quant_rows<Q_SILU>(S, cols, n_tok, d, 1, z, s);
+    if (act == DQ_ACT_GELU_TANH) return launch_quant_rows<Q_GELU>(S, cols, n_tok, d, 1, z, s);
+    return DQ_ERR_NOT_SUPPORTED;
+}
+
+int dq_norm_quant_f16(const float* d_a, const float* d_b, float* d_h, const float* d_w, size_t cols, size_t n_tok,
+                      float eps, float* d_y, int n_fmt, const int* fmts, void* const* outs, const DqZeroSpans& z,
+                      void* stream) {
+    if (n_fmt < 1 || n_fmt > 2 || !fmts || !outs || !d_a || !d_w) return DQ_ERR_INVALID_ARG;
+    if (cols % 256 || cols > QUANT_MAX_COLS || n_tok > (1u << 20)) return DQ_ERR_NOT_SUPPORTED;
+    if (n_tok == 0) return DQ_OK;
+    QuantDst d[2] = {};
+    for (int k = 0; k < n_fmt; ++k) {
+        if (!quant_fmt_ok(fmts[k])) return DQ_ERR_NOT_SUPPORTED;
+        if (!outs[k]) return DQ_ERR_INVALID_ARG;
+        d[k] = quant_dst(fmts[k], cols, n_tok, outs[k]);
+    }
+    QuantSrc S{};
+    S.x = d_a;
+    S.g = d_b;
+    S.w = d_w;
+    S.h = d_h;
+    S.y = d_y;
+    S.eps = eps;
+    return launch_quant_rows<Q_NORM>(S, cols, n_tok, d, n_fmt, z, (hipStream_t)stream);
 }
 
 extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_out,
@@ -958,8 +1086,8 @@ static bool plan_ok(int fmt, int nwn, int split, int nsb) {
     if (nwn == 2) return fmt != DQ_FMT_Q8_0 && nsb % (2 * split) == 0;
     return true;
 }
-static GemmPlan plan_gemm(int fmt, size_t rows, size_t n_tok, int nsb) {
-    const size_t c = (size_t)cus();
+static GemmPlan plan_gemm(int fmt, size_t rows, size_t n_tok, int nsb, int cu_budget = 0) {
+    const size_t c = cu_budget > 0 ? (size_t)cu_budget : (size_t)cus();
     const size_t mb = (n_tok + BM - 1) / BM;
     GemmPlan best{4, 1};
     size_t best_cost = ~(size_t)0;
@@ -987,17 +1115,23 @@ static GemmPlan plan_gemm(int fmt, size_t rows, size_t n_tok, int nsb) {
 
 template <int FMT>
 static int launch_plan(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, float* d_y, bool y_zeroed,
-                       hipStream_t s) {
-    const GemmPlan p = plan_gemm(FMT, rows, n_tok, nsb);
+                       hipStream_t s, int cu_budget) {
+    const GemmPlan p = plan_gemm(FMT, rows, n_tok, nsb, cu_budget);
     if constexpr (FMT != DQ_FMT_Q8_0) {
         if (p.nwn == 2) return launch_gemm<FMT, 2, 2, 2>(g, rows, n_tok, nsb, p.split, d_y, y_zeroed, s);
     }
     return launch_gemm<FMT, 4, 1, 3>(g, rows, n_tok, nsb, p.split, d_y, y_zeroed, s);
 }
 
-bool dq_gemm_adds_into_y(int fmt, size_t rows, size_t cols, size_t n_tok) {
+bool dq_gemm_adds_into_y(int fmt, size_t rows, size_t cols, size_t n_tok, int cu_budget) {
     if (cols % 256 || rows == 0 || n_tok == 0) return false;
-    return plan_gemm(fmt, rows, n_tok, (int)(cols / 256)).split > 1;
+    return plan_gemm(fmt, rows, n_tok, (int)(cols / 256), cu_budget).split > 1;
+}
+
+size_t dq_gemm_workgroups(int fmt, size_t rows, size_t cols, size_t n_tok, int cu_budget) {
+    if (cols % 256 || rows == 0 || n_tok == 0) return 0;
+    const GemmPlan p = plan_gemm(fmt, rows, n_tok, (int)(cols / 256), cu_budget);
+    return ((n_tok + BM - 1) / BM) * ((rows + 64 * p.nwn - 1) / (64 * p.nwn)) * p.split;
 }
 
 // GEMM on the workspace written by dq_quantize_act_f16.
@@ -1007,7 +1141,7 @@ extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols
 }
 
 int dq_gemm_f16act_zeroed(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work, size_t n_tok,
-                          float* d_y, bool y_zeroed, void* stream) {
+                          float* d_y, bool y_zeroed, void* stream, int cu_budget) {
     DqLayout L;
     if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K && fmt != DQ_FMT_Q8_0 && fmt != DQ_FMT_Q4_0)
         return DQ_ERR_NOT_SUPPORTED;
@@ -1029,10 +1163,10 @@ int dq_gemm_f16act_zeroed(int fmt, const void* d_w, size_t rows, size_t cols, co
     g.K = (int)cols;
     const int nsb = (int)cols / 256;  // super-blocks (cols % 256 == 0)
     switch (fmt) {
-    case DQ_FMT_Q4_K: return launch_plan<DQ_FMT_Q4_K>(g, rows, n_tok, nsb, d_y, y_zeroed, s);
-    case DQ_FMT_Q8_0: return launch_plan<DQ_FMT_Q8_0>(g, rows, n_tok, nsb, d_y, y_zeroed, s);
-    case DQ_FMT_Q4_0: return launch_plan<DQ_FMT_Q4_0>(g, rows, n_tok, nsb, d_y, y_zeroed, s);
-    default: return launch_plan<DQ_FMT_Q6_K>(g, rows, n_tok, nsb, d_y, y_zeroed, s);
+    case DQ_FMT_Q4_K: return launch_plan<DQ_FMT_Q4_K>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+    case DQ_FMT_Q8_0: return launch_plan<DQ_FMT_Q8_0>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+    case DQ_FMT_Q4_0: return launch_plan<DQ_FMT_Q4_0>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+    default: return launch_plan<DQ_FMT_Q6_K>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
     }
 }
 

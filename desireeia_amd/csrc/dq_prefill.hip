@@ -29,6 +29,7 @@
 // Range: the cached values and the scaled query must lie inside fp16
 // (|x| < 65504), which Q8_0 rows of activations satisfy.
 #include <cstdlib>
+#include <mutex>
 
 #include "dq_common.h"
 #include "dq_f16.h"
@@ -555,19 +556,6 @@ __global__ __launch_bounds__(256) void add_kernel(const float* __restrict__ a, c
     reinterpret_cast<float4*>(out)[i] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
 }
 
-// h = act(gate) * up: silu(x) = x / (1 + expf(-x)) or gelu_tanh (models/dense_forward.cpp
-// :53-55, :3606-3611), in place into up, 4 per lane.
-template <int ACT>
-__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const float* __restrict__ gate, float* __restrict__ up,
-                                                           size_t n4) {
-    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n4) return;
-    const float4 g = reinterpret_cast<const float4*>(gate)[i];
-    const float4 u = reinterpret_cast<const float4*>(up)[i];
-    reinterpret_cast<float4*>(up)[i] = make_float4(dq_ffn_act<ACT>(g.x) * u.x, dq_ffn_act<ACT>(g.y) * u.y,
-                                                   dq_ffn_act<ACT>(g.z) * u.z, dq_ffn_act<ACT>(g.w) * u.w);
-}
-
 // ---------------------------------------------------------- layer prefill --
 // Workspace of dq_layer_prefill: fp32 activations of the chunk, then one
 // GEMM activation workspace per K-quant format (sized for the widest input).
@@ -665,6 +653,53 @@ int prefill_cus() {
                 : 256;
     }
     return c;
+}
+
+// ------------------------------------------------------------ side streams --
+// Products of one input that leave most of the GPU idle on their own (the K
+// and V projections beside Q: 64 workgroups each at a 512-token chunk) run
+// side by side: the first on the caller's stream, the others on side streams
+// forked from it by an event and joined back before the next kernel, each
+// planned for its share of the CUs. The side streams (default priority) and
+// events are created once per device outside graph capture; a call under
+// capture before they exist runs the products one after another. Under
+// capture the fork and join become graph edges.
+constexpr int SIDE_N = 3;
+struct SideStreams {
+    hipStream_t st[SIDE_N] = {};
+    hipEvent_t fork = nullptr, join[SIDE_N] = {};
+    bool ok = false;
+};
+constexpr int SIDE_DEVICES = 64;
+SideStreams g_side[SIDE_DEVICES];
+std::mutex g_side_mu;
+
+SideStreams* side_streams(hipStream_t s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= SIDE_DEVICES) return nullptr;
+    std::lock_guard<std::mutex> lk(g_side_mu);
+    SideStreams& g = g_side[dev];
+    if (g.ok) return &g;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    bool good = hipEventCreateWithFlags(&g.fork, hipEventDisableTiming) == hipSuccess;
+    for (int i = 0; i < SIDE_N && good; ++i)
+        good = hipStreamCreateWithFlags(&g.st[i], hipStreamNonBlocking) == hipSuccess &&
+               hipEventCreateWithFlags(&g.join[i], hipEventDisableTiming) == hipSuccess;
+    if (!good) {
+        (void)hipGetLastError();
+        for (int i = 0; i < SIDE_N; ++i) {
+            if (g.st[i]) (void)hipStreamDestroy(g.st[i]);
+            if (g.join[i]) (void)hipEventDestroy(g.join[i]);
+            g.st[i] = nullptr;
+            g.join[i] = nullptr;
+        }
+        if (g.fork) (void)hipEventDestroy(g.fork);
+        g.fork = nullptr;
+        return nullptr;
+    }
+    g.ok = true;
+    return &g;
 }
 
 }  // namespace
@@ -802,6 +837,7 @@ int dq_rms_norm_rows(const float* d_a, const float* d_b, float* d_h, const float
 int dq_layer_prefill_workspace_bytes(const dq_layer_t* L, uint32_t n_tok, size_t* bytes) {
     if (!L || !bytes) return DQ_ERR_INVALID_ARG;
     if (!prefill_layer_ok(L)) return DQ_ERR_NOT_SUPPORTED;
+    (void)side_streams(nullptr);  // set up here, outside any graph capture, when possible
     *bytes = prefill_carve(L, n_tok, nullptr).total;
     return DQ_OK;
 }
@@ -829,35 +865,133 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
     auto cls = [](int fmt) { return fmt == DQ_FMT_Q4_K ? 0 : (fmt == DQ_FMT_Q6_K ? 1 : 2); };
     auto gw = [&](int fmt) { return w.gw[cls(fmt)]; };
     // products of one input x [T][cols] with up to four matrices: one
-    // activation quantization per distinct format
+    // activation quantization per distinct format class (with glu_gate, of
+    // the gated FFN product act(glu_gate) * x). When the smallest product
+    // would leave more than half the CUs idle on its own, they run side by
+    // side (side_streams), each planned for its share of the CUs still free,
+    // largest first: product 0 and its class's quantizer on the caller's
+    // stream, then a fork; the other products of that class on side streams
+    // of their own, another class's quantizer and products together on one
+    // side stream.
+    const float* glu_gate = nullptr;
+    int glu_act = DQ_ACT_SILU;
+    // with norm_w, x is first produced by the RMSNorm of norm_a (+ norm_b,
+    // kept in norm_h) fused with the quantization (dq_norm_quant_f16)
+    const float *norm_a = nullptr, *norm_b = nullptr, *norm_w = nullptr;
+    float* norm_h = nullptr;
     auto products = [&](const float* x, size_t cols, int n, const int* fmt, const void* const* wm, const size_t* rows,
                         float* const* y) -> int {
-        // the quantizer of a format class also clears the outputs its
-        // K-split products add their partials into
-        bool done[3] = {false, false, false}, zeroed[4] = {false, false, false, false};
-        for (int j = 0; j < n; ++j) {
-            const int fi = cls(fmt[j]);
-            if (!done[fi]) {
-                DqZeroSpans z{};
-                int k = 0;
-                for (int i = j; i < n; ++i) {
-                    if (k == DqZeroSpans::N || cls(fmt[i]) != fi || !dq_gemm_adds_into_y(fmt[i], rows[i], cols, T) ||
-                        !dq_zero_span_ok(y[i], rows[i] * T))
-                        continue;
-                    z.p[k] = y[i];
-                    z.n[k++] = rows[i] * T;
-                    zeroed[i] = true;
-                }
-                DQP_TRY(dq_quantize_act_f16_zero(fmt[j], x, cols, T, gw(fmt[j]), z, stream));
-                done[fi] = true;
+        const int C = dq_gemm_cus();
+        int budget[4] = {0, 0, 0, 0};
+        SideStreams* ss = nullptr;
+        if (n > 1) {
+            size_t smallest = ~(size_t)0;
+            for (int j = 0; j < n; ++j) {
+                const size_t wg = dq_gemm_workgroups(fmt[j], rows[j], cols, T);
+                if (wg < smallest) smallest = wg;
             }
-            DQP_TRY(dq_gemm_f16act_zeroed(fmt[j], wm[j], rows[j], cols, gw(fmt[j]), T, y[j], zeroed[j], stream));
+            if (2 * smallest < (size_t)C) ss = side_streams(s);
+        }
+        if (ss) {
+            int order[4] = {0, 1, 2, 3};
+            for (int a = 1; a < n; ++a)  // by rows, largest first (stable)
+                for (int b = a; b > 0 && rows[order[b]] > rows[order[b - 1]]; --b) {
+                    const int t = order[b];
+                    order[b] = order[b - 1];
+                    order[b - 1] = t;
+                }
+            long rem_c = C;
+            size_t rem_w = 0;
+            for (int j = 0; j < n; ++j) rem_w += rows[j];
+            for (int a = 0; a < n; ++a) {
+                const int j = order[a];
+                const long share = (long)((double)rem_c * (double)rows[j] / (double)rem_w);
+                const int b = (int)(share > 8 ? share : 8);
+                budget[j] = b;
+                const long wg = (long)dq_gemm_workgroups(fmt[j], rows[j], cols, T, b);
+                const long left = rem_c - (wg < b ? wg : b);
+                rem_c = left > 8 ? left : 8;
+                rem_w -= rows[j];
+            }
+        }
+        // the stream of each product: -1 the caller's, else a side stream
+        int lane[4] = {-1, -1, -1, -1}, n_side = 0, class_side[3] = {-1, -1, -1};
+        const int c0 = cls(fmt[0]);
+        if (ss) {
+            for (int j = 1; j < n; ++j) {
+                const int c = cls(fmt[j]);
+                if (c == c0) {
+                    if (n_side < SIDE_N) lane[j] = n_side++;
+                } else if (class_side[c] >= 0) {
+                    lane[j] = class_side[c];
+                } else if (n_side < SIDE_N) {
+                    lane[j] = class_side[c] = n_side++;
+                }
+            }
+        }
+        // a class's quantizer runs on the stream of its first product and
+        // clears the outputs its K-split products add their partials into
+        bool done[3] = {false, false, false}, zeroed[4] = {false, false, false, false};
+        auto spans = [&](int j, unsigned classes) {
+            DqZeroSpans z{};
+            int k = 0;
+            for (int i = j; i < n; ++i) {
+                if (k == DqZeroSpans::N || !((classes >> cls(fmt[i])) & 1u) ||
+                    !dq_gemm_adds_into_y(fmt[i], rows[i], cols, T, budget[i]) || !dq_zero_span_ok(y[i], rows[i] * T))
+                    continue;
+                z.p[k] = y[i];
+                z.n[k++] = rows[i] * T;
+                zeroed[i] = true;
+            }
+            return z;
+        };
+        auto quantize = [&](int j, hipStream_t qs) -> int {
+            const int fi = cls(fmt[j]);
+            const DqZeroSpans z = spans(j, 1u << fi);
+            done[fi] = true;
+            return dq_quantize_act_f16_zero(fmt[j], x, cols, T, gw(fmt[j]), z, qs, glu_gate, glu_act);
+        };
+        if (norm_w) {
+            // the norm that produces x, fused with the quantization for
+            // product 0's class and the first other class (x itself is
+            // written only for a third class)
+            int nf = 1, fq[2] = {fmt[0], 0};
+            for (int j = 1; j < n && nf < 2; ++j)
+                if (cls(fmt[j]) != cls(fmt[0])) fq[nf++] = fmt[j];
+            void* outs[2] = {gw(fq[0]), nf > 1 ? gw(fq[1]) : nullptr};
+            const unsigned classes = (1u << cls(fq[0])) | (nf > 1 ? 1u << cls(fq[1]) : 0u);
+            bool third = false;
+            for (int j = 0; j < n; ++j) third |= !((classes >> cls(fmt[j])) & 1u);
+            const DqZeroSpans z = spans(0, classes);
+            DQP_TRY(dq_norm_quant_f16(norm_a, norm_b, norm_h, norm_w, cols, T, L->rms_eps,
+                                      third ? const_cast<float*>(x) : nullptr, nf, fq, outs, z, s));
+            for (int k = 0; k < nf; ++k) done[cls(fq[k])] = true;
+        } else {
+            DQP_TRY(quantize(0, s));
+        }
+        // one fork after product 0's quantizer (a fork before it, letting
+        // another class's quantizer run beside it, measured slower: the
+        // replayed graph then ran that quantizer after product 0)
+        if (n_side > 0) {
+            if (hipEventRecord(ss->fork, s) != hipSuccess) return DQ_ERR_IO;
+            for (int i = 0; i < n_side; ++i)
+                if (hipStreamWaitEvent(ss->st[i], ss->fork, 0) != hipSuccess) return DQ_ERR_IO;
+        }
+        for (int j = 0; j < n; ++j) {
+            const hipStream_t js = lane[j] < 0 ? s : ss->st[lane[j]];
+            if (!done[cls(fmt[j])]) DQP_TRY(quantize(j, js));
+            DQP_TRY(dq_gemm_f16act_zeroed(fmt[j], wm[j], rows[j], cols, gw(fmt[j]), T, y[j], zeroed[j], js,
+                                          budget[j]));
+        }
+        for (int i = 0; i < n_side; ++i) {
+            if (hipEventRecord(ss->join[i], ss->st[i]) != hipSuccess) return DQ_ERR_IO;
+            if (hipStreamWaitEvent(s, ss->join[i], 0) != hipSuccess) return DQ_ERR_IO;
         }
         return DQ_OK;
     };
     // attention block (models/dense_forward.cpp:3264-3290, 3300-3362, 3430-3460)
-    rms_norm_rows_kernel<<<n_tok, 256, 0, s>>>(d_x, nullptr, nullptr, L->attn_norm, (int)E, L->rms_eps, w.xn);
-    DQP_TRY(dq_launch_status());
+    norm_a = d_x;
+    norm_w = L->attn_norm;
     {
         // with the attention gate's matrix, which reads the same normalised
         // input (:3525-3526)
@@ -867,6 +1001,7 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         float* const y[4] = {w.q, w.k, w.v, w.ag};
         DQP_TRY(products(w.xn, E, L->wag ? 4 : 3, f, m, r, y));
     }
+    norm_w = nullptr;
     DQP_TRY(dq_rope_kv_write_batch_post(w.q, w.k, w.v, QD, KVD, d_rope, L->n_rot, n_tok, L->n_head, L->n_head_kv,
                                         L->head_dim, d_kc, d_vc, pos0, n_ctx, dq_layer_post(L), stream));
     DQP_TRY(dq_attn_prefill_q8(w.q, d_kc, d_vc, n_tok, L->n_head, L->n_head_kv, L->head_dim, (uint32_t)QD, pos0,
@@ -885,11 +1020,13 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
     // residual + FFN norm (:3539-3560), gated FFN (:3600-3624)
     if (L->post_attn_norm) {  // sandwich norm of the projection before the residual
         DQP_TRY(dq_post_norm_add(w.down, L->post_attn_norm, d_x, w.h, E, n_tok, L->rms_eps, stream));
-        rms_norm_rows_kernel<<<n_tok, 256, 0, s>>>(w.h, nullptr, nullptr, L->ffn_norm, (int)E, L->rms_eps, w.xn);
-    } else {
-        rms_norm_rows_kernel<<<n_tok, 256, 0, s>>>(w.down, d_x, w.h, L->ffn_norm, (int)E, L->rms_eps, w.xn);
+        norm_a = w.h;
+    } else {  // the residual, kept in h, and the FFN norm of it
+        norm_a = w.down;
+        norm_b = d_x;
+        norm_h = w.h;
     }
-    DQP_TRY(dq_launch_status());
+    norm_w = L->ffn_norm;
     {
         const int f[2] = {L->fmt_up, L->fmt_gate};
         const void* m[2] = {L->wup, L->wgate};
@@ -897,13 +1034,12 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         float* const y[2] = {w.up, w.gate};
         DQP_TRY(products(w.xn, E, 2, f, m, r, y));
     }
-    const size_t nf4 = T * F / 4;
-    // the batch branch's activation: silu, or gelu_tanh per element (:3608-3609)
-    if (L->act_gelu)
-        silu_mul_rows_kernel<DQ_ACT_GELU_TANH><<<(unsigned)((nf4 + 255) / 256), 256, 0, s>>>(w.gate, w.up, nf4);
-    else
-        silu_mul_rows_kernel<DQ_ACT_SILU><<<(unsigned)((nf4 + 255) / 256), 256, 0, s>>>(w.gate, w.up, nf4);
-    DQP_TRY(dq_launch_status());
+    norm_w = nullptr;
+    // the batch branch's activation, silu or gelu_tanh per element
+    // (:3608-3609), formed by the down projection's quantizer as it reads
+    // gate and up
+    glu_gate = w.gate;
+    glu_act = L->act_gelu ? DQ_ACT_GELU_TANH : DQ_ACT_SILU;
     {
         const int f[1] = {L->fmt_down};
         const void* m[1] = {L->wdown};

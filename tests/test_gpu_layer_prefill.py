@@ -122,6 +122,7 @@ def gpu_fns(gpu, layer, kc, vc, pos0, T):
 
 Q80_ALL = {nm: synth.Q8_0 for nm in ("q", "k", "v", "o", "gate", "up", "down")}
 Q40_FFN = {"gate": synth.Q4_0, "up": synth.Q4_0, "v": synth.Q8_0}
+THREE_CLASSES = {"k": synth.Q6_K, "v": synth.Q8_0}  # Q, K, V in three activation layouts
 
 
 @pytest.mark.parametrize("E,n_head,n_kv,F,pos0,n_tok,types,qwen", [
@@ -130,6 +131,7 @@ Q40_FFN = {"gate": synth.Q4_0, "up": synth.Q4_0, "v": synth.Q8_0}
     (512, 4, 2, 1024, 70, 130, None, False),      # two attention query blocks, GEMM M tail
     (512, 8, 2, 1536, 30, 48, Q80_ALL, False),    # a Q8_0 model
     (512, 8, 2, 1536, 10, 40, Q40_FFN, False),    # Q4_0 FFN, Q8_0 V, Q4_K/Q6_K elsewhere
+    (512, 8, 2, 1536, 10, 40, THREE_CLASSES, False),  # the Q/K/V input quantized in three layouts
     (512, 8, 2, 1536, 20, 40, None, True),        # Qwen-style: Q/K/V biases, per-head QK-norm
     (512, 8, 2, 1536, 20, 40, None, "gelu"),      # gated GELU FFN (gelu_tanh)
     (512, 8, 2, 1536, 20, 40, None, "gemma"),     # gated GELU and sandwich norms
