@@ -41,6 +41,7 @@ SIGNATURES = {
     "dq_gemv_group": (c_int, [c_p, c_size, c_size, c_p, c_p, c_p, c_p]),
     "dq_gemv_f32": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p, c_p]),
     "dq_gemv_group_f32": (c_int, [c_p, c_size, c_size, c_p, c_p]),
+    "dq_gemv_group_fused": (c_int, [c_p, c_size, c_size, c_int, c_p, c_p, c_f, c_p]),
     "dq_rope_cache": (c_int, [c_p, c_u32, c_u32, c_f]),
     "dq_norm_quant": (c_int, [c_p, c_p, c_p, c_p, c_size, c_f, c_p, c_p, c_p, c_p]),
     "dq_silu_quant": (c_int, [c_p, c_p, c_size, c_p, c_p, c_p, c_p]),

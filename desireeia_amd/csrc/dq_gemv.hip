@@ -758,6 +758,263 @@ __global__ __launch_bounds__(NW * 64) void gemv_flat16_kernel(Jobs J, int items,
                                  reinterpret_cast<float(*)[R][4]>(&part[gi][0][0]), 0, live);
 }
 
+// The decoder layer's per-256 GEMV groups with the activation formed in the
+// kernel from fp32 inputs, so that no launch sits between the GEMV and the
+// kernel that wrote those inputs:
+//  * XS_NORM: y = h * (1/sqrtf(mean(h^2) + eps)) * w (the layer's RMSNorm:
+//    squares in float, summed in double; models/dense_forward.cpp:129-165);
+//  * XS_SILU / XS_GEGLU: y = act(gate) * up (dq_ffn_act);
+// then the per-256 quantizer into LDS (xrow_quant), as gemv_flat16_kernel.
+// Every workgroup forms and quantizes the whole activation (one or two
+// passes of 1024 columns per wave, loads issued before the weights). Jobs
+// may be Q4_K and Q6_K together (the Q/K/V group): each job's groups start
+// at a multiple of the workgroup's GPW groups, so a workgroup runs one
+// format and its barriers are uniform. The norm's double sum runs per lane,
+// over the wave by xor shuffles and over the waves in order: another order
+// than norm_quant_kernel's, so the scale can differ in the last bit of the
+// double (not of the float, except within ~1e-13 relative of a float
+// rounding boundary); act(gate) * up is value by value, bit-identical.
+enum XSrcKind { XS_NORM = DQ_FUSE_NORM, XS_SILU = DQ_FUSE_SILU, XS_GEGLU = DQ_FUSE_GEGLU };
+struct XSrc {
+    const float* a;  // XS_NORM: h; else gate
+    const float* b;  // XS_NORM: the norm weights; else up
+    float eps;
+};
+
+template <int FA, int FB, int R, int KS, int NW, int XS>
+__global__ __launch_bounds__(NW * 64) void gemv_src_kernel(Jobs J, int items, int per, XSrc S) {
+    static_assert(NW == 16 || NW == 8 || (NW == 4 && KS == 1), "waves per workgroup");
+    constexpr int XP = (KS == 4 && NW == 8) ? 2 : 1;  // passes per wave (cols <= 1024 NW XP)
+    constexpr int GPW = KS == 1 ? NW : NW / 4;        // groups per workgroup
+    extern __shared__ __align__(16) uint8_t xl[];
+    __shared__ float part[GPW][R][4];
+    __shared__ double red[NW];
+    const int lane = threadIdx.x & (DQ_WAVE - 1);
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / DQ_WAVE));
+    const int ks = KS == 1 ? 0 : (wv & 3);
+    const int gi = KS == 1 ? wv : (wv >> 2);
+    const int i0 = min(ks * per, items);
+    const int i1 = min(i0 + per, items);
+    const int ngroups = J.g0[J.n];
+    const int g = GPW * (int)blockIdx.x + gi;
+    const bool live = g < ngroups;
+    const int cols = 64 * items;
+    const int nblk = 2 * items;
+    int gl0 = 0;
+    const int j0 = job_of(J, min(GPW * (int)blockIdx.x, ngroups - 1), &gl0);  // workgroup-uniform
+
+    auto body = [&](auto fc) {
+        constexpr int F = decltype(fc)::value;
+        using W = typename Fmt<F>::W;
+        XRow xa[XP], xb[XP];
+#pragma unroll
+        for (int p = 0; p < XP; ++p) {
+            xrow_load(xa[p], S.a, cols, wv + NW * p, lane);
+            xrow_load(xb[p], S.b, cols, wv + NW * p, lane);
+        }
+        W w[R][1];
+        load_group<F, R, 1>(w, J, min(g, ngroups - 1), ngroups, i0, i1, lane, nullptr);
+        __builtin_amdgcn_sched_barrier(0);
+        XRow y[XP];
+        if constexpr (XS == XS_NORM) {
+            double acc = 0.0;
+#pragma unroll
+            for (int p = 0; p < XP; ++p) {
+                // a 256-block of the row lies wholly inside or outside the columns
+                const bool in = 1024 * (wv + NW * p) + 256 * (lane >> 4) < cols;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 v = xa[p].v[k];
+                    const float s0 = v.x * v.x, s1 = v.y * v.y, s2 = v.z * v.z, s3 = v.w * v.w;
+                    acc += in ? (double)s0 : 0.0;
+                    acc += in ? (double)s1 : 0.0;
+                    acc += in ? (double)s2 : 0.0;
+                    acc += in ? (double)s3 : 0.0;
+                }
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, DQ_WAVE);
+            if (lane == 0) red[wv] = acc;
+            __syncthreads();
+            double t = 0.0;
+#pragma unroll
+            for (int i = 0; i < NW; ++i) t += red[i];
+            const float sc = 1.0f / sqrtf((float)(t / (double)cols) + S.eps);
+#pragma unroll
+            for (int p = 0; p < XP; ++p)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 v = xa[p].v[k], ww = xb[p].v[k];
+                    y[p].v[k] = float4{v.x * sc * ww.x, v.y * sc * ww.y, v.z * sc * ww.z, v.w * sc * ww.w};
+                }
+        } else {
+            constexpr int ACT = XS == XS_GEGLU ? DQ_ACT_GEGLU : DQ_ACT_SILU;
+#pragma unroll
+            for (int p = 0; p < XP; ++p)
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float4 gv = xa[p].v[k], uv = xb[p].v[k];
+                    y[p].v[k] = float4{dq_ffn_act<ACT>(gv.x) * uv.x, dq_ffn_act<ACT>(gv.y) * uv.y,
+                                       dq_ffn_act<ACT>(gv.z) * uv.z, dq_ffn_act<ACT>(gv.w) * uv.w};
+                }
+        }
+#pragma unroll
+        for (int p = 0; p < XP; ++p) {
+            if (1024 * (wv + NW * p) < cols)
+                xrow_quant(y[p], cols, wv + NW * p, lane, nblk, xl);
+            else
+                asm volatile("" ::"v"(y[p].v[0].x), "v"(y[p].v[1].x), "v"(y[p].v[2].x), "v"(y[p].v[3].x));
+        }
+        __syncthreads();
+        if (KS == 1 && !live) return;  // KS 1 has no barrier after this one
+        XItem X[1];
+        Fmt<F>::load_x(X[0], min(i0 + lane, i1 - 1), reinterpret_cast<const int8_t*>(xl),
+                       reinterpret_cast<const float*>(xl + 32 * nblk),
+                       reinterpret_cast<const int32_t*>(xl + 36 * nblk));
+        compute_group<F, R, 1, KS>(w, X, J, min(g, ngroups - 1), i0, i1, lane, ks,
+                                   reinterpret_cast<float(*)[R][4]>(&part[gi][0][0]), 0, live);
+    };
+    if (FA == FB || J.fmt[j0] == FA)
+        body(std::integral_constant<int, FA>{});
+    else
+        body(std::integral_constant<int, FB>{});
+}
+
+// Persistent form of gemv_src_kernel (the gate+up group, whose weights do not
+// fit in flight at once): 4-wave workgroups walking units of 4 groups (one
+// per wave, one item per lane: cols <= 4096, no K split) with gemv_kernel's
+// two-deep pipeline, after forming and quantizing the activation once per
+// workgroup (one pass of 1024 columns per wave).
+// GLU >= 0 (DQ_ACT_SILU / DQ_ACT_GEGLU; R = 2): the paired gated FFN. Jobs
+// 0 and 1 are gate and up with the same rows; group g is row g of both, whose
+// sums (the same as the unpaired launch's) give y0[g] = act(gate) * up
+// (dq_ffn_act, models/dense_forward.cpp:53-55, :107-126) in the epilogue, so
+// the FFN's activation leaves the kernel as one fp32 vector.
+template <int F, int R, int XS, int XP = 1, int GLU = -1>
+__global__ __launch_bounds__(256) void gemv_src_persist_kernel(Jobs J, int items, XSrc S) {
+    static_assert(GLU < 0 || R == 2, "a pair per group");
+    using W = typename Fmt<F>::W;
+    extern __shared__ __align__(16) uint8_t xl[];
+    __shared__ double red[4];
+    const int lane = threadIdx.x & (DQ_WAVE - 1);
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / DQ_WAVE));
+    const int ngroups = J.g0[J.n];
+    const int stride = 4 * (int)gridDim.x;
+    int g = 4 * (int)blockIdx.x + wv;
+    const bool active = g < ngroups;  // uniform per wave
+    const int cols = 64 * items, nblk = 2 * items;
+    const uint8_t* dummy = reinterpret_cast<const uint8_t*>(S.a);
+
+    XRow xa[XP], xb[XP];
+#pragma unroll
+    for (int p = 0; p < XP; ++p) {
+        xrow_load(xa[p], S.a, cols, wv + 4 * p, lane);
+        xrow_load(xb[p], S.b, cols, wv + 4 * p, lane);
+    }
+    W b0[R][1], b1[R][1];
+    // GLU: row g of gate (job 0) and of up (job 1); past the last group a
+    // cached dummy location
+    auto load_pair = [&](W(&w)[R][1], int gg) {
+        const bool live = gg < ngroups;
+        const int xi = min(lane, items - 1);
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+            load_item<F>(w[rr][0], J.w[rr], J.L[rr], (size_t)(live ? gg : 0), xi, live, dummy);
+    };
+    auto compute_pair = [&](const W(&w)[R][1], const XItem& Xi, int gg, int xi) {
+        float a[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const float p = Fmt<F>::dot(w[rr][0], Xi, xi);
+            a[rr] = dq_wave_sum_uniform(0.0f + (lane < items ? p : 0.0f));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (GLU >= 0)
+            if (lane == 0) J.y[0][gg] = dq_ffn_act<GLU>(a[0]) * a[1];
+    };
+    if constexpr (GLU >= 0)
+        load_pair(b0, active ? g : ngroups);
+    else
+        load_group<F, R, 1>(b0, J, active ? g : ngroups, ngroups, 0, items, lane, dummy);
+    __builtin_amdgcn_sched_barrier(0);
+    XRow y[XP];
+    if constexpr (XS == XS_NORM) {
+        double acc = 0.0;
+#pragma unroll
+        for (int p = 0; p < XP; ++p) {
+            const bool in = 1024 * (wv + 4 * p) + 256 * (lane >> 4) < cols;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 v = xa[p].v[k];
+                const float s0 = v.x * v.x, s1 = v.y * v.y, s2 = v.z * v.z, s3 = v.w * v.w;
+                acc += in ? (double)s0 : 0.0;
+                acc += in ? (double)s1 : 0.0;
+                acc += in ? (double)s2 : 0.0;
+                acc += in ? (double)s3 : 0.0;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, DQ_WAVE);
+        if (lane == 0) red[wv] = acc;
+        __syncthreads();
+        const double t = ((red[0] + red[1]) + red[2]) + red[3];
+        const float sc = 1.0f / sqrtf((float)(t / (double)cols) + S.eps);
+#pragma unroll
+        for (int p = 0; p < XP; ++p)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 v = xa[p].v[k], ww = xb[p].v[k];
+                y[p].v[k] = float4{v.x * sc * ww.x, v.y * sc * ww.y, v.z * sc * ww.z, v.w * sc * ww.w};
+            }
+    } else {
+        constexpr int ACT = XS == XS_GEGLU ? DQ_ACT_GEGLU : DQ_ACT_SILU;
+#pragma unroll
+        for (int p = 0; p < XP; ++p)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 gv = xa[p].v[k], uv = xb[p].v[k];
+                y[p].v[k] = float4{dq_ffn_act<ACT>(gv.x) * uv.x, dq_ffn_act<ACT>(gv.y) * uv.y,
+                                   dq_ffn_act<ACT>(gv.z) * uv.z, dq_ffn_act<ACT>(gv.w) * uv.w};
+            }
+    }
+#pragma unroll
+    for (int p = 0; p < XP; ++p) {
+        if (1024 * (wv + 4 * p) < cols)
+            xrow_quant(y[p], cols, wv + 4 * p, lane, nblk, xl);
+        else
+            asm volatile("" ::"v"(y[p].v[0].x), "v"(y[p].v[1].x), "v"(y[p].v[2].x), "v"(y[p].v[3].x));
+    }
+    __syncthreads();
+    if (!active) return;  // no barrier follows (no K split)
+    XItem X[1];
+    Fmt<F>::load_x(X[0], min(lane, items - 1), reinterpret_cast<const int8_t*>(xl),
+                   reinterpret_cast<const float*>(xl + 32 * nblk), reinterpret_cast<const int32_t*>(xl + 36 * nblk));
+    if constexpr (GLU >= 0) {
+        const int xi = min(lane, items - 1);
+        for (;;) {
+            load_pair(b1, g + stride);
+            compute_pair(b0, X[0], g, xi);
+            g += stride;
+            if (g >= ngroups) break;
+            load_pair(b0, g + stride);
+            compute_pair(b1, X[0], g, xi);
+            g += stride;
+            if (g >= ngroups) break;
+        }
+    } else {
+        for (;;) {
+            load_group<F, R, 1>(b1, J, g + stride, ngroups, 0, items, lane, dummy);
+            compute_group<F, R, 1, 1>(b0, X, J, g, 0, items, lane, 0, nullptr, 0);
+            g += stride;
+            if (g >= ngroups) break;
+            load_group<F, R, 1>(b0, J, g + stride, ngroups, 0, items, lane, dummy);
+            compute_group<F, R, 1, 1>(b1, X, J, g, 0, items, lane, 0, nullptr, 1);
+            g += stride;
+            if (g >= ngroups) break;
+        }
+    }
+}
+
 int g_num_cus = 0;
 
 int num_cus() {
@@ -982,6 +1239,111 @@ int launch_flat16(const Jobs& J, int items, int per, const float* xf, hipStream_
     return launch_flat16_fit<FMT, KS, 16>(J, items, per, xf, s);
 }
 
+// ---- gemv_src_kernel launches
+// Group prefix of J for R rows per group, every job's groups rounded up to a
+// multiple of gpw (a workgroup's groups then belong to one job).
+void set_groups_aligned(Jobs& J, int R, int gpw) {
+    J.g0[0] = 0;
+    for (int j = 0; j < J.n; ++j) J.g0[j + 1] = J.g0[j] + ((J.rows[j] + R - 1) / R + gpw - 1) / gpw * gpw;
+}
+
+// Workgroups of gemv_src_kernel<...> one CU holds at once (cached).
+template <int FA, int FB, int R, int KS, int NW, int XS>
+int src_resident(size_t lds) {
+    static int c = -1;
+    if (c < 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &nb, reinterpret_cast<const void*>(&gemv_src_kernel<FA, FB, R, KS, NW, XS>), NW * 64, lds) !=
+            hipSuccess)
+            nb = 0;
+        c = nb;
+    }
+    return c;
+}
+
+template <int FA, int FB, int R, int KS, int NW, int XS>
+int launch_src_r(Jobs J, int items, int per, const XSrc& S, hipStream_t s) {
+    constexpr int GPW = KS == 1 ? NW : NW / 4;
+    set_groups_aligned(J, R, GPW);
+    const unsigned grid = (unsigned)(J.g0[J.n] / GPW);
+    gemv_src_kernel<FA, FB, R, KS, NW, XS><<<grid, NW * 64, (size_t)80 * items, s>>>(J, items, per, S);
+    return dq_launch_status();
+}
+
+// The fewest rows per group (K split: the most that still cover every CU,
+// else the fewest that fit) whose workgroups are all resident at once, as
+// launch_flat16_fit; NO_FLAT when none fits.
+template <int FA, int FB, int KS, int NW, int XS>
+int launch_src_fit(const Jobs& J, int items, int per, const XSrc& S, hipStream_t s) {
+    const size_t lds = (size_t)80 * items;
+    constexpr int GPW = KS == 1 ? NW : NW / 4;
+    const long cus = num_cus();
+    auto wgs = [&](int r) {
+        Jobs t = J;
+        set_groups_aligned(t, r, GPW);
+        return (long)(t.g0[t.n] / GPW);
+    };
+    auto fits = [&](int r, int resident) { return resident > 0 && wgs(r) <= cus * resident; };
+    if constexpr (KS == 4) {
+        const int res4 = src_resident<FA, FB, 4, KS, NW, XS>(lds);
+        if (wgs(4) >= cus && fits(4, res4)) return launch_src_r<FA, FB, 4, KS, NW, XS>(J, items, per, S, s);
+        if (fits(2, src_resident<FA, FB, 2, KS, NW, XS>(lds)))
+            return launch_src_r<FA, FB, 2, KS, NW, XS>(J, items, per, S, s);
+        if (fits(4, res4)) return launch_src_r<FA, FB, 4, KS, NW, XS>(J, items, per, S, s);
+    } else {
+        if (fits(1, src_resident<FA, FB, 1, KS, NW, XS>(lds)))
+            return launch_src_r<FA, FB, 1, KS, NW, XS>(J, items, per, S, s);
+        if (fits(2, src_resident<FA, FB, 2, KS, NW, XS>(lds)))
+            return launch_src_r<FA, FB, 2, KS, NW, XS>(J, items, per, S, s);
+        if (fits(4, src_resident<FA, FB, 4, KS, NW, XS>(lds)))
+            return launch_src_r<FA, FB, 4, KS, NW, XS>(J, items, per, S, s);
+    }
+    return NO_FLAT;
+}
+
+// The persistent form for one format (two rows per group, as gemv_kernel's
+// grid: at most DQ_GEMV_WPC waves per CU, every workgroup walking the same
+// number of units).
+template <int F, int XS, int GLU = -1>
+int launch_src_persist(Jobs J, size_t cols, const XSrc& S, hipStream_t s) {
+    static const int wpc = env_int("DQ_GEMV_WPC", 8);
+    constexpr int R = 2;
+    if constexpr (GLU >= 0) {  // one group per pair of rows
+        J.g0[0] = 0;
+        J.g0[1] = J.g0[2] = J.rows[0];
+    } else {
+        set_groups(J, R);
+    }
+    const int units = (J.g0[J.n] + 3) / 4;
+    const int max_wg = max(1, num_cus() * wpc / 4);
+    const int iters = (units + max_wg - 1) / max_wg;
+    const unsigned grid = (unsigned)((units + iters - 1) / iters);
+    const int items = (int)(cols / 64);  // <= 64: one item per lane
+    gemv_src_persist_kernel<F, R, XS, 1, GLU><<<grid, 256, (size_t)80 * items, s>>>(J, items, S);
+    return dq_launch_status();
+}
+
+// Instantiated shapes (one item per lane): rows of <= 4096 columns without a
+// K split (4-wave workgroups; the norm form of one format takes the
+// persistent grid where the flat one does not fit), rows of 4097..16384
+// columns with the K split (8 waves of two passes, else 16 waves of one).
+template <int FA, int FB, int XS>
+int launch_src(const Jobs& J, size_t cols, const XSrc& S, hipStream_t s) {
+    const int items = (int)(cols / 64);
+    if (cols <= 4096) {
+        const int rc = launch_src_fit<FA, FB, 1, 4, XS>(J, items, items, S, s);
+        if (rc != NO_FLAT) return rc;
+        if constexpr (FA == FB) return launch_src_persist<FA, XS>(J, cols, S, s);
+        return NO_FLAT;
+    }
+    if (cols > 16384) return NO_FLAT;
+    const int per = (items + 15) / 16 * 4;  // whole 256-blocks per K quarter
+    const int rc = launch_src_fit<FA, FB, 4, 8, XS>(J, items, per, S, s);
+    if (rc != NO_FLAT) return rc;
+    return launch_src_fit<FA, FB, 4, 16, XS>(J, items, per, S, s);
+}
+
 // Waves of gemv_flat_kernel<FMT, R, KS, XQ, XR> that one CU holds at once
 // (its register and LDS needs; cached per instantiation; XR as flat_xr).
 template <int FMT, int R, int KS>
@@ -1204,4 +1566,57 @@ extern "C" int dq_gemv_group_f32(const dq_gemv_job_t* jobs, size_t n, size_t col
     for (size_t j = 0; jobs && j < n; ++j) any = any || jobs[j].rows;
     if (!d_x && any) return DQ_ERR_INVALID_ARG;
     return run_jobs(jobs, n, cols, nullptr, nullptr, nullptr, d_x, (hipStream_t)stream);
+}
+
+extern "C" int dq_gemv_group_fused(const dq_gemv_job_t* jobs, size_t n, size_t cols, int kind, const float* d_a,
+                                   const float* d_b, float eps, void* stream) {
+    if (kind < DQ_FUSE_NORM || kind > DQ_FUSE_NORM_GEGLU) return DQ_ERR_NOT_SUPPORTED;
+    const bool glu = kind == DQ_FUSE_NORM_SILU || kind == DQ_FUSE_NORM_GEGLU;
+    if (glu && (n != 2 || !jobs || jobs[0].fmt != jobs[1].fmt || jobs[0].rows != jobs[1].rows || jobs[0].d_res ||
+                jobs[1].d_res || cols > 4096))
+        return DQ_ERR_NOT_SUPPORTED;
+    if (n == 0 || !jobs || n > DQ_GEMV_MAX_JOBS || cols % 256 || cols == 0) return DQ_ERR_NOT_SUPPORTED;
+    if (!d_a || !d_b) return DQ_ERR_INVALID_ARG;
+    DqLayout L[DQ_GEMV_MAX_JOBS];
+    bool q4 = false, q6 = false;
+    Jobs J{};
+    for (size_t j = 0; j < n; ++j) {
+        if (jobs[j].fmt != DQ_FMT_Q4_K && jobs[j].fmt != DQ_FMT_Q6_K) return DQ_ERR_NOT_SUPPORTED;
+        if (!dq_layout(jobs[j].fmt, jobs[j].rows, cols, &L[j]) || jobs[j].rows > 0x3FFFFFFF)
+            return DQ_ERR_NOT_SUPPORTED;
+        if (jobs[j].rows == 0) continue;
+        if (!jobs[j].d_w || !jobs[j].d_y) return DQ_ERR_INVALID_ARG;
+        q4 = q4 || jobs[j].fmt == DQ_FMT_Q4_K;
+        q6 = q6 || jobs[j].fmt == DQ_FMT_Q6_K;
+        J.w[J.n] = (const uint8_t*)jobs[j].d_w;
+        J.fmt[J.n] = jobs[j].fmt;
+        J.L[J.n] = L[j];
+        J.y[J.n] = jobs[j].d_y;
+        J.res[J.n] = jobs[j].d_res;
+        J.rows[J.n] = (int)jobs[j].rows;
+        ++J.n;
+    }
+    if (J.n == 0) return DQ_OK;
+    const XSrc S{d_a, d_b, eps};
+    const hipStream_t s = (hipStream_t)stream;
+    constexpr int A = DQ_FMT_Q4_K, B = DQ_FMT_Q6_K;
+    int rc = NO_FLAT;
+    if (glu) {
+        // gate and up of one format, paired in the persistent kernel
+        if (kind == DQ_FUSE_NORM_SILU)
+            rc = q4 ? launch_src_persist<A, XS_NORM, DQ_ACT_SILU>(J, cols, S, s)
+                    : launch_src_persist<B, XS_NORM, DQ_ACT_SILU>(J, cols, S, s);
+        else
+            rc = q4 ? launch_src_persist<A, XS_NORM, DQ_ACT_GEGLU>(J, cols, S, s)
+                    : launch_src_persist<B, XS_NORM, DQ_ACT_GEGLU>(J, cols, S, s);
+    } else if (kind == DQ_FUSE_NORM) {
+        rc = q4 && q6 ? launch_src<A, B, XS_NORM>(J, cols, S, s)
+                      : (q4 ? launch_src<A, A, XS_NORM>(J, cols, S, s) : launch_src<B, B, XS_NORM>(J, cols, S, s));
+    } else if (!(q4 && q6)) {
+        if (kind == DQ_FUSE_SILU)
+            rc = q4 ? launch_src<A, A, XS_SILU>(J, cols, S, s) : launch_src<B, B, XS_SILU>(J, cols, S, s);
+        else
+            rc = q4 ? launch_src<A, A, XS_GEGLU>(J, cols, S, s) : launch_src<B, B, XS_GEGLU>(J, cols, S, s);
+    }
+    return rc == NO_FLAT ? DQ_ERR_NOT_SUPPORTED : rc;
 }

@@ -470,16 +470,27 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
         if (n32) DQ_TRY(dq_gemv_group(k32, n32, cols, w.bq, w.bs, w.bi, stream));
         return DQ_OK;
     };
+    // The RMSNorm and its per-256 quantization inside the group's GEMV kernel
+    // when every matrix of the group is a K-quant (no launch before the
+    // GEMV); else norm_quant, then the grouped launches.
+    auto norm_group = [&](const float* x, const float* nw, const dq_gemv_job_t* jobs, int n) -> int {
+        bool need32 = false;
+        for (int j = 0; j < n; ++j) need32 = need32 || per32(jobs[j].fmt);
+        if (!need32) {
+            const int rc = dq_gemv_group_fused(jobs, n, E, DQ_FUSE_NORM, x, nw, L->rms_eps, stream);
+            if (rc != DQ_ERR_NOT_SUPPORTED) return rc;
+        }
+        DQ_TRY(norm_acts(x, nw, need32));
+        return run_group(jobs, n, E);
+    };
     // ---- attention block
-    DQ_TRY(norm_acts(d_x, L->attn_norm,
-                     per32(L->fmt_q) || per32(L->fmt_k) || per32(L->fmt_v) || (L->wag && per32(L->fmt_ag))));
     {
         // the attention gate's matrix reads the same normalised input (:4108)
         const dq_gemv_job_t jobs[4] = {{L->fmt_q, L->wq, QD, w.q, nullptr},
                                        {L->fmt_k, L->wk, KVD, w.k, nullptr},
                                        {L->fmt_v, L->wv, KVD, w.v, nullptr},
                                        {L->fmt_ag, L->wag, L->n_head, w.ag, nullptr}};
-        DQ_TRY(run_group(jobs, L->wag ? 4 : 3, E));
+        DQ_TRY(norm_group(d_x, L->attn_norm, jobs, L->wag ? 4 : 3));
     }
     // the optional biases and QK-norm, RoPE, the new K/V rows and attention in
     // one launch when the rotation covers the whole head (else the separate
@@ -515,13 +526,36 @@ int dq_layer_decode(const dq_layer_t* L, const float* d_x, float* d_x_out, const
         DQ_TRY(residual(L->fmt_o, L->wo, E, QD, w.bq, w.bs, w.bi, d_x, L->post_attn_norm, w.x2));
     }
     // ---- feed-forward block
-    DQ_TRY(norm_acts(w.x2, L->ffn_norm, per32(L->fmt_gate) || per32(L->fmt_up)));
     {
         const dq_gemv_job_t jobs[2] = {{L->fmt_gate, L->wgate, F, w.gate, nullptr},
                                        {L->fmt_up, L->wup, F, w.up, nullptr}};
-        DQ_TRY(run_group(jobs, 2, E));
+        // gate and up paired in one kernel that also applies the norm before
+        // and act(gate) * up after them: h (in w.gate) leaves as one fp32
+        // vector, which the down GEMV quantizes in its own kernel (with the
+        // residual in its epilogue, or before the sandwich norm)
+        const int rc = dq_gemv_group_fused(jobs, 2, E, L->act_gelu ? DQ_FUSE_NORM_GEGLU : DQ_FUSE_NORM_SILU, w.x2,
+                                           L->ffn_norm, L->rms_eps, stream);
+        if (rc != DQ_ERR_NOT_SUPPORTED) {
+            DQ_TRY(rc);
+            const float* post = L->post_ffn_norm;
+            const dq_gemv_job_t dj = {L->fmt_down, L->wdown, E, post ? w.tmp : d_x_out, post ? nullptr : w.x2};
+            DQ_TRY(dq_gemv_group_f32(&dj, 1, F, w.gate, stream));
+            return post ? dq_post_norm_add(w.tmp, post, w.x2, d_x_out, E, 1, L->rms_eps, stream) : DQ_OK;
+        }
+        DQ_TRY(norm_group(w.x2, L->ffn_norm, jobs, 2));
     }
     if (kquant(L->fmt_down)) {
+        // act(gate) * up and its per-256 quantization inside the down GEMV's
+        // kernel where it applies (with the residual in its epilogue, or
+        // before the sandwich norm)
+        const float* post = L->post_ffn_norm;
+        const dq_gemv_job_t job = {L->fmt_down, L->wdown, E, post ? w.tmp : d_x_out, post ? nullptr : w.x2};
+        const int rc = dq_gemv_group_fused(&job, 1, F, L->act_gelu ? DQ_FUSE_GEGLU : DQ_FUSE_SILU, w.gate, w.up, 0.0f,
+                                         stream);
+        if (rc != DQ_ERR_NOT_SUPPORTED) {
+            DQ_TRY(rc);
+            return post ? dq_post_norm_add(w.tmp, post, w.x2, d_x_out, E, 1, L->rms_eps, stream) : DQ_OK;
+        }
         DQ_TRY(dq_act_quant(w.gate, w.up, F, L->act_gelu, w.aq, w.as, w.ai, stream));
         DQ_TRY(residual(L->fmt_down, L->wdown, E, F, w.aq, w.as, w.ai, w.x2, L->post_ffn_norm, d_x_out));
     } else {

@@ -185,6 +185,30 @@ def matmul_group(mats, x, outs=None, residuals=None):
     return ys
 
 
+FUSE_NORM, FUSE_SILU, FUSE_GEGLU, FUSE_NORM_SILU, FUSE_NORM_GEGLU = 1, 2, 3, 4, 5
+
+
+def gemv_group_fused(mats, kind, a, b, eps=0.0, outs=None, residuals=None):
+    """Grouped per-256 GEMV whose kernel forms its activation from fp32
+    inputs (dq_gemv_group_fused): kind FUSE_NORM y = rms_norm(a) * b (b the
+    norm weights), FUSE_SILU / FUSE_GEGLU y = act(a) * b (gate, up);
+    FUSE_NORM_SILU / FUSE_NORM_GEGLU: mats = (gate, up), outs[0] receives
+    act(gate) * up."""
+    lib = _lib.load()
+    a, b = a.contiguous(), b.contiguous()
+    n = len(mats)
+    ys = outs if outs is not None else [torch.empty(m.rows, dtype=torch.float32, device=m.buf.device) for m in mats]
+    res = residuals if residuals is not None else [None] * n
+    jobs = (_lib.GemvJob * max(n, 1))()
+    for j, m in enumerate(mats):
+        jobs[j].fmt, jobs[j].d_w, jobs[j].rows = m.fmt, m.buf.data_ptr(), m.rows
+        jobs[j].d_y = ys[j].data_ptr()
+        jobs[j].d_res = res[j].data_ptr() if res[j] is not None else None
+    _lib.check(lib.dq_gemv_group_fused(jobs, n, mats[0].cols if n else 0, kind, _ptr(a), _ptr(b), eps, _stream()),
+               "dq_gemv_group_fused")
+    return ys
+
+
 def gemm_workspace(mat, n_tok):
     lib = _lib.load()
     n = ctypes.c_size_t(0)

@@ -274,6 +274,36 @@ int dq_norm_quant(const float* d_a, const float* d_b, float* d_h, const float* d
                   int8_t* d_q, float* d_scale, int32_t* d_isum, void* stream);
 int dq_silu_quant(const float* d_gate, const float* d_up, size_t n, int8_t* d_q, float* d_scale, int32_t* d_isum,
                   void* stream);
+/* A grouped per-256 GEMV (as dq_gemv_group, jobs of Q4_K and Q6_K; the
+ * norm form may mix the two) whose kernel forms the activation from fp32
+ * inputs and quantizes it per 256 itself, so no launch sits between it and
+ * the kernel that wrote them: the layer's norm_quant + Q/K/V or gate/up, and
+ * silu_quant + down, as one launch each. kind DQ_FUSE_NORM: y = rms_norm_vec
+ * (d_a) * d_b (d_b the norm weights, eps); DQ_FUSE_SILU / DQ_FUSE_GEGLU:
+ * y = act(d_a) * d_b (gate, up; eps unused). The GEMV outputs equal those of
+ * dq_norm_quant / dq_silu_quant followed by dq_gemv_group: bit-identical for
+ * the activation forms; the norm's double sum of squares runs in another
+ * order (the same float scale except within ~1e-13 relative of a float
+ * rounding boundary). cols % 256 == 0 and cols <= 16384; -2
+ * (DQ_ERR_NOT_SUPPORTED), with nothing launched, for other shapes and
+ * formats and where the kernel's grid does not hold the group (more rows
+ * than its workgroups can keep in flight at once; at cols <= 4096 a group of
+ * one format has a persistent form without that limit). No counterpart in
+ * the reference (its CUDA layer runs these as separate kernels).
+ * DQ_FUSE_NORM_SILU / DQ_FUSE_NORM_GEGLU: the norm form for the gated FFN's
+ * gate (jobs[0]) and up (jobs[1]) matrices, of one format and the same
+ * rows, no residuals, cols <= 4096: row r of both is computed by one wave
+ * and jobs[0].d_y[r] = act(gate_r) * up_r is the only output (jobs[1].d_y is
+ * not written), the fp32 input of the down projection (dq_gemv_f32 then
+ * quantizes it in its own kernel). gate_r and up_r are the unpaired form's
+ * values, and act the reference's (models/dense_forward.cpp:53-55, :107-126). */
+#define DQ_FUSE_NORM 1
+#define DQ_FUSE_SILU 2
+#define DQ_FUSE_GEGLU 3
+#define DQ_FUSE_NORM_SILU 4
+#define DQ_FUSE_NORM_GEGLU 5
+int dq_gemv_group_fused(const dq_gemv_job_t* jobs, size_t n, size_t cols, int kind, const float* d_a,
+                        const float* d_b, float eps, void* stream);
 /* h = silu(gate) * up in fp32 (models/dense_forward.cpp:53-55), the input of a
  * Q8_0 / Q4_0 down projection (which quantizes per 32 itself). */
 int dq_silu_mul(const float* d_gate, const float* d_up, size_t n, float* d_h, void* stream);
