@@ -98,13 +98,15 @@ class GemvCase:
 class GemmCase:
     """Prefill GEMM (config 3): X [n_tok][cols] fp32 -> Y [n_tok][rows]."""
 
-    def __init__(self, qtype, rows, cols, n_tok, seed, dev):
+    def __init__(self, qtype, rows, cols, n_tok, seed, dev, tiles=False):
         import torch
         from desireeia_amd import ops, synth
         self.qtype, self.rows, self.cols, self.n_tok = qtype, rows, cols, n_tok
         w = synth.gen_weights(qtype, rows, cols, seed)
         m0 = ops.QuantMatrix.from_gguf(qtype, w, rows, cols, device=dev)
         self.mats = [m0, m0.clone()]
+        if tiles:  # the opt-in tile copies (dq_gemm_tiles_pack) in place of the packed rows
+            self.mats = [ops.GemmTiles(m) for m in self.mats]
         self.x = torch.from_numpy(synth.gen_act((n_tok, cols), seed + 1)).to(dev)
         self.work = ops.gemm_workspace(m0, n_tok)
         self.y = torch.empty(n_tok, rows, dtype=torch.float32, device=dev)
@@ -277,7 +279,7 @@ class LayerPrefillCase:
     attention, norms, SiLU, residuals). RMSNorm weights 0.25 / sqrt(4096) and
     0.3 / sqrt(4096) keep the synthetic activations O(1)."""
 
-    def __init__(self, dev, pos0=0, n_tok=512, seed=60):
+    def __init__(self, dev, pos0=0, n_tok=512, seed=60, tiles=False):
         import torch
         from desireeia_amd import ops, synth
         E, H, KV, HD, F = 4096, 32, 8, 128, 14336
@@ -288,6 +290,8 @@ class LayerPrefillCase:
                 for i, (nm, (qt, r, c)) in enumerate(shapes.items())}
         an, fn = torch.full((E,), 0.25 / 64), torch.full((E,), 0.3 / 64)
         self.layer = ops.DecoderLayer(mats, an, fn, H, KV, HD, pos0 + n_tok, device=dev)
+        if tiles:  # the products read tile copies of the matrices (dq_gemm_tiles_pack)
+            self.layer.use_gemm_tiles()
         g = torch.Generator(device=dev).manual_seed(seed)
         if pos0:
             self.layer.cache.write_batch(torch.randn(pos0, KV * HD, device=dev, generator=g),
@@ -748,9 +752,9 @@ def main():
         return
     gemm_shapes = {"gemm_q4k": (synth.Q4_K, 14336, 4096, 512), "gemm_q6k": (synth.Q6_K, 4096, 14336, 512),
                    "gemm_q80": (synth.Q8_0, 14336, 4096, 512)}
-    if args.only in gemm_shapes:
-        qt, r, c, t = gemm_shapes[args.only]
-        g = GemmCase(qt, r, c, t, 21, dev)
+    if args.only in gemm_shapes or (args.only or "").replace("_tiles", "") in gemm_shapes:
+        qt, r, c, t = gemm_shapes[args.only.replace("_tiles", "")]
+        g = GemmCase(qt, r, c, t, 21, dev, tiles=args.only.endswith("_tiles"))
         us = graph_time(g.kernel, 10, max(1, args.steps // 10))
         us_step = graph_time(g.step, 10, max(1, args.steps // 10))
         log(f"{args.only}: gemm kernel {us:.1f} us = {g.flops() / us / 1e6:.1f} TFLOP/s; "
@@ -782,8 +786,8 @@ def main():
         us = graph_time(pc.kernel, 4, max(1, args.steps // 4))
         log(f"attn_prefill: {us:.1f} us, {pc.flops() / us / 1e6:.1f} TFLOP/s (algorithmic)")
         return
-    if args.only == "layer_prefill":
-        lp = LayerPrefillCase(dev)
+    if args.only in ("layer_prefill", "layer_prefill_tiles"):
+        lp = LayerPrefillCase(dev, tiles=args.only.endswith("_tiles"))
         us = graph_time(lp.step, 1, max(1, args.steps))
         log(f"layer_prefill: {us:.1f} us/layer, {lp.n_tok / us * 1e6:.0f} tok/s, {lp.flops() / us / 1e6:.1f} TFLOP/s")
         return
@@ -877,6 +881,21 @@ def main():
                     "quantize_plus_gemm_TFLOPs": round(g.flops() / us_q / 1e6, 1)}
         log(f"{k}: {us:.1f} us  {tf:.1f} TFLOP/s; with the activation quantization {us_q:.1f} us")
         del g
+        # the same product on the opt-in tile copy of the weights (dq_gemm_tiles_pack)
+        g = GemmCase(qt, r, c, t, 21, dev, tiles=True)
+        kt = replay_times(g.kernel, 10, 10)
+        us = sorted(kt)[len(kt) // 2]
+        us_q = sorted(replay_times(g.step, 10, 10))[5]
+        tf = g.flops() / us / 1e6
+        extra[k + "_tiles"] = {"shape": f"{t}x{c} . {c}x{r}", "kernel_us": round(us, 2),
+                               "kernel_us_best": round(min(kt), 2), "TFLOPs": round(tf, 1),
+                               "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4),
+                               "frac_int8_mfma": round(tf / INT8_PEAK_TOPS, 4),
+                               "quantize_plus_gemm_us": round(us_q, 2),
+                               "quantize_plus_gemm_TFLOPs": round(g.flops() / us_q / 1e6, 1)}
+        log(f"{k} (tile copy of the weights): {us:.1f} us  {tf:.1f} TFLOP/s; with the activation quantization "
+            f"{us_q:.1f} us")
+        del g
     # config 4: decode attention alone and the whole decoder layer
     ac = AttnCase(dev)
     us = graph_time(ac.kernel, len(ac.caches), 10)
@@ -914,6 +933,17 @@ def main():
     extra["layer_prefill_q4km_512tok"] = {"us_per_layer": round(us, 1), "tokens_per_s": round(lp.n_tok / us * 1e6, 1),
                                           "TFLOPs_alg": round(tf, 1), "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4)}
     log(f"decoder layer prefill (512 tokens): {us:.1f} us/layer  {lp.n_tok / us * 1e6:.0f} tok/s  {tf:.1f} TFLOP/s")
+    del lp
+    # the same layer with tile copies of its matrices for the products (dq_gemm_tiles_pack)
+    lp = LayerPrefillCase(dev, tiles=True)
+    us = graph_time(lp.step, 1, 5)
+    tf = lp.flops() / us / 1e6
+    extra["layer_prefill_q4km_512tok_tiles"] = {"us_per_layer": round(us, 1),
+                                                "tokens_per_s": round(lp.n_tok / us * 1e6, 1),
+                                                "TFLOPs_alg": round(tf, 1),
+                                                "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4)}
+    log(f"decoder layer prefill (512 tokens, tile copies of the weights): {us:.1f} us/layer  "
+        f"{lp.n_tok / us * 1e6:.0f} tok/s  {tf:.1f} TFLOP/s")
     del lp
     hc = HeadCase(dev)
     us = graph_time(hc.logits_step, 4, 5)

@@ -28,6 +28,8 @@ SIGNATURES = {
     "dq_gemm": (c_int, [c_int, c_p, c_size, c_size, c_p, c_size, c_p, c_p, c_size, c_p]),
     "dq_quantize_act_f16": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p]),
     "dq_gemm_f16act": (c_int, [c_int, c_p, c_size, c_size, c_p, c_size, c_p, c_p]),
+    "dq_gemm_tiles_bytes": (c_int, [c_int, c_size, c_size, ctypes.POINTER(c_size)]),
+    "dq_gemm_tiles_pack": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p]),
     "dq_kv_write": (c_int, [c_p, c_p, c_u32, c_u32, c_p, c_p, c_u32, c_p, c_u32, c_p]),
     "dq_attn_workspace_bytes": (c_int, [c_u32, c_u32, c_u32, c_u32, ctypes.POINTER(c_size)]),
     "dq_attn_decode_q8": (c_int, [c_p, c_p, c_p, c_u32, c_u32, c_u32, c_u32, c_u32, c_p, c_u32, c_p, c_p, c_size,

@@ -38,6 +38,7 @@ struct WInfo {
     int fmt;
     size_t rows, cols;
     const void* base;  // == the key for a matrix; the matrix for a Q8_0 scale view
+    void* tiles;       // the prefill GEMM's tile copy (DESIREEIA_GEMM_TILES), or NULL
 };
 
 struct LayerGraph {
@@ -276,7 +277,23 @@ bool upload_packed(int fmt, const uint8_t* data, size_t rows, size_t cols, void*
         (void)hipFree(dev);
         return false;
     }
-    g.reg[dev] = WInfo{fmt, rows, cols, dev};
+    // opt-in (DESIREEIA_GEMM_TILES=1): a tile copy for the prefill GEMMs
+    // beside the packed rows the decode GEMV reads (the weights held twice)
+    void* tiles = nullptr;
+    const bool want_tiles = env_flag("DESIREEIA_GEMM_TILES");  // read per upload
+    size_t tb = 0;
+    if (want_tiles && cols % 256 == 0 && dq_gemm_tiles_bytes(fmt, rows, cols, &tb) == DQ_OK) {
+        if (hipMalloc(&tiles, tb) != hipSuccess) {
+            (void)hipGetLastError();
+            tiles = nullptr;
+        } else if (dq_gemm_tiles_pack(fmt, dev, rows, cols, tiles, g.stream) != DQ_OK ||
+                   hipStreamSynchronize(g.stream) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(tiles);
+            tiles = nullptr;
+        }
+    }
+    g.reg[dev] = WInfo{fmt, rows, cols, dev, tiles};
     *out = dev;
     return true;
 }
@@ -358,7 +375,7 @@ bool matmul_q8_0_cuda_upload_weights(const uint8_t* q8_data, size_t rows, size_t
     // the scale plane of the packed matrix, handed out as the engine's
     // separate scale pointer (a view: freeing it frees nothing)
     void* view = (uint8_t*)dev + L.d_off;
-    g.reg[view] = WInfo{DQ_FMT_Q8_0, rows, cols, dev};
+    g.reg[view] = WInfo{DQ_FMT_Q8_0, rows, cols, dev, nullptr};
     *out_d_qs = dev;
     *out_d_scale = view;
     return true;
@@ -391,8 +408,10 @@ void cuda_free_device(void* p) {
             ++gi;
         }
     }
+    void* tiles = it != g.reg.end() ? it->second.tiles : nullptr;
     if (it != g.reg.end()) g.reg.erase(it);
     if (g.stream) (void)hipStreamSynchronize(g.stream);
+    if (tiles) (void)hipFree(tiles);
     (void)hipFree(p);
     (void)hipGetLastError();
 }
@@ -500,8 +519,11 @@ int matmul_kquant_cuda_batch(int format, const void* d_w, size_t rows, size_t co
     if (!reserve(g.xbuf, n_tok * cols * 4) || !reserve(g.ybuf, n_tok * rows * 4) || !reserve(g.work, wbytes))
         return DQ_ERR_IO;
     if (hipMemcpyAsync(g.xbuf.p, x, n_tok * cols * 4, hipMemcpyHostToDevice, g.stream) != hipSuccess) return io_fail();
-    const int rc = dq_gemm(format, d_w, rows, cols, (const float*)g.xbuf.p, n_tok, (float*)g.ybuf.p, g.work.p,
-                           g.work.cap, g.stream);
+    // the matrix's tile copy where the engine keeps one (same results)
+    const WInfo* wi = lookup(d_w);
+    const bool tl = wi && wi->base == d_w && wi->tiles;
+    const int rc = dq_gemm(tl ? (format | DQ_FMT_GEMM_TILES) : format, tl ? wi->tiles : d_w, rows, cols,
+                           (const float*)g.xbuf.p, n_tok, (float*)g.ybuf.p, g.work.p, g.work.cap, g.stream);
     if (rc != DQ_OK) return rc == DQ_ERR_IO ? io_fail() : rc;
     if (hipMemcpyAsync(y, g.ybuf.p, n_tok * rows * 4, hipMemcpyDeviceToHost, g.stream) != hipSuccess) return io_fail();
     return sync();
@@ -982,10 +1004,12 @@ int cuda_layer_forward_batch(const struct CudaLayerBatchArgs* A) {
     const int f[8] = {L.fmt_q, L.fmt_k, L.fmt_v, L.fmt_o, L.fmt_gate, L.fmt_up, L.fmt_down, L.fmt_ag};
     const size_t r[8] = {A->q_dim, A->kv_dim, A->kv_dim, A->n_embd, A->n_ff, A->n_ff, A->n_embd, A->n_head};
     const size_t c[8] = {A->n_embd, A->n_embd, A->n_embd, A->q_dim, A->n_embd, A->n_embd, A->n_ff, A->n_embd};
+    const void** tl[8] = {&L.tq, &L.tk, &L.tv, &L.to, &L.tgate, &L.tup, &L.tdown, &L.tag};
     for (int j = 0; j < (L.wag ? 8 : 7); ++j) {
         const WInfo* wi = lookup(w[j]);
         if (!wi || wi->base != w[j] || wi->fmt != f[j] || wi->rows != r[j] || wi->cols != c[j])
             return DQ_ERR_NOT_SUPPORTED;
+        *tl[j] = wi->tiles;  // the products read the tile copies where they exist
     }
     size_t wbytes = 0;
     if (dq_layer_prefill_workspace_bytes(&L, A->n_tok, &wbytes) != DQ_OK) return DQ_ERR_NOT_SUPPORTED;

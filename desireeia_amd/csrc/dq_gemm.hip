@@ -133,6 +133,7 @@ struct GemmArgs {
     int lda, M, N, K;
     int m0, n0;
     uint32_t magic;         // 0x54005400 (kept in a register: see run_steps)
+    int n_stages;           // tiled weights: super-stages per row
 };
 
 // DMA issue. Every wave issues the same, compile-time number of load
@@ -164,10 +165,48 @@ __device__ __forceinline__ void issue_a(const GemmArgs& g, uint8_t* stage_base, 
     }
 }
 
-template <int NWN, int KIND>
+// Weight tiles (dq_gemm_tiles_pack, opt-in): for every 64-row slice of the
+// matrix and super-stage, the bytes one wave stages into its ring slot, in
+// the ring's own order (items already at their swizzled slots, the scales as
+// the ring's 4-byte slots), one contiguous run: per quant sub-plane
+// [64 rows][SB slots][16 B], then the aux region (Q4_K: 64 super-block
+// headers of 16 B; Q6_K: the 64 rows' 4 int8 scales of each of the 2 items,
+// then d in the low half of a 4-byte slot; Q8_0 / Q4_0: the two fp16 block
+// scales of each of the SB items). Slices run over whole 256-row tiles (rows
+// past the matrix are zero), super-stages fastest, so a wave's K steps read
+// one contiguous stream and every DMA instruction 64 lanes x 16 (or 4)
+// consecutive bytes.
+template <int KIND>
+constexpr int tile_plane_bytes() { return 64 * sb_of<KIND>() * 16; }
+template <int KIND>
+constexpr int tile_aux_bytes() { return KIND == B_Q4K ? 64 * 16 : KIND == B_Q6K ? 3 * 256 : sb_of<KIND>() * 256; }
+template <int KIND>
+constexpr int tile_slice_bytes() { return planes_of<KIND>() * tile_plane_bytes<KIND>() + tile_aux_bytes<KIND>(); }
+
+template <int NWN, int KIND, bool TL = false>
 __device__ __forceinline__ void issue_b(const GemmArgs& g, uint8_t* bb, int sb, int wn, int lane) {
     using R = Ring<NWN, KIND>;
     constexpr int SB = R::SB, BN = R::BN;
+    if constexpr (TL) {
+        constexpr int PL = tile_plane_bytes<KIND>();
+        const uint8_t* src = g.w + ((size_t)(g.n0 / 64 + wn) * g.n_stages + sb) * tile_slice_bytes<KIND>();
+#pragma unroll
+        for (int p = 0; p < planes_of<KIND>(); ++p)
+#pragma unroll
+            for (int k = 0; k < SB; ++k)
+                lds_dma<16>(src + p * PL + (64 * k + lane) * 16, bb + p * R::PLANE + (64 * wn * SB + 64 * k) * 16);
+        const uint8_t* aux = src + planes_of<KIND>() * PL;
+        if constexpr (KIND == B_Q4K) {
+            lds_dma<16>(aux + lane * 16, bb + R::AUX + 64 * wn * 16);
+            const int blk = wn & 1, m = min(g.m0 + blk * 64 + lane, g.M - 1);
+            lds_dma<16>(g.minp + ((size_t)sb * g.M + m) * 8, bb + R::MIN + blk * 64 * 16);
+        } else {
+            constexpr int NA = KIND == B_Q6K ? 3 : SB;  // 4-byte aux slots per row
+#pragma unroll
+            for (int c = 0; c < NA; ++c) lds_dma<4>(aux + c * 256 + lane * 4, bb + R::AUX + c * BN * 4 + 64 * wn * 4);
+        }
+        return;
+    }
     const int item0 = SB * sb;
     // planes: instruction k covers own rows 64 SB^-1 ... : slot s = 64k + lane
 #pragma unroll
@@ -430,7 +469,7 @@ __device__ __forceinline__ h8 a_frag(const uint8_t* base, int kk, int i, int lan
 // 3 with the next step's slice-0 activation fragments; at the last phase the
 // next super-stage's B side (landed by the wait), overlapped with the Q4_K
 // min-term slice. Q4_K builds the min-term weight fragments in phase 1.
-template <int NWN, int KIND, int NS, int T>
+template <int NWN, int KIND, int NS, int T, bool TL>
 __device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* aring, uint8_t* bring, int& astage, int sb,
                                           int a_next, int b_next, Pre& P, f16v (&acc)[4][2], int wn, int lane) {
     using R = Ring<NWN, KIND>;
@@ -478,7 +517,7 @@ __device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* aring, uin
     wait_vm<mid_wait<NWN, KIND, NS, T>()>();
     dq_lds_barrier();
     issue_a<NWN, KIND>(g, aring + astage * R::A_STAGE, a_next, wn, lane);
-    if constexpr (T == 0) issue_b<NWN, KIND>(g, bring + (b_next % NB) * R::B_STAGE, b_next, wn, lane);
+    if constexpr (T == 0) issue_b<NWN, KIND, TL>(g, bring + (b_next % NB) * R::B_STAGE, b_next, wn, lane);
     DQ_PIN();
     // slice 3
     DQ_MF(af3, bf3, 0); P.af[0] = a_frag(anext, 0, 0, lane); DQ_PIN();
@@ -533,18 +572,18 @@ __device__ __forceinline__ void gemm_step(const GemmArgs& g, uint8_t* aring, uin
 // steady state would have issued them, waits for the first step's, and
 // prefetches it; then SB steps per iteration. DMAs past the range re-read the
 // group's last step / super-stage (valid addresses, never consumed).
-template <int NWN, int KIND, int NS>
+template <int NWN, int KIND, int NS, bool TL>
 __device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* aring, uint8_t* bring, int sb0, int sb1,
                                           f16v (&acc)[4][2], int wn, int lane) {
     using R = Ring<NWN, KIND>;
     constexpr int SB = R::SB, NB = R::NB, PA = a_loads<NWN>(), PB = b_loads<KIND>();
     if (sb0 >= sb1) return;  // uniform over the workgroup (the planner gives every K group the same count)
     const int s0 = SB * sb0, s_last = SB * sb1 - 1, sb_last = sb1 - 1;
-    issue_b<NWN, KIND>(g, bring + (sb0 % NB) * R::B_STAGE, sb0, wn, lane);
+    issue_b<NWN, KIND, TL>(g, bring + (sb0 % NB) * R::B_STAGE, sb0, wn, lane);
     issue_a<NWN, KIND>(g, aring, s0, wn, lane);
     issue_a<NWN, KIND>(g, aring + R::A_STAGE, min(s0 + 1, s_last), wn, lane);
     if constexpr (NB == 3)
-        issue_b<NWN, KIND>(g, bring + ((sb0 + 1) % NB) * R::B_STAGE, min(sb0 + 1, sb_last), wn, lane);
+        issue_b<NWN, KIND, TL>(g, bring + ((sb0 + 1) % NB) * R::B_STAGE, min(sb0 + 1, sb_last), wn, lane);
     if constexpr (NS == 3) issue_a<NWN, KIND>(g, aring + 2 * R::A_STAGE, min(s0 + 2, s_last), wn, lane);
     // wait for B(sb0) and A(s0): the loads issued after A(s0) may stay in flight
     wait_vm<(NS - 1) * PA + (NB == 3 ? PB : 0)>();
@@ -559,11 +598,11 @@ __device__ __forceinline__ void run_steps(const GemmArgs& g, uint8_t* aring, uin
     for (int sb = sb0; sb < sb1; ++sb) {
         const int st = SB * sb;
         const int bn = min(sb + NB - 1, sb_last);
-        gemm_step<NWN, KIND, NS, 0>(g, aring, bring, astage, sb, min(st + NS, s_last), bn, P, acc, wn, lane);
-        gemm_step<NWN, KIND, NS, 1>(g, aring, bring, astage, sb, min(st + 1 + NS, s_last), bn, P, acc, wn, lane);
+        gemm_step<NWN, KIND, NS, 0, TL>(g, aring, bring, astage, sb, min(st + NS, s_last), bn, P, acc, wn, lane);
+        gemm_step<NWN, KIND, NS, 1, TL>(g, aring, bring, astage, sb, min(st + 1 + NS, s_last), bn, P, acc, wn, lane);
         if constexpr (SB == 4) {
-            gemm_step<NWN, KIND, NS, 2>(g, aring, bring, astage, sb, min(st + 2 + NS, s_last), bn, P, acc, wn, lane);
-            gemm_step<NWN, KIND, NS, 3>(g, aring, bring, astage, sb, min(st + 3 + NS, s_last), bn, P, acc, wn, lane);
+            gemm_step<NWN, KIND, NS, 2, TL>(g, aring, bring, astage, sb, min(st + 2 + NS, s_last), bn, P, acc, wn, lane);
+            gemm_step<NWN, KIND, NS, 3, TL>(g, aring, bring, astage, sb, min(st + 3 + NS, s_last), bn, P, acc, wn, lane);
         }
     }
     wait_vm<0>();  // drain the DMAs issued past the end
@@ -592,7 +631,7 @@ __device__ __forceinline__ void tile_of(int id, int mb, int nb, int* m_blk, int*
 // selects a K split (atomic_out: partials added into zeroed y, at most 2 so
 // the sum is order-independent). KSW = 2: the K groups' partials are added
 // through LDS in group order.
-template <int FMT, int NWN, int KSW, int NS>
+template <int FMT, int NWN, int KSW, int NS, bool TL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void gemm_kernel(GemmArgs g, float* __restrict__ y, int nsb, int sb_per_split, int atomic_out) {
     static_assert(NWN * KSW == 4, "4 waves per workgroup");
@@ -626,7 +665,7 @@ void gemm_kernel(GemmArgs g, float* __restrict__ y, int nsb, int sb_per_split, i
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     uint8_t* gr = ring + kg * GROUP;
-    run_steps<NWN, KIND, NS>(g, gr, gr + NS * R::A_STAGE, sb0, sb1, acc, wn, lane);
+    run_steps<NWN, KIND, NS, TL>(g, gr, gr + NS * R::A_STAGE, sb0, sb1, acc, wn, lane);
 
     // K group 1 hands its partial to group 0 through the (drained) ring, one
     // half of the tile (j) at a time: acc0 + acc1 in that order
@@ -966,6 +1005,7 @@ static size_t inv_off(int fmt, size_t cols, size_t n_tok) {
 
 extern "C" int dq_gemm_workspace_bytes(int fmt, size_t rows, size_t cols, size_t n_tok, size_t* bytes) {
     (void)rows;
+    fmt &= ~DQ_FMT_GEMM_TILES;
     if (!bytes) return DQ_ERR_INVALID_ARG;
     if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K && fmt != DQ_FMT_Q8_0 && fmt != DQ_FMT_Q4_0)
         return DQ_ERR_NOT_SUPPORTED;
@@ -1052,7 +1092,7 @@ extern "C" int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_
     return dq_quantize_act_f16_zero(fmt, d_x, cols, n_tok, d_out, DqZeroSpans{}, stream);
 }
 
-template <int FMT, int NWN, int KSW, int NS>
+template <int FMT, int NWN, int KSW, int NS, bool TL>
 static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, int split, float* d_y, bool y_zeroed,
                        hipStream_t s) {
     const int mb = (int)((n_tok + BM - 1) / BM), nb = (int)((rows + 64 * NWN - 1) / (64 * NWN));
@@ -1065,7 +1105,7 @@ static int launch_gemm(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, in
         zero_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(d_y, n);
     }
     const dim3 grid((unsigned)(mb * nb), 1, split);
-    gemm_kernel<FMT, NWN, KSW, NS><<<grid, 256, 0, s>>>(g, d_y, nsb, per, split > 1);
+    gemm_kernel<FMT, NWN, KSW, NS, TL><<<grid, 256, 0, s>>>(g, d_y, nsb, per, split > 1);
     return dq_launch_status();
 }
 
@@ -1113,14 +1153,14 @@ static GemmPlan plan_gemm(int fmt, size_t rows, size_t n_tok, int nsb, int cu_bu
     return plan_ok(fmt, o.nwn, o.split, nsb) ? o : best;
 }
 
-template <int FMT>
+template <int FMT, bool TL>
 static int launch_plan(const GemmArgs& g, size_t rows, size_t n_tok, int nsb, float* d_y, bool y_zeroed,
                        hipStream_t s, int cu_budget) {
     const GemmPlan p = plan_gemm(FMT, rows, n_tok, nsb, cu_budget);
     if constexpr (FMT != DQ_FMT_Q8_0) {
-        if (p.nwn == 2) return launch_gemm<FMT, 2, 2, 2>(g, rows, n_tok, nsb, p.split, d_y, y_zeroed, s);
+        if (p.nwn == 2) return launch_gemm<FMT, 2, 2, 2, TL>(g, rows, n_tok, nsb, p.split, d_y, y_zeroed, s);
     }
-    return launch_gemm<FMT, 4, 1, 3>(g, rows, n_tok, nsb, p.split, d_y, y_zeroed, s);
+    return launch_gemm<FMT, 4, 1, 3, TL>(g, rows, n_tok, nsb, p.split, d_y, y_zeroed, s);
 }
 
 bool dq_gemm_adds_into_y(int fmt, size_t rows, size_t cols, size_t n_tok, int cu_budget) {
@@ -1134,15 +1174,116 @@ size_t dq_gemm_workgroups(int fmt, size_t rows, size_t cols, size_t n_tok, int c
     return ((n_tok + BM - 1) / BM) * ((rows + 64 * p.nwn - 1) / (64 * p.nwn)) * p.split;
 }
 
+// ------------------------------------------------------------ weight tiles --
+namespace {
+template <int KIND>
+__global__ __launch_bounds__(256) void gemm_tiles_pack_kernel(const uint8_t* __restrict__ w, DqLayout L, int rows,
+                                                              int n_stages, long n_units, uint8_t* __restrict__ out) {
+    constexpr int SB = sb_of<KIND>(), PL = tile_plane_bytes<KIND>();
+    const long u = (long)blockIdx.x * 256 + threadIdx.x;  // (slice, super-stage, row of the slice)
+    if (u >= n_units) return;
+    const int nl = (int)(u % 64);
+    const long ss = u / 64;
+    const int st = (int)(ss % n_stages), slice = (int)(ss / n_stages);
+    const int row = slice * 64 + nl;
+    const bool live = row < rows;
+    uint8_t* dst = out + (size_t)ss * tile_slice_bytes<KIND>();
+    const dq_u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int p = 0; p < planes_of<KIND>(); ++p)
+#pragma unroll
+        for (int slot = 0; slot < SB; ++slot) {
+            const int item = SB * st + (slot ^ swz<SB>(nl));
+            const dq_u32x4 v = live ? *reinterpret_cast<const dq_u32x4*>(w + L.q_off + p * L.p_stride +
+                                                                        (size_t)row * L.q_row + 16 * (size_t)item)
+                                    : z;
+            *reinterpret_cast<dq_u32x4*>(dst + p * PL + (nl * SB + slot) * 16) = v;
+        }
+    uint8_t* aux = dst + planes_of<KIND>() * PL;
+    if constexpr (KIND == B_Q4K) {
+        const dq_u32x4 v = live ? *reinterpret_cast<const dq_u32x4*>(w + L.s_off + (size_t)row * L.s_row + 16 * (size_t)st)
+                                : z;
+        *reinterpret_cast<dq_u32x4*>(aux + nl * 16) = v;
+    } else if constexpr (KIND == B_Q6K) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            *reinterpret_cast<uint32_t*>(aux + c * 256 + nl * 4) =
+                live ? *reinterpret_cast<const uint32_t*>(w + L.s_off + (size_t)row * L.s_row + 4 * (size_t)(SB * st + c))
+                     : 0u;
+        *reinterpret_cast<uint32_t*>(aux + 512 + nl * 4) =
+            live ? (uint32_t)*reinterpret_cast<const uint16_t*>(w + L.d_off + (size_t)row * L.d_row +
+                                                                2 * (size_t)((SB * st) >> 2))
+                 : 0u;
+    } else {
+#pragma unroll
+        for (int c = 0; c < SB; ++c)
+            *reinterpret_cast<uint32_t*>(aux + c * 256 + nl * 4) =
+                live ? *reinterpret_cast<const uint32_t*>(w + L.d_off + (size_t)row * L.d_row + 4 * (size_t)(SB * st + c))
+                     : 0u;
+    }
+}
+
+int tiles_geometry(int fmt, size_t rows, size_t cols, int* n_stages, long* n_slices, size_t* bytes) {
+    int kind, sb;
+    size_t slice;
+    switch (fmt) {
+    case DQ_FMT_Q4_K: kind = B_Q4K; slice = tile_slice_bytes<B_Q4K>(); break;
+    case DQ_FMT_Q6_K: kind = B_Q6K; slice = tile_slice_bytes<B_Q6K>(); break;
+    case DQ_FMT_Q8_0: kind = B_Q80; slice = tile_slice_bytes<B_Q80>(); break;
+    case DQ_FMT_Q4_0: kind = B_Q40; slice = tile_slice_bytes<B_Q40>(); break;
+    default: return DQ_ERR_NOT_SUPPORTED;
+    }
+    if (cols % 256 || cols == 0 || rows == 0 || rows > (1u << 30)) return DQ_ERR_NOT_SUPPORTED;
+    sb = (kind == B_Q6K || kind == B_Q80) ? 2 : 4;
+    *n_stages = (int)(cols / 64) / sb;
+    *n_slices = (long)((rows + 255) / 256) * 4;  // whole 256-row tiles
+    *bytes = (size_t)*n_slices * *n_stages * slice;
+    return DQ_OK;
+}
+}  // namespace
+
+extern "C" int dq_gemm_tiles_bytes(int fmt, size_t rows, size_t cols, size_t* bytes) {
+    if (!bytes) return DQ_ERR_INVALID_ARG;
+    int ns;
+    long nsl;
+    return tiles_geometry(fmt, rows, cols, &ns, &nsl, bytes);
+}
+
+extern "C" int dq_gemm_tiles_pack(int fmt, const void* d_packed, size_t rows, size_t cols, void* d_tiles,
+                                  void* stream) {
+    int ns;
+    long nsl;
+    size_t bytes;
+    const int rc = tiles_geometry(fmt, rows, cols, &ns, &nsl, &bytes);
+    if (rc != DQ_OK) return rc;
+    if (!d_packed || !d_tiles) return DQ_ERR_INVALID_ARG;
+    DqLayout L;
+    if (!dq_layout(fmt, rows, cols, &L)) return DQ_ERR_NOT_SUPPORTED;
+    const long units = nsl * ns * 64;
+    const unsigned grid = (unsigned)((units + 255) / 256);
+    const hipStream_t s = (hipStream_t)stream;
+    const uint8_t* w = (const uint8_t*)d_packed;
+    uint8_t* o = (uint8_t*)d_tiles;
+    switch (fmt) {
+    case DQ_FMT_Q4_K: gemm_tiles_pack_kernel<B_Q4K><<<grid, 256, 0, s>>>(w, L, (int)rows, ns, units, o); break;
+    case DQ_FMT_Q6_K: gemm_tiles_pack_kernel<B_Q6K><<<grid, 256, 0, s>>>(w, L, (int)rows, ns, units, o); break;
+    case DQ_FMT_Q8_0: gemm_tiles_pack_kernel<B_Q80><<<grid, 256, 0, s>>>(w, L, (int)rows, ns, units, o); break;
+    default: gemm_tiles_pack_kernel<B_Q40><<<grid, 256, 0, s>>>(w, L, (int)rows, ns, units, o); break;
+    }
+    return dq_launch_status();
+}
+
 // GEMM on the workspace written by dq_quantize_act_f16.
 extern "C" int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work,
                               size_t n_tok, float* d_y, void* stream) {
     return dq_gemm_f16act_zeroed(fmt, d_w, rows, cols, d_work, n_tok, d_y, false, stream);
 }
 
-int dq_gemm_f16act_zeroed(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work, size_t n_tok,
+int dq_gemm_f16act_zeroed(int fmt_in, const void* d_w, size_t rows, size_t cols, const void* d_work, size_t n_tok,
                           float* d_y, bool y_zeroed, void* stream, int cu_budget) {
     DqLayout L;
+    const bool tiled = (fmt_in & DQ_FMT_GEMM_TILES) != 0;
+    const int fmt = fmt_in & ~DQ_FMT_GEMM_TILES;
     if (fmt != DQ_FMT_Q4_K && fmt != DQ_FMT_Q6_K && fmt != DQ_FMT_Q8_0 && fmt != DQ_FMT_Q4_0)
         return DQ_ERR_NOT_SUPPORTED;
     if (!dq_layout(fmt, rows, cols, &L) || cols % 256) return DQ_ERR_NOT_SUPPORTED;
@@ -1162,17 +1303,27 @@ int dq_gemm_f16act_zeroed(int fmt, const void* d_w, size_t rows, size_t cols, co
     g.N = (int)rows;
     g.K = (int)cols;
     const int nsb = (int)cols / 256;  // super-blocks (cols % 256 == 0)
+    g.n_stages = (int)(cols / 64) / (fmt == DQ_FMT_Q6_K || fmt == DQ_FMT_Q8_0 ? 2 : 4);
+    if (tiled) {
+        switch (fmt) {
+        case DQ_FMT_Q4_K: return launch_plan<DQ_FMT_Q4_K, true>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+        case DQ_FMT_Q8_0: return launch_plan<DQ_FMT_Q8_0, true>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+        case DQ_FMT_Q4_0: return launch_plan<DQ_FMT_Q4_0, true>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+        default: return launch_plan<DQ_FMT_Q6_K, true>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+        }
+    }
     switch (fmt) {
-    case DQ_FMT_Q4_K: return launch_plan<DQ_FMT_Q4_K>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
-    case DQ_FMT_Q8_0: return launch_plan<DQ_FMT_Q8_0>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
-    case DQ_FMT_Q4_0: return launch_plan<DQ_FMT_Q4_0>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
-    default: return launch_plan<DQ_FMT_Q6_K>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+    case DQ_FMT_Q4_K: return launch_plan<DQ_FMT_Q4_K, false>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+    case DQ_FMT_Q8_0: return launch_plan<DQ_FMT_Q8_0, false>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+    case DQ_FMT_Q4_0: return launch_plan<DQ_FMT_Q4_0, false>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
+    default: return launch_plan<DQ_FMT_Q6_K, false>(g, rows, n_tok, nsb, d_y, y_zeroed, s, cu_budget);
     }
 }
 
 
-extern "C" int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,
+extern "C" int dq_gemm(int fmt_in, const void* d_w, size_t rows, size_t cols, const float* d_x, size_t n_tok,
                        float* d_y, void* d_work, size_t work_bytes, void* stream) {
+    const int fmt = fmt_in & ~DQ_FMT_GEMM_TILES;  // the activation side is the format's
     size_t need = 0;
     const int rc = dq_gemm_workspace_bytes(fmt, rows, cols, n_tok, &need);
     if (rc != DQ_OK) return rc;
@@ -1191,5 +1342,5 @@ extern "C" int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const
     }
     const int r1 = dq_quantize_act_f16_zero(fmt, d_x, cols, n_tok, d_work, z, stream);
     if (r1 != DQ_OK) return r1;
-    return dq_gemm_f16act_zeroed(fmt, d_w, rows, cols, d_work, n_tok, d_y, zero, stream);
+    return dq_gemm_f16act_zeroed(fmt_in, d_w, rows, cols, d_work, n_tok, d_y, zero, stream);
 }

@@ -880,7 +880,7 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
     const float *norm_a = nullptr, *norm_b = nullptr, *norm_w = nullptr;
     float* norm_h = nullptr;
     auto products = [&](const float* x, size_t cols, int n, const int* fmt, const void* const* wm, const size_t* rows,
-                        float* const* y) -> int {
+                        float* const* y, const void* const* tm) -> int {
         const int C = dq_gemm_cus();
         int budget[4] = {0, 0, 0, 0};
         SideStreams* ss = nullptr;
@@ -980,8 +980,9 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         for (int j = 0; j < n; ++j) {
             const hipStream_t js = lane[j] < 0 ? s : ss->st[lane[j]];
             if (!done[cls(fmt[j])]) DQP_TRY(quantize(j, js));
-            DQP_TRY(dq_gemm_f16act_zeroed(fmt[j], wm[j], rows[j], cols, gw(fmt[j]), T, y[j], zeroed[j], js,
-                                          budget[j]));
+            // the matrix's tile copy where the layer has one (same results)
+            DQP_TRY(dq_gemm_f16act_zeroed(tm[j] ? (fmt[j] | DQ_FMT_GEMM_TILES) : fmt[j], tm[j] ? tm[j] : wm[j],
+                                          rows[j], cols, gw(fmt[j]), T, y[j], zeroed[j], js, budget[j]));
         }
         for (int i = 0; i < n_side; ++i) {
             if (hipEventRecord(ss->join[i], ss->st[i]) != hipSuccess) return DQ_ERR_IO;
@@ -999,7 +1000,8 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         const void* m[4] = {L->wq, L->wk, L->wv, L->wag};
         const size_t r[4] = {QD, KVD, KVD, L->n_head};
         float* const y[4] = {w.q, w.k, w.v, w.ag};
-        DQP_TRY(products(w.xn, E, L->wag ? 4 : 3, f, m, r, y));
+        const void* t[4] = {L->tq, L->tk, L->tv, L->tag};
+        DQP_TRY(products(w.xn, E, L->wag ? 4 : 3, f, m, r, y, t));
     }
     norm_w = nullptr;
     DQP_TRY(dq_rope_kv_write_batch_post(w.q, w.k, w.v, QD, KVD, d_rope, L->n_rot, n_tok, L->n_head, L->n_head_kv,
@@ -1015,7 +1017,8 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         const void* m[1] = {L->wo};
         const size_t r[1] = {E};
         float* const y[1] = {w.down};
-        DQP_TRY(products(w.attn, QD, 1, f, m, r, y));
+        const void* t[1] = {L->to};
+        DQP_TRY(products(w.attn, QD, 1, f, m, r, y, t));
     }
     // residual + FFN norm (:3539-3560), gated FFN (:3600-3624)
     if (L->post_attn_norm) {  // sandwich norm of the projection before the residual
@@ -1032,7 +1035,8 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         const void* m[2] = {L->wup, L->wgate};
         const size_t r[2] = {F, F};
         float* const y[2] = {w.up, w.gate};
-        DQP_TRY(products(w.xn, E, 2, f, m, r, y));
+        const void* t[2] = {L->tup, L->tgate};
+        DQP_TRY(products(w.xn, E, 2, f, m, r, y, t));
     }
     norm_w = nullptr;
     // the batch branch's activation, silu or gelu_tanh per element
@@ -1045,7 +1049,8 @@ int dq_layer_prefill(const dq_layer_t* L, const float* d_x, float* d_x_out, cons
         const void* m[1] = {L->wdown};
         const size_t r[1] = {E};
         float* const y[1] = {w.down};
-        DQP_TRY(products(w.up, F, 1, f, m, r, y));
+        const void* t[1] = {L->tdown};
+        DQP_TRY(products(w.up, F, 1, f, m, r, y, t));
     }
     const size_t ne4 = T * E / 4;
     if (L->post_ffn_norm)  // sandwich norm of the FFN output before the residual

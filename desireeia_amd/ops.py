@@ -216,6 +216,26 @@ def gemm_workspace(mat, n_tok):
     return torch.empty(max(n.value, 1), dtype=torch.uint8, device=mat.buf.device)
 
 
+GEMM_TILES = 0x200
+
+
+class GemmTiles:
+    """The opt-in tile copy of a matrix for the prefill GEMM
+    (dq_gemm_tiles_pack): each 64-row slice's bytes of one GEMM stage in one
+    contiguous run. Passed to gemm() in place of the QuantMatrix; results are
+    bit-identical. The packed matrix stays what the decode GEMV reads."""
+
+    def __init__(self, mat):
+        lib = _lib.load()
+        n = ctypes.c_size_t(0)
+        _lib.check(lib.dq_gemm_tiles_bytes(mat.fmt, mat.rows, mat.cols, ctypes.byref(n)), "dq_gemm_tiles_bytes")
+        self.buf = torch.empty(n.value, dtype=torch.uint8, device=mat.buf.device)
+        _lib.check(lib.dq_gemm_tiles_pack(mat.fmt, _ptr(mat.buf), mat.rows, mat.cols, _ptr(self.buf), _stream()),
+                   "dq_gemm_tiles_pack")
+        self.fmt = mat.fmt | GEMM_TILES
+        self.rows, self.cols = mat.rows, mat.cols
+
+
 def gemm(mat, x, out=None, work=None):
     """Y[n_tok][rows] = X W^T with the semantics of matmul_<fmt>_batch (n_tok >= 4),
     reference core/matmul.cpp:2090-2125."""
@@ -388,7 +408,10 @@ class LayerDesc(ctypes.Structure):
                 ("bq", ctypes.c_void_p), ("bk", ctypes.c_void_p), ("bv", ctypes.c_void_p),
                 ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p), ("act_gelu", ctypes.c_int),
                 ("post_attn_norm", ctypes.c_void_p), ("post_ffn_norm", ctypes.c_void_p),
-                ("wag", ctypes.c_void_p), ("fmt_ag", ctypes.c_int)]
+                ("wag", ctypes.c_void_p), ("fmt_ag", ctypes.c_int),
+                ("tq", ctypes.c_void_p), ("tk", ctypes.c_void_p), ("tv", ctypes.c_void_p), ("to", ctypes.c_void_p),
+                ("tgate", ctypes.c_void_p), ("tup", ctypes.c_void_p), ("tdown", ctypes.c_void_p),
+                ("tag", ctypes.c_void_p)]
 
 
 def rope_cache(n_rot, pos, theta):
@@ -446,6 +469,17 @@ class DecoderLayer:
         _lib.check(lib.dq_layer_workspace_bytes(ctypes.byref(d), n_ctx, ctypes.byref(n)), "dq_layer_workspace_bytes")
         self.work = torch.empty(max(n.value, 1), dtype=torch.uint8, device=device)
         self.rope = torch.empty(self.n_rot, dtype=torch.float32, device=device)
+
+    def use_gemm_tiles(self):
+        """Gives the prefill layer tile copies of the matrices (GemmTiles):
+        the weights are then held twice; the decode layer is unchanged."""
+        self.tiles = {nm: GemmTiles(self.mats[nm]) for nm in self.NAMES}
+        for nm in self.NAMES:
+            setattr(self.desc, "t" + nm, self.tiles[nm].buf.data_ptr())
+        if self.attn_gate is not None:
+            self.tiles["ag"] = GemmTiles(self.attn_gate)
+            self.desc.tag = self.tiles["ag"].buf.data_ptr()
+        return self
 
     def set_rope(self, pos):
         self.rope.copy_(rope_cache(self.n_rot, pos, self.rope_theta))

@@ -38,6 +38,9 @@ extern "C" {
 #define DQ_FMT_Q4_0 1
 #define DQ_FMT_Q4_K 5
 #define DQ_FMT_Q6_K 7
+/* Flag on a prefill-GEMM format (dq_gemm, dq_gemm_f16act, dq_gemm_workspace_bytes): the weights are the
+ * tile copy of dq_gemm_tiles_pack, not the packed rows. */
+#define DQ_FMT_GEMM_TILES 0x200
 /* Q4_K experts in the expert-tile layout of dq_moe_tiles_pack (dq_moe_t only). */
 #define DQ_FMT_Q4_K_TILES 0x105
 
@@ -158,6 +161,20 @@ int dq_gemm(int fmt, const void* d_w, size_t rows, size_t cols, const float* d_x
 int dq_quantize_act_f16(int fmt, const float* d_x, size_t cols, size_t n_tok, void* d_work, void* stream);
 int dq_gemm_f16act(int fmt, const void* d_w, size_t rows, size_t cols, const void* d_work, size_t n_tok,
                    float* d_y, void* stream);
+/* An opt-in second copy of a matrix for prefill-heavy use: the tile layout
+ * in which every 64-row slice's bytes of one GEMM stage (the quant
+ * sub-planes in the kernel's LDS order, then the stage's scales) are one
+ * contiguous run, so each weight DMA of the GEMM reads 64 lanes x 16
+ * consecutive bytes instead of 4 lanes per 64-byte row piece. d_packed is
+ * the packed form of cuda_upload_weights / dq_weights_pack; d_tiles receives
+ * dq_gemm_tiles_bytes() bytes (rows rounded up to 256). Pass
+ * fmt | DQ_FMT_GEMM_TILES and the tile copy to dq_gemm / dq_gemm_f16act:
+ * the results are bit-identical to the packed rows'. The packed rows stay
+ * what the decode GEMV reads, so a matrix with both forms holds its weights
+ * twice. No counterpart in the reference (its prefill reads the GGUF
+ * blocks). */
+int dq_gemm_tiles_bytes(int fmt, size_t rows, size_t cols, size_t* bytes);
+int dq_gemm_tiles_pack(int fmt, const void* d_packed, size_t rows, size_t cols, void* d_tiles, void* stream);
 
 /* Q8_0 KV cache of one layer, laid out [pos][kv_head][hd/32 blocks of 34 B]
  * (models/dense_forward.cpp:2425, :4038-4043). dq_kv_write replaces
@@ -348,6 +365,9 @@ typedef struct {
     const float *post_attn_norm, *post_ffn_norm; /* device [n_embd], optional (NULL): sandwich norms */
     const void* wag; /* optional (NULL) per-head attention output gate [n_head][n_embd], packed, format fmt_ag */
     int fmt_ag;
+    /* optional (NULL) tile copies (dq_gemm_tiles_pack) of wq .. wdown and wag: the prefill layer's GEMMs read
+     * them instead of the packed rows, with the same results; the decode layer ignores them */
+    const void *tq, *tk, *tv, *to, *tgate, *tup, *tdown, *tag;
 } dq_layer_t;
 
 int dq_layer_workspace_bytes(const dq_layer_t* layer, uint32_t n_ctx, size_t* bytes);

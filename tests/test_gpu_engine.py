@@ -160,6 +160,27 @@ def test_batch(lib, orc, qtype, rows, cols, n_tok):
     m.free()
 
 
+@pytest.mark.parametrize("qtype,rows,cols,n_tok", [(Q4_K, 14336, 4096, 64), (Q6_K, 4096, 14336, 16),
+                                                   (Q8_0, 1000, 1024, 32), (Q4_0, 300, 512, 8)])
+def test_batch_gemm_tiles(lib, qtype, rows, cols, n_tok, monkeypatch):
+    """With DESIREEIA_GEMM_TILES=1 an upload also keeps the prefill GEMM's tile
+    copy, which matmul_kquant_cuda_batch then reads: the same numbers as the
+    packed rows."""
+    print(f"batch tiles type={qtype} {rows}x{cols} n_tok={n_tok}", flush=True)
+    x = synth.gen_act((n_tok, cols), seed=18)
+    m = Mat(lib, qtype, rows, cols, seed=17)
+    monkeypatch.setenv("DESIREEIA_GEMM_TILES", "1")
+    mt = Mat(lib, qtype, rows, cols, seed=17)
+    monkeypatch.delenv("DESIREEIA_GEMM_TILES")
+    ya = np.full((n_tok, rows), np.nan, np.float32)
+    yb = np.full((n_tok, rows), np.nan, np.float32)
+    assert lib.matmul_kquant_cuda_batch(m.fmt, m.qs, rows, cols, P(x), n_tok, P(ya)) == OK
+    assert lib.matmul_kquant_cuda_batch(mt.fmt, mt.qs, rows, cols, P(x), n_tok, P(yb)) == OK
+    assert np.array_equal(ya, yb)
+    m.free()
+    mt.free()
+
+
 def test_batch_not_supported(lib):
     # K not a multiple of 256 (the prefill GEMM's step): NOT_SUPPORTED, y untouched
     m = Mat(lib, Q4_0, 64, 320, seed=1)
@@ -734,6 +755,37 @@ def test_layer_forward_batch(lib, orc):
         for m in L[0].values():
             m.free()
     lib.cuda_kv_cache_release()
+
+
+def test_layer_forward_batch_tiles(lib, orc, monkeypatch):
+    """cuda_layer_forward_batch on matrices uploaded with their tile copies
+    (DESIREEIA_GEMM_TILES=1) gives exactly the output and cache rows of the
+    same matrices uploaded without them."""
+    E, n_head, n_kv, F, n_ctx, prior, T = 512, 8, 2, 1024, 128, 20, 60
+    hd = 128
+    kc, vc, pb = prior_cache(orc, 1, n_ctx, n_kv, hd, prior, seed=61)
+    t = (Q4_K, Q4_K, Q6_K, Q4_K, Q4_K, Q4_K, Q6_K)
+    x = np.random.default_rng(62).standard_normal((T, E)).astype(np.float32)
+    rope = np.stack([orc.rope_cache(hd, prior + i, 500000.0) for i in range(T)])
+    outs = []
+    for tiles in (False, True):
+        if tiles:
+            monkeypatch.setenv("DESIREEIA_GEMM_TILES", "1")
+        mats, an, fn, _ = make_layer(lib, orc, E, n_head, n_kv, F, t, 70)
+        monkeypatch.delenv("DESIREEIA_GEMM_TILES", raising=False)
+        an *= 0.25 / np.sqrt(E)
+        fn *= 0.3 / np.sqrt(E)
+        assert lib.cuda_kv_cache_reserve(kc.size)
+        assert lib.cuda_kv_cache_upload(P(kc), P(vc), kc.size)
+        out = np.full((T, E), np.nan, np.float32)
+        hk, hv = kc.copy(), vc.copy()
+        A = batch_args(mats, an, fn, E, n_head, n_kv, F, 0, prior, T, 0, T, rope, x, out, hk, hv, 1, 1, 1)
+        assert lib.cuda_layer_forward_batch(ctypes.byref(A)) == OK
+        outs.append((out, hk, hv))
+        for m in mats.values():
+            m.free()
+    assert np.array_equal(outs[0][0], outs[1][0])
+    assert np.array_equal(outs[0][1], outs[1][1]) and np.array_equal(outs[0][2], outs[1][2])
 
 
 @pytest.mark.parametrize("gelu,sandwich,gate", [(False, False, False), (True, False, False), (True, True, False),

@@ -255,3 +255,38 @@ def test_gemm_in_place(gpu, qtype, n, n_tok):
     yv = big[n // 2:].view(n_tok, n)
     ops.gemm(m, xv, out=yv)
     assert torch.equal(yv, want)
+
+
+@pytest.mark.parametrize("qtype,rows,cols,n_tok", [
+    (synth.Q4_K, 14336, 4096, 512),   # config 3 shapes: 4x1 tiles
+    (synth.Q6_K, 4096, 14336, 512),   # 2x2 tiles with the K split
+    (synth.Q8_0, 14336, 4096, 512),
+    (synth.Q4_0, 4096, 14336, 512),
+    (synth.Q4_K, 300, 512, 37),       # ragged: rows past the matrix in the last tile
+    (synth.Q6_K, 1000, 768, 130),
+    (synth.Q8_0, 65, 256, 8),
+    (synth.Q4_0, 513, 1024, 300),
+])
+def test_gemm_tiles_match_rows(gpu, qtype, rows, cols, n_tok):
+    """The tile copy (dq_gemm_tiles_pack, DQ_FMT_GEMM_TILES) gives exactly the
+    packed rows' result: the same bytes reach the same LDS slots."""
+    print(f"gemm tiles type={qtype} rows={rows} cols={cols} n_tok={n_tok}", flush=True)
+    w = synth.gen_weights(qtype, rows, cols, seed=rows + cols)
+    x = torch.from_numpy(synth.gen_act((n_tok, cols), seed=n_tok)).to(gpu)
+    m = ops.QuantMatrix.from_gguf(qtype, w, rows, cols)
+    t = ops.GemmTiles(m)
+    a = ops.gemm(m, x).cpu().numpy()
+    b = ops.gemm(t, x).cpu().numpy()
+    assert np.array_equal(a, b)
+
+
+def test_gemm_tiles_sizes(gpu):
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    # whole 256-row tiles: 300 rows of Q4_K at 512 columns = 2 tiles x 4 slices x 2 stages x 9 KB
+    assert lib.dq_gemm_tiles_bytes(synth.FMT_Q4_K, 300, 512, ctypes.byref(n)) == 0
+    assert n.value == 2 * 4 * 2 * (2 * 4096 + 1024)
+    assert lib.dq_gemm_tiles_bytes(synth.FMT_Q6_K, 256, 768, ctypes.byref(n)) == 0
+    assert n.value == 4 * 6 * (3 * 2048 + 768)
+    assert lib.dq_gemm_tiles_bytes(synth.FMT_Q4_K, 300, 500, ctypes.byref(n)) == -2
+    assert lib.dq_gemm_tiles_bytes(9, 300, 512, ctypes.byref(n)) == -2

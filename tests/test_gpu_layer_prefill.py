@@ -216,6 +216,28 @@ def test_layer_prefill_chunks(gpu, orc):
     assert np.array_equal(w1, w2) and np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
 
 
+@pytest.mark.parametrize("E,n_head,n_kv,F,pos0,n_tok,types,attn_gate", [
+    (4096, 32, 8, 14336, 3584, 512, None, False),   # config 4's layer over a 512-token chunk (Q4_K_M mix)
+    (512, 8, 2, 1536, 70, 100, {"q": synth.Q8_0, "k": synth.Q4_0, "v": synth.Q8_0, "o": synth.Q4_0,
+                                 "gate": synth.Q8_0, "up": synth.Q8_0, "down": synth.Q4_0}, True),  # per-32 formats, gate
+])
+def test_layer_prefill_tiles(gpu, orc, E, n_head, n_kv, F, pos0, n_tok, types, attn_gate):
+    """The prefill layer on tile copies of its matrices (dq_layer_t tq ..
+    tdown, tag) gives exactly the output and cache of the packed rows."""
+    print(f"prefill tiles E={E} n_tok={n_tok} types={types}", flush=True)
+    n_ctx = pos0 + n_tok
+    la, _, _, _, _ = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos0, seed=51, norm_scale=conditioned(E),
+                                types=types, attn_gate=attn_gate)
+    lb, _, _, _, _ = make_layer(gpu, orc, E, n_head, n_kv, F, n_ctx, pos0, seed=51, norm_scale=conditioned(E),
+                                types=types, attn_gate=attn_gate)
+    lb.use_gemm_tiles()
+    x = torch.from_numpy(np.random.default_rng(52).standard_normal((n_tok, E)).astype(np.float32)).to(gpu)
+    ya = la.prefill(x, pos0).cpu().numpy()
+    yb = lb.prefill(x, pos0).cpu().numpy()
+    assert np.array_equal(ya, yb)
+    assert torch.equal(la.cache.k, lb.cache.k) and torch.equal(la.cache.v, lb.cache.v)
+
+
 def test_decode_after_prefill(gpu, orc):
     """A 48-token prompt through dq_layer_prefill, then one decode step
     (dq_layer_decode) on the cache it left: the oracle's decode step on that
