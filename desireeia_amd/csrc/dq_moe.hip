@@ -392,8 +392,8 @@ struct ASrc {
 };
 __device__ __forceinline__ ASrc a_sources(const _Float16* A, const _Float16* minp, int K, int c, int p_end, int tid) {
     ASrc s;
-    // the block sums of pair lane % 32 (contiguous over the pairs; every wave
-    // loads the same slots)
+    // the block sums of pair lane % 32 (contiguous over the pairs; wave 0
+    // loads them, issue_a)
     s.m = minp + (size_t)min(c + (tid & 31), p_end - 1) * 8;
 #pragma unroll
     for (int j = 0; j < A_LOADS; ++j) {
@@ -404,10 +404,22 @@ __device__ __forceinline__ ASrc a_sources(const _Float16* A, const _Float16* min
     }
     return s;
 }
-__device__ __forceinline__ void issue_a(const ASrc& s, int n_pairs, int st, uint8_t* dst, int tid) {
-    __builtin_amdgcn_global_load_lds(s.m + (size_t)st * n_pairs * 8, DQ_LDS_PTR(dst + A_MAIN_BYTES), 16, 0, 0);
+// Only the instructions that carry one of the pass's n_tok tokens are issued
+// (instruction j of wave w holds tokens 8j + 2w and 8j + 2w + 1): an expert
+// with 16 tokens reads half the tile. The slots of the tokens past n_tok keep
+// stale bytes; they feed only MFMA output columns that are never stored.
+// (The activation rows, re-read from L2 by every row tile of the expert, cost
+// as much DMA as the weights at 32 rows: with them removed the weights stream
+// at the device's plain read rate.)
+// The block sums (one 1 KB instruction) are loaded by wave 0 alone: every
+// wave waits for its own DMAs before the step's barrier.
+__device__ __forceinline__ void issue_a(const ASrc& s, int n_pairs, int st, uint8_t* dst, int tid, int n_tok) {
+    const int w2 = 2 * __builtin_amdgcn_readfirstlane(tid >> 6);
+    if (w2 == 0)
+        __builtin_amdgcn_global_load_lds(s.m + (size_t)st * n_pairs * 8, DQ_LDS_PTR(dst + A_MAIN_BYTES), 16, 0, 0);
 #pragma unroll
     for (int j = 0; j < A_LOADS; ++j) {
+        if (8 * j + w2 >= n_tok) break;  // wave-uniform
         uint8_t* base = dst + (size_t)(j * 64 * WAVES + (tid & ~63)) * 16;  // wave-uniform
         __builtin_amdgcn_global_load_lds(s.a[j] + 256 * (size_t)st, DQ_LDS_PTR(base), 16, 0, 0);
     }
@@ -564,8 +576,9 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         for (int r = 0; r < 16; ++r) acc[r] = acc1[r] = 0.0f;
         {
             const ASrc as = a_sources(G.A, G.minp, G.K, c, p_end, tid);
+            const int n_tok = min(TT, p_end - c);  // the pass's tokens
             // prologue: the first step in flight
-            issue_a(as, G.n_pairs, s0, aring[0], tid);
+            issue_a(as, G.n_pairs, s0, aring[0], tid, n_tok);
             if constexpr (TILED) issue_w_tiles(base + (chunk0 + s0) * WT_BYTES, wring[0], tid);
             else issue_w(base, L, row0, nrows, s0, wring[0], tid);
             // one main step from ring stage S = (st - s0) % 2, a constant in
@@ -576,7 +589,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
                 wait_vm<0>();      // this step's DMAs, the only ones outstanding, have landed
                 dq_lds_barrier();  // ... in every wave; stage 1 - S is free
                 if (st + 1 < main_end) {
-                    issue_a(as, G.n_pairs, st + 1, aring[1 - S], tid);
+                    issue_a(as, G.n_pairs, st + 1, aring[1 - S], tid, n_tok);
                     if constexpr (TILED) issue_w_tiles(base + (chunk0 + st + 1) * WT_BYTES, wring[1 - S], tid);
                     else issue_w(base, L, row0, nrows, st + 1, wring[1 - S], tid);
                 }
