@@ -12,8 +12,8 @@
  * 2. Engine layer: the GPU operator entry points the reference engine's model
  *    code calls (core/engine.h:502-811, compiled there under
  *    DESIREEIA_CUDA_ENABLED), same names, argument meaning and error
- *    behaviour, with host pointers for x/y and one synchronisation per call.
- *    See INTEGRATION.md for the C++ shim the engine would link.
+ *    behaviour, with host pointers for x/y and one synchronisation per call;
+ *    a thin C++ shim maps the engine's calls (references, std types) onto them.
  */
 #ifndef DESIREEIA_HIP_H
 #define DESIREEIA_HIP_H
@@ -520,7 +520,7 @@ int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint3
  *   - one process-global stream, scratch that grows on demand and one device
  *     KV cache; not thread-safe (as the reference backend).
  * Where the reference passes a C++ reference (a struct or an out-parameter),
- * the C ABI takes a pointer; INTEGRATION.md gives the one-line C++ overloads.
+ * the C ABI takes a pointer (a one-line C++ overload restores the reference form).
  * Arithmetic follows the reference CPU functions the engine would otherwise
  * run (matmul_q8_0 / q4_0 / q4_k / q6_k, their _batch forms, the dense
  * layer); the format ids are those of the reference (0 = Q8_0, 1 = Q4_0,
