@@ -229,68 +229,57 @@ __global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ 
     if (b == 0 && lane == 0) inv[p] = 1.0f / sc;  // the output factor
 }
 
-// The down projection's activation row of pair p in one workgroup: h =
-// silu(g) * u (models/dense_forward.cpp:53-55) with g, u the sums over the K
-// splits of the gate and up outputs (split order 0, 1, ...), its range scale
-// (row_scale_of), and the per-256 quantization as moe_act_kernel writes it.
-// SILU_WAVES waves, wave w takes the 256-blocks w, w + SILU_WAVES, ...; h
-// stays in registers (F <= SILU_WAVES * SILU_J * 256).
-constexpr int SILU_WAVES = 16, SILU_J = 4;  // n_ff <= 16384
-__global__ __launch_bounds__(64 * SILU_WAVES) void moe_silu_act_kernel(const float* __restrict__ gate,
-                                                                       const float* __restrict__ up, int nsplit,
-                                                                       size_t split_stride, int F, int n_rows,
-                                                                       _Float16* __restrict__ A,
-                                                                       _Float16* __restrict__ minp,
-                                                                       float* __restrict__ inv) {
-    __shared__ float wmax[SILU_WAVES];
-    const int p = blockIdx.x;
+// The down projection's activation of pair p over the K range of the down
+// GEMM's split q (its super-blocks [q * sps, min((q + 1) * sps, F / 256))),
+// one workgroup of 4 waves per (pair, split): h = silu(g) * u
+// (models/dense_forward.cpp:53-55) with g, u the sums over the K splits of
+// the gate and up outputs (split order 0, 1, ...), the range scale s of that
+// range (row_scale_of its max |h|) and the per-256 quantization as
+// moe_act_kernel writes it; inv[q * n_rows + p] = 1/s. A range scale per
+// split is exact: the GEMM undoes each split's s on that split's partial
+// (powers of two, fp16 and fp32 alike), and the per-256 integers and scales
+// do not depend on s. Wave w takes the 256-blocks w, w + 4, ... of the range:
+// a first pass finds the maximum, a second recomputes h (its loads hit L2)
+// and quantizes it.
+__global__ __launch_bounds__(256) void moe_silu_act_kernel(const float* __restrict__ gate, const float* __restrict__ up,
+                                                           int nsplit, size_t split_stride, int F, int n_rows,
+                                                           int n_dsplit, int sps, _Float16* __restrict__ A,
+                                                           _Float16* __restrict__ minp, float* __restrict__ inv) {
+    __shared__ float wmax[4];
+    const int p = blockIdx.x / n_dsplit, q = blockIdx.x % n_dsplit;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nblk = F / 256;
-    float4 g[SILU_J], u[SILU_J];
-    // every load of the row issued before the first use
-#pragma unroll
-    for (int j = 0; j < SILU_J; ++j) {
-        const int b = wave + SILU_WAVES * j;
-        const size_t o = (size_t)p * F + 256 * (size_t)min(b, nblk - 1) + 4 * lane;
-        g[j] = *reinterpret_cast<const float4*>(gate + o);
-        u[j] = *reinterpret_cast<const float4*>(up + o);
-    }
-    for (int s = 1; s < nsplit; ++s) {
-#pragma unroll
-        for (int j = 0; j < SILU_J; ++j) {
-            const int b = wave + SILU_WAVES * j;
-            const size_t o = s * split_stride + (size_t)p * F + 256 * (size_t)min(b, nblk - 1) + 4 * lane;
-            const float4 g2 = *reinterpret_cast<const float4*>(gate + o);
-            const float4 u2 = *reinterpret_cast<const float4*>(up + o);
-            g[j].x += g2.x, g[j].y += g2.y, g[j].z += g2.z, g[j].w += g2.w;
-            u[j].x += u2.x, u[j].y += u2.y, u[j].z += u2.z, u[j].w += u2.w;
+    const int b0 = q * sps, b1 = min(b0 + sps, F / 256);
+    auto h_of = [&](int b, float (&h)[4]) {
+        const size_t o = (size_t)p * F + 256 * (size_t)b + 4 * lane;
+        float4 g = *reinterpret_cast<const float4*>(gate + o);
+        float4 u = *reinterpret_cast<const float4*>(up + o);
+        for (int s = 1; s < nsplit; ++s) {
+            const float4 g2 = *reinterpret_cast<const float4*>(gate + s * split_stride + o);
+            const float4 u2 = *reinterpret_cast<const float4*>(up + s * split_stride + o);
+            g.x += g2.x, g.y += g2.y, g.z += g2.z, g.w += g2.w;
+            u.x += u2.x, u.y += u2.y, u.z += u2.z, u.w += u2.w;
         }
-    }
-    float h[SILU_J][4];
+        const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) h[i] = gv[i] / (1.0f + expf(-gv[i])) * uv[i];
+    };
     float mx = 0.0f;
-#pragma unroll
-    for (int j = 0; j < SILU_J; ++j) {
-        const float gv[4] = {g[j].x, g[j].y, g[j].z, g[j].w}, uv[4] = {u[j].x, u[j].y, u[j].z, u[j].w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            h[j][i] = gv[i] / (1.0f + expf(-gv[i])) * uv[i];
-            if (wave + SILU_WAVES * j < nblk) mx = fmaxf(mx, fabsf(h[j][i]));
-        }
+    for (int b = b0 + wave; b < b1; b += 4) {
+        float h[4];
+        h_of(b, h);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3]))));
     }
     mx = dq_wave_max(mx);
     if (lane == 0) wmax[wave] = mx;
     __syncthreads();
-    float r = wmax[0];
-#pragma unroll
-    for (int w = 1; w < SILU_WAVES; ++w) r = fmaxf(r, wmax[w]);
-    const float sc = row_scale_of(r);
+    const float sc = row_scale_of(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
     _Float16* row = A + (size_t)p * F;
-#pragma unroll
-    for (int j = 0; j < SILU_J; ++j) {
-        const int b = wave + SILU_WAVES * j;
-        if (b < nblk) quant_256_block(h[j], sc, lane, b, p, n_rows, row, minp);
+    for (int b = b0 + wave; b < b1; b += 4) {
+        float h[4];
+        h_of(b, h);
+        quant_256_block(h, sc, lane, b, p, n_rows, row, minp);
     }
-    if (threadIdx.x == 0) inv[p] = 1.0f / sc;
+    if (threadIdx.x == 0) inv[(size_t)q * n_rows + p] = 1.0f / sc;
 }
 
 // ------------------------------------------------------------ expert GEMM --
@@ -300,7 +289,7 @@ struct MoeGemm {
     float* y[2];          // outputs [nsplit][n_pairs][rows]
     const _Float16* A;    // activation rows [n_pairs][K]
     const _Float16* minp; // their block sums [K/256][n_pairs][8]
-    const float* inv;     // per pair: 1/s of its activation row
+    const float* inv;     // [nsplit][n_pairs]: 1/s of each pair's activation over each split's K range
     const int32_t* offsets;
     int rows, K, n_pairs, nsplit, steps_per_split, main_steps;
     int n_exp, n_tiles;
@@ -565,6 +554,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     const uint8_t* base = G.w[mat];
     const DqLayout L = G.L[mat];
     float* __restrict__ y = G.y[mat] + (size_t)split * G.n_pairs * G.rows;
+    const float* __restrict__ inv_s = G.inv + (size_t)split * G.n_pairs;  // the split's factors
     const int s0 = split * G.steps_per_split;
     const int main_end = min(G.main_steps, s0 + G.steps_per_split);
     if (s0 >= main_end) return;  // uniform
@@ -637,7 +627,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
         // load inside the store's branch would be waited for one at a time).
         float inv[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) inv[r] = G.inv[min(c + (r >> 2) * 8 + h * 4 + (r & 3), p_end - 1)];
+        for (int r = 0; r < 16; ++r) inv[r] = inv_s[min(c + (r >> 2) * 8 + h * 4 + (r & 3), p_end - 1)];
         if (row_ok) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -716,7 +706,7 @@ MoeWs carve(const dq_moe_t* m, uint32_t n_tok, int split_gu, int split_d, uint8_
     w.slot_pos = (int32_t*)take(n_ent * 4);
     w.xscale = (float*)take((size_t)n_tok * 4);
     w.inv_in = (float*)take(n_ent * 4);
-    w.inv_h = (float*)take(n_ent * 4);
+    w.inv_h = (float*)take((size_t)split_d * n_ent * 4);
     w.a_in = (_Float16*)take(n_ent * E * 2);
     w.min_in = (_Float16*)take(n_ent * (E / 32) * 2);
     w.gate = (float*)take((size_t)split_gu * n_ent * F * 4);
@@ -733,7 +723,7 @@ bool moe_ok(const dq_moe_t* m) {
     if (m->n_expert == 0 || m->n_expert > MOE_MAX_EXPERT) return false;
     if (m->n_expert_used == 0 || m->n_expert_used > MOE_MAX_K || m->n_expert_used > m->n_expert) return false;
     if (m->n_embd == 0 || m->n_embd % 256 || m->n_ff == 0 || m->n_ff % 256) return false;
-    if (m->n_embd > (1u << 20) || m->n_ff > 256u * SILU_WAVES * SILU_J) return false;
+    if (m->n_embd > (1u << 20) || m->n_ff > (1u << 20)) return false;
     if ((size_t)m->n_expert * m->n_ff > 0x3FFFFFFF || (size_t)m->n_expert * m->n_embd > 0x3FFFFFFF) return false;
     return true;
 }
@@ -864,8 +854,11 @@ int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint3
                        w.inv_in,
                        w.offsets, n_ent, sgu, w.gate, w.up, s));
     // h = silu(gate) * up, quantized for the down projection
-    moe_silu_act_kernel<<<n_ent, 64 * SILU_WAVES, 0, s>>>(w.gate, w.up, sgu, (size_t)n_ent * F, F, n_ent, w.a_h,
-                                                          w.min_h, w.inv_h);
+    {
+        const int sps = (F / 256 + sd - 1) / sd;  // the down GEMM's super-blocks per split (launch_gemm)
+        moe_silu_act_kernel<<<(unsigned)((size_t)n_ent * sd), 256, 0, s>>>(
+            w.gate, w.up, sgu, (size_t)n_ent * F, F, n_ent, sd, sps, w.a_h, w.min_h, w.inv_h);
+    }
     DQ_TRY(dq_launch_status());
     DQ_TRY(launch_gemm(tiled, (const uint8_t*)m->wdown, nullptr, 1, n_exp, E, F, w.a_h, w.min_h, w.inv_h, w.offsets,
                        n_ent,

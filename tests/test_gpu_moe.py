@@ -66,6 +66,7 @@ def moe_oracle_all(orc, ws, n_exp, E, F, x, lg, n_tok, k, threads=8):
     (5, 8, 2, 512, 768, False),       # most experts get no token
     (300, 4, 2, 256, 512, True),      # one expert gets > 128 tokens (several passes)
     (1, 2, 2, 256, 256, False),       # one token, every expert
+    (4, 4, 2, 256, 16640, False),     # n_ff past 16384 (65 super-blocks over 8 uneven down splits)
 ])
 def test_moe_ffn(gpu, orc, n_tok, n_exp, k, E, F, skew):
     print(f"moe n_tok={n_tok} experts={n_exp} k={k} E={E} F={F}", flush=True)
