@@ -14,13 +14,14 @@
 // Design: the reference CPU path re-streams every expert's weights once per
 // token. Here the tokens routed to an expert are gathered into one list, and
 // each weight byte is read from HBM once for all of them:
-//  * routing: one wave per token, lane = expert (the token's activation range
-//    scale computed alongside);
+//  * routing: one wave per token, lane = expert;
 //  * lists: expert-major, ascending (token, slot) order (deterministic), by
-//    wave ballots in one workgroup;
-//  * activation rows per (token, expert) pair: the per-256 integers and scale
-//    of the reference, entered into the MFMA as fp16(q * d * s) (s a
-//    power-of-two range scale undone on the output), plus the 8 block sums
+//    wave ballots in one workgroup (the same workgroup as the routing, for
+//    up to 1024 tokens);
+//  * activation rows per (token, expert) pair, one workgroup per pair: the
+//    per-256 integers and scale of the reference, entered into the MFMA as
+//    fp16(q * d * s) (s a power-of-two range scale of the row, undone on the
+//    output), plus the 8 block sums
 //    fp16(d * isum_j * s) per super-block in a plane with the pairs
 //    contiguous, which carry the Q4_K min term as one extra 16-wide MFMA
 //    slice per super-block against fp16(-dmin * m_j);
@@ -52,54 +53,36 @@ constexpr int WAVES = 4;       // waves per workgroup, 32 weight rows each
 constexpr int NSTAGE = 2;      // LDS ring stages (one step in flight while one computes)
 
 // ---------------------------------------------------------------- routing --
-// One wave per token, lane e = expert e. The max is order-independent; the
-// double sum runs sequentially over the experts as the reference's loop does.
-__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int n_tok, int n_exp,
-                                                        int k, int norm_w, float w_scale, int32_t* __restrict__ ids,
-                                                        float* __restrict__ wts, const float* __restrict__ x,
-                                                        int E, float* __restrict__ xscale) {
-    const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= n_tok) return;  // uniform per wave
-    if (x) {
-        // the range scale of the token's activation row (row_scale_of)
-        float mx = 0.0f;
-        for (int c0 = 0; c0 < E; c0 += 16 * 256) {
-            // unconditional loads (clamped addresses) so all 16 are in flight at once
-            float4 f[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-                f[j] = *reinterpret_cast<const float4*>(x + (size_t)t * E + min(c0 + 256 * j + 4 * lane, E - 4));
-#pragma unroll
-            for (int j = 0; j < 16; ++j)
-                if (c0 + 256 * j + 4 * lane < E)
-                    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f[j].x), fabsf(f[j].y)), fmaxf(fabsf(f[j].z), fabsf(f[j].w))));
-        }
-        mx = dq_wave_max(mx);
-        if (lane == 0) xscale[t] = row_scale_of(mx);
-    }
-    const float* lg = logits + (size_t)t * n_exp;
-    const float v = lane < n_exp ? lg[lane] : 0.0f;
-    float m = lg[0];
+// The route of one token in a segment of W lanes of a wave (W a power of two,
+// n_exp <= W <= 64; lanes base .. base + W - 1), lane base + e = expert e
+// holding logit lv: softmax (the max is order-independent; the double sum
+// runs sequentially over the experts as the reference's loop does), k rounds
+// of arg-max over the unused experts (lower index on ties) by a butterfly
+// within the segment, renormalisation. The results do not depend on W. Lane
+// e = 0 of a segment with write set writes the token's ids and weights (and
+// the ids to s_ids when given). Every lane of the wave must call it.
+__device__ __forceinline__ void route_token(float lv, int e, int base, int W, int n_exp, int k, int norm_w,
+                                            float w_scale, bool write, int32_t* __restrict__ ids,
+                                            float* __restrict__ wts, int32_t* s_ids) {
+    const float v = e < n_exp ? lv : 0.0f;
+    float m = __shfl(v, base, DQ_WAVE);
     for (int i = 1; i < n_exp; ++i) {
-        const float o = __shfl(v, i, DQ_WAVE);
+        const float o = __shfl(v, base + i, DQ_WAVE);
         m = (m < o) ? o : m;
     }
-    const float e = lane < n_exp ? expf(v - m) : 0.0f;
+    const float ex = e < n_exp ? expf(v - m) : 0.0f;
     double sum = 0.0;
-    for (int i = 0; i < n_exp; ++i) sum += (double)__shfl(e, i, DQ_WAVE);
-    float p = (float)((double)e / sum);
+    for (int i = 0; i < n_exp; ++i) sum += (double)__shfl(ex, base + i, DQ_WAVE);
+    float p = (float)((double)ex / sum);
     if (isnan(p)) p = 0.0f;
-    // k rounds of argmax over the unused experts (ties: lower index)
-    float key = lane < n_exp ? p : -2.0f;
+    float key = e < n_exp ? p : -2.0f;
     float w[MOE_MAX_K];
     int id[MOE_MAX_K];
     float wsum = 0.0f;
     for (int s = 0; s < k; ++s) {
         float bv = key;
-        int bi = lane;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
+        int bi = e;
+        for (int off = W >> 1; off >= 1; off >>= 1) {
             const float ov = __shfl_xor(bv, off, DQ_WAVE);
             const int oi = __shfl_xor(bi, off, DQ_WAVE);
             if (ov > bv || (ov == bv && oi < bi)) {
@@ -108,36 +91,48 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict_
             }
         }
         id[s] = bi;
-        w[s] = __shfl(p, bi, DQ_WAVE);
+        w[s] = __shfl(p, base + bi, DQ_WAVE);
         wsum += w[s];
-        if (lane == bi) key = -1.0f;
+        if (e == bi) key = -1.0f;
     }
-    if (lane == 0) {
+    if (e == 0 && write) {
         for (int s = 0; s < k; ++s) {
             float ws = w[s];
             if (norm_w && wsum > 1e-9f) ws /= wsum;
             if (w_scale != 0.0f && w_scale != 1.0f) ws *= w_scale;
-            ids[(size_t)t * k + s] = id[s];
-            wts[(size_t)t * k + s] = ws;
+            ids[s] = id[s];
+            wts[s] = ws;
+            if (s_ids) s_ids[s] = id[s];
         }
     }
 }
 
+// One wave per token (the logit load unconditional, clamped).
+__global__ __launch_bounds__(256) void moe_route_kernel(const float* __restrict__ logits, int n_tok, int n_exp,
+                                                        int k, int norm_w, float w_scale, int32_t* __restrict__ ids,
+                                                        float* __restrict__ wts) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= n_tok) return;  // uniform per wave
+    const float lv = logits[(size_t)t * n_exp + (lane < n_exp ? lane : n_exp - 1)];
+    route_token(lv, lane, 0, 64, n_exp, k, norm_w, w_scale, true, ids + (size_t)t * k, wts + (size_t)t * k, nullptr);
+}
+
 // Per-expert lists of the (token, slot) entries i = t*k + s, expert-major and
 // in ascending i; slot_pos[i] = the entry's position in that order. One
-// workgroup of 4 waves takes the entries 256 at a time (wave w: 64w..64w+63
-// of the round); per expert a ballot gives each wave's count and each lane's
-// rank among the earlier lanes of its wave. Pass 1 counts, pass 2 places.
-__global__ __launch_bounds__(256) void moe_lists_kernel(const int32_t* __restrict__ ids, int n_ent, int n_exp,
-                                                        int32_t* __restrict__ offsets, int32_t* __restrict__ pairs,
-                                                        int32_t* __restrict__ slot_pos) {
-    __shared__ int wcnt[4][MOE_MAX_EXPERT];
-    __shared__ int base[MOE_MAX_EXPERT + 1];
+// workgroup of NW waves takes the entries 64 NW at a time (wave w: entries
+// 64w..64w+63 of the round); per expert a ballot gives each wave's count and
+// each lane's rank among the earlier lanes of its wave. Pass 1 counts, pass 2
+// places.
+template <int NW>
+__device__ __forceinline__ void build_lists(const int32_t* ids, int n_ent, int n_exp, int32_t* __restrict__ offsets,
+                                            int32_t* __restrict__ pairs, int32_t* __restrict__ slot_pos,
+                                            int (&wcnt)[NW][MOE_MAX_EXPERT], int (&base)[MOE_MAX_EXPERT + 1]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint64_t lt = lane ? (~0ull >> (64 - lane)) : 0ull;  // lanes below this one
     // pass 1: per-expert totals, lane e of each wave accumulating expert e
     int mine = 0;
-    for (int c0 = 0; c0 < n_ent; c0 += 256) {
+    for (int c0 = 0; c0 < n_ent; c0 += 64 * NW) {
         const int i = c0 + tid;
         const int id = i < n_ent ? ids[i] : -1;
         for (int e = 0; e < n_exp; ++e) {
@@ -147,18 +142,25 @@ __global__ __launch_bounds__(256) void moe_lists_kernel(const int32_t* __restric
     }
     if (lane < n_exp) wcnt[wave][lane] = mine;
     __syncthreads();
+    if (tid < n_exp) {
+        int c = 0;
+        for (int w = 0; w < NW; ++w) c += wcnt[w][tid];
+        base[tid] = c;
+    }
+    __syncthreads();
     if (tid == 0) {
         int o = 0;
         for (int e = 0; e < n_exp; ++e) {
+            const int c = base[e];
             base[e] = o;
-            o += wcnt[0][e] + wcnt[1][e] + wcnt[2][e] + wcnt[3][e];
+            o += c;
         }
         base[n_exp] = o;
     }
     __syncthreads();
     if (tid <= n_exp) offsets[tid] = base[tid];
     // pass 2: positions
-    for (int c0 = 0; c0 < n_ent; c0 += 256) {
+    for (int c0 = 0; c0 < n_ent; c0 += 64 * NW) {
         const int i = c0 + tid;
         const int id = i < n_ent ? ids[i] : -1;
         int rank = 0;
@@ -175,9 +177,61 @@ __global__ __launch_bounds__(256) void moe_lists_kernel(const int32_t* __restric
             slot_pos[i] = pos;
         }
         __syncthreads();
-        if (tid < n_exp) base[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+        if (tid < n_exp) {
+            int c = 0;
+            for (int w = 0; w < NW; ++w) c += wcnt[w][tid];
+            base[tid] += c;
+        }
         __syncthreads();
     }
+}
+
+__global__ __launch_bounds__(256) void moe_lists_kernel(const int32_t* __restrict__ ids, int n_ent, int n_exp,
+                                                        int32_t* __restrict__ offsets, int32_t* __restrict__ pairs,
+                                                        int32_t* __restrict__ slot_pos) {
+    __shared__ int wcnt[4][MOE_MAX_EXPERT];
+    __shared__ int base[MOE_MAX_EXPERT + 1];
+    build_lists<4>(ids, n_ent, n_exp, offsets, pairs, slot_pos, wcnt, base);
+}
+
+// Routing and lists in one workgroup, for up to RL_MAX_TOK tokens (one launch
+// instead of two): a wave routes 64 / W tokens at once, one per segment of W
+// lanes (W = n_exp rounded up to a power of two), the logit loads of
+// RL_BATCH rounds in flight together, keeping the ids in LDS; then the lists
+// as moe_lists_kernel builds them.
+constexpr int RL_WAVES = 16, RL_MAX_TOK = 1024, RL_BATCH = 4;
+__global__ __launch_bounds__(64 * RL_WAVES) void moe_route_lists_kernel(
+    const float* __restrict__ logits, int n_tok, int n_exp, int k, int norm_w, float w_scale,
+    int32_t* __restrict__ ids, float* __restrict__ wts, int32_t* __restrict__ offsets, int32_t* __restrict__ pairs,
+    int32_t* __restrict__ slot_pos) {
+    __shared__ int32_t s_ids[RL_MAX_TOK * MOE_MAX_K];
+    __shared__ int wcnt[RL_WAVES][MOE_MAX_EXPERT];
+    __shared__ int base[MOE_MAX_EXPERT + 1];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int W = 1;
+    while (W < n_exp) W <<= 1;
+    const int G = 64 / W, seg = lane / W, e = lane & (W - 1);
+    const int le = e < n_exp ? e : n_exp - 1;
+    const int per = RL_WAVES * G;  // tokens per round of the workgroup
+    for (int r0 = 0; r0 < n_tok; r0 += per * RL_BATCH) {  // uniform
+        float lv[RL_BATCH];
+#pragma unroll
+        for (int j = 0; j < RL_BATCH; ++j)
+            lv[j] = logits[(size_t)min(r0 + j * per + wave * G + seg, n_tok - 1) * n_exp + le];
+#pragma unroll
+        for (int j = 0; j < RL_BATCH; ++j) {
+            const int t0 = r0 + j * per + wave * G;  // the wave's first token this round
+            if (t0 < n_tok) {                        // wave-uniform
+                const int t = t0 + seg;
+                const bool live = t < n_tok;
+                const int tc = live ? t : 0;
+                route_token(lv[j], e, seg * W, W, n_exp, k, norm_w, w_scale, live, ids + (size_t)tc * k,
+                            wts + (size_t)tc * k, s_ids + tc * k);
+            }
+        }
+    }
+    __syncthreads();
+    build_lists<RL_WAVES>(s_ids, n_tok * k, n_exp, offsets, pairs, slot_pos, wcnt, base);
 }
 
 // ------------------------------------------------------- activation rows --
@@ -210,23 +264,74 @@ __device__ __forceinline__ void quant_256_block(const float (&v)[4], float sc, i
     if ((lane & 7) == 0) minp[((size_t)b * n_rows + p) * 8 + (lane >> 3)] = (_Float16)((d * (float)isum) * sc);
 }
 
-// Row p of A from token pairs[p] / k of x: one wave per (pair, 256-block);
-// the row scales come from the route kernel; inv[p] = 1/s.
-__global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ x, const float* __restrict__ rscale,
-                                                      const int32_t* __restrict__ pairs, int k, int n_rows, int K,
-                                                      _Float16* __restrict__ A, _Float16* __restrict__ minp,
-                                                      float* __restrict__ inv) {
-    const int lane = threadIdx.x & 63;
+// The range scale of a workgroup's row segment from each wave's max |v|:
+// row_scale_of of the 4 waves' maximum.
+__device__ __forceinline__ float wg_range_scale(float mx, float (&wmax)[4], int lane, int wave) {
+    mx = dq_wave_max(mx);
+    if (lane == 0) wmax[wave] = mx;
+    __syncthreads();
+    return row_scale_of(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+}
+
+__device__ __forceinline__ float amax4(const float (&h)[4]) {
+    return fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3])));
+}
+
+// Row p of A from token pairs[p] / k of x, one workgroup of 4 waves per pair:
+// the row's range scale s = row_scale_of(max |x|) and the per-256
+// quantization (quant_256_block); inv[p] = 1/s. Wave w takes the 256-blocks
+// w, w + 4, ... REG (rows of up to 4 * ACT_RB blocks): all of a wave's loads
+// are issued at once (unconditional, clamped to the row) and the values stay
+// in registers from the maximum to the quantization; otherwise two passes
+// (the second's loads hit L2).
+constexpr int ACT_RB = 4;  // 256-blocks per wave held in registers
+template <bool REG>
+__global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ x, const int32_t* __restrict__ pairs,
+                                                      int k, int n_rows, int K, _Float16* __restrict__ A,
+                                                      _Float16* __restrict__ minp, float* __restrict__ inv) {
+    __shared__ float wmax[4];
+    const int p = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nblk = K / 256;
-    const long w = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (w >= (long)n_rows * nblk) return;  // uniform per wave
-    const int p = (int)(w / nblk), b = (int)(w % nblk);
-    const size_t srow = (size_t)(pairs[p] / k);
-    const float sc = rscale[srow];
-    const float4 f = *reinterpret_cast<const float4*>(x + srow * K + 256 * b + 4 * lane);
-    const float v[4] = {f.x, f.y, f.z, f.w};
-    quant_256_block(v, sc, lane, b, p, n_rows, A + (size_t)p * K, minp);
-    if (b == 0 && lane == 0) inv[p] = 1.0f / sc;  // the output factor
+    const float* xr = x + (size_t)(pairs[p] / k) * K;
+    _Float16* row = A + (size_t)p * K;
+    auto load = [&](int b, float (&v)[4]) {
+        const float4 f = *reinterpret_cast<const float4*>(xr + 256 * b + 4 * lane);
+        v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+    };
+    float sc;
+    if constexpr (REG) {
+        float v[ACT_RB][4];
+#pragma unroll
+        for (int i = 0; i < ACT_RB; ++i) {
+            const int b = wave + 4 * i;
+            load(b < nblk ? b : 0, v[i]);  // blocks past the row: block 0 again, left out
+        }
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < ACT_RB; ++i)
+            if (wave + 4 * i < nblk) mx = fmaxf(mx, amax4(v[i]));
+        sc = wg_range_scale(mx, wmax, lane, wave);
+#pragma unroll
+        for (int i = 0; i < ACT_RB; ++i) {
+            const int b = wave + 4 * i;
+            if (b < nblk) quant_256_block(v[i], sc, lane, b, p, n_rows, row, minp);  // wave-uniform
+        }
+    } else {
+        float mx = 0.0f;
+        for (int b = wave; b < nblk; b += 4) {
+            float v[4];
+            load(b, v);
+            mx = fmaxf(mx, amax4(v));
+        }
+        sc = wg_range_scale(mx, wmax, lane, wave);
+        for (int b = wave; b < nblk; b += 4) {
+            float v[4];
+            load(b, v);
+            quant_256_block(v, sc, lane, b, p, n_rows, row, minp);
+        }
+    }
+    if (threadIdx.x == 0) inv[p] = 1.0f / sc;  // the output factor
 }
 
 // The down projection's activation of pair p over the K range of the down
@@ -238,9 +343,14 @@ __global__ __launch_bounds__(256) void moe_act_kernel(const float* __restrict__ 
 // moe_act_kernel writes it; inv[q * n_rows + p] = 1/s. A range scale per
 // split is exact: the GEMM undoes each split's s on that split's partial
 // (powers of two, fp16 and fp32 alike), and the per-256 integers and scales
-// do not depend on s. Wave w takes the 256-blocks w, w + 4, ... of the range:
-// a first pass finds the maximum, a second recomputes h (its loads hit L2)
-// and quantizes it.
+// do not depend on s. Wave w takes the 256-blocks w, w + 4, ... of the range.
+// REG (ranges of up to 4 * RB blocks): the wave's gate and up loads are all
+// issued at once (unconditional, clamped to the range), h stays in registers
+// from the maximum to the quantization, one memory round trip in all;
+// otherwise a first pass finds the maximum and a second recomputes h (its
+// loads hit L2) and quantizes it.
+constexpr int SILU_RB = 4;  // 256-blocks per wave held in registers
+template <bool REG>
 __global__ __launch_bounds__(256) void moe_silu_act_kernel(const float* __restrict__ gate, const float* __restrict__ up,
                                                            int nsplit, size_t split_stride, int F, int n_rows,
                                                            int n_dsplit, int sps, _Float16* __restrict__ A,
@@ -249,35 +359,64 @@ __global__ __launch_bounds__(256) void moe_silu_act_kernel(const float* __restri
     const int p = blockIdx.x / n_dsplit, q = blockIdx.x % n_dsplit;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int b0 = q * sps, b1 = min(b0 + sps, F / 256);
-    auto h_of = [&](int b, float (&h)[4]) {
+    auto load = [&](int b, float4& g, float4& u) {
         const size_t o = (size_t)p * F + 256 * (size_t)b + 4 * lane;
-        float4 g = *reinterpret_cast<const float4*>(gate + o);
-        float4 u = *reinterpret_cast<const float4*>(up + o);
+        g = *reinterpret_cast<const float4*>(gate + o);
+        u = *reinterpret_cast<const float4*>(up + o);
         for (int s = 1; s < nsplit; ++s) {
             const float4 g2 = *reinterpret_cast<const float4*>(gate + s * split_stride + o);
             const float4 u2 = *reinterpret_cast<const float4*>(up + s * split_stride + o);
             g.x += g2.x, g.y += g2.y, g.z += g2.z, g.w += g2.w;
             u.x += u2.x, u.y += u2.y, u.z += u2.z, u.w += u2.w;
         }
+    };
+    auto h_of = [](const float4& g, const float4& u, float (&h)[4]) {
         const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) h[i] = gv[i] / (1.0f + expf(-gv[i])) * uv[i];
     };
-    float mx = 0.0f;
-    for (int b = b0 + wave; b < b1; b += 4) {
-        float h[4];
-        h_of(b, h);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3]))));
-    }
-    mx = dq_wave_max(mx);
-    if (lane == 0) wmax[wave] = mx;
-    __syncthreads();
-    const float sc = row_scale_of(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
     _Float16* row = A + (size_t)p * F;
-    for (int b = b0 + wave; b < b1; b += 4) {
-        float h[4];
-        h_of(b, h);
-        quant_256_block(h, sc, lane, b, p, n_rows, row, minp);
+    float sc;
+    if constexpr (REG) {
+        // blocks past the range (or all of an empty one) load a block of the
+        // row instead and are left out
+        const int bx = min(b0, F / 256 - 1);
+        float4 g[SILU_RB], u[SILU_RB];
+#pragma unroll
+        for (int i = 0; i < SILU_RB; ++i) {
+            const int b = b0 + wave + 4 * i;
+            load(b < b1 ? b : bx, g[i], u[i]);
+        }
+        float h[SILU_RB][4];
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < SILU_RB; ++i) {
+            h_of(g[i], u[i], h[i]);
+            if (b0 + wave + 4 * i < b1) mx = fmaxf(mx, amax4(h[i]));
+        }
+        sc = wg_range_scale(mx, wmax, lane, wave);
+#pragma unroll
+        for (int i = 0; i < SILU_RB; ++i) {
+            const int b = b0 + wave + 4 * i;
+            if (b < b1) quant_256_block(h[i], sc, lane, b, p, n_rows, row, minp);  // wave-uniform
+        }
+    } else {
+        float mx = 0.0f;
+        for (int b = b0 + wave; b < b1; b += 4) {
+            float4 g, u;
+            float h[4];
+            load(b, g, u);
+            h_of(g, u, h);
+            mx = fmaxf(mx, amax4(h));
+        }
+        sc = wg_range_scale(mx, wmax, lane, wave);
+        for (int b = b0 + wave; b < b1; b += 4) {
+            float4 g, u;
+            float h[4];
+            load(b, g, u);
+            h_of(g, u, h);
+            quant_256_block(h, sc, lane, b, p, n_rows, row, minp);
+        }
     }
     if (threadIdx.x == 0) inv[(size_t)q * n_rows + p] = 1.0f / sc;
 }
@@ -289,7 +428,9 @@ struct MoeGemm {
     float* y[2];          // outputs [nsplit][n_pairs][rows]
     const _Float16* A;    // activation rows [n_pairs][K]
     const _Float16* minp; // their block sums [K/256][n_pairs][8]
-    const float* inv;     // [nsplit][n_pairs]: 1/s of each pair's activation over each split's K range
+    const float* inv;     // 1/s of each pair's activation: [nsplit][n_pairs] (a range scale per split's K
+                          // range, inv_stride = n_pairs) or [n_pairs] (one per row, inv_stride = 0)
+    size_t inv_stride;
     const int32_t* offsets;
     int rows, K, n_pairs, nsplit, steps_per_split, main_steps;
     int n_exp, n_tiles;
@@ -554,7 +695,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(2, 2
     const uint8_t* base = G.w[mat];
     const DqLayout L = G.L[mat];
     float* __restrict__ y = G.y[mat] + (size_t)split * G.n_pairs * G.rows;
-    const float* __restrict__ inv_s = G.inv + (size_t)split * G.n_pairs;  // the split's factors
+    const float* __restrict__ inv_s = G.inv + (size_t)split * G.inv_stride;  // the split's factors
     const int s0 = split * G.steps_per_split;
     const int main_end = min(G.main_steps, s0 + G.steps_per_split);
     if (s0 >= main_end) return;  // uniform
@@ -661,7 +802,7 @@ __global__ __launch_bounds__(256) void moe_scatter_kernel(const float* __restric
 // ------------------------------------------------------------- workspace --
 struct MoeWs {
     int32_t *ids, *offsets, *pairs, *slot_pos;
-    float *wts, *xscale, *inv_in, *inv_h;
+    float *wts, *inv_in, *inv_h;
     _Float16 *a_in, *a_h, *min_in, *min_h;
     float *gate, *up, *down;
     size_t total;
@@ -704,7 +845,6 @@ MoeWs carve(const dq_moe_t* m, uint32_t n_tok, int split_gu, int split_d, uint8_
     w.offsets = (int32_t*)take((m->n_expert + 1) * 4);
     w.pairs = (int32_t*)take(n_ent * 4);
     w.slot_pos = (int32_t*)take(n_ent * 4);
-    w.xscale = (float*)take((size_t)n_tok * 4);
     w.inv_in = (float*)take(n_ent * 4);
     w.inv_h = (float*)take((size_t)split_d * n_ent * 4);
     w.a_in = (_Float16*)take(n_ent * E * 2);
@@ -736,8 +876,8 @@ void splits(const dq_moe_t* m, int* sgu, int* sd) {
 }
 
 int launch_gemm(bool tiled, const uint8_t* w0, const uint8_t* w1, int n_mat, int n_exp, int rows, int K,
-                const _Float16* A, const _Float16* minp, const float* inv, const int32_t* offsets, int n_pairs,
-                int nsplit, float* y0, float* y1, hipStream_t s) {
+                const _Float16* A, const _Float16* minp, const float* inv, bool inv_per_split,
+                const int32_t* offsets, int n_pairs, int nsplit, float* y0, float* y1, hipStream_t s) {
     MoeGemm G{};
     G.w[0] = w0;
     G.w[1] = w1 ? w1 : w0;
@@ -748,6 +888,7 @@ int launch_gemm(bool tiled, const uint8_t* w0, const uint8_t* w1, int n_mat, int
     G.A = A;
     G.minp = minp;
     G.inv = inv;
+    G.inv_stride = inv_per_split ? (size_t)n_pairs : 0;
     G.offsets = offsets;
     G.rows = rows;
     G.K = K;
@@ -786,8 +927,7 @@ int dq_moe_route(const float* d_logits, uint32_t n_tok, uint32_t n_expert, uint3
     if (!d_logits || !d_ids || !d_wts) return DQ_ERR_INVALID_ARG;
     if (n_tok > (1u << 24)) return DQ_ERR_NOT_SUPPORTED;
     moe_route_kernel<<<(n_tok + 3) / 4, 256, 0, (hipStream_t)stream>>>(d_logits, (int)n_tok, (int)n_expert, (int)k,
-                                                                       norm_w, w_scale, d_ids, d_wts, nullptr, 0,
-                                                                       nullptr);
+                                                                       norm_w, w_scale, d_ids, d_wts);
     return dq_launch_status();
 }
 
@@ -835,34 +975,44 @@ int dq_moe_ffn(const dq_moe_t* m, const float* d_x, const float* d_logits, uint3
     const int k = (int)m->n_expert_used, n_exp = (int)m->n_expert;
     const int E = (int)m->n_embd, F = (int)m->n_ff;
     const int n_ent = (int)n_tok * k;
-    // routing (with the row scales of x) and the per-expert lists
-    moe_route_kernel<<<(n_tok + 3) / 4, 256, 0, s>>>(d_logits, (int)n_tok, n_exp, k, m->norm_w, m->w_scale, w.ids,
-                                                     w.wts, d_x, E, w.xscale);
-    DQ_TRY(dq_launch_status());
-    moe_lists_kernel<<<1, 256, 0, s>>>(w.ids, n_ent, n_exp, w.offsets, w.pairs, w.slot_pos);
-    DQ_TRY(dq_launch_status());
-    // activation rows of the pairs
-    {
-        const long waves = (long)n_ent * (E / 256);
-        moe_act_kernel<<<(unsigned)((waves + 3) / 4), 256, 0, s>>>(d_x, w.xscale, w.pairs, k, n_ent, E, w.a_in,
-                                                                   w.min_in, w.inv_in);
+    // routing and the per-expert lists (one launch up to RL_MAX_TOK tokens)
+    if (n_tok <= (uint32_t)RL_MAX_TOK) {
+        moe_route_lists_kernel<<<1, 64 * RL_WAVES, 0, s>>>(d_logits, (int)n_tok, n_exp, k, m->norm_w, m->w_scale,
+                                                           w.ids, w.wts, w.offsets, w.pairs, w.slot_pos);
+        DQ_TRY(dq_launch_status());
+    } else {
+        moe_route_kernel<<<(n_tok + 3) / 4, 256, 0, s>>>(d_logits, (int)n_tok, n_exp, k, m->norm_w, m->w_scale,
+                                                         w.ids, w.wts);
+        DQ_TRY(dq_launch_status());
+        moe_lists_kernel<<<1, 256, 0, s>>>(w.ids, n_ent, n_exp, w.offsets, w.pairs, w.slot_pos);
         DQ_TRY(dq_launch_status());
     }
+    // activation rows of the pairs, each with its range scale
+    if (E / 256 <= 4 * ACT_RB)
+        moe_act_kernel<true><<<(unsigned)n_ent, 256, 0, s>>>(d_x, w.pairs, k, n_ent, E, w.a_in, w.min_in, w.inv_in);
+    else
+        moe_act_kernel<false><<<(unsigned)n_ent, 256, 0, s>>>(d_x, w.pairs, k, n_ent, E, w.a_in, w.min_in, w.inv_in);
+    DQ_TRY(dq_launch_status());
     // gate and up of every pair (one launch, two matrices)
     const bool tiled = m->fmt == DQ_FMT_Q4_K_TILES;
+    // (one range scale per activation row, whatever the K split)
     DQ_TRY(launch_gemm(tiled, (const uint8_t*)m->wgate, (const uint8_t*)m->wup, 2, n_exp, F, E, w.a_in, w.min_in,
-                       w.inv_in,
-                       w.offsets, n_ent, sgu, w.gate, w.up, s));
+                       w.inv_in, false, w.offsets, n_ent, sgu, w.gate, w.up, s));
     // h = silu(gate) * up, quantized for the down projection
     {
         const int sps = (F / 256 + sd - 1) / sd;  // the down GEMM's super-blocks per split (launch_gemm)
-        moe_silu_act_kernel<<<(unsigned)((size_t)n_ent * sd), 256, 0, s>>>(
-            w.gate, w.up, sgu, (size_t)n_ent * F, F, n_ent, sd, sps, w.a_h, w.min_h, w.inv_h);
+        const unsigned wgs = (unsigned)((size_t)n_ent * sd);
+        if (sps <= 4 * SILU_RB)
+            moe_silu_act_kernel<true><<<wgs, 256, 0, s>>>(w.gate, w.up, sgu, (size_t)n_ent * F, F, n_ent, sd, sps,
+                                                          w.a_h, w.min_h, w.inv_h);
+        else
+            moe_silu_act_kernel<false><<<wgs, 256, 0, s>>>(w.gate, w.up, sgu, (size_t)n_ent * F, F, n_ent, sd, sps,
+                                                           w.a_h, w.min_h, w.inv_h);
     }
     DQ_TRY(dq_launch_status());
-    DQ_TRY(launch_gemm(tiled, (const uint8_t*)m->wdown, nullptr, 1, n_exp, E, F, w.a_h, w.min_h, w.inv_h, w.offsets,
-                       n_ent,
-                       sd, w.down, nullptr, s));
+    // (a range scale per down split)
+    DQ_TRY(launch_gemm(tiled, (const uint8_t*)m->wdown, nullptr, 1, n_exp, E, F, w.a_h, w.min_h, w.inv_h, true,
+                       w.offsets, n_ent, sd, w.down, nullptr, s));
     {
         const size_t n = (size_t)n_tok * E;
         moe_scatter_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(w.down, sd, (size_t)n_ent * E, w.slot_pos,

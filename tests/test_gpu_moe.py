@@ -67,6 +67,10 @@ def moe_oracle_all(orc, ws, n_exp, E, F, x, lg, n_tok, k, threads=8):
     (300, 4, 2, 256, 512, True),      # one expert gets > 128 tokens (several passes)
     (1, 2, 2, 256, 256, False),       # one token, every expert
     (4, 4, 2, 256, 16640, False),     # n_ff past 16384 (65 super-blocks over 8 uneven down splits)
+    (3, 4, 2, 4352, 256, False),      # rows of 17 blocks: the activation rows' two-pass form
+    (3, 4, 2, 256, 33280, False),     # 17 super-blocks per down split: SiLU's two-pass form
+    (40, 6, 2, 512, 1024, False),     # routing segments of 8 lanes with 2 lanes unused
+    (20, 64, 8, 512, 1024, False),    # 64 experts, top-8: one token per wave
 ])
 def test_moe_ffn(gpu, orc, n_tok, n_exp, k, E, F, skew):
     print(f"moe n_tok={n_tok} experts={n_exp} k={k} E={E} F={F}", flush=True)
@@ -92,6 +96,27 @@ def test_moe_ffn(gpu, orc, n_tok, n_exp, k, E, F, skew):
     # a second call on the same workspace gives the same bits
     again = moe(torch.from_numpy(x).to(gpu), torch.from_numpy(lg).to(gpu)).cpu().numpy()
     assert np.array_equal(got, again)
+
+
+def test_moe_route_launch_forms_agree(gpu, orc):
+    """Past 1024 tokens the routing and the lists run as two launches (one
+    wave per token, then one workgroup) instead of one workgroup. A token's
+    output does not depend on the other tokens of the call (its expert tiles
+    add the same products in the same order), so the first 1000 of 1100
+    tokens must equal a 1000-token call bit for bit; the whole call is held to
+    the oracle at the product tolerance."""
+    n_exp, k, E, F, n = 4, 2, 512, 1024, 1100
+    ws, mats = make_moe(gpu, n_exp, E, F, seed=91)
+    x = synth.gen_act((n, E), seed=13)
+    lg = synth.gen_act((n, n_exp), seed=14)
+    moe = ops.MoeLayer(*mats, n_expert=n_exp, n_expert_used=k)
+    two = moe(torch.from_numpy(x).to(gpu), torch.from_numpy(lg).to(gpu)).cpu().numpy()
+    one = moe(torch.from_numpy(x[:1000]).to(gpu), torch.from_numpy(lg[:1000]).to(gpu)).cpu().numpy()
+    assert np.array_equal(two[:1000], one)
+    want = moe_oracle_all(orc, ws, n_exp, E, F, x, lg, n, k)
+    e = rel(two, want)
+    print(f"  rel err {e:.3e}", flush=True)
+    assert e <= TOL
 
 
 def test_moe_not_supported(gpu):
