@@ -448,6 +448,36 @@ def stream_read_ceiling(dev, nbytes, reps=20):
     return out, max(out.values())
 
 
+def lds_probe_patterns():
+    """Per-lane LDS byte offsets for dq_lds_read_probe (16-byte reads):
+    - quads(i, j): lane quad i (lanes 4i..4i+3) reads bytes 0..63, quad j
+      bytes 256..319 (the same 16 banks at another address), every other lane
+      bytes 64..127 at its lane's slot (one address per slot: broadcasts on
+      other banks). Only quads i and j can conflict, and they do exactly when
+      one cycle serves both: every pair of the first half-wave's 8 quads, then
+      quad 0 against each quad of the second half-wave;
+    - contiguous: lane l at 16 l;
+    - the prefill GEMM's Q4_K weight-fragment reads (64-byte rows, lane l on
+      row l % 32, sub-plane l / 32 at a 16 KiB plane stride, item 0) with the
+      earlier chunk swizzle ((row / 2) ^ (row / 8)) % 4 and the current
+      (row / 4) % 4."""
+    pats = []
+    for i in range(8):
+        for j in range(i + 1, 16):
+            if j >= 8 and i > 0:
+                continue
+            offs = [64 + 16 * (l % 4) for l in range(64)]
+            for l in range(4):
+                offs[4 * i + l] = 16 * l
+                offs[4 * j + l] = 256 + 16 * l
+            pats.append((f"quads({i},{j})", offs))
+    pats.append(("contiguous", [16 * l for l in range(64)]))
+    for nm, swz in (("q4k_b_earlier_swizzle", lambda n: ((n >> 1) ^ (n >> 3)) & 3),
+                    ("q4k_b_current_swizzle", lambda n: (n >> 2) & 3)):
+        pats.append((nm, [16384 * (l >> 5) + 64 * (l & 31) + 16 * swz(l & 31) for l in range(64)]))
+    return pats
+
+
 # ------------------------------------------------------------------ CPU side
 
 def host_description():
@@ -744,6 +774,19 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copy: {args.steps} x {src.numel()} bytes")
+        return
+    if args.only == "lds_phases":
+        # one dispatch per pattern, to be run under a SQ_LDS_BANK_CONFLICT
+        # counter pass (the dispatch order is logged)
+        lib = _lib.load()
+        from desireeia_amd import ops
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+        for name, offs in lds_probe_patterns():
+            d_off = torch.tensor(offs, dtype=torch.int32, device=dev)
+            _lib.check(lib.dq_lds_read_probe(ops._ptr(d_off), 2000, 1024, 0, ops._ptr(sink), 0x9E3779B9,
+                                             ops._stream()), "dq_lds_read_probe")
+            torch.cuda.synchronize()
+            log(f"lds pattern: {name}")
         return
     if args.only == "ceiling":
         for nb in (33103872, 17858560):

@@ -17,6 +17,7 @@ SIGNATURES = {
     "dq_version": (c_int, []),
     "dq_device_count": (c_int, []),
     "dq_stream_read": (c_int, [c_p, c_size, c_u32, c_u32, c_p, c_u32, c_p]),
+    "dq_lds_read_probe": (c_int, [c_p, c_u32, c_u32, c_int, c_p, c_u32, c_p]),
     "dq_dequantize_row": (c_int, [c_int, c_p, c_p, c_i64, c_p]),
     "dq_weights_bytes": (c_int, [c_int, c_size, c_size, ctypes.POINTER(c_size)]),
     "dq_weights_pack": (c_int, [c_int, c_p, c_size, c_size, c_p, c_p]),

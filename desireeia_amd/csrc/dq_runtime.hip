@@ -1,7 +1,9 @@
-// dq_runtime.hip - library version, device query, and the streaming-read
-// probe the benchmark uses to measure the device's read ceiling at a GEMV's
-// size (a read of N bytes with no arithmetic: what a bandwidth-bound kernel
-// of that size can at best approach on this device).
+// dq_runtime.hip - library version, device query, and two probes the
+// benchmark uses: the streaming read that measures the device's read ceiling
+// at a GEMV's size (a read of N bytes with no arithmetic: what a
+// bandwidth-bound kernel of that size can at best approach on this device),
+// and the LDS read probe whose bank-conflict counts show which lanes a
+// 16-byte LDS read serves together (the fragment swizzles depend on it).
 #include "dq_common.h"
 
 extern "C" int dq_version(void) { return 1; }
@@ -37,7 +39,36 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const uint4* __restric
     if (acc == never) sink[0] = acc;
 }
 
+constexpr int PROBE_LDS = 65536;  // bytes of LDS the probe reads
+
+// One wave per workgroup: lane l reads 16 bytes at LDS byte offset
+// offs[l] + it * stride (wrapped into the 64 KiB buffer, 16-byte aligned) for
+// it = 0 .. iters - 1, one ds_read_b128 per iteration; the loaded words are
+// folded and stored only if they equal `never`. With stride 0 every
+// iteration repeats the same access pattern (the stride, a kernel argument,
+// keeps the compiler from hoisting the read out of the loop).
+__global__ __launch_bounds__(64) void lds_read_probe_kernel(const int32_t* __restrict__ offs, int iters, int stride,
+                                                            uint32_t* __restrict__ sink, uint32_t never) {
+    __shared__ __align__(16) uint8_t buf[PROBE_LDS];
+    for (int i = threadIdx.x; i < PROBE_LDS / 4; i += 64) reinterpret_cast<uint32_t*>(buf)[i] = i * 2654435761u;
+    __syncthreads();
+    const int off = offs[threadIdx.x];
+    uint4 acc = {0u, 0u, 0u, 0u};
+    for (int it = 0; it < iters; ++it) {
+        const uint4 v = *reinterpret_cast<const uint4*>(buf + ((off + it * stride) & (PROBE_LDS - 16)));
+        acc.x ^= v.x, acc.y += v.y, acc.z ^= v.z, acc.w += v.w;
+    }
+    if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == never) sink[0] = acc.x;
+}
+
 }  // namespace
+
+extern "C" int dq_lds_read_probe(const int32_t* d_offsets, uint32_t iters, uint32_t n_wg, int32_t stride,
+                                 uint32_t* d_sink, uint32_t never, void* stream) {
+    if (!d_offsets || !d_sink || n_wg == 0 || n_wg > 65535 || iters > (1u << 20)) return DQ_ERR_INVALID_ARG;
+    lds_read_probe_kernel<<<n_wg, 64, 0, (hipStream_t)stream>>>(d_offsets, (int)iters, stride, d_sink, never);
+    return dq_launch_status();
+}
 
 extern "C" int dq_stream_read(const void* d_src, size_t bytes, uint32_t waves_per_cu, uint32_t depth_kb,
                               uint32_t* d_sink, uint32_t never, void* stream) {

@@ -70,6 +70,16 @@ int dq_device_count(void);
 int dq_stream_read(const void* d_src, size_t bytes, uint32_t waves_per_cu, uint32_t depth_kb, uint32_t* d_sink,
                    uint32_t never, void* stream);
 
+/* LDS read probe (no counterpart in the reference: it shows which lanes this
+ * device's LDS serves together for a 16-byte read). n_wg one-wave workgroups;
+ * lane l of each reads 16 bytes at LDS byte offset d_offsets[l] + it * stride
+ * (64 device int32; wrapped into a 64 KiB buffer, 16-byte aligned) for iters
+ * iterations (at most 2^20), one ds_read_b128 each; run it under a
+ * SQ_LDS_BANK_CONFLICT counter pass. Writes d_sink[0] only if the folded
+ * words equal `never`. */
+int dq_lds_read_probe(const int32_t* d_offsets, uint32_t iters, uint32_t n_wg, int32_t stride, uint32_t* d_sink,
+                      uint32_t never, void* stream);
+
 /* Replaces desireeia_dequantize_row (quant/quant.cpp:912-984) for the on-path
  * types Q4_0, Q8_0, Q8_1, Q4_K, Q6_K: GGUF blocks in, n fp32 values out,
  * bit-exact. n must be a multiple of the block size. Other types: -2. */
