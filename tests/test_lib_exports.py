@@ -50,3 +50,20 @@ def test_no_oracle_in_product_library():
     import subprocess
     out = subprocess.run(["nm", "-D", _lib.LIB_PATH], capture_output=True, text=True).stdout
     assert "dqo_" not in out and "dqr_" not in out
+
+
+def test_lds_probe_patterns():
+    """bench.lds_probe_patterns: 64 in-range, 16-byte aligned offsets each;
+    in a quad-pair pattern only quads i and j touch the first 16 banks, at
+    different addresses, and every other lane reads one address per slot."""
+    import bench
+    pats = dict(bench.lds_probe_patterns())
+    assert len(pats) == 39
+    for name, offs in pats.items():
+        assert len(offs) == 64 and all(0 <= o <= 65536 - 16 and o % 16 == 0 for o in offs), name
+    for i, j in ((0, 3), (1, 2), (0, 15)):
+        offs = pats[f"quads({i},{j})"]
+        low = sorted({l // 4 for l in range(64) if offs[l] % 256 < 64})
+        assert low == [i, j]
+        assert {offs[4 * i + l] for l in range(4)}.isdisjoint({offs[4 * j + l] for l in range(4)})
+        assert {offs[l] for l in range(64) if l // 4 not in (i, j)} == {64, 80, 96, 112}
